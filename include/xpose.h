@@ -1,0 +1,280 @@
+/*
+ * xpose.h — C ABI of the MI355X (gfx950) Gemma-3 int4 decode hot path.
+ *
+ * Plain C: device pointers, sizes and an opaque stream handle; no C++ or torch
+ * types cross this boundary. Every entry point returns 0 on success or a
+ * negative XP_E* code; xp_last_error() then holds a message that names the
+ * entry point and the offending argument (the reference throws
+ * std::runtime_error with the kernel name, examples/llm/decode.cpp:46-56;
+ * here the C++ wrapper in xpose_amd/csrc/session.hpp turns the code back into
+ * that exception).
+ *
+ * Threading: like the reference Context (agent-docs/vulkore-core.md:76) the
+ * library is single-threaded per device. Scratch owned by the library (split-k
+ * tickets, attention partials) is shared by every call on a device, so calls
+ * that overlap on two streams of one device race.
+ *
+ * Packed weights (unchanged from the reference, examples/llm/decode.hpp:46-48,
+ * :361-370):
+ *   nibbles  KM4 plane: uint4 wq[(g*nblk + b)*64 + t], g = j/64, t = j%64,
+ *            b = k/32; 32-bit component (k>>3)&3, nibble (k&7)*4;
+ *            weight = nibble - 8.  `rows` = K (input length, multiple of 32),
+ *            `cols` = N (outputs, multiple of 64).
+ *   scales   one per (block, column), in one of three planes (xp_scale_fmt):
+ *            XP_SCALE_F16_QUAD  uint16 sc[((b/4)*cols + j)*4 + (b%4)]  (fp16)
+ *            XP_SCALE_BF16_QUAD same arrangement, bf16 payload — the reference
+ *                               Km4Bf16 plane (decode.hpp:369-370)
+ *            XP_SCALE_F32       float  sc[b*cols + j]  — the reference Km4
+ *                               plane (llm_matvec.cl:187-200)
+ *            The two quad planes need nblk % 4 == 0 (decode.cpp:997-1005).
+ */
+#ifndef XPOSE_H
+#define XPOSE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- status codes ------------------------------------------------------ */
+#define XP_OK            0
+#define XP_E_ARG        -1   /* bad argument (shape, null pointer, range)   */
+#define XP_E_HIP        -2   /* a HIP runtime call failed                    */
+#define XP_E_NOMEM      -3   /* device or host allocation failed             */
+#define XP_E_STATE      -4   /* call not valid in the current state          */
+#define XP_E_DEVICE     -5   /* a kernel reported a device-side error        */
+
+typedef void* xp_stream;   /* a hipStream_t; NULL = the default stream */
+
+enum xp_scale_fmt {
+    XP_SCALE_F16_QUAD  = 0,
+    XP_SCALE_BF16_QUAD = 1,
+    XP_SCALE_F32       = 2
+};
+
+/* ---- library / device -------------------------------------------------- */
+const char* xp_last_error(void);
+const char* xp_version(void);
+/* Selects device `dev` for this thread and sets up per-device scratch. */
+int xp_init(int dev);
+/* name (NUL-terminated, truncated to cap), CU count, HBM bytes, gcnArch. */
+int xp_device_info(char* name, size_t cap, int* n_cu, size_t* hbm_bytes,
+                   char* arch, size_t arch_cap);
+
+/* ---- memory / streams / events (plumbing for hosts without a runtime) --- */
+int xp_malloc(void** dptr, size_t bytes);
+int xp_free(void* dptr);
+int xp_memcpy_htod(void* dst, const void* src, size_t bytes);
+int xp_memcpy_dtoh(void* dst, const void* src, size_t bytes);
+int xp_memcpy_dtod(void* dst, const void* src, size_t bytes);
+int xp_memset(void* dst, int value, size_t bytes);
+int xp_synchronize(void);
+int xp_stream_create(xp_stream* s);
+int xp_stream_destroy(xp_stream s);
+int xp_stream_synchronize(xp_stream s);
+typedef void* xp_event;
+int xp_event_create(xp_event* e);
+int xp_event_destroy(xp_event e);
+int xp_event_record(xp_event e, xp_stream s);
+int xp_event_elapsed_ms(xp_event start, xp_event stop, float* ms);
+
+/* ---- kernel-level entry points (the named-kernel contract) -------------- */
+
+/* int4 KM4 matvec: out[j] = sum_k in[k] * (nibble(k,j) - 8) * scale(k/32, j).
+ * Replaces mv_km4 / mv_km4_bs (+ _split and mv_reduce)
+ * (kernels/llm_matvec.cl:187-200, :339-356, :422-456, :128-135) and the COL
+ * gold's semantics (kernels/llm.cl:488-573). `split` = number of k-chunks
+ * (0 = choose); chunks are whole scale quads; split > 1 sums the chunks in
+ * ascending order (deterministic). out must not alias in. */
+int xp_mv_int4(float* out, const float* in, const void* wq, const void* scales,
+               int scale_fmt, uint32_t rows, uint32_t cols, uint32_t split,
+               xp_stream stream);
+
+/* Several int4 matvecs that share one input vector, in one launch
+ * (Q/K/V, or gate/up). out_i has cols_i floats. n <= 4. */
+int xp_mv_int4_multi(uint32_t n, float* const* outs, const float* in,
+                     const void* const* wqs, const void* const* scales,
+                     const uint32_t* cols, int scale_fmt, uint32_t rows,
+                     xp_stream stream);
+
+/* Debug/unpack entry: expands a KM4 nibble plane to int8 weights w[k*cols+j]
+ * = nibble - 8 (row-major [rows][cols]), for bit-exact unpack checks. */
+int xp_unpack_km4(int8_t* out, const void* wq, uint32_t rows, uint32_t cols,
+                  xp_stream stream);
+/* Decodes n raw fp16 bit patterns to fp32 on the device (the reference's
+ * fp16_decode sweep kernel, kernels/llm_quant.cl:79-87). */
+int xp_fp16_decode(float* out, const uint16_t* src, uint32_t n, xp_stream stream);
+
+/* Two-pass Gemma RMSNorm in one launch: out = in * rsqrt(mean(in^2)+eps) *
+ * (1 + w). Replaces rmsnorm_sumsq + rmsnorm_apply_gemma
+ * (kernels/llm_transformer.cl:96-116). out may alias in. */
+int xp_rmsnorm_gemma(float* out, const float* in, const float* w, uint32_t n,
+                     float eps, xp_stream stream);
+
+/* Per-head Gemma RMSNorm (QK-norm). Replaces rmsnorm_heads_gemma
+ * (kernels/llm_transformer.cl:122-134). */
+int xp_rmsnorm_heads_gemma(float* out, const float* in, const float* w,
+                           uint32_t n_heads, uint32_t head_dim, float eps,
+                           xp_stream stream);
+
+/* In-place rotate-half RoPE. Replaces rope (kernels/llm_transformer.cl:158-179). */
+int xp_rope(float* x, uint32_t n_heads, uint32_t head_dim, uint32_t pos,
+            float theta, xp_stream stream);
+
+/* QK-norm + RoPE on q and k, then append k and v at `pos` to fp16 caches
+ * laid out [t][kv_heads][head_dim]. Fuses rmsnorm_heads_gemma x2, rope x2
+ * and kv_append x2 (llm_transformer.cl:122-179, :590-595;
+ * decode.cpp:1678-1683). q_out/k_out receive the normed, rotated vectors. */
+int xp_qk_norm_rope_append(float* q_out, float* k_out, const float* q_raw,
+                           const float* k_raw, const float* v,
+                           const float* q_norm_w, const float* k_norm_w,
+                           uint16_t* kcache, uint16_t* vcache,
+                           uint32_t n_heads, uint32_t kv_heads, uint32_t head_dim,
+                           uint32_t pos, float theta, float eps, xp_stream stream);
+
+/* Decode attention over fp16 caches for keys [kv_start, kv_start+span):
+ * out[h][d] = sum_j softmax_j(scale * q_h . k_j) * v_j[d], GQA head map
+ * h / (n_heads/kv_heads). Replaces attention_scores(_mq4), softmax_rows(_*),
+ * attention_apply(_mq4) + _reduce (llm_transformer.cl:287-557). */
+int xp_attention_decode(float* out, const float* q, const uint16_t* kcache,
+                        const uint16_t* vcache, uint32_t n_heads,
+                        uint32_t kv_heads, uint32_t head_dim, uint32_t span,
+                        uint32_t kv_start, float scale, xp_stream stream);
+
+/* out = gelu_tanh(gate) * up. Replaces geglu (llm_transformer.cl:223-231). */
+int xp_geglu(float* out, const float* gate, const float* up, uint32_t n,
+             xp_stream stream);
+/* x += y. Replaces add_residual (llm_transformer.cl:564-568). */
+int xp_add_residual(float* x, const float* y, uint32_t n, xp_stream stream);
+/* cache[pos*n + i] = fp16(src[i]). kv_append with an fp16 cache
+ * (llm_transformer.cl:590-595). */
+int xp_kv_append_f16(uint16_t* cache, const float* src, uint32_t n,
+                     uint32_t pos, xp_stream stream);
+
+/* Greedy argmax, lowest index on ties. out_val[0] = value, out_idx[0] = index.
+ * Replaces argmax_partial/_reduce/_final (llm_sampling.cl:57-123). */
+int xp_argmax(uint32_t* out_idx, float* out_val, const float* logits,
+              uint32_t n, xp_stream stream);
+/* Best 4 of each strided chain e = p (mod nparts), descending, sentinel
+ * (-inf, 0xFFFFFFFF). Replaces topk4_partial (llm_sampling.cl:318-347). */
+int xp_topk4_harvest(float* cval, uint32_t* cidx, const float* logits,
+                     uint32_t n, uint32_t nparts, xp_stream stream);
+
+/* ---- synthetic inputs (host side, counter-based, any thread count) ------ */
+/* Philox4x32-10 (Salmon et al., SC'11): out = philox(ctr, key). */
+void xp_philox4x32_10(const uint32_t ctr[4], const uint32_t key[2], uint32_t out[4]);
+/* KM4 nibble plane for tensor `tensor_id`: uint4 i = philox((i,0,0,0),
+ * (seed, tensor_id)); every nibble is uniform on [0,15]. */
+int xp_synth_nibbles(uint32_t* wq, uint32_t rows, uint32_t cols, uint32_t seed,
+                     uint32_t tensor_id);
+/* fp16 scales fp16_rne(|N(0, sigma)|), logical index e = b*cols + j, written
+ * in the plane `scale_fmt` (F16 quad or F32). */
+int xp_synth_scales(void* sc, int scale_fmt, uint32_t rows, uint32_t cols,
+                    float sigma, uint32_t seed, uint32_t tensor_id);
+/* n floats ~ N(mean, sigma) (stream `tensor_id`). */
+int xp_synth_normal(float* out, size_t n, float mean, float sigma, uint32_t seed,
+                    uint32_t tensor_id);
+/* n fp16 values fp16_rne(N(mean, sigma)). */
+int xp_synth_normal_f16(uint16_t* out, size_t n, float mean, float sigma,
+                        uint32_t seed, uint32_t tensor_id);
+/* Round-to-nearest-even fp32 -> fp16 bits. */
+uint16_t xp_f32_to_f16(float f);
+
+/* ---- decode session (engine level) --------------------------------------
+ * Mirrors DecodeSession (examples/llm/decode.hpp:605-676): construct = load,
+ * prefill(ids), decode_step() -> token (sample first from the previous
+ * pass's logits, then run the network on it, decode.cpp:1819-1866), reset(),
+ * last_logits(), position(). Weights come from xp_session_upload (packed
+ * KM4 planes, the reference's layout) or xp_session_synthesize (the seeded
+ * synthetic model); the GGUF loader is not part of this library. */
+typedef struct xp_session xp_session;
+
+typedef struct {
+    uint32_t n_layers, hidden, ffn, n_heads, n_kv_heads, head_dim, vocab, max_seq;
+    uint32_t global_every;      /* layer l is global iff (l+1) % global_every == 0 */
+    uint32_t sliding_window;    /* window of the local layers (decode.hpp:327-352) */
+    float    rms_eps, rope_theta_global, rope_theta_local;
+    float    embed_scale;       /* 0 => sqrt(hidden) */
+    float    attn_scale;        /* 0 => 1/sqrt(head_dim) */
+    int32_t  scale_fmt;         /* xp_scale_fmt of every int4 weight */
+    /* Sampling (decode.hpp:158-202). mode 0 = greedy (device argmax),
+     * 1 = temperature / top-k / top-p over the top-4-per-chain harvest. The
+     * draw's uniform is Philox(key = (seed, seq_id), counter = step). */
+    int32_t  sample_mode;
+    float    temperature;
+    uint32_t top_k;
+    float    top_p;
+    uint32_t seed;
+    uint32_t seq_id;
+    uint32_t topk_parts;
+} xp_config;
+
+/* Tensor ids for upload / synthesis. Matrices are (rows = input length,
+ * cols = outputs): Q hidden->n_heads*hd, K/V hidden->kv_heads*hd,
+ * O n_heads*hd->hidden, GATE/UP hidden->ffn, DOWN ffn->hidden, LM_HEAD
+ * (tied embedding) hidden->vocab. OR a matrix id with XP_T_SCALES for its
+ * scale plane. Norm weights are stored as multiplier - 1 (the kernels apply
+ * 1 + w, decode.cpp:1490-1515). Per-layer ids take layer >= 0; LM_HEAD and
+ * FINAL_NORM take layer = -1. */
+enum xp_tensor {
+    XP_T_Q = 0, XP_T_K = 1, XP_T_V = 2, XP_T_O = 3, XP_T_GATE = 4, XP_T_UP = 5, XP_T_DOWN = 6,
+    XP_T_ATTN_NORM = 16, XP_T_POST_ATTN_NORM = 17, XP_T_FFN_NORM = 18,
+    XP_T_POST_FFN_NORM = 19, XP_T_Q_NORM = 20, XP_T_K_NORM = 21,
+    XP_T_LM_HEAD = 32, XP_T_FINAL_NORM = 33,
+    XP_T_SCALES = 0x100
+};
+
+typedef struct {
+    double   ms;            /* wall time of the last call */
+    double   gpu_ms;        /* graph replays + wait */
+    double   sample_ms;     /* host draw (temperature mode) */
+    double   tokens_per_sec;
+    uint32_t position;
+    uint32_t launches;      /* kernels per token step */
+} xp_metrics;
+
+/* Gemma-3-1B shape and defaults (DecodeConfig::gemma3_1b, decode.hpp:204-356)
+ * with fp16 quad scales and greedy sampling. */
+void xp_config_gemma3_1b(xp_config* c);
+int  xp_session_create(const xp_config* c, xp_session** out);
+int  xp_session_destroy(xp_session* s);
+int  xp_tensor_bytes(const xp_config* c, int layer, int tensor, size_t* bytes);
+int  xp_session_upload(xp_session* s, int layer, int tensor, const void* host, size_t bytes);
+/* The synthetic model of the benchmark configs, bit-identical to what
+ * xp_synth_tensor returns: nibbles uniform on [0,15], fp16 scales
+ * |N(0, 0.02)|, norm multipliers N(1, 0.1) (stored minus 1). */
+int  xp_synth_tensor(const xp_config* c, uint32_t seed, int layer, int tensor, void* host,
+                     size_t bytes);
+int  xp_session_synthesize(xp_session* s, uint32_t seed);
+/* KV cache rows [pos0, pos0+n) of layer's K (which = 0) or V (1), fp16. */
+int  xp_session_kv_upload(xp_session* s, int layer, int which, uint32_t pos0, uint32_t n,
+                          const uint16_t* host);
+int  xp_session_kv_download(xp_session* s, int layer, int which, uint32_t pos0, uint32_t n,
+                            uint16_t* host);
+/* Moves the position without running the network (the cache rows below
+ * `pos` must already hold keys/values, e.g. from xp_session_kv_upload). */
+int  xp_session_set_position(xp_session* s, uint32_t pos);
+int  xp_session_prefill(xp_session* s, const uint32_t* ids, uint32_t n);
+int  xp_session_decode_step(xp_session* s, uint32_t* token);
+/* n greedy steps queued back to back with one wait; tokens[i] is step i's id. */
+int  xp_session_decode_steps(xp_session* s, uint32_t n, uint32_t* tokens);
+int  xp_session_reset(xp_session* s);
+int  xp_session_position(const xp_session* s, uint32_t* pos);
+int  xp_session_last_logits(xp_session* s, float* host, uint32_t n);
+/* Raw harvest of the last pass (temperature mode): 4*topk_parts pairs. */
+int  xp_session_last_candidates(xp_session* s, float* val, uint32_t* idx, uint32_t n);
+int  xp_session_last_metrics(const xp_session* s, xp_metrics* m);
+int  xp_session_weight_bytes(const xp_session* s, size_t* bytes);
+int  xp_session_kv_bytes(const xp_session* s, size_t* bytes);
+/* Host draw over (value, index) candidates, in place (decode.cpp:1873-1917),
+ * with u in [0,1) standing in for the reference's mt19937_64 draw. */
+uint32_t xp_draw(float* val, uint32_t* idx, uint32_t n, float temperature, uint32_t top_k,
+                 float top_p, double u);
+double xp_philox_uniform(uint32_t seed, uint32_t seq, uint32_t step);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* XPOSE_H */

@@ -1,0 +1,771 @@
+/*
+ * oracle.c — CPU restatement of the reference Gemma-3 decode arithmetic.
+ * TEST INFRASTRUCTURE ONLY (see oracle.h): the checker for libxpose and the
+ * timed CPU baseline in bench.py; never linked into the product.
+ *
+ * Line citations are into /root/reference (badnikhil/Xpose). Parallel loops
+ * (OpenMP) only split independent output elements; each element's arithmetic
+ * is the reference's sequential order, so results do not depend on the
+ * thread count.
+ */
+#include "oracle.h"
+
+#include <math.h>
+#include <omp.h>
+#include <stdlib.h>
+#include <string.h>
+
+static int g_threads = 0;   /* 0 = OpenMP default */
+static int nthreads(void) { return g_threads > 0 ? g_threads : omp_get_max_threads(); }
+
+/* ------------------------------------------------------------------ */
+/* Scalar formats                                                       */
+/* ------------------------------------------------------------------ */
+
+static float as_float(uint32_t u) { float f; memcpy(&f, &u, 4); return f; }
+static uint32_t as_uint(float f) { uint32_t u; memcpy(&u, &f, 4); return u; }
+
+/* fp16_to_fp32, kernels/llm_quant.cl:56-77: integer bit surgery, subnormals
+ * normalised by a shift loop, Inf/NaN mantissa kept. */
+float xo_fp16_to_fp32(uint32_t h) {
+    uint32_t sign = (h & 0x8000u) << 16;
+    uint32_t exp = (h >> 10) & 0x1Fu;
+    uint32_t mant = h & 0x3FFu;
+    uint32_t bits;
+    if (exp == 0u) {
+        if (mant == 0u) {
+            bits = sign;
+        } else {
+            uint32_t m = mant;
+            int e = -1;
+            do { m <<= 1; e++; } while ((m & 0x400u) == 0u);
+            m &= 0x3FFu;
+            bits = sign | ((uint32_t)(112 - e) << 23) | (m << 13);
+        }
+    } else if (exp == 31u) {
+        bits = sign | 0x7F800000u | (mant << 13);
+    } else {
+        bits = sign | ((exp + 112u) << 23) | (mant << 13);
+    }
+    return as_float(bits);
+}
+
+/* Round-to-nearest-even fp32 -> fp16 (the build's KV-cache store; the
+ * reference keeps fp32 KV, decode.cpp:1544-1545). */
+uint16_t xo_fp32_to_fp16(float f) {
+    uint32_t x = as_uint(f);
+    uint32_t sign = (x >> 16) & 0x8000u;
+    uint32_t ax = x & 0x7FFFFFFFu;
+    if (ax >= 0x7F800000u) return (uint16_t)(sign | (ax > 0x7F800000u ? 0x7E00u : 0x7C00u));
+    if (ax >= 0x477FF000u) return (uint16_t)(sign | 0x7C00u);
+    if (ax >= 0x38800000u) {
+        uint32_t r = ax - ((127u - 15u) << 23);
+        r = (r + 0x0FFFu + ((r >> 13) & 1u)) >> 13;
+        return (uint16_t)(sign | r);
+    }
+    if (ax <= 0x33000000u) return (uint16_t)sign;
+    uint32_t e = ax >> 23;
+    uint32_t mant = (ax & 0x7FFFFFu) | 0x800000u;
+    uint32_t shift = 126u - e;
+    uint32_t m = mant >> shift;
+    uint32_t rem = mant & ((1u << shift) - 1u);
+    uint32_t half = 1u << (shift - 1u);
+    if (rem > half || (rem == half && (m & 1u))) ++m;
+    return (uint16_t)(sign | m);
+}
+
+/* bf16lo, kernels/llm_matvec.cl:407. */
+float xo_bf16_to_fp32(uint32_t h) { return as_float((h & 0xFFFFu) << 16); }
+
+/* ------------------------------------------------------------------ */
+/* int4 matvec                                                          */
+/* ------------------------------------------------------------------ */
+
+/* q4dot8, kernels/llm_matvec.cl:54-65. */
+float xo_q4dot8(uint32_t w, const float* v) {
+    float s;
+    s  = v[0] * ((float)((w      ) & 15u) - 8.0f);
+    s += v[1] * ((float)((w >>  4) & 15u) - 8.0f);
+    s += v[2] * ((float)((w >>  8) & 15u) - 8.0f);
+    s += v[3] * ((float)((w >> 12) & 15u) - 8.0f);
+    s += v[4] * ((float)((w >> 16) & 15u) - 8.0f);
+    s += v[5] * ((float)((w >> 20) & 15u) - 8.0f);
+    s += v[6] * ((float)((w >> 24) & 15u) - 8.0f);
+    s += v[7] * ((float)((w >> 28) & 15u) - 8.0f);
+    return s;
+}
+
+/* q4dot32, kernels/llm_matvec.cl:68-72. */
+float xo_q4dot32(const uint32_t* w4, const float* v) {
+    return xo_q4dot8(w4[0], v) + xo_q4dot8(w4[1], v + 8) +
+           xo_q4dot8(w4[2], v + 16) + xo_q4dot8(w4[3], v + 24);
+}
+
+/* Scale of (block b, column j). fp16 / bf16 quad planes follow the Km4Bf16
+ * arrangement sc[(b/4)*cols + j] holding blocks 4q..4q+3 (decode.hpp:369-370,
+ * llm_matvec.cl:412-419); fp32 is [b][col] (llm_matvec.cl:187-200). */
+float xo_scale_at(const void* sc, int fmt, uint32_t cols, uint32_t b, uint32_t j) {
+    if (fmt == 2) return ((const float*)sc)[(size_t)b * cols + j];
+    uint32_t h = ((const uint16_t*)sc)[((size_t)(b / 4) * cols + j) * 4 + (b % 4)];
+    return fmt == 0 ? xo_fp16_to_fp32(h) : xo_bf16_to_fp32(h);
+}
+
+/* part[c] = q4dot32(block of column c) for the 64 columns of one KM4 group
+ * block: the reference order per column, vectorisable across columns. */
+static void block_dot64(float* part, const uint32_t* blk, const float* v) {
+    float d[4][64];
+    for (int comp = 0; comp < 4; ++comp) {
+        const float* vv = v + 8 * comp;
+        float* s = d[comp];
+        for (int c = 0; c < 64; ++c)
+            s[c] = vv[0] * ((float)(blk[4 * c + comp] & 15u) - 8.0f);
+        for (int i = 1; i < 8; ++i)
+            for (int c = 0; c < 64; ++c)
+                s[c] += vv[i] * ((float)((blk[4 * c + comp] >> (4 * i)) & 15u) - 8.0f);
+    }
+    for (int c = 0; c < 64; ++c) part[c] = ((d[0][c] + d[1][c]) + d[2][c]) + d[3][c];
+}
+
+/* mv_km4, kernels/llm_matvec.cl:187-200 (acc += q4dot32 * scale per block),
+ * over a block range of one group; acc carried by the caller. */
+static void km4_group(float* acc, const float* in, const uint32_t* wq, const void* sc, int fmt,
+                      uint32_t nblk, uint32_t cols, uint32_t g, uint32_t b0, uint32_t b1) {
+    float part[64];
+    for (uint32_t b = b0; b < b1; ++b) {
+        block_dot64(part, wq + ((size_t)g * nblk + b) * 256, in + (size_t)b * 32);
+        for (int c = 0; c < 64; ++c) acc[c] += part[c] * xo_scale_at(sc, fmt, cols, b, g * 64 + c);
+    }
+}
+
+void xo_mv_km4(float* out, const float* in, const uint32_t* wq, const void* sc, int fmt,
+               uint32_t rows, uint32_t cols) {
+    const uint32_t nblk = rows / 32, G = cols / 64;
+#pragma omp parallel for schedule(static) num_threads(nthreads())
+    for (int64_t g = 0; g < (int64_t)G; ++g) {
+        float acc[64] = {0};
+        km4_group(acc, in, wq, sc, fmt, nblk, cols, (uint32_t)g, 0, nblk);
+        memcpy(out + g * 64, acc, sizeof acc);
+    }
+}
+
+/* mv_km4_bs + km4_quad, kernels/llm_matvec.cl:412-434: a quad of scaled
+ * block dots is summed first, then added to acc. */
+void xo_mv_km4_bs(float* out, const float* in, const uint32_t* wq, const void* sc, int fmt,
+                  uint32_t rows, uint32_t cols) {
+    const uint32_t nblk = rows / 32, G = cols / 64, nq = nblk / 4;
+#pragma omp parallel for schedule(static) num_threads(nthreads())
+    for (int64_t g = 0; g < (int64_t)G; ++g) {
+        float acc[64] = {0}, a[64], part[64];
+        for (uint32_t q = 0; q < nq; ++q) {
+            for (uint32_t i = 0; i < 4; ++i) {
+                const uint32_t b = q * 4 + i;
+                block_dot64(part, wq + ((size_t)g * nblk + b) * 256, in + (size_t)b * 32);
+                for (int c = 0; c < 64; ++c) {
+                    const float p = part[c] * xo_scale_at(sc, fmt, cols, b, (uint32_t)g * 64 + c);
+                    a[c] = i == 0 ? p : a[c] + p;
+                }
+            }
+            for (int c = 0; c < 64; ++c) acc[c] += a[c];
+        }
+        memcpy(out + g * 64, acc, sizeof acc);
+    }
+}
+
+/* mv_km4_split, kernels/llm_matvec.cl:339-356: block ranges
+ * per = ceil(nblk/split), partial[p*cols + j]. */
+void xo_mv_km4_split(float* partial, const float* in, const uint32_t* wq, const void* sc,
+                     int fmt, uint32_t rows, uint32_t cols, uint32_t split) {
+    const uint32_t nblk = rows / 32, G = cols / 64;
+    const uint32_t per = (nblk + split - 1u) / split;
+#pragma omp parallel for schedule(static) num_threads(nthreads())
+    for (int64_t t = 0; t < (int64_t)G * split; ++t) {
+        const uint32_t g = (uint32_t)(t % G), p = (uint32_t)(t / G);
+        const uint32_t s0 = p * per, s1 = s0 + per < nblk ? s0 + per : nblk;
+        float acc[64] = {0};
+        if (s0 < nblk) km4_group(acc, in, wq, sc, fmt, nblk, cols, g, s0, s1);
+        memcpy(partial + (size_t)p * cols + (size_t)g * 64, acc, sizeof acc);
+    }
+}
+
+/* mv_reduce, kernels/llm_matvec.cl:128-135. */
+void xo_mv_reduce(float* out, const float* partial, uint32_t cols, uint32_t split) {
+    for (uint32_t j = 0; j < cols; ++j) {
+        float acc = 0.0f;
+        for (uint32_t p = 0; p < split; ++p) acc += partial[(size_t)p * cols + j];
+        out[j] = acc;
+    }
+}
+
+/* matvec_q4 (COL layout), kernels/llm.cl:488-513: the reference's gold. */
+void xo_matvec_q4_col(float* out, const float* in, const uint32_t* wq, const float* scale,
+                      uint32_t rows, uint32_t cols) {
+    const uint32_t nblk = rows / 32;
+#pragma omp parallel for schedule(static) num_threads(nthreads())
+    for (int64_t jj = 0; jj < (int64_t)cols; ++jj) {
+        const uint32_t j = (uint32_t)jj;
+        const uint32_t shift = (j & 7u) * 4u;
+        float acc = 0.0f;
+        for (uint32_t b = 0; b < nblk; ++b) {
+            const float s = scale[(size_t)b * cols + j];
+            float part = 0.0f;
+            for (uint32_t t = 0; t < 32; ++t) {
+                const uint32_t k = b * 32 + t;
+                const uint32_t word = wq[((size_t)k * cols + j) >> 3];
+                const float wv = (float)((word >> shift) & 0x0Fu) - 8.0f;
+                part += in[k] * wv;
+            }
+            acc += part * s;
+        }
+        out[j] = acc;
+    }
+}
+
+/* nib(k, j), examples/llm/matvec_bench.cpp:45-55. */
+uint32_t xo_nib_hash(uint32_t k, uint32_t j) {
+    uint32_t h = k * 2654435761u ^ (j + 0x9e3779b9u) * 2246822519u;
+    h ^= h >> 15;
+    h *= 2654435761u;
+    h ^= h >> 13;
+    return h & 15u;
+}
+
+/* pack_km4, matvec_bench.cpp:88-99. */
+void xo_pack_km4_hash(uint32_t* wq, uint32_t rows, uint32_t cols) {
+    const size_t nblk = rows / 32;
+    memset(wq, 0, (size_t)rows * cols / 2);
+    for (uint32_t j = 0; j < cols; ++j) {
+        const size_t base = ((size_t)(j / 64) * nblk * 64 + (j % 64)) * 4;
+        for (uint32_t k = 0; k < rows; ++k)
+            wq[base + (size_t)(k / 32) * 64 * 4 + ((k >> 3) & 3u)] |=
+                xo_nib_hash(k, j) << ((k & 7u) * 4u);
+    }
+}
+
+/* pack_col, matvec_bench.cpp:58-64. */
+void xo_pack_col_hash(uint32_t* wq, uint32_t rows, uint32_t cols) {
+    memset(wq, 0, (size_t)rows * cols / 2);
+    for (uint32_t k = 0; k < rows; ++k)
+        for (uint32_t j = 0; j < cols; ++j)
+            wq[((size_t)k * cols + j) >> 3] |= xo_nib_hash(k, j) << ((j & 7u) * 4u);
+}
+
+/* KM4 unpack, decode.hpp:46-48: out[k*cols + j] = nibble - 8. */
+void xo_unpack_km4(int8_t* out, const uint32_t* wq, uint32_t rows, uint32_t cols) {
+    const size_t nblk = rows / 32;
+    for (uint32_t j = 0; j < cols; ++j) {
+        const size_t base = ((size_t)(j / 64) * nblk * 64 + (j % 64)) * 4;
+        for (uint32_t k = 0; k < rows; ++k) {
+            const uint32_t w = wq[base + (size_t)(k / 32) * 256 + ((k >> 3) & 3u)];
+            out[(size_t)k * cols + j] = (int8_t)((int)((w >> ((k & 7u) * 4u)) & 15u) - 8);
+        }
+    }
+}
+
+/* ------------------------------------------------------------------ */
+/* Transformer ops (kernels/llm_transformer.cl)                         */
+/* ------------------------------------------------------------------ */
+
+static float rsqrt_ref(float x) { return 1.0f / sqrtf(x); }
+
+/* rmsnorm_sumsq, llm_transformer.cl:96-103. */
+void xo_rmsnorm_sumsq(float* partial, const float* in, uint32_t n, uint32_t nparts) {
+    for (uint32_t p = 0; p < nparts; ++p) {
+        float acc = 0.0f;
+        for (uint32_t k = p; k < n; k += nparts) acc += in[k] * in[k];
+        partial[p] = acc;
+    }
+}
+
+/* rmsnorm_apply_gemma, llm_transformer.cl:106-116. */
+void xo_rmsnorm_apply_gemma(float* out, const float* in, const float* w, const float* partial,
+                            uint32_t n, uint32_t nparts, float eps) {
+    float ss = 0.0f;
+    for (uint32_t p = 0; p < nparts; ++p) ss += partial[p];
+    const float scale = rsqrt_ref(ss / (float)n + eps);
+    for (uint32_t i = 0; i < n; ++i) out[i] = in[i] * scale * (1.0f + w[i]);
+}
+
+void xo_rmsnorm_gemma2(float* out, const float* in, const float* w, uint32_t n,
+                       uint32_t nparts, float eps) {
+    float partial[1024];
+    if (nparts > 1024) nparts = 1024;
+    xo_rmsnorm_sumsq(partial, in, n, nparts);
+    xo_rmsnorm_apply_gemma(out, in, w, partial, n, nparts, eps);
+}
+
+/* rmsnorm_heads_gemma, llm_transformer.cl:122-134. */
+void xo_rmsnorm_heads_gemma(float* out, const float* in, const float* w, uint32_t n_heads,
+                            uint32_t head_dim, float eps) {
+    for (uint32_t h = 0; h < n_heads; ++h) {
+        const uint32_t base = h * head_dim;
+        float ss = 0.0f;
+        for (uint32_t k = 0; k < head_dim; ++k) ss += in[base + k] * in[base + k];
+        const float scale = rsqrt_ref(ss / (float)head_dim + eps);
+        for (uint32_t d = 0; d < head_dim; ++d)
+            out[base + d] = in[base + d] * scale * (1.0f + w[d]);
+    }
+}
+
+/* rope, llm_transformer.cl:158-179 (rotate-half, angle via exp2/log2). */
+void xo_rope(float* x, uint32_t n_heads, uint32_t head_dim, uint32_t pos, float theta) {
+    const uint32_t half_dim = head_dim >> 1;
+    for (uint32_t h = 0; h < n_heads; ++h)
+        for (uint32_t d = 0; d < half_dim; ++d) {
+            const uint32_t base = h * head_dim + d;
+            const float frac = (float)(2u * d) / (float)head_dim;
+            const float inv = exp2f(-log2f(theta) * frac);
+            const float ang = (float)pos * inv;
+            const float c = cosf(ang), s = sinf(ang);
+            const float lo = x[base], hi = x[base + half_dim];
+            x[base] = lo * c - hi * s;
+            x[base + half_dim] = lo * s + hi * c;
+        }
+}
+
+/* tanh_approx + geglu, llm_transformer.cl:213-231. */
+static float tanh_approx(float z) {
+    z = fminf(fmaxf(z, -10.0f), 10.0f);
+    const float e = expf(-2.0f * z);
+    return (1.0f - e) / (1.0f + e);
+}
+
+void xo_geglu(float* out, const float* gate, const float* up, uint32_t n) {
+    for (uint32_t i = 0; i < n; ++i) {
+        const float g = gate[i];
+        const float inner = 0.7978845608028654f * (g + 0.044715f * g * g * g);
+        const float gelu = 0.5f * g * (1.0f + tanh_approx(inner));
+        out[i] = gelu * up[i];
+    }
+}
+
+/* add_residual, llm_transformer.cl:564-568. */
+void xo_add_residual(float* x, const float* y, uint32_t n) {
+    for (uint32_t i = 0; i < n; ++i) x[i] += y[i];
+}
+
+/* kv_append, llm_transformer.cl:590-595, into an fp16 cache. */
+void xo_kv_append_f16(uint16_t* cache, const float* src, uint32_t n, uint32_t pos) {
+    for (uint32_t i = 0; i < n; ++i) cache[(size_t)pos * n + i] = xo_fp32_to_fp16(src[i]);
+}
+
+/* attention_scores, llm_transformer.cl:287-305. */
+void xo_attention_scores(float* scores, const float* q, const float* kcache, uint32_t n_heads,
+                         uint32_t kv_heads, uint32_t head_dim, uint32_t span, float scale,
+                         uint32_t kv_start) {
+    const uint32_t group = n_heads / kv_heads;
+    for (uint32_t h = 0; h < n_heads; ++h)
+        for (uint32_t j = 0; j < span; ++j) {
+            const uint32_t kvh = h / group;
+            const size_t qb = (size_t)h * head_dim;
+            const size_t kb = ((size_t)(kv_start + j) * kv_heads + kvh) * head_dim;
+            float acc = 0.0f;
+            for (uint32_t d = 0; d < head_dim; ++d) acc += q[qb + d] * kcache[kb + d];
+            scores[(size_t)h * span + j] = acc * scale;
+        }
+}
+
+/* softmax_rows, llm_transformer.cl:318-335. */
+void xo_softmax_rows(float* x, uint32_t n_rows, uint32_t n_cols) {
+    for (uint32_t r = 0; r < n_rows; ++r) {
+        float* row = x + (size_t)r * n_cols;
+        float m = -INFINITY;
+        for (uint32_t j = 0; j < n_cols; ++j) m = fmaxf(m, row[j]);
+        float sum = 0.0f;
+        for (uint32_t j = 0; j < n_cols; ++j) {
+            const float e = expf(row[j] - m);
+            row[j] = e;
+            sum += e;
+        }
+        const float inv = 1.0f / sum;
+        for (uint32_t j = 0; j < n_cols; ++j) row[j] *= inv;
+    }
+}
+
+/* attention_apply, llm_transformer.cl:478-497. */
+void xo_attention_apply(float* out, const float* probs, const float* vcache, uint32_t n_heads,
+                        uint32_t kv_heads, uint32_t head_dim, uint32_t span, uint32_t kv_start) {
+    const uint32_t group = n_heads / kv_heads;
+    const uint32_t vstride = kv_heads * head_dim;
+    for (uint32_t h = 0; h < n_heads; ++h)
+        for (uint32_t d = 0; d < head_dim; ++d) {
+            const uint32_t kvh = h / group;
+            const size_t pb = (size_t)h * span;
+            const size_t vb = ((size_t)kv_start * kv_heads + kvh) * head_dim + d;
+            float acc = 0.0f;
+            for (uint32_t j = 0; j < span; ++j) acc += probs[pb + j] * vcache[vb + (size_t)j * vstride];
+            out[(size_t)h * head_dim + d] = acc;
+        }
+}
+
+void xo_attention_f16(float* out, const float* q, const uint16_t* kcache, const uint16_t* vcache,
+                      uint32_t n_heads, uint32_t kv_heads, uint32_t head_dim, uint32_t span,
+                      uint32_t kv_start, float scale) {
+    const size_t row = (size_t)kv_heads * head_dim;
+    const size_t n = (size_t)span * row;
+    float* k = (float*)malloc(n * sizeof(float));
+    float* v = (float*)malloc(n * sizeof(float));
+    float* sc = (float*)malloc((size_t)n_heads * span * sizeof(float));
+    for (size_t i = 0; i < n; ++i) {
+        k[i] = xo_fp16_to_fp32(kcache[(size_t)kv_start * row + i]);
+        v[i] = xo_fp16_to_fp32(vcache[(size_t)kv_start * row + i]);
+    }
+    xo_attention_scores(sc, q, k, n_heads, kv_heads, head_dim, span, scale, 0);
+    xo_softmax_rows(sc, n_heads, span);
+    xo_attention_apply(out, sc, v, n_heads, kv_heads, head_dim, span, 0);
+    free(k);
+    free(v);
+    free(sc);
+}
+
+/* ------------------------------------------------------------------ */
+/* Sampling (kernels/llm_sampling.cl, decode.cpp:1873-1917)             */
+/* ------------------------------------------------------------------ */
+
+/* argmax_partial, llm_sampling.cl:57-70: strict > keeps the earliest k. */
+void xo_argmax_partial(float* pval, uint32_t* pidx, const float* logits, uint32_t n,
+                       uint32_t nparts) {
+    for (uint32_t p = 0; p < nparts; ++p) {
+        float bv = -INFINITY;
+        uint32_t bi = 0u;
+        for (uint32_t k = p; k < n; k += nparts) {
+            const float v = logits[k];
+            if (v > bv) { bv = v; bi = k; }
+        }
+        pval[p] = bv;
+        pidx[p] = bi;
+    }
+}
+
+/* argmax_reduce, llm_sampling.cl:84-98: (value, index) lexicographic. */
+void xo_argmax_reduce(float* oval, uint32_t* oidx, const float* pval, const uint32_t* pidx,
+                      uint32_t n, uint32_t nparts) {
+    for (uint32_t p = 0; p < nparts; ++p) {
+        float bv = -INFINITY;
+        uint32_t bi = 0xFFFFFFFFu;
+        for (uint32_t k = p; k < n; k += nparts) {
+            const float v = pval[k];
+            const uint32_t e = pidx[k];
+            if (v > bv || (v == bv && e < bi)) { bv = v; bi = e; }
+        }
+        oval[p] = bv;
+        oidx[p] = bi;
+    }
+}
+
+/* argmax_final, llm_sampling.cl:106-123. */
+void xo_argmax_final(float* out, uint32_t* idx_out, const float* pval, const uint32_t* pidx,
+                     uint32_t nparts) {
+    float bv = -INFINITY;
+    uint32_t bi = 0xFFFFFFFFu;
+    for (uint32_t p = 0; p < nparts; ++p) {
+        const float v = pval[p];
+        const uint32_t k = pidx[p];
+        if (v > bv || (v == bv && k < bi)) { bv = v; bi = k; }
+    }
+    out[0] = (float)bi;
+    out[1] = bv;
+    idx_out[0] = bi;
+}
+
+/* vocab -> 4096 -> 64 -> 1 (decode.cpp:1766-1773, decode.hpp argmax_parts). */
+uint32_t xo_argmax_tree(const float* logits, uint32_t n, float* val_out) {
+    static float v1[4096], v2[64];
+    static uint32_t i1[4096], i2[64];
+    float out[2];
+    uint32_t idx;
+    xo_argmax_partial(v1, i1, logits, n, 4096);
+    xo_argmax_reduce(v2, i2, v1, i1, 4096, 64);
+    xo_argmax_final(out, &idx, v2, i2, 64);
+    if (val_out) *val_out = out[1];
+    return idx;
+}
+
+/* topk4_partial, llm_sampling.cl:318-347. */
+void xo_topk4_partial(float* cval, uint32_t* cidx, const float* x, uint32_t n, uint32_t nparts) {
+    for (uint32_t p = 0; p < nparts; ++p) {
+        float v0 = -INFINITY, v1 = -INFINITY, v2 = -INFINITY, v3 = -INFINITY;
+        uint32_t i0 = 0xFFFFFFFFu, i1 = 0xFFFFFFFFu, i2 = 0xFFFFFFFFu, i3 = 0xFFFFFFFFu;
+        for (uint32_t e = p; e < n; e += nparts) {
+            const float v = x[e];
+            if (!(v > v3)) continue;
+            if (v > v0) {
+                v3 = v2; i3 = i2; v2 = v1; i2 = i1; v1 = v0; i1 = i0; v0 = v; i0 = e;
+            } else if (v > v1) {
+                v3 = v2; i3 = i2; v2 = v1; i2 = i1; v1 = v; i1 = e;
+            } else if (v > v2) {
+                v3 = v2; i3 = i2; v2 = v; i2 = e;
+            } else {
+                v3 = v; i3 = e;
+            }
+        }
+        const uint32_t o = p * 4u;
+        cval[o + 0] = v0; cidx[o + 0] = i0;
+        cval[o + 1] = v1; cidx[o + 1] = i1;
+        cval[o + 2] = v2; cidx[o + 2] = i2;
+        cval[o + 3] = v3; cidx[o + 3] = i3;
+    }
+}
+
+/* topk_partial, llm_sampling.cl:257-281 (k <= 64). */
+void xo_topk_partial(float* cval, uint32_t* cidx, const float* x, uint32_t n, uint32_t nparts,
+                     uint32_t k) {
+    if (k > 64u) k = 64u;
+    for (uint32_t p = 0; p < nparts; ++p) {
+        float bv[64];
+        uint32_t bi[64];
+        for (uint32_t j = 0; j < k; ++j) { bv[j] = -INFINITY; bi[j] = 0xFFFFFFFFu; }
+        for (uint32_t e = p; e < n; e += nparts) {
+            const float v = x[e];
+            if (!(v > bv[k - 1u])) continue;
+            uint32_t j = k - 1u;
+            while (j > 0u && v > bv[j - 1u]) {
+                bv[j] = bv[j - 1u];
+                bi[j] = bi[j - 1u];
+                --j;
+            }
+            bv[j] = v;
+            bi[j] = e;
+        }
+        for (uint32_t j = 0; j < k; ++j) {
+            cval[p * k + j] = bv[j];
+            cidx[p * k + j] = bi[j];
+        }
+    }
+}
+
+/* topk_rank_select, llm_sampling.cl:349-369. */
+void xo_topk_rank_select(float* oval, uint32_t* oidx, const float* cval, const uint32_t* cidx,
+                         uint32_t ncand, uint32_t k) {
+    for (uint32_t i = 0; i < ncand; ++i) {
+        const float v = cval[i];
+        const uint32_t d = cidx[i];
+        if (d == 0xFFFFFFFFu) continue;
+        uint32_t rank = 0u;
+        for (uint32_t j = 0; j < ncand; ++j) {
+            const float w = cval[j];
+            const uint32_t e = cidx[j];
+            if (e == 0xFFFFFFFFu) continue;
+            if (w > v || (w == v && e < d)) ++rank;
+        }
+        if (rank < k) { oval[rank] = v; oidx[rank] = d; }
+    }
+}
+
+/* topp_cutoff, llm_sampling.cl:399-415. */
+void xo_topp_cutoff(float* w, uint32_t k, float p) {
+    float total = 0.0f;
+    for (uint32_t j = 0; j < k; ++j) total += w[j];
+    if (!(total > 0.0f)) return;
+    float cum = 0.0f;
+    for (uint32_t j = 0; j < k; ++j) {
+        if (cum >= p * total) w[j] = 0.0f;
+        else cum += w[j];
+    }
+}
+
+/* multinomial_sample, llm_sampling.cl:424-446. */
+void xo_multinomial_sample(float* out, uint32_t* idx_out, const float* w, const uint32_t* idx,
+                           uint32_t k, float u) {
+    float total = 0.0f;
+    for (uint32_t j = 0; j < k; ++j) total += w[j];
+    const float target = u * total;
+    float cum = 0.0f;
+    uint32_t chosen = 0u;
+    float cw = 0.0f;
+    for (uint32_t j = 0; j < k; ++j) {
+        cum += w[j];
+        if (w[j] > 0.0f) { chosen = idx[j]; cw = w[j]; }
+        if (cum > target) break;
+    }
+    out[0] = (float)chosen;
+    out[1] = cw;
+    idx_out[0] = chosen;
+}
+
+/* Philox4x32-10 (Salmon et al., SC'11). */
+void xo_philox4x32_10(const uint32_t ctr[4], const uint32_t key[2], uint32_t out[4]) {
+    uint32_t c0 = ctr[0], c1 = ctr[1], c2 = ctr[2], c3 = ctr[3], k0 = key[0], k1 = key[1];
+    for (int r = 0; r < 10; ++r) {
+        if (r) { k0 += 0x9E3779B9u; k1 += 0xBB67AE85u; }
+        const uint64_t p0 = (uint64_t)0xD2511F53u * c0, p1 = (uint64_t)0xCD9E8D57u * c2;
+        const uint32_t n0 = (uint32_t)(p1 >> 32) ^ c1 ^ k0;
+        const uint32_t n2 = (uint32_t)(p0 >> 32) ^ c3 ^ k1;
+        c0 = n0; c1 = (uint32_t)p1; c2 = n2; c3 = (uint32_t)p0;
+    }
+    out[0] = c0; out[1] = c1; out[2] = c2; out[3] = c3;
+}
+
+double xo_philox_uniform(uint32_t seed, uint32_t seq, uint32_t step) {
+    const uint32_t c[4] = {step, 0u, 0u, 0u}, k[2] = {seed, seq};
+    uint32_t o[4];
+    xo_philox4x32_10(c, k, o);
+    const uint64_t m = ((uint64_t)o[0] << 21) | (o[1] >> 11);
+    return (double)m * (1.0 / 9007199254740992.0);
+}
+
+static int better(float av, uint32_t ai, float bv, uint32_t bi) {
+    return av > bv || (av == bv && ai < bi);
+}
+
+/* Insertion sort by (value desc, index asc): n <= a few hundred here. */
+static void sort_cand(float* v, uint32_t* ix, uint32_t n) {
+    for (uint32_t i = 1; i < n; ++i) {
+        const float cv = v[i];
+        const uint32_t ci = ix[i];
+        uint32_t j = i;
+        while (j > 0 && better(cv, ci, v[j - 1], ix[j - 1])) {
+            v[j] = v[j - 1];
+            ix[j] = ix[j - 1];
+            --j;
+        }
+        v[j] = cv;
+        ix[j] = ci;
+    }
+}
+
+/* DecodeSession::draw, decode.cpp:1873-1917. The top-k selection keeps the
+ * reference's set (nth_element by (value desc, index asc)); the kept set is
+ * then walked in that sorted order, where the reference walks nth_element's
+ * unspecified order unless top-p sorts it. */
+uint32_t xo_draw(float* val, uint32_t* idx, uint32_t n, float temperature, uint32_t top_k,
+                 float top_p, double u) {
+    if (n == 0) return 0;
+    const float t = temperature > 0.0f ? temperature : 1.0f;
+    sort_cand(val, idx, n);
+    const uint32_t k = top_k ? (top_k < n ? top_k : n) : n;
+    n = k;
+    float maxl = -INFINITY;
+    for (uint32_t i = 0; i < n; ++i) maxl = fmaxf(maxl, val[i]);
+    double sum = 0;
+    for (uint32_t i = 0; i < n; ++i) {
+        val[i] = expf((val[i] - maxl) / t);
+        sum += val[i];
+    }
+    if (top_p > 0.0f && top_p < 1.0f && sum > 0) {
+        double acc = 0, cut = top_p * sum;
+        uint32_t keep = 0;
+        for (; keep < n; ++keep) {
+            acc += val[keep];
+            if (acc >= cut) break;
+        }
+        n = n < keep + 1 ? n : keep + 1;
+        sum = 0;
+        for (uint32_t i = 0; i < n; ++i) sum += val[i];
+    }
+    double r = u * sum;
+    for (uint32_t i = 0; i < n; ++i) {
+        r -= val[i];
+        if (r <= 0) return idx[i];
+    }
+    return idx[n - 1];
+}
+
+/* ------------------------------------------------------------------ */
+/* Full decode step                                                     */
+/* ------------------------------------------------------------------ */
+
+static void mv(float* out, const float* in, const xo_qweight* w) {
+    xo_mv_km4(out, in, w->wq, w->sc, 0, w->rows, w->cols);
+}
+
+void xo_embed(float* x, const xo_model* m, uint32_t token) {
+    const xo_qweight* e = &m->lm_head;
+    const uint32_t nblk = e->rows / 32;
+    const size_t base = ((size_t)(token / 64) * nblk * 64 + (token % 64)) * 4;
+    const float sc = sqrtf((float)m->hidden);
+    for (uint32_t k = 0; k < e->rows; ++k) {
+        const uint32_t w = e->wq[base + (size_t)(k / 32) * 256 + ((k >> 3) & 3u)];
+        const float q = (float)((int)((w >> ((k & 7u) * 4u)) & 15u) - 8);
+        const float v = q * xo_scale_at(e->sc, 0, e->cols, k / 32, token);
+        x[k] = v * sc;
+    }
+}
+
+static float* g_x = NULL;   /* residual stream carried between calls */
+static uint32_t g_x_n = 0;
+
+int xo_forward(const xo_model* m, uint32_t token, uint32_t pos, float* logits, int threads) {
+    const uint32_t H = m->hidden, F = m->ffn, hd = m->head_dim;
+    const uint32_t qd = m->n_heads * hd, kvd = m->n_kv_heads * hd;
+    const uint32_t seq_len = pos + 1;
+    const float eps = m->rms_eps;
+    const float ascale = 1.0f / sqrtf((float)hd);
+    if (pos >= m->max_seq || token >= m->vocab) return -1;
+    g_threads = threads;
+
+    float* x = (float*)malloc(H * sizeof(float));
+    float* xb = (float*)malloc((H > qd ? H : qd) * sizeof(float));
+    float* xb2 = (float*)malloc(H * sizeof(float));
+    float* q_raw = (float*)malloc(qd * sizeof(float));
+    float* q = (float*)malloc(qd * sizeof(float));
+    float* k_raw = (float*)malloc(kvd * sizeof(float));
+    float* k = (float*)malloc(kvd * sizeof(float));
+    float* v = (float*)malloc(kvd * sizeof(float));
+    float* att = (float*)malloc(qd * sizeof(float));
+    float* g = (float*)malloc(F * sizeof(float));
+    float* u = (float*)malloc(F * sizeof(float));
+    float* hb = (float*)malloc(F * sizeof(float));
+
+    xo_embed(x, m, token);   /* write_embedding, decode.cpp:1618-1627 */
+    for (uint32_t l = 0; l < m->n_layers; ++l) {
+        const xo_layer* w = &m->layers[l];
+        const int global = m->global_every == 0 || (l + 1) % m->global_every == 0;
+        const float theta = global ? m->theta_global : m->theta_local;
+        const uint32_t win = global ? 0u : m->sliding_window;
+        const uint32_t kv_start = (win == 0 || seq_len <= win) ? 0u : seq_len - win;
+        const uint32_t span = seq_len - kv_start;
+
+        xo_rmsnorm_gemma2(xb, x, w->attn_norm, H, 64, eps);
+        mv(q_raw, xb, &w->q);
+        mv(k_raw, xb, &w->k);
+        mv(v, xb, &w->v);
+        xo_rmsnorm_heads_gemma(q, q_raw, w->q_norm, m->n_heads, hd, eps);
+        xo_rmsnorm_heads_gemma(k, k_raw, w->k_norm, m->n_kv_heads, hd, eps);
+        xo_rope(q, m->n_heads, hd, pos, theta);
+        xo_rope(k, m->n_kv_heads, hd, pos, theta);
+        xo_kv_append_f16(w->kcache, k, kvd, pos);
+        xo_kv_append_f16(w->vcache, v, kvd, pos);
+        xo_attention_f16(att, q, w->kcache, w->vcache, m->n_heads, m->n_kv_heads, hd, span,
+                         kv_start, ascale);
+        mv(xb, att, &w->o);
+        xo_rmsnorm_gemma2(xb2, xb, w->post_attn_norm, H, 64, eps);
+        xo_add_residual(x, xb2, H);
+
+        xo_rmsnorm_gemma2(xb, x, w->ffn_norm, H, 64, eps);
+        mv(g, xb, &w->gate);
+        mv(u, xb, &w->up);
+        xo_geglu(hb, g, u, F);
+        mv(xb, hb, &w->down);
+        xo_rmsnorm_gemma2(xb2, xb, w->post_ffn_norm, H, 64, eps);
+        xo_add_residual(x, xb2, H);
+    }
+    xo_rmsnorm_gemma2(xb, x, m->final_norm, H, 64, eps);
+    if (logits) mv(logits, xb, &m->lm_head);
+
+    if (g_x_n < H) {
+        free(g_x);
+        g_x = (float*)malloc(H * sizeof(float));
+        g_x_n = H;
+    }
+    memcpy(g_x, x, H * sizeof(float));
+    free(x); free(xb); free(xb2); free(q_raw); free(q); free(k_raw); free(k); free(v);
+    free(att); free(g); free(u); free(hb);
+    return 0;
+}
+
+int xo_generate_greedy(const xo_model* m, const uint32_t* prompt, uint32_t n_prompt,
+                       uint32_t n_gen, uint32_t* out, int threads) {
+    if (n_prompt == 0) return -1;
+    float* logits = (float*)malloc((size_t)m->vocab * sizeof(float));
+    uint32_t pos = 0;
+    int rc = 0;
+    for (uint32_t i = 0; i < n_prompt && rc == 0; ++i, ++pos)
+        rc = xo_forward(m, prompt[i], pos, i + 1 == n_prompt ? logits : NULL, threads);
+    for (uint32_t s = 0; s < n_gen && rc == 0; ++s, ++pos) {
+        const uint32_t tok = xo_argmax_tree(logits, m->vocab, NULL);   /* sample first */
+        out[s] = tok;
+        rc = xo_forward(m, tok, pos, logits, threads);
+    }
+    free(logits);
+    return rc;
+}

@@ -1,0 +1,160 @@
+/*
+ * oracle.h — CPU restatement of the reference (badnikhil/Xpose "Vulkore")
+ * Gemma-3 decode arithmetic. TEST INFRASTRUCTURE ONLY: tests/, the graft
+ * entry's smoke() and bench.py's cpu_baseline leg may load it, as the checker
+ * or the timed CPU baseline. The product (libxpose) never calls it.
+ *
+ * Every function follows the reference source line for line in its
+ * arithmetic (operation order, which products are rounded, tie rules); each
+ * cites the file:line it restates. Built with -ffp-contract=off so each
+ * written a*b+c rounds twice, as OpenCL C without contraction does.
+ *
+ * Pinning (what checks each function beyond restating it; tests/test_oracle.py):
+ *  xo_fp16_to_fp32          all 65536 patterns vs numpy float16 (exact)
+ *  xo_q4dot8/32, mv_*       nibble closed form; float64 brute force; COL gold
+ *                           == KM4 on the reference's nib() fixture
+ *                           (matvec_bench.cpp:45-55) at all six shapes
+ *  xo_rmsnorm_*             numpy closed form (rtol 1e-5)
+ *  xo_rope                  rotation invariants (norm kept, pos 0 identity,
+ *                           composition pos a then b == a+b)
+ *  xo_geglu                 numpy tanh-GELU
+ *  attention                numpy softmax(q.K)V, rows sum to 1, window
+ *                           negative control (kernel_tests.cpp:483-621)
+ *  argmax / topk            planted max 190037 (kernel_tests.cpp:695-711),
+ *                           ties -> lowest index (sampling_test.cpp:171-178),
+ *                           sort-based top-k with duplicates (:427-480)
+ *  topp / multinomial       known answers of sampling_test.cpp:537-607
+ *  xo_forward               numpy re-derivation of one layer; greedy token
+ *                           ids are pinned by this oracle only (parity
+ *                           unpinned against the reference itself: no
+ *                           reference-held end-to-end fixture exists).
+ */
+#ifndef XPOSE_ORACLE_H
+#define XPOSE_ORACLE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- scalar formats ---- */
+float    xo_fp16_to_fp32(uint32_t h);
+uint16_t xo_fp32_to_fp16(float f);
+float    xo_bf16_to_fp32(uint32_t h);
+
+/* ---- int4 matvec ---- */
+float xo_q4dot8(uint32_t w, const float* v);
+float xo_q4dot32(const uint32_t* w4, const float* v);
+/* scale_fmt: 0 fp16 quad plane, 1 bf16 quad plane, 2 fp32 [b][col]. */
+float xo_scale_at(const void* sc, int scale_fmt, uint32_t cols, uint32_t b, uint32_t j);
+void  xo_mv_km4(float* out, const float* in, const uint32_t* wq, const void* sc,
+                int scale_fmt, uint32_t rows, uint32_t cols);
+void  xo_mv_km4_bs(float* out, const float* in, const uint32_t* wq, const void* sc,
+                   int scale_fmt, uint32_t rows, uint32_t cols);
+void  xo_mv_km4_split(float* partial, const float* in, const uint32_t* wq, const void* sc,
+                      int scale_fmt, uint32_t rows, uint32_t cols, uint32_t split);
+void  xo_mv_reduce(float* out, const float* partial, uint32_t cols, uint32_t split);
+void  xo_matvec_q4_col(float* out, const float* in, const uint32_t* wq,
+                       const float* scale, uint32_t rows, uint32_t cols);
+uint32_t xo_nib_hash(uint32_t k, uint32_t j);
+void  xo_pack_km4_hash(uint32_t* wq, uint32_t rows, uint32_t cols);
+void  xo_pack_col_hash(uint32_t* wq, uint32_t rows, uint32_t cols);
+void  xo_unpack_km4(int8_t* out, const uint32_t* wq, uint32_t rows, uint32_t cols);
+
+/* ---- transformer ops ---- */
+void xo_rmsnorm_sumsq(float* partial, const float* in, uint32_t n, uint32_t nparts);
+void xo_rmsnorm_apply_gemma(float* out, const float* in, const float* w,
+                            const float* partial, uint32_t n, uint32_t nparts, float eps);
+void xo_rmsnorm_gemma2(float* out, const float* in, const float* w, uint32_t n,
+                       uint32_t nparts, float eps);
+void xo_rmsnorm_heads_gemma(float* out, const float* in, const float* w,
+                            uint32_t n_heads, uint32_t head_dim, float eps);
+void xo_rope(float* x, uint32_t n_heads, uint32_t head_dim, uint32_t pos, float theta);
+void xo_geglu(float* out, const float* gate, const float* up, uint32_t n);
+void xo_add_residual(float* x, const float* y, uint32_t n);
+void xo_kv_append_f16(uint16_t* cache, const float* src, uint32_t n, uint32_t pos);
+void xo_attention_scores(float* scores, const float* q, const float* kcache,
+                         uint32_t n_heads, uint32_t kv_heads, uint32_t head_dim,
+                         uint32_t span, float scale, uint32_t kv_start);
+void xo_softmax_rows(float* x, uint32_t n_rows, uint32_t n_cols);
+void xo_attention_apply(float* out, const float* probs, const float* vcache,
+                        uint32_t n_heads, uint32_t kv_heads, uint32_t head_dim,
+                        uint32_t span, uint32_t kv_start);
+/* scores -> softmax -> apply over fp16 caches (widened exactly). */
+void xo_attention_f16(float* out, const float* q, const uint16_t* kcache,
+                      const uint16_t* vcache, uint32_t n_heads, uint32_t kv_heads,
+                      uint32_t head_dim, uint32_t span, uint32_t kv_start, float scale);
+
+/* ---- sampling ---- */
+void xo_argmax_partial(float* pval, uint32_t* pidx, const float* logits, uint32_t n,
+                       uint32_t nparts);
+void xo_argmax_reduce(float* oval, uint32_t* oidx, const float* pval, const uint32_t* pidx,
+                      uint32_t n, uint32_t nparts);
+void xo_argmax_final(float* out, uint32_t* idx_out, const float* pval, const uint32_t* pidx,
+                     uint32_t nparts);
+/* The decode path's tree: n -> 4096 -> 64 -> 1. */
+uint32_t xo_argmax_tree(const float* logits, uint32_t n, float* val_out);
+void xo_topk4_partial(float* cval, uint32_t* cidx, const float* x, uint32_t n,
+                      uint32_t nparts);
+void xo_topk_partial(float* cval, uint32_t* cidx, const float* x, uint32_t n,
+                     uint32_t nparts, uint32_t k);
+void xo_topk_rank_select(float* oval, uint32_t* oidx, const float* cval,
+                         const uint32_t* cidx, uint32_t ncand, uint32_t k);
+void xo_topp_cutoff(float* w, uint32_t k, float p);
+void xo_multinomial_sample(float* out, uint32_t* idx_out, const float* w,
+                           const uint32_t* idx, uint32_t k, float u);
+/* Host draw (decode.cpp:1873-1917) over (value, index) candidates, modified
+ * in place; u in [0,1) replaces the reference's mt19937_64 draw. */
+uint32_t xo_draw(float* val, uint32_t* idx, uint32_t n, float temperature, uint32_t top_k,
+                 float top_p, double u);
+/* Philox-derived uniform for sequence `seq` at step `step` (53-bit, [0,1)). */
+double xo_philox_uniform(uint32_t seed, uint32_t seq, uint32_t step);
+void xo_philox4x32_10(const uint32_t ctr[4], const uint32_t key[2], uint32_t out[4]);
+
+/* ---- full decode step (record_token order, decode.cpp:1634-1780) ---- */
+typedef struct {
+    const uint32_t* wq;   /* KM4 nibble plane */
+    const uint16_t* sc;   /* fp16 quad scale plane */
+    uint32_t rows, cols;
+} xo_qweight;
+
+typedef struct {
+    xo_qweight q, k, v, o, gate, up, down;
+    const float* attn_norm;      /* all norm weights stored as multiplier - 1 */
+    const float* post_attn_norm;
+    const float* ffn_norm;
+    const float* post_ffn_norm;
+    const float* q_norm;
+    const float* k_norm;
+    uint16_t* kcache;            /* [max_seq][kv_heads*head_dim] fp16 */
+    uint16_t* vcache;
+} xo_layer;
+
+typedef struct {
+    uint32_t n_layers, hidden, ffn, n_heads, n_kv_heads, head_dim, vocab, max_seq;
+    uint32_t global_every, sliding_window;
+    float rms_eps, theta_global, theta_local;
+    const xo_layer* layers;
+    xo_qweight lm_head;          /* tied: rows = hidden, cols = vocab */
+    const float* final_norm;
+} xo_model;
+
+/* Embedding of `token`: column token of the tied table, dequantised, times
+ * sqrt(float(hidden)) (decode.cpp:1618-1627). */
+void xo_embed(float* x, const xo_model* m, uint32_t token);
+/* One forward pass at `pos` on `token`; appends K/V at pos. Writes vocab
+ * logits when logits != NULL (the lm_head is skipped otherwise). Uses
+ * `threads` OpenMP threads for the matvecs (0 = runtime default). */
+int xo_forward(const xo_model* m, uint32_t token, uint32_t pos, float* logits,
+               int threads);
+/* Greedy generation: prefill `n_prompt` ids from pos 0, then `n_gen`
+ * sample-first decode steps (decode.cpp:1790-1866). out receives n_gen ids. */
+int xo_generate_greedy(const xo_model* m, const uint32_t* prompt, uint32_t n_prompt,
+                       uint32_t n_gen, uint32_t* out, int threads);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

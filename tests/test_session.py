@@ -1,0 +1,316 @@
+"""The decode session (engine level): the token step of DecodeSession
+(examples/llm/decode.cpp:1634-1866) on the GPU against the oracle's
+xo_forward on the same packed weights, KV contents and token ids.
+
+Bars: greedy token ids bit-exact; logits within 1e-3
+relative (|d| <= 1e-3 * max|logits|); KV rows within one fp16 ulp.
+"""
+import numpy as np
+import pytest
+
+LOGIT_TOL = 1e-3
+
+
+def cfg_small(X, **kw):
+    base = dict(n_layers=6, vocab=32768, max_seq=1024)
+    base.update(kw)
+    return X.XpConfig.gemma3_1b(**base)
+
+
+def all_tensors(X, cfg, seed):
+    t = {}
+    for l in range(cfg.n_layers):
+        for m in X.MATRICES:
+            t[(l, m)] = X.synth_tensor(cfg, seed, l, m)
+            t[(l, m | X.T_SCALES)] = X.synth_tensor(cfg, seed, l, m | X.T_SCALES)
+        for n in X.NORMS:
+            t[(l, n)] = X.synth_tensor(cfg, seed, l, n)
+    for k in (X.T_LM_HEAD, X.T_LM_HEAD | X.T_SCALES, X.T_FINAL_NORM):
+        t[(-1, k)] = X.synth_tensor(cfg, seed, -1, k)
+    return t
+
+
+def make_pair(X, xo, cfg, seed=0x5EED0002):
+    t = all_tensors(X, cfg, seed)
+    sess = X.DecodeSession(cfg)
+    for (l, k), a in t.items():
+        sess.upload(l, k, a)
+    model = xo.OracleModel(cfg, lambda l, k: t[(l, k)])
+    return sess, model
+
+
+def logits_close(got, want):
+    err = np.abs(got.astype(np.float64) - want).max()
+    return err <= LOGIT_TOL * np.abs(want).max(), f"max_abs={err:.3e} max|want|={np.abs(want).max():.3e}"
+
+
+def top5(x):
+    return np.lexsort((np.arange(x.size), -x))[:5]
+
+
+# ---------------------------------------------------------------- CPU ----
+
+def test_weight_bytes_match_the_algorithmic_count(xh):
+    """Nibbles + fp16 scales of one Gemma-3-1B token = 562,360,320 B, the
+    figure the HBM roofline is priced on (reference: 536.3 MiB,
+    agent-docs/llm-inference.md:105)."""
+    X = xh
+    cfg = X.XpConfig.gemma3_1b()
+    total = 0
+    for l in range(cfg.n_layers):
+        for m in X.MATRICES:
+            total += X.tensor_bytes(cfg, l, m) + X.tensor_bytes(cfg, l, m | X.T_SCALES)
+    total += X.tensor_bytes(cfg, -1, X.T_LM_HEAD) + X.tensor_bytes(cfg, -1, X.T_LM_HEAD | X.T_SCALES)
+    assert total == 562_360_320
+    assert X.tensor_bytes(cfg, 0, X.T_GATE) == 1152 * 6912 // 2
+    assert X.tensor_bytes(cfg, 0, X.T_GATE | X.T_SCALES) == 36 * 6912 * 2
+
+
+def test_synth_tensor_is_deterministic(xh):
+    X = xh
+    cfg = cfg_small(X, n_layers=2)
+    a = X.synth_tensor(cfg, 5, 1, X.T_DOWN)
+    assert np.array_equal(a, X.synth_tensor(cfg, 5, 1, X.T_DOWN))
+    assert not np.array_equal(a, X.synth_tensor(cfg, 6, 1, X.T_DOWN))
+    n = X.synth_tensor(cfg, 5, 0, X.T_Q_NORM)
+    assert n.size == 256 and abs(n.mean()) < 0.03 and 0.07 < n.std() < 0.13
+
+
+def test_config_and_tensor_errors(xh):
+    X = xh
+    bad = X.XpConfig.gemma3_1b(head_dim=1024)
+    with pytest.raises(X.XposeError) as e:
+        X.DecodeSession(bad)
+    assert "head_dim" in str(e.value)
+    cfg = X.XpConfig.gemma3_1b()
+    with pytest.raises(X.XposeError):
+        X.tensor_bytes(cfg, 26, X.T_Q)
+    with pytest.raises(X.XposeError):
+        X.tensor_bytes(cfg, 0, X.T_LM_HEAD)
+
+
+def test_oracle_embedding_closed_form(xh, xo):
+    X = xh
+    cfg = cfg_small(X, n_layers=1, vocab=4096)
+    t = all_tensors(X, cfg, 11)
+    model = xo.OracleModel(cfg, lambda l, k: t[(l, k)])
+    import ctypes as C
+    tok = 3001
+    x = np.empty(cfg.hidden, np.float32)
+    xo.lib().xo_embed(x, C.byref(model.model), tok)
+    W = np.empty(cfg.hidden * cfg.vocab, np.int8)
+    xo.lib().xo_unpack_km4(W, t[(-1, X.T_LM_HEAD)], cfg.hidden, cfg.vocab)
+    W = W.reshape(cfg.hidden, cfg.vocab)
+    sc = t[(-1, X.T_LM_HEAD | X.T_SCALES)].reshape(cfg.hidden // 128, cfg.vocab, 4)
+    s = sc.transpose(0, 2, 1).reshape(cfg.hidden // 32, cfg.vocab).view(np.float16)
+    col = W[:, tok].astype(np.float32) * np.repeat(s[:, tok].astype(np.float32), 32)
+    assert np.array_equal(x, (col * np.float32(np.sqrt(np.float32(1152)))).astype(np.float32))
+
+
+def test_oracle_generate_matches_forward_loop(xh, xo):
+    """xo_generate_greedy == prefill + sample-first decode written out."""
+    X = xh
+    cfg = cfg_small(X, n_layers=2, vocab=4096, max_seq=64)
+    t = all_tensors(X, cfg, 12)
+    ids = xo.OracleModel(cfg, lambda l, k: t[(l, k)]).generate_greedy([5, 9, 3], 4)
+    m = xo.OracleModel(cfg, lambda l, k: t[(l, k)])
+    m.forward(5, 0, False)
+    m.forward(9, 1, False)
+    lg = m.forward(3, 2, True)
+    out = []
+    for pos in range(3, 7):
+        tok = xo.argmax_tree(lg)[0]
+        out.append(tok)
+        lg = m.forward(tok, pos, True)
+    assert list(ids) == out
+
+
+# ---------------------------------------------------------------- GPU ----
+
+@pytest.mark.gpu
+def test_gpu_one_layer_cfg2(xp, xo):
+    """one local Gemma-3-1B layer, 512 prior fp16 KV rows
+    ~ N(0,1), decode at position 512 (kv_start 1, span 512)."""
+    X = xp
+    print("case session one-layer cfg2", flush=True)
+    cfg = X.XpConfig.gemma3_1b(n_layers=1, max_seq=1024)
+    sess, model = make_pair(X, xo, cfg)
+    kvd = cfg.n_kv_heads * cfg.head_dim
+    k = X.synth_normal_f16(512 * kvd, 77, 1)
+    v = X.synth_normal_f16(512 * kvd, 77, 2)
+    sess.kv_upload(0, 0, 0, k)
+    sess.kv_upload(0, 1, 0, v)
+    model.kcache[0][:512 * kvd] = k
+    model.vcache[0][:512 * kvd] = v
+    sess.set_position(512)
+    sess.prefill([123456])
+    want = model.forward(123456, 512, True)
+    ok, msg = logits_close(sess.last_logits(), want)
+    assert ok, msg
+    for which, ref in ((0, model.kcache[0]), (1, model.vcache[0])):
+        row = sess.kv_download(0, which, 512, 1).astype(np.int32)
+        assert np.abs(row - ref[512 * kvd:513 * kvd].astype(np.int32)).max() <= 1
+        assert np.array_equal(sess.kv_download(0, which, 0, 512), ref[:512 * kvd])
+
+
+@pytest.mark.gpu
+def test_gpu_small_model_greedy(xp, xo):
+    X = xp
+    print("case session small greedy", flush=True)
+    cfg = cfg_small(X)
+    sess, model = make_pair(X, xo, cfg)
+    prompt = np.random.default_rng(4).integers(0, cfg.vocab, 32).astype(np.uint32)
+    want = model.generate_greedy(prompt, 24)
+    sess.prefill(prompt)
+    got = [sess.decode_step() for _ in range(24)]
+    assert list(want) == got
+    assert sess.position == 32 + 24
+
+
+@pytest.mark.gpu
+def test_gpu_small_model_logits_every_step(xp, xo):
+    X = xp
+    print("case session small logits", flush=True)
+    cfg = cfg_small(X, n_layers=7, vocab=16384)
+    sess, model = make_pair(X, xo, cfg)
+    prompt = [7, 1000, 16000, 3]
+    for i, t in enumerate(prompt[:-1]):
+        model.forward(t, i, False)
+    lg = model.forward(prompt[-1], len(prompt) - 1, True)
+    sess.prefill(prompt)
+    ok, msg = logits_close(sess.last_logits(), lg)
+    assert ok, msg
+    pos = len(prompt)
+    for step in range(12):
+        tok = sess.decode_step()
+        assert tok == xo.argmax_tree(lg)[0]
+        lg = model.forward(tok, pos, True)
+        got = sess.last_logits()
+        ok, msg = logits_close(got, lg)
+        assert ok, f"step {step}: {msg}"
+        assert np.array_equal(top5(got), top5(lg)), step
+        pos += 1
+
+
+@pytest.mark.gpu
+def test_gpu_decode_steps_equals_decode_step(xp, xo):
+    X = xp
+    print("case session decode_steps", flush=True)
+    cfg = cfg_small(X, n_layers=3)
+    t = all_tensors(X, cfg, 21)
+    a, b = X.DecodeSession(cfg), X.DecodeSession(cfg)
+    for (l, k), arr in t.items():
+        a.upload(l, k, arr)
+        b.upload(l, k, arr)
+    a.prefill([1, 2, 3])
+    b.prefill([1, 2, 3])
+    many = a.decode_steps(20)
+    one = [b.decode_step() for _ in range(20)]
+    assert list(many) == one
+    assert np.array_equal(a.last_logits().view(np.uint32), b.last_logits().view(np.uint32))
+
+
+@pytest.mark.gpu
+def test_gpu_full_model_greedy_cfg3(xp, xo):
+    """BASELINE config 3 (shortened): full Gemma-3-1B architecture, random
+    int4 weights, tied 262144 x 1152 table; prefill then greedy decode."""
+    X = xp
+    print("case session full model cfg3", flush=True)
+    cfg = X.XpConfig.gemma3_1b(max_seq=2048)
+    sess, model = make_pair(X, xo, cfg)
+    prompt = np.random.default_rng(32).integers(0, cfg.vocab, 8).astype(np.uint32)
+    for i, t in enumerate(prompt[:-1]):
+        model.forward(int(t), i, False, 16)
+    lg = model.forward(int(prompt[-1]), len(prompt) - 1, True, 16)
+    sess.prefill(prompt)
+    ok, msg = logits_close(sess.last_logits(), lg)
+    assert ok, msg
+    pos = len(prompt)
+    for step in range(6):
+        tok = sess.decode_step()
+        assert tok == xo.argmax_tree(lg)[0], step
+        lg = model.forward(tok, pos, True, 16)
+        ok, msg = logits_close(sess.last_logits(), lg)
+        assert ok, f"step {step}: {msg}"
+        pos += 1
+
+
+@pytest.mark.gpu
+def test_gpu_full_model_deep_context_cfg4(xp, xo):
+    """BASELINE config 4 (shortened): KV of all 26 layers pre-filled with fp16
+    N(0,1) to position 4096; decode from 4096 (global layers span 4097,
+    local layers the last 512)."""
+    X = xp
+    print("case session full model cfg4", flush=True)
+    cfg = X.XpConfig.gemma3_1b(max_seq=4160)
+    sess, model = make_pair(X, xo, cfg)
+    kvd = cfg.n_kv_heads * cfg.head_dim
+    for l in range(cfg.n_layers):
+        for which, cache in ((0, model.kcache), (1, model.vcache)):
+            rows = X.synth_normal_f16(4096 * kvd, 4096, 2 * l + which)
+            sess.kv_upload(l, which, 0, rows)
+            cache[l][:4096 * kvd] = rows
+    sess.set_position(4096)
+    sess.prefill([4242])
+    lg = model.forward(4242, 4096, True, 16)
+    ok, msg = logits_close(sess.last_logits(), lg)
+    assert ok, msg
+    pos = 4097
+    for step in range(3):
+        tok = sess.decode_step()
+        assert tok == xo.argmax_tree(lg)[0]
+        lg = model.forward(tok, pos, True, 16)
+        ok, msg = logits_close(sess.last_logits(), lg)
+        assert ok, f"step {step}: {msg}"
+        pos += 1
+
+
+@pytest.mark.gpu
+def test_gpu_temperature_sampling(xp, xo):
+    """Temperature 0.8 / top-k 64 / top-p 0.95 over the top-4-per-chain
+    harvest, Philox uniform per (sequence, step) (BASELINE config 5 draw)."""
+    X = xp
+    print("case session temperature", flush=True)
+    cfg = cfg_small(X, n_layers=4, sample_mode=1, temperature=0.8, top_k=64, top_p=0.95,
+                    seed=99, seq_id=3, topk_parts=1024)
+    sess, model = make_pair(X, xo, cfg)
+    prompt = [11, 22, 33]
+    for i, t in enumerate(prompt[:-1]):
+        model.forward(t, i, False)
+    lg = model.forward(prompt[-1], 2, True)
+    sess.prefill(prompt)
+    pos = 3
+    for step in range(16):
+        cv = np.empty(4096, np.float32)
+        ci = np.empty(4096, np.uint32)
+        xo.lib().xo_topk4_partial(cv, ci, lg, cfg.vocab, 1024)
+        gv, gi = sess.last_candidates()
+        assert np.array_equal(gi, ci), step          # same candidate set
+        keep = ci != 0xFFFFFFFF
+        u = xo.lib().xo_philox_uniform(99, 3, step)
+        want = xo.lib().xo_draw(cv[keep].copy(), ci[keep].copy(), int(keep.sum()), 0.8, 64,
+                                0.95, u)
+        tok = sess.decode_step()
+        assert tok == want, step
+        lg = model.forward(tok, pos, True)
+        pos += 1
+
+
+@pytest.mark.gpu
+def test_gpu_session_error_paths(xp):
+    X = xp
+    cfg = cfg_small(X, n_layers=1, max_seq=16)
+    s = X.DecodeSession(cfg)
+    s.synthesize(1)
+    with pytest.raises(X.XposeError) as e:
+        s.decode_step()
+    assert e.value.code == -4
+    with pytest.raises(X.XposeError):
+        s.prefill(list(range(17)))
+    with pytest.raises(X.XposeError):
+        s.prefill([cfg.vocab])
+    s.prefill(list(range(15)))
+    s.decode_step()
+    with pytest.raises(X.XposeError) as e:
+        s.decode_step()
+    assert "full" in str(e.value)

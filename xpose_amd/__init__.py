@@ -1,0 +1,405 @@
+"""xpose_amd — MI355X (gfx950) Gemma-3 int4 decode hot path.
+
+Python binding of the C ABI in include/xpose.h (libxpose.so, built in-tree by
+xpose_amd/build.py). The binding is ctypes + numpy only: device memory and
+streams come from the library itself, so no second HIP runtime is loaded.
+Loading fails loudly if the shared object is missing; there is no CPU
+fallback for any entry point.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "libxpose.so")
+
+XP_SCALE_F16_QUAD = 0
+XP_SCALE_BF16_QUAD = 1
+XP_SCALE_F32 = 2
+
+_lib = None
+
+# Tensor ids (enum xp_tensor in include/xpose.h).
+T_Q, T_K, T_V, T_O, T_GATE, T_UP, T_DOWN = range(7)
+T_ATTN_NORM, T_POST_ATTN_NORM, T_FFN_NORM, T_POST_FFN_NORM, T_Q_NORM, T_K_NORM = range(16, 22)
+T_LM_HEAD, T_FINAL_NORM = 32, 33
+T_SCALES = 0x100
+MATRICES = (T_Q, T_K, T_V, T_O, T_GATE, T_UP, T_DOWN)
+NORMS = (T_ATTN_NORM, T_POST_ATTN_NORM, T_FFN_NORM, T_POST_FFN_NORM, T_Q_NORM, T_K_NORM)
+
+
+class XpConfig(C.Structure):
+    """xp_config (include/xpose.h), the reference's DecodeConfig + Sampling."""
+    _fields_ = [(n, C.c_uint32) for n in ("n_layers", "hidden", "ffn", "n_heads", "n_kv_heads",
+                                          "head_dim", "vocab", "max_seq", "global_every",
+                                          "sliding_window")] + \
+               [(n, C.c_float) for n in ("rms_eps", "rope_theta_global", "rope_theta_local",
+                                         "embed_scale", "attn_scale")] + \
+               [("scale_fmt", C.c_int32), ("sample_mode", C.c_int32),
+                ("temperature", C.c_float), ("top_k", C.c_uint32), ("top_p", C.c_float),
+                ("seed", C.c_uint32), ("seq_id", C.c_uint32), ("topk_parts", C.c_uint32)]
+
+    @classmethod
+    def gemma3_1b(cls, **overrides) -> "XpConfig":
+        c = cls()
+        lib().xp_config_gemma3_1b(C.byref(c))
+        for k, v in overrides.items():
+            setattr(c, k, v)
+        return c
+
+    def is_global(self, layer: int) -> bool:
+        return self.global_every == 0 or (layer + 1) % self.global_every == 0
+
+
+class XpMetrics(C.Structure):
+    _fields_ = [("ms", C.c_double), ("gpu_ms", C.c_double), ("sample_ms", C.c_double),
+                ("tokens_per_sec", C.c_double), ("position", C.c_uint32),
+                ("launches", C.c_uint32)]
+
+
+class XposeError(RuntimeError):
+    """A libxpose entry point returned a non-zero status."""
+
+    def __init__(self, fn: str, code: int, msg: str):
+        super().__init__(f"{fn} failed ({code}): {msg}")
+        self.code = code
+
+
+def _declare(lib: C.CDLL) -> None:
+    vp, u32, i32, f32, sz = C.c_void_p, C.c_uint32, C.c_int, C.c_float, C.c_size_t
+    P = C.POINTER
+    sig = {
+        "xp_last_error": (C.c_char_p, []),
+        "xp_version": (C.c_char_p, []),
+        "xp_init": (i32, [i32]),
+        "xp_device_info": (i32, [C.c_char_p, sz, P(i32), P(sz), C.c_char_p, sz]),
+        "xp_malloc": (i32, [P(vp), sz]),
+        "xp_free": (i32, [vp]),
+        "xp_memcpy_htod": (i32, [vp, vp, sz]),
+        "xp_memcpy_dtoh": (i32, [vp, vp, sz]),
+        "xp_memcpy_dtod": (i32, [vp, vp, sz]),
+        "xp_memset": (i32, [vp, i32, sz]),
+        "xp_synchronize": (i32, []),
+        "xp_stream_create": (i32, [P(vp)]),
+        "xp_stream_destroy": (i32, [vp]),
+        "xp_stream_synchronize": (i32, [vp]),
+        "xp_event_create": (i32, [P(vp)]),
+        "xp_event_destroy": (i32, [vp]),
+        "xp_event_record": (i32, [vp, vp]),
+        "xp_event_elapsed_ms": (i32, [vp, vp, P(f32)]),
+        "xp_mv_int4": (i32, [vp, vp, vp, vp, i32, u32, u32, u32, vp]),
+        "xp_mv_int4_multi": (i32, [u32, P(vp), vp, P(vp), P(vp), P(u32), i32, u32, vp]),
+        "xp_unpack_km4": (i32, [vp, vp, u32, u32, vp]),
+        "xp_fp16_decode": (i32, [vp, vp, u32, vp]),
+        "xp_philox4x32_10": (None, [P(u32), P(u32), P(u32)]),
+        "xp_synth_nibbles": (i32, [vp, u32, u32, u32, u32]),
+        "xp_synth_scales": (i32, [vp, i32, u32, u32, f32, u32, u32]),
+        "xp_synth_normal": (i32, [vp, sz, f32, f32, u32, u32]),
+        "xp_synth_normal_f16": (i32, [vp, sz, f32, f32, u32, u32]),
+        "xp_f32_to_f16": (C.c_uint16, [f32]),
+        "xp_config_gemma3_1b": (None, [P(XpConfig)]),
+        "xp_session_create": (i32, [P(XpConfig), P(vp)]),
+        "xp_session_destroy": (i32, [vp]),
+        "xp_tensor_bytes": (i32, [P(XpConfig), i32, i32, P(sz)]),
+        "xp_session_upload": (i32, [vp, i32, i32, vp, sz]),
+        "xp_synth_tensor": (i32, [P(XpConfig), u32, i32, i32, vp, sz]),
+        "xp_session_synthesize": (i32, [vp, u32]),
+        "xp_session_kv_upload": (i32, [vp, i32, i32, u32, u32, vp]),
+        "xp_session_kv_download": (i32, [vp, i32, i32, u32, u32, vp]),
+        "xp_session_set_position": (i32, [vp, u32]),
+        "xp_session_prefill": (i32, [vp, vp, u32]),
+        "xp_session_decode_step": (i32, [vp, P(u32)]),
+        "xp_session_decode_steps": (i32, [vp, u32, vp]),
+        "xp_session_reset": (i32, [vp]),
+        "xp_session_position": (i32, [vp, P(u32)]),
+        "xp_session_last_logits": (i32, [vp, vp, u32]),
+        "xp_session_last_candidates": (i32, [vp, vp, vp, u32]),
+        "xp_session_last_metrics": (i32, [vp, P(XpMetrics)]),
+        "xp_session_weight_bytes": (i32, [vp, P(sz)]),
+        "xp_session_kv_bytes": (i32, [vp, P(sz)]),
+        "xp_draw": (u32, [vp, vp, u32, f32, u32, f32, C.c_double]),
+        "xp_philox_uniform": (C.c_double, [u32, u32, u32]),
+    }
+    optional = {
+        "xp_rmsnorm_gemma": (i32, [vp, vp, vp, u32, f32, vp]),
+        "xp_rmsnorm_heads_gemma": (i32, [vp, vp, vp, u32, u32, f32, vp]),
+        "xp_rope": (i32, [vp, u32, u32, u32, f32, vp]),
+        "xp_qk_norm_rope_append": (i32, [vp, vp, vp, vp, vp, vp, vp, vp, vp, u32, u32, u32,
+                                         u32, f32, f32, vp]),
+        "xp_attention_decode": (i32, [vp, vp, vp, vp, u32, u32, u32, u32, u32, f32, vp]),
+        "xp_geglu": (i32, [vp, vp, vp, u32, vp]),
+        "xp_add_residual": (i32, [vp, vp, u32, vp]),
+        "xp_kv_append_f16": (i32, [vp, vp, u32, u32, vp]),
+        "xp_argmax": (i32, [vp, vp, vp, u32, vp]),
+        "xp_topk4_harvest": (i32, [vp, vp, vp, u32, u32, vp]),
+    }
+    for name, (res, args) in sig.items():
+        fn = getattr(lib, name)
+        fn.restype, fn.argtypes = res, args
+    for name, (res, args) in optional.items():
+        if hasattr(lib, name):
+            fn = getattr(lib, name)
+            fn.restype, fn.argtypes = res, args
+
+
+def lib() -> C.CDLL:
+    """The loaded libxpose.so (raises if it has not been built)."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise ImportError(
+                f"{LIB_PATH} is missing: build it with `python -m xpose_amd.build` "
+                "(the HIP path has no CPU fallback)")
+        l = C.CDLL(LIB_PATH)
+        _declare(l)
+        _lib = l
+    return _lib
+
+
+def check(name: str, code: int) -> None:
+    if code != 0:
+        raise XposeError(name, code, lib().xp_last_error().decode(errors="replace"))
+
+
+def call(name: str, *args) -> None:
+    """Calls a status-returning entry point and raises XposeError on failure."""
+    check(name, getattr(lib(), name)(*args))
+
+
+def init(dev: int = 0) -> None:
+    call("xp_init", dev)
+
+
+def device_info() -> dict:
+    name = C.create_string_buffer(256)
+    arch = C.create_string_buffer(64)
+    cu = C.c_int()
+    hbm = C.c_size_t()
+    call("xp_device_info", name, 256, C.byref(cu), C.byref(hbm), arch, 64)
+    return {"name": name.value.decode(), "arch": arch.value.decode(), "n_cu": cu.value,
+            "hbm_bytes": hbm.value}
+
+
+class DeviceBuffer:
+    """A device allocation owned by Python (freed on close / garbage collection)."""
+
+    def __init__(self, nbytes: int):
+        self.nbytes = int(nbytes)
+        p = C.c_void_p()
+        call("xp_malloc", C.byref(p), self.nbytes)
+        self.ptr = p.value or 0
+
+    @classmethod
+    def from_array(cls, a: np.ndarray) -> "DeviceBuffer":
+        a = np.ascontiguousarray(a)
+        b = cls(a.nbytes)
+        b.upload(a)
+        return b
+
+    def upload(self, a: np.ndarray, offset: int = 0) -> None:
+        a = np.ascontiguousarray(a)
+        assert offset + a.nbytes <= self.nbytes, "upload past the end of the buffer"
+        call("xp_memcpy_htod", C.c_void_p(self.ptr + offset), a.ctypes.data, a.nbytes)
+
+    def download(self, dtype, count: int | None = None, offset: int = 0) -> np.ndarray:
+        dt = np.dtype(dtype)
+        if count is None:
+            count = (self.nbytes - offset) // dt.itemsize
+        out = np.empty(count, dtype=dt)
+        assert offset + out.nbytes <= self.nbytes, "download past the end of the buffer"
+        call("xp_memcpy_dtoh", out.ctypes.data, C.c_void_p(self.ptr + offset), out.nbytes)
+        return out
+
+    def fill_bytes(self, value: int) -> None:
+        call("xp_memset", C.c_void_p(self.ptr), value, self.nbytes)
+
+    def close(self) -> None:
+        if self.ptr and _lib is not None:
+            _lib.xp_free(C.c_void_p(self.ptr))
+        self.ptr = 0
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    @property
+    def vp(self) -> C.c_void_p:
+        return C.c_void_p(self.ptr)
+
+
+def synchronize() -> None:
+    call("xp_synchronize")
+
+
+# ---- synthetic inputs (host side; no GPU needed) ---------------------------
+
+def philox4x32_10(ctr, key) -> np.ndarray:
+    c = (C.c_uint32 * 4)(*[int(v) & 0xFFFFFFFF for v in ctr])
+    k = (C.c_uint32 * 2)(*[int(v) & 0xFFFFFFFF for v in key])
+    o = (C.c_uint32 * 4)()
+    lib().xp_philox4x32_10(c, k, o)
+    return np.array(list(o), dtype=np.uint32)
+
+
+def synth_nibbles(rows: int, cols: int, seed: int, tensor_id: int) -> np.ndarray:
+    """KM4 nibble plane as uint32[rows*cols/8] (4 words per 32-weight block)."""
+    w = np.empty(rows * cols // 8, dtype=np.uint32)
+    call("xp_synth_nibbles", w.ctypes.data, rows, cols, seed, tensor_id)
+    return w
+
+
+def synth_scales(rows: int, cols: int, seed: int, tensor_id: int, sigma: float = 0.02,
+                 fmt: int = XP_SCALE_F16_QUAD) -> np.ndarray:
+    nblk = rows // 32
+    if fmt == XP_SCALE_F16_QUAD:
+        s = np.empty(nblk * cols, dtype=np.uint16)
+    else:
+        s = np.empty(nblk * cols, dtype=np.float32)
+    call("xp_synth_scales", s.ctypes.data, fmt, rows, cols, sigma, seed, tensor_id)
+    return s
+
+
+def synth_normal(n: int, seed: int, tensor_id: int, mean: float = 0.0,
+                 sigma: float = 1.0) -> np.ndarray:
+    out = np.empty(n, dtype=np.float32)
+    call("xp_synth_normal", out.ctypes.data, n, mean, sigma, seed, tensor_id)
+    return out
+
+
+def synth_normal_f16(n: int, seed: int, tensor_id: int, mean: float = 0.0,
+                     sigma: float = 1.0) -> np.ndarray:
+    out = np.empty(n, dtype=np.uint16)
+    call("xp_synth_normal_f16", out.ctypes.data, n, mean, sigma, seed, tensor_id)
+    return out
+
+
+def f32_to_f16_bits(x: float) -> int:
+    return int(lib().xp_f32_to_f16(float(x)))
+
+
+# ---- synthetic model tensors (bit-identical to what a session synthesizes) --
+
+def tensor_bytes(cfg: XpConfig, layer: int, tensor: int) -> int:
+    b = C.c_size_t()
+    call("xp_tensor_bytes", C.byref(cfg), layer, tensor, C.byref(b))
+    return b.value
+
+
+def synth_tensor(cfg: XpConfig, seed: int, layer: int, tensor: int) -> np.ndarray:
+    """uint32 nibble planes, uint16 (fp16 quad) / float32 scale planes, float32 norms."""
+    nb = tensor_bytes(cfg, layer, tensor)
+    base = tensor & ~T_SCALES
+    if base in MATRICES or base == T_LM_HEAD:
+        if tensor & T_SCALES:
+            dt = np.float32 if cfg.scale_fmt == XP_SCALE_F32 else np.uint16
+        else:
+            dt = np.uint32
+    else:
+        dt = np.float32
+    out = np.empty(nb // np.dtype(dt).itemsize, dtype=dt)
+    call("xp_synth_tensor", C.byref(cfg), seed, layer, tensor, out.ctypes.data, nb)
+    return out
+
+
+class DecodeSession:
+    """The engine-level entry points of the reference DecodeSession
+    (examples/llm/decode.hpp:605-676) over the C ABI."""
+
+    def __init__(self, cfg: XpConfig):
+        self.cfg = cfg
+        h = C.c_void_p()
+        call("xp_session_create", C.byref(cfg), C.byref(h))
+        self.h = h
+
+    def close(self) -> None:
+        if self.h and self.h.value and _lib is not None:
+            _lib.xp_session_destroy(self.h)
+        self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def synthesize(self, seed: int) -> None:
+        call("xp_session_synthesize", self.h, seed)
+
+    def upload(self, layer: int, tensor: int, a: np.ndarray) -> None:
+        a = np.ascontiguousarray(a)
+        call("xp_session_upload", self.h, layer, tensor, a.ctypes.data, a.nbytes)
+
+    def kv_upload(self, layer: int, which: int, pos0: int, rows: np.ndarray) -> None:
+        rows = np.ascontiguousarray(rows, np.uint16)
+        kvd = self.cfg.n_kv_heads * self.cfg.head_dim
+        call("xp_session_kv_upload", self.h, layer, which, pos0, rows.size // kvd,
+             rows.ctypes.data)
+
+    def kv_download(self, layer: int, which: int, pos0: int, n: int) -> np.ndarray:
+        kvd = self.cfg.n_kv_heads * self.cfg.head_dim
+        out = np.empty(n * kvd, np.uint16)
+        call("xp_session_kv_download", self.h, layer, which, pos0, n, out.ctypes.data)
+        return out
+
+    def set_position(self, pos: int) -> None:
+        call("xp_session_set_position", self.h, pos)
+
+    def prefill(self, ids) -> None:
+        ids = np.ascontiguousarray(ids, np.uint32)
+        call("xp_session_prefill", self.h, ids.ctypes.data, ids.size)
+
+    def decode_step(self) -> int:
+        t = C.c_uint32()
+        call("xp_session_decode_step", self.h, C.byref(t))
+        return t.value
+
+    def decode_steps(self, n: int) -> np.ndarray:
+        out = np.empty(n, np.uint32)
+        call("xp_session_decode_steps", self.h, n, out.ctypes.data)
+        return out
+
+    def reset(self) -> None:
+        call("xp_session_reset", self.h)
+
+    @property
+    def position(self) -> int:
+        p = C.c_uint32()
+        call("xp_session_position", self.h, C.byref(p))
+        return p.value
+
+    def last_logits(self) -> np.ndarray:
+        out = np.empty(self.cfg.vocab, np.float32)
+        call("xp_session_last_logits", self.h, out.ctypes.data, out.size)
+        return out
+
+    def last_candidates(self):
+        n = 4 * self.cfg.topk_parts
+        v = np.empty(n, np.float32)
+        i = np.empty(n, np.uint32)
+        call("xp_session_last_candidates", self.h, v.ctypes.data, i.ctypes.data, n)
+        return v, i
+
+    def last_metrics(self) -> XpMetrics:
+        m = XpMetrics()
+        call("xp_session_last_metrics", self.h, C.byref(m))
+        return m
+
+    def weight_bytes(self) -> int:
+        b = C.c_size_t()
+        call("xp_session_weight_bytes", self.h, C.byref(b))
+        return b.value
+
+
+def draw(val, idx, temperature: float, top_k: int, top_p: float, u: float) -> int:
+    v = np.array(val, np.float32)
+    i = np.array(idx, np.uint32)
+    return int(lib().xp_draw(v.ctypes.data, i.ctypes.data, v.size, temperature, top_k, top_p, u))
+
+
+def philox_uniform(seed: int, seq: int, step: int) -> float:
+    return float(lib().xp_philox_uniform(seed, seq, step))

@@ -1,0 +1,173 @@
+// Vocabulary reductions for sampling (kernels/llm_sampling.cl part 1).
+//
+// argmax: the reference needs a 3-level dispatch tree (262144 -> 4096 -> 64
+// -> 1, llm_sampling.cl:42-48) because it has no workgroup memory. Here one
+// launch does it: each workgroup reduces a contiguous slice with 16-byte
+// loads and wave shuffles, and the last workgroup to finish (arrival ticket)
+// reduces the per-workgroup winners. The comparison is (value, index)
+// lexicographic — larger value, then lower index — and every slot starts at
+// (-inf, 0), so the result equals the reference's serial scan
+// (llm_transformer.cl:618-629) and its tree (llm_sampling.cl:50-56) for every
+// input, NaNs included (a NaN never compares greater).
+#include "xp_device.hpp"
+#include "xp_launch.hpp"
+
+namespace xp {
+
+constexpr int kAmThreads = 256;
+
+__device__ __forceinline__ void am_better(float& bv, uint32_t& bi, float v, uint32_t i) {
+    if (v > bv || (v == bv && i < bi)) { bv = v; bi = i; }
+}
+
+__device__ __forceinline__ void am_wave(float& bv, uint32_t& bi) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        const float v = __shfl_xor(bv, o, kWave);
+        const uint32_t i = __shfl_xor(bi, o, kWave);
+        am_better(bv, bi, v, i);
+    }
+}
+
+struct AmArgs {
+    uint32_t* out_idx;
+    float* out_val;
+    const float* logits;
+    uint32_t n;
+    uint32_t per_wg;        // elements per workgroup (multiple of 4)
+    float* pval;            // [gridDim.x]
+    uint32_t* pidx;
+    uint32_t* ticket;
+};
+
+__global__ __launch_bounds__(kAmThreads) void argmax_kernel(AmArgs a) {
+    __shared__ float sv[kAmThreads / kWave];
+    __shared__ uint32_t si[kAmThreads / kWave];
+    __shared__ uint32_t last;
+    const uint32_t tid = threadIdx.x;
+    const uint32_t lo = blockIdx.x * a.per_wg;
+    const uint32_t hi = min(lo + a.per_wg, a.n);
+    float bv = -INFINITY;
+    uint32_t bi = 0u;
+    const uint32_t n4 = (hi > lo) ? (hi - lo) / 4 : 0;
+    const float4* p4 = reinterpret_cast<const float4*>(a.logits + lo);
+    for (uint32_t i = tid; i < n4; i += blockDim.x) {
+        const float4 v = p4[i];
+        const uint32_t k = lo + 4 * i;
+        am_better(bv, bi, v.x, k);
+        am_better(bv, bi, v.y, k + 1);
+        am_better(bv, bi, v.z, k + 2);
+        am_better(bv, bi, v.w, k + 3);
+    }
+    for (uint32_t k = lo + 4 * n4 + tid; k < hi; k += blockDim.x) am_better(bv, bi, a.logits[k], k);
+    am_wave(bv, bi);
+    if (tid % kWave == 0) { sv[tid / kWave] = bv; si[tid / kWave] = bi; }
+    __syncthreads();
+    if (tid == 0) {
+        for (int w = 1; w < kAmThreads / kWave; ++w) am_better(bv, bi, sv[w], si[w]);
+        a.pval[blockIdx.x] = bv;
+        a.pidx[blockIdx.x] = bi;
+        __threadfence();
+        last = atomicAdd(a.ticket, 1u);
+    }
+    __syncthreads();
+    if (last != gridDim.x - 1) return;
+    __threadfence();
+    bv = -INFINITY;
+    bi = 0u;
+    for (uint32_t w = tid; w < gridDim.x; w += blockDim.x)
+        am_better(bv, bi, __builtin_nontemporal_load(a.pval + w),
+                  __builtin_nontemporal_load(a.pidx + w));
+    am_wave(bv, bi);
+    __syncthreads();
+    if (tid % kWave == 0) { sv[tid / kWave] = bv; si[tid / kWave] = bi; }
+    __syncthreads();
+    if (tid == 0) {
+        for (int w = 1; w < kAmThreads / kWave; ++w) am_better(bv, bi, sv[w], si[w]);
+        *a.out_idx = bi;
+        if (a.out_val) *a.out_val = bv;
+        *a.ticket = 0u;
+    }
+}
+
+// topk4_partial, llm_sampling.cl:318-347: one thread per strided chain
+// e = p (mod nparts), best four by strict '>' (earliest index on ties),
+// unfilled slots (-inf, 0xFFFFFFFF). Pure comparisons: bit-identical output.
+__global__ void topk4_kernel(float* cval, uint32_t* cidx, const float* x, uint32_t n,
+                             uint32_t nparts) {
+    const uint32_t p = blockIdx.x * blockDim.x + threadIdx.x;
+    if (p >= nparts) return;
+    float v0 = -INFINITY, v1 = -INFINITY, v2 = -INFINITY, v3 = -INFINITY;
+    uint32_t i0 = 0xFFFFFFFFu, i1 = 0xFFFFFFFFu, i2 = 0xFFFFFFFFu, i3 = 0xFFFFFFFFu;
+    for (uint32_t e = p; e < n; e += nparts) {
+        const float v = x[e];
+        if (!(v > v3)) continue;
+        if (v > v0) {
+            v3 = v2; i3 = i2; v2 = v1; i2 = i1; v1 = v0; i1 = i0; v0 = v; i0 = e;
+        } else if (v > v1) {
+            v3 = v2; i3 = i2; v2 = v1; i2 = i1; v1 = v; i1 = e;
+        } else if (v > v2) {
+            v3 = v2; i3 = i2; v2 = v; i2 = e;
+        } else {
+            v3 = v; i3 = e;
+        }
+    }
+    const uint32_t o = p * 4u;
+    cval[o + 0] = v0; cidx[o + 0] = i0;
+    cval[o + 1] = v1; cidx[o + 1] = i1;
+    cval[o + 2] = v2; cidx[o + 2] = i2;
+    cval[o + 3] = v3; cidx[o + 3] = i3;
+}
+
+// Shared with the decode session, which owns its own partial/ticket buffers.
+int launch_argmax(uint32_t* out_idx, float* out_val, const float* logits, uint32_t n,
+                  float* pval, uint32_t* pidx, uint32_t* ticket, hipStream_t st) {
+    AmArgs a{out_idx, out_val, logits, n, 0, pval, pidx, ticket};
+    uint32_t nwg = (n + 4095) / 4096;
+    if (nwg > uint32_t(kAmMaxWg)) nwg = kAmMaxWg;
+    if (nwg < 1) nwg = 1;
+    a.per_wg = ((n + nwg - 1) / nwg + 3) & ~3u;
+    nwg = (n + a.per_wg - 1) / a.per_wg;
+    if (nwg < 1) nwg = 1;
+    hipLaunchKernelGGL(argmax_kernel, dim3(nwg), dim3(kAmThreads), 0, st, a);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return set_error(XP_E_HIP, "argmax: launch -> %s", hipGetErrorString(e));
+    return XP_OK;
+}
+
+int launch_topk4(float* cval, uint32_t* cidx, const float* x, uint32_t n, uint32_t nparts,
+                 hipStream_t st) {
+    hipLaunchKernelGGL(topk4_kernel, dim3((nparts + 255) / 256), dim3(256), 0, st, cval, cidx, x,
+                       n, nparts);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return set_error(XP_E_HIP, "topk4: launch -> %s", hipGetErrorString(e));
+    return XP_OK;
+}
+
+}  // namespace xp
+
+using namespace xp;
+
+extern "C" {
+
+int xp_argmax(uint32_t* out_idx, float* out_val, const float* logits, uint32_t n,
+              xp_stream stream) {
+    XP_REQUIRE(out_idx && logits, "null pointer");
+    XP_REQUIRE(n > 0, "n must be positive");
+    XP_REQUIRE((reinterpret_cast<uintptr_t>(logits) & 15u) == 0, "logits must be 16-byte aligned");
+    DeviceScratch* sc = scratch();
+    if (!sc) return XP_E_HIP;
+    if (!ensure_partial(sc, 2 * kAmMaxWg) || !ensure_tickets(sc, 1)) return XP_E_NOMEM;
+    return launch_argmax(out_idx, out_val, logits, n, sc->partial,
+                         reinterpret_cast<uint32_t*>(sc->partial + kAmMaxWg), sc->tickets,
+                         as_stream(stream));
+}
+
+int xp_topk4_harvest(float* cval, uint32_t* cidx, const float* logits, uint32_t n,
+                     uint32_t nparts, xp_stream stream) {
+    XP_REQUIRE(cval && cidx && logits, "null pointer");
+    XP_REQUIRE(nparts > 0, "nparts must be positive");
+    return launch_topk4(cval, cidx, logits, n, nparts, as_stream(stream));
+}
+
+}  // extern "C"

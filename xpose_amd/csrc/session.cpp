@@ -1,0 +1,768 @@
+// Decode session: the token step of DecodeSession (examples/llm/decode.cpp:
+// 1634-1866) on gfx950.
+//
+// One token step is recorded once into a HIP graph and replayed for every
+// token. Everything that changes per token lives in device memory: the
+// position and the token id (`state`), the KV cache, and the sampled ids
+// (`hist`). Attention derives its window and span from the device position,
+// so the graph never needs re-recording — the reference rejected static
+// re-recording for exactly this reason (agent-docs/llm-inference.md:319-330)
+// and instead re-records 838 dispatches per token on the host.
+//
+// Greedy decoding keeps the sampled token on the device: the argmax of pass t
+// is the token pass t+1 embeds, which is the reference's sample-first order
+// (decode.cpp:1830-1861) without a host round trip, so decode_steps(n) can
+// queue n replays behind one wait.
+#include "xp_internal.hpp"
+#include "xp_launch.hpp"
+
+#include <algorithm>
+#include <chrono>
+#include <cmath>
+#include <cstring>
+#include <new>
+#include <vector>
+
+namespace xp {
+
+int launch_embed(float* x, const void* wq, const void* sc, int fmt, uint32_t hidden,
+                 uint32_t vocab, float embed_scale, const uint32_t* state, uint32_t* hist,
+                 hipStream_t st);
+int launch_norm_res_norm(float* x, const float* y, const float* w_post, const float* w_pre,
+                         float* out, uint32_t n, float eps, hipStream_t st);
+int launch_advance(uint32_t* state, hipStream_t st);
+uint16_t f32_to_f16(float f);
+
+namespace {
+
+double now_ms() {
+    using namespace std::chrono;
+    return duration<double, std::milli>(steady_clock::now().time_since_epoch()).count();
+}
+
+constexpr int kNMat = 7;
+constexpr int kNNorm = 6;
+constexpr size_t kAlign = 256;
+constexpr uint32_t kTicketMv = 0, kTicketAttn = 8192, kTicketAm = 8192 + 64, kTickets = 8192 + 128;
+
+size_t align_up(size_t v) { return (v + kAlign - 1) & ~(kAlign - 1); }
+
+bool mat_dims(const xp_config& c, int m, uint32_t& rows, uint32_t& cols) {
+    const uint32_t qd = c.n_heads * c.head_dim, kvd = c.n_kv_heads * c.head_dim;
+    switch (m) {
+        case XP_T_Q: rows = c.hidden; cols = qd; return true;
+        case XP_T_K:
+        case XP_T_V: rows = c.hidden; cols = kvd; return true;
+        case XP_T_O: rows = qd; cols = c.hidden; return true;
+        case XP_T_GATE:
+        case XP_T_UP: rows = c.hidden; cols = c.ffn; return true;
+        case XP_T_DOWN: rows = c.ffn; cols = c.hidden; return true;
+        case XP_T_LM_HEAD: rows = c.hidden; cols = c.vocab; return true;
+        default: return false;
+    }
+}
+
+size_t scale_bytes(const xp_config& c, uint32_t rows, uint32_t cols) {
+    const size_t n = size_t(rows / 32) * cols;
+    return c.scale_fmt == XP_SCALE_F32 ? n * 4 : n * 2;
+}
+
+// Bytes of a tensor, or 0 if the (layer, tensor) pair is not valid.
+size_t tensor_bytes(const xp_config& c, int layer, int tensor) {
+    const bool scales = (tensor & XP_T_SCALES) != 0;
+    const int t = tensor & ~XP_T_SCALES;
+    uint32_t rows = 0, cols = 0;
+    if (t == XP_T_LM_HEAD) {
+        if (layer != -1 || !mat_dims(c, t, rows, cols)) return 0;
+    } else if (t <= XP_T_DOWN) {
+        if (layer < 0 || uint32_t(layer) >= c.n_layers || !mat_dims(c, t, rows, cols)) return 0;
+    } else if (scales) {
+        return 0;
+    } else if (t == XP_T_FINAL_NORM) {
+        return layer == -1 ? size_t(c.hidden) * 4 : 0;
+    } else if (t >= XP_T_ATTN_NORM && t <= XP_T_K_NORM) {
+        if (layer < 0 || uint32_t(layer) >= c.n_layers) return 0;
+        return (t >= XP_T_Q_NORM ? size_t(c.head_dim) : size_t(c.hidden)) * 4;
+    } else {
+        return 0;
+    }
+    return scales ? scale_bytes(c, rows, cols) : size_t(rows) * cols / 2;
+}
+
+// Synthetic tensor stream id: unique per (layer, tensor).
+uint32_t synth_id(int layer, int tensor) {
+    return uint32_t(layer + 1) * 1024u + uint32_t(tensor & 0x3FF) * 2u +
+           ((tensor & XP_T_SCALES) ? 1u : 0u);
+}
+
+int check_config(const xp_config& c) {
+    if (!c.n_layers || !c.hidden || !c.ffn || !c.n_heads || !c.n_kv_heads || !c.head_dim ||
+        !c.vocab || !c.max_seq)
+        return set_error(XP_E_ARG, "config: every shape field must be positive");
+    if (c.hidden % 128 || c.ffn % 128 || (c.n_heads * c.head_dim) % 128)
+        return set_error(XP_E_ARG, "config: matvec inputs (hidden=%u, ffn=%u, q_dim=%u) must be "
+                         "multiples of 128", c.hidden, c.ffn, c.n_heads * c.head_dim);
+    if (c.vocab % 64 || (c.n_kv_heads * c.head_dim) % 64)
+        return set_error(XP_E_ARG, "config: vocab and kv_dim must be multiples of 64");
+    if (c.head_dim % 64 || c.head_dim > 512 || c.n_heads % c.n_kv_heads ||
+        c.n_heads / c.n_kv_heads > 8)
+        return set_error(XP_E_ARG, "config: head_dim=%u (multiple of 64, <= 512), heads %u/%u "
+                         "(<= 8 per kv head)", c.head_dim, c.n_heads, c.n_kv_heads);
+    if (c.hidden > 8192)
+        return set_error(XP_E_ARG, "config: hidden=%u > 8192", c.hidden);
+    if (c.scale_fmt != XP_SCALE_F16_QUAD && c.scale_fmt != XP_SCALE_BF16_QUAD &&
+        c.scale_fmt != XP_SCALE_F32)
+        return set_error(XP_E_ARG, "config: unknown scale_fmt %d", c.scale_fmt);
+    if (c.sample_mode != 0 && c.sample_mode != 1)
+        return set_error(XP_E_ARG, "config: sample_mode %d (0 greedy, 1 temperature)",
+                         c.sample_mode);
+    if (c.sample_mode == 1 && (c.topk_parts == 0 || c.topk_parts > c.vocab))
+        return set_error(XP_E_ARG, "config: topk_parts=%u must be in [1, vocab]", c.topk_parts);
+    return XP_OK;
+}
+
+}  // namespace
+
+struct Session {
+    xp_config cfg{};
+    hipStream_t st = nullptr;
+    int n_cu = 256;
+    char* warena = nullptr;
+    size_t wbytes = 0;
+    char* kvarena = nullptr;
+    size_t kvbytes = 0;
+    char* aarena = nullptr;
+    struct Layer {
+        void* w[kNMat];
+        void* s[kNMat];
+        float* norm[kNNorm];
+        uint16_t* kc;
+        uint16_t* vc;
+    };
+    std::vector<Layer> L;
+    void* lm_w = nullptr;
+    void* lm_s = nullptr;
+    float* final_norm = nullptr;
+    float *x, *xb, *xb2, *q_raw, *k_raw, *v, *q, *k, *att, *gate, *up, *hb, *logits;
+    float* mv_partial = nullptr;
+    size_t mv_partial_cap = 0;
+    float* attn_part = nullptr;
+    uint32_t* tickets = nullptr;
+    float* am_val = nullptr;
+    uint32_t* am_idx = nullptr;
+    float* am_out = nullptr;
+    float* cand_val = nullptr;
+    uint32_t* cand_idx = nullptr;
+    uint32_t* state = nullptr;   // [0] position, [1] token
+    uint32_t* hist = nullptr;    // [max_seq] token run at each position
+    uint32_t* h_ids = nullptr;   // pinned staging for host-chosen token ids
+    hipGraphExec_t graph[3] = {nullptr, nullptr, nullptr};   // prefill, greedy, harvest
+    uint32_t launches[3] = {0, 0, 0};
+    uint32_t pos = 0;
+    uint32_t step = 0;           // draws made (Philox counter)
+    bool logits_valid = false;
+    xp_metrics met{};
+    std::vector<float> cv;
+    std::vector<uint32_t> ci;
+
+    float embed_scale() const {
+        return cfg.embed_scale > 0.0f ? cfg.embed_scale : std::sqrt(float(cfg.hidden));
+    }
+    float attn_scale() const {
+        return cfg.attn_scale > 0.0f ? cfg.attn_scale : 1.0f / std::sqrt(float(cfg.head_dim));
+    }
+    bool is_global(uint32_t l) const {
+        return cfg.global_every == 0 || (l + 1) % cfg.global_every == 0;
+    }
+
+    int record(int variant, uint32_t& n);
+    int graph_for(int variant);
+    int run(int variant);
+};
+
+int Session::record(int variant, uint32_t& n) {
+    const xp_config& c = cfg;
+    const uint32_t H = c.hidden, qd = c.n_heads * c.head_dim, kvd = c.n_kv_heads * c.head_dim;
+    const int fmt = c.scale_fmt;
+    const float eps = c.rms_eps;
+    int rc;
+    n = 0;
+#define XP_STEP(call)                \
+    do {                             \
+        if ((rc = (call)) != XP_OK) return rc; \
+        ++n;                         \
+    } while (0)
+    XP_STEP(launch_embed(x, lm_w, lm_s, fmt, H, c.vocab, embed_scale(), state, hist, st));
+    XP_STEP(launch_norm_res_norm(x, nullptr, nullptr, L[0].norm[0], xb, H, eps, st));
+    for (uint32_t l = 0; l < c.n_layers; ++l) {
+        Layer& w = L[l];
+        const bool glob = is_global(l);
+        const float theta = glob ? c.rope_theta_global : c.rope_theta_local;
+        const MvMatDesc qkv[3] = {{q_raw, w.w[XP_T_Q], w.s[XP_T_Q], qd},
+                                  {k_raw, w.w[XP_T_K], w.s[XP_T_K], kvd},
+                                  {v, w.w[XP_T_V], w.s[XP_T_V], kvd}};
+        XP_STEP(launch_mv(qkv, 3, xb, fmt, H, 0, mv_partial, mv_partial_cap, tickets + kTicketMv,
+                          8192, st, "session qkv"));
+        QkArgs qa{q, k, q_raw, k_raw, v, w.norm[4], w.norm[5], w.kc, w.vc,
+                  c.n_heads, c.n_kv_heads, c.head_dim, eps, state, 0};
+        XP_STEP(launch_qk(qa, theta, st));
+        AttnArgs aa{};
+        aa.out = att; aa.q = q; aa.kc = w.kc; aa.vc = w.vc;
+        aa.n_heads = c.n_heads; aa.kv_heads = c.n_kv_heads; aa.head_dim = c.head_dim;
+        aa.pos_dev = state;
+        aa.window = glob ? 0u : c.sliding_window;
+        aa.scale = attn_scale();
+        aa.part = attn_part;
+        aa.tickets = tickets + kTicketAttn;
+        const uint32_t max_span = glob || c.sliding_window == 0
+                                      ? c.max_seq : std::min(c.sliding_window, c.max_seq);
+        XP_STEP(launch_attention(aa, max_span, st));
+        const MvMatDesc o{xb2, w.w[XP_T_O], w.s[XP_T_O], H};
+        XP_STEP(launch_mv(&o, 1, att, fmt, qd, 0, mv_partial, mv_partial_cap, tickets + kTicketMv,
+                          8192, st, "session o_proj"));
+        XP_STEP(launch_norm_res_norm(x, xb2, w.norm[1], w.norm[2], xb, H, eps, st));
+        const MvMatDesc gu[2] = {{gate, w.w[XP_T_GATE], w.s[XP_T_GATE], c.ffn},
+                                 {up, w.w[XP_T_UP], w.s[XP_T_UP], c.ffn}};
+        XP_STEP(launch_mv(gu, 2, xb, fmt, H, 0, mv_partial, mv_partial_cap, tickets + kTicketMv,
+                          8192, st, "session gate/up"));
+        XP_STEP(xp_geglu(hb, gate, up, c.ffn, st));
+        const MvMatDesc d{xb2, w.w[XP_T_DOWN], w.s[XP_T_DOWN], H};
+        XP_STEP(launch_mv(&d, 1, hb, fmt, c.ffn, 0, mv_partial, mv_partial_cap,
+                          tickets + kTicketMv, 8192, st, "session down"));
+        const float* next = (l + 1 < c.n_layers) ? L[l + 1].norm[0] : final_norm;
+        XP_STEP(launch_norm_res_norm(x, xb2, w.norm[3], next, xb, H, eps, st));
+    }
+    if (variant >= 1) {
+        const MvMatDesc lm{logits, lm_w, lm_s, c.vocab};
+        XP_STEP(launch_mv(&lm, 1, xb, fmt, H, 0, mv_partial, mv_partial_cap, tickets + kTicketMv,
+                          8192, st, "session lm_head"));
+        if (variant == 1)
+            XP_STEP(launch_argmax(state + 1, am_out, logits, c.vocab, am_val, am_idx,
+                                  tickets + kTicketAm, st));
+        else
+            XP_STEP(launch_topk4(cand_val, cand_idx, logits, c.vocab, c.topk_parts, st));
+    }
+    XP_STEP(launch_advance(state, st));
+#undef XP_STEP
+    return XP_OK;
+}
+
+int Session::graph_for(int variant) {
+    if (graph[variant]) return XP_OK;
+    hipGraph_t g = nullptr;
+    XP_HIP(hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal));
+    uint32_t n = 0;
+    const int rc = record(variant, n);
+    const hipError_t e = hipStreamEndCapture(st, &g);
+    if (rc != XP_OK) {
+        if (g) (void)hipGraphDestroy(g);
+        return rc;
+    }
+    if (e != hipSuccess)
+        return set_error(XP_E_HIP, "session: stream capture failed: %s", hipGetErrorString(e));
+    const hipError_t ie = hipGraphInstantiate(&graph[variant], g, nullptr, nullptr, 0);
+    (void)hipGraphDestroy(g);
+    if (ie != hipSuccess) {
+        graph[variant] = nullptr;
+        return set_error(XP_E_HIP, "session: hipGraphInstantiate: %s", hipGetErrorString(ie));
+    }
+    launches[variant] = n;
+    return XP_OK;
+}
+
+int Session::run(int variant) {
+    int rc = graph_for(variant);
+    if (rc != XP_OK) return rc;
+    XP_HIP(hipGraphLaunch(graph[variant], st));
+    return XP_OK;
+}
+
+// Host draw, examples/llm/decode.cpp:1873-1917: candidates ordered by (value
+// desc, index asc) and cut to top_k; c = exp((v - max) / T) in float, sums in
+// double; top-p keeps through the first candidate whose running mass reaches
+// p * sum; r = u * sum walked down the list. The kept candidates are walked in
+// sorted order (the reference walks nth_element's unspecified order unless
+// top-p sorts them).
+uint32_t draw(float* val, uint32_t* idx, uint32_t n, float temperature, uint32_t top_k,
+              float top_p, double u) {
+    if (n == 0) return 0;
+    const float t = temperature > 0.0f ? temperature : 1.0f;
+    std::vector<uint32_t> ord(n);
+    for (uint32_t i = 0; i < n; ++i) ord[i] = i;
+    std::sort(ord.begin(), ord.end(), [&](uint32_t a, uint32_t b) {
+        return val[a] > val[b] || (val[a] == val[b] && idx[a] < idx[b]);
+    });
+    std::vector<float> v(n);
+    std::vector<uint32_t> id(n);
+    for (uint32_t i = 0; i < n; ++i) { v[i] = val[ord[i]]; id[i] = idx[ord[i]]; }
+    const uint32_t k = top_k ? std::min(top_k, n) : n;
+    n = k;
+    float maxl = -INFINITY;
+    for (uint32_t i = 0; i < n; ++i) maxl = std::max(maxl, v[i]);
+    double sum = 0;
+    for (uint32_t i = 0; i < n; ++i) {
+        v[i] = std::exp((v[i] - maxl) / t);
+        sum += v[i];
+    }
+    if (top_p > 0.0f && top_p < 1.0f && sum > 0) {
+        double acc = 0, cut = top_p * sum;
+        uint32_t keep = 0;
+        for (; keep < n; ++keep) {
+            acc += v[keep];
+            if (acc >= cut) break;
+        }
+        n = std::min(n, keep + 1);
+        sum = 0;
+        for (uint32_t i = 0; i < n; ++i) sum += v[i];
+    }
+    for (uint32_t i = 0; i < n; ++i) { val[i] = v[i]; idx[i] = id[i]; }
+    double r = u * sum;
+    for (uint32_t i = 0; i < n; ++i) {
+        r -= v[i];
+        if (r <= 0) return id[i];
+    }
+    return id[n - 1];
+}
+
+double philox_uniform(uint32_t seed, uint32_t seq, uint32_t step) {
+    const uint32_t c[4] = {step, 0u, 0u, 0u}, k[2] = {seed, seq};
+    uint32_t o[4];
+    xp_philox4x32_10(c, k, o);
+    const uint64_t m = (uint64_t(o[0]) << 21) | (o[1] >> 11);
+    return double(m) * (1.0 / 9007199254740992.0);
+}
+
+}  // namespace xp
+
+using namespace xp;
+
+struct xp_session {
+    Session s;
+};
+
+namespace {
+
+int destroy(xp_session* h) {
+    if (!h) return XP_OK;
+    Session& s = h->s;
+    for (auto& g : s.graph)
+        if (g) (void)hipGraphExecDestroy(g);
+    if (s.st) (void)hipStreamSynchronize(s.st);
+    if (s.warena) (void)hipFree(s.warena);
+    if (s.kvarena) (void)hipFree(s.kvarena);
+    if (s.aarena) (void)hipFree(s.aarena);
+    if (s.h_ids) (void)hipHostFree(s.h_ids);
+    if (s.st) (void)hipStreamDestroy(s.st);
+    delete h;
+    return XP_OK;
+}
+
+// Draws the next token from the last harvest (temperature mode).
+int sample_from_candidates(Session& s, uint32_t& token) {
+    const uint32_t nc = 4 * s.cfg.topk_parts;
+    s.cv.resize(nc);
+    s.ci.resize(nc);
+    XP_HIP(hipMemcpy(s.cv.data(), s.cand_val, nc * 4, hipMemcpyDeviceToHost));
+    XP_HIP(hipMemcpy(s.ci.data(), s.cand_idx, nc * 4, hipMemcpyDeviceToHost));
+    uint32_t m = 0;
+    for (uint32_t i = 0; i < nc; ++i)
+        if (s.ci[i] != 0xFFFFFFFFu) { s.cv[m] = s.cv[i]; s.ci[m] = s.ci[i]; ++m; }
+    const double u = philox_uniform(s.cfg.seed, s.cfg.seq_id, s.step++);
+    token = draw(s.cv.data(), s.ci.data(), m, s.cfg.temperature, s.cfg.top_k, s.cfg.top_p, u);
+    return XP_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+void xp_config_gemma3_1b(xp_config* c) {
+    if (!c) return;
+    std::memset(c, 0, sizeof *c);
+    c->n_layers = 26; c->hidden = 1152; c->ffn = 6912; c->n_heads = 4; c->n_kv_heads = 1;
+    c->head_dim = 256; c->vocab = 262144; c->max_seq = 8192;
+    c->global_every = 6; c->sliding_window = 512;
+    c->rms_eps = 1e-6f; c->rope_theta_global = 1e6f; c->rope_theta_local = 1e4f;
+    c->embed_scale = 0.0f; c->attn_scale = 0.0f;
+    c->scale_fmt = XP_SCALE_F16_QUAD;
+    c->sample_mode = 0; c->temperature = 1.0f; c->top_k = 0; c->top_p = 1.0f;
+    c->seed = 1234; c->seq_id = 0; c->topk_parts = 1024;
+}
+
+int xp_tensor_bytes(const xp_config* c, int layer, int tensor, size_t* bytes) {
+    XP_REQUIRE(c && bytes, "null pointer");
+    const size_t b = tensor_bytes(*c, layer, tensor);
+    XP_REQUIRE(b > 0, "no tensor %d at layer %d", tensor, layer);
+    *bytes = b;
+    return XP_OK;
+}
+
+int xp_synth_tensor(const xp_config* c, uint32_t seed, int layer, int tensor, void* host,
+                    size_t bytes) {
+    XP_REQUIRE(c && host, "null pointer");
+    const size_t need = tensor_bytes(*c, layer, tensor);
+    XP_REQUIRE(need > 0, "no tensor %d at layer %d", tensor, layer);
+    XP_REQUIRE(bytes == need, "tensor %d at layer %d is %zu bytes, got %zu", tensor, layer, need,
+               bytes);
+    const int t = tensor & ~XP_T_SCALES;
+    const uint32_t id = synth_id(layer, tensor);
+    uint32_t rows = 0, cols = 0;
+    if (mat_dims(*c, t, rows, cols)) {
+        if (tensor & XP_T_SCALES) {
+            XP_REQUIRE(c->scale_fmt != XP_SCALE_BF16_QUAD,
+                       "synthetic scales are fp16 (F16 quad or F32 planes)");
+            return xp_synth_scales(host, c->scale_fmt, rows, cols, 0.02f, seed, id);
+        }
+        return xp_synth_nibbles(static_cast<uint32_t*>(host), rows, cols, seed, id);
+    }
+    // Norm weight: multiplier m ~ N(1, 0.1) stored as m - 1.
+    const size_t n = bytes / 4;
+    float* f = static_cast<float*>(host);
+    int rc = xp_synth_normal(f, n, 1.0f, 0.1f, seed, id);
+    if (rc != XP_OK) return rc;
+    for (size_t i = 0; i < n; ++i) f[i] = f[i] - 1.0f;
+    return XP_OK;
+}
+
+int xp_session_create(const xp_config* cfg, xp_session** out) {
+    XP_REQUIRE(cfg && out, "null pointer");
+    *out = nullptr;
+    int rc = check_config(*cfg);
+    if (rc != XP_OK) return rc;
+    xp_session* h = new (std::nothrow) xp_session;
+    if (!h) return set_error(XP_E_NOMEM, "xp_session_create: out of host memory");
+    Session& s = h->s;
+    s.cfg = *cfg;
+    const xp_config& c = s.cfg;
+    try {
+        int dev = 0;
+        hipDeviceProp_t p;
+        if (hipGetDevice(&dev) != hipSuccess || hipGetDeviceProperties(&p, dev) != hipSuccess) {
+            destroy(h);
+            return set_error(XP_E_HIP, "xp_session_create: no HIP device");
+        }
+        s.n_cu = p.multiProcessorCount;
+        if (hipStreamCreateWithFlags(&s.st, hipStreamNonBlocking) != hipSuccess) {
+            destroy(h);
+            return set_error(XP_E_HIP, "xp_session_create: hipStreamCreate failed");
+        }
+        // ---- weights: one arena, every tensor 256-byte aligned
+        size_t wb = 0;
+        for (uint32_t l = 0; l < c.n_layers; ++l) {
+            for (int m = 0; m < kNMat; ++m)
+                wb += align_up(tensor_bytes(c, l, m)) + align_up(tensor_bytes(c, l, m | XP_T_SCALES));
+            for (int nn = 0; nn < kNNorm; ++nn) wb += align_up(tensor_bytes(c, l, XP_T_ATTN_NORM + nn));
+        }
+        wb += align_up(tensor_bytes(c, -1, XP_T_LM_HEAD)) +
+              align_up(tensor_bytes(c, -1, XP_T_LM_HEAD | XP_T_SCALES)) +
+              align_up(tensor_bytes(c, -1, XP_T_FINAL_NORM));
+        if (hipMalloc(&s.warena, wb) != hipSuccess) {
+            destroy(h);
+            return set_error(XP_E_NOMEM, "xp_session_create: %zu weight bytes", wb);
+        }
+        s.wbytes = wb;
+        char* p8 = s.warena;
+        auto take = [&](size_t b) { char* r = p8; p8 += align_up(b); return r; };
+        s.L.resize(c.n_layers);
+        for (uint32_t l = 0; l < c.n_layers; ++l) {
+            for (int m = 0; m < kNMat; ++m) {
+                s.L[l].w[m] = take(tensor_bytes(c, l, m));
+                s.L[l].s[m] = take(tensor_bytes(c, l, m | XP_T_SCALES));
+            }
+            for (int nn = 0; nn < kNNorm; ++nn)
+                s.L[l].norm[nn] = reinterpret_cast<float*>(take(tensor_bytes(c, l, XP_T_ATTN_NORM + nn)));
+        }
+        s.lm_w = take(tensor_bytes(c, -1, XP_T_LM_HEAD));
+        s.lm_s = take(tensor_bytes(c, -1, XP_T_LM_HEAD | XP_T_SCALES));
+        s.final_norm = reinterpret_cast<float*>(take(tensor_bytes(c, -1, XP_T_FINAL_NORM)));
+        // ---- KV cache: [t][kv_heads][head_dim] fp16 per layer, K and V
+        const size_t kvrow = size_t(c.n_kv_heads) * c.head_dim;
+        const size_t per = align_up(size_t(c.max_seq) * kvrow * 2);
+        s.kvbytes = per * 2 * c.n_layers;
+        if (hipMalloc(&s.kvarena, s.kvbytes) != hipSuccess) {
+            destroy(h);
+            return set_error(XP_E_NOMEM, "xp_session_create: %zu KV bytes", s.kvbytes);
+        }
+        (void)hipMemset(s.kvarena, 0, s.kvbytes);
+        for (uint32_t l = 0; l < c.n_layers; ++l) {
+            s.L[l].kc = reinterpret_cast<uint16_t*>(s.kvarena + per * (2 * l));
+            s.L[l].vc = reinterpret_cast<uint16_t*>(s.kvarena + per * (2 * l + 1));
+        }
+        // ---- activations and scratch
+        const uint32_t H = c.hidden, qd = c.n_heads * c.head_dim, kvd = c.n_kv_heads * c.head_dim;
+        size_t mvp = 0;
+        mvp = std::max(mvp, mv_partial_floats(H, qd + 2 * kvd, 0, s.n_cu));
+        mvp = std::max(mvp, mv_partial_floats(qd, H, 0, s.n_cu));
+        mvp = std::max(mvp, mv_partial_floats(H, 2 * c.ffn, 0, s.n_cu));
+        mvp = std::max(mvp, mv_partial_floats(c.ffn, H, 0, s.n_cu));
+        mvp = std::max(mvp, mv_partial_floats(H, c.vocab, 0, s.n_cu));
+        s.mv_partial_cap = std::max<size_t>(mvp, 64);
+        const size_t attnp = attn_partial_floats(c.n_kv_heads, c.n_heads, c.head_dim, c.max_seq);
+        const uint32_t nc = c.sample_mode == 1 ? 4 * c.topk_parts : 4;
+        const size_t sizes[] = {
+            H * 4, std::max(H, qd) * 4, H * 4, qd * 4, kvd * 4, kvd * 4, qd * 4, kvd * 4, qd * 4,
+            c.ffn * 4ull, c.ffn * 4ull, c.ffn * 4ull, c.vocab * 4ull,
+            s.mv_partial_cap * 4, attnp * 4, kTickets * 4ull, kAmMaxWg * 4ull, kAmMaxWg * 4ull, 16,
+            nc * 4ull, nc * 4ull, 64, c.max_seq * 4ull};
+        size_t ab = 0;
+        for (size_t z : sizes) ab += align_up(z);
+        if (hipMalloc(&s.aarena, ab) != hipSuccess) {
+            destroy(h);
+            return set_error(XP_E_NOMEM, "xp_session_create: %zu activation bytes", ab);
+        }
+        (void)hipMemset(s.aarena, 0, ab);
+        p8 = s.aarena;
+        size_t si = 0;
+        auto nxt = [&]() { return take(sizes[si++]); };
+        s.x = (float*)nxt(); s.xb = (float*)nxt(); s.xb2 = (float*)nxt(); s.q_raw = (float*)nxt();
+        s.k_raw = (float*)nxt(); s.v = (float*)nxt(); s.q = (float*)nxt(); s.k = (float*)nxt();
+        s.att = (float*)nxt(); s.gate = (float*)nxt(); s.up = (float*)nxt(); s.hb = (float*)nxt();
+        s.logits = (float*)nxt(); s.mv_partial = (float*)nxt(); s.attn_part = (float*)nxt();
+        s.tickets = (uint32_t*)nxt(); s.am_val = (float*)nxt(); s.am_idx = (uint32_t*)nxt();
+        s.am_out = (float*)nxt(); s.cand_val = (float*)nxt(); s.cand_idx = (uint32_t*)nxt();
+        s.state = (uint32_t*)nxt(); s.hist = (uint32_t*)nxt();
+        if (hipHostMalloc(reinterpret_cast<void**>(&s.h_ids), size_t(c.max_seq) * 4) !=
+            hipSuccess) {
+            s.h_ids = nullptr;
+            destroy(h);
+            return set_error(XP_E_NOMEM, "xp_session_create: pinned staging");
+        }
+        if (hipDeviceSynchronize() != hipSuccess) {
+            destroy(h);
+            return set_error(XP_E_HIP, "xp_session_create: initialisation failed");
+        }
+    } catch (const std::bad_alloc&) {
+        destroy(h);
+        return set_error(XP_E_NOMEM, "xp_session_create: out of host memory");
+    }
+    *out = h;
+    return XP_OK;
+}
+
+int xp_session_destroy(xp_session* h) { return destroy(h); }
+
+int xp_session_upload(xp_session* h, int layer, int tensor, const void* host, size_t bytes) {
+    XP_REQUIRE(h && host, "null pointer");
+    Session& s = h->s;
+    const size_t need = tensor_bytes(s.cfg, layer, tensor);
+    XP_REQUIRE(need > 0, "no tensor %d at layer %d", tensor, layer);
+    XP_REQUIRE(bytes == need, "tensor %d at layer %d is %zu bytes, got %zu", tensor, layer, need,
+               bytes);
+    const bool sc = (tensor & XP_T_SCALES) != 0;
+    const int t = tensor & ~XP_T_SCALES;
+    void* dst = nullptr;
+    if (t == XP_T_LM_HEAD) dst = sc ? s.lm_s : s.lm_w;
+    else if (t == XP_T_FINAL_NORM) dst = s.final_norm;
+    else if (t <= XP_T_DOWN) dst = sc ? s.L[layer].s[t] : s.L[layer].w[t];
+    else dst = s.L[layer].norm[t - XP_T_ATTN_NORM];
+    XP_HIP(hipMemcpy(dst, host, bytes, hipMemcpyHostToDevice));
+    return XP_OK;
+}
+
+int xp_session_synthesize(xp_session* h, uint32_t seed) {
+    XP_REQUIRE(h, "null session");
+    Session& s = h->s;
+    std::vector<char> buf;
+    auto one = [&](int layer, int tensor) -> int {
+        const size_t b = tensor_bytes(s.cfg, layer, tensor);
+        buf.resize(b);
+        int rc = xp_synth_tensor(&s.cfg, seed, layer, tensor, buf.data(), b);
+        if (rc == XP_OK) rc = xp_session_upload(h, layer, tensor, buf.data(), b);
+        return rc;
+    };
+    try {
+        int rc;
+        for (uint32_t l = 0; l < s.cfg.n_layers; ++l) {
+            for (int m = 0; m < kNMat; ++m) {
+                if ((rc = one(int(l), m)) != XP_OK) return rc;
+                if ((rc = one(int(l), m | XP_T_SCALES)) != XP_OK) return rc;
+            }
+            for (int nn = 0; nn < kNNorm; ++nn)
+                if ((rc = one(int(l), XP_T_ATTN_NORM + nn)) != XP_OK) return rc;
+        }
+        if ((rc = one(-1, XP_T_LM_HEAD)) != XP_OK) return rc;
+        if ((rc = one(-1, XP_T_LM_HEAD | XP_T_SCALES)) != XP_OK) return rc;
+        return one(-1, XP_T_FINAL_NORM);
+    } catch (const std::bad_alloc&) {
+        return set_error(XP_E_NOMEM, "xp_session_synthesize: out of host memory");
+    }
+}
+
+int xp_session_kv_upload(xp_session* h, int layer, int which, uint32_t pos0, uint32_t n,
+                         const uint16_t* host) {
+    XP_REQUIRE(h && host, "null pointer");
+    Session& s = h->s;
+    XP_REQUIRE(layer >= 0 && uint32_t(layer) < s.cfg.n_layers && (which == 0 || which == 1),
+               "layer %d / which %d out of range", layer, which);
+    XP_REQUIRE(uint64_t(pos0) + n <= s.cfg.max_seq, "rows [%u, %u) exceed max_seq %u", pos0,
+               pos0 + n, s.cfg.max_seq);
+    const size_t row = size_t(s.cfg.n_kv_heads) * s.cfg.head_dim;
+    uint16_t* base = which ? s.L[layer].vc : s.L[layer].kc;
+    XP_HIP(hipMemcpy(base + row * pos0, host, row * n * 2, hipMemcpyHostToDevice));
+    return XP_OK;
+}
+
+int xp_session_kv_download(xp_session* h, int layer, int which, uint32_t pos0, uint32_t n,
+                           uint16_t* host) {
+    XP_REQUIRE(h && host, "null pointer");
+    Session& s = h->s;
+    XP_REQUIRE(layer >= 0 && uint32_t(layer) < s.cfg.n_layers && (which == 0 || which == 1),
+               "layer %d / which %d out of range", layer, which);
+    XP_REQUIRE(uint64_t(pos0) + n <= s.cfg.max_seq, "rows [%u, %u) exceed max_seq %u", pos0,
+               pos0 + n, s.cfg.max_seq);
+    const size_t row = size_t(s.cfg.n_kv_heads) * s.cfg.head_dim;
+    const uint16_t* base = which ? s.L[layer].vc : s.L[layer].kc;
+    XP_HIP(hipStreamSynchronize(s.st));
+    XP_HIP(hipMemcpy(host, base + row * pos0, row * n * 2, hipMemcpyDeviceToHost));
+    return XP_OK;
+}
+
+int xp_session_set_position(xp_session* h, uint32_t pos) {
+    XP_REQUIRE(h, "null session");
+    Session& s = h->s;
+    XP_REQUIRE(pos <= s.cfg.max_seq, "position %u > max_seq %u", pos, s.cfg.max_seq);
+    XP_HIP(hipStreamSynchronize(s.st));
+    s.pos = pos;
+    s.logits_valid = false;
+    XP_HIP(hipMemcpy(s.state, &pos, 4, hipMemcpyHostToDevice));
+    return XP_OK;
+}
+
+int xp_session_reset(xp_session* h) { return xp_session_set_position(h, 0); }
+
+int xp_session_prefill(xp_session* h, const uint32_t* ids, uint32_t n) {
+    XP_REQUIRE(h, "null session");
+    if (n == 0) return XP_OK;
+    XP_REQUIRE(ids, "ids is null");
+    Session& s = h->s;
+    XP_REQUIRE(uint64_t(s.pos) + n <= s.cfg.max_seq, "prompt exceeds max_seq (%u)",
+               s.cfg.max_seq);
+    for (uint32_t i = 0; i < n; ++i)
+        XP_REQUIRE(ids[i] < s.cfg.vocab, "token id %u is outside the vocabulary", ids[i]);
+    const double t0 = now_ms();
+    XP_HIP(hipStreamSynchronize(s.st));
+    std::memcpy(s.h_ids, ids, size_t(n) * 4);
+    const int last = s.cfg.sample_mode == 0 ? 1 : 2;
+    for (uint32_t i = 0; i < n; ++i) {
+        XP_HIP(hipMemcpyAsync(s.state + 1, s.h_ids + i, 4, hipMemcpyHostToDevice, s.st));
+        int rc = s.run(i + 1 == n ? last : 0);
+        if (rc != XP_OK) return rc;
+    }
+    XP_HIP(hipStreamSynchronize(s.st));
+    s.pos += n;
+    s.logits_valid = true;
+    const double ms = now_ms() - t0;
+    s.met = xp_metrics{ms, ms, 0.0, ms > 0 ? n * 1000.0 / ms : 0.0, s.pos, s.launches[0]};
+    return XP_OK;
+}
+
+int xp_session_decode_step(xp_session* h, uint32_t* token) {
+    XP_REQUIRE(h && token, "null pointer");
+    Session& s = h->s;
+    if (s.pos == 0 || !s.logits_valid)
+        return set_error(XP_E_STATE, "decode_step() before prefill() - there is no context to "
+                         "condition on");
+    if (s.pos >= s.cfg.max_seq)
+        return set_error(XP_E_STATE, "KV cache is full (max_seq %u)", s.cfg.max_seq);
+    const double t0 = now_ms();
+    double ts = 0;
+    int variant = 1;
+    if (s.cfg.sample_mode == 1) {
+        variant = 2;
+        uint32_t tok = 0;
+        int rc = sample_from_candidates(s, tok);
+        if (rc != XP_OK) return rc;
+        s.h_ids[0] = tok;
+        XP_HIP(hipMemcpyAsync(s.state + 1, s.h_ids, 4, hipMemcpyHostToDevice, s.st));
+        ts = now_ms() - t0;
+    }
+    const double t1 = now_ms();
+    int rc = s.run(variant);
+    if (rc != XP_OK) return rc;
+    XP_HIP(hipMemcpyAsync(s.h_ids + 1, s.hist + s.pos, 4, hipMemcpyDeviceToHost, s.st));
+    XP_HIP(hipStreamSynchronize(s.st));
+    *token = s.h_ids[1];
+    const double t2 = now_ms();
+    ++s.pos;
+    s.met = xp_metrics{t2 - t0, t2 - t1, ts, (t2 - t0) > 0 ? 1000.0 / (t2 - t0) : 0.0, s.pos,
+                       s.launches[variant]};
+    return XP_OK;
+}
+
+int xp_session_decode_steps(xp_session* h, uint32_t n, uint32_t* tokens) {
+    XP_REQUIRE(h, "null session");
+    if (n == 0) return XP_OK;
+    Session& s = h->s;
+    XP_REQUIRE(s.cfg.sample_mode == 0, "decode_steps queues greedy steps only");
+    if (s.pos == 0 || !s.logits_valid)
+        return set_error(XP_E_STATE, "decode_steps() before prefill()");
+    if (uint64_t(s.pos) + n > s.cfg.max_seq)
+        return set_error(XP_E_STATE, "KV cache is full (max_seq %u)", s.cfg.max_seq);
+    const double t0 = now_ms();
+    int rc = s.graph_for(1);
+    if (rc != XP_OK) return rc;
+    for (uint32_t i = 0; i < n; ++i) XP_HIP(hipGraphLaunch(s.graph[1], s.st));
+    XP_HIP(hipStreamSynchronize(s.st));
+    const double t1 = now_ms();
+    if (tokens) XP_HIP(hipMemcpy(tokens, s.hist + s.pos, size_t(n) * 4, hipMemcpyDeviceToHost));
+    s.pos += n;
+    s.met = xp_metrics{t1 - t0, t1 - t0, 0.0, (t1 - t0) > 0 ? n * 1000.0 / (t1 - t0) : 0.0, s.pos,
+                       s.launches[1]};
+    return XP_OK;
+}
+
+int xp_session_position(const xp_session* h, uint32_t* pos) {
+    XP_REQUIRE(h && pos, "null pointer");
+    *pos = h->s.pos;
+    return XP_OK;
+}
+
+int xp_session_last_logits(xp_session* h, float* host, uint32_t n) {
+    XP_REQUIRE(h && host, "null pointer");
+    Session& s = h->s;
+    XP_REQUIRE(n <= s.cfg.vocab, "n=%u > vocab %u", n, s.cfg.vocab);
+    XP_HIP(hipStreamSynchronize(s.st));
+    XP_HIP(hipMemcpy(host, s.logits, size_t(n) * 4, hipMemcpyDeviceToHost));
+    return XP_OK;
+}
+
+int xp_session_last_candidates(xp_session* h, float* val, uint32_t* idx, uint32_t n) {
+    XP_REQUIRE(h && val && idx, "null pointer");
+    Session& s = h->s;
+    XP_REQUIRE(s.cfg.sample_mode == 1, "the harvest runs in temperature mode only");
+    XP_REQUIRE(n <= 4 * s.cfg.topk_parts, "n=%u > %u candidates", n, 4 * s.cfg.topk_parts);
+    XP_HIP(hipStreamSynchronize(s.st));
+    XP_HIP(hipMemcpy(val, s.cand_val, size_t(n) * 4, hipMemcpyDeviceToHost));
+    XP_HIP(hipMemcpy(idx, s.cand_idx, size_t(n) * 4, hipMemcpyDeviceToHost));
+    return XP_OK;
+}
+
+int xp_session_last_metrics(const xp_session* h, xp_metrics* m) {
+    XP_REQUIRE(h && m, "null pointer");
+    *m = h->s.met;
+    return XP_OK;
+}
+
+int xp_session_weight_bytes(const xp_session* h, size_t* bytes) {
+    XP_REQUIRE(h && bytes, "null pointer");
+    *bytes = h->s.wbytes;
+    return XP_OK;
+}
+
+int xp_session_kv_bytes(const xp_session* h, size_t* bytes) {
+    XP_REQUIRE(h && bytes, "null pointer");
+    *bytes = h->s.kvbytes;
+    return XP_OK;
+}
+
+uint32_t xp_draw(float* val, uint32_t* idx, uint32_t n, float temperature, uint32_t top_k,
+                 float top_p, double u) {
+    if (!val || !idx) return 0;
+    return draw(val, idx, n, temperature, top_k, top_p, u);
+}
+
+double xp_philox_uniform(uint32_t seed, uint32_t seq, uint32_t step) {
+    return philox_uniform(seed, seq, step);
+}
+
+}  // extern "C"

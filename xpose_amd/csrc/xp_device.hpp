@@ -1,0 +1,102 @@
+// Device-side helpers shared by the gfx950 kernels: fp16/bf16 scale decode,
+// the int4 block dot, and wave-level reductions. Wave size is 64 throughout.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <hip/hip_fp16.h>
+
+#include <cstdint>
+
+namespace xp {
+
+constexpr int kWave = 64;
+
+// Native clang vectors: the nontemporal-load builtin needs them (HIP's uint4
+// is a struct).
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+// Streaming loads: weights are read exactly once per token.
+__device__ __forceinline__ u32x4 ld_stream4(const u32x4* p) {
+    return __builtin_nontemporal_load(p);
+}
+__device__ __forceinline__ u32x2 ld_stream2(const u32x2* p) {
+    return __builtin_nontemporal_load(p);
+}
+constexpr uint32_t kBlk = 32;   // quantisation block along k (BLK, llm_matvec.cl:25)
+constexpr uint32_t kGrp = 64;   // KM4 column-group width (GRP, llm_matvec.cl:26)
+
+// fp16 bits -> fp32. The hardware conversion is exact for every finite fp16
+// and for +-inf, which is what the reference's bit-surgery decoder computes
+// (kernels/llm_quant.cl:56-77); NaNs stay NaNs.
+__device__ __forceinline__ float f16_bits_to_f32(uint32_t h) {
+    return __half2float(__ushort_as_half(static_cast<unsigned short>(h & 0xFFFFu)));
+}
+
+// bf16 is the top half of an fp32 word (bf16lo/bf16hi, llm_matvec.cl:407-408).
+__device__ __forceinline__ float bf16lo(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float bf16hi(uint32_t w) { return __uint_as_float(w & 0xFFFF0000u); }
+
+// fp32 -> fp16 bits, round to nearest even (v_cvt_f16_f32 under the default
+// round-to-nearest mode).
+__device__ __forceinline__ uint16_t f32_to_f16_bits(float f) {
+    return __half_as_ushort(__float2half_rn(f));
+}
+
+// Byte n of a word as float: maps to v_cvt_f32_ubyte{0..3}.
+__device__ __forceinline__ float ub(uint32_t w, int n) {
+    return static_cast<float>((w >> (8 * n)) & 0xFFu);
+}
+
+// Sum over one 8-nibble word of nib_i * x_i, where the caller's activation
+// slice `xs` holds x for even i and x/16 for odd i. Masking the word with
+// 0x0F0F0F0F leaves the even nibbles as bytes; masking with 0xF0F0F0F0 leaves
+// 16 * (odd nibble) as bytes, and the /16 already applied to x makes the
+// product exact. Nibbles are the raw biased values 0..15; the caller folds
+// the -8 bias in as -8 * sum(x) per block.
+//
+// The empty asm hides the masks' provenance from the combiner, which would
+// otherwise rewrite each byte read into a 4-bit v_bfe plus a conversion; with
+// it every nibble costs one v_cvt_f32_ubyteN and one FMA.
+__device__ __forceinline__ uint32_t opaque(uint32_t v) {
+    asm("" : "+v"(v));
+    return v;
+}
+__device__ __forceinline__ float nib8_dot(uint32_t w, const float4 xa, const float4 xb,
+                                          float acc) {
+    const uint32_t lo = opaque(w & 0x0F0F0F0Fu);   // nibbles 0,2,4,6
+    const uint32_t hi = opaque(w & 0xF0F0F0F0u);   // 16 * nibbles 1,3,5,7
+    acc = fmaf(xa.x, ub(lo, 0), acc);
+    acc = fmaf(xa.y, ub(hi, 0), acc);
+    acc = fmaf(xa.z, ub(lo, 1), acc);
+    acc = fmaf(xa.w, ub(hi, 1), acc);
+    acc = fmaf(xb.x, ub(lo, 2), acc);
+    acc = fmaf(xb.y, ub(hi, 2), acc);
+    acc = fmaf(xb.z, ub(lo, 3), acc);
+    acc = fmaf(xb.w, ub(hi, 3), acc);
+    return acc;
+}
+
+// Wave-wide sum / max via DPP-backed shuffles.
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
+    return v;
+}
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, kWave));
+    return v;
+}
+
+// gelu_pytorch_tanh with the reference's clamped-exp tanh
+// (kernels/llm_transformer.cl:213-231). expf is the device libm exp.
+__device__ __forceinline__ float gelu_tanh(float g) {
+    float z = 0.7978845608028654f * (g + 0.044715f * g * g * g);
+    z = fminf(fmaxf(z, -10.0f), 10.0f);
+    const float e = expf(-2.0f * z);
+    const float t = (1.0f - e) / (1.0f + e);
+    return 0.5f * g * (1.0f + t);
+}
+
+}  // namespace xp
