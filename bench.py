@@ -1,0 +1,201 @@
+"""Benchmark: Gemma-3-1B int4 batch-1 greedy decode at context 4096 on one
+MI355X (BASELINE config 4 shape), plus the int4 matvec HBM roofline leg and
+the CPU baseline (the oracle's C restatement on the host cores).
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--ctx 4096]
+                    [--cpu-seconds S] [--no-cpu]
+
+A step is one decode token: embed, 26 layers, final norm, the 262144-wide
+lm_head and the on-device argmax that picks the next token. Weights (random
+int4, fp16 group scales) and the KV cache (fp16 N(0,1) rows 0..ctx-1) are
+resident in HBM before timing; the K timed steps are queued back to back
+between two device synchronisations. Prints one JSON line.
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes as C
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0          # MI355X HBM3E
+SEED = 0x5EED0003
+# Algorithmic HBM bytes of one token at seq_len s (weights + fp16 scales,
+# KV reads, norm weights, logits write + argmax read, KV append).
+WEIGHT_BYTES = 562_360_320
+NORM_BYTES = 537_088
+LOGIT_BYTES = 2_097_152
+APPEND_BYTES = 13_312
+
+
+def token_bytes(seq_len: int) -> int:
+    kv = 1024 * (4 * seq_len + 22 * min(seq_len, 512))
+    return WEIGHT_BYTES + kv + NORM_BYTES + LOGIT_BYTES + APPEND_BYTES
+
+
+def lm_head_bytes(rows=1152, cols=262144) -> int:
+    return rows * cols // 2 + (rows // 32) * cols * 2 + rows * 4 + cols * 4
+
+
+def matvec_leg(X, rows: int, cols: int, copies: int, iters: int):
+    """Average per-launch time of xp_mv_int4 over `iters` back-to-back launches
+    cycling `copies` distinct weight planes (> 256 MB in total so the
+    Infinity Cache cannot serve them), HIP events on the launch stream."""
+    wq = X.synth_nibbles(rows, cols, SEED, 901)
+    sc = X.synth_scales(rows, cols, SEED, 902)
+    x = X.synth_normal(rows, SEED, 903)
+    dws = [X.DeviceBuffer.from_array(wq) for _ in range(copies)]
+    dss = [X.DeviceBuffer.from_array(sc) for _ in range(copies)]
+    dx = X.DeviceBuffer.from_array(x)
+    dout = X.DeviceBuffer(cols * 4)
+    st = C.c_void_p()
+    X.call("xp_stream_create", C.byref(st))
+    W = (C.c_void_p * copies)(*[d.ptr for d in dws])
+    S = (C.c_void_p * copies)(*[d.ptr for d in dss])
+    ms = C.c_float()
+    X.call("xp_mv_int4_timed", dout.vp, dx.vp, W, S, copies, X.XP_SCALE_F16_QUAD, rows, cols, 0,
+           iters, st, C.byref(ms))
+    X.call("xp_stream_destroy", st)
+    per_s = ms.value / 1e3 / iters
+    nbytes = rows * cols // 2 + (rows // 32) * cols * 2 + rows * 4 + cols * 4
+    return nbytes, per_s
+
+
+def cpu_baseline(X, cfg, ctx: int, seconds: float, threads: int):
+    """The oracle (C restatement, OpenMP over output columns) decoding greedy
+    tokens of the same model from position ctx, for about `seconds`."""
+    import oracle
+    tensors = {}
+    for l in range(cfg.n_layers):
+        for m in X.MATRICES:
+            tensors[(l, m)] = X.synth_tensor(cfg, SEED, l, m)
+            tensors[(l, m | X.T_SCALES)] = X.synth_tensor(cfg, SEED, l, m | X.T_SCALES)
+        for n in X.NORMS:
+            tensors[(l, n)] = X.synth_tensor(cfg, SEED, l, n)
+    for k in (X.T_LM_HEAD, X.T_LM_HEAD | X.T_SCALES, X.T_FINAL_NORM):
+        tensors[(-1, k)] = X.synth_tensor(cfg, SEED, -1, k)
+    model = oracle.OracleModel(cfg, lambda l, k: tensors[(l, k)])
+    kvd = cfg.n_kv_heads * cfg.head_dim
+    for l in range(cfg.n_layers):
+        model.kcache[l][:ctx * kvd] = X.synth_normal_f16(ctx * kvd, ctx, 2 * l)
+        model.vcache[l][:ctx * kvd] = X.synth_normal_f16(ctx * kvd, ctx, 2 * l + 1)
+    lg = model.forward(4242, ctx, True, threads)
+    pos, n, t0 = ctx + 1, 0, time.perf_counter()
+    while True:
+        tok = oracle.argmax_tree(lg)[0]
+        lg = model.forward(tok, pos, True, threads)
+        pos += 1
+        n += 1
+        el = time.perf_counter() - t0
+        if el >= seconds or n >= 1000:
+            break
+    return n / el, n, el
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=64)
+    ap.add_argument("--warmup", type=int, default=8)
+    ap.add_argument("--ctx", type=int, default=4096)
+    ap.add_argument("--cpu-seconds", type=float, default=15.0)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--mv-iters", type=int, default=60)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported "
+              "(the batch-1 decode path does not shard, see DESIGN.md)", file=sys.stderr)
+        return 2
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if world != 1:
+        print("bench.py: launched with WORLD_SIZE != 1; this build measures one GPU",
+              file=sys.stderr)
+        return 2
+
+    import xpose_amd as X
+    X.init(0)
+    info = X.device_info()
+    ctx = args.ctx
+    cfg = X.XpConfig.gemma3_1b(max_seq=8192)
+    if ctx + 1 + args.warmup + args.steps > cfg.max_seq:
+        print("bench.py: ctx + steps exceed max_seq 8192", file=sys.stderr)
+        return 2
+
+    sess = X.DecodeSession(cfg)
+    sess.synthesize(SEED)
+    kvd = cfg.n_kv_heads * cfg.head_dim
+    for l in range(cfg.n_layers):
+        sess.kv_upload(l, 0, 0, X.synth_normal_f16(ctx * kvd, ctx, 2 * l))
+        sess.kv_upload(l, 1, 0, X.synth_normal_f16(ctx * kvd, ctx, 2 * l + 1))
+    sess.set_position(ctx)
+    sess.prefill([4242])                    # runs position ctx, leaves logits
+    if args.warmup:
+        sess.decode_steps(args.warmup)
+    X.synchronize()
+    t0 = time.perf_counter()
+    ids = sess.decode_steps(args.steps)
+    X.synchronize()
+    el = time.perf_counter() - t0
+    tok_s = args.steps / el
+    ms_step = el * 1e3 / args.steps
+    mid_seq = ctx + 1 + args.warmup + args.steps // 2
+    tb = token_bytes(mid_seq)
+    launches = sess.last_metrics().launches
+    sess.close()
+
+    # Roofline leg: the dominant kernel of the step, the lm_head int4 matvec.
+    nbytes, per_s = matvec_leg(X, 1152, 262144, copies=3, iters=args.mv_iters)
+    achieved = nbytes / per_s / 1e9
+    # BASELINE config 1 shape (gate 6912 x 1152), 64 rotating copies.
+    nb1, per1 = matvec_leg(X, 1152, 6912, copies=64, iters=640)
+
+    cpu = None
+    if not args.no_cpu:
+        threads = min(16, os.cpu_count() or 1)
+        cpu_tok_s, n_cpu, cpu_el = cpu_baseline(X, cfg, ctx, args.cpu_seconds, threads)
+        cpu = {"value": round(cpu_tok_s, 3), "unit": "tok/s", "cores": threads, "kind": "port",
+               "sample": f"{n_cpu} greedy decode steps of the same Gemma-3-1B int4 model from "
+                         f"position {ctx + 1} (KV pre-filled), oracle C restatement, "
+                         f"{threads} OpenMP threads, {cpu_el:.1f} s"}
+
+    line = {
+        "metric": "decode tok/s Gemma-3-1B int4 bs=1 @ctx 4096; int4 matvec HBM GB/s vs peak",
+        "value": round(tok_s, 2),
+        "unit": "tok/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (random int4 weights, fp16 group-32 scales, fp16 KV N(0,1))",
+        "config": {"workload": "gemma3-1b-int4-greedy-decode", "ctx": ctx, "batch": 1,
+                   "layers": 26, "hidden": 1152, "vocab": 262144, "weights": "int4 g32 + fp16",
+                   "kv": "fp16", "launches_per_step": launches},
+        "roofline": {"bound": "hbm", "kernel": "mv_int4 lm_head 1152x262144",
+                     "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "bytes_per_launch": nbytes, "us_per_launch": round(per_s * 1e6, 3)},
+        "token_roofline": {"bytes_per_token": tb, "roofline_tok_s": round(HBM_PEAK_GBS * 1e9 / tb, 1),
+                           "frac": round(tok_s * tb / (HBM_PEAK_GBS * 1e9), 4)},
+        "matvec_cfg1": {"shape": "6912x1152", "bytes": nb1, "us_per_launch": round(per1 * 1e6, 3),
+                        "GBs": round(nb1 / per1 / 1e9, 1)},
+        "cpu_baseline": cpu,
+        "device": info["arch"],
+        "ids_head": [int(v) for v in ids[:4]],
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

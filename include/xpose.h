@@ -99,6 +99,14 @@ int xp_mv_int4_multi(uint32_t n, float* const* outs, const float* in,
                      const uint32_t* cols, int scale_fmt, uint32_t rows,
                      xp_stream stream);
 
+/* Measurement: `iters` back-to-back xp_mv_int4 launches on `stream`, cycling
+ * through `ncopies` weight/scale planes (so each launch streams from HBM),
+ * bracketed by HIP events; *ms = elapsed time of the whole loop. */
+int xp_mv_int4_timed(float* out, const float* in, const void* const* wqs,
+                     const void* const* scales, uint32_t ncopies, int scale_fmt,
+                     uint32_t rows, uint32_t cols, uint32_t split, uint32_t iters,
+                     xp_stream stream, float* ms);
+
 /* Debug/unpack entry: expands a KM4 nibble plane to int8 weights w[k*cols+j]
  * = nibble - 8 (row-major [rows][cols]), for bit-exact unpack checks. */
 int xp_unpack_km4(int8_t* out, const void* wq, uint32_t rows, uint32_t cols,

@@ -91,7 +91,9 @@ __device__ __forceinline__ float block_dot(const u32x4 w, const float* xb, float
     return (pa + pb) - 8.0f * xsum;
 }
 
-template <int FMT>
+// SPLIT = false: one chunk covers all of k (the wide lm_head shape); no
+// partials, no ticket. A separate instantiation so profiles name it apart.
+template <int FMT, bool SPLIT>
 __global__ __launch_bounds__(kMvWaves * kWave) void mv_int4_kernel(MvArgs a) {
     extern __shared__ float smem[];
     const uint32_t wave = threadIdx.x / kWave;
@@ -173,23 +175,31 @@ __global__ __launch_bounds__(kMvWaves * kWave) void mv_int4_kernel(MvArgs a) {
         }
     }
 
-    if (a.split == 1) {
+    if constexpr (!SPLIT) {
         out[j] = acc;
         return;
     }
     const size_t stride = size_t(a.groups) * kGrp;
-    a.partial[size_t(s) * stride + size_t(gg) * kGrp + lane] = acc;
-    __threadfence();
+    st_dev(a.partial + size_t(s) * stride + size_t(gg) * kGrp + lane, acc);
+    wait_mem();
     uint32_t old = 0;
-    if (lane == 0) old = atomicAdd(&a.tickets[gg], 1u);
+    if (lane == 0) old = take_ticket(&a.tickets[gg]);
     old = __shfl(old, 0, kWave);
     if (old != a.split - 1) return;
-    __threadfence();
+    // Batches of 8 independent loads, summed in ascending chunk order.
+    const float* pp = a.partial + size_t(gg) * kGrp + lane;
     float sum = 0.0f;
-    for (uint32_t p = 0; p < a.split; ++p)
-        sum += __builtin_nontemporal_load(a.partial + size_t(p) * stride + size_t(gg) * kGrp + lane);
+    uint32_t p = 0;
+    for (; p + 8 <= a.split; p += 8) {
+        float v[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) v[i] = ld_dev(pp + size_t(p + i) * stride);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) sum += v[i];
+    }
+    for (; p < a.split; ++p) sum += ld_dev(pp + size_t(p) * stride);
     out[j] = sum;
-    if (lane == 0) a.tickets[gg] = 0u;
+    if (lane == 0) st_dev(&a.tickets[gg], 0u);
 }
 
 __global__ void unpack_km4_kernel(int8_t* out, const u32x4* wq, uint32_t rows, uint32_t cols) {
@@ -213,9 +223,13 @@ __global__ void fp16_decode_kernel(float* out, const uint16_t* src, uint32_t n) 
 
 namespace {
 
+// Enough tasks to give every CU several waves, but at most 16 chunks: the
+// last chunk of a group to finish reads every partial, in batches of 8
+// loads at device-coherence latency, so its tail grows with the split.
 uint32_t choose_split(uint32_t groups, uint32_t nquads, int n_cu) {
     const uint32_t target = uint32_t(n_cu > 0 ? n_cu : 256) * 8u;   // ~8 tasks per CU
     uint32_t split = (target + groups - 1) / groups;
+    if (split > 16) split = 16;
     if (split < 1) split = 1;
     if (split > nquads) split = nquads;
     return split;
@@ -303,17 +317,17 @@ int launch_mv(const MvMatDesc* mats, uint32_t n, const float* x, int fmt, uint32
         return set_error(XP_E_ARG, "%s: k-chunk of %u quads needs %zu B of LDS (> 64 KiB); "
                          "pass a larger split", who, a.qpc, lds);
     const dim3 grid(a.wg_per_chunk * a.split), block(kMvWaves * kWave);
+#define XP_MV_LAUNCH(F)                                                                    \
+    if (a.split > 1)                                                                       \
+        hipLaunchKernelGGL((mv_int4_kernel<F, true>), grid, block, lds, st, a);            \
+    else                                                                                   \
+        hipLaunchKernelGGL((mv_int4_kernel<F, false>), grid, block, lds, st, a);
     switch (fmt) {
-        case XP_SCALE_F16_QUAD:
-            hipLaunchKernelGGL(mv_int4_kernel<XP_SCALE_F16_QUAD>, grid, block, lds, st, a);
-            break;
-        case XP_SCALE_BF16_QUAD:
-            hipLaunchKernelGGL(mv_int4_kernel<XP_SCALE_BF16_QUAD>, grid, block, lds, st, a);
-            break;
-        default:
-            hipLaunchKernelGGL(mv_int4_kernel<XP_SCALE_F32>, grid, block, lds, st, a);
-            break;
+        case XP_SCALE_F16_QUAD: XP_MV_LAUNCH(XP_SCALE_F16_QUAD) break;
+        case XP_SCALE_BF16_QUAD: XP_MV_LAUNCH(XP_SCALE_BF16_QUAD) break;
+        default: XP_MV_LAUNCH(XP_SCALE_F32) break;
     }
+#undef XP_MV_LAUNCH
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return set_error(XP_E_HIP, "%s: launch -> %s", who, hipGetErrorString(e));
     return XP_OK;
@@ -341,6 +355,32 @@ int xp_mv_int4_multi(uint32_t n, float* const* outs, const float* in, const void
     for (uint32_t i = 0; i < n; ++i) m[i] = MvMatDesc{outs[i], wqs[i], scales[i], cols[i]};
     return launch_mv(m, n, in, scale_fmt, rows, 0, nullptr, 0, nullptr, 0, as_stream(stream),
                      "xp_mv_int4_multi");
+}
+
+int xp_mv_int4_timed(float* out, const float* in, const void* const* wqs,
+                     const void* const* scales, uint32_t ncopies, int scale_fmt, uint32_t rows,
+                     uint32_t cols, uint32_t split, uint32_t iters, xp_stream stream, float* ms) {
+    XP_REQUIRE(wqs && scales && ms && ncopies > 0 && iters > 0, "bad arguments");
+    hipStream_t st = as_stream(stream);
+    hipEvent_t e0 = nullptr, e1 = nullptr;
+    XP_HIP(hipEventCreate(&e0));
+    XP_HIP(hipEventCreate(&e1));
+    int rc = XP_OK;
+    // One untimed pass over every copy so scratch is sized before timing.
+    for (uint32_t i = 0; i < ncopies && rc == XP_OK; ++i)
+        rc = xp_mv_int4(out, in, wqs[i], scales[i], scale_fmt, rows, cols, split, stream);
+    if (rc == XP_OK && hipStreamSynchronize(st) != hipSuccess) rc = set_error(XP_E_HIP, "sync");
+    if (rc == XP_OK && hipEventRecord(e0, st) != hipSuccess) rc = set_error(XP_E_HIP, "event");
+    for (uint32_t i = 0; i < iters && rc == XP_OK; ++i)
+        rc = xp_mv_int4(out, in, wqs[i % ncopies], scales[i % ncopies], scale_fmt, rows, cols,
+                        split, stream);
+    if (rc == XP_OK && hipEventRecord(e1, st) != hipSuccess) rc = set_error(XP_E_HIP, "event");
+    if (rc == XP_OK && hipEventSynchronize(e1) != hipSuccess) rc = set_error(XP_E_HIP, "sync");
+    if (rc == XP_OK && hipEventElapsedTime(ms, e0, e1) != hipSuccess)
+        rc = set_error(XP_E_HIP, "elapsed");
+    (void)hipEventDestroy(e0);
+    (void)hipEventDestroy(e1);
+    return rc;
 }
 
 int xp_unpack_km4(int8_t* out, const void* wq, uint32_t rows, uint32_t cols, xp_stream stream) {

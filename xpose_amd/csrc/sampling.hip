@@ -65,19 +65,17 @@ __global__ __launch_bounds__(kAmThreads) void argmax_kernel(AmArgs a) {
     __syncthreads();
     if (tid == 0) {
         for (int w = 1; w < kAmThreads / kWave; ++w) am_better(bv, bi, sv[w], si[w]);
-        a.pval[blockIdx.x] = bv;
-        a.pidx[blockIdx.x] = bi;
-        __threadfence();
-        last = atomicAdd(a.ticket, 1u);
+        st_dev(a.pval + blockIdx.x, bv);
+        st_dev(a.pidx + blockIdx.x, bi);
+        wait_mem();
+        last = take_ticket(a.ticket);
     }
     __syncthreads();
     if (last != gridDim.x - 1) return;
-    __threadfence();
     bv = -INFINITY;
     bi = 0u;
     for (uint32_t w = tid; w < gridDim.x; w += blockDim.x)
-        am_better(bv, bi, __builtin_nontemporal_load(a.pval + w),
-                  __builtin_nontemporal_load(a.pidx + w));
+        am_better(bv, bi, ld_dev(a.pval + w), ld_dev(a.pidx + w));
     am_wave(bv, bi);
     __syncthreads();
     if (tid % kWave == 0) { sv[tid / kWave] = bv; si[tid / kWave] = bi; }
@@ -86,7 +84,7 @@ __global__ __launch_bounds__(kAmThreads) void argmax_kernel(AmArgs a) {
         for (int w = 1; w < kAmThreads / kWave; ++w) am_better(bv, bi, sv[w], si[w]);
         *a.out_idx = bi;
         if (a.out_val) *a.out_val = bv;
-        *a.ticket = 0u;
+        st_dev(a.ticket, 0u);
     }
 }
 

@@ -19,6 +19,7 @@
 #include <algorithm>
 #include <chrono>
 #include <cmath>
+#include <cstdlib>
 #include <cstring>
 #include <new>
 #include <vector>
@@ -104,10 +105,14 @@ int check_config(const xp_config& c) {
                          "multiples of 128", c.hidden, c.ffn, c.n_heads * c.head_dim);
     if (c.vocab % 64 || (c.n_kv_heads * c.head_dim) % 64)
         return set_error(XP_E_ARG, "config: vocab and kv_dim must be multiples of 64");
-    if (c.head_dim % 64 || c.head_dim > 512 || c.n_heads % c.n_kv_heads ||
-        c.n_heads / c.n_kv_heads > 8)
-        return set_error(XP_E_ARG, "config: head_dim=%u (multiple of 64, <= 512), heads %u/%u "
-                         "(<= 8 per kv head)", c.head_dim, c.n_heads, c.n_kv_heads);
+    const uint32_t grp = c.n_heads % c.n_kv_heads ? 0 : c.n_heads / c.n_kv_heads;
+    if ((c.head_dim != 64 && c.head_dim != 128 && c.head_dim != 256 && c.head_dim != 512) ||
+        (grp != 1 && grp != 2 && grp != 4 && grp != 8) || (grp == 8 && c.head_dim == 512))
+        return set_error(XP_E_ARG, "config: head_dim=%u (64/128/256/512), heads %u over %u kv "
+                         "heads (1, 2, 4 or 8 per kv head)", c.head_dim, c.n_heads, c.n_kv_heads);
+    if (c.max_seq > 8192)
+        return set_error(XP_E_ARG, "config: max_seq=%u > 8192 (the attention split plan's "
+                         "limit)", c.max_seq);
     if (c.hidden > 8192)
         return set_error(XP_E_ARG, "config: hidden=%u > 8192", c.hidden);
     if (c.scale_fmt != XP_SCALE_F16_QUAD && c.scale_fmt != XP_SCALE_BF16_QUAD &&
@@ -158,6 +163,7 @@ struct Session {
     uint32_t* h_ids = nullptr;   // pinned staging for host-chosen token ids
     hipGraphExec_t graph[3] = {nullptr, nullptr, nullptr};   // prefill, greedy, harvest
     uint32_t launches[3] = {0, 0, 0};
+    bool use_graph = true;       // XP_SESSION_NO_GRAPH=1 launches each kernel directly
     uint32_t pos = 0;
     uint32_t step = 0;           // draws made (Philox counter)
     bool logits_valid = false;
@@ -271,6 +277,12 @@ int Session::graph_for(int variant) {
 }
 
 int Session::run(int variant) {
+    if (!use_graph) {
+        uint32_t n = 0;
+        const int r = record(variant, n);
+        launches[variant] = n;
+        return r;
+    }
     int rc = graph_for(variant);
     if (rc != XP_OK) return rc;
     XP_HIP(hipGraphLaunch(graph[variant], st));
@@ -434,6 +446,7 @@ int xp_session_create(const xp_config* cfg, xp_session** out) {
     Session& s = h->s;
     s.cfg = *cfg;
     const xp_config& c = s.cfg;
+    if (const char* e = std::getenv("XP_SESSION_NO_GRAPH")) s.use_graph = (e[0] == '\0' || e[0] == '0');
     try {
         int dev = 0;
         hipDeviceProp_t p;
@@ -699,9 +712,10 @@ int xp_session_decode_steps(xp_session* h, uint32_t n, uint32_t* tokens) {
     if (uint64_t(s.pos) + n > s.cfg.max_seq)
         return set_error(XP_E_STATE, "KV cache is full (max_seq %u)", s.cfg.max_seq);
     const double t0 = now_ms();
-    int rc = s.graph_for(1);
-    if (rc != XP_OK) return rc;
-    for (uint32_t i = 0; i < n; ++i) XP_HIP(hipGraphLaunch(s.graph[1], s.st));
+    for (uint32_t i = 0; i < n; ++i) {
+        int rc = s.run(1);
+        if (rc != XP_OK) return rc;
+    }
     XP_HIP(hipStreamSynchronize(s.st));
     const double t1 = now_ms();
     if (tokens) XP_HIP(hipMemcpy(tokens, s.hist + s.pos, size_t(n) * 4, hipMemcpyDeviceToHost));

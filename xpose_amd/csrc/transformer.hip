@@ -128,17 +128,23 @@ __global__ __launch_bounds__(256) void qk_norm_rope_append_kernel(QkArgs a, Rope
 }
 
 // ---- decode attention (split-span, fp16 KV) ----------------------------------
-// Grid: (nsplit, kv_heads). Workgroup (s, g) scores keys
-// [kv_start + s*chunk, ...) against the `group` query heads that share kv head
-// g, reading each key and value once (the mq4 idea, llm_transformer.cl:
-// 418-464, 499-557). It writes per-split (max, sum of exp, unnormalised o);
-// the last workgroup of kv head g to finish (arrival ticket) combines the
-// splits in ascending order — the online-softmax rescale of
-// softmax_rows_finish (llm_transformer.cl:385-405).
-constexpr int kAttnThreads = 256;
-constexpr int kAttnChunk   = 32;    // keys per workgroup
-constexpr int kAttnMaxGrp  = 8;     // query heads per kv head
-
+// Grid: (nsplit, kv_heads). Workgroup (s, g) takes a contiguous chunk of the
+// attended keys [kv_start + s*chunk, ...) for the G query heads that share kv
+// head g, reading every key and value once for all G heads (the mq4 idea,
+// llm_transformer.cl:418-464, 499-557):
+//   scores  head_dim/8 threads per key, 16-byte fp16 loads, q held in
+//           registers, shuffle reduction; several keys in flight per thread
+//   softmax one wave per head over the chunk (max, exp, sum)
+//   values  head_dim/2 threads per key, 4-byte loads, several keys in flight
+// Each split publishes (max, sum of exp, unnormalised o) per head; the last
+// workgroup of kv head g to arrive (arrival ticket) rescales and sums the
+// splits in ascending order — softmax_rows_finish's online combine
+// (llm_transformer.cl:385-405). One split writes the normalised output.
+constexpr int kAttnThreads  = 256;
+constexpr int kAttnMinChunk = 32;    // keys per workgroup at short spans
+constexpr int kAttnChunk    = 128;   // most keys one workgroup takes
+constexpr int kAttnMaxSplit = 64;    // workgroups per kv head
+constexpr int kAttnMaxGrp   = 8;     // query heads per kv head
 
 __device__ __forceinline__ void attn_range(const AttnArgs& a, uint32_t& span, uint32_t& kv0) {
     if (a.pos_dev) {
@@ -151,98 +157,184 @@ __device__ __forceinline__ void attn_range(const AttnArgs& a, uint32_t& span, ui
     }
 }
 
+template <int G, int HD>
 __global__ __launch_bounds__(kAttnThreads) void attention_decode_kernel(AttnArgs a) {
-    __shared__ float qs[kAttnMaxGrp * kMaxHeadDim];
-    __shared__ float ps[kAttnMaxGrp * kAttnChunk];
-    __shared__ float stat[kAttnMaxGrp * 2];
+    constexpr int TPK = HD / 8;                 // threads per key (scores)
+    constexpr int KPP = kAttnThreads / TPK;     // keys per pass (scores)
+    constexpr int TPV = HD / 2;                 // threads per key (values)
+    constexpr int KPV = kAttnThreads / TPV;     // keys per pass (values)
+    constexpr int ROW = 2 + HD;
+    __shared__ float ps[G * kAttnChunk];
+    __shared__ float red[KPV * G * HD];
+    __shared__ float mstat[G], lstat[G];
+    __shared__ float fs[kAttnMaxSplit * G];
+    __shared__ float ls[kAttnMaxSplit * G];
     __shared__ uint32_t last;
     uint32_t span, kv0;
     attn_range(a, span, kv0);
     const uint32_t g = blockIdx.y, s = blockIdx.x;
-    const uint32_t G = a.group, hd = a.head_dim;
     const uint32_t chunk = (span + a.nsplit - 1) / a.nsplit;
     const uint32_t j0 = s * chunk;
     const uint32_t j1 = min(j0 + chunk, span);
-    const uint32_t nk = j1 > j0 ? j1 - j0 : 0;
-    const uint32_t tid = threadIdx.x, wave = tid / kWave, lane = tid % kWave;
-    const uint32_t rowlen = 2 + hd;
-    float* part = a.part + (size_t(g) * a.nsplit + s) * G * rowlen;
+    const int nk = j1 > j0 ? int(j1 - j0) : 0;
+    const int tid = threadIdx.x;
+    const size_t rowstride = size_t(a.kv_heads) * HD;   // fp16 elements per cache row
+    const uint16_t* kbase = a.kc + size_t(kv0 + j0) * rowstride + size_t(g) * HD;
+    const uint16_t* vbase = a.vc + size_t(kv0 + j0) * rowstride + size_t(g) * HD;
 
-    for (uint32_t i = tid; i < G * hd; i += blockDim.x)
-        qs[i] = a.q[size_t(g) * G * hd + i];   // heads g*G .. g*G+G-1 are contiguous
-    __syncthreads();
-
-    // Scores: each wave takes keys j0+wave, j0+wave+4, ...; a lane covers
-    // head_dim/64 consecutive dims of the key.
-    const uint32_t per = hd / kWave;   // dims per lane (4 for head_dim 256)
-    for (uint32_t jj = wave; jj < nk; jj += kAttnThreads / kWave) {
-        const uint16_t* kr = a.kc + (size_t(kv0 + j0 + jj) * a.kv_heads + g) * hd + lane * per;
-        float kf[kMaxHeadDim / kWave];
-        for (uint32_t e = 0; e < per; ++e) kf[e] = f16_bits_to_f32(kr[e]);
-        for (uint32_t h = 0; h < G; ++h) {
-            float acc = 0.0f;
-            for (uint32_t e = 0; e < per; ++e) acc = fmaf(qs[h * hd + lane * per + e], kf[e], acc);
-            acc = wave_sum(acc);
-            if (lane == 0) ps[h * kAttnChunk + jj] = acc * a.scale;
+    // ---- scores
+    {
+        const int sub = tid % TPK, kp = tid / TPK;
+        float q[G][8];
+#pragma unroll
+        for (int h = 0; h < G; ++h)
+#pragma unroll
+            for (int e = 0; e < 8; ++e) q[h][e] = a.q[(size_t(g) * G + h) * HD + sub * 8 + e];
+        for (int base = 0; base < nk; base += 4 * KPP) {
+            u32x4 kw[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const int j = base + u * KPP + kp;
+                kw[u] = (j < nk) ? *reinterpret_cast<const u32x4*>(kbase + size_t(j) * rowstride + sub * 8)
+                                 : u32x4{0u, 0u, 0u, 0u};
+            }
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const int j = base + u * KPP + kp;
+                float kf[8];
+                kf[0] = f16_bits_to_f32(kw[u].x); kf[1] = f16_bits_to_f32(kw[u].x >> 16);
+                kf[2] = f16_bits_to_f32(kw[u].y); kf[3] = f16_bits_to_f32(kw[u].y >> 16);
+                kf[4] = f16_bits_to_f32(kw[u].z); kf[5] = f16_bits_to_f32(kw[u].z >> 16);
+                kf[6] = f16_bits_to_f32(kw[u].w); kf[7] = f16_bits_to_f32(kw[u].w >> 16);
+#pragma unroll
+                for (int h = 0; h < G; ++h) {
+                    float d = 0.0f;
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) d = fmaf(q[h][e], kf[e], d);
+#pragma unroll
+                    for (int o = TPK / 2; o > 0; o >>= 1) d += __shfl_xor(d, o, kWave);
+                    if (sub == 0 && j < nk) ps[h * kAttnChunk + j] = d * a.scale;
+                }
+            }
         }
     }
     __syncthreads();
-    // Chunk softmax statistics per head (unnormalised).
-    if (tid < G) {
+    // ---- chunk softmax, one wave per head
+    for (int h = tid / kWave; h < G; h += kAttnThreads / kWave) {
+        const int l = tid % kWave;
         float m = -INFINITY;
-        for (uint32_t jj = 0; jj < nk; ++jj) m = fmaxf(m, ps[tid * kAttnChunk + jj]);
-        float l = 0.0f;
-        for (uint32_t jj = 0; jj < nk; ++jj) {
-            const float e = expf(ps[tid * kAttnChunk + jj] - m);
-            ps[tid * kAttnChunk + jj] = e;
-            l += e;
+        for (int j = l; j < nk; j += kWave) m = fmaxf(m, ps[h * kAttnChunk + j]);
+        m = wave_max(m);
+        float sum = 0.0f;
+        for (int j = l; j < nk; j += kWave) {
+            const float e = expf(ps[h * kAttnChunk + j] - m);
+            ps[h * kAttnChunk + j] = e;
+            sum += e;
         }
-        stat[2 * tid] = m;
-        stat[2 * tid + 1] = l;
+        sum = wave_sum(sum);
+        if (l == 0) { mstat[h] = m; lstat[h] = sum; }
     }
     __syncthreads();
-    // Weighted values: thread d accumulates dim d for every head.
-    for (uint32_t d = tid; d < hd; d += blockDim.x) {
-        float o[kAttnMaxGrp];
-        for (uint32_t h = 0; h < G; ++h) o[h] = 0.0f;
-        for (uint32_t jj = 0; jj < nk; ++jj) {
-            const float v = f16_bits_to_f32(a.vc[(size_t(kv0 + j0 + jj) * a.kv_heads + g) * hd + d]);
-            for (uint32_t h = 0; h < G; ++h) o[h] = fmaf(ps[h * kAttnChunk + jj], v, o[h]);
+    // ---- weighted values
+    {
+        const int dp = tid % TPV, ks = tid / TPV;
+        float o[G][2];
+#pragma unroll
+        for (int h = 0; h < G; ++h) o[h][0] = o[h][1] = 0.0f;
+        for (int base = 0; base < nk; base += 4 * KPV) {
+            uint32_t vw[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const int j = base + u * KPV + ks;
+                vw[u] = (j < nk) ? *reinterpret_cast<const uint32_t*>(vbase + size_t(j) * rowstride + dp * 2)
+                                 : 0u;
+            }
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const int j = base + u * KPV + ks;
+                if (j < nk) {
+                    const float v0 = f16_bits_to_f32(vw[u]), v1 = f16_bits_to_f32(vw[u] >> 16);
+#pragma unroll
+                    for (int h = 0; h < G; ++h) {
+                        const float p = ps[h * kAttnChunk + j];
+                        o[h][0] = fmaf(p, v0, o[h][0]);
+                        o[h][1] = fmaf(p, v1, o[h][1]);
+                    }
+                }
+            }
         }
-        for (uint32_t h = 0; h < G; ++h) part[h * rowlen + 2 + d] = o[h];
+#pragma unroll
+        for (int h = 0; h < G; ++h) {
+            red[(ks * G + h) * HD + dp * 2] = o[h][0];
+            red[(ks * G + h) * HD + dp * 2 + 1] = o[h][1];
+        }
+    }
+    __syncthreads();
+    if (a.nsplit == 1) {
+        for (int i = tid; i < G * HD; i += kAttnThreads) {
+            const int h = i / HD;
+            float acc = 0.0f;
+            for (int k2 = 0; k2 < KPV; ++k2) acc += red[k2 * G * HD + i];
+            a.out[size_t(g) * G * HD + i] = acc / lstat[h];
+        }
+        return;
+    }
+    float* part = a.part + (size_t(g) * a.nsplit + s) * G * ROW;
+    for (int i = tid; i < G * HD; i += kAttnThreads) {
+        const int h = i / HD, d = i % HD;
+        float acc = 0.0f;
+        for (int k2 = 0; k2 < KPV; ++k2) acc += red[k2 * G * HD + i];
+        st_dev(part + h * ROW + 2 + d, acc);
     }
     if (tid < G) {
-        part[tid * rowlen] = stat[2 * tid];
-        part[tid * rowlen + 1] = stat[2 * tid + 1];
+        st_dev(part + tid * ROW, nk > 0 ? mstat[tid] : -INFINITY);
+        st_dev(part + tid * ROW + 1, nk > 0 ? lstat[tid] : 0.0f);
     }
-
-    // Last workgroup of this kv head combines every split.
-    __threadfence();
+    wait_mem();
     __syncthreads();
-    if (tid == 0) last = atomicAdd(&a.tickets[g], 1u);
+    if (tid == 0) last = take_ticket(&a.tickets[g]);
     __syncthreads();
     if (last != a.nsplit - 1) return;
-    __threadfence();
-    const float* base = a.part + size_t(g) * a.nsplit * G * rowlen;
-    for (uint32_t i = tid; i < G * hd; i += blockDim.x) {
-        const uint32_t h = i / hd, d = i % hd;
-        float M = -INFINITY;
-        for (uint32_t p = 0; p < a.nsplit; ++p) {
-            const float* r = base + (size_t(p) * G + h) * rowlen;
-            if (__builtin_nontemporal_load(r + 1) > 0.0f) M = fmaxf(M, __builtin_nontemporal_load(r));
-        }
-        float L = 0.0f, o = 0.0f;
-        for (uint32_t p = 0; p < a.nsplit; ++p) {
-            const float* r = base + (size_t(p) * G + h) * rowlen;
-            const float l = __builtin_nontemporal_load(r + 1);
-            if (!(l > 0.0f)) continue;
-            const float f = expf(__builtin_nontemporal_load(r) - M);
-            L += l * f;
-            o += __builtin_nontemporal_load(r + 2 + d) * f;
-        }
-        a.out[(size_t(g) * G + h) * hd + d] = o / L;
+
+    // ---- combine (last workgroup): factors f[p][h] = exp(m_p - M) in LDS
+    const float* base = a.part + size_t(g) * a.nsplit * G * ROW;
+    for (uint32_t i = tid; i < a.nsplit * G; i += kAttnThreads) {
+        const float* r = base + size_t(i) * ROW;   // i = p * G + h
+        const float m = ld_dev(r), l = ld_dev(r + 1);
+        fs[i] = l > 0.0f ? m : -INFINITY;
+        ls[i] = l;
     }
-    if (tid == 0) a.tickets[g] = 0u;
+    __syncthreads();
+    if (tid < G) {
+        float M = -INFINITY;
+        for (uint32_t p = 0; p < a.nsplit; ++p) M = fmaxf(M, fs[p * G + tid]);
+        float L = 0.0f;
+        for (uint32_t p = 0; p < a.nsplit; ++p) {
+            const float m = fs[p * G + tid];
+            const float f = (m == -INFINITY) ? 0.0f : expf(m - M);
+            L += ls[p * G + tid] * f;
+            fs[p * G + tid] = f;
+        }
+        lstat[tid] = L;
+    }
+    __syncthreads();
+    const size_t pstride = size_t(G) * ROW;
+    for (int i = tid; i < G * HD; i += kAttnThreads) {
+        const int h = i / HD, d = i % HD;
+        const float* col = base + size_t(h) * ROW + 2 + d;
+        float o = 0.0f;
+        uint32_t p = 0;
+        for (; p + 8 <= a.nsplit; p += 8) {
+            float v[8];
+#pragma unroll
+            for (int q = 0; q < 8; ++q) v[q] = ld_dev(col + (p + q) * pstride);
+#pragma unroll
+            for (int q = 0; q < 8; ++q) o = fmaf(v[q], fs[(p + q) * G + h], o);
+        }
+        for (; p < a.nsplit; ++p) o = fmaf(ld_dev(col + p * pstride), fs[p * G + h], o);
+        a.out[size_t(g) * G * HD + i] = o / lstat[h];
+    }
+    if (tid == 0) st_dev(&a.tickets[g], 0u);
 }
 
 // ---- elementwise ------------------------------------------------------------
@@ -280,7 +372,8 @@ int launch_qk(const QkArgs& a, float theta, hipStream_t st) {
 }
 
 uint32_t attn_splits(uint32_t span) {
-    uint32_t n = (span + kAttnChunk - 1) / kAttnChunk;
+    uint32_t n = (span + kAttnMinChunk - 1) / kAttnMinChunk;
+    if (n > uint32_t(kAttnMaxSplit)) n = kAttnMaxSplit;
     return n < 1 ? 1 : n;
 }
 
@@ -290,30 +383,44 @@ size_t attn_partial_floats(uint32_t kv_heads, uint32_t n_heads, uint32_t head_di
 }
 
 int launch_attention(AttnArgs a, uint32_t max_span, hipStream_t st) {
-    if (a.head_dim == 0 || a.head_dim % kWave || a.head_dim > uint32_t(kMaxHeadDim))
-        return set_error(XP_E_ARG, "attention: head_dim=%u must be a multiple of 64, <= %d",
-                         a.head_dim, kMaxHeadDim);
+    if (a.head_dim != 64 && a.head_dim != 128 && a.head_dim != 256 && a.head_dim != 512)
+        return set_error(XP_E_ARG, "attention: head_dim=%u must be 64, 128, 256 or 512",
+                         a.head_dim);
     if (a.kv_heads == 0 || a.n_heads % a.kv_heads)
         return set_error(XP_E_ARG, "attention: n_heads=%u not a multiple of kv_heads=%u",
                          a.n_heads, a.kv_heads);
+    if (max_span == 0 || max_span > uint32_t(kAttnMaxSplit * kAttnChunk))
+        return set_error(XP_E_ARG, "attention: span %u outside [1, %d]", max_span,
+                         kAttnMaxSplit * kAttnChunk);
     a.group = a.n_heads / a.kv_heads;
-    if (a.group > uint32_t(kAttnMaxGrp))
-        return set_error(XP_E_ARG, "attention: %u query heads per kv head (max %d)", a.group,
-                         kAttnMaxGrp);
+    const uint32_t G = a.group;
+    if (G != 1 && G != 2 && G != 4 && G != 8)
+        return set_error(XP_E_ARG, "attention: %u query heads per kv head (1, 2, 4 or 8)", G);
     a.nsplit = attn_splits(max_span);
-    if (!a.part || !a.tickets) {
+    if (a.nsplit > 1 && (!a.part || !a.tickets)) {
         DeviceScratch* sc = scratch();
         if (!sc) return XP_E_HIP;
-        const size_t need = size_t(a.kv_heads) * a.nsplit * a.group * (2 + a.head_dim);
+        const size_t need = size_t(a.kv_heads) * a.nsplit * G * (2 + a.head_dim);
         if (!ensure_partial(sc, need) || !ensure_tickets(sc, a.kv_heads)) return XP_E_NOMEM;
         a.part = sc->partial;
         a.tickets = sc->tickets;
     }
-    hipLaunchKernelGGL(attention_decode_kernel, dim3(a.nsplit, a.kv_heads), dim3(kAttnThreads),
-                       0, st, a);
-    hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return set_error(XP_E_HIP, "attention: launch -> %s", hipGetErrorString(e));
-    return XP_OK;
+    const dim3 grid(a.nsplit, a.kv_heads), block(kAttnThreads);
+#define XP_ATTN(GG, HH)                                                                    \
+    if (G == GG && a.head_dim == HH) {                                                     \
+        hipLaunchKernelGGL((attention_decode_kernel<GG, HH>), grid, block, 0, st, a);      \
+        hipError_t e = hipGetLastError();                                                  \
+        if (e != hipSuccess)                                                               \
+            return set_error(XP_E_HIP, "attention: launch -> %s", hipGetErrorString(e));   \
+        return XP_OK;                                                                      \
+    }
+    XP_ATTN(1, 64) XP_ATTN(1, 128) XP_ATTN(1, 256) XP_ATTN(1, 512)
+    XP_ATTN(2, 64) XP_ATTN(2, 128) XP_ATTN(2, 256) XP_ATTN(2, 512)
+    XP_ATTN(4, 64) XP_ATTN(4, 128) XP_ATTN(4, 256) XP_ATTN(4, 512)
+    XP_ATTN(8, 64) XP_ATTN(8, 128) XP_ATTN(8, 256)
+#undef XP_ATTN
+    return set_error(XP_E_ARG, "attention: no kernel for %u heads/kv head at head_dim %u", G,
+                     a.head_dim);
 }
 
 }  // namespace xp

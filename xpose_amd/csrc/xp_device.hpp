@@ -77,6 +77,33 @@ __device__ __forceinline__ float nib8_dot(uint32_t w, const float4 xa, const flo
     return acc;
 }
 
+// Cross-workgroup hand-off without an L2 flush. An agent-scope fence on
+// gfx950 writes back and invalidates the whole L2 (buffer_wbl2 / buffer_inv
+// sc1), which serialises when every wave does it. Instead, data another
+// workgroup will read is stored with agent-scope relaxed atomics (sc1,
+// written through to the device coherence point), the writer waits for its
+// stores to complete before taking an arrival ticket, and the reader loads
+// with agent-scope relaxed atomics (sc1, re-read from the coherence point).
+__device__ __forceinline__ void st_dev(float* p, float v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void st_dev(uint32_t* p, uint32_t v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float ld_dev(const float* p) {
+    return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint32_t ld_dev(const uint32_t* p) {
+    return __hip_atomic_load(const_cast<uint32_t*>(p), __ATOMIC_RELAXED,
+                             __HIP_MEMORY_SCOPE_AGENT);
+}
+// Blocks until every memory operation this wave issued has completed.
+__device__ __forceinline__ void wait_mem() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+// Arrival ticket: returns the number of arrivals before this one.
+__device__ __forceinline__ uint32_t take_ticket(uint32_t* t) {
+    return __hip_atomic_fetch_add(t, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 // Wave-wide sum / max via DPP-backed shuffles.
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll
