@@ -8,9 +8,8 @@
 // one task = (group g, chunk of k): lane t owns output 64g+t and issues one
 // global_load_dwordx4 per block, so a wave reads 1 KiB contiguous per block.
 // No cross-lane reduction is needed inside a task. The activation chunk is
-// staged once per workgroup in LDS (odd elements pre-scaled by 1/16, see
-// nib8_dot) together with per-block sums of x, which fold the -8 nibble bias
-// into one FMA per block.
+// staged once per workgroup in LDS as 20-bit block fixed point (see
+// block_dot), which turns the unpack-and-multiply into integer dot products.
 //
 // Split-k. Narrow matrices (1152 or 1536 outputs = 18-24 groups) cannot fill
 // 256 CUs with one task per group, so k is split into `split` chunks of whole
@@ -76,27 +75,81 @@ struct QuadScales {
     }
 };
 
-// One block: sum_t xs[t] * nibble_t over a 16-byte KM4 word group, with the
-// -8 bias folded in via the block sum of x.
-__device__ __forceinline__ float block_dot(const u32x4 w, const float* xb, float xsum) {
-    float pa = 0.0f, pb = 0.0f;
-    pa = nib8_dot(w.x, *reinterpret_cast<const float4*>(xb + 0),
-                  *reinterpret_cast<const float4*>(xb + 4), pa);
-    pb = nib8_dot(w.y, *reinterpret_cast<const float4*>(xb + 8),
-                  *reinterpret_cast<const float4*>(xb + 12), pb);
-    pa = nib8_dot(w.z, *reinterpret_cast<const float4*>(xb + 16),
-                  *reinterpret_cast<const float4*>(xb + 20), pa);
-    pb = nib8_dot(w.w, *reinterpret_cast<const float4*>(xb + 24),
-                  *reinterpret_cast<const float4*>(xb + 28), pb);
-    return (pa + pb) - 8.0f * xsum;
+// Activation staging. Each workgroup stores its k-chunk of x in LDS as 20-bit
+// block fixed point: for block b, sx_b = max|x| / 2^18 and q_k = rint(x_k /
+// sx_b), so |q_k| <= 2^18 and |x_k - sx_b q_k| <= 2^-19 max|x|. q_k is kept as
+// five planes of signed 4-bit digits (q = sum_p d_p 16^p, d_p in [-8, 7]):
+// plane p, word c of a block packs the digits of k = 32b + 8c .. 32b + 8c + 7
+// at nibble positions 0..7, which are the positions the KM4 word gives the
+// weights of those k. The signed weight nibble - 8 is (nibble ^ 8) read as a
+// two's-complement nibble, so one v_dot8_i32_i4 per (word, plane) multiplies
+// eight weights by eight digits exactly, and the block product
+// sum_k (n_k - 8) q_k is an exact int32 (|.| <= 2^26). Per block that is 4
+// XORs, 20 dot8 and 4 shift-adds for 2048 multiply-adds per wave, against
+// two conversions and one FMA per weight in fp32.
+constexpr int      kQxPlanes = 5;
+constexpr float    kQxRange  = 262144.0f;    // 2^18
+constexpr uint32_t kQxBias   = 0x88888u;     // 8 * (1 + 16 + 16^2 + 16^3 + 16^4)
+
+struct QxBlock {
+    u32x4 p[kQxPlanes];
+};
+
+// sum_k (nibble_k - 8) * q_k over one block, exact.
+__device__ __forceinline__ int32_t block_dot(u32x4 w, const QxBlock& q) {
+    w ^= 0x88888888u;
+    uint32_t d = 0;
+#pragma unroll
+    for (int p = 0; p < kQxPlanes; ++p) {
+        int32_t s = __builtin_amdgcn_sdot8(int32_t(w.x), int32_t(q.p[p].x), 0, false);
+        s = __builtin_amdgcn_sdot8(int32_t(w.y), int32_t(q.p[p].y), s, false);
+        s = __builtin_amdgcn_sdot8(int32_t(w.z), int32_t(q.p[p].z), s, false);
+        s = __builtin_amdgcn_sdot8(int32_t(w.w), int32_t(q.p[p].w), s, false);
+        d += uint32_t(s) << (4 * p);   // two's-complement wrap; the total fits
+    }
+    return int32_t(d);
 }
 
-// SPLIT = false: one chunk covers all of k (the wide lm_head shape); no
-// partials, no ticket. A separate instantiation so profiles name it apart.
+// Quantises eight consecutive activations (task i = (block i/4, word i%4))
+// into the five digit-plane words of that block and, for word 0, the block
+// scale. The four tasks of a block are adjacent lanes of one wave.
+__device__ __forceinline__ void stage_x8(QxBlock* qx, float* sx, uint32_t i, float4 v0,
+                                         float4 v1) {
+    const float v[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
+    float m = 0.0f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) m = fmaxf(m, fabsf(v[e]));
+    m = fmaxf(m, __shfl_xor(m, 1, kWave));
+    m = fmaxf(m, __shfl_xor(m, 2, kWave));
+    const float r = m > 0.0f ? kQxRange / m : 0.0f;
+    uint32_t t[8];
+    // q + bias has hex digits d_p + 8; xor-ing the bias back gives each
+    // digit as a two's-complement nibble.
+#pragma unroll
+    for (int e = 0; e < 8; ++e) t[e] = uint32_t(__float2int_rn(v[e] * r) + int32_t(kQxBias)) ^ kQxBias;
+    const uint32_t lb = i >> 2, c = i & 3u;
+#pragma unroll
+    for (int p = 0; p < kQxPlanes; ++p) {
+        uint32_t word = 0;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) word |= ((t[e] >> (4 * p)) & 15u) << (4 * e);
+        reinterpret_cast<uint32_t*>(&qx[lb].p[p])[c] = word;
+    }
+    if (c == 0) sx[lb] = m * (1.0f / kQxRange);
+}
+
+// One wave = one task = (column group, k-chunk). SPLIT = false: the chunk is
+// all of k (the wide lm_head shape); no partials, no ticket. A separate
+// instantiation so that profiles name the two apart. At most 128 VGPRs, so
+// four tasks share each SIMD (the lm_head's 4096 tasks then run in one round
+// on 256 CUs).
 template <int FMT, bool SPLIT>
-__global__ __launch_bounds__(kMvWaves * kWave) void mv_int4_kernel(MvArgs a) {
-    extern __shared__ float smem[];
-    const uint32_t wave = threadIdx.x / kWave;
+__global__ __launch_bounds__(kMvWaves * kWave) __attribute__((amdgpu_waves_per_eu(4)))
+void mv_int4_kernel(MvArgs a) {
+    extern __shared__ QxBlock smem_qx[];
+    // The wave index is uniform across a wave; saying so keeps the task's
+    // bookkeeping in scalar registers.
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
     const uint32_t lane = threadIdx.x % kWave;
     const uint32_t s    = blockIdx.x / a.wg_per_chunk;
     const uint32_t gg   = (blockIdx.x % a.wg_per_chunk) * kMvWaves + wave;
@@ -104,74 +157,117 @@ __global__ __launch_bounds__(kMvWaves * kWave) void mv_int4_kernel(MvArgs a) {
     const uint32_t q1   = min(q0 + a.qpc, a.nquads);
     const uint32_t b0   = q0 * 4;
     const uint32_t b1   = min(q1 * 4, a.nblk);
-    const uint32_t nkc  = (b1 - b0) * kBlk;
-
-    float* xs   = smem;                    // [qpc*128] activations (odd /16)
-    float* bsum = smem + a.qpc * 128;      // [qpc*4] per-block sum of x
-
+    const uint32_t nbc  = b1 - b0;
+    QxBlock* qx = smem_qx;
+    float*   sx = reinterpret_cast<float*>(smem_qx + a.qpc * 4);
     const float* xg = a.x + size_t(b0) * kBlk;
-    for (uint32_t i = threadIdx.x; i < nkc; i += blockDim.x) {
-        const float v = xg[i];
-        xs[i] = (i & 1u) ? v * 0.0625f : v;
-    }
-    for (uint32_t bb = threadIdx.x; bb < b1 - b0; bb += blockDim.x) {
-        float t = 0.0f;
-        for (uint32_t k = 0; k < kBlk; ++k) t += xg[bb * kBlk + k];
-        bsum[bb] = t;
-    }
-    __syncthreads();
-    if (gg >= a.groups) return;
 
-    float*       out = nullptr;
-    const u32x4* wq  = nullptr;
-    const void*  sc  = nullptr;
-    uint32_t cols = 0, gl = 0;
+    // Staging tasks beyond the first blockDim.x (chunks over 64 blocks) go
+    // first; the first batch's activations are loaded next, ahead of the
+    // weight prefetch, so that waiting for them does not wait for weights.
+    for (uint32_t i = threadIdx.x + blockDim.x; i < nbc * 4; i += blockDim.x)
+        stage_x8(qx, sx, i, reinterpret_cast<const float4*>(xg)[2 * i],
+                 reinterpret_cast<const float4*>(xg)[2 * i + 1]);
+    float4 xv0 = {0.0f, 0.0f, 0.0f, 0.0f}, xv1 = xv0;
+    if (threadIdx.x < nbc * 4) {
+        xv0 = reinterpret_cast<const float4*>(xg)[2 * threadIdx.x];
+        xv1 = reinterpret_cast<const float4*>(xg)[2 * threadIdx.x + 1];
+    }
+
+    // Waves past the last group (only in a chunk's last workgroup) prefetch
+    // group 0 of matrix 0 like any other wave and drop the result, so every
+    // wave issues the same loads and the wait counts stay exact.
+    const bool active = gg < a.groups;
+    uint32_t mi = 0;
 #pragma unroll
-    for (int i = 0; i < kMvMaxMats; ++i) {
-        if (uint32_t(i) < a.n_mats && gg >= a.m[i].grp0) {
-            out = a.m[i].out; wq = a.m[i].wq; sc = a.m[i].sc;
-            cols = a.m[i].cols; gl = gg - a.m[i].grp0;
+    for (int i = 1; i < kMvMaxMats; ++i)
+        if (uint32_t(i) < a.n_mats && gg >= a.m[i].grp0) mi = uint32_t(i);
+    if (!active) mi = 0;
+    float*       out = a.m[0].out;
+    const u32x4* wq  = a.m[0].wq;
+    const void*  sc  = a.m[0].sc;
+    uint32_t cols = a.m[0].cols;
+#pragma unroll
+    for (int i = 1; i < kMvMaxMats; ++i) {
+        if (uint32_t(i) == mi) {
+            out = a.m[i].out; wq = a.m[i].wq; sc = a.m[i].sc; cols = a.m[i].cols;
         }
     }
+    uint32_t grp0 = 0;
+#pragma unroll
+    for (int i = 1; i < kMvMaxMats; ++i)
+        if (uint32_t(i) == mi) grp0 = a.m[i].grp0;
+    const uint32_t gl = active ? gg - grp0 : 0u;
     const uint32_t j  = gl * kGrp + lane;
     const u32x4*   wp = wq + size_t(gl) * a.nblk * kGrp + lane;
+    const uint32_t nq = nbc / 4;   // whole quads in the chunk
+
+    // Three quads in flight: while quad n is multiplied, quads n+1 and n+2
+    // (16 x 16-byte weight loads + their scales) are outstanding. Block
+    // indices are clamped into the chunk, so a prefetch past its end (chunks
+    // of fewer than three quads) re-reads the chunk's last block.
+    u32x4 w[3][4];
+    QuadScales<FMT> qs[3];
+    const uint32_t blast = b1 - 1;
+    auto load_quad = [&](int r, uint32_t q) {
+        const uint32_t b = b0 + 4 * q;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) w[r][i] = ld_stream4(wp + size_t(min(b + i, blast)) * kGrp);
+        qs[r].load(sc, cols, j, min(b, blast & ~3u));
+    };
+    auto mul_quad = [&](int r, uint32_t q, float& acc) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const uint32_t lb = 4 * q + i;
+            const float f = qs[r].get(i) * sx[lb];
+            acc = fmaf(f, float(block_dot(w[r][i], qx[lb])), acc);
+        }
+    };
+    load_quad(0, 0);
+    load_quad(1, 1);
+    load_quad(2, 2);
+
+    if (threadIdx.x < nbc * 4) stage_x8(qx, sx, threadIdx.x, xv0, xv1);
+    __syncthreads();
+    if (!active) return;
 
     float acc = 0.0f;
-    const uint32_t nfull = (b1 - b0) / 4;
-    if (nfull > 0) {
-        // Two-stage pipeline over whole quads: quad n+1's four 16-byte loads
-        // and its scales are in flight while quad n is multiplied. The last
-        // prefetch re-reads the final quad instead of branching.
-        u32x4 w[4];
-        QuadScales<FMT> qs;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) w[i] = ld_stream4(wp + size_t(b0 + i) * kGrp);
-        qs.load(sc, cols, j, b0);
-        for (uint32_t qi = 0; qi < nfull; ++qi) {
-            const uint32_t b  = b0 + 4 * qi;
-            const uint32_t bn = (qi + 1 < nfull) ? b + 4 : b;
-            u32x4 wn[4];
-            QuadScales<FMT> qn;
-#pragma unroll
-            for (int i = 0; i < 4; ++i) wn[i] = ld_stream4(wp + size_t(bn + i) * kGrp);
-            qn.load(sc, cols, j, bn);
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const uint32_t lb = b - b0 + i;
-                acc = fmaf(qs.get(i), block_dot(w[i], xs + lb * kBlk, bsum[lb]), acc);
-            }
-#pragma unroll
-            for (int i = 0; i < 4; ++i) w[i] = wn[i];
-            qs = qn;
-        }
+    uint32_t q = 0;
+    // Steady state: every reload is in range. The scheduling barriers keep
+    // each reload right after the multiply that frees its registers (left
+    // alone, the scheduler sinks all three reloads to the end of the body).
+    for (; q + 6 <= nq; q += 3) {
+        mul_quad(0, q, acc);
+        __builtin_amdgcn_sched_barrier(0);
+        load_quad(0, q + 3);
+        __builtin_amdgcn_sched_barrier(0);
+        mul_quad(1, q + 1, acc);
+        __builtin_amdgcn_sched_barrier(0);
+        load_quad(1, q + 4);
+        __builtin_amdgcn_sched_barrier(0);
+        mul_quad(2, q + 2, acc);
+        __builtin_amdgcn_sched_barrier(0);
+        load_quad(2, q + 5);
+        __builtin_amdgcn_sched_barrier(0);
     }
+    const uint32_t rem = nq - q;    // 0..5 quads left; buffers hold q..q+2
+    if (rem > 0) {
+        mul_quad(0, q, acc);
+        if (rem > 3) load_quad(0, q + 3);
+    }
+    if (rem > 1) {
+        mul_quad(1, q + 1, acc);
+        if (rem > 4) load_quad(1, q + 4);
+    }
+    if (rem > 2) mul_quad(2, q + 2, acc);
+    if (rem > 3) mul_quad(0, q + 3, acc);
+    if (rem > 4) mul_quad(1, q + 4, acc);
     if constexpr (FMT == XP_SCALE_F32) {
         // Blocks past the last whole quad (nblk % 4 != 0, fp32 plane only).
-        for (uint32_t b = b0 + 4 * nfull; b < b1; ++b) {
-            const uint32_t lb = b - b0;
-            const u32x4 wb = ld_stream4(wp + size_t(b) * kGrp);
-            const float sb = reinterpret_cast<const float*>(sc)[size_t(b) * cols + j];
-            acc = fmaf(sb, block_dot(wb, xs + lb * kBlk, bsum[lb]), acc);
+        for (uint32_t lb = 4 * nq; lb < nbc; ++lb) {
+            const u32x4 wb = ld_stream4(wp + size_t(b0 + lb) * kGrp);
+            const float sb = reinterpret_cast<const float*>(sc)[size_t(b0 + lb) * cols + j];
+            acc = fmaf(sb * sx[lb], float(block_dot(wb, qx[lb])), acc);
         }
     }
 
@@ -259,6 +355,8 @@ int launch_mv(const MvMatDesc* mats, uint32_t n, const float* x, int fmt, uint32
               uint32_t split, float* partial, size_t partial_cap, uint32_t* tickets,
               size_t tickets_cap, hipStream_t st, const char* who) {
     if (!x) return set_error(XP_E_ARG, "%s: in is null", who);
+    if (reinterpret_cast<uintptr_t>(x) & 15u)
+        return set_error(XP_E_ARG, "%s: in must be 16-byte aligned", who);
     if (n < 1 || n > uint32_t(kMvMaxMats))
         return set_error(XP_E_ARG, "%s: %u matrices (1..%d)", who, n, kMvMaxMats);
     if (rows == 0 || rows % kBlk != 0)
@@ -312,7 +410,7 @@ int launch_mv(const MvMatDesc* mats, uint32_t n, const float* x, int fmt, uint32
             a.tickets = tickets;
         }
     }
-    const size_t lds = (size_t(a.qpc) * 128 + size_t(a.qpc) * 4) * sizeof(float);
+    const size_t lds = size_t(a.qpc) * 4 * (sizeof(QxBlock) + sizeof(float));
     if (lds > 64 * 1024)
         return set_error(XP_E_ARG, "%s: k-chunk of %u quads needs %zu B of LDS (> 64 KiB); "
                          "pass a larger split", who, a.qpc, lds);

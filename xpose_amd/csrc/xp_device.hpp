@@ -43,40 +43,6 @@ __device__ __forceinline__ uint16_t f32_to_f16_bits(float f) {
     return __half_as_ushort(__float2half_rn(f));
 }
 
-// Byte n of a word as float: maps to v_cvt_f32_ubyte{0..3}.
-__device__ __forceinline__ float ub(uint32_t w, int n) {
-    return static_cast<float>((w >> (8 * n)) & 0xFFu);
-}
-
-// Sum over one 8-nibble word of nib_i * x_i, where the caller's activation
-// slice `xs` holds x for even i and x/16 for odd i. Masking the word with
-// 0x0F0F0F0F leaves the even nibbles as bytes; masking with 0xF0F0F0F0 leaves
-// 16 * (odd nibble) as bytes, and the /16 already applied to x makes the
-// product exact. Nibbles are the raw biased values 0..15; the caller folds
-// the -8 bias in as -8 * sum(x) per block.
-//
-// The empty asm hides the masks' provenance from the combiner, which would
-// otherwise rewrite each byte read into a 4-bit v_bfe plus a conversion; with
-// it every nibble costs one v_cvt_f32_ubyteN and one FMA.
-__device__ __forceinline__ uint32_t opaque(uint32_t v) {
-    asm("" : "+v"(v));
-    return v;
-}
-__device__ __forceinline__ float nib8_dot(uint32_t w, const float4 xa, const float4 xb,
-                                          float acc) {
-    const uint32_t lo = opaque(w & 0x0F0F0F0Fu);   // nibbles 0,2,4,6
-    const uint32_t hi = opaque(w & 0xF0F0F0F0u);   // 16 * nibbles 1,3,5,7
-    acc = fmaf(xa.x, ub(lo, 0), acc);
-    acc = fmaf(xa.y, ub(hi, 0), acc);
-    acc = fmaf(xa.z, ub(lo, 1), acc);
-    acc = fmaf(xa.w, ub(hi, 1), acc);
-    acc = fmaf(xb.x, ub(lo, 2), acc);
-    acc = fmaf(xb.y, ub(hi, 2), acc);
-    acc = fmaf(xb.z, ub(lo, 3), acc);
-    acc = fmaf(xb.w, ub(hi, 3), acc);
-    return acc;
-}
-
 // Cross-workgroup hand-off without an L2 flush. An agent-scope fence on
 // gfx950 writes back and invalidates the whole L2 (buffer_wbl2 / buffer_inv
 // sc1), which serialises when every wave does it. Instead, data another
