@@ -147,7 +147,9 @@ def main() -> int:
     ms_step = el * 1e3 / args.steps
     mid_seq = ctx + 1 + args.warmup + args.steps // 2
     tb = token_bytes(mid_seq)
-    launches = sess.last_metrics().launches
+    met = sess.last_metrics()
+    launches = met.launches
+    exec_mode = {1: "graph", 2: "launch", 3: "token-kernel"}.get(met.exec_mode, str(met.exec_mode))
     sess.close()
 
     # Roofline leg: the dominant kernel of the step, the lm_head int4 matvec.
@@ -180,7 +182,8 @@ def main() -> int:
         "data": "synthetic (random int4 weights, fp16 group-32 scales, fp16 KV N(0,1))",
         "config": {"workload": "gemma3-1b-int4-greedy-decode", "ctx": ctx, "batch": 1,
                    "layers": 26, "hidden": 1152, "vocab": 262144, "weights": "int4 g32 + fp16",
-                   "kv": "fp16", "launches_per_step": launches},
+                   "kv": "fp16", "launches_per_step": launches,
+                   "exec": exec_mode},
         "roofline": {"bound": "hbm", "kernel": "mv_int4 lm_head 1152x262144",
                      "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,

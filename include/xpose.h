@@ -217,7 +217,17 @@ typedef struct {
     uint32_t seed;
     uint32_t seq_id;
     uint32_t topk_parts;
+    /* How a token step executes: XP_EXEC_AUTO (the persistent token kernel
+     * when the shape allows it, else the graph), XP_EXEC_GRAPH (one captured
+     * graph of per-op kernels), XP_EXEC_LAUNCH (per-op kernels launched one
+     * by one) or XP_EXEC_TOKEN (the persistent kernel; creation fails if the
+     * shape or device does not allow it). */
+    int32_t  exec_mode;
 } xp_config;
+
+enum xp_exec_mode {
+    XP_EXEC_AUTO = 0, XP_EXEC_GRAPH = 1, XP_EXEC_LAUNCH = 2, XP_EXEC_TOKEN = 3
+};
 
 /* Tensor ids for upload / synthesis. Matrices are (rows = input length,
  * cols = outputs): Q hidden->n_heads*hd, K/V hidden->kv_heads*hd,
@@ -241,6 +251,7 @@ typedef struct {
     double   tokens_per_sec;
     uint32_t position;
     uint32_t launches;      /* kernels per token step */
+    int32_t  exec_mode;     /* the mode in use (XP_EXEC_*, never AUTO) */
 } xp_metrics;
 
 /* Gemma-3-1B shape and defaults (DecodeConfig::gemma3_1b, decode.hpp:204-356)
@@ -275,7 +286,17 @@ int  xp_session_last_logits(xp_session* s, float* host, uint32_t n);
 int  xp_session_last_candidates(xp_session* s, float* val, uint32_t* idx, uint32_t n);
 int  xp_session_last_metrics(const xp_session* s, xp_metrics* m);
 int  xp_session_weight_bytes(const xp_session* s, size_t* bytes);
+/* The execution the session uses (XP_EXEC_TOKEN, _GRAPH or _LAUNCH). */
+int  xp_session_exec_mode(const xp_session* s, int32_t* mode);
 int  xp_session_kv_bytes(const xp_session* s, size_t* bytes);
+/* Stage timeline of the persistent token kernel (XP_EXEC_TOKEN only), for
+ * profiling: once enabled, every launch records for event e and workgroup w
+ * a timestamp at host[e * grid + w] in 100 MHz ticks (s_memrealtime), 0
+ * where w had no work: e = 0 kernel start; e = 1 + 6 l + k the end of layer
+ * l's stage k (QKV, attention, combine, O, gate/up, down); e = 6 L + 1 the
+ * lm_head; e = 6 L + 2 the argmax. *grid receives the workgroup count. */
+int  xp_session_trace(xp_session* s, int enable);
+int  xp_session_last_trace(xp_session* s, uint64_t* host, size_t n, uint32_t* grid);
 /* Host draw over (value, index) candidates, in place (decode.cpp:1873-1917),
  * with u in [0,1) standing in for the reference's mt19937_64 draw. */
 uint32_t xp_draw(float* val, uint32_t* idx, uint32_t n, float temperature, uint32_t top_k,

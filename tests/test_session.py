@@ -10,6 +10,16 @@ import pytest
 
 LOGIT_TOL = 1e-3
 
+# Every engine-level GPU test runs on both executions of the token step: the
+# persistent token kernel (token_kernel.hip) and the captured graph of per-op
+# kernels. XP_EXEC_TOKEN makes session creation fail rather than fall back.
+EXEC_MODES = [pytest.param(3, id="token"), pytest.param(1, id="graph")]
+
+
+@pytest.fixture(params=EXEC_MODES)
+def mode(request):
+    return request.param
+
 
 def cfg_small(X, **kw):
     base = dict(n_layers=6, vocab=32768, max_seq=1024)
@@ -33,6 +43,7 @@ def all_tensors(X, cfg, seed):
 def make_pair(X, xo, cfg, seed=0x5EED0002):
     t = all_tensors(X, cfg, seed)
     sess = X.DecodeSession(cfg)
+    assert sess.exec_mode == cfg.exec_mode
     for (l, k), a in t.items():
         sess.upload(l, k, a)
     model = xo.OracleModel(cfg, lambda l, k: t[(l, k)])
@@ -128,12 +139,12 @@ def test_oracle_generate_matches_forward_loop(xh, xo):
 # ---------------------------------------------------------------- GPU ----
 
 @pytest.mark.gpu
-def test_gpu_one_layer_cfg2(xp, xo):
+def test_gpu_one_layer_cfg2(xp, xo, mode):
     """one local Gemma-3-1B layer, 512 prior fp16 KV rows
     ~ N(0,1), decode at position 512 (kv_start 1, span 512)."""
     X = xp
     print("case session one-layer cfg2", flush=True)
-    cfg = X.XpConfig.gemma3_1b(n_layers=1, max_seq=1024)
+    cfg = X.XpConfig.gemma3_1b(n_layers=1, max_seq=1024, exec_mode=mode)
     sess, model = make_pair(X, xo, cfg)
     kvd = cfg.n_kv_heads * cfg.head_dim
     k = X.synth_normal_f16(512 * kvd, 77, 1)
@@ -154,10 +165,10 @@ def test_gpu_one_layer_cfg2(xp, xo):
 
 
 @pytest.mark.gpu
-def test_gpu_small_model_greedy(xp, xo):
+def test_gpu_small_model_greedy(xp, xo, mode):
     X = xp
     print("case session small greedy", flush=True)
-    cfg = cfg_small(X)
+    cfg = cfg_small(X, exec_mode=mode)
     sess, model = make_pair(X, xo, cfg)
     prompt = np.random.default_rng(4).integers(0, cfg.vocab, 32).astype(np.uint32)
     want = model.generate_greedy(prompt, 24)
@@ -168,10 +179,10 @@ def test_gpu_small_model_greedy(xp, xo):
 
 
 @pytest.mark.gpu
-def test_gpu_small_model_logits_every_step(xp, xo):
+def test_gpu_small_model_logits_every_step(xp, xo, mode):
     X = xp
     print("case session small logits", flush=True)
-    cfg = cfg_small(X, n_layers=7, vocab=16384)
+    cfg = cfg_small(X, n_layers=7, vocab=16384, exec_mode=mode)
     sess, model = make_pair(X, xo, cfg)
     prompt = [7, 1000, 16000, 3]
     for i, t in enumerate(prompt[:-1]):
@@ -193,12 +204,13 @@ def test_gpu_small_model_logits_every_step(xp, xo):
 
 
 @pytest.mark.gpu
-def test_gpu_decode_steps_equals_decode_step(xp, xo):
+def test_gpu_decode_steps_equals_decode_step(xp, xo, mode):
     X = xp
     print("case session decode_steps", flush=True)
-    cfg = cfg_small(X, n_layers=3)
+    cfg = cfg_small(X, n_layers=3, exec_mode=mode)
     t = all_tensors(X, cfg, 21)
     a, b = X.DecodeSession(cfg), X.DecodeSession(cfg)
+    assert a.exec_mode == b.exec_mode == mode
     for (l, k), arr in t.items():
         a.upload(l, k, arr)
         b.upload(l, k, arr)
@@ -211,12 +223,12 @@ def test_gpu_decode_steps_equals_decode_step(xp, xo):
 
 
 @pytest.mark.gpu
-def test_gpu_full_model_greedy_cfg3(xp, xo):
+def test_gpu_full_model_greedy_cfg3(xp, xo, mode):
     """BASELINE config 3 (shortened): full Gemma-3-1B architecture, random
     int4 weights, tied 262144 x 1152 table; prefill then greedy decode."""
     X = xp
     print("case session full model cfg3", flush=True)
-    cfg = X.XpConfig.gemma3_1b(max_seq=2048)
+    cfg = X.XpConfig.gemma3_1b(max_seq=2048, exec_mode=mode)
     sess, model = make_pair(X, xo, cfg)
     prompt = np.random.default_rng(32).integers(0, cfg.vocab, 8).astype(np.uint32)
     for i, t in enumerate(prompt[:-1]):
@@ -236,13 +248,13 @@ def test_gpu_full_model_greedy_cfg3(xp, xo):
 
 
 @pytest.mark.gpu
-def test_gpu_full_model_deep_context_cfg4(xp, xo):
+def test_gpu_full_model_deep_context_cfg4(xp, xo, mode):
     """BASELINE config 4 (shortened): KV of all 26 layers pre-filled with fp16
     N(0,1) to position 4096; decode from 4096 (global layers span 4097,
     local layers the last 512)."""
     X = xp
     print("case session full model cfg4", flush=True)
-    cfg = X.XpConfig.gemma3_1b(max_seq=4160)
+    cfg = X.XpConfig.gemma3_1b(max_seq=4160, exec_mode=mode)
     sess, model = make_pair(X, xo, cfg)
     kvd = cfg.n_kv_heads * cfg.head_dim
     for l in range(cfg.n_layers):
@@ -266,13 +278,13 @@ def test_gpu_full_model_deep_context_cfg4(xp, xo):
 
 
 @pytest.mark.gpu
-def test_gpu_temperature_sampling(xp, xo):
+def test_gpu_temperature_sampling(xp, xo, mode):
     """Temperature 0.8 / top-k 64 / top-p 0.95 over the top-4-per-chain
     harvest, Philox uniform per (sequence, step) (BASELINE config 5 draw)."""
     X = xp
     print("case session temperature", flush=True)
     cfg = cfg_small(X, n_layers=4, sample_mode=1, temperature=0.8, top_k=64, top_p=0.95,
-                    seed=99, seq_id=3, topk_parts=1024)
+                    seed=99, seq_id=3, topk_parts=1024, exec_mode=mode)
     sess, model = make_pair(X, xo, cfg)
     prompt = [11, 22, 33]
     for i, t in enumerate(prompt[:-1]):

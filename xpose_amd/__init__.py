@@ -20,6 +20,8 @@ XP_SCALE_F16_QUAD = 0
 XP_SCALE_BF16_QUAD = 1
 XP_SCALE_F32 = 2
 
+XP_EXEC_AUTO, XP_EXEC_GRAPH, XP_EXEC_LAUNCH, XP_EXEC_TOKEN = 0, 1, 2, 3
+
 _lib = None
 
 # Tensor ids (enum xp_tensor in include/xpose.h).
@@ -40,7 +42,8 @@ class XpConfig(C.Structure):
                                          "embed_scale", "attn_scale")] + \
                [("scale_fmt", C.c_int32), ("sample_mode", C.c_int32),
                 ("temperature", C.c_float), ("top_k", C.c_uint32), ("top_p", C.c_float),
-                ("seed", C.c_uint32), ("seq_id", C.c_uint32), ("topk_parts", C.c_uint32)]
+                ("seed", C.c_uint32), ("seq_id", C.c_uint32), ("topk_parts", C.c_uint32),
+                ("exec_mode", C.c_int32)]
 
     @classmethod
     def gemma3_1b(cls, **overrides) -> "XpConfig":
@@ -57,7 +60,7 @@ class XpConfig(C.Structure):
 class XpMetrics(C.Structure):
     _fields_ = [("ms", C.c_double), ("gpu_ms", C.c_double), ("sample_ms", C.c_double),
                 ("tokens_per_sec", C.c_double), ("position", C.c_uint32),
-                ("launches", C.c_uint32)]
+                ("launches", C.c_uint32), ("exec_mode", C.c_int32)]
 
 
 class XposeError(RuntimeError):
@@ -122,6 +125,9 @@ def _declare(lib: C.CDLL) -> None:
         "xp_session_last_metrics": (i32, [vp, P(XpMetrics)]),
         "xp_session_weight_bytes": (i32, [vp, P(sz)]),
         "xp_session_kv_bytes": (i32, [vp, P(sz)]),
+        "xp_session_trace": (i32, [vp, i32]),
+        "xp_session_exec_mode": (i32, [vp, P(C.c_int32)]),
+        "xp_session_last_trace": (i32, [vp, vp, sz, P(u32)]),
         "xp_draw": (u32, [vp, vp, u32, f32, u32, f32, C.c_double]),
         "xp_philox_uniform": (C.c_double, [u32, u32, u32]),
     }
@@ -395,6 +401,29 @@ class DecodeSession:
         b = C.c_size_t()
         call("xp_session_weight_bytes", self.h, C.byref(b))
         return b.value
+
+    @property
+    def exec_mode(self) -> int:
+        """XP_EXEC_TOKEN (3), XP_EXEC_GRAPH (1) or XP_EXEC_LAUNCH (2)."""
+        m = C.c_int32()
+        call("xp_session_exec_mode", self.h, C.byref(m))
+        return m.value
+
+    def trace(self, enable: bool = True) -> None:
+        """Record the persistent kernel's barrier timeline from now on."""
+        call("xp_session_trace", self.h, 1 if enable else 0)
+
+    def last_trace(self) -> np.ndarray:
+        """[6 * n_layers + 3][grid] ticks (100 MHz) of the last launch: kernel
+        start, the end of each layer's six stages, lm_head, argmax; 0 where a
+        workgroup had no work in a stage."""
+        g = C.c_uint32()
+        probe = np.empty(1, np.uint64)
+        call("xp_session_last_trace", self.h, probe.ctypes.data, 1, C.byref(g))
+        ne = 6 * self.cfg.n_layers + 3
+        out = np.empty(ne * g.value, np.uint64)
+        call("xp_session_last_trace", self.h, out.ctypes.data, out.size, C.byref(g))
+        return out.reshape(ne, g.value)
 
 
 def draw(val, idx, temperature: float, top_k: int, top_p: float, u: float) -> int:

@@ -31,6 +31,7 @@ HIP_FLAGS = [
 ]
 
 LIB_SOURCES = ["runtime.cpp", "synth.cpp", "matvec.hip", "transformer.hip", "sampling.hip",
+               "token_kernel.hip",
                "session_kernels.hip", "session.cpp"]
 
 

@@ -75,69 +75,6 @@ struct QuadScales {
     }
 };
 
-// Activation staging. Each workgroup stores its k-chunk of x in LDS as 20-bit
-// block fixed point: for block b, sx_b = max|x| / 2^18 and q_k = rint(x_k /
-// sx_b), so |q_k| <= 2^18 and |x_k - sx_b q_k| <= 2^-19 max|x|. q_k is kept as
-// five planes of signed 4-bit digits (q = sum_p d_p 16^p, d_p in [-8, 7]):
-// plane p, word c of a block packs the digits of k = 32b + 8c .. 32b + 8c + 7
-// at nibble positions 0..7, which are the positions the KM4 word gives the
-// weights of those k. The signed weight nibble - 8 is (nibble ^ 8) read as a
-// two's-complement nibble, so one v_dot8_i32_i4 per (word, plane) multiplies
-// eight weights by eight digits exactly, and the block product
-// sum_k (n_k - 8) q_k is an exact int32 (|.| <= 2^26). Per block that is 4
-// XORs, 20 dot8 and 4 shift-adds for 2048 multiply-adds per wave, against
-// two conversions and one FMA per weight in fp32.
-constexpr int      kQxPlanes = 5;
-constexpr float    kQxRange  = 262144.0f;    // 2^18
-constexpr uint32_t kQxBias   = 0x88888u;     // 8 * (1 + 16 + 16^2 + 16^3 + 16^4)
-
-struct QxBlock {
-    u32x4 p[kQxPlanes];
-};
-
-// sum_k (nibble_k - 8) * q_k over one block, exact.
-__device__ __forceinline__ int32_t block_dot(u32x4 w, const QxBlock& q) {
-    w ^= 0x88888888u;
-    uint32_t d = 0;
-#pragma unroll
-    for (int p = 0; p < kQxPlanes; ++p) {
-        int32_t s = __builtin_amdgcn_sdot8(int32_t(w.x), int32_t(q.p[p].x), 0, false);
-        s = __builtin_amdgcn_sdot8(int32_t(w.y), int32_t(q.p[p].y), s, false);
-        s = __builtin_amdgcn_sdot8(int32_t(w.z), int32_t(q.p[p].z), s, false);
-        s = __builtin_amdgcn_sdot8(int32_t(w.w), int32_t(q.p[p].w), s, false);
-        d += uint32_t(s) << (4 * p);   // two's-complement wrap; the total fits
-    }
-    return int32_t(d);
-}
-
-// Quantises eight consecutive activations (task i = (block i/4, word i%4))
-// into the five digit-plane words of that block and, for word 0, the block
-// scale. The four tasks of a block are adjacent lanes of one wave.
-__device__ __forceinline__ void stage_x8(QxBlock* qx, float* sx, uint32_t i, float4 v0,
-                                         float4 v1) {
-    const float v[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
-    float m = 0.0f;
-#pragma unroll
-    for (int e = 0; e < 8; ++e) m = fmaxf(m, fabsf(v[e]));
-    m = fmaxf(m, __shfl_xor(m, 1, kWave));
-    m = fmaxf(m, __shfl_xor(m, 2, kWave));
-    const float r = m > 0.0f ? kQxRange / m : 0.0f;
-    uint32_t t[8];
-    // q + bias has hex digits d_p + 8; xor-ing the bias back gives each
-    // digit as a two's-complement nibble.
-#pragma unroll
-    for (int e = 0; e < 8; ++e) t[e] = uint32_t(__float2int_rn(v[e] * r) + int32_t(kQxBias)) ^ kQxBias;
-    const uint32_t lb = i >> 2, c = i & 3u;
-#pragma unroll
-    for (int p = 0; p < kQxPlanes; ++p) {
-        uint32_t word = 0;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) word |= ((t[e] >> (4 * p)) & 15u) << (4 * e);
-        reinterpret_cast<uint32_t*>(&qx[lb].p[p])[c] = word;
-    }
-    if (c == 0) sx[lb] = m * (1.0f / kQxRange);
-}
-
 // One wave = one task = (column group, k-chunk). SPLIT = false: the chunk is
 // all of k (the wide lm_head shape); no partials, no ticket. A separate
 // instantiation so that profiles name the two apart. At most 128 VGPRs, so

@@ -16,19 +16,6 @@ namespace xp {
 
 constexpr int kAmThreads = 256;
 
-__device__ __forceinline__ void am_better(float& bv, uint32_t& bi, float v, uint32_t i) {
-    if (v > bv || (v == bv && i < bi)) { bv = v; bi = i; }
-}
-
-__device__ __forceinline__ void am_wave(float& bv, uint32_t& bi) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) {
-        const float v = __shfl_xor(bv, o, kWave);
-        const uint32_t i = __shfl_xor(bi, o, kWave);
-        am_better(bv, bi, v, i);
-    }
-}
-
 struct AmArgs {
     uint32_t* out_idx;
     float* out_val;

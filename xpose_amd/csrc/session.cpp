@@ -137,6 +137,7 @@ struct Session {
     char* kvarena = nullptr;
     size_t kvbytes = 0;
     char* aarena = nullptr;
+    char* tarena = nullptr;      // persistent-kernel tables and exchange buffers
     struct Layer {
         void* w[kNMat];
         void* s[kNMat];
@@ -163,7 +164,13 @@ struct Session {
     uint32_t* h_ids = nullptr;   // pinned staging for host-chosen token ids
     hipGraphExec_t graph[3] = {nullptr, nullptr, nullptr};   // prefill, greedy, harvest
     uint32_t launches[3] = {0, 0, 0};
-    bool use_graph = true;       // XP_SESSION_NO_GRAPH=1 launches each kernel directly
+    int mode = XP_EXEC_GRAPH;    // XP_EXEC_TOKEN (persistent kernel), _GRAPH or _LAUNCH
+    // Persistent token kernel: layer table, exchange buffers, barrier flags.
+    TokLayer* d_layers = nullptr;
+    TokArgs ta{};
+    uint32_t tok_grid = 0;
+    uint32_t tag = 0;            // tag of the last queued launch (exchange slots)
+    unsigned long long* trace_buf = nullptr;
     uint32_t pos = 0;
     uint32_t step = 0;           // draws made (Philox counter)
     bool logits_valid = false;
@@ -182,6 +189,7 @@ struct Session {
     }
 
     int record(int variant, uint32_t& n);
+    int run_token(int variant);
     int graph_for(int variant);
     int run(int variant);
 };
@@ -276,8 +284,21 @@ int Session::graph_for(int variant) {
     return XP_OK;
 }
 
+int Session::run_token(int variant) {
+    ta.want_logits = variant >= 1 ? 1u : 0u;
+    ta.greedy = variant == 1 ? 1u : 0u;
+    if (++tag == 0) ++tag;       // slots start at tag 0; a launch never uses it
+    ta.tag = tag;
+    int rc = launch_token(ta, tok_grid, st);
+    if (rc != XP_OK) return rc;
+    launches[variant] = variant == 2 ? 2u : 1u;
+    if (variant == 2) return launch_topk4(cand_val, cand_idx, logits, cfg.vocab, cfg.topk_parts, st);
+    return XP_OK;
+}
+
 int Session::run(int variant) {
-    if (!use_graph) {
+    if (mode == XP_EXEC_TOKEN) return run_token(variant);
+    if (mode == XP_EXEC_LAUNCH) {
         uint32_t n = 0;
         const int r = record(variant, n);
         launches[variant] = n;
@@ -363,6 +384,8 @@ int destroy(xp_session* h) {
     if (s.warena) (void)hipFree(s.warena);
     if (s.kvarena) (void)hipFree(s.kvarena);
     if (s.aarena) (void)hipFree(s.aarena);
+    if (s.tarena) (void)hipFree(s.tarena);
+    if (s.trace_buf) (void)hipFree(s.trace_buf);
     if (s.h_ids) (void)hipHostFree(s.h_ids);
     if (s.st) (void)hipStreamDestroy(s.st);
     delete h;
@@ -384,9 +407,121 @@ int sample_from_candidates(Session& s, uint32_t& token) {
     return XP_OK;
 }
 
+// Layer table, RoPE tables and exchange buffers of the persistent token
+// kernel (token_kernel.hip); switches the session to it.
+int setup_token(Session& s) {
+    const xp_config& c = s.cfg;
+    const uint32_t grid = uint32_t(s.n_cu);
+    const uint32_t qd = c.n_heads * c.head_dim;
+    const TokLL lay = tok_ll_layout(c.hidden, c.ffn, c.n_heads, c.head_dim, grid);
+    const size_t sizes[] = {
+        size_t(c.n_layers) * sizeof(TokLayer),                   // layer table
+        size_t(c.head_dim / 2) * 4, size_t(c.head_dim / 2) * 4,  // freq local / global
+        (size_t(c.n_layers) * lay.layer + 2 * size_t(grid)) * 8}; // exchange slots
+    size_t tb = 0;
+    for (size_t z : sizes) tb += align_up(z);
+    if (hipMalloc(&s.tarena, tb) != hipSuccess)
+        return set_error(XP_E_NOMEM, "xp_session_create: %zu token-kernel bytes", tb);
+    if (hipMemset(s.tarena, 0, tb) != hipSuccess)
+        return set_error(XP_E_HIP, "xp_session_create: clearing token-kernel buffers failed");
+    char* p = s.tarena;
+    size_t si = 0;
+    auto nxt = [&]() { char* r = p; p += align_up(sizes[si++]); return r; };
+    s.d_layers = reinterpret_cast<TokLayer*>(nxt());
+    float* fl = reinterpret_cast<float*>(nxt());
+    float* fg = reinterpret_cast<float*>(nxt());
+    TokArgs& a = s.ta;
+    a.ll = reinterpret_cast<unsigned long long*>(nxt());
+    a.ll_layer = lay.layer;
+    std::vector<TokLayer> tl(c.n_layers);
+    for (uint32_t l = 0; l < c.n_layers; ++l) {
+        for (int m = 0; m < kNMat; ++m) { tl[l].w[m] = s.L[l].w[m]; tl[l].s[m] = s.L[l].s[m]; }
+        for (int n = 0; n < kNNorm; ++n) tl[l].norm[n] = s.L[l].norm[n];
+        tl[l].kc = s.L[l].kc;
+        tl[l].vc = s.L[l].vc;
+        tl[l].global = s.is_global(l) ? 1u : 0u;
+        tl[l].pad = 0;
+    }
+    std::vector<float> f(c.head_dim / 2);
+    auto freq = [&](float theta) {
+        for (uint32_t d = 0; d < c.head_dim / 2; ++d)
+            f[d] = std::exp2f(-std::log2f(theta) * (float(2u * d) / float(c.head_dim)));
+    };
+    XP_HIP(hipMemcpy(s.d_layers, tl.data(), tl.size() * sizeof(TokLayer), hipMemcpyHostToDevice));
+    freq(c.rope_theta_local);
+    XP_HIP(hipMemcpy(fl, f.data(), f.size() * 4, hipMemcpyHostToDevice));
+    freq(c.rope_theta_global);
+    XP_HIP(hipMemcpy(fg, f.data(), f.size() * 4, hipMemcpyHostToDevice));
+    a.layers = s.d_layers;
+    a.n_layers = c.n_layers;
+    a.hidden = c.hidden;
+    a.ffn = c.ffn;
+    a.n_heads = c.n_heads;
+    a.vocab = c.vocab;
+    a.window = c.sliding_window;
+    a.eps = c.rms_eps;
+    a.embed_scale = s.embed_scale();
+    a.attn_scale = s.attn_scale();
+    a.fmt = c.scale_fmt;
+    a.lm_w = s.lm_w;
+    a.lm_s = s.lm_s;
+    a.final_norm = s.final_norm;
+    a.freq_local = fl;
+    a.freq_global = fg;
+    a.logits = s.logits;
+    a.state = s.state;
+    a.hist = s.hist;
+    s.tok_grid = grid;
+    s.tag = 0;
+    s.mode = XP_EXEC_TOKEN;
+    return XP_OK;
+}
+
+// Device status word of the persistent kernel (state[2]): non-zero after a
+// barrier wait ran past its spin limit.
+int check_status(Session& s) {
+    if (s.mode != XP_EXEC_TOKEN) return XP_OK;
+    uint32_t status = 0;
+    XP_HIP(hipMemcpy(&status, s.state + 2, 4, hipMemcpyDeviceToHost));
+    if (status != 0)
+        return set_error(XP_E_DEVICE, "token kernel: a device-wide barrier timed out (status %u); "
+                         "the session's results are invalid", status);
+    return XP_OK;
+}
+
 }  // namespace
 
 extern "C" {
+
+int xp_session_trace(xp_session* h, int enable) {
+    XP_REQUIRE(h, "null session");
+    Session& s = h->s;
+    XP_REQUIRE(s.mode == XP_EXEC_TOKEN, "barrier traces exist for the persistent token kernel only");
+    XP_HIP(hipStreamSynchronize(s.st));
+    if (!enable) {
+        s.ta.trace = nullptr;
+        return XP_OK;
+    }
+    if (!s.trace_buf) {
+        const size_t n = size_t(tok_trace_events(s.cfg.n_layers)) * s.tok_grid;
+        XP_HIP(hipMalloc(&s.trace_buf, n * 8));
+        XP_HIP(hipMemset(s.trace_buf, 0, n * 8));
+    }
+    s.ta.trace = s.trace_buf;
+    return XP_OK;
+}
+
+int xp_session_last_trace(xp_session* h, uint64_t* host, size_t n, uint32_t* grid) {
+    XP_REQUIRE(h && host && grid, "null pointer");
+    Session& s = h->s;
+    XP_REQUIRE(s.trace_buf != nullptr, "tracing was never enabled");
+    const size_t cap = size_t(tok_trace_events(s.cfg.n_layers)) * s.tok_grid;
+    XP_REQUIRE(n <= cap, "n=%zu > %zu trace slots", n, cap);
+    XP_HIP(hipStreamSynchronize(s.st));
+    XP_HIP(hipMemcpy(host, s.trace_buf, n * 8, hipMemcpyDeviceToHost));
+    *grid = s.tok_grid;
+    return XP_OK;
+}
 
 void xp_config_gemma3_1b(xp_config* c) {
     if (!c) return;
@@ -446,7 +581,10 @@ int xp_session_create(const xp_config* cfg, xp_session** out) {
     Session& s = h->s;
     s.cfg = *cfg;
     const xp_config& c = s.cfg;
-    if (const char* e = std::getenv("XP_SESSION_NO_GRAPH")) s.use_graph = (e[0] == '\0' || e[0] == '0');
+    if (c.exec_mode < XP_EXEC_AUTO || c.exec_mode > XP_EXEC_TOKEN) {
+        delete h;
+        return set_error(XP_E_ARG, "config: unknown exec_mode %d", c.exec_mode);
+    }
     try {
         int dev = 0;
         hipDeviceProp_t p;
@@ -540,6 +678,24 @@ int xp_session_create(const xp_config* cfg, xp_session** out) {
             destroy(h);
             return set_error(XP_E_NOMEM, "xp_session_create: pinned staging");
         }
+        // ---- execution mode
+        s.mode = c.exec_mode == XP_EXEC_LAUNCH ? XP_EXEC_LAUNCH : XP_EXEC_GRAPH;
+        const int tok_ok = (c.exec_mode == XP_EXEC_AUTO || c.exec_mode == XP_EXEC_TOKEN)
+                               ? tok_supported(c.hidden, c.ffn, c.n_heads, c.n_kv_heads,
+                                               c.head_dim, c.vocab, c.max_seq, c.scale_fmt, s.n_cu)
+                               : XP_E_ARG;
+        if (c.exec_mode == XP_EXEC_TOKEN && tok_ok != XP_OK) {
+            destroy(h);
+            return tok_ok;
+        }
+        if (tok_ok == XP_OK) {
+            int rc = setup_token(s);
+            if (rc != XP_OK) {
+                destroy(h);
+                return rc;
+            }
+        }
+        clear_error();
         if (hipDeviceSynchronize() != hipSuccess) {
             destroy(h);
             return set_error(XP_E_HIP, "xp_session_create: initialisation failed");
@@ -662,10 +818,11 @@ int xp_session_prefill(xp_session* h, const uint32_t* ids, uint32_t n) {
         if (rc != XP_OK) return rc;
     }
     XP_HIP(hipStreamSynchronize(s.st));
+    if (int rc = check_status(s); rc != XP_OK) return rc;
     s.pos += n;
     s.logits_valid = true;
     const double ms = now_ms() - t0;
-    s.met = xp_metrics{ms, ms, 0.0, ms > 0 ? n * 1000.0 / ms : 0.0, s.pos, s.launches[0]};
+    s.met = xp_metrics{ms, ms, 0.0, ms > 0 ? n * 1000.0 / ms : 0.0, s.pos, s.launches[0], s.mode};
     return XP_OK;
 }
 
@@ -694,11 +851,12 @@ int xp_session_decode_step(xp_session* h, uint32_t* token) {
     if (rc != XP_OK) return rc;
     XP_HIP(hipMemcpyAsync(s.h_ids + 1, s.hist + s.pos, 4, hipMemcpyDeviceToHost, s.st));
     XP_HIP(hipStreamSynchronize(s.st));
+    if (int rc2 = check_status(s); rc2 != XP_OK) return rc2;
     *token = s.h_ids[1];
     const double t2 = now_ms();
     ++s.pos;
     s.met = xp_metrics{t2 - t0, t2 - t1, ts, (t2 - t0) > 0 ? 1000.0 / (t2 - t0) : 0.0, s.pos,
-                       s.launches[variant]};
+                       s.launches[variant], s.mode};
     return XP_OK;
 }
 
@@ -718,10 +876,11 @@ int xp_session_decode_steps(xp_session* h, uint32_t n, uint32_t* tokens) {
     }
     XP_HIP(hipStreamSynchronize(s.st));
     const double t1 = now_ms();
+    if (int rc = check_status(s); rc != XP_OK) return rc;
     if (tokens) XP_HIP(hipMemcpy(tokens, s.hist + s.pos, size_t(n) * 4, hipMemcpyDeviceToHost));
     s.pos += n;
     s.met = xp_metrics{t1 - t0, t1 - t0, 0.0, (t1 - t0) > 0 ? n * 1000.0 / (t1 - t0) : 0.0, s.pos,
-                       s.launches[1]};
+                       s.launches[1], s.mode};
     return XP_OK;
 }
 
@@ -760,6 +919,12 @@ int xp_session_last_metrics(const xp_session* h, xp_metrics* m) {
 int xp_session_weight_bytes(const xp_session* h, size_t* bytes) {
     XP_REQUIRE(h && bytes, "null pointer");
     *bytes = h->s.wbytes;
+    return XP_OK;
+}
+
+int xp_session_exec_mode(const xp_session* h, int32_t* mode) {
+    XP_REQUIRE(h && mode, "null pointer");
+    *mode = h->s.mode;
     return XP_OK;
 }
 

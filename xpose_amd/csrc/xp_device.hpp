@@ -23,6 +23,23 @@ __device__ __forceinline__ u32x4 ld_stream4(const u32x4* p) {
 __device__ __forceinline__ u32x2 ld_stream2(const u32x2* p) {
     return __builtin_nontemporal_load(p);
 }
+// Global-address-space views. Pointers read out of device memory (a layer
+// table) are generic to the compiler, which then emits FLAT accesses; FLAT
+// loads also count against lgkmcnt, so every later LDS or scalar wait would
+// wait for them. These casts keep such accesses on the global path.
+#define XP_GLOBAL __attribute__((address_space(1)))
+__device__ __forceinline__ u32x4 ldg_stream4(const u32x4* p) {
+    return __builtin_nontemporal_load((const XP_GLOBAL u32x4*)p);
+}
+__device__ __forceinline__ u32x2 ldg_stream2(const u32x2* p) {
+    return __builtin_nontemporal_load((const XP_GLOBAL u32x2*)p);
+}
+__device__ __forceinline__ u32x4 ldg4(const void* p) { return *(const XP_GLOBAL u32x4*)p; }
+__device__ __forceinline__ uint32_t ldg32(const void* p) { return *(const XP_GLOBAL uint32_t*)p; }
+__device__ __forceinline__ uint16_t ldg16(const void* p) { return *(const XP_GLOBAL uint16_t*)p; }
+__device__ __forceinline__ float ldgf(const float* p) { return *(const XP_GLOBAL float*)p; }
+__device__ __forceinline__ void stg16(void* p, uint16_t v) { *(XP_GLOBAL uint16_t*)p = v; }
+
 constexpr uint32_t kBlk = 32;   // quantisation block along k (BLK, llm_matvec.cl:25)
 constexpr uint32_t kGrp = 64;   // KM4 column-group width (GRP, llm_matvec.cl:26)
 
@@ -43,6 +60,69 @@ __device__ __forceinline__ uint16_t f32_to_f16_bits(float f) {
     return __half_as_ushort(__float2half_rn(f));
 }
 
+// Activation staging. Each workgroup stores its k-chunk of x in LDS as 20-bit
+// block fixed point: for block b, sx_b = max|x| / 2^18 and q_k = rint(x_k /
+// sx_b), so |q_k| <= 2^18 and |x_k - sx_b q_k| <= 2^-19 max|x|. q_k is kept as
+// five planes of signed 4-bit digits (q = sum_p d_p 16^p, d_p in [-8, 7]):
+// plane p, word c of a block packs the digits of k = 32b + 8c .. 32b + 8c + 7
+// at nibble positions 0..7, which are the positions the KM4 word gives the
+// weights of those k. The signed weight nibble - 8 is (nibble ^ 8) read as a
+// two's-complement nibble, so one v_dot8_i32_i4 per (word, plane) multiplies
+// eight weights by eight digits exactly, and the block product
+// sum_k (n_k - 8) q_k is an exact int32 (|.| <= 2^26). Per block that is 4
+// XORs, 20 dot8 and 4 shift-adds for 2048 multiply-adds per wave, against
+// two conversions and one FMA per weight in fp32.
+constexpr int      kQxPlanes = 5;
+constexpr float    kQxRange  = 262144.0f;    // 2^18
+constexpr uint32_t kQxBias   = 0x88888u;     // 8 * (1 + 16 + 16^2 + 16^3 + 16^4)
+
+struct QxBlock {
+    u32x4 p[kQxPlanes];
+};
+
+// sum_k (nibble_k - 8) * q_k over one block, exact.
+__device__ __forceinline__ int32_t block_dot(u32x4 w, const QxBlock& q) {
+    w ^= 0x88888888u;
+    uint32_t d = 0;
+#pragma unroll
+    for (int p = 0; p < kQxPlanes; ++p) {
+        int32_t s = __builtin_amdgcn_sdot8(int32_t(w.x), int32_t(q.p[p].x), 0, false);
+        s = __builtin_amdgcn_sdot8(int32_t(w.y), int32_t(q.p[p].y), s, false);
+        s = __builtin_amdgcn_sdot8(int32_t(w.z), int32_t(q.p[p].z), s, false);
+        s = __builtin_amdgcn_sdot8(int32_t(w.w), int32_t(q.p[p].w), s, false);
+        d += uint32_t(s) << (4 * p);   // two's-complement wrap; the total fits
+    }
+    return int32_t(d);
+}
+
+// Quantises eight consecutive activations (task i = (block i/4, word i%4))
+// into the five digit-plane words of that block and, for word 0, the block
+// scale. The four tasks of a block are adjacent lanes of one wave.
+__device__ __forceinline__ void stage_x8(QxBlock* qx, float* sx, uint32_t i, float4 v0,
+                                         float4 v1) {
+    const float v[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
+    float m = 0.0f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) m = fmaxf(m, fabsf(v[e]));
+    m = fmaxf(m, __shfl_xor(m, 1, kWave));
+    m = fmaxf(m, __shfl_xor(m, 2, kWave));
+    const float r = m > 0.0f ? kQxRange / m : 0.0f;
+    uint32_t t[8];
+    // q + bias has hex digits d_p + 8; xor-ing the bias back gives each
+    // digit as a two's-complement nibble.
+#pragma unroll
+    for (int e = 0; e < 8; ++e) t[e] = uint32_t(__float2int_rn(v[e] * r) + int32_t(kQxBias)) ^ kQxBias;
+    const uint32_t lb = i >> 2, c = i & 3u;
+#pragma unroll
+    for (int p = 0; p < kQxPlanes; ++p) {
+        uint32_t word = 0;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) word |= ((t[e] >> (4 * p)) & 15u) << (4 * e);
+        reinterpret_cast<uint32_t*>(&qx[lb].p[p])[c] = word;
+    }
+    if (c == 0) sx[lb] = m * (1.0f / kQxRange);
+}
+
 // Cross-workgroup hand-off without an L2 flush. An agent-scope fence on
 // gfx950 writes back and invalidates the whole L2 (buffer_wbl2 / buffer_inv
 // sc1), which serialises when every wave does it. Instead, data another
@@ -51,23 +131,31 @@ __device__ __forceinline__ uint16_t f32_to_f16_bits(float f) {
 // stores to complete before taking an arrival ticket, and the reader loads
 // with agent-scope relaxed atomics (sc1, re-read from the coherence point).
 __device__ __forceinline__ void st_dev(float* p, float v) {
-    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store((XP_GLOBAL float*)p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 __device__ __forceinline__ void st_dev(uint32_t* p, uint32_t v) {
-    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store((XP_GLOBAL uint32_t*)p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 __device__ __forceinline__ float ld_dev(const float* p) {
-    return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return __hip_atomic_load((XP_GLOBAL float*)p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 __device__ __forceinline__ uint32_t ld_dev(const uint32_t* p) {
-    return __hip_atomic_load(const_cast<uint32_t*>(p), __ATOMIC_RELAXED,
+    return __hip_atomic_load((XP_GLOBAL uint32_t*)p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void st_dev64(unsigned long long* p, unsigned long long v) {
+    __hip_atomic_store((XP_GLOBAL unsigned long long*)p, v, __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ unsigned long long ld_dev64(const unsigned long long* p) {
+    return __hip_atomic_load((XP_GLOBAL unsigned long long*)p, __ATOMIC_RELAXED,
                              __HIP_MEMORY_SCOPE_AGENT);
 }
 // Blocks until every memory operation this wave issued has completed.
 __device__ __forceinline__ void wait_mem() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 // Arrival ticket: returns the number of arrivals before this one.
 __device__ __forceinline__ uint32_t take_ticket(uint32_t* t) {
-    return __hip_atomic_fetch_add(t, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return __hip_atomic_fetch_add((XP_GLOBAL uint32_t*)t, 1u, __ATOMIC_RELAXED,
+                                  __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // Wave-wide sum / max via DPP-backed shuffles.
@@ -80,6 +168,21 @@ __device__ __forceinline__ float wave_max(float v) {
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, kWave));
     return v;
+}
+
+// (value, index) argmax step: larger value wins, then the lower index
+// (kernels/llm_sampling.cl:50-56).
+__device__ __forceinline__ void am_better(float& bv, uint32_t& bi, float v, uint32_t i) {
+    if (v > bv || (v == bv && i < bi)) { bv = v; bi = i; }
+}
+
+__device__ __forceinline__ void am_wave(float& bv, uint32_t& bi) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        const float v = __shfl_xor(bv, o, kWave);
+        const uint32_t i = __shfl_xor(bi, o, kWave);
+        am_better(bv, bi, v, i);
+    }
 }
 
 // gelu_pytorch_tanh with the reference's clamped-exp tanh

@@ -68,4 +68,77 @@ int launch_argmax(uint32_t* out_idx, float* out_val, const float* logits, uint32
 int launch_topk4(float* cval, uint32_t* cidx, const float* x, uint32_t n, uint32_t nparts,
                  hipStream_t st);
 
+
+// ---- persistent token step (token_kernel.hip) ----
+// Per-layer pointers, kept in device memory and read with uniform loads.
+struct TokLayer {
+    const void*  w[7];      // Q K V O GATE UP DOWN nibble planes (KM4)
+    const void*  s[7];      // their scale planes (fp16 / bf16 quads)
+    const float* norm[6];   // attn, post_attn, ffn, post_ffw, q_norm, k_norm (stored w - 1)
+    uint16_t*    kc;        // fp16 caches [t][head_dim] (one kv head)
+    uint16_t*    vc;
+    uint32_t     global;    // 1: full-context layer, 0: sliding window
+    uint32_t     pad;
+};
+
+struct TokArgs {
+    const TokLayer* layers;
+    uint32_t n_layers, hidden, ffn, n_heads, vocab, window;
+    float eps, embed_scale, attn_scale;
+    int fmt;                              // XP_SCALE_F16_QUAD or XP_SCALE_BF16_QUAD
+    const void* lm_w;
+    const void* lm_s;
+    const float* final_norm;
+    const float* freq_local;              // [head_dim/2] theta^(-2d/head_dim)
+    const float* freq_global;
+    // Exchange slots: 8 bytes = (launch tag << 32) | fp32 bits, written with
+    // one device-coherent store and read until the tag matches. Per layer
+    // (stride ll_layer): xa[hidden] | xb[hidden] | qkv[q_dim + 2 hd] |
+    // attp[grid][n_heads][2 + hd] | atto[q_dim] | o[hidden] | gu[2 ffn] |
+    // dnp[ffn/2048 chunks][hidden]; then am[2 grid] once.
+    unsigned long long* ll;
+    size_t ll_layer;
+    float* logits;                        // [vocab]
+    uint32_t* state;                      // [0] position, [1] token, [2] status
+    uint32_t* hist;                       // [max_seq] token run at each position
+    unsigned long long* trace;            // optional: [stage event][grid] timestamps
+    uint32_t tag;                         // this launch's tag (never 0)
+    uint32_t want_logits;                 // 0: prefill pass without the lm_head
+    uint32_t greedy;                      // 1: the argmax becomes the next token
+};
+
+// Exchange-slot offsets within one layer's block (in slots).
+struct TokLL {
+    size_t xa, xb, qkv, attp, atto, o, gu, dnp, layer;
+};
+__host__ __device__ inline TokLL tok_ll_layout(uint32_t hidden, uint32_t ffn, uint32_t n_heads, uint32_t head_dim,
+                           uint32_t grid) {
+    TokLL t{};
+    const size_t qd = size_t(n_heads) * head_dim;
+    t.xa = 0;
+    t.xb = t.xa + hidden;
+    t.qkv = t.xb + hidden;
+    t.attp = t.qkv + qd + 2 * head_dim;
+    t.atto = t.attp + size_t(grid) * n_heads * (2 + head_dim);
+    t.o = t.atto + qd;
+    t.gu = t.o + hidden;
+    t.dnp = t.gu + 2 * size_t(ffn);
+    t.layer = t.dnp + size_t((ffn + 2047) / 2048) * hidden;
+    t.layer = (t.layer + 31) & ~size_t(31);
+    return t;
+}
+
+constexpr int kTokThreads = 512;
+// Trace events per launch, one timestamp per workgroup each: kernel start,
+// then per layer the completion of QKV, attention, combine, O, gate/up and
+// down (zero where the workgroup had no work), then lm_head and argmax.
+inline uint32_t tok_trace_events(uint32_t n_layers) { return 6u * n_layers + 3u; }
+// Dynamic LDS the token kernel asks for; larger than half a CU's LDS so that
+// no CU holds two of the grid's workgroups.
+size_t tok_lds_bytes();
+// Checks the kernel can run this shape on the current device (grid = CUs).
+int tok_supported(uint32_t hidden, uint32_t ffn, uint32_t n_heads, uint32_t n_kv_heads,
+                  uint32_t head_dim, uint32_t vocab, uint32_t max_seq, int fmt, int n_cu);
+int launch_token(const TokArgs& a, uint32_t grid, hipStream_t st);
+
 }  // namespace xp
