@@ -239,22 +239,24 @@ struct TkTile {
     uint32_t     m;        // matrix index (XP_T_Q .. XP_T_DOWN)
 };
 
-// Wave w's quads of a tile: qa + w and qa + w + 8 (tiles hold at most 16).
+// Wave w's blocks of a tile: 4 qa + w + 8 r for r < 8 (tiles hold at most
+// 16 quads = 64 blocks), each with its scale quad (the block's scale is
+// component b % 4). Spreading blocks rather than quads over the 8 waves keeps
+// a 9-quad tile at 5 blocks per wave.
 struct TkQuads {
-    u32x4 w[2][4];
-    u32x2 s[2];
+    u32x4 w[8];
+    u32x2 s[8];
 };
 
 __device__ __forceinline__ void tk_prefetch(const TkTile& t, TkQuads& p, uint32_t wave,
                                             uint32_t lane) {
+    const uint32_t b1 = 4u * t.qb;
 #pragma unroll
-    for (int r = 0; r < 2; ++r) {
-        const uint32_t q = t.qa + wave + 8u * r;
-        if (q < t.qb) {
-            const u32x4* wp = t.wq + (size_t(t.g) * t.nblk + 4u * q) * kGrp + lane;
-#pragma unroll
-            for (int i = 0; i < 4; ++i) p.w[r][i] = ldg_stream4(wp + i * kGrp);
-            p.s[r] = ldg_stream2(reinterpret_cast<const u32x2*>(t.sc) + size_t(q) * t.cols +
+    for (int r = 0; r < 8; ++r) {
+        const uint32_t b = 4u * t.qa + wave + 8u * r;
+        if (b < b1) {
+            p.w[r] = ldg_stream4(t.wq + (size_t(t.g) * t.nblk + b) * kGrp + lane);
+            p.s[r] = ldg_stream2(reinterpret_cast<const u32x2*>(t.sc) + size_t(b / 4u) * t.cols +
                                  t.g * kGrp + lane);
         }
     }
@@ -275,16 +277,14 @@ __device__ __forceinline__ void tk_stage(TkSmem& S, uint32_t nb) {
 __device__ __forceinline__ float tk_tile(const TkTile& t, const TkQuads& p, TkSmem& S, uint32_t qbase, int fmt,
                          uint32_t wave, uint32_t lane) {
     float acc = 0.0f;
+    const uint32_t b1 = 4u * t.qb;
 #pragma unroll
-    for (int r = 0; r < 2; ++r) {
-        const uint32_t q = t.qa + wave + 8u * r;
-        if (q < t.qb) {
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const uint32_t lb = 4u * (q - qbase) + i;
-                const float f = tk_scale(p.s[r], i, fmt) * S.sx[lb];
-                acc = fmaf(f, float(block_dot(p.w[r][i], S.qx[lb])), acc);
-            }
+    for (int r = 0; r < 8; ++r) {
+        const uint32_t b = 4u * t.qa + wave + 8u * r;
+        if (b < b1) {
+            const uint32_t lb = b - 4u * qbase;
+            const float f = tk_scale(p.s[r], int(b % 4u), fmt) * S.sx[lb];
+            acc = fmaf(f, float(block_dot(p.w[r], S.qx[lb])), acc);
         }
     }
     S.red[wave][lane] = acc;
@@ -530,8 +530,7 @@ __global__ __launch_bounds__(kTkThreads) void token_kernel(TokArgs a) {
                     float d = 0.0f;
 #pragma unroll
                     for (int e = 0; e < 16; ++e) d = fmaf(qp[e], kf[e], d);
-#pragma unroll
-                    for (int o = 8; o > 0; o >>= 1) d += __shfl_xor(d, o, kWave);
+                    d = row16_sum(d);   // the 16 lanes of key jk are one DPP row
                     if (part == 0) S.sc[h][jk] = valid ? d * a.attn_scale : -INFINITY;
                 }
             }

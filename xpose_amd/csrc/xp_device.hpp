@@ -104,8 +104,9 @@ __device__ __forceinline__ void stage_x8(QxBlock* qx, float* sx, uint32_t i, flo
     float m = 0.0f;
 #pragma unroll
     for (int e = 0; e < 8; ++e) m = fmaxf(m, fabsf(v[e]));
-    m = fmaxf(m, __shfl_xor(m, 1, kWave));
-    m = fmaxf(m, __shfl_xor(m, 2, kWave));
+    // max over the block's four tasks (one lane quad): quad_perm xor 1, xor 2
+    m = fmaxf(m, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(m), 0xB1, 0xF, 0xF, false)));
+    m = fmaxf(m, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(m), 0x4E, 0xF, 0xF, false)));
     const float r = m > 0.0f ? kQxRange / m : 0.0f;
     uint32_t t[8];
     // q + bias has hex digits d_p + 8; xor-ing the bias back gives each
@@ -158,16 +159,38 @@ __device__ __forceinline__ uint32_t take_ticket(uint32_t* t) {
                                   __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// Wave-wide sum / max via DPP-backed shuffles.
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
+// Wave-wide sum / max with DPP row operations (a few cycles per step, no LDS
+// round trip): xor 1 and xor 2 inside quads, the half-row and row mirrors
+// for 8 and 16 lanes, then row_bcast:15 / row_bcast:31 fold the four rows
+// into lane 63, whose value is read back as a wave-uniform scalar.
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ float dpp_f(float v, float old) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(old), __float_as_int(v), CTRL,
+                                                      ROW_MASK, 0xF, false));
+}
+// Sum over each row of 16 lanes, left in every lane of the row.
+__device__ __forceinline__ float row16_sum(float v) {
+    v += dpp_f<0xB1, 0xF>(v, 0.0f);    // quad_perm [1,0,3,2]
+    v += dpp_f<0x4E, 0xF>(v, 0.0f);    // quad_perm [2,3,0,1]
+    v += dpp_f<0x141, 0xF>(v, 0.0f);   // row_half_mirror
+    v += dpp_f<0x140, 0xF>(v, 0.0f);   // row_mirror
     return v;
 }
+__device__ __forceinline__ float wave_sum(float v) {
+    v = row16_sum(v);
+    v += dpp_f<0x142, 0xA>(v, 0.0f);   // row_bcast:15 -> rows 1, 3
+    v += dpp_f<0x143, 0xC>(v, 0.0f);   // row_bcast:31 -> rows 2, 3
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+}
+// Lanes a step does not write read -inf, the max identity.
 __device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, kWave));
-    return v;
+    v = fmaxf(v, dpp_f<0xB1, 0xF>(v, -INFINITY));
+    v = fmaxf(v, dpp_f<0x4E, 0xF>(v, -INFINITY));
+    v = fmaxf(v, dpp_f<0x141, 0xF>(v, -INFINITY));
+    v = fmaxf(v, dpp_f<0x140, 0xF>(v, -INFINITY));
+    v = fmaxf(v, dpp_f<0x142, 0xA>(v, -INFINITY));
+    v = fmaxf(v, dpp_f<0x143, 0xC>(v, -INFINITY));
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
 }
 
 // (value, index) argmax step: larger value wins, then the lower index
