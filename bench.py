@@ -6,10 +6,16 @@ the CPU baseline (the oracle's C restatement on the host cores).
                     [--cpu-seconds S] [--no-cpu]
 
 A step is one decode token: embed, 26 layers, final norm, the 262144-wide
-lm_head and the on-device argmax that picks the next token. Weights (random
-int4, fp16 group scales) and the KV cache (fp16 N(0,1) rows 0..ctx-1) are
-resident in HBM before timing; the K timed steps are queued back to back
-between two device synchronisations. Prints one JSON line.
+lm_head and the on-device argmax that picks the next token — one launch of
+the persistent token kernel. Weights (random int4, fp16 group scales) and the
+KV cache (fp16 N(0,1) rows 0..ctx-1) are resident in HBM before timing; the K
+timed steps are queued back to back between two device synchronisations.
+
+`roofline` prices the token kernel (the only kernel of the step): algorithmic
+HBM bytes of one token at its mean position over the kernel's mean duration,
+taken with HIP events on the session's stream around the K launches. The
+standalone int4 matvec (lm_head shape, and BASELINE config 1's gate shape with
+64 rotating weight copies) is reported beside it. Prints one JSON line.
 """
 from __future__ import annotations
 
@@ -26,6 +32,10 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0          # MI355X HBM3E
+# Measured HBM bytes of one token-kernel launch at this workload: rocprofv3
+# FETCH_SIZE x 2.0 + WRITE_SIZE x 1.0 (factors from a 256 MiB copy), see
+# profiles/token_kernel_gemma3_1b_ctx4096.md.
+TOKEN_TRAFFIC_BYTES = 654_004_367 + 13_731_901
 SEED = 0x5EED0003
 # Algorithmic HBM bytes of one token at seq_len s (weights + fp16 scales,
 # KV reads, norm weights, logits write + argmax read, KV append).
@@ -68,6 +78,16 @@ def matvec_leg(X, rows: int, cols: int, copies: int, iters: int):
     return nbytes, per_s
 
 
+def stream_ceiling(X, nbytes: int = 1 << 30, iters: int = 20) -> float:
+    """Achievable HBM read bandwidth (GB/s): the 16-byte streaming probe over a
+    1 GiB buffer (4x the Infinity Cache)."""
+    buf = X.DeviceBuffer(nbytes)
+    X.call("xp_memset", buf.vp, 0, nbytes)
+    ms = C.c_float()
+    X.call("xp_stream_read_timed", buf.vp, nbytes, iters, None, C.byref(ms))
+    return nbytes * iters / (ms.value / 1e3) / 1e9
+
+
 def cpu_baseline(X, cfg, ctx: int, seconds: float, threads: int):
     """The oracle (C restatement, OpenMP over output columns) decoding greedy
     tokens of the same model from position ctx, for about `seconds`."""
@@ -108,6 +128,8 @@ def main() -> int:
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--mv-iters", type=int, default=60)
+    ap.add_argument("--only", choices=["all", "matvec"], default="all",
+                    help="matvec: only the standalone matvec and streaming legs (for profiling)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported "
@@ -122,6 +144,23 @@ def main() -> int:
     import xpose_amd as X
     X.init(0)
     info = X.device_info()
+    if args.only == "matvec":
+        nbytes, per_s = matvec_leg(X, 1152, 262144, copies=3, iters=args.mv_iters)
+        nb1, per1 = matvec_leg(X, 1152, 6912, copies=64, iters=640)
+        ceil = stream_ceiling(X)
+        # A 256 MiB copy: 256 MiB fetched and 256 MiB written, the calibration
+        # point for rocprofv3's FETCH_SIZE / WRITE_SIZE counters.
+        cb = 256 << 20
+        src, dst = X.DeviceBuffer(cb), X.DeviceBuffer(cb)
+        X.call("xp_memset", src.vp, 1, cb)
+        X.call("xp_copy", dst.vp, src.vp, cb, None)
+        X.synchronize()
+        print(json.dumps({"matvec_lm_head": {"us_per_launch": round(per_s * 1e6, 3),
+                                             "GBs": round(nbytes / per_s / 1e9, 1)},
+                          "matvec_cfg1": {"us_per_launch": round(per1 * 1e6, 3),
+                                          "GBs": round(nb1 / per1 / 1e9, 1)},
+                          "stream_ceiling_GBs": round(ceil, 1)}), flush=True)
+        return 0
     ctx = args.ctx
     cfg = X.XpConfig.gemma3_1b(max_seq=8192)
     if ctx + 1 + args.warmup + args.steps > cfg.max_seq:
@@ -149,6 +188,7 @@ def main() -> int:
     tb = token_bytes(mid_seq)
     met = sess.last_metrics()
     launches = met.launches
+    kern_s = met.gpu_ms / 1e3 / args.steps          # device time per token-kernel launch
     exec_mode = {1: "graph", 2: "launch", 3: "token-kernel"}.get(met.exec_mode, str(met.exec_mode))
     sess.close()
 
@@ -157,6 +197,7 @@ def main() -> int:
     achieved = nbytes / per_s / 1e9
     # BASELINE config 1 shape (gate 6912 x 1152), 64 rotating copies.
     nb1, per1 = matvec_leg(X, 1152, 6912, copies=64, iters=640)
+    ceil = stream_ceiling(X)
 
     cpu = None
     if not args.no_cpu:
@@ -184,12 +225,17 @@ def main() -> int:
                    "layers": 26, "hidden": 1152, "vocab": 262144, "weights": "int4 g32 + fp16",
                    "kv": "fp16", "launches_per_step": launches,
                    "exec": exec_mode},
-        "roofline": {"bound": "hbm", "kernel": "mv_int4 lm_head 1152x262144",
-                     "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
-                     "bytes_per_launch": nbytes, "us_per_launch": round(per_s * 1e6, 3)},
-        "token_roofline": {"bytes_per_token": tb, "roofline_tok_s": round(HBM_PEAK_GBS * 1e9 / tb, 1),
-                           "frac": round(tok_s * tb / (HBM_PEAK_GBS * 1e9), 4)},
+        "roofline": {"bound": "hbm", "kernel": "token_kernel (whole decode token)",
+                     "achieved": round(tb / kern_s / 1e9, 1), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(tb / kern_s / 1e9 / HBM_PEAK_GBS, 4),
+                     "traffic": TOKEN_TRAFFIC_BYTES, "bytes_per_launch": tb,
+                     "us_per_launch": round(kern_s * 1e6, 3),
+                     "roofline_tok_s": round(HBM_PEAK_GBS * 1e9 / tb, 1)},
+        "matvec_lm_head": {"shape": "262144x1152", "bytes": nbytes,
+                           "us_per_launch": round(per_s * 1e6, 3),
+                           "GBs": round(achieved, 1), "frac": round(achieved / HBM_PEAK_GBS, 4),
+                           "frac_of_stream_ceiling": round(achieved / ceil, 4)},
+        "stream_ceiling_GBs": round(ceil, 1),
         "matvec_cfg1": {"shape": "6912x1152", "bytes": nb1, "us_per_launch": round(per1 * 1e6, 3),
                         "GBs": round(nb1 / per1 / 1e9, 1)},
         "cpu_baseline": cpu,

@@ -115,6 +115,17 @@ int xp_unpack_km4(int8_t* out, const void* wq, uint32_t rows, uint32_t cols,
  * fp16_decode sweep kernel, kernels/llm_quant.cl:79-87). */
 int xp_fp16_decode(float* out, const uint16_t* src, uint32_t n, xp_stream stream);
 
+/* Bandwidth probes. xp_stream_read_timed: `iters` launches that read `bytes`
+ * with 16-byte loads and write nothing (the reference's stream4 probe,
+ * kernels/llm_matvec.cl:357-378), bracketed by HIP events; *ms = their total
+ * time. The measured ceiling the matvec and the token step are reported
+ * against beside the spec peak. xp_copy: dst = src (16-byte aligned, bytes a
+ * multiple of 16) — a transfer of known size for calibrating HBM byte
+ * counters. */
+int xp_stream_read_timed(const void* buf, size_t bytes, uint32_t iters, xp_stream stream,
+                         float* ms);
+int xp_copy(void* dst, const void* src, size_t bytes, xp_stream stream);
+
 /* Two-pass Gemma RMSNorm in one launch: out = in * rsqrt(mean(in^2)+eps) *
  * (1 + w). Replaces rmsnorm_sumsq + rmsnorm_apply_gemma
  * (kernels/llm_transformer.cl:96-116). out may alias in. */
@@ -246,7 +257,9 @@ enum xp_tensor {
 
 typedef struct {
     double   ms;            /* wall time of the last call */
-    double   gpu_ms;        /* graph replays + wait */
+    double   gpu_ms;        /* decode_step: launch + wait (host clock);
+                               decode_steps: HIP events on the session stream
+                               around the queued steps (device time) */
     double   sample_ms;     /* host draw (temperature mode) */
     double   tokens_per_sec;
     uint32_t position;

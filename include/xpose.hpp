@@ -1,0 +1,166 @@
+// xpose.hpp — C++ host interface of the MI355X Gemma-3 decode path.
+//
+// Mirrors vulkore::llm::DecodeSession (examples/llm/decode.hpp:605-676) over
+// the C ABI of xpose.h, so the reference's callers (the decode CLI,
+// examples/llm/decode.cpp:2720-3006, and the Android JNI layer,
+// android/app/src/main/cpp/llm_jni.cpp:110-164) switch by changing the class
+// they construct:
+//
+//   reference                                 here
+//   DecodeSession(Paths, DecodeConfig)        DecodeSession(Config) + upload /
+//                                             synthesize (weights arrive packed)
+//   prefill(std::span<const uint32_t>)        prefill(const uint32_t*, size_t) /
+//                                             prefill(const std::vector<uint32_t>&)
+//   uint32_t decode_step()                    uint32_t decode_step()
+//   reset(), position(), config()             same
+//   last_metrics(), last_logits()             same (Metrics mirrors the reference's)
+//   last_candidates()                         same ((value, index) pairs)
+//   weight_bytes(), kv_bytes(), device_name() same
+//
+// Errors are exceptions, as in the reference (check.hpp:16-35, decode.cpp:
+// 46-56): every failing entry point throws std::runtime_error carrying the
+// entry point's name and the library's message. Header-only; link libxpose.so.
+#ifndef XPOSE_HPP
+#define XPOSE_HPP
+
+#include <cstddef>
+#include <cstdint>
+#include <stdexcept>
+#include <string>
+#include <utility>
+#include <vector>
+
+#include "xpose.h"
+
+namespace xpose {
+
+inline void check(int rc, const char* what) {
+    if (rc != XP_OK)
+        throw std::runtime_error(std::string(what) + " failed (" + std::to_string(rc) +
+                                 "): " + xp_last_error());
+}
+
+namespace llm {
+
+// The reference's Sampling + DecodeConfig, one struct (decode.hpp:153-436).
+struct Config : xp_config {
+    Config() { xp_config_gemma3_1b(this); }
+    static Config gemma3_1b() { return Config(); }
+};
+
+// decode.hpp:573-582, with the execution mode in place of submits.
+struct Metrics {
+    double   ms             = 0;
+    double   gpu_ms         = 0;
+    double   sample_ms      = 0;
+    double   tokens_per_sec = 0;
+    uint32_t dispatches     = 0;   // kernel launches per token step
+    uint32_t position       = 0;
+    int32_t  exec_mode      = 0;   // XP_EXEC_TOKEN, _GRAPH or _LAUNCH
+};
+
+class DecodeSession {
+public:
+    explicit DecodeSession(const Config& cfg) : cfg_(cfg) {
+        check(xp_init(0), "xp_init");
+        check(xp_session_create(&cfg_, &s_), "xp_session_create");
+    }
+    ~DecodeSession() {
+        if (s_) xp_session_destroy(s_);
+    }
+    DecodeSession(const DecodeSession&) = delete;
+    DecodeSession& operator=(const DecodeSession&) = delete;
+
+    // Packed weights (KM4 nibble planes, quad scale planes, norm weights
+    // stored as multiplier - 1): the reference's upload_packed
+    // (decode.cpp:652) with the layout of xpose.h.
+    void upload(int layer, int tensor, const void* host, size_t bytes) {
+        check(xp_session_upload(s_, layer, tensor, host, bytes), "xp_session_upload");
+    }
+    // The seeded synthetic model of the benchmark configurations.
+    void synthesize(uint32_t seed) { check(xp_session_synthesize(s_, seed), "xp_session_synthesize"); }
+    void set_position(uint32_t pos) { check(xp_session_set_position(s_, pos), "xp_session_set_position"); }
+    void kv_upload(int layer, int which, uint32_t pos0, uint32_t n, const uint16_t* rows) {
+        check(xp_session_kv_upload(s_, layer, which, pos0, n, rows), "xp_session_kv_upload");
+    }
+
+    void prefill(const uint32_t* ids, size_t n) {
+        check(xp_session_prefill(s_, ids, uint32_t(n)), "xp_session_prefill");
+    }
+    void prefill(const std::vector<uint32_t>& ids) { prefill(ids.data(), ids.size()); }
+
+    uint32_t decode_step() {
+        uint32_t t = 0;
+        check(xp_session_decode_step(s_, &t), "xp_session_decode_step");
+        return t;
+    }
+    // n greedy steps queued behind one wait (greedy mode only).
+    std::vector<uint32_t> decode_steps(uint32_t n) {
+        std::vector<uint32_t> out(n);
+        check(xp_session_decode_steps(s_, n, out.data()), "xp_session_decode_steps");
+        return out;
+    }
+    void reset() { check(xp_session_reset(s_), "xp_session_reset"); }
+
+    uint32_t position() const {
+        uint32_t p = 0;
+        check(xp_session_position(s_, &p), "xp_session_position");
+        return p;
+    }
+    const Config& config() const { return cfg_; }
+    Metrics last_metrics() const {
+        xp_metrics m{};
+        check(xp_session_last_metrics(s_, &m), "xp_session_last_metrics");
+        Metrics r;
+        r.ms = m.ms;
+        r.gpu_ms = m.gpu_ms;
+        r.sample_ms = m.sample_ms;
+        r.tokens_per_sec = m.tokens_per_sec;
+        r.dispatches = m.launches;
+        r.position = m.position;
+        r.exec_mode = m.exec_mode;
+        return r;
+    }
+    std::vector<float> last_logits() const {
+        std::vector<float> v(cfg_.vocab);
+        check(xp_session_last_logits(s_, v.data(), cfg_.vocab), "xp_session_last_logits");
+        return v;
+    }
+    std::vector<std::pair<float, uint32_t>> last_candidates() const {
+        const uint32_t n = 4 * cfg_.topk_parts;
+        std::vector<float> v(n);
+        std::vector<uint32_t> i(n);
+        check(xp_session_last_candidates(s_, v.data(), i.data(), n), "xp_session_last_candidates");
+        std::vector<std::pair<float, uint32_t>> r;
+        r.reserve(n);
+        for (uint32_t k = 0; k < n; ++k)
+            if (i[k] != 0xFFFFFFFFu) r.emplace_back(v[k], i[k]);
+        return r;
+    }
+    uint64_t weight_bytes() const {
+        size_t b = 0;
+        check(xp_session_weight_bytes(s_, &b), "xp_session_weight_bytes");
+        return b;
+    }
+    uint64_t kv_bytes() const {
+        size_t b = 0;
+        check(xp_session_kv_bytes(s_, &b), "xp_session_kv_bytes");
+        return b;
+    }
+    std::string device_name() const {
+        char name[256] = {0}, arch[64] = {0};
+        int n_cu = 0;
+        size_t hbm = 0;
+        check(xp_device_info(name, sizeof name, &n_cu, &hbm, arch, sizeof arch), "xp_device_info");
+        return std::string(name) + " (" + arch + ")";
+    }
+
+private:
+    Config cfg_;
+    xp_session* s_ = nullptr;
+};
+
+}  // namespace llm
+}  // namespace xpose
+
+#endif  // XPOSE_HPP

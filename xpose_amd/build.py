@@ -31,7 +31,7 @@ HIP_FLAGS = [
 ]
 
 LIB_SOURCES = ["runtime.cpp", "synth.cpp", "matvec.hip", "transformer.hip", "sampling.hip",
-               "token_kernel.hip",
+               "token_kernel.hip", "probe.hip",
                "session_kernels.hip", "session.cpp"]
 
 
@@ -69,6 +69,22 @@ def build_lib(verbose: bool = False, extra: list[str] | None = None) -> str:
     return LIB
 
 
+CLI_SRC = os.path.join(ROOT, "xpose_amd", "cli", "xpose_decode.cpp")
+CLI_BIN = os.path.join(ROOT, "xpose_amd", "bin", "xpose_decode")
+
+
+def build_cli(verbose: bool = False) -> str:
+    """The C++ decode CLI over include/xpose.hpp (host code only, links
+    libxpose.so, found next to it at run time through $ORIGIN)."""
+    os.makedirs(os.path.dirname(CLI_BIN), exist_ok=True)
+    tmp = CLI_BIN + ".tmp"
+    _run(["g++", "-O2", "-std=c++17", "-Wall", "-I", os.path.join(ROOT, "include"), CLI_SRC,
+          "-o", tmp, "-L", os.path.dirname(LIB), "-l:libxpose.so",
+          "-Wl,-rpath,$ORIGIN/..", "-Wl,-rpath-link,/opt/rocm/lib"], verbose)
+    os.replace(tmp, CLI_BIN)
+    return CLI_BIN
+
+
 def build_oracle(verbose: bool = False) -> str:
     # -ffp-contract=off: every a*b+c in the restatement rounds twice, exactly
     # as written; -march=x86-64-v3 so the object runs on any AVX2 host.
@@ -83,6 +99,7 @@ def build_oracle(verbose: bool = False) -> str:
 def build_all(verbose: bool = False) -> None:
     build_oracle(verbose)
     build_lib(verbose)
+    build_cli(verbose)
 
 
 if __name__ == "__main__":

@@ -1,0 +1,155 @@
+// xpose_decode — command-line decode driver over include/xpose.hpp, the
+// counterpart of the reference's decode CLI (examples/llm/decode.cpp:
+// 2720-3006) for the seeded synthetic Gemma-3-1B model (no GGUF or tokenizer
+// on this path: weights are random int4 with fp16 group scales).
+//
+//   xpose_decode [--layers N] [--prompt N] [--tokens N] [--ctx P] [--seed S]
+//                [--exec token|graph|launch] [--curve] [--ids]
+//
+// --ctx P pre-fills every layer's KV cache with fp16 N(0,1) rows 0..P-1 and
+// decodes from position P; otherwise a --prompt of
+// uniform-random ids is prefilled first (config 3). --curve reports tok/s per
+// 512-position bucket and the deepest/shallowest ratio, the reference's
+// flatness metric (decode.cpp:2977-2999). Prints per-step gpu ms min / median
+// / mean like the reference (decode.cpp:2961-2972).
+#include <algorithm>
+#include <chrono>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <map>
+#include <string>
+#include <vector>
+
+#include "xpose.hpp"
+
+namespace {
+
+double now_ms() {
+    using namespace std::chrono;
+    return duration<double, std::milli>(steady_clock::now().time_since_epoch()).count();
+}
+
+int usage() {
+    std::fprintf(stderr,
+                 "usage: xpose_decode [--layers N] [--prompt N] [--tokens N] [--ctx P] "
+                 "[--seed S] [--exec token|graph|launch] [--curve] [--ids]\n");
+    return 2;
+}
+
+}  // namespace
+
+int main(int argc, char** argv) {
+    uint32_t layers = 26, prompt = 32, tokens = 128, ctx = 0, seed = 0x5EED0003u;
+    int exec = XP_EXEC_AUTO;
+    bool curve = false, print_ids = false;
+    for (int i = 1; i < argc; ++i) {
+        const std::string a = argv[i];
+        auto next = [&]() -> const char* { return i + 1 < argc ? argv[++i] : nullptr; };
+        const char* v = nullptr;
+        if (a == "--layers" && (v = next())) layers = uint32_t(std::strtoul(v, nullptr, 0));
+        else if (a == "--prompt" && (v = next())) prompt = uint32_t(std::strtoul(v, nullptr, 0));
+        else if (a == "--tokens" && (v = next())) tokens = uint32_t(std::strtoul(v, nullptr, 0));
+        else if (a == "--ctx" && (v = next())) ctx = uint32_t(std::strtoul(v, nullptr, 0));
+        else if (a == "--seed" && (v = next())) seed = uint32_t(std::strtoul(v, nullptr, 0));
+        else if (a == "--exec" && (v = next())) {
+            const std::string m = v;
+            exec = m == "token" ? XP_EXEC_TOKEN : m == "graph" ? XP_EXEC_GRAPH
+                 : m == "launch" ? XP_EXEC_LAUNCH : -1;
+            if (exec < 0) return usage();
+        } else if (a == "--curve") curve = true;
+        else if (a == "--ids") print_ids = true;
+        else return usage();
+    }
+    try {
+        xpose::llm::Config cfg;
+        cfg.n_layers = layers;
+        cfg.exec_mode = exec;
+        const double t0 = now_ms();
+        xpose::llm::DecodeSession sess(cfg);
+        sess.synthesize(seed);
+        const double load_ms = now_ms() - t0;
+        std::printf("device      %s\n", sess.device_name().c_str());
+        std::printf("weights     %.1f MiB packed int4 + fp16 scales (synthesised in %.0f ms)\n",
+                    double(sess.weight_bytes()) / (1024.0 * 1024.0), load_ms);
+        std::printf("kv cache    %.1f MiB (%u positions)\n",
+                    double(sess.kv_bytes()) / (1024.0 * 1024.0), cfg.max_seq);
+
+        std::vector<uint32_t> ids;
+        if (ctx > 0) {
+            const uint32_t row = cfg.n_kv_heads * cfg.head_dim;
+            std::vector<uint16_t> rows(size_t(ctx) * row);
+            for (uint32_t l = 0; l < cfg.n_layers; ++l)
+                for (int which = 0; which < 2; ++which) {
+                    xpose::check(xp_synth_normal_f16(rows.data(), rows.size(), 0.0f, 1.0f, ctx,
+                                                     2u * l + uint32_t(which)),
+                                 "xp_synth_normal_f16");
+                    sess.kv_upload(int(l), which, 0, ctx, rows.data());
+                }
+            sess.set_position(ctx);
+            ids.push_back(4242);
+        } else {
+            // Prompt ids uniform on [0, vocab): Philox stream 0x7000.
+            for (uint32_t i = 0; i < prompt; ++i) {
+                const uint32_t c[4] = {i, 0u, 0u, 0u}, k[2] = {seed, 0x7000u};
+                uint32_t o[4];
+                xp_philox4x32_10(c, k, o);
+                ids.push_back(o[0] % cfg.vocab);
+            }
+        }
+        if (ids.size() + ctx + tokens > cfg.max_seq) {
+            std::fprintf(stderr, "xpose_decode: %zu + %u + %u positions exceed max_seq %u\n",
+                         ids.size(), ctx, tokens, cfg.max_seq);
+            return 2;
+        }
+        sess.prefill(ids);
+        const auto pm = sess.last_metrics();
+        const char* mode = pm.exec_mode == XP_EXEC_TOKEN ? "persistent token kernel"
+                         : pm.exec_mode == XP_EXEC_GRAPH ? "captured graph" : "per-op launches";
+        std::printf("execution   %s, %u launch(es) per token\n", mode, pm.dispatches);
+        std::printf("prefill     %zu tokens in %.2f ms\n\n", ids.size(), pm.ms);
+
+        std::vector<double> step_ms;
+        std::vector<uint32_t> pos_of, out;
+        double total = 0;
+        for (uint32_t i = 0; i < tokens; ++i) {
+            out.push_back(sess.decode_step());
+            const auto m = sess.last_metrics();
+            step_ms.push_back(m.gpu_ms);
+            pos_of.push_back(m.position);
+            total += m.ms;
+        }
+        std::printf("decode      %u tokens, %.4f ms/token, %.1f tok/s (host wall per step)\n",
+                    tokens, total / tokens, tokens * 1000.0 / total);
+        std::vector<double> s = step_ms;
+        std::sort(s.begin(), s.end());
+        double sum = 0;
+        for (double x : s) sum += x;
+        std::printf("gpu ms      min %.4f | median %.4f | mean %.4f   (n=%zu)\n", s.front(),
+                    s[s.size() / 2], sum / double(s.size()), s.size());
+        if (curve) {
+            std::map<uint32_t, std::vector<double>> b;
+            for (size_t i = 0; i < step_ms.size(); ++i) b[(pos_of[i] - 1) / 512].push_back(step_ms[i]);
+            double lo = 1e30, hi = 0;
+            std::printf("\nposition bucket      tok/s     median ms\n");
+            for (auto& kv : b) {
+                std::sort(kv.second.begin(), kv.second.end());
+                const double med = kv.second[kv.second.size() / 2];
+                lo = std::min(lo, med);
+                hi = std::max(hi, med);
+                std::printf("%5u-%-5u      %9.1f    %.4f\n", kv.first * 512, kv.first * 512 + 511,
+                            1000.0 / med, med);
+            }
+            std::printf("deepest / shallowest median ms: %.3f\n", hi / lo);
+        }
+        if (print_ids) {
+            std::printf("ids");
+            for (uint32_t t : out) std::printf(" %u", t);
+            std::printf("\n");
+        }
+    } catch (const std::exception& e) {
+        std::fprintf(stderr, "xpose_decode: %s\n", e.what());
+        return 1;
+    }
+    return 0;
+}

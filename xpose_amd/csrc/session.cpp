@@ -162,6 +162,7 @@ struct Session {
     uint32_t* state = nullptr;   // [0] position, [1] token
     uint32_t* hist = nullptr;    // [max_seq] token run at each position
     uint32_t* h_ids = nullptr;   // pinned staging for host-chosen token ids
+    uint32_t* h_stat = nullptr;  // pinned: [0] device status word after a step
     hipGraphExec_t graph[3] = {nullptr, nullptr, nullptr};   // prefill, greedy, harvest
     uint32_t launches[3] = {0, 0, 0};
     int mode = XP_EXEC_GRAPH;    // XP_EXEC_TOKEN (persistent kernel), _GRAPH or _LAUNCH
@@ -171,6 +172,7 @@ struct Session {
     uint32_t tok_grid = 0;
     uint32_t tag = 0;            // tag of the last queued launch (exchange slots)
     unsigned long long* trace_buf = nullptr;
+    hipEvent_t ev[2] = {nullptr, nullptr};   // decode_steps: device time of the queued steps
     uint32_t pos = 0;
     uint32_t step = 0;           // draws made (Philox counter)
     bool logits_valid = false;
@@ -380,6 +382,8 @@ int destroy(xp_session* h) {
     Session& s = h->s;
     for (auto& g : s.graph)
         if (g) (void)hipGraphExecDestroy(g);
+    for (auto& e : s.ev)
+        if (e) (void)hipEventDestroy(e);
     if (s.st) (void)hipStreamSynchronize(s.st);
     if (s.warena) (void)hipFree(s.warena);
     if (s.kvarena) (void)hipFree(s.kvarena);
@@ -387,6 +391,7 @@ int destroy(xp_session* h) {
     if (s.tarena) (void)hipFree(s.tarena);
     if (s.trace_buf) (void)hipFree(s.trace_buf);
     if (s.h_ids) (void)hipHostFree(s.h_ids);
+    if (s.h_stat) (void)hipHostFree(s.h_stat);
     if (s.st) (void)hipStreamDestroy(s.st);
     delete h;
     return XP_OK;
@@ -412,7 +417,6 @@ int sample_from_candidates(Session& s, uint32_t& token) {
 int setup_token(Session& s) {
     const xp_config& c = s.cfg;
     const uint32_t grid = uint32_t(s.n_cu);
-    const uint32_t qd = c.n_heads * c.head_dim;
     const TokLL lay = tok_ll_layout(c.hidden, c.ffn, c.n_heads, c.head_dim, grid);
     const size_t sizes[] = {
         size_t(c.n_layers) * sizeof(TokLayer),                   // layer table
@@ -478,14 +482,20 @@ int setup_token(Session& s) {
 }
 
 // Device status word of the persistent kernel (state[2]): non-zero after a
-// barrier wait ran past its spin limit.
+// wait for another workgroup's data ran past its spin limit. queue_status
+// copies it to pinned memory behind the queued work; check_status reads that
+// copy after the stream has been synchronised.
+int queue_status(Session& s) {
+    if (s.mode != XP_EXEC_TOKEN) return XP_OK;
+    XP_HIP(hipMemcpyAsync(s.h_stat, s.state + 2, 4, hipMemcpyDeviceToHost, s.st));
+    return XP_OK;
+}
 int check_status(Session& s) {
     if (s.mode != XP_EXEC_TOKEN) return XP_OK;
-    uint32_t status = 0;
-    XP_HIP(hipMemcpy(&status, s.state + 2, 4, hipMemcpyDeviceToHost));
-    if (status != 0)
-        return set_error(XP_E_DEVICE, "token kernel: a device-wide barrier timed out (status %u); "
-                         "the session's results are invalid", status);
+    if (s.h_stat[0] != 0)
+        return set_error(XP_E_DEVICE, "token kernel: a wait for another workgroup's data ran "
+                         "past its spin limit (status %u); the session's results are invalid",
+                         s.h_stat[0]);
     return XP_OK;
 }
 
@@ -673,8 +683,8 @@ int xp_session_create(const xp_config* cfg, xp_session** out) {
         s.am_out = (float*)nxt(); s.cand_val = (float*)nxt(); s.cand_idx = (uint32_t*)nxt();
         s.state = (uint32_t*)nxt(); s.hist = (uint32_t*)nxt();
         if (hipHostMalloc(reinterpret_cast<void**>(&s.h_ids), size_t(c.max_seq) * 4) !=
-            hipSuccess) {
-            s.h_ids = nullptr;
+                hipSuccess ||
+            hipHostMalloc(reinterpret_cast<void**>(&s.h_stat), 16) != hipSuccess) {
             destroy(h);
             return set_error(XP_E_NOMEM, "xp_session_create: pinned staging");
         }
@@ -817,6 +827,7 @@ int xp_session_prefill(xp_session* h, const uint32_t* ids, uint32_t n) {
         int rc = s.run(i + 1 == n ? last : 0);
         if (rc != XP_OK) return rc;
     }
+    if (int rc = queue_status(s); rc != XP_OK) return rc;
     XP_HIP(hipStreamSynchronize(s.st));
     if (int rc = check_status(s); rc != XP_OK) return rc;
     s.pos += n;
@@ -850,6 +861,7 @@ int xp_session_decode_step(xp_session* h, uint32_t* token) {
     int rc = s.run(variant);
     if (rc != XP_OK) return rc;
     XP_HIP(hipMemcpyAsync(s.h_ids + 1, s.hist + s.pos, 4, hipMemcpyDeviceToHost, s.st));
+    if (int rc2 = queue_status(s); rc2 != XP_OK) return rc2;
     XP_HIP(hipStreamSynchronize(s.st));
     if (int rc2 = check_status(s); rc2 != XP_OK) return rc2;
     *token = s.h_ids[1];
@@ -869,18 +881,27 @@ int xp_session_decode_steps(xp_session* h, uint32_t n, uint32_t* tokens) {
         return set_error(XP_E_STATE, "decode_steps() before prefill()");
     if (uint64_t(s.pos) + n > s.cfg.max_seq)
         return set_error(XP_E_STATE, "KV cache is full (max_seq %u)", s.cfg.max_seq);
+    if (!s.ev[0]) {
+        XP_HIP(hipEventCreate(&s.ev[0]));
+        XP_HIP(hipEventCreate(&s.ev[1]));
+    }
     const double t0 = now_ms();
+    XP_HIP(hipEventRecord(s.ev[0], s.st));
     for (uint32_t i = 0; i < n; ++i) {
         int rc = s.run(1);
         if (rc != XP_OK) return rc;
     }
+    XP_HIP(hipEventRecord(s.ev[1], s.st));
+    if (int rc = queue_status(s); rc != XP_OK) return rc;
     XP_HIP(hipStreamSynchronize(s.st));
     const double t1 = now_ms();
+    float dev_ms = 0.0f;
+    XP_HIP(hipEventElapsedTime(&dev_ms, s.ev[0], s.ev[1]));
     if (int rc = check_status(s); rc != XP_OK) return rc;
     if (tokens) XP_HIP(hipMemcpy(tokens, s.hist + s.pos, size_t(n) * 4, hipMemcpyDeviceToHost));
     s.pos += n;
-    s.met = xp_metrics{t1 - t0, t1 - t0, 0.0, (t1 - t0) > 0 ? n * 1000.0 / (t1 - t0) : 0.0, s.pos,
-                       s.launches[1], s.mode};
+    s.met = xp_metrics{t1 - t0, double(dev_ms), 0.0, (t1 - t0) > 0 ? n * 1000.0 / (t1 - t0) : 0.0,
+                       s.pos, s.launches[1], s.mode};
     return XP_OK;
 }
 

@@ -144,7 +144,6 @@ constexpr int kAttnThreads  = 256;
 constexpr int kAttnMinChunk = 32;    // keys per workgroup at short spans
 constexpr int kAttnChunk    = 128;   // most keys one workgroup takes
 constexpr int kAttnMaxSplit = 64;    // workgroups per kv head
-constexpr int kAttnMaxGrp   = 8;     // query heads per kv head
 
 __device__ __forceinline__ void attn_range(const AttnArgs& a, uint32_t& span, uint32_t& kv0) {
     if (a.pos_dev) {

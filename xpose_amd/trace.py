@@ -1,0 +1,76 @@
+"""Stage timeline of the persistent token kernel.
+
+    python -m xpose_amd.trace [--ctx 4096] [--layers 26] [--seed S]
+
+Builds the seeded synthetic Gemma-3-1B model, pre-fills the KV cache to
+position ctx (fp16 N(0,1)), decodes a few warm-up tokens, then records one
+token with xp_session_trace and prints, per layer, how long each of the six
+stages added to the critical path: the time from the previous stage's last
+finisher to this stage's last finisher (100 MHz s_memrealtime stamps).
+"""
+from __future__ import annotations
+
+import argparse
+
+import numpy as np
+
+STAGES = ("QKV", "attention", "combine", "O", "gate/up", "down")
+
+
+def timeline(tr: np.ndarray, n_layers: int):
+    """Per-layer stage increments (us), lm_head and argmax increments, total."""
+    tr = tr.astype(np.int64)
+    t0 = tr[0][tr[0] > 0].min()
+    prev = 0.0
+    rows = []
+    for l in range(n_layers):
+        inc = []
+        for k in range(6):
+            end = (tr[1 + 6 * l + k].max() - t0) / 100.0
+            inc.append(end - prev)
+            prev = end
+        rows.append(inc)
+    lm = (tr[6 * n_layers + 1].max() - t0) / 100.0
+    am = (tr[6 * n_layers + 2].max() - t0) / 100.0
+    return np.array(rows), lm - prev, am - lm, am
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--ctx", type=int, default=4096)
+    ap.add_argument("--layers", type=int, default=26)
+    ap.add_argument("--seed", type=lambda s: int(s, 0), default=0x5EED0003)
+    args = ap.parse_args()
+    import xpose_amd as X
+    X.init(0)
+    cfg = X.XpConfig.gemma3_1b(n_layers=args.layers, exec_mode=X.XP_EXEC_TOKEN)
+    sess = X.DecodeSession(cfg)
+    sess.synthesize(args.seed)
+    kvd = cfg.n_kv_heads * cfg.head_dim
+    for l in range(cfg.n_layers):
+        sess.kv_upload(l, 0, 0, X.synth_normal_f16(args.ctx * kvd, args.ctx, 2 * l))
+        sess.kv_upload(l, 1, 0, X.synth_normal_f16(args.ctx * kvd, args.ctx, 2 * l + 1))
+    sess.set_position(args.ctx)
+    sess.prefill([4242])
+    sess.decode_steps(4)
+    sess.trace(True)
+    sess.decode_steps(1)
+    rows, lm, am, total = timeline(sess.last_trace(), cfg.n_layers)
+    glob = [l for l in range(cfg.n_layers) if cfg.is_global(l)]
+    loc = [l for l in range(cfg.n_layers) if not cfg.is_global(l)]
+    print(f"token at position {args.ctx + 5}: {total:.1f} us "
+          f"({len(loc)} local + {len(glob)} global layers)")
+    print(f"{'stage':10s} {'local mean':>11s} {'global mean':>12s}   (us added to the critical path)")
+    for k, name in enumerate(STAGES):
+        lm_ = rows[loc, k].mean() if loc else float("nan")
+        gm_ = rows[glob, k].mean() if glob else float("nan")
+        print(f"{name:10s} {lm_:11.2f} {gm_:12.2f}")
+    print(f"{'per layer':10s} {rows[loc].sum(1).mean() if loc else 0:11.2f} "
+          f"{rows[glob].sum(1).mean() if glob else 0:12.2f}")
+    print(f"lm_head    {lm:11.2f}\nargmax     {am:11.2f}")
+    sess.close()
+    return 0
+
+
+if __name__ == "__main__":
+    raise SystemExit(main())
