@@ -691,8 +691,9 @@ int xp_session_create(const xp_config* cfg, xp_session** out) {
         // ---- execution mode
         s.mode = c.exec_mode == XP_EXEC_LAUNCH ? XP_EXEC_LAUNCH : XP_EXEC_GRAPH;
         const int tok_ok = (c.exec_mode == XP_EXEC_AUTO || c.exec_mode == XP_EXEC_TOKEN)
-                               ? tok_supported(c.hidden, c.ffn, c.n_heads, c.n_kv_heads,
-                                               c.head_dim, c.vocab, c.max_seq, c.scale_fmt, s.n_cu)
+                               ? tok_supported(c.n_layers, c.hidden, c.ffn, c.n_heads,
+                                               c.n_kv_heads, c.head_dim, c.vocab, c.max_seq,
+                                               c.scale_fmt, s.n_cu)
                                : XP_E_ARG;
         if (c.exec_mode == XP_EXEC_TOKEN && tok_ok != XP_OK) {
             destroy(h);

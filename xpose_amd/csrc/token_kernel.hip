@@ -61,10 +61,15 @@ constexpr int      kTkMaxGrid   = 1024;
 constexpr uint32_t kSpinLimit   = 1u << 24;
 constexpr int      kTkBig       = 17408;                 // floats of stage scratch
 constexpr int      kTkFetch     = 12;                    // slot loads in flight per thread
+constexpr int      kTkMaxLayers = 64;
 
 typedef unsigned long long ll_t;
 
 struct TkSmem {
+    // The layer table, copied from device memory at kernel start. Read from
+    // global memory at each use, its pointers cost a dependent load that
+    // also waits for every outstanding weight prefetch (in-order vmcnt).
+    TokLayer lt[kTkMaxLayers];
     float    xs[kTkMaxHidden];               // residual stream
     float    xn[kTkMaxHidden];               // input of the current stage
     float    xt[kTkMaxHidden];               // second input (o / down sums)
@@ -388,6 +393,13 @@ __global__ __launch_bounds__(kTkThreads) void token_kernel(TokArgs a) {
     const uint32_t seq = pos + 1u;
     const TokLL lay = tok_ll_layout(H, a.ffn, a.n_heads, kTkHD, nwg);
 
+    {
+        static_assert(sizeof(TokLayer) % 8 == 0, "layer table copies in 8-byte words");
+        const unsigned long long* src = reinterpret_cast<const unsigned long long*>(a.layers);
+        unsigned long long* dst = reinterpret_cast<unsigned long long*>(S.lt);
+        const uint32_t nw = a.n_layers * uint32_t(sizeof(TokLayer) / 8);
+        for (uint32_t i = tid; i < nw; i += kTkThreads) dst[i] = src[i];
+    }
     // RoPE rotation for this position, both thetas (llm_transformer.cl:158-179).
     if (tid < kTkHD) {
         const uint32_t th = tid / (kTkHD / 2), d = tid % (kTkHD / 2);
@@ -413,7 +425,7 @@ __global__ __launch_bounds__(kTkThreads) void token_kernel(TokArgs a) {
     TkQuads pre;
 
     for (uint32_t l = 0; l < a.n_layers; ++l) {
-        const TokLayer& L = a.layers[l];
+        const TokLayer& L = S.lt[l];
         ll_t* LL = a.ll + size_t(l) * a.ll_layer;
         // ================= QKV =================
         for (uint32_t t = t_qkv; t < n_qkv; t += nwg) {
@@ -421,7 +433,7 @@ __global__ __launch_bounds__(kTkThreads) void token_kernel(TokArgs a) {
             tk_prefetch(tt, pre, wave, lane);
             TkNormW w_in, w_post;
             tk_load_norm(w_in, L.norm[0], H);
-            if (l > 0) tk_load_norm(w_post, a.layers[l - 1u].norm[3], H);
+            if (l > 0) tk_load_norm(w_post, S.lt[l - 1u].norm[3], H);
             if (l == 0) tk_embed(a, S, tok);
             else tk_after_ffn(a, S, lay, l - 1u, w_post);
             if (t == 0) {
@@ -713,7 +725,7 @@ __global__ __launch_bounds__(kTkThreads) void token_kernel(TokArgs a) {
         load_u(2, 2);
     }
     TkNormW wf_post, wf_in;
-    tk_load_norm(wf_post, a.layers[a.n_layers - 1u].norm[3], H);
+    tk_load_norm(wf_post, S.lt[a.n_layers - 1u].norm[3], H);
     tk_load_norm(wf_in, a.final_norm, H);
     tk_after_ffn(a, S, lay, a.n_layers - 1u, wf_post);
     tk_norm(a, S, wf_in);
@@ -781,12 +793,14 @@ __global__ __launch_bounds__(kTkThreads) void token_kernel(TokArgs a) {
 size_t tok_lds_bytes() {
     // Over half of the 160 KiB a gfx950 CU has, so that each CU holds exactly
     // one workgroup of the grid.
+    static_assert(sizeof(TkSmem) <= 160 * 1024, "token kernel LDS exceeds a gfx950 CU");
     const size_t need = (sizeof(TkSmem) + 1023) & ~size_t(1023);
     return need > 96 * 1024 ? need : 96 * 1024;
 }
 
-int tok_supported(uint32_t hidden, uint32_t ffn, uint32_t n_heads, uint32_t n_kv_heads,
-                  uint32_t head_dim, uint32_t vocab, uint32_t max_seq, int fmt, int n_cu) {
+int tok_supported(uint32_t n_layers, uint32_t hidden, uint32_t ffn, uint32_t n_heads,
+                  uint32_t n_kv_heads, uint32_t head_dim, uint32_t vocab, uint32_t max_seq,
+                  int fmt, int n_cu) {
     if (head_dim != uint32_t(kTkHD) || n_kv_heads != 1 || n_heads == 0 ||
         n_heads > uint32_t(kTkMaxQH))
         return set_error(XP_E_ARG, "token kernel: needs head_dim 256, one kv head, <= 8 q heads");
@@ -798,6 +812,8 @@ int tok_supported(uint32_t hidden, uint32_t ffn, uint32_t n_heads, uint32_t n_kv
     if (uint64_t(nch + 1u) * hidden > uint64_t(kTkBig) ||
         uint64_t(max_seq + kTkC - 1u) / kTkC * 66u > uint64_t(kTkBig))
         return set_error(XP_E_ARG, "token kernel: stage scratch too small for this shape");
+    if (n_layers == 0 || n_layers > uint32_t(kTkMaxLayers))
+        return set_error(XP_E_ARG, "token kernel: at most %d layers", kTkMaxLayers);
     if (n_cu < 64 || n_cu > kTkMaxGrid || uint64_t(n_cu) * kTkC < max_seq)
         return set_error(XP_E_ARG, "token kernel: %d CUs cannot cover max_seq %u", n_cu, max_seq);
     return XP_OK;

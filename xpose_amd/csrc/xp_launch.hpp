@@ -137,8 +137,9 @@ inline uint32_t tok_trace_events(uint32_t n_layers) { return 6u * n_layers + 3u;
 // no CU holds two of the grid's workgroups.
 size_t tok_lds_bytes();
 // Checks the kernel can run this shape on the current device (grid = CUs).
-int tok_supported(uint32_t hidden, uint32_t ffn, uint32_t n_heads, uint32_t n_kv_heads,
-                  uint32_t head_dim, uint32_t vocab, uint32_t max_seq, int fmt, int n_cu);
+int tok_supported(uint32_t n_layers, uint32_t hidden, uint32_t ffn, uint32_t n_heads,
+                  uint32_t n_kv_heads, uint32_t head_dim, uint32_t vocab, uint32_t max_seq,
+                  int fmt, int n_cu);
 int launch_token(const TokArgs& a, uint32_t grid, hipStream_t st);
 
 }  // namespace xp
