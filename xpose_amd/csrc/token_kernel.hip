@@ -11,36 +11,44 @@
 //   QKV -> attention -> softmax combine -> O -> gate/up -> down -> next QKV
 //
 // Synchronisation is dataflow, not barriers. Every value that crosses
-// workgroups lives in an 8-byte slot holding (launch tag, fp32 bits), written
-// with one device-coherent store; a consumer re-reads the slots it needs
-// until every tag is this launch's (the low-latency protocol of collective
-// libraries). A stage therefore waits one store-to-load latency for exactly
-// the data it uses, and nothing waits for workgroups it does not depend on.
-// Each workgroup walks the stages in order and skips those it has no work
-// in; every stage's inputs are produced by earlier stages, so the walk is a
+// workgroups lives in an 8-byte slot holding (launch tag, fp32 bits); slots
+// are written two at a time with one 16-byte device-coherent store (sc1), and
+// a consumer re-reads the 16-byte pairs it needs (sc1 loads) until every tag
+// is this launch's (the low-latency protocol of collective libraries). A
+// stage therefore waits one store-to-load latency for exactly the data it
+// uses, and nothing waits for workgroups it does not depend on. Each
+// workgroup walks the stages in order and skips those it has no work in;
+// every stage's inputs are produced by earlier stages, so the walk is a
 // topological order and the grid cannot deadlock. Waits are bounded: past the
 // spin limit a workgroup records an error in state[2] and continues, so the
 // grid always drains; the host reports the error.
 //
-// Other design points:
-//  * The residual stream is carried between stages through the xa / xb slots
-//    (x entering the layer, x after the attention block); the consumers
-//    recompute the 1152-wide RMSNorms themselves.
+// The kernel is compiled for one model shape (hidden, ffn, query heads) at a
+// time, so every per-thread loop has a compile-time trip count and no
+// branches on the shape. Latency, not bandwidth, sets the time of a stage
+// (each moves 0.1-8 MB of weights across 256 CUs), so the design keeps every
+// stage's dependent chain short:
+//  * Vectors crossing a stage boundary are owned by threads: thread i holds
+//    elements 8i .. 8i+7 in registers from the slot fetch through the
+//    residual add, the RMSNorm and the fixed-point staging (whose block of 32
+//    is then one lane quad). Only the staged planes go through LDS.
+//  * Block reductions take one barrier (rotating partial buffers).
 //  * Each stage's weights (the attention stage's KV rows) are loaded into
 //    registers before the workgroup waits for the stage's inputs: weights
 //    do not depend on activations, so HBM streaming overlaps the waiting.
-//  * Matvec tiles are (64-column group, <= 16 quads of k); the 8 waves of the
-//    workgroup take quads w and w + 8 (the int4 x fixed-point dot of
-//    matvec.hip) and reduce through LDS in a fixed order. The down projection
-//    (k = 6912) is split into chunks of 16 quads whose partial sums the next
-//    layer adds in chunk order, so every result is deterministic.
+//  * Matvec tiles are (64-column group, a range of k blocks); wave w takes
+//    blocks w, w + 8, ... (clamped to the range, the excess ones zeroed, so
+//    the loop has no branches) and the 8 wave partials are summed through LDS
+//    in a fixed order. The down projection (k = 6912) is split into chunks of
+//    16 quads whose partial sums the next layer adds in chunk order, so every
+//    result is deterministic.
 //  * Attention: one workgroup per 32 keys of [kv_start, pos]; each computes
 //    QK-norm + RoPE of q and k itself, scores, a chunk softmax (max, sum of
 //    exp) and the unnormalised weighted values; 4 workgroups per query head
 //    then combine the chunks (softmax_rows_finish's rescale,
-//    llm_transformer.cl:385-405). The current key/value come from registers
-//    (fp16-rounded, as the cache holds them) and are appended to the cache by
-//    the chunk that contains them, for later tokens.
+//    llm_transformer.cl:385-405). The current key/value are used from LDS
+//    (fp16-rounded, as the cache holds them) and appended to the cache by the
+//    chunk that contains them, for later tokens.
 //  * RoPE cos/sin for the token's position are computed once per workgroup
 //    at kernel start (256 accurate sincosf, one per thread).
 #include "xp_device.hpp"
@@ -52,108 +60,151 @@ namespace {
 
 constexpr int      kTkThreads   = kTokThreads;
 constexpr int      kTkWaves     = kTkThreads / kWave;    // 8
-constexpr int      kTkHD        = 256;                   // head_dim
-constexpr int      kTkMaxQH     = 8;                     // query heads (one kv head)
-constexpr int      kTkC         = 32;                    // keys per attention workgroup
-constexpr int      kTkMaxHidden = 2048;
-constexpr int      kTkMaxBlk    = 64;                    // staged 32-blocks of x (2048 k)
+constexpr uint32_t kTkHD        = 256;                   // head_dim
+constexpr uint32_t kTkMaxQH     = 8;                     // query heads (one kv head)
+constexpr uint32_t kTkC         = 32;                    // keys per attention workgroup
+constexpr uint32_t kTkMaxBlk    = 64;                    // staged 32-blocks (2048 k)
 constexpr int      kTkMaxGrid   = 1024;
 constexpr uint32_t kSpinLimit   = 1u << 24;
 constexpr int      kTkBig       = 17408;                 // floats of stage scratch
-constexpr int      kTkFetch     = 12;                    // slot loads in flight per thread
 constexpr int      kTkMaxLayers = 64;
+// Cache policy of the slot buffer operations: device scope (sc1), i.e.
+// written through to, and read from, the point where all XCDs are coherent.
+constexpr int      kAuxDev      = 16;
+// Buffer descriptor word 3 for raw (untyped, unswizzled) gfx9 buffers.
+constexpr int      kRsrcWord3   = 0x00020000;
+// Poll back-off of the gate/up stage's wait (which spans QKV, attention,
+// combine and O), in units of 64 cycles.
+constexpr int      kGuSleep     = 32;
 
 typedef unsigned long long ll_t;
+typedef __amdgpu_buffer_rsrc_t rsrc_t;
+
+// The model shape the kernel is compiled for.
+template <uint32_t H_, uint32_t FFN_, uint32_t NH_>
+struct TkShape {
+    static constexpr uint32_t H = H_, FFN = FFN_, NH = NH_;
+    static constexpr uint32_t QD = NH * kTkHD;              // q width
+    static constexpr uint32_t QKVD = QD + 2 * kTkHD;        // q | k | v
+    static constexpr uint32_t HB = H / kBlk;                // 32-blocks of a hidden vector
+    static constexpr uint32_t HO = H / 4;                   // owner threads of a hidden vector
+    static constexpr uint32_t QO = QD / 4;                  // owner threads of the attention output
+    static constexpr uint32_t DQ = 16;                      // quads per down chunk
+    static constexpr uint32_t NQF = FFN / 128;              // quads of ffn
+    static constexpr uint32_t NCH = (NQF + DQ - 1) / DQ;    // down chunks
+    static constexpr uint32_t N_QKV = QKVD / kGrp;
+    static constexpr uint32_t N_COMB = NH * 4;
+    static constexpr uint32_t N_O = H / kGrp;
+    static constexpr uint32_t N_GU = 2 * FFN / kGrp;
+    static constexpr uint32_t N_DN = (H / kGrp) * NCH;
+    static constexpr uint32_t NQH = H / 128;                // lm_head quads per column
+    static_assert(H % 128 == 0 && FFN % 128 == 0, "hidden and ffn must be multiples of 128");
+    static_assert(HO <= uint32_t(kTkThreads) && QO <= uint32_t(kTkThreads) &&
+                  DQ * 128 / 4 <= uint32_t(kTkThreads), "vector too wide for four per thread");
+    static_assert(HB <= kTkMaxBlk && QD / kBlk <= kTkMaxBlk && DQ * 4 <= kTkMaxBlk, "staging");
+    static_assert(NH >= 1 && NH <= kTkMaxQH, "1..8 query heads");
+    static_assert((FFN + 2047) / 2048 == NCH, "chunk count must match the slot layout");
+    static_assert(N_O <= N_QKV && N_O <= N_GU, "x is stored by the first H / 64 tiles");
+};
 
 struct TkSmem {
     // The layer table, copied from device memory at kernel start. Read from
     // global memory at each use, its pointers cost a dependent load that
     // also waits for every outstanding weight prefetch (in-order vmcnt).
     TokLayer lt[kTkMaxLayers];
-    float    xs[kTkMaxHidden];               // residual stream
-    float    xn[kTkMaxHidden];               // input of the current stage
-    float    xt[kTkMaxHidden];               // second input (o / down sums)
-    QxBlock  qx[kTkMaxBlk];                  // fixed-point staging of xn
+    QxBlock  qx[kTkMaxBlk];                  // fixed-point staging of a stage's input
     float    sx[kTkMaxBlk];
+    alignas(16) float rs[4][kTkWaves];       // block reductions (rotating)
     float    red[kTkWaves][kWave];           // per-wave tile partials
-    float    rs[kTkWaves];                   // block reductions
-    float    rt[kTkWaves];
     float    cs[2][kTkHD / 2];               // RoPE cos / sin at this position,
     float    sn[2][kTkHD / 2];               // [0] local theta, [1] global theta
-    float    qh[kTkMaxQH][kTkHD];            // normed, rotated q
+    float    xq[kTkMaxQH * kTkHD + 2 * kTkHD];   // raw q | k | v
+    alignas(16) float qh[kTkMaxQH][kTkHD];   // normed, rotated q
     float    kn[kTkHD];                      // current key / value (fp16-rounded)
     float    vn[kTkHD];
-    float    sc[kTkMaxQH][kTkC];             // scores, then exp
-    // Stage scratch: the down chunks of the residual add, the value partials
-    // of attention's 4 key groups ([4][n_heads][256]), the combine's inputs.
-    float    big[kTkBig];
+    alignas(16) float sc[kTkC][kTkMaxQH];    // scores, then exp ([key][head])
     float    mh[kTkMaxQH];
     float    lh[kTkMaxQH];
+    // Stage scratch: the value partials of attention's 4 key groups
+    // ([4][n_heads][256]), the combine's chunk data ([chunk][66]).
+    alignas(16) float big[kTkBig];
     float    fm[2 * kTkMaxGrid];             // combine: per-chunk factors; argmax slots
     float    amv[kTkWaves];
     uint32_t ami[kTkWaves];
 };
 
 // ---- exchange slots -------------------------------------------------------------
-__device__ __forceinline__ void ll_put(ll_t* p, float v, uint32_t tag) {
-    st_dev64(p, (ll_t(tag) << 32) | ll_t(__float_as_uint(v)));
+// A 16-byte pair of slots: x = value 0, y = tag 0, z = value 1, w = tag 1.
+__device__ __forceinline__ u32x4 ll_ld2(rsrc_t r, uint32_t voff, uint32_t soff) {
+    return __builtin_amdgcn_raw_buffer_load_b128(r, int(voff), int(soff), kAuxDev);
 }
-__device__ __forceinline__ float ll_val(ll_t v) { return __uint_as_float(uint32_t(v)); }
+__device__ __forceinline__ void ll_st2(rsrc_t r, uint32_t voff, uint32_t soff, float a, float b,
+                                       uint32_t tag) {
+    __builtin_amdgcn_raw_buffer_store_b128(u32x4{__float_as_uint(a), tag, __float_as_uint(b), tag},
+                                           r, int(voff), int(soff), kAuxDev);
+}
+__device__ __forceinline__ void ll_st1(rsrc_t r, uint32_t voff, uint32_t soff, float a, uint32_t tag) {
+    __builtin_amdgcn_raw_buffer_store_b64(u32x2{__float_as_uint(a), tag}, r, int(voff), int(soff),
+                                          kAuxDev);
+}
+__device__ __forceinline__ bool ll_ok(u32x4 v, uint32_t tag) { return (v.y == tag) & (v.w == tag); }
 
-// dst[i] = value of slot at(i) for i < n, waiting until every slot carries
-// this launch's tag. Up to kTkFetch loads per thread are issued together and
-// only the stale ones are re-issued, so data that is ready costs one
-// round trip. Bounded: past the spin limit the workgroup records an error in
-// state[2] and keeps whatever the slots hold. All threads; ends with a
-// workgroup barrier.
-template <class At>
-__device__ __forceinline__ void ll_fetch_at(float* dst, uint32_t n, uint32_t tag, uint32_t* state, At at) {
-    for (uint32_t base = 0; base < n; base += kTkFetch * kTkThreads) {
-        ll_t v[kTkFetch];
+// Loads the N slot pairs at byte offsets off[i] (+ soff) that are active and
+// re-reads them until both tags of every pair are `tag`, sleeping SLEEP x 64
+// cycles between rounds (a wait that is long by construction can poll less).
+// Bounded: past the spin limit the thread records an error in state[2] and
+// keeps what it has. Per thread; no barrier.
+template <int N, int SLEEP = 0>
+__device__ __forceinline__ void ll_wait(rsrc_t r, uint32_t soff, const uint32_t (&off)[N],
+                                        const bool (&act)[N], u32x4 (&v)[N], uint32_t tag,
+                                        uint32_t* state) {
+    const u32x4 ready = {0u, tag, 0u, tag};
 #pragma unroll
-        for (int r = 0; r < kTkFetch; ++r) {
-            const uint32_t i = base + r * kTkThreads + threadIdx.x;
-            v[r] = i < n ? ld_dev64(at(i)) : (ll_t(tag) << 32);
-        }
-        uint32_t spins = 0;
-        for (;;) {
-            bool ok = true;
+    for (int i = 0; i < N; ++i) v[i] = act[i] ? ll_ld2(r, off[i], soff) : ready;
+    uint32_t spins = 0;
+    for (;;) {
+        bool ok = true;
 #pragma unroll
-            for (int r = 0; r < kTkFetch; ++r) ok &= uint32_t(v[r] >> 32) == tag;
-            if (ok) break;
-            ++spins;
-            if ((spins & 255u) == 0) {
-                if (ld_dev(state + 2) != 0u) break;
-                if (spins > kSpinLimit) {
-                    st_dev(state + 2, 1u);
-                    break;
-                }
-            }
-#pragma unroll
-            for (int r = 0; r < kTkFetch; ++r) {
-                const uint32_t i = base + r * kTkThreads + threadIdx.x;
-                if (uint32_t(v[r] >> 32) != tag) v[r] = ld_dev64(at(i));
+        for (int i = 0; i < N; ++i) ok &= ll_ok(v[i], tag);
+        if (ok) break;
+        if ((++spins & 255u) == 0u) {
+            if (ld_dev(state + 2) != 0u) break;
+            if (spins > kSpinLimit) {
+                st_dev(state + 2, 1u);
+                break;
             }
         }
+        // The slots change under us: re-read them all (a stale-only re-read
+        // does not unroll, and the ready pairs cannot change).
+        if constexpr (SLEEP > 0) __builtin_amdgcn_s_sleep(SLEEP);
+        asm volatile("" ::: "memory");
 #pragma unroll
-        for (int r = 0; r < kTkFetch; ++r) {
-            const uint32_t i = base + r * kTkThreads + threadIdx.x;
-            if (i < n) dst[i] = ll_val(v[r]);
-        }
+        for (int i = 0; i < N; ++i) v[i] = act[i] ? ll_ld2(r, off[i], soff) : ready;
     }
-    __syncthreads();
 }
 
-// Contiguous slots p[0 .. n).
-__device__ __forceinline__ void ll_fetch(float* dst, const ll_t* p, uint32_t n, uint32_t tag,
-                                         uint32_t* state) {
-    ll_fetch_at(dst, n, tag, state, [=](uint32_t i) { return p + i; });
+// Owner layout: thread i holds elements kOwn i .. kOwn i + kOwn - 1 of a
+// vector crossing a stage boundary, kOwn / 2 slot pairs.
+constexpr uint32_t kOwn  = 4;
+constexpr uint32_t kOwnP = kOwn / 2;
+
+// Byte offsets of this thread's kOwn consecutive slots starting at slot s0.
+__device__ __forceinline__ void own_offsets(uint32_t* off, uint32_t s0) {
+#pragma unroll
+    for (uint32_t j = 0; j < kOwnP; ++j) off[j] = (s0 + 2u * j) * 8u;
 }
-// Two contiguous ranges at once: dst[0 .. n0) from p0, dst[n0 .. n0 + n1) from p1.
-__device__ __forceinline__ void ll_fetch2(float* dst, const ll_t* p0, uint32_t n0, const ll_t* p1,
-                                          uint32_t n1, uint32_t tag, uint32_t* state) {
-    ll_fetch_at(dst, n0 + n1, tag, state,
-                [=](uint32_t i) { return i < n0 ? p0 + i : p1 + (i - n0); });
+__device__ __forceinline__ void own_unpack(float (&x)[kOwn], const u32x4* v) {
+#pragma unroll
+    for (uint32_t j = 0; j < kOwnP; ++j) {
+        x[2 * j] = __uint_as_float(v[j].x);
+        x[2 * j + 1] = __uint_as_float(v[j].z);
+    }
+}
+// Owner put: x[0 .. kOwn) into slots s0 .. s0 + kOwn.
+__device__ __forceinline__ void own_put(rsrc_t r, uint32_t soff, uint32_t s0, const float (&x)[kOwn],
+                                        uint32_t tag) {
+#pragma unroll
+    for (uint32_t j = 0; j < kOwnP; ++j) ll_st2(r, (s0 + 2u * j) * 8u, soff, x[2 * j], x[2 * j + 1], tag);
 }
 
 __device__ __forceinline__ void tk_trace(const TokArgs& a, uint32_t event) {
@@ -161,226 +212,190 @@ __device__ __forceinline__ void tk_trace(const TokArgs& a, uint32_t event) {
         a.trace[size_t(event) * gridDim.x + blockIdx.x] = __builtin_amdgcn_s_memrealtime();
 }
 
-// ---- small block-wide helpers (512 threads) -------------------------------------
-__device__ __forceinline__ float tk_block_sum(float v, float* rs) {
+// ---- block-wide reductions (512 threads, one barrier) ---------------------------
+// Every thread returns the same total, summed in a fixed order. rs must not be
+// written again before another barrier has passed (the kernel rotates four).
+__device__ __forceinline__ float blk_sum(float v, float* rs) {
     v = wave_sum(v);
-    const uint32_t w = threadIdx.x / kWave;
-    if (threadIdx.x % kWave == 0) rs[w] = v;
+    if ((threadIdx.x & (kWave - 1)) == 0) rs[threadIdx.x / kWave] = v;
     __syncthreads();
-    float t = 0.0f;
-#pragma unroll
-    for (int i = 0; i < kTkWaves; ++i) t += rs[i];
-    __syncthreads();
-    return t;
+    const float4 p = *reinterpret_cast<const float4*>(rs);
+    const float4 q = *reinterpret_cast<const float4*>(rs + 4);
+    return ((p.x + p.y) + (p.z + p.w)) + ((q.x + q.y) + (q.z + q.w));
 }
-__device__ __forceinline__ float tk_block_max(float v, float* rs) {
+__device__ __forceinline__ float blk_max(float v, float* rs) {
     v = wave_max(v);
-    const uint32_t w = threadIdx.x / kWave;
-    if (threadIdx.x % kWave == 0) rs[w] = v;
+    if ((threadIdx.x & (kWave - 1)) == 0) rs[threadIdx.x / kWave] = v;
     __syncthreads();
-    float t = -INFINITY;
-#pragma unroll
-    for (int i = 0; i < kTkWaves; ++i) t = fmaxf(t, rs[i]);
-    __syncthreads();
-    return t;
+    const float4 p = *reinterpret_cast<const float4*>(rs);
+    const float4 q = *reinterpret_cast<const float4*>(rs + 4);
+    return fmaxf(fmaxf(fmaxf(p.x, p.y), fmaxf(p.z, p.w)), fmaxf(fmaxf(q.x, q.y), fmaxf(q.z, q.w)));
 }
 
-// A norm weight vector held in registers: element tid + r * 512 in v[r].
-// Loaded before a stage waits for its inputs, like the matvec weights.
-struct TkNormW {
-    float v[kTkMaxHidden / kTkThreads];
-};
-__device__ __forceinline__ void tk_load_norm(TkNormW& w, const float* p, uint32_t n) {
+// kOwn consecutive floats of a vector in global memory (owner layout).
+__device__ __forceinline__ void ld_own(float (&w)[kOwn], const float* p) {
 #pragma unroll
-    for (int r = 0; r < kTkMaxHidden / kTkThreads; ++r) {
-        const uint32_t i = threadIdx.x + r * kTkThreads;
-        w.v[r] = i < n ? ldgf(p + i) : 0.0f;
+    for (uint32_t j = 0; j < kOwn / 4; ++j) {
+        const u32x4 v = ldg4(p + 4 * j);
+        w[4 * j + 0] = __uint_as_float(v.x);
+        w[4 * j + 1] = __uint_as_float(v.y);
+        w[4 * j + 2] = __uint_as_float(v.z);
+        w[4 * j + 3] = __uint_as_float(v.w);
     }
 }
 
-// Gemma RMSNorm of S.xs into S.xn: xn = xs * rsqrt(mean(xs^2) + eps) * (1 + w).
-__device__ __forceinline__ void tk_norm(const TokArgs& a, TkSmem& S, const TkNormW& w) {
-    float ss = 0.0f;
-    for (uint32_t i = threadIdx.x; i < a.hidden; i += kTkThreads) ss += S.xs[i] * S.xs[i];
-    ss = tk_block_sum(ss, S.rs);
-    const float scale = 1.0f / sqrtf(ss / float(a.hidden) + a.eps);
-#pragma unroll
-    for (int r = 0; r < kTkMaxHidden / kTkThreads; ++r) {
-        const uint32_t i = threadIdx.x + r * kTkThreads;
-        if (i < a.hidden) S.xn[i] = S.xs[i] * scale * (1.0f + w.v[r]);
-    }
-    __syncthreads();
-}
-
-// S.xs = S.xn + S.xt * rsqrt(mean(xt^2) + eps) * (1 + w_post): the residual
+// Owner-layout Gemma RMSNorm steps (non-owner threads hold zeros and take part
+// in the reduction). x = a + t * rsqrt(mean(t^2) + eps) * (1 + w): the residual
 // add of a normed sublayer output (decode.cpp:1739-1751).
-__device__ __forceinline__ void tk_residual(const TokArgs& a, TkSmem& S, const TkNormW& w_post) {
+template <uint32_t H>
+__device__ __forceinline__ void own_residual(float (&x)[kOwn], const float (&a)[kOwn],
+                                             const float (&t)[kOwn], const float (&w)[kOwn], float eps,
+                                             float* rs) {
     float ss = 0.0f;
-    for (uint32_t i = threadIdx.x; i < a.hidden; i += kTkThreads) ss += S.xt[i] * S.xt[i];
-    ss = tk_block_sum(ss, S.rs);
-    const float scale = 1.0f / sqrtf(ss / float(a.hidden) + a.eps);
 #pragma unroll
-    for (int r = 0; r < kTkMaxHidden / kTkThreads; ++r) {
-        const uint32_t i = threadIdx.x + r * kTkThreads;
-        if (i < a.hidden) S.xs[i] = S.xn[i] + S.xt[i] * scale * (1.0f + w_post.v[r]);
-    }
-    __syncthreads();
+    for (uint32_t e = 0; e < kOwn; ++e) ss = fmaf(t[e], t[e], ss);
+    ss = blk_sum(ss, rs);
+    const float scale = 1.0f / sqrtf(ss / float(H) + eps);
+#pragma unroll
+    for (uint32_t e = 0; e < kOwn; ++e) x[e] = a[e] + t[e] * scale * (1.0f + w[e]);
+}
+// y = x * rsqrt(mean(x^2) + eps) * (1 + w) (rmsnorm_apply_gemma).
+template <uint32_t H>
+__device__ __forceinline__ void own_norm(float (&y)[kOwn], const float (&x)[kOwn], const float (&w)[kOwn],
+                                         float eps, float* rs) {
+    float ss = 0.0f;
+#pragma unroll
+    for (uint32_t e = 0; e < kOwn; ++e) ss = fmaf(x[e], x[e], ss);
+    ss = blk_sum(ss, rs);
+    const float scale = 1.0f / sqrtf(ss / float(H) + eps);
+#pragma unroll
+    for (uint32_t e = 0; e < kOwn; ++e) y[e] = x[e] * scale * (1.0f + w[e]);
 }
 
-__device__ __forceinline__ float tk_scale(u32x2 raw, int i, int fmt) {
-    const uint32_t w = (i < 2) ? raw.x : raw.y;
-    if (fmt == XP_SCALE_F16_QUAD) return f16_bits_to_f32((i & 1) ? (w >> 16) : w);
-    return (i & 1) ? bf16hi(w) : bf16lo(w);
+// Fixed-point staging (the planes of stage_x8, xp_device.hpp) from four
+// consecutive activations per thread: task i covers elements 4 (i % 8) .. + 3
+// of block i / 8, i.e. half h = i % 2 of word c = (i / 2) % 4 of each digit
+// plane; the eight tasks of a block are adjacent lanes of one wave. The
+// block maximum, the scale and every digit are those stage_x8 computes.
+__device__ __forceinline__ void stage_x4(QxBlock* qx, float* sx, uint32_t i, const float (&v)[4]) {
+    float m = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
+    // max over the block's eight tasks: quad_perm xor 1, xor 2, then row_half_mirror
+    m = fmaxf(m, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(m), 0xB1, 0xF, 0xF, false)));
+    m = fmaxf(m, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(m), 0x4E, 0xF, 0xF, false)));
+    m = fmaxf(m, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(m), 0x141, 0xF, 0xF, false)));
+    const float r = m > 0.0f ? kQxRange / m : 0.0f;
+    uint32_t t[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) t[e] = uint32_t(__float2int_rn(v[e] * r) + int32_t(kQxBias)) ^ kQxBias;
+    const uint32_t lb = i >> 3, hw = i & 7u;   // half-word 2 c + h of each plane
+#pragma unroll
+    for (int p = 0; p < kQxPlanes; ++p) {
+        uint32_t half = 0;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) half |= ((t[e] >> (4 * p)) & 15u) << (4 * e);
+        reinterpret_cast<uint16_t*>(&qx[lb].p[p])[hw] = uint16_t(half);
+    }
+    if (hw == 0) sx[lb] = m * (1.0f / kQxRange);
+}
+// Stages the owner vector of thread i < nblocks * 32 / kOwn as fixed-point
+// planes in S.qx / S.sx; the caller then waits at a barrier.
+__device__ __forceinline__ void own_stage(TkSmem& S, const float (&x)[kOwn]) {
+    static_assert(kOwn == 4, "staging from four elements per thread");
+    stage_x4(S.qx, S.sx, threadIdx.x, x);
+}
+
+// Scale i (0..3) of a block quad's four fp16 / bf16 scales, without branches.
+template <int FMT>
+__device__ __forceinline__ float tk_scale(u32x2 raw, uint32_t i) {
+    const uint32_t w = (i & 2u) ? raw.y : raw.x;
+    const uint32_t h = (w >> (16u * (i & 1u))) & 0xFFFFu;
+    if constexpr (FMT == XP_SCALE_F16_QUAD) return f16_bits_to_f32(h);
+    else return __uint_as_float(h << 16);
 }
 
 // ---- matvec tiles ------------------------------------------------------------------
-struct TkTile {
-    const u32x4* wq;
-    const void*  sc;
-    uint32_t     nblk;     // k / 32 of the matrix
-    uint32_t     cols;
-    uint32_t     g;        // column group
-    uint32_t     qa, qb;   // quads [qa, qb) of k
-    uint32_t     m;        // matrix index (XP_T_Q .. XP_T_DOWN)
+// A tile: column group g of a KM4 matrix (nblk 32-blocks of k, cols columns),
+// k blocks [b0, b0 + nb). Wave w takes blocks b0 + min(w + 8 r, nb - 1) for
+// r < R; a repeated (clamped) block is computed and weighted by zero.
+template <int R>
+struct TkW {
+    u32x4 w[R];
+    u32x2 s[R];
 };
 
-// Wave w's blocks of a tile: 4 qa + w + 8 r for r < 8 (tiles hold at most
-// 16 quads = 64 blocks), each with its scale quad (the block's scale is
-// component b % 4). Spreading blocks rather than quads over the 8 waves keeps
-// a 9-quad tile at 5 blocks per wave.
-struct TkQuads {
-    u32x4 w[8];
-    u32x2 s[8];
-};
-
-__device__ __forceinline__ void tk_prefetch(const TkTile& t, TkQuads& p, uint32_t wave,
-                                            uint32_t lane) {
-    const uint32_t b1 = 4u * t.qb;
+template <int R>
+__device__ __forceinline__ void tile_prefetch(TkW<R>& p, const void* wq, const void* sc, uint32_t nblk,
+                                              uint32_t cols, uint32_t g, uint32_t b0, uint32_t nb,
+                                              uint32_t wave, uint32_t lane) {
+    const u32x4* w = static_cast<const u32x4*>(wq);
+    const u32x2* s = static_cast<const u32x2*>(sc);
 #pragma unroll
-    for (int r = 0; r < 8; ++r) {
-        const uint32_t b = 4u * t.qa + wave + 8u * r;
-        if (b < b1) {
-            p.w[r] = ldg_stream4(t.wq + (size_t(t.g) * t.nblk + b) * kGrp + lane);
-            p.s[r] = ldg_stream2(reinterpret_cast<const u32x2*>(t.sc) + size_t(b / 4u) * t.cols +
-                                 t.g * kGrp + lane);
-        }
+    for (int r = 0; r < R; ++r) {
+        const uint32_t b = b0 + min(wave + 8u * r, nb - 1u);
+        p.w[r] = ldg_stream4(w + (size_t(g) * nblk + b) * kGrp + lane);
+        p.s[r] = ldg_stream2(s + size_t(b / 4u) * cols + g * kGrp + lane);
     }
 }
 
-// Stages S.xn[0 .. nb*32) (k relative to the tile's first block) as
-// fixed-point planes S.qx[0 .. nb).
-__device__ __forceinline__ void tk_stage(TkSmem& S, uint32_t nb) {
-    for (uint32_t i = threadIdx.x; i < nb * 4; i += kTkThreads) {
-        const float4* p = reinterpret_cast<const float4*>(S.xn) + 2 * i;
-        stage_x8(S.qx, S.sx, i, p[0], p[1]);
-    }
-    __syncthreads();
-}
-
-// The wave's share of tile t (staged planes start at quad qbase), reduced over
-// the 8 waves in order; the result is valid in wave 0 (lane = column).
-__device__ __forceinline__ float tk_tile(const TkTile& t, const TkQuads& p, TkSmem& S, uint32_t qbase, int fmt,
-                         uint32_t wave, uint32_t lane) {
+// Dot of the wave's blocks with the staged planes (S.qx[0] = block b0, a
+// multiple of 4, so the scale of block b0 + w + 8 r is component w % 4 of its
+// quad), reduced over the 8 waves in order. The result is valid in wave 0
+// (lane = column); the caller publishes it. Starts after the staging
+// barrier; ends with a barrier.
+template <int FMT, int R>
+__device__ __forceinline__ float tile_dot(const TkW<R>& p, TkSmem& S, uint32_t nb, uint32_t wave,
+                                          uint32_t lane) {
     float acc = 0.0f;
-    const uint32_t b1 = 4u * t.qb;
 #pragma unroll
-    for (int r = 0; r < 8; ++r) {
-        const uint32_t b = 4u * t.qa + wave + 8u * r;
-        if (b < b1) {
-            const uint32_t lb = b - 4u * qbase;
-            const float f = tk_scale(p.s[r], int(b % 4u), fmt) * S.sx[lb];
-            acc = fmaf(f, float(block_dot(p.w[r], S.qx[lb])), acc);
-        }
+    for (int r = 0; r < R; ++r) {
+        const uint32_t lb = min(wave + 8u * r, nb - 1u);
+        float f = tk_scale<FMT>(p.s[r], wave % 4u) * S.sx[lb];
+        if (wave + 8u * r >= nb) f = 0.0f;
+        acc = fmaf(f, float(block_dot(p.w[r], S.qx[lb])), acc);
     }
     S.red[wave][lane] = acc;
     __syncthreads();
-    float r = 0.0f;
+    float y = 0.0f;
     if (wave == 0) {
 #pragma unroll
-        for (int w = 0; w < kTkWaves; ++w) r += S.red[w][lane];
+        for (int w = 0; w < kTkWaves; ++w) y += S.red[w][lane];
     }
-    __syncthreads();
-    return r;
+    return y;
 }
 
-// QKV: tile = one 64-column group of q|k|v over all of k.
-__device__ __forceinline__ TkTile tk_qkv_tile(const TokArgs& a, const TokLayer& L, uint32_t t) {
-    const uint32_t qg = a.n_heads * kTkHD / kGrp, kg = kTkHD / kGrp;
-    const uint32_t m = t < qg ? 0u : (t < qg + kg ? 1u : 2u);
-    const uint32_t g = m == 0 ? t : (m == 1 ? t - qg : t - qg - kg);
-    return TkTile{static_cast<const u32x4*>(L.w[m]), L.s[m], a.hidden / kBlk,
-                  m == 0 ? a.n_heads * kTkHD : uint32_t(kTkHD), g, 0u, a.hidden / 128u, m};
-}
-__device__ __forceinline__ TkTile tk_o_tile(const TokArgs& a, const TokLayer& L, uint32_t t) {
-    return TkTile{static_cast<const u32x4*>(L.w[3]), L.s[3], a.n_heads * kTkHD / kBlk,
-                  a.hidden, t, 0u, a.n_heads * kTkHD / 128u, 3u};
-}
-__device__ __forceinline__ TkTile tk_gu_tile(const TokArgs& a, const TokLayer& L, uint32_t t) {
-    const uint32_t ng = a.ffn / kGrp;
-    const uint32_t m = t < ng ? 4u : 5u;
-    return TkTile{static_cast<const u32x4*>(L.w[m]), L.s[m], a.hidden / kBlk, a.ffn,
-                  t < ng ? t : t - ng, 0u, a.hidden / 128u, m};
-}
-// Down: tile = (column group, chunk of 16 quads = 2048 k).
-__device__ __forceinline__ uint32_t tk_down_chunks(uint32_t ffn) { return (ffn / 128u + 15u) / 16u; }
-__device__ __forceinline__ TkTile tk_down_tile(const TokArgs& a, const TokLayer& L, uint32_t t) {
-    const uint32_t nq = a.ffn / 128u, nch = tk_down_chunks(a.ffn);
-    const uint32_t g = t / nch, c = t % nch;
-    return TkTile{static_cast<const u32x4*>(L.w[6]), L.s[6], a.ffn / kBlk, a.hidden, g, 16u * c,
-                  min(16u * c + 16u, nq), 6u};
-}
-
-// ---- embedding (decode.cpp:1618-1627, as a gather from the tied int4 table) ----
-__device__ __forceinline__ void tk_embed(const TokArgs& a, TkSmem& S, uint32_t tok) {
-    const uint32_t nblk = a.hidden / kBlk;
-    const u32x4* wq = static_cast<const u32x4*>(a.lm_w);
-    for (uint32_t k = threadIdx.x; k < a.hidden; k += kTkThreads) {
-        const uint32_t b = k / kBlk, t = k % kBlk;
-        const u32x4 w = ldg4(wq + (size_t(tok / kGrp) * nblk + b) * kGrp + (tok % kGrp));
-        const uint32_t word = (t < 8) ? w.x : (t < 16) ? w.y : (t < 24) ? w.z : w.w;
-        const float q = float(int((word >> ((t & 7u) * 4u)) & 15u) - 8);
-        const uint16_t h =
-            ldg16(static_cast<const uint16_t*>(a.lm_s) + (size_t(b / 4) * a.vocab + tok) * 4 + (b % 4));
-        const float s = a.fmt == XP_SCALE_F16_QUAD ? f16_bits_to_f32(h)
-                                                   : __uint_as_float(uint32_t(h) << 16);
-        S.xs[k] = (q * s) * a.embed_scale;
-    }
-    __syncthreads();
-}
-
-// S.xs = x entering layer l + 1 from layer l's slots: xb + post_ffw_norm(sum
-// of the down chunks, in chunk order). The chunks are contiguous slots
-// (dnp follows xb's layer block at a fixed offset); fetched with xb in one
-// batch.
-__device__ __forceinline__ void tk_after_ffn(const TokArgs& a, TkSmem& S, const TokLL& lay, uint32_t l,
-                             const TkNormW& w_post) {
-    const ll_t* base = a.ll + size_t(l) * a.ll_layer;
-    const uint32_t nch = tk_down_chunks(a.ffn), H = a.hidden;
-    // big[0 .. H) = xb, big[H + c H .. ) = chunk c
-    ll_fetch2(S.big, base + lay.xb, H, base + lay.dnp, nch * H, a.tag, a.state);
-    for (uint32_t i = threadIdx.x; i < H; i += kTkThreads) {
-        float t = S.big[H + i];
-        for (uint32_t c = 1; c < nch; ++c) t += S.big[H + c * H + i];
-        S.xn[i] = S.big[i];
-        S.xt[i] = t;
-    }
-    __syncthreads();
-    tk_residual(a, S, w_post);
+// Wave 0 publishes its 64 column results y (lane = column) at slot s0 + lane.
+__device__ __forceinline__ void tile_put(rsrc_t r, uint32_t soff, uint32_t s0, float y, uint32_t lane,
+                                         uint32_t tag) {
+    const float yn = dpp_f<0xB1, 0xF>(y, 0.0f);   // lane ^ 1
+    if ((lane & 1u) == 0u) ll_st2(r, (s0 + lane) * 8u, soff, y, yn, tag);
 }
 
 __device__ __forceinline__ float f16_round(float v) { return f16_bits_to_f32(f32_to_f16_bits(v)); }
 
+// v, as a value the compiler cannot see through.
+__device__ __forceinline__ uint32_t opaque(uint32_t v) {
+    asm volatile("" : "+v"(v));
+    return v;
+}
+
 }  // namespace
 
+template <class Sh, int FMT>
 __global__ __launch_bounds__(kTkThreads) void token_kernel(TokArgs a) {
+    constexpr uint32_t H = Sh::H, FFN = Sh::FFN, NH = Sh::NH, QD = Sh::QD;
+    constexpr uint32_t NCH = Sh::NCH;
     extern __shared__ __align__(16) unsigned char tk_lds[];
     TkSmem& S = *reinterpret_cast<TkSmem*>(tk_lds);
-    const uint32_t tid  = threadIdx.x;
+    // Thread-derived values are re-derived through an opaque copy at every
+    // layer, so that the compiler recomputes per-thread offsets inside each
+    // stage instead of keeping them all in registers across the layer loop.
+    uint32_t tid = threadIdx.x;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(tid / kWave);
-    const uint32_t lane = tid % kWave;
+    uint32_t lane = tid % kWave;
     const uint32_t wg   = blockIdx.x;
     const uint32_t nwg  = gridDim.x;
     const uint32_t tag  = a.tag;
+    const float    eps  = a.eps;
     tk_trace(a, 0);
 
     const uint32_t pos = a.state[0];
@@ -388,10 +403,13 @@ __global__ __launch_bounds__(kTkThreads) void token_kernel(TokArgs a) {
     if (tok >= a.vocab) tok = 0;                 // the host validates ids
     if (wg == 0 && tid == 0) a.hist[pos] = tok;
 
-    const uint32_t H = a.hidden;
-    const uint32_t qd = a.n_heads * kTkHD;
     const uint32_t seq = pos + 1u;
-    const TokLL lay = tok_ll_layout(H, a.ffn, a.n_heads, kTkHD, nwg);
+    const TokLL lay = tok_ll_layout(H, FFN, NH, kTkHD, nwg);
+    const uint32_t lstride = uint32_t(a.ll_layer) * 8u;   // bytes per layer of slots
+    const rsrc_t rr = __builtin_amdgcn_make_buffer_rsrc(
+        a.ll, short(0), int(a.n_layers * lstride + 16u * nwg), kRsrcWord3);
+    uint32_t rk = 0;                              // rotating reduction buffer
+    auto RS = [&]() { return S.rs[(rk++) & 3u]; };
 
     {
         static_assert(sizeof(TokLayer) % 8 == 0, "layer table copies in 8-byte words");
@@ -411,41 +429,120 @@ __global__ __launch_bounds__(kTkThreads) void token_kernel(TokArgs a) {
     }
     __syncthreads();
 
-    const uint32_t n_qkv  = (qd + 2u * kTkHD) / kGrp;
-    const uint32_t n_comb = a.n_heads * 4u;
-    const uint32_t n_o    = H / kGrp;
-    const uint32_t n_gu   = 2u * a.ffn / kGrp;
-    const uint32_t nch    = tk_down_chunks(a.ffn);
-    const uint32_t n_dn   = (H / kGrp) * nch;
     // Workgroup -> tile maps: tile t of a stage runs on workgroup (off + t) %
     // grid, so this workgroup's first tile is (wg - off) mod grid.
-    const uint32_t off_comb = n_qkv % nwg, off_gu = (n_qkv + n_comb) % nwg;
+    const uint32_t off_comb = Sh::N_QKV % nwg, off_gu = (Sh::N_QKV + Sh::N_COMB) % nwg;
     const uint32_t t_qkv = wg, t_comb = (wg + nwg - off_comb) % nwg, t_o = wg;
     const uint32_t t_gu = (wg + nwg - off_gu) % nwg, t_dn = wg;
-    TkQuads pre;
+    bool hown = tid < Sh::HO;                     // owns kOwn elements of a hidden vector
+
+    // x entering layer l (l > 0) from layer l - 1's slots, in owner registers:
+    // xb + post_ffw_norm(sum of the down chunks, in chunk order).
+    auto after_ffn = [&](float (&x)[kOwn], uint32_t lp, const float (&w_post)[kOwn]) {
+        const uint32_t soff = lp * lstride;
+        float xb[kOwn] = {}, t[kOwn] = {};
+        if (hown) {
+            constexpr uint32_t NL = kOwnP * (1 + NCH);
+            uint32_t off[NL];
+            bool act[NL];
+            u32x4 v[NL];
+            own_offsets(&off[0], uint32_t(lay.xb) + kOwn * tid);
+#pragma unroll
+            for (uint32_t c = 0; c < NCH; ++c)
+                own_offsets(&off[kOwnP * (1 + c)], uint32_t(lay.dnp) + c * H + kOwn * tid);
+#pragma unroll
+            for (uint32_t i = 0; i < NL; ++i) act[i] = true;
+            ll_wait(rr, soff, off, act, v, tag, a.state);
+            own_unpack(xb, &v[0]);
+            own_unpack(t, &v[kOwnP]);
+#pragma unroll
+            for (uint32_t c = 1; c < NCH; ++c) {
+                float u[kOwn];
+                own_unpack(u, &v[kOwnP * (1 + c)]);
+#pragma unroll
+                for (uint32_t e = 0; e < kOwn; ++e) t[e] += u[e];
+            }
+        }
+        own_residual<H>(x, xb, t, w_post, eps, RS());
+    };
+
+    // Weight prefetch. A workgroup's first QKV tile of layer l + 1 is loaded
+    // before it waits in layer l's down stage, and its down tile before it
+    // waits in the gate/up stage: a workgroup busy in the previous stage
+    // would otherwise start streaming those weights only when its inputs are
+    // already there.
+    constexpr int RQ = int(Sh::HB + 7) / 8;           // QKV and gate/up blocks per wave
+    constexpr int RD = int(Sh::DQ * 4) / 8;           // down blocks per wave
+    auto qkv_tile = [&](uint32_t t, uint32_t& m, uint32_t& g) {
+        constexpr uint32_t qg = QD / kGrp, kg = kTkHD / kGrp;
+        m = t < qg ? 0u : (t < qg + kg ? 1u : 2u);
+        g = m == 0 ? t : (m == 1 ? t - qg : t - qg - kg);
+    };
+    auto prefetch_qkv = [&](TkW<RQ>& p, uint32_t l, uint32_t t) {
+        uint32_t m, g;
+        qkv_tile(t, m, g);
+        tile_prefetch(p, S.lt[l].w[m], S.lt[l].s[m], Sh::HB, m == 0 ? QD : kTkHD, g, 0u, Sh::HB, wave,
+                      lane);
+    };
+    auto prefetch_dn = [&](TkW<RD>& p, uint32_t l, uint32_t t) {
+        const uint32_t g = t / NCH, q0 = Sh::DQ * (t % NCH);
+        tile_prefetch(p, S.lt[l].w[6], S.lt[l].s[6], FFN / kBlk, H, g, 4u * q0,
+                      4u * min(Sh::DQ, Sh::NQF - q0), wave, lane);
+    };
+    TkW<RQ> pq;
+    if (t_qkv < Sh::N_QKV) prefetch_qkv(pq, 0u, t_qkv);
 
     for (uint32_t l = 0; l < a.n_layers; ++l) {
+        tid = opaque(threadIdx.x);
+        lane = tid % kWave;
+        hown = tid < Sh::HO;
         const TokLayer& L = S.lt[l];
-        ll_t* LL = a.ll + size_t(l) * a.ll_layer;
+        const uint32_t soff = l * lstride;
         // ================= QKV =================
-        for (uint32_t t = t_qkv; t < n_qkv; t += nwg) {
-            const TkTile tt = tk_qkv_tile(a, L, t);
-            tk_prefetch(tt, pre, wave, lane);
-            TkNormW w_in, w_post;
-            tk_load_norm(w_in, L.norm[0], H);
-            if (l > 0) tk_load_norm(w_post, S.lt[l - 1u].norm[3], H);
-            if (l == 0) tk_embed(a, S, tok);
-            else tk_after_ffn(a, S, lay, l - 1u, w_post);
-            if (t == 0) {
-                for (uint32_t i = tid; i < H; i += kTkThreads) ll_put(LL + lay.xa + i, S.xs[i], tag);
+        for (uint32_t t = t_qkv; t < Sh::N_QKV; t += nwg) {
+            uint32_t m, g;
+            qkv_tile(t, m, g);
+            if (t != t_qkv) prefetch_qkv(pq, l, t);
+            float w_in[kOwn] = {}, w_post[kOwn] = {}, x[kOwn] = {};
+            if (hown) {
+                ld_own(w_in, L.norm[0] + kOwn * tid);
+                if (l > 0) ld_own(w_post, S.lt[l - 1u].norm[3] + kOwn * tid);
             }
-            tk_norm(a, S, w_in);
-            tk_stage(S, H / kBlk);
-            const float r = tk_tile(tt, pre, S, 0u, a.fmt, wave, lane);
+            if (l == 0) {
+                // embedding (decode.cpp:1618-1627) as a gather from the tied int4 table
+                if (hown) {
+                    // element k = kOwn tid + e: block k / 32, word (k % 32) / 8, nibble k % 8
+                    const uint32_t k0 = kOwn * tid, b = k0 / kBlk, c = (k0 % kBlk) / 8u, n0 = k0 % 8u;
+                    const uint32_t* wq = static_cast<const uint32_t*>(a.lm_w);
+                    const uint32_t word =
+                        ldg32(wq + ((size_t(tok / kGrp) * Sh::HB + b) * kGrp + (tok % kGrp)) * 4u + c);
+                    const uint16_t h = ldg16(static_cast<const uint16_t*>(a.lm_s) +
+                                             (size_t(b / 4u) * a.vocab + tok) * 4u + (b % 4u));
+                    const float s = FMT == XP_SCALE_F16_QUAD ? f16_bits_to_f32(h)
+                                                             : __uint_as_float(uint32_t(h) << 16);
+#pragma unroll
+                    for (uint32_t e = 0; e < kOwn; ++e) {
+                        const float q = float(int((word >> (4u * (n0 + e))) & 15u) - 8);
+                        x[e] = (q * s) * a.embed_scale;
+                    }
+                }
+            } else {
+                after_ffn(x, l - 1u, w_post);
+            }
+            float xn[kOwn];
+            own_norm<H>(xn, x, w_in, eps, RS());
+            if (hown) own_stage(S, xn);
+            __syncthreads();
+            const float y = tile_dot<FMT>(pq, S, Sh::HB, wave, lane);
             if (wave == 0) {
-                const uint32_t o = tt.m == 0u ? 0u : (tt.m == 1u ? qd : qd + kTkHD);
-                ll_put(LL + lay.qkv + o + tt.g * kGrp + lane, r, tag);
+                const uint32_t o = m == 0u ? 0u : (m == 1u ? QD : QD + kTkHD);
+                tile_put(rr, soff, uint32_t(lay.qkv) + o + g * kGrp, y, lane, tag);
             }
+            // x entering the layer, for the gate/up stage: tile t < H / 64
+            // stores elements 64 t .. 64 t + 63 (spread so that no workgroup
+            // issues many stores). Stored last: a later wait on this wave's
+            // memory counter also waits for its stores.
+            if (t < Sh::N_O && tid / (kGrp / kOwn) == t) own_put(rr, soff, uint32_t(lay.xa) + kOwn * tid, x, tag);
         }
         tk_trace(a, 1u + 6u * l);
 
@@ -457,51 +554,72 @@ __global__ __launch_bounds__(kTkThreads) void token_kernel(TokArgs a) {
         const uint32_t s_att = nwg - 1u - wg;
         if (s_att < n_att) {
             const uint32_t j0 = s_att * kTkC;
-            // score mapping: key jk = tid / 16, 16 dims at part * 16
+            // score mapping: key jk = tid / 16; part p holds dims 64 c + 4 p .. + 3,
+            // c < 4 (the 16 parts of a key read 16 consecutive float4 of q: no
+            // LDS bank conflicts)
             const uint32_t jk = tid / 16u, part = tid % 16u;
             // value mapping: dims 2*dp, 2*dp+1 of keys kgv*8 .. kgv*8+7
             const uint32_t dp = tid % 128u, kgv = tid / 128u;
-            u32x4 kr[2] = {u32x4{0u, 0u, 0u, 0u}, u32x4{0u, 0u, 0u, 0u}};
+            u32x2 kr[4];
             uint32_t vw[8];
+#pragma unroll
+            for (int c = 0; c < 4; ++c) kr[c] = u32x2{0u, 0u};
 #pragma unroll
             for (int i = 0; i < 8; ++i) vw[i] = 0u;
             if (j0 + jk < span) {
-                const u32x4* kp = reinterpret_cast<const u32x4*>(
-                    L.kc + size_t(kv0 + j0 + jk) * kTkHD + part * 16u);
-                kr[0] = ldg4(kp);
-                kr[1] = ldg4(kp + 1);
+                const uint16_t* kp = L.kc + size_t(kv0 + j0 + jk) * kTkHD + 4u * part;
+#pragma unroll
+                for (int c = 0; c < 4; ++c) kr[c] = *(const XP_GLOBAL u32x2*)(kp + 64 * c);
             }
 #pragma unroll
             for (int i = 0; i < 8; ++i) {
                 const uint32_t jj = j0 + kgv * 8u + i;
-                if (jj < span)
-                    vw[i] = ldg32(L.vc + size_t(kv0 + jj) * kTkHD + 2u * dp);
+                if (jj < span) vw[i] = ldg32(L.vc + size_t(kv0 + jj) * kTkHD + 2u * dp);
             }
-            // QK-norm weights of this wave's first head, then q_raw | k_raw | v
-            float wqk[4];
+            // QK-norm weights of this wave's head (waves 0..NH-1: q heads, NH: the kv head)
+            static_assert(NH < uint32_t(kTkWaves), "one wave per q head plus one for the kv head");
+            float wqk[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+            if (wave <= NH) {
+                const float* w = wave < NH ? L.norm[4] : L.norm[5];
+#pragma unroll
+                for (int c = 0; c < 4; ++c) wqk[c] = ldgf(w + lane + 64 * c);
+            }
             {
-                const float* w = wave < a.n_heads ? L.norm[4] : L.norm[5];
+                // raw q | k | v: pairs tid and tid + 512
+                constexpr uint32_t NP = Sh::QKVD / 2;
+                constexpr int NL = int((NP + kTkThreads - 1) / kTkThreads);
+                uint32_t off[NL];
+                bool act[NL];
+                u32x4 v[NL];
 #pragma unroll
-                for (int c = 0; c < 4; ++c) wqk[c] = wave <= a.n_heads ? ldgf(w + lane + 64 * c) : 0.0f;
+                for (int i = 0; i < NL; ++i) {
+                    const uint32_t pi = tid + uint32_t(kTkThreads) * i;
+                    act[i] = pi < NP;
+                    off[i] = (uint32_t(lay.qkv) + 2u * min(pi, NP - 1u)) * 8u;
+                }
+                ll_wait(rr, soff, off, act, v, tag, a.state);
+#pragma unroll
+                for (int i = 0; i < NL; ++i) {
+                    const uint32_t pi = tid + uint32_t(kTkThreads) * i;
+                    if (act[i])
+                        *reinterpret_cast<float2*>(&S.xq[2u * pi]) =
+                            float2{__uint_as_float(v[i].x), __uint_as_float(v[i].z)};
+                }
             }
-            ll_fetch(S.xn, LL + lay.qkv, qd + 2u * kTkHD, tag, a.state);
+            __syncthreads();
             const uint32_t th = glob ? 1u : 0u;
-            // QK-norm + RoPE, one wave per head (q heads, then the kv head)
-            for (uint32_t hh = wave; hh <= a.n_heads; hh += kTkWaves) {
-                const bool isq = hh < a.n_heads;
-                const float* src = isq ? S.xn + hh * kTkHD : S.xn + qd;
-                float wc[4];
-#pragma unroll
-                for (int c = 0; c < 4; ++c)
-                    wc[c] = hh == wave ? wqk[c] : ldgf((isq ? L.norm[4] : L.norm[5]) + lane + 64 * c);
+            // QK-norm + RoPE, one wave per head: the q heads, then the kv head
+            // (which follows them in q | k | v)
+            if (wave <= NH) {
+                const float* src = S.xq + wave * kTkHD;
                 float e[4];
 #pragma unroll
                 for (int c = 0; c < 4; ++c) e[c] = src[lane + 64 * c];
                 float ss = e[0] * e[0] + e[1] * e[1] + e[2] * e[2] + e[3] * e[3];
                 ss = wave_sum(ss);
-                const float scale = 1.0f / sqrtf(ss / float(kTkHD) + a.eps);
+                const float scale = 1.0f / sqrtf(ss / float(kTkHD) + eps);
 #pragma unroll
-                for (int c = 0; c < 4; ++c) e[c] = e[c] * scale * (1.0f + wc[c]);
+                for (int c = 0; c < 4; ++c) e[c] = e[c] * scale * (1.0f + wqk[c]);
                 // rotate-half pairs (d, d + 128): (e0, e2) at d = lane, (e1, e3) at lane + 64
 #pragma unroll
                 for (int c = 0; c < 2; ++c) {
@@ -510,121 +628,166 @@ __global__ __launch_bounds__(kTkThreads) void token_kernel(TokArgs a) {
                     e[c] = lo * cv - hi * sv;
                     e[c + 2] = lo * sv + hi * cv;
                 }
-                if (isq) {
+                if (wave < NH) {
 #pragma unroll
-                    for (int c = 0; c < 4; ++c) S.qh[hh][lane + 64 * c] = e[c];
+                    for (int c = 0; c < 4; ++c) S.qh[wave][lane + 64 * c] = e[c];
                 } else {
 #pragma unroll
                     for (int c = 0; c < 4; ++c) S.kn[lane + 64 * c] = f16_round(e[c]);
                 }
             }
-            if (tid < kTkHD) S.vn[tid] = f16_round(S.xn[qd + kTkHD + tid]);
+            if (tid < kTkHD) S.vn[tid] = f16_round(S.xq[QD + kTkHD + tid]);
             __syncthreads();
-            if (s_att == n_att - 1u && tid < kTkHD) {
-                stg16(L.kc + size_t(pos) * kTkHD + tid, f32_to_f16_bits(S.kn[tid]));
-                stg16(L.vc + size_t(pos) * kTkHD + tid, f32_to_f16_bits(S.vn[tid]));
-            }
-            // scores
+            // scores (the current key comes from S.kn, read unconditionally so
+            // that the choice is a select, not a branch)
             {
                 const uint32_t jj = j0 + jk;
                 const bool valid = jj < span;
                 const bool cur = kv0 + jj == pos;
                 float kf[16];
-                const uint32_t kw[8] = {kr[0].x, kr[0].y, kr[0].z, kr[0].w,
-                                        kr[1].x, kr[1].y, kr[1].z, kr[1].w};
 #pragma unroll
-                for (int e = 0; e < 8; ++e) {
-                    kf[2 * e] = cur ? S.kn[part * 16u + 2 * e] : f16_bits_to_f32(kw[e]);
-                    kf[2 * e + 1] = cur ? S.kn[part * 16u + 2 * e + 1] : f16_bits_to_f32(kw[e] >> 16);
+                for (int c = 0; c < 4; ++c) {
+                    const float4 kc = *reinterpret_cast<const float4*>(&S.kn[64 * c + 4u * part]);
+                    kf[4 * c + 0] = cur ? kc.x : f16_bits_to_f32(kr[c].x);
+                    kf[4 * c + 1] = cur ? kc.y : f16_bits_to_f32(kr[c].x >> 16);
+                    kf[4 * c + 2] = cur ? kc.z : f16_bits_to_f32(kr[c].y);
+                    kf[4 * c + 3] = cur ? kc.w : f16_bits_to_f32(kr[c].y >> 16);
                 }
-                for (uint32_t h = 0; h < a.n_heads; ++h) {
-                    const float* qp = &S.qh[h][part * 16u];
-                    float d = 0.0f;
+                float d[NH];
 #pragma unroll
-                    for (int e = 0; e < 16; ++e) d = fmaf(qp[e], kf[e], d);
-                    d = row16_sum(d);   // the 16 lanes of key jk are one DPP row
-                    if (part == 0) S.sc[h][jk] = valid ? d * a.attn_scale : -INFINITY;
+                for (uint32_t h = 0; h < NH; ++h) {
+                    float acc = 0.0f;
+#pragma unroll
+                    for (int c = 0; c < 4; ++c) {
+                        const float4 q = *reinterpret_cast<const float4*>(&S.qh[h][64 * c + 4u * part]);
+                        acc = fmaf(q.x, kf[4 * c + 0], acc);
+                        acc = fmaf(q.y, kf[4 * c + 1], acc);
+                        acc = fmaf(q.z, kf[4 * c + 2], acc);
+                        acc = fmaf(q.w, kf[4 * c + 3], acc);
+                    }
+                    d[h] = acc;
+                }
+#pragma unroll
+                for (uint32_t h = 0; h < NH; ++h) d[h] = row16_sum(d[h]);   // key jk's 16 lanes = one DPP row
+                if (part == 0) {
+#pragma unroll
+                    for (uint32_t h = 0; h < NH; ++h) S.sc[jk][h] = valid ? d[h] * a.attn_scale : -INFINITY;
                 }
             }
             __syncthreads();
             // chunk softmax, one wave per head
-            for (uint32_t h = wave; h < a.n_heads; h += kTkWaves) {
-                const float v = lane < uint32_t(kTkC) ? S.sc[h][lane] : -INFINITY;
-                const float m = wave_max(v);
-                const float e = (lane < uint32_t(kTkC) && v != -INFINITY) ? expf(v - m) : 0.0f;
+            if (wave < NH) {
+                const uint32_t h = wave;
+                const float v = S.sc[lane % kTkC][h];
+                const bool in = lane < kTkC && v != -INFINITY;
+                const float m = wave_max(in ? v : -INFINITY);
+                const float e = in ? expf(v - m) : 0.0f;
                 const float l2 = wave_sum(e);
-                if (lane < uint32_t(kTkC)) S.sc[h][lane] = e;
+                if (lane < kTkC) S.sc[lane][h] = e;
                 if (lane == 0) { S.mh[h] = m; S.lh[h] = l2; }
             }
             __syncthreads();
-            // weighted values
+            // weighted values (keys past the span have weight 0 and value 0)
             {
-                float o0[kTkMaxQH], o1[kTkMaxQH];
+                const float2 vc = *reinterpret_cast<const float2*>(&S.vn[2u * dp]);
+                float o0[NH], o1[NH];
 #pragma unroll
-                for (int h = 0; h < kTkMaxQH; ++h) o0[h] = o1[h] = 0.0f;
+                for (uint32_t h = 0; h < NH; ++h) o0[h] = o1[h] = 0.0f;
 #pragma unroll
                 for (int i = 0; i < 8; ++i) {
-                    const uint32_t jl = kgv * 8u + i, jj = j0 + jl;
-                    if (jj < span) {
-                        const bool cur = kv0 + jj == pos;
-                        const float v0 = cur ? S.vn[2 * dp] : f16_bits_to_f32(vw[i]);
-                        const float v1 = cur ? S.vn[2 * dp + 1] : f16_bits_to_f32(vw[i] >> 16);
+                    const uint32_t jl = kgv * 8u + i;
+                    const bool cur = kv0 + j0 + jl == pos;
+                    const float v0 = cur ? vc.x : f16_bits_to_f32(vw[i]);
+                    const float v1 = cur ? vc.y : f16_bits_to_f32(vw[i] >> 16);
+                    float pr[NH];
+                    if constexpr (NH % 4 == 0) {
 #pragma unroll
-                        for (int h = 0; h < kTkMaxQH; ++h) {
-                            if (uint32_t(h) < a.n_heads) {
-                                const float p = S.sc[h][jl];
-                                o0[h] = fmaf(p, v0, o0[h]);
-                                o1[h] = fmaf(p, v1, o1[h]);
-                            }
+                        for (uint32_t h4 = 0; h4 < NH; h4 += 4) {
+                            const float4 q = *reinterpret_cast<const float4*>(&S.sc[jl][h4]);
+                            pr[h4] = q.x; pr[h4 + 1] = q.y; pr[h4 + 2] = q.z; pr[h4 + 3] = q.w;
                         }
+                    } else {
+#pragma unroll
+                        for (uint32_t h = 0; h < NH; ++h) pr[h] = S.sc[jl][h];
+                    }
+#pragma unroll
+                    for (uint32_t h = 0; h < NH; ++h) {
+                        o0[h] = fmaf(pr[h], v0, o0[h]);
+                        o1[h] = fmaf(pr[h], v1, o1[h]);
                     }
                 }
 #pragma unroll
-                for (int h = 0; h < kTkMaxQH; ++h) {
-                    if (uint32_t(h) < a.n_heads) {
-                        float* vr = S.big + (kgv * a.n_heads + h) * kTkHD;
-                        vr[2 * dp] = o0[h];
-                        vr[2 * dp + 1] = o1[h];
-                    }
-                }
+                for (uint32_t h = 0; h < NH; ++h)
+                    *reinterpret_cast<float2*>(&S.big[(kgv * NH + h) * kTkHD + 2u * dp]) =
+                        float2{o0[h], o1[h]};
             }
             __syncthreads();
-            ll_t* pb = LL + lay.attp + size_t(s_att) * a.n_heads * (2u + kTkHD);
-            for (uint32_t i = tid; i < a.n_heads * kTkHD; i += kTkThreads) {
-                const uint32_t h = i / kTkHD, d = i % kTkHD;
-                const uint32_t hs = a.n_heads * kTkHD;
-                const float* vr = S.big + h * kTkHD + d;
-                const float o = ((vr[0] + vr[hs]) + vr[2 * hs]) + vr[3 * hs];
-                ll_put(pb + h * (2u + kTkHD) + 2u + d, o, tag);
+            // chunk record: per head (max, sum of exp, unnormalised output[256])
+            const uint32_t pb = uint32_t(lay.attp) + s_att * NH * (2u + kTkHD);
+#pragma unroll
+            for (uint32_t i = tid; i < NH * (kTkHD / 2u); i += kTkThreads) {
+                const uint32_t h = i / (kTkHD / 2u), d2 = 2u * (i % (kTkHD / 2u));
+                constexpr uint32_t hs = NH * kTkHD;
+                const float* vr = S.big + h * kTkHD + d2;
+                const float2 a0 = *reinterpret_cast<const float2*>(vr);
+                const float2 a1 = *reinterpret_cast<const float2*>(vr + hs);
+                const float2 a2 = *reinterpret_cast<const float2*>(vr + 2 * hs);
+                const float2 a3 = *reinterpret_cast<const float2*>(vr + 3 * hs);
+                ll_st2(rr, (pb + h * (2u + kTkHD) + 2u + d2) * 8u, soff, ((a0.x + a1.x) + a2.x) + a3.x,
+                       ((a0.y + a1.y) + a2.y) + a3.y, tag);
             }
-            if (tid < a.n_heads) {
-                ll_put(pb + tid * (2u + kTkHD), S.mh[tid], tag);
-                ll_put(pb + tid * (2u + kTkHD) + 1u, S.lh[tid], tag);
+            if (tid < NH) ll_st2(rr, (pb + tid * (2u + kTkHD)) * 8u, soff, S.mh[tid], S.lh[tid], tag);
+            // the chunk holding the current position appends its key / value
+            // to the caches for later tokens (after the results: stores)
+            if (s_att == n_att - 1u && tid < kTkHD) {
+                stg16(L.kc + size_t(pos) * kTkHD + tid, f32_to_f16_bits(S.kn[tid]));
+                stg16(L.vc + size_t(pos) * kTkHD + tid, f32_to_f16_bits(S.vn[tid]));
             }
+            __syncthreads();
         }
         tk_trace(a, 2u + 6u * l);
 
         // ================= combine =================
-        for (uint32_t c = t_comb; c < n_comb; c += nwg) {
+        for (uint32_t c = t_comb; c < Sh::N_COMB; c += nwg) {
             const uint32_t h = c / 4u, d0 = (c % 4u) * 64u;
-            const size_t rstride = size_t(a.n_heads) * (2u + kTkHD);
-            const ll_t* base = LL + lay.attp + size_t(h) * (2u + kTkHD);
+            const uint32_t rstride = NH * (2u + kTkHD);
+            const uint32_t base = uint32_t(lay.attp) + h * (2u + kTkHD);
             // big[s * 66 + 0 / 1] = (max, sum of exp) of chunk s,
-            // big[s * 66 + 2 + d] = its unnormalised output at dim d0 + d.
-            ll_fetch_at(S.big, n_att * 66u, tag, a.state, [=](uint32_t i) {
-                const uint32_t sidx = i / 66u, e = i % 66u;
-                return base + sidx * rstride + (e < 2u ? e : d0 + e);
-            });
+            // big[s * 66 + 2 + d] = its unnormalised output at dim d0 + d:
+            // 33 slot pairs per chunk, fetched 4 per thread at a time.
+            const uint32_t np = n_att * 33u;
+            for (uint32_t b = 0; b < np; b += 4u * kTkThreads) {
+                uint32_t off[4];
+                bool act[4];
+                u32x4 v[4];
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const uint32_t i = b + uint32_t(r) * kTkThreads + tid;
+                    act[r] = i < np;
+                    const uint32_t ic = act[r] ? i : 0u;
+                    const uint32_t s = ic / 33u, e = ic % 33u;
+                    off[r] = (base + s * rstride + (e == 0u ? 0u : 2u + d0 + 2u * (e - 1u))) * 8u;
+                }
+                ll_wait(rr, soff, off, act, v, tag, a.state);
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const uint32_t i = b + uint32_t(r) * kTkThreads + tid;
+                    if (act[r])
+                        *reinterpret_cast<float2*>(&S.big[2u * i]) =
+                            float2{__uint_as_float(v[r].x), __uint_as_float(v[r].z)};
+                }
+            }
+            __syncthreads();
             float m = -INFINITY;
             for (uint32_t s = tid; s < n_att; s += kTkThreads) m = fmaxf(m, S.big[s * 66u]);
-            const float M = tk_block_max(m, S.rs);
+            const float M = blk_max(m, RS());
             float lsum = 0.0f;
             for (uint32_t s = tid; s < n_att; s += kTkThreads) {
                 const float f = expf(S.big[s * 66u] - M);
                 S.fm[s] = f;
                 lsum += f * S.big[s * 66u + 1u];
             }
-            const float Ltot = tk_block_sum(lsum, S.rt);   // also orders the fm writes
+            const float Ltot = blk_sum(lsum, RS());   // also orders the fm writes
             const uint32_t d = tid % 64u, sg = tid / 64u;
             float o = 0.0f;
             for (uint32_t s = sg; s < n_att; s += kTkWaves) o = fmaf(S.big[s * 66u + 2u + d], S.fm[s], o);
@@ -634,64 +797,98 @@ __global__ __launch_bounds__(kTkThreads) void token_kernel(TokArgs a) {
                 float r = 0.0f;
 #pragma unroll
                 for (int w = 0; w < kTkWaves; ++w) r += S.red[w][d];
-                ll_put(LL + lay.atto + h * kTkHD + d0 + d, r / Ltot, tag);
+                tile_put(rr, soff, uint32_t(lay.atto) + h * kTkHD + d0, r / Ltot, lane, tag);
             }
             __syncthreads();
         }
         tk_trace(a, 3u + 6u * l);
 
         // ================= O projection =================
-        for (uint32_t t = t_o; t < n_o; t += nwg) {
-            const TkTile tt = tk_o_tile(a, L, t);
-            tk_prefetch(tt, pre, wave, lane);
-            ll_fetch(S.xn, LL + lay.atto, qd, tag, a.state);
-            tk_stage(S, qd / kBlk);
-            const float r = tk_tile(tt, pre, S, 0u, a.fmt, wave, lane);
-            if (wave == 0) ll_put(LL + lay.o + tt.g * kGrp + lane, r, tag);
+        for (uint32_t t = t_o; t < Sh::N_O; t += nwg) {
+            constexpr uint32_t nb = QD / kBlk;
+            TkW<(nb + 7) / 8> p;
+            tile_prefetch(p, L.w[3], L.s[3], nb, H, t, 0u, nb, wave, lane);
+            if (tid < Sh::QO) {
+                uint32_t off[kOwnP];
+                bool act[kOwnP];
+                u32x4 v[kOwnP];
+#pragma unroll
+                for (uint32_t j = 0; j < kOwnP; ++j) act[j] = true;
+                own_offsets(off, uint32_t(lay.atto) + kOwn * tid);
+                ll_wait(rr, soff, off, act, v, tag, a.state);
+                float x[kOwn];
+                own_unpack(x, v);
+                own_stage(S, x);
+            }
+            __syncthreads();
+            const float y = tile_dot<FMT>(p, S, nb, wave, lane);
+            if (wave == 0) tile_put(rr, soff, uint32_t(lay.o) + t * kGrp, y, lane, tag);
         }
         tk_trace(a, 4u + 6u * l);
 
         // ================= gate / up =================
-        for (uint32_t t = t_gu; t < n_gu; t += nwg) {
-            const TkTile tt = tk_gu_tile(a, L, t);
-            tk_prefetch(tt, pre, wave, lane);
-            TkNormW w_post, w_in;
-            tk_load_norm(w_post, L.norm[1], H);
-            tk_load_norm(w_in, L.norm[2], H);
-            ll_fetch2(S.big, LL + lay.xa, H, LL + lay.o, H, tag, a.state);
-            for (uint32_t i = tid; i < H; i += kTkThreads) {
-                S.xn[i] = S.big[i];
-                S.xt[i] = S.big[H + i];
+        TkW<RD> pdn;
+        if (t_dn < Sh::N_DN) prefetch_dn(pdn, l, t_dn);
+        for (uint32_t t = t_gu; t < Sh::N_GU; t += nwg) {
+            constexpr uint32_t ng = FFN / kGrp;
+            const uint32_t m = t < ng ? 4u : 5u, g = t < ng ? t : t - ng;
+            TkW<RQ> p;
+            tile_prefetch(p, L.w[m], L.s[m], Sh::HB, FFN, g, 0u, Sh::HB, wave, lane);
+            float w_post[kOwn] = {}, w_in[kOwn] = {}, xa[kOwn] = {}, o[kOwn] = {};
+            if (hown) {
+                ld_own(w_post, L.norm[1] + kOwn * tid);
+                ld_own(w_in, L.norm[2] + kOwn * tid);
+                uint32_t off[2 * kOwnP];
+                bool act[2 * kOwnP];
+                u32x4 v[2 * kOwnP];
+#pragma unroll
+                for (uint32_t j = 0; j < 2 * kOwnP; ++j) act[j] = true;
+                own_offsets(&off[0], uint32_t(lay.xa) + kOwn * tid);
+                own_offsets(&off[kOwnP], uint32_t(lay.o) + kOwn * tid);
+                ll_wait<2 * kOwnP, kGuSleep>(rr, soff, off, act, v, tag, a.state);
+                own_unpack(xa, &v[0]);
+                own_unpack(o, &v[kOwnP]);
             }
+            float x[kOwn], xn[kOwn];
+            own_residual<H>(x, xa, o, w_post, eps, RS());
+            own_norm<H>(xn, x, w_in, eps, RS());
+            if (hown) own_stage(S, xn);
             __syncthreads();
-            tk_residual(a, S, w_post);
-            if (t == 0) {
-                for (uint32_t i = tid; i < H; i += kTkThreads) ll_put(LL + lay.xb + i, S.xs[i], tag);
-            }
-            tk_norm(a, S, w_in);
-            tk_stage(S, H / kBlk);
-            const float r = tk_tile(tt, pre, S, 0u, a.fmt, wave, lane);
-            if (wave == 0) {
-                const uint32_t o = tt.m == 4u ? 0u : a.ffn;
-                ll_put(LL + lay.gu + o + tt.g * kGrp + lane, r, tag);
-            }
+            const float y = tile_dot<FMT>(p, S, Sh::HB, wave, lane);
+            if (wave == 0) tile_put(rr, soff, uint32_t(lay.gu) + (m == 4u ? 0u : FFN) + g * kGrp, y, lane, tag);
+            // x after the attention block, for the next layer: spread and stored last, as xa
+            if (t < Sh::N_O && tid / (kGrp / kOwn) == t) own_put(rr, soff, uint32_t(lay.xb) + kOwn * tid, x, tag);
         }
         tk_trace(a, 5u + 6u * l);
 
         // ================= down =================
-        for (uint32_t t = t_dn; t < n_dn; t += nwg) {
-            const TkTile tt = tk_down_tile(a, L, t);
-            tk_prefetch(tt, pre, wave, lane);
-            const uint32_t k0 = tt.qa * 128u, nk = (tt.qb - tt.qa) * 128u;
-            ll_fetch2(S.big, LL + lay.gu + k0, nk, LL + lay.gu + a.ffn + k0, nk, tag, a.state);
-            for (uint32_t i = tid; i < nk; i += kTkThreads)
-                S.xn[i] = gelu_tanh(S.big[i]) * S.big[nk + i];
+        for (uint32_t t = t_dn; t < Sh::N_DN; t += nwg) {
+            const uint32_t g = t / NCH, c = t % NCH;
+            const uint32_t q0 = Sh::DQ * c, nq = min(Sh::DQ, Sh::NQF - q0);
+            const uint32_t nb = 4u * nq, k0 = 128u * q0;
+            if (t != t_dn) prefetch_dn(pdn, l, t);
+            if (t == t_dn && l + 1u < a.n_layers && t_qkv < Sh::N_QKV) prefetch_qkv(pq, l + 1u, t_qkv);
+            if (tid < nb * (kBlk / kOwn)) {
+                uint32_t off[2 * kOwnP];
+                bool act[2 * kOwnP];
+                u32x4 v[2 * kOwnP];
+#pragma unroll
+                for (uint32_t j = 0; j < 2 * kOwnP; ++j) act[j] = true;
+                own_offsets(&off[0], uint32_t(lay.gu) + k0 + kOwn * tid);
+                own_offsets(&off[kOwnP], uint32_t(lay.gu) + FFN + k0 + kOwn * tid);
+                ll_wait(rr, soff, off, act, v, tag, a.state);
+                float gt[kOwn], up[kOwn], hx[kOwn];
+                own_unpack(gt, &v[0]);
+                own_unpack(up, &v[kOwnP]);
+#pragma unroll
+                for (uint32_t e = 0; e < kOwn; ++e) hx[e] = gelu_tanh(gt[e]) * up[e];
+                own_stage(S, hx);
+            }
             __syncthreads();
-            tk_stage(S, nk / kBlk);
-            const float r = tk_tile(tt, pre, S, tt.qa, a.fmt, wave, lane);
-            if (wave == 0)
-                ll_put(LL + lay.dnp + size_t(t % nch) * H + tt.g * kGrp + lane, r, tag);
+            const float y = tile_dot<FMT>(pdn, S, nb, wave, lane);
+            if (wave == 0) tile_put(rr, soff, uint32_t(lay.dnp) + c * H + g * kGrp, y, lane, tag);
         }
+        if (t_dn >= Sh::N_DN && l + 1u < a.n_layers && t_qkv < Sh::N_QKV) prefetch_qkv(pq, l + 1u, t_qkv);
         tk_trace(a, 6u + 6u * l);
     }
 
@@ -703,7 +900,7 @@ __global__ __launch_bounds__(kTkThreads) void token_kernel(TokArgs a) {
     // ================= final norm, lm_head, argmax =================
     const uint32_t ng = a.vocab / kGrp;
     const uint32_t gw = wg * kTkWaves + wave, nw = nwg * kTkWaves;
-    const uint32_t nqh = H / 128u;
+    constexpr uint32_t nqh = Sh::NQH;
     const u32x4* lmw = static_cast<const u32x4*>(a.lm_w);
     // Quad stream of this wave: groups gw, gw + nw, ...; k/128 quads each.
     const uint32_t my_groups = gw < ng ? (ng - gw + nw - 1u) / nw : 0u;
@@ -713,7 +910,7 @@ __global__ __launch_bounds__(kTkThreads) void token_kernel(TokArgs a) {
     auto load_u = [&](int r, uint32_t u) {
         const uint32_t uc = min(u, nu - 1u);
         const uint32_t g = gw + (uc / nqh) * nw, q = uc % nqh;
-        const u32x4* wp = lmw + (size_t(g) * (H / kBlk) + 4u * q) * kGrp + lane;
+        const u32x4* wp = lmw + (size_t(g) * Sh::HB + 4u * q) * kGrp + lane;
 #pragma unroll
         for (int i = 0; i < 4; ++i) w3[r][i] = ldg_stream4(wp + i * kGrp);
         s3[r] = ldg_stream2(reinterpret_cast<const u32x2*>(a.lm_s) + size_t(q) * a.vocab +
@@ -724,12 +921,17 @@ __global__ __launch_bounds__(kTkThreads) void token_kernel(TokArgs a) {
         load_u(1, 1);
         load_u(2, 2);
     }
-    TkNormW wf_post, wf_in;
-    tk_load_norm(wf_post, S.lt[a.n_layers - 1u].norm[3], H);
-    tk_load_norm(wf_in, a.final_norm, H);
-    tk_after_ffn(a, S, lay, a.n_layers - 1u, wf_post);
-    tk_norm(a, S, wf_in);
-    tk_stage(S, H / kBlk);
+    {
+        float wf_post[kOwn] = {}, wf_in[kOwn] = {}, x[kOwn], xn[kOwn];
+        if (hown) {
+            ld_own(wf_post, S.lt[a.n_layers - 1u].norm[3] + kOwn * tid);
+            ld_own(wf_in, a.final_norm + kOwn * tid);
+        }
+        after_ffn(x, a.n_layers - 1u, wf_post);
+        own_norm<H>(xn, x, wf_in, eps, RS());
+        if (hown) own_stage(S, xn);
+        __syncthreads();
+    }
     float bv = -INFINITY;
     uint32_t bi = 0u;
     float acc = 0.0f;
@@ -738,7 +940,7 @@ __global__ __launch_bounds__(kTkThreads) void token_kernel(TokArgs a) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const uint32_t lb = 4u * q + i;
-            const float f = tk_scale(s3[r], i, a.fmt) * S.sx[lb];
+            const float f = tk_scale<FMT>(s3[r], i) * S.sx[lb];
             acc = fmaf(f, float(block_dot(w3[r][i], S.qx[lb])), acc);
         }
         if (q == nqh - 1u) {
@@ -763,20 +965,31 @@ __global__ __launch_bounds__(kTkThreads) void token_kernel(TokArgs a) {
     am_wave(bv, bi);
     if (lane == 0) { S.amv[wave] = bv; S.ami[wave] = bi; }
     __syncthreads();
-    ll_t* am = a.ll + size_t(a.n_layers) * a.ll_layer;
+    const uint32_t am_off = a.n_layers * lstride;   // argmax slots: (value, index) per workgroup
     if (tid == 0) {
         for (int w = 1; w < kTkWaves; ++w) am_better(bv, bi, S.amv[w], S.ami[w]);
-        ll_put(am + 2u * wg, bv, tag);
-        ll_put(am + 2u * wg + 1u, __uint_as_float(bi), tag);
+        ll_st2(rr, 16u * wg, am_off, bv, __uint_as_float(bi), tag);
     }
     tk_trace(a, 1u + 6u * a.n_layers);
     if (wg != 0) return;
-    __syncthreads();
-    ll_fetch(S.fm, am, 2u * nwg, tag, a.state);
+    __syncthreads();   // tid 0 has read S.amv
     bv = -INFINITY;
     bi = 0u;
-    for (uint32_t i = tid; i < nwg; i += kTkThreads)
-        am_better(bv, bi, S.fm[2 * i], __float_as_uint(S.fm[2 * i + 1]));
+    for (uint32_t i0 = 0; i0 < nwg; i0 += 4u * kTkThreads) {
+        uint32_t off[4];
+        bool act[4];
+        u32x4 v[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const uint32_t i = i0 + uint32_t(r) * kTkThreads + tid;
+            act[r] = i < nwg;
+            off[r] = 16u * (act[r] ? i : 0u);
+        }
+        ll_wait(rr, am_off, off, act, v, tag, a.state);
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+            if (act[r]) am_better(bv, bi, __uint_as_float(v[r].x), v[r].z);
+    }
     am_wave(bv, bi);
     if (lane == 0) { S.amv[wave] = bv; S.ami[wave] = bi; }
     __syncthreads();
@@ -790,6 +1003,21 @@ __global__ __launch_bounds__(kTkThreads) void token_kernel(TokArgs a) {
     tk_trace(a, 2u + 6u * a.n_layers);
 }
 
+namespace {
+// The shapes the kernel is built for.
+using TkGemma3_1B = TkShape<1152, 6912, 4>;
+
+const void* token_entry(uint32_t hidden, uint32_t ffn, uint32_t n_heads, int fmt) {
+    if (hidden == TkGemma3_1B::H && ffn == TkGemma3_1B::FFN && n_heads == TkGemma3_1B::NH) {
+        if (fmt == XP_SCALE_F16_QUAD)
+            return reinterpret_cast<const void*>(token_kernel<TkGemma3_1B, XP_SCALE_F16_QUAD>);
+        if (fmt == XP_SCALE_BF16_QUAD)
+            return reinterpret_cast<const void*>(token_kernel<TkGemma3_1B, XP_SCALE_BF16_QUAD>);
+    }
+    return nullptr;
+}
+}  // namespace
+
 size_t tok_lds_bytes() {
     // Over half of the 160 KiB a gfx950 CU has, so that each CU holds exactly
     // one workgroup of the grid.
@@ -801,39 +1029,47 @@ size_t tok_lds_bytes() {
 int tok_supported(uint32_t n_layers, uint32_t hidden, uint32_t ffn, uint32_t n_heads,
                   uint32_t n_kv_heads, uint32_t head_dim, uint32_t vocab, uint32_t max_seq,
                   int fmt, int n_cu) {
-    if (head_dim != uint32_t(kTkHD) || n_kv_heads != 1 || n_heads == 0 ||
-        n_heads > uint32_t(kTkMaxQH))
-        return set_error(XP_E_ARG, "token kernel: needs head_dim 256, one kv head, <= 8 q heads");
-    if (hidden > uint32_t(kTkMaxHidden) || hidden % 128 || ffn % 128 || vocab % kGrp)
-        return set_error(XP_E_ARG, "token kernel: hidden <= 2048, multiples of 128");
+    if (head_dim != kTkHD || n_kv_heads != 1)
+        return set_error(XP_E_ARG, "token kernel: needs head_dim 256 and one kv head");
     if (fmt != XP_SCALE_F16_QUAD && fmt != XP_SCALE_BF16_QUAD)
         return set_error(XP_E_ARG, "token kernel: fp16 or bf16 quad scales only");
-    const uint32_t nch = (ffn / 128u + 15u) / 16u;
-    if (uint64_t(nch + 1u) * hidden > uint64_t(kTkBig) ||
-        uint64_t(max_seq + kTkC - 1u) / kTkC * 66u > uint64_t(kTkBig))
-        return set_error(XP_E_ARG, "token kernel: stage scratch too small for this shape");
+    if (!token_entry(hidden, ffn, n_heads, fmt))
+        return set_error(XP_E_ARG,
+                         "token kernel: built for hidden 1152, ffn 6912, 4 query heads (got %u, %u, %u)",
+                         hidden, ffn, n_heads);
+    if (vocab % kGrp)
+        return set_error(XP_E_ARG, "token kernel: vocab must be a multiple of 64");
+    if (uint64_t(max_seq + kTkC - 1u) / kTkC * 66u > uint64_t(kTkBig))
+        return set_error(XP_E_ARG, "token kernel: stage scratch too small for max_seq %u", max_seq);
     if (n_layers == 0 || n_layers > uint32_t(kTkMaxLayers))
         return set_error(XP_E_ARG, "token kernel: at most %d layers", kTkMaxLayers);
     if (n_cu < 64 || n_cu > kTkMaxGrid || uint64_t(n_cu) * kTkC < max_seq)
         return set_error(XP_E_ARG, "token kernel: %d CUs cannot cover max_seq %u", n_cu, max_seq);
+    const TokLL lay = tok_ll_layout(hidden, ffn, n_heads, head_dim, uint32_t(n_cu));
+    if ((uint64_t(n_layers) * lay.layer + 2u * uint64_t(n_cu)) * 8u >= (1ull << 31))
+        return set_error(XP_E_ARG, "token kernel: exchange slots exceed 2 GiB");
     return XP_OK;
 }
 
 int launch_token(const TokArgs& a, uint32_t grid, hipStream_t st) {
-    static bool attr_set = false;
+    const void* fn = token_entry(a.hidden, a.ffn, a.n_heads, a.fmt);
+    if (!fn) return set_error(XP_E_ARG, "token kernel: no build for this shape");
+    // Raised once per kernel instance (the attribute is per function).
+    static const void* attr_set[4] = {};
     const size_t lds = tok_lds_bytes();
-    if (!attr_set) {
-        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(token_kernel),
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, int(lds));
+    bool have = false;
+    for (const void* f : attr_set) have |= f == fn;
+    if (!have) {
+        hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, int(lds));
         if (e != hipSuccess)
             return set_error(XP_E_HIP, "token kernel: %zu B of LDS -> %s", lds,
                              hipGetErrorString(e));
-        attr_set = true;
+        for (const void*& f : attr_set)
+            if (!f) { f = fn; break; }
     }
     TokArgs copy = a;
     void* args[] = {&copy};
-    hipError_t e = hipLaunchCooperativeKernel(reinterpret_cast<const void*>(token_kernel),
-                                              dim3(grid), dim3(kTkThreads), args, lds, st);
+    hipError_t e = hipLaunchCooperativeKernel(fn, dim3(grid), dim3(kTkThreads), args, lds, st);
     if (e != hipSuccess)
         return set_error(XP_E_HIP, "token kernel: cooperative launch of %u workgroups -> %s", grid,
                          hipGetErrorString(e));

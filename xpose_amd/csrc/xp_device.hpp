@@ -209,12 +209,14 @@ __device__ __forceinline__ void am_wave(float& bv, uint32_t& bi) {
 }
 
 // gelu_pytorch_tanh with the reference's clamped-exp tanh
-// (kernels/llm_transformer.cl:213-231). expf is the device libm exp.
+// (kernels/llm_transformer.cl:213-231). expf is the device libm exp; the
+// quotient uses the hardware reciprocal (1 ulp), not a correctly rounded
+// division.
 __device__ __forceinline__ float gelu_tanh(float g) {
     float z = 0.7978845608028654f * (g + 0.044715f * g * g * g);
     z = fminf(fmaxf(z, -10.0f), 10.0f);
     const float e = expf(-2.0f * z);
-    const float t = (1.0f - e) / (1.0f + e);
+    const float t = (1.0f - e) * __builtin_amdgcn_rcpf(1.0f + e);
     return 0.5f * g * (1.0f + t);
 }
 
