@@ -89,12 +89,17 @@ struct TkShape {
     static constexpr uint32_t HB = H / kBlk;                // 32-blocks of a hidden vector
     static constexpr uint32_t HO = H / 4;                   // owner threads of a hidden vector
     static constexpr uint32_t QO = QD / 4;                  // owner threads of the attention output
-    static constexpr uint32_t DQ = 16;                      // quads per down chunk
+    static constexpr uint32_t DQ = kTokDownQuads;           // quads per down chunk
     static constexpr uint32_t NQF = FFN / 128;              // quads of ffn
     static constexpr uint32_t NCH = (NQF + DQ - 1) / DQ;    // down chunks
-    static constexpr uint32_t N_QKV = QKVD / kGrp;
+    static constexpr uint32_t KQ = kTokQkvSplit;            // k halves of q|k|v
+    static constexpr uint32_t KO = kTokOSplit;              // k halves of o
+    static constexpr uint32_t QB = HB / KQ;                 // blocks per q|k|v tile
+    static constexpr uint32_t OB = QD / kBlk / KO;          // blocks per o tile
+    static constexpr uint32_t NOG = H / kGrp;               // o column groups
+    static constexpr uint32_t N_QKV = QKVD / kGrp * KQ;
     static constexpr uint32_t N_COMB = NH * 4;
-    static constexpr uint32_t N_O = H / kGrp;
+    static constexpr uint32_t N_O = NOG * KO;
     static constexpr uint32_t N_GU = 2 * FFN / kGrp;
     static constexpr uint32_t N_DN = (H / kGrp) * NCH;
     static constexpr uint32_t NQH = H / 128;                // lm_head quads per column
@@ -103,8 +108,9 @@ struct TkShape {
                   DQ * 128 / 4 <= uint32_t(kTkThreads), "vector too wide for four per thread");
     static_assert(HB <= kTkMaxBlk && QD / kBlk <= kTkMaxBlk && DQ * 4 <= kTkMaxBlk, "staging");
     static_assert(NH >= 1 && NH <= kTkMaxQH, "1..8 query heads");
-    static_assert((FFN + 2047) / 2048 == NCH, "chunk count must match the slot layout");
-    static_assert(N_O <= N_QKV && N_O <= N_GU, "x is stored by the first H / 64 tiles");
+    static_assert(tok_down_chunks(FFN) == NCH, "chunk count must match the slot layout");
+    static_assert(HB % KQ == 0 && (QD / kBlk) % KO == 0, "k splits must divide the blocks");
+    static_assert(NOG <= N_QKV && NOG <= N_GU, "x is stored by the first H / 64 tiles");
 };
 
 struct TkSmem {
@@ -297,11 +303,13 @@ __device__ __forceinline__ void stage_x4(QxBlock* qx, float* sx, uint32_t i, con
     }
     if (hw == 0) sx[lb] = m * (1.0f / kQxRange);
 }
-// Stages the owner vector of thread i < nblocks * 32 / kOwn as fixed-point
-// planes in S.qx / S.sx; the caller then waits at a barrier.
-__device__ __forceinline__ void own_stage(TkSmem& S, const float (&x)[kOwn]) {
+// Stages an owner vector as fixed-point planes in S.qx / S.sx: task i (i <
+// nblocks * 32 / kOwn, eight adjacent lanes per block) holds elements
+// kOwn i .. kOwn i + kOwn - 1 of the staged range. The caller then waits at a
+// barrier.
+__device__ __forceinline__ void own_stage(TkSmem& S, const float (&x)[kOwn], uint32_t i) {
     static_assert(kOwn == 4, "staging from four elements per thread");
-    stage_x4(S.qx, S.sx, threadIdx.x, x);
+    stage_x4(S.qx, S.sx, i, x);
 }
 
 // Scale i (0..3) of a block quad's four fp16 / bf16 scales, without branches.
@@ -337,19 +345,20 @@ __device__ __forceinline__ void tile_prefetch(TkW<R>& p, const void* wq, const v
     }
 }
 
-// Dot of the wave's blocks with the staged planes (S.qx[0] = block b0, a
-// multiple of 4, so the scale of block b0 + w + 8 r is component w % 4 of its
-// quad), reduced over the 8 waves in order. The result is valid in wave 0
-// (lane = column); the caller publishes it. Starts after the staging
+// Dot of the wave's blocks with the staged planes (S.qx[0] = block b0; the
+// scale of block b0 + w + 8 r is component (b0 + w) % 4 of its quad, the
+// same for all r), reduced over the 8 waves in order. The result is valid in
+// wave 0 (lane = column); the caller publishes it. Starts after the staging
 // barrier; ends with a barrier.
 template <int FMT, int R>
-__device__ __forceinline__ float tile_dot(const TkW<R>& p, TkSmem& S, uint32_t nb, uint32_t wave,
-                                          uint32_t lane) {
+__device__ __forceinline__ float tile_dot(const TkW<R>& p, TkSmem& S, uint32_t b0, uint32_t nb,
+                                          uint32_t wave, uint32_t lane) {
     float acc = 0.0f;
+    const uint32_t sc = (b0 + wave) % 4u;
 #pragma unroll
     for (int r = 0; r < R; ++r) {
         const uint32_t lb = min(wave + 8u * r, nb - 1u);
-        float f = tk_scale<FMT>(p.s[r], wave % 4u) * S.sx[lb];
+        float f = tk_scale<FMT>(p.s[r], sc) * S.sx[lb];
         if (wave + 8u * r >= nb) f = 0.0f;
         acc = fmaf(f, float(block_dot(p.w[r], S.qx[lb])), acc);
     }
@@ -430,9 +439,13 @@ __global__ __launch_bounds__(kTkThreads) void token_kernel(TokArgs a) {
     __syncthreads();
 
     // Workgroup -> tile maps: tile t of a stage runs on workgroup (off + t) %
-    // grid, so this workgroup's first tile is (wg - off) mod grid.
-    const uint32_t off_comb = Sh::N_QKV % nwg, off_gu = (Sh::N_QKV + Sh::N_COMB) % nwg;
-    const uint32_t t_qkv = wg, t_comb = (wg + nwg - off_comb) % nwg, t_o = wg;
+    // grid, so this workgroup's first tile is (wg - off) mod grid. QKV,
+    // combine, O and down start at workgroup 0 (combine's workgroups have no
+    // other work until O, which waits for all of combine anyway); gate/up
+    // starts past the O workgroups, whose O tile would otherwise delay their
+    // gate/up weight prefetch; attention runs from the last workgroup down.
+    const uint32_t off_gu = Sh::N_O % nwg;
+    const uint32_t t_qkv = wg, t_comb = wg, t_o = wg;
     const uint32_t t_gu = (wg + nwg - off_gu) % nwg, t_dn = wg;
     bool hown = tid < Sh::HO;                     // owns kOwn elements of a hidden vector
 
@@ -471,25 +484,29 @@ __global__ __launch_bounds__(kTkThreads) void token_kernel(TokArgs a) {
     // waits in the gate/up stage: a workgroup busy in the previous stage
     // would otherwise start streaming those weights only when its inputs are
     // already there.
-    constexpr int RQ = int(Sh::HB + 7) / 8;           // QKV and gate/up blocks per wave
+    constexpr int RQ = int(Sh::HB + 7) / 8;           // gate/up blocks per wave
+    constexpr int RK = int(Sh::QB + 7) / 8;           // QKV blocks per wave
     constexpr int RD = int(Sh::DQ * 4) / 8;           // down blocks per wave
-    auto qkv_tile = [&](uint32_t t, uint32_t& m, uint32_t& g) {
+    // QKV tile t: column group g of matrix m (q, k, v), k half c.
+    auto qkv_tile = [&](uint32_t t, uint32_t& m, uint32_t& g, uint32_t& c) {
         constexpr uint32_t qg = QD / kGrp, kg = kTkHD / kGrp;
-        m = t < qg ? 0u : (t < qg + kg ? 1u : 2u);
-        g = m == 0 ? t : (m == 1 ? t - qg : t - qg - kg);
+        const uint32_t tt = t / Sh::KQ;
+        c = t % Sh::KQ;
+        m = tt < qg ? 0u : (tt < qg + kg ? 1u : 2u);
+        g = m == 0 ? tt : (m == 1 ? tt - qg : tt - qg - kg);
     };
-    auto prefetch_qkv = [&](TkW<RQ>& p, uint32_t l, uint32_t t) {
-        uint32_t m, g;
-        qkv_tile(t, m, g);
-        tile_prefetch(p, S.lt[l].w[m], S.lt[l].s[m], Sh::HB, m == 0 ? QD : kTkHD, g, 0u, Sh::HB, wave,
-                      lane);
+    auto prefetch_qkv = [&](TkW<RK>& p, uint32_t l, uint32_t t) {
+        uint32_t m, g, c;
+        qkv_tile(t, m, g, c);
+        tile_prefetch(p, S.lt[l].w[m], S.lt[l].s[m], Sh::HB, m == 0 ? QD : kTkHD, g, c * Sh::QB, Sh::QB,
+                      wave, lane);
     };
     auto prefetch_dn = [&](TkW<RD>& p, uint32_t l, uint32_t t) {
         const uint32_t g = t / NCH, q0 = Sh::DQ * (t % NCH);
         tile_prefetch(p, S.lt[l].w[6], S.lt[l].s[6], FFN / kBlk, H, g, 4u * q0,
                       4u * min(Sh::DQ, Sh::NQF - q0), wave, lane);
     };
-    TkW<RQ> pq;
+    TkW<RK> pq;
     if (t_qkv < Sh::N_QKV) prefetch_qkv(pq, 0u, t_qkv);
 
     for (uint32_t l = 0; l < a.n_layers; ++l) {
@@ -500,8 +517,8 @@ __global__ __launch_bounds__(kTkThreads) void token_kernel(TokArgs a) {
         const uint32_t soff = l * lstride;
         // ================= QKV =================
         for (uint32_t t = t_qkv; t < Sh::N_QKV; t += nwg) {
-            uint32_t m, g;
-            qkv_tile(t, m, g);
+            uint32_t m, g, c;
+            qkv_tile(t, m, g, c);
             if (t != t_qkv) prefetch_qkv(pq, l, t);
             float w_in[kOwn] = {}, w_post[kOwn] = {}, x[kOwn] = {};
             if (hown) {
@@ -531,18 +548,23 @@ __global__ __launch_bounds__(kTkThreads) void token_kernel(TokArgs a) {
             }
             float xn[kOwn];
             own_norm<H>(xn, x, w_in, eps, RS());
-            if (hown) own_stage(S, xn);
+            {
+                // stage this tile's k half: blocks c QB .. c QB + QB - 1
+                constexpr uint32_t tpb = kBlk / kOwn;   // owner threads per block
+                const uint32_t i = tid - c * Sh::QB * tpb;
+                if (hown && i < Sh::QB * tpb) own_stage(S, xn, i);
+            }
             __syncthreads();
-            const float y = tile_dot<FMT>(pq, S, Sh::HB, wave, lane);
+            const float y = tile_dot<FMT>(pq, S, c * Sh::QB, Sh::QB, wave, lane);
             if (wave == 0) {
-                const uint32_t o = m == 0u ? 0u : (m == 1u ? QD : QD + kTkHD);
+                const uint32_t o = c * Sh::QKVD + (m == 0u ? 0u : (m == 1u ? QD : QD + kTkHD));
                 tile_put(rr, soff, uint32_t(lay.qkv) + o + g * kGrp, y, lane, tag);
             }
             // x entering the layer, for the gate/up stage: tile t < H / 64
             // stores elements 64 t .. 64 t + 63 (spread so that no workgroup
             // issues many stores). Stored last: a later wait on this wave's
             // memory counter also waits for its stores.
-            if (t < Sh::N_O && tid / (kGrp / kOwn) == t) own_put(rr, soff, uint32_t(lay.xa) + kOwn * tid, x, tag);
+            if (t < Sh::NOG && tid / (kGrp / kOwn) == t) own_put(rr, soff, uint32_t(lay.xa) + kOwn * tid, x, tag);
         }
         tk_trace(a, 1u + 6u * l);
 
@@ -585,25 +607,33 @@ __global__ __launch_bounds__(kTkThreads) void token_kernel(TokArgs a) {
                 for (int c = 0; c < 4; ++c) wqk[c] = ldgf(w + lane + 64 * c);
             }
             {
-                // raw q | k | v: pairs tid and tid + 512
+                // raw q | k | v = sum of the k halves' partials: pairs tid and
+                // tid + 512 of each half
                 constexpr uint32_t NP = Sh::QKVD / 2;
                 constexpr int NL = int((NP + kTkThreads - 1) / kTkThreads);
-                uint32_t off[NL];
-                bool act[NL];
-                u32x4 v[NL];
+                uint32_t off[NL * Sh::KQ];
+                bool act[NL * Sh::KQ];
+                u32x4 v[NL * Sh::KQ];
 #pragma unroll
-                for (int i = 0; i < NL; ++i) {
-                    const uint32_t pi = tid + uint32_t(kTkThreads) * i;
-                    act[i] = pi < NP;
-                    off[i] = (uint32_t(lay.qkv) + 2u * min(pi, NP - 1u)) * 8u;
+                for (uint32_t c = 0; c < Sh::KQ; ++c) {
+#pragma unroll
+                    for (int i = 0; i < NL; ++i) {
+                        const uint32_t pi = tid + uint32_t(kTkThreads) * i;
+                        act[c * NL + i] = pi < NP;
+                        off[c * NL + i] = (uint32_t(lay.qkv) + c * Sh::QKVD + 2u * min(pi, NP - 1u)) * 8u;
+                    }
                 }
                 ll_wait(rr, soff, off, act, v, tag, a.state);
 #pragma unroll
                 for (int i = 0; i < NL; ++i) {
                     const uint32_t pi = tid + uint32_t(kTkThreads) * i;
-                    if (act[i])
-                        *reinterpret_cast<float2*>(&S.xq[2u * pi]) =
-                            float2{__uint_as_float(v[i].x), __uint_as_float(v[i].z)};
+                    float s0 = __uint_as_float(v[i].x), s1 = __uint_as_float(v[i].z);
+#pragma unroll
+                    for (uint32_t c = 1; c < Sh::KQ; ++c) {
+                        s0 += __uint_as_float(v[c * NL + i].x);
+                        s1 += __uint_as_float(v[c * NL + i].z);
+                    }
+                    if (act[i]) *reinterpret_cast<float2*>(&S.xq[2u * pi]) = float2{s0, s1};
                 }
             }
             __syncthreads();
@@ -805,24 +835,26 @@ __global__ __launch_bounds__(kTkThreads) void token_kernel(TokArgs a) {
 
         // ================= O projection =================
         for (uint32_t t = t_o; t < Sh::N_O; t += nwg) {
-            constexpr uint32_t nb = QD / kBlk;
+            // column group g, k half c: attention output [c QD / KO, (c + 1) QD / KO)
+            const uint32_t g = t / Sh::KO, c = t % Sh::KO;
+            constexpr uint32_t nb = Sh::OB;
             TkW<(nb + 7) / 8> p;
-            tile_prefetch(p, L.w[3], L.s[3], nb, H, t, 0u, nb, wave, lane);
-            if (tid < Sh::QO) {
+            tile_prefetch(p, L.w[3], L.s[3], QD / kBlk, H, g, c * nb, nb, wave, lane);
+            if (tid < Sh::QO / Sh::KO) {
                 uint32_t off[kOwnP];
                 bool act[kOwnP];
                 u32x4 v[kOwnP];
 #pragma unroll
                 for (uint32_t j = 0; j < kOwnP; ++j) act[j] = true;
-                own_offsets(off, uint32_t(lay.atto) + kOwn * tid);
+                own_offsets(off, uint32_t(lay.atto) + c * (QD / Sh::KO) + kOwn * tid);
                 ll_wait(rr, soff, off, act, v, tag, a.state);
                 float x[kOwn];
                 own_unpack(x, v);
-                own_stage(S, x);
+                own_stage(S, x, tid);
             }
             __syncthreads();
-            const float y = tile_dot<FMT>(p, S, nb, wave, lane);
-            if (wave == 0) tile_put(rr, soff, uint32_t(lay.o) + t * kGrp, y, lane, tag);
+            const float y = tile_dot<FMT>(p, S, c * nb, nb, wave, lane);
+            if (wave == 0) tile_put(rr, soff, uint32_t(lay.o) + c * H + g * kGrp, y, lane, tag);
         }
         tk_trace(a, 4u + 6u * l);
 
@@ -838,26 +870,36 @@ __global__ __launch_bounds__(kTkThreads) void token_kernel(TokArgs a) {
             if (hown) {
                 ld_own(w_post, L.norm[1] + kOwn * tid);
                 ld_own(w_in, L.norm[2] + kOwn * tid);
-                uint32_t off[2 * kOwnP];
-                bool act[2 * kOwnP];
-                u32x4 v[2 * kOwnP];
+                constexpr uint32_t NL = (1 + Sh::KO) * kOwnP;
+                uint32_t off[NL];
+                bool act[NL];
+                u32x4 v[NL];
 #pragma unroll
-                for (uint32_t j = 0; j < 2 * kOwnP; ++j) act[j] = true;
+                for (uint32_t j = 0; j < NL; ++j) act[j] = true;
                 own_offsets(&off[0], uint32_t(lay.xa) + kOwn * tid);
-                own_offsets(&off[kOwnP], uint32_t(lay.o) + kOwn * tid);
-                ll_wait<2 * kOwnP, kGuSleep>(rr, soff, off, act, v, tag, a.state);
+#pragma unroll
+                for (uint32_t c = 0; c < Sh::KO; ++c)
+                    own_offsets(&off[kOwnP * (1 + c)], uint32_t(lay.o) + c * H + kOwn * tid);
+                ll_wait<NL, kGuSleep>(rr, soff, off, act, v, tag, a.state);
                 own_unpack(xa, &v[0]);
                 own_unpack(o, &v[kOwnP]);
+#pragma unroll
+                for (uint32_t c = 1; c < Sh::KO; ++c) {
+                    float u[kOwn];
+                    own_unpack(u, &v[kOwnP * (1 + c)]);
+#pragma unroll
+                    for (uint32_t e = 0; e < kOwn; ++e) o[e] += u[e];
+                }
             }
             float x[kOwn], xn[kOwn];
             own_residual<H>(x, xa, o, w_post, eps, RS());
             own_norm<H>(xn, x, w_in, eps, RS());
-            if (hown) own_stage(S, xn);
+            if (hown) own_stage(S, xn, tid);
             __syncthreads();
-            const float y = tile_dot<FMT>(p, S, Sh::HB, wave, lane);
+            const float y = tile_dot<FMT>(p, S, 0u, Sh::HB, wave, lane);
             if (wave == 0) tile_put(rr, soff, uint32_t(lay.gu) + (m == 4u ? 0u : FFN) + g * kGrp, y, lane, tag);
             // x after the attention block, for the next layer: spread and stored last, as xa
-            if (t < Sh::N_O && tid / (kGrp / kOwn) == t) own_put(rr, soff, uint32_t(lay.xb) + kOwn * tid, x, tag);
+            if (t < Sh::NOG && tid / (kGrp / kOwn) == t) own_put(rr, soff, uint32_t(lay.xb) + kOwn * tid, x, tag);
         }
         tk_trace(a, 5u + 6u * l);
 
@@ -882,10 +924,10 @@ __global__ __launch_bounds__(kTkThreads) void token_kernel(TokArgs a) {
                 own_unpack(up, &v[kOwnP]);
 #pragma unroll
                 for (uint32_t e = 0; e < kOwn; ++e) hx[e] = gelu_tanh(gt[e]) * up[e];
-                own_stage(S, hx);
+                own_stage(S, hx, tid);
             }
             __syncthreads();
-            const float y = tile_dot<FMT>(pdn, S, nb, wave, lane);
+            const float y = tile_dot<FMT>(pdn, S, 4u * q0, nb, wave, lane);
             if (wave == 0) tile_put(rr, soff, uint32_t(lay.dnp) + c * H + g * kGrp, y, lane, tag);
         }
         if (t_dn >= Sh::N_DN && l + 1u < a.n_layers && t_qkv < Sh::N_QKV) prefetch_qkv(pq, l + 1u, t_qkv);
@@ -929,7 +971,7 @@ __global__ __launch_bounds__(kTkThreads) void token_kernel(TokArgs a) {
         }
         after_ffn(x, a.n_layers - 1u, wf_post);
         own_norm<H>(xn, x, wf_in, eps, RS());
-        if (hown) own_stage(S, xn);
+        if (hown) own_stage(S, xn, tid);
         __syncthreads();
     }
     float bv = -INFINITY;

@@ -93,9 +93,9 @@ struct TokArgs {
     const float* freq_global;
     // Exchange slots: 8 bytes = (launch tag << 32) | fp32 bits, written with
     // one device-coherent store and read until the tag matches. Per layer
-    // (stride ll_layer): xa[hidden] | xb[hidden] | qkv[q_dim + 2 hd] |
-    // attp[grid][n_heads][2 + hd] | atto[q_dim] | o[hidden] | gu[2 ffn] |
-    // dnp[ffn/2048 chunks][hidden]; then am[2 grid] once.
+    // (stride ll_layer): xa[hidden] | xb[hidden] | qkv[split][q_dim + 2 hd] |
+    // attp[grid][n_heads][2 + hd] | atto[q_dim] | o[split][hidden] | gu[2 ffn] |
+    // dnp[down chunks][hidden]; then am[2 grid] once.
     unsigned long long* ll;
     size_t ll_layer;
     float* logits;                        // [vocab]
@@ -106,6 +106,16 @@ struct TokArgs {
     uint32_t want_logits;                 // 0: prefill pass without the lm_head
     uint32_t greedy;                      // 1: the argmax becomes the next token
 };
+
+// The token kernel's down projection is split along k into chunks of this
+// many quads (128 k each); the next layer adds the chunks' partial sums. The
+// q|k|v and o projections are split along k into this many halves likewise.
+constexpr uint32_t kTokDownQuads = 8;
+constexpr uint32_t kTokQkvSplit = 2;
+constexpr uint32_t kTokOSplit = 2;
+__host__ __device__ constexpr uint32_t tok_down_chunks(uint32_t ffn) {
+    return (ffn / 128u + kTokDownQuads - 1u) / kTokDownQuads;
+}
 
 // Exchange-slot offsets within one layer's block (in slots).
 struct TokLL {
@@ -118,12 +128,12 @@ __host__ __device__ inline TokLL tok_ll_layout(uint32_t hidden, uint32_t ffn, ui
     t.xa = 0;
     t.xb = t.xa + hidden;
     t.qkv = t.xb + hidden;
-    t.attp = t.qkv + qd + 2 * head_dim;
+    t.attp = t.qkv + kTokQkvSplit * (qd + 2 * head_dim);
     t.atto = t.attp + size_t(grid) * n_heads * (2 + head_dim);
     t.o = t.atto + qd;
-    t.gu = t.o + hidden;
+    t.gu = t.o + kTokOSplit * size_t(hidden);
     t.dnp = t.gu + 2 * size_t(ffn);
-    t.layer = t.dnp + size_t((ffn + 2047) / 2048) * hidden;
+    t.layer = t.dnp + size_t(tok_down_chunks(ffn)) * hidden;
     t.layer = (t.layer + 31) & ~size_t(31);
     return t;
 }
