@@ -181,6 +181,51 @@ int xp_argmax(uint32_t* out_idx, float* out_val, const float* logits,
 int xp_topk4_harvest(float* cval, uint32_t* cidx, const float* logits,
                      uint32_t n, uint32_t nparts, xp_stream stream);
 
+/* ---- full-vocabulary sampling chain (llm_sampling.cl:130-225, 257-281,
+ * 349-386, 399-488) ------------------------------------------------------
+ * One entry per reference kernel, same argument meaning; strided chains are
+ * e = p (mod nparts). Bit-identical to the reference's fp32 arithmetic on the
+ * same inputs except exp (device libm) in xp_softmax_exp_partial. */
+/* logits[i] *= inv_temp (apply_temperature, :130-134; T == 0 goes to argmax). */
+int xp_apply_temperature(float* logits, float inv_temp, uint32_t n, xp_stream stream);
+/* pmax[p] = max of chain p (reduce_max_partial, :156-163). */
+int xp_reduce_max_partial(float* pmax, const float* x, uint32_t n, uint32_t nparts,
+                          xp_stream stream);
+/* stats[0] = max of pmax[0..nparts) (reduce_max_final, :165-172). */
+int xp_reduce_max_final(float* stats, const float* pmax, uint32_t nparts, xp_stream stream);
+/* out[k] = exp(x[k] - stats[0]), psum[p] = chain p's sum in chain order
+ * (softmax_exp_partial, :175-191); out may alias x. */
+int xp_softmax_exp_partial(float* out, float* psum, const float* x, const float* stats,
+                           uint32_t n, uint32_t nparts, xp_stream stream);
+/* out[p] = chain p's sum (reduce_sum_partial, :202-209). */
+int xp_reduce_sum_partial(float* out, const float* in, uint32_t n, uint32_t nparts,
+                          xp_stream stream);
+/* stats[1] = serial sum of psum (reduce_sum_final, :211-218). */
+int xp_reduce_sum_final(float* stats, const float* psum, uint32_t nparts, xp_stream stream);
+/* out[i] /= stats[1] (softmax_normalize, :220-225). */
+int xp_softmax_normalize(float* out, const float* stats, uint32_t n, xp_stream stream);
+/* Chain p's best k (k <= 64), descending, strict '>', unfilled slots
+ * (-inf, 0xFFFFFFFF), at cval/cidx[p*k ..] (topk_partial, :257-281). */
+int xp_topk_partial(float* cval, uint32_t* cidx, const float* x, uint32_t n, uint32_t nparts,
+                    uint32_t k, xp_stream stream);
+/* oval/oidx[rank] for every filled candidate with rank < k, rank = number of
+ * candidates beating it by (value desc, index asc) (topk_rank_select, :349-369). */
+int xp_topk_rank_select(float* oval, uint32_t* oidx, const float* cval, const uint32_t* cidx,
+                        uint32_t ncand, uint32_t k, xp_stream stream);
+/* logits[i] = -inf where logits[i] < topk_val[k-1] (topk_mask, :380-386). */
+int xp_topk_mask(float* logits, const float* topk_val, uint32_t k, uint32_t n, xp_stream stream);
+/* Zeroes w[j] once the mass before j reaches p * total (topp_cutoff, :399-415). */
+int xp_topp_cutoff(float* w, uint32_t k, float p, xp_stream stream);
+/* CDF walk at u * total over w[0..k), ids idx; out = {id as float, weight},
+ * idx_out[0] = id (multinomial_sample, :424-446). */
+int xp_multinomial_sample(float* out, uint32_t* idx_out, const float* w, const uint32_t* idx,
+                          uint32_t k, float u, xp_stream stream);
+/* The same draw over the full vocabulary through the chain sums left by
+ * xp_softmax_exp_partial / xp_reduce_sum_final (multinomial_strided, :462-488). */
+int xp_multinomial_strided(float* out, uint32_t* idx_out, const float* w, const float* psum,
+                           const float* stats, uint32_t n, uint32_t nparts, float u,
+                           xp_stream stream);
+
 /* ---- synthetic inputs (host side, counter-based, any thread count) ------ */
 /* Philox4x32-10 (Salmon et al., SC'11): out = philox(ctr, key). */
 void xp_philox4x32_10(const uint32_t ctr[4], const uint32_t key[2], uint32_t out[4]);

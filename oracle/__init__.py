@@ -78,6 +78,15 @@ def lib() -> C.CDLL:
             "xo_argmax_reduce": (None, [F32P, U32P, F32P, U32P, u32, u32]),
             "xo_argmax_final": (None, [F32P, U32P, F32P, U32P, u32]),
             "xo_argmax_tree": (u32, [F32P, u32, C.POINTER(f32)]),
+            "xo_apply_temperature": (None, [F32P, f32, u32]),
+            "xo_reduce_max_partial": (None, [F32P, F32P, u32, u32]),
+            "xo_reduce_max_final": (None, [F32P, F32P, u32]),
+            "xo_softmax_exp_partial": (None, [F32P, F32P, F32P, F32P, u32, u32]),
+            "xo_reduce_sum_partial": (None, [F32P, F32P, u32, u32]),
+            "xo_reduce_sum_final": (None, [F32P, F32P, u32]),
+            "xo_softmax_normalize": (None, [F32P, F32P, u32]),
+            "xo_topk_mask": (None, [F32P, F32P, u32, u32]),
+            "xo_multinomial_strided": (None, [F32P, U32P, F32P, F32P, F32P, u32, u32, f32]),
             "xo_topk4_partial": (None, [F32P, U32P, F32P, u32, u32]),
             "xo_topk_partial": (None, [F32P, U32P, F32P, u32, u32, u32]),
             "xo_topk_rank_select": (None, [F32P, U32P, F32P, U32P, u32, u32]),

@@ -582,6 +582,96 @@ void xo_multinomial_sample(float* out, uint32_t* idx_out, const float* w, const 
     idx_out[0] = chosen;
 }
 
+/* ---- full-vocabulary sampling chain, llm_sampling.cl:130-206, 380-386, 455-488 ---- */
+
+/* apply_temperature, llm_sampling.cl:130-134. */
+void xo_apply_temperature(float* logits, float inv_temp, uint32_t n) {
+    for (uint32_t i = 0; i < n; ++i) logits[i] = logits[i] * inv_temp;
+}
+
+/* reduce_max_partial, llm_sampling.cl:156-163: max of strided chain p. */
+void xo_reduce_max_partial(float* pmax, const float* x, uint32_t n, uint32_t nparts) {
+    for (uint32_t p = 0; p < nparts; ++p) {
+        float m = -INFINITY;
+        for (uint32_t k = p; k < n; k += nparts) m = fmaxf(m, x[k]);
+        pmax[p] = m;
+    }
+}
+
+/* reduce_max_final, llm_sampling.cl:165-172. */
+void xo_reduce_max_final(float* stats, const float* pmax, uint32_t nparts) {
+    float m = -INFINITY;
+    for (uint32_t p = 0; p < nparts; ++p) m = fmaxf(m, pmax[p]);
+    stats[0] = m;
+}
+
+/* softmax_exp_partial, llm_sampling.cl:175-191: out[k] = exp(x[k] - max),
+ * psum[p] = chain p's sum in chain order. out may alias x. */
+void xo_softmax_exp_partial(float* out, float* psum, const float* x, const float* stats,
+                            uint32_t n, uint32_t nparts) {
+    const float m = stats[0];
+    for (uint32_t p = 0; p < nparts; ++p) {
+        float sum = 0.0f;
+        for (uint32_t k = p; k < n; k += nparts) {
+            const float e = expf(x[k] - m);
+            out[k] = e;
+            sum += e;
+        }
+        psum[p] = sum;
+    }
+}
+
+/* reduce_sum_partial, llm_sampling.cl:202-209. */
+void xo_reduce_sum_partial(float* out, const float* in, uint32_t n, uint32_t nparts) {
+    for (uint32_t p = 0; p < nparts; ++p) {
+        float sum = 0.0f;
+        for (uint32_t k = p; k < n; k += nparts) sum += in[k];
+        out[p] = sum;
+    }
+}
+
+/* reduce_sum_final, llm_sampling.cl:211-218. */
+void xo_reduce_sum_final(float* stats, const float* psum, uint32_t nparts) {
+    float sum = 0.0f;
+    for (uint32_t p = 0; p < nparts; ++p) sum += psum[p];
+    stats[1] = sum;
+}
+
+/* softmax_normalize, llm_sampling.cl:220-225. */
+void xo_softmax_normalize(float* out, const float* stats, uint32_t n) {
+    for (uint32_t i = 0; i < n; ++i) out[i] = out[i] / stats[1];
+}
+
+/* topk_mask, llm_sampling.cl:380-386: logits below topk_val[k-1] -> -inf. */
+void xo_topk_mask(float* logits, const float* topk_val, uint32_t k, uint32_t n) {
+    const float t = topk_val[k - 1u];
+    for (uint32_t i = 0; i < n; ++i)
+        if (logits[i] < t) logits[i] = -INFINITY;
+}
+
+/* multinomial_strided, llm_sampling.cl:462-488: walk the chain sums to the
+ * owning chain, then that chain's elements; a permuted CDF of w. */
+void xo_multinomial_strided(float* out, uint32_t* idx_out, const float* w, const float* psum,
+                            const float* stats, uint32_t n, uint32_t nparts, float u) {
+    const float target = u * stats[1];
+    float cum = 0.0f;
+    uint32_t chain = nparts - 1u;
+    for (uint32_t p = 0; p < nparts; ++p) {
+        const float sp = psum[p];
+        if (cum + sp > target) { chain = p; break; }
+        cum += sp;
+    }
+    uint32_t chosen = chain;
+    for (uint32_t k = chain; k < n; k += nparts) {
+        chosen = k;
+        cum += w[k];
+        if (cum > target) break;
+    }
+    out[0] = (float)chosen;
+    out[1] = w[chosen];
+    idx_out[0] = chosen;
+}
+
 /* Philox4x32-10 (Salmon et al., SC'11). */
 void xo_philox4x32_10(const uint32_t ctr[4], const uint32_t key[2], uint32_t out[4]) {
     uint32_t c0 = ctr[0], c1 = ctr[1], c2 = ctr[2], c3 = ctr[3], k0 = key[0], k1 = key[1];

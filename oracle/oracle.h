@@ -9,7 +9,8 @@
  * cites the file:line it restates. Built with -ffp-contract=off so each
  * written a*b+c rounds twice, as OpenCL C without contraction does.
  *
- * Pinning (what checks each function beyond restating it; tests/test_oracle.py):
+ * Pinning (what checks each function beyond restating it; the CPU tests in
+ * tests/test_matvec.py, test_transformer.py, test_sampling.py, test_session.py):
  *  xo_fp16_to_fp32          all 65536 patterns vs numpy float16 (exact)
  *  xo_q4dot8/32, mv_*       nibble closed form; float64 brute force; COL gold
  *                           == KM4 on the reference's nib() fixture
@@ -24,6 +25,13 @@
  *                           ties -> lowest index (sampling_test.cpp:171-178),
  *                           sort-based top-k with duplicates (:427-480)
  *  topp / multinomial       known answers of sampling_test.cpp:537-607
+ *  vocab softmax chain      numpy float64 softmax (rtol 1e-5), rows sum to 1,
+ *                           chain max/sum vs numpy over the same strides,
+ *                           max-subtraction invariance (x + c gives the same
+ *                           probabilities); temperature = exact fp32 product
+ *  topk_mask                survivors == elements >= the k-th largest (numpy)
+ *  multinomial_strided      float64 walk of the chain-permuted CDF at u away
+ *                           from boundaries; draw frequencies vs weights
  *  xo_forward               numpy re-derivation of one layer; greedy token
  *                           ids are pinned by this oracle only (parity
  *                           unpinned against the reference itself: no
@@ -110,6 +118,18 @@ void xo_multinomial_sample(float* out, uint32_t* idx_out, const float* w,
 uint32_t xo_draw(float* val, uint32_t* idx, uint32_t n, float temperature, uint32_t top_k,
                  float top_p, double u);
 /* Philox-derived uniform for sequence `seq` at step `step` (53-bit, [0,1)). */
+/* full-vocabulary sampling chain (llm_sampling.cl:130-225, 380-386, 455-488) */
+void xo_apply_temperature(float* logits, float inv_temp, uint32_t n);
+void xo_reduce_max_partial(float* pmax, const float* x, uint32_t n, uint32_t nparts);
+void xo_reduce_max_final(float* stats, const float* pmax, uint32_t nparts);
+void xo_softmax_exp_partial(float* out, float* psum, const float* x, const float* stats,
+                            uint32_t n, uint32_t nparts);
+void xo_reduce_sum_partial(float* out, const float* in, uint32_t n, uint32_t nparts);
+void xo_reduce_sum_final(float* stats, const float* psum, uint32_t nparts);
+void xo_softmax_normalize(float* out, const float* stats, uint32_t n);
+void xo_topk_mask(float* logits, const float* topk_val, uint32_t k, uint32_t n);
+void xo_multinomial_strided(float* out, uint32_t* idx_out, const float* w, const float* psum,
+                            const float* stats, uint32_t n, uint32_t nparts, float u);
 double xo_philox_uniform(uint32_t seed, uint32_t seq, uint32_t step);
 void xo_philox4x32_10(const uint32_t ctr[4], const uint32_t key[2], uint32_t out[4]);
 

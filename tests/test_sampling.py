@@ -7,10 +7,12 @@ CPU sort with a duplicated 3.25 at 1234/9999 (:424-500), top-p on
 probs ~ exp(-0.35 j) with ids 1000 + 37 j (:537-577) and the CDF walk at
 u = s/32 (:579-607).
 """
+import math
+
 import numpy as np
 import pytest
 
-from conftest import hold
+from conftest import allclose_report, hold
 
 VOCAB = 262144
 PLANTED = 190037
@@ -208,3 +210,268 @@ def test_gpu_topk4_harvest_bit_exact(xp, xo, nparts):
     xp.synchronize()
     assert np.array_equal(dv.download(np.float32).view(np.uint32), wv.view(np.uint32))
     assert np.array_equal(di.download(np.uint32), wi)
+
+
+# ------------------------------------------- full-vocabulary chain (a22) ----
+# The reference's device sampling chain (llm_sampling.cl:130-225, 257-281,
+# 349-386, 399-488). CPU: the oracle against numpy closed forms and
+# invariants. GPU: each kernel against the oracle on the same inputs —
+# bit-exact except exp (softmax_exp_partial, rtol 2e-6), with every later
+# step fed the device's own inputs so its output is compared bit for bit.
+
+def vocab_logits(seed=7, n=VOCAB):
+    r = np.random.default_rng(seed)
+    x = r.normal(0.0, 3.0, n).astype(np.float32)
+    x[1234 % n] = x[9999 % n] = 11.25  # a tie at the top
+    return x
+
+
+def chain_view(x, nparts):
+    """Element k of chain p is x[p + j * nparts]; returns a list of chains."""
+    return [x[p::nparts] for p in range(nparts)]
+
+
+def test_oracle_vocab_softmax_chain(xo):
+    L = xo.lib()
+    inv_t = np.float32(1.0 / 0.8)
+    for nparts in (256, 4096, 1):
+        x = vocab_logits(nparts)
+        t = x.copy()
+        L.xo_apply_temperature(t, inv_t, t.size)
+        assert np.array_equal(t, x * inv_t)                      # one fp32 product each
+        pmax = np.empty(nparts, np.float32)
+        L.xo_reduce_max_partial(pmax, t, t.size, nparts)
+        assert np.array_equal(pmax, np.array([c.max() for c in chain_view(t, nparts)]))
+        stats = np.zeros(2, np.float32)
+        L.xo_reduce_max_final(stats, pmax, nparts)
+        assert stats[0] == t.max()
+        e = np.empty_like(t)
+        psum = np.empty(nparts, np.float32)
+        L.xo_softmax_exp_partial(e, psum, t, stats, t.size, nparts)
+        # exp of the fp32 difference the chain forms: only expf's own rounding
+        want = np.exp((t - t.max()).astype(np.float64))
+        assert np.allclose(e, want, rtol=1e-6, atol=0)
+        # a serial fp32 sum of m terms is within (m - 1) 2^-24 sum|x| of the
+        # exact sum (Higham's bound): tight for 1024-term chains, loose for one
+        # 262144-term chain
+        for c, got in zip(chain_view(want, nparts), psum):
+            assert abs(got - math.fsum(c)) <= (c.size - 1) * 2.0 ** -24 * c.sum() + 1e-30
+        rs = np.empty(nparts, np.float32)
+        L.xo_reduce_sum_partial(rs, e, e.size, nparts)
+        assert np.array_equal(rs, psum)                          # same chains, same order
+        L.xo_reduce_sum_final(stats, psum, nparts)
+        bound = (VOCAB / nparts + nparts) * 2.0 ** -24 * want.sum()
+        assert abs(stats[1] - math.fsum(want)) <= bound
+        L.xo_softmax_normalize(e, stats, e.size)
+        rel = bound / want.sum() + 1e-6
+        assert abs(math.fsum(e.astype(np.float64)) - 1.0) < rel      # rows sum to 1
+        assert np.allclose(e, want / want.sum(), rtol=rel, atol=0)
+    # max subtraction: a constant shift leaves the probabilities unchanged
+    x = vocab_logits(3, 4096)
+    probs = []
+    for shift in (0.0, 40.0):
+        y = (x + np.float32(shift)).astype(np.float32)
+        pm, st = np.empty(64, np.float32), np.zeros(2, np.float32)
+        L.xo_reduce_max_partial(pm, y, y.size, 64)
+        L.xo_reduce_max_final(st, pm, 64)
+        e, ps = np.empty_like(y), np.empty(64, np.float32)
+        L.xo_softmax_exp_partial(e, ps, y, st, y.size, 64)
+        L.xo_reduce_sum_final(st, ps, 64)
+        L.xo_softmax_normalize(e, st, e.size)
+        probs.append(e)
+    assert np.allclose(probs[0], probs[1], rtol=1e-4, atol=1e-9)
+
+
+def test_oracle_topk_mask(xo):
+    x = vocab_logits(11)
+    for k in (1, 40, 64):
+        order = np.lexsort((np.arange(VOCAB), -x))
+        tv = x[order[:k]].astype(np.float32)
+        m = x.copy()
+        xo.lib().xo_topk_mask(m, tv, k, VOCAB)
+        keep = x >= tv[k - 1]
+        assert np.array_equal(np.isfinite(m), keep)
+        assert np.array_equal(m[keep], x[keep])
+
+
+def strided_cdf64(w, nparts):
+    """float64 CDF of w in chain order (chain 0's elements, chain 1's, ...)."""
+    order = np.concatenate([np.arange(p, w.size, nparts) for p in range(nparts)])
+    pos = np.empty(w.size, np.int64)
+    pos[order] = np.arange(w.size)
+    return np.cumsum(w[order].astype(np.float64)), pos
+
+
+def test_oracle_multinomial_strided(xo):
+    L = xo.lib()
+    n, nparts = 4096, 64
+    x = vocab_logits(5, n)
+    st, pm = np.zeros(2, np.float32), np.empty(nparts, np.float32)
+    L.xo_reduce_max_partial(pm, x, n, nparts)
+    L.xo_reduce_max_final(st, pm, nparts)
+    w, ps = np.empty_like(x), np.empty(nparts, np.float32)
+    L.xo_softmax_exp_partial(w, ps, x, st, n, nparts)
+    L.xo_reduce_sum_final(st, ps, nparts)
+    out, oi = np.empty(2, np.float32), np.empty(1, np.uint32)
+    cdf, pos = strided_cdf64(w, nparts)
+    T = cdf[-1]
+    S = 20000
+    counts = np.zeros(n)
+    for s in range(S):
+        u = np.float32((s + 0.5) / S)
+        L.xo_multinomial_strided(out, oi, w, ps, st, n, nparts, u)
+        j = int(oi[0])
+        # the chosen element's CDF step holds u * total, up to fp32 rounding
+        lo = cdf[pos[j] - 1] if pos[j] > 0 else 0.0
+        assert lo - 1e-4 * T <= float(u) * T <= cdf[pos[j]] + 1e-4 * T
+        assert out[0] == np.float32(j) and out[1] == w[j]
+        counts[j] += 1
+    # evenly spaced u: each element is drawn its weight's share of the grid
+    p = w.astype(np.float64) / T
+    assert np.all(np.abs(counts / S - p) < 2.0 / S + 2e-4)
+
+
+def test_sampling_chain_argument_errors(xh):
+    """Entry points validate before launching: no GPU needed for these."""
+    X = xh
+    with pytest.raises(X.XposeError) as e:
+        X.call("xp_topk_partial", 1, 1, 1, 16, 4, 65, None)
+    assert "k=65" in str(e.value)
+    with pytest.raises(X.XposeError):
+        X.call("xp_topk_partial", None, 1, 1, 16, 4, 8, None)
+    with pytest.raises(X.XposeError):
+        X.call("xp_apply_temperature", 1, float("inf"), 16, None)
+    with pytest.raises(X.XposeError):
+        X.call("xp_multinomial_strided", 1, 1, 1, 1, 1, 16, 32, 0.5, None)
+    with pytest.raises(X.XposeError):
+        X.call("xp_reduce_sum_final", 1, 1, 0, None)
+
+
+def dbuf(xp, a):
+    return xp.DeviceBuffer.from_array(np.ascontiguousarray(a))
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("nparts", [256, 4096])
+def test_gpu_vocab_softmax_chain(xp, xo, nparts):
+    print(f"case vocab softmax chain nparts={nparts}", flush=True)
+    L = xo.lib()
+    x = vocab_logits(nparts)
+    inv_t = np.float32(1.0 / 0.8)
+    dx = dbuf(xp, x)
+    xp.call("xp_apply_temperature", dx.vp, float(inv_t), VOCAB, None)
+    xp.synchronize()
+    t = x.copy()
+    L.xo_apply_temperature(t, inv_t, VOCAB)
+    assert np.array_equal(dx.download(np.float32), t)
+    dpm, dst = xp.DeviceBuffer(4 * nparts), dbuf(xp, np.zeros(2, np.float32))
+    xp.call("xp_reduce_max_partial", dpm.vp, dx.vp, VOCAB, nparts, None)
+    xp.call("xp_reduce_max_final", dst.vp, dpm.vp, nparts, None)
+    xp.synchronize()
+    pm, st = np.empty(nparts, np.float32), np.zeros(2, np.float32)
+    L.xo_reduce_max_partial(pm, t, VOCAB, nparts)
+    L.xo_reduce_max_final(st, pm, nparts)
+    assert np.array_equal(dpm.download(np.float32), pm)
+    assert dst.download(np.float32)[0] == st[0]
+    # exp: device libm against the host's, within 2 ulp-ish
+    de, dps = xp.DeviceBuffer(4 * VOCAB), xp.DeviceBuffer(4 * nparts)
+    xp.call("xp_softmax_exp_partial", de.vp, dps.vp, dx.vp, dst.vp, VOCAB, nparts, None)
+    xp.synchronize()
+    e, ps = np.empty_like(t), np.empty(nparts, np.float32)
+    L.xo_softmax_exp_partial(e, ps, t, st, VOCAB, nparts)
+    ge, gps = de.download(np.float32), dps.download(np.float32)
+    ok, msg = allclose_report(ge, e, 2e-6, 1e-30)
+    assert ok, msg
+    ok, msg = allclose_report(gps, ps, 1e-5, 0)
+    assert ok, msg
+    # from here on the oracle gets the device's inputs: bit-exact
+    L.xo_softmax_exp_partial(e, ps, t, st, VOCAB, nparts)
+    drs = xp.DeviceBuffer(4 * nparts)
+    xp.call("xp_reduce_sum_partial", drs.vp, de.vp, VOCAB, nparts, None)
+    xp.call("xp_reduce_sum_final", dst.vp, dps.vp, nparts, None)
+    xp.synchronize()
+    rs = np.empty(nparts, np.float32)
+    L.xo_reduce_sum_partial(rs, ge, VOCAB, nparts)
+    assert np.array_equal(drs.download(np.float32), rs)
+    assert np.array_equal(rs, gps)
+    st2 = st.copy()
+    L.xo_reduce_sum_final(st2, gps, nparts)
+    gst = dst.download(np.float32)
+    assert gst[1] == st2[1]
+    for s in range(16):
+        u = np.float32((s + 0.25) / 16)
+        do, di = xp.DeviceBuffer(8), xp.DeviceBuffer(4)
+        xp.call("xp_multinomial_strided", do.vp, di.vp, de.vp, dps.vp, dst.vp, VOCAB, nparts,
+                float(u), None)
+        xp.synchronize()
+        out, oi = np.empty(2, np.float32), np.empty(1, np.uint32)
+        L.xo_multinomial_strided(out, oi, ge, gps, gst, VOCAB, nparts, u)
+        assert int(di.download(np.uint32)[0]) == int(oi[0])
+        assert np.array_equal(do.download(np.float32), out)
+    xp.call("xp_softmax_normalize", de.vp, dst.vp, VOCAB, None)
+    xp.synchronize()
+    L.xo_softmax_normalize(ge, gst, VOCAB)
+    got = de.download(np.float32)
+    assert np.array_equal(got, ge)
+    assert abs(got.astype(np.float64).sum() - 1.0) < 1e-5
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("k,nparts", [(1, 256), (40, 256), (64, 256), (40, 4096), (64, 33)])
+def test_gpu_topk_chain_bit_exact(xp, xo, k, nparts):
+    print(f"case topk chain k={k} nparts={nparts}", flush=True)
+    L = xo.lib()
+    x = logits_with_plant()
+    x[1234] = x[9999] = 3.25
+    r = np.random.default_rng(k)
+    x[r.integers(0, VOCAB, 200)] = 2.5                     # many exact ties
+    ncand = nparts * k
+    cv, ci = np.empty(ncand, np.float32), np.empty(ncand, np.uint32)
+    L.xo_topk_partial(cv, ci, x, VOCAB, nparts, k)
+    dx = dbuf(xp, x)
+    dcv, dci = xp.DeviceBuffer(4 * ncand), xp.DeviceBuffer(4 * ncand)
+    xp.call("xp_topk_partial", dcv.vp, dci.vp, dx.vp, VOCAB, nparts, k, None)
+    xp.synchronize()
+    assert np.array_equal(dcv.download(np.float32).view(np.uint32), cv.view(np.uint32))
+    assert np.array_equal(dci.download(np.uint32), ci)
+    ov, oi = np.full(k, -7.0, np.float32), np.full(k, 7, np.uint32)
+    L.xo_topk_rank_select(ov, oi, cv, ci, ncand, k)
+    dov, doi = dbuf(xp, np.full(k, -7.0, np.float32)), dbuf(xp, np.full(k, 7, np.uint32))
+    xp.call("xp_topk_rank_select", dov.vp, doi.vp, dcv.vp, dci.vp, ncand, k, None)
+    xp.synchronize()
+    assert np.array_equal(doi.download(np.uint32), oi)
+    assert np.array_equal(dov.download(np.float32), ov)
+    assert np.array_equal(oi, np.lexsort((np.arange(VOCAB), -x))[:k])
+    xp.call("xp_topk_mask", dx.vp, dov.vp, k, VOCAB, None)
+    xp.synchronize()
+    m = x.copy()
+    L.xo_topk_mask(m, ov, k, VOCAB)
+    assert np.array_equal(dx.download(np.float32), m)
+
+
+@pytest.mark.gpu
+def test_gpu_topp_multinomial_known_answers(xp, xo):
+    """sampling_test.cpp:537-607: probs ~ exp(-0.35 j), K = 40, ids 1000 + 37 j,
+    p in {0.5, 0.9, 0.99}, u = s / 32."""
+    print("case topp/multinomial", flush=True)
+    L = xo.lib()
+    K = 40
+    probs = np.exp(-0.35 * np.arange(K, dtype=np.float32)).astype(np.float32)
+    probs = (probs / probs.astype(np.float64).sum()).astype(np.float32)
+    ids = (1000 + 37 * np.arange(K)).astype(np.uint32)
+    for p in (0.5, 0.9, 0.99):
+        w = probs.copy()
+        L.xo_topp_cutoff(w, K, np.float32(p))
+        dw = dbuf(xp, probs)
+        xp.call("xp_topp_cutoff", dw.vp, K, p, None)
+        xp.synchronize()
+        assert np.array_equal(dw.download(np.float32), w)
+        for s in range(32):
+            u = np.float32(s / 32)
+            out, oi = np.empty(2, np.float32), np.empty(1, np.uint32)
+            L.xo_multinomial_sample(out, oi, w, ids, K, u)
+            do, di = xp.DeviceBuffer(8), xp.DeviceBuffer(4)
+            xp.call("xp_multinomial_sample", do.vp, di.vp, dw.vp, hold(dbuf(xp, ids)), K, float(u), None)
+            xp.synchronize()
+            assert int(di.download(np.uint32)[0]) == int(oi[0])
+            assert np.array_equal(do.download(np.float32), out)

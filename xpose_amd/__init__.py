@@ -145,6 +145,19 @@ def _declare(lib: C.CDLL) -> None:
         "xp_kv_append_f16": (i32, [vp, vp, u32, u32, vp]),
         "xp_argmax": (i32, [vp, vp, vp, u32, vp]),
         "xp_topk4_harvest": (i32, [vp, vp, vp, u32, u32, vp]),
+        "xp_apply_temperature": (i32, [vp, f32, u32, vp]),
+        "xp_reduce_max_partial": (i32, [vp, vp, u32, u32, vp]),
+        "xp_reduce_max_final": (i32, [vp, vp, u32, vp]),
+        "xp_softmax_exp_partial": (i32, [vp, vp, vp, vp, u32, u32, vp]),
+        "xp_reduce_sum_partial": (i32, [vp, vp, u32, u32, vp]),
+        "xp_reduce_sum_final": (i32, [vp, vp, u32, vp]),
+        "xp_softmax_normalize": (i32, [vp, vp, u32, vp]),
+        "xp_topk_partial": (i32, [vp, vp, vp, u32, u32, u32, vp]),
+        "xp_topk_rank_select": (i32, [vp, vp, vp, vp, u32, u32, vp]),
+        "xp_topk_mask": (i32, [vp, vp, u32, u32, vp]),
+        "xp_topp_cutoff": (i32, [vp, u32, f32, vp]),
+        "xp_multinomial_sample": (i32, [vp, vp, vp, vp, u32, f32, vp]),
+        "xp_multinomial_strided": (i32, [vp, vp, vp, vp, vp, u32, u32, f32, vp]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(lib, name)

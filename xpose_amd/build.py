@@ -31,7 +31,7 @@ HIP_FLAGS = [
 ]
 
 LIB_SOURCES = ["runtime.cpp", "synth.cpp", "matvec.hip", "transformer.hip", "sampling.hip",
-               "token_kernel.hip", "probe.hip",
+               "sampling_chain.hip", "token_kernel.hip", "probe.hip",
                "session_kernels.hip", "session.cpp"]
 
 

@@ -1,0 +1,369 @@
+// The full-vocabulary sampling chain (kernels/llm_sampling.cl:130-225,
+// 257-281, 349-386, 399-488): temperature, the strided-chain max / exp-sum
+// softmax, per-chain top-k with rank selection, the top-k mask, top-p and the
+// two multinomial draws. In the reference these are verified building blocks
+// that decode does not call; here each is one gfx950 kernel behind an
+// xp_<name> entry point with the reference's argument meaning.
+//
+// Every kernel evaluates what the reference evaluates in the same order:
+// chain p is walked k = p, p + nparts, ... by one thread (consecutive threads
+// take consecutive chains, so each step of the walk is one coalesced load
+// across the wave), and the serial finalisers stay serial. Sums, comparisons,
+// the division and the cumulative walks are therefore bit-identical to the
+// reference's fp32 arithmetic on the same inputs; only exp (the device libm
+// against llvmpipe's) can differ in the last bits.
+//
+// Where the reference's one-thread-per-chain form would hold a 64-entry array
+// per thread (topk_partial), the array lives in LDS, column-major across the
+// workgroup's threads so that a step of the insertion touches 64 different
+// banks. rank selection stages the candidate list through LDS in tiles.
+#include "xp_device.hpp"
+#include "xp_launch.hpp"
+
+namespace xp {
+
+namespace {
+
+constexpr uint32_t kScThreads = 256;
+constexpr uint32_t kTopkMax = 64;          // XP_TOPK_MAX, llm_sampling.cl:255
+constexpr uint32_t kTopkThreads = 64;      // one wave: 64 x 64 x 8 B = 32 KiB of LDS
+constexpr uint32_t kRankTile = 2048;       // candidates staged per LDS tile
+constexpr uint32_t kNone = 0xFFFFFFFFu;    // unfilled candidate slot
+
+uint32_t blocks(uint32_t n, uint32_t per) { return (n + per - 1) / per; }
+
+}  // namespace
+
+__global__ __launch_bounds__(kScThreads) void temperature_kernel(float* x, float inv_temp, uint32_t n) {
+    const uint32_t i = blockIdx.x * kScThreads + threadIdx.x;
+    if (i < n) x[i] = x[i] * inv_temp;
+}
+
+__global__ __launch_bounds__(kScThreads) void reduce_max_partial_kernel(float* pmax, const float* x,
+                                                                        uint32_t n, uint32_t nparts) {
+    const uint32_t p = blockIdx.x * kScThreads + threadIdx.x;
+    if (p >= nparts) return;
+    float m = -INFINITY;
+    for (uint32_t k = p; k < n; k += nparts) m = fmaxf(m, x[k]);
+    pmax[p] = m;
+}
+
+// The maximum is the same in any order (fmax drops NaNs either way), so the
+// finaliser is a parallel reduction.
+__global__ __launch_bounds__(1024) void reduce_max_final_kernel(float* stats, const float* pmax,
+                                                                uint32_t nparts) {
+    __shared__ float wm[1024 / kWave];
+    float m = -INFINITY;
+    for (uint32_t p = threadIdx.x; p < nparts; p += 1024) m = fmaxf(m, pmax[p]);
+    m = wave_max(m);
+    if (threadIdx.x % kWave == 0) wm[threadIdx.x / kWave] = m;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        for (int w = 1; w < 1024 / kWave; ++w) m = fmaxf(m, wm[w]);
+        stats[0] = m;
+    }
+}
+
+__global__ __launch_bounds__(kScThreads) void softmax_exp_partial_kernel(float* out, float* psum,
+                                                                         const float* x,
+                                                                         const float* stats,
+                                                                         uint32_t n, uint32_t nparts) {
+    const uint32_t p = blockIdx.x * kScThreads + threadIdx.x;
+    if (p >= nparts) return;
+    const float m = stats[0];
+    float s = 0.0f;
+    for (uint32_t k = p; k < n; k += nparts) {
+        const float e = expf(x[k] - m);
+        out[k] = e;
+        s += e;
+    }
+    psum[p] = s;
+}
+
+__global__ __launch_bounds__(kScThreads) void reduce_sum_partial_kernel(float* out, const float* in,
+                                                                        uint32_t n, uint32_t nparts) {
+    const uint32_t p = blockIdx.x * kScThreads + threadIdx.x;
+    if (p >= nparts) return;
+    float s = 0.0f;
+    for (uint32_t k = p; k < n; k += nparts) s += in[k];
+    out[p] = s;
+}
+
+// Serial, as the reference: the fp32 sum depends on its order. The loads are
+// issued 16 ahead; the adds stay in order.
+__global__ void reduce_sum_final_kernel(float* stats, const float* psum, uint32_t nparts) {
+    if (threadIdx.x != 0) return;
+    float s = 0.0f;
+    uint32_t p = 0;
+    for (; p + 16 <= nparts; p += 16) {
+        float v[16];
+#pragma unroll
+        for (int i = 0; i < 16; ++i) v[i] = psum[p + i];
+#pragma unroll
+        for (int i = 0; i < 16; ++i) s += v[i];
+    }
+    for (; p < nparts; ++p) s += psum[p];
+    stats[1] = s;
+}
+
+__global__ __launch_bounds__(kScThreads) void softmax_normalize_kernel(float* out, const float* stats,
+                                                                       uint32_t n) {
+    const uint32_t i = blockIdx.x * kScThreads + threadIdx.x;
+    if (i < n) out[i] = out[i] / stats[1];
+}
+
+// Chain p's best k (descending, strict '>' so the earliest index wins a tie),
+// unfilled slots (-inf, none). bv / bi are [slot][thread] in LDS.
+__global__ __launch_bounds__(kTopkThreads) void topk_partial_kernel(float* cval, uint32_t* cidx,
+                                                                    const float* x, uint32_t n,
+                                                                    uint32_t nparts, uint32_t k) {
+    __shared__ float bv[kTopkMax][kTopkThreads];
+    __shared__ uint32_t bi[kTopkMax][kTopkThreads];
+    const uint32_t t = threadIdx.x;
+    const uint32_t p = blockIdx.x * kTopkThreads + t;
+    for (uint32_t j = 0; j < k; ++j) { bv[j][t] = -INFINITY; bi[j][t] = kNone; }
+    if (p >= nparts) return;
+    float thr = -INFINITY;                       // bv[k - 1][t]
+    for (uint32_t e = p; e < n; e += nparts) {
+        const float v = x[e];
+        if (!(v > thr)) continue;
+        uint32_t j = k - 1u;
+        while (j > 0u && v > bv[j - 1u][t]) {
+            bv[j][t] = bv[j - 1u][t];
+            bi[j][t] = bi[j - 1u][t];
+            --j;
+        }
+        bv[j][t] = v;
+        bi[j][t] = e;
+        thr = bv[k - 1u][t];
+    }
+    for (uint32_t j = 0; j < k; ++j) {
+        cval[size_t(p) * k + j] = bv[j][t];
+        cidx[size_t(p) * k + j] = bi[j][t];
+    }
+}
+
+// Candidate i's rank = number of filled candidates beating it by (value
+// desc, index asc); rank < k writes out[rank]. Candidates pass through LDS in
+// tiles that every thread of the workgroup scans.
+__global__ __launch_bounds__(kScThreads) void topk_rank_select_kernel(float* oval, uint32_t* oidx,
+                                                                      const float* cval,
+                                                                      const uint32_t* cidx,
+                                                                      uint32_t ncand, uint32_t k) {
+    __shared__ float tv[kRankTile];
+    __shared__ uint32_t ti[kRankTile];
+    const uint32_t i = blockIdx.x * kScThreads + threadIdx.x;
+    const bool mine = i < ncand;
+    const float v = mine ? cval[i] : -INFINITY;
+    const uint32_t d = mine ? cidx[i] : kNone;
+    uint32_t rank = 0;
+    for (uint32_t base = 0; base < ncand; base += kRankTile) {
+        const uint32_t m = min(kRankTile, ncand - base);
+        __syncthreads();
+        for (uint32_t j = threadIdx.x; j < m; j += kScThreads) {
+            tv[j] = cval[base + j];
+            ti[j] = cidx[base + j];
+        }
+        __syncthreads();
+        for (uint32_t j = 0; j < m; ++j) {
+            const float w = tv[j];
+            const uint32_t e = ti[j];
+            rank += (e != kNone) & ((w > v) | ((w == v) & (e < d)));
+        }
+    }
+    if (mine && d != kNone && rank < k) {
+        oval[rank] = v;
+        oidx[rank] = d;
+    }
+}
+
+__global__ __launch_bounds__(kScThreads) void topk_mask_kernel(float* logits, const float* topk_val,
+                                                               uint32_t k, uint32_t n) {
+    const uint32_t i = blockIdx.x * kScThreads + threadIdx.x;
+    if (i >= n) return;
+    const float t = topk_val[k - 1u];
+    if (logits[i] < t) logits[i] = -INFINITY;
+}
+
+// One thread, serial over k (the reference's top-p is a single work-item).
+__global__ void topp_cutoff_kernel(float* w, uint32_t k, float p) {
+    if (threadIdx.x != 0) return;
+    float total = 0.0f;
+    for (uint32_t j = 0; j < k; ++j) total += w[j];
+    if (!(total > 0.0f)) return;
+    float cum = 0.0f;
+    for (uint32_t j = 0; j < k; ++j) {
+        if (cum >= p * total) w[j] = 0.0f;
+        else cum += w[j];
+    }
+}
+
+__global__ void multinomial_sample_kernel(float* out, uint32_t* idx_out, const float* w,
+                                          const uint32_t* idx, uint32_t k, float u) {
+    if (threadIdx.x != 0) return;
+    float total = 0.0f;
+    for (uint32_t j = 0; j < k; ++j) total += w[j];
+    const float target = u * total;
+    float cum = 0.0f;
+    uint32_t chosen = 0u;
+    float cw = 0.0f;
+    for (uint32_t j = 0; j < k; ++j) {
+        cum += w[j];
+        if (w[j] > 0.0f) { chosen = idx[j]; cw = w[j]; }
+        if (cum > target) break;
+    }
+    out[0] = float(chosen);
+    out[1] = cw;
+    idx_out[0] = chosen;
+}
+
+__global__ void multinomial_strided_kernel(float* out, uint32_t* idx_out, const float* w,
+                                           const float* psum, const float* stats, uint32_t n,
+                                           uint32_t nparts, float u) {
+    if (threadIdx.x != 0) return;
+    const float target = u * stats[1];
+    float cum = 0.0f;
+    uint32_t chain = nparts - 1u;
+    for (uint32_t p = 0; p < nparts; ++p) {
+        const float s = psum[p];
+        if (cum + s > target) { chain = p; break; }
+        cum += s;
+    }
+    uint32_t chosen = chain;
+    for (uint32_t e = chain; e < n; e += nparts) {
+        chosen = e;
+        cum += w[e];
+        if (cum > target) break;
+    }
+    out[0] = float(chosen);
+    out[1] = w[chosen];
+    idx_out[0] = chosen;
+}
+
+}  // namespace xp
+
+using namespace xp;
+
+#define XP_SC_LAUNCH(name) \
+    do { \
+        hipError_t e_ = hipGetLastError(); \
+        if (e_ != hipSuccess) return set_error(XP_E_HIP, name ": launch -> %s", hipGetErrorString(e_)); \
+        return XP_OK; \
+    } while (0)
+
+extern "C" {
+
+int xp_apply_temperature(float* logits, float inv_temp, uint32_t n, xp_stream stream) {
+    XP_REQUIRE(logits, "null pointer");
+    XP_REQUIRE(n > 0, "n must be positive");
+    XP_REQUIRE(std::isfinite(inv_temp), "inv_temp must be finite (route T == 0 to argmax)");
+    hipLaunchKernelGGL(temperature_kernel, dim3(blocks(n, kScThreads)), dim3(kScThreads), 0,
+                       as_stream(stream), logits, inv_temp, n);
+    XP_SC_LAUNCH("xp_apply_temperature");
+}
+
+int xp_reduce_max_partial(float* pmax, const float* x, uint32_t n, uint32_t nparts,
+                          xp_stream stream) {
+    XP_REQUIRE(pmax && x, "null pointer");
+    XP_REQUIRE(n > 0 && nparts > 0, "n and nparts must be positive");
+    hipLaunchKernelGGL(reduce_max_partial_kernel, dim3(blocks(nparts, kScThreads)), dim3(kScThreads),
+                       0, as_stream(stream), pmax, x, n, nparts);
+    XP_SC_LAUNCH("xp_reduce_max_partial");
+}
+
+int xp_reduce_max_final(float* stats, const float* pmax, uint32_t nparts, xp_stream stream) {
+    XP_REQUIRE(stats && pmax, "null pointer");
+    XP_REQUIRE(nparts > 0, "nparts must be positive");
+    hipLaunchKernelGGL(reduce_max_final_kernel, dim3(1), dim3(1024), 0, as_stream(stream), stats,
+                       pmax, nparts);
+    XP_SC_LAUNCH("xp_reduce_max_final");
+}
+
+int xp_softmax_exp_partial(float* out, float* psum, const float* x, const float* stats, uint32_t n,
+                           uint32_t nparts, xp_stream stream) {
+    XP_REQUIRE(out && psum && x && stats, "null pointer");
+    XP_REQUIRE(n > 0 && nparts > 0, "n and nparts must be positive");
+    hipLaunchKernelGGL(softmax_exp_partial_kernel, dim3(blocks(nparts, kScThreads)), dim3(kScThreads),
+                       0, as_stream(stream), out, psum, x, stats, n, nparts);
+    XP_SC_LAUNCH("xp_softmax_exp_partial");
+}
+
+int xp_reduce_sum_partial(float* out, const float* in, uint32_t n, uint32_t nparts,
+                          xp_stream stream) {
+    XP_REQUIRE(out && in, "null pointer");
+    XP_REQUIRE(n > 0 && nparts > 0, "n and nparts must be positive");
+    hipLaunchKernelGGL(reduce_sum_partial_kernel, dim3(blocks(nparts, kScThreads)), dim3(kScThreads),
+                       0, as_stream(stream), out, in, n, nparts);
+    XP_SC_LAUNCH("xp_reduce_sum_partial");
+}
+
+int xp_reduce_sum_final(float* stats, const float* psum, uint32_t nparts, xp_stream stream) {
+    XP_REQUIRE(stats && psum, "null pointer");
+    XP_REQUIRE(nparts > 0, "nparts must be positive");
+    hipLaunchKernelGGL(reduce_sum_final_kernel, dim3(1), dim3(64), 0, as_stream(stream), stats, psum,
+                       nparts);
+    XP_SC_LAUNCH("xp_reduce_sum_final");
+}
+
+int xp_softmax_normalize(float* out, const float* stats, uint32_t n, xp_stream stream) {
+    XP_REQUIRE(out && stats, "null pointer");
+    XP_REQUIRE(n > 0, "n must be positive");
+    hipLaunchKernelGGL(softmax_normalize_kernel, dim3(blocks(n, kScThreads)), dim3(kScThreads), 0,
+                       as_stream(stream), out, stats, n);
+    XP_SC_LAUNCH("xp_softmax_normalize");
+}
+
+int xp_topk_partial(float* cval, uint32_t* cidx, const float* x, uint32_t n, uint32_t nparts,
+                    uint32_t k, xp_stream stream) {
+    XP_REQUIRE(cval && cidx && x, "null pointer");
+    XP_REQUIRE(n > 0 && nparts > 0, "n and nparts must be positive");
+    XP_REQUIRE(k >= 1 && k <= kTopkMax, "k=%u must be in [1, %u]", k, kTopkMax);
+    hipLaunchKernelGGL(topk_partial_kernel, dim3(blocks(nparts, kTopkThreads)), dim3(kTopkThreads), 0,
+                       as_stream(stream), cval, cidx, x, n, nparts, k);
+    XP_SC_LAUNCH("xp_topk_partial");
+}
+
+int xp_topk_rank_select(float* oval, uint32_t* oidx, const float* cval, const uint32_t* cidx,
+                        uint32_t ncand, uint32_t k, xp_stream stream) {
+    XP_REQUIRE(oval && oidx && cval && cidx, "null pointer");
+    XP_REQUIRE(ncand > 0 && k > 0, "ncand and k must be positive");
+    hipLaunchKernelGGL(topk_rank_select_kernel, dim3(blocks(ncand, kScThreads)), dim3(kScThreads), 0,
+                       as_stream(stream), oval, oidx, cval, cidx, ncand, k);
+    XP_SC_LAUNCH("xp_topk_rank_select");
+}
+
+int xp_topk_mask(float* logits, const float* topk_val, uint32_t k, uint32_t n, xp_stream stream) {
+    XP_REQUIRE(logits && topk_val, "null pointer");
+    XP_REQUIRE(n > 0 && k > 0, "n and k must be positive");
+    hipLaunchKernelGGL(topk_mask_kernel, dim3(blocks(n, kScThreads)), dim3(kScThreads), 0,
+                       as_stream(stream), logits, topk_val, k, n);
+    XP_SC_LAUNCH("xp_topk_mask");
+}
+
+int xp_topp_cutoff(float* w, uint32_t k, float p, xp_stream stream) {
+    XP_REQUIRE(w, "null pointer");
+    XP_REQUIRE(k > 0, "k must be positive");
+    hipLaunchKernelGGL(topp_cutoff_kernel, dim3(1), dim3(64), 0, as_stream(stream), w, k, p);
+    XP_SC_LAUNCH("xp_topp_cutoff");
+}
+
+int xp_multinomial_sample(float* out, uint32_t* idx_out, const float* w, const uint32_t* idx,
+                          uint32_t k, float u, xp_stream stream) {
+    XP_REQUIRE(out && idx_out && w && idx, "null pointer");
+    XP_REQUIRE(k > 0, "k must be positive");
+    hipLaunchKernelGGL(multinomial_sample_kernel, dim3(1), dim3(64), 0, as_stream(stream), out, idx_out,
+                       w, idx, k, u);
+    XP_SC_LAUNCH("xp_multinomial_sample");
+}
+
+int xp_multinomial_strided(float* out, uint32_t* idx_out, const float* w, const float* psum,
+                           const float* stats, uint32_t n, uint32_t nparts, float u,
+                           xp_stream stream) {
+    XP_REQUIRE(out && idx_out && w && psum && stats, "null pointer");
+    XP_REQUIRE(n > 0 && nparts > 0 && nparts <= n, "need 0 < nparts <= n");
+    hipLaunchKernelGGL(multinomial_strided_kernel, dim3(1), dim3(64), 0, as_stream(stream), out,
+                       idx_out, w, psum, stats, n, nparts, u);
+    XP_SC_LAUNCH("xp_multinomial_strided");
+}
+
+}  // extern "C"
