@@ -357,6 +357,38 @@ int  xp_session_trace(xp_session* s, int enable);
 int  xp_session_last_trace(xp_session* s, uint64_t* host, size_t n, uint32_t* grid);
 /* Host draw over (value, index) candidates, in place (decode.cpp:1873-1917),
  * with u in [0,1) standing in for the reference's mt19937_64 draw. */
+/* ---- batched decode (up to 16 sequences per step) -------------------------
+ * n_seq independent sequences decoded together on the weights of `weights`
+ * (shared, not copied: the session must outlive the batch). Each sequence has
+ * its own fp16 KV cache of max_seq positions, its position and its draw
+ * counter; sequence i draws with Philox(key = (seed, seq_id + i), counter =
+ * its step) using the session's temperature / top_k (<= 64) / top_p (greedy
+ * when sample_mode is 0), over the reference's harvest (best 4 of 4096
+ * strided chains) reduced to its exact best 64 on the device. The matvecs
+ * are M = 16 MFMA GEMMs (int4 widened to bf16 in registers, fp32 activations
+ * as two bf16 terms). No reference counterpart: the reference decodes one
+ * sequence per DecodeSession (decode.hpp:605-676). */
+typedef struct xp_batch xp_batch;
+int xp_batch_create(const xp_session* weights, uint32_t n_seq, uint32_t max_seq, xp_batch** out);
+int xp_batch_destroy(xp_batch* b);
+int xp_batch_kv_upload(xp_batch* b, uint32_t seq, int layer, int which, uint32_t start,
+                       uint32_t count, const uint16_t* src);
+int xp_batch_kv_download(xp_batch* b, uint32_t seq, int layer, int which, uint32_t start,
+                         uint32_t count, uint16_t* dst);
+int xp_batch_set_positions(xp_batch* b, const uint32_t* pos);
+int xp_batch_positions(xp_batch* b, uint32_t* pos);
+/* Runs the network on tokens[n_seq] at the current positions (their K / V
+ * appended there), advances every position, keeps the logits and candidates. */
+int xp_batch_forward(xp_batch* b, const uint32_t* tokens);
+/* Sample-first step for every sequence (decode.cpp:1830-1850): draws
+ * tokens_out from the last logits, then runs xp_batch_forward on them. */
+int xp_batch_decode_step(xp_batch* b, uint32_t* tokens_out);
+int xp_batch_last_logits(xp_batch* b, uint32_t seq, float* out, uint32_t n);
+/* The best n <= 64 candidates of sequence seq, (value desc, index asc). */
+int xp_batch_last_candidates(xp_batch* b, uint32_t seq, float* val, uint32_t* idx, uint32_t n);
+/* Device time of the last forward (HIP events around the graph). */
+int xp_batch_last_ms(xp_batch* b, float* ms);
+
 uint32_t xp_draw(float* val, uint32_t* idx, uint32_t n, float temperature, uint32_t top_k,
                  float top_p, double u);
 double xp_philox_uniform(uint32_t seed, uint32_t seq, uint32_t step);

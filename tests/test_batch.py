@@ -1,0 +1,181 @@
+"""Batched decode (xp_batch_*): up to 16 sequences per step on one session's
+weights, the matvecs as M = 16 MFMA GEMMs.
+
+Every sequence is checked against the oracle run alone on the same packed
+weights, its own KV cache and its own token ids: logits within 1e-3 relative
+(|d| <= 1e-3 max|logits|), the appended K/V rows likewise (|d| <= 1e-3 max|row|;
+the activations enter the GEMM as two bf16 terms, 2^-18 relative), the
+device's 64 best candidates equal to the reference harvest (best 4 of 4096
+strided chains, llm_sampling.cl:318-347) of the same logits reduced to its
+64 best, bit for bit, and the drawn tokens equal to the host draw
+(decode.cpp:1873-1917) over that harvest with Philox(seed, seq_id + i, step).
+"""
+import numpy as np
+import pytest
+
+from test_session import all_tensors, logits_close
+
+HARVEST = 4096
+
+
+def build(X, xo, cfg, seed=0x5EED0005):
+    t = all_tensors(X, cfg, seed)
+    sess = X.DecodeSession(cfg)
+    for (l, k), a in t.items():
+        sess.upload(l, k, a)
+    return sess, t
+
+
+def harvest_best(xo, logits, k=64):
+    """The reference harvest of `logits`, then its k best by (value desc, index asc)."""
+    n = logits.size
+    cv = np.empty(4 * HARVEST, np.float32)
+    ci = np.empty(4 * HARVEST, np.uint32)
+    xo.lib().xo_topk4_partial(cv, ci, logits, n, HARVEST)
+    keep = ci != 0xFFFFFFFF
+    cv, ci = cv[keep], ci[keep]
+    order = np.lexsort((ci, -cv))[:k]
+    return cv, ci, cv[order], ci[order]
+
+
+# ---------------------------------------------------------------- CPU ----
+
+def test_batch_argument_errors(xh):
+    X = xh
+    with pytest.raises(X.XposeError):
+        X.call("xp_batch_create", None, 4, 128, None)
+
+
+# ---------------------------------------------------------------- GPU ----
+
+@pytest.mark.gpu
+def test_gpu_batch_matches_oracle_per_sequence(xp, xo):
+    """Five sequences at different depths (two past the 512-position window of
+    the local layers), greedy, three steps; the oracle runs each sequence
+    alone."""
+    X = xp
+    print("case batch vs oracle", flush=True)
+    cfg = X.XpConfig.gemma3_1b(n_layers=6, vocab=32768, max_seq=1024)
+    sess, t = build(X, xo, cfg)
+    kvd = cfg.n_kv_heads * cfg.head_dim
+    depths = [3, 130, 511, 600, 1000]
+    B = len(depths)
+    batch = X.DecodeBatch(sess, B, cfg.max_seq)
+    models = []
+    for i, d in enumerate(depths):
+        m = xo.OracleModel(cfg, lambda l, k: t[(l, k)])
+        for l in range(cfg.n_layers):
+            k = X.synth_normal_f16(d * kvd, 1000 + i, 2 * l)
+            v = X.synth_normal_f16(d * kvd, 1000 + i, 2 * l + 1)
+            batch.kv_upload(i, l, 0, 0, k)
+            batch.kv_upload(i, l, 1, 0, v)
+            m.kcache[l][:d * kvd] = k
+            m.vcache[l][:d * kvd] = v
+        models.append(m)
+    batch.set_positions(depths)
+    toks = np.array([7, 31000, 4242, 17, 9999], np.uint32)
+    pos = np.array(depths)
+    batch.forward(toks)
+    for step in range(3):
+        assert np.array_equal(batch.positions(), pos + 1)
+        nxt = np.empty(B, np.uint32)
+        for i in range(B):
+            want = models[i].forward(int(toks[i]), int(pos[i]), True)
+            got = batch.last_logits(i)
+            ok, msg = logits_close(got, want)
+            assert ok, f"step {step} seq {i} depth {pos[i]}: {msg}"
+            for which, ref in ((0, models[i].kcache), (1, models[i].vcache)):
+                row = batch.kv_download(i, 0, which, int(pos[i]), 1).view(np.float16)
+                want_row = ref[0][pos[i] * kvd:(pos[i] + 1) * kvd].view(np.float16)
+                err = np.abs(row.astype(np.float64) - want_row.astype(np.float64)).max()
+                assert err <= 1e-3 * np.abs(want_row.astype(np.float64)).max(), (step, i, which, err)
+            _, _, bv, bi = harvest_best(xo, got)
+            gv, gi = batch.last_candidates(i)
+            assert np.array_equal(gi, bi), (step, i)
+            assert np.array_equal(gv.view(np.uint32), bv.view(np.uint32)), (step, i)
+            nxt[i] = gi[0]
+        # greedy: the drawn token is the best candidate; decode_step then
+        # runs the network on it at the next position
+        assert np.array_equal(batch.decode_step(), nxt)
+        toks, pos = nxt, pos + 1
+    batch.close()
+    sess.close()
+
+
+@pytest.mark.gpu
+def test_gpu_batch_sampling_draws(xp, xo):
+    """Temperature 0.8 / top-k 64 / top-p 0.95 per sequence, Philox key
+    (seed, seq_id + i): the drawn tokens equal the host draw over the
+    reference harvest of each sequence's device logits."""
+    X = xp
+    print("case batch sampling", flush=True)
+    cfg = X.XpConfig.gemma3_1b(n_layers=2, vocab=65536, max_seq=512, sample_mode=1,
+                               temperature=0.8, top_k=64, top_p=0.95, seed=1234, seq_id=40)
+    sess, t = build(X, xo, cfg)
+    B = 16
+    batch = X.DecodeBatch(sess, B, cfg.max_seq)
+    r = np.random.default_rng(5)
+    batch.set_positions(r.integers(0, 300, B))
+    batch.forward(r.integers(0, cfg.vocab, B))
+    for step in range(6):
+        want = np.empty(B, np.uint32)
+        for i in range(B):
+            cv, ci, _, _ = harvest_best(xo, batch.last_logits(i))
+            u = xo.lib().xo_philox_uniform(1234, 40 + i, step)
+            want[i] = xo.lib().xo_draw(cv.copy(), ci.copy(), cv.size, 0.8, 64, 0.95, u)
+        got = batch.decode_step()
+        assert np.array_equal(got, want), step
+    batch.close()
+    sess.close()
+
+
+@pytest.mark.gpu
+def test_gpu_batch_one_sequence_equals_session(xp, xo):
+    """A batch of one sequence and the single-sequence session (persistent
+    token kernel) on the same weights and KV give the same logits to the
+    end-to-end bar."""
+    X = xp
+    print("case batch of one vs session", flush=True)
+    cfg = X.XpConfig.gemma3_1b(n_layers=4, vocab=32768, max_seq=1024)
+    sess, t = build(X, xo, cfg)
+    kvd = cfg.n_kv_heads * cfg.head_dim
+    batch = X.DecodeBatch(sess, 1, cfg.max_seq)
+    for l in range(cfg.n_layers):
+        for which in (0, 1):
+            rows = X.synth_normal_f16(700 * kvd, 3, 2 * l + which)
+            sess.kv_upload(l, which, 0, rows)
+            batch.kv_upload(0, l, which, 0, rows)
+    sess.set_position(700)
+    batch.set_positions([700])
+    sess.prefill([555])
+    batch.forward([555])
+    ok, msg = logits_close(batch.last_logits(0), sess.last_logits())
+    assert ok, msg
+    batch.close()
+    sess.close()
+
+
+@pytest.mark.gpu
+def test_gpu_batch_error_paths(xp, xo):
+    X = xp
+    print("case batch errors", flush=True)
+    cfg = X.XpConfig.gemma3_1b(n_layers=1, vocab=16384, max_seq=256)
+    sess, _ = build(X, xo, cfg)
+    for n in (0, 17):
+        with pytest.raises(X.XposeError):
+            X.DecodeBatch(sess, n, 256)
+    with pytest.raises(X.XposeError):
+        X.DecodeBatch(sess, 2, 9000)
+    b = X.DecodeBatch(sess, 2, 256)
+    with pytest.raises(X.XposeError):
+        b.set_positions([0, 256])
+    with pytest.raises(X.XposeError):
+        b.decode_step()                       # no logits yet
+    b.set_positions([254, 255])
+    b.forward([1, 2])
+    with pytest.raises(X.XposeError):
+        b.forward([1, 2])                     # sequence 1 is at max_seq
+    with pytest.raises(X.XposeError):
+        b.forward([1, 99999])                 # token >= vocab
+    b.close()
+    sess.close()

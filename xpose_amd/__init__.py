@@ -110,6 +110,17 @@ def _declare(lib: C.CDLL) -> None:
         "xp_config_gemma3_1b": (None, [P(XpConfig)]),
         "xp_session_create": (i32, [P(XpConfig), P(vp)]),
         "xp_session_destroy": (i32, [vp]),
+        "xp_batch_create": (i32, [vp, u32, u32, P(vp)]),
+        "xp_batch_destroy": (i32, [vp]),
+        "xp_batch_kv_upload": (i32, [vp, u32, i32, i32, u32, u32, vp]),
+        "xp_batch_kv_download": (i32, [vp, u32, i32, i32, u32, u32, vp]),
+        "xp_batch_set_positions": (i32, [vp, vp]),
+        "xp_batch_positions": (i32, [vp, vp]),
+        "xp_batch_forward": (i32, [vp, vp]),
+        "xp_batch_decode_step": (i32, [vp, vp]),
+        "xp_batch_last_logits": (i32, [vp, u32, vp, u32]),
+        "xp_batch_last_candidates": (i32, [vp, u32, vp, vp, u32]),
+        "xp_batch_last_ms": (i32, [vp, P(f32)]),
         "xp_tensor_bytes": (i32, [P(XpConfig), i32, i32, P(sz)]),
         "xp_session_upload": (i32, [vp, i32, i32, vp, sz]),
         "xp_synth_tensor": (i32, [P(XpConfig), u32, i32, i32, vp, sz]),
@@ -327,6 +338,77 @@ def synth_tensor(cfg: XpConfig, seed: int, layer: int, tensor: int) -> np.ndarra
     out = np.empty(nb // np.dtype(dt).itemsize, dtype=dt)
     call("xp_synth_tensor", C.byref(cfg), seed, layer, tensor, out.ctypes.data, nb)
     return out
+
+
+class DecodeBatch:
+    """Up to 16 sequences decoded together on a DecodeSession's weights
+    (xp_batch_*). The session must stay open while the batch lives."""
+
+    def __init__(self, sess: "DecodeSession", n_seq: int, max_seq: int):
+        self.sess = sess
+        self.n = n_seq
+        self.max_seq = max_seq
+        h = C.c_void_p()
+        call("xp_batch_create", sess.h, n_seq, max_seq, C.byref(h))
+        self.h = h
+
+    def close(self) -> None:
+        if self.h and self.h.value and _lib is not None:
+            _lib.xp_batch_destroy(self.h)
+        self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def kv_upload(self, seq: int, layer: int, which: int, pos0: int, rows: np.ndarray) -> None:
+        rows = np.ascontiguousarray(rows, np.uint16)
+        kvd = self.sess.cfg.n_kv_heads * self.sess.cfg.head_dim
+        call("xp_batch_kv_upload", self.h, seq, layer, which, pos0, rows.size // kvd, rows.ctypes.data)
+
+    def kv_download(self, seq: int, layer: int, which: int, pos0: int, n: int) -> np.ndarray:
+        kvd = self.sess.cfg.n_kv_heads * self.sess.cfg.head_dim
+        out = np.empty(n * kvd, np.uint16)
+        call("xp_batch_kv_download", self.h, seq, layer, which, pos0, n, out.ctypes.data)
+        return out
+
+    def set_positions(self, pos) -> None:
+        pos = np.ascontiguousarray(pos, np.uint32)
+        assert pos.size == self.n
+        call("xp_batch_set_positions", self.h, pos.ctypes.data)
+
+    def positions(self) -> np.ndarray:
+        out = np.empty(self.n, np.uint32)
+        call("xp_batch_positions", self.h, out.ctypes.data)
+        return out
+
+    def forward(self, tokens) -> None:
+        t = np.ascontiguousarray(tokens, np.uint32)
+        assert t.size == self.n
+        call("xp_batch_forward", self.h, t.ctypes.data)
+
+    def decode_step(self) -> np.ndarray:
+        out = np.empty(self.n, np.uint32)
+        call("xp_batch_decode_step", self.h, out.ctypes.data)
+        return out
+
+    def last_logits(self, seq: int) -> np.ndarray:
+        out = np.empty(self.sess.cfg.vocab, np.float32)
+        call("xp_batch_last_logits", self.h, seq, out.ctypes.data, out.size)
+        return out
+
+    def last_candidates(self, seq: int, n: int = 64):
+        v = np.empty(n, np.float32)
+        i = np.empty(n, np.uint32)
+        call("xp_batch_last_candidates", self.h, seq, v.ctypes.data, i.ctypes.data, n)
+        return v, i
+
+    def last_ms(self) -> float:
+        ms = C.c_float()
+        call("xp_batch_last_ms", self.h, C.byref(ms))
+        return ms.value
 
 
 class DecodeSession:

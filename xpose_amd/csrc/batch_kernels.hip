@@ -1,0 +1,383 @@
+// Batched decode (up to 16 independent sequences per step) on gfx950.
+//
+// The token step's matvecs become M = 16 GEMMs on the matrix cores: rows are
+// the sequences, and v_mfma_f32_16x16x32_bf16 takes one 32-wide quantisation
+// block of k at a time, so every block's integer product is scaled by its own
+// weight scale after the instruction. Weights stay in the packed KM4 layout;
+// the nibbles are widened to bf16 in registers:
+//
+//   B operand  lane l holds column 16 t + l % 16 and k = 8 (l / 16) + 0..7,
+//              i.e. word l / 16 of that column's 16-byte KM4 block, one dword
+//              load per lane (a wave reads 256 contiguous bytes). Dword j of
+//              the operand is ((w >> 4 j) & 0x000F000F) | 0x43004300: the
+//              bf16 pair (128 + n_j, 128 + n_{j+4}), exact. Operand slot s
+//              therefore holds nibble e(s) = s / 2 + 4 (s % 2).
+//   A operand  lane l holds sequence l % 16 and the same eight k in the same
+//              slot order, as two bf16 terms x = hi + lo (|x - hi - lo| <=
+//              2^-18 |x|), staged once per step by bprep_kernel.
+//   epilogue   C = A_hi B + A_lo B over the block, then
+//              y += scale(block, column) * (C - 136 * sum_k (hi + lo)),
+//              which removes the +128 magic and the nibble bias of 8.
+//
+// Each wave owns one 64-column KM4 group (four 16-column MFMA tiles); the four
+// waves of a workgroup share a k chunk whose staged A blocks pass through LDS.
+// Chunks are split-K partials reduced in ascending order by the workgroup that
+// arrives last, so results are deterministic.
+#include "xp_device.hpp"
+#include "xp_launch.hpp"
+
+namespace xp {
+
+namespace {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+constexpr uint32_t kBmmThreads = 512;       // eight waves share one column group
+constexpr uint32_t kPrepThreads = 1024;
+
+__device__ __forceinline__ bf16x8 as_bf16x8(u32x4 v) { return __builtin_bit_cast(bf16x8, v); }
+
+// The eight B-operand bf16 (128 + nibble) of one KM4 word, slot s = nibble e(s).
+__device__ __forceinline__ u32x4 widen_nibbles(uint32_t w) {
+    u32x4 d;
+    d.x = (w & 0x000F000Fu) | 0x43004300u;
+    d.y = ((w >> 4) & 0x000F000Fu) | 0x43004300u;
+    d.z = ((w >> 8) & 0x000F000Fu) | 0x43004300u;
+    d.w = ((w >> 12) & 0x000F000Fu) | 0x43004300u;
+    return d;
+}
+
+template <int FMT>
+__device__ __forceinline__ float quad_scale(u32x2 raw, uint32_t i) {
+    const uint32_t w = (i & 2u) ? raw.y : raw.x;
+    const uint32_t h = (w >> (16u * (i & 1u))) & 0xFFFFu;
+    if constexpr (FMT == XP_SCALE_F16_QUAD) return f16_bits_to_f32(h);
+    else return __uint_as_float(h << 16);
+}
+
+__device__ __forceinline__ uint32_t bf16_bits_rn(float f) {
+    return uint32_t(__builtin_bit_cast(uint16_t, __bf16(f)));
+}
+
+}  // namespace
+
+// ---- staging -------------------------------------------------------------------
+// One workgroup per sequence b; thread i holds elements 8 p .. 8 p + 7 for p =
+// i, i + 1024, ... (every width here is one pass) in registers from the load
+// through the norms to the staged operand. Modes (x, y: [batch][K] fp32, row b):
+//   0  stage rmsnorm(x) (1 + w_pre)
+//   1  x += rmsnorm(y) (1 + w_post) (written back), then stage rmsnorm(x) (1 + w_pre)
+//   2  stage y
+//   3  stage gelu_tanh(y) * u
+// Staged: A[blk][0 / 1][lane] = the hi / lo bf16 operand of lane l = b + 16 c
+// for k = 32 blk + 8 c + e(s); asum[blk][b] = sum of hi + lo over the block.
+__device__ __forceinline__ void ld8f(float (&v)[8], const float* p) {
+    const float4 a = *reinterpret_cast<const float4*>(p), b = *reinterpret_cast<const float4*>(p + 4);
+    v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w; v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+}
+
+__global__ __launch_bounds__(kPrepThreads) void bprep_kernel(BprepArgs a) {
+    __shared__ float red[2][kPrepThreads / kWave];
+    const uint32_t b = blockIdx.x, tid = threadIdx.x;
+    const uint32_t K = a.K, npair = K / 8;    // (block, word) pairs of eight elements
+    const uint32_t p = tid;
+    const bool own = p < npair;
+    float* x = a.x ? a.x + size_t(b) * K : nullptr;
+    const float* y = a.y ? a.y + size_t(b) * K : nullptr;
+    const float* u = a.u ? a.u + size_t(b) * K : nullptr;
+    auto bsum = [&](float v, int slot) {
+        v = wave_sum(v);
+        if (tid % kWave == 0) red[slot][tid / kWave] = v;
+        __syncthreads();
+        float t = 0.0f;
+#pragma unroll
+        for (int w = 0; w < int(kPrepThreads / kWave); ++w) t += red[slot][w];
+        return t;
+    };
+    float v[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
+    if (a.mode <= 1) {
+        float xv[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f}, wpre[8];
+        if (own) {
+            ld8f(xv, x + 8 * p);
+            ld8f(wpre, a.w_pre + 8 * p);
+        }
+        if (a.mode == 1) {
+            float yv[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f}, wpost[8];
+            if (own) {
+                ld8f(yv, y + 8 * p);
+                ld8f(wpost, a.w_post + 8 * p);
+            }
+            float ss = 0.0f;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) ss = fmaf(yv[e], yv[e], ss);
+            const float post = 1.0f / sqrtf(bsum(ss, 0) / float(K) + a.eps);
+            if (own) {
+#pragma unroll
+                for (int e = 0; e < 8; ++e) xv[e] = xv[e] + yv[e] * post * (1.0f + wpost[e]);
+                float4* xo = reinterpret_cast<float4*>(x + 8 * p);
+                xo[0] = float4{xv[0], xv[1], xv[2], xv[3]};
+                xo[1] = float4{xv[4], xv[5], xv[6], xv[7]};
+            }
+        }
+        float sx = 0.0f;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) sx = fmaf(xv[e], xv[e], sx);
+        const float pre = 1.0f / sqrtf(bsum(sx, 1) / float(K) + a.eps);
+        if (own) {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) v[e] = xv[e] * pre * (1.0f + wpre[e]);
+        }
+    } else if (own) {
+        ld8f(v, y + 8 * p);
+        if (a.mode == 3) {
+            float uv[8];
+            ld8f(uv, u + 8 * p);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) v[e] = gelu_tanh(v[e]) * uv[e];
+        }
+    }
+    if (!own) return;
+    const uint32_t blk = p / 4u, c = p % 4u;
+    // slot s <- element e(s) = s / 2 + 4 (s % 2)
+    uint32_t hi[8], lo[8];
+    float sum = 0.0f;
+#pragma unroll
+    for (int sl = 0; sl < 8; ++sl) {
+        const float t = v[sl / 2 + 4 * (sl % 2)];
+        const uint32_t h = bf16_bits_rn(t);
+        const float hf = __uint_as_float(h << 16);
+        const uint32_t l = bf16_bits_rn(t - hf);
+        hi[sl] = h;
+        lo[sl] = l;
+        sum += hf + __uint_as_float(l << 16);
+    }
+    const u32x4 H{hi[0] | (hi[1] << 16), hi[2] | (hi[3] << 16), hi[4] | (hi[5] << 16),
+                  hi[6] | (hi[7] << 16)};
+    const u32x4 L{lo[0] | (lo[1] << 16), lo[2] | (lo[3] << 16), lo[4] | (lo[5] << 16),
+                  lo[6] | (lo[7] << 16)};
+    const uint32_t lane = b + 16u * c;
+    u32x4* A = static_cast<u32x4*>(a.a);
+    A[(size_t(blk) * 2 + 0) * 64 + lane] = H;
+    A[(size_t(blk) * 2 + 1) * 64 + lane] = L;
+    // block sum over its four words: adjacent lanes (p = 4 blk + c, whole quads active)
+    sum += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(sum), 0xB1, 0xF, 0xF, false));
+    sum += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(sum), 0x4E, 0xF, 0xF, false));
+    if (c == 0) a.asum[size_t(blk) * 16 + b] = sum;
+}
+
+// ---- embedding --------------------------------------------------------------------
+// x[b][k] = dequant(tied table column tok[b])[k] * embed_scale (decode.cpp:1618-1627).
+__global__ __launch_bounds__(256) void bembed_kernel(float* x, const void* wq, const void* sc, int fmt,
+                                                     uint32_t hidden, uint32_t vocab, float embed_scale,
+                                                     const uint32_t* tok) {
+    const uint32_t b = blockIdx.y, k = blockIdx.x * 256 + threadIdx.x;
+    if (k >= hidden) return;
+    uint32_t t = tok[b];
+    if (t >= vocab) t = 0;
+    const uint32_t nblk = hidden / kBlk, blk = k / kBlk, i = k % kBlk;
+    const uint32_t* w = static_cast<const uint32_t*>(wq);
+    const uint32_t word = w[((size_t(t / kGrp) * nblk + blk) * kGrp + (t % kGrp)) * 4 + i / 8];
+    const float q = float(int((word >> (4 * (i % 8))) & 15u) - 8);
+    const uint16_t h = static_cast<const uint16_t*>(sc)[(size_t(blk / 4) * vocab + t) * 4 + blk % 4];
+    const float s = fmt == XP_SCALE_F16_QUAD ? f16_bits_to_f32(h) : __uint_as_float(uint32_t(h) << 16);
+    x[size_t(b) * hidden + k] = (q * s) * embed_scale;
+}
+
+// ---- M = 16 int4 GEMM ------------------------------------------------------------
+// Workgroup (g, s): column group g, k split s; its eight waves take
+// consecutive chunks of kc <= kBmmMaxPerWave blocks, load every operand of
+// their chunk at once (one memory latency per wave, not one per block), and
+// sum their 16 x 64 results through LDS in wave order. With nsplit > 1 the
+// splits publish partials and the last to arrive (ticket per group) adds them
+// in split order.
+constexpr uint32_t kBmmWaves = 8;
+constexpr uint32_t kBmmMaxPerWave = 5;
+
+template <int FMT>
+__global__ __launch_bounds__(kBmmThreads) void bmm_int4_kernel(BmmArgs a) {
+    __shared__ float red[kBmmWaves][kGrp * 16];
+    __shared__ uint32_t last;
+    const uint32_t tid = threadIdx.x, wave = tid / kWave, lane = tid % kWave;
+    const uint32_t gg = blockIdx.x, s = blockIdx.y;
+    uint32_t m = 0;
+    while (m + 1 < a.n_mats && gg >= a.groups[m + 1]) ++m;
+    const uint32_t g = gg - a.groups[m];
+    const uint32_t cols = a.mats[m].cols;
+    const uint32_t* wq = static_cast<const uint32_t*>(a.mats[m].wq);
+    const u32x2* sq = static_cast<const u32x2*>(a.mats[m].sc);
+    const u32x4* A = static_cast<const u32x4*>(a.a);
+    const uint32_t col16 = lane % 16u, wsel = lane / 16u;
+    const uint32_t kb0 = min((s * kBmmWaves + wave) * a.kc, a.nblk);
+    const uint32_t kb1 = min(kb0 + a.kc, a.nblk);
+    f32x4 acc[4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) acc[t] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    // operands of one block
+    struct Ops {
+        u32x4 hi, lo;
+        float4 as;
+        uint32_t w[4];
+        u32x2 sc[4];
+    };
+    auto load = [&](Ops& o, uint32_t blk) {
+        o.hi = A[(size_t(blk) * 2 + 0) * 64 + lane];
+        o.lo = A[(size_t(blk) * 2 + 1) * 64 + lane];
+        o.as = *reinterpret_cast<const float4*>(a.asum + size_t(blk) * 16 + 4u * wsel);
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            o.w[t] = __builtin_nontemporal_load(
+                wq + ((size_t(g) * a.nblk + blk) * kGrp + 16u * t + col16) * 4 + wsel);
+            o.sc[t] = sq[size_t(blk / 4) * cols + g * kGrp + 16u * t + col16];
+        }
+    };
+    Ops ops[kBmmMaxPerWave];
+#pragma unroll
+    for (uint32_t j = 0; j < kBmmMaxPerWave; ++j)
+        if (kb0 + j < kb1) load(ops[j], kb0 + j);
+#pragma unroll
+    for (uint32_t j = 0; j < kBmmMaxPerWave; ++j) {
+        if (kb0 + j >= kb1) break;
+        const uint32_t blk = kb0 + j;
+        const Ops& cur = ops[j];
+        const bf16x8 ahi = as_bf16x8(cur.hi), alo = as_bf16x8(cur.lo);
+        const float corr[4] = {136.0f * cur.as.x, 136.0f * cur.as.y, 136.0f * cur.as.z, 136.0f * cur.as.w};
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            const bf16x8 bw = as_bf16x8(widen_nibbles(cur.w[t]));
+            f32x4 c = {0.0f, 0.0f, 0.0f, 0.0f};
+            c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ahi, bw, c, 0, 0, 0);
+            c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(alo, bw, c, 0, 0, 0);
+            const float f = quad_scale<FMT>(cur.sc[t], blk % 4u);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) acc[t][r] = fmaf(f, c[r] - corr[r], acc[t][r]);
+        }
+    }
+    // o = lane * 16 + t * 4 + r  <->  row 4 (lane / 16) + r, column 16 t + lane % 16
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) red[wave][lane * 16 + t * 4 + r] = acc[t][r];
+    __syncthreads();
+    float v[2];
+    uint32_t row[2], col[2];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        const uint32_t o = tid + j * kBmmThreads;
+        float sum = 0.0f;
+#pragma unroll
+        for (int w = 0; w < int(kBmmWaves); ++w) sum += red[w][o];
+        v[j] = sum;
+        const uint32_t ol = o / 16u, ot = (o % 16u) / 4u, orr = o % 4u;
+        row[j] = 4u * (ol / 16u) + orr;
+        col[j] = g * kGrp + 16u * ot + ol % 16u;
+    }
+    float* out = a.mats[m].out;
+    if (a.nsplit == 1) {
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+            if (row[j] < a.rows) out[size_t(row[j]) * cols + col[j]] = v[j];
+        return;
+    }
+    float* part = a.part + (size_t(s) * gridDim.x + gg) * (kGrp * 16);
+#pragma unroll
+    for (int j = 0; j < 2; ++j) st_dev(part + tid + j * kBmmThreads, v[j]);
+    wait_mem();
+    __syncthreads();
+    if (tid == 0) last = take_ticket(a.tickets + gg);
+    __syncthreads();
+    if (last != a.nsplit - 1) return;
+    // last arrival: every split's partial, loaded together, added in split order
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        float sum = 0.0f;
+        for (uint32_t p0 = 0; p0 < a.nsplit; p0 += 8) {
+            float pv[8];
+#pragma unroll
+            for (uint32_t q = 0; q < 8; ++q)
+                pv[q] = p0 + q < a.nsplit
+                            ? ld_dev(a.part + (size_t(p0 + q) * gridDim.x + gg) * (kGrp * 16) + tid + j * kBmmThreads)
+                            : 0.0f;
+#pragma unroll
+            for (uint32_t q = 0; q < 8; ++q)
+                if (p0 + q < a.nsplit) sum += pv[q];
+        }
+        if (row[j] < a.rows) out[size_t(row[j]) * cols + col[j]] = sum;
+    }
+    if (tid == 0) st_dev(a.tickets + gg, 0u);
+}
+
+// Position advance for every sequence of a batch.
+__global__ void badvance_kernel(uint32_t* pos, uint32_t n) {
+    const uint32_t i = threadIdx.x;
+    if (i < n) pos[i] += 1u;
+}
+
+// ---- launchers --------------------------------------------------------------------
+int launch_bprep(const BprepArgs& a, uint32_t batch, hipStream_t st) {
+    if (a.K % 32 || a.K == 0 || a.K > 8 * kPrepThreads)
+        return set_error(XP_E_ARG, "bprep: K=%u must be a multiple of 32, at most %u", a.K, 8 * kPrepThreads);
+    if (batch == 0 || batch > 16) return set_error(XP_E_ARG, "bprep: batch %u outside [1, 16]", batch);
+    hipLaunchKernelGGL(bprep_kernel, dim3(batch), dim3(kPrepThreads), 0, st, a);
+    XP_LAUNCHED();
+    return XP_OK;
+}
+
+int launch_bembed(float* x, const void* wq, const void* sc, int fmt, uint32_t hidden, uint32_t vocab,
+                  float embed_scale, const uint32_t* tok, uint32_t batch, hipStream_t st) {
+    hipLaunchKernelGGL(bembed_kernel, dim3((hidden + 255) / 256, batch), dim3(256), 0, st, x, wq, sc, fmt,
+                       hidden, vocab, embed_scale, tok);
+    XP_LAUNCHED();
+    return XP_OK;
+}
+
+int launch_badvance(uint32_t* pos, uint32_t batch, hipStream_t st) {
+    hipLaunchKernelGGL(badvance_kernel, dim3(1), dim3(64), 0, st, pos, batch);
+    XP_LAUNCHED();
+    return XP_OK;
+}
+
+// At most kBmmMaxPerWave blocks per wave; splits only when eight waves cannot
+// cover k that way (the 6912-long down projection).
+uint32_t bmm_split(uint32_t total_cols, uint32_t nblk, int n_cu) {
+    (void)total_cols;
+    (void)n_cu;
+    return (nblk + kBmmWaves * kBmmMaxPerWave - 1) / (kBmmWaves * kBmmMaxPerWave);
+}
+
+size_t bmm_partial_floats(uint32_t total_cols, uint32_t nblk, int n_cu) {
+    const uint32_t s = bmm_split(total_cols, nblk, n_cu);
+    return s > 1 ? size_t(s) * (total_cols / kGrp) * kGrp * 16u : 0;
+}
+
+int launch_bmm(BmmArgs a, int fmt, int n_cu, hipStream_t st, const char* who) {
+    if (a.n_mats == 0 || a.n_mats > 4) return set_error(XP_E_ARG, "%s: 1..4 matrices", who);
+    if (a.rows == 0 || a.rows > 16) return set_error(XP_E_ARG, "%s: rows %u outside [1, 16]", who, a.rows);
+    a.groups[0] = 0;
+    for (uint32_t i = 0; i < a.n_mats; ++i) {
+        if (a.mats[i].cols % kGrp) return set_error(XP_E_ARG, "%s: cols %u not a multiple of 64", who, a.mats[i].cols);
+        a.groups[i + 1] = a.groups[i] + a.mats[i].cols / kGrp;
+    }
+    const uint32_t total = a.groups[a.n_mats] * kGrp;
+    a.n_colwg = a.groups[a.n_mats];
+    a.nsplit = bmm_split(total, a.nblk, n_cu);
+    a.kc = (a.nblk + kBmmWaves * a.nsplit - 1) / (kBmmWaves * a.nsplit);
+    a.nsplit = (a.nblk + kBmmWaves * a.kc - 1) / (kBmmWaves * a.kc);
+    if (a.nsplit > 1) {
+        if (!a.part || a.part_cap < size_t(a.nsplit) * a.n_colwg * kGrp * 16u)
+            return set_error(XP_E_ARG, "%s: split-K partial buffer too small", who);
+        if (!a.tickets || a.tickets_cap < a.n_colwg) return set_error(XP_E_ARG, "%s: too few tickets", who);
+    }
+    const dim3 grid(a.n_colwg, a.nsplit);
+    if (fmt == XP_SCALE_F16_QUAD)
+        hipLaunchKernelGGL(bmm_int4_kernel<XP_SCALE_F16_QUAD>, grid, dim3(kBmmThreads), 0, st, a);
+    else if (fmt == XP_SCALE_BF16_QUAD)
+        hipLaunchKernelGGL(bmm_int4_kernel<XP_SCALE_BF16_QUAD>, grid, dim3(kBmmThreads), 0, st, a);
+    else
+        return set_error(XP_E_ARG, "%s: the batched GEMM takes fp16 or bf16 quad scales", who);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return set_error(XP_E_HIP, "%s: launch -> %s", who, hipGetErrorString(e));
+    return XP_OK;
+}
+
+}  // namespace xp

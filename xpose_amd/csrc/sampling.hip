@@ -80,6 +80,9 @@ __global__ __launch_bounds__(kAmThreads) void argmax_kernel(AmArgs a) {
 // unfilled slots (-inf, 0xFFFFFFFF). Pure comparisons: bit-identical output.
 __global__ void topk4_kernel(float* cval, uint32_t* cidx, const float* x, uint32_t n,
                              uint32_t nparts) {
+    x += size_t(blockIdx.y) * n;                 // batched rows (grid.y)
+    cval += size_t(blockIdx.y) * nparts * 4u;
+    cidx += size_t(blockIdx.y) * nparts * 4u;
     const uint32_t p = blockIdx.x * blockDim.x + threadIdx.x;
     if (p >= nparts) return;
     float v0 = -INFINITY, v1 = -INFINITY, v2 = -INFINITY, v3 = -INFINITY;
@@ -121,8 +124,8 @@ int launch_argmax(uint32_t* out_idx, float* out_val, const float* logits, uint32
 }
 
 int launch_topk4(float* cval, uint32_t* cidx, const float* x, uint32_t n, uint32_t nparts,
-                 hipStream_t st) {
-    hipLaunchKernelGGL(topk4_kernel, dim3((nparts + 255) / 256), dim3(256), 0, st, cval, cidx, x,
+                 hipStream_t st, uint32_t rows) {
+    hipLaunchKernelGGL(topk4_kernel, dim3((nparts + 255) / 256, rows), dim3(256), 0, st, cval, cidx, x,
                        n, nparts);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return set_error(XP_E_HIP, "topk4: launch -> %s", hipGetErrorString(e));

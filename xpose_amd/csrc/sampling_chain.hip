@@ -119,6 +119,9 @@ __global__ __launch_bounds__(kTopkThreads) void topk_partial_kernel(float* cval,
                                                                     uint32_t nparts, uint32_t k) {
     __shared__ float bv[kTopkMax][kTopkThreads];
     __shared__ uint32_t bi[kTopkMax][kTopkThreads];
+    x += size_t(blockIdx.y) * n;                       // batched rows (grid.y)
+    cval += size_t(blockIdx.y) * nparts * k;
+    cidx += size_t(blockIdx.y) * nparts * k;
     const uint32_t t = threadIdx.x;
     const uint32_t p = blockIdx.x * kTopkThreads + t;
     for (uint32_t j = 0; j < k; ++j) { bv[j][t] = -INFINITY; bi[j][t] = kNone; }
@@ -152,6 +155,10 @@ __global__ __launch_bounds__(kScThreads) void topk_rank_select_kernel(float* ova
                                                                       uint32_t ncand, uint32_t k) {
     __shared__ float tv[kRankTile];
     __shared__ uint32_t ti[kRankTile];
+    cval += size_t(blockIdx.y) * ncand;                 // batched rows (grid.y)
+    cidx += size_t(blockIdx.y) * ncand;
+    oval += size_t(blockIdx.y) * k;
+    oidx += size_t(blockIdx.y) * k;
     const uint32_t i = blockIdx.x * kScThreads + threadIdx.x;
     const bool mine = i < ncand;
     const float v = mine ? cval[i] : -INFINITY;
@@ -238,6 +245,122 @@ __global__ void multinomial_strided_kernel(float* out, uint32_t* idx_out, const 
     out[0] = float(chosen);
     out[1] = w[chosen];
     idx_out[0] = chosen;
+}
+
+// Exact best k of a candidate list, one workgroup per row: a most-significant-
+// byte-first radix select finds the k-th largest (value, as an order-preserving
+// key); the candidates at or above it (k plus any ties) are gathered in LDS and
+// ranked among themselves by (value desc, index asc). Exact while fewer than
+// 256 - k candidates tie with the k-th largest value.
+constexpr uint32_t kSelThreads = 1024;
+constexpr uint32_t kSelPer = 16;             // candidates per thread (16384 per row)
+constexpr uint32_t kSelKeep = 256;           // survivors ranked (k + ties)
+
+__device__ __forceinline__ uint32_t order_key(float v) {
+    const uint32_t u = __float_as_uint(v);
+    return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+__global__ __launch_bounds__(kSelThreads) void select_rows_kernel(float* oval, uint32_t* oidx,
+                                                                  const float* cval,
+                                                                  const uint32_t* cidx,
+                                                                  uint32_t ncand, uint32_t k) {
+    __shared__ uint32_t hist[256];
+    __shared__ uint32_t sel[3];               // prefix, needed, survivors
+    __shared__ float sv[kSelKeep];
+    __shared__ uint32_t si[kSelKeep];
+    const uint32_t r = blockIdx.x, tid = threadIdx.x;
+    cval += size_t(r) * ncand;
+    cidx += size_t(r) * ncand;
+    if (tid < k) {   // slots no candidate reaches stay unfilled
+        oval[size_t(r) * k + tid] = -INFINITY;
+        oidx[size_t(r) * k + tid] = kNone;
+    }
+    uint32_t key[kSelPer];
+#pragma unroll
+    for (uint32_t j = 0; j < kSelPer; ++j) {
+        const uint32_t i = tid + j * kSelThreads;
+        key[j] = (i < ncand && cidx[i] != kNone) ? order_key(cval[i]) : 0u;   // 0: below every value
+    }
+    uint32_t prefix = 0, mask = 0, need = k;
+    for (int shift = 24; shift >= 0; shift -= 8) {
+        if (tid < 256) hist[tid] = 0;
+        __syncthreads();
+#pragma unroll
+        for (uint32_t j = 0; j < kSelPer; ++j)
+            if (key[j] != 0u && (key[j] & mask) == prefix) atomicAdd(&hist[(key[j] >> shift) & 255u], 1u);
+        __syncthreads();
+        if (tid < kWave) {
+            // lane l covers bins 255 - 4 l .. 252 - 4 l; inclusive prefix of
+            // the lane counts from the top bin down, then the crossing lane
+            // walks its own four bins
+            const uint32_t l = tid;
+            const uint32_t c0 = hist[255 - 4 * l], c1 = hist[254 - 4 * l], c2 = hist[253 - 4 * l],
+                           c3 = hist[252 - 4 * l];
+            const uint32_t mine = c0 + c1 + c2 + c3;
+            uint32_t incl = mine;
+#pragma unroll
+            for (int o = 1; o < kWave; o <<= 1) {
+                const uint32_t t = __shfl_up(incl, o, kWave);
+                if (l >= uint32_t(o)) incl += t;
+            }
+            const uint32_t excl = incl - mine;
+            if (excl < need && incl >= need) {   // exactly one lane
+                uint32_t acc = excl, d = 255 - 4 * l;
+                const uint32_t cs[4] = {c0, c1, c2, c3};
+                for (int j = 0; j < 4; ++j) {
+                    if (acc + cs[j] >= need) { d = 255 - 4 * l - j; break; }
+                    acc += cs[j];
+                }
+                sel[0] = prefix | (d << shift);
+                sel[1] = need - acc;
+            }
+            if (l == kWave - 1 && incl < need) {   // fewer than need keys: keep them all
+                sel[0] = prefix;
+                sel[1] = need;
+            }
+        }
+        __syncthreads();
+        prefix = sel[0];
+        need = sel[1];
+        mask |= 255u << shift;
+        __syncthreads();
+    }
+    // prefix = the k-th largest key (or 0 when fewer than k candidates exist)
+    if (tid == 0) sel[2] = 0;
+    __syncthreads();
+#pragma unroll
+    for (uint32_t j = 0; j < kSelPer; ++j) {
+        const uint32_t i = tid + j * kSelThreads;
+        if (key[j] != 0u && key[j] >= prefix) {
+            const uint32_t slot = atomicAdd(&sel[2], 1u);
+            if (slot < kSelKeep) { sv[slot] = cval[i]; si[slot] = cidx[i]; }
+        }
+    }
+    __syncthreads();
+    const uint32_t m = min(sel[2], kSelKeep);
+    if (tid < m) {
+        const float v = sv[tid];
+        const uint32_t d = si[tid];
+        uint32_t rank = 0;
+        for (uint32_t j = 0; j < m; ++j) rank += (sv[j] > v) | ((sv[j] == v) & (si[j] < d));
+        if (rank < k) {
+            oval[size_t(r) * k + rank] = v;
+            oidx[size_t(r) * k + rank] = d;
+        }
+    }
+}
+
+int launch_select_rows(float* oval, uint32_t* oidx, const float* cval, const uint32_t* cidx,
+                       uint32_t ncand, uint32_t k, uint32_t rows, hipStream_t st) {
+    if (k < 1 || k > kTopkMax || rows == 0 || ncand == 0 || ncand > kSelThreads * kSelPer)
+        return set_error(XP_E_ARG, "select rows: k=%u rows=%u ncand=%u (<= %u)", k, rows, ncand,
+                         kSelThreads * kSelPer);
+    hipLaunchKernelGGL(select_rows_kernel, dim3(rows), dim3(kSelThreads), 0, st, oval, oidx, cval, cidx,
+                       ncand, k);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return set_error(XP_E_HIP, "select rows: launch -> %s", hipGetErrorString(e));
+    return XP_OK;
 }
 
 }  // namespace xp

@@ -375,6 +375,30 @@ struct xp_session {
     Session s;
 };
 
+namespace xp {
+int session_weights(const xp_session* h, SessionWeights* out) {
+    XP_REQUIRE(h && out, "null pointer");
+    const Session& s = h->s;
+    XP_REQUIRE(s.cfg.n_layers <= uint32_t(kMaxSessionLayers), "at most %d layers", kMaxSessionLayers);
+    out->cfg = s.cfg;
+    out->n_cu = s.n_cu;
+    out->embed_scale = s.embed_scale();
+    out->attn_scale = s.attn_scale();
+    for (uint32_t l = 0; l < s.cfg.n_layers; ++l) {
+        for (int m = 0; m < kNMat; ++m) {
+            out->layer[l].w[m] = s.L[l].w[m];
+            out->layer[l].s[m] = s.L[l].s[m];
+        }
+        for (int n = 0; n < kNNorm; ++n) out->layer[l].norm[n] = s.L[l].norm[n];
+        out->layer[l].global = s.is_global(l);
+    }
+    out->lm_w = s.lm_w;
+    out->lm_s = s.lm_s;
+    out->final_norm = s.final_norm;
+    return XP_OK;
+}
+}  // namespace xp
+
 namespace {
 
 int destroy(xp_session* h) {

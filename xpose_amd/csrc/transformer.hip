@@ -99,7 +99,15 @@ __global__ void rope_kernel(float* x, uint32_t n_heads, uint32_t head_dim, uint3
 __global__ __launch_bounds__(256) void qk_norm_rope_append_kernel(QkArgs a, RopeFreq f) {
     __shared__ float red[16];
     const uint32_t half = a.head_dim >> 1;
-    const uint32_t pos = a.pos_dev ? *a.pos_dev : a.pos;
+    const uint32_t b = blockIdx.y;   // batched sequence
+    a.q_raw += size_t(b) * a.bq;
+    a.q_out += size_t(b) * a.bq;
+    a.k_raw += size_t(b) * a.bkv;
+    a.k_out += size_t(b) * a.bkv;
+    a.v += size_t(b) * a.bkv;
+    a.kcache += b * a.bcache;
+    a.vcache += b * a.bcache;
+    const uint32_t pos = a.pos_dev ? a.pos_dev[b] : a.pos;
     const bool is_q = blockIdx.x < a.n_heads;
     const uint32_t h = is_q ? blockIdx.x : blockIdx.x - a.n_heads;
     const float* x = (is_q ? a.q_raw : a.k_raw) + size_t(h) * a.head_dim;
@@ -147,7 +155,7 @@ constexpr int kAttnMaxSplit = 64;    // workgroups per kv head
 
 __device__ __forceinline__ void attn_range(const AttnArgs& a, uint32_t& span, uint32_t& kv0) {
     if (a.pos_dev) {
-        const uint32_t seq = *a.pos_dev + 1u;
+        const uint32_t seq = a.pos_dev[blockIdx.z] + 1u;
         kv0 = (a.window == 0 || seq <= a.window) ? 0u : seq - a.window;
         span = seq - kv0;
     } else {
@@ -169,6 +177,15 @@ __global__ __launch_bounds__(kAttnThreads) void attention_decode_kernel(AttnArgs
     __shared__ float fs[kAttnMaxSplit * G];
     __shared__ float ls[kAttnMaxSplit * G];
     __shared__ uint32_t last;
+    {   // batched sequence blockIdx.z
+        const uint32_t b = blockIdx.z;
+        a.q += size_t(b) * a.bq;
+        a.out += size_t(b) * a.bq;
+        a.kc += b * a.bcache;
+        a.vc += b * a.bcache;
+        if (a.part) a.part += b * a.bpart;
+        if (a.tickets) a.tickets += size_t(b) * a.kv_heads;
+    }
     uint32_t span, kv0;
     attn_range(a, span, kv0);
     const uint32_t g = blockIdx.y, s = blockIdx.x;
@@ -362,7 +379,7 @@ int launch_qk(const QkArgs& a, float theta, hipStream_t st) {
         return set_error(XP_E_ARG, "qk_norm_rope_append: empty head count");
     RopeFreq f;
     rope_freq(f, a.head_dim, theta);
-    hipLaunchKernelGGL(qk_norm_rope_append_kernel, dim3(a.n_heads + a.kv_heads),
+    hipLaunchKernelGGL(qk_norm_rope_append_kernel, dim3(a.n_heads + a.kv_heads, a.batch ? a.batch : 1),
                        dim3(a.head_dim / 2), 0, st, a, f);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return set_error(XP_E_HIP, "qk_norm_rope_append: launch -> %s",
@@ -396,6 +413,9 @@ int launch_attention(AttnArgs a, uint32_t max_span, hipStream_t st) {
     if (G != 1 && G != 2 && G != 4 && G != 8)
         return set_error(XP_E_ARG, "attention: %u query heads per kv head (1, 2, 4 or 8)", G);
     a.nsplit = attn_splits(max_span);
+    if (a.batch == 0) a.batch = 1;
+    if (a.batch > 1 && a.nsplit > 1 && (!a.part || !a.tickets || a.bpart == 0))
+        return set_error(XP_E_ARG, "attention: a batch needs its own partials and tickets");
     if (a.nsplit > 1 && (!a.part || !a.tickets)) {
         DeviceScratch* sc = scratch();
         if (!sc) return XP_E_HIP;
@@ -404,7 +424,7 @@ int launch_attention(AttnArgs a, uint32_t max_span, hipStream_t st) {
         a.part = sc->partial;
         a.tickets = sc->tickets;
     }
-    const dim3 grid(a.nsplit, a.kv_heads), block(kAttnThreads);
+    const dim3 grid(a.nsplit, a.kv_heads, a.batch), block(kAttnThreads);
 #define XP_ATTN(GG, HH)                                                                    \
     if (G == GG && a.head_dim == HH) {                                                     \
         hipLaunchKernelGGL((attention_decode_kernel<GG, HH>), grid, block, 0, st, a);      \

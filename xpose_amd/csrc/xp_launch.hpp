@@ -36,8 +36,13 @@ struct QkArgs {
     uint16_t* vcache;
     uint32_t n_heads, kv_heads, head_dim;
     float eps;
-    const uint32_t* pos_dev;   // when non-null, the position is read here
+    const uint32_t* pos_dev;   // when non-null, the position is read here (pos_dev[b])
     uint32_t pos;
+    // Batched sequences (grid.y = batch): element strides between sequence b
+    // and b + 1 of q_raw / q_out, of k_raw / v / k_out, and of the caches.
+    uint32_t batch = 1;
+    uint32_t bq = 0, bkv = 0;
+    size_t bcache = 0;
 };
 int launch_qk(const QkArgs& a, float theta, hipStream_t st);
 
@@ -55,6 +60,12 @@ struct AttnArgs {
     uint32_t nsplit;
     float* part;               // [kv_heads][nsplit][group][2 + head_dim]
     uint32_t* tickets;         // [kv_heads]
+    // Batched sequences (grid.z = batch): sequence b reads q + b bq, the caches
+    // at + b bcache, position pos_dev[b], and writes out + b bq, its own partials
+    // (+ b bpart) and tickets (+ b kv_heads).
+    uint32_t batch = 1;
+    uint32_t bq = 0;
+    size_t bcache = 0, bpart = 0;
 };
 uint32_t attn_splits(uint32_t max_span);
 size_t attn_partial_floats(uint32_t kv_heads, uint32_t n_heads, uint32_t head_dim,
@@ -66,8 +77,73 @@ constexpr int kAmMaxWg = 256;
 int launch_argmax(uint32_t* out_idx, float* out_val, const float* logits, uint32_t n,
                   float* pval, uint32_t* pidx, uint32_t* ticket, hipStream_t st);
 int launch_topk4(float* cval, uint32_t* cidx, const float* x, uint32_t n, uint32_t nparts,
-                 hipStream_t st);
+                 hipStream_t st, uint32_t rows = 1);
+// The best k (<= 64) of each of `rows` candidate lists (row r at cval / cidx +
+// r ncand), sorted by (value desc, index asc), into oval / oidx [rows][k];
+// exact. Unfilled list slots carry index 0xFFFFFFFF and are skipped.
+int launch_select_rows(float* oval, uint32_t* oidx, const float* cval, const uint32_t* cidx,
+                       uint32_t ncand, uint32_t k, uint32_t rows, hipStream_t st);
 
+
+// ---- batched decode (batch_kernels.hip) ----
+// Staging of one sequence row per workgroup into the M = 16 MFMA operand
+// (see bprep_kernel for the modes).
+struct BprepArgs {
+    int mode;
+    float* x;                  // [batch][K] residual stream (modes 0, 1)
+    const float* y;            // [batch][K] sublayer output / input / gate
+    const float* u;            // [batch][K] up (mode 3)
+    const float* w_post;
+    const float* w_pre;
+    void* a;                   // [K/32][2][64] 16-byte staged hi / lo operand
+    float* asum;               // [K/32][16]
+    uint32_t K;
+    float eps;
+};
+int launch_bprep(const BprepArgs& a, uint32_t batch, hipStream_t st);
+int launch_bembed(float* x, const void* wq, const void* sc, int fmt, uint32_t hidden, uint32_t vocab,
+                  float embed_scale, const uint32_t* tok, uint32_t batch, hipStream_t st);
+int launch_badvance(uint32_t* pos, uint32_t batch, hipStream_t st);
+// y[m][row][col] = sum_k A[row][k] W_m[k][col] for the staged A (rows = sequences).
+struct BmmArgs {
+    const void* a;             // staged operand (BprepArgs::a)
+    const float* asum;
+    MvMatDesc mats[4];         // out is [rows][cols] row-major
+    uint32_t n_mats;
+    uint32_t groups[5];        // set by launch_bmm
+    uint32_t nblk;             // k / 32
+    uint32_t rows;             // sequences (<= 16)
+    uint32_t kc, nsplit, n_colwg;   // set by launch_bmm
+    float* part;
+    size_t part_cap;
+    uint32_t* tickets;
+    uint32_t tickets_cap;
+};
+uint32_t bmm_split(uint32_t total_cols, uint32_t nblk, int n_cu);
+size_t bmm_partial_floats(uint32_t total_cols, uint32_t nblk, int n_cu);
+int launch_bmm(BmmArgs a, int fmt, int n_cu, hipStream_t st, const char* who);
+
+// ---- a decode session's device weights, for the batch (session.cpp) ----
+constexpr int kMaxSessionLayers = 64;
+struct SessionWeights {
+    xp_config cfg;
+    int n_cu;
+    float embed_scale, attn_scale;
+    struct Layer {
+        const void* w[7];       // Q K V O GATE UP DOWN
+        const void* s[7];
+        const float* norm[6];   // attn, post_attn, ffn, post_ffw, q_norm, k_norm
+        bool global;
+    } layer[kMaxSessionLayers];
+    const void* lm_w;
+    const void* lm_s;
+    const float* final_norm;
+};
+int session_weights(const xp_session* h, SessionWeights* out);
+// The session's host draw and Philox uniform (decode.cpp:1873-1917).
+uint32_t draw(float* val, uint32_t* idx, uint32_t n, float temperature, uint32_t top_k,
+              float top_p, double u);
+double philox_uniform(uint32_t seed, uint32_t seq, uint32_t step);
 
 // ---- persistent token step (token_kernel.hip) ----
 // Per-layer pointers, kept in device memory and read with uniform loads.
