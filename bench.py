@@ -16,6 +16,14 @@ HBM bytes of one token at its mean position over the kernel's mean duration,
 taken with HIP events on the session's stream around the K launches. The
 standalone int4 matvec (lm_head shape, and BASELINE config 1's gate shape with
 64 rotating weight copies) is reported beside it. Prints one JSON line.
+
+Beside the headline, the line carries the other BASELINE configurations as
+measurements (not the metric): `cfg4` (decode from 4097 to 8192, tok/s per
+512-position bucket and the deepest / shallowest ratio), `cfg3` (32-token
+prompt, 128 greedy tokens), `attention` (one global layer's decode attention
+at spans 4096 and 8192, HBM GB/s of its K + V bytes) and `cfg5` (16 sequences
+batched, temperature / top-k / top-p sampling, tok/s over all sequences and
+the step's algorithmic bytes). `--no-configs` skips them.
 """
 from __future__ import annotations
 
@@ -88,6 +96,125 @@ def stream_ceiling(X, nbytes: int = 1 << 30, iters: int = 20) -> float:
     return nbytes * iters / (ms.value / 1e3) / 1e9
 
 
+def attention_leg(X, span: int, iters: int = 192):
+    """Decode attention of one global layer (4 query heads, 1 KV head, head_dim
+    256) over `span` fp16 positions: per-launch time over back-to-back launches
+    cycling K/V copies totalling > 256 MiB, and the HBM GB/s of 1024 * span
+    bytes (K + V) per launch."""
+    kvd, heads = 256, 4
+    per = span * kvd * 2
+    copies = max(4, -(-(384 << 20) // (2 * per)))
+    k0 = X.DeviceBuffer.from_array(X.synth_normal_f16(span * kvd, SEED, 931))
+    v0 = X.DeviceBuffer.from_array(X.synth_normal_f16(span * kvd, SEED, 932))
+    ks, vs = [k0], [v0]
+    for _ in range(copies - 1):
+        k, v = X.DeviceBuffer(per), X.DeviceBuffer(per)
+        X.call("xp_memcpy_dtod", k.vp, k0.vp, per)
+        X.call("xp_memcpy_dtod", v.vp, v0.vp, per)
+        ks.append(k)
+        vs.append(v)
+    q = X.DeviceBuffer.from_array(X.synth_normal(heads * kvd, SEED, 933))
+    out = X.DeviceBuffer(heads * kvd * 4)
+    K = (C.c_void_p * copies)(*[d.ptr for d in ks])
+    V = (C.c_void_p * copies)(*[d.ptr for d in vs])
+    ms = C.c_float()
+    X.call("xp_attention_decode_timed", out.vp, q.vp, K, V, copies, heads, 1, kvd, span, 0,
+           1.0 / 16.0, iters, None, C.byref(ms))
+    X.synchronize()
+    per_s = ms.value / 1e3 / iters
+    return {"span": span, "bytes": 1024 * span, "us_per_launch": round(per_s * 1e6, 3),
+            "GBs": round(1024 * span / per_s / 1e9, 1)}
+
+
+def cfg3_leg(X, sess, cfg, n_gen: int = 128):
+    """prefill a 32-token prompt of uniform random ids from
+    position 0, then greedy-decode `n_gen` tokens (decode tok/s, prefill
+    excluded)."""
+    r = np.random.default_rng(SEED)
+    prompt = r.integers(0, cfg.vocab, 32).astype(np.uint32)
+    sess.set_position(0)
+    t0 = time.perf_counter()
+    sess.prefill(prompt)
+    X.synchronize()
+    t_pre = time.perf_counter() - t0
+    t0 = time.perf_counter()
+    ids = sess.decode_steps(n_gen)
+    X.synchronize()
+    el = time.perf_counter() - t0
+    return {"prompt": 32, "generated": n_gen, "decode_tok_s": round(n_gen / el, 1),
+            "prefill_ms": round(t_pre * 1e3, 3), "ids_head": [int(v) for v in ids[:4]]}
+
+
+def cfg4_leg(X, sess, cfg, ctx: int = 4096):
+    """KV pre-filled to `ctx`, then greedy decode out to
+    max_seq (8192); tok/s per 512-position bucket and the deepest / shallowest
+    ratio (flatness)."""
+    sess.set_position(ctx)
+    sess.prefill([4242])
+    X.synchronize()
+    buckets = []
+    pos = ctx + 1
+    while pos < cfg.max_seq:
+        n = min(512, cfg.max_seq - pos)
+        t0 = time.perf_counter()
+        sess.decode_steps(n)
+        X.synchronize()
+        el = time.perf_counter() - t0
+        buckets.append({"from": pos, "steps": n, "tok_s": round(n / el, 1)})
+        pos += n
+    rates = [b["tok_s"] for b in buckets]
+    return {"ctx": ctx, "to": cfg.max_seq, "buckets": buckets,
+            "deepest_over_shallowest": round(rates[-1] / rates[0], 4)}
+
+
+def batch_bytes(depths) -> int:
+    """Algorithmic HBM bytes of one batched step: weights and norms once, each
+    sequence's KV reads at its depth, logits write + read and KV append per
+    sequence."""
+    kv = sum(1024 * (4 * int(s) + 22 * min(int(s), 512)) for s in depths)
+    return WEIGHT_BYTES + NORM_BYTES + kv + len(depths) * (LOGIT_BYTES + APPEND_BYTES)
+
+
+def cfg5_leg(X, sess, cfg, n_seq: int = 16, steps: int = 20, warmup: int = 3):
+    """16 independent sequences at depths uniform in
+    [128, 4096] (Philox), temperature 0.8 / top-k 64 / top-p 0.95 with a
+    Philox draw per (sequence, step); tokens/s over all sequences."""
+    seed = 0x5EED0005
+    u = np.array([X.philox_uniform(seed, i, 0) for i in range(n_seq)])
+    depths = (128 + np.floor(u * (4096 - 128 + 1))).astype(np.int64)
+    S = 4096 + warmup + steps + 2
+    b = X.DecodeBatch(sess, n_seq, S)
+    kvd = cfg.n_kv_heads * cfg.head_dim
+    dmax = int(depths.max())
+    for l in range(cfg.n_layers):
+        for which in (0, 1):
+            rows = X.synth_normal_f16(dmax * kvd, seed, 2 * l + which)
+            for i, d in enumerate(depths):
+                b.kv_upload(i, l, which, 0, rows[:int(d) * kvd])
+    b.set_positions(depths)
+    b.forward(np.arange(n_seq) * 1000 + 7)
+    for _ in range(warmup):
+        b.decode_step()
+    X.synchronize()
+    d0 = b.positions().astype(np.int64)
+    dev_ms = []
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        b.decode_step()
+        dev_ms.append(b.last_ms())
+    el = time.perf_counter() - t0
+    b.close()
+    mid = d0 + steps // 2
+    nb = batch_bytes(mid)
+    ms_dev = float(np.mean(dev_ms))
+    return {"sequences": n_seq, "depths": [int(v) for v in depths], "steps": steps,
+            "tok_s": round(n_seq * steps / el, 1), "ms_per_step": round(el * 1e3 / steps, 4),
+            "device_ms_per_step": round(ms_dev, 4),
+            "bytes_per_step": nb, "GBs": round(nb / (ms_dev / 1e3) / 1e9, 1),
+            "frac": round(nb / (ms_dev / 1e3) / 1e9 / HBM_PEAK_GBS, 4),
+            "sampling": "T 0.8, top-k 64, top-p 0.95, Philox(seed, seq, step)"}
+
+
 def cpu_baseline(X, cfg, ctx: int, seconds: float, threads: int):
     """The oracle (C restatement, OpenMP over output columns) decoding greedy
     tokens of the same model from position ctx, for about `seconds`."""
@@ -127,6 +254,8 @@ def main() -> int:
     ap.add_argument("--ctx", type=int, default=4096)
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-configs", action="store_true",
+                    help="skip the BASELINE config 3 / 4 / 5 and attention legs")
     ap.add_argument("--mv-iters", type=int, default=60)
     ap.add_argument("--only", choices=["all", "matvec"], default="all",
                     help="matvec: only the standalone matvec and streaming legs (for profiling)")
@@ -190,6 +319,17 @@ def main() -> int:
     launches = met.launches
     kern_s = met.gpu_ms / 1e3 / args.steps          # device time per token-kernel launch
     exec_mode = {1: "graph", 2: "launch", 3: "token-kernel"}.get(met.exec_mode, str(met.exec_mode))
+    extra = {}
+    if not args.no_configs:
+        extra["cfg4"] = cfg4_leg(X, sess, cfg, ctx)       # reads the pre-filled rows 0..ctx-1
+        extra["cfg3"] = cfg3_leg(X, sess, cfg)
+        extra["attention"] = [attention_leg(X, sp) for sp in (4096, 8192)]
+        scfg = X.XpConfig.gemma3_1b(max_seq=8192, sample_mode=1, temperature=0.8, top_k=64,
+                                    top_p=0.95, seed=0x5EED0005)
+        bsess = X.DecodeSession(scfg)
+        bsess.synthesize(SEED)
+        extra["cfg5"] = cfg5_leg(X, bsess, scfg)
+        bsess.close()
     sess.close()
 
     # Roofline leg: the dominant kernel of the step, the lm_head int4 matvec.
@@ -239,6 +379,7 @@ def main() -> int:
         "matvec_cfg1": {"shape": "6912x1152", "bytes": nb1, "us_per_launch": round(per1 * 1e6, 3),
                         "GBs": round(nb1 / per1 / 1e9, 1)},
         "cpu_baseline": cpu,
+        **extra,
         "device": info["arch"],
         "ids_head": [int(v) for v in ids[:4]],
     }

@@ -162,6 +162,15 @@ int xp_attention_decode(float* out, const float* q, const uint16_t* kcache,
                         uint32_t kv_heads, uint32_t head_dim, uint32_t span,
                         uint32_t kv_start, float scale, xp_stream stream);
 
+/* Measurement: `iters` back-to-back xp_attention_decode launches on `stream`,
+ * cycling through `ncopies` K/V cache pairs (so each launch streams its span
+ * from HBM), bracketed by HIP events; *ms = elapsed time of the whole loop. */
+int xp_attention_decode_timed(float* out, const float* q, const uint16_t* const* kcaches,
+                              const uint16_t* const* vcaches, uint32_t ncopies, uint32_t n_heads,
+                              uint32_t kv_heads, uint32_t head_dim, uint32_t span,
+                              uint32_t kv_start, float scale, uint32_t iters, xp_stream stream,
+                              float* ms);
+
 /* out = gelu_tanh(gate) * up. Replaces geglu (llm_transformer.cl:223-231). */
 int xp_geglu(float* out, const float* gate, const float* up, uint32_t n,
              xp_stream stream);

@@ -7,6 +7,7 @@ atol 1e-6 (:43-89, :136-142), sentinel liveness, the windowed kv_start = 43
 case with its negative control (:483-621), and the chained attention block
 (:713-799).
 """
+import ctypes as C
 import numpy as np
 import pytest
 
@@ -315,3 +316,34 @@ def test_gpu_geglu_residual_kv_append(xp, xo):
     cw = cache.copy()
     xo.lib().xo_kv_append_f16(cw, src, HEAD_DIM, 5)
     assert np.array_equal(dc.download(np.uint16), cw)
+
+
+@pytest.mark.gpu
+def test_gpu_attention_timed_equals_single_launch(xp, xo):
+    """The measurement loop leaves the output of its last launch: equal to one
+    xp_attention_decode over the same K/V copy, to the oracle's bar."""
+    print("case attention timed", flush=True)
+    r = rng()
+    span = 700
+    q = u(r, HEADS * HEAD_DIM)
+    ks = [f16_bits(u(r, span * HEAD_DIM)) for _ in range(3)]
+    vs = [f16_bits(u(r, span * HEAD_DIM)) for _ in range(3)]
+    dk = [dev(xp, k) for k in ks]
+    dv = [dev(xp, v) for v in vs]
+    d = sentinel(xp, HEADS * HEAD_DIM)
+    K = (C.c_void_p * 3)(*[b.ptr for b in dk])
+    V = (C.c_void_p * 3)(*[b.ptr for b in dv])
+    ms = C.c_float()
+    iters = 5                                   # last launch uses copy (5 - 1) % 3 = 1
+    xp.call("xp_attention_decode_timed", d.vp, hold(dev(xp, q)), K, V, 3, HEADS, KV_HEADS,
+            HEAD_DIM, span, 0, np.float32(1 / 16), iters, None, C.byref(ms))
+    xp.synchronize()
+    assert ms.value > 0
+    want = np.empty(HEADS * HEAD_DIM, np.float32)
+    xo.lib().xo_attention_f16(want, q, ks[1], vs[1], HEADS, KV_HEADS, HEAD_DIM, span, 0,
+                              np.float32(1 / 16))
+    ok, msg = allclose_report(d.download(np.float32), want, RTOL, 1e-5)
+    assert ok, msg
+    with pytest.raises(xp.XposeError):
+        xp.call("xp_attention_decode_timed", d.vp, d.vp, K, V, 0, HEADS, KV_HEADS, HEAD_DIM,
+                span, 0, np.float32(1 / 16), iters, None, C.byref(ms))

@@ -151,6 +151,8 @@ def _declare(lib: C.CDLL) -> None:
         "xp_qk_norm_rope_append": (i32, [vp, vp, vp, vp, vp, vp, vp, vp, vp, u32, u32, u32,
                                          u32, f32, f32, vp]),
         "xp_attention_decode": (i32, [vp, vp, vp, vp, u32, u32, u32, u32, u32, f32, vp]),
+        "xp_attention_decode_timed": (i32, [vp, vp, vp, vp, u32, u32, u32, u32, u32, u32, f32, u32,
+                                            vp, C.POINTER(C.c_float)]),
         "xp_geglu": (i32, [vp, vp, vp, u32, vp]),
         "xp_add_residual": (i32, [vp, vp, u32, vp]),
         "xp_kv_append_f16": (i32, [vp, vp, u32, u32, vp]),

@@ -268,7 +268,7 @@ int xp_batch_create(const xp_session* weights, uint32_t n_seq, uint32_t max_seq,
     gemm_need(c.vocab, H);
     b.part_cap = part_cap;
     b.tickets_cap = tick;
-    b.attn_part_seq = attn_partial_floats(c.n_kv_heads, c.n_heads, c.head_dim, max_seq);
+    b.attn_part_seq = attn_partial_floats(c.n_kv_heads, c.n_heads, c.head_dim);
     const size_t kvseq = size_t(max_seq) * kvd;                 // fp16 elements per (layer, K/V, seq)
     std::vector<size_t> sz = {
         size_t(c.n_layers) * 2 * B * kvseq * 2,                 // KV caches

@@ -106,13 +106,12 @@ int check_config(const xp_config& c) {
     if (c.vocab % 64 || (c.n_kv_heads * c.head_dim) % 64)
         return set_error(XP_E_ARG, "config: vocab and kv_dim must be multiples of 64");
     const uint32_t grp = c.n_heads % c.n_kv_heads ? 0 : c.n_heads / c.n_kv_heads;
-    if ((c.head_dim != 64 && c.head_dim != 128 && c.head_dim != 256 && c.head_dim != 512) ||
-        (grp != 1 && grp != 2 && grp != 4 && grp != 8) || (grp == 8 && c.head_dim == 512))
-        return set_error(XP_E_ARG, "config: head_dim=%u (64/128/256/512), heads %u over %u kv "
-                         "heads (1, 2, 4 or 8 per kv head)", c.head_dim, c.n_heads, c.n_kv_heads);
+    if (c.head_dim != 256 || (grp != 1 && grp != 2 && grp != 4))
+        return set_error(XP_E_ARG, "config: head_dim=%u (must be 256), heads %u over %u kv "
+                         "heads (1, 2 or 4 per kv head)", c.head_dim, c.n_heads, c.n_kv_heads);
     if (c.max_seq > 8192)
-        return set_error(XP_E_ARG, "config: max_seq=%u > 8192 (the attention split plan's "
-                         "limit)", c.max_seq);
+        return set_error(XP_E_ARG, "config: max_seq=%u > 8192 (the reference's context limit)",
+                         c.max_seq);
     if (c.hidden > 8192)
         return set_error(XP_E_ARG, "config: hidden=%u > 8192", c.hidden);
     if (c.scale_fmt != XP_SCALE_F16_QUAD && c.scale_fmt != XP_SCALE_BF16_QUAD &&
@@ -682,7 +681,7 @@ int xp_session_create(const xp_config* cfg, xp_session** out) {
         mvp = std::max(mvp, mv_partial_floats(c.ffn, H, 0, s.n_cu));
         mvp = std::max(mvp, mv_partial_floats(H, c.vocab, 0, s.n_cu));
         s.mv_partial_cap = std::max<size_t>(mvp, 64);
-        const size_t attnp = attn_partial_floats(c.n_kv_heads, c.n_heads, c.head_dim, c.max_seq);
+        const size_t attnp = attn_partial_floats(c.n_kv_heads, c.n_heads, c.head_dim);
         const uint32_t nc = c.sample_mode == 1 ? 4 * c.topk_parts : 4;
         const size_t sizes[] = {
             H * 4, std::max(H, qd) * 4, H * 4, qd * 4, kvd * 4, kvd * 4, qd * 4, kvd * 4, qd * 4,

@@ -68,17 +68,13 @@ constexpr int      kTkMaxGrid   = 1024;
 constexpr uint32_t kSpinLimit   = 1u << 24;
 constexpr int      kTkBig       = 17408;                 // floats of stage scratch
 constexpr int      kTkMaxLayers = 64;
-// Cache policy of the slot buffer operations: device scope (sc1), i.e.
-// written through to, and read from, the point where all XCDs are coherent.
-constexpr int      kAuxDev      = 16;
-// Buffer descriptor word 3 for raw (untyped, unswizzled) gfx9 buffers.
-constexpr int      kRsrcWord3   = 0x00020000;
+// Slot buffer operations use device scope (sc1, kAuxDev) on raw buffer
+// resources (kRsrcWord3).
 // Poll back-off of the gate/up stage's wait (which spans QKV, attention,
 // combine and O), in units of 64 cycles.
 constexpr int      kGuSleep     = 32;
 
 typedef unsigned long long ll_t;
-typedef __amdgpu_buffer_rsrc_t rsrc_t;
 
 // The model shape the kernel is compiled for.
 template <uint32_t H_, uint32_t FFN_, uint32_t NH_>
@@ -1112,6 +1108,13 @@ int launch_token(const TokArgs& a, uint32_t grid, hipStream_t st) {
     TokArgs copy = a;
     void* args[] = {&copy};
     hipError_t e = hipLaunchCooperativeKernel(fn, dim3(grid), dim3(kTkThreads), args, lds, st);
+    if (e == hipErrorIllegalState)
+        // The runtime refuses cooperative launches on a device where another
+        // process has already made one (measured on MI355X / ROCm 7).
+        return set_error(XP_E_HIP, "token kernel: cooperative launch of %u workgroups refused (%s): "
+                         "another process on this GPU has made a cooperative launch; run one "
+                         "decode process per GPU, or use the graph execution mode", grid,
+                         hipGetErrorString(e));
     if (e != hipSuccess)
         return set_error(XP_E_HIP, "token kernel: cooperative launch of %u workgroups -> %s", grid,
                          hipGetErrorString(e));

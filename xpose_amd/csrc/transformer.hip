@@ -136,22 +136,65 @@ __global__ __launch_bounds__(256) void qk_norm_rope_append_kernel(QkArgs a, Rope
 }
 
 // ---- decode attention (split-span, fp16 KV) ----------------------------------
-// Grid: (nsplit, kv_heads). Workgroup (s, g) takes a contiguous chunk of the
-// attended keys [kv_start + s*chunk, ...) for the G query heads that share kv
-// head g, reading every key and value once for all G heads (the mq4 idea,
-// llm_transformer.cl:418-464, 499-557):
-//   scores  head_dim/8 threads per key, 16-byte fp16 loads, q held in
-//           registers, shuffle reduction; several keys in flight per thread
-//   softmax one wave per head over the chunk (max, exp, sum)
-//   values  head_dim/2 threads per key, 4-byte loads, several keys in flight
+// Grid: (nsplit, kv_heads, batch). Workgroup (s, g, b) takes a contiguous chunk
+// of sequence b's attended keys for the G query heads that share kv head g,
+// reading every key and value once for all G heads (the mq4 idea,
+// llm_transformer.cl:418-464, 499-557), in passes of up to 128 keys:
+//   loads   32 lanes per 512-byte key row (16-byte loads, 8 dims per lane);
+//           lane group kp = tid / 32 takes keys kp, kp + 16, ..., kp + 112,
+//           and all 8 K and 8 V loads of a pass are in flight together
+//   scores  each lane dots its 8 dims with the G query heads; the G x 8
+//           partial dots of a row group are summed by a reduce-scatter over
+//           its 32 lanes (5 swizzle steps, each halving the values a lane
+//           holds), so lane i ends with one (head, key) score
+//   softmax one wave per head over the pass, online across passes (running
+//           max and sum, the accumulated values rescaled by exp(m_old - m_new))
+//   values  the same lanes accumulate p x v for their 8 dims, then the 16 row
+//           groups are summed (lane pairs by shuffle, waves through LDS)
 // Each split publishes (max, sum of exp, unnormalised o) per head; the last
-// workgroup of kv head g to arrive (arrival ticket) rescales and sums the
-// splits in ascending order — softmax_rows_finish's online combine
-// (llm_transformer.cl:385-405). One split writes the normalised output.
-constexpr int kAttnThreads  = 256;
-constexpr int kAttnMinChunk = 32;    // keys per workgroup at short spans
-constexpr int kAttnChunk    = 128;   // most keys one workgroup takes
-constexpr int kAttnMaxSplit = 64;    // workgroups per kv head
+// workgroup of (b, g) to arrive (arrival ticket) rescales and sums the splits —
+// softmax_rows_finish's online combine (llm_transformer.cl:385-405) — with
+// 16-byte device-scope loads spread over all its threads, in a fixed order.
+constexpr int kAttnThreads  = 512;
+constexpr int kAttnHD       = 256;                        // head_dim
+constexpr int kAttnLanes    = kAttnHD / 8;                // lanes per key row
+constexpr int kAttnRows     = kAttnThreads / kAttnLanes;  // 16 row groups
+constexpr int kAttnU        = 8;                          // keys per lane per pass
+constexpr int kAttnPass     = kAttnRows * kAttnU;         // 128 keys per pass
+constexpr int kAttnMinChunk = 32;                         // fewest keys per split
+constexpr int kAttnMaxSplit = 64;                         // splits per (sequence, kv head)
+constexpr int kAttnMaxG     = 4;                          // query heads per kv head
+constexpr int kAttnStat     = 8;                          // floats of (max[4], sum[4]) per record
+
+__host__ __device__ constexpr uint32_t attn_record(uint32_t G) { return kAttnStat + G * kAttnHD; }
+
+template <int M>
+__device__ __forceinline__ float swz_xor(float x) {   // x of lane ^ M within 32 lanes
+    return __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(x), (M << 10) | 0x1F));
+}
+// Reduce-scatter of v[0..N) over the 32 lanes of a row group, masks M, M/2 ..
+// 1: each step keeps the lower (lane bit clear) or upper half of the values and
+// adds the partner's copy of it; once one value is left it is summed plainly.
+// Lane l ends with the sum of value (l % 32) / (32 / N) (N <= 32).
+template <int N, int M>
+__device__ __forceinline__ void reduce_scatter32(float* v, uint32_t lane) {
+    if constexpr (M >= 1) {
+        if constexpr (N >= 2) {
+            constexpr int H = N / 2;
+            const bool up = (lane & M) != 0;
+#pragma unroll
+            for (int i = 0; i < H; ++i) {
+                const float keep = up ? v[H + i] : v[i];
+                const float send = up ? v[i] : v[H + i];
+                v[i] = keep + swz_xor<M>(send);
+            }
+            reduce_scatter32<H, M / 2>(v, lane);
+        } else {
+            v[0] += swz_xor<M>(v[0]);
+            reduce_scatter32<1, M / 2>(v, lane);
+        }
+    }
+}
 
 __device__ __forceinline__ void attn_range(const AttnArgs& a, uint32_t& span, uint32_t& kv0) {
     if (a.pos_dev) {
@@ -164,18 +207,22 @@ __device__ __forceinline__ void attn_range(const AttnArgs& a, uint32_t& span, ui
     }
 }
 
-template <int G, int HD>
+__device__ __forceinline__ void f16x8(float (&f)[8], u32x4 w) {
+    f[0] = f16_bits_to_f32(w.x); f[1] = f16_bits_to_f32(w.x >> 16);
+    f[2] = f16_bits_to_f32(w.y); f[3] = f16_bits_to_f32(w.y >> 16);
+    f[4] = f16_bits_to_f32(w.z); f[5] = f16_bits_to_f32(w.z >> 16);
+    f[6] = f16_bits_to_f32(w.w); f[7] = f16_bits_to_f32(w.w >> 16);
+}
+
+template <int G>
 __global__ __launch_bounds__(kAttnThreads) void attention_decode_kernel(AttnArgs a) {
-    constexpr int TPK = HD / 8;                 // threads per key (scores)
-    constexpr int KPP = kAttnThreads / TPK;     // keys per pass (scores)
-    constexpr int TPV = HD / 2;                 // threads per key (values)
-    constexpr int KPV = kAttnThreads / TPV;     // keys per pass (values)
-    constexpr int ROW = 2 + HD;
-    __shared__ float ps[G * kAttnChunk];
-    __shared__ float red[KPV * G * HD];
-    __shared__ float mstat[G], lstat[G];
-    __shared__ float fs[kAttnMaxSplit * G];
-    __shared__ float ls[kAttnMaxSplit * G];
+    constexpr int HD = kAttnHD, NV = G * kAttnU, DUP = 32 / NV;
+    constexpr uint32_t REC = attn_record(G);
+    constexpr int NCOL = G * HD / 4, R = kAttnThreads / NCOL;   // combine: float4 columns, groups
+    __shared__ float ps[G][kAttnPass];
+    __shared__ float run[3][G];                  // running max, running sum, pass rescale
+    __shared__ __attribute__((aligned(16))) float red[kAttnThreads / kWave][G * HD];
+    __shared__ float fs[kAttnMaxSplit][G];
     __shared__ uint32_t last;
     {   // batched sequence blockIdx.z
         const uint32_t b = blockIdx.z;
@@ -189,122 +236,136 @@ __global__ __launch_bounds__(kAttnThreads) void attention_decode_kernel(AttnArgs
     uint32_t span, kv0;
     attn_range(a, span, kv0);
     const uint32_t g = blockIdx.y, s = blockIdx.x;
-    const uint32_t chunk = (span + a.nsplit - 1) / a.nsplit;
-    const uint32_t j0 = s * chunk;
-    const uint32_t j1 = min(j0 + chunk, span);
-    const int nk = j1 > j0 ? int(j1 - j0) : 0;
-    const int tid = threadIdx.x;
+    uint32_t chunk = (span + a.nsplit - 1) / a.nsplit;
+    if (chunk < uint32_t(kAttnMinChunk)) chunk = kAttnMinChunk;
+    const uint32_t j0 = min(s * chunk, span);
+    const int nk = int(min(j0 + chunk, span) - j0);
+    const int tid = threadIdx.x, lane = tid % kWave, wave = tid / kWave;
+    const int sub = tid % kAttnLanes, kp = tid / kAttnLanes;
     const size_t rowstride = size_t(a.kv_heads) * HD;   // fp16 elements per cache row
-    const uint16_t* kbase = a.kc + size_t(kv0 + j0) * rowstride + size_t(g) * HD;
-    const uint16_t* vbase = a.vc + size_t(kv0 + j0) * rowstride + size_t(g) * HD;
+    const uint16_t* kbase = a.kc + size_t(kv0 + j0) * rowstride + size_t(g) * HD + sub * 8;
+    const uint16_t* vbase = a.vc + size_t(kv0 + j0) * rowstride + size_t(g) * HD + sub * 8;
 
-    // ---- scores
-    {
-        const int sub = tid % TPK, kp = tid / TPK;
-        float q[G][8];
+    float q[G][8], o[G][8];
 #pragma unroll
-        for (int h = 0; h < G; ++h)
+    for (int h = 0; h < G; ++h) {
+        const float4* qp = reinterpret_cast<const float4*>(a.q + (size_t(g) * G + h) * HD + sub * 8);
+        const float4 q0 = qp[0], q1 = qp[1];
+        q[h][0] = q0.x; q[h][1] = q0.y; q[h][2] = q0.z; q[h][3] = q0.w;
+        q[h][4] = q1.x; q[h][5] = q1.y; q[h][6] = q1.z; q[h][7] = q1.w;
 #pragma unroll
-            for (int e = 0; e < 8; ++e) q[h][e] = a.q[(size_t(g) * G + h) * HD + sub * 8 + e];
-        for (int base = 0; base < nk; base += 4 * KPP) {
-            u32x4 kw[4];
-#pragma unroll
-            for (int u = 0; u < 4; ++u) {
-                const int j = base + u * KPP + kp;
-                kw[u] = (j < nk) ? *reinterpret_cast<const u32x4*>(kbase + size_t(j) * rowstride + sub * 8)
-                                 : u32x4{0u, 0u, 0u, 0u};
-            }
-#pragma unroll
-            for (int u = 0; u < 4; ++u) {
-                const int j = base + u * KPP + kp;
-                float kf[8];
-                kf[0] = f16_bits_to_f32(kw[u].x); kf[1] = f16_bits_to_f32(kw[u].x >> 16);
-                kf[2] = f16_bits_to_f32(kw[u].y); kf[3] = f16_bits_to_f32(kw[u].y >> 16);
-                kf[4] = f16_bits_to_f32(kw[u].z); kf[5] = f16_bits_to_f32(kw[u].z >> 16);
-                kf[6] = f16_bits_to_f32(kw[u].w); kf[7] = f16_bits_to_f32(kw[u].w >> 16);
-#pragma unroll
-                for (int h = 0; h < G; ++h) {
-                    float d = 0.0f;
-#pragma unroll
-                    for (int e = 0; e < 8; ++e) d = fmaf(q[h][e], kf[e], d);
-#pragma unroll
-                    for (int o = TPK / 2; o > 0; o >>= 1) d += __shfl_xor(d, o, kWave);
-                    if (sub == 0 && j < nk) ps[h * kAttnChunk + j] = d * a.scale;
-                }
-            }
-        }
+        for (int e = 0; e < 8; ++e) o[h][e] = 0.0f;
     }
-    __syncthreads();
-    // ---- chunk softmax, one wave per head
-    for (int h = tid / kWave; h < G; h += kAttnThreads / kWave) {
-        const int l = tid % kWave;
-        float m = -INFINITY;
-        for (int j = l; j < nk; j += kWave) m = fmaxf(m, ps[h * kAttnChunk + j]);
-        m = wave_max(m);
-        float sum = 0.0f;
-        for (int j = l; j < nk; j += kWave) {
-            const float e = expf(ps[h * kAttnChunk + j] - m);
-            ps[h * kAttnChunk + j] = e;
-            sum += e;
-        }
-        sum = wave_sum(sum);
-        if (l == 0) { mstat[h] = m; lstat[h] = sum; }
+    if (tid < G) {
+        run[0][tid] = -INFINITY;
+        run[1][tid] = 0.0f;
     }
-    __syncthreads();
-    // ---- weighted values
-    {
-        const int dp = tid % TPV, ks = tid / TPV;
-        float o[G][2];
+    for (int c0 = 0; c0 < nk; c0 += kAttnPass) {
+        u32x4 kw[kAttnU], vw[kAttnU];
 #pragma unroll
-        for (int h = 0; h < G; ++h) o[h][0] = o[h][1] = 0.0f;
-        for (int base = 0; base < nk; base += 4 * KPV) {
-            uint32_t vw[4];
+        for (int u = 0; u < kAttnU; ++u) {
+            const int j = c0 + kp + kAttnRows * u;
+            kw[u] = j < nk ? ldg4(kbase + size_t(j) * rowstride) : u32x4{0u, 0u, 0u, 0u};
+        }
 #pragma unroll
-            for (int u = 0; u < 4; ++u) {
-                const int j = base + u * KPV + ks;
-                vw[u] = (j < nk) ? *reinterpret_cast<const uint32_t*>(vbase + size_t(j) * rowstride + dp * 2)
-                                 : 0u;
-            }
+        for (int u = 0; u < kAttnU; ++u) {
+            const int j = c0 + kp + kAttnRows * u;
+            vw[u] = j < nk ? ldg4(vbase + size_t(j) * rowstride) : u32x4{0u, 0u, 0u, 0u};
+        }
+        // ---- scores
+        float sv[NV];
 #pragma unroll
-            for (int u = 0; u < 4; ++u) {
-                const int j = base + u * KPV + ks;
-                if (j < nk) {
-                    const float v0 = f16_bits_to_f32(vw[u]), v1 = f16_bits_to_f32(vw[u] >> 16);
+        for (int u = 0; u < kAttnU; ++u) {
+            float kf[8];
+            f16x8(kf, kw[u]);
 #pragma unroll
-                    for (int h = 0; h < G; ++h) {
-                        const float p = ps[h * kAttnChunk + j];
-                        o[h][0] = fmaf(p, v0, o[h][0]);
-                        o[h][1] = fmaf(p, v1, o[h][1]);
-                    }
-                }
+            for (int h = 0; h < G; ++h) {
+                float d = 0.0f;
+#pragma unroll
+                for (int e = 0; e < 8; ++e) d = fmaf(q[h][e], kf[e], d);
+                sv[h * kAttnU + u] = d;
             }
         }
+        reduce_scatter32<NV, 16>(sv, uint32_t(lane));
+        {
+            const int idx = (lane % 32) / DUP, h = idx / kAttnU, u = idx % kAttnU;
+            const int j = kp + kAttnRows * u;
+            if (lane % DUP == 0) ps[h][j] = (c0 + j < nk) ? sv[0] * a.scale : -INFINITY;
+        }
+        __syncthreads();
+        // ---- softmax of the pass, online across passes: wave h takes head h
+        if (wave < G) {
+            const int h = wave;
+            const float s0 = ps[h][lane], s1 = ps[h][lane + kWave];
+            const float mold = run[0][h];
+            const float mnew = fmaxf(mold, wave_max(fmaxf(s0, s1)));   // finite: key c0 is live
+            const float p0 = expf(s0 - mnew), p1 = expf(s1 - mnew);
+            ps[h][lane] = p0;
+            ps[h][lane + kWave] = p1;
+            const float sum = wave_sum(p0 + p1);
+            if (lane == 0) {
+                const float alpha = expf(mold - mnew);   // 0 on the first pass
+                run[0][h] = mnew;
+                run[1][h] = run[1][h] * alpha + sum;
+                run[2][h] = alpha;
+            }
+        }
+        __syncthreads();
+        // ---- weighted values
 #pragma unroll
         for (int h = 0; h < G; ++h) {
-            red[(ks * G + h) * HD + dp * 2] = o[h][0];
-            red[(ks * G + h) * HD + dp * 2 + 1] = o[h][1];
+            const float al = run[2][h];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) o[h][e] *= al;
+        }
+#pragma unroll
+        for (int u = 0; u < kAttnU; ++u) {
+            float vf[8];
+            f16x8(vf, vw[u]);
+            const int j = kp + kAttnRows * u;
+#pragma unroll
+            for (int h = 0; h < G; ++h) {
+                const float p = ps[h][j];
+#pragma unroll
+                for (int e = 0; e < 8; ++e) o[h][e] = fmaf(p, vf[e], o[h][e]);
+            }
+        }
+        __syncthreads();   // ps and run[2] are rewritten by the next pass
+    }
+    // ---- sum the 16 row groups: lane pairs (l, l + 32), then the 8 waves
+#pragma unroll
+    for (int h = 0; h < G; ++h)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) o[h][e] += __shfl_xor(o[h][e], 32, kWave);
+    if (lane < 32) {
+#pragma unroll
+        for (int h = 0; h < G; ++h) {
+            float4* r4 = reinterpret_cast<float4*>(&red[wave][h * HD + sub * 8]);
+            r4[0] = float4{o[h][0], o[h][1], o[h][2], o[h][3]};
+            r4[1] = float4{o[h][4], o[h][5], o[h][6], o[h][7]};
         }
     }
     __syncthreads();
     if (a.nsplit == 1) {
         for (int i = tid; i < G * HD; i += kAttnThreads) {
-            const int h = i / HD;
             float acc = 0.0f;
-            for (int k2 = 0; k2 < KPV; ++k2) acc += red[k2 * G * HD + i];
-            a.out[size_t(g) * G * HD + i] = acc / lstat[h];
+#pragma unroll
+            for (int w = 0; w < kAttnThreads / kWave; ++w) acc += red[w][i];
+            a.out[size_t(g) * G * HD + i] = acc / run[1][i / HD];
         }
         return;
     }
-    float* part = a.part + (size_t(g) * a.nsplit + s) * G * ROW;
+    float* part = a.part + size_t(g) * a.nsplit * REC;
+    float* rec = part + size_t(s) * REC;
     for (int i = tid; i < G * HD; i += kAttnThreads) {
-        const int h = i / HD, d = i % HD;
         float acc = 0.0f;
-        for (int k2 = 0; k2 < KPV; ++k2) acc += red[k2 * G * HD + i];
-        st_dev(part + h * ROW + 2 + d, acc);
+#pragma unroll
+        for (int w = 0; w < kAttnThreads / kWave; ++w) acc += red[w][i];
+        st_dev(rec + kAttnStat + i, acc);
     }
     if (tid < G) {
-        st_dev(part + tid * ROW, nk > 0 ? mstat[tid] : -INFINITY);
-        st_dev(part + tid * ROW + 1, nk > 0 ? lstat[tid] : 0.0f);
+        st_dev(rec + tid, run[0][tid]);                 // -inf for an empty split
+        st_dev(rec + kAttnMaxG + tid, run[1][tid]);     // 0 for an empty split
     }
     wait_mem();
     __syncthreads();
@@ -312,43 +373,58 @@ __global__ __launch_bounds__(kAttnThreads) void attention_decode_kernel(AttnArgs
     __syncthreads();
     if (last != a.nsplit - 1) return;
 
-    // ---- combine (last workgroup): factors f[p][h] = exp(m_p - M) in LDS
-    const float* base = a.part + size_t(g) * a.nsplit * G * ROW;
-    for (uint32_t i = tid; i < a.nsplit * G; i += kAttnThreads) {
-        const float* r = base + size_t(i) * ROW;   // i = p * G + h
-        const float m = ld_dev(r), l = ld_dev(r + 1);
-        fs[i] = l > 0.0f ? m : -INFINITY;
-        ls[i] = l;
+    // ---- combine (last workgroup). Thread (r, col) takes float4 column col of
+    // the output over splits r, r + R, ...; its loads are issued before wave h
+    // reads head h's statistics (one split per lane) and computes the factors
+    // f_p = exp(m_p - M) and L = sum_p l_p f_p, so both wait on one round trip.
+    {
+        constexpr int B = kAttnMaxSplit / R;
+        const int col = tid % NCOL, r = tid / NCOL, h = col * 4 / HD;
+        const rsrc_t rs = make_rsrc(part, a.nsplit * REC * 4u);
+        const uint32_t off = (kAttnStat + col * 4) * 4u;
+        u32x4 v[B];
+#pragma unroll
+        for (int i = 0; i < B; ++i) {
+            const uint32_t p = r + i * R;
+            v[i] = p < a.nsplit ? ld_dev16(rs, p * REC * 4u + off) : u32x4{0u, 0u, 0u, 0u};
+        }
+        if (wave < G) {
+            const int hh = wave;
+            const bool live = uint32_t(lane) < a.nsplit;
+            const float m = live ? ld_dev(part + size_t(lane) * REC + hh) : -INFINITY;
+            const float l = live ? ld_dev(part + size_t(lane) * REC + kAttnMaxG + hh) : 0.0f;
+            const float mm = l > 0.0f ? m : -INFINITY;
+            const float M = wave_max(mm);
+            const float f = mm == -INFINITY ? 0.0f : expf(mm - M);
+            const float L = wave_sum(l * f);
+            if (live) fs[lane][hh] = f;
+            if (lane == 0) run[1][hh] = L;
+        }
+        __syncthreads();
+        float4 acc = float4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int i = 0; i < B; ++i) {
+            const uint32_t p = r + i * R;
+            const float f = p < a.nsplit ? fs[p][h] : 0.0f;
+            acc.x = fmaf(__uint_as_float(v[i].x), f, acc.x);
+            acc.y = fmaf(__uint_as_float(v[i].y), f, acc.y);
+            acc.z = fmaf(__uint_as_float(v[i].z), f, acc.z);
+            acc.w = fmaf(__uint_as_float(v[i].w), f, acc.w);
+        }
+        reinterpret_cast<float4*>(&red[0][0])[r * NCOL + col] = acc;
     }
     __syncthreads();
-    if (tid < G) {
-        float M = -INFINITY;
-        for (uint32_t p = 0; p < a.nsplit; ++p) M = fmaxf(M, fs[p * G + tid]);
-        float L = 0.0f;
-        for (uint32_t p = 0; p < a.nsplit; ++p) {
-            const float m = fs[p * G + tid];
-            const float f = (m == -INFINITY) ? 0.0f : expf(m - M);
-            L += ls[p * G + tid] * f;
-            fs[p * G + tid] = f;
-        }
-        lstat[tid] = L;
-    }
-    __syncthreads();
-    const size_t pstride = size_t(G) * ROW;
-    for (int i = tid; i < G * HD; i += kAttnThreads) {
-        const int h = i / HD, d = i % HD;
-        const float* col = base + size_t(h) * ROW + 2 + d;
-        float o = 0.0f;
-        uint32_t p = 0;
-        for (; p + 8 <= a.nsplit; p += 8) {
-            float v[8];
+    if (tid < NCOL) {
+        const float4* r4 = reinterpret_cast<const float4*>(&red[0][0]);
+        float4 t = r4[tid];
 #pragma unroll
-            for (int q = 0; q < 8; ++q) v[q] = ld_dev(col + (p + q) * pstride);
-#pragma unroll
-            for (int q = 0; q < 8; ++q) o = fmaf(v[q], fs[(p + q) * G + h], o);
+        for (int r = 1; r < R; ++r) {
+            const float4 v = r4[r * NCOL + tid];
+            t.x += v.x; t.y += v.y; t.z += v.z; t.w += v.w;
         }
-        for (; p < a.nsplit; ++p) o = fmaf(ld_dev(col + p * pstride), fs[p * G + h], o);
-        a.out[size_t(g) * G * HD + i] = o / lstat[h];
+        const float inv = 1.0f / run[1][tid * 4 / HD];
+        reinterpret_cast<float4*>(a.out + size_t(g) * G * HD)[tid] =
+            float4{t.x * inv, t.y * inv, t.z * inv, t.w * inv};
     }
     if (tid == 0) st_dev(&a.tickets[g], 0u);
 }
@@ -387,59 +463,55 @@ int launch_qk(const QkArgs& a, float theta, hipStream_t st) {
     return XP_OK;
 }
 
-uint32_t attn_splits(uint32_t span) {
-    uint32_t n = (span + kAttnMinChunk - 1) / kAttnMinChunk;
+uint32_t attn_splits(uint32_t max_span, uint32_t batch, uint32_t kv_heads) {
+    // Enough workgroups to give every CU one (256), at most two passes of keys
+    // per split, at least kAttnMinChunk keys per split, at most kAttnMaxSplit.
+    const uint32_t units = (batch ? batch : 1) * (kv_heads ? kv_heads : 1);
+    uint32_t n = (256 + units - 1) / units;
+    const uint32_t by_len = (max_span + 2 * kAttnPass - 1) / (2 * kAttnPass);
+    if (n < by_len) n = by_len;
+    const uint32_t most = (max_span + kAttnMinChunk - 1) / kAttnMinChunk;
+    if (n > most) n = most;
     if (n > uint32_t(kAttnMaxSplit)) n = kAttnMaxSplit;
     return n < 1 ? 1 : n;
 }
 
-size_t attn_partial_floats(uint32_t kv_heads, uint32_t n_heads, uint32_t head_dim,
-                           uint32_t max_span) {
-    return size_t(kv_heads) * attn_splits(max_span) * (n_heads / kv_heads) * (2 + head_dim);
+size_t attn_partial_floats(uint32_t kv_heads, uint32_t n_heads, uint32_t head_dim) {
+    (void)head_dim;
+    return size_t(kv_heads) * kAttnMaxSplit * attn_record(kv_heads ? n_heads / kv_heads : 1);
 }
 
 int launch_attention(AttnArgs a, uint32_t max_span, hipStream_t st) {
-    if (a.head_dim != 64 && a.head_dim != 128 && a.head_dim != 256 && a.head_dim != 512)
-        return set_error(XP_E_ARG, "attention: head_dim=%u must be 64, 128, 256 or 512",
-                         a.head_dim);
+    if (a.head_dim != uint32_t(kAttnHD))
+        return set_error(XP_E_ARG, "attention: head_dim=%u must be %d", a.head_dim, kAttnHD);
     if (a.kv_heads == 0 || a.n_heads % a.kv_heads)
         return set_error(XP_E_ARG, "attention: n_heads=%u not a multiple of kv_heads=%u",
                          a.n_heads, a.kv_heads);
-    if (max_span == 0 || max_span > uint32_t(kAttnMaxSplit * kAttnChunk))
-        return set_error(XP_E_ARG, "attention: span %u outside [1, %d]", max_span,
-                         kAttnMaxSplit * kAttnChunk);
+    if (max_span == 0) return set_error(XP_E_ARG, "attention: empty span");
     a.group = a.n_heads / a.kv_heads;
     const uint32_t G = a.group;
-    if (G != 1 && G != 2 && G != 4 && G != 8)
-        return set_error(XP_E_ARG, "attention: %u query heads per kv head (1, 2, 4 or 8)", G);
-    a.nsplit = attn_splits(max_span);
+    if (G != 1 && G != 2 && G != 4)
+        return set_error(XP_E_ARG, "attention: %u query heads per kv head (1, 2 or 4)", G);
     if (a.batch == 0) a.batch = 1;
+    a.nsplit = attn_splits(max_span, a.batch, a.kv_heads);
     if (a.batch > 1 && a.nsplit > 1 && (!a.part || !a.tickets || a.bpart == 0))
         return set_error(XP_E_ARG, "attention: a batch needs its own partials and tickets");
     if (a.nsplit > 1 && (!a.part || !a.tickets)) {
         DeviceScratch* sc = scratch();
         if (!sc) return XP_E_HIP;
-        const size_t need = size_t(a.kv_heads) * a.nsplit * G * (2 + a.head_dim);
+        const size_t need = attn_partial_floats(a.kv_heads, a.n_heads, a.head_dim);
         if (!ensure_partial(sc, need) || !ensure_tickets(sc, a.kv_heads)) return XP_E_NOMEM;
         a.part = sc->partial;
         a.tickets = sc->tickets;
     }
     const dim3 grid(a.nsplit, a.kv_heads, a.batch), block(kAttnThreads);
-#define XP_ATTN(GG, HH)                                                                    \
-    if (G == GG && a.head_dim == HH) {                                                     \
-        hipLaunchKernelGGL((attention_decode_kernel<GG, HH>), grid, block, 0, st, a);      \
-        hipError_t e = hipGetLastError();                                                  \
-        if (e != hipSuccess)                                                               \
-            return set_error(XP_E_HIP, "attention: launch -> %s", hipGetErrorString(e));   \
-        return XP_OK;                                                                      \
-    }
-    XP_ATTN(1, 64) XP_ATTN(1, 128) XP_ATTN(1, 256) XP_ATTN(1, 512)
-    XP_ATTN(2, 64) XP_ATTN(2, 128) XP_ATTN(2, 256) XP_ATTN(2, 512)
-    XP_ATTN(4, 64) XP_ATTN(4, 128) XP_ATTN(4, 256) XP_ATTN(4, 512)
-    XP_ATTN(8, 64) XP_ATTN(8, 128) XP_ATTN(8, 256)
-#undef XP_ATTN
-    return set_error(XP_E_ARG, "attention: no kernel for %u heads/kv head at head_dim %u", G,
-                     a.head_dim);
+    if (G == 1) hipLaunchKernelGGL(attention_decode_kernel<1>, grid, block, 0, st, a);
+    else if (G == 2) hipLaunchKernelGGL(attention_decode_kernel<2>, grid, block, 0, st, a);
+    else hipLaunchKernelGGL(attention_decode_kernel<4>, grid, block, 0, st, a);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess)
+        return set_error(XP_E_HIP, "attention: launch -> %s", hipGetErrorString(e));
+    return XP_OK;
 }
 
 }  // namespace xp
@@ -508,6 +580,35 @@ int xp_attention_decode(float* out, const float* q, const uint16_t* kcache,
     a.n_heads = n_heads; a.kv_heads = kv_heads; a.head_dim = head_dim;
     a.span = span; a.kv_start = kv_start; a.scale = scale;
     return launch_attention(a, span, as_stream(stream));
+}
+
+int xp_attention_decode_timed(float* out, const float* q, const uint16_t* const* kcaches,
+                              const uint16_t* const* vcaches, uint32_t ncopies, uint32_t n_heads,
+                              uint32_t kv_heads, uint32_t head_dim, uint32_t span,
+                              uint32_t kv_start, float scale, uint32_t iters, xp_stream stream,
+                              float* ms) {
+    XP_REQUIRE(kcaches && vcaches && ms && ncopies > 0 && iters > 0, "bad arguments");
+    hipStream_t st = as_stream(stream);
+    hipEvent_t e0 = nullptr, e1 = nullptr;
+    XP_HIP(hipEventCreate(&e0));
+    XP_HIP(hipEventCreate(&e1));
+    int rc = XP_OK;
+    // One untimed pass over every copy so the split scratch is sized before timing.
+    for (uint32_t i = 0; i < ncopies && rc == XP_OK; ++i)
+        rc = xp_attention_decode(out, q, kcaches[i], vcaches[i], n_heads, kv_heads, head_dim,
+                                 span, kv_start, scale, stream);
+    if (rc == XP_OK && hipStreamSynchronize(st) != hipSuccess) rc = set_error(XP_E_HIP, "sync");
+    if (rc == XP_OK && hipEventRecord(e0, st) != hipSuccess) rc = set_error(XP_E_HIP, "event");
+    for (uint32_t i = 0; i < iters && rc == XP_OK; ++i)
+        rc = xp_attention_decode(out, q, kcaches[i % ncopies], vcaches[i % ncopies], n_heads,
+                                 kv_heads, head_dim, span, kv_start, scale, stream);
+    if (rc == XP_OK && hipEventRecord(e1, st) != hipSuccess) rc = set_error(XP_E_HIP, "event");
+    if (rc == XP_OK && hipEventSynchronize(e1) != hipSuccess) rc = set_error(XP_E_HIP, "sync");
+    if (rc == XP_OK && hipEventElapsedTime(ms, e0, e1) != hipSuccess)
+        rc = set_error(XP_E_HIP, "elapsed");
+    (void)hipEventDestroy(e0);
+    (void)hipEventDestroy(e1);
+    return rc;
 }
 
 int xp_geglu(float* out, const float* gate, const float* up, uint32_t n, xp_stream stream) {

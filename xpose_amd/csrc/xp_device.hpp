@@ -151,6 +151,18 @@ __device__ __forceinline__ unsigned long long ld_dev64(const unsigned long long*
     return __hip_atomic_load((XP_GLOBAL unsigned long long*)p, __ATOMIC_RELAXED,
                              __HIP_MEMORY_SCOPE_AGENT);
 }
+// Raw buffer resources for 16-byte device-scope accesses. Cache policy sc1
+// (aux 16) writes through to, and reads from, the point where all XCDs are
+// coherent; word 3 describes a raw (untyped, unswizzled) gfx9 buffer.
+typedef __amdgpu_buffer_rsrc_t rsrc_t;
+constexpr int kAuxDev    = 16;
+constexpr int kRsrcWord3 = 0x00020000;
+__device__ __forceinline__ rsrc_t make_rsrc(const void* p, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), short(0), int(bytes), kRsrcWord3);
+}
+__device__ __forceinline__ u32x4 ld_dev16(rsrc_t r, uint32_t byte_off) {
+    return __builtin_amdgcn_raw_buffer_load_b128(r, int(byte_off), 0, kAuxDev);
+}
 // Blocks until every memory operation this wave issued has completed.
 __device__ __forceinline__ void wait_mem() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 // Arrival ticket: returns the number of arrivals before this one.

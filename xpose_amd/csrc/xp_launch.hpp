@@ -58,7 +58,7 @@ struct AttnArgs {
     uint32_t window;           // 0 = global (with pos_dev)
     float scale;
     uint32_t nsplit;
-    float* part;               // [kv_heads][nsplit][group][2 + head_dim]
+    float* part;               // [kv_heads][nsplit][8 + group * head_dim]
     uint32_t* tickets;         // [kv_heads]
     // Batched sequences (grid.z = batch): sequence b reads q + b bq, the caches
     // at + b bcache, position pos_dev[b], and writes out + b bq, its own partials
@@ -67,9 +67,10 @@ struct AttnArgs {
     uint32_t bq = 0;
     size_t bcache = 0, bpart = 0;
 };
-uint32_t attn_splits(uint32_t max_span);
-size_t attn_partial_floats(uint32_t kv_heads, uint32_t n_heads, uint32_t head_dim,
-                           uint32_t max_span);
+// Splits per (sequence, kv head) for a launch over `batch` sequences whose
+// spans are at most max_span; the partials one sequence needs (any span).
+uint32_t attn_splits(uint32_t max_span, uint32_t batch, uint32_t kv_heads);
+size_t attn_partial_floats(uint32_t kv_heads, uint32_t n_heads, uint32_t head_dim);
 int launch_attention(AttnArgs a, uint32_t max_span, hipStream_t st);
 
 // ---- sampling ----
