@@ -1,5 +1,5 @@
 """Benchmark: Gemma-3-1B int4 batch-1 greedy decode at context 4096 on one
-MI355X (BASELINE config 4 shape), plus the int4 matvec HBM roofline leg and
+MI355X (benchmark config 4 shape), plus the int4 matvec HBM roofline leg and
 the CPU baseline (the oracle's C restatement on the host cores).
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--ctx 4096]
@@ -14,10 +14,10 @@ timed steps are queued back to back between two device synchronisations.
 `roofline` prices the token kernel (the only kernel of the step): algorithmic
 HBM bytes of one token at its mean position over the kernel's mean duration,
 taken with HIP events on the session's stream around the K launches. The
-standalone int4 matvec (lm_head shape, and BASELINE config 1's gate shape with
+standalone int4 matvec (lm_head shape, and benchmark config 1's gate shape with
 64 rotating weight copies) is reported beside it. Prints one JSON line.
 
-Beside the headline, the line carries the other BASELINE configurations as
+Beside the headline, the line carries the other benchmark configurations as
 measurements (not the metric): `cfg4` (decode from 4097 to 8192, tok/s per
 512-position bucket and the deepest / shallowest ratio), `cfg3` (32-token
 prompt, 128 greedy tokens), `attention` (one global layer's decode attention
@@ -43,7 +43,7 @@ HBM_PEAK_GBS = 8000.0          # MI355X HBM3E
 # Measured HBM bytes of one token-kernel launch at this workload: rocprofv3
 # FETCH_SIZE x 2.0 + WRITE_SIZE x 1.0 (factors from a 256 MiB copy), see
 # profiles/token_kernel_gemma3_1b_ctx4096.md.
-TOKEN_TRAFFIC_BYTES = 654_004_367 + 13_731_901
+TOKEN_TRAFFIC_BYTES = 701_748_720 + 15_258_688
 SEED = 0x5EED0003
 # Algorithmic HBM bytes of one token at seq_len s (weights + fp16 scales,
 # KV reads, norm weights, logits write + argmax read, KV append).
@@ -127,7 +127,7 @@ def attention_leg(X, span: int, iters: int = 192):
 
 
 def cfg3_leg(X, sess, cfg, n_gen: int = 128):
-    """prefill a 32-token prompt of uniform random ids from
+    """benchmark config 3: prefill a 32-token prompt of uniform random ids from
     position 0, then greedy-decode `n_gen` tokens (decode tok/s, prefill
     excluded)."""
     r = np.random.default_rng(SEED)
@@ -146,7 +146,7 @@ def cfg3_leg(X, sess, cfg, n_gen: int = 128):
 
 
 def cfg4_leg(X, sess, cfg, ctx: int = 4096):
-    """KV pre-filled to `ctx`, then greedy decode out to
+    """benchmark config 4: KV pre-filled to `ctx`, then greedy decode out to
     max_seq (8192); tok/s per 512-position bucket and the deepest / shallowest
     ratio (flatness)."""
     sess.set_position(ctx)
@@ -176,7 +176,7 @@ def batch_bytes(depths) -> int:
 
 
 def cfg5_leg(X, sess, cfg, n_seq: int = 16, steps: int = 20, warmup: int = 3):
-    """16 independent sequences at depths uniform in
+    """benchmark config 5: 16 independent sequences at depths uniform in
     [128, 4096] (Philox), temperature 0.8 / top-k 64 / top-p 0.95 with a
     Philox draw per (sequence, step); tokens/s over all sequences."""
     seed = 0x5EED0005
@@ -255,14 +255,15 @@ def main() -> int:
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-configs", action="store_true",
-                    help="skip the BASELINE config 3 / 4 / 5 and attention legs")
+                    help="skip the benchmark config 3 / 4 / 5 and attention legs")
     ap.add_argument("--mv-iters", type=int, default=60)
-    ap.add_argument("--only", choices=["all", "matvec"], default="all",
-                    help="matvec: only the standalone matvec and streaming legs (for profiling)")
+    ap.add_argument("--only", choices=["all", "matvec", "attention", "cfg5"], default="all",
+                    help="one leg alone, for profiling: the standalone matvec and streaming "
+                         "legs, the attention leg, or the batched decode (config 5)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported "
-              "(the batch-1 decode path does not shard, see DESIGN.md)", file=sys.stderr)
+              "(one GPU per process; batch-1 decode does not benefit from tensor parallelism)", file=sys.stderr)
         return 2
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if world != 1:
@@ -289,6 +290,17 @@ def main() -> int:
                           "matvec_cfg1": {"us_per_launch": round(per1 * 1e6, 3),
                                           "GBs": round(nb1 / per1 / 1e9, 1)},
                           "stream_ceiling_GBs": round(ceil, 1)}), flush=True)
+        return 0
+    if args.only == "attention":
+        print(json.dumps({"attention": [attention_leg(X, sp) for sp in (4096, 8192)]}), flush=True)
+        return 0
+    if args.only == "cfg5":
+        scfg = X.XpConfig.gemma3_1b(max_seq=8192, sample_mode=1, temperature=0.8, top_k=64,
+                                    top_p=0.95, seed=0x5EED0005)
+        bsess = X.DecodeSession(scfg)
+        bsess.synthesize(SEED)
+        print(json.dumps({"cfg5": cfg5_leg(X, bsess, scfg)}), flush=True)
+        bsess.close()
         return 0
     ctx = args.ctx
     cfg = X.XpConfig.gemma3_1b(max_seq=8192)
@@ -335,7 +347,7 @@ def main() -> int:
     # Roofline leg: the dominant kernel of the step, the lm_head int4 matvec.
     nbytes, per_s = matvec_leg(X, 1152, 262144, copies=3, iters=args.mv_iters)
     achieved = nbytes / per_s / 1e9
-    # BASELINE config 1 shape (gate 6912 x 1152), 64 rotating copies.
+    # benchmark config 1 shape (gate 6912 x 1152), 64 rotating copies.
     nb1, per1 = matvec_leg(X, 1152, 6912, copies=64, iters=640)
     ceil = stream_ceiling(X)
 

@@ -1,5 +1,5 @@
 """Batched decode (xp_batch_*): up to 16 sequences per step on one session's
-weights, the matvecs as M = 16 MFMA GEMMs.
+weights, the matvecs as M = 16 MFMA GEMMs (benchmark config 5).
 
 Every sequence is checked against the oracle run alone on the same packed
 weights, its own KV cache and its own token ids: logits within 1e-3 relative

@@ -2,7 +2,7 @@
 (examples/llm/decode.cpp:1634-1866) on the GPU against the oracle's
 xo_forward on the same packed weights, KV contents and token ids.
 
-Bars: greedy token ids bit-exact; logits within 1e-3
+Bars (the benchmark specification): greedy token ids bit-exact; logits within 1e-3
 relative (|d| <= 1e-3 * max|logits|); KV rows within one fp16 ulp.
 """
 import numpy as np
@@ -140,7 +140,7 @@ def test_oracle_generate_matches_forward_loop(xh, xo):
 
 @pytest.mark.gpu
 def test_gpu_one_layer_cfg2(xp, xo, mode):
-    """one local Gemma-3-1B layer, 512 prior fp16 KV rows
+    """benchmark config 2: one local Gemma-3-1B layer, 512 prior fp16 KV rows
     ~ N(0,1), decode at position 512 (kv_start 1, span 512)."""
     X = xp
     print("case session one-layer cfg2", flush=True)
@@ -224,7 +224,7 @@ def test_gpu_decode_steps_equals_decode_step(xp, xo, mode):
 
 @pytest.mark.gpu
 def test_gpu_full_model_greedy_cfg3(xp, xo, mode):
-    """BASELINE config 3 (shortened): full Gemma-3-1B architecture, random
+    """benchmark config 3 (shortened): full Gemma-3-1B architecture, random
     int4 weights, tied 262144 x 1152 table; prefill then greedy decode."""
     X = xp
     print("case session full model cfg3", flush=True)
@@ -249,7 +249,7 @@ def test_gpu_full_model_greedy_cfg3(xp, xo, mode):
 
 @pytest.mark.gpu
 def test_gpu_full_model_deep_context_cfg4(xp, xo, mode):
-    """BASELINE config 4 (shortened): KV of all 26 layers pre-filled with fp16
+    """benchmark config 4 (shortened): KV of all 26 layers pre-filled with fp16
     N(0,1) to position 4096; decode from 4096 (global layers span 4097,
     local layers the last 512)."""
     X = xp
@@ -280,7 +280,7 @@ def test_gpu_full_model_deep_context_cfg4(xp, xo, mode):
 @pytest.mark.gpu
 def test_gpu_temperature_sampling(xp, xo, mode):
     """Temperature 0.8 / top-k 64 / top-p 0.95 over the top-4-per-chain
-    harvest, Philox uniform per (sequence, step) (BASELINE config 5 draw)."""
+    harvest, Philox uniform per (sequence, step) (benchmark config 5 draw)."""
     X = xp
     print("case session temperature", flush=True)
     cfg = cfg_small(X, n_layers=4, sample_mode=1, temperature=0.8, top_k=64, top_p=0.95,

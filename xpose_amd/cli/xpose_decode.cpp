@@ -7,7 +7,7 @@
 //                [--exec token|graph|launch] [--curve] [--ids]
 //
 // --ctx P pre-fills every layer's KV cache with fp16 N(0,1) rows 0..P-1 and
-// decodes from position P; otherwise a --prompt of
+// decodes from position P (benchmark config 4); otherwise a --prompt of
 // uniform-random ids is prefilled first (config 3). --curve reports tok/s per
 // 512-position bucket and the deepest/shallowest ratio, the reference's
 // flatness metric (decode.cpp:2977-2999). Prints per-step gpu ms min / median

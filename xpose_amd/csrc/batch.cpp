@@ -1,5 +1,5 @@
 // Batched decode: up to 16 independent sequences per step on one session's
-// weights. The reference decodes one sequence per
+// weights (benchmark config 5). The reference decodes one sequence per
 // DecodeSession (examples/llm/decode.cpp:1634-1866); a batch runs the same
 // token step for every sequence at once, so the 0.56 GB of int4 weights are
 // read once per step instead of once per sequence and the matvecs become

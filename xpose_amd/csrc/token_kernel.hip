@@ -29,9 +29,9 @@
 // (each moves 0.1-8 MB of weights across 256 CUs), so the design keeps every
 // stage's dependent chain short:
 //  * Vectors crossing a stage boundary are owned by threads: thread i holds
-//    elements 8i .. 8i+7 in registers from the slot fetch through the
-//    residual add, the RMSNorm and the fixed-point staging (whose block of 32
-//    is then one lane quad). Only the staged planes go through LDS.
+//    elements 4i .. 4i+3 (kOwn) in registers from the slot fetch through the
+//    residual add, the RMSNorm and the fixed-point staging (a block of 32 is
+//    then eight lanes). Only the staged planes go through LDS.
 //  * Block reductions take one barrier (rotating partial buffers).
 //  * Each stage's weights (the attention stage's KV rows) are loaded into
 //    registers before the workgroup waits for the stage's inputs: weights
@@ -40,7 +40,8 @@
 //    blocks w, w + 8, ... (clamped to the range, the excess ones zeroed, so
 //    the loop has no branches) and the 8 wave partials are summed through LDS
 //    in a fixed order. The down projection (k = 6912) is split into chunks of
-//    16 quads whose partial sums the next layer adds in chunk order, so every
+//    kTokDownQuads quads, and q|k|v and o into kTokQkvSplit / kTokOSplit k
+//    halves, whose partial sums the consumer adds in chunk order, so every
 //    result is deterministic.
 //  * Attention: one workgroup per 32 keys of [kv_start, pos]; each computes
 //    QK-norm + RoPE of q and k itself, scores, a chunk softmax (max, sum of
