@@ -45,6 +45,7 @@ extern "C" {
 #define XP_E_NOMEM      -3   /* device or host allocation failed             */
 #define XP_E_STATE      -4   /* call not valid in the current state          */
 #define XP_E_DEVICE     -5   /* a kernel reported a device-side error        */
+#define XP_E_FORMAT     -6   /* a model or cache file is malformed or unreadable */
 
 typedef void* xp_stream;   /* a hipStream_t; NULL = the default stream */
 
@@ -261,7 +262,7 @@ uint16_t xp_f32_to_f16(float f);
  * pass's logits, then run the network on it, decode.cpp:1819-1866), reset(),
  * last_logits(), position(). Weights come from xp_session_upload (packed
  * KM4 planes, the reference's layout) or xp_session_synthesize (the seeded
- * synthetic model); the GGUF loader is not part of this library. */
+ * synthetic model) or xp_session_load_gguf (a GGUF model, requantised). */
 typedef struct xp_session xp_session;
 
 typedef struct {
@@ -299,13 +300,16 @@ enum xp_exec_mode {
  * O n_heads*hd->hidden, GATE/UP hidden->ffn, DOWN ffn->hidden, LM_HEAD
  * (tied embedding) hidden->vocab. OR a matrix id with XP_T_SCALES for its
  * scale plane. Norm weights are stored as multiplier - 1 (the kernels apply
- * 1 + w, decode.cpp:1490-1515). Per-layer ids take layer >= 0; LM_HEAD and
- * FINAL_NORM take layer = -1. */
+ * 1 + w, decode.cpp:1490-1515). Per-layer ids take layer >= 0; LM_HEAD,
+ * FINAL_NORM and EMBED take layer = -1. EMBED is optional: fp32
+ * [vocab][hidden] embedding rows (a model loaded from GGUF embeds from its
+ * original table, as decode.cpp:1618-1627 does); without it the embedding
+ * is the dequantised LM_HEAD column. */
 enum xp_tensor {
     XP_T_Q = 0, XP_T_K = 1, XP_T_V = 2, XP_T_O = 3, XP_T_GATE = 4, XP_T_UP = 5, XP_T_DOWN = 6,
     XP_T_ATTN_NORM = 16, XP_T_POST_ATTN_NORM = 17, XP_T_FFN_NORM = 18,
     XP_T_POST_FFN_NORM = 19, XP_T_Q_NORM = 20, XP_T_K_NORM = 21,
-    XP_T_LM_HEAD = 32, XP_T_FINAL_NORM = 33,
+    XP_T_LM_HEAD = 32, XP_T_FINAL_NORM = 33, XP_T_EMBED = 34,
     XP_T_SCALES = 0x100
 };
 
@@ -328,6 +332,9 @@ int  xp_session_create(const xp_config* c, xp_session** out);
 int  xp_session_destroy(xp_session* s);
 int  xp_tensor_bytes(const xp_config* c, int layer, int tensor, size_t* bytes);
 int  xp_session_upload(xp_session* s, int layer, int tensor, const void* host, size_t bytes);
+/* Bytes [offset, offset + bytes) of a tensor, for streaming large ones. */
+int  xp_session_upload_part(xp_session* s, int layer, int tensor, size_t offset,
+                            const void* host, size_t bytes);
 /* The synthetic model of the benchmark configs, bit-identical to what
  * xp_synth_tensor returns: nibbles uniform on [0,15], fp16 scales
  * |N(0, 0.02)|, norm multipliers N(1, 0.1) (stored minus 1). */
@@ -401,6 +408,90 @@ int xp_batch_last_ms(xp_batch* b, float* ms);
 uint32_t xp_draw(float* val, uint32_t* idx, uint32_t n, float temperature, uint32_t top_k,
                  float top_p, double u);
 double xp_philox_uniform(uint32_t seed, uint32_t seq, uint32_t step);
+
+/* ---- GGUF load path -------------------------------------------------------
+ * Host side, no GPU (except xp_session_load_gguf's uploads). Replaces GGUFFile
+ * (examples/llm/model/gguf.hpp:173-215, gguf.cpp:234-645), the requantising
+ * packer (decode.cpp:60-229: symmetric int4, q = round(v / s) + 8 clamped to
+ * [0, 15], s = amax / 7 rounded to whichever neighbouring bf16 value has the
+ * smaller block error; KM4 nibble plane + bf16 quad scale plane) and the
+ * load path with its packed-weight cache (decode.cpp:710-1328). The cache is
+ * this library's own format: a header stamped with the model file's size,
+ * mtime and a digest of its first and last 64 KiB, the scale format and the
+ * packer revision; a table of (name, shape, byte counts, digest) per tensor;
+ * written to "<path>.tmp" and renamed into place. Any mismatch repacks. */
+typedef struct xp_gguf xp_gguf;
+enum xp_ggml_type {
+    XP_GGML_F32 = 0, XP_GGML_F16 = 1, XP_GGML_Q4_0 = 2, XP_GGML_Q4_1 = 3, XP_GGML_Q5_0 = 6,
+    XP_GGML_Q5_1 = 7, XP_GGML_Q8_0 = 8, XP_GGML_Q4_K = 12, XP_GGML_Q6_K = 14, XP_GGML_BF16 = 30
+};
+typedef struct {
+    uint32_t version;
+    uint64_t n_tensors, n_meta, alignment, data_offset, file_size;
+} xp_gguf_info;
+/* ModelConfig (gguf.hpp:144-165): the "<arch>." keys. */
+typedef struct {
+    char     arch[32];
+    uint32_t n_layers, n_heads, n_kv_heads, hidden, ffn, context_length;
+    uint32_t key_length, value_length, vocab, sliding_window, head_dim;
+    float    rope_freq_base, rms_eps;
+} xp_gguf_model;
+typedef struct {
+    double   total_ms, pack_ms, cache_ms, upload_ms;
+    uint64_t packed_bytes;      /* int4 planes + scale planes */
+    int32_t  from_cache;        /* 1: the cache was valid and used */
+    int32_t  cache_written;     /* 1: a new cache file was written */
+    uint32_t threads;
+    uint32_t n_tensors;
+} xp_load_stats;
+enum xp_load_flags {
+    XP_LOAD_REPACK = 1,         /* ignore a valid cache (still rewrite it) */
+    XP_LOAD_NORM_RAW = 2,       /* the file's norms are w, not 1 + w: no "- 1" */
+    XP_LOAD_NO_EMBED = 4        /* embed from the int4 LM_HEAD instead of the file's table */
+};
+int xp_gguf_open(const char* path, xp_gguf** out);
+int xp_gguf_close(xp_gguf* g);
+int xp_gguf_get_info(xp_gguf* g, xp_gguf_info* info);
+int xp_gguf_get_model(xp_gguf* g, xp_gguf_model* m);
+int xp_gguf_tensor_count(xp_gguf* g, uint64_t* n);
+int xp_gguf_tensor_at(xp_gguf* g, uint64_t i, char* name, size_t cap);
+/* dims[4] (dims[0] fastest); unused dims are 1. */
+int xp_gguf_tensor_info(xp_gguf* g, const char* name, uint32_t* type, uint32_t* n_dims,
+                        uint64_t* dims, uint64_t* nbytes);
+int xp_gguf_meta_number(xp_gguf* g, const char* key, double* value);
+int xp_gguf_meta_string(xp_gguf* g, const char* key, char* out, size_t cap, size_t* len);
+int xp_gguf_meta_array_length(xp_gguf* g, const char* key, uint64_t* n);
+/* GGUFFile::dequantize (gguf.cpp:439-645): n elements (whole blocks). */
+int xp_dequantize(uint32_t type, const void* src, float* out, uint64_t n);
+/* Rows [row0, row0 + nrows) of a 2-D tensor, fp32 [nrows][dims[0]]
+ * (RowReader, decode.cpp:60-96). */
+int xp_gguf_dequantize_rows(xp_gguf* g, const char* name, uint64_t row0, uint64_t nrows,
+                            float* out);
+/* Shapes from the file onto c (DecodeConfig::from_model, decode.cpp:258-275);
+ * c's policy fields (max_seq, sampling, global_every, scale_fmt, ...) stay. */
+int xp_config_from_gguf(xp_gguf* g, xp_config* c);
+/* Requantises w[cols][rows] (GGUF row order: row j of length `rows` is
+ * output column j) to the KM4 plane wq (rows * cols / 2 bytes) and the scale
+ * plane sc (XP_SCALE_BF16_QUAD: rows / 32 * cols * 2 bytes; XP_SCALE_F32:
+ * rows / 32 * cols * 4 bytes, s = amax / 7 unrounded). threads 0 = all cores. */
+int xp_pack_int4(const float* w, uint32_t rows, uint32_t cols, int scale_fmt, uint32_t threads,
+                 void* wq, void* sc);
+/* Packs every matrix of the model for config c (7 per layer, then the
+ * output head: output.weight, or token_embd.weight when tied) into the cache
+ * at cache_path, no GPU. */
+int xp_gguf_pack_model(xp_gguf* g, const xp_config* c, const char* cache_path, uint32_t threads,
+                       xp_load_stats* st);
+/* --verify-cache (decode.cpp:2580-2661): repacks every matrix and compares
+ * the cache payload byte for byte; *mismatches = tensors that differ (0 =
+ * identical). XP_E_FORMAT if there is no valid cache. */
+int xp_gguf_verify_cache(xp_gguf* g, const xp_config* c, const char* cache_path,
+                         uint32_t threads, uint32_t* mismatches);
+/* Loads the model into a session created with shapes from the same file:
+ * matrices from a valid cache (digests checked) or packed afresh (and
+ * cached when cache_path is given), norms minus 1, and the fp32 embedding
+ * table (XP_T_EMBED) from token_embd.weight. */
+int xp_session_load_gguf(xp_session* s, xp_gguf* g, const char* cache_path, uint32_t flags,
+                         uint32_t threads, xp_load_stats* st);
 
 #ifdef __cplusplus
 }

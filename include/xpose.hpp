@@ -7,8 +7,10 @@
 // they construct:
 //
 //   reference                                 here
-//   DecodeSession(Paths, DecodeConfig)        DecodeSession(Config) + upload /
-//                                             synthesize (weights arrive packed)
+//   DecodeSession(Paths, DecodeConfig)        DecodeSession(Model, Config, cache) (GGUF,
+//                                             requantised or from the pack cache), or
+//                                             DecodeSession(Config) + upload / synthesize
+//   GGUFFile::open, --verify-cache            Model(path), Model::verify_cache
 //   prefill(std::span<const uint32_t>)        prefill(const uint32_t*, size_t) /
 //                                             prefill(const std::vector<uint32_t>&)
 //   uint32_t decode_step()                    uint32_t decode_step()
@@ -59,12 +61,58 @@ struct Metrics {
     int32_t  exec_mode      = 0;   // XP_EXEC_TOKEN, _GRAPH or _LAUNCH
 };
 
+// A GGUF model file (GGUFFile, examples/llm/model/gguf.hpp:173-215).
+class Model {
+public:
+    explicit Model(const std::string& path) : path_(path) {
+        check(xp_gguf_open(path.c_str(), &g_), "xp_gguf_open");
+    }
+    ~Model() {
+        if (g_) xp_gguf_close(g_);
+    }
+    Model(const Model&) = delete;
+    Model& operator=(const Model&) = delete;
+
+    // The file's shapes over `base` (DecodeConfig::from_model, decode.cpp:258-275);
+    // a GGUF model packs to bf16 scales unless fp32 is asked for.
+    Config config(Config base = Config()) const {
+        check(xp_config_from_gguf(g_, &base), "xp_config_from_gguf");
+        if (base.scale_fmt != XP_SCALE_F32) base.scale_fmt = XP_SCALE_BF16_QUAD;
+        return base;
+    }
+    // --verify-cache (decode.cpp:2580-2661): repack and compare the cache
+    // byte for byte; returns the number of matrices that differ.
+    uint32_t verify_cache(const Config& c, const std::string& cache, uint32_t threads = 0) const {
+        uint32_t bad = 0;
+        check(xp_gguf_verify_cache(g_, &c, cache.c_str(), threads, &bad), "xp_gguf_verify_cache");
+        return bad;
+    }
+    const std::string& path() const { return path_; }
+    xp_gguf* handle() const { return g_; }
+
+private:
+    std::string path_;
+    xp_gguf* g_ = nullptr;
+};
+
 class DecodeSession {
 public:
     explicit DecodeSession(const Config& cfg) : cfg_(cfg) {
         check(xp_init(0), "xp_init");
         check(xp_session_create(&cfg_, &s_), "xp_session_create");
     }
+    // The reference's DecodeSession(Paths, DecodeConfig): shapes from the
+    // file, policy fields from `cfg`, weights requantised on load or read
+    // from the pack cache at `cache` ("" = no cache).
+    DecodeSession(const Model& m, const Config& cfg, const std::string& cache = std::string(),
+                  uint32_t flags = 0)
+        : DecodeSession(m.config(cfg)) {
+        check(xp_session_load_gguf(s_, m.handle(), cache.empty() ? nullptr : cache.c_str(), flags,
+                                   0, &load_),
+              "xp_session_load_gguf");
+    }
+    // Where the load time went (LoadStats, decode.hpp:584-603).
+    const xp_load_stats& load_stats() const { return load_; }
     ~DecodeSession() {
         if (s_) xp_session_destroy(s_);
     }
@@ -158,6 +206,7 @@ public:
 private:
     Config cfg_;
     xp_session* s_ = nullptr;
+    xp_load_stats load_{};
 };
 
 }  // namespace llm

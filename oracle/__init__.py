@@ -40,7 +40,8 @@ class Model(C.Structure):
                                           "global_every", "sliding_window")] + \
                [("rms_eps", C.c_float), ("theta_global", C.c_float),
                 ("theta_local", C.c_float), ("layers", C.c_void_p),
-                ("lm_head", QWeight), ("final_norm", C.c_void_p)]
+                ("lm_head", QWeight), ("final_norm", C.c_void_p), ("scale_fmt", C.c_int32),
+                ("embed", C.c_void_p)]
 
 
 def lib() -> C.CDLL:
@@ -96,6 +97,10 @@ def lib() -> C.CDLL:
             "xo_philox_uniform": (f64, [u32, u32, u32]),
             "xo_philox4x32_10": (None, [U32P, U32P, U32P]),
             "xo_embed": (None, [F32P, C.POINTER(Model), u32]),
+            "xo_dequantize": (i32, [u32, vp, F32P, C.c_uint64]),
+            "xo_pack_int4": (None, [F32P, u32, u32, i32, U32P, vp]),
+            "xo_quantise": (u32, [f32, f32]),
+            "xo_best_bf16_scale": (f32, [F32P, f32]),
             "xo_forward": (i32, [C.POINTER(Model), u32, u32, vp, i32]),
             "xo_generate_greedy": (i32, [C.POINTER(Model), U32P, u32, u32, U32P, i32]),
         }
@@ -125,6 +130,24 @@ def rmsnorm_gemma(x, w, eps: float = 1e-6, nparts: int = 64) -> np.ndarray:
     return out
 
 
+def dequantize(ggml_type: int, raw, n: int) -> np.ndarray:
+    out = np.empty(n, np.float32)
+    raw = np.ascontiguousarray(raw)
+    if lib().xo_dequantize(ggml_type, raw.ctypes.data, out, n) != 0:
+        raise ValueError(f"xo_dequantize: type {ggml_type} / {n} elements")
+    return out
+
+
+def pack_int4(w_cols, bf16: bool = True):
+    """The reference packer over w[cols][rows]: (KM4 plane, scale plane)."""
+    w_cols = _f32(w_cols)
+    cols, rows = w_cols.shape
+    wq = np.empty(rows * cols // 8, np.uint32)
+    sc = np.empty(rows // 32 * cols, np.uint16 if bf16 else np.float32)
+    lib().xo_pack_int4(w_cols, rows, cols, 1 if bf16 else 0, wq, sc.ctypes.data)
+    return wq, sc
+
+
 def argmax_tree(logits) -> tuple[int, float]:
     v = C.c_float()
     i = lib().xo_argmax_tree(_f32(logits), np.asarray(logits).size, C.byref(v))
@@ -136,7 +159,9 @@ class OracleModel:
     (fp16 quad scales), an fp16 KV cache, and xo_forward in record_token
     order. `get(layer, tensor)` supplies each tensor as a numpy array."""
 
-    def __init__(self, cfg, get):
+    def __init__(self, cfg, get, embed=None):
+        """`embed`: optional fp32 [vocab][hidden] embedding rows (a GGUF
+        model's table); the scale planes are in cfg.scale_fmt."""
         import xpose_amd as X
         self.cfg = cfg
         self._keep = []
@@ -181,6 +206,11 @@ class OracleModel:
         m.layers = C.cast(layers, C.c_void_p)
         m.lm_head = qw(-1, X.T_LM_HEAD)
         m.final_norm = fn.ctypes.data
+        m.scale_fmt = cfg.scale_fmt
+        if embed is not None:
+            e = np.ascontiguousarray(embed, np.float32)
+            self._keep.append(e)
+            m.embed = e.ctypes.data
         self.model = m
 
     def forward(self, token: int, pos: int, want_logits: bool = True, threads: int = 0):

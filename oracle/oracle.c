@@ -754,11 +754,17 @@ uint32_t xo_draw(float* val, uint32_t* idx, uint32_t n, float temperature, uint3
 /* Full decode step                                                     */
 /* ------------------------------------------------------------------ */
 
+static int g_fmt = 0;   /* scale format of the model in xo_forward */
 static void mv(float* out, const float* in, const xo_qweight* w) {
-    xo_mv_km4(out, in, w->wq, w->sc, 0, w->rows, w->cols);
+    xo_mv_km4(out, in, w->wq, w->sc, g_fmt, w->rows, w->cols);
 }
 
 void xo_embed(float* x, const xo_model* m, uint32_t token) {
+    if (m->embed) {   /* the GGUF row (RowReader::read), times the scale */
+        const float sc = sqrtf((float)m->hidden);
+        for (uint32_t k = 0; k < m->hidden; ++k) x[k] = m->embed[(size_t)token * m->hidden + k] * sc;
+        return;
+    }
     const xo_qweight* e = &m->lm_head;
     const uint32_t nblk = e->rows / 32;
     const size_t base = ((size_t)(token / 64) * nblk * 64 + (token % 64)) * 4;
@@ -766,7 +772,7 @@ void xo_embed(float* x, const xo_model* m, uint32_t token) {
     for (uint32_t k = 0; k < e->rows; ++k) {
         const uint32_t w = e->wq[base + (size_t)(k / 32) * 256 + ((k >> 3) & 3u)];
         const float q = (float)((int)((w >> ((k & 7u) * 4u)) & 15u) - 8);
-        const float v = q * xo_scale_at(e->sc, 0, e->cols, k / 32, token);
+        const float v = q * xo_scale_at(e->sc, m->scale_fmt, e->cols, k / 32, token);
         x[k] = v * sc;
     }
 }
@@ -782,6 +788,7 @@ int xo_forward(const xo_model* m, uint32_t token, uint32_t pos, float* logits, i
     const float ascale = 1.0f / sqrtf((float)hd);
     if (pos >= m->max_seq || token >= m->vocab) return -1;
     g_threads = threads;
+    g_fmt = m->scale_fmt;
 
     float* x = (float*)malloc(H * sizeof(float));
     float* xb = (float*)malloc((H > qd ? H : qd) * sizeof(float));
@@ -858,4 +865,238 @@ int xo_generate_greedy(const xo_model* m, const uint32_t* prompt, uint32_t n_pro
     }
     free(logits);
     return rc;
+}
+
+/* ------------------------------------------------------------------ */
+/* GGUF load path                                                       */
+/* ------------------------------------------------------------------ */
+
+static uint16_t rd_u16(const uint8_t* p) { uint16_t v; memcpy(&v, p, 2); return v; }
+static float rd_half(const uint8_t* p) { return xo_fp16_to_fp32(rd_u16(p)); }
+
+/* get_scale_min_k4, gguf.cpp:436-446. */
+static void k4_scale_min(int j, const uint8_t* q, uint8_t* d, uint8_t* m) {
+    if (j < 4) {
+        *d = q[j] & 63;
+        *m = q[j + 4] & 63;
+    } else {
+        *d = (uint8_t)((q[j + 4] & 0xF) | ((q[j - 4] >> 6) << 4));
+        *m = (uint8_t)((q[j + 4] >> 4) | ((q[j] >> 6) << 4));
+    }
+}
+
+/* GGUFFile::dequantize, gguf.cpp:448-645, in the reference's loop order. */
+int xo_dequantize(uint32_t type, const void* src, float* dst, uint64_t n) {
+    const uint8_t* p = (const uint8_t*)src;
+    uint64_t b, i;
+    int j, l;
+    switch (type) {
+        case 0: /* F32, :456-458 */
+            memcpy(dst, p, (size_t)n * 4);
+            return 0;
+        case 1: /* F16, :460-466 */
+            for (i = 0; i < n; ++i) dst[i] = rd_half(p + i * 2);
+            return 0;
+        case 30: /* BF16, :468-476 */
+            for (i = 0; i < n; ++i) dst[i] = as_float((uint32_t)rd_u16(p + i * 2) << 16);
+            return 0;
+        case 2: /* Q4_0, :478-494 */
+            if (n % 32) return -1;
+            for (b = 0; b < n / 32; ++b) {
+                const uint8_t* blk = p + b * 18;
+                const float d = rd_half(blk);
+                const uint8_t* qs = blk + 2;
+                float* y = dst + b * 32;
+                for (j = 0; j < 16; ++j) {
+                    y[j] = (float)((int)(qs[j] & 0x0F) - 8) * d;
+                    y[j + 16] = (float)((int)(qs[j] >> 4) - 8) * d;
+                }
+            }
+            return 0;
+        case 3: /* Q4_1, :496-512 */
+            if (n % 32) return -1;
+            for (b = 0; b < n / 32; ++b) {
+                const uint8_t* blk = p + b * 20;
+                const float d = rd_half(blk), m = rd_half(blk + 2);
+                const uint8_t* qs = blk + 4;
+                float* y = dst + b * 32;
+                for (j = 0; j < 16; ++j) {
+                    y[j] = (float)(qs[j] & 0x0F) * d + m;
+                    y[j + 16] = (float)(qs[j] >> 4) * d + m;
+                }
+            }
+            return 0;
+        case 6: /* Q5_0, :514-549 */
+        case 7: /* Q5_1 */ {
+            const int is_1 = type == 7;
+            const size_t stride = is_1 ? 24 : 22;
+            if (n % 32) return -1;
+            for (b = 0; b < n / 32; ++b) {
+                const uint8_t* blk = p + b * stride;
+                const float d = rd_half(blk);
+                const float m = is_1 ? rd_half(blk + 2) : 0.0f;
+                uint32_t qh;
+                memcpy(&qh, blk + (is_1 ? 4 : 2), 4);
+                const uint8_t* qs = blk + (is_1 ? 8 : 6);
+                float* y = dst + b * 32;
+                for (j = 0; j < 16; ++j) {
+                    const uint8_t xh0 = (uint8_t)(((qh >> (j + 0)) << 4) & 0x10);
+                    const uint8_t xh1 = (uint8_t)((qh >> (j + 12)) & 0x10);
+                    const int q0 = (int)((qs[j] & 0x0F) | xh0);
+                    const int q1 = (int)((qs[j] >> 4) | xh1);
+                    if (is_1) {
+                        y[j] = (float)q0 * d + m;
+                        y[j + 16] = (float)q1 * d + m;
+                    } else {
+                        y[j] = (float)(q0 - 16) * d;
+                        y[j + 16] = (float)(q1 - 16) * d;
+                    }
+                }
+            }
+            return 0;
+        }
+        case 8: /* Q8_0, :551-562 */
+            if (n % 32) return -1;
+            for (b = 0; b < n / 32; ++b) {
+                const uint8_t* blk = p + b * 34;
+                const float d = rd_half(blk);
+                const int8_t* qs = (const int8_t*)(blk + 2);
+                for (j = 0; j < 32; ++j) dst[b * 32 + j] = (float)qs[j] * d;
+            }
+            return 0;
+        case 12: /* Q4_K, :564-595 */
+            if (n % 256) return -1;
+            for (b = 0; b < n / 256; ++b) {
+                const uint8_t* blk = p + b * 144;
+                const float d = rd_half(blk), dmin = rd_half(blk + 2);
+                const uint8_t* scales = blk + 4;
+                const uint8_t* qs = blk + 16;
+                float* y = dst + b * 256;
+                int is = 0;
+                for (j = 0; j < 256; j += 64) {
+                    uint8_t sc, m;
+                    k4_scale_min(is + 0, scales, &sc, &m);
+                    const float d1 = d * sc, m1 = dmin * m;
+                    k4_scale_min(is + 1, scales, &sc, &m);
+                    const float d2 = d * sc, m2 = dmin * m;
+                    for (l = 0; l < 32; ++l) *y++ = d1 * (float)(qs[l] & 0xF) - m1;
+                    for (l = 0; l < 32; ++l) *y++ = d2 * (float)(qs[l] >> 4) - m2;
+                    qs += 32;
+                    is += 2;
+                }
+            }
+            return 0;
+        case 14: /* Q6_K, :597-631 */
+            if (n % 256) return -1;
+            for (b = 0; b < n / 256; ++b) {
+                const uint8_t* blk = p + b * 210;
+                const uint8_t* ql = blk;
+                const uint8_t* qh = blk + 128;
+                const int8_t* sc = (const int8_t*)(blk + 192);
+                const float d = rd_half(blk + 208);
+                float* y = dst + b * 256;
+                int n2;
+                for (n2 = 0; n2 < 256; n2 += 128) {
+                    for (l = 0; l < 32; ++l) {
+                        const int is = l / 16;
+                        const int q1 = (int)((ql[l] & 0xF) | (((qh[l] >> 0) & 3) << 4)) - 32;
+                        const int q2 = (int)((ql[l + 32] & 0xF) | (((qh[l] >> 2) & 3) << 4)) - 32;
+                        const int q3 = (int)((ql[l] >> 4) | (((qh[l] >> 4) & 3) << 4)) - 32;
+                        const int q4 = (int)((ql[l + 32] >> 4) | (((qh[l] >> 6) & 3) << 4)) - 32;
+                        y[l + 0] = d * sc[is + 0] * (float)q1;
+                        y[l + 32] = d * sc[is + 2] * (float)q2;
+                        y[l + 64] = d * sc[is + 4] * (float)q3;
+                        y[l + 96] = d * sc[is + 6] * (float)q4;
+                    }
+                    y += 128;
+                    ql += 64;
+                    qh += 32;
+                    sc += 8;
+                }
+            }
+            return 0;
+        default:
+            return -1;
+    }
+}
+
+/* quantise, decode.cpp:101-104: round half away from zero, +8, clamp. */
+uint32_t xo_quantise(float v, float inv_scale) {
+    long r = lroundf(v * inv_scale);
+    int q = (int)r + 8;
+    return (uint32_t)(q < 0 ? 0 : (q > 15 ? 15 : q));
+}
+
+/* best_bf16_scale, decode.cpp:127-151: the two bf16 values around s0 (s0
+ * truncated, and one bf16 ulp up), the one with the smaller double-precision
+ * squared block error, the lower on a tie. */
+static double bf16_err(const float* blk, float s) {
+    if (!(s > 0.0f)) return INFINITY;
+    const float inv = 1.0f / s;
+    double e = 0.0;
+    for (int t = 0; t < 32; ++t) {
+        const double d = (double)((int)xo_quantise(blk[t], inv) - 8) * (double)s - (double)blk[t];
+        e += d * d;
+    }
+    return e;
+}
+
+float xo_best_bf16_scale(const float* blk, float s0) {
+    if (!(s0 > 0.0f)) return 0.0f;
+    const uint32_t ulo = as_uint(s0) & 0xFFFF0000u;
+    const float lo = as_float(ulo), hi = as_float(ulo + 0x10000u);
+    return bf16_err(blk, lo) <= bf16_err(blk, hi) ? lo : hi;
+}
+
+/* pack_group (decode.cpp:177-229, Km4 branch) over every column group, then
+ * pack_scales_bf16_cols (:157-172) for the bf16 plane. */
+void xo_pack_int4(const float* w, uint32_t rows, uint32_t cols, int bf16, uint32_t* wq,
+                  void* scv) {
+    const uint32_t nblk = rows / 32;
+    float* scales = (float*)malloc((size_t)nblk * cols * sizeof(float));
+    for (uint32_t group = 0; group < cols / 64; ++group) {
+        const float* cols64 = w + (size_t)group * 64 * rows;
+        const uint32_t j0 = group * 64;
+        float inv[64];
+        for (uint32_t b = 0; b < nblk; ++b) {
+            for (uint32_t c = 0; c < 64; ++c) {
+                const float* r = cols64 + (size_t)c * rows + b * 32;
+                float amax = 0.0f;
+                for (uint32_t t = 0; t < 32; ++t) {
+                    const float a = fabsf(r[t]);
+                    if (a > amax) amax = a;
+                }
+                const float s = bf16 ? xo_best_bf16_scale(r, amax / 7.0f) : amax / 7.0f;
+                scales[(size_t)b * cols + j0 + c] = s;
+                inv[c] = s > 0.0f ? 1.0f / s : 0.0f;
+            }
+            const size_t base = ((size_t)group * nblk + b) * 64;
+            for (uint32_t c = 0; c < 64; ++c) {
+                uint32_t v4[4] = {0, 0, 0, 0};
+                for (uint32_t t = 0; t < 32; ++t) {
+                    const uint32_t k = b * 32 + t;
+                    v4[(t >> 3) & 3u] |= xo_quantise(cols64[(size_t)c * rows + k], inv[c])
+                                         << ((t & 7u) * 4);
+                }
+                uint32_t* d = wq + (base + c) * 4;
+                d[0] = v4[0]; d[1] = v4[1]; d[2] = v4[2]; d[3] = v4[3];
+            }
+        }
+    }
+    if (bf16) {
+        uint32_t* out = (uint32_t*)scv;
+        for (uint32_t q = 0; q < nblk / 4; ++q)
+            for (uint32_t j = 0; j < cols; ++j) {
+                const size_t d = ((size_t)q * cols + j) * 2;
+                out[d] = 0;
+                out[d + 1] = 0;
+                for (uint32_t i = 0; i < 4; ++i) {
+                    const uint32_t bits = as_uint(scales[(size_t)(q * 4 + i) * cols + j]) >> 16;
+                    out[d + (i >> 1)] |= bits << ((i & 1u) * 16);
+                }
+            }
+    } else {
+        memcpy(scv, scales, (size_t)nblk * cols * sizeof(float));
+    }
+    free(scales);
 }

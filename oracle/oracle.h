@@ -136,7 +136,7 @@ void xo_philox4x32_10(const uint32_t ctr[4], const uint32_t key[2], uint32_t out
 /* ---- full decode step (record_token order, decode.cpp:1634-1780) ---- */
 typedef struct {
     const uint32_t* wq;   /* KM4 nibble plane */
-    const uint16_t* sc;   /* fp16 quad scale plane */
+    const void* sc;       /* scale plane in the model's scale_fmt */
     uint32_t rows, cols;
 } xo_qweight;
 
@@ -159,10 +159,13 @@ typedef struct {
     const xo_layer* layers;
     xo_qweight lm_head;          /* tied: rows = hidden, cols = vocab */
     const float* final_norm;
+    int32_t scale_fmt;           /* 0 fp16 quad, 1 bf16 quad, 2 fp32 [b][cols] */
+    const float* embed;          /* optional fp32 [vocab][hidden] embedding rows */
 } xo_model;
 
-/* Embedding of `token`: column token of the tied table, dequantised, times
- * sqrt(float(hidden)) (decode.cpp:1618-1627). */
+/* Embedding of `token` times sqrt(float(hidden)) (decode.cpp:1618-1627): row
+ * `token` of m->embed when given (the GGUF row, as the reference reads it),
+ * else column token of the tied int4 table, dequantised. */
 void xo_embed(float* x, const xo_model* m, uint32_t token);
 /* One forward pass at `pos` on `token`; appends K/V at pos. Writes vocab
  * logits when logits != NULL (the lm_head is skipped otherwise). Uses
@@ -173,6 +176,21 @@ int xo_forward(const xo_model* m, uint32_t token, uint32_t pos, float* logits,
  * sample-first decode steps (decode.cpp:1790-1866). out receives n_gen ids. */
 int xo_generate_greedy(const xo_model* m, const uint32_t* prompt, uint32_t n_prompt,
                        uint32_t n_gen, uint32_t* out, int threads);
+
+/* ---- GGUF load path (examples/llm/model/gguf.cpp, decode.cpp:60-229) ---- */
+/* GGUFFile::dequantize (gguf.cpp:439-645) for F32, F16, BF16, Q4_0, Q4_1,
+ * Q5_0, Q5_1, Q8_0, Q4_K, Q6_K; returns 0, or -1 for another type or a
+ * partial block. */
+int xo_dequantize(uint32_t type, const void* src, float* dst, uint64_t n);
+/* The requantising packer (decode.cpp:97-229) over a whole matrix:
+ * w[cols][rows] (row j = output column j), bf16 != 0 for best_bf16_scale and
+ * the bf16 quad plane (uint16 sc[((b/4)*cols + j)*4 + b%4]), else fp32 scales
+ * amax/7 as float sc[b*cols + j]. wq: the KM4 plane (rows*cols/8 words). */
+void xo_pack_int4(const float* w, uint32_t rows, uint32_t cols, int bf16, uint32_t* wq,
+                  void* sc);
+/* quantise() (decode.cpp:97-104) and best_bf16_scale() (:127-151) alone. */
+uint32_t xo_quantise(float v, float inv_scale);
+float xo_best_bf16_scale(const float* blk32, float s0);
 
 #ifdef __cplusplus
 }

@@ -24,6 +24,28 @@ def test_cli_usage_errors_exit_2():
     assert r.returncode == 2
 
 
+def test_cli_verify_cache(xh, tmp_path):
+    """--verify-cache (decode.cpp:2580-2661) through the C++ Model class: PASS
+    on a fresh cache, FAIL once a payload byte is flipped; no GPU involved."""
+    import gguf_util as G
+    X = xh
+    model = str(tmp_path / "m.gguf")
+    G.gemma_model(model, n_layers=1, hidden=256, ffn=512, n_heads=1, vocab=512)
+    g = X.Gguf(model)
+    cfg = g.config(X.XpConfig.gemma3_1b(scale_fmt=X.XP_SCALE_BF16_QUAD))
+    g.pack_model(cfg, model + ".xpack")
+    g.close()
+    r = run("--model", model, "--layers", 1, "--verify-cache")
+    assert r.returncode == 0 and "PASS" in r.stdout, r.stdout + r.stderr
+    data = bytearray(open(model + ".xpack", "rb").read())
+    data[1000] ^= 1
+    open(model + ".xpack", "wb").write(bytes(data))
+    r = run("--model", model, "--layers", 1, "--verify-cache")
+    assert r.returncode == 1 and "FAIL" in r.stdout, r.stdout + r.stderr
+    r = run("--verify-cache")
+    assert r.returncode == 2
+
+
 def cli_ids(out: str):
     line = [l for l in out.splitlines() if l.startswith("ids ")][0]
     return [int(t) for t in line.split()[1:]]
@@ -58,3 +80,38 @@ def test_gpu_cli_matches_python_session(xp):
     sess.prefill(np.array(prompt, np.uint32))
     got = [sess.decode_step() for _ in range(n)]
     assert got == outs["token"]
+
+
+@pytest.mark.gpu
+def test_gpu_cli_gguf_matches_python_session(xp, tmp_path):
+    """--model: the CLI's C++ GGUF load (DecodeSession(Model, Config, cache))
+    and the Python binding's give the same greedy ids on a small GGUF model."""
+    import ctypes as C
+    import gguf_util as G
+    X = xp
+    print("case cli gguf", flush=True)
+    model = str(tmp_path / "m.gguf")
+    G.gemma_model(model, n_layers=2, hidden=256, ffn=512, n_heads=1, vocab=1024, seed=31)
+    seed, prompt_len, n = 0x5EED0003, 4, 6
+    r = run("--model", model, "--prompt", prompt_len, "--tokens", n, "--seed", seed, "--ids")
+    assert r.returncode == 0, r.stderr
+    assert "cache written" in r.stdout, r.stdout
+    ids = cli_ids(r.stdout)
+    r2 = run("--model", model, "--prompt", prompt_len, "--tokens", n, "--seed", seed, "--ids")
+    assert r2.returncode == 0 and "from the pack cache" in r2.stdout, r2.stdout + r2.stderr
+    assert cli_ids(r2.stdout) == ids
+    prompt = []
+    for i in range(prompt_len):
+        c = (C.c_uint32 * 4)(i, 0, 0, 0)
+        k = (C.c_uint32 * 2)(seed, 0x7000)
+        o = (C.c_uint32 * 4)()
+        X.lib().xp_philox4x32_10(c, k, o)
+        prompt.append(o[0] % 1024)
+    g = X.Gguf(model)
+    cfg = g.config(X.XpConfig.gemma3_1b(scale_fmt=X.XP_SCALE_BF16_QUAD))
+    sess = X.DecodeSession(cfg)
+    sess.load_gguf(g)
+    sess.prefill(np.array(prompt, np.uint32))
+    assert [sess.decode_step() for _ in range(n)] == ids
+    sess.close()
+    g.close()

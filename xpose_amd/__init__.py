@@ -27,7 +27,7 @@ _lib = None
 # Tensor ids (enum xp_tensor in include/xpose.h).
 T_Q, T_K, T_V, T_O, T_GATE, T_UP, T_DOWN = range(7)
 T_ATTN_NORM, T_POST_ATTN_NORM, T_FFN_NORM, T_POST_FFN_NORM, T_Q_NORM, T_K_NORM = range(16, 22)
-T_LM_HEAD, T_FINAL_NORM = 32, 33
+T_LM_HEAD, T_FINAL_NORM, T_EMBED = 32, 33, 34
 T_SCALES = 0x100
 MATRICES = (T_Q, T_K, T_V, T_O, T_GATE, T_UP, T_DOWN)
 NORMS = (T_ATTN_NORM, T_POST_ATTN_NORM, T_FFN_NORM, T_POST_FFN_NORM, T_Q_NORM, T_K_NORM)
@@ -55,6 +55,30 @@ class XpConfig(C.Structure):
 
     def is_global(self, layer: int) -> bool:
         return self.global_every == 0 or (layer + 1) % self.global_every == 0
+
+
+class GgufInfo(C.Structure):
+    _fields_ = [("version", C.c_uint32)] + [(n, C.c_uint64) for n in (
+        "n_tensors", "n_meta", "alignment", "data_offset", "file_size")]
+
+
+class GgufModel(C.Structure):
+    _fields_ = [("arch", C.c_char * 32)] + [(n, C.c_uint32) for n in (
+        "n_layers", "n_heads", "n_kv_heads", "hidden", "ffn", "context_length", "key_length",
+        "value_length", "vocab", "sliding_window", "head_dim")] + [
+        ("rope_freq_base", C.c_float), ("rms_eps", C.c_float)]
+
+
+class LoadStats(C.Structure):
+    _fields_ = [(n, C.c_double) for n in ("total_ms", "pack_ms", "cache_ms", "upload_ms")] + [
+        ("packed_bytes", C.c_uint64), ("from_cache", C.c_int32), ("cache_written", C.c_int32),
+        ("threads", C.c_uint32), ("n_tensors", C.c_uint32)]
+
+
+# enum xp_ggml_type / xp_load_flags
+GGML_F32, GGML_F16, GGML_Q4_0, GGML_Q4_1, GGML_Q5_0, GGML_Q5_1, GGML_Q8_0 = 0, 1, 2, 3, 6, 7, 8
+GGML_Q4_K, GGML_Q6_K, GGML_BF16 = 12, 14, 30
+LOAD_REPACK, LOAD_NORM_RAW, LOAD_NO_EMBED = 1, 2, 4
 
 
 class XpMetrics(C.Structure):
@@ -123,6 +147,25 @@ def _declare(lib: C.CDLL) -> None:
         "xp_batch_last_ms": (i32, [vp, P(f32)]),
         "xp_tensor_bytes": (i32, [P(XpConfig), i32, i32, P(sz)]),
         "xp_session_upload": (i32, [vp, i32, i32, vp, sz]),
+        "xp_session_upload_part": (i32, [vp, i32, i32, sz, vp, sz]),
+        "xp_gguf_open": (i32, [C.c_char_p, P(vp)]),
+        "xp_gguf_close": (i32, [vp]),
+        "xp_gguf_get_info": (i32, [vp, P(GgufInfo)]),
+        "xp_gguf_get_model": (i32, [vp, P(GgufModel)]),
+        "xp_gguf_tensor_count": (i32, [vp, P(C.c_uint64)]),
+        "xp_gguf_tensor_at": (i32, [vp, C.c_uint64, C.c_char_p, sz]),
+        "xp_gguf_tensor_info": (i32, [vp, C.c_char_p, P(u32), P(u32), P(C.c_uint64),
+                                      P(C.c_uint64)]),
+        "xp_gguf_meta_number": (i32, [vp, C.c_char_p, P(C.c_double)]),
+        "xp_gguf_meta_string": (i32, [vp, C.c_char_p, C.c_char_p, sz, P(sz)]),
+        "xp_gguf_meta_array_length": (i32, [vp, C.c_char_p, P(C.c_uint64)]),
+        "xp_dequantize": (i32, [u32, vp, vp, C.c_uint64]),
+        "xp_gguf_dequantize_rows": (i32, [vp, C.c_char_p, C.c_uint64, C.c_uint64, vp]),
+        "xp_config_from_gguf": (i32, [vp, P(XpConfig)]),
+        "xp_pack_int4": (i32, [vp, u32, u32, i32, u32, vp, vp]),
+        "xp_gguf_pack_model": (i32, [vp, P(XpConfig), C.c_char_p, u32, P(LoadStats)]),
+        "xp_gguf_verify_cache": (i32, [vp, P(XpConfig), C.c_char_p, u32, P(u32)]),
+        "xp_session_load_gguf": (i32, [vp, vp, C.c_char_p, u32, u32, P(LoadStats)]),
         "xp_synth_tensor": (i32, [P(XpConfig), u32, i32, i32, vp, sz]),
         "xp_session_synthesize": (i32, [vp, u32]),
         "xp_session_kv_upload": (i32, [vp, i32, i32, u32, u32, vp]),
@@ -437,6 +480,14 @@ class DecodeSession:
     def synthesize(self, seed: int) -> None:
         call("xp_session_synthesize", self.h, seed)
 
+    def load_gguf(self, g: "Gguf", cache: str | None = None, flags: int = 0,
+                  threads: int = 0) -> LoadStats:
+        """Requantises and uploads a GGUF model (xp_session_load_gguf)."""
+        st = LoadStats()
+        call("xp_session_load_gguf", self.h, g.h, cache.encode() if cache else None, flags,
+             threads, C.byref(st))
+        return st
+
     def upload(self, layer: int, tensor: int, a: np.ndarray) -> None:
         a = np.ascontiguousarray(a)
         call("xp_session_upload", self.h, layer, tensor, a.ctypes.data, a.nbytes)
@@ -533,3 +584,117 @@ def draw(val, idx, temperature: float, top_k: int, top_p: float, u: float) -> in
 
 def philox_uniform(seed: int, seq: int, step: int) -> float:
     return float(lib().xp_philox_uniform(seed, seq, step))
+
+
+class Gguf:
+    """An open GGUF model file (xp_gguf_*): metadata, tensor table,
+    dequantisation, and the packed-weight cache."""
+
+    def __init__(self, path: str):
+        h = C.c_void_p()
+        call("xp_gguf_open", path.encode(), C.byref(h))
+        self.h = h
+        self.path = path
+
+    def close(self) -> None:
+        if self.h and self.h.value and _lib is not None:
+            _lib.xp_gguf_close(self.h)
+        self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def info(self) -> GgufInfo:
+        i = GgufInfo()
+        call("xp_gguf_get_info", self.h, C.byref(i))
+        return i
+
+    def model(self) -> GgufModel:
+        m = GgufModel()
+        call("xp_gguf_get_model", self.h, C.byref(m))
+        return m
+
+    def tensor_names(self) -> list[str]:
+        n = C.c_uint64()
+        call("xp_gguf_tensor_count", self.h, C.byref(n))
+        buf = C.create_string_buffer(256)
+        out = []
+        for i in range(n.value):
+            call("xp_gguf_tensor_at", self.h, i, buf, 256)
+            out.append(buf.value.decode())
+        return out
+
+    def tensor(self, name: str) -> tuple[int, tuple, int]:
+        """(ggml type, dims (fastest first, n_dims of them), bytes)."""
+        t, nd, nb = C.c_uint32(), C.c_uint32(), C.c_uint64()
+        dims = (C.c_uint64 * 4)()
+        call("xp_gguf_tensor_info", self.h, name.encode(), C.byref(t), C.byref(nd), dims,
+             C.byref(nb))
+        return t.value, tuple(dims[i] for i in range(nd.value)), nb.value
+
+    def number(self, key: str) -> float:
+        v = C.c_double()
+        call("xp_gguf_meta_number", self.h, key.encode(), C.byref(v))
+        return v.value
+
+    def string(self, key: str) -> str:
+        n = C.c_size_t()
+        call("xp_gguf_meta_string", self.h, key.encode(), None, 0, C.byref(n))
+        buf = C.create_string_buffer(n.value + 1)
+        call("xp_gguf_meta_string", self.h, key.encode(), buf, n.value + 1, None)
+        return buf.raw[:n.value].decode(errors="replace")
+
+    def array_length(self, key: str) -> int:
+        n = C.c_uint64()
+        call("xp_gguf_meta_array_length", self.h, key.encode(), C.byref(n))
+        return n.value
+
+    def rows(self, name: str, row0: int = 0, nrows: int | None = None) -> np.ndarray:
+        """Rows of a 2-D tensor dequantised to fp32 [nrows][dims[0]]."""
+        _, dims, _ = self.tensor(name)
+        total = 1
+        for d in dims[1:]:
+            total *= d
+        if nrows is None:
+            nrows = total - row0
+        out = np.empty((nrows, dims[0]), np.float32)
+        call("xp_gguf_dequantize_rows", self.h, name.encode(), row0, nrows, out.ctypes.data)
+        return out
+
+    def config(self, base: XpConfig | None = None) -> XpConfig:
+        """The shapes of this file over `base` (default the Gemma-3-1B config)."""
+        c = base if base is not None else XpConfig.gemma3_1b()
+        call("xp_config_from_gguf", self.h, C.byref(c))
+        return c
+
+    def pack_model(self, cfg: XpConfig, cache: str, threads: int = 0) -> LoadStats:
+        st = LoadStats()
+        call("xp_gguf_pack_model", self.h, C.byref(cfg), cache.encode(), threads, C.byref(st))
+        return st
+
+    def verify_cache(self, cfg: XpConfig, cache: str, threads: int = 0) -> int:
+        bad = C.c_uint32()
+        call("xp_gguf_verify_cache", self.h, C.byref(cfg), cache.encode(), threads, C.byref(bad))
+        return bad.value
+
+
+def dequantize(ggml_type: int, raw: np.ndarray, n: int) -> np.ndarray:
+    out = np.empty(n, np.float32)
+    raw = np.ascontiguousarray(raw)
+    call("xp_dequantize", ggml_type, raw.ctypes.data, out.ctypes.data, n)
+    return out
+
+
+def pack_int4(w_cols: np.ndarray, scale_fmt: int = XP_SCALE_BF16_QUAD, threads: int = 0):
+    """Requantises w[cols][rows] (GGUF row order) to (KM4 plane, scale plane)."""
+    w_cols = np.ascontiguousarray(w_cols, np.float32)
+    cols, rows = w_cols.shape
+    wq = np.empty(rows * cols // 8, np.uint32)
+    sc = np.empty(rows // 32 * cols, np.uint16 if scale_fmt == XP_SCALE_BF16_QUAD else np.float32)
+    call("xp_pack_int4", w_cols.ctypes.data, rows, cols, scale_fmt, threads, wq.ctypes.data,
+         sc.ctypes.data)
+    return wq, sc
+

@@ -1,11 +1,16 @@
 // xpose_decode — command-line decode driver over include/xpose.hpp, the
 // counterpart of the reference's decode CLI (examples/llm/decode.cpp:
-// 2720-3006) for the seeded synthetic Gemma-3-1B model (no GGUF or tokenizer
-// on this path: weights are random int4 with fp16 group scales).
+// 2720-3006): the seeded synthetic Gemma-3-1B model (random int4 weights with
+// fp16 group scales), or a GGUF model with --model (requantised to int4 with
+// bf16 scales, through the pack cache). There is no tokenizer on this path:
+// prompts are token ids.
 //
 //   xpose_decode [--layers N] [--prompt N] [--tokens N] [--ctx P] [--seed S]
 //                [--exec token|graph|launch] [--curve] [--ids]
+//                [--model FILE [--cache PATH | --no-cache] [--repack] [--verify-cache]]
 //
+// --cache defaults to FILE.xpack. --verify-cache repacks every matrix and
+// compares the cache byte for byte, then exits (no GPU).
 // --ctx P pre-fills every layer's KV cache with fp16 N(0,1) rows 0..P-1 and
 // decodes from position P (benchmark config 4); otherwise a --prompt of
 // uniform-random ids is prefilled first (config 3). --curve reports tok/s per
@@ -18,6 +23,7 @@
 #include <cstdlib>
 #include <cstring>
 #include <map>
+#include <memory>
 #include <string>
 #include <vector>
 
@@ -33,7 +39,9 @@ double now_ms() {
 int usage() {
     std::fprintf(stderr,
                  "usage: xpose_decode [--layers N] [--prompt N] [--tokens N] [--ctx P] "
-                 "[--seed S] [--exec token|graph|launch] [--curve] [--ids]\n");
+                 "[--seed S] [--exec token|graph|launch] [--curve] [--ids]\n"
+                 "                    [--model FILE [--cache PATH | --no-cache] [--repack] "
+                 "[--verify-cache]]\n");
     return 2;
 }
 
@@ -42,7 +50,8 @@ int usage() {
 int main(int argc, char** argv) {
     uint32_t layers = 26, prompt = 32, tokens = 128, ctx = 0, seed = 0x5EED0003u;
     int exec = XP_EXEC_AUTO;
-    bool curve = false, print_ids = false;
+    bool curve = false, print_ids = false, no_cache = false, repack = false, verify = false;
+    std::string model, cache;
     for (int i = 1; i < argc; ++i) {
         const std::string a = argv[i];
         auto next = [&]() -> const char* { return i + 1 < argc ? argv[++i] : nullptr; };
@@ -59,19 +68,54 @@ int main(int argc, char** argv) {
             if (exec < 0) return usage();
         } else if (a == "--curve") curve = true;
         else if (a == "--ids") print_ids = true;
+        else if (a == "--model" && (v = next())) model = v;
+        else if (a == "--cache" && (v = next())) cache = v;
+        else if (a == "--no-cache") no_cache = true;
+        else if (a == "--repack") repack = true;
+        else if (a == "--verify-cache") verify = true;
         else return usage();
     }
+    if ((verify || repack || no_cache || !cache.empty()) && model.empty()) return usage();
+    if (!model.empty() && cache.empty() && !no_cache) cache = model + ".xpack";
     try {
         xpose::llm::Config cfg;
         cfg.n_layers = layers;
         cfg.exec_mode = exec;
+        std::unique_ptr<xpose::llm::Model> gguf;
+        if (!model.empty()) {
+            gguf.reset(new xpose::llm::Model(model));
+            cfg = gguf->config(cfg);
+            if (verify) {
+                const uint32_t bad = gguf->verify_cache(cfg, cache);
+                std::printf("%s: %s\n", cache.c_str(),
+                            bad ? "FAIL: the cache does not match a fresh pack"
+                                : "PASS: cached bytes are identical to a fresh pack");
+                return bad ? 1 : 0;
+            }
+        }
         const double t0 = now_ms();
-        xpose::llm::DecodeSession sess(cfg);
-        sess.synthesize(seed);
+        std::unique_ptr<xpose::llm::DecodeSession> sp;
+        if (gguf)
+            sp.reset(new xpose::llm::DecodeSession(*gguf, cfg, no_cache ? std::string() : cache,
+                                                   repack ? XP_LOAD_REPACK : 0u));
+        else
+            sp.reset(new xpose::llm::DecodeSession(cfg));
+        xpose::llm::DecodeSession& sess = *sp;
+        if (!gguf) sess.synthesize(seed);
         const double load_ms = now_ms() - t0;
         std::printf("device      %s\n", sess.device_name().c_str());
-        std::printf("weights     %.1f MiB packed int4 + fp16 scales (synthesised in %.0f ms)\n",
-                    double(sess.weight_bytes()) / (1024.0 * 1024.0), load_ms);
+        if (gguf) {
+            const xp_load_stats& ls = sess.load_stats();
+            std::printf("weights     %.1f MiB packed int4 + bf16 scales from %s in %.0f ms "
+                        "(%s; pack %.0f ms, cache %.0f ms, upload %.0f ms, %u threads)\n",
+                        double(sess.weight_bytes()) / (1024.0 * 1024.0), model.c_str(), load_ms,
+                        ls.from_cache ? "from the pack cache"
+                                      : (ls.cache_written ? "packed, cache written" : "packed"),
+                        ls.pack_ms, ls.cache_ms, ls.upload_ms, ls.threads);
+        } else {
+            std::printf("weights     %.1f MiB packed int4 + fp16 scales (synthesised in %.0f ms)\n",
+                        double(sess.weight_bytes()) / (1024.0 * 1024.0), load_ms);
+        }
         std::printf("kv cache    %.1f MiB (%u positions)\n",
                     double(sess.kv_bytes()) / (1024.0 * 1024.0), cfg.max_seq);
 

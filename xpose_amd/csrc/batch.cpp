@@ -98,7 +98,7 @@ int Batch::record() {
         g.tickets_cap = tickets_cap;
         return launch_bmm(g, fmt, w.n_cu, st, who);
     };
-    XB(launch_bembed(x, w.lm_w, w.lm_s, fmt, H, c.vocab, w.embed_scale, d_tok, B, st));
+    XB(launch_bembed(x, w.lm_w, w.lm_s, fmt, H, c.vocab, w.embed_scale, d_tok, B, w.embed, st));
     XB(prep(0, x, nullptr, nullptr, nullptr, w.layer[0].norm[0], H));
     for (uint32_t l = 0; l < c.n_layers; ++l) {
         const SessionWeights::Layer& L = w.layer[l];

@@ -170,11 +170,15 @@ __global__ __launch_bounds__(kPrepThreads) void bprep_kernel(BprepArgs a) {
 // x[b][k] = dequant(tied table column tok[b])[k] * embed_scale (decode.cpp:1618-1627).
 __global__ __launch_bounds__(256) void bembed_kernel(float* x, const void* wq, const void* sc, int fmt,
                                                      uint32_t hidden, uint32_t vocab, float embed_scale,
-                                                     const uint32_t* tok) {
+                                                     const uint32_t* tok, const float* table) {
     const uint32_t b = blockIdx.y, k = blockIdx.x * 256 + threadIdx.x;
     if (k >= hidden) return;
     uint32_t t = tok[b];
     if (t >= vocab) t = 0;
+    if (table) {   // the model's own fp32 embedding rows
+        x[size_t(b) * hidden + k] = table[size_t(t) * hidden + k] * embed_scale;
+        return;
+    }
     const uint32_t nblk = hidden / kBlk, blk = k / kBlk, i = k % kBlk;
     const uint32_t* w = static_cast<const uint32_t*>(wq);
     const uint32_t word = w[((size_t(t / kGrp) * nblk + blk) * kGrp + (t % kGrp)) * 4 + i / 8];
@@ -324,9 +328,10 @@ int launch_bprep(const BprepArgs& a, uint32_t batch, hipStream_t st) {
 }
 
 int launch_bembed(float* x, const void* wq, const void* sc, int fmt, uint32_t hidden, uint32_t vocab,
-                  float embed_scale, const uint32_t* tok, uint32_t batch, hipStream_t st) {
+                  float embed_scale, const uint32_t* tok, uint32_t batch, const float* table,
+                  hipStream_t st) {
     hipLaunchKernelGGL(bembed_kernel, dim3((hidden + 255) / 256, batch), dim3(256), 0, st, x, wq, sc, fmt,
-                       hidden, vocab, embed_scale, tok);
+                       hidden, vocab, embed_scale, tok, table);
     XP_LAUNCHED();
     return XP_OK;
 }

@@ -28,7 +28,7 @@ namespace xp {
 
 int launch_embed(float* x, const void* wq, const void* sc, int fmt, uint32_t hidden,
                  uint32_t vocab, float embed_scale, const uint32_t* state, uint32_t* hist,
-                 hipStream_t st);
+                 const float* table, hipStream_t st);
 int launch_norm_res_norm(float* x, const float* y, const float* w_post, const float* w_pre,
                          float* out, uint32_t n, float eps, hipStream_t st);
 int launch_advance(uint32_t* state, hipStream_t st);
@@ -81,6 +81,8 @@ size_t tensor_bytes(const xp_config& c, int layer, int tensor) {
         return 0;
     } else if (t == XP_T_FINAL_NORM) {
         return layer == -1 ? size_t(c.hidden) * 4 : 0;
+    } else if (t == XP_T_EMBED) {
+        return layer == -1 ? size_t(c.vocab) * c.hidden * 4 : 0;
     } else if (t >= XP_T_ATTN_NORM && t <= XP_T_K_NORM) {
         if (layer < 0 || uint32_t(layer) >= c.n_layers) return 0;
         return (t >= XP_T_Q_NORM ? size_t(c.head_dim) : size_t(c.hidden)) * 4;
@@ -148,6 +150,7 @@ struct Session {
     void* lm_w = nullptr;
     void* lm_s = nullptr;
     float* final_norm = nullptr;
+    float* embed = nullptr;      // optional fp32 [vocab][hidden] embedding rows
     float *x, *xb, *xb2, *q_raw, *k_raw, *v, *q, *k, *att, *gate, *up, *hb, *logits;
     float* mv_partial = nullptr;
     size_t mv_partial_cap = 0;
@@ -207,7 +210,7 @@ int Session::record(int variant, uint32_t& n) {
         if ((rc = (call)) != XP_OK) return rc; \
         ++n;                         \
     } while (0)
-    XP_STEP(launch_embed(x, lm_w, lm_s, fmt, H, c.vocab, embed_scale(), state, hist, st));
+    XP_STEP(launch_embed(x, lm_w, lm_s, fmt, H, c.vocab, embed_scale(), state, hist, embed, st));
     XP_STEP(launch_norm_res_norm(x, nullptr, nullptr, L[0].norm[0], xb, H, eps, st));
     for (uint32_t l = 0; l < c.n_layers; ++l) {
         Layer& w = L[l];
@@ -394,6 +397,7 @@ int session_weights(const xp_session* h, SessionWeights* out) {
     out->lm_w = s.lm_w;
     out->lm_s = s.lm_s;
     out->final_norm = s.final_norm;
+    out->embed = s.embed;
     return XP_OK;
 }
 }  // namespace xp
@@ -412,6 +416,7 @@ int destroy(xp_session* h) {
     if (s.kvarena) (void)hipFree(s.kvarena);
     if (s.aarena) (void)hipFree(s.aarena);
     if (s.tarena) (void)hipFree(s.tarena);
+    if (s.embed) (void)hipFree(s.embed);
     if (s.trace_buf) (void)hipFree(s.trace_buf);
     if (s.h_ids) (void)hipHostFree(s.h_ids);
     if (s.h_stat) (void)hipHostFree(s.h_stat);
@@ -493,6 +498,7 @@ int setup_token(Session& s) {
     a.lm_w = s.lm_w;
     a.lm_s = s.lm_s;
     a.final_norm = s.final_norm;
+    a.embed_f32 = s.embed;
     a.freq_local = fl;
     a.freq_global = fg;
     a.logits = s.logits;
@@ -746,19 +752,47 @@ int xp_session_destroy(xp_session* h) { return destroy(h); }
 
 int xp_session_upload(xp_session* h, int layer, int tensor, const void* host, size_t bytes) {
     XP_REQUIRE(h && host, "null pointer");
-    Session& s = h->s;
-    const size_t need = tensor_bytes(s.cfg, layer, tensor);
+    const size_t need = tensor_bytes(h->s.cfg, layer, tensor);
     XP_REQUIRE(need > 0, "no tensor %d at layer %d", tensor, layer);
     XP_REQUIRE(bytes == need, "tensor %d at layer %d is %zu bytes, got %zu", tensor, layer, need,
                bytes);
+    return xp_session_upload_part(h, layer, tensor, 0, host, bytes);
+}
+
+int xp_session_upload_part(xp_session* h, int layer, int tensor, size_t offset, const void* host,
+                           size_t bytes) {
+    XP_REQUIRE(h && host, "null pointer");
+    Session& s = h->s;
+    const size_t need = tensor_bytes(s.cfg, layer, tensor);
+    XP_REQUIRE(need > 0, "no tensor %d at layer %d", tensor, layer);
+    XP_REQUIRE(offset <= need && bytes <= need - offset,
+               "bytes [%zu, +%zu) outside tensor %d at layer %d (%zu bytes)", offset, bytes, tensor,
+               layer, need);
     const bool sc = (tensor & XP_T_SCALES) != 0;
     const int t = tensor & ~XP_T_SCALES;
     void* dst = nullptr;
-    if (t == XP_T_LM_HEAD) dst = sc ? s.lm_s : s.lm_w;
+    if (t == XP_T_EMBED) {
+        if (!s.embed) {
+            // First use: allocate the table and drop recorded graphs, whose
+            // embedding step was recorded without it.
+            XP_HIP(hipStreamSynchronize(s.st));
+            if (hipMalloc(&s.embed, need) != hipSuccess) {
+                s.embed = nullptr;
+                return set_error(XP_E_NOMEM, "xp_session_upload_part: %zu embedding bytes", need);
+            }
+            for (auto& g : s.graph)
+                if (g) {
+                    (void)hipGraphExecDestroy(g);
+                    g = nullptr;
+                }
+            s.ta.embed_f32 = s.embed;
+        }
+        dst = s.embed;
+    } else if (t == XP_T_LM_HEAD) dst = sc ? s.lm_s : s.lm_w;
     else if (t == XP_T_FINAL_NORM) dst = s.final_norm;
     else if (t <= XP_T_DOWN) dst = sc ? s.L[layer].s[t] : s.L[layer].w[t];
     else dst = s.L[layer].norm[t - XP_T_ATTN_NORM];
-    XP_HIP(hipMemcpy(dst, host, bytes, hipMemcpyHostToDevice));
+    XP_HIP(hipMemcpy(static_cast<char*>(dst) + offset, host, bytes, hipMemcpyHostToDevice));
     return XP_OK;
 }
 

@@ -30,13 +30,17 @@ __device__ __forceinline__ float blk_sum(float v, float* red) {
 // state[0] = position, state[1] = token to run.
 __global__ void embed_kernel(float* x, const u32x4* wq, const void* sc, int fmt,
                              uint32_t hidden, uint32_t vocab, float embed_scale,
-                             const uint32_t* state, uint32_t* hist) {
+                             const uint32_t* state, uint32_t* hist, const float* table) {
     const uint32_t pos = state[0];
     uint32_t tok = state[1];
     if (tok >= vocab) tok = 0;   // the host validates ids; never read out of bounds
     const uint32_t k = blockIdx.x * blockDim.x + threadIdx.x;
     if (k == 0) hist[pos] = tok;
     if (k >= hidden) return;
+    if (table) {   // the model's own fp32 embedding rows
+        x[k] = table[size_t(tok) * hidden + k] * embed_scale;
+        return;
+    }
     const uint32_t nblk = hidden / kBlk, b = k / kBlk;
     const u32x4 w = wq[(size_t(tok / kGrp) * nblk + b) * kGrp + (tok % kGrp)];
     const uint32_t t = k % kBlk;
@@ -88,10 +92,10 @@ __global__ void advance_kernel(uint32_t* state) { state[0] += 1u; }
 
 int launch_embed(float* x, const void* wq, const void* sc, int fmt, uint32_t hidden,
                  uint32_t vocab, float embed_scale, const uint32_t* state, uint32_t* hist,
-                 hipStream_t st) {
+                 const float* table, hipStream_t st) {
     hipLaunchKernelGGL(embed_kernel, dim3((hidden + 255) / 256), dim3(256), 0, st, x,
                        reinterpret_cast<const u32x4*>(wq), sc, fmt, hidden, vocab, embed_scale,
-                       state, hist);
+                       state, hist, table);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return set_error(XP_E_HIP, "embed: launch -> %s", hipGetErrorString(e));
     return XP_OK;

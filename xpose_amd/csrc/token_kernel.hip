@@ -522,7 +522,17 @@ __global__ __launch_bounds__(kTkThreads) void token_kernel(TokArgs a) {
                 ld_own(w_in, L.norm[0] + kOwn * tid);
                 if (l > 0) ld_own(w_post, S.lt[l - 1u].norm[3] + kOwn * tid);
             }
-            if (l == 0) {
+            if (l == 0 && a.embed_f32) {
+                // embedding (decode.cpp:1618-1627) from the model's fp32 rows
+                if (hown) {
+                    const float4 e4 = *reinterpret_cast<const float4*>(
+                        a.embed_f32 + size_t(tok) * H + kOwn * tid);
+                    x[0] = e4.x * a.embed_scale;
+                    x[1] = e4.y * a.embed_scale;
+                    x[2] = e4.z * a.embed_scale;
+                    x[3] = e4.w * a.embed_scale;
+                }
+            } else if (l == 0) {
                 // embedding (decode.cpp:1618-1627) as a gather from the tied int4 table
                 if (hown) {
                     // element k = kOwn tid + e: block k / 32, word (k % 32) / 8, nibble k % 8

@@ -103,7 +103,8 @@ struct BprepArgs {
 };
 int launch_bprep(const BprepArgs& a, uint32_t batch, hipStream_t st);
 int launch_bembed(float* x, const void* wq, const void* sc, int fmt, uint32_t hidden, uint32_t vocab,
-                  float embed_scale, const uint32_t* tok, uint32_t batch, hipStream_t st);
+                  float embed_scale, const uint32_t* tok, uint32_t batch, const float* table,
+                  hipStream_t st);
 int launch_badvance(uint32_t* pos, uint32_t batch, hipStream_t st);
 // y[m][row][col] = sum_k A[row][k] W_m[k][col] for the staged A (rows = sequences).
 struct BmmArgs {
@@ -139,6 +140,7 @@ struct SessionWeights {
     const void* lm_w;
     const void* lm_s;
     const float* final_norm;
+    const float* embed;         // optional fp32 [vocab][hidden] embedding rows
 };
 int session_weights(const xp_session* h, SessionWeights* out);
 // The session's host draw and Philox uniform (decode.cpp:1873-1917).
@@ -166,6 +168,7 @@ struct TokArgs {
     const void* lm_w;
     const void* lm_s;
     const float* final_norm;
+    const float* embed_f32;               // optional fp32 [vocab][hidden] embedding rows
     const float* freq_local;              // [head_dim/2] theta^(-2d/head_dim)
     const float* freq_global;
     // Exchange slots: 8 bytes = (launch tag << 32) | fp32 bits, written with
