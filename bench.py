@@ -127,12 +127,16 @@ def attention_leg(X, span: int, iters: int = 192):
 
 
 def cfg3_leg(X, sess, cfg, n_gen: int = 128):
-    """benchmark config 3: prefill a 32-token prompt of uniform random ids from
-    position 0, then greedy-decode `n_gen` tokens (decode tok/s, prefill
+    """Benchmark config 3: prefill a 32-token prompt of uniform random ids from
+    position 0 (timed on its second run: the first builds the batched prefill
+    step), then greedy-decode `n_gen` tokens (decode tok/s, prefill
     excluded)."""
     r = np.random.default_rng(SEED)
     prompt = r.integers(0, cfg.vocab, 32).astype(np.uint32)
     sess.set_position(0)
+    sess.prefill(prompt)             # first use builds the batched prefill step
+    sess.set_position(0)
+    X.synchronize()
     t0 = time.perf_counter()
     sess.prefill(prompt)
     X.synchronize()
@@ -142,7 +146,8 @@ def cfg3_leg(X, sess, cfg, n_gen: int = 128):
     X.synchronize()
     el = time.perf_counter() - t0
     return {"prompt": 32, "generated": n_gen, "decode_tok_s": round(n_gen / el, 1),
-            "prefill_ms": round(t_pre * 1e3, 3), "ids_head": [int(v) for v in ids[:4]]}
+            "prefill_ms": round(t_pre * 1e3, 3), "prefill_tok_s": round(32 / t_pre, 1),
+            "ids_head": [int(v) for v in ids[:4]]}
 
 
 def cfg4_leg(X, sess, cfg, ctx: int = 4096):

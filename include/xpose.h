@@ -289,7 +289,15 @@ typedef struct {
      * by one) or XP_EXEC_TOKEN (the persistent kernel; creation fails if the
      * shape or device does not allow it). */
     int32_t  exec_mode;
+    /* How xp_session_prefill runs a prompt of n >= 3 tokens: XP_PREFILL_AUTO
+     * (the first n - 1 tokens through the batched M = 16 step, 16 positions
+     * per pass on the session's KV cache, then the last token on the
+     * session's own path) or XP_PREFILL_TOKENS (one token step per token,
+     * the reference's decode-shaped prefill, decode.cpp:1785-1815). */
+    int32_t  prefill_mode;
 } xp_config;
+
+enum xp_prefill_mode { XP_PREFILL_AUTO = 0, XP_PREFILL_TOKENS = 1 };
 
 enum xp_exec_mode {
     XP_EXEC_AUTO = 0, XP_EXEC_GRAPH = 1, XP_EXEC_LAUNCH = 2, XP_EXEC_TOKEN = 3

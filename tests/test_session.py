@@ -334,3 +334,51 @@ def test_gpu_session_error_paths(xp):
     with pytest.raises(X.XposeError) as e:
         s.decode_step()
     assert "full" in str(e.value)
+
+
+@pytest.mark.gpu
+def test_gpu_batched_prefill(xp, xo, mode):
+    """xp_session_prefill with XP_PREFILL_AUTO runs the first n - 1 prompt
+    tokens through the batched step (16 positions per pass on the session's
+    KV cache): against the oracle's token-by-token prefill, every appended
+    K/V row within 1e-3 of its row's max (the batched GEMM's A operand is two
+    bf16 terms), the last logits within 1e-3; against XP_PREFILL_TOKENS the
+    same; rows past the prompt untouched. The prompt (37 tokens) is not a
+    multiple of 16 and starts at 490, so it crosses the 512-position window
+    of the local layers."""
+    X = xp
+    print("case batched prefill", flush=True)
+    pos0, n = 490, 37
+    kvd = 256
+    outs = {}
+    for pm in (X.XP_PREFILL_AUTO, X.XP_PREFILL_TOKENS):
+        cfg = cfg_small(X, n_layers=6, vocab=16384, exec_mode=mode, prefill_mode=pm)
+        sess, model = make_pair(X, xo, cfg)
+        for l in range(cfg.n_layers):
+            for which in (0, 1):
+                rows = X.synth_normal_f16(cfg.max_seq * kvd, 77, 2 * l + which)
+                sess.kv_upload(l, which, 0, rows)
+                (model.kcache if which == 0 else model.vcache)[l][:] = rows
+        sess.set_position(pos0)
+        prompt = np.random.default_rng(8).integers(0, cfg.vocab, n).astype(np.uint32)
+        sess.prefill(prompt)
+        assert sess.position == pos0 + n
+        want = None
+        for i, t in enumerate(prompt):
+            want = model.forward(int(t), pos0 + i, i == n - 1)
+        ok, msg = logits_close(sess.last_logits(), want)
+        assert ok, f"prefill mode {pm}: {msg}"
+        for l in range(cfg.n_layers):
+            for which, ref in ((0, model.kcache[l]), (1, model.vcache[l])):
+                got = sess.kv_download(l, which, pos0, n).view(np.float16).astype(np.float64)
+                exp = ref[pos0 * kvd:(pos0 + n) * kvd].view(np.float16).astype(np.float64)
+                err = np.abs(got - exp).reshape(n, kvd).max(axis=1)
+                assert np.all(err <= 1e-3 * np.abs(exp).reshape(n, kvd).max(axis=1)), (pm, l, which)
+                past = sess.kv_download(l, which, pos0 + n, 8)
+                assert np.array_equal(past, ref[(pos0 + n) * kvd:(pos0 + n + 8) * kvd]), (pm, l)
+        outs[pm] = ([sess.decode_step() for _ in range(4)], sess.last_logits())
+        sess.close()
+    a, b = outs[X.XP_PREFILL_AUTO], outs[X.XP_PREFILL_TOKENS]
+    assert a[0] == b[0]
+    ok, msg = logits_close(a[1], b[1])
+    assert ok, msg

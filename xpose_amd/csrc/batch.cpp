@@ -67,6 +67,9 @@ struct Batch {
     std::vector<uint32_t> pos, steps;
     bool logits_valid = false;
     float last_ms = 0.0f;
+    // Prefill mode: the rows are consecutive positions of one sequence and
+    // share the session's KV cache; the step ends after the last layer.
+    bool prefill = false;
 
     int record();
     int forward(const uint32_t* tokens);
@@ -112,8 +115,10 @@ int Batch::record() {
         qa.batch = B;
         qa.bq = qd;
         qa.bkv = kvd;
-        qa.bcache = size_t(S) * kvd;
+        qa.bcache = prefill ? 0 : size_t(S) * kvd;   // prefill rows share one cache
         XB(launch_qk(qa, glob ? c.rope_theta_global : c.rope_theta_local, st));
+        // prefill: the last layer's K/V rows are the last thing the step must produce
+        if (prefill && l + 1 == c.n_layers) break;
         AttnArgs aa{};
         aa.out = att; aa.q = q; aa.kc = kc[l]; aa.vc = vc[l];
         aa.n_heads = c.n_heads; aa.kv_heads = c.n_kv_heads; aa.head_dim = c.head_dim;
@@ -124,7 +129,7 @@ int Batch::record() {
         aa.tickets = attn_tickets;
         aa.batch = B;
         aa.bq = qd;
-        aa.bcache = size_t(S) * kvd;
+        aa.bcache = prefill ? 0 : size_t(S) * kvd;
         aa.bpart = attn_part_seq;
         const uint32_t max_span = glob || c.sliding_window == 0 ? S : std::min(c.sliding_window, S);
         XB(launch_attention(aa, max_span, st));
@@ -141,11 +146,13 @@ int Batch::record() {
         const float* next = l + 1 < c.n_layers ? w.layer[l + 1].norm[0] : w.final_norm;
         XB(prep(1, x, dn, nullptr, L.norm[3], next, H));
     }
-    const MvMatDesc lm{logits, w.lm_w, w.lm_s, c.vocab};
-    XB(gemm(&lm, 1, H, "batch lm_head"));
-    XB(launch_topk4(cval, cidx, logits, c.vocab, kHarvestParts, st, B));
-    XB(launch_select_rows(oval, oidx, cval, cidx, kHarvest, kCand, B, st));
-    XB(launch_badvance(d_pos, B, st));
+    if (!prefill) {
+        const MvMatDesc lm{logits, w.lm_w, w.lm_s, c.vocab};
+        XB(gemm(&lm, 1, H, "batch lm_head"));
+        XB(launch_topk4(cval, cidx, logits, c.vocab, kHarvestParts, st, B));
+        XB(launch_select_rows(oval, oidx, cval, cidx, kHarvest, kCand, B, st));
+        XB(launch_badvance(d_pos, B, st));
+    }
 #undef XB
     return XP_OK;
 }
@@ -180,8 +187,10 @@ int Batch::forward(const uint32_t* tokens) {
     XP_HIP(hipEventRecord(ev[0], st));
     XP_HIP(hipGraphLaunch(graph, st));
     XP_HIP(hipEventRecord(ev[1], st));
-    XP_HIP(hipMemcpyAsync(h_val, oval, size_t(B) * kCand * 4, hipMemcpyDeviceToHost, st));
-    XP_HIP(hipMemcpyAsync(h_idx, oidx, size_t(B) * kCand * 4, hipMemcpyDeviceToHost, st));
+    if (!prefill) {
+        XP_HIP(hipMemcpyAsync(h_val, oval, size_t(B) * kCand * 4, hipMemcpyDeviceToHost, st));
+        XP_HIP(hipMemcpyAsync(h_idx, oidx, size_t(B) * kCand * 4, hipMemcpyDeviceToHost, st));
+    }
     XP_HIP(hipStreamSynchronize(st));
     (void)hipEventElapsedTime(&last_ms, ev[0], ev[1]);
     for (uint32_t i = 0; i < B; ++i) ++pos[i];
@@ -212,9 +221,13 @@ struct xp_batch {
     Batch b;
 };
 
-extern "C" {
+namespace {
 
-int xp_batch_create(const xp_session* weights, uint32_t n_seq, uint32_t max_seq, xp_batch** out) {
+// A batch of n_seq rows over the session's weights. prefill: the rows are
+// positions of one sequence on the session's own KV cache (no caches of its
+// own, no lm_head or sampling).
+int make_batch(const xp_session* weights, uint32_t n_seq, uint32_t max_seq, bool prefill,
+               xp_batch** out) {
     XP_REQUIRE(weights && out, "null pointer");
     *out = nullptr;
     XP_REQUIRE(n_seq >= 1 && n_seq <= kBatchMax, "n_seq=%u must be in [1, %u]", n_seq, kBatchMax);
@@ -250,6 +263,7 @@ int xp_batch_create(const xp_session* weights, uint32_t n_seq, uint32_t max_seq,
     }
     b.B = n_seq;
     b.S = max_seq;
+    b.prefill = prefill;
     b.pos.assign(n_seq, 0);
     b.steps.assign(n_seq, 0);
     const uint32_t B = n_seq, H = c.hidden, qd = c.n_heads * c.head_dim,
@@ -271,7 +285,7 @@ int xp_batch_create(const xp_session* weights, uint32_t n_seq, uint32_t max_seq,
     b.attn_part_seq = attn_partial_floats(c.n_kv_heads, c.n_heads, c.head_dim);
     const size_t kvseq = size_t(max_seq) * kvd;                 // fp16 elements per (layer, K/V, seq)
     std::vector<size_t> sz = {
-        size_t(c.n_layers) * 2 * B * kvseq * 2,                 // KV caches
+        prefill ? 0 : size_t(c.n_layers) * 2 * B * kvseq * 2,   // KV caches
         size_t(B) * H * 4, size_t(B) * qd * 4, size_t(B) * kvd * 4, size_t(B) * kvd * 4,
         size_t(B) * qd * 4, size_t(B) * kvd * 4, size_t(B) * qd * 4, size_t(B) * H * 4,
         size_t(B) * F * 4, size_t(B) * F * 4, size_t(B) * H * 4, size_t(B) * c.vocab * 4,
@@ -292,8 +306,8 @@ int xp_batch_create(const xp_session* weights, uint32_t n_seq, uint32_t max_seq,
     auto nxt = [&]() { char* r = p; p += al(sz[si++]); return r; };
     uint16_t* kv = reinterpret_cast<uint16_t*>(nxt());
     for (uint32_t l = 0; l < c.n_layers; ++l) {
-        b.kc[l] = kv + (size_t(l) * 2 + 0) * B * kvseq;
-        b.vc[l] = kv + (size_t(l) * 2 + 1) * B * kvseq;
+        b.kc[l] = prefill ? b.w.layer[l].kc : kv + (size_t(l) * 2 + 0) * B * kvseq;
+        b.vc[l] = prefill ? b.w.layer[l].vc : kv + (size_t(l) * 2 + 1) * B * kvseq;
     }
     b.x = reinterpret_cast<float*>(nxt());
     b.q_raw = reinterpret_cast<float*>(nxt());
@@ -327,6 +341,67 @@ int xp_batch_create(const xp_session* weights, uint32_t n_seq, uint32_t max_seq,
         return fail(XP_E_HIP, "hipEventCreate failed");
     *out = h;
     return XP_OK;
+}
+
+}  // namespace
+
+namespace xp {
+
+struct PrefillBatch {
+    xp_batch* b = nullptr;
+};
+
+PrefillBatch* prefill_batch_create(const xp_session* s) {
+    xp_batch* b = nullptr;
+    SessionWeights w;
+    if (session_weights(s, &w) != XP_OK) return nullptr;
+    if (make_batch(s, kBatchMax, w.cfg.max_seq, true, &b) != XP_OK) return nullptr;
+    PrefillBatch* p = new (std::nothrow) PrefillBatch;
+    if (!p) {
+        release(&b->b);
+        delete b;
+        set_error(XP_E_NOMEM, "prefill: out of host memory");
+        return nullptr;
+    }
+    p->b = b;
+    return p;
+}
+
+int prefill_batch_run(PrefillBatch* p, const uint32_t* ids, uint32_t n, uint32_t pos0) {
+    Batch& b = p->b->b;
+    uint32_t pos[kBatchMax], tok[kBatchMax];
+    for (uint32_t c0 = 0; c0 < n; c0 += kBatchMax) {
+        const uint32_t m = std::min(kBatchMax, n - c0);
+        // rows past the prompt repeat its last token at its position: they
+        // write the same K/V row with the same values
+        for (uint32_t r = 0; r < kBatchMax; ++r) {
+            const uint32_t i = c0 + std::min(r, m - 1);
+            pos[r] = pos0 + i;
+            tok[r] = ids[i];
+        }
+        XP_HIP(hipMemcpyAsync(b.d_pos, pos, sizeof pos, hipMemcpyHostToDevice, b.st));
+        b.pos.assign(pos, pos + kBatchMax);
+        int rc = b.forward(tok);
+        if (rc != XP_OK) return rc;
+    }
+    return XP_OK;
+}
+
+void prefill_batch_destroy(PrefillBatch* p) {
+    if (!p) return;
+    if (p->b) {
+        release(&p->b->b);
+        delete p->b;
+    }
+    delete p;
+}
+
+}  // namespace xp
+
+extern "C" {
+
+int xp_batch_create(const xp_session* weights, uint32_t n_seq, uint32_t max_seq, xp_batch** out) {
+    return make_batch(weights, n_seq, max_seq, false, out);
 }
 
 int xp_batch_destroy(xp_batch* h) {

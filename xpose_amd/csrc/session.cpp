@@ -151,6 +151,8 @@ struct Session {
     void* lm_s = nullptr;
     float* final_norm = nullptr;
     float* embed = nullptr;      // optional fp32 [vocab][hidden] embedding rows
+    PrefillBatch* pre = nullptr; // batched prefill (created on first use)
+    bool pre_unavailable = false;
     float *x, *xb, *xb2, *q_raw, *k_raw, *v, *q, *k, *att, *gate, *up, *hb, *logits;
     float* mv_partial = nullptr;
     size_t mv_partial_cap = 0;
@@ -392,6 +394,8 @@ int session_weights(const xp_session* h, SessionWeights* out) {
             out->layer[l].s[m] = s.L[l].s[m];
         }
         for (int n = 0; n < kNNorm; ++n) out->layer[l].norm[n] = s.L[l].norm[n];
+        out->layer[l].kc = s.L[l].kc;
+        out->layer[l].vc = s.L[l].vc;
         out->layer[l].global = s.is_global(l);
     }
     out->lm_w = s.lm_w;
@@ -407,6 +411,7 @@ namespace {
 int destroy(xp_session* h) {
     if (!h) return XP_OK;
     Session& s = h->s;
+    if (s.pre) prefill_batch_destroy(s.pre);
     for (auto& g : s.graph)
         if (g) (void)hipGraphExecDestroy(g);
     for (auto& e : s.ev)
@@ -880,7 +885,25 @@ int xp_session_prefill(xp_session* h, const uint32_t* ids, uint32_t n) {
     XP_HIP(hipStreamSynchronize(s.st));
     std::memcpy(s.h_ids, ids, size_t(n) * 4);
     const int last = s.cfg.sample_mode == 0 ? 1 : 2;
-    for (uint32_t i = 0; i < n; ++i) {
+    uint32_t first = 0;
+    if (n >= 3 && s.cfg.prefill_mode == XP_PREFILL_AUTO && !s.pre_unavailable) {
+        if (!s.pre && !(s.pre = prefill_batch_create(h))) {
+            s.pre_unavailable = true;   // the shape does not fit: token by token
+            clear_error();
+        }
+        if (s.pre) {
+            // positions pos .. pos + n - 2 through the batched step, then the
+            // last token on the session's own path
+            int rc = prefill_batch_run(s.pre, ids, n - 1, s.pos);
+            if (rc != XP_OK) return rc;
+            first = n - 1;
+            s.h_stat[3] = s.pos + first;
+            XP_HIP(hipMemcpyAsync(s.state, s.h_stat + 3, 4, hipMemcpyHostToDevice, s.st));
+            XP_HIP(hipMemcpyAsync(s.hist + s.pos, s.h_ids, size_t(first) * 4,
+                                  hipMemcpyHostToDevice, s.st));
+        }
+    }
+    for (uint32_t i = first; i < n; ++i) {
         XP_HIP(hipMemcpyAsync(s.state + 1, s.h_ids + i, 4, hipMemcpyHostToDevice, s.st));
         int rc = s.run(i + 1 == n ? last : 0);
         if (rc != XP_OK) return rc;

@@ -135,6 +135,8 @@ struct SessionWeights {
         const void* w[7];       // Q K V O GATE UP DOWN
         const void* s[7];
         const float* norm[6];   // attn, post_attn, ffn, post_ffw, q_norm, k_norm
+        uint16_t* kc;           // the session's KV cache of the layer
+        uint16_t* vc;
         bool global;
     } layer[kMaxSessionLayers];
     const void* lm_w;
@@ -143,6 +145,14 @@ struct SessionWeights {
     const float* embed;         // optional fp32 [vocab][hidden] embedding rows
 };
 int session_weights(const xp_session* h, SessionWeights* out);
+// Batched prefill of a session (batch.cpp): tokens ids[0..n) at positions
+// pos0 .. pos0 + n - 1 through the batched step, 16 positions per pass, rows
+// sharing the session's KV cache; writes the KV rows, no logits. create
+// returns nullptr (error set) when the shape does not fit the batched step.
+struct PrefillBatch;
+PrefillBatch* prefill_batch_create(const xp_session* s);
+int prefill_batch_run(PrefillBatch* p, const uint32_t* ids, uint32_t n, uint32_t pos0);
+void prefill_batch_destroy(PrefillBatch* p);
 // The session's host draw and Philox uniform (decode.cpp:1873-1917).
 uint32_t draw(float* val, uint32_t* idx, uint32_t n, float temperature, uint32_t top_k,
               float top_p, double u);
