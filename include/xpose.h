@@ -501,6 +501,38 @@ int xp_gguf_verify_cache(xp_gguf* g, const xp_config* c, const char* cache_path,
 int xp_session_load_gguf(xp_session* s, xp_gguf* g, const char* cache_path, uint32_t flags,
                          uint32_t threads, xp_load_stats* st);
 
+/* ---- tokenizer ------------------------------------------------------------
+ * SentencePiece from the GGUF vocabulary (Tokenizer, model/tokenizer.hpp:46-94,
+ * tokenizer.cpp:70-374): control / unknown tokens cut out first (longest
+ * spelling), fragments normalised (space -> U+2581, one leading U+2581 when
+ * add_space_prefix), best-score adjacent merges (leftmost on a tie), byte
+ * fallback to "<0xAB>" tokens. The handle borrows the xp_gguf's strings:
+ * destroy it before closing the file. */
+typedef struct xp_tokenizer xp_tokenizer;
+typedef struct {
+    uint32_t vocab;
+    int32_t  bos, eos, unk, pad;        /* -1 when the file names none */
+    int32_t  add_bos, add_eos, add_space_prefix;
+} xp_tokenizer_ids;
+int xp_tokenizer_create(xp_gguf* g, xp_tokenizer** out);
+int xp_tokenizer_destroy(xp_tokenizer* t);
+int xp_tokenizer_info(xp_tokenizer* t, xp_tokenizer_ids* info);
+/* encode: *n = number of ids; ids may be NULL to size the output first. */
+int xp_tokenize(xp_tokenizer* t, const char* text, size_t len, int add_bos, int add_eos,
+                int32_t* ids, size_t cap, size_t* n);
+/* decode (skip_special drops control / unknown tokens); *len = bytes, the
+ * output is NUL-terminated within cap. */
+int xp_detokenize(xp_tokenizer* t, const int32_t* ids, size_t n, int skip_special, char* out,
+                  size_t cap, size_t* len);
+/* One token's text: piece = as decoded (byte resolved, U+2581 -> ' '),
+ * text = the raw vocabulary spelling. */
+int xp_token_piece(xp_tokenizer* t, int32_t id, char* out, size_t cap, size_t* len);
+int xp_token_text(xp_tokenizer* t, int32_t id, char* out, size_t cap, size_t* len);
+/* The id of an exact spelling (the lowest id on duplicates), -1 if none. */
+int xp_token_find(xp_tokenizer* t, const char* spelling, size_t len, int32_t* id);
+/* token_type (0 when out of range) and score. */
+int xp_token_kind(xp_tokenizer* t, int32_t id, int32_t* kind, float* score);
+
 #ifdef __cplusplus
 }
 #endif

@@ -95,6 +95,60 @@ private:
     xp_gguf* g_ = nullptr;
 };
 
+// The model's SentencePiece tokenizer (Tokenizer, model/tokenizer.hpp:46-94).
+// Borrows the Model's strings: destroy it before the Model.
+class Tokenizer {
+public:
+    explicit Tokenizer(const Model& m) {
+        check(xp_tokenizer_create(m.handle(), &t_), "xp_tokenizer_create");
+        check(xp_tokenizer_info(t_, &ids_), "xp_tokenizer_info");
+    }
+    ~Tokenizer() {
+        if (t_) xp_tokenizer_destroy(t_);
+    }
+    Tokenizer(const Tokenizer&) = delete;
+    Tokenizer& operator=(const Tokenizer&) = delete;
+
+    std::vector<uint32_t> encode(const std::string& text, bool add_bos, bool add_eos = false) const {
+        size_t n = 0;
+        check(xp_tokenize(t_, text.data(), text.size(), add_bos, add_eos, nullptr, 0, &n), "xp_tokenize");
+        std::vector<int32_t> ids(n);
+        check(xp_tokenize(t_, text.data(), text.size(), add_bos, add_eos, ids.data(), n, &n),
+              "xp_tokenize");
+        return std::vector<uint32_t>(ids.begin(), ids.end());
+    }
+    std::string decode(const std::vector<int32_t>& ids, bool skip_special = true) const {
+        size_t n = 0;
+        check(xp_detokenize(t_, ids.data(), ids.size(), skip_special, nullptr, 0, &n), "xp_detokenize");
+        std::string s(n + 1, '\0');
+        check(xp_detokenize(t_, ids.data(), ids.size(), skip_special, &s[0], s.size(), &n),
+              "xp_detokenize");
+        s.resize(n);
+        return s;
+    }
+    std::string decode_one(int32_t id) const {
+        size_t n = 0;
+        check(xp_token_piece(t_, id, nullptr, 0, &n), "xp_token_piece");
+        std::string s(n + 1, '\0');
+        check(xp_token_piece(t_, id, &s[0], s.size(), &n), "xp_token_piece");
+        s.resize(n);
+        return s;
+    }
+    int32_t id_for(const std::string& spelling) const {
+        int32_t id = -1;
+        check(xp_token_find(t_, spelling.data(), spelling.size(), &id), "xp_token_find");
+        return id;
+    }
+    int32_t bos_id() const { return ids_.bos; }
+    int32_t eos_id() const { return ids_.eos; }
+    int32_t unk_id() const { return ids_.unk; }
+    size_t vocab_size() const { return ids_.vocab; }
+
+private:
+    xp_tokenizer* t_ = nullptr;
+    xp_tokenizer_ids ids_{};
+};
+
 class DecodeSession {
 public:
     explicit DecodeSession(const Config& cfg) : cfg_(cfg) {

@@ -206,8 +206,28 @@ def encode_q8_0(x: np.ndarray) -> bytes:
     return out.tobytes()
 
 
+def chat_vocab(vocab: int):
+    """A Gemma-like vocabulary of `vocab` entries: <pad> <eos> <bos> <unk>
+    <start_of_turn> <end_of_turn>, 256 byte tokens, letters, then fillers.
+    Returns (tokens, types); bos = 2, eos = 1, unk = 3."""
+    toks = ["<pad>", "<eos>", "<bos>", "<unk>", "<start_of_turn>", "<end_of_turn>"]
+    types = [3, 3, 3, 2, 3, 3]
+    toks += [f"<0x{i:02X}>" for i in range(256)]
+    types += [6] * 256
+    for c in "abcdefghijklmnopqrstuvwxyz":
+        toks += [c, "▁" + c]
+        types += [1, 1]
+    toks += ["▁", "\n"]
+    types += [1, 1]
+    while len(toks) < vocab:
+        toks.append(f"w{len(toks)}")
+        types.append(1)
+    return toks[:vocab], types[:vocab]
+
+
 def gemma_model(path: str, n_layers: int, hidden: int, ffn: int, n_heads: int, vocab: int,
-                seed: int = 7, head_dim: int = 256, mat_type: str = "q8_0") -> dict:
+                seed: int = 7, head_dim: int = 256, mat_type: str = "q8_0",
+                chat: bool = False) -> dict:
     """A small Gemma-3-architecture GGUF: Q8_0 (or F32) matrices ~ N(0, 0.05),
     norms 1 + N(0, 0.1) (the file stores 1 + w), token_embd tied. Returns the
     fp32 values the file holds as {name: array [rows][row_len]}."""
@@ -221,6 +241,13 @@ def gemma_model(path: str, n_layers: int, hidden: int, ffn: int, n_heads: int, v
             ("gemma3.attention.sliding_window", U32, 512), ("gemma3.rope.freq_base", F32, 1e6),
             ("gemma3.attention.layer_norm_rms_epsilon", F32, 1e-6),
             ("tokenizer.ggml.tokens", ARR, (STR, [f"t{i}" for i in range(vocab)]))]
+    if chat:
+        toks, types = chat_vocab(vocab)
+        meta[-1] = ("tokenizer.ggml.tokens", ARR, (STR, toks))
+        meta += [("tokenizer.ggml.token_type", ARR, (I32, types)),
+                 ("tokenizer.ggml.scores", ARR, (F32, [0.0] * vocab)),
+                 ("tokenizer.ggml.bos_token_id", U32, 2), ("tokenizer.ggml.eos_token_id", U32, 1),
+                 ("tokenizer.ggml.unknown_token_id", U32, 3)]
     tensors, values = [], {}
 
     def mat(name, rows_in, cols_out):

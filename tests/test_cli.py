@@ -115,3 +115,39 @@ def test_gpu_cli_gguf_matches_python_session(xp, tmp_path):
     assert [sess.decode_step() for _ in range(n)] == ids
     sess.close()
     g.close()
+
+
+@pytest.mark.gpu
+def test_gpu_cli_text_chat(xp, tmp_path):
+    """--text / --chat: the prompt goes through the model's tokenizer (BOS,
+    the turn template), and the ids the CLI generates equal the Python
+    session's on the same encoded prompt."""
+    import gguf_util as G
+    X = xp
+    print("case cli text", flush=True)
+    model = str(tmp_path / "m.gguf")
+    G.gemma_model(model, n_layers=2, hidden=256, ffn=512, n_heads=1, vocab=1024, seed=41, chat=True)
+    r = run("--model", model, "--no-cache", "--text", "hello world", "--chat", "--tokens", 6,
+            "--ids")
+    assert r.returncode == 0, r.stderr
+    assert "<start_of_turn>user\nhello world<end_of_turn>" in r.stdout
+    ids = cli_ids(r.stdout)
+    g = X.Gguf(model)
+    tok = X.Tokenizer(g)
+    prompt = tok.encode("<start_of_turn>user\nhello world<end_of_turn>\n<start_of_turn>model\n",
+                        add_bos=True)
+    assert prompt[0] == 2 and prompt[1] == 4          # <bos> <start_of_turn>
+    cfg = g.config(X.XpConfig.gemma3_1b(scale_fmt=X.XP_SCALE_BF16_QUAD))
+    sess = X.DecodeSession(cfg)
+    sess.load_gguf(g)
+    sess.prefill(np.array(prompt, np.uint32))
+    got = []
+    for _ in range(6):
+        t = sess.decode_step()
+        if t in (1, 5):                               # <eos>, <end_of_turn>
+            break
+        got.append(t)
+    assert got == ids
+    tok.close()
+    sess.close()
+    g.close()

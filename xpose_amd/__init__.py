@@ -76,6 +76,11 @@ class LoadStats(C.Structure):
         ("threads", C.c_uint32), ("n_tensors", C.c_uint32)]
 
 
+class TokenizerIds(C.Structure):
+    _fields_ = [("vocab", C.c_uint32)] + [(n, C.c_int32) for n in (
+        "bos", "eos", "unk", "pad", "add_bos", "add_eos", "add_space_prefix")]
+
+
 # enum xp_ggml_type / xp_load_flags
 GGML_F32, GGML_F16, GGML_Q4_0, GGML_Q4_1, GGML_Q5_0, GGML_Q5_1, GGML_Q8_0 = 0, 1, 2, 3, 6, 7, 8
 GGML_Q4_K, GGML_Q6_K, GGML_BF16 = 12, 14, 30
@@ -167,6 +172,15 @@ def _declare(lib: C.CDLL) -> None:
         "xp_gguf_pack_model": (i32, [vp, P(XpConfig), C.c_char_p, u32, P(LoadStats)]),
         "xp_gguf_verify_cache": (i32, [vp, P(XpConfig), C.c_char_p, u32, P(u32)]),
         "xp_session_load_gguf": (i32, [vp, vp, C.c_char_p, u32, u32, P(LoadStats)]),
+        "xp_tokenizer_create": (i32, [vp, P(vp)]),
+        "xp_tokenizer_destroy": (i32, [vp]),
+        "xp_tokenizer_info": (i32, [vp, P(TokenizerIds)]),
+        "xp_tokenize": (i32, [vp, C.c_char_p, sz, i32, i32, vp, sz, P(sz)]),
+        "xp_detokenize": (i32, [vp, vp, sz, i32, C.c_char_p, sz, P(sz)]),
+        "xp_token_piece": (i32, [vp, i32, C.c_char_p, sz, P(sz)]),
+        "xp_token_text": (i32, [vp, i32, C.c_char_p, sz, P(sz)]),
+        "xp_token_find": (i32, [vp, C.c_char_p, sz, P(i32)]),
+        "xp_token_kind": (i32, [vp, i32, P(i32), P(f32)]),
         "xp_synth_tensor": (i32, [P(XpConfig), u32, i32, i32, vp, sz]),
         "xp_session_synthesize": (i32, [vp, u32]),
         "xp_session_kv_upload": (i32, [vp, i32, i32, u32, u32, vp]),
@@ -698,4 +712,64 @@ def pack_int4(w_cols: np.ndarray, scale_fmt: int = XP_SCALE_BF16_QUAD, threads: 
     call("xp_pack_int4", w_cols.ctypes.data, rows, cols, scale_fmt, threads, wq.ctypes.data,
          sc.ctypes.data)
     return wq, sc
+
+
+class Tokenizer:
+    """The SentencePiece tokenizer of a GGUF file (xp_tokenizer_*). Keep the
+    Gguf open while the tokenizer is in use."""
+
+    def __init__(self, g: Gguf):
+        h = C.c_void_p()
+        call("xp_tokenizer_create", g.h, C.byref(h))
+        self.h = h
+        self.g = g
+        i = TokenizerIds()
+        call("xp_tokenizer_info", h, C.byref(i))
+        self.ids = i
+
+    def close(self) -> None:
+        if self.h and self.h.value and _lib is not None:
+            _lib.xp_tokenizer_destroy(self.h)
+        self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def encode(self, text: str | bytes, add_bos: bool = False, add_eos: bool = False) -> list[int]:
+        raw = text.encode() if isinstance(text, str) else bytes(text)
+        n = C.c_size_t()
+        call("xp_tokenize", self.h, raw, len(raw), int(add_bos), int(add_eos), None, 0, C.byref(n))
+        out = (C.c_int32 * max(1, n.value))()
+        call("xp_tokenize", self.h, raw, len(raw), int(add_bos), int(add_eos), out, n.value,
+             C.byref(n))
+        return list(out[:n.value])
+
+    def decode(self, ids, skip_special: bool = True) -> bytes:
+        a = (C.c_int32 * max(1, len(ids)))(*ids)
+        n = C.c_size_t()
+        call("xp_detokenize", self.h, a, len(ids), int(skip_special), None, 0, C.byref(n))
+        buf = C.create_string_buffer(n.value + 1)
+        call("xp_detokenize", self.h, a, len(ids), int(skip_special), buf, n.value + 1, C.byref(n))
+        return buf.raw[:n.value]
+
+    def piece(self, token: int) -> bytes:
+        n = C.c_size_t()
+        call("xp_token_piece", self.h, token, None, 0, C.byref(n))
+        buf = C.create_string_buffer(n.value + 1)
+        call("xp_token_piece", self.h, token, buf, n.value + 1, C.byref(n))
+        return buf.raw[:n.value]
+
+    def find(self, spelling: str | bytes) -> int:
+        raw = spelling.encode() if isinstance(spelling, str) else bytes(spelling)
+        i = C.c_int32()
+        call("xp_token_find", self.h, raw, len(raw), C.byref(i))
+        return i.value
+
+    def kind(self, token: int) -> int:
+        k, s = C.c_int32(), C.c_float()
+        call("xp_token_kind", self.h, token, C.byref(k), C.byref(s))
+        return k.value
 

@@ -7,10 +7,14 @@
 //
 //   xpose_decode [--layers N] [--prompt N] [--tokens N] [--ctx P] [--seed S]
 //                [--exec token|graph|launch] [--curve] [--ids]
-//                [--model FILE [--cache PATH | --no-cache] [--repack] [--verify-cache]]
+//                [--model FILE [--cache PATH | --no-cache] [--repack] [--verify-cache]
+//                 [--text TEXT [--chat]]]
 //
 // --cache defaults to FILE.xpack. --verify-cache repacks every matrix and
-// compares the cache byte for byte, then exits (no GPU).
+// compares the cache byte for byte, then exits (no GPU). --text encodes TEXT
+// with the model's tokenizer (BOS first), streams the generated text and
+// stops at <eos> / <end_of_turn>; --chat wraps it in Gemma's turn template
+// (decode.cpp:2832-2834, 2919-2946).
 // --ctx P pre-fills every layer's KV cache with fp16 N(0,1) rows 0..P-1 and
 // decodes from position P (benchmark config 4); otherwise a --prompt of
 // uniform-random ids is prefilled first (config 3). --curve reports tok/s per
@@ -41,7 +45,7 @@ int usage() {
                  "usage: xpose_decode [--layers N] [--prompt N] [--tokens N] [--ctx P] "
                  "[--seed S] [--exec token|graph|launch] [--curve] [--ids]\n"
                  "                    [--model FILE [--cache PATH | --no-cache] [--repack] "
-                 "[--verify-cache]]\n");
+                 "[--verify-cache] [--text TEXT [--chat]]]\n");
     return 2;
 }
 
@@ -51,7 +55,8 @@ int main(int argc, char** argv) {
     uint32_t layers = 26, prompt = 32, tokens = 128, ctx = 0, seed = 0x5EED0003u;
     int exec = XP_EXEC_AUTO;
     bool curve = false, print_ids = false, no_cache = false, repack = false, verify = false;
-    std::string model, cache;
+    bool chat = false;
+    std::string model, cache, text;
     for (int i = 1; i < argc; ++i) {
         const std::string a = argv[i];
         auto next = [&]() -> const char* { return i + 1 < argc ? argv[++i] : nullptr; };
@@ -73,9 +78,13 @@ int main(int argc, char** argv) {
         else if (a == "--no-cache") no_cache = true;
         else if (a == "--repack") repack = true;
         else if (a == "--verify-cache") verify = true;
+        else if (a == "--text" && (v = next())) text = v;
+        else if (a == "--chat") chat = true;
         else return usage();
     }
-    if ((verify || repack || no_cache || !cache.empty()) && model.empty()) return usage();
+    if ((verify || repack || no_cache || !cache.empty() || !text.empty() || chat) && model.empty())
+        return usage();
+    if (chat && text.empty()) return usage();
     if (!model.empty() && cache.empty() && !no_cache) cache = model + ".xpack";
     try {
         xpose::llm::Config cfg;
@@ -119,8 +128,18 @@ int main(int argc, char** argv) {
         std::printf("kv cache    %.1f MiB (%u positions)\n",
                     double(sess.kv_bytes()) / (1024.0 * 1024.0), cfg.max_seq);
 
+        std::unique_ptr<xpose::llm::Tokenizer> tok;
+        int32_t stop1 = -1, stop2 = -1;
+        if (!text.empty()) {
+            tok.reset(new xpose::llm::Tokenizer(*gguf));
+            if (chat) text = "<start_of_turn>user\n" + text + "<end_of_turn>\n<start_of_turn>model\n";
+            stop1 = tok->eos_id();
+            stop2 = tok->id_for("<end_of_turn>");
+        }
         std::vector<uint32_t> ids;
-        if (ctx > 0) {
+        if (tok) {
+            ids = tok->encode(text, true);
+        } else if (ctx > 0) {
             const uint32_t row = cfg.n_kv_heads * cfg.head_dim;
             std::vector<uint16_t> rows(size_t(ctx) * row);
             for (uint32_t l = 0; l < cfg.n_layers; ++l)
@@ -156,15 +175,35 @@ int main(int argc, char** argv) {
         std::vector<double> step_ms;
         std::vector<uint32_t> pos_of, out;
         double total = 0;
+        if (tok) {
+            std::printf("%s", text.c_str());
+            std::fflush(stdout);
+        }
         for (uint32_t i = 0; i < tokens; ++i) {
             out.push_back(sess.decode_step());
+            if (tok) {
+                // Gemma ends a turn with <end_of_turn>, not <eos> (decode.cpp:2927-2929)
+                const int32_t t = int32_t(out.back());
+                if (!curve && (t == stop1 || t == stop2)) {
+                    out.pop_back();
+                    break;
+                }
+                std::printf("%s", tok->decode_one(t).c_str());
+                std::fflush(stdout);
+            }
             const auto m = sess.last_metrics();
             step_ms.push_back(m.gpu_ms);
             pos_of.push_back(m.position);
             total += m.ms;
         }
-        std::printf("decode      %u tokens, %.4f ms/token, %.1f tok/s (host wall per step)\n",
-                    tokens, total / tokens, tokens * 1000.0 / total);
+        if (tok) std::printf("\n\n");
+        const size_t done = step_ms.size();
+        if (done == 0) {
+            std::printf("decode      0 tokens\n");
+            return 0;
+        }
+        std::printf("decode      %zu tokens, %.4f ms/token, %.1f tok/s (host wall per step)\n",
+                    done, total / double(done), double(done) * 1000.0 / total);
         std::vector<double> s = step_ms;
         std::sort(s.begin(), s.end());
         double sum = 0;
