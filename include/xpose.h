@@ -476,7 +476,9 @@ int xp_dequantize(uint32_t type, const void* src, float* out, uint64_t n);
 int xp_gguf_dequantize_rows(xp_gguf* g, const char* name, uint64_t row0, uint64_t nrows,
                             float* out);
 /* Shapes from the file onto c (DecodeConfig::from_model, decode.cpp:258-275);
- * c's policy fields (max_seq, sampling, global_every, scale_fmt, ...) stay. */
+ * c's policy fields (max_seq, sampling, global_every, scale_fmt, ...) stay,
+ * and so does a sliding_window other than the default 512 (the merge of
+ * decode.cpp:1422-1434); otherwise the file's window extent is taken. */
 int xp_config_from_gguf(xp_gguf* g, xp_config* c);
 /* Requantises w[cols][rows] (GGUF row order: row j of length `rows` is
  * output column j) to the KM4 plane wq (rows * cols / 2 bytes) and the scale

@@ -157,12 +157,13 @@ public:
     }
     // The reference's DecodeSession(Paths, DecodeConfig): shapes from the
     // file, policy fields from `cfg`, weights requantised on load or read
-    // from the pack cache at `cache` ("" = no cache).
+    // from the pack cache at `cache` ("" = no cache), packed on `threads`
+    // host threads (0 = all, Paths::pack_threads).
     DecodeSession(const Model& m, const Config& cfg, const std::string& cache = std::string(),
-                  uint32_t flags = 0)
+                  uint32_t flags = 0, uint32_t threads = 0)
         : DecodeSession(m.config(cfg)) {
         check(xp_session_load_gguf(s_, m.handle(), cache.empty() ? nullptr : cache.c_str(), flags,
-                                   0, &load_),
+                                   threads, &load_),
               "xp_session_load_gguf");
     }
     // Where the load time went (LoadStats, decode.hpp:584-603).

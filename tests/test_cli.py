@@ -22,6 +22,12 @@ def test_cli_usage_errors_exit_2():
     assert r.returncode == 2 and "usage" in r.stderr
     r = run("--no-such-flag")
     assert r.returncode == 2
+    r = run("--prompt", "hello")                  # a text prompt needs --model
+    assert r.returncode == 2 and "usage" in r.stderr
+    r = run("--model", "m.gguf", "--chat")        # --chat needs a prompt
+    assert r.returncode == 2
+    r = run("--model", "m.gguf", "--prompt-file", "/nonexistent/prompt.txt")
+    assert r.returncode == 2 and "cannot open" in r.stderr
 
 
 def test_cli_verify_cache(xh, tmp_path):
@@ -35,8 +41,10 @@ def test_cli_verify_cache(xh, tmp_path):
     cfg = g.config(X.XpConfig.gemma3_1b(scale_fmt=X.XP_SCALE_BF16_QUAD))
     g.pack_model(cfg, model + ".xpack")
     g.close()
-    r = run("--model", model, "--layers", 1, "--verify-cache")
+    r = run("--model", model, "--layers", 1, "--verify-cache", "--pack-threads", 2)
     assert r.returncode == 0 and "PASS" in r.stdout, r.stdout + r.stderr
+    r = run("--model", model, "--pack-cache", model + ".other", "--verify-cache")
+    assert r.returncode == 1 and "no valid cache" in r.stderr
     data = bytearray(open(model + ".xpack", "rb").read())
     data[1000] ^= 1
     open(model + ".xpack", "wb").write(bytes(data))
@@ -61,7 +69,7 @@ def test_gpu_cli_matches_python_session(xp):
     seed, layers, prompt_len, n = 0x5EED0003, 3, 8, 12
     outs = {}
     for mode in ("token", "graph"):
-        r = run("--layers", layers, "--prompt", prompt_len, "--tokens", n, "--seed", seed,
+        r = run("--layers", layers, "--prompt-len", prompt_len, "-n", n, "--weights-seed", seed,
                 "--exec", mode, "--ids")
         assert r.returncode == 0, r.stderr
         outs[mode] = cli_ids(r.stdout)
@@ -93,11 +101,12 @@ def test_gpu_cli_gguf_matches_python_session(xp, tmp_path):
     model = str(tmp_path / "m.gguf")
     G.gemma_model(model, n_layers=2, hidden=256, ffn=512, n_heads=1, vocab=1024, seed=31)
     seed, prompt_len, n = 0x5EED0003, 4, 6
-    r = run("--model", model, "--prompt", prompt_len, "--tokens", n, "--seed", seed, "--ids")
+    r = run("--model", model, "--prompt-len", prompt_len, "-n", n, "--weights-seed", seed, "--ids")
     assert r.returncode == 0, r.stderr
     assert "cache written" in r.stdout, r.stdout
     ids = cli_ids(r.stdout)
-    r2 = run("--model", model, "--prompt", prompt_len, "--tokens", n, "--seed", seed, "--ids")
+    r2 = run("--model", model, "--prompt-len", prompt_len, "-n", n, "--weights-seed", seed,
+             "--ids")
     assert r2.returncode == 0 and "from the pack cache" in r2.stdout, r2.stdout + r2.stderr
     assert cli_ids(r2.stdout) == ids
     prompt = []
@@ -127,8 +136,9 @@ def test_gpu_cli_text_chat(xp, tmp_path):
     print("case cli text", flush=True)
     model = str(tmp_path / "m.gguf")
     G.gemma_model(model, n_layers=2, hidden=256, ffn=512, n_heads=1, vocab=1024, seed=41, chat=True)
-    r = run("--model", model, "--no-cache", "--text", "hello world", "--chat", "--tokens", 6,
-            "--ids")
+    pf = tmp_path / "prompt.txt"
+    pf.write_bytes(b"hello world")
+    r = run("--model", model, "--no-pack-cache", "--prompt-file", pf, "--chat", "-n", 6, "--ids")
     assert r.returncode == 0, r.stderr
     assert "<start_of_turn>user\nhello world<end_of_turn>" in r.stdout
     ids = cli_ids(r.stdout)

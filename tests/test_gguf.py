@@ -416,3 +416,18 @@ def test_gpu_load_gguf_gemma_shapes(xp, xo, tmp_path):
     print("case gguf gemma shapes", flush=True)
     check_load(xp, xo, tmp_path, dict(n_layers=2, hidden=1152, ffn=6912, n_heads=4, vocab=16384),
                steps=2, seed=22)
+
+
+def test_config_window_merge(xh, tmp_path):
+    """The file's sliding_window replaces the default 512; a window the caller
+    set to anything else survives (decode.cpp:1427-1434)."""
+    X = xh
+    path = str(tmp_path / "w.gguf")
+    G.write_gguf(path, [("general.architecture", G.STR, "gemma3"),
+                        ("gemma3.block_count", G.U32, 3),
+                        ("gemma3.attention.sliding_window", G.U32, 1024)], [])
+    g = X.Gguf(path)
+    assert g.config(X.XpConfig.gemma3_1b()).sliding_window == 1024
+    c = g.config(X.XpConfig.gemma3_1b(sliding_window=128, global_every=4))
+    assert (c.sliding_window, c.global_every, c.n_layers) == (128, 4, 3)
+    g.close()

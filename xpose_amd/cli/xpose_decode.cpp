@@ -1,26 +1,30 @@
 // xpose_decode — command-line decode driver over include/xpose.hpp, the
 // counterpart of the reference's decode CLI (examples/llm/decode.cpp:
-// 2720-3006): the seeded synthetic Gemma-3-1B model (random int4 weights with
-// fp16 group scales), or a GGUF model with --model (requantised to int4 with
-// bf16 scales, through the pack cache). There is no tokenizer on this path:
-// prompts are token ids.
+// 2720-3006), with the reference's flag spellings where the two overlap:
 //
-//   xpose_decode [--layers N] [--prompt N] [--tokens N] [--ctx P] [--seed S]
-//                [--exec token|graph|launch] [--curve] [--ids]
-//                [--model FILE [--cache PATH | --no-cache] [--repack] [--verify-cache]
-//                 [--text TEXT [--chat]]]
+//   xpose_decode --model FILE [--prompt TEXT | --prompt-file F] [--chat] [-n N]
+//                [--pack-cache F | --no-pack-cache] [--repack] [--pack-threads N]
+//                [--verify-cache]
+//   xpose_decode [--layers N] [--prompt-len N | --ctx P] [-n N] [--weights-seed S]
+//   common:      [--max-seq N] [--window N] [--global-every N] [--temp T]
+//                [--top-k K] [--top-p P] [--seed S] [--exec token|graph|launch]
+//                [--curve] [--ids]
 //
-// --cache defaults to FILE.xpack. --verify-cache repacks every matrix and
-// compares the cache byte for byte, then exits (no GPU). --text encodes TEXT
-// with the model's tokenizer (BOS first), streams the generated text and
-// stops at <eos> / <end_of_turn>; --chat wraps it in Gemma's turn template
-// (decode.cpp:2832-2834, 2919-2946).
-// --ctx P pre-fills every layer's KV cache with fp16 N(0,1) rows 0..P-1 and
-// decodes from position P (benchmark config 4); otherwise a --prompt of
-// uniform-random ids is prefilled first (config 3). --curve reports tok/s per
-// 512-position bucket and the deepest/shallowest ratio, the reference's
-// flatness metric (decode.cpp:2977-2999). Prints per-step gpu ms min / median
-// / mean like the reference (decode.cpp:2961-2972).
+// With --model the GGUF file is requantised to int4 with bf16 scales through
+// the pack cache (default FILE.xpack); --verify-cache repacks every matrix,
+// compares the cache byte for byte and exits (no GPU). The prompt text is
+// encoded with the model's tokenizer (BOS first), --chat wraps it in Gemma's
+// turn template (decode.cpp:2888-2890), the generated text is streamed and
+// generation stops at <eos> or <end_of_turn> unless --curve
+// (decode.cpp:2919-2946). Without a prompt, or without --model, the prompt is
+// --prompt-len uniform-random ids (benchmark config 3; the seeded synthetic
+// model when there is no --model). --ctx P instead pre-fills every layer's KV
+// cache with fp16 N(0,1) rows 0..P-1 and decodes from position P (config 4).
+// --temp / --top-k / --top-p switch to temperature sampling, --seed sets its
+// Philox key (decode.cpp:2800-2806). --curve reports tok/s per 512-position
+// bucket and the deepest/shallowest ratio, the reference's flatness metric
+// (decode.cpp:2977-2999). Prints per-step gpu ms min / median / mean like the
+// reference (decode.cpp:2961-2972).
 #include <algorithm>
 #include <chrono>
 #include <cstdio>
@@ -42,30 +46,56 @@ double now_ms() {
 
 int usage() {
     std::fprintf(stderr,
-                 "usage: xpose_decode [--layers N] [--prompt N] [--tokens N] [--ctx P] "
-                 "[--seed S] [--exec token|graph|launch] [--curve] [--ids]\n"
-                 "                    [--model FILE [--cache PATH | --no-cache] [--repack] "
-                 "[--verify-cache] [--text TEXT [--chat]]]\n");
+                 "usage: xpose_decode --model FILE [--prompt TEXT | --prompt-file F] [--chat] "
+                 "[-n N]\n"
+                 "                    [--pack-cache F | --no-pack-cache] [--repack] "
+                 "[--pack-threads N] [--verify-cache]\n"
+                 "       xpose_decode [--layers N] [--prompt-len N | --ctx P] [-n N] "
+                 "[--weights-seed S]\n"
+                 "       common: [--max-seq N] [--window N] [--global-every N] [--temp T] "
+                 "[--top-k K] [--top-p P]\n"
+                 "               [--seed S] [--exec token|graph|launch] [--curve] [--ids]\n");
     return 2;
+}
+
+bool read_file(const char* path, std::string& out) {
+    std::FILE* fp = std::fopen(path, "rb");
+    if (!fp) return false;
+    char buf[4096];
+    size_t got;
+    while ((got = std::fread(buf, 1, sizeof buf, fp)) > 0) out.append(buf, got);
+    std::fclose(fp);
+    return true;
 }
 
 }  // namespace
 
 int main(int argc, char** argv) {
-    uint32_t layers = 26, prompt = 32, tokens = 128, ctx = 0, seed = 0x5EED0003u;
+    uint32_t layers = 26, prompt_len = 32, tokens = 128, ctx = 0, seed = 0x5EED0003u;
+    uint32_t pack_threads = 0;
     int exec = XP_EXEC_AUTO;
     bool curve = false, print_ids = false, no_cache = false, repack = false, verify = false;
-    bool chat = false;
+    bool chat = false, have_text = false;
     std::string model, cache, text;
+    // Policy fields applied over the model's shapes, as the reference's
+    // DecodeConfig fields are: {name, value} pairs kept in flag order.
+    std::vector<std::pair<std::string, double>> policy;
     for (int i = 1; i < argc; ++i) {
         const std::string a = argv[i];
         auto next = [&]() -> const char* { return i + 1 < argc ? argv[++i] : nullptr; };
+        auto num = [&](uint32_t& dst) {
+            const char* v = next();
+            if (!v) return false;
+            dst = uint32_t(std::strtoul(v, nullptr, 0));
+            return true;
+        };
         const char* v = nullptr;
-        if (a == "--layers" && (v = next())) layers = uint32_t(std::strtoul(v, nullptr, 0));
-        else if (a == "--prompt" && (v = next())) prompt = uint32_t(std::strtoul(v, nullptr, 0));
-        else if (a == "--tokens" && (v = next())) tokens = uint32_t(std::strtoul(v, nullptr, 0));
-        else if (a == "--ctx" && (v = next())) ctx = uint32_t(std::strtoul(v, nullptr, 0));
-        else if (a == "--seed" && (v = next())) seed = uint32_t(std::strtoul(v, nullptr, 0));
+        if (a == "--layers") { if (!num(layers)) return usage(); }
+        else if (a == "--prompt-len") { if (!num(prompt_len)) return usage(); }
+        else if (a == "-n" || a == "--tokens") { if (!num(tokens)) return usage(); }
+        else if (a == "--ctx") { if (!num(ctx)) return usage(); }
+        else if (a == "--weights-seed") { if (!num(seed)) return usage(); }
+        else if (a == "--pack-threads") { if (!num(pack_threads)) return usage(); }
         else if (a == "--exec" && (v = next())) {
             const std::string m = v;
             exec = m == "token" ? XP_EXEC_TOKEN : m == "graph" ? XP_EXEC_GRAPH
@@ -74,18 +104,43 @@ int main(int argc, char** argv) {
         } else if (a == "--curve") curve = true;
         else if (a == "--ids") print_ids = true;
         else if (a == "--model" && (v = next())) model = v;
-        else if (a == "--cache" && (v = next())) cache = v;
-        else if (a == "--no-cache") no_cache = true;
+        else if (a == "--pack-cache" && (v = next())) cache = v;
+        else if (a == "--no-pack-cache") no_cache = true;
         else if (a == "--repack") repack = true;
         else if (a == "--verify-cache") verify = true;
-        else if (a == "--text" && (v = next())) text = v;
+        else if (a == "--prompt" && (v = next())) { text = v; have_text = true; }
+        else if (a == "--prompt-file" && (v = next())) {
+            text.clear();
+            if (!read_file(v, text)) {
+                std::fprintf(stderr, "cannot open %s\n", v);
+                return 2;
+            }
+            have_text = true;
+        }
         else if (a == "--chat") chat = true;
+        else if ((a == "--max-seq" || a == "--window" || a == "--global-every" || a == "--temp" ||
+                  a == "--top-k" || a == "--top-p" || a == "--seed") && (v = next()))
+            policy.emplace_back(a, std::strtod(v, nullptr));
         else return usage();
     }
-    if ((verify || repack || no_cache || !cache.empty() || !text.empty() || chat) && model.empty())
+    if ((verify || repack || no_cache || !cache.empty() || have_text || chat) && model.empty())
         return usage();
-    if (chat && text.empty()) return usage();
+    if (chat && !have_text) return usage();
     if (!model.empty() && cache.empty() && !no_cache) cache = model + ".xpack";
+    auto apply_policy = [&](xpose::llm::Config& c) {
+        for (const auto& [name, x] : policy) {
+            if (name == "--max-seq") c.max_seq = uint32_t(x);
+            else if (name == "--window") c.sliding_window = uint32_t(x);
+            else if (name == "--global-every") c.global_every = uint32_t(x);
+            else if (name == "--seed") c.seed = uint32_t(x);
+            else {
+                c.sample_mode = 1;
+                if (name == "--temp") c.temperature = float(x);
+                else if (name == "--top-k") c.top_k = uint32_t(x);
+                else c.top_p = float(x);
+            }
+        }
+    };
     try {
         xpose::llm::Config cfg;
         cfg.n_layers = layers;
@@ -94,8 +149,9 @@ int main(int argc, char** argv) {
         if (!model.empty()) {
             gguf.reset(new xpose::llm::Model(model));
             cfg = gguf->config(cfg);
+            apply_policy(cfg);
             if (verify) {
-                const uint32_t bad = gguf->verify_cache(cfg, cache);
+                const uint32_t bad = gguf->verify_cache(cfg, cache, pack_threads);
                 std::printf("%s: %s\n", cache.c_str(),
                             bad ? "FAIL: the cache does not match a fresh pack"
                                 : "PASS: cached bytes are identical to a fresh pack");
@@ -106,9 +162,11 @@ int main(int argc, char** argv) {
         std::unique_ptr<xpose::llm::DecodeSession> sp;
         if (gguf)
             sp.reset(new xpose::llm::DecodeSession(*gguf, cfg, no_cache ? std::string() : cache,
-                                                   repack ? XP_LOAD_REPACK : 0u));
-        else
+                                                   repack ? XP_LOAD_REPACK : 0u, pack_threads));
+        else {
+            apply_policy(cfg);
             sp.reset(new xpose::llm::DecodeSession(cfg));
+        }
         xpose::llm::DecodeSession& sess = *sp;
         if (!gguf) sess.synthesize(seed);
         const double load_ms = now_ms() - t0;
@@ -130,7 +188,7 @@ int main(int argc, char** argv) {
 
         std::unique_ptr<xpose::llm::Tokenizer> tok;
         int32_t stop1 = -1, stop2 = -1;
-        if (!text.empty()) {
+        if (have_text) {
             tok.reset(new xpose::llm::Tokenizer(*gguf));
             if (chat) text = "<start_of_turn>user\n" + text + "<end_of_turn>\n<start_of_turn>model\n";
             stop1 = tok->eos_id();
@@ -153,7 +211,7 @@ int main(int argc, char** argv) {
             ids.push_back(4242);
         } else {
             // Prompt ids uniform on [0, vocab): Philox stream 0x7000.
-            for (uint32_t i = 0; i < prompt; ++i) {
+            for (uint32_t i = 0; i < prompt_len; ++i) {
                 const uint32_t c[4] = {i, 0u, 0u, 0u}, k[2] = {seed, 0x7000u};
                 uint32_t o[4];
                 xp_philox4x32_10(c, k, o);

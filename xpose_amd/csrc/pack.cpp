@@ -597,7 +597,12 @@ int xp_config_from_gguf(xp_gguf* g, xp_config* c) {
     if (m.vocab) c->vocab = m.vocab;
     c->rms_eps = m.rms_eps;
     c->rope_theta_global = m.rope_base;
-    if (m.sliding_window) c->sliding_window = m.sliding_window;
+    // A window the caller moved off the default is a command-line choice and
+    // survives the merge (decode.cpp:1427-1434); otherwise the file's extent.
+    xp_config d;
+    xp_config_gemma3_1b(&d);
+    if (m.sliding_window && c->sliding_window == d.sliding_window)
+        c->sliding_window = m.sliding_window;
     return XP_OK;
 }
 
