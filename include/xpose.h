@@ -503,6 +503,85 @@ int xp_gguf_verify_cache(xp_gguf* g, const xp_config* c, const char* cache_path,
 int xp_session_load_gguf(xp_session* s, xp_gguf* g, const char* cache_path, uint32_t flags,
                          uint32_t threads, xp_load_stats* st);
 
+/* ---- native-format weights ------------------------------------------------
+ * GGUF's own Q8_0 / Q5_0 / Q4_K / Q6_K blocks, used without requantising
+ * (kernels/llm_quant.cl:83-615, examples/llm/quant_repack.{hpp,cpp}). Matrix
+ * convention of that code: `rows` outputs, each a GGUF row of `cols`
+ * reduction elements (cols = dims[0], a multiple of 32, of 256 for Q4_K /
+ * Q6_K); out[r] = sum_k w[r][k] in[k].
+ *
+ * Native layout, straight from the file: xp_dequant_native replaces
+ * dequant_q8_0 / _q5_0 / _q4_k / _q6_k (llm_quant.cl:92-99, 144-149,
+ * 200-219, 284-291) and is bit-identical to xp_dequantize; xp_mv_native
+ * replaces matvec_q8_0 / _q5_0 / _q4_k / _q6_k (llm_quant.cl:101-121,
+ * 151-170, 221-272, 293-322). `src` must be 2-byte aligned.
+ *
+ * Repacked layout (RepackedTensor, quant_repack.hpp:13-67), made once at
+ * load: output row r = 64 g + t, k-block kb = k / 32, j = k % 32, slot
+ * idx = (g nkb + kb) 64 + t with nkb = cols / 32, rows padded to a multiple
+ * of 64 with zero planes.
+ *   quant  Q4_K / Q5_0 / Q6_K: words 4 idx .. 4 idx + 3, the low nibble of
+ *          quant j at bits 4 (j % 8) of word j / 8 (the int4 plane's shape);
+ *          Q8_0: words 8 idx .. 8 idx + 7, the int8 of j at bits 8 (j % 4)
+ *          of word j / 4.
+ *   high   Q5_0: word idx, bit j = bit 4 of quant j; Q6_K: words 2 idx +
+ *          j / 16, bits 2 (j % 16) = bits 4-5 of quant j; else absent.
+ *   scale  fp32 per slot (Q6_K: two, 2 idx + j / 16): d for Q8_0 / Q5_0,
+ *          d * sub-scale for Q4_K / Q6_K.
+ *   bias   fp32 per slot, Q4_K only: dmin * sub-min.
+ * Weight (r, k) = scale * q (Q8_0), scale * (q - 16) (Q5_0), scale * (q - 32)
+ * (Q6_K), scale * q - bias (Q4_K): the same fp32 operations the dequantiser
+ * performs, so xp_rq_reconstruct == xp_dequantize bit for bit. */
+typedef struct {
+    uint32_t type;          /* XP_GGML_Q8_0, _Q5_0, _Q4_K or _Q6_K */
+    uint32_t rows;          /* outputs */
+    uint32_t padded_rows;   /* rows rounded up to a multiple of 64 */
+    uint32_t cols;          /* reduction length */
+    uint32_t nkb;           /* cols / 32 */
+    uint32_t reserved;
+    uint64_t quant_bytes, high_bytes, scale_bytes, bias_bytes;   /* 0 = plane absent */
+    uint64_t native_bytes;  /* the GGUF blocks of the same matrix (native_bytes()) */
+} xp_rq_layout;
+
+/* Device planes of one repacked matrix, as xp_rq_layout describes them. */
+typedef struct {
+    uint32_t        type, rows, cols, reserved;
+    const void*     quant;  /* 16-byte aligned */
+    const uint32_t* high;   /* Q5_0 / Q6_K, else NULL */
+    const float*    scale;
+    const float*    bias;   /* Q4_K, else NULL */
+} xp_rq_tensor;
+
+/* Plane sizes for a matrix; XP_E_ARG for another type, cols % 32 != 0 or
+ * (Q4_K / Q6_K) cols % 256 != 0, as repack() refuses. */
+int xp_rq_layout_of(uint32_t type, uint32_t rows, uint32_t cols, xp_rq_layout* out);
+/* repack() (quant_repack.cpp:135-217): rows x cols native blocks at src
+ * (rows * native_bytes / rows contiguous) into host planes of the layout's
+ * sizes (high / bias may be NULL when absent); rows are packed on `threads`
+ * host threads (0 = all). */
+int xp_rq_repack(const xp_rq_layout* l, const void* src, uint32_t threads, void* quant,
+                 uint32_t* high, float* scale, float* bias);
+/* reconstruct() over the whole matrix (quant_repack.cpp:219-239):
+ * out[r * cols + k], host planes. */
+int xp_rq_reconstruct(const xp_rq_layout* l, const void* quant, const uint32_t* high,
+                      const float* scale, const float* bias, float* out);
+/* matvec_rq4_k / _rq5_0 / _rq6_k / _rq8_0 (llm_quant.cl:515-549) for
+ * split == 1, their _split forms + mv_reduce (llm_quant.cl:574-615) for
+ * split > 1 (here one launch: the last k-chunk of a row group to finish sums
+ * the partials in chunk order), split == 0 picks one. `in` is fp32 [cols],
+ * 16-byte aligned; out [rows]. Within 1e-5 of max|out| of the float64
+ * product (activations are staged as 20-bit block fixed point; every block
+ * product is an exact integer). */
+int xp_mv_rq(float* out, const float* in, const xp_rq_tensor* w, uint32_t split,
+             xp_stream stream);
+/* `iters` calls of xp_mv_rq rotating over `ncopies` weight copies; *ms is
+ * the total elapsed time on the stream (HIP events). */
+int xp_mv_rq_timed(float* out, const float* in, const xp_rq_tensor* ws, uint32_t ncopies,
+                   uint32_t split, uint32_t iters, xp_stream stream, float* ms);
+int xp_dequant_native(float* out, const void* src, uint32_t type, uint64_t n, xp_stream stream);
+int xp_mv_native(float* out, const float* in, const void* src, uint32_t type, uint32_t rows,
+                 uint32_t cols, xp_stream stream);
+
 /* ---- tokenizer ------------------------------------------------------------
  * SentencePiece from the GGUF vocabulary (Tokenizer, model/tokenizer.hpp:46-94,
  * tokenizer.cpp:70-374): control / unknown tokens cut out first (longest

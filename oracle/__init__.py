@@ -101,6 +101,8 @@ def lib() -> C.CDLL:
             "xo_pack_int4": (None, [F32P, u32, u32, i32, U32P, vp]),
             "xo_quantise": (u32, [f32, f32]),
             "xo_best_bf16_scale": (f32, [F32P, f32]),
+            "xo_rq_repack": (i32, [u32, vp, u32, u32, U32P, vp, F32P, vp]),
+            "xo_rq_reconstruct": (f32, [u32, u32, U32P, vp, F32P, vp, u32, u32]),
             "xo_forward": (i32, [C.POINTER(Model), u32, u32, vp, i32]),
             "xo_generate_greedy": (i32, [C.POINTER(Model), U32P, u32, u32, U32P, i32]),
         }
@@ -146,6 +148,39 @@ def pack_int4(w_cols, bf16: bool = True):
     sc = np.empty(rows // 32 * cols, np.uint16 if bf16 else np.float32)
     lib().xo_pack_int4(w_cols, rows, cols, 1 if bf16 else 0, wq, sc.ctypes.data)
     return wq, sc
+
+
+RQ_TYPES = {8: (8, 0, 1, False), 6: (4, 1, 1, False), 12: (4, 0, 1, True), 14: (4, 2, 2, False)}
+
+
+def rq_repack(ggml_type: int, raw, rows: int, cols: int) -> dict:
+    """repack() of quant_repack.cpp: the planes of a rows x cols native
+    matrix as numpy arrays (quant, high, scale, bias; None where absent)."""
+    qw, hw, sw, has_bias = RQ_TYPES[ggml_type]
+    slots = (rows + 63) // 64 * (cols // 32) * 64
+    quant = np.empty(slots * qw, np.uint32)
+    high = np.empty(slots * hw, np.uint32) if hw else None
+    scale = np.empty(slots * sw, np.float32)
+    bias = np.empty(slots, np.float32) if has_bias else None
+    raw = np.ascontiguousarray(raw)
+    rc = lib().xo_rq_repack(ggml_type, raw.ctypes.data, rows, cols, quant,
+                            None if high is None else high.ctypes.data, scale,
+                            None if bias is None else bias.ctypes.data)
+    if rc != 0:
+        raise ValueError(f"xo_rq_repack refused type {ggml_type} {rows} x {cols}")
+    return {"quant": quant, "high": high, "scale": scale, "bias": bias}
+
+
+def rq_reconstruct(ggml_type: int, planes: dict, rows: int, cols: int) -> np.ndarray:
+    """reconstruct() at every (r, k): float32 [rows][cols]."""
+    out = np.empty((rows, cols), np.float32)
+    f = lib().xo_rq_reconstruct
+    h = None if planes["high"] is None else planes["high"].ctypes.data
+    b = None if planes["bias"] is None else planes["bias"].ctypes.data
+    for r in range(rows):
+        for k in range(cols):
+            out[r, k] = f(ggml_type, cols // 32, planes["quant"], h, planes["scale"], b, r, k)
+    return out
 
 
 def argmax_tree(logits) -> tuple[int, float]:

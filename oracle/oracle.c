@@ -1100,3 +1100,164 @@ void xo_pack_int4(const float* w, uint32_t rows, uint32_t cols, int bf16, uint32
     }
     free(scales);
 }
+
+/* ------------------------------------------------------------------ */
+/* Native-format repack (examples/llm/quant_repack.cpp)                 */
+/* ------------------------------------------------------------------ */
+
+/* quant_repack.cpp's fp16() (:8-28) is llm_quant.cl's decoder again:
+ * xo_fp16_to_fp32. get_scale_min_k4 (:35-43): k4_scale_min above. */
+
+/* extract_q8_0 / _q5_0 / _q4_k / _q6_k, quant_repack.cpp:62-127: one row's
+ * raw (unbiased) quants, its scales (granularity 32, Q6_K 16) and, for Q4_K,
+ * its biases. */
+static void rq_extract(uint32_t type, const uint8_t* row, uint32_t cols, uint8_t* qraw,
+                       float* scale, float* bias) {
+    uint32_t b, j, s, l, h, g;
+    switch (type) {
+        case 8:
+            for (b = 0; b < cols / 32; ++b) {
+                const uint8_t* blk = row + (size_t)b * 34;
+                scale[b] = rd_half(blk);
+                for (j = 0; j < 32; ++j) qraw[b * 32 + j] = blk[2 + j];
+            }
+            break;
+        case 6:
+            for (b = 0; b < cols / 32; ++b) {
+                const uint8_t* blk = row + (size_t)b * 22;
+                uint32_t qh;
+                scale[b] = rd_half(blk);
+                qh = (uint32_t)blk[2] | ((uint32_t)blk[3] << 8) | ((uint32_t)blk[4] << 16) |
+                     ((uint32_t)blk[5] << 24);
+                for (j = 0; j < 32; ++j) {
+                    const uint32_t byte = blk[6 + j % 16];
+                    const uint32_t lo = j < 16 ? (byte & 0xF) : (byte >> 4);
+                    qraw[b * 32 + j] = (uint8_t)(lo | (((qh >> j) & 1u) << 4));
+                }
+            }
+            break;
+        case 12:
+            for (b = 0; b < cols / 256; ++b) {
+                const uint8_t* blk = row + (size_t)b * 144;
+                const float dd = rd_half(blk), dmin = rd_half(blk + 2);
+                for (s = 0; s < 8; ++s) {
+                    uint8_t sc, mn;
+                    k4_scale_min((int)s, blk + 4, &sc, &mn);
+                    scale[b * 8 + s] = dd * (float)sc;
+                    bias[b * 8 + s] = dmin * (float)mn;
+                    for (l = 0; l < 32; ++l) {
+                        const uint32_t byte = blk[16 + (s / 2) * 32 + l];
+                        qraw[b * 256 + s * 32 + l] = (uint8_t)((s & 1) ? (byte >> 4) : (byte & 0xF));
+                    }
+                }
+            }
+            break;
+        case 14:
+            for (b = 0; b < cols / 256; ++b) {
+                const uint8_t* blk = row + (size_t)b * 210;
+                const float dd = rd_half(blk + 208);
+                for (h = 0; h < 2; ++h)
+                    for (g = 0; g < 4; ++g)
+                        for (l = 0; l < 32; ++l) {
+                            const uint32_t byte = blk[h * 64 + l + (g & 1) * 32];
+                            const uint32_t lo = g < 2 ? (byte & 0xF) : (byte >> 4);
+                            const uint32_t hi = (blk[128 + h * 32 + l] >> (2 * g)) & 3u;
+                            const uint32_t r = h * 128 + g * 32 + l;
+                            qraw[b * 256 + r] = (uint8_t)(lo | (hi << 4));
+                            if (l % 16 == 0)
+                                scale[(b * 256 + r) / 16] =
+                                    dd * (float)(int8_t)blk[192 + h * 8 + l / 16 + 2 * g];
+                        }
+            }
+            break;
+    }
+}
+
+/* repack(), quant_repack.cpp:135-217: the planes (sized for the padded
+ * rows) are zeroed, then each row's extract is interleaved at slot
+ * idx = (g nkb + kb) 64 + t. Returns -1 where repack() returns false. */
+int xo_rq_repack(uint32_t type, const void* src, uint32_t rows, uint32_t cols, uint32_t* quant,
+                 uint32_t* high, float* scale, float* bias) {
+    uint32_t gran = 32, qwords = 4, hwords = 0, nkb, padded, r, kb, j;
+    int has_bias = 0;
+    size_t slots, row_bytes;
+    uint8_t* qraw;
+    float *rs, *rb;
+    if (cols == 0 || cols % 32 != 0 || rows == 0) return -1;
+    switch (type) {
+        case 8: qwords = 8; row_bytes = (size_t)(cols / 32) * 34; break;
+        case 6: hwords = 1; row_bytes = (size_t)(cols / 32) * 22; break;
+        case 12:
+            if (cols % 256) return -1;
+            has_bias = 1;
+            row_bytes = (size_t)(cols / 256) * 144;
+            break;
+        case 14:
+            if (cols % 256) return -1;
+            hwords = 2;
+            gran = 16;
+            row_bytes = (size_t)(cols / 256) * 210;
+            break;
+        default: return -1;
+    }
+    nkb = cols / 32;
+    padded = (rows + 63) / 64 * 64;
+    slots = (size_t)(padded / 64) * nkb * 64;
+    memset(quant, 0, slots * qwords * 4);
+    if (hwords) memset(high, 0, slots * hwords * 4);
+    memset(scale, 0, slots * (32 / gran) * 4);
+    if (has_bias) memset(bias, 0, slots * 4);
+    qraw = (uint8_t*)malloc(cols);
+    rs = (float*)malloc((size_t)(cols / gran) * 4);
+    rb = (float*)malloc((size_t)(cols / 32) * 4);
+    for (r = 0; r < rows; ++r) {
+        const uint32_t g = r / 64, t = r % 64;
+        rq_extract(type, (const uint8_t*)src + (size_t)r * row_bytes, cols, qraw, rs, rb);
+        for (kb = 0; kb < nkb; ++kb) {
+            const size_t idx = ((size_t)g * nkb + kb) * 64 + t;
+            for (j = 0; j < 32; ++j) {
+                const uint32_t q = qraw[kb * 32 + j];
+                if (type == 8) {
+                    quant[idx * 8 + j / 4] |= q << (8 * (j % 4));
+                } else {
+                    quant[idx * 4 + j / 8] |= (q & 0xFu) << (4 * (j % 8));
+                    if (type == 6) high[idx] |= ((q >> 4) & 1u) << j;
+                    else if (type == 14) high[idx * 2 + j / 16] |= ((q >> 4) & 3u) << (2 * (j % 16));
+                }
+            }
+            if (gran == 16) {
+                scale[idx * 2] = rs[kb * 2];
+                scale[idx * 2 + 1] = rs[kb * 2 + 1];
+            } else {
+                scale[idx] = rs[kb];
+            }
+            if (has_bias) bias[idx] = rb[kb];
+        }
+    }
+    free(qraw);
+    free(rs);
+    free(rb);
+    return 0;
+}
+
+/* reconstruct(), quant_repack.cpp:219-239. */
+float xo_rq_reconstruct(uint32_t type, uint32_t nkb, const uint32_t* quant, const uint32_t* high,
+                        const float* scale, const float* bias, uint32_t r, uint32_t k) {
+    const uint32_t g = r / 64, tt = r % 64, kb = k / 32, j = k % 32;
+    const size_t idx = ((size_t)g * nkb + kb) * 64 + tt;
+    uint32_t q;
+    if (type == 8) {
+        const uint32_t byte = (quant[idx * 8 + j / 4] >> (8 * (j % 4))) & 0xFFu;
+        return scale[idx] * (float)((int)(byte ^ 0x80u) - 128);
+    }
+    q = (quant[idx * 4 + j / 8] >> (4 * (j % 8))) & 0xFu;
+    if (type == 6) {
+        q |= ((high[idx] >> j) & 1u) << 4;
+        return scale[idx] * (float)((int)q - 16);
+    }
+    if (type == 14) {
+        q |= ((high[idx * 2 + j / 16] >> (2 * (j % 16))) & 3u) << 4;
+        return scale[idx * 2 + j / 16] * (float)((int)q - 32);
+    }
+    return scale[idx] * (float)q - bias[idx];
+}

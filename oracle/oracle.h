@@ -192,6 +192,17 @@ void xo_pack_int4(const float* w, uint32_t rows, uint32_t cols, int bf16, uint32
 uint32_t xo_quantise(float v, float inv_scale);
 float xo_best_bf16_scale(const float* blk32, float s0);
 
+/* ---- native-format repack (examples/llm/quant_repack.cpp) ---- */
+/* repack() (:135-217) of rows x cols native blocks (type 8 Q8_0, 6 Q5_0,
+ * 12 Q4_K, 14 Q6_K) into planes sized for rows padded to 64 (zeroed here);
+ * high / bias unused (may be NULL) where the type has none. 0, or -1 where
+ * repack() refuses. */
+int xo_rq_repack(uint32_t type, const void* src, uint32_t rows, uint32_t cols, uint32_t* quant,
+                 uint32_t* high, float* scale, float* bias);
+/* reconstruct() (:219-239): element (r, k) of the repacked matrix. */
+float xo_rq_reconstruct(uint32_t type, uint32_t nkb, const uint32_t* quant, const uint32_t* high,
+                        const float* scale, const float* bias, uint32_t r, uint32_t k);
+
 #ifdef __cplusplus
 }
 #endif

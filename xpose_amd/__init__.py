@@ -87,6 +87,22 @@ GGML_Q4_K, GGML_Q6_K, GGML_BF16 = 12, 14, 30
 LOAD_REPACK, LOAD_NORM_RAW, LOAD_NO_EMBED = 1, 2, 4
 
 
+class RqLayout(C.Structure):
+    """xp_rq_layout: plane sizes of a repacked native-format matrix."""
+    _fields_ = [("type", C.c_uint32), ("rows", C.c_uint32), ("padded_rows", C.c_uint32),
+                ("cols", C.c_uint32), ("nkb", C.c_uint32), ("reserved", C.c_uint32),
+                ("quant_bytes", C.c_uint64), ("high_bytes", C.c_uint64),
+                ("scale_bytes", C.c_uint64), ("bias_bytes", C.c_uint64),
+                ("native_bytes", C.c_uint64)]
+
+
+class RqTensor(C.Structure):
+    """xp_rq_tensor: device planes of one repacked matrix."""
+    _fields_ = [("type", C.c_uint32), ("rows", C.c_uint32), ("cols", C.c_uint32),
+                ("reserved", C.c_uint32), ("quant", C.c_void_p), ("high", C.c_void_p),
+                ("scale", C.c_void_p), ("bias", C.c_void_p)]
+
+
 class XpMetrics(C.Structure):
     _fields_ = [("ms", C.c_double), ("gpu_ms", C.c_double), ("sample_ms", C.c_double),
                 ("tokens_per_sec", C.c_double), ("position", C.c_uint32),
@@ -166,6 +182,13 @@ def _declare(lib: C.CDLL) -> None:
         "xp_gguf_meta_string": (i32, [vp, C.c_char_p, C.c_char_p, sz, P(sz)]),
         "xp_gguf_meta_array_length": (i32, [vp, C.c_char_p, P(C.c_uint64)]),
         "xp_dequantize": (i32, [u32, vp, vp, C.c_uint64]),
+        "xp_rq_layout_of": (i32, [u32, u32, u32, P(RqLayout)]),
+        "xp_rq_repack": (i32, [P(RqLayout), vp, u32, vp, vp, vp, vp]),
+        "xp_rq_reconstruct": (i32, [P(RqLayout), vp, vp, vp, vp, vp]),
+        "xp_mv_rq": (i32, [vp, vp, P(RqTensor), u32, vp]),
+        "xp_mv_rq_timed": (i32, [vp, vp, P(RqTensor), u32, u32, u32, vp, P(f32)]),
+        "xp_dequant_native": (i32, [vp, vp, u32, C.c_uint64, vp]),
+        "xp_mv_native": (i32, [vp, vp, vp, u32, u32, u32, vp]),
         "xp_gguf_dequantize_rows": (i32, [vp, C.c_char_p, C.c_uint64, C.c_uint64, vp]),
         "xp_config_from_gguf": (i32, [vp, P(XpConfig)]),
         "xp_pack_int4": (i32, [vp, u32, u32, i32, u32, vp, vp]),
@@ -712,6 +735,61 @@ def pack_int4(w_cols: np.ndarray, scale_fmt: int = XP_SCALE_BF16_QUAD, threads: 
     call("xp_pack_int4", w_cols.ctypes.data, rows, cols, scale_fmt, threads, wq.ctypes.data,
          sc.ctypes.data)
     return wq, sc
+
+
+def rq_layout(ggml_type: int, rows: int, cols: int) -> RqLayout:
+    l = RqLayout()
+    call("xp_rq_layout_of", ggml_type, rows, cols, C.byref(l))
+    return l
+
+
+def _ptr(a):
+    return None if a is None else a.ctypes.data
+
+
+def rq_repack(ggml_type: int, raw: np.ndarray, rows: int, cols: int, threads: int = 0) -> dict:
+    """xp_rq_repack: host planes {layout, quant, high, scale, bias} (None
+    where the type has no such plane) of rows x cols native blocks."""
+    l = rq_layout(ggml_type, rows, cols)
+    planes = {"layout": l,
+              "quant": np.empty(l.quant_bytes // 4, np.uint32),
+              "high": np.empty(l.high_bytes // 4, np.uint32) if l.high_bytes else None,
+              "scale": np.empty(l.scale_bytes // 4, np.float32),
+              "bias": np.empty(l.bias_bytes // 4, np.float32) if l.bias_bytes else None}
+    raw = np.ascontiguousarray(raw)
+    call("xp_rq_repack", C.byref(l), raw.ctypes.data, threads, _ptr(planes["quant"]),
+         _ptr(planes["high"]), _ptr(planes["scale"]), _ptr(planes["bias"]))
+    return planes
+
+
+def rq_reconstruct(planes: dict) -> np.ndarray:
+    """xp_rq_reconstruct: float32 [rows][cols]."""
+    l = planes["layout"]
+    out = np.empty((l.rows, l.cols), np.float32)
+    call("xp_rq_reconstruct", C.byref(l), _ptr(planes["quant"]), _ptr(planes["high"]),
+         _ptr(planes["scale"]), _ptr(planes["bias"]), out.ctypes.data)
+    return out
+
+
+class RqWeights:
+    """A repacked matrix's planes in device memory; .tensor is the
+    xp_rq_tensor that xp_mv_rq takes."""
+
+    def __init__(self, planes: dict):
+        l = planes["layout"]
+        self.layout = l
+        self.bufs = {k: DeviceBuffer.from_array(planes[k])
+                     for k in ("quant", "high", "scale", "bias") if planes[k] is not None}
+        t = RqTensor()
+        t.type, t.rows, t.cols = l.type, l.rows, l.cols
+        for k in ("quant", "high", "scale", "bias"):
+            setattr(t, k, self.bufs[k].ptr if k in self.bufs else None)
+        self.tensor = t
+
+    def close(self) -> None:
+        for b in self.bufs.values():
+            b.close()
+        self.bufs = {}
 
 
 class Tokenizer:

@@ -23,6 +23,10 @@ int launch_mv(const MvMatDesc* mats, uint32_t n, const float* x, int fmt, uint32
               uint32_t split, float* partial, size_t partial_cap, uint32_t* tickets,
               size_t tickets_cap, hipStream_t st, const char* who);
 
+// ---- repacked native-format matvec (xp_mv_rq) ----
+int launch_mv_rq(float* out, const float* x, const xp_rq_tensor& w, uint32_t split,
+                 hipStream_t st, const char* who);
+
 // ---- QK-norm + RoPE + KV append ----
 struct QkArgs {
     float* q_out;
