@@ -23,7 +23,9 @@ measurements (not the metric): `cfg4` (decode from 4097 to 8192, tok/s per
 prompt, 128 greedy tokens), `attention` (one global layer's decode attention
 at spans 4096 and 8192, HBM GB/s of its K + V bytes) and `cfg5` (16 sequences
 batched, temperature / top-k / top-p sampling, tok/s over all sequences and
-the step's algorithmic bytes). `--no-configs` skips them.
+the step's algorithmic bytes) and `native` (the repacked native-format
+matvecs, Q5_0 / Q8_0 / Q4_K / Q6_K at the shapes Gemma-3-1B's Q4_K_M file
+holds them in, HBM GB/s of their planes). `--no-configs` skips them.
 """
 from __future__ import annotations
 
@@ -84,6 +86,59 @@ def matvec_leg(X, rows: int, cols: int, copies: int, iters: int):
     per_s = ms.value / 1e3 / iters
     nbytes = rows * cols // 2 + (rows // 32) * cols * 2 + rows * 4 + cols * 4
     return nbytes, per_s
+
+
+# Native-format weights at the shapes Gemma-3-1B's Q4_K_M file holds them in
+# (outputs x reduction): ggml type, block elements, block bytes, fp16 field offsets.
+NATIVE_CASES = [("Q5_0", 6, 32, 22, (0,), 6912, 1152), ("Q8_0", 8, 32, 34, (0,), 262144, 1152),
+                ("Q4_K", 12, 256, 144, (0, 2), 1152, 6912), ("Q6_K", 14, 256, 210, (208,), 1152, 6912)]
+
+
+def native_blocks(nblocks: int, size: int, fields, seed: int) -> np.ndarray:
+    """Random block bytes with each fp16 field's exponent in [8, 22] (the
+    reference's quant_test input recipe)."""
+    rng = np.random.default_rng(seed)
+    raw = rng.integers(0, 256, nblocks * size, dtype=np.uint8).reshape(nblocks, size)
+    for off in fields:
+        h = (rng.integers(0, 2, nblocks) << 15) | rng.integers(0, 1024, nblocks) \
+            | ((8 + rng.integers(0, 15, nblocks)) << 10)
+        raw[:, off] = (h & 0xFF).astype(np.uint8)
+        raw[:, off + 1] = (h >> 8).astype(np.uint8)
+    return raw.reshape(-1)
+
+
+def native_leg(X, iters: int = 400):
+    """xp_mv_rq per format: per-launch time over back-to-back launches cycling
+    enough weight copies to exceed 384 MiB, HIP events on the launch stream,
+    and the HBM GB/s of the planes + x + y (algorithmic bytes per launch)."""
+    out = []
+    for name, t, elems, size, fields, rows, cols in NATIVE_CASES:
+        raw = native_blocks(rows * cols // elems, size, fields, 0x5EED0100 + t)
+        planes = X.rq_repack(t, raw, rows, cols)
+        del raw
+        l = planes["layout"]
+        plane_bytes = l.quant_bytes + l.high_bytes + l.scale_bytes + l.bias_bytes
+        copies = max(1, min(64, -(-(384 << 20) // plane_bytes)))
+        ws = [X.RqWeights(planes) for _ in range(copies)]
+        del planes
+        T = (X.RqTensor * copies)(*[w.tensor for w in ws])
+        dx = X.DeviceBuffer.from_array(X.synth_normal(cols, SEED, 960 + t))
+        dout = X.DeviceBuffer(rows * 4)
+        st = C.c_void_p()
+        X.call("xp_stream_create", C.byref(st))
+        ms = C.c_float()
+        n = max(copies, iters if rows < 100000 else iters // 8)
+        X.call("xp_mv_rq_timed", dout.vp, dx.vp, T, copies, 0, n, st, C.byref(ms))
+        X.call("xp_stream_destroy", st)
+        per_s = ms.value / 1e3 / n
+        nbytes = plane_bytes + cols * 4 + rows * 4
+        out.append({"type": name, "shape": f"{rows}x{cols}", "bytes": nbytes,
+                    "native_bytes": l.native_bytes, "us_per_launch": round(per_s * 1e6, 3),
+                    "GBs": round(nbytes / per_s / 1e9, 1),
+                    "frac": round(nbytes / per_s / 1e9 / HBM_PEAK_GBS, 4)})
+        for w in ws:
+            w.close()
+    return out
 
 
 def stream_ceiling(X, nbytes: int = 1 << 30, iters: int = 20) -> float:
@@ -262,9 +317,11 @@ def main() -> int:
     ap.add_argument("--no-configs", action="store_true",
                     help="skip the benchmark config 3 / 4 / 5 and attention legs")
     ap.add_argument("--mv-iters", type=int, default=60)
-    ap.add_argument("--only", choices=["all", "matvec", "attention", "cfg5"], default="all",
+    ap.add_argument("--only", choices=["all", "matvec", "attention", "cfg5", "native"],
+                    default="all",
                     help="one leg alone, for profiling: the standalone matvec and streaming "
-                         "legs, the attention leg, or the batched decode (config 5)")
+                         "legs, the attention leg, the batched decode (config 5), or the "
+                         "native-format (repacked Q8_0 / Q5_0 / Q4_K / Q6_K) matvecs")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported "
@@ -295,6 +352,9 @@ def main() -> int:
                           "matvec_cfg1": {"us_per_launch": round(per1 * 1e6, 3),
                                           "GBs": round(nb1 / per1 / 1e9, 1)},
                           "stream_ceiling_GBs": round(ceil, 1)}), flush=True)
+        return 0
+    if args.only == "native":
+        print(json.dumps({"native": native_leg(X)}), flush=True)
         return 0
     if args.only == "attention":
         print(json.dumps({"attention": [attention_leg(X, sp) for sp in (4096, 8192)]}), flush=True)
@@ -347,6 +407,7 @@ def main() -> int:
         bsess.synthesize(SEED)
         extra["cfg5"] = cfg5_leg(X, bsess, scfg)
         bsess.close()
+        extra["native"] = native_leg(X)
     sess.close()
 
     # Roofline leg: the dominant kernel of the step, the lm_head int4 matvec.
