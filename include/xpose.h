@@ -376,7 +376,9 @@ int  xp_session_kv_bytes(const xp_session* s, size_t* bytes);
  * a timestamp at host[e * grid + w] in 100 MHz ticks (s_memrealtime), 0
  * where w had no work: e = 0 kernel start; e = 1 + 6 l + k the end of layer
  * l's stage k (QKV, attention, combine, O, gate/up, down); e = 6 L + 1 the
- * lm_head; e = 6 L + 2 the argmax. *grid receives the workgroup count. */
+ * lm_head; e = 6 L + 2 the argmax; e = 6 L + 3 + 6 l + k the time w's
+ * inputs of layer l's stage k had all arrived (its wait and the barrier
+ * after it done). *grid receives the workgroup count. */
 int  xp_session_trace(xp_session* s, int enable);
 int  xp_session_last_trace(xp_session* s, uint64_t* host, size_t n, uint32_t* grid);
 /* Host draw over (value, index) candidates, in place (decode.cpp:1873-1917),

@@ -382,3 +382,35 @@ def test_gpu_batched_prefill(xp, xo, mode):
     assert a[0] == b[0]
     ok, msg = logits_close(a[1], b[1])
     assert ok, msg
+
+
+@pytest.mark.gpu
+def test_gpu_token_trace_timeline(xp):
+    """xp_session_trace: stage ends are ordered (each stage's last finisher
+    after the previous one's), every stage has working workgroups, and a
+    workgroup's input arrival precedes its stage end."""
+    X = xp
+    from xpose_amd.trace import arrivals, timeline
+    cfg = cfg_small(X, n_layers=3, exec_mode=3)
+    sess = X.DecodeSession(cfg)
+    sess.synthesize(0x5EED0003)
+    sess.prefill(np.array([7, 8, 9], np.uint32))
+    sess.trace(True)
+    sess.decode_steps(1)
+    tr = sess.last_trace().astype(np.int64)
+    n = cfg.n_layers
+    assert tr.shape[0] == 12 * n + 3 and (tr[0] > 0).all()
+    ends = [tr[1 + e].max() for e in range(6 * n + 2)]
+    assert all(b >= a for a, b in zip(ends, ends[1:])), ends
+    for l in range(n):
+        for k in range(6):
+            arr, end = tr[3 + 6 * n + 6 * l + k], tr[1 + 6 * l + k]
+            w = arr > 0
+            assert w.any(), (l, k)
+            assert (arr[w] <= end[w]).all(), (l, k)
+    rows, lm, am, total = timeline(tr, n)
+    assert total > 0 and lm > 0 and (rows >= 0).all()
+    a = arrivals(tr, n)
+    assert (a[:, :, 1] >= 0).all() and (a[:, :, 2] >= 0).all()
+    sess.trace(False)
+    sess.close()

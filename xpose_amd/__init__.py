@@ -602,13 +602,13 @@ class DecodeSession:
         call("xp_session_trace", self.h, 1 if enable else 0)
 
     def last_trace(self) -> np.ndarray:
-        """[6 * n_layers + 3][grid] ticks (100 MHz) of the last launch: kernel
-        start, the end of each layer's six stages, lm_head, argmax; 0 where a
-        workgroup had no work in a stage."""
+        """[12 * n_layers + 3][grid] ticks (100 MHz) of the last launch: kernel
+        start, the end of each layer's six stages, lm_head, argmax, then each
+        stage's input arrival; 0 where a workgroup had no work in a stage."""
         g = C.c_uint32()
         probe = np.empty(1, np.uint64)
         call("xp_session_last_trace", self.h, probe.ctypes.data, 1, C.byref(g))
-        ne = 6 * self.cfg.n_layers + 3
+        ne = 12 * self.cfg.n_layers + 3
         out = np.empty(ne * g.value, np.uint64)
         call("xp_session_last_trace", self.h, out.ctypes.data, out.size, C.byref(g))
         return out.reshape(ne, g.value)

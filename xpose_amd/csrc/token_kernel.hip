@@ -71,8 +71,8 @@ constexpr int      kTkBig       = 17408;                 // floats of stage scra
 constexpr int      kTkMaxLayers = 64;
 // Slot buffer operations use device scope (sc1, kAuxDev) on raw buffer
 // resources (kRsrcWord3).
-// Poll back-off of the gate/up stage's wait (which spans QKV, attention,
-// combine and O), in units of 64 cycles.
+// Poll back-off of the first phase of the gate/up stage's wait (one thread
+// watching for the layer's attention output), in units of 64 cycles.
 constexpr int      kGuSleep     = 32;
 
 typedef unsigned long long ll_t;
@@ -214,6 +214,19 @@ __device__ __forceinline__ void tk_trace(const TokArgs& a, uint32_t event) {
     if (a.trace && threadIdx.x == 0)
         a.trace[size_t(event) * gridDim.x + blockIdx.x] = __builtin_amdgcn_s_memrealtime();
 }
+// Stage end of layer l, stage k (event 1 + 6 l + k) and the time this
+// workgroup's inputs of that stage had all arrived (event 3 + 6 n_layers +
+// 6 l + k; 0 when the workgroup had no work in the stage).
+__device__ __forceinline__ void tk_trace_stage(const TokArgs& a, uint32_t l, uint32_t k,
+                                               unsigned long long t_in) {
+    if (a.trace && threadIdx.x == 0) {
+        a.trace[size_t(1u + 6u * l + k) * gridDim.x + blockIdx.x] = __builtin_amdgcn_s_memrealtime();
+        a.trace[size_t(3u + 6u * a.n_layers + 6u * l + k) * gridDim.x + blockIdx.x] = t_in;
+    }
+}
+__device__ __forceinline__ unsigned long long tk_now(const TokArgs& a) {
+    return a.trace ? __builtin_amdgcn_s_memrealtime() : 0ull;
+}
 
 // ---- block-wide reductions (512 threads, one barrier) ---------------------------
 // Every thread returns the same total, summed in a fixed order. rs must not be
@@ -350,21 +363,37 @@ __device__ __forceinline__ void tile_prefetch(TkW<R>& p, const void* wq, const v
 template <int FMT, int R>
 __device__ __forceinline__ float tile_dot(const TkW<R>& p, TkSmem& S, uint32_t b0, uint32_t nb,
                                           uint32_t wave, uint32_t lane) {
-    float acc = 0.0f;
     const uint32_t sc = (b0 + wave) % 4u;
+    // Every block's staged planes and scale are read before any is used: the
+    // reads return in order while the first blocks are multiplied, instead of
+    // one LDS round trip per block.
+    QxBlock q[R];
+    float sxv[R];
 #pragma unroll
     for (int r = 0; r < R; ++r) {
         const uint32_t lb = min(wave + 8u * r, nb - 1u);
-        float f = tk_scale<FMT>(p.s[r], sc) * S.sx[lb];
+        sxv[r] = S.sx[lb];
+        q[r] = S.qx[lb];
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    float acc = 0.0f;
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        float f = tk_scale<FMT>(p.s[r], sc) * sxv[r];
         if (wave + 8u * r >= nb) f = 0.0f;
-        acc = fmaf(f, float(block_dot(p.w[r], S.qx[lb])), acc);
+        acc = fmaf(f, float(block_dot(p.w[r], q[r])), acc);
     }
     S.red[wave][lane] = acc;
     __syncthreads();
     float y = 0.0f;
     if (wave == 0) {
+        // all eight partials in flight at once, then summed in wave order
+        float pw[kTkWaves];
 #pragma unroll
-        for (int w = 0; w < kTkWaves; ++w) y += S.red[w][lane];
+        for (int w = 0; w < kTkWaves; ++w) pw[w] = S.red[w][lane];
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int w = 0; w < kTkWaves; ++w) y += pw[w];
     }
     return y;
 }
@@ -513,6 +542,7 @@ __global__ __launch_bounds__(kTkThreads) void token_kernel(TokArgs a) {
         const TokLayer& L = S.lt[l];
         const uint32_t soff = l * lstride;
         // ================= QKV =================
+        unsigned long long t_in = 0;
         for (uint32_t t = t_qkv; t < Sh::N_QKV; t += nwg) {
             uint32_t m, g, c;
             qkv_tile(t, m, g, c);
@@ -553,6 +583,7 @@ __global__ __launch_bounds__(kTkThreads) void token_kernel(TokArgs a) {
             } else {
                 after_ffn(x, l - 1u, w_post);
             }
+            if (t == t_qkv) t_in = tk_now(a);
             float xn[kOwn];
             own_norm<H>(xn, x, w_in, eps, RS());
             {
@@ -573,7 +604,8 @@ __global__ __launch_bounds__(kTkThreads) void token_kernel(TokArgs a) {
             // memory counter also waits for its stores.
             if (t < Sh::NOG && tid / (kGrp / kOwn) == t) own_put(rr, soff, uint32_t(lay.xa) + kOwn * tid, x, tag);
         }
-        tk_trace(a, 1u + 6u * l);
+        tk_trace_stage(a, l, 0u, t_in);
+        t_in = 0;
 
         // ================= attention =================
         const bool glob = L.global != 0u;
@@ -644,6 +676,7 @@ __global__ __launch_bounds__(kTkThreads) void token_kernel(TokArgs a) {
                 }
             }
             __syncthreads();
+            t_in = tk_now(a);
             const uint32_t th = glob ? 1u : 0u;
             // QK-norm + RoPE, one wave per head: the q heads, then the kv head
             // (which follows them in q | k | v)
@@ -782,7 +815,8 @@ __global__ __launch_bounds__(kTkThreads) void token_kernel(TokArgs a) {
             }
             __syncthreads();
         }
-        tk_trace(a, 2u + 6u * l);
+        tk_trace_stage(a, l, 1u, t_in);
+        t_in = 0;
 
         // ================= combine =================
         for (uint32_t c = t_comb; c < Sh::N_COMB; c += nwg) {
@@ -815,6 +849,7 @@ __global__ __launch_bounds__(kTkThreads) void token_kernel(TokArgs a) {
                 }
             }
             __syncthreads();
+            if (c == t_comb) t_in = tk_now(a);
             float m = -INFINITY;
             for (uint32_t s = tid; s < n_att; s += kTkThreads) m = fmaxf(m, S.big[s * 66u]);
             const float M = blk_max(m, RS());
@@ -838,7 +873,8 @@ __global__ __launch_bounds__(kTkThreads) void token_kernel(TokArgs a) {
             }
             __syncthreads();
         }
-        tk_trace(a, 3u + 6u * l);
+        tk_trace_stage(a, l, 2u, t_in);
+        t_in = 0;
 
         // ================= O projection =================
         for (uint32_t t = t_o; t < Sh::N_O; t += nwg) {
@@ -860,10 +896,12 @@ __global__ __launch_bounds__(kTkThreads) void token_kernel(TokArgs a) {
                 own_stage(S, x, tid);
             }
             __syncthreads();
+            if (t == t_o) t_in = tk_now(a);
             const float y = tile_dot<FMT>(p, S, c * nb, nb, wave, lane);
             if (wave == 0) tile_put(rr, soff, uint32_t(lay.o) + c * H + g * kGrp, y, lane, tag);
         }
-        tk_trace(a, 4u + 6u * l);
+        tk_trace_stage(a, l, 3u, t_in);
+        t_in = 0;
 
         // ================= gate / up =================
         TkW<RD> pdn;
@@ -877,6 +915,21 @@ __global__ __launch_bounds__(kTkThreads) void token_kernel(TokArgs a) {
             if (hown) {
                 ld_own(w_post, L.norm[1] + kOwn * tid);
                 ld_own(w_in, L.norm[2] + kOwn * tid);
+            }
+            // This wait spans QKV, attention, combine and O. Until the layer's
+            // attention output exists (the combine stage's first pair, written
+            // about two stages before the O partials) one thread polls it with
+            // back-off; only then do the owners poll every input without
+            // sleeping. Two hundred workgroups polling all their inputs for the
+            // whole span load the fabric that the other stages' exchanges cross.
+            if (tid == 0) {
+                const uint32_t off1[1] = {uint32_t(lay.atto) * 8u};
+                const bool act1[1] = {true};
+                u32x4 v1[1];
+                ll_wait<1, kGuSleep>(rr, soff, off1, act1, v1, tag, a.state);
+            }
+            __syncthreads();
+            if (hown) {
                 constexpr uint32_t NL = (1 + Sh::KO) * kOwnP;
                 uint32_t off[NL];
                 bool act[NL];
@@ -887,7 +940,7 @@ __global__ __launch_bounds__(kTkThreads) void token_kernel(TokArgs a) {
 #pragma unroll
                 for (uint32_t c = 0; c < Sh::KO; ++c)
                     own_offsets(&off[kOwnP * (1 + c)], uint32_t(lay.o) + c * H + kOwn * tid);
-                ll_wait<NL, kGuSleep>(rr, soff, off, act, v, tag, a.state);
+                ll_wait(rr, soff, off, act, v, tag, a.state);
                 own_unpack(xa, &v[0]);
                 own_unpack(o, &v[kOwnP]);
 #pragma unroll
@@ -900,6 +953,7 @@ __global__ __launch_bounds__(kTkThreads) void token_kernel(TokArgs a) {
             }
             float x[kOwn], xn[kOwn];
             own_residual<H>(x, xa, o, w_post, eps, RS());
+            if (t == t_gu) t_in = tk_now(a);
             own_norm<H>(xn, x, w_in, eps, RS());
             if (hown) own_stage(S, xn, tid);
             __syncthreads();
@@ -908,7 +962,8 @@ __global__ __launch_bounds__(kTkThreads) void token_kernel(TokArgs a) {
             // x after the attention block, for the next layer: spread and stored last, as xa
             if (t < Sh::NOG && tid / (kGrp / kOwn) == t) own_put(rr, soff, uint32_t(lay.xb) + kOwn * tid, x, tag);
         }
-        tk_trace(a, 5u + 6u * l);
+        tk_trace_stage(a, l, 4u, t_in);
+        t_in = 0;
 
         // ================= down =================
         for (uint32_t t = t_dn; t < Sh::N_DN; t += nwg) {
@@ -934,11 +989,12 @@ __global__ __launch_bounds__(kTkThreads) void token_kernel(TokArgs a) {
                 own_stage(S, hx, tid);
             }
             __syncthreads();
+            if (t == t_dn) t_in = tk_now(a);
             const float y = tile_dot<FMT>(pdn, S, 4u * q0, nb, wave, lane);
             if (wave == 0) tile_put(rr, soff, uint32_t(lay.dnp) + c * H + g * kGrp, y, lane, tag);
         }
         if (t_dn >= Sh::N_DN && l + 1u < a.n_layers && t_qkv < Sh::N_QKV) prefetch_qkv(pq, l + 1u, t_qkv);
-        tk_trace(a, 6u + 6u * l);
+        tk_trace_stage(a, l, 5u, t_in);
     }
 
     if (!a.want_logits) {

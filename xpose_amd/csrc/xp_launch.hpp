@@ -236,7 +236,7 @@ constexpr int kTokThreads = 512;
 // Trace events per launch, one timestamp per workgroup each: kernel start,
 // then per layer the completion of QKV, attention, combine, O, gate/up and
 // down (zero where the workgroup had no work), then lm_head and argmax.
-inline uint32_t tok_trace_events(uint32_t n_layers) { return 6u * n_layers + 3u; }
+inline uint32_t tok_trace_events(uint32_t n_layers) { return 12u * n_layers + 3u; }
 // Dynamic LDS the token kernel asks for; larger than half a CU's LDS so that
 // no CU holds two of the grid's workgroups.
 size_t tok_lds_bytes();

@@ -6,7 +6,11 @@ Builds the seeded synthetic Gemma-3-1B model, pre-fills the KV cache to
 position ctx (fp16 N(0,1)), decodes a few warm-up tokens, then records one
 token with xp_session_trace and prints, per layer, how long each of the six
 stages added to the critical path: the time from the previous stage's last
-finisher to this stage's last finisher (100 MHz s_memrealtime stamps).
+finisher to this stage's last finisher (100 MHz s_memrealtime stamps). That
+increment is split into `wait` (previous stage's last finisher to the last
+workgroup's input arrival: the exchange latency plus producer skew) and
+`body` (last arrival to last finisher); `wg body` is the mean over working
+workgroups of their own arrival-to-finish time.
 """
 from __future__ import annotations
 
@@ -33,6 +37,28 @@ def timeline(tr: np.ndarray, n_layers: int):
     lm = (tr[6 * n_layers + 1].max() - t0) / 100.0
     am = (tr[6 * n_layers + 2].max() - t0) / 100.0
     return np.array(rows), lm - prev, am - lm, am
+
+
+def arrivals(tr: np.ndarray, n_layers: int):
+    """[n_layers][6][3]: wait, body and mean per-workgroup body (us) per stage."""
+    tr = tr.astype(np.int64)
+    t0 = tr[0][tr[0] > 0].min()
+    out = np.zeros((n_layers, 6, 3))
+    prev = 0.0
+    for l in range(n_layers):
+        for k in range(6):
+            end = tr[1 + 6 * l + k]
+            arr = tr[6 * n_layers + 3 + 6 * l + k]
+            work = arr > 0
+            end_max = (end.max() - t0) / 100.0
+            if work.any():
+                in_max = (arr[work].max() - t0) / 100.0
+                wg_body = ((end[work] - arr[work]) / 100.0).mean()
+            else:
+                in_max, wg_body = end_max, 0.0
+            out[l, k] = (in_max - prev, end_max - in_max, wg_body)
+            prev = end_max
+    return out
 
 
 def main() -> int:
@@ -67,6 +93,14 @@ def main() -> int:
         print(f"{name:10s} {lm_:11.2f} {gm_:12.2f}")
     print(f"{'per layer':10s} {rows[loc].sum(1).mean() if loc else 0:11.2f} "
           f"{rows[glob].sum(1).mean() if glob else 0:12.2f}")
+    arr = arrivals(sess.last_trace(), cfg.n_layers)
+    print(f"\n{'stage':10s} {'wait':>7s} {'body':>7s} {'wg body':>8s}   local layers (us)"
+          f"   {'wait':>7s} {'body':>7s} {'wg body':>8s}   global layers")
+    for k, name in enumerate(STAGES):
+        lv = arr[loc, k].mean(0) if loc else np.full(3, np.nan)
+        gv = arr[glob, k].mean(0) if glob else np.full(3, np.nan)
+        print(f"{name:10s} {lv[0]:7.2f} {lv[1]:7.2f} {lv[2]:8.2f}   {'':13s}"
+              f"   {gv[0]:7.2f} {gv[1]:7.2f} {gv[2]:8.2f}")
     print(f"lm_head    {lm:11.2f}\nargmax     {am:11.2f}")
     sess.close()
     return 0
