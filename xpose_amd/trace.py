@@ -1,6 +1,6 @@
 """Stage timeline of the persistent token kernel.
 
-    python -m xpose_amd.trace [--ctx 4096] [--layers 26] [--seed S]
+    python -m xpose_amd.trace [--ctx 4096] [--layers 26] [--seed S] [--repeat N]
 
 Builds the seeded synthetic Gemma-3-1B model, pre-fills the KV cache to
 position ctx (fp16 N(0,1)), decodes a few warm-up tokens, then records one
@@ -10,7 +10,8 @@ finisher to this stage's last finisher (100 MHz s_memrealtime stamps). That
 increment is split into `wait` (previous stage's last finisher to the last
 workgroup's input arrival: the exchange latency plus producer skew) and
 `body` (last arrival to last finisher); `wg body` is the mean over working
-workgroups of their own arrival-to-finish time.
+workgroups of their own arrival-to-finish time. --repeat N records N
+consecutive tokens and reports the means (and the spread of the total).
 """
 from __future__ import annotations
 
@@ -66,6 +67,7 @@ def main() -> int:
     ap.add_argument("--ctx", type=int, default=4096)
     ap.add_argument("--layers", type=int, default=26)
     ap.add_argument("--seed", type=lambda s: int(s, 0), default=0x5EED0003)
+    ap.add_argument("--repeat", type=int, default=1)
     args = ap.parse_args()
     import xpose_amd as X
     X.init(0)
@@ -80,11 +82,20 @@ def main() -> int:
     sess.prefill([4242])
     sess.decode_steps(4)
     sess.trace(True)
-    sess.decode_steps(1)
-    rows, lm, am, total = timeline(sess.last_trace(), cfg.n_layers)
+    runs = []
+    for _ in range(max(1, args.repeat)):
+        sess.decode_steps(1)
+        tr = sess.last_trace()
+        runs.append((timeline(tr, cfg.n_layers), arrivals(tr, cfg.n_layers)))
+    rows = np.mean([r[0][0] for r in runs], axis=0)
+    lm = float(np.mean([r[0][1] for r in runs]))
+    am = float(np.mean([r[0][2] for r in runs]))
+    totals = np.array([r[0][3] for r in runs])
+    total = float(totals.mean())
     glob = [l for l in range(cfg.n_layers) if cfg.is_global(l)]
     loc = [l for l in range(cfg.n_layers) if not cfg.is_global(l)]
-    print(f"token at position {args.ctx + 5}: {total:.1f} us "
+    spread = f", min {totals.min():.1f} max {totals.max():.1f} over {len(runs)}" if len(runs) > 1 else ""
+    print(f"token at position {args.ctx + 5}: {total:.1f} us{spread} "
           f"({len(loc)} local + {len(glob)} global layers)")
     print(f"{'stage':10s} {'local mean':>11s} {'global mean':>12s}   (us added to the critical path)")
     for k, name in enumerate(STAGES):
@@ -93,7 +104,7 @@ def main() -> int:
         print(f"{name:10s} {lm_:11.2f} {gm_:12.2f}")
     print(f"{'per layer':10s} {rows[loc].sum(1).mean() if loc else 0:11.2f} "
           f"{rows[glob].sum(1).mean() if glob else 0:12.2f}")
-    arr = arrivals(sess.last_trace(), cfg.n_layers)
+    arr = np.mean([r[1] for r in runs], axis=0)
     print(f"\n{'stage':10s} {'wait':>7s} {'body':>7s} {'wg body':>8s}   local layers (us)"
           f"   {'wait':>7s} {'body':>7s} {'wg body':>8s}   global layers")
     for k, name in enumerate(STAGES):
