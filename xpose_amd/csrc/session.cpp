@@ -509,6 +509,24 @@ int setup_token(Session& s) {
     a.logits = s.logits;
     a.state = s.state;
     a.hist = s.hist;
+    // Workgroup placement: local layers keep attention and its combine on the
+    // XCD of workgroups grid - 1 - 8 s when every workgroup w sits on the XCD
+    // of w % 8 and workgroups 0..7 are on eight different XCDs. Anything else
+    // (or a failed probe) keeps every exchange device-coherent.
+    a.xcd_local = 0;
+    a.xcd_id = 0;
+    std::vector<uint32_t> xcc(grid);
+    if (grid >= 8 && probe_token_xcc(grid, s.st, xcc.data()) == XP_OK) {
+        bool periodic = true;
+        for (uint32_t w = 0; w < grid; ++w) periodic &= xcc[w] == xcc[w % 8];
+        for (uint32_t i = 0; i < 8; ++i)
+            for (uint32_t j = 0; j < i; ++j) periodic &= xcc[i] != xcc[j];
+        if (periodic) {
+            a.xcd_local = 1;
+            a.xcd_id = xcc[(grid - 1) % 8];
+        }
+    }
+    clear_error();
     s.tok_grid = grid;
     s.tag = 0;
     s.mode = XP_EXEC_TOKEN;

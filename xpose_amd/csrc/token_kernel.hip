@@ -146,6 +146,18 @@ __device__ __forceinline__ void ll_st2(rsrc_t r, uint32_t voff, uint32_t soff, f
     __builtin_amdgcn_raw_buffer_store_b128(u32x4{__float_as_uint(a), tag, __float_as_uint(b), tag},
                                            r, int(voff), int(soff), kAuxDev);
 }
+// The same store kept in the XCD's L2 (written back, not through): visible
+// to loads of any scope issued on the same XCD only.
+__device__ __forceinline__ void ll_st2_xcd(rsrc_t r, uint32_t voff, uint32_t soff, float a, float b,
+                                           uint32_t tag) {
+    __builtin_amdgcn_raw_buffer_store_b128(u32x4{__float_as_uint(a), tag, __float_as_uint(b), tag},
+                                           r, int(voff), int(soff), 0);
+}
+__device__ __forceinline__ uint32_t xcc_id() {
+    uint32_t x;
+    asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(x));
+    return x & 0xFu;
+}
 __device__ __forceinline__ void ll_st1(rsrc_t r, uint32_t voff, uint32_t soff, float a, uint32_t tag) {
     __builtin_amdgcn_raw_buffer_store_b64(u32x2{__float_as_uint(a), tag}, r, int(voff), int(soff),
                                           kAuxDev);
@@ -474,6 +486,9 @@ __global__ __launch_bounds__(kTkThreads) void token_kernel(TokArgs a) {
     const uint32_t t_qkv = wg, t_comb = wg, t_o = wg;
     const uint32_t t_gu = (wg + nwg - off_gu) % nwg, t_dn = wg;
     bool hown = tid < Sh::HO;                     // owns kOwn elements of a hidden vector
+    // This workgroup is on the XCD the host found workgroups grid - 1 - 8 s on
+    // (else its attention records go through the device coherence point).
+    const bool on_xcd = xcc_id() == a.xcd_id;
 
     // x entering layer l (l > 0) from layer l - 1's slots, in owner registers:
     // xb + post_ffw_norm(sum of the down chunks, in chunk order).
@@ -612,7 +627,14 @@ __global__ __launch_bounds__(kTkThreads) void token_kernel(TokArgs a) {
         const uint32_t kv0 = (glob || a.window == 0u || seq <= a.window) ? 0u : seq - a.window;
         const uint32_t span = seq - kv0;
         const uint32_t n_att = (span + kTkC - 1u) / kTkC;
-        const uint32_t s_att = nwg - 1u - wg;
+        // Local layers, when the XCD map was verified: chunk s on workgroup
+        // grid - 1 - 8 s and combine tile c on grid - 1 - 8 c, all on one XCD,
+        // so the chunk records cross that XCD's L2 only. Otherwise chunk s on
+        // grid - 1 - s and combine tile c on workgroup c.
+        const bool xl = a.xcd_local != 0u && !glob && n_att * 8u <= nwg && Sh::N_COMB * 8u <= nwg;
+        const uint32_t rx = nwg - 1u - wg;
+        const uint32_t s_att = !xl ? rx : (rx % 8u == 0u ? rx / 8u : ~0u);
+        const bool xl_st = xl && on_xcd;
         if (s_att < n_att) {
             const uint32_t j0 = s_att * kTkC;
             // score mapping: key jk = tid / 16; part p holds dims 64 c + 4 p .. + 3,
@@ -803,10 +825,16 @@ __global__ __launch_bounds__(kTkThreads) void token_kernel(TokArgs a) {
                 const float2 a1 = *reinterpret_cast<const float2*>(vr + hs);
                 const float2 a2 = *reinterpret_cast<const float2*>(vr + 2 * hs);
                 const float2 a3 = *reinterpret_cast<const float2*>(vr + 3 * hs);
-                ll_st2(rr, (pb + h * (2u + kTkHD) + 2u + d2) * 8u, soff, ((a0.x + a1.x) + a2.x) + a3.x,
-                       ((a0.y + a1.y) + a2.y) + a3.y, tag);
+                const uint32_t vo = (pb + h * (2u + kTkHD) + 2u + d2) * 8u;
+                const float r0 = ((a0.x + a1.x) + a2.x) + a3.x, r1 = ((a0.y + a1.y) + a2.y) + a3.y;
+                if (xl_st) ll_st2_xcd(rr, vo, soff, r0, r1, tag);
+                else ll_st2(rr, vo, soff, r0, r1, tag);
             }
-            if (tid < NH) ll_st2(rr, (pb + tid * (2u + kTkHD)) * 8u, soff, S.mh[tid], S.lh[tid], tag);
+            if (tid < NH) {
+                const uint32_t vo = (pb + tid * (2u + kTkHD)) * 8u;
+                if (xl_st) ll_st2_xcd(rr, vo, soff, S.mh[tid], S.lh[tid], tag);
+                else ll_st2(rr, vo, soff, S.mh[tid], S.lh[tid], tag);
+            }
             // the chunk holding the current position appends its key / value
             // to the caches for later tokens (after the results: stores)
             if (s_att == n_att - 1u && tid < kTkHD) {
@@ -819,7 +847,8 @@ __global__ __launch_bounds__(kTkThreads) void token_kernel(TokArgs a) {
         t_in = 0;
 
         // ================= combine =================
-        for (uint32_t c = t_comb; c < Sh::N_COMB; c += nwg) {
+        const uint32_t c0 = !xl ? t_comb : (rx % 8u == 0u ? rx / 8u : Sh::N_COMB);
+        for (uint32_t c = c0; c < Sh::N_COMB; c += nwg) {
             const uint32_t h = c / 4u, d0 = (c % 4u) * 64u;
             const uint32_t rstride = NH * (2u + kTkHD);
             const uint32_t base = uint32_t(lay.attp) + h * (2u + kTkHD);
@@ -849,7 +878,7 @@ __global__ __launch_bounds__(kTkThreads) void token_kernel(TokArgs a) {
                 }
             }
             __syncthreads();
-            if (c == t_comb) t_in = tk_now(a);
+            if (c == c0) t_in = tk_now(a);
             float m = -INFINITY;
             for (uint32_t s = tid; s < n_att; s += kTkThreads) m = fmaxf(m, S.big[s * 66u]);
             const float M = blk_max(m, RS());
@@ -1153,6 +1182,27 @@ int tok_supported(uint32_t n_layers, uint32_t hidden, uint32_t ffn, uint32_t n_h
     const TokLL lay = tok_ll_layout(hidden, ffn, n_heads, head_dim, uint32_t(n_cu));
     if ((uint64_t(n_layers) * lay.layer + 2u * uint64_t(n_cu)) * 8u >= (1ull << 31))
         return set_error(XP_E_ARG, "token kernel: exchange slots exceed 2 GiB");
+    return XP_OK;
+}
+
+// Each workgroup records the XCC (XCD) it runs on; launched exactly as the
+// token kernel is (threads, LDS, cooperative), so it sees the same placement.
+__global__ __launch_bounds__(kTkThreads) void xcc_probe_kernel(uint32_t* out) {
+    if (threadIdx.x == 0) out[blockIdx.x] = xcc_id();
+}
+
+int probe_token_xcc(uint32_t grid, hipStream_t st, uint32_t* out) {
+    const size_t lds = tok_lds_bytes();
+    const void* fn = reinterpret_cast<const void*>(&xcc_probe_kernel);
+    XP_HIP(hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, int(lds)));
+    uint32_t* d = nullptr;
+    XP_HIP(hipMalloc(&d, size_t(grid) * 4));
+    void* args[] = {&d};
+    hipError_t e = hipLaunchCooperativeKernel(fn, dim3(grid), dim3(kTkThreads), args, lds, st);
+    if (e == hipSuccess) e = hipMemcpyAsync(out, d, size_t(grid) * 4, hipMemcpyDeviceToHost, st);
+    if (e == hipSuccess) e = hipStreamSynchronize(st);
+    (void)hipFree(d);
+    if (e != hipSuccess) return set_error(XP_E_HIP, "token kernel: XCC probe -> %s", hipGetErrorString(e));
     return XP_OK;
 }
 

@@ -199,6 +199,12 @@ struct TokArgs {
     uint32_t tag;                         // this launch's tag (never 0)
     uint32_t want_logits;                 // 0: prefill pass without the lm_head
     uint32_t greedy;                      // 1: the argmax becomes the next token
+    // Non-zero when workgroups grid - 1, grid - 9, grid - 17, ... were found on
+    // one XCD (xcd_id, the hardware XCC id): local layers then run attention
+    // and its combine there and exchange their partials through that XCD's
+    // L2 instead of the device coherence point.
+    uint32_t xcd_local;
+    uint32_t xcd_id;
 };
 
 // The token kernel's down projection is split along k into chunks of this
@@ -245,5 +251,8 @@ int tok_supported(uint32_t n_layers, uint32_t hidden, uint32_t ffn, uint32_t n_h
                   uint32_t n_kv_heads, uint32_t head_dim, uint32_t vocab, uint32_t max_seq,
                   int fmt, int n_cu);
 int launch_token(const TokArgs& a, uint32_t grid, hipStream_t st);
+// The XCC id of every workgroup of a token-kernel-shaped launch of `grid`
+// workgroups (out: grid entries, host memory).
+int probe_token_xcc(uint32_t grid, hipStream_t st, uint32_t* out);
 
 }  // namespace xp
