@@ -509,12 +509,12 @@ int setup_token(Session& s) {
     a.logits = s.logits;
     a.state = s.state;
     a.hist = s.hist;
-    // Workgroup placement: local layers keep attention and its combine on the
-    // XCD of workgroups grid - 1 - 8 s when every workgroup w sits on the XCD
-    // of w % 8 and workgroups 0..7 are on eight different XCDs. Anything else
-    // (or a failed probe) keeps every exchange device-coherent.
+    // Workgroup placement: the kernel groups producers and consumers by XCD
+    // when every workgroup w sits on the XCD of w % 8 and workgroups 0..7 are
+    // on eight different XCDs. Anything else (or a failed probe) keeps every
+    // exchange device-coherent.
     a.xcd_local = 0;
-    a.xcd_id = 0;
+    a.xcd_ids = 0;
     std::vector<uint32_t> xcc(grid);
     if (grid >= 8 && probe_token_xcc(grid, s.st, xcc.data()) == XP_OK) {
         bool periodic = true;
@@ -523,7 +523,7 @@ int setup_token(Session& s) {
             for (uint32_t j = 0; j < i; ++j) periodic &= xcc[i] != xcc[j];
         if (periodic) {
             a.xcd_local = 1;
-            a.xcd_id = xcc[(grid - 1) % 8];
+            for (uint32_t r = 0; r < 8; ++r) a.xcd_ids |= (xcc[r] & 15u) << (4 * r);
         }
     }
     clear_error();

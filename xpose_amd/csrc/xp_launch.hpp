@@ -199,12 +199,12 @@ struct TokArgs {
     uint32_t tag;                         // this launch's tag (never 0)
     uint32_t want_logits;                 // 0: prefill pass without the lm_head
     uint32_t greedy;                      // 1: the argmax becomes the next token
-    // Non-zero when workgroups grid - 1, grid - 9, grid - 17, ... were found on
-    // one XCD (xcd_id, the hardware XCC id): local layers then run attention
-    // and its combine there and exchange their partials through that XCD's
-    // L2 instead of the device coherence point.
+    // Non-zero when every workgroup w was found on the XCD of w % 8, whose
+    // hardware XCC id is nibble w % 8 of xcd_ids: a local layer's attention
+    // and combine then run on one XCD (workgroups grid - 1 - 8 s) and
+    // exchange through its L2 instead of the device coherence point.
     uint32_t xcd_local;
-    uint32_t xcd_id;
+    uint32_t xcd_ids;
 };
 
 // The token kernel's down projection is split along k into chunks of this
