@@ -486,9 +486,9 @@ __global__ __launch_bounds__(kTkThreads) void token_kernel(TokArgs a) {
     const uint32_t t_qkv = wg, t_comb = wg, t_o = wg;
     const uint32_t t_gu = (wg + nwg - off_gu) % nwg, t_dn = wg;
     bool hown = tid < Sh::HO;                     // owns kOwn elements of a hidden vector
-    // This workgroup is on the XCD the host found workgroups grid - 1 - 8 s on
-    // (else its attention records go through the device coherence point).
-    const bool on_xcd = xcc_id() == a.xcd_id;
+    // This workgroup is on the XCD the host found its residue class on (else
+    // its XCD-local results go through the device coherence point).
+    const bool on_xcd = xcc_id() == ((a.xcd_ids >> (4u * (wg % 8u))) & 15u);
 
     // x entering layer l (l > 0) from layer l - 1's slots, in owner registers:
     // xb + post_ffw_norm(sum of the down chunks, in chunk order).
