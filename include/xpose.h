@@ -236,6 +236,53 @@ int xp_multinomial_strided(float* out, uint32_t* idx_out, const float* w, const 
                            const float* stats, uint32_t n, uint32_t nparts, float u,
                            xp_stream stream);
 
+/* ---- prefill shapes (kernels/llm_sampling.cl:496-736) ----------------------
+ * Row-indexed twins of the decode kernels, one entry per reference kernel,
+ * same arguments and layouts (row-major; q, scores and outputs
+ * [head][query][...]; fp32 caches [t][kv_head][head_dim]). Row reductions
+ * run one wave per row. */
+/* softmax_rows_stats (:527-547): stats[2r] = row max, stats[2r+1] = sum of
+ * exp(x - max); a row with no finite maximum gives (0, 1). */
+int xp_softmax_rows_stats(float* stats, const float* x, uint32_t n_rows, uint32_t n_cols,
+                          xp_stream stream);
+/* softmax_rows_apply (:549-556): x = exp(x - max) / sum, in place. */
+int xp_softmax_rows_apply(float* x, const float* stats, uint32_t n_rows, uint32_t n_cols,
+                          xp_stream stream);
+/* attention_scores_prefill (:574-600): scores[h][qi][t] = scale q.k, -inf
+ * where t > q_offset + qi (causal) or, window != 0, t + window <= q_offset +
+ * qi. q, kcache 16-byte aligned, head_dim % 4 == 0. */
+int xp_attention_scores_prefill(float* scores, const float* q, const float* kcache, uint32_t n_heads,
+                                uint32_t kv_heads, uint32_t head_dim, uint32_t n_query,
+                                uint32_t seq_len, uint32_t q_offset, uint32_t window, float scale,
+                                xp_stream stream);
+/* attention_apply_prefill (:605-627): out[h][qi][d] = sum_t probs[h][qi][t]
+ * v[t][kv_head(h)][d]. */
+int xp_attention_apply_prefill(float* out, const float* probs, const float* vcache, uint32_t n_heads,
+                               uint32_t kv_heads, uint32_t head_dim, uint32_t n_query,
+                               uint32_t seq_len, xp_stream stream);
+/* rmsnorm_rows_sumsq (:634-642) and rmsnorm_rows_apply_gemma (:645-656):
+ * out = in rsqrt(rowss / n + eps) (1 + w), w shared across rows. */
+int xp_rmsnorm_rows_sumsq(float* rowss, const float* in, uint32_t n_rows, uint32_t n,
+                          xp_stream stream);
+int xp_rmsnorm_rows_apply_gemma(float* out, const float* in, const float* w, const float* rowss,
+                                uint32_t n_rows, uint32_t n, float eps, xp_stream stream);
+/* rmsnorm_heads_rows_gemma (:659-672): per-head QK-norm over
+ * [token][head][head_dim]; out must not alias in. */
+int xp_rmsnorm_heads_rows_gemma(float* out, const float* in, const float* w, uint32_t n_tokens,
+                                uint32_t n_heads, uint32_t head_dim, float eps, xp_stream stream);
+/* rope_prefill (:687-708): rotate-half RoPE in place, token ti at position
+ * pos0 + ti. */
+int xp_rope_prefill(float* x, uint32_t n_tokens, uint32_t n_heads, uint32_t head_dim, uint32_t pos0,
+                    float theta, xp_stream stream);
+/* kv_append_rows (:714-721): cache[(pos0 + t) row + j] = src[t row + j]. */
+int xp_kv_append_rows(float* cache, const float* src, uint32_t n_tokens, uint32_t row, uint32_t pos0,
+                      xp_stream stream);
+/* embed_lookup_rows (:728-736): out[t][j] = table[tokens[t]][j]; `vocab`
+ * (an argument the reference does not take) bounds the ids: an id >= vocab
+ * gives a zero row. */
+int xp_embed_lookup_rows(float* out, const float* table, const uint32_t* tokens, uint32_t n_tokens,
+                         uint32_t n, uint32_t vocab, xp_stream stream);
+
 /* ---- synthetic inputs (host side, counter-based, any thread count) ------ */
 /* Philox4x32-10 (Salmon et al., SC'11): out = philox(ctr, key). */
 void xp_philox4x32_10(const uint32_t ctr[4], const uint32_t key[2], uint32_t out[4]);

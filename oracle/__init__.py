@@ -102,6 +102,16 @@ def lib() -> C.CDLL:
             "xo_quantise": (u32, [f32, f32]),
             "xo_best_bf16_scale": (f32, [F32P, f32]),
             "xo_rq_repack": (i32, [u32, vp, u32, u32, U32P, vp, F32P, vp]),
+            "xo_softmax_rows_stats": (None, [F32P, F32P, u32, u32]),
+            "xo_softmax_rows_apply": (None, [F32P, F32P, u32, u32]),
+            "xo_attention_scores_prefill": (None, [F32P, F32P, F32P, u32, u32, u32, u32, u32, u32, u32, f32]),
+            "xo_attention_apply_prefill": (None, [F32P, F32P, F32P, u32, u32, u32, u32, u32]),
+            "xo_rmsnorm_rows_sumsq": (None, [F32P, F32P, u32, u32]),
+            "xo_rmsnorm_rows_apply_gemma": (None, [F32P, F32P, F32P, F32P, u32, u32, f32]),
+            "xo_rmsnorm_heads_rows_gemma": (None, [F32P, F32P, F32P, u32, u32, u32, f32]),
+            "xo_rope_prefill": (None, [F32P, u32, u32, u32, u32, f32]),
+            "xo_kv_append_rows": (None, [F32P, F32P, u32, u32, u32]),
+            "xo_embed_lookup_rows": (None, [F32P, F32P, U32P, u32, u32]),
             "xo_rq_reconstruct": (f32, [u32, u32, U32P, vp, F32P, vp, u32, u32]),
             "xo_forward": (i32, [C.POINTER(Model), u32, u32, vp, i32]),
             "xo_generate_greedy": (i32, [C.POINTER(Model), U32P, u32, u32, U32P, i32]),

@@ -1261,3 +1261,161 @@ float xo_rq_reconstruct(uint32_t type, uint32_t nkb, const uint32_t* quant, cons
     }
     return scale[idx] * (float)q - bias[idx];
 }
+
+/* ------------------------------------------------------------------ */
+/* Prefill shapes (kernels/llm_sampling.cl:496-736), row-indexed twins  */
+/* ------------------------------------------------------------------ */
+
+/* softmax_rows_stats, llm_sampling.cl:527-547: per row max and sum of exp;
+ * a row with no finite maximum gives (0, 1). */
+void xo_softmax_rows_stats(float* stats, const float* x, uint32_t n_rows, uint32_t n_cols) {
+    uint32_t r, j;
+    for (r = 0; r < n_rows; ++r) {
+        const float* row = x + (size_t)r * n_cols;
+        float m = -INFINITY, s = 0.0f;
+        for (j = 0; j < n_cols; ++j) m = fmaxf(m, row[j]);
+        if (!isfinite(m)) {
+            stats[2 * r] = 0.0f;
+            stats[2 * r + 1] = 1.0f;
+            continue;
+        }
+        for (j = 0; j < n_cols; ++j) s += expf(row[j] - m);
+        stats[2 * r] = m;
+        stats[2 * r + 1] = s;
+    }
+}
+
+/* softmax_rows_apply, llm_sampling.cl:549-556. */
+void xo_softmax_rows_apply(float* x, const float* stats, uint32_t n_rows, uint32_t n_cols) {
+    size_t i;
+    for (i = 0; i < (size_t)n_rows * n_cols; ++i) {
+        const size_t r = i / n_cols;
+        x[i] = expf(x[i] - stats[2 * r]) / stats[2 * r + 1];
+    }
+}
+
+/* attention_scores_prefill, llm_sampling.cl:574-600: scores[h][qi][t],
+ * causal (t <= q_offset + qi) and, when window != 0, t + window > qpos;
+ * masked entries are -inf. */
+void xo_attention_scores_prefill(float* scores, const float* q, const float* kcache,
+                                 uint32_t n_heads, uint32_t kv_heads, uint32_t head_dim,
+                                 uint32_t n_query, uint32_t seq_len, uint32_t q_offset,
+                                 uint32_t window, float scale) {
+    const size_t total = (size_t)n_heads * n_query * seq_len;
+    const uint32_t group = n_heads / kv_heads;
+    size_t i;
+    for (i = 0; i < total; ++i) {
+        const uint32_t t = (uint32_t)(i % seq_len);
+        const uint32_t hq = (uint32_t)(i / seq_len);
+        const uint32_t qi = hq % n_query, h = hq / n_query;
+        const uint32_t qpos = q_offset + qi;
+        const size_t qb = ((size_t)h * n_query + qi) * head_dim;
+        const size_t kb = ((size_t)t * kv_heads + h / group) * head_dim;
+        float acc = 0.0f;
+        uint32_t d;
+        if (t > qpos || (window != 0u && t + window <= qpos)) {
+            scores[i] = -INFINITY;
+            continue;
+        }
+        for (d = 0; d < head_dim; ++d) acc += q[qb + d] * kcache[kb + d];
+        scores[i] = acc * scale;
+    }
+}
+
+/* attention_apply_prefill, llm_sampling.cl:605-627:
+ * out[h][qi][d] = sum_t probs[h][qi][t] v[t][kv_head(h)][d]. */
+void xo_attention_apply_prefill(float* out, const float* probs, const float* vcache,
+                                uint32_t n_heads, uint32_t kv_heads, uint32_t head_dim,
+                                uint32_t n_query, uint32_t seq_len) {
+    const size_t total = (size_t)n_heads * n_query * head_dim;
+    const uint32_t group = n_heads / kv_heads, vstride = kv_heads * head_dim;
+    size_t i;
+    for (i = 0; i < total; ++i) {
+        const uint32_t d = (uint32_t)(i % head_dim);
+        const uint32_t hq = (uint32_t)(i / head_dim);
+        const uint32_t qi = hq % n_query, h = hq / n_query;
+        const size_t pb = ((size_t)h * n_query + qi) * seq_len;
+        const uint32_t vb = (h / group) * head_dim + d;
+        float acc = 0.0f;
+        uint32_t t;
+        for (t = 0; t < seq_len; ++t) acc += probs[pb + t] * vcache[(size_t)t * vstride + vb];
+        out[i] = acc;
+    }
+}
+
+/* rmsnorm_rows_sumsq, llm_sampling.cl:634-642. */
+void xo_rmsnorm_rows_sumsq(float* rowss, const float* in, uint32_t n_rows, uint32_t n) {
+    uint32_t r, j;
+    for (r = 0; r < n_rows; ++r) {
+        float ss = 0.0f;
+        for (j = 0; j < n; ++j) {
+            const float v = in[(size_t)r * n + j];
+            ss += v * v;
+        }
+        rowss[r] = ss;
+    }
+}
+
+/* rmsnorm_rows_apply_gemma, llm_sampling.cl:645-656. */
+void xo_rmsnorm_rows_apply_gemma(float* out, const float* in, const float* w, const float* rowss,
+                                 uint32_t n_rows, uint32_t n, float eps) {
+    size_t i;
+    for (i = 0; i < (size_t)n_rows * n; ++i) {
+        const size_t r = i / n, j = i - r * n;
+        const float scale = rsqrt_ref(rowss[r] / (float)n + eps);
+        out[i] = in[i] * scale * (1.0f + w[j]);
+    }
+}
+
+/* rmsnorm_heads_rows_gemma, llm_sampling.cl:659-672: [token][head][head_dim]. */
+void xo_rmsnorm_heads_rows_gemma(float* out, const float* in, const float* w, uint32_t n_tokens,
+                                 uint32_t n_heads, uint32_t head_dim, float eps) {
+    const size_t total = (size_t)n_tokens * n_heads * head_dim;
+    size_t i;
+    for (i = 0; i < total; ++i) {
+        const uint32_t d = (uint32_t)(i % head_dim);
+        const size_t base = (i / head_dim) * head_dim;
+        float ss = 0.0f;
+        uint32_t j;
+        for (j = 0; j < head_dim; ++j) {
+            const float v = in[base + j];
+            ss += v * v;
+        }
+        out[i] = in[i] * rsqrt_ref(ss / (float)head_dim + eps) * (1.0f + w[d]);
+    }
+}
+
+/* rope_prefill, llm_sampling.cl:687-708: rotate-half, token ti at pos0 + ti. */
+void xo_rope_prefill(float* x, uint32_t n_tokens, uint32_t n_heads, uint32_t head_dim,
+                     uint32_t pos0, float theta) {
+    const uint32_t hdhalf = head_dim / 2u;
+    const size_t total = (size_t)n_tokens * n_heads * hdhalf;
+    size_t i;
+    for (i = 0; i < total; ++i) {
+        const uint32_t d = (uint32_t)(i % hdhalf);
+        const size_t th = i / hdhalf;
+        const uint32_t ti = (uint32_t)(th / n_heads);
+        const size_t base = th * head_dim + d;
+        const float frac = (float)(2u * d) / (float)head_dim;
+        const float inv = exp2f(-log2f(theta) * frac);
+        const float ang = (float)(pos0 + ti) * inv;
+        const float c = cosf(ang), s = sinf(ang);
+        const float a = x[base], b = x[base + hdhalf];
+        x[base] = a * c - b * s;
+        x[base + hdhalf] = b * c + a * s;
+    }
+}
+
+/* kv_append_rows, llm_sampling.cl:714-721 (fp32 cache [t][row]). */
+void xo_kv_append_rows(float* cache, const float* src, uint32_t n_tokens, uint32_t row,
+                       uint32_t pos0) {
+    memcpy(cache + (size_t)pos0 * row, src, (size_t)n_tokens * row * 4);
+}
+
+/* embed_lookup_rows, llm_sampling.cl:728-736. */
+void xo_embed_lookup_rows(float* out, const float* table, const uint32_t* tokens,
+                          uint32_t n_tokens, uint32_t n) {
+    uint32_t t;
+    for (t = 0; t < n_tokens; ++t)
+        memcpy(out + (size_t)t * n, table + (size_t)tokens[t] * n, (size_t)n * 4);
+}

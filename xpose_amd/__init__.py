@@ -182,6 +182,16 @@ def _declare(lib: C.CDLL) -> None:
         "xp_gguf_meta_string": (i32, [vp, C.c_char_p, C.c_char_p, sz, P(sz)]),
         "xp_gguf_meta_array_length": (i32, [vp, C.c_char_p, P(C.c_uint64)]),
         "xp_dequantize": (i32, [u32, vp, vp, C.c_uint64]),
+        "xp_softmax_rows_stats": (i32, [vp, vp, u32, u32, vp]),
+        "xp_softmax_rows_apply": (i32, [vp, vp, u32, u32, vp]),
+        "xp_attention_scores_prefill": (i32, [vp, vp, vp, u32, u32, u32, u32, u32, u32, u32, f32, vp]),
+        "xp_attention_apply_prefill": (i32, [vp, vp, vp, u32, u32, u32, u32, u32, vp]),
+        "xp_rmsnorm_rows_sumsq": (i32, [vp, vp, u32, u32, vp]),
+        "xp_rmsnorm_rows_apply_gemma": (i32, [vp, vp, vp, vp, u32, u32, f32, vp]),
+        "xp_rmsnorm_heads_rows_gemma": (i32, [vp, vp, vp, u32, u32, u32, f32, vp]),
+        "xp_rope_prefill": (i32, [vp, u32, u32, u32, u32, f32, vp]),
+        "xp_kv_append_rows": (i32, [vp, vp, u32, u32, u32, vp]),
+        "xp_embed_lookup_rows": (i32, [vp, vp, vp, u32, u32, u32, vp]),
         "xp_rq_layout_of": (i32, [u32, u32, u32, P(RqLayout)]),
         "xp_rq_repack": (i32, [P(RqLayout), vp, u32, vp, vp, vp, vp]),
         "xp_rq_reconstruct": (i32, [P(RqLayout), vp, vp, vp, vp, vp]),

@@ -18,16 +18,6 @@ namespace xp {
 // theta^(-2d/head_dim) for d < head_dim/2, evaluated on the host with the
 // reference's formula exp2(-log2(theta) * frac) (llm_transformer.cl:168-169),
 // passed by value so a captured launch replays it unchanged.
-struct RopeFreq {
-    float inv[kMaxHeadDim / 2];
-};
-
-static void rope_freq(RopeFreq& f, uint32_t head_dim, float theta) {
-    for (uint32_t d = 0; d < head_dim / 2; ++d) {
-        const float frac = float(2u * d) / float(head_dim);
-        f.inv[d] = std::exp2f(-std::log2f(theta) * frac);
-    }
-}
 
 // Block-wide sum for blockDim.x <= 1024, result broadcast to every thread.
 __device__ __forceinline__ float block_sum(float v, float* red) {

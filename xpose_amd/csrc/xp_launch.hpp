@@ -3,12 +3,27 @@
 // a captured token step allocates.
 #pragma once
 
+#include <cmath>
+
 #include "xp_internal.hpp"
 
 namespace xp {
 
 constexpr int kMvMaxMats = 4;
 constexpr int kMaxHeadDim = 512;
+
+// RoPE inverse frequencies theta^(-2d / head_dim), formed on the host
+// (exp2(-log2(theta) 2d / head_dim), llm_transformer.cl:158-179) and passed
+// by value, so every RoPE kernel rotates by the same angles.
+struct RopeFreq {
+    float inv[kMaxHeadDim / 2];
+};
+inline void rope_freq(RopeFreq& f, uint32_t head_dim, float theta) {
+    for (uint32_t d = 0; d < head_dim / 2; ++d) {
+        const float frac = float(2u * d) / float(head_dim);
+        f.inv[d] = std::exp2f(-std::log2f(theta) * frac);
+    }
+}
 
 // ---- int4 matvec ----
 struct MvMatDesc {
