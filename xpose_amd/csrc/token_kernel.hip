@@ -483,7 +483,23 @@ __global__ __launch_bounds__(kTkThreads) void token_kernel(TokArgs a) {
     // starts past the O workgroups, whose O tile would otherwise delay their
     // gate/up weight prefetch; attention runs from the last workgroup down.
     const uint32_t off_gu = Sh::N_O % nwg;
-    const uint32_t t_qkv = wg, t_comb = wg, t_o = wg;
+    const uint32_t t_comb = wg, t_o = wg;
+    // QKV tiles run on workgroups past the down tiles' (from N_DN on, skipping
+    // those of residue 7 mod 8, the local attention's XCD), when the grid has
+    // room: a workgroup with both a down and a QKV tile would request its QKV
+    // weights ahead of one of the two waits, and memory requests complete in
+    // order. Otherwise tile t on workgroup t.
+    uint32_t t_qkv = wg, qkv_above = 0u;
+    const bool qsep = Sh::N_DN + (Sh::N_QKV * 8u + 6u) / 7u + 8u <= nwg;
+    if (qsep) {
+        // rank of wg among the workgroups >= b whose residue is not 7 (the
+        // residue-7 workgroups below x number x / 8)
+        const uint32_t b = Sh::N_DN;
+        auto rank = [&](uint32_t x) { return (x - b) - (x / 8u - b / 8u); };
+        t_qkv = (wg < b || wg % 8u == 7u) ? Sh::N_QKV : rank(wg);
+        // QKV workgroups above this one (ranks rank(wg + 1) .. N_QKV - 1)
+        qkv_above = wg + 1u <= b ? Sh::N_QKV : Sh::N_QKV - min(Sh::N_QKV, rank(wg + 1u));
+    }
     const uint32_t t_gu = (wg + nwg - off_gu) % nwg, t_dn = wg;
     bool hown = tid < Sh::HO;                     // owns kOwn elements of a hidden vector
     // This workgroup is on the XCD the host found its residue class on (else
@@ -630,10 +646,15 @@ __global__ __launch_bounds__(kTkThreads) void token_kernel(TokArgs a) {
         // Local layers, when the XCD map was verified: chunk s on workgroup
         // grid - 1 - 8 s and combine tile c on grid - 1 - 8 c, all on one XCD,
         // so the chunk records cross that XCD's L2 only. Otherwise chunk s on
-        // grid - 1 - s and combine tile c on workgroup c.
+        // the s-th workgroup from the last down that has no QKV tile (a QKV
+        // workgroup would issue its chunk's key / value loads only after its
+        // tile, ahead of its wait for q | k | v), or on grid - 1 - s when the
+        // grid has too few of those; combine tile c on workgroup c.
         const bool xl = a.xcd_local != 0u && !glob && n_att * 8u <= nwg && Sh::N_COMB * 8u <= nwg;
         const uint32_t rx = nwg - 1u - wg;
-        const uint32_t s_att = !xl ? rx : (rx % 8u == 0u ? rx / 8u : ~0u);
+        const bool ask = qsep && n_att + Sh::N_QKV <= nwg;
+        const uint32_t s_att = xl ? (rx % 8u == 0u ? rx / 8u : ~0u)
+                                  : !ask ? rx : (t_qkv < Sh::N_QKV ? ~0u : rx - qkv_above);
         const bool xl_st = xl && on_xcd;
         if (s_att < n_att) {
             const uint32_t j0 = s_att * kTkC;
