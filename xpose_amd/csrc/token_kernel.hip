@@ -642,42 +642,52 @@ __global__ __launch_bounds__(kTkThreads) void token_kernel(TokArgs a) {
         const bool glob = L.global != 0u;
         const uint32_t kv0 = (glob || a.window == 0u || seq <= a.window) ? 0u : seq - a.window;
         const uint32_t span = seq - kv0;
-        const uint32_t n_att = (span + kTkC - 1u) / kTkC;
         // Local layers, when the XCD map was verified: chunk s on workgroup
         // grid - 1 - 8 s and combine tile c on grid - 1 - 8 c, all on one XCD,
-        // so the chunk records cross that XCD's L2 only. Otherwise chunk s on
+        // so the chunk records cross that XCD's L2 only; the chunks hold 16
+        // keys when that XCD has a workgroup for each (half the score and
+        // value work per workgroup), else kTkC. Otherwise chunk s on
         // the s-th workgroup from the last down that has no QKV tile (a QKV
         // workgroup would issue its chunk's key / value loads only after its
         // tile, ahead of its wait for q | k | v), or on grid - 1 - s when the
         // grid has too few of those; combine tile c on workgroup c.
-        const bool xl = a.xcd_local != 0u && !glob && n_att * 8u <= nwg && Sh::N_COMB * 8u <= nwg;
+        const bool xl_ok = a.xcd_local != 0u && !glob && Sh::N_COMB * 8u <= nwg;
+        const uint32_t cw = xl_ok && (span + 15u) / 16u * 8u <= nwg ? 16u : kTkC;
+        const uint32_t n_att = (span + cw - 1u) / cw;
+        const bool xl = xl_ok && n_att * 8u <= nwg;
         const uint32_t rx = nwg - 1u - wg;
         const bool ask = qsep && n_att + Sh::N_QKV <= nwg;
         const uint32_t s_att = xl ? (rx % 8u == 0u ? rx / 8u : ~0u)
                                   : !ask ? rx : (t_qkv < Sh::N_QKV ? ~0u : rx - qkv_above);
         const bool xl_st = xl && on_xcd;
-        if (s_att < n_att) {
-            const uint32_t j0 = s_att * kTkC;
-            // score mapping: key jk = tid / 16; part p holds dims 64 c + 4 p .. + 3,
-            // c < 4 (the 16 parts of a key read 16 consecutive float4 of q: no
-            // LDS bank conflicts)
-            const uint32_t jk = tid / 16u, part = tid % 16u;
-            // value mapping: dims 2*dp, 2*dp+1 of keys kgv*8 .. kgv*8+7
+        // one chunk of CW keys (CW = 16 or kTkC)
+        auto attend = [&](auto cw_c) {
+            constexpr uint32_t CW = decltype(cw_c)::value;
+            constexpr uint32_t TPK = kTkThreads / CW;        // threads per key (scores)
+            constexpr uint32_t NCK = kTkHD / (4u * TPK);      // float4 of a key per thread
+            constexpr uint32_t KPG = CW / (kTkThreads / 128u); // keys per value group
+            static_assert(TPK == 16u || TPK == 32u, "a key's parts span one or two DPP rows");
+            const uint32_t j0 = s_att * CW;
+            // score mapping: key jk = tid / TPK; part p holds dims 4 TPK c + 4 p .. + 3,
+            // c < NCK (the parts of a key read consecutive float4 of q: no LDS
+            // bank conflicts)
+            const uint32_t jk = tid / TPK, part = tid % TPK;
+            // value mapping: dims 2*dp, 2*dp+1 of keys kgv*KPG .. kgv*KPG+KPG-1
             const uint32_t dp = tid % 128u, kgv = tid / 128u;
-            u32x2 kr[4];
-            uint32_t vw[8];
+            u32x2 kr[NCK];
+            uint32_t vw[KPG];
 #pragma unroll
-            for (int c = 0; c < 4; ++c) kr[c] = u32x2{0u, 0u};
+            for (uint32_t c = 0; c < NCK; ++c) kr[c] = u32x2{0u, 0u};
 #pragma unroll
-            for (int i = 0; i < 8; ++i) vw[i] = 0u;
+            for (uint32_t i = 0; i < KPG; ++i) vw[i] = 0u;
             if (j0 + jk < span) {
                 const uint16_t* kp = L.kc + size_t(kv0 + j0 + jk) * kTkHD + 4u * part;
 #pragma unroll
-                for (int c = 0; c < 4; ++c) kr[c] = *(const XP_GLOBAL u32x2*)(kp + 64 * c);
+                for (uint32_t c = 0; c < NCK; ++c) kr[c] = *(const XP_GLOBAL u32x2*)(kp + 4u * TPK * c);
             }
 #pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                const uint32_t jj = j0 + kgv * 8u + i;
+            for (uint32_t i = 0; i < KPG; ++i) {
+                const uint32_t jj = j0 + kgv * KPG + i;
                 if (jj < span) vw[i] = ldg32(L.vc + size_t(kv0 + jj) * kTkHD + 2u * dp);
             }
             // QK-norm weights of this wave's head (waves 0..NH-1: q heads, NH: the kv head)
@@ -757,10 +767,10 @@ __global__ __launch_bounds__(kTkThreads) void token_kernel(TokArgs a) {
                 const uint32_t jj = j0 + jk;
                 const bool valid = jj < span;
                 const bool cur = kv0 + jj == pos;
-                float kf[16];
+                float kf[4 * NCK];
 #pragma unroll
-                for (int c = 0; c < 4; ++c) {
-                    const float4 kc = *reinterpret_cast<const float4*>(&S.kn[64 * c + 4u * part]);
+                for (uint32_t c = 0; c < NCK; ++c) {
+                    const float4 kc = *reinterpret_cast<const float4*>(&S.kn[4u * TPK * c + 4u * part]);
                     kf[4 * c + 0] = cur ? kc.x : f16_bits_to_f32(kr[c].x);
                     kf[4 * c + 1] = cur ? kc.y : f16_bits_to_f32(kr[c].x >> 16);
                     kf[4 * c + 2] = cur ? kc.z : f16_bits_to_f32(kr[c].y);
@@ -771,8 +781,8 @@ __global__ __launch_bounds__(kTkThreads) void token_kernel(TokArgs a) {
                 for (uint32_t h = 0; h < NH; ++h) {
                     float acc = 0.0f;
 #pragma unroll
-                    for (int c = 0; c < 4; ++c) {
-                        const float4 q = *reinterpret_cast<const float4*>(&S.qh[h][64 * c + 4u * part]);
+                    for (uint32_t c = 0; c < NCK; ++c) {
+                        const float4 q = *reinterpret_cast<const float4*>(&S.qh[h][4u * TPK * c + 4u * part]);
                         acc = fmaf(q.x, kf[4 * c + 0], acc);
                         acc = fmaf(q.y, kf[4 * c + 1], acc);
                         acc = fmaf(q.z, kf[4 * c + 2], acc);
@@ -780,8 +790,13 @@ __global__ __launch_bounds__(kTkThreads) void token_kernel(TokArgs a) {
                     }
                     d[h] = acc;
                 }
+                // key jk's lanes: one DPP row (TPK 16), or two (TPK 32: rows 2 r, 2 r + 1)
 #pragma unroll
-                for (uint32_t h = 0; h < NH; ++h) d[h] = row16_sum(d[h]);   // key jk's 16 lanes = one DPP row
+                for (uint32_t h = 0; h < NH; ++h) {
+                    d[h] = row16_sum(d[h]);
+                    if constexpr (TPK == 32u)
+                        d[h] += __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(d[h]), 0x401F));
+                }
                 if (part == 0) {
 #pragma unroll
                     for (uint32_t h = 0; h < NH; ++h) S.sc[jk][h] = valid ? d[h] * a.attn_scale : -INFINITY;
@@ -791,12 +806,12 @@ __global__ __launch_bounds__(kTkThreads) void token_kernel(TokArgs a) {
             // chunk softmax, one wave per head
             if (wave < NH) {
                 const uint32_t h = wave;
-                const float v = S.sc[lane % kTkC][h];
-                const bool in = lane < kTkC && v != -INFINITY;
+                const float v = S.sc[lane % CW][h];
+                const bool in = lane < CW && v != -INFINITY;
                 const float m = wave_max(in ? v : -INFINITY);
                 const float e = in ? expf(v - m) : 0.0f;
                 const float l2 = wave_sum(e);
-                if (lane < kTkC) S.sc[lane][h] = e;
+                if (lane < CW) S.sc[lane][h] = e;
                 if (lane == 0) { S.mh[h] = m; S.lh[h] = l2; }
             }
             __syncthreads();
@@ -807,8 +822,8 @@ __global__ __launch_bounds__(kTkThreads) void token_kernel(TokArgs a) {
 #pragma unroll
                 for (uint32_t h = 0; h < NH; ++h) o0[h] = o1[h] = 0.0f;
 #pragma unroll
-                for (int i = 0; i < 8; ++i) {
-                    const uint32_t jl = kgv * 8u + i;
+                for (uint32_t i = 0; i < KPG; ++i) {
+                    const uint32_t jl = kgv * KPG + i;
                     const bool cur = kv0 + j0 + jl == pos;
                     const float v0 = cur ? vc.x : f16_bits_to_f32(vw[i]);
                     const float v1 = cur ? vc.y : f16_bits_to_f32(vw[i] >> 16);
@@ -863,6 +878,10 @@ __global__ __launch_bounds__(kTkThreads) void token_kernel(TokArgs a) {
                 stg16(L.vc + size_t(pos) * kTkHD + tid, f32_to_f16_bits(S.vn[tid]));
             }
             __syncthreads();
+        };
+        if (s_att < n_att) {
+            if (cw == 16u) attend(std::integral_constant<uint32_t, 16u>{});
+            else attend(std::integral_constant<uint32_t, kTkC>{});
         }
         tk_trace_stage(a, l, 1u, t_in);
         t_in = 0;
