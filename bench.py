@@ -45,7 +45,7 @@ HBM_PEAK_GBS = 8000.0          # MI355X HBM3E
 # Measured HBM bytes of one token-kernel launch at this workload: rocprofv3
 # FETCH_SIZE x 2.0 + WRITE_SIZE x 1.0 (factors from a 256 MiB copy), see
 # profiles/token_kernel_gemma3_1b_ctx4096.md.
-TOKEN_TRAFFIC_BYTES = 680_802_980 + 15_191_104
+TOKEN_TRAFFIC_BYTES = 692_586_812 + 18_097_216
 SEED = 0x5EED0003
 # Algorithmic HBM bytes of one token at seq_len s (weights + fp16 scales,
 # KV reads, norm weights, logits write + argmax read, KV append).
