@@ -342,9 +342,18 @@ typedef struct {
      * session's own path) or XP_PREFILL_TOKENS (one token step per token,
      * the reference's decode-shaped prefill, decode.cpp:1785-1815). */
     int32_t  prefill_mode;
+    /* Where the persistent token kernel runs its exchanges: XP_PLACE_AUTO
+     * (local layers keep attention, its chunk records and their combine on
+     * one XCD, exchanging through that XCD's L2, when the session's probe
+     * launch finds workgroup w on the XCD of w % 8; otherwise as
+     * XP_PLACE_DEVICE) or XP_PLACE_DEVICE (every exchange through the device
+     * coherence point, 32-key attention chunks). Results agree within
+     * rounding; this build's own choice, no reference counterpart. */
+    int32_t  placement;
 } xp_config;
 
 enum xp_prefill_mode { XP_PREFILL_AUTO = 0, XP_PREFILL_TOKENS = 1 };
+enum xp_placement { XP_PLACE_AUTO = 0, XP_PLACE_DEVICE = 1 };
 
 enum xp_exec_mode {
     XP_EXEC_AUTO = 0, XP_EXEC_GRAPH = 1, XP_EXEC_LAUNCH = 2, XP_EXEC_TOKEN = 3

@@ -254,7 +254,22 @@ def test_gpu_full_model_deep_context_cfg4(xp, xo, mode):
     local layers the last 512)."""
     X = xp
     print("case session full model cfg4", flush=True)
-    cfg = X.XpConfig.gemma3_1b(max_seq=4160, exec_mode=mode)
+    deep_context_check(X, xo, X.XpConfig.gemma3_1b(max_seq=4160, exec_mode=mode))
+
+
+@pytest.mark.gpu
+def test_gpu_token_device_placement_cfg4(xp, xo):
+    """Config 4 on the token kernel with XP_PLACE_DEVICE: every exchange
+    through the device coherence point and 32-key attention chunks in the
+    local layers, the path a device whose workgroup placement the session's
+    probe cannot verify takes."""
+    X = xp
+    print("case session token device placement cfg4", flush=True)
+    deep_context_check(X, xo, X.XpConfig.gemma3_1b(max_seq=4160, exec_mode=X.XP_EXEC_TOKEN,
+                                                     placement=X.XP_PLACE_DEVICE))
+
+
+def deep_context_check(X, xo, cfg):
     sess, model = make_pair(X, xo, cfg)
     kvd = cfg.n_kv_heads * cfg.head_dim
     for l in range(cfg.n_layers):
@@ -334,6 +349,9 @@ def test_gpu_session_error_paths(xp):
     with pytest.raises(X.XposeError) as e:
         s.decode_step()
     assert "full" in str(e.value)
+    with pytest.raises(X.XposeError) as e:
+        X.DecodeSession(cfg_small(X, n_layers=1, max_seq=16, placement=7))
+    assert "placement" in str(e.value)
 
 
 @pytest.mark.gpu

@@ -22,6 +22,7 @@ XP_SCALE_F32 = 2
 
 XP_EXEC_AUTO, XP_EXEC_GRAPH, XP_EXEC_LAUNCH, XP_EXEC_TOKEN = 0, 1, 2, 3
 XP_PREFILL_AUTO, XP_PREFILL_TOKENS = 0, 1
+XP_PLACE_AUTO, XP_PLACE_DEVICE = 0, 1
 
 _lib = None
 
@@ -44,7 +45,7 @@ class XpConfig(C.Structure):
                [("scale_fmt", C.c_int32), ("sample_mode", C.c_int32),
                 ("temperature", C.c_float), ("top_k", C.c_uint32), ("top_p", C.c_float),
                 ("seed", C.c_uint32), ("seq_id", C.c_uint32), ("topk_parts", C.c_uint32),
-                ("exec_mode", C.c_int32), ("prefill_mode", C.c_int32)]
+                ("exec_mode", C.c_int32), ("prefill_mode", C.c_int32), ("placement", C.c_int32)]
 
     @classmethod
     def gemma3_1b(cls, **overrides) -> "XpConfig":

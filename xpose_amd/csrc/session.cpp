@@ -511,12 +511,12 @@ int setup_token(Session& s) {
     a.hist = s.hist;
     // Workgroup placement: the kernel groups producers and consumers by XCD
     // when every workgroup w sits on the XCD of w % 8 and workgroups 0..7 are
-    // on eight different XCDs. Anything else (or a failed probe) keeps every
-    // exchange device-coherent.
+    // on eight different XCDs. Anything else (a failed probe, or
+    // XP_PLACE_DEVICE) keeps every exchange device-coherent.
     a.xcd_local = 0;
     a.xcd_ids = 0;
     std::vector<uint32_t> xcc(grid);
-    if (grid >= 8 && probe_token_xcc(grid, s.st, xcc.data()) == XP_OK) {
+    if (c.placement == XP_PLACE_AUTO && grid >= 8 && probe_token_xcc(grid, s.st, xcc.data()) == XP_OK) {
         bool periodic = true;
         for (uint32_t w = 0; w < grid; ++w) periodic &= xcc[w] == xcc[w % 8];
         for (uint32_t i = 0; i < 8; ++i)
@@ -646,6 +646,10 @@ int xp_session_create(const xp_config* cfg, xp_session** out) {
     if (c.exec_mode < XP_EXEC_AUTO || c.exec_mode > XP_EXEC_TOKEN) {
         delete h;
         return set_error(XP_E_ARG, "config: unknown exec_mode %d", c.exec_mode);
+    }
+    if (c.placement != XP_PLACE_AUTO && c.placement != XP_PLACE_DEVICE) {
+        delete h;
+        return set_error(XP_E_ARG, "config: unknown placement %d", c.placement);
     }
     try {
         int dev = 0;
