@@ -235,6 +235,74 @@ void mv_int4_kernel(MvArgs a) {
     if (lane == 0) st_dev(&a.tickets[gg], 0u);
 }
 
+// Wide, shallow shapes (config 1: 108 column groups over 9 quads of k): one
+// workgroup per column group, its eight waves splitting k (wave w takes quads
+// w and w + 8) and meeting in LDS, summed in wave order. Every weight load is
+// issued before the activations are staged, and no partial buffer or ticket
+// is needed: one HBM round trip instead of three. Quad scale planes only.
+constexpr int kMvWgWaves = 8;
+constexpr int kMvWgQuads = 2;   // quads per wave: nquads <= 16
+
+template <int FMT>
+__global__ __launch_bounds__(kMvWgWaves * kWave) void mv_int4_wg_kernel(MvArgs a) {
+    extern __shared__ QxBlock smem_qx[];
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+    const uint32_t lane = threadIdx.x % kWave;
+    const uint32_t gg = blockIdx.x;
+    QxBlock* qx = smem_qx;
+    float* sx = reinterpret_cast<float*>(smem_qx + a.nblk);
+    float* red = sx + a.nblk;   // [kMvWgWaves][64]
+    uint32_t mi = 0;
+#pragma unroll
+    for (int i = 1; i < kMvMaxMats; ++i)
+        if (uint32_t(i) < a.n_mats && gg >= a.m[i].grp0) mi = uint32_t(i);
+    float*       out = a.m[0].out;
+    const u32x4* wq  = a.m[0].wq;
+    const void*  sc  = a.m[0].sc;
+    uint32_t cols = a.m[0].cols, grp0 = 0;
+#pragma unroll
+    for (int i = 1; i < kMvMaxMats; ++i) {
+        if (uint32_t(i) == mi) {
+            out = a.m[i].out; wq = a.m[i].wq; sc = a.m[i].sc; cols = a.m[i].cols; grp0 = a.m[i].grp0;
+        }
+    }
+    const uint32_t gl = gg - grp0, j = gl * kGrp + lane;
+    const u32x4* wp = wq + size_t(gl) * a.nblk * kGrp + lane;
+    u32x4 w[kMvWgQuads][4];
+    QuadScales<FMT> qs[kMvWgQuads];
+#pragma unroll
+    for (int r = 0; r < kMvWgQuads; ++r) {
+        const uint32_t b = 4u * min(wave + uint32_t(kMvWgWaves) * r, a.nquads - 1u);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) w[r][i] = ld_stream4(wp + size_t(b + i) * kGrp);
+        qs[r].load(sc, cols, j, b);
+    }
+    const float4* x4 = reinterpret_cast<const float4*>(a.x);
+    for (uint32_t i = threadIdx.x; i < a.nblk * 4u; i += blockDim.x)
+        stage_x8(qx, sx, i, x4[2 * i], x4[2 * i + 1]);
+    __syncthreads();
+    float acc = 0.0f;
+#pragma unroll
+    for (int r = 0; r < kMvWgQuads; ++r) {
+        const uint32_t q = wave + uint32_t(kMvWgWaves) * r;
+        if (q < a.nquads) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const uint32_t lb = 4u * q + i;
+                acc = fmaf(qs[r].get(i) * sx[lb], float(block_dot(w[r][i], qx[lb])), acc);
+            }
+        }
+    }
+    red[wave * kGrp + lane] = acc;
+    __syncthreads();
+    if (wave == 0) {
+        float y = 0.0f;
+#pragma unroll
+        for (int v = 0; v < kMvWgWaves; ++v) y += red[v * kGrp + lane];
+        out[j] = y;
+    }
+}
+
 __global__ void unpack_km4_kernel(int8_t* out, const u32x4* wq, uint32_t rows, uint32_t cols) {
     const uint32_t j = blockIdx.x * blockDim.x + threadIdx.x;   // column
     const uint32_t b = blockIdx.y;                              // block
@@ -329,8 +397,25 @@ int launch_mv(const MvMatDesc* mats, uint32_t n, const float* x, int fmt, uint32
     a.x = x;
     a.nblk = nblk;
     a.nquads = (nblk + 3) / 4;
-    split_plan(groups, a.nquads, split, n_cu, a.split, a.qpc);
     a.groups = groups;
+    // Automatic plan for a shape wide enough to fill the GPU with one
+    // workgroup per column group and shallow enough for two quads per wave:
+    // the workgroup kernel instead of split-k.
+    if (split == 0 && fmt != XP_SCALE_F32 && groups >= 64 &&
+        a.nquads <= uint32_t(kMvWgWaves * kMvWgQuads) && choose_split(groups, a.nquads, n_cu) > 1) {
+        const size_t lds = size_t(nblk) * (sizeof(QxBlock) + sizeof(float)) +
+                           size_t(kMvWgWaves) * kGrp * sizeof(float);
+        if (fmt == XP_SCALE_F16_QUAD)
+            hipLaunchKernelGGL((mv_int4_wg_kernel<XP_SCALE_F16_QUAD>), dim3(groups),
+                               dim3(kMvWgWaves * kWave), lds, st, a);
+        else
+            hipLaunchKernelGGL((mv_int4_wg_kernel<XP_SCALE_BF16_QUAD>), dim3(groups),
+                               dim3(kMvWgWaves * kWave), lds, st, a);
+        hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return set_error(XP_E_HIP, "%s: launch -> %s", who, hipGetErrorString(e));
+        return XP_OK;
+    }
+    split_plan(groups, a.nquads, split, n_cu, a.split, a.qpc);
     a.wg_per_chunk = (groups + kMvWaves - 1) / kMvWaves;
     if (a.split > 1) {
         const size_t need = size_t(a.split) * groups * kGrp;
