@@ -268,6 +268,15 @@ __global__ __launch_bounds__(kMvWgWaves * kWave) void mv_int4_wg_kernel(MvArgs a
     }
     const uint32_t gl = gg - grp0, j = gl * kGrp + lane;
     const u32x4* wp = wq + size_t(gl) * a.nblk * kGrp + lane;
+    // The activations (at most 64 blocks: one staging task per thread) are
+    // loaded ahead of the weights, so that staging them waits for them only.
+    const float4* x4 = reinterpret_cast<const float4*>(a.x);
+    const bool stager = threadIdx.x < a.nblk * 4u;
+    float4 xv0 = {0.0f, 0.0f, 0.0f, 0.0f}, xv1 = xv0;
+    if (stager) {
+        xv0 = x4[2 * threadIdx.x];
+        xv1 = x4[2 * threadIdx.x + 1];
+    }
     u32x4 w[kMvWgQuads][4];
     QuadScales<FMT> qs[kMvWgQuads];
 #pragma unroll
@@ -277,9 +286,7 @@ __global__ __launch_bounds__(kMvWgWaves * kWave) void mv_int4_wg_kernel(MvArgs a
         for (int i = 0; i < 4; ++i) w[r][i] = ld_stream4(wp + size_t(b + i) * kGrp);
         qs[r].load(sc, cols, j, b);
     }
-    const float4* x4 = reinterpret_cast<const float4*>(a.x);
-    for (uint32_t i = threadIdx.x; i < a.nblk * 4u; i += blockDim.x)
-        stage_x8(qx, sx, i, x4[2 * i], x4[2 * i + 1]);
+    if (stager) stage_x8(qx, sx, threadIdx.x, xv0, xv1);
     __syncthreads();
     float acc = 0.0f;
 #pragma unroll
