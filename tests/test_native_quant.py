@@ -159,6 +159,9 @@ def test_gpu_mv_native(xp, t):
 # 1152-wide matrices, Q4_K / Q6_K the 6912-wide ffn_down and attn_output.
 GEMMA = {Q5_0: [(6912, 1152), (1024, 1152)], Q8_0: [(6912, 1152), (256, 1152)],
          Q4_K: [(1152, 6912), (1152, 1024)], Q6_K: [(1152, 6912), (1152, 1024)]}
+# Wide, shallow shapes (>= 64 row groups, <= 40 k-blocks): with split 0 the
+# launcher runs one workgroup per row group (Q5_0 / Q8_0 6912 x 1152 above).
+WIDE = {Q4_K: [(4096, 1024)], Q6_K: [(4096, 1024)]}
 
 
 @pytest.mark.gpu
@@ -167,7 +170,7 @@ def test_gpu_mv_rq(xp, t):
     """Plain (split 1), split-k (4) and the launcher's choice (0) against the
     float64 product; each call repeated gives the same bits."""
     X = xp
-    shapes = [synth_shape(t)] + [s for s in GEMMA[t] if s[1] % FMT[t][3] == 0]
+    shapes = [synth_shape(t)] + [s for s in GEMMA[t] + WIDE.get(t, []) if s[1] % FMT[t][3] == 0]
     for rows, cols in shapes:
         raw, x = case(t, rows, cols, 41 + t)
         w = X.dequantize(t, raw, rows * cols).reshape(rows, cols).astype(np.float64)

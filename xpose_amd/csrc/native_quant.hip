@@ -533,6 +533,69 @@ uint32_t native_block_bytes(uint32_t t) {
 
 }  // namespace
 
+// Wide, shallow shapes (Q5_0 6912 x 1152: 108 row groups, 36 k-blocks): one
+// workgroup per row group, its eight waves splitting the k-blocks (wave w
+// takes blocks w, w + 8, ...) and meeting in LDS, summed in wave order. The
+// activations are loaded ahead of the weights; no partials, no ticket.
+constexpr int kRqWgWaves = 8;
+constexpr int kRqWgBlk = 5;   // k-blocks per wave: nkb <= 40
+
+template <uint32_t T>
+__global__ __launch_bounds__(kRqWgWaves * kWave) void mv_rq_wg_kernel(RqArgs a) {
+    using F = RqFmt<T>;
+    extern __shared__ QxBlock smem_rq[];
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+    const uint32_t lane = threadIdx.x % kWave;
+    const uint32_t gg = blockIdx.x;
+    RqLds x;
+    float* sx;
+    if constexpr (T == kQ80) {
+        uint32_t* pl = reinterpret_cast<uint32_t*>(smem_rq);
+        sx = reinterpret_cast<float*>(pl + size_t(a.nkb) * 24);
+        x = RqLds{nullptr, nullptr, pl, sx};
+    } else {
+        int32_t* ws = reinterpret_cast<int32_t*>(smem_rq + a.nkb);
+        sx = reinterpret_cast<float*>(ws + size_t(a.nkb) * 4);
+        x = RqLds{smem_rq, ws, nullptr, sx};
+    }
+    float* red = reinterpret_cast<float*>(reinterpret_cast<char*>(smem_rq) +
+                                          ((size_t(a.nkb) * kRqLdsPerBlock + 15u) & ~size_t(15)));
+    const float4* x4 = reinterpret_cast<const float4*>(a.x);
+    const bool stager = threadIdx.x < a.nkb * 4u;
+    float4 xv0 = {0.0f, 0.0f, 0.0f, 0.0f}, xv1 = xv0;
+    if (stager) {
+        xv0 = x4[2 * threadIdx.x];
+        xv1 = x4[2 * threadIdx.x + 1];
+    }
+    const size_t slot0 = size_t(gg) * a.nkb * kGrp + lane;
+    typename F::Blk buf[kRqWgBlk];
+#pragma unroll
+    for (int r = 0; r < kRqWgBlk; ++r)
+        F::load(buf[r], a, slot0 + size_t(min(wave + uint32_t(kRqWgWaves) * r, a.nkb - 1u)) * kGrp);
+    if (stager) {
+        if constexpr (T == kQ80)
+            stage_b8(const_cast<uint32_t*>(x.b8), sx, threadIdx.x, xv0, xv1);
+        else
+            stage_nib(const_cast<QxBlock*>(x.qx), const_cast<int32_t*>(x.wsum), sx, threadIdx.x, xv0, xv1);
+    }
+    __syncthreads();
+    float acc = 0.0f;
+#pragma unroll
+    for (int r = 0; r < kRqWgBlk; ++r) {
+        const uint32_t kb = wave + uint32_t(kRqWgWaves) * r;
+        if (kb < a.nkb) acc += F::dot(buf[r], x, kb);
+    }
+    red[wave * kGrp + lane] = acc;
+    __syncthreads();
+    if (wave == 0) {
+        float y = 0.0f;
+#pragma unroll
+        for (int v = 0; v < kRqWgWaves; ++v) y += red[v * kGrp + lane];
+        const uint32_t row = gg * kGrp + lane;
+        if (row < a.rows) a.out[row] = y;
+    }
+}
+
 int launch_mv_rq(float* out, const float* x, const xp_rq_tensor& w, uint32_t split,
                  hipStream_t st, const char* who) {
     if (!out || !x) return set_error(XP_E_ARG, "%s: null pointer", who);
@@ -563,6 +626,27 @@ int launch_mv_rq(float* out, const float* x, const xp_rq_tensor& w, uint32_t spl
     // Enough tasks for ~8 waves per CU, at most kRqMaxSplit chunks, and every
     // chunk's staged activations within 64 KiB of LDS.
     const uint32_t lds_min = (a.nkb * kRqLdsPerBlock + 65535u) / 65536u;
+    const uint32_t n_cu = uint32_t(sc->n_cu > 0 ? sc->n_cu : 256);
+    // Automatic plan for a shape wide enough to fill the GPU with one
+    // workgroup per row group and shallow enough for five k-blocks per wave:
+    // the workgroup kernel instead of split-k.
+    if (split == 0 && a.groups >= 64 && a.nkb <= uint32_t(kRqWgWaves * kRqWgBlk) &&
+        a.groups < n_cu * 8u) {
+        a.kpc = a.nkb;
+        a.split = 1;
+        const size_t lds = ((size_t(a.nkb) * kRqLdsPerBlock + 15u) & ~size_t(15)) +
+                           size_t(kRqWgWaves) * kGrp * sizeof(float);
+        const dim3 grid(a.groups), block(kRqWgWaves * kWave);
+        switch (w.type) {
+            case kQ80: hipLaunchKernelGGL((mv_rq_wg_kernel<kQ80>), grid, block, lds, st, a); break;
+            case kQ50: hipLaunchKernelGGL((mv_rq_wg_kernel<kQ50>), grid, block, lds, st, a); break;
+            case kQ4K: hipLaunchKernelGGL((mv_rq_wg_kernel<kQ4K>), grid, block, lds, st, a); break;
+            default: hipLaunchKernelGGL((mv_rq_wg_kernel<kQ6K>), grid, block, lds, st, a); break;
+        }
+        const hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return set_error(XP_E_HIP, "%s: launch -> %s", who, hipGetErrorString(e));
+        return XP_OK;
+    }
     if (split == 0) {
         const uint32_t target = uint32_t(sc->n_cu > 0 ? sc->n_cu : 256) * 8u;
         split = (target + a.groups - 1) / a.groups;
