@@ -533,45 +533,53 @@ uint32_t native_block_bytes(uint32_t t) {
 
 }  // namespace
 
-// Wide, shallow shapes (Q5_0 6912 x 1152: 108 row groups, 36 k-blocks): one
-// workgroup per row group, its eight waves splitting the k-blocks (wave w
-// takes blocks w, w + 8, ...) and meeting in LDS, summed in wave order. The
-// activations are loaded ahead of the weights; no partials, no ticket.
+// Workgroup tasks: one workgroup per (row group, k-chunk of at most 40
+// k-blocks), its eight waves splitting the chunk's blocks (wave w takes
+// blocks w, w + 8, ...) and meeting in LDS, summed in wave order. Wide,
+// shallow shapes (Q5_0 6912 x 1152: 108 row groups, 36 k-blocks) take one
+// chunk: no partials, no ticket. Narrow, deep ones (Q4_K / Q6_K 1152 x 6912:
+// 18 row groups, 216 k-blocks) take at most eight chunks (SPLIT): the
+// partials, an arrival ticket and one batch of partial loads by the last
+// chunk, summed in ascending chunk order. The activations are loaded ahead
+// of the weights.
 constexpr int kRqWgWaves = 8;
-constexpr int kRqWgBlk = 5;   // k-blocks per wave: nkb <= 40
+constexpr int kRqWgBlk = 5;                                 // k-blocks per wave
+constexpr uint32_t kRqWgChunk = kRqWgWaves * kRqWgBlk;      // k-blocks per chunk
+constexpr uint32_t kRqWgMaxSplit = 8;
 
-template <uint32_t T>
+template <uint32_t T, bool SPLIT>
 __global__ __launch_bounds__(kRqWgWaves * kWave) void mv_rq_wg_kernel(RqArgs a) {
     using F = RqFmt<T>;
     extern __shared__ QxBlock smem_rq[];
     const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
     const uint32_t lane = threadIdx.x % kWave;
-    const uint32_t gg = blockIdx.x;
+    const uint32_t gg = blockIdx.x % a.groups, s = blockIdx.x / a.groups;
+    const uint32_t kb0 = s * a.kpc, nkc = min(a.kpc, a.nkb - kb0);
     RqLds x;
     float* sx;
     if constexpr (T == kQ80) {
         uint32_t* pl = reinterpret_cast<uint32_t*>(smem_rq);
-        sx = reinterpret_cast<float*>(pl + size_t(a.nkb) * 24);
+        sx = reinterpret_cast<float*>(pl + size_t(a.kpc) * 24);
         x = RqLds{nullptr, nullptr, pl, sx};
     } else {
-        int32_t* ws = reinterpret_cast<int32_t*>(smem_rq + a.nkb);
-        sx = reinterpret_cast<float*>(ws + size_t(a.nkb) * 4);
+        int32_t* ws = reinterpret_cast<int32_t*>(smem_rq + a.kpc);
+        sx = reinterpret_cast<float*>(ws + size_t(a.kpc) * 4);
         x = RqLds{smem_rq, ws, nullptr, sx};
     }
     float* red = reinterpret_cast<float*>(reinterpret_cast<char*>(smem_rq) +
-                                          ((size_t(a.nkb) * kRqLdsPerBlock + 15u) & ~size_t(15)));
-    const float4* x4 = reinterpret_cast<const float4*>(a.x);
-    const bool stager = threadIdx.x < a.nkb * 4u;
+                                          ((size_t(a.kpc) * kRqLdsPerBlock + 15u) & ~size_t(15)));
+    const float4* x4 = reinterpret_cast<const float4*>(a.x + size_t(kb0) * kBlk);
+    const bool stager = threadIdx.x < nkc * 4u;
     float4 xv0 = {0.0f, 0.0f, 0.0f, 0.0f}, xv1 = xv0;
     if (stager) {
         xv0 = x4[2 * threadIdx.x];
         xv1 = x4[2 * threadIdx.x + 1];
     }
-    const size_t slot0 = size_t(gg) * a.nkb * kGrp + lane;
+    const size_t slot0 = (size_t(gg) * a.nkb + kb0) * kGrp + lane;
     typename F::Blk buf[kRqWgBlk];
 #pragma unroll
     for (int r = 0; r < kRqWgBlk; ++r)
-        F::load(buf[r], a, slot0 + size_t(min(wave + uint32_t(kRqWgWaves) * r, a.nkb - 1u)) * kGrp);
+        F::load(buf[r], a, slot0 + size_t(min(wave + uint32_t(kRqWgWaves) * r, nkc - 1u)) * kGrp);
     if (stager) {
         if constexpr (T == kQ80)
             stage_b8(const_cast<uint32_t*>(x.b8), sx, threadIdx.x, xv0, xv1);
@@ -582,18 +590,38 @@ __global__ __launch_bounds__(kRqWgWaves * kWave) void mv_rq_wg_kernel(RqArgs a) 
     float acc = 0.0f;
 #pragma unroll
     for (int r = 0; r < kRqWgBlk; ++r) {
-        const uint32_t kb = wave + uint32_t(kRqWgWaves) * r;
-        if (kb < a.nkb) acc += F::dot(buf[r], x, kb);
+        const uint32_t lb = wave + uint32_t(kRqWgWaves) * r;
+        if (lb < nkc) acc += F::dot(buf[r], x, lb);
     }
     red[wave * kGrp + lane] = acc;
     __syncthreads();
-    if (wave == 0) {
-        float y = 0.0f;
+    if (wave != 0) return;
+    float y = 0.0f;
 #pragma unroll
-        for (int v = 0; v < kRqWgWaves; ++v) y += red[v * kGrp + lane];
-        const uint32_t row = gg * kGrp + lane;
+    for (int v = 0; v < kRqWgWaves; ++v) y += red[v * kGrp + lane];
+    const uint32_t row = gg * kGrp + lane;
+    if constexpr (!SPLIT) {
         if (row < a.rows) a.out[row] = y;
+        return;
     }
+    const size_t stride = size_t(a.groups) * kGrp;
+    st_dev(a.partial + size_t(s) * stride + size_t(gg) * kGrp + lane, y);
+    wait_mem();
+    uint32_t old = 0;
+    if (lane == 0) old = take_ticket(&a.tickets[gg]);
+    old = __shfl(old, 0, kWave);
+    if (old != a.split - 1) return;
+    // every partial in one batch (split <= 8), summed in ascending chunk order
+    const float* pp = a.partial + size_t(gg) * kGrp + lane;
+    float v[kRqWgMaxSplit];
+#pragma unroll
+    for (uint32_t p = 0; p < kRqWgMaxSplit; ++p) v[p] = p < a.split ? ld_dev(pp + size_t(p) * stride) : 0.0f;
+    float sum = 0.0f;
+#pragma unroll
+    for (uint32_t p = 0; p < kRqWgMaxSplit; ++p)
+        if (p < a.split) sum += v[p];
+    if (row < a.rows) a.out[row] = sum;
+    if (lane == 0) st_dev(&a.tickets[gg], 0u);
 }
 
 int launch_mv_rq(float* out, const float* x, const xp_rq_tensor& w, uint32_t split,
@@ -627,25 +655,44 @@ int launch_mv_rq(float* out, const float* x, const xp_rq_tensor& w, uint32_t spl
     // chunk's staged activations within 64 KiB of LDS.
     const uint32_t lds_min = (a.nkb * kRqLdsPerBlock + 65535u) / 65536u;
     const uint32_t n_cu = uint32_t(sc->n_cu > 0 ? sc->n_cu : 256);
-    // Automatic plan for a shape wide enough to fill the GPU with one
-    // workgroup per row group and shallow enough for five k-blocks per wave:
-    // the workgroup kernel instead of split-k.
-    if (split == 0 && a.groups >= 64 && a.nkb <= uint32_t(kRqWgWaves * kRqWgBlk) &&
-        a.groups < n_cu * 8u) {
-        a.kpc = a.nkb;
-        a.split = 1;
-        const size_t lds = ((size_t(a.nkb) * kRqLdsPerBlock + 15u) & ~size_t(15)) +
-                           size_t(kRqWgWaves) * kGrp * sizeof(float);
-        const dim3 grid(a.groups), block(kRqWgWaves * kWave);
-        switch (w.type) {
-            case kQ80: hipLaunchKernelGGL((mv_rq_wg_kernel<kQ80>), grid, block, lds, st, a); break;
-            case kQ50: hipLaunchKernelGGL((mv_rq_wg_kernel<kQ50>), grid, block, lds, st, a); break;
-            case kQ4K: hipLaunchKernelGGL((mv_rq_wg_kernel<kQ4K>), grid, block, lds, st, a); break;
-            default: hipLaunchKernelGGL((mv_rq_wg_kernel<kQ6K>), grid, block, lds, st, a); break;
+    // Automatic plan for a shape narrower than eight waves per CU: workgroup
+    // tasks, one chunk per row group when the whole k fits one (and the
+    // groups alone give most CUs a task), else as many chunks as give every
+    // CU a task, at most eight, each within kRqWgChunk blocks.
+    if (split == 0 && a.groups < n_cu * 8u) {
+        uint32_t sp = 1;
+        if (a.nkb > kRqWgChunk || a.groups < 64) {
+            sp = std::max(1u, std::min(kRqWgMaxSplit, n_cu / a.groups));
+            sp = std::max(sp, (a.nkb + kRqWgChunk - 1) / kRqWgChunk);
         }
-        const hipError_t e = hipGetLastError();
-        if (e != hipSuccess) return set_error(XP_E_HIP, "%s: launch -> %s", who, hipGetErrorString(e));
-        return XP_OK;
+        if (sp <= kRqWgMaxSplit) {
+            a.kpc = (a.nkb + sp - 1) / sp;
+            a.split = (a.nkb + a.kpc - 1) / a.kpc;
+            if (a.split > 1) {
+                if (!ensure_partial(sc, size_t(a.split) * a.groups * kGrp)) return XP_E_NOMEM;
+                if (!ensure_tickets(sc, a.groups)) return XP_E_NOMEM;
+                a.partial = sc->partial;
+                a.tickets = sc->tickets;
+            }
+            const size_t lds = ((size_t(a.kpc) * kRqLdsPerBlock + 15u) & ~size_t(15)) +
+                               size_t(kRqWgWaves) * kGrp * sizeof(float);
+            const dim3 grid(a.groups * a.split), block(kRqWgWaves * kWave);
+#define XP_RQ_WG_LAUNCH(T)                                                                  \
+    if (a.split > 1)                                                                        \
+        hipLaunchKernelGGL((mv_rq_wg_kernel<T, true>), grid, block, lds, st, a);            \
+    else                                                                                    \
+        hipLaunchKernelGGL((mv_rq_wg_kernel<T, false>), grid, block, lds, st, a);
+            switch (w.type) {
+                case kQ80: XP_RQ_WG_LAUNCH(kQ80) break;
+                case kQ50: XP_RQ_WG_LAUNCH(kQ50) break;
+                case kQ4K: XP_RQ_WG_LAUNCH(kQ4K) break;
+                default: XP_RQ_WG_LAUNCH(kQ6K) break;
+            }
+#undef XP_RQ_WG_LAUNCH
+            const hipError_t e = hipGetLastError();
+            if (e != hipSuccess) return set_error(XP_E_HIP, "%s: launch -> %s", who, hipGetErrorString(e));
+            return XP_OK;
+        }
     }
     if (split == 0) {
         const uint32_t target = uint32_t(sc->n_cu > 0 ? sc->n_cu : 256) * 8u;
