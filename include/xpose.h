@@ -629,7 +629,10 @@ int xp_rq_reconstruct(const xp_rq_layout* l, const void* quant, const uint32_t* 
 /* matvec_rq4_k / _rq5_0 / _rq6_k / _rq8_0 (llm_quant.cl:515-549) for
  * split == 1, their _split forms + mv_reduce (llm_quant.cl:574-615) for
  * split > 1 (here one launch: the last k-chunk of a row group to finish sums
- * the partials in chunk order), split == 0 picks one. `in` is fp32 [cols],
+ * the partials in chunk order), split == 0 picks one: for shapes narrower
+ * than eight waves per CU, one workgroup per (row group, k-chunk of <= 40
+ * blocks, <= 8 chunks) whose waves split the chunk (deterministic: wave
+ * order, then chunk order). `in` is fp32 [cols],
  * 16-byte aligned; out [rows]. Within 1e-5 of max|out| of the float64
  * product (activations are staged as 20-bit block fixed point; every block
  * product is an exact integer). */
