@@ -455,7 +455,9 @@ def main() -> int:
                            "frac_of_stream_ceiling": round(achieved / ceil, 4)},
         "stream_ceiling_GBs": round(ceil, 1),
         "matvec_cfg1": {"shape": "6912x1152", "bytes": nb1, "us_per_launch": round(per1 * 1e6, 3),
-                        "GBs": round(nb1 / per1 / 1e9, 1)},
+                        "GBs": round(nb1 / per1 / 1e9, 1),
+                        "frac": round(nb1 / per1 / 1e9 / HBM_PEAK_GBS, 4),
+                        "frac_of_stream_ceiling": round(nb1 / per1 / 1e9 / ceil, 4)},
         "cpu_baseline": cpu,
         **extra,
         "device": info["arch"],
