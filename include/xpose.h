@@ -88,10 +88,11 @@ int xp_event_elapsed_ms(xp_event start, xp_event stop, float* ms);
  * (kernels/llm_matvec.cl:187-200, :339-356, :422-456, :128-135) and the COL
  * gold's semantics (kernels/llm.cl:488-573). `split` = number of k-chunks
  * (0 = choose); chunks are whole scale quads; split > 1 sums the chunks in
- * ascending order (deterministic). With split = 0, a wide and shallow shape
- * (>= 64 column groups, <= 16 quads of k, quad scale planes) instead runs
- * one workgroup per column group, its eight waves' partials summed in wave
- * order (deterministic, no scratch). out must not alias in. */
+ * ascending order (deterministic). With split = 0 and quad scale planes, a
+ * shape narrower than eight waves per CU instead runs one workgroup per
+ * (column group, k-chunk of <= 16 quads, <= 8 chunks), its eight waves'
+ * partials summed in wave order, then the chunks in chunk order
+ * (deterministic). out must not alias in. */
 int xp_mv_int4(float* out, const float* in, const void* wq, const void* scales,
                int scale_fmt, uint32_t rows, uint32_t cols, uint32_t split,
                xp_stream stream);

@@ -235,23 +235,30 @@ void mv_int4_kernel(MvArgs a) {
     if (lane == 0) st_dev(&a.tickets[gg], 0u);
 }
 
-// Wide, shallow shapes (config 1: 108 column groups over 9 quads of k): one
-// workgroup per column group, its eight waves splitting k (wave w takes quads
-// w and w + 8) and meeting in LDS, summed in wave order. Every weight load is
-// issued before the activations are staged, and no partial buffer or ticket
-// is needed: one HBM round trip instead of three. Quad scale planes only.
+// Workgroup tasks: one workgroup per (column group, k-chunk of at most 16
+// quads), its eight waves splitting the chunk (wave w takes quads w and
+// w + 8) and meeting in LDS, summed in wave order. Wide, shallow shapes
+// (config 1: 108 column groups over 9 quads of k) take one chunk: no partial
+// buffer, no ticket, one HBM round trip. Narrow, deep ones take at most eight
+// chunks (SPLIT): partials, an arrival ticket and one batch of partial loads
+// by the last chunk, summed in ascending chunk order. The activations are
+// loaded ahead of the weights, so staging them overlaps the weight fetch.
+// Quad scale planes only.
 constexpr int kMvWgWaves = 8;
-constexpr int kMvWgQuads = 2;   // quads per wave: nquads <= 16
+constexpr int kMvWgQuads = 2;                                 // quads per wave
+constexpr uint32_t kMvWgChunk = kMvWgWaves * kMvWgQuads;      // quads per chunk
+constexpr uint32_t kMvWgMaxSplit = 8;
 
-template <int FMT>
+template <int FMT, bool SPLIT>
 __global__ __launch_bounds__(kMvWgWaves * kWave) void mv_int4_wg_kernel(MvArgs a) {
     extern __shared__ QxBlock smem_qx[];
     const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
     const uint32_t lane = threadIdx.x % kWave;
-    const uint32_t gg = blockIdx.x;
+    const uint32_t gg = blockIdx.x % a.groups, s = blockIdx.x / a.groups;
+    const uint32_t q0 = s * a.qpc, nqc = min(a.qpc, a.nquads - q0), nbc = 4u * nqc;
     QxBlock* qx = smem_qx;
-    float* sx = reinterpret_cast<float*>(smem_qx + a.nblk);
-    float* red = sx + a.nblk;   // [kMvWgWaves][64]
+    float* sx = reinterpret_cast<float*>(smem_qx + 4u * a.qpc);
+    float* red = sx + 4u * a.qpc;   // [kMvWgWaves][64]
     uint32_t mi = 0;
 #pragma unroll
     for (int i = 1; i < kMvMaxMats; ++i)
@@ -268,10 +275,9 @@ __global__ __launch_bounds__(kMvWgWaves * kWave) void mv_int4_wg_kernel(MvArgs a
     }
     const uint32_t gl = gg - grp0, j = gl * kGrp + lane;
     const u32x4* wp = wq + size_t(gl) * a.nblk * kGrp + lane;
-    // The activations (at most 64 blocks: one staging task per thread) are
-    // loaded ahead of the weights, so that staging them waits for them only.
-    const float4* x4 = reinterpret_cast<const float4*>(a.x);
-    const bool stager = threadIdx.x < a.nblk * 4u;
+    // the chunk's activations (at most 64 blocks: one staging task per thread)
+    const float4* x4 = reinterpret_cast<const float4*>(a.x + size_t(4u * q0) * kBlk);
+    const bool stager = threadIdx.x < nbc * 4u;
     float4 xv0 = {0.0f, 0.0f, 0.0f, 0.0f}, xv1 = xv0;
     if (stager) {
         xv0 = x4[2 * threadIdx.x];
@@ -281,7 +287,7 @@ __global__ __launch_bounds__(kMvWgWaves * kWave) void mv_int4_wg_kernel(MvArgs a
     QuadScales<FMT> qs[kMvWgQuads];
 #pragma unroll
     for (int r = 0; r < kMvWgQuads; ++r) {
-        const uint32_t b = 4u * min(wave + uint32_t(kMvWgWaves) * r, a.nquads - 1u);
+        const uint32_t b = 4u * (q0 + min(wave + uint32_t(kMvWgWaves) * r, nqc - 1u));
 #pragma unroll
         for (int i = 0; i < 4; ++i) w[r][i] = ld_stream4(wp + size_t(b + i) * kGrp);
         qs[r].load(sc, cols, j, b);
@@ -291,23 +297,43 @@ __global__ __launch_bounds__(kMvWgWaves * kWave) void mv_int4_wg_kernel(MvArgs a
     float acc = 0.0f;
 #pragma unroll
     for (int r = 0; r < kMvWgQuads; ++r) {
-        const uint32_t q = wave + uint32_t(kMvWgWaves) * r;
-        if (q < a.nquads) {
+        const uint32_t lq = wave + uint32_t(kMvWgWaves) * r;
+        if (lq < nqc) {
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                const uint32_t lb = 4u * q + i;
+                const uint32_t lb = 4u * lq + i;
                 acc = fmaf(qs[r].get(i) * sx[lb], float(block_dot(w[r][i], qx[lb])), acc);
             }
         }
     }
     red[wave * kGrp + lane] = acc;
     __syncthreads();
-    if (wave == 0) {
-        float y = 0.0f;
+    if (wave != 0) return;
+    float y = 0.0f;
 #pragma unroll
-        for (int v = 0; v < kMvWgWaves; ++v) y += red[v * kGrp + lane];
+    for (int v = 0; v < kMvWgWaves; ++v) y += red[v * kGrp + lane];
+    if constexpr (!SPLIT) {
         out[j] = y;
+        return;
     }
+    const size_t stride = size_t(a.groups) * kGrp;
+    st_dev(a.partial + size_t(s) * stride + size_t(gg) * kGrp + lane, y);
+    wait_mem();
+    uint32_t old = 0;
+    if (lane == 0) old = take_ticket(&a.tickets[gg]);
+    old = __shfl(old, 0, kWave);
+    if (old != a.split - 1) return;
+    // every partial in one batch (split <= 8), summed in ascending chunk order
+    const float* pp = a.partial + size_t(gg) * kGrp + lane;
+    float v[kMvWgMaxSplit];
+#pragma unroll
+    for (uint32_t p = 0; p < kMvWgMaxSplit; ++p) v[p] = p < a.split ? ld_dev(pp + size_t(p) * stride) : 0.0f;
+    float sum = 0.0f;
+#pragma unroll
+    for (uint32_t p = 0; p < kMvWgMaxSplit; ++p)
+        if (p < a.split) sum += v[p];
+    out[j] = sum;
+    if (lane == 0) st_dev(&a.tickets[gg], 0u);
 }
 
 __global__ void unpack_km4_kernel(int8_t* out, const u32x4* wq, uint32_t rows, uint32_t cols) {
@@ -405,22 +431,57 @@ int launch_mv(const MvMatDesc* mats, uint32_t n, const float* x, int fmt, uint32
     a.nblk = nblk;
     a.nquads = (nblk + 3) / 4;
     a.groups = groups;
-    // Automatic plan for a shape wide enough to fill the GPU with one
-    // workgroup per column group and shallow enough for two quads per wave:
-    // the workgroup kernel instead of split-k.
-    if (split == 0 && fmt != XP_SCALE_F32 && groups >= 64 &&
-        a.nquads <= uint32_t(kMvWgWaves * kMvWgQuads) && choose_split(groups, a.nquads, n_cu) > 1) {
-        const size_t lds = size_t(nblk) * (sizeof(QxBlock) + sizeof(float)) +
-                           size_t(kMvWgWaves) * kGrp * sizeof(float);
-        if (fmt == XP_SCALE_F16_QUAD)
-            hipLaunchKernelGGL((mv_int4_wg_kernel<XP_SCALE_F16_QUAD>), dim3(groups),
-                               dim3(kMvWgWaves * kWave), lds, st, a);
-        else
-            hipLaunchKernelGGL((mv_int4_wg_kernel<XP_SCALE_BF16_QUAD>), dim3(groups),
-                               dim3(kMvWgWaves * kWave), lds, st, a);
-        hipError_t e = hipGetLastError();
-        if (e != hipSuccess) return set_error(XP_E_HIP, "%s: launch -> %s", who, hipGetErrorString(e));
-        return XP_OK;
+    // Automatic plan for a shape narrower than eight waves per CU (quad scale
+    // planes): workgroup tasks, one chunk per column group when the whole k
+    // fits one (and the groups alone give most CUs a task), else as many
+    // chunks as give every CU a task, at most eight, each within kMvWgChunk
+    // quads. A caller-provided partial buffer too small for that plan keeps
+    // the split-k plan it was sized for.
+    if (split == 0 && fmt != XP_SCALE_F32 && groups < uint32_t(n_cu) * 8u) {
+        uint32_t sp = 1;
+        if (a.nquads > kMvWgChunk || groups < 64) {
+            sp = std::max(1u, std::min(kMvWgMaxSplit, uint32_t(n_cu) / groups));
+            sp = std::max(sp, (a.nquads + kMvWgChunk - 1) / kMvWgChunk);
+        }
+        const uint32_t qpc = (a.nquads + sp - 1) / sp, nsp = (a.nquads + qpc - 1) / qpc;
+        const size_t need = nsp > 1 ? size_t(nsp) * groups * kGrp : 0;
+        bool ok = sp <= kMvWgMaxSplit;
+        if (ok && nsp > 1) {
+            if (sc) {
+                if (!ensure_partial(sc, need)) return XP_E_NOMEM;
+                if (!ensure_tickets(sc, groups)) return XP_E_NOMEM;
+                a.partial = sc->partial;
+                a.tickets = sc->tickets;
+            } else if (partial_cap >= need && tickets_cap >= groups) {
+                a.partial = partial;
+                a.tickets = tickets;
+            } else {
+                ok = false;
+            }
+        }
+        if (ok) {
+            a.qpc = qpc;
+            a.split = nsp;
+            const size_t lds = size_t(4u * qpc) * (sizeof(QxBlock) + sizeof(float)) +
+                               size_t(kMvWgWaves) * kGrp * sizeof(float);
+            const dim3 grid(groups * nsp), block(kMvWgWaves * kWave);
+#define XP_MV_WG_LAUNCH(F)                                                                 \
+    if (nsp > 1)                                                                           \
+        hipLaunchKernelGGL((mv_int4_wg_kernel<F, true>), grid, block, lds, st, a);         \
+    else                                                                                   \
+        hipLaunchKernelGGL((mv_int4_wg_kernel<F, false>), grid, block, lds, st, a);
+            if (fmt == XP_SCALE_F16_QUAD) {
+                XP_MV_WG_LAUNCH(XP_SCALE_F16_QUAD)
+            } else {
+                XP_MV_WG_LAUNCH(XP_SCALE_BF16_QUAD)
+            }
+#undef XP_MV_WG_LAUNCH
+            hipError_t e = hipGetLastError();
+            if (e != hipSuccess) return set_error(XP_E_HIP, "%s: launch -> %s", who, hipGetErrorString(e));
+            return XP_OK;
+        }
+        a.partial = nullptr;
+        a.tickets = nullptr;
     }
     split_plan(groups, a.nquads, split, n_cu, a.split, a.qpc);
     a.wg_per_chunk = (groups + kMvWaves - 1) / kMvWaves;
