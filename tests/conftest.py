@@ -15,14 +15,6 @@ def pytest_configure(config):
     config.addinivalue_line("markers", "gpu: needs an AMD GPU (gfx950) and libxpose.so")
 
 
-def pytest_collection_modifyitems(config, items):
-    """The decode CLI tests start the token kernel in a child process. The
-    runtime refuses a cooperative launch on a GPU where another process (this
-    one, once any session test has run) has already made one, so those tests
-    run first."""
-    items.sort(key=lambda it: 0 if os.path.basename(str(it.fspath)) == "test_cli.py" else 1)
-
-
 @pytest.fixture(scope="session")
 def xh():
     """The product binding for host-side entry points (synthetic inputs, ABI

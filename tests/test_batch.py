@@ -130,6 +130,65 @@ def test_gpu_batch_sampling_draws(xp, xo):
 
 
 @pytest.mark.gpu
+def test_gpu_batch_full_size_cfg5(xp, xo):
+    """Benchmark config 5 at full size: 26 layers, vocab 262144, 16 sequences
+    at the benchmark's Philox depths in [128, 4096] (global-layer spans to
+    ~4000), T 0.8 / top-k 64 / top-p 0.95. Each sequence against the oracle
+    run alone on its own KV cache for two steps: logits, appended K/V rows,
+    the 64 device candidates and the drawn tokens."""
+    X = xp
+    print("case batch full-size cfg5", flush=True)
+    seed = 0x5EED0005
+    cfg = X.XpConfig.gemma3_1b(max_seq=4104, sample_mode=1, temperature=0.8, top_k=64,
+                               top_p=0.95, seed=seed, seq_id=0)
+    sess, t = build(X, xo, cfg)
+    n_seq = 16
+    u = np.array([X.philox_uniform(seed, i, 0) for i in range(n_seq)])
+    depths = (128 + np.floor(u * (4096 - 128 + 1))).astype(np.int64)   # as bench.py's cfg5 leg
+    assert depths.max() > 3000 and depths.min() < 1000, depths
+    kvd = cfg.n_kv_heads * cfg.head_dim
+    batch = X.DecodeBatch(sess, n_seq, cfg.max_seq)
+    models = []
+    for i, d in enumerate(depths):
+        m = xo.OracleModel(cfg, lambda l, k: t[(l, k)])
+        for l in range(cfg.n_layers):
+            for which, cache in ((0, m.kcache), (1, m.vcache)):
+                rows = X.synth_normal_f16(int(d) * kvd, 5000 + i, 2 * l + which)
+                batch.kv_upload(i, l, which, 0, rows)
+                cache[l][:int(d) * kvd] = rows
+        models.append(m)
+    batch.set_positions(depths)
+    toks = (np.arange(n_seq) * 16381 + 7).astype(np.uint32) % cfg.vocab
+    pos = depths.copy()
+    batch.forward(toks)
+    for step in range(2):
+        want_tok = np.empty(n_seq, np.uint32)
+        for i in range(n_seq):
+            want = models[i].forward(int(toks[i]), int(pos[i]), True, 16)
+            got = batch.last_logits(i)
+            ok, msg = logits_close(got, want)
+            assert ok, f"step {step} seq {i} depth {pos[i]}: {msg}"
+            for which, ref in ((0, models[i].kcache), (1, models[i].vcache)):
+                for l in (0, 5, 25):
+                    row = batch.kv_download(i, l, which, int(pos[i]), 1).view(np.float16)
+                    want_row = ref[l][pos[i] * kvd:(pos[i] + 1) * kvd].view(np.float16)
+                    err = np.abs(row.astype(np.float64) - want_row.astype(np.float64)).max()
+                    assert err <= 1e-3 * np.abs(want_row.astype(np.float64)).max(), (step, i, l, which)
+            cv, ci, bv, bi = harvest_best(xo, got)
+            gv, gi = batch.last_candidates(i)
+            assert np.array_equal(gi, bi), (step, i)
+            assert np.array_equal(gv.view(np.uint32), bv.view(np.uint32)), (step, i)
+            uu = xo.lib().xo_philox_uniform(seed, i, step)
+            want_tok[i] = xo.lib().xo_draw(cv.copy(), ci.copy(), cv.size, 0.8, 64, 0.95, uu)
+        got_tok = batch.decode_step()
+        assert np.array_equal(got_tok, want_tok), step
+        toks, pos = got_tok, pos + 1
+    print("cfg5 draws distinct per step:", len(set(toks.tolist())), flush=True)
+    batch.close()
+    sess.close()
+
+
+@pytest.mark.gpu
 def test_gpu_batch_one_sequence_equals_session(xp, xo):
     """A batch of one sequence and the single-sequence session (persistent
     token kernel) on the same weights and KV give the same logits to the

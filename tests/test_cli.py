@@ -91,6 +91,32 @@ def test_gpu_cli_matches_python_session(xp):
 
 
 @pytest.mark.gpu
+def test_gpu_cli_token_kernel_after_in_process_session(xp):
+    """A child process on the same GPU runs the persistent token kernel while
+    this process holds a token-kernel session that has launched: the launch
+    is a plain one, so nothing is refused and AUTO picks the token kernel in
+    both; the ids agree."""
+    X = xp
+    print("case cli after in-process token session", flush=True)
+    seed, layers = 0x5EED0003, 3
+    cfg = X.XpConfig.gemma3_1b(n_layers=layers, exec_mode=X.XP_EXEC_AUTO)
+    sess = X.DecodeSession(cfg)
+    assert sess.exec_mode == X.XP_EXEC_TOKEN
+    sess.synthesize(seed)
+    sess.prefill(np.array([1, 2, 3], np.uint32))
+    sess.decode_steps(4)
+    r = run("--layers", layers, "--prompt-len", 8, "-n", 6, "--weights-seed", seed, "--ids")
+    assert r.returncode == 0, r.stderr
+    assert "persistent token kernel" in r.stdout, r.stdout
+    r2 = run("--layers", layers, "--prompt-len", 8, "-n", 6, "--weights-seed", seed, "--ids",
+             "--exec", "graph")
+    assert r2.returncode == 0, r2.stderr
+    assert cli_ids(r.stdout) == cli_ids(r2.stdout)
+    sess.decode_steps(2)                  # this process's session still runs
+    sess.close()
+
+
+@pytest.mark.gpu
 def test_gpu_cli_gguf_matches_python_session(xp, tmp_path):
     """--model: the CLI's C++ GGUF load (DecodeSession(Model, Config, cache))
     and the Python binding's give the same greedy ids on a small GGUF model."""

@@ -208,3 +208,54 @@ def test_gpu_fp16_decode_all_patterns(xp, xo):
     nan = np.isnan(want)
     assert np.array_equal(np.isnan(got), nan)
     assert np.array_equal(got[~nan].view(np.uint32), want[~nan].view(np.uint32))
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("name,rows,cols", [("q", 1152, 1024), ("kv", 1152, 256),
+                                            ("o_proj", 1024, 1152), ("down", 6912, 1152),
+                                            ("gate", 1152, 6912)])
+def test_gpu_matvec_auto_plan_repeatable(xp, xo, name, rows, cols):
+    """The automatic plan (split 0): workgroup tasks per (column group,
+    k-chunk) with the last arrival summing the chunks in order for the narrow
+    shapes, one workgroup per column group for the wide one. The same call
+    twice gives the same bits."""
+    print(f"case matvec auto plan {name}", flush=True)
+    wq, sc, x = synth_case(xp, rows, cols)
+    a = run_mv(xp, wq, sc, x, rows, cols, 0)
+    b = run_mv(xp, wq, sc, x, rows, cols, 0)
+    assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+    want = xo.mv_km4(x, wq, sc, rows, cols, 0)
+    assert np.abs(a - want).max() / np.abs(want).max() < 1e-5
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("cols", [(1024, 256, 256), (6912, 6912)], ids=["qkv", "gate_up"])
+def test_gpu_matvec_multi_matches_oracle(xp, xo, cols):
+    """xp_mv_int4_multi: matrices of different widths sharing one input (the
+    session's q | k | v and gate | up launches), each against the oracle."""
+    import ctypes as C
+    X = xp
+    rows = 1152
+    print(f"case matvec multi {cols}", flush=True)
+    x = X.synth_normal(rows, 0x5EED0001, 3)
+    mats = [(X.synth_nibbles(rows, c, 0x5EED0001, 10 + i),
+             X.synth_scales(rows, c, 0x5EED0001, 20 + i, 0.02, 0)) for i, c in enumerate(cols)]
+    dx = X.DeviceBuffer.from_array(x)
+    dws = [X.DeviceBuffer.from_array(w) for w, _ in mats]
+    dss = [X.DeviceBuffer.from_array(s) for _, s in mats]
+    douts = [X.DeviceBuffer(c * 4) for c in cols]
+    for d, c in zip(douts, cols):
+        d.upload(np.full(c, -1e30, np.float32))
+    n = len(cols)
+    P = C.c_void_p * n
+    outs = P(*[d.vp for d in douts])
+    wqs = P(*[d.vp for d in dws])
+    scs = P(*[d.vp for d in dss])
+    cs = (C.c_uint32 * n)(*cols)
+    X.call("xp_mv_int4_multi", n, outs, dx.vp, wqs, scs, cs, 0, rows, None)
+    X.synchronize()
+    for i, c in enumerate(cols):
+        got = douts[i].download(np.float32)
+        want = xo.mv_km4(x, mats[i][0], mats[i][1], rows, c, 0)
+        assert not (got == np.float32(-1e30)).any(), i
+        assert np.abs(got - want).max() / np.abs(want).max() < 1e-5, i

@@ -269,27 +269,116 @@ def test_gpu_token_device_placement_cfg4(xp, xo):
                                                      placement=X.XP_PLACE_DEVICE))
 
 
-def deep_context_check(X, xo, cfg):
+def deep_context_check(X, xo, cfg, fill=4096, steps=3):
     sess, model = make_pair(X, xo, cfg)
     kvd = cfg.n_kv_heads * cfg.head_dim
     for l in range(cfg.n_layers):
         for which, cache in ((0, model.kcache), (1, model.vcache)):
-            rows = X.synth_normal_f16(4096 * kvd, 4096, 2 * l + which)
+            rows = X.synth_normal_f16(fill * kvd, 4096, 2 * l + which)
             sess.kv_upload(l, which, 0, rows)
-            cache[l][:4096 * kvd] = rows
-    sess.set_position(4096)
+            cache[l][:fill * kvd] = rows
+    sess.set_position(fill)
     sess.prefill([4242])
-    lg = model.forward(4242, 4096, True, 16)
+    lg = model.forward(4242, fill, True, 16)
     ok, msg = logits_close(sess.last_logits(), lg)
     assert ok, msg
-    pos = 4097
-    for step in range(3):
+    pos = fill + 1
+    for step in range(steps):
         tok = sess.decode_step()
         assert tok == xo.argmax_tree(lg)[0]
         lg = model.forward(tok, pos, True, 16)
         ok, msg = logits_close(sess.last_logits(), lg)
         assert ok, f"step {step}: {msg}"
         pos += 1
+    return sess
+
+
+DEEP_MODES = [pytest.param(3, 0, id="token-auto"), pytest.param(3, 1, id="token-device"),
+              pytest.param(1, 0, id="graph")]
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("exec_mode,placement", DEEP_MODES)
+def test_gpu_full_model_max_context_8192(xp, xo, exec_mode, placement):
+    """The deep end of benchmark config 4 at the default max_seq 8192: KV of
+    all 26 layers pre-filled to position 8190, then positions 8190 and 8191
+    (the last the cache holds): the global layers attend 8191 and 8192
+    keys, which on the token kernel is 256 attention chunks, every
+    workgroup of the global combine."""
+    X = xp
+    print(f"case session max context 8192 exec {exec_mode} placement {placement}", flush=True)
+    cfg = X.XpConfig.gemma3_1b(exec_mode=exec_mode, placement=placement)
+    assert cfg.max_seq == 8192
+    sess = deep_context_check(X, xo, cfg, fill=8190, steps=1)
+    assert sess.position == 8192
+    with pytest.raises(X.XposeError):
+        sess.decode_step()                   # the cache is full
+    sess.close()
+
+
+def untied_pair(X, xo, cfg, seed, embed_seed):
+    """make_pair plus an fp32 N(0, 1) embedding table (XP_T_EMBED) that is not
+    the lm_head: a greedy stream then moves from token to token instead of
+    settling on the fixed point a tied random table has."""
+    t = all_tensors(X, cfg, seed)
+    emb = np.random.default_rng(embed_seed).normal(0, 1, (cfg.vocab, cfg.hidden)).astype(np.float32)
+    sess = X.DecodeSession(cfg)
+    assert sess.exec_mode == cfg.exec_mode
+    for (l, k), a in t.items():
+        sess.upload(l, k, a)
+    sess.upload(-1, X.T_EMBED, emb)
+    model = xo.OracleModel(cfg, lambda l, k: t[(l, k)], embed=emb)
+    return sess, model
+
+
+def greedy_stream_check(xo, sess, model, prompt, n_gen, min_distinct):
+    """Sample-first greedy decode (decode.cpp:1830-1861) against the oracle:
+    every id equal, logits within 1e-3 at every step, the stream holding at
+    least min_distinct ids; prints the oracle's top-2 gap of each decision."""
+    lg = None
+    for i, t in enumerate(prompt):
+        lg = model.forward(int(t), i, i == len(prompt) - 1, 16)
+    sess.prefill(prompt)
+    ids, gaps = [], []
+    for step in range(n_gen):
+        ok, msg = logits_close(sess.last_logits(), lg)
+        assert ok, f"step {step}: {msg}"
+        order = top5(lg)
+        gaps.append(float((lg[order[0]] - lg[order[1]]) / np.abs(lg).max()))
+        tok = sess.decode_step()
+        assert tok == int(order[0]), (step, tok, int(order[0]))
+        ids.append(tok)
+        lg = model.forward(tok, len(prompt) + step, True, 16)
+    print("ids", ids, "top-2 gaps / max|logits|:", " ".join(f"{g:.1e}" for g in gaps), flush=True)
+    assert len(set(ids)) >= min_distinct, ids
+
+
+@pytest.mark.gpu
+def test_gpu_greedy_stream_varies(xp, xo, mode):
+    """24 greedy tokens after a 32-token prompt on a 6-layer model with an
+    untied table: 24 distinct ids on the oracle (smallest top-2 gap 5e-3 of
+    max|logits|), each equal on the GPU."""
+    X = xp
+    print("case session varying greedy stream", flush=True)
+    cfg = cfg_small(X, exec_mode=mode)
+    sess, model = untied_pair(X, xo, cfg, 0x5EED0002, 17)
+    prompt = np.random.default_rng(4).integers(0, cfg.vocab, 32).astype(np.uint32)
+    greedy_stream_check(xo, sess, model, prompt, 24, 16)
+    sess.close()
+
+
+@pytest.mark.gpu
+def test_gpu_full_model_greedy_stream_varies(xp, xo, mode):
+    """The full Gemma-3-1B shape with an untied 262144 x 1152 fp32 table: 12
+    greedy tokens after an 8-token prompt, 10 distinct ids on the oracle
+    (smallest top-2 gap 4e-3 of max|logits|), each equal on the GPU."""
+    X = xp
+    print("case session full model varying greedy stream", flush=True)
+    cfg = X.XpConfig.gemma3_1b(max_seq=2048, exec_mode=mode)
+    sess, model = untied_pair(X, xo, cfg, 0x5EED0002, 18)
+    prompt = np.random.default_rng(32).integers(0, cfg.vocab, 8).astype(np.uint32)
+    greedy_stream_check(xo, sess, model, prompt, 12, 8)
+    sess.close()
 
 
 @pytest.mark.gpu

@@ -446,10 +446,27 @@ int sample_from_candidates(Session& s, uint32_t& token) {
 }
 
 // Layer table, RoPE tables and exchange buffers of the persistent token
-// kernel (token_kernel.hip); switches the session to it.
+// kernel (token_kernel.hip); switches the session to it. Fails (and leaves
+// the session on its graph path) when the device cannot hold the kernel's
+// grid of one workgroup per CU resident at once: the occupancy query, then a
+// probe launch of the same shape whose workgroups wait (bounded) for each
+// other.
 int setup_token(Session& s) {
     const xp_config& c = s.cfg;
     const uint32_t grid = uint32_t(s.n_cu);
+    int per_cu = 0;
+    if (int rc = tok_occupancy(c.hidden, c.ffn, c.n_heads, c.scale_fmt, &per_cu); rc != XP_OK)
+        return rc;
+    if (per_cu < 1)
+        return set_error(XP_E_HIP, "token kernel: a CU cannot hold one 512-thread workgroup with "
+                         "%zu B of LDS", tok_lds_bytes());
+    std::vector<uint32_t> probe(grid);
+    if (int rc = probe_token_grid(grid, s.st, probe.data()); rc != XP_OK) return rc;
+    uint32_t resident = 0;
+    for (uint32_t w = 0; w < grid; ++w) resident += (probe[w] >> 8) & 1u;
+    if (resident != grid)
+        return set_error(XP_E_DEVICE, "token kernel: %u of %u workgroups saw the whole grid "
+                         "resident (another kernel holds CUs of this GPU)", resident, grid);
     const TokLL lay = tok_ll_layout(c.hidden, c.ffn, c.n_heads, c.head_dim, grid);
     const size_t sizes[] = {
         size_t(c.n_layers) * sizeof(TokLayer),                   // layer table
@@ -515,18 +532,17 @@ int setup_token(Session& s) {
     // XP_PLACE_DEVICE) keeps every exchange device-coherent.
     a.xcd_local = 0;
     a.xcd_ids = 0;
-    std::vector<uint32_t> xcc(grid);
-    if (c.placement == XP_PLACE_AUTO && grid >= 8 && probe_token_xcc(grid, s.st, xcc.data()) == XP_OK) {
+    if (c.placement == XP_PLACE_AUTO && grid >= 8) {
+        auto xcc = [&](uint32_t w) { return probe[w] & 0xFFu; };
         bool periodic = true;
-        for (uint32_t w = 0; w < grid; ++w) periodic &= xcc[w] == xcc[w % 8];
+        for (uint32_t w = 0; w < grid; ++w) periodic &= xcc(w) == xcc(w % 8);
         for (uint32_t i = 0; i < 8; ++i)
-            for (uint32_t j = 0; j < i; ++j) periodic &= xcc[i] != xcc[j];
+            for (uint32_t j = 0; j < i; ++j) periodic &= xcc(i) != xcc(j);
         if (periodic) {
             a.xcd_local = 1;
-            for (uint32_t r = 0; r < 8; ++r) a.xcd_ids |= (xcc[r] & 15u) << (4 * r);
+            for (uint32_t r = 0; r < 8; ++r) a.xcd_ids |= (xcc(r) & 15u) << (4 * r);
         }
     }
-    clear_error();
     s.tok_grid = grid;
     s.tag = 0;
     s.mode = XP_EXEC_TOKEN;
@@ -542,12 +558,24 @@ int queue_status(Session& s) {
     XP_HIP(hipMemcpyAsync(s.h_stat, s.state + 2, 4, hipMemcpyDeviceToHost, s.st));
     return XP_OK;
 }
+// Either error leaves the session's logits and the KV rows of the failed
+// step invalid until the caller sets a position (xp_session_set_position or
+// xp_session_reset), which also clears the status word.
 int check_status(Session& s) {
     if (s.mode != XP_EXEC_TOKEN) return XP_OK;
-    if (s.h_stat[0] != 0)
+    const uint32_t st = s.h_stat[0];
+    if (st & 2u) {
+        // Later launches exchange every value through the device coherence
+        // point (as XP_PLACE_DEVICE does).
+        s.ta.xcd_local = 0;
+        return set_error(XP_E_DEVICE, "token kernel: the workgroup -> XCD placement changed since "
+                         "the session's probe (status %u); XCD-local exchange is now off. The "
+                         "step's results and KV rows are invalid: set a position to go on", st);
+    }
+    if (st != 0)
         return set_error(XP_E_DEVICE, "token kernel: a wait for another workgroup's data ran "
-                         "past its spin limit (status %u); the session's results are invalid",
-                         s.h_stat[0]);
+                         "past its spin limit (status %u); the step's results and KV rows are "
+                         "invalid: set a position to go on", st);
     return XP_OK;
 }
 
@@ -757,10 +785,12 @@ int xp_session_create(const xp_config* cfg, xp_session** out) {
         }
         if (tok_ok == XP_OK) {
             int rc = setup_token(s);
-            if (rc != XP_OK) {
+            if (rc != XP_OK && c.exec_mode == XP_EXEC_TOKEN) {
                 destroy(h);
                 return rc;
             }
+            // XP_EXEC_AUTO: a device that cannot run the token kernel keeps
+            // the graph path chosen above
         }
         clear_error();
         if (hipDeviceSynchronize() != hipSuccess) {
@@ -888,7 +918,12 @@ int xp_session_set_position(xp_session* h, uint32_t pos) {
     XP_HIP(hipStreamSynchronize(s.st));
     s.pos = pos;
     s.logits_valid = false;
-    XP_HIP(hipMemcpy(s.state, &pos, 4, hipMemcpyHostToDevice));
+    // position, then the token kernel's status word: a failed step's error
+    // does not outlive the context the caller rebuilds from here
+    const uint32_t st[3] = {pos, 0u, 0u};
+    XP_HIP(hipMemcpy(s.state, &st[0], 4, hipMemcpyHostToDevice));
+    XP_HIP(hipMemcpy(s.state + 2, &st[2], 4, hipMemcpyHostToDevice));
+    s.h_stat[0] = 0;
     return XP_OK;
 }
 

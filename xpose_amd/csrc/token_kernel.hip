@@ -1,4 +1,4 @@
-// One decode token as ONE persistent cooperative kernel on gfx950.
+// One decode token as ONE persistent kernel on gfx950.
 //
 // The reference records 838 dispatches per token into one Vulkan submit
 // (examples/llm/decode.cpp:1634-1780, agent-docs/llm-inference.md:88-103).
@@ -185,7 +185,8 @@ __device__ __forceinline__ void ll_wait(rsrc_t r, uint32_t soff, const uint32_t 
         if ((++spins & 255u) == 0u) {
             if (ld_dev(state + 2) != 0u) break;
             if (spins > kSpinLimit) {
-                st_dev(state + 2, 1u);
+                __hip_atomic_fetch_or((XP_GLOBAL uint32_t*)(state + 2), 1u, __ATOMIC_RELAXED,
+                                      __HIP_MEMORY_SCOPE_AGENT);
                 break;
             }
         }
@@ -505,6 +506,14 @@ __global__ __launch_bounds__(kTkThreads) void token_kernel(TokArgs a) {
     // This workgroup is on the XCD the host found its residue class on (else
     // its XCD-local results go through the device coherence point).
     const bool on_xcd = xcc_id() == ((a.xcd_ids >> (4u * (wg % 8u))) & 15u);
+    // The XCD-local stages (local layers' attention and combine) run on the
+    // workgroups grid - 1 - 8 s and exchange through one XCD's L2, which a
+    // workgroup placed elsewhere cannot see. Such a placement change is
+    // reported as status bit 2 at once (every wait then gives up), not as a
+    // spin-limit failure; the host then stops using the XCD-local exchange.
+    if (a.xcd_local && !on_xcd && (nwg - 1u - wg) % 8u == 0u && tid == 0)
+        __hip_atomic_fetch_or((XP_GLOBAL uint32_t*)(a.state + 2), 2u, __ATOMIC_RELAXED,
+                              __HIP_MEMORY_SCOPE_AGENT);
 
     // x entering layer l (l > 0) from layer l - 1's slots, in owner registers:
     // xb + post_ffw_norm(sum of the down chunks, in chunk order).
@@ -1225,27 +1234,57 @@ int tok_supported(uint32_t n_layers, uint32_t hidden, uint32_t ffn, uint32_t n_h
     return XP_OK;
 }
 
-// Each workgroup records the XCC (XCD) it runs on; launched exactly as the
-// token kernel is (threads, LDS, cooperative), so it sees the same placement.
-__global__ __launch_bounds__(kTkThreads) void xcc_probe_kernel(uint32_t* out) {
-    if (threadIdx.x == 0) out[blockIdx.x] = xcc_id();
+// Each workgroup records the XCC (XCD) it runs on and whether the whole grid
+// was resident at once: it takes an arrival ticket and waits, bounded, for
+// the grid's last arrival (out[w] = XCC id | 0x100 when it saw every
+// arrival). Launched exactly as the token kernel is (threads, LDS), so it
+// sees the same placement and the same residency.
+__global__ __launch_bounds__(kTkThreads) void grid_probe_kernel(uint32_t* out, uint32_t* count,
+                                                                uint32_t spin_limit) {
+    if (threadIdx.x == 0) {
+        const uint32_t n = gridDim.x;
+        (void)take_ticket(count);
+        uint32_t seen = ld_dev(count), spins = 0;
+        while (seen < n && ++spins < spin_limit) {
+            __builtin_amdgcn_s_sleep(8);
+            seen = ld_dev(count);
+        }
+        out[blockIdx.x] = xcc_id() | (seen >= n ? 0x100u : 0u);
+    }
 }
 
-int probe_token_xcc(uint32_t grid, hipStream_t st, uint32_t* out) {
+int probe_token_grid(uint32_t grid, hipStream_t st, uint32_t* out) {
     const size_t lds = tok_lds_bytes();
-    const void* fn = reinterpret_cast<const void*>(&xcc_probe_kernel);
+    const void* fn = reinterpret_cast<const void*>(&grid_probe_kernel);
     XP_HIP(hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, int(lds)));
     uint32_t* d = nullptr;
-    XP_HIP(hipMalloc(&d, size_t(grid) * 4));
-    void* args[] = {&d};
-    hipError_t e = hipLaunchCooperativeKernel(fn, dim3(grid), dim3(kTkThreads), args, lds, st);
+    XP_HIP(hipMalloc(&d, size_t(grid + 1) * 4));
+    uint32_t* count = d + grid;
+    uint32_t limit = 1u << 18;                   // ~0.1 s of 512-cycle sleeps
+    void* args[] = {&d, &count, &limit};
+    hipError_t e = hipMemsetAsync(count, 0, 4, st);
+    if (e == hipSuccess) e = hipLaunchKernel(fn, dim3(grid), dim3(kTkThreads), args, lds, st);
     if (e == hipSuccess) e = hipMemcpyAsync(out, d, size_t(grid) * 4, hipMemcpyDeviceToHost, st);
     if (e == hipSuccess) e = hipStreamSynchronize(st);
     (void)hipFree(d);
-    if (e != hipSuccess) return set_error(XP_E_HIP, "token kernel: XCC probe -> %s", hipGetErrorString(e));
+    if (e != hipSuccess) return set_error(XP_E_HIP, "token kernel: grid probe -> %s", hipGetErrorString(e));
     return XP_OK;
 }
 
+int tok_occupancy(uint32_t hidden, uint32_t ffn, uint32_t n_heads, int fmt, int* blocks_per_cu) {
+    const void* fn = token_entry(hidden, ffn, n_heads, fmt);
+    if (!fn) return set_error(XP_E_ARG, "token kernel: no build for this shape");
+    const size_t lds = tok_lds_bytes();
+    XP_HIP(hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, int(lds)));
+    XP_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(blocks_per_cu, fn, kTkThreads, lds));
+    return XP_OK;
+}
+
+// A plain launch: the kernel needs its workgroups co-resident (one per CU,
+// checked at session set-up by the occupancy query and the grid probe) but
+// never waits at a grid barrier, so it needs no cooperative launch. Every
+// wait in it is bounded, so a grid that is not resident after all (another
+// kernel holding CUs) ends with a status error instead of hanging.
 int launch_token(const TokArgs& a, uint32_t grid, hipStream_t st) {
     const void* fn = token_entry(a.hidden, a.ffn, a.n_heads, a.fmt);
     if (!fn) return set_error(XP_E_ARG, "token kernel: no build for this shape");
@@ -1264,16 +1303,9 @@ int launch_token(const TokArgs& a, uint32_t grid, hipStream_t st) {
     }
     TokArgs copy = a;
     void* args[] = {&copy};
-    hipError_t e = hipLaunchCooperativeKernel(fn, dim3(grid), dim3(kTkThreads), args, lds, st);
-    if (e == hipErrorIllegalState)
-        // The runtime refuses cooperative launches on a device where another
-        // process has already made one (measured on MI355X / ROCm 7).
-        return set_error(XP_E_HIP, "token kernel: cooperative launch of %u workgroups refused (%s): "
-                         "another process on this GPU has made a cooperative launch; run one "
-                         "decode process per GPU, or use the graph execution mode", grid,
-                         hipGetErrorString(e));
+    hipError_t e = hipLaunchKernel(fn, dim3(grid), dim3(kTkThreads), args, lds, st);
     if (e != hipSuccess)
-        return set_error(XP_E_HIP, "token kernel: cooperative launch of %u workgroups -> %s", grid,
+        return set_error(XP_E_HIP, "token kernel: launch of %u workgroups -> %s", grid,
                          hipGetErrorString(e));
     return XP_OK;
 }

@@ -208,7 +208,9 @@ struct TokArgs {
     unsigned long long* ll;
     size_t ll_layer;
     float* logits;                        // [vocab]
-    uint32_t* state;                      // [0] position, [1] token, [2] status
+    uint32_t* state;                      // [0] position, [1] token, [2] status bits:
+                                          // 1 a wait ran past its spin limit,
+                                          // 2 the XCD placement changed
     uint32_t* hist;                       // [max_seq] token run at each position
     unsigned long long* trace;            // optional: [stage event][grid] timestamps
     uint32_t tag;                         // this launch's tag (never 0)
@@ -266,8 +268,11 @@ int tok_supported(uint32_t n_layers, uint32_t hidden, uint32_t ffn, uint32_t n_h
                   uint32_t n_kv_heads, uint32_t head_dim, uint32_t vocab, uint32_t max_seq,
                   int fmt, int n_cu);
 int launch_token(const TokArgs& a, uint32_t grid, hipStream_t st);
-// The XCC id of every workgroup of a token-kernel-shaped launch of `grid`
-// workgroups (out: grid entries, host memory).
-int probe_token_xcc(uint32_t grid, hipStream_t st, uint32_t* out);
+// Workgroups of the token kernel one CU can hold at once.
+int tok_occupancy(uint32_t hidden, uint32_t ffn, uint32_t n_heads, int fmt, int* blocks_per_cu);
+// For every workgroup of a token-kernel-shaped launch of `grid` workgroups
+// (out: grid entries, host memory): its XCC id, | 0x100 when it saw the
+// whole grid resident at once.
+int probe_token_grid(uint32_t grid, hipStream_t st, uint32_t* out);
 
 }  // namespace xp
