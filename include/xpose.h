@@ -97,6 +97,23 @@ int xp_mv_int4(float* out, const float* in, const void* wq, const void* scales,
                int scale_fmt, uint32_t rows, uint32_t cols, uint32_t split,
                xp_stream stream);
 
+/* xp_mv_int4 that allocates nothing. No counterpart in the reference: it is
+ * for callers that cannot allocate device memory (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc). Its
+ * split-k / k-chunk partial sums and arrival tickets live in a fixed
+ * per-GPU scratch (a device array of 1 MiB of partials + 4096 tickets, held
+ * by each GPU the library runs on until the process ends, set up by xp_init
+ * or by the first call on a device); the caller passes only inputs and
+ * outputs. Same kernels, plans and results as xp_mv_int4; a plan that needs
+ * more partials than the scratch holds first falls back from the k-chunk
+ * plan to the split-k plan, and an explicit split whose partials do not fit
+ * is rejected with XP_E_ARG. Every call on one GPU shares that GPU's
+ * scratch: calls that overlap on one GPU (different streams, threads)
+ * race; calls ordered on one stream do not. */
+int xp_mv_int4_noalloc(float* out, const float* in, const void* wq, const void* scales,
+                       int scale_fmt, uint32_t rows, uint32_t cols, uint32_t split,
+                       xp_stream stream);
+
 /* Several int4 matvecs that share one input vector, in one launch
  * (Q/K/V, or gate/up). out_i has cols_i floats. n <= 4. */
 int xp_mv_int4_multi(uint32_t n, float* const* outs, const float* in,

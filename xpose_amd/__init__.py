@@ -141,6 +141,7 @@ def _declare(lib: C.CDLL) -> None:
         "xp_event_record": (i32, [vp, vp]),
         "xp_event_elapsed_ms": (i32, [vp, vp, P(f32)]),
         "xp_mv_int4": (i32, [vp, vp, vp, vp, i32, u32, u32, u32, vp]),
+        "xp_mv_int4_noalloc": (i32, [vp, vp, vp, vp, i32, u32, u32, u32, vp]),
         "xp_mv_int4_multi": (i32, [u32, P(vp), vp, P(vp), P(vp), P(u32), i32, u32, vp]),
         "xp_unpack_km4": (i32, [vp, vp, u32, u32, vp]),
         "xp_mv_int4_timed": (i32, [vp, vp, P(vp), P(vp), u32, i32, u32, u32, u32, u32, vp,

@@ -20,6 +20,9 @@
 #include "xp_device.hpp"
 #include "xp_launch.hpp"
 
+#include <mutex>
+#include <vector>
+
 namespace xp {
 
 constexpr int kMvWaves   = 4;   // tasks (waves) per workgroup
@@ -391,7 +394,7 @@ size_t mv_partial_floats(uint32_t rows, uint32_t total_cols, uint32_t split, int
 
 int launch_mv(const MvMatDesc* mats, uint32_t n, const float* x, int fmt, uint32_t rows,
               uint32_t split, float* partial, size_t partial_cap, uint32_t* tickets,
-              size_t tickets_cap, hipStream_t st, const char* who) {
+              size_t tickets_cap, hipStream_t st, const char* who, int n_cu_hint) {
     if (!x) return set_error(XP_E_ARG, "%s: in is null", who);
     if (reinterpret_cast<uintptr_t>(x) & 15u)
         return set_error(XP_E_ARG, "%s: in must be 16-byte aligned", who);
@@ -419,7 +422,7 @@ int launch_mv(const MvMatDesc* mats, uint32_t n, const float* x, int fmt, uint32
                        mats[i].cols, groups};
         groups += mats[i].cols / kGrp;
     }
-    int n_cu = 256;
+    int n_cu = n_cu_hint > 0 ? n_cu_hint : 256;
     DeviceScratch* sc = nullptr;
     if (!partial || !tickets) {
         sc = scratch();
@@ -494,8 +497,9 @@ int launch_mv(const MvMatDesc* mats, uint32_t n, const float* x, int fmt, uint32
             a.tickets = sc->tickets;
         } else {
             if (partial_cap < need || tickets_cap < groups)
-                return set_error(XP_E_ARG, "%s: scratch too small (%zu < %zu floats or %zu < %u "
-                                 "tickets)", who, partial_cap, need, tickets_cap, groups);
+                return set_error(XP_E_ARG, "%s: split %u of %u columns needs %zu partial floats "
+                                 "and %u tickets; the scratch holds %zu and %zu", who, a.split,
+                                 groups * kGrp, need, groups, partial_cap, tickets_cap);
             a.partial = partial;
             a.tickets = tickets;
         }
@@ -521,11 +525,78 @@ int launch_mv(const MvMatDesc* mats, uint32_t n, const float* x, int fmt, uint32
     return XP_OK;
 }
 
+// ---- allocation-free entry point -------------------------------------------------
+// Scratch of xp_mv_int4_noalloc: split-k / k-chunk partial sums (words
+// [0, kNaPartialFloats)), then the arrival tickets of the last-arrival
+// reductions (zero at rest: every kernel that takes one returns it to zero).
+// A file-scope device array, so each GPU the library runs on holds its own
+// copy (1 MiB + 16 KiB) until the process ends; host code reaches it only
+// through the address hipGetSymbolAddress returns for the current device.
+constexpr size_t   kNaPartialFloats = size_t(1) << 18;
+constexpr uint32_t kNaTickets       = 4096;
+
+}  // namespace xp
+
+static __device__ __align__(256) uint32_t scratch[xp::kNaPartialFloats + xp::kNaTickets];
+
+namespace xp {
+
+namespace {
+__global__ void zero_words_kernel(uint32_t* p, uint32_t n) {
+    const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) p[i] = 0u;
+}
+std::mutex g_na_mu;
+std::vector<MvNoAlloc> g_na;   // per device; partial == nullptr until set up
+}  // namespace
+
+int mv_noalloc_setup(hipStream_t st, bool sync, MvNoAlloc* out) {
+    int dev = 0;
+    XP_HIP(hipGetDevice(&dev));
+    std::lock_guard<std::mutex> lk(g_na_mu);
+    if (dev >= int(g_na.size())) g_na.resize(size_t(dev) + 1, MvNoAlloc{});
+    MvNoAlloc& d = g_na[size_t(dev)];
+    if (!d.partial) {
+        void* p = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(::scratch));
+        if (e != hipSuccess || !p)
+            return set_error(XP_E_HIP, "xp_mv_int4_noalloc: hipGetSymbolAddress(scratch) on device "
+                             "%d -> %s", dev, hipGetErrorString(e));
+        hipDeviceProp_t prop;
+        XP_HIP(hipGetDeviceProperties(&prop, dev));
+        uint32_t* words = static_cast<uint32_t*>(p);
+        // Tickets start at zero. A fill kernel, not a memset: the first call
+        // may be inside a caller's graph capture.
+        hipLaunchKernelGGL(zero_words_kernel, dim3((kNaTickets + 255) / 256), dim3(256), 0, st,
+                           words + kNaPartialFloats, kNaTickets);
+        XP_HIP(hipGetLastError());
+        if (sync) XP_HIP(hipStreamSynchronize(st));
+        d.partial = reinterpret_cast<float*>(words);
+        d.partial_floats = kNaPartialFloats;
+        d.tickets = words + kNaPartialFloats;
+        d.n_tickets = kNaTickets;
+        d.n_cu = prop.multiProcessorCount;
+    }
+    *out = d;
+    return XP_OK;
+}
+
 }  // namespace xp
 
 using namespace xp;
 
 extern "C" {
+
+int xp_mv_int4_noalloc(float* out, const float* in, const void* wq, const void* scales,
+                       int scale_fmt, uint32_t rows, uint32_t cols, uint32_t split,
+                       xp_stream stream) {
+    const hipStream_t st = as_stream(stream);
+    MvNoAlloc d{};
+    if (int rc = mv_noalloc_setup(st, false, &d); rc != XP_OK) return rc;
+    MvMatDesc m{out, wq, scales, cols};
+    return launch_mv(&m, 1, in, scale_fmt, rows, split, d.partial, d.partial_floats, d.tickets,
+                     d.n_tickets, st, "xp_mv_int4_noalloc", d.n_cu);
+}
 
 int xp_mv_int4(float* out, const float* in, const void* wq, const void* scales, int scale_fmt,
                uint32_t rows, uint32_t cols, uint32_t split, xp_stream stream) {

@@ -3,6 +3,7 @@
 // include/vulkore/{context,buffer,sync}.hpp) the decode path needs, reduced
 // to thin HIP calls.
 #include "xp_internal.hpp"
+#include "xp_launch.hpp"
 
 #include <cstdio>
 #include <cstring>
@@ -112,7 +113,8 @@ int xp_init(int dev) {
     if (!s) return XP_E_HIP;
     if (!ensure_tickets(s, 65536)) return XP_E_NOMEM;
     if (!ensure_partial(s, 1u << 20)) return XP_E_NOMEM;
-    return XP_OK;
+    MvNoAlloc na{};
+    return mv_noalloc_setup(nullptr, true, &na);
 }
 
 int xp_device_info(char* name, size_t cap, int* n_cu, size_t* hbm_bytes, char* arch,

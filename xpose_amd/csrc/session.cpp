@@ -222,7 +222,7 @@ int Session::record(int variant, uint32_t& n) {
                                   {k_raw, w.w[XP_T_K], w.s[XP_T_K], kvd},
                                   {v, w.w[XP_T_V], w.s[XP_T_V], kvd}};
         XP_STEP(launch_mv(qkv, 3, xb, fmt, H, 0, mv_partial, mv_partial_cap, tickets + kTicketMv,
-                          8192, st, "session qkv"));
+                          8192, st, "session qkv", n_cu));
         QkArgs qa{q, k, q_raw, k_raw, v, w.norm[4], w.norm[5], w.kc, w.vc,
                   c.n_heads, c.n_kv_heads, c.head_dim, eps, state, 0};
         XP_STEP(launch_qk(qa, theta, st));
@@ -239,23 +239,23 @@ int Session::record(int variant, uint32_t& n) {
         XP_STEP(launch_attention(aa, max_span, st));
         const MvMatDesc o{xb2, w.w[XP_T_O], w.s[XP_T_O], H};
         XP_STEP(launch_mv(&o, 1, att, fmt, qd, 0, mv_partial, mv_partial_cap, tickets + kTicketMv,
-                          8192, st, "session o_proj"));
+                          8192, st, "session o_proj", n_cu));
         XP_STEP(launch_norm_res_norm(x, xb2, w.norm[1], w.norm[2], xb, H, eps, st));
         const MvMatDesc gu[2] = {{gate, w.w[XP_T_GATE], w.s[XP_T_GATE], c.ffn},
                                  {up, w.w[XP_T_UP], w.s[XP_T_UP], c.ffn}};
         XP_STEP(launch_mv(gu, 2, xb, fmt, H, 0, mv_partial, mv_partial_cap, tickets + kTicketMv,
-                          8192, st, "session gate/up"));
+                          8192, st, "session gate/up", n_cu));
         XP_STEP(xp_geglu(hb, gate, up, c.ffn, st));
         const MvMatDesc d{xb2, w.w[XP_T_DOWN], w.s[XP_T_DOWN], H};
         XP_STEP(launch_mv(&d, 1, hb, fmt, c.ffn, 0, mv_partial, mv_partial_cap,
-                          tickets + kTicketMv, 8192, st, "session down"));
+                          tickets + kTicketMv, 8192, st, "session down", n_cu));
         const float* next = (l + 1 < c.n_layers) ? L[l + 1].norm[0] : final_norm;
         XP_STEP(launch_norm_res_norm(x, xb2, w.norm[3], next, xb, H, eps, st));
     }
     if (variant >= 1) {
         const MvMatDesc lm{logits, lm_w, lm_s, c.vocab};
         XP_STEP(launch_mv(&lm, 1, xb, fmt, H, 0, mv_partial, mv_partial_cap, tickets + kTicketMv,
-                          8192, st, "session lm_head"));
+                          8192, st, "session lm_head", n_cu));
         if (variant == 1)
             XP_STEP(launch_argmax(state + 1, am_out, logits, c.vocab, am_val, am_idx,
                                   tickets + kTicketAm, st));

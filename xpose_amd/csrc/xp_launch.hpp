@@ -34,9 +34,22 @@ struct MvMatDesc {
 };
 // Partial floats a call with these shapes needs for a given split (0 = auto).
 size_t mv_partial_floats(uint32_t rows, uint32_t total_cols, uint32_t split, int n_cu);
+// With caller-provided partial and ticket buffers, n_cu is the CU count the
+// plan is made for (0: 256); without them the library's scratch is used.
 int launch_mv(const MvMatDesc* mats, uint32_t n, const float* x, int fmt, uint32_t rows,
               uint32_t split, float* partial, size_t partial_cap, uint32_t* tickets,
-              size_t tickets_cap, hipStream_t st, const char* who);
+              size_t tickets_cap, hipStream_t st, const char* who, int n_cu = 0);
+// Set-up of the allocation-free matvec entry point on the current device:
+// the device address of its fixed scratch (partial sums, then tickets), its
+// tickets cleared once by a fill kernel on `st` (synchronised when `sync`).
+struct MvNoAlloc {
+    float*    partial;
+    size_t    partial_floats;
+    uint32_t* tickets;
+    size_t    n_tickets;
+    int       n_cu;
+};
+int mv_noalloc_setup(hipStream_t st, bool sync, MvNoAlloc* out);
 
 // ---- repacked native-format matvec (xp_mv_rq) ----
 int launch_mv_rq(float* out, const float* x, const xp_rq_tensor& w, uint32_t split,
