@@ -527,12 +527,14 @@ int setup_token(Session& s) {
     a.state = s.state;
     a.hist = s.hist;
     // Workgroup placement: the kernel groups producers and consumers by XCD
-    // when every workgroup w sits on the XCD of w % 8 and workgroups 0..7 are
-    // on eight different XCDs. Anything else (a failed probe, or
-    // XP_PLACE_DEVICE) keeps every exchange device-coherent.
+    // when the probe found the grid dealt to eight distinct XCDs in turn
+    // (workgroup w on the XCD of w % 8); the kernel then takes each
+    // workgroup's role from the XCD it runs on, since a launch's starting XCD
+    // varies. Anything else (XP_PLACE_DEVICE, another layout) keeps every
+    // exchange device-coherent.
     a.xcd_local = 0;
     a.xcd_ids = 0;
-    if (c.placement == XP_PLACE_AUTO && grid >= 8) {
+    if (c.placement == XP_PLACE_AUTO && grid >= 8 && grid % 8 == 0) {
         auto xcc = [&](uint32_t w) { return probe[w] & 0xFFu; };
         bool periodic = true;
         for (uint32_t w = 0; w < grid; ++w) periodic &= xcc(w) == xcc(w % 8);
@@ -568,9 +570,9 @@ int check_status(Session& s) {
         // Later launches exchange every value through the device coherence
         // point (as XP_PLACE_DEVICE does).
         s.ta.xcd_local = 0;
-        return set_error(XP_E_DEVICE, "token kernel: the workgroup -> XCD placement changed since "
-                         "the session's probe (status %u); XCD-local exchange is now off. The "
-                         "step's results and KV rows are invalid: set a position to go on", st);
+        return set_error(XP_E_DEVICE, "token kernel: a workgroup ran on an XCD the session's "
+                         "probe never saw (status %u); XCD-local exchange is now off. The step's "
+                         "results and KV rows are invalid: set a position to go on", st);
     }
     if (st != 0)
         return set_error(XP_E_DEVICE, "token kernel: a wait for another workgroup's data ran "

@@ -223,18 +223,18 @@ __device__ __forceinline__ void own_put(rsrc_t r, uint32_t soff, uint32_t s0, co
     for (uint32_t j = 0; j < kOwnP; ++j) ll_st2(r, (s0 + 2u * j) * 8u, soff, x[2 * j], x[2 * j + 1], tag);
 }
 
-__device__ __forceinline__ void tk_trace(const TokArgs& a, uint32_t event) {
+__device__ __forceinline__ void tk_trace(const TokArgs& a, uint32_t wg, uint32_t event) {
     if (a.trace && threadIdx.x == 0)
-        a.trace[size_t(event) * gridDim.x + blockIdx.x] = __builtin_amdgcn_s_memrealtime();
+        a.trace[size_t(event) * gridDim.x + wg] = __builtin_amdgcn_s_memrealtime();
 }
 // Stage end of layer l, stage k (event 1 + 6 l + k) and the time this
 // workgroup's inputs of that stage had all arrived (event 3 + 6 n_layers +
 // 6 l + k; 0 when the workgroup had no work in the stage).
-__device__ __forceinline__ void tk_trace_stage(const TokArgs& a, uint32_t l, uint32_t k,
+__device__ __forceinline__ void tk_trace_stage(const TokArgs& a, uint32_t wg, uint32_t l, uint32_t k,
                                                unsigned long long t_in) {
     if (a.trace && threadIdx.x == 0) {
-        a.trace[size_t(1u + 6u * l + k) * gridDim.x + blockIdx.x] = __builtin_amdgcn_s_memrealtime();
-        a.trace[size_t(3u + 6u * a.n_layers + 6u * l + k) * gridDim.x + blockIdx.x] = t_in;
+        a.trace[size_t(1u + 6u * l + k) * gridDim.x + wg] = __builtin_amdgcn_s_memrealtime();
+        a.trace[size_t(3u + 6u * a.n_layers + 6u * l + k) * gridDim.x + wg] = t_in;
     }
 }
 __device__ __forceinline__ unsigned long long tk_now(const TokArgs& a) {
@@ -440,11 +440,33 @@ __global__ __launch_bounds__(kTkThreads) void token_kernel(TokArgs a) {
     uint32_t tid = threadIdx.x;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(tid / kWave);
     uint32_t lane = tid % kWave;
-    const uint32_t wg   = blockIdx.x;
+    // The workgroup's role id. With the XCD-local exchange on, role w must
+    // run on the XCD the host's probe found residue w % 8 on. The hardware
+    // deals a launch's workgroups to the eight XCDs in a fixed cyclic order,
+    // but the XCD it starts from moves between launches (measured), so each
+    // workgroup takes, within its aligned group of eight, the slot of the
+    // XCD it actually runs on: a bijection whenever each aligned group of
+    // eight covers the eight XCDs. A workgroup on an XCD the probe never saw
+    // reports status bit 2 at once (every wait then gives up), and the host
+    // stops using the XCD-local exchange.
     const uint32_t nwg  = gridDim.x;
+    uint32_t wg = blockIdx.x;
+    bool on_xcd = true;
+    if (a.xcd_local) {
+        const uint32_t x = xcc_id();
+        uint32_t slot = 8u;
+#pragma unroll
+        for (uint32_t r = 0; r < 8u; ++r)
+            if (((a.xcd_ids >> (4u * r)) & 15u) == x) slot = r;
+        on_xcd = slot < 8u;
+        if (on_xcd) wg = (wg & ~7u) | slot;
+        else if (tid == 0)
+            __hip_atomic_fetch_or((XP_GLOBAL uint32_t*)(a.state + 2), 2u, __ATOMIC_RELAXED,
+                                  __HIP_MEMORY_SCOPE_AGENT);
+    }
     const uint32_t tag  = a.tag;
     const float    eps  = a.eps;
-    tk_trace(a, 0);
+    tk_trace(a, wg, 0);
 
     const uint32_t pos = a.state[0];
     uint32_t tok = a.state[1];
@@ -503,17 +525,6 @@ __global__ __launch_bounds__(kTkThreads) void token_kernel(TokArgs a) {
     }
     const uint32_t t_gu = (wg + nwg - off_gu) % nwg, t_dn = wg;
     bool hown = tid < Sh::HO;                     // owns kOwn elements of a hidden vector
-    // This workgroup is on the XCD the host found its residue class on (else
-    // its XCD-local results go through the device coherence point).
-    const bool on_xcd = xcc_id() == ((a.xcd_ids >> (4u * (wg % 8u))) & 15u);
-    // The XCD-local stages (local layers' attention and combine) run on the
-    // workgroups grid - 1 - 8 s and exchange through one XCD's L2, which a
-    // workgroup placed elsewhere cannot see. Such a placement change is
-    // reported as status bit 2 at once (every wait then gives up), not as a
-    // spin-limit failure; the host then stops using the XCD-local exchange.
-    if (a.xcd_local && !on_xcd && (nwg - 1u - wg) % 8u == 0u && tid == 0)
-        __hip_atomic_fetch_or((XP_GLOBAL uint32_t*)(a.state + 2), 2u, __ATOMIC_RELAXED,
-                              __HIP_MEMORY_SCOPE_AGENT);
 
     // x entering layer l (l > 0) from layer l - 1's slots, in owner registers:
     // xb + post_ffw_norm(sum of the down chunks, in chunk order).
@@ -644,7 +655,7 @@ __global__ __launch_bounds__(kTkThreads) void token_kernel(TokArgs a) {
             // memory counter also waits for its stores.
             if (t < Sh::NOG && tid / (kGrp / kOwn) == t) own_put(rr, soff, uint32_t(lay.xa) + kOwn * tid, x, tag);
         }
-        tk_trace_stage(a, l, 0u, t_in);
+        tk_trace_stage(a, wg, l, 0u, t_in);
         t_in = 0;
 
         // ================= attention =================
@@ -892,7 +903,7 @@ __global__ __launch_bounds__(kTkThreads) void token_kernel(TokArgs a) {
             if (cw == 16u) attend(std::integral_constant<uint32_t, 16u>{});
             else attend(std::integral_constant<uint32_t, kTkC>{});
         }
-        tk_trace_stage(a, l, 1u, t_in);
+        tk_trace_stage(a, wg, l, 1u, t_in);
         t_in = 0;
 
         // ================= combine =================
@@ -951,7 +962,7 @@ __global__ __launch_bounds__(kTkThreads) void token_kernel(TokArgs a) {
             }
             __syncthreads();
         }
-        tk_trace_stage(a, l, 2u, t_in);
+        tk_trace_stage(a, wg, l, 2u, t_in);
         t_in = 0;
 
         // ================= O projection =================
@@ -978,7 +989,7 @@ __global__ __launch_bounds__(kTkThreads) void token_kernel(TokArgs a) {
             const float y = tile_dot<FMT>(p, S, c * nb, nb, wave, lane);
             if (wave == 0) tile_put(rr, soff, uint32_t(lay.o) + c * H + g * kGrp, y, lane, tag);
         }
-        tk_trace_stage(a, l, 3u, t_in);
+        tk_trace_stage(a, wg, l, 3u, t_in);
         t_in = 0;
 
         // ================= gate / up =================
@@ -1040,7 +1051,7 @@ __global__ __launch_bounds__(kTkThreads) void token_kernel(TokArgs a) {
             // x after the attention block, for the next layer: spread and stored last, as xa
             if (t < Sh::NOG && tid / (kGrp / kOwn) == t) own_put(rr, soff, uint32_t(lay.xb) + kOwn * tid, x, tag);
         }
-        tk_trace_stage(a, l, 4u, t_in);
+        tk_trace_stage(a, wg, l, 4u, t_in);
         t_in = 0;
 
         // ================= down =================
@@ -1072,7 +1083,7 @@ __global__ __launch_bounds__(kTkThreads) void token_kernel(TokArgs a) {
             if (wave == 0) tile_put(rr, soff, uint32_t(lay.dnp) + c * H + g * kGrp, y, lane, tag);
         }
         if (t_dn >= Sh::N_DN && l + 1u < a.n_layers && t_qkv < Sh::N_QKV) prefetch_qkv(pq, l + 1u, t_qkv);
-        tk_trace_stage(a, l, 5u, t_in);
+        tk_trace_stage(a, wg, l, 5u, t_in);
     }
 
     if (!a.want_logits) {
@@ -1153,7 +1164,7 @@ __global__ __launch_bounds__(kTkThreads) void token_kernel(TokArgs a) {
         for (int w = 1; w < kTkWaves; ++w) am_better(bv, bi, S.amv[w], S.ami[w]);
         ll_st2(rr, 16u * wg, am_off, bv, __uint_as_float(bi), tag);
     }
-    tk_trace(a, 1u + 6u * a.n_layers);
+    tk_trace(a, wg, 1u + 6u * a.n_layers);
     if (wg != 0) return;
     __syncthreads();   // tid 0 has read S.amv
     bv = -INFINITY;
@@ -1183,7 +1194,7 @@ __global__ __launch_bounds__(kTkThreads) void token_kernel(TokArgs a) {
         a.state[3] = bi;
         reinterpret_cast<float*>(a.state)[4] = bv;
     }
-    tk_trace(a, 2u + 6u * a.n_layers);
+    tk_trace(a, wg, 2u + 6u * a.n_layers);
 }
 
 namespace {

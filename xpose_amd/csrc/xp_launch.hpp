@@ -229,10 +229,12 @@ struct TokArgs {
     uint32_t tag;                         // this launch's tag (never 0)
     uint32_t want_logits;                 // 0: prefill pass without the lm_head
     uint32_t greedy;                      // 1: the argmax becomes the next token
-    // Non-zero when every workgroup w was found on the XCD of w % 8, whose
-    // hardware XCC id is nibble w % 8 of xcd_ids: a local layer's attention
-    // and combine then run on one XCD (workgroups grid - 1 - 8 s) and
-    // exchange through its L2 instead of the device coherence point.
+    // Non-zero when the probe found the grid dealt to eight distinct XCDs in
+    // turn; nibble r of xcd_ids is the hardware XCC id of residue r. Each
+    // workgroup then takes the role id whose residue is its own XCD's (the
+    // starting XCD of a launch varies), and a local layer's attention and
+    // combine run on one XCD (roles grid - 1 - 8 s) and exchange through its
+    // L2 instead of the device coherence point.
     uint32_t xcd_local;
     uint32_t xcd_ids;
 };
