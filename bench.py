@@ -46,6 +46,9 @@ HBM_PEAK_GBS = 8000.0          # MI355X HBM3E
 # FETCH_SIZE x 2.0 + WRITE_SIZE x 1.0 (factors from a 256 MiB copy), see
 # profiles/token_kernel_gemma3_1b_ctx4096.md.
 TOKEN_TRAFFIC_BYTES = 692_586_812 + 18_097_216
+TRAFFIC_SOURCE = ("rocprofv3 --pmc FETCH_SIZE and --pmc WRITE_SIZE of this bench's token step "
+                  "(profiles/token_kernel_gemma3_1b_ctx4096.md), scaled by a 256 MiB copy's "
+                  "readings; a constant of this build, not counted in this run")
 SEED = 0x5EED0003
 # Algorithmic HBM bytes of one token at seq_len s (weights + fp16 scales,
 # KV reads, norm weights, logits write + argmax read, KV append).
@@ -149,6 +152,49 @@ def stream_ceiling(X, nbytes: int = 1 << 30, iters: int = 20) -> float:
     ms = C.c_float()
     X.call("xp_stream_read_timed", buf.vp, nbytes, iters, None, C.byref(ms))
     return nbytes * iters / (ms.value / 1e3) / 1e9
+
+
+def same_size_ceiling(X, nbytes: int, copies: int = 64, iters: int = 640):
+    """The streaming probe at the matvec's own size, back to back over
+    `copies` buffers (> 256 MiB together, so HBM serves them), at the grid
+    that measured fastest at 4.5 MB (512 workgroups), and the launch floor
+    (the same loop reading 16 bytes per thread): us per launch each."""
+    nb = nbytes // 16 * 16
+    bufs = [X.DeviceBuffer(nb) for _ in range(copies)]
+    for b in bufs:
+        X.call("xp_memset", b.vp, 1, nb)
+    P = (C.c_void_p * copies)(*[b.ptr for b in bufs])
+    ms = C.c_float()
+    X.call("xp_stream_read_rot_timed", P, copies, nb, 512, iters, None, C.byref(ms))
+    ceil_us = ms.value * 1e3 / iters
+    X.call("xp_stream_read_rot_timed", P, copies, 16 * 512 * 256, 256, iters, None, C.byref(ms))
+    floor_us = ms.value * 1e3 / iters
+    for b in bufs:
+        b.close()
+    return ceil_us, floor_us
+
+
+def graph_leg(X, ctx: int, steps: int = 32):
+    """The same decode on the captured-graph path (per-op kernels), tok/s."""
+    cfg = X.XpConfig.gemma3_1b(max_seq=8192, exec_mode=X.XP_EXEC_GRAPH)
+    sess = X.DecodeSession(cfg)
+    sess.synthesize(SEED)
+    kvd = cfg.n_kv_heads * cfg.head_dim
+    for l in range(cfg.n_layers):
+        sess.kv_upload(l, 0, 0, X.synth_normal_f16(ctx * kvd, ctx, 2 * l))
+        sess.kv_upload(l, 1, 0, X.synth_normal_f16(ctx * kvd, ctx, 2 * l + 1))
+    sess.set_position(ctx)
+    sess.prefill([4242])
+    sess.decode_steps(4)
+    X.synchronize()
+    t0 = time.perf_counter()
+    sess.decode_steps(steps)
+    X.synchronize()
+    el = time.perf_counter() - t0
+    launches = sess.last_metrics().launches
+    sess.close()
+    return {"tok_s": round(steps / el, 1), "ms_per_step": round(el * 1e3 / steps, 4),
+            "launches_per_step": launches}
 
 
 def attention_leg(X, span: int, iters: int = 192):
@@ -408,6 +454,7 @@ def main() -> int:
         extra["cfg5"] = cfg5_leg(X, bsess, scfg)
         bsess.close()
         extra["native"] = native_leg(X)
+        extra["graph_path"] = graph_leg(X, ctx)
     sess.close()
 
     # Roofline leg: the dominant kernel of the step, the lm_head int4 matvec.
@@ -416,15 +463,22 @@ def main() -> int:
     # benchmark config 1 shape (gate 6912 x 1152), 64 rotating copies.
     nb1, per1 = matvec_leg(X, 1152, 6912, copies=64, iters=640)
     ceil = stream_ceiling(X)
+    ceil1_us, floor_us = same_size_ceiling(X, nb1)
 
     cpu = None
     if not args.no_cpu:
-        threads = min(16, os.cpu_count() or 1)
+        # Every host core this process may run on, capped by OMP_NUM_THREADS
+        # when the host sets it (the GPU box gives one GPU's job 16 threads).
+        affinity = len(os.sched_getaffinity(0))
+        omp = int(os.environ.get("OMP_NUM_THREADS", "0") or 0)
+        threads = min(affinity, omp) if omp > 0 else affinity
         cpu_tok_s, n_cpu, cpu_el = cpu_baseline(X, cfg, ctx, args.cpu_seconds, threads)
         cpu = {"value": round(cpu_tok_s, 3), "unit": "tok/s", "cores": threads, "kind": "port",
+               "host_cpus_affinity": affinity, "omp_num_threads": omp or None,
                "sample": f"{n_cpu} greedy decode steps of the same Gemma-3-1B int4 model from "
                          f"position {ctx + 1} (KV pre-filled), oracle C restatement, "
-                         f"{threads} OpenMP threads, {cpu_el:.1f} s"}
+                         f"{threads} OpenMP threads ({affinity} CPUs in this process's "
+                         f"affinity mask), {cpu_el:.1f} s"}
 
     line = {
         "metric": "decode tok/s Gemma-3-1B int4 bs=1 @ctx 4096; int4 matvec HBM GB/s vs peak",
@@ -437,7 +491,11 @@ def main() -> int:
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f32",
+        "dtype": "int4w-fix20a-f32acc",
+        "arithmetic": "int4 weights with fp16 group-32 scales; each 32-block dot product exact in "
+                      "int32 against the activations as 20-bit block fixed point (|x - s q| <= "
+                      "2^-19 max|x| per block), scaled and accumulated in fp32; norms, RoPE, "
+                      "attention, softmax, GeGLU fp32; KV cache fp16",
         "data": "synthetic (random int4 weights, fp16 group-32 scales, fp16 KV N(0,1))",
         "config": {"workload": "gemma3-1b-int4-greedy-decode", "ctx": ctx, "batch": 1,
                    "layers": 26, "hidden": 1152, "vocab": 262144, "weights": "int4 g32 + fp16",
@@ -446,7 +504,8 @@ def main() -> int:
         "roofline": {"bound": "hbm", "kernel": "token_kernel (whole decode token)",
                      "achieved": round(tb / kern_s / 1e9, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(tb / kern_s / 1e9 / HBM_PEAK_GBS, 4),
-                     "traffic": TOKEN_TRAFFIC_BYTES, "bytes_per_launch": tb,
+                     "traffic": TOKEN_TRAFFIC_BYTES,
+                     "traffic_source": TRAFFIC_SOURCE, "bytes_per_launch": tb,
                      "us_per_launch": round(kern_s * 1e6, 3),
                      "roofline_tok_s": round(HBM_PEAK_GBS * 1e9 / tb, 1)},
         "matvec_lm_head": {"shape": "262144x1152", "bytes": nbytes,
@@ -457,7 +516,12 @@ def main() -> int:
         "matvec_cfg1": {"shape": "6912x1152", "bytes": nb1, "us_per_launch": round(per1 * 1e6, 3),
                         "GBs": round(nb1 / per1 / 1e9, 1),
                         "frac": round(nb1 / per1 / 1e9 / HBM_PEAK_GBS, 4),
-                        "frac_of_stream_ceiling": round(nb1 / per1 / 1e9 / ceil, 4)},
+                        "frac_of_stream_ceiling": round(nb1 / per1 / 1e9 / ceil, 4),
+                        "same_size_stream_us": round(ceil1_us, 3),
+                        "launch_floor_us": round(floor_us, 3),
+                        "frac_of_same_size_stream": round(ceil1_us / (per1 * 1e6), 4),
+                        "note": "back-to-back launches; a launch that reads 16 B per thread "
+                                "takes launch_floor_us, which bounds any kernel of this size"},
         "cpu_baseline": cpu,
         **extra,
         "device": info["arch"],

@@ -6,8 +6,8 @@
  * negative XP_E* code; xp_last_error() then holds a message that names the
  * entry point and the offending argument (the reference throws
  * std::runtime_error with the kernel name, examples/llm/decode.cpp:46-56;
- * here the C++ wrapper in xpose_amd/csrc/session.hpp turns the code back into
- * that exception).
+ * here the C++ wrapper in include/xpose.hpp turns the code back into that
+ * exception).
  *
  * Threading: like the reference Context (agent-docs/vulkore-core.md:76) the
  * library is single-threaded per device. Scratch owned by the library (split-k
@@ -90,9 +90,11 @@ int xp_event_elapsed_ms(xp_event start, xp_event stop, float* ms);
  * (0 = choose); chunks are whole scale quads; split > 1 sums the chunks in
  * ascending order (deterministic). With split = 0 and quad scale planes, a
  * shape narrower than eight waves per CU instead runs one workgroup per
- * (column group, k-chunk of <= 16 quads, <= 8 chunks), its eight waves'
- * partials summed in wave order, then the chunks in chunk order
- * (deterministic). out must not alias in. */
+ * (column group, column slice of 64/S columns, S = 2 for >= 64 groups else
+ * 4) over all of k when k <= 8192, or else one per (column group, k-chunk of
+ * <= 16 quads, <= 8 chunks); the eight waves' partials are summed in wave
+ * order, then the chunks in chunk order (deterministic). out must not alias
+ * in. */
 int xp_mv_int4(float* out, const float* in, const void* wq, const void* scales,
                int scale_fmt, uint32_t rows, uint32_t cols, uint32_t split,
                xp_stream stream);
@@ -146,6 +148,12 @@ int xp_fp16_decode(float* out, const uint16_t* src, uint32_t n, xp_stream stream
  * counters. */
 int xp_stream_read_timed(const void* buf, size_t bytes, uint32_t iters, xp_stream stream,
                          float* ms);
+/* The same probe over `nbufs` buffers of `bytes` each, launch i reading
+ * buffer i % nbufs with `grid` workgroups of 512 threads (0 = one per CU),
+ * each a contiguous chunk: the streaming ceiling at a given size when the
+ * buffers together exceed the 256 MiB Infinity Cache. */
+int xp_stream_read_rot_timed(const void* const* bufs, uint32_t nbufs, size_t bytes, uint32_t grid,
+                             uint32_t iters, xp_stream stream, float* ms);
 int xp_copy(void* dst, const void* src, size_t bytes, xp_stream stream);
 
 /* Two-pass Gemma RMSNorm in one launch: out = in * rsqrt(mean(in^2)+eps) *

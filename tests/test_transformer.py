@@ -248,8 +248,11 @@ def run_attention(xp, q, kb, vb, span, kv0, scale):
 
 @pytest.mark.gpu
 @pytest.mark.parametrize("seq,kv0", [(131, 0), (131, 43), (1, 0), (512, 0), (513, 1),
-                                     (4097, 0), (8192, 0), (8192, 7680)])
+                                     (1100, 0), (2047, 0), (4097, 0), (8192, 0), (8192, 7680)])
 def test_gpu_attention(xp, xo, seq, kv0):
+    """Spans 1..8192: up to 256 splits of at least 32 keys, combined in one
+    level (at most 16 splits) or two (groups of 16; 1100 keys: 35 splits,
+    the last group of 3; 4097: 129 splits, the last group of 1)."""
     print(f"case attention seq={seq} kv0={kv0}", flush=True)
     r = rng()
     q = u(r, HEADS * HEAD_DIM)
@@ -261,6 +264,9 @@ def test_gpu_attention(xp, xo, seq, kv0):
     got = run_attention(xp, q, kb, vb, span, kv0, scale)
     ok, msg = allclose_report(got, want, RTOL, 1e-5)
     assert ok, msg
+    # the combine sums in a fixed order: the same call gives the same bits
+    again = run_attention(xp, q, kb, vb, span, kv0, scale)
+    assert np.array_equal(got.view(np.uint32), again.view(np.uint32))
     if kv0:
         # Negative control (kernel_tests.cpp:538-552): ignoring kv_start gives
         # a measurably different answer, so the check above can see it.

@@ -58,11 +58,12 @@ def test_gpu_noalloc_matvec_equals_library_entry(xp, xo):
 @pytest.mark.gpu
 def test_gpu_noalloc_matvec_limits(xp, xo):
     X = xp
-    # A shape whose k-chunk plan needs more partials than the fixed scratch
-    # (4 chunks x 1025 groups x 64 = 262,400 floats > 262,144): the split-k
-    # plan (2 chunks) instead; the library entry keeps the k-chunk plan.
-    print("case noalloc fallback 6912 x 65600", flush=True)
-    rows, cols = 6912, 65600
+    # A shape too deep for column slices (k 16384) whose k-chunk plan needs
+    # more partials than the fixed scratch (8 chunks x 600 groups x 64 =
+    # 307,200 floats > 262,144): the split-k plan (4 chunks) instead; the
+    # library entry keeps the k-chunk plan.
+    print("case noalloc fallback 16384 x 38400", flush=True)
+    rows, cols = 16384, 38400
     wq, sc, x = synth_case(X, rows, cols, seed=11)
     a = run_na(X, wq, sc, x, rows, cols, 0)
     b = run_mv(X, wq, sc, x, rows, cols, 0)

@@ -292,7 +292,7 @@ int make_batch(const xp_session* weights, uint32_t n_seq, uint32_t max_seq, bool
         size_t(kmax / kBlkB) * 2 * 64 * 16,                      // staged operand
         size_t(kmax / kBlkB) * 16 * 4,                           // block sums
         std::max<size_t>(part_cap, 1) * 4, size_t(tick) * 4,
-        size_t(B) * b.attn_part_seq * 4 + 4, size_t(B) * c.n_kv_heads * 4,
+        size_t(B) * b.attn_part_seq * 4 + 4, size_t(B) * c.n_kv_heads * kAttnTicketsPerHead * 4,
         size_t(B) * kHarvest * 4, size_t(B) * kHarvest * 4,
         size_t(B) * kCand * 4, size_t(B) * kCand * 4, size_t(B) * 4, size_t(B) * 4};
     size_t total = 0;

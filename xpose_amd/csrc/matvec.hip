@@ -339,6 +339,110 @@ __global__ __launch_bounds__(kMvWgWaves * kWave) void mv_int4_wg_kernel(MvArgs a
     if (lane == 0) st_dev(&a.tickets[gg], 0u);
 }
 
+// Column-slice workgroups: workgroup (column group g, slice h of S)
+// computes the 64 / S columns 64 g + h 64 / S ... of all of k. Lane l of a
+// wave takes column l % (64 / S) of the slice and block slot l / (64 / S) of
+// each S-block step, so one wave load is S contiguous runs of 1024 / S
+// bytes, and the grid holds S times as many workgroups as column groups
+// (config 1: 108 groups, 216 workgroups at S = 2). Every workgroup stages
+// all of x (at most 256 blocks, two staging tasks per thread); the eight
+// waves take steps w, w + 8, ... (at most kMvSliceRounds each); their sums
+// meet in LDS and are added in wave, then slot order (deterministic). No
+// partials, no ticket: one HBM round trip, where a k-chunk plan's last
+// arrival adds a ticket and a partial-sum round trip (measured on MI355X:
+// q 1152 x 1024 2.9 us per launch against 5.7). Quad scale planes only.
+constexpr uint32_t kMvSliceRounds = 8;
+constexpr uint32_t kMvSliceMaxBlk = 256;
+
+template <int FMT, int S, int R>
+__global__ __launch_bounds__(kMvWgWaves * kWave) void mv_int4_slice_kernel(MvArgs a) {
+    constexpr uint32_t CPS = kGrp / S;                                 // columns per slice
+    static_assert(R >= 1 && R <= int(kMvSliceRounds), "steps per wave");
+    extern __shared__ QxBlock smem_qx[];
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+    const uint32_t lane = threadIdx.x % kWave;
+    const uint32_t gg = blockIdx.x / S, h = blockIdx.x % S;
+    const uint32_t nblk = a.nblk, nsteps = (nblk + S - 1) / S;
+    QxBlock* qx = smem_qx;
+    float* sx = reinterpret_cast<float*>(smem_qx + nblk);
+    float* red = sx + nblk;   // [kMvWgWaves][64]
+    uint32_t mi = 0;
+#pragma unroll
+    for (int i = 1; i < kMvMaxMats; ++i)
+        if (uint32_t(i) < a.n_mats && gg >= a.m[i].grp0) mi = uint32_t(i);
+    float*       out = a.m[0].out;
+    const u32x4* wq  = a.m[0].wq;
+    const void*  sc  = a.m[0].sc;
+    uint32_t cols = a.m[0].cols, grp0 = 0;
+#pragma unroll
+    for (int i = 1; i < kMvMaxMats; ++i) {
+        if (uint32_t(i) == mi) {
+            out = a.m[i].out; wq = a.m[i].wq; sc = a.m[i].sc; cols = a.m[i].cols; grp0 = a.m[i].grp0;
+        }
+    }
+    const uint32_t gl = gg - grp0, c = h * CPS + lane % CPS, bs = lane / CPS;
+    const uint32_t j = gl * kGrp + c;
+    const u32x4* wp = wq + size_t(gl) * nblk * kGrp + c;
+    // all of x, staging tasks (8 elements each) i and i + 512 of thread i
+    // (the second only past 128 blocks), loaded ahead of the weights
+    constexpr uint32_t NT = kMvWgWaves * kWave;
+    constexpr uint32_t NX = uint32_t(R) * kMvWgWaves * S > 128u ? 2u : 1u;
+    const float4* x4 = reinterpret_cast<const float4*>(a.x);
+    const uint32_t ntask = nblk * 4u;
+    float4 xv[NX][2];
+#pragma unroll
+    for (uint32_t k = 0; k < NX; ++k) {
+        const uint32_t i = threadIdx.x + k * NT;
+        xv[k][0] = xv[k][1] = float4{0.0f, 0.0f, 0.0f, 0.0f};
+        if (i < ntask) {
+            xv[k][0] = x4[2 * i];
+            xv[k][1] = x4[2 * i + 1];
+        }
+    }
+    // step t = wave + 8 r covers blocks S t .. S t + S - 1; this lane's block
+    // is S t + bs, clamped (and weighted by zero) past the end
+    u32x4 w[R];
+    uint32_t sw[R];
+    const uint32_t* sc32 = static_cast<const uint32_t*>(sc);
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        // steps past the end load a valid block (clamped) and weigh it by zero
+        const uint32_t t = min(wave + uint32_t(kMvWgWaves) * r, nsteps - 1u);
+        const uint32_t b = min(t * S + bs, nblk - 1u);
+        w[r] = ld_stream4(wp + size_t(b) * kGrp);
+        // the 32-bit word holding scale b % 4 of quad b / 4 of column j
+        sw[r] = __builtin_nontemporal_load(sc32 + (size_t(b >> 2) * cols + j) * 2u +
+                                           ((b >> 1) & 1u));
+    }
+#pragma unroll
+    for (uint32_t k = 0; k < NX; ++k) {
+        const uint32_t i = threadIdx.x + k * NT;
+        if (i < ntask) stage_x8(qx, sx, i, xv[k][0], xv[k][1]);
+    }
+    __syncthreads();
+    float acc = 0.0f;
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        const uint32_t t = wave + uint32_t(kMvWgWaves) * r, b = t * S + bs;
+        if (t < nsteps) {
+            const uint32_t bb = min(b, nblk - 1u);
+            const uint32_t hb = (sw[r] >> (16u * (bb & 1u))) & 0xFFFFu;
+            const float scale = FMT == XP_SCALE_F16_QUAD ? f16_bits_to_f32(hb) : __uint_as_float(hb << 16);
+            const float f = b < nblk ? scale * sx[bb] : 0.0f;
+            acc = fmaf(f, float(block_dot(w[r], qx[bb])), acc);
+        }
+    }
+    red[wave * kGrp + lane] = acc;
+    __syncthreads();
+    if (wave != 0 || lane >= CPS) return;
+    float y = 0.0f;
+#pragma unroll
+    for (uint32_t v = 0; v < uint32_t(kMvWgWaves); ++v)
+#pragma unroll
+        for (uint32_t q = 0; q < uint32_t(S); ++q) y += red[v * kGrp + q * CPS + lane];
+    out[j] = y;
+}
+
 __global__ void unpack_km4_kernel(int8_t* out, const u32x4* wq, uint32_t rows, uint32_t cols) {
     const uint32_t j = blockIdx.x * blockDim.x + threadIdx.x;   // column
     const uint32_t b = blockIdx.y;                              // block
@@ -441,6 +545,43 @@ int launch_mv(const MvMatDesc* mats, uint32_t n, const float* x, int fmt, uint32
     // quads. A caller-provided partial buffer too small for that plan keeps
     // the split-k plan it was sized for.
     if (split == 0 && fmt != XP_SCALE_F32 && groups < uint32_t(n_cu) * 8u) {
+        // Column slices when each workgroup can hold its column group's whole
+        // k (at most kMvSliceRounds steps per wave): two per group for wide
+        // shapes (>= 64 groups; config 1: 216 workgroups), four for narrow
+        // ones. Measured per launch on MI355X (back to back, 2.8 us launch
+        // floor): config 1 3.3 us (one workgroup per group: 3.9), q 2.9 us,
+        // o 2.9 us (k-chunks with a last-arrival sum: 5.7, 6.1).
+        uint32_t S = groups >= 64 ? 2u : 4u;
+        while (S < 4u && (nblk + S - 1) / S > kMvWgWaves * kMvSliceRounds) S *= 2u;
+        if (nblk <= kMvSliceMaxBlk && (nblk + S - 1) / S <= kMvWgWaves * kMvSliceRounds) {
+            a.split = 1;
+            a.qpc = a.nquads;
+            const size_t lds = size_t(nblk) * (sizeof(QxBlock) + sizeof(float)) +
+                               size_t(kMvWgWaves) * kGrp * sizeof(float);
+            const dim3 grid(groups * S), block(kMvWgWaves * kWave);
+            // steps per wave, rounded up to 1, 2, 4 or 8 (one instance each)
+            const uint32_t need = ((nblk + S - 1) / S + kMvWgWaves - 1) / kMvWgWaves;
+            const uint32_t R = need <= 1 ? 1 : need <= 2 ? 2 : need <= 4 ? 4 : 8;
+#define XP_MV_SLICE_R(F, SS)                                                                         \
+    if (R == 1) hipLaunchKernelGGL((mv_int4_slice_kernel<F, SS, 1>), grid, block, lds, st, a);       \
+    else if (R == 2) hipLaunchKernelGGL((mv_int4_slice_kernel<F, SS, 2>), grid, block, lds, st, a);  \
+    else if (R == 4) hipLaunchKernelGGL((mv_int4_slice_kernel<F, SS, 4>), grid, block, lds, st, a);  \
+    else hipLaunchKernelGGL((mv_int4_slice_kernel<F, SS, 8>), grid, block, lds, st, a);
+#define XP_MV_SLICE_LAUNCH(F)                                                                 \
+    if (S == 4) { XP_MV_SLICE_R(F, 4) }                                                        \
+    else if (S == 2) { XP_MV_SLICE_R(F, 2) }                                                   \
+    else { XP_MV_SLICE_R(F, 1) }
+            if (fmt == XP_SCALE_F16_QUAD) {
+                XP_MV_SLICE_LAUNCH(XP_SCALE_F16_QUAD)
+            } else {
+                XP_MV_SLICE_LAUNCH(XP_SCALE_BF16_QUAD)
+            }
+#undef XP_MV_SLICE_LAUNCH
+#undef XP_MV_SLICE_R
+            hipError_t e = hipGetLastError();
+            if (e != hipSuccess) return set_error(XP_E_HIP, "%s: launch -> %s", who, hipGetErrorString(e));
+            return XP_OK;
+        }
         uint32_t sp = 1;
         if (a.nquads > kMvWgChunk || groups < 64) {
             sp = std::max(1u, std::min(kMvWgMaxSplit, uint32_t(n_cu) / groups));

@@ -91,6 +91,46 @@ int xp_stream_read_timed(const void* buf, size_t bytes, uint32_t iters, xp_strea
     return rc;
 }
 
+int xp_stream_read_rot_timed(const void* const* bufs, uint32_t nbufs, size_t bytes, uint32_t grid,
+                             uint32_t iters, xp_stream stream, float* ms) {
+    XP_REQUIRE(bufs && ms && nbufs > 0, "null pointer or no buffers");
+    XP_REQUIRE(bytes >= 16 && bytes % 16 == 0, "bytes=%zu must be a positive multiple of 16",
+               bytes);
+    for (uint32_t i = 0; i < nbufs; ++i)
+        XP_REQUIRE(bufs[i] && (reinterpret_cast<uintptr_t>(bufs[i]) & 15u) == 0,
+                   "buffer %u is null or not 16-byte aligned", i);
+    XP_REQUIRE(iters > 0, "iters must be positive");
+    XP_REQUIRE(grid <= 65536, "grid=%u > 65536", grid);
+    DeviceScratch* sc = scratch();
+    if (!sc) return XP_E_HIP;
+    if (!ensure_partial(sc, 4)) return XP_E_NOMEM;
+    uint32_t* sink = reinterpret_cast<uint32_t*>(sc->partial);   // never written in practice
+    hipStream_t st = as_stream(stream);
+    const uint32_t g = grid ? grid : n_cu();
+    hipEvent_t e0 = nullptr, e1 = nullptr;
+    XP_HIP(hipEventCreate(&e0));
+    XP_HIP(hipEventCreate(&e1));
+    int rc = XP_OK;
+    for (uint32_t i = 0; i < nbufs; ++i)   // one untimed pass
+        hipLaunchKernelGGL(stream_read_kernel, dim3(g), dim3(kStreamThreads), 0, st, sink,
+                           static_cast<const u32x4*>(bufs[i]), bytes / 16);
+    if (hipEventRecord(e0, st) != hipSuccess) rc = set_error(XP_E_HIP, "xp_stream_read_rot_timed: event");
+    for (uint32_t i = 0; i < iters && rc == XP_OK; ++i)
+        hipLaunchKernelGGL(stream_read_kernel, dim3(g), dim3(kStreamThreads), 0, st, sink,
+                           static_cast<const u32x4*>(bufs[i % nbufs]), bytes / 16);
+    if (rc == XP_OK && hipGetLastError() != hipSuccess)
+        rc = set_error(XP_E_HIP, "xp_stream_read_rot_timed: launch failed");
+    if (rc == XP_OK && hipEventRecord(e1, st) != hipSuccess)
+        rc = set_error(XP_E_HIP, "xp_stream_read_rot_timed: event");
+    if (rc == XP_OK && hipEventSynchronize(e1) != hipSuccess)
+        rc = set_error(XP_E_HIP, "xp_stream_read_rot_timed: sync");
+    if (rc == XP_OK && hipEventElapsedTime(ms, e0, e1) != hipSuccess)
+        rc = set_error(XP_E_HIP, "xp_stream_read_rot_timed: elapsed");
+    (void)hipEventDestroy(e0);
+    (void)hipEventDestroy(e1);
+    return rc;
+}
+
 int xp_copy(void* dst, const void* src, size_t bytes, xp_stream stream) {
     XP_REQUIRE(dst && src, "null pointer");
     XP_REQUIRE(bytes % 16 == 0, "bytes=%zu must be a multiple of 16", bytes);

@@ -44,7 +44,10 @@ double now_ms() {
 constexpr int kNMat = 7;
 constexpr int kNNorm = 6;
 constexpr size_t kAlign = 256;
-constexpr uint32_t kTicketMv = 0, kTicketAttn = 8192, kTicketAm = 8192 + 64, kTickets = 8192 + 128;
+// Ticket regions: matvec split-k, decode attention (kAttnTicketsPerHead per
+// kv head, at most 60 kv heads), argmax.
+constexpr uint32_t kTicketMv = 0, kTicketAttn = 8192, kTicketAm = 8192 + 1024, kTickets = 8192 + 1088;
+constexpr uint32_t kMaxKvHeads = (kTicketAm - kTicketAttn) / kAttnTicketsPerHead;
 
 size_t align_up(size_t v) { return (v + kAlign - 1) & ~(kAlign - 1); }
 
@@ -114,6 +117,8 @@ int check_config(const xp_config& c) {
     if (c.max_seq > 8192)
         return set_error(XP_E_ARG, "config: max_seq=%u > 8192 (the reference's context limit)",
                          c.max_seq);
+    if (c.n_kv_heads > kMaxKvHeads)
+        return set_error(XP_E_ARG, "config: n_kv_heads=%u > %u", c.n_kv_heads, kMaxKvHeads);
     if (c.hidden > 8192)
         return set_error(XP_E_ARG, "config: hidden=%u > 8192", c.hidden);
     if (c.scale_fmt != XP_SCALE_F16_QUAD && c.scale_fmt != XP_SCALE_BF16_QUAD &&

@@ -129,34 +129,45 @@ __global__ __launch_bounds__(256) void qk_norm_rope_append_kernel(QkArgs a, Rope
 // Grid: (nsplit, kv_heads, batch). Workgroup (s, g, b) takes a contiguous chunk
 // of sequence b's attended keys for the G query heads that share kv head g,
 // reading every key and value once for all G heads (the mq4 idea,
-// llm_transformer.cl:418-464, 499-557), in passes of up to 128 keys:
+// llm_transformer.cl:418-464, 499-557), in passes of 16 U keys:
 //   loads   32 lanes per 512-byte key row (16-byte loads, 8 dims per lane);
-//           lane group kp = tid / 32 takes keys kp, kp + 16, ..., kp + 112,
-//           and all 8 K and 8 V loads of a pass are in flight together
-//   scores  each lane dots its 8 dims with the G query heads; the G x 8
+//           lane group kp = tid / 32 takes keys kp, kp + 16, ..., and all U
+//           K and U V loads of a pass are in flight together
+//   scores  each lane dots its 8 dims with the G query heads; the G x U
 //           partial dots of a row group are summed by a reduce-scatter over
-//           its 32 lanes (5 swizzle steps, each halving the values a lane
-//           holds), so lane i ends with one (head, key) score
+//           its 32 lanes (each swizzle step halving the values a lane holds),
+//           so lane i ends with one (head, key) score
 //   softmax one wave per head over the pass, online across passes (running
 //           max and sum, the accumulated values rescaled by exp(m_old - m_new))
 //   values  the same lanes accumulate p x v for their 8 dims, then the 16 row
 //           groups are summed (lane pairs by shuffle, waves through LDS)
-// Each split publishes (max, sum of exp, unnormalised o) per head; the last
-// workgroup of (b, g) to arrive (arrival ticket) rescales and sums the splits —
-// softmax_rows_finish's online combine (llm_transformer.cl:385-405) — with
-// 16-byte device-scope loads spread over all its threads, in a fixed order.
+// U (2, 4 or 8) follows the chunk length, so a 32-key chunk does a quarter
+// of a 128-key pass's arithmetic. Up to 256 splits (at least 32 keys each)
+// give every CU a workgroup at one sequence's long spans. Each split
+// publishes (max, sum of exp, unnormalised o) per head; the last workgroup
+// of each group of 16 splits to arrive (arrival ticket) rescales and sums
+// the group — softmax_rows_finish's online combine (llm_transformer.cl:
+// 385-405) — into one record of the same form, and the last group to arrive
+// combines the group records, so no workgroup reads more than 16 records;
+// one group combines straight into the output. Records are read with 16-byte
+// device-scope loads spread over all the combining workgroup's threads, and
+// summed in a fixed order (deterministic).
 constexpr int kAttnThreads  = 512;
 constexpr int kAttnHD       = 256;                        // head_dim
 constexpr int kAttnLanes    = kAttnHD / 8;                // lanes per key row
 constexpr int kAttnRows     = kAttnThreads / kAttnLanes;  // 16 row groups
-constexpr int kAttnU        = 8;                          // keys per lane per pass
-constexpr int kAttnPass     = kAttnRows * kAttnU;         // 128 keys per pass
+constexpr int kAttnMaxPass  = kAttnRows * 8;              // most keys per pass (U = 8)
 constexpr int kAttnMinChunk = 32;                         // fewest keys per split
-constexpr int kAttnMaxSplit = 64;                         // splits per (sequence, kv head)
+constexpr int kAttnMaxSplit = 256;                        // splits per (sequence, kv head)
+constexpr int kAttnFan      = 16;                         // records one combine reads
+constexpr int kAttnGroups   = kAttnMaxSplit / kAttnFan;   // level-1 records
 constexpr int kAttnMaxG     = 4;                          // query heads per kv head
 constexpr int kAttnStat     = 8;                          // floats of (max[4], sum[4]) per record
 
 __host__ __device__ constexpr uint32_t attn_record(uint32_t G) { return kAttnStat + G * kAttnHD; }
+// Records per (sequence, kv head): the splits', then the level-1 groups'.
+constexpr uint32_t kAttnRecords = kAttnMaxSplit + kAttnGroups;
+static_assert(kAttnTicketsPerHead == 1 + kAttnGroups, "tickets: level 2, then one per group");
 
 template <int M>
 __device__ __forceinline__ float swz_xor(float x) {   // x of lane ^ M within 32 lanes
@@ -204,15 +215,90 @@ __device__ __forceinline__ void f16x8(float (&f)[8], u32x4 w) {
     f[6] = f16_bits_to_f32(w.w); f[7] = f16_bits_to_f32(w.w >> 16);
 }
 
+// Combine n <= kAttnFan records (stride REC floats, in device memory) of
+// kv head g: f_p = exp(m_p - M), L = sum_p l_p f_p, o = sum_p f_p o_p in
+// record order. Final: out[h][d] = o / L. Else a record (M, L, o) at rec_out.
+// Thread (r, col) loads float4 column col over records r, r + R, ...; wave h
+// reads head h's statistics (one record per lane). All threads take part.
 template <int G>
-__global__ __launch_bounds__(kAttnThreads) void attention_decode_kernel(AttnArgs a) {
-    constexpr int HD = kAttnHD, NV = G * kAttnU, DUP = 32 / NV;
+__device__ __forceinline__ void attn_combine(const float* recs, uint32_t n, bool final, float* out,
+                                             float* rec_out, float (&red)[kAttnThreads / kWave][G * kAttnHD],
+                                             float (&fs)[kAttnFan][G], float (&run)[3][G]) {
+    constexpr int HD = kAttnHD;
     constexpr uint32_t REC = attn_record(G);
-    constexpr int NCOL = G * HD / 4, R = kAttnThreads / NCOL;   // combine: float4 columns, groups
-    __shared__ float ps[G][kAttnPass];
+    constexpr int NCOL = G * HD / 4, R = kAttnThreads / NCOL, B = kAttnFan / R;
+    static_assert(kAttnFan % R == 0, "records per thread");
+    const int tid = threadIdx.x, lane = tid % kWave, wave = tid / kWave;
+    const int col = tid % NCOL, r = tid / NCOL, h = col * 4 / HD;
+    const rsrc_t rs = make_rsrc(recs, n * REC * 4u);
+    const uint32_t off = (kAttnStat + col * 4) * 4u;
+    u32x4 v[B];
+#pragma unroll
+    for (int i = 0; i < B; ++i) {
+        const uint32_t p = r + i * R;
+        v[i] = p < n ? ld_dev16(rs, p * REC * 4u + off) : u32x4{0u, 0u, 0u, 0u};
+    }
+    if (wave < G) {
+        const int hh = wave;
+        const bool live = uint32_t(lane) < n;
+        const float m = live ? ld_dev(recs + size_t(lane) * REC + hh) : -INFINITY;
+        const float l = live ? ld_dev(recs + size_t(lane) * REC + kAttnMaxG + hh) : 0.0f;
+        const float mm = l > 0.0f ? m : -INFINITY;
+        const float M = wave_max(mm);
+        const float f = mm == -INFINITY ? 0.0f : expf(mm - M);
+        const float L = wave_sum(l * f);
+        if (live) fs[lane][hh] = f;
+        if (lane == 0) {
+            run[0][hh] = M;
+            run[1][hh] = L;
+        }
+    }
+    __syncthreads();
+    float4 acc = float4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int i = 0; i < B; ++i) {
+        const uint32_t p = r + i * R;
+        const float f = p < n ? fs[p][h] : 0.0f;
+        acc.x = fmaf(__uint_as_float(v[i].x), f, acc.x);
+        acc.y = fmaf(__uint_as_float(v[i].y), f, acc.y);
+        acc.z = fmaf(__uint_as_float(v[i].z), f, acc.z);
+        acc.w = fmaf(__uint_as_float(v[i].w), f, acc.w);
+    }
+    reinterpret_cast<float4*>(&red[0][0])[r * NCOL + col] = acc;
+    __syncthreads();
+    if (tid < NCOL) {
+        const float4* r4 = reinterpret_cast<const float4*>(&red[0][0]);
+        float4 t = r4[tid];
+#pragma unroll
+        for (int q = 1; q < R; ++q) {
+            const float4 u = r4[q * NCOL + tid];
+            t.x += u.x; t.y += u.y; t.z += u.z; t.w += u.w;
+        }
+        const int hh = tid * 4 / HD;
+        if (final) {
+            const float inv = 1.0f / run[1][hh];
+            reinterpret_cast<float4*>(out)[tid] = float4{t.x * inv, t.y * inv, t.z * inv, t.w * inv};
+        } else {
+            float* o = rec_out + kAttnStat + tid * 4;
+            st_dev(o, t.x); st_dev(o + 1, t.y); st_dev(o + 2, t.z); st_dev(o + 3, t.w);
+        }
+    }
+    if (!final && tid < G) {
+        st_dev(rec_out + tid, run[0][tid]);
+        st_dev(rec_out + kAttnMaxG + tid, run[1][tid]);
+    }
+}
+
+template <int G, int U>
+__global__ __launch_bounds__(kAttnThreads) void attention_decode_kernel(AttnArgs a) {
+    constexpr int HD = kAttnHD, NV = G * U, DUP = 32 / NV, PASS = kAttnRows * U;
+    constexpr int PV = (PASS + kWave - 1) / kWave;           // softmax values per lane
+    constexpr uint32_t REC = attn_record(G);
+    static_assert(NV <= 32 && (32 % NV) == 0, "G x U partial dots over 32 lanes");
+    __shared__ float ps[G][PASS];
     __shared__ float run[3][G];                  // running max, running sum, pass rescale
     __shared__ __attribute__((aligned(16))) float red[kAttnThreads / kWave][G * HD];
-    __shared__ float fs[kAttnMaxSplit][G];
+    __shared__ float fs[kAttnFan][G];
     __shared__ uint32_t last;
     {   // batched sequence blockIdx.z
         const uint32_t b = blockIdx.z;
@@ -221,7 +307,7 @@ __global__ __launch_bounds__(kAttnThreads) void attention_decode_kernel(AttnArgs
         a.kc += b * a.bcache;
         a.vc += b * a.bcache;
         if (a.part) a.part += b * a.bpart;
-        if (a.tickets) a.tickets += size_t(b) * a.kv_heads;
+        if (a.tickets) a.tickets += size_t(b) * a.kv_heads * kAttnTicketsPerHead;
     }
     uint32_t span, kv0;
     attn_range(a, span, kv0);
@@ -250,22 +336,22 @@ __global__ __launch_bounds__(kAttnThreads) void attention_decode_kernel(AttnArgs
         run[0][tid] = -INFINITY;
         run[1][tid] = 0.0f;
     }
-    for (int c0 = 0; c0 < nk; c0 += kAttnPass) {
-        u32x4 kw[kAttnU], vw[kAttnU];
+    for (int c0 = 0; c0 < nk; c0 += PASS) {
+        u32x4 kw[U], vw[U];
 #pragma unroll
-        for (int u = 0; u < kAttnU; ++u) {
+        for (int u = 0; u < U; ++u) {
             const int j = c0 + kp + kAttnRows * u;
             kw[u] = j < nk ? ldg4(kbase + size_t(j) * rowstride) : u32x4{0u, 0u, 0u, 0u};
         }
 #pragma unroll
-        for (int u = 0; u < kAttnU; ++u) {
+        for (int u = 0; u < U; ++u) {
             const int j = c0 + kp + kAttnRows * u;
             vw[u] = j < nk ? ldg4(vbase + size_t(j) * rowstride) : u32x4{0u, 0u, 0u, 0u};
         }
         // ---- scores
         float sv[NV];
 #pragma unroll
-        for (int u = 0; u < kAttnU; ++u) {
+        for (int u = 0; u < U; ++u) {
             float kf[8];
             f16x8(kf, kw[u]);
 #pragma unroll
@@ -273,12 +359,12 @@ __global__ __launch_bounds__(kAttnThreads) void attention_decode_kernel(AttnArgs
                 float d = 0.0f;
 #pragma unroll
                 for (int e = 0; e < 8; ++e) d = fmaf(q[h][e], kf[e], d);
-                sv[h * kAttnU + u] = d;
+                sv[h * U + u] = d;
             }
         }
         reduce_scatter32<NV, 16>(sv, uint32_t(lane));
         {
-            const int idx = (lane % 32) / DUP, h = idx / kAttnU, u = idx % kAttnU;
+            const int idx = (lane % 32) / DUP, h = idx / U, u = idx % U;
             const int j = kp + kAttnRows * u;
             if (lane % DUP == 0) ps[h][j] = (c0 + j < nk) ? sv[0] * a.scale : -INFINITY;
         }
@@ -286,13 +372,25 @@ __global__ __launch_bounds__(kAttnThreads) void attention_decode_kernel(AttnArgs
         // ---- softmax of the pass, online across passes: wave h takes head h
         if (wave < G) {
             const int h = wave;
-            const float s0 = ps[h][lane], s1 = ps[h][lane + kWave];
+            float sp[PV];
+            float mx = -INFINITY;
+#pragma unroll
+            for (int i = 0; i < PV; ++i) {
+                const int idx = lane + kWave * i;
+                sp[i] = idx < PASS ? ps[h][idx] : -INFINITY;
+                mx = fmaxf(mx, sp[i]);
+            }
             const float mold = run[0][h];
-            const float mnew = fmaxf(mold, wave_max(fmaxf(s0, s1)));   // finite: key c0 is live
-            const float p0 = expf(s0 - mnew), p1 = expf(s1 - mnew);
-            ps[h][lane] = p0;
-            ps[h][lane + kWave] = p1;
-            const float sum = wave_sum(p0 + p1);
+            const float mnew = fmaxf(mold, wave_max(mx));   // finite: key c0 is live
+            float sum = 0.0f;
+#pragma unroll
+            for (int i = 0; i < PV; ++i) {
+                const int idx = lane + kWave * i;
+                const float p = idx < PASS ? expf(sp[i] - mnew) : 0.0f;
+                if (idx < PASS) ps[h][idx] = p;
+                sum += p;
+            }
+            sum = wave_sum(sum);
             if (lane == 0) {
                 const float alpha = expf(mold - mnew);   // 0 on the first pass
                 run[0][h] = mnew;
@@ -309,7 +407,7 @@ __global__ __launch_bounds__(kAttnThreads) void attention_decode_kernel(AttnArgs
             for (int e = 0; e < 8; ++e) o[h][e] *= al;
         }
 #pragma unroll
-        for (int u = 0; u < kAttnU; ++u) {
+        for (int u = 0; u < U; ++u) {
             float vf[8];
             f16x8(vf, vw[u]);
             const int j = kp + kAttnRows * u;
@@ -336,16 +434,18 @@ __global__ __launch_bounds__(kAttnThreads) void attention_decode_kernel(AttnArgs
         }
     }
     __syncthreads();
+    float* out = a.out + size_t(g) * G * HD;
     if (a.nsplit == 1) {
         for (int i = tid; i < G * HD; i += kAttnThreads) {
             float acc = 0.0f;
 #pragma unroll
             for (int w = 0; w < kAttnThreads / kWave; ++w) acc += red[w][i];
-            a.out[size_t(g) * G * HD + i] = acc / run[1][i / HD];
+            out[i] = acc / run[1][i / HD];
         }
         return;
     }
-    float* part = a.part + size_t(g) * a.nsplit * REC;
+    float* part = a.part + size_t(g) * kAttnRecords * REC;
+    uint32_t* tk = a.tickets + size_t(g) * kAttnTicketsPerHead;   // [0] level 2, [1 + grp] level 1
     float* rec = part + size_t(s) * REC;
     for (int i = tid; i < G * HD; i += kAttnThreads) {
         float acc = 0.0f;
@@ -357,66 +457,26 @@ __global__ __launch_bounds__(kAttnThreads) void attention_decode_kernel(AttnArgs
         st_dev(rec + tid, run[0][tid]);                 // -inf for an empty split
         st_dev(rec + kAttnMaxG + tid, run[1][tid]);     // 0 for an empty split
     }
+    // ---- level 1: the last split of its group of kAttnFan combines the group
+    const uint32_t grp = s / kAttnFan, ng = (a.nsplit + kAttnFan - 1) / kAttnFan;
+    const uint32_t n1 = min(uint32_t(kAttnFan), a.nsplit - grp * kAttnFan);
     wait_mem();
     __syncthreads();
-    if (tid == 0) last = take_ticket(&a.tickets[g]);
+    if (tid == 0) last = take_ticket(&tk[1 + grp]);
     __syncthreads();
-    if (last != a.nsplit - 1) return;
-
-    // ---- combine (last workgroup). Thread (r, col) takes float4 column col of
-    // the output over splits r, r + R, ...; its loads are issued before wave h
-    // reads head h's statistics (one split per lane) and computes the factors
-    // f_p = exp(m_p - M) and L = sum_p l_p f_p, so both wait on one round trip.
-    {
-        constexpr int B = kAttnMaxSplit / R;
-        const int col = tid % NCOL, r = tid / NCOL, h = col * 4 / HD;
-        const rsrc_t rs = make_rsrc(part, a.nsplit * REC * 4u);
-        const uint32_t off = (kAttnStat + col * 4) * 4u;
-        u32x4 v[B];
-#pragma unroll
-        for (int i = 0; i < B; ++i) {
-            const uint32_t p = r + i * R;
-            v[i] = p < a.nsplit ? ld_dev16(rs, p * REC * 4u + off) : u32x4{0u, 0u, 0u, 0u};
-        }
-        if (wave < G) {
-            const int hh = wave;
-            const bool live = uint32_t(lane) < a.nsplit;
-            const float m = live ? ld_dev(part + size_t(lane) * REC + hh) : -INFINITY;
-            const float l = live ? ld_dev(part + size_t(lane) * REC + kAttnMaxG + hh) : 0.0f;
-            const float mm = l > 0.0f ? m : -INFINITY;
-            const float M = wave_max(mm);
-            const float f = mm == -INFINITY ? 0.0f : expf(mm - M);
-            const float L = wave_sum(l * f);
-            if (live) fs[lane][hh] = f;
-            if (lane == 0) run[1][hh] = L;
-        }
-        __syncthreads();
-        float4 acc = float4{0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-        for (int i = 0; i < B; ++i) {
-            const uint32_t p = r + i * R;
-            const float f = p < a.nsplit ? fs[p][h] : 0.0f;
-            acc.x = fmaf(__uint_as_float(v[i].x), f, acc.x);
-            acc.y = fmaf(__uint_as_float(v[i].y), f, acc.y);
-            acc.z = fmaf(__uint_as_float(v[i].z), f, acc.z);
-            acc.w = fmaf(__uint_as_float(v[i].w), f, acc.w);
-        }
-        reinterpret_cast<float4*>(&red[0][0])[r * NCOL + col] = acc;
-    }
+    if (last != n1 - 1) return;
+    if (tid == 0) st_dev(&tk[1 + grp], 0u);
+    float* grec = part + size_t(kAttnMaxSplit + grp) * REC;
+    attn_combine<G>(part + size_t(grp) * kAttnFan * REC, n1, ng == 1, out, grec, red, fs, run);
+    if (ng == 1) return;
+    // ---- level 2: the last group combines the group records
+    wait_mem();
     __syncthreads();
-    if (tid < NCOL) {
-        const float4* r4 = reinterpret_cast<const float4*>(&red[0][0]);
-        float4 t = r4[tid];
-#pragma unroll
-        for (int r = 1; r < R; ++r) {
-            const float4 v = r4[r * NCOL + tid];
-            t.x += v.x; t.y += v.y; t.z += v.z; t.w += v.w;
-        }
-        const float inv = 1.0f / run[1][tid * 4 / HD];
-        reinterpret_cast<float4*>(a.out + size_t(g) * G * HD)[tid] =
-            float4{t.x * inv, t.y * inv, t.z * inv, t.w * inv};
-    }
-    if (tid == 0) st_dev(&a.tickets[g], 0u);
+    if (tid == 0) last = take_ticket(&tk[0]);
+    __syncthreads();
+    if (last != ng - 1) return;
+    if (tid == 0) st_dev(&tk[0], 0u);
+    attn_combine<G>(part + size_t(kAttnMaxSplit) * REC, ng, true, out, nullptr, red, fs, run);
 }
 
 // ---- elementwise ------------------------------------------------------------
@@ -454,11 +514,11 @@ int launch_qk(const QkArgs& a, float theta, hipStream_t st) {
 }
 
 uint32_t attn_splits(uint32_t max_span, uint32_t batch, uint32_t kv_heads) {
-    // Enough workgroups to give every CU one (256), at most two passes of keys
+    // Enough workgroups to give every CU one (256), at most two 128-key passes
     // per split, at least kAttnMinChunk keys per split, at most kAttnMaxSplit.
     const uint32_t units = (batch ? batch : 1) * (kv_heads ? kv_heads : 1);
     uint32_t n = (256 + units - 1) / units;
-    const uint32_t by_len = (max_span + 2 * kAttnPass - 1) / (2 * kAttnPass);
+    const uint32_t by_len = (max_span + 2 * kAttnMaxPass - 1) / (2 * kAttnMaxPass);
     if (n < by_len) n = by_len;
     const uint32_t most = (max_span + kAttnMinChunk - 1) / kAttnMinChunk;
     if (n > most) n = most;
@@ -468,7 +528,7 @@ uint32_t attn_splits(uint32_t max_span, uint32_t batch, uint32_t kv_heads) {
 
 size_t attn_partial_floats(uint32_t kv_heads, uint32_t n_heads, uint32_t head_dim) {
     (void)head_dim;
-    return size_t(kv_heads) * kAttnMaxSplit * attn_record(kv_heads ? n_heads / kv_heads : 1);
+    return size_t(kv_heads) * kAttnRecords * attn_record(kv_heads ? n_heads / kv_heads : 1);
 }
 
 int launch_attention(AttnArgs a, uint32_t max_span, hipStream_t st) {
@@ -490,14 +550,29 @@ int launch_attention(AttnArgs a, uint32_t max_span, hipStream_t st) {
         DeviceScratch* sc = scratch();
         if (!sc) return XP_E_HIP;
         const size_t need = attn_partial_floats(a.kv_heads, a.n_heads, a.head_dim);
-        if (!ensure_partial(sc, need) || !ensure_tickets(sc, a.kv_heads)) return XP_E_NOMEM;
+        if (!ensure_partial(sc, need) || !ensure_tickets(sc, size_t(a.kv_heads) * kAttnTicketsPerHead))
+            return XP_E_NOMEM;
         a.part = sc->partial;
         a.tickets = sc->tickets;
     }
+    // keys per lane per pass: a quarter pass for 32-key chunks, a half for
+    // 64, a whole 128-key pass beyond
+    uint32_t chunk = (max_span + a.nsplit - 1) / a.nsplit;
+    if (chunk < uint32_t(kAttnMinChunk)) chunk = kAttnMinChunk;
+    const int U = chunk <= 32 ? 2 : (chunk <= 64 ? 4 : 8);
     const dim3 grid(a.nsplit, a.kv_heads, a.batch), block(kAttnThreads);
-    if (G == 1) hipLaunchKernelGGL(attention_decode_kernel<1>, grid, block, 0, st, a);
-    else if (G == 2) hipLaunchKernelGGL(attention_decode_kernel<2>, grid, block, 0, st, a);
-    else hipLaunchKernelGGL(attention_decode_kernel<4>, grid, block, 0, st, a);
+#define XP_ATTN_LAUNCH(GG)                                                                          \
+    if (U == 2) hipLaunchKernelGGL((attention_decode_kernel<GG, 2>), grid, block, 0, st, a);       \
+    else if (U == 4) hipLaunchKernelGGL((attention_decode_kernel<GG, 4>), grid, block, 0, st, a);  \
+    else hipLaunchKernelGGL((attention_decode_kernel<GG, 8>), grid, block, 0, st, a);
+    if (G == 1) {
+        XP_ATTN_LAUNCH(1)
+    } else if (G == 2) {
+        XP_ATTN_LAUNCH(2)
+    } else {
+        XP_ATTN_LAUNCH(4)
+    }
+#undef XP_ATTN_LAUNCH
     hipError_t e = hipGetLastError();
     if (e != hipSuccess)
         return set_error(XP_E_HIP, "attention: launch -> %s", hipGetErrorString(e));

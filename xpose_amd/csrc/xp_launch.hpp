@@ -90,15 +90,18 @@ struct AttnArgs {
     uint32_t window;           // 0 = global (with pos_dev)
     float scale;
     uint32_t nsplit;
-    float* part;               // [kv_heads][nsplit][8 + group * head_dim]
-    uint32_t* tickets;         // [kv_heads]
+    float* part;               // [kv_heads][256 + 16][8 + group * head_dim]
+    uint32_t* tickets;         // [kv_heads][kAttnTicketsPerHead], zero at rest
     // Batched sequences (grid.z = batch): sequence b reads q + b bq, the caches
     // at + b bcache, position pos_dev[b], and writes out + b bq, its own partials
-    // (+ b bpart) and tickets (+ b kv_heads).
+    // (+ b bpart) and tickets (+ b kv_heads kAttnTicketsPerHead).
     uint32_t batch = 1;
     uint32_t bq = 0;
     size_t bcache = 0, bpart = 0;
 };
+// Arrival tickets per (sequence, kv head) of the decode attention: one for
+// the final combine, one per group of 16 splits (at most 256 splits).
+constexpr uint32_t kAttnTicketsPerHead = 17;
 // Splits per (sequence, kv head) for a launch over `batch` sequences whose
 // spans are at most max_span; the partials one sequence needs (any span).
 uint32_t attn_splits(uint32_t max_span, uint32_t batch, uint32_t kv_heads);
