@@ -189,21 +189,54 @@ __global__ __launch_bounds__(256) void bembed_kernel(float* x, const void* wq, c
 }
 
 // ---- M = 16 int4 GEMM ------------------------------------------------------------
-// Workgroup (g, s): column group g, k split s; its eight waves take
-// consecutive chunks of kc <= kBmmMaxPerWave blocks, load every operand of
-// their chunk at once (one memory latency per wave, not one per block), and
-// sum their 16 x 64 results through LDS in wave order. With nsplit > 1 the
-// splits publish partials and the last to arrive (ticket per group) adds them
-// in split order.
+// Workgroup (cb, s): a block of 16 T columns (T MFMA tiles: 4 = one 64-column
+// KM4 group, 1 = a quarter of one, for narrow shapes whose groups alone would
+// leave most CUs idle), k split s; its eight waves take consecutive chunks of
+// kc <= kBmmMaxPerWave blocks, load every operand of their chunk at once (one
+// memory latency per wave, not one per block), and sum their 16 x 16 T
+// results through LDS in wave order. With nsplit > 1 the splits publish
+// partials and the last to arrive (ticket per column block) adds them in
+// split order.
 constexpr uint32_t kBmmWaves = 8;
 constexpr uint32_t kBmmMaxPerWave = 5;
 
-template <int FMT>
+// The staged operand of one block from fp32 rows, in registers (the same
+// values and slot order bprep_kernel writes): lane l holds row l % 16 and k =
+// 32 blk + 8 (l / 16) + e(s); as = the block sums of rows 4 (l / 16) + 0..3.
+__device__ __forceinline__ void stage_regs(u32x4& H, u32x4& L, float4& as, const float (&v)[8],
+                                           uint32_t wsel) {
+    uint32_t hi[8], lo[8];
+    float sum = 0.0f;
+#pragma unroll
+    for (int sl = 0; sl < 8; ++sl) {
+        const float t = v[sl / 2 + 4 * (sl % 2)];
+        const uint32_t h = bf16_bits_rn(t);
+        const float hf = __uint_as_float(h << 16);
+        const uint32_t l = bf16_bits_rn(t - hf);
+        hi[sl] = h;
+        lo[sl] = l;
+        sum += hf + __uint_as_float(l << 16);
+    }
+    H = u32x4{hi[0] | (hi[1] << 16), hi[2] | (hi[3] << 16), hi[4] | (hi[5] << 16), hi[6] | (hi[7] << 16)};
+    L = u32x4{lo[0] | (lo[1] << 16), lo[2] | (lo[3] << 16), lo[4] | (lo[5] << 16), lo[6] | (lo[7] << 16)};
+    // the row's block sum over its four 8-element groups (lanes 16 apart),
+    // added as bprep_kernel adds them: (g0 + g1) + (g2 + g3)
+    sum += __shfl_xor(sum, 16, kWave);
+    sum += __shfl_xor(sum, 32, kWave);
+    as = float4{__shfl(sum, int(4 * wsel + 0), kWave), __shfl(sum, int(4 * wsel + 1), kWave),
+                __shfl(sum, int(4 * wsel + 2), kWave), __shfl(sum, int(4 * wsel + 3), kWave)};
+}
+
+template <int FMT, int T, int AM>
 __global__ __launch_bounds__(kBmmThreads) void bmm_int4_kernel(BmmArgs a) {
-    __shared__ float red[kBmmWaves][kGrp * 16];
+    constexpr uint32_t NO = 256u * T;            // outputs of a workgroup: 16 rows x 16 T columns
+    constexpr uint32_t PER = (NO + kBmmThreads - 1) / kBmmThreads;
+    constexpr uint32_t SUBS = 4u / T;            // column blocks per 64-column group
+    __shared__ float red[kBmmWaves][NO];
     __shared__ uint32_t last;
     const uint32_t tid = threadIdx.x, wave = tid / kWave, lane = tid % kWave;
-    const uint32_t gg = blockIdx.x, s = blockIdx.y;
+    const uint32_t cb = blockIdx.x, s = blockIdx.y;
+    const uint32_t gg = cb / SUBS, c16 = (cb % SUBS) * 16u * T;   // group, first column in it
     uint32_t m = 0;
     while (m + 1 < a.n_mats && gg >= a.groups[m + 1]) ++m;
     const uint32_t g = gg - a.groups[m];
@@ -214,25 +247,44 @@ __global__ __launch_bounds__(kBmmThreads) void bmm_int4_kernel(BmmArgs a) {
     const uint32_t col16 = lane % 16u, wsel = lane / 16u;
     const uint32_t kb0 = min((s * kBmmWaves + wave) * a.kc, a.nblk);
     const uint32_t kb1 = min(kb0 + a.kc, a.nblk);
-    f32x4 acc[4];
+    f32x4 acc[T];
 #pragma unroll
-    for (int t = 0; t < 4; ++t) acc[t] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-    // operands of one block
+    for (int t = 0; t < T; ++t) acc[t] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    // operands of one block (raw fp32 rows in AM 2 / 3, staged after the loads)
+    constexpr int NR = AM == 3 ? 4 : (AM == 2 ? 2 : 1);
     struct Ops {
         u32x4 hi, lo;
         float4 as;
-        uint32_t w[4];
-        u32x2 sc[4];
+        float4 raw[NR];
+        uint32_t w[T];
+        u32x2 sc[T];
     };
     auto load = [&](Ops& o, uint32_t blk) {
-        o.hi = A[(size_t(blk) * 2 + 0) * 64 + lane];
-        o.lo = A[(size_t(blk) * 2 + 1) * 64 + lane];
-        o.as = *reinterpret_cast<const float4*>(a.asum + size_t(blk) * 16 + 4u * wsel);
+        if constexpr (AM == 0) {
+            o.hi = A[(size_t(blk) * 2 + 0) * 64 + lane];
+            o.lo = A[(size_t(blk) * 2 + 1) * 64 + lane];
+            o.as = *reinterpret_cast<const float4*>(a.asum + size_t(blk) * 16 + 4u * wsel);
+        } else {
+            // row col16 (sequences past a.rows read as zeros), k 32 blk + 8 wsel ..
 #pragma unroll
-        for (int t = 0; t < 4; ++t) {
-            o.w[t] = __builtin_nontemporal_load(
-                wq + ((size_t(g) * a.nblk + blk) * kGrp + 16u * t + col16) * 4 + wsel);
-            o.sc[t] = sq[size_t(blk / 4) * cols + g * kGrp + 16u * t + col16];
+            for (int i = 0; i < NR; ++i) o.raw[i] = float4{0.0f, 0.0f, 0.0f, 0.0f};
+            if (col16 < a.rows) {
+                const size_t off = size_t(col16) * a.lda + size_t(blk) * kBlk + 8u * wsel;
+                const float4* xa4 = reinterpret_cast<const float4*>(a.xa + off);
+                o.raw[0] = xa4[0];
+                o.raw[1] = xa4[1];
+                if constexpr (AM == 3) {
+                    const float4* xu4 = reinterpret_cast<const float4*>(a.xu + off);
+                    o.raw[2] = xu4[0];
+                    o.raw[3] = xu4[1];
+                }
+            }
+        }
+#pragma unroll
+        for (int t = 0; t < T; ++t) {
+            const uint32_t cg = c16 + 16u * t + col16;   // column within the group
+            o.w[t] = __builtin_nontemporal_load(wq + ((size_t(g) * a.nblk + blk) * kGrp + cg) * 4 + wsel);
+            o.sc[t] = sq[size_t(blk / 4) * cols + g * kGrp + cg];
         }
     };
     Ops ops[kBmmMaxPerWave];
@@ -243,11 +295,22 @@ __global__ __launch_bounds__(kBmmThreads) void bmm_int4_kernel(BmmArgs a) {
     for (uint32_t j = 0; j < kBmmMaxPerWave; ++j) {
         if (kb0 + j >= kb1) break;
         const uint32_t blk = kb0 + j;
-        const Ops& cur = ops[j];
+        Ops& cur = ops[j];
+        if constexpr (AM != 0) {
+            float v[8] = {cur.raw[0].x, cur.raw[0].y, cur.raw[0].z, cur.raw[0].w,
+                          cur.raw[1].x, cur.raw[1].y, cur.raw[1].z, cur.raw[1].w};
+            if constexpr (AM == 3) {
+                const float u[8] = {cur.raw[2].x, cur.raw[2].y, cur.raw[2].z, cur.raw[2].w,
+                                    cur.raw[3].x, cur.raw[3].y, cur.raw[3].z, cur.raw[3].w};
+#pragma unroll
+                for (int e = 0; e < 8; ++e) v[e] = gelu_tanh(v[e]) * u[e];
+            }
+            stage_regs(cur.hi, cur.lo, cur.as, v, wsel);
+        }
         const bf16x8 ahi = as_bf16x8(cur.hi), alo = as_bf16x8(cur.lo);
         const float corr[4] = {136.0f * cur.as.x, 136.0f * cur.as.y, 136.0f * cur.as.z, 136.0f * cur.as.w};
 #pragma unroll
-        for (int t = 0; t < 4; ++t) {
+        for (int t = 0; t < T; ++t) {
             const bf16x8 bw = as_bf16x8(widen_nibbles(cur.w[t]));
             f32x4 c = {0.0f, 0.0f, 0.0f, 0.0f};
             c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ahi, bw, c, 0, 0, 0);
@@ -257,50 +320,55 @@ __global__ __launch_bounds__(kBmmThreads) void bmm_int4_kernel(BmmArgs a) {
             for (int r = 0; r < 4; ++r) acc[t][r] = fmaf(f, c[r] - corr[r], acc[t][r]);
         }
     }
-    // o = lane * 16 + t * 4 + r  <->  row 4 (lane / 16) + r, column 16 t + lane % 16
+    // o = lane * 4 T + t * 4 + r  <->  row 4 (lane / 16) + r, column 16 t + lane % 16
 #pragma unroll
-    for (int t = 0; t < 4; ++t)
+    for (int t = 0; t < T; ++t)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) red[wave][lane * 16 + t * 4 + r] = acc[t][r];
+        for (int r = 0; r < 4; ++r) red[wave][lane * 4u * T + t * 4 + r] = acc[t][r];
     __syncthreads();
-    float v[2];
-    uint32_t row[2], col[2];
+    float v[PER];
+    uint32_t row[PER], col[PER];
+    bool own[PER];
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
+    for (uint32_t j = 0; j < PER; ++j) {
         const uint32_t o = tid + j * kBmmThreads;
+        own[j] = o < NO;
+        const uint32_t oc = own[j] ? o : 0u;
         float sum = 0.0f;
 #pragma unroll
-        for (int w = 0; w < int(kBmmWaves); ++w) sum += red[w][o];
+        for (int w = 0; w < int(kBmmWaves); ++w) sum += red[w][oc];
         v[j] = sum;
-        const uint32_t ol = o / 16u, ot = (o % 16u) / 4u, orr = o % 4u;
+        const uint32_t ol = oc / (4u * T), ot = (oc % (4u * T)) / 4u, orr = oc % 4u;
         row[j] = 4u * (ol / 16u) + orr;
-        col[j] = g * kGrp + 16u * ot + ol % 16u;
+        col[j] = g * kGrp + c16 + 16u * ot + ol % 16u;
     }
     float* out = a.mats[m].out;
     if (a.nsplit == 1) {
 #pragma unroll
-        for (int j = 0; j < 2; ++j)
-            if (row[j] < a.rows) out[size_t(row[j]) * cols + col[j]] = v[j];
+        for (uint32_t j = 0; j < PER; ++j)
+            if (own[j] && row[j] < a.rows) out[size_t(row[j]) * cols + col[j]] = v[j];
         return;
     }
-    float* part = a.part + (size_t(s) * gridDim.x + gg) * (kGrp * 16);
+    float* part = a.part + (size_t(s) * gridDim.x + cb) * NO;
 #pragma unroll
-    for (int j = 0; j < 2; ++j) st_dev(part + tid + j * kBmmThreads, v[j]);
+    for (uint32_t j = 0; j < PER; ++j)
+        if (own[j]) st_dev(part + tid + j * kBmmThreads, v[j]);
     wait_mem();
     __syncthreads();
-    if (tid == 0) last = take_ticket(a.tickets + gg);
+    if (tid == 0) last = take_ticket(a.tickets + cb);
     __syncthreads();
     if (last != a.nsplit - 1) return;
     // last arrival: every split's partial, loaded together, added in split order
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
+    for (uint32_t j = 0; j < PER; ++j) {
+        if (!own[j]) continue;
         float sum = 0.0f;
         for (uint32_t p0 = 0; p0 < a.nsplit; p0 += 8) {
             float pv[8];
 #pragma unroll
             for (uint32_t q = 0; q < 8; ++q)
                 pv[q] = p0 + q < a.nsplit
-                            ? ld_dev(a.part + (size_t(p0 + q) * gridDim.x + gg) * (kGrp * 16) + tid + j * kBmmThreads)
+                            ? ld_dev(a.part + (size_t(p0 + q) * gridDim.x + cb) * NO + tid + j * kBmmThreads)
                             : 0.0f;
 #pragma unroll
             for (uint32_t q = 0; q < 8; ++q)
@@ -308,7 +376,7 @@ __global__ __launch_bounds__(kBmmThreads) void bmm_int4_kernel(BmmArgs a) {
         }
         if (row[j] < a.rows) out[size_t(row[j]) * cols + col[j]] = sum;
     }
-    if (tid == 0) st_dev(a.tickets + gg, 0u);
+    if (tid == 0) st_dev(a.tickets + cb, 0u);
 }
 
 // Position advance for every sequence of a batch.
@@ -373,13 +441,31 @@ int launch_bmm(BmmArgs a, int fmt, int n_cu, hipStream_t st, const char* who) {
             return set_error(XP_E_ARG, "%s: split-K partial buffer too small", who);
         if (!a.tickets || a.tickets_cap < a.n_colwg) return set_error(XP_E_ARG, "%s: too few tickets", who);
     }
-    const dim3 grid(a.n_colwg, a.nsplit);
-    if (fmt == XP_SCALE_F16_QUAD)
-        hipLaunchKernelGGL(bmm_int4_kernel<XP_SCALE_F16_QUAD>, grid, dim3(kBmmThreads), 0, st, a);
-    else if (fmt == XP_SCALE_BF16_QUAD)
-        hipLaunchKernelGGL(bmm_int4_kernel<XP_SCALE_BF16_QUAD>, grid, dim3(kBmmThreads), 0, st, a);
-    else
+    // Quarter-group column blocks (one MFMA tile per wave) when the groups
+    // alone would give fewer than half the CUs a workgroup.
+    const bool quarter = a.n_colwg * a.nsplit * 2u < uint32_t(n_cu > 0 ? n_cu : 256);
+    const uint32_t nblocks = a.n_colwg * (quarter ? 4u : 1u);
+    if (a.nsplit > 1 && a.tickets_cap < nblocks)
+        return set_error(XP_E_ARG, "%s: too few tickets (%u < %u)", who, a.tickets_cap, nblocks);
+    if (a.amode != 0 && a.amode != 2 && a.amode != 3)
+        return set_error(XP_E_ARG, "%s: operand mode %u", who, a.amode);
+    if (a.amode != 0 && (!a.xa || (a.amode == 3 && !a.xu) || a.lda < a.nblk * kBlk ||
+                         ((reinterpret_cast<uintptr_t>(a.xa) | reinterpret_cast<uintptr_t>(a.xu)) & 15u) ||
+                         a.lda % 4u))
+        return set_error(XP_E_ARG, "%s: fp32 operand rows must be 16-byte aligned, lda >= k", who);
+    const dim3 grid(nblocks, a.nsplit);
+    if (fmt != XP_SCALE_F16_QUAD && fmt != XP_SCALE_BF16_QUAD)
         return set_error(XP_E_ARG, "%s: the batched GEMM takes fp16 or bf16 quad scales", who);
+#define XP_BMM_AM(F, TT)                                                                            \
+    if (a.amode == 2) hipLaunchKernelGGL((bmm_int4_kernel<F, TT, 2>), grid, dim3(kBmmThreads), 0, st, a);      \
+    else if (a.amode == 3) hipLaunchKernelGGL((bmm_int4_kernel<F, TT, 3>), grid, dim3(kBmmThreads), 0, st, a); \
+    else hipLaunchKernelGGL((bmm_int4_kernel<F, TT, 0>), grid, dim3(kBmmThreads), 0, st, a);
+    if (fmt == XP_SCALE_F16_QUAD) {
+        if (quarter) { XP_BMM_AM(XP_SCALE_F16_QUAD, 1) } else { XP_BMM_AM(XP_SCALE_F16_QUAD, 4) }
+    } else {
+        if (quarter) { XP_BMM_AM(XP_SCALE_BF16_QUAD, 1) } else { XP_BMM_AM(XP_SCALE_BF16_QUAD, 4) }
+    }
+#undef XP_BMM_AM
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return set_error(XP_E_HIP, "%s: launch -> %s", who, hipGetErrorString(e));
     return XP_OK;

@@ -95,7 +95,7 @@ struct TkShape {
     static constexpr uint32_t OB = QD / kBlk / KO;          // blocks per o tile
     static constexpr uint32_t NOG = H / kGrp;               // o column groups
     static constexpr uint32_t N_QKV = QKVD / kGrp * KQ;
-    static constexpr uint32_t N_COMB = NH * 4;
+    static constexpr uint32_t N_COMB = NH * 4;              // local layers' combine tiles
     static constexpr uint32_t N_O = NOG * KO;
     static constexpr uint32_t N_GU = 2 * FFN / kGrp;
     static constexpr uint32_t N_DN = (H / kGrp) * NCH;
@@ -907,61 +907,78 @@ __global__ __launch_bounds__(kTkThreads) void token_kernel(TokArgs a) {
         t_in = 0;
 
         // ================= combine =================
-        const uint32_t c0 = !xl ? t_comb : (rx % 8u == 0u ? rx / 8u : Sh::N_COMB);
-        for (uint32_t c = c0; c < Sh::N_COMB; c += nwg) {
-            const uint32_t h = c / 4u, d0 = (c % 4u) * 64u;
-            const uint32_t rstride = NH * (2u + kTkHD);
-            const uint32_t base = uint32_t(lay.attp) + h * (2u + kTkHD);
-            // big[s * 66 + 0 / 1] = (max, sum of exp) of chunk s,
-            // big[s * 66 + 2 + d] = its unnormalised output at dim d0 + d:
-            // 33 slot pairs per chunk, fetched 4 per thread at a time.
-            const uint32_t np = n_att * 33u;
-            for (uint32_t b = 0; b < np; b += 4u * kTkThreads) {
-                uint32_t off[4];
-                bool act[4];
-                u32x4 v[4];
+        // Tile (h, d0): head h, CD dims from d0: 64 in local layers (16 tiles,
+        // on the attention XCD when it exchanges there), 32 in global layers
+        // (32 tiles): a global layer's span is up to 256 chunk records, and
+        // halving each tile's share of them halves its fetch (measured: the
+        // global combine 5.3 -> 4.2 us; local layers keep 64, whose O wait
+        // grew with 32).
+        auto combine = [&](auto cd_c) {
+            constexpr uint32_t CD = decltype(cd_c)::value;
+            constexpr uint32_t PP = 1u + CD / 2u;       // slot pairs per chunk: stats, then CD / 2
+            constexpr uint32_t CS = 2u * PP;            // floats per chunk in big
+            constexpr uint32_t NG = kTkThreads / CD;    // chunk groups of the weighted sum
+            constexpr uint32_t NCB = NH * (kTkHD / CD);
+            static_assert(NG * CD <= sizeof(S.red) / sizeof(float), "weighted-sum scratch");
+            const uint32_t c0 = !xl ? t_comb : (rx % 8u == 0u ? rx / 8u : NCB);
+            for (uint32_t c = c0; c < NCB; c += nwg) {
+                const uint32_t h = c / (kTkHD / CD), d0 = (c % (kTkHD / CD)) * CD;
+                const uint32_t rstride = NH * (2u + kTkHD);
+                const uint32_t base = uint32_t(lay.attp) + h * (2u + kTkHD);
+                // big[s CS + 0 / 1] = (max, sum of exp) of chunk s,
+                // big[s CS + 2 + d] = its unnormalised output at dim d0 + d:
+                // PP slot pairs per chunk, fetched 4 per thread at a time.
+                const uint32_t np = n_att * PP;
+                for (uint32_t b = 0; b < np; b += 4u * kTkThreads) {
+                    uint32_t off[4];
+                    bool act[4];
+                    u32x4 v[4];
 #pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    const uint32_t i = b + uint32_t(r) * kTkThreads + tid;
-                    act[r] = i < np;
-                    const uint32_t ic = act[r] ? i : 0u;
-                    const uint32_t s = ic / 33u, e = ic % 33u;
-                    off[r] = (base + s * rstride + (e == 0u ? 0u : 2u + d0 + 2u * (e - 1u))) * 8u;
+                    for (int r = 0; r < 4; ++r) {
+                        const uint32_t i = b + uint32_t(r) * kTkThreads + tid;
+                        act[r] = i < np;
+                        const uint32_t ic = act[r] ? i : 0u;
+                        const uint32_t s = ic / PP, e = ic % PP;
+                        off[r] = (base + s * rstride + (e == 0u ? 0u : 2u + d0 + 2u * (e - 1u))) * 8u;
+                    }
+                    ll_wait(rr, soff, off, act, v, tag, a.state);
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        const uint32_t i = b + uint32_t(r) * kTkThreads + tid;
+                        if (act[r])
+                            *reinterpret_cast<float2*>(&S.big[2u * i]) =
+                                float2{__uint_as_float(v[r].x), __uint_as_float(v[r].z)};
+                    }
                 }
-                ll_wait(rr, soff, off, act, v, tag, a.state);
-#pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    const uint32_t i = b + uint32_t(r) * kTkThreads + tid;
-                    if (act[r])
-                        *reinterpret_cast<float2*>(&S.big[2u * i]) =
-                            float2{__uint_as_float(v[r].x), __uint_as_float(v[r].z)};
+                __syncthreads();
+                if (c == c0) t_in = tk_now(a);
+                float m = -INFINITY;
+                for (uint32_t s = tid; s < n_att; s += kTkThreads) m = fmaxf(m, S.big[s * CS]);
+                const float M = blk_max(m, RS());
+                float lsum = 0.0f;
+                for (uint32_t s = tid; s < n_att; s += kTkThreads) {
+                    const float f = expf(S.big[s * CS] - M);
+                    S.fm[s] = f;
+                    lsum += f * S.big[s * CS + 1u];
                 }
-            }
-            __syncthreads();
-            if (c == c0) t_in = tk_now(a);
-            float m = -INFINITY;
-            for (uint32_t s = tid; s < n_att; s += kTkThreads) m = fmaxf(m, S.big[s * 66u]);
-            const float M = blk_max(m, RS());
-            float lsum = 0.0f;
-            for (uint32_t s = tid; s < n_att; s += kTkThreads) {
-                const float f = expf(S.big[s * 66u] - M);
-                S.fm[s] = f;
-                lsum += f * S.big[s * 66u + 1u];
-            }
-            const float Ltot = blk_sum(lsum, RS());   // also orders the fm writes
-            const uint32_t d = tid % 64u, sg = tid / 64u;
-            float o = 0.0f;
-            for (uint32_t s = sg; s < n_att; s += kTkWaves) o = fmaf(S.big[s * 66u + 2u + d], S.fm[s], o);
-            S.red[sg][d] = o;
-            __syncthreads();
-            if (sg == 0) {
-                float r = 0.0f;
+                const float Ltot = blk_sum(lsum, RS());   // also orders the fm writes
+                const uint32_t d = tid % CD, sg = tid / CD;
+                float o = 0.0f;
+                for (uint32_t s = sg; s < n_att; s += NG) o = fmaf(S.big[s * CS + 2u + d], S.fm[s], o);
+                float* red = &S.red[0][0];
+                red[sg * CD + d] = o;
+                __syncthreads();
+                if (sg == 0) {
+                    float r = 0.0f;
 #pragma unroll
-                for (int w = 0; w < kTkWaves; ++w) r += S.red[w][d];
-                tile_put(rr, soff, uint32_t(lay.atto) + h * kTkHD + d0, r / Ltot, lane, tag);
+                    for (uint32_t w = 0; w < NG; ++w) r += red[w * CD + d];
+                    tile_put(rr, soff, uint32_t(lay.atto) + h * kTkHD + d0, r / Ltot, lane, tag);
+                }
+                __syncthreads();
             }
-            __syncthreads();
-        }
+        };
+        if (glob) combine(std::integral_constant<uint32_t, 32u>{});
+        else combine(std::integral_constant<uint32_t, 64u>{});
         tk_trace_stage(a, wg, l, 2u, t_in);
         t_in = 0;
 

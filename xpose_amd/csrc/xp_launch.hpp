@@ -145,6 +145,13 @@ int launch_badvance(uint32_t* pos, uint32_t batch, hipStream_t st);
 struct BmmArgs {
     const void* a;             // staged operand (BprepArgs::a)
     const float* asum;
+    // Or the operand's fp32 rows ([rows][lda]), converted in the GEMM:
+    // amode 2 stages xa as is (bprep mode 2), 3 stages gelu_tanh(xa) * xu
+    // (bprep mode 3); 0 reads a / asum.
+    const float* xa;
+    const float* xu;
+    uint32_t amode;
+    uint32_t lda;
     MvMatDesc mats[4];         // out is [rows][cols] row-major
     uint32_t n_mats;
     uint32_t groups[5];        // set by launch_bmm
