@@ -363,11 +363,12 @@ def main() -> int:
     ap.add_argument("--no-configs", action="store_true",
                     help="skip the benchmark config 3 / 4 / 5 and attention legs")
     ap.add_argument("--mv-iters", type=int, default=60)
-    ap.add_argument("--only", choices=["all", "matvec", "attention", "cfg5", "native"],
+    ap.add_argument("--only", choices=["all", "matvec", "attention", "cfg5", "native", "graph"],
                     default="all",
                     help="one leg alone, for profiling: the standalone matvec and streaming "
-                         "legs, the attention leg, the batched decode (config 5), or the "
-                         "native-format (repacked Q8_0 / Q5_0 / Q4_K / Q6_K) matvecs")
+                         "legs, the attention leg, the batched decode (config 5), the "
+                         "native-format (repacked Q8_0 / Q5_0 / Q4_K / Q6_K) matvecs, or the "
+                         "decode on the graph of per-op kernels")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported "
@@ -404,6 +405,9 @@ def main() -> int:
         return 0
     if args.only == "attention":
         print(json.dumps({"attention": [attention_leg(X, sp) for sp in (4096, 8192)]}), flush=True)
+        return 0
+    if args.only == "graph":
+        print(json.dumps({"graph_path": graph_leg(X, args.ctx)}), flush=True)
         return 0
     if args.only == "cfg5":
         scfg = X.XpConfig.gemma3_1b(max_seq=8192, sample_mode=1, temperature=0.8, top_k=64,

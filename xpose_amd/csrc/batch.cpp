@@ -117,17 +117,31 @@ int Batch::record() {
                                   {k_raw, L.w[XP_T_K], L.s[XP_T_K], kvd},
                                   {v, L.w[XP_T_V], L.s[XP_T_V], kvd}};
         XB(gemm(qkv, 3, H, "batch qkv"));
-        QkArgs qa{q, k, q_raw, k_raw, v, L.norm[4], L.norm[5], kc[l], vc[l],
-                  c.n_heads, c.n_kv_heads, c.head_dim, eps, d_pos, 0};
-        qa.batch = B;
-        qa.bq = qd;
-        qa.bkv = kvd;
-        qa.bcache = prefill ? 0 : size_t(S) * kvd;   // prefill rows share one cache
-        XB(launch_qk(qa, glob ? c.rope_theta_global : c.rope_theta_local, st));
-        // prefill: the last layer's K/V rows are the last thing the step must produce
-        if (prefill && l + 1 == c.n_layers) break;
+        const float theta = glob ? c.rope_theta_global : c.rope_theta_local;
+        if (prefill) {
+            // prefill rows share one cache: every row's key / value is
+            // appended before any row attends (a row's span includes the
+            // rows before it)
+            QkArgs qa{q, k, q_raw, k_raw, v, L.norm[4], L.norm[5], kc[l], vc[l],
+                      c.n_heads, c.n_kv_heads, c.head_dim, eps, d_pos, 0};
+            qa.batch = B;
+            qa.bq = qd;
+            qa.bkv = kvd;
+            qa.bcache = 0;
+            XB(launch_qk(qa, theta, st));
+            // the last layer's K/V rows are the last thing the step must produce
+            if (l + 1 == c.n_layers) break;
+        }
         AttnArgs aa{};
         aa.out = att; aa.q = q; aa.kc = kc[l]; aa.vc = vc[l];
+        if (!prefill) {
+            // decode: QK-norm, RoPE and the KV append inside the attention launch
+            aa.q_raw = q_raw; aa.k_raw = k_raw; aa.v_raw = v;
+            aa.qw = L.norm[4]; aa.kw = L.norm[5];
+            aa.eps = eps;
+            aa.theta = theta;
+            aa.bkv = kvd;
+        }
         aa.n_heads = c.n_heads; aa.kv_heads = c.n_kv_heads; aa.head_dim = c.head_dim;
         aa.pos_dev = d_pos;
         aa.window = glob ? 0u : c.sliding_window;

@@ -228,11 +228,13 @@ int Session::record(int variant, uint32_t& n) {
                                   {v, w.w[XP_T_V], w.s[XP_T_V], kvd}};
         XP_STEP(launch_mv(qkv, 3, xb, fmt, H, 0, mv_partial, mv_partial_cap, tickets + kTicketMv,
                           8192, st, "session qkv", n_cu));
-        QkArgs qa{q, k, q_raw, k_raw, v, w.norm[4], w.norm[5], w.kc, w.vc,
-                  c.n_heads, c.n_kv_heads, c.head_dim, eps, state, 0};
-        XP_STEP(launch_qk(qa, theta, st));
+        // QK-norm, RoPE and the KV append run inside the attention launch
         AttnArgs aa{};
-        aa.out = att; aa.q = q; aa.kc = w.kc; aa.vc = w.vc;
+        aa.out = att; aa.kc = w.kc; aa.vc = w.vc;
+        aa.q_raw = q_raw; aa.k_raw = k_raw; aa.v_raw = v;
+        aa.qw = w.norm[4]; aa.kw = w.norm[5];
+        aa.eps = eps;
+        aa.theta = theta;
         aa.n_heads = c.n_heads; aa.kv_heads = c.n_kv_heads; aa.head_dim = c.head_dim;
         aa.pos_dev = state;
         aa.window = glob ? 0u : c.sliding_window;

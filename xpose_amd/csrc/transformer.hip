@@ -289,8 +289,8 @@ __device__ __forceinline__ void attn_combine(const float* recs, uint32_t n, bool
     }
 }
 
-template <int G, int U>
-__global__ __launch_bounds__(kAttnThreads) void attention_decode_kernel(AttnArgs a) {
+template <int G, int U, bool FQ>
+__global__ __launch_bounds__(kAttnThreads) void attention_decode_kernel(AttnArgs a, RopeFreq f) {
     constexpr int HD = kAttnHD, NV = G * U, DUP = 32 / NV, PASS = kAttnRows * U;
     constexpr int PV = (PASS + kWave - 1) / kWave;           // softmax values per lane
     constexpr uint32_t REC = attn_record(G);
@@ -322,22 +322,9 @@ __global__ __launch_bounds__(kAttnThreads) void attention_decode_kernel(AttnArgs
     const uint16_t* kbase = a.kc + size_t(kv0 + j0) * rowstride + size_t(g) * HD + sub * 8;
     const uint16_t* vbase = a.vc + size_t(kv0 + j0) * rowstride + size_t(g) * HD + sub * 8;
 
-    float q[G][8], o[G][8];
-#pragma unroll
-    for (int h = 0; h < G; ++h) {
-        const float4* qp = reinterpret_cast<const float4*>(a.q + (size_t(g) * G + h) * HD + sub * 8);
-        const float4 q0 = qp[0], q1 = qp[1];
-        q[h][0] = q0.x; q[h][1] = q0.y; q[h][2] = q0.z; q[h][3] = q0.w;
-        q[h][4] = q1.x; q[h][5] = q1.y; q[h][6] = q1.z; q[h][7] = q1.w;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) o[h][e] = 0.0f;
-    }
-    if (tid < G) {
-        run[0][tid] = -INFINITY;
-        run[1][tid] = 0.0f;
-    }
-    for (int c0 = 0; c0 < nk; c0 += PASS) {
-        u32x4 kw[U], vw[U];
+    // K / V of one pass: U keys per lane, all loads in flight together
+    u32x4 kw[U], vw[U];
+    auto load_pass = [&](int c0) {
 #pragma unroll
         for (int u = 0; u < U; ++u) {
             const int j = c0 + kp + kAttnRows * u;
@@ -347,6 +334,112 @@ __global__ __launch_bounds__(kAttnThreads) void attention_decode_kernel(AttnArgs
         for (int u = 0; u < U; ++u) {
             const int j = c0 + kp + kAttnRows * u;
             vw[u] = j < nk ? ldg4(vbase + size_t(j) * rowstride) : u32x4{0u, 0u, 0u, 0u};
+        }
+    };
+    load_pass(0);   // the first pass's keys do not depend on q
+
+    float q[G][8], o[G][8];
+    // Fused QK-norm + RoPE (qk_norm_rope_append_kernel's arithmetic): waves
+    // 0 .. G-1 norm and rotate query head g G + wave, wave G the key, wave
+    // G + 1 rounds the value; lane l holds dims l + 64 c, so rotate-half pairs
+    // (d, d + 128) are (c, c + 2) of one lane. q lands in red[0], cos / sin
+    // in red[1], the fp16 key / value in red[2]; each thread then takes its
+    // eight dims into registers (red is free again before the combine). The
+    // raw rows are requested before the angles are computed, behind the
+    // first pass's K / V loads.
+    u32x4 kcur = {0u, 0u, 0u, 0u}, vcur = {0u, 0u, 0u, 0u};
+    if constexpr (FQ) {
+        const uint32_t b = blockIdx.z, pos = a.pos_dev[b];
+        float* cs = &red[1][0];
+        uint16_t* kv16 = reinterpret_cast<uint16_t*>(&red[2][0]);   // key [0, HD), value [HD, 2 HD)
+        float e[4] = {0.0f, 0.0f, 0.0f, 0.0f}, w4[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+        if (wave <= G + 1) {
+            const float* src = wave < G   ? a.q_raw + size_t(b) * a.bq + (size_t(g) * G + wave) * HD
+                               : wave == G ? a.k_raw + size_t(b) * a.bkv + size_t(g) * HD
+                                           : a.v_raw + size_t(b) * a.bkv + size_t(g) * HD;
+#pragma unroll
+            for (int c = 0; c < 4; ++c) e[c] = src[lane + 64 * c];
+            if (wave <= G) {
+                const float* w = wave < G ? a.qw : a.kw;
+#pragma unroll
+                for (int c = 0; c < 4; ++c) w4[c] = w[lane + 64 * c];
+            }
+        }
+        if (tid < HD / 2) {
+            float sv, cv;
+            sincosf(float(pos) * f.inv[tid], &sv, &cv);
+            cs[tid] = cv;
+            cs[HD / 2 + tid] = sv;
+        }
+        __syncthreads();
+        if (wave <= G) {
+            const float ss = wave_sum(e[0] * e[0] + e[1] * e[1] + e[2] * e[2] + e[3] * e[3]);
+            const float scale = 1.0f / sqrtf(ss / float(HD) + a.eps);
+#pragma unroll
+            for (int c = 0; c < 4; ++c) e[c] = e[c] * scale * (1.0f + w4[c]);
+#pragma unroll
+            for (int c = 0; c < 2; ++c) {
+                const float cv = cs[lane + 64 * c], sv = cs[HD / 2 + lane + 64 * c];
+                const float lo = e[c], hi = e[c + 2];
+                e[c] = lo * cv - hi * sv;
+                e[c + 2] = lo * sv + hi * cv;
+            }
+            if (wave < G) {
+#pragma unroll
+                for (int c = 0; c < 4; ++c) red[0][wave * HD + lane + 64 * c] = e[c];
+            } else {
+#pragma unroll
+                for (int c = 0; c < 4; ++c) kv16[lane + 64 * c] = f32_to_f16_bits(e[c]);
+            }
+        } else if (wave == G + 1) {
+#pragma unroll
+            for (int c = 0; c < 4; ++c) kv16[HD + lane + 64 * c] = f32_to_f16_bits(e[c]);
+        }
+        __syncthreads();
+#pragma unroll
+        for (int h = 0; h < G; ++h) {
+            const float4 q0 = *reinterpret_cast<const float4*>(&red[0][h * HD + sub * 8]);
+            const float4 q1 = *reinterpret_cast<const float4*>(&red[0][h * HD + sub * 8 + 4]);
+            q[h][0] = q0.x; q[h][1] = q0.y; q[h][2] = q0.z; q[h][3] = q0.w;
+            q[h][4] = q1.x; q[h][5] = q1.y; q[h][6] = q1.z; q[h][7] = q1.w;
+        }
+        kcur = *reinterpret_cast<const u32x4*>(kv16 + sub * 8);
+        vcur = *reinterpret_cast<const u32x4*>(kv16 + HD + sub * 8);
+        // the split holding the current position appends its key / value
+        // for later steps (this launch reads them from kcur / vcur)
+        if (span > 0 && (span - 1u) / chunk == s && tid < kAttnLanes) {
+            const size_t row = size_t(pos) * rowstride + size_t(g) * HD + sub * 8;
+            *reinterpret_cast<u32x4*>(const_cast<uint16_t*>(a.kc) + row) = kcur;
+            *reinterpret_cast<u32x4*>(const_cast<uint16_t*>(a.vc) + row) = vcur;
+        }
+        __syncthreads();   // red is rewritten by the combine
+    } else {
+#pragma unroll
+        for (int h = 0; h < G; ++h) {
+            const float4* qp = reinterpret_cast<const float4*>(a.q + (size_t(g) * G + h) * HD + sub * 8);
+            const float4 q0 = qp[0], q1 = qp[1];
+            q[h][0] = q0.x; q[h][1] = q0.y; q[h][2] = q0.z; q[h][3] = q0.w;
+            q[h][4] = q1.x; q[h][5] = q1.y; q[h][6] = q1.z; q[h][7] = q1.w;
+        }
+    }
+#pragma unroll
+    for (int h = 0; h < G; ++h)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) o[h][e] = 0.0f;
+    if (tid < G) {
+        run[0][tid] = -INFINITY;
+        run[1][tid] = 0.0f;
+    }
+    for (int c0 = 0; c0 < nk; c0 += PASS) {
+        if (c0 > 0) load_pass(c0);
+        if constexpr (FQ) {
+            // the current position (the span's last key) from registers
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const bool cur = j0 + uint32_t(c0 + kp + kAttnRows * u) == span - 1u;
+                kw[u] = cur ? kcur : kw[u];
+                vw[u] = cur ? vcur : vw[u];
+            }
         }
         // ---- scores
         float sv[NV];
@@ -560,11 +653,24 @@ int launch_attention(AttnArgs a, uint32_t max_span, hipStream_t st) {
     uint32_t chunk = (max_span + a.nsplit - 1) / a.nsplit;
     if (chunk < uint32_t(kAttnMinChunk)) chunk = kAttnMinChunk;
     const int U = chunk <= 32 ? 2 : (chunk <= 64 ? 4 : 8);
+    const bool fq = a.q_raw != nullptr;
+    RopeFreq f{};
+    if (fq) {
+        if (!a.pos_dev || !a.k_raw || !a.v_raw || !a.qw || !a.kw || !(a.theta > 0.0f))
+            return set_error(XP_E_ARG, "attention: the fused QK-norm / RoPE form needs pos_dev, k_raw, "
+                                       "v_raw, both norm weights and theta > 0");
+        rope_freq(f, a.head_dim, a.theta);
+    } else if (!a.q) {
+        return set_error(XP_E_ARG, "attention: null q");
+    }
     const dim3 grid(a.nsplit, a.kv_heads, a.batch), block(kAttnThreads);
-#define XP_ATTN_LAUNCH(GG)                                                                          \
-    if (U == 2) hipLaunchKernelGGL((attention_decode_kernel<GG, 2>), grid, block, 0, st, a);       \
-    else if (U == 4) hipLaunchKernelGGL((attention_decode_kernel<GG, 4>), grid, block, 0, st, a);  \
-    else hipLaunchKernelGGL((attention_decode_kernel<GG, 8>), grid, block, 0, st, a);
+#define XP_ATTN_U(GG, FF)                                                                                 \
+    if (U == 2) hipLaunchKernelGGL((attention_decode_kernel<GG, 2, FF>), grid, block, 0, st, a, f);      \
+    else if (U == 4) hipLaunchKernelGGL((attention_decode_kernel<GG, 4, FF>), grid, block, 0, st, a, f); \
+    else hipLaunchKernelGGL((attention_decode_kernel<GG, 8, FF>), grid, block, 0, st, a, f);
+#define XP_ATTN_LAUNCH(GG)        \
+    if (fq) { XP_ATTN_U(GG, true) } \
+    else { XP_ATTN_U(GG, false) }
     if (G == 1) {
         XP_ATTN_LAUNCH(1)
     } else if (G == 2) {
@@ -573,6 +679,7 @@ int launch_attention(AttnArgs a, uint32_t max_span, hipStream_t st) {
         XP_ATTN_LAUNCH(4)
     }
 #undef XP_ATTN_LAUNCH
+#undef XP_ATTN_U
     hipError_t e = hipGetLastError();
     if (e != hipSuccess)
         return set_error(XP_E_HIP, "attention: launch -> %s", hipGetErrorString(e));

@@ -98,6 +98,22 @@ struct AttnArgs {
     uint32_t batch = 1;
     uint32_t bq = 0;
     size_t bcache = 0, bpart = 0;
+    // Fused QK-norm + RoPE + KV append (decode with pos_dev, every sequence
+    // its own cache rows): with q_raw set, each workgroup forms the normed,
+    // rotated q of its kv head's query heads and the current key / value
+    // from q_raw, k_raw and v_raw (sequence b at + b bq, + b bkv) itself, uses
+    // the current key / value from LDS, and the split holding the current
+    // position appends them to the caches; q is not read. Not for prefill
+    // rows that share one cache (a row's span includes rows the same launch
+    // appends).
+    const float* q_raw = nullptr;
+    const float* k_raw = nullptr;
+    const float* v_raw = nullptr;
+    const float* qw = nullptr;   // QK-norm weights of the query heads / the key
+    const float* kw = nullptr;
+    float eps = 0.0f;
+    float theta = 0.0f;          // RoPE base of the layer
+    uint32_t bkv = 0;
 };
 // Arrival tickets per (sequence, kv head) of the decode attention: one for
 // the final combine, one per group of 16 splits (at most 256 splits).
