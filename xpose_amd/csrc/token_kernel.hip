@@ -74,6 +74,26 @@ constexpr int      kTkMaxLayers = 64;
 // Poll back-off of the first phase of the gate/up stage's wait (one thread
 // watching for the layer's attention output), in units of 64 cycles.
 constexpr int      kGuSleep     = 32;
+// Column slices of the q|k|v, o and down tiles: a tile covers 64 / S columns
+// of a column group over its whole k range, lane l taking column l / S and
+// block slot l % S of each S-block step, so a wave's S-block step is one dot
+// per lane and the tile's outputs are complete without more k splits (a
+// consumer re-reads fewer partials while it polls). Gate/up keeps whole
+// column groups. Build-time knobs (-D) for sweeps.
+#ifndef XP_TOK_QKV_SLICES
+#define XP_TOK_QKV_SLICES 2
+#endif
+#ifndef XP_TOK_O_SLICES
+#define XP_TOK_O_SLICES 2
+#endif
+#ifndef XP_TOK_DOWN_SLICES
+#define XP_TOK_DOWN_SLICES 2
+#endif
+constexpr uint32_t kTkSQ = XP_TOK_QKV_SLICES;
+constexpr uint32_t kTkSO = XP_TOK_O_SLICES;
+constexpr uint32_t kTkSD = XP_TOK_DOWN_SLICES;
+static_assert((kTkSQ == 1 || kTkSQ == 2 || kTkSQ == 4) && (kTkSO == 1 || kTkSO == 2 || kTkSO == 4) &&
+              (kTkSD == 1 || kTkSD == 2 || kTkSD == 4), "1, 2 or 4 column slices");
 
 typedef unsigned long long ll_t;
 
@@ -94,11 +114,17 @@ struct TkShape {
     static constexpr uint32_t QB = HB / KQ;                 // blocks per q|k|v tile
     static constexpr uint32_t OB = QD / kBlk / KO;          // blocks per o tile
     static constexpr uint32_t NOG = H / kGrp;               // o column groups
-    static constexpr uint32_t N_QKV = QKVD / kGrp * KQ;
+    static constexpr uint32_t SQ = kTkSQ, SO = kTkSO, SD = kTkSD;   // column slices
+    static constexpr uint32_t N_QKV = QKVD / kGrp * KQ * SQ;
     static constexpr uint32_t N_COMB = NH * 4;              // local layers' combine tiles
-    static constexpr uint32_t N_O = NOG * KO;
+    static constexpr uint32_t N_O = NOG * KO * SO;
     static constexpr uint32_t N_GU = 2 * FFN / kGrp;
-    static constexpr uint32_t N_DN = (H / kGrp) * NCH;
+    static constexpr uint32_t N_DN = (H / kGrp) * NCH * SD;
+    // S-block steps per wave of a tile (blocks / (8 waves x S slots), rounded up)
+    static constexpr int RK = int((QB + 8 * SQ - 1) / (8 * SQ));
+    static constexpr int RO = int((OB + 8 * SO - 1) / (8 * SO));
+    static constexpr int RD = int((DQ * 4 + 8 * SD - 1) / (8 * SD));
+    static constexpr int RQ = int((HB + 7) / 8);
     static constexpr uint32_t NQH = H / 128;                // lm_head quads per column
     static_assert(H % 128 == 0 && FFN % 128 == 0, "hidden and ffn must be multiples of 128");
     static_assert(HO <= uint32_t(kTkThreads) && QO <= uint32_t(kTkThreads) &&
@@ -288,17 +314,30 @@ __device__ __forceinline__ void own_residual(float (&x)[kOwn], const float (&a)[
 #pragma unroll
     for (uint32_t e = 0; e < kOwn; ++e) x[e] = a[e] + t[e] * scale * (1.0f + w[e]);
 }
-// y = x * rsqrt(mean(x^2) + eps) * (1 + w) (rmsnorm_apply_gemma).
-template <uint32_t H>
-__device__ __forceinline__ void own_norm(float (&y)[kOwn], const float (&x)[kOwn], const float (&w)[kOwn],
-                                         float eps, float* rs) {
+// RMSNorm feeding a matvec (rmsnorm_apply_gemma, y = x * rsqrt(mean(x^2) +
+// eps) * (1 + w)), with its scalar deferred: the matvec of y is that scalar
+// times the matvec of x (1 + w), and the block fixed-point staging is
+// invariant to a common scale. own_norm_defer returns x (1 + w) and leaves
+// each wave's partial sum of x^2 in rs; after the staging barrier,
+// norm_scale(rs) is the scalar the caller multiplies its dot products by.
+// The sum is then formed while the vector is staged, not before.
+__device__ __forceinline__ void own_norm_defer(float (&y)[kOwn], const float (&x)[kOwn],
+                                               const float (&w)[kOwn], float* rs) {
     float ss = 0.0f;
 #pragma unroll
-    for (uint32_t e = 0; e < kOwn; ++e) ss = fmaf(x[e], x[e], ss);
-    ss = blk_sum(ss, rs);
-    const float scale = 1.0f / sqrtf(ss / float(H) + eps);
-#pragma unroll
-    for (uint32_t e = 0; e < kOwn; ++e) y[e] = x[e] * scale * (1.0f + w[e]);
+    for (uint32_t e = 0; e < kOwn; ++e) {
+        ss = fmaf(x[e], x[e], ss);
+        y[e] = x[e] * (1.0f + w[e]);
+    }
+    ss = wave_sum(ss);
+    if ((threadIdx.x & (kWave - 1)) == 0) rs[threadIdx.x / kWave] = ss;
+}
+template <uint32_t H>
+__device__ __forceinline__ float norm_scale(const float* rs, float eps) {
+    const float4 p = *reinterpret_cast<const float4*>(rs);
+    const float4 q = *reinterpret_cast<const float4*>(rs + 4);
+    const float ss = ((p.x + p.y) + (p.z + p.w)) + ((q.x + q.y) + (q.z + q.w));
+    return 1.0f / sqrtf(ss / float(H) + eps);
 }
 
 // Fixed-point staging (the planes of stage_x8, xp_device.hpp) from four
@@ -345,65 +384,74 @@ __device__ __forceinline__ float tk_scale(u32x2 raw, uint32_t i) {
 }
 
 // ---- matvec tiles ------------------------------------------------------------------
-// A tile: column group g of a KM4 matrix (nblk 32-blocks of k, cols columns),
-// k blocks [b0, b0 + nb). Wave w takes blocks b0 + min(w + 8 r, nb - 1) for
-// r < R; a repeated (clamped) block is computed and weighted by zero.
+// A tile: columns h CW .. h CW + CW - 1 (CW = 64 / S) of column group g of a
+// KM4 matrix (nblk 32-blocks of k, cols columns), k blocks [b0, b0 + nb).
+// Lane l takes column h CW + l / S and block slot q = l % S; wave w takes the
+// S-block steps w + 8 r (r < R), i.e. block b0 + min(S (w + 8 r) + q, nb - 1);
+// a repeated (clamped) block is computed and weighted by zero. S = 1 is one
+// whole column group, lane = column.
 template <int R>
 struct TkW {
     u32x4 w[R];
     u32x2 s[R];
 };
 
-template <int R>
+template <int R, uint32_t S = 1>
 __device__ __forceinline__ void tile_prefetch(TkW<R>& p, const void* wq, const void* sc, uint32_t nblk,
-                                              uint32_t cols, uint32_t g, uint32_t b0, uint32_t nb,
-                                              uint32_t wave, uint32_t lane) {
+                                              uint32_t cols, uint32_t g, uint32_t h, uint32_t b0,
+                                              uint32_t nb, uint32_t wave, uint32_t lane) {
+    constexpr uint32_t CW = kGrp / S;
     const u32x4* w = static_cast<const u32x4*>(wq);
     const u32x2* s = static_cast<const u32x2*>(sc);
+    const uint32_t cl = h * CW + lane / S, q = lane % S;
 #pragma unroll
     for (int r = 0; r < R; ++r) {
-        const uint32_t b = b0 + min(wave + 8u * r, nb - 1u);
-        p.w[r] = ldg_stream4(w + (size_t(g) * nblk + b) * kGrp + lane);
-        p.s[r] = ldg_stream2(s + size_t(b / 4u) * cols + g * kGrp + lane);
+        const uint32_t b = b0 + min(S * (wave + 8u * r) + q, nb - 1u);
+        p.w[r] = ldg_stream4(w + (size_t(g) * nblk + b) * kGrp + cl);
+        p.s[r] = ldg_stream2(s + size_t(b / 4u) * cols + g * kGrp + cl);
     }
 }
 
 // Dot of the wave's blocks with the staged planes (S.qx[0] = block b0; the
-// scale of block b0 + w + 8 r is component (b0 + w) % 4 of its quad, the
-// same for all r), reduced over the 8 waves in order. The result is valid in
-// wave 0 (lane = column); the caller publishes it. Starts after the staging
-// barrier; ends with a barrier.
-template <int FMT, int R>
-__device__ __forceinline__ float tile_dot(const TkW<R>& p, TkSmem& S, uint32_t b0, uint32_t nb,
+// scale of block b0 + S (w + 8 r) + q is component (b0 + S w + q) % 4 of its
+// quad, the same for all r), the S block slots of a column added across
+// adjacent lanes, then reduced over the 8 waves in order. The result is valid
+// in wave 0, lane l holding column l / S; the caller publishes it. Starts
+// after the staging barrier; ends with a barrier.
+template <int FMT, int R, uint32_t S = 1>
+__device__ __forceinline__ float tile_dot(const TkW<R>& p, TkSmem& Sm, uint32_t b0, uint32_t nb,
                                           uint32_t wave, uint32_t lane) {
-    const uint32_t sc = (b0 + wave) % 4u;
+    const uint32_t q = lane % S;
+    const uint32_t sc = (b0 + S * wave + q) % 4u;
     // Every block's staged planes and scale are read before any is used: the
     // reads return in order while the first blocks are multiplied, instead of
     // one LDS round trip per block.
-    QxBlock q[R];
+    QxBlock qb[R];
     float sxv[R];
 #pragma unroll
     for (int r = 0; r < R; ++r) {
-        const uint32_t lb = min(wave + 8u * r, nb - 1u);
-        sxv[r] = S.sx[lb];
-        q[r] = S.qx[lb];
+        const uint32_t lb = min(S * (wave + 8u * r) + q, nb - 1u);
+        sxv[r] = Sm.sx[lb];
+        qb[r] = Sm.qx[lb];
     }
     __builtin_amdgcn_sched_barrier(0);
     float acc = 0.0f;
 #pragma unroll
     for (int r = 0; r < R; ++r) {
         float f = tk_scale<FMT>(p.s[r], sc) * sxv[r];
-        if (wave + 8u * r >= nb) f = 0.0f;
-        acc = fmaf(f, float(block_dot(p.w[r], q[r])), acc);
+        if (S * (wave + 8u * r) + q >= nb) f = 0.0f;
+        acc = fmaf(f, float(block_dot(p.w[r], qb[r])), acc);
     }
-    S.red[wave][lane] = acc;
+    if constexpr (S >= 2) acc += dpp_f<0xB1, 0xF>(acc, 0.0f);   // quad_perm [1,0,3,2]: slot q ^ 1
+    if constexpr (S >= 4) acc += dpp_f<0x4E, 0xF>(acc, 0.0f);   // quad_perm [2,3,0,1]: slot q ^ 2
+    Sm.red[wave][lane] = acc;
     __syncthreads();
     float y = 0.0f;
     if (wave == 0) {
         // all eight partials in flight at once, then summed in wave order
         float pw[kTkWaves];
 #pragma unroll
-        for (int w = 0; w < kTkWaves; ++w) pw[w] = S.red[w][lane];
+        for (int w = 0; w < kTkWaves; ++w) pw[w] = Sm.red[w][lane];
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int w = 0; w < kTkWaves; ++w) y += pw[w];
@@ -411,11 +459,16 @@ __device__ __forceinline__ float tile_dot(const TkW<R>& p, TkSmem& S, uint32_t b
     return y;
 }
 
-// Wave 0 publishes its 64 column results y (lane = column) at slot s0 + lane.
+// Wave 0 publishes its 64 / S column results y (lane l holding column l / S)
+// at slots s0 + column: lane 2 S m stores columns 2 m and 2 m + 1, the second
+// read from lane 2 S m + S (row_shl within a DPP row; quad_perm xor 1 for S = 1).
+template <uint32_t S = 1>
 __device__ __forceinline__ void tile_put(rsrc_t r, uint32_t soff, uint32_t s0, float y, uint32_t lane,
                                          uint32_t tag) {
-    const float yn = dpp_f<0xB1, 0xF>(y, 0.0f);   // lane ^ 1
-    if ((lane & 1u) == 0u) ll_st2(r, (s0 + lane) * 8u, soff, y, yn, tag);
+    float yn;
+    if constexpr (S == 1) yn = dpp_f<0xB1, 0xF>(y, 0.0f);
+    else yn = dpp_f<0x100 + int(S), 0xF>(y, 0.0f);
+    if (lane % (2u * S) == 0u) ll_st2(r, (s0 + lane / S) * 8u, soff, y, yn, tag);
 }
 
 __device__ __forceinline__ float f16_round(float v) { return f16_bits_to_f32(f32_to_f16_bits(v)); }
@@ -561,27 +614,33 @@ __global__ __launch_bounds__(kTkThreads) void token_kernel(TokArgs a) {
     // waits in the gate/up stage: a workgroup busy in the previous stage
     // would otherwise start streaming those weights only when its inputs are
     // already there.
-    constexpr int RQ = int(Sh::HB + 7) / 8;           // gate/up blocks per wave
-    constexpr int RK = int(Sh::QB + 7) / 8;           // QKV blocks per wave
-    constexpr int RD = int(Sh::DQ * 4) / 8;           // down blocks per wave
-    // QKV tile t: column group g of matrix m (q, k, v), k half c.
-    auto qkv_tile = [&](uint32_t t, uint32_t& m, uint32_t& g, uint32_t& c) {
+    constexpr int RQ = Sh::RQ;                        // gate/up blocks per wave
+    constexpr int RK = Sh::RK;                        // QKV S-block steps per wave
+    constexpr int RD = Sh::RD;                        // down S-block steps per wave
+    constexpr int RO = Sh::RO;                        // o S-block steps per wave
+    // QKV tile t = ((column group of q | k | v) KQ + k part c) SQ + slice h:
+    // matrix m (q, k, v), its column group g.
+    auto qkv_tile = [&](uint32_t t, uint32_t& m, uint32_t& g, uint32_t& c, uint32_t& h) {
         constexpr uint32_t qg = QD / kGrp, kg = kTkHD / kGrp;
-        const uint32_t tt = t / Sh::KQ;
-        c = t % Sh::KQ;
+        h = t % Sh::SQ;
+        const uint32_t tc = t / Sh::SQ;
+        const uint32_t tt = tc / Sh::KQ;
+        c = tc % Sh::KQ;
         m = tt < qg ? 0u : (tt < qg + kg ? 1u : 2u);
         g = m == 0 ? tt : (m == 1 ? tt - qg : tt - qg - kg);
     };
     auto prefetch_qkv = [&](TkW<RK>& p, uint32_t l, uint32_t t) {
-        uint32_t m, g, c;
-        qkv_tile(t, m, g, c);
-        tile_prefetch(p, S.lt[l].w[m], S.lt[l].s[m], Sh::HB, m == 0 ? QD : kTkHD, g, c * Sh::QB, Sh::QB,
-                      wave, lane);
+        uint32_t m, g, c, h;
+        qkv_tile(t, m, g, c, h);
+        tile_prefetch<RK, Sh::SQ>(p, S.lt[l].w[m], S.lt[l].s[m], Sh::HB, m == 0 ? QD : kTkHD, g, h,
+                                  c * Sh::QB, Sh::QB, wave, lane);
     };
+    // down tile t = (column group g NCH + k chunk c) SD + slice h
     auto prefetch_dn = [&](TkW<RD>& p, uint32_t l, uint32_t t) {
-        const uint32_t g = t / NCH, q0 = Sh::DQ * (t % NCH);
-        tile_prefetch(p, S.lt[l].w[6], S.lt[l].s[6], FFN / kBlk, H, g, 4u * q0,
-                      4u * min(Sh::DQ, Sh::NQF - q0), wave, lane);
+        const uint32_t h = t % Sh::SD, tc = t / Sh::SD;
+        const uint32_t g = tc / NCH, q0 = Sh::DQ * (tc % NCH);
+        tile_prefetch<RD, Sh::SD>(p, S.lt[l].w[6], S.lt[l].s[6], FFN / kBlk, H, g, h, 4u * q0,
+                                  4u * min(Sh::DQ, Sh::NQF - q0), wave, lane);
     };
     TkW<RK> pq;
     if (t_qkv < Sh::N_QKV) prefetch_qkv(pq, 0u, t_qkv);
@@ -595,8 +654,8 @@ __global__ __launch_bounds__(kTkThreads) void token_kernel(TokArgs a) {
         // ================= QKV =================
         unsigned long long t_in = 0;
         for (uint32_t t = t_qkv; t < Sh::N_QKV; t += nwg) {
-            uint32_t m, g, c;
-            qkv_tile(t, m, g, c);
+            uint32_t m, g, c, h;
+            qkv_tile(t, m, g, c, h);
             if (t != t_qkv) prefetch_qkv(pq, l, t);
             float w_in[kOwn] = {}, w_post[kOwn] = {}, x[kOwn] = {};
             if (hown) {
@@ -636,7 +695,8 @@ __global__ __launch_bounds__(kTkThreads) void token_kernel(TokArgs a) {
             }
             if (t == t_qkv) t_in = tk_now(a);
             float xn[kOwn];
-            own_norm<H>(xn, x, w_in, eps, RS());
+            float* rsn = RS();
+            own_norm_defer(xn, x, w_in, rsn);
             {
                 // stage this tile's k half: blocks c QB .. c QB + QB - 1
                 constexpr uint32_t tpb = kBlk / kOwn;   // owner threads per block
@@ -644,10 +704,12 @@ __global__ __launch_bounds__(kTkThreads) void token_kernel(TokArgs a) {
                 if (hown && i < Sh::QB * tpb) own_stage(S, xn, i);
             }
             __syncthreads();
-            const float y = tile_dot<FMT>(pq, S, c * Sh::QB, Sh::QB, wave, lane);
+            float y = tile_dot<FMT, RK, Sh::SQ>(pq, S, c * Sh::QB, Sh::QB, wave, lane);
             if (wave == 0) {
+                y *= norm_scale<H>(rsn, eps);
                 const uint32_t o = c * Sh::QKVD + (m == 0u ? 0u : (m == 1u ? QD : QD + kTkHD));
-                tile_put(rr, soff, uint32_t(lay.qkv) + o + g * kGrp, y, lane, tag);
+                tile_put<Sh::SQ>(rr, soff, uint32_t(lay.qkv) + o + g * kGrp + h * (kGrp / Sh::SQ), y,
+                                 lane, tag);
             }
             // x entering the layer, for the gate/up stage: tile t < H / 64
             // stores elements 64 t .. 64 t + 63 (spread so that no workgroup
@@ -984,11 +1046,13 @@ __global__ __launch_bounds__(kTkThreads) void token_kernel(TokArgs a) {
 
         // ================= O projection =================
         for (uint32_t t = t_o; t < Sh::N_O; t += nwg) {
-            // column group g, k half c: attention output [c QD / KO, (c + 1) QD / KO)
-            const uint32_t g = t / Sh::KO, c = t % Sh::KO;
+            // t = (column group g KO + k part c) SO + slice h: attention
+            // output [c QD / KO, (c + 1) QD / KO)
+            const uint32_t h = t % Sh::SO, tc = t / Sh::SO;
+            const uint32_t g = tc / Sh::KO, c = tc % Sh::KO;
             constexpr uint32_t nb = Sh::OB;
-            TkW<(nb + 7) / 8> p;
-            tile_prefetch(p, L.w[3], L.s[3], QD / kBlk, H, g, c * nb, nb, wave, lane);
+            TkW<RO> p;
+            tile_prefetch<RO, Sh::SO>(p, L.w[3], L.s[3], QD / kBlk, H, g, h, c * nb, nb, wave, lane);
             if (tid < Sh::QO / Sh::KO) {
                 uint32_t off[kOwnP];
                 bool act[kOwnP];
@@ -1003,8 +1067,10 @@ __global__ __launch_bounds__(kTkThreads) void token_kernel(TokArgs a) {
             }
             __syncthreads();
             if (t == t_o) t_in = tk_now(a);
-            const float y = tile_dot<FMT>(p, S, c * nb, nb, wave, lane);
-            if (wave == 0) tile_put(rr, soff, uint32_t(lay.o) + c * H + g * kGrp, y, lane, tag);
+            const float y = tile_dot<FMT, RO, Sh::SO>(p, S, c * nb, nb, wave, lane);
+            if (wave == 0)
+                tile_put<Sh::SO>(rr, soff, uint32_t(lay.o) + c * H + g * kGrp + h * (kGrp / Sh::SO), y,
+                                 lane, tag);
         }
         tk_trace_stage(a, wg, l, 3u, t_in);
         t_in = 0;
@@ -1016,7 +1082,7 @@ __global__ __launch_bounds__(kTkThreads) void token_kernel(TokArgs a) {
             constexpr uint32_t ng = FFN / kGrp;
             const uint32_t m = t < ng ? 4u : 5u, g = t < ng ? t : t - ng;
             TkW<RQ> p;
-            tile_prefetch(p, L.w[m], L.s[m], Sh::HB, FFN, g, 0u, Sh::HB, wave, lane);
+            tile_prefetch(p, L.w[m], L.s[m], Sh::HB, FFN, g, 0u, 0u, Sh::HB, wave, lane);
             float w_post[kOwn] = {}, w_in[kOwn] = {}, xa[kOwn] = {}, o[kOwn] = {};
             if (hown) {
                 ld_own(w_post, L.norm[1] + kOwn * tid);
@@ -1060,11 +1126,15 @@ __global__ __launch_bounds__(kTkThreads) void token_kernel(TokArgs a) {
             float x[kOwn], xn[kOwn];
             own_residual<H>(x, xa, o, w_post, eps, RS());
             if (t == t_gu) t_in = tk_now(a);
-            own_norm<H>(xn, x, w_in, eps, RS());
+            float* rsn = RS();
+            own_norm_defer(xn, x, w_in, rsn);
             if (hown) own_stage(S, xn, tid);
             __syncthreads();
-            const float y = tile_dot<FMT>(p, S, 0u, Sh::HB, wave, lane);
-            if (wave == 0) tile_put(rr, soff, uint32_t(lay.gu) + (m == 4u ? 0u : FFN) + g * kGrp, y, lane, tag);
+            float y = tile_dot<FMT>(p, S, 0u, Sh::HB, wave, lane);
+            if (wave == 0) {
+                y *= norm_scale<H>(rsn, eps);
+                tile_put(rr, soff, uint32_t(lay.gu) + (m == 4u ? 0u : FFN) + g * kGrp, y, lane, tag);
+            }
             // x after the attention block, for the next layer: spread and stored last, as xa
             if (t < Sh::NOG && tid / (kGrp / kOwn) == t) own_put(rr, soff, uint32_t(lay.xb) + kOwn * tid, x, tag);
         }
@@ -1073,7 +1143,8 @@ __global__ __launch_bounds__(kTkThreads) void token_kernel(TokArgs a) {
 
         // ================= down =================
         for (uint32_t t = t_dn; t < Sh::N_DN; t += nwg) {
-            const uint32_t g = t / NCH, c = t % NCH;
+            const uint32_t h = t % Sh::SD, tc = t / Sh::SD;
+            const uint32_t g = tc / NCH, c = tc % NCH;
             const uint32_t q0 = Sh::DQ * c, nq = min(Sh::DQ, Sh::NQF - q0);
             const uint32_t nb = 4u * nq, k0 = 128u * q0;
             if (t != t_dn) prefetch_dn(pdn, l, t);
@@ -1096,8 +1167,10 @@ __global__ __launch_bounds__(kTkThreads) void token_kernel(TokArgs a) {
             }
             __syncthreads();
             if (t == t_dn) t_in = tk_now(a);
-            const float y = tile_dot<FMT>(pdn, S, 4u * q0, nb, wave, lane);
-            if (wave == 0) tile_put(rr, soff, uint32_t(lay.dnp) + c * H + g * kGrp, y, lane, tag);
+            const float y = tile_dot<FMT, RD, Sh::SD>(pdn, S, 4u * q0, nb, wave, lane);
+            if (wave == 0)
+                tile_put<Sh::SD>(rr, soff, uint32_t(lay.dnp) + c * H + g * kGrp + h * (kGrp / Sh::SD), y,
+                                 lane, tag);
         }
         if (t_dn >= Sh::N_DN && l + 1u < a.n_layers && t_qkv < Sh::N_QKV) prefetch_qkv(pq, l + 1u, t_qkv);
         tk_trace_stage(a, wg, l, 5u, t_in);
@@ -1132,6 +1205,7 @@ __global__ __launch_bounds__(kTkThreads) void token_kernel(TokArgs a) {
         load_u(1, 1);
         load_u(2, 2);
     }
+    float* rsn_lm;
     {
         float wf_post[kOwn] = {}, wf_in[kOwn] = {}, x[kOwn], xn[kOwn];
         if (hown) {
@@ -1139,10 +1213,12 @@ __global__ __launch_bounds__(kTkThreads) void token_kernel(TokArgs a) {
             ld_own(wf_in, a.final_norm + kOwn * tid);
         }
         after_ffn(x, a.n_layers - 1u, wf_post);
-        own_norm<H>(xn, x, wf_in, eps, RS());
+        rsn_lm = RS();
+        own_norm_defer(xn, x, wf_in, rsn_lm);
         if (hown) own_stage(S, xn, tid);
         __syncthreads();
     }
+    const float lm_scale = norm_scale<H>(rsn_lm, eps);
     float bv = -INFINITY;
     uint32_t bi = 0u;
     float acc = 0.0f;
@@ -1156,6 +1232,7 @@ __global__ __launch_bounds__(kTkThreads) void token_kernel(TokArgs a) {
         }
         if (q == nqh - 1u) {
             const uint32_t j = (gw + (u / nqh) * nw) * kGrp + lane;
+            acc *= lm_scale;
             a.logits[j] = acc;
             am_better(bv, bi, acc, j);
             acc = 0.0f;

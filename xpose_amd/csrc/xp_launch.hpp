@@ -268,9 +268,20 @@ struct TokArgs {
 // The token kernel's down projection is split along k into chunks of this
 // many quads (128 k each); the next layer adds the chunks' partial sums. The
 // q|k|v and o projections are split along k into this many halves likewise.
-constexpr uint32_t kTokDownQuads = 8;
-constexpr uint32_t kTokQkvSplit = 2;
-constexpr uint32_t kTokOSplit = 2;
+// Build-time knobs (-D) for sweeps; the whole library must be built with the
+// same values, since the session sizes the exchange slots from them.
+#ifndef XP_TOK_DOWN_QUADS
+#define XP_TOK_DOWN_QUADS 14
+#endif
+#ifndef XP_TOK_QKV_SPLIT
+#define XP_TOK_QKV_SPLIT 1
+#endif
+#ifndef XP_TOK_O_SPLIT
+#define XP_TOK_O_SPLIT 1
+#endif
+constexpr uint32_t kTokDownQuads = XP_TOK_DOWN_QUADS;
+constexpr uint32_t kTokQkvSplit = XP_TOK_QKV_SPLIT;
+constexpr uint32_t kTokOSplit = XP_TOK_O_SPLIT;
 __host__ __device__ constexpr uint32_t tok_down_chunks(uint32_t ffn) {
     return (ffn / 128u + kTokDownQuads - 1u) / kTokDownQuads;
 }
