@@ -147,7 +147,6 @@ struct TkSmem {
     float    red[kTkWaves][kWave];           // per-wave tile partials
     float    cs[2][kTkHD / 2];               // RoPE cos / sin at this position,
     float    sn[2][kTkHD / 2];               // [0] local theta, [1] global theta
-    float    xq[kTkMaxQH * kTkHD + 2 * kTkHD];   // raw q | k | v
     alignas(16) float qh[kTkMaxQH][kTkHD];   // normed, rotated q
     float    kn[kTkHD];                      // current key / value (fp16-rounded)
     float    vn[kTkHD];
@@ -747,102 +746,84 @@ __global__ __launch_bounds__(kTkThreads) void token_kernel(TokArgs a) {
             constexpr uint32_t CW = decltype(cw_c)::value;
             constexpr uint32_t TPK = kTkThreads / CW;        // threads per key (scores)
             constexpr uint32_t NCK = kTkHD / (4u * TPK);      // float4 of a key per thread
-            constexpr uint32_t KPG = CW / (kTkThreads / 128u); // keys per value group
+            constexpr uint32_t HK = CW / 2u;                  // keys per lane half (values)
             static_assert(TPK == 16u || TPK == 32u, "a key's parts span one or two DPP rows");
+            static_assert(kTkHD == 32u * kTkWaves, "values: 32 dims per wave");
+            static_assert(NH % 4u == 0u, "values: each lane stores one of four heads");
             const uint32_t j0 = s_att * CW;
             // score mapping: key jk = tid / TPK; part p holds dims 4 TPK c + 4 p .. + 3,
             // c < NCK (the parts of a key read consecutive float4 of q: no LDS
             // bank conflicts)
             const uint32_t jk = tid / TPK, part = tid % TPK;
-            // value mapping: dims 2*dp, 2*dp+1 of keys kgv*KPG .. kgv*KPG+KPG-1
-            const uint32_t dp = tid % 128u, kgv = tid / 128u;
+            // value mapping: wave w, lane l: dim dv = 32 w + l % 32 of keys
+            // kh HK .. kh HK + HK - 1, kh = l / 32, all query heads; the two
+            // key halves meet across lanes l and l ^ 32
+            const uint32_t dv = 32u * wave + lane % 32u, kh = lane / 32u;
+            // Key / value rows past the span are clamped to its last row and
+            // every load is unconditional (a guarded load becomes a branch
+            // that waits for it); whatever such a row holds (the last one is
+            // the current position, not yet appended) is dropped by selects.
             u32x2 kr[NCK];
-            uint32_t vw[KPG];
-#pragma unroll
-            for (uint32_t c = 0; c < NCK; ++c) kr[c] = u32x2{0u, 0u};
-#pragma unroll
-            for (uint32_t i = 0; i < KPG; ++i) vw[i] = 0u;
-            if (j0 + jk < span) {
-                const uint16_t* kp = L.kc + size_t(kv0 + j0 + jk) * kTkHD + 4u * part;
+            uint32_t vh[HK];
+            {
+                const uint16_t* kp = L.kc + size_t(kv0 + min(j0 + jk, span - 1u)) * kTkHD + 4u * part;
 #pragma unroll
                 for (uint32_t c = 0; c < NCK; ++c) kr[c] = *(const XP_GLOBAL u32x2*)(kp + 4u * TPK * c);
             }
 #pragma unroll
-            for (uint32_t i = 0; i < KPG; ++i) {
-                const uint32_t jj = j0 + kgv * KPG + i;
-                if (jj < span) vw[i] = ldg32(L.vc + size_t(kv0 + jj) * kTkHD + 2u * dp);
-            }
-            // QK-norm weights of this wave's head (waves 0..NH-1: q heads, NH: the kv head)
-            static_assert(NH < uint32_t(kTkWaves), "one wave per q head plus one for the kv head");
+            for (uint32_t i = 0; i < HK; ++i)
+                vh[i] = ldg16(L.vc + size_t(kv0 + min(j0 + kh * HK + i, span - 1u)) * kTkHD + dv);
+            // Wave h <= NH + 1 takes vector h of q | k | v (the q heads, the
+            // key, the value): lane l holds elements 2 l, 2 l + 1, 2 l + 128,
+            // 2 l + 129 (slot pairs l and l + 64), so its rotate-half pairs
+            // (d, d + 128) are its own. QK-norm weights at the same elements.
+            static_assert(NH + 2u <= uint32_t(kTkWaves), "one wave per q head, the key and the value");
+            static_assert(kTkHD == 256u, "two slot pairs per lane per head");
             float wqk[4] = {0.0f, 0.0f, 0.0f, 0.0f};
             if (wave <= NH) {
-                const float* w = wave < NH ? L.norm[4] : L.norm[5];
-#pragma unroll
-                for (int c = 0; c < 4; ++c) wqk[c] = ldgf(w + lane + 64 * c);
+                const float* w = (wave < NH ? L.norm[4] : L.norm[5]) + 2u * lane;
+                const u32x2 w0 = *(const XP_GLOBAL u32x2*)(w);
+                const u32x2 w1 = *(const XP_GLOBAL u32x2*)(w + kTkHD / 2u);
+                wqk[0] = __uint_as_float(w0.x); wqk[1] = __uint_as_float(w0.y);
+                wqk[2] = __uint_as_float(w1.x); wqk[3] = __uint_as_float(w1.y);
             }
-            {
-                // raw q | k | v = sum of the k halves' partials: pairs tid and
-                // tid + 512 of each half
-                constexpr uint32_t NP = Sh::QKVD / 2;
-                constexpr int NL = int((NP + kTkThreads - 1) / kTkThreads);
-                uint32_t off[NL * Sh::KQ];
-                bool act[NL * Sh::KQ];
-                u32x4 v[NL * Sh::KQ];
-#pragma unroll
-                for (uint32_t c = 0; c < Sh::KQ; ++c) {
-#pragma unroll
-                    for (int i = 0; i < NL; ++i) {
-                        const uint32_t pi = tid + uint32_t(kTkThreads) * i;
-                        act[c * NL + i] = pi < NP;
-                        off[c * NL + i] = (uint32_t(lay.qkv) + c * Sh::QKVD + 2u * min(pi, NP - 1u)) * 8u;
-                    }
-                }
+            const uint32_t th = glob ? 1u : 0u;
+            if (wave <= NH + 1u) {
+                static_assert(Sh::KQ == 1u, "attention reads q | k | v whole (no k parts)");
+                uint32_t off[2];
+                const bool act[2] = {true, true};
+                u32x4 v[2];
+                const uint32_t p0 = uint32_t(lay.qkv) + wave * kTkHD + 2u * lane;
+                off[0] = p0 * 8u;
+                off[1] = (p0 + kTkHD / 2u) * 8u;
                 ll_wait(rr, soff, off, act, v, tag, a.state);
+                float e[4] = {__uint_as_float(v[0].x), __uint_as_float(v[0].z), __uint_as_float(v[1].x),
+                              __uint_as_float(v[1].z)};
+                if (wave <= NH) {
+                    // QK-norm (wave sum) and RoPE of this head, in registers
+                    float ss = e[0] * e[0] + e[1] * e[1] + e[2] * e[2] + e[3] * e[3];
+                    ss = wave_sum(ss);
+                    const float scale = 1.0f / sqrtf(ss / float(kTkHD) + eps);
 #pragma unroll
-                for (int i = 0; i < NL; ++i) {
-                    const uint32_t pi = tid + uint32_t(kTkThreads) * i;
-                    float s0 = __uint_as_float(v[i].x), s1 = __uint_as_float(v[i].z);
+                    for (int c = 0; c < 4; ++c) e[c] = e[c] * scale * (1.0f + wqk[c]);
 #pragma unroll
-                    for (uint32_t c = 1; c < Sh::KQ; ++c) {
-                        s0 += __uint_as_float(v[c * NL + i].x);
-                        s1 += __uint_as_float(v[c * NL + i].z);
+                    for (int c = 0; c < 2; ++c) {
+                        const float cv = S.cs[th][2u * lane + c], sv = S.sn[th][2u * lane + c];
+                        const float lo = e[c], hi = e[c + 2];
+                        e[c] = lo * cv - hi * sv;
+                        e[c + 2] = lo * sv + hi * cv;
                     }
-                    if (act[i]) *reinterpret_cast<float2*>(&S.xq[2u * pi]) = float2{s0, s1};
                 }
+                float* dst = wave < NH ? S.qh[wave] : (wave == NH ? S.kn : S.vn);
+                if (wave >= NH) {
+#pragma unroll
+                    for (int c = 0; c < 4; ++c) e[c] = f16_round(e[c]);
+                }
+                *reinterpret_cast<float2*>(dst + 2u * lane) = float2{e[0], e[1]};
+                *reinterpret_cast<float2*>(dst + kTkHD / 2u + 2u * lane) = float2{e[2], e[3]};
             }
             __syncthreads();
             t_in = tk_now(a);
-            const uint32_t th = glob ? 1u : 0u;
-            // QK-norm + RoPE, one wave per head: the q heads, then the kv head
-            // (which follows them in q | k | v)
-            if (wave <= NH) {
-                const float* src = S.xq + wave * kTkHD;
-                float e[4];
-#pragma unroll
-                for (int c = 0; c < 4; ++c) e[c] = src[lane + 64 * c];
-                float ss = e[0] * e[0] + e[1] * e[1] + e[2] * e[2] + e[3] * e[3];
-                ss = wave_sum(ss);
-                const float scale = 1.0f / sqrtf(ss / float(kTkHD) + eps);
-#pragma unroll
-                for (int c = 0; c < 4; ++c) e[c] = e[c] * scale * (1.0f + wqk[c]);
-                // rotate-half pairs (d, d + 128): (e0, e2) at d = lane, (e1, e3) at lane + 64
-#pragma unroll
-                for (int c = 0; c < 2; ++c) {
-                    const float cv = S.cs[th][lane + 64 * c], sv = S.sn[th][lane + 64 * c];
-                    const float lo = e[c], hi = e[c + 2];
-                    e[c] = lo * cv - hi * sv;
-                    e[c + 2] = lo * sv + hi * cv;
-                }
-                if (wave < NH) {
-#pragma unroll
-                    for (int c = 0; c < 4; ++c) S.qh[wave][lane + 64 * c] = e[c];
-                } else {
-#pragma unroll
-                    for (int c = 0; c < 4; ++c) S.kn[lane + 64 * c] = f16_round(e[c]);
-                }
-            }
-            if (tid < kTkHD) S.vn[tid] = f16_round(S.xq[QD + kTkHD + tid]);
-            __syncthreads();
             // scores (the current key comes from S.kn, read unconditionally so
             // that the choice is a select, not a branch)
             {
@@ -898,17 +879,17 @@ __global__ __launch_bounds__(kTkThreads) void token_kernel(TokArgs a) {
             }
             __syncthreads();
             // weighted values (keys past the span have weight 0 and value 0)
+            const uint32_t pb = uint32_t(lay.attp) + s_att * NH * (2u + kTkHD);
             {
-                const float2 vc = *reinterpret_cast<const float2*>(&S.vn[2u * dp]);
-                float o0[NH], o1[NH];
+                const float vc = S.vn[dv];
+                float o[NH];
 #pragma unroll
-                for (uint32_t h = 0; h < NH; ++h) o0[h] = o1[h] = 0.0f;
+                for (uint32_t h = 0; h < NH; ++h) o[h] = 0.0f;
 #pragma unroll
-                for (uint32_t i = 0; i < KPG; ++i) {
-                    const uint32_t jl = kgv * KPG + i;
-                    const bool cur = kv0 + j0 + jl == pos;
-                    const float v0 = cur ? vc.x : f16_bits_to_f32(vw[i]);
-                    const float v1 = cur ? vc.y : f16_bits_to_f32(vw[i] >> 16);
+                for (uint32_t i = 0; i < HK; ++i) {
+                    const uint32_t jl = kh * HK + i;
+                    const float vr = kv0 + j0 + jl == pos ? vc : f16_bits_to_f32(vh[i]);
+                    const float vv = j0 + jl < span ? vr : 0.0f;
                     float pr[NH];
                     if constexpr (NH % 4 == 0) {
 #pragma unroll
@@ -921,32 +902,34 @@ __global__ __launch_bounds__(kTkThreads) void token_kernel(TokArgs a) {
                         for (uint32_t h = 0; h < NH; ++h) pr[h] = S.sc[jl][h];
                     }
 #pragma unroll
-                    for (uint32_t h = 0; h < NH; ++h) {
-                        o0[h] = fmaf(pr[h], v0, o0[h]);
-                        o1[h] = fmaf(pr[h], v1, o1[h]);
+                    for (uint32_t h = 0; h < NH; ++h) o[h] = fmaf(pr[h], vv, o[h]);
+                }
+                // the other key half (lane ^ 32), then the neighbouring dim (lane ^ 1)
+#pragma unroll
+                for (uint32_t h = 0; h < NH; ++h) o[h] += __shfl_xor(o[h], 32, kWave);
+                // chunk record: per head (max, sum of exp, unnormalised output[256]);
+                // lane l stores dims (dv & ~1, dv | 1) of head 2 kh + (l & 1) (and
+                // of the heads NH / 2 further on when NH > 4)
+#pragma unroll
+                for (uint32_t h0 = 0; h0 < NH; h0 += 4) {
+                    // lanes l and l ^ 1 store different heads: each takes the
+                    // value of the head it stores from its own registers and
+                    // from the neighbour's (quad_perm xor 1, one per head)
+                    const uint32_t hs = h0 + 2u * kh + (lane & 1u);
+                    float mine = o[h0], nb = 0.0f;
+#pragma unroll
+                    for (uint32_t k = 0; k < 4; ++k) {
+                        const float t = dpp_f<0xB1, 0xF>(o[h0 + k], 0.0f);
+                        if (h0 + k == hs) { mine = o[h0 + k]; nb = t; }
+                    }
+                    {
+                        const bool ev = (lane & 1u) == 0u;
+                        const float r0 = ev ? mine : nb, r1 = ev ? nb : mine;
+                        const uint32_t vo = (pb + hs * (2u + kTkHD) + 2u + (dv & ~1u)) * 8u;
+                        if (xl_st) ll_st2_xcd(rr, vo, soff, r0, r1, tag);
+                        else ll_st2(rr, vo, soff, r0, r1, tag);
                     }
                 }
-#pragma unroll
-                for (uint32_t h = 0; h < NH; ++h)
-                    *reinterpret_cast<float2*>(&S.big[(kgv * NH + h) * kTkHD + 2u * dp]) =
-                        float2{o0[h], o1[h]};
-            }
-            __syncthreads();
-            // chunk record: per head (max, sum of exp, unnormalised output[256])
-            const uint32_t pb = uint32_t(lay.attp) + s_att * NH * (2u + kTkHD);
-#pragma unroll
-            for (uint32_t i = tid; i < NH * (kTkHD / 2u); i += kTkThreads) {
-                const uint32_t h = i / (kTkHD / 2u), d2 = 2u * (i % (kTkHD / 2u));
-                constexpr uint32_t hs = NH * kTkHD;
-                const float* vr = S.big + h * kTkHD + d2;
-                const float2 a0 = *reinterpret_cast<const float2*>(vr);
-                const float2 a1 = *reinterpret_cast<const float2*>(vr + hs);
-                const float2 a2 = *reinterpret_cast<const float2*>(vr + 2 * hs);
-                const float2 a3 = *reinterpret_cast<const float2*>(vr + 3 * hs);
-                const uint32_t vo = (pb + h * (2u + kTkHD) + 2u + d2) * 8u;
-                const float r0 = ((a0.x + a1.x) + a2.x) + a3.x, r1 = ((a0.y + a1.y) + a2.y) + a3.y;
-                if (xl_st) ll_st2_xcd(rr, vo, soff, r0, r1, tag);
-                else ll_st2(rr, vo, soff, r0, r1, tag);
             }
             if (tid < NH) {
                 const uint32_t vo = (pb + tid * (2u + kTkHD)) * 8u;
