@@ -118,7 +118,7 @@ struct TkShape {
     static constexpr uint32_t N_QKV = QKVD / kGrp * KQ * SQ;
     static constexpr uint32_t N_COMB = NH * 4;              // local layers' combine tiles
     static constexpr uint32_t N_O = NOG * KO * SO;
-    static constexpr uint32_t N_GU = 2 * FFN / kGrp;
+    static constexpr uint32_t N_GU = FFN / (kGrp / 2);          // gate|up tiles of 32 ffn indices
     static constexpr uint32_t N_DN = (H / kGrp) * NCH * SD;
     // S-block steps per wave of a tile (blocks / (8 waves x S slots), rounded up)
     static constexpr int RK = int((QB + 8 * SQ - 1) / (8 * SQ));
@@ -1062,10 +1062,23 @@ __global__ __launch_bounds__(kTkThreads) void token_kernel(TokArgs a) {
         TkW<RD> pdn;
         if (t_dn < Sh::N_DN) prefetch_dn(pdn, l, t_dn);
         for (uint32_t t = t_gu; t < Sh::N_GU; t += nwg) {
-            constexpr uint32_t ng = FFN / kGrp;
-            const uint32_t m = t < ng ? 4u : 5u, g = t < ng ? t : t - ng;
+            // Tile t: ffn indices 32 t .. 32 t + 31 (column group g = t / 2,
+            // half t % 2) of the gate (lanes 0..31) and the up projection
+            // (lanes 32..63) over the whole k, so the tile ends with the
+            // GeGLU of its 32 indices (gelu(gate) * up, llm_transformer.cl:213-231).
+            const uint32_t g = t / 2u, cl = (t % 2u) * 32u + lane % 32u;
+            const uint32_t m = lane < 32u ? 4u : 5u;
             TkW<RQ> p;
-            tile_prefetch(p, L.w[m], L.s[m], Sh::HB, FFN, g, 0u, 0u, Sh::HB, wave, lane);
+            {
+                const u32x4* w = static_cast<const u32x4*>(L.w[m]);
+                const u32x2* sc = static_cast<const u32x2*>(L.s[m]);
+#pragma unroll
+                for (int r = 0; r < RQ; ++r) {
+                    const uint32_t b = min(wave + 8u * uint32_t(r), Sh::HB - 1u);
+                    p.w[r] = ldg_stream4(w + (size_t(g) * Sh::HB + b) * kGrp + cl);
+                    p.s[r] = ldg_stream2(sc + size_t(b / 4u) * FFN + g * kGrp + cl);
+                }
+            }
             float w_post[kOwn] = {}, w_in[kOwn] = {}, xa[kOwn] = {}, o[kOwn] = {};
             if (hown) {
                 ld_own(w_post, L.norm[1] + kOwn * tid);
@@ -1116,7 +1129,11 @@ __global__ __launch_bounds__(kTkThreads) void token_kernel(TokArgs a) {
             float y = tile_dot<FMT>(p, S, 0u, Sh::HB, wave, lane);
             if (wave == 0) {
                 y *= norm_scale<H>(rsn, eps);
-                tile_put(rr, soff, uint32_t(lay.gu) + (m == 4u ? 0u : FFN) + g * kGrp, y, lane, tag);
+                const float up = __shfl_xor(y, 32, kWave);
+                const float hv = gelu_tanh(y) * up;   // lanes 0..31: index 32 t + lane
+                const float hn = dpp_f<0xB1, 0xF>(hv, 0.0f);
+                if (lane < 32u && (lane & 1u) == 0u)
+                    ll_st2(rr, (uint32_t(lay.gu) + 32u * t + lane) * 8u, soff, hv, hn, tag);
             }
             // x after the attention block, for the next layer: spread and stored last, as xa
             if (t < Sh::NOG && tid / (kGrp / kOwn) == t) own_put(rr, soff, uint32_t(lay.xb) + kOwn * tid, x, tag);
@@ -1133,19 +1150,16 @@ __global__ __launch_bounds__(kTkThreads) void token_kernel(TokArgs a) {
             if (t != t_dn) prefetch_dn(pdn, l, t);
             if (t == t_dn && l + 1u < a.n_layers && t_qkv < Sh::N_QKV) prefetch_qkv(pq, l + 1u, t_qkv);
             if (tid < nb * (kBlk / kOwn)) {
-                uint32_t off[2 * kOwnP];
-                bool act[2 * kOwnP];
-                u32x4 v[2 * kOwnP];
+                // GeGLU output h of this chunk's k range (the gate/up tiles apply it)
+                uint32_t off[kOwnP];
+                bool act[kOwnP];
+                u32x4 v[kOwnP];
 #pragma unroll
-                for (uint32_t j = 0; j < 2 * kOwnP; ++j) act[j] = true;
+                for (uint32_t j = 0; j < kOwnP; ++j) act[j] = true;
                 own_offsets(&off[0], uint32_t(lay.gu) + k0 + kOwn * tid);
-                own_offsets(&off[kOwnP], uint32_t(lay.gu) + FFN + k0 + kOwn * tid);
                 ll_wait(rr, soff, off, act, v, tag, a.state);
-                float gt[kOwn], up[kOwn], hx[kOwn];
-                own_unpack(gt, &v[0]);
-                own_unpack(up, &v[kOwnP]);
-#pragma unroll
-                for (uint32_t e = 0; e < kOwn; ++e) hx[e] = gelu_tanh(gt[e]) * up[e];
+                float hx[kOwn];
+                own_unpack(hx, &v[0]);
                 own_stage(S, hx, tid);
             }
             __syncthreads();

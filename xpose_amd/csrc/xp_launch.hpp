@@ -242,7 +242,7 @@ struct TokArgs {
     // Exchange slots: 8 bytes = (launch tag << 32) | fp32 bits, written with
     // one device-coherent store and read until the tag matches. Per layer
     // (stride ll_layer): xa[hidden] | xb[hidden] | qkv[split][q_dim + 2 hd] |
-    // attp[grid][n_heads][2 + hd] | atto[q_dim] | o[split][hidden] | gu[2 ffn] |
+    // attp[grid][n_heads][2 + hd] | atto[q_dim] | o[split][hidden] | gu[ffn] (GeGLU output) |
     // dnp[down chunks][hidden]; then am[2 grid] once.
     unsigned long long* ll;
     size_t ll_layer;
@@ -301,7 +301,7 @@ __host__ __device__ inline TokLL tok_ll_layout(uint32_t hidden, uint32_t ffn, ui
     t.atto = t.attp + size_t(grid) * n_heads * (2 + head_dim);
     t.o = t.atto + qd;
     t.gu = t.o + kTokOSplit * size_t(hidden);
-    t.dnp = t.gu + 2 * size_t(ffn);
+    t.dnp = t.gu + size_t(ffn);
     t.layer = t.dnp + size_t(tok_down_chunks(ffn)) * hidden;
     t.layer = (t.layer + 31) & ~size_t(31);
     return t;
