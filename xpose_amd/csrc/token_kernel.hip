@@ -584,23 +584,33 @@ __global__ __launch_bounds__(kTkThreads) void token_kernel(TokArgs a) {
         const uint32_t soff = lp * lstride;
         float xb[kOwn] = {}, t[kOwn] = {};
         if (hown) {
-            constexpr uint32_t NL = kOwnP * (1 + NCH);
+            // xb (written in the gate/up stage, a stage before the down
+            // chunks) first, so that the polls of the chunks carry only them
+            {
+                uint32_t off[kOwnP];
+                bool act[kOwnP];
+                u32x4 v[kOwnP];
+                own_offsets(&off[0], uint32_t(lay.xb) + kOwn * tid);
+#pragma unroll
+                for (uint32_t i = 0; i < kOwnP; ++i) act[i] = true;
+                ll_wait(rr, soff, off, act, v, tag, a.state);
+                own_unpack(xb, &v[0]);
+            }
+            constexpr uint32_t NL = kOwnP * NCH;
             uint32_t off[NL];
             bool act[NL];
             u32x4 v[NL];
-            own_offsets(&off[0], uint32_t(lay.xb) + kOwn * tid);
 #pragma unroll
             for (uint32_t c = 0; c < NCH; ++c)
-                own_offsets(&off[kOwnP * (1 + c)], uint32_t(lay.dnp) + c * H + kOwn * tid);
+                own_offsets(&off[kOwnP * c], uint32_t(lay.dnp) + c * H + kOwn * tid);
 #pragma unroll
             for (uint32_t i = 0; i < NL; ++i) act[i] = true;
             ll_wait(rr, soff, off, act, v, tag, a.state);
-            own_unpack(xb, &v[0]);
-            own_unpack(t, &v[kOwnP]);
+            own_unpack(t, &v[0]);
 #pragma unroll
             for (uint32_t c = 1; c < NCH; ++c) {
                 float u[kOwn];
-                own_unpack(u, &v[kOwnP * (1 + c)]);
+                own_unpack(u, &v[kOwnP * c]);
 #pragma unroll
                 for (uint32_t e = 0; e < kOwn; ++e) t[e] += u[e];
             }
@@ -1098,23 +1108,32 @@ __global__ __launch_bounds__(kTkThreads) void token_kernel(TokArgs a) {
             }
             __syncthreads();
             if (hown) {
-                constexpr uint32_t NL = (1 + Sh::KO) * kOwnP;
+                // xa (written in the QKV stage) first, then the o partials alone
+                {
+                    uint32_t off[kOwnP];
+                    bool act[kOwnP];
+                    u32x4 v[kOwnP];
+#pragma unroll
+                    for (uint32_t j = 0; j < kOwnP; ++j) act[j] = true;
+                    own_offsets(&off[0], uint32_t(lay.xa) + kOwn * tid);
+                    ll_wait(rr, soff, off, act, v, tag, a.state);
+                    own_unpack(xa, &v[0]);
+                }
+                constexpr uint32_t NL = Sh::KO * kOwnP;
                 uint32_t off[NL];
                 bool act[NL];
                 u32x4 v[NL];
 #pragma unroll
                 for (uint32_t j = 0; j < NL; ++j) act[j] = true;
-                own_offsets(&off[0], uint32_t(lay.xa) + kOwn * tid);
 #pragma unroll
                 for (uint32_t c = 0; c < Sh::KO; ++c)
-                    own_offsets(&off[kOwnP * (1 + c)], uint32_t(lay.o) + c * H + kOwn * tid);
+                    own_offsets(&off[kOwnP * c], uint32_t(lay.o) + c * H + kOwn * tid);
                 ll_wait(rr, soff, off, act, v, tag, a.state);
-                own_unpack(xa, &v[0]);
-                own_unpack(o, &v[kOwnP]);
+                own_unpack(o, &v[0]);
 #pragma unroll
                 for (uint32_t c = 1; c < Sh::KO; ++c) {
                     float u[kOwn];
-                    own_unpack(u, &v[kOwnP * (1 + c)]);
+                    own_unpack(u, &v[kOwnP * c]);
 #pragma unroll
                     for (uint32_t e = 0; e < kOwn; ++e) o[e] += u[e];
                 }
