@@ -63,7 +63,18 @@ constexpr int      kTkThreads   = kTokThreads;
 constexpr int      kTkWaves     = kTkThreads / kWave;    // 8
 constexpr uint32_t kTkHD        = 256;                   // head_dim
 constexpr uint32_t kTkMaxQH     = 8;                     // query heads (one kv head)
-constexpr uint32_t kTkC         = 32;                    // keys per attention workgroup
+// Keys per attention workgroup in global layers (and in local layers that
+// do not exchange through one XCD); a build-time knob (32 or 64) for sweeps.
+#ifndef XP_TOK_GLOBAL_KEYS
+#define XP_TOK_GLOBAL_KEYS 64
+#endif
+constexpr uint32_t kTkC         = XP_TOK_GLOBAL_KEYS;
+static_assert(kTkC == 32 || kTkC == 64, "32 or 64 keys per global attention chunk");
+// Dims per combine tile in global layers (32 or 64; local layers use 64).
+#ifndef XP_TOK_GLOBAL_CD
+#define XP_TOK_GLOBAL_CD 32
+#endif
+constexpr uint32_t kTkGlobalCD  = XP_TOK_GLOBAL_CD;
 constexpr uint32_t kTkMaxBlk    = 64;                    // staged 32-blocks (2048 k)
 constexpr int      kTkMaxGrid   = 1024;
 constexpr uint32_t kSpinLimit   = 1u << 24;
@@ -757,7 +768,8 @@ __global__ __launch_bounds__(kTkThreads) void token_kernel(TokArgs a) {
             constexpr uint32_t TPK = kTkThreads / CW;        // threads per key (scores)
             constexpr uint32_t NCK = kTkHD / (4u * TPK);      // float4 of a key per thread
             constexpr uint32_t HK = CW / 2u;                  // keys per lane half (values)
-            static_assert(TPK == 16u || TPK == 32u, "a key's parts span one or two DPP rows");
+            static_assert(TPK == 8u || TPK == 16u || TPK == 32u,
+                          "a key's parts span half a DPP row, one row or two");
             static_assert(kTkHD == 32u * kTkWaves, "values: 32 dims per wave");
             static_assert(NH % 4u == 0u, "values: each lane stores one of four heads");
             const uint32_t j0 = s_att * CW;
@@ -863,10 +875,17 @@ __global__ __launch_bounds__(kTkThreads) void token_kernel(TokArgs a) {
                     }
                     d[h] = acc;
                 }
-                // key jk's lanes: one DPP row (TPK 16), or two (TPK 32: rows 2 r, 2 r + 1)
+                // key jk's lanes: half a DPP row (TPK 8), one (TPK 16), or two
+                // (TPK 32: rows 2 r, 2 r + 1)
 #pragma unroll
                 for (uint32_t h = 0; h < NH; ++h) {
-                    d[h] = row16_sum(d[h]);
+                    if constexpr (TPK == 8u) {
+                        d[h] += dpp_f<0xB1, 0xF>(d[h], 0.0f);    // quad_perm [1,0,3,2]
+                        d[h] += dpp_f<0x4E, 0xF>(d[h], 0.0f);    // quad_perm [2,3,0,1]
+                        d[h] += dpp_f<0x141, 0xF>(d[h], 0.0f);   // row_half_mirror
+                    } else {
+                        d[h] = row16_sum(d[h]);
+                    }
                     if constexpr (TPK == 32u)
                         d[h] += __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(d[h]), 0x401F));
                 }
@@ -1032,7 +1051,7 @@ __global__ __launch_bounds__(kTkThreads) void token_kernel(TokArgs a) {
                 __syncthreads();
             }
         };
-        if (glob) combine(std::integral_constant<uint32_t, 32u>{});
+        if (glob) combine(std::integral_constant<uint32_t, kTkGlobalCD>{});
         else combine(std::integral_constant<uint32_t, 64u>{});
         tk_trace_stage(a, wg, l, 2u, t_in);
         t_in = 0;
