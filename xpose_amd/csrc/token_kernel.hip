@@ -1026,16 +1026,25 @@ __global__ __launch_bounds__(kTkThreads) void token_kernel(TokArgs a) {
                 }
                 __syncthreads();
                 if (c == c0) t_in = tk_now(a);
-                float m = -INFINITY;
-                for (uint32_t s = tid; s < n_att; s += kTkThreads) m = fmaxf(m, S.big[s * CS]);
-                const float M = blk_max(m, RS());
-                float lsum = 0.0f;
-                for (uint32_t s = tid; s < n_att; s += kTkThreads) {
-                    const float f = expf(S.big[s * CS] - M);
-                    S.fm[s] = f;
-                    lsum += f * S.big[s * CS + 1u];
+                // wave 0 forms the rescale factors exp(m_s - max m) and the
+                // softmax denominator (chunk records <= a few hundred: lane
+                // reductions, no block-wide ones)
+                float* rl = RS();
+                if (wave == 0) {
+                    float m = -INFINITY;
+                    for (uint32_t s = lane; s < n_att; s += kWave) m = fmaxf(m, S.big[s * CS]);
+                    const float M = wave_max(m);
+                    float lsum = 0.0f;
+                    for (uint32_t s = lane; s < n_att; s += kWave) {
+                        const float f = expf(S.big[s * CS] - M);
+                        S.fm[s] = f;
+                        lsum += f * S.big[s * CS + 1u];
+                    }
+                    lsum = wave_sum(lsum);
+                    if (lane == 0) rl[0] = lsum;
                 }
-                const float Ltot = blk_sum(lsum, RS());   // also orders the fm writes
+                __syncthreads();
+                const float Ltot = rl[0];
                 const uint32_t d = tid % CD, sg = tid / CD;
                 float o = 0.0f;
                 for (uint32_t s = sg; s < n_att; s += NG) o = fmaf(S.big[s * CS + 2u + d], S.fm[s], o);
