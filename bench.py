@@ -45,7 +45,7 @@ HBM_PEAK_GBS = 8000.0          # MI355X HBM3E
 # Measured HBM bytes of one token-kernel launch at this workload: rocprofv3
 # FETCH_SIZE x 2.0 + WRITE_SIZE x 1.0 (factors from a 256 MiB copy), see
 # profiles/token_kernel_gemma3_1b_ctx4096.md.
-TOKEN_TRAFFIC_BYTES = 699_408_998 + 18_097_254
+TOKEN_TRAFFIC_BYTES = 646_948_204 + 13_318_720
 TRAFFIC_SOURCE = ("rocprofv3 --pmc FETCH_SIZE and --pmc WRITE_SIZE of this bench's token step "
                   "(profiles/token_kernel_gemma3_1b_ctx4096.md), scaled by a 256 MiB copy's "
                   "readings; a constant of this build, not counted in this run")
@@ -152,6 +152,27 @@ def stream_ceiling(X, nbytes: int = 1 << 30, iters: int = 20) -> float:
     ms = C.c_float()
     X.call("xp_stream_read_timed", buf.vp, nbytes, iters, None, C.byref(ms))
     return nbytes * iters / (ms.value / 1e3) / 1e9
+
+
+def exchange_leg(X, stages: int = 64, reps: int = 10):
+    """Cross-workgroup exchange latency (xp_exchange_chain_timed): a chain of
+    stages whose producers publish 64 tagged floats each and whose next-stage
+    roles wait for all of them; ns per stage, best and mean of `reps` launches,
+    for producer counts at the token kernel's fan-ins, spread over the XCDs or
+    on one XCD, stores device-coherent or kept in L2."""
+    rows = []
+    for n, stride, l2 in ((1, 1, 0), (1, 8, 0), (1, 8, 1), (4, 1, 0), (18, 1, 0), (18, 8, 0),
+                          (18, 8, 1), (32, 8, 0), (32, 8, 1), (48, 1, 0), (126, 1, 0),
+                          (216, 1, 0), (256, 1, 0)):
+        v = []
+        for _ in range(reps):
+            ns = C.c_float()
+            X.call("xp_exchange_chain_timed", n, stages, stride, l2, None, C.byref(ns))
+            v.append(ns.value)
+        rows.append({"producers": n, "roles": "one XCD" if stride == 8 else "all XCDs",
+                     "stores": "L2" if l2 else "device", "ns_per_stage_best": round(min(v), 1),
+                     "ns_per_stage_mean": round(sum(v) / len(v), 1)})
+    return rows
 
 
 def same_size_ceiling(X, nbytes: int, copies: int = 64, iters: int = 640):
@@ -363,7 +384,8 @@ def main() -> int:
     ap.add_argument("--no-configs", action="store_true",
                     help="skip the benchmark config 3 / 4 / 5 and attention legs")
     ap.add_argument("--mv-iters", type=int, default=60)
-    ap.add_argument("--only", choices=["all", "matvec", "attention", "cfg5", "native", "graph"],
+    ap.add_argument("--only", choices=["all", "matvec", "attention", "cfg5", "native", "graph",
+                                       "exchange"],
                     default="all",
                     help="one leg alone, for profiling: the standalone matvec and streaming "
                          "legs, the attention leg, the batched decode (config 5), the "
@@ -399,6 +421,9 @@ def main() -> int:
                           "matvec_cfg1": {"us_per_launch": round(per1 * 1e6, 3),
                                           "GBs": round(nb1 / per1 / 1e9, 1)},
                           "stream_ceiling_GBs": round(ceil, 1)}), flush=True)
+        return 0
+    if args.only == "exchange":
+        print(json.dumps({"exchange_chain": exchange_leg(X), "device": info.get("arch", "")}))
         return 0
     if args.only == "native":
         print(json.dumps({"native": native_leg(X)}), flush=True)

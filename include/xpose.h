@@ -155,6 +155,19 @@ int xp_stream_read_timed(const void* buf, size_t bytes, uint32_t iters, xp_strea
 int xp_stream_read_rot_timed(const void* const* bufs, uint32_t nbufs, size_t bytes, uint32_t grid,
                              uint32_t iters, xp_stream stream, float* ms);
 int xp_copy(void* dst, const void* src, size_t bytes, xp_stream stream);
+/* Exchange-latency probe (no reference counterpart: it measures the
+ * cross-workgroup hand-off the persistent token kernel is built on, alone).
+ * A chain of `stages` stages on a grid of one 512-thread workgroup per CU:
+ * each of the `producers` roles of a stage publishes 64 tagged floats (32
+ * 16-byte pairs), and every role of the next stage first waits until it has
+ * read all of them. stride 1 spreads the roles over all XCDs, stride 8 keeps
+ * them on one XCD; l2_local (stride 8 only) keeps the stores in that XCD's
+ * L2 instead of writing them through to the device coherence point.
+ * *ns_per_stage = (last publish - first publish) / (stages - 1), from the
+ * workgroups' 100 MHz s_memrealtime stamps. XP_E_DEVICE if a wait timed out
+ * (the grid was not resident at once). */
+int xp_exchange_chain_timed(uint32_t producers, uint32_t stages, uint32_t stride, int l2_local,
+                            xp_stream stream, float* ns_per_stage);
 
 /* Two-pass Gemma RMSNorm in one launch: out = in * rsqrt(mean(in^2)+eps) *
  * (1 + w). Replaces rmsnorm_sumsq + rmsnorm_apply_gemma

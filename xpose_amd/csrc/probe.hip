@@ -8,6 +8,8 @@
 // highest in a sweep of chunked and grid-stride layouts on MI355X). As in the
 // reference, the only store is guarded by a value the sum cannot take, so
 // every load stays live and nothing is written.
+#include <vector>
+
 #include "xp_device.hpp"
 #include "xp_launch.hpp"
 
@@ -40,6 +42,83 @@ __global__ __launch_bounds__(kProbeThreads) void copy_kernel(u32x4* dst, const u
     const size_t stride = size_t(gridDim.x) * kProbeThreads;
     for (size_t i = size_t(blockIdx.x) * kProbeThreads + threadIdx.x; i < n; i += stride)
         __builtin_nontemporal_store(ld_stream4(src + i), dst + i);
+}
+
+// Exchange-latency chain: the token kernel's cross-workgroup hand-off
+// measured alone. `stages` stages; stage s has `n` producer roles, each of
+// which publishes a 64-float vector as 32 tagged 16-byte pairs; every role of
+// stage s + 1 first waits until it has read all n vectors of stage s with the
+// current tag (all 512 threads re-reading their pairs, as the token kernel's
+// consumers do). Role r of stage s runs on workgroup ((s n + r) mod (grid /
+// stride)) stride: stride 1 spreads the roles over all XCDs, stride 8 keeps
+// them on the workgroups of one XCD (the hardware deals a launch's
+// workgroups to the eight XCDs in turn). Stores are device-coherent (sc1),
+// or with l2 set kept in the XCD's L2 (valid for stride 8 only). The grid
+// must be resident at once (one 512-thread workgroup per CU); every wait is
+// bounded and a timeout sets status. Each workgroup records the 100 MHz
+// s_memrealtime of its first and last publish.
+constexpr int kXcThreads = 512;
+struct XcArgs {
+    u32x4* slots;                 // [stages][n][32] pairs
+    unsigned long long* times;    // [grid][2]
+    uint32_t* status;
+    uint32_t stages, n, tag, stride, l2, spin_limit;
+};
+
+__global__ __launch_bounds__(kXcThreads) void exchange_chain_kernel(XcArgs a) {
+    const uint32_t wg = blockIdx.x, tid = threadIdx.x;
+    const uint32_t tag = a.tag;
+    const rsrc_t rr = make_rsrc(a.slots, a.stages * a.n * 32u * 16u);
+    const uint32_t n_slots = gridDim.x / a.stride;
+    unsigned long long t_first = 0, t_last = 0;
+    constexpr int M = 16;                                  // pairs per thread (n <= 256)
+    for (uint32_t s = 0; s < a.stages; ++s) {
+        for (uint32_t r = 0; r < a.n; ++r) {
+            if (((s * a.n + r) % n_slots) * a.stride != wg) continue;
+            if (s > 0) {
+                const uint32_t np = a.n * 32u, base = (s - 1u) * a.n * 32u;
+                const u32x4 ready = {0u, tag, 0u, tag};
+                uint32_t off[M];
+                bool act[M];
+                u32x4 v[M];
+#pragma unroll
+                for (int i = 0; i < M; ++i) {
+                    const uint32_t p = tid + uint32_t(i) * kXcThreads;
+                    act[i] = p < np;
+                    off[i] = (base + (act[i] ? p : 0u)) * 16u;
+                }
+#pragma unroll
+                for (int i = 0; i < M; ++i) v[i] = act[i] ? ld_dev16(rr, off[i]) : ready;
+                for (uint32_t spins = 0;; ++spins) {
+                    bool ok = true;
+#pragma unroll
+                    for (int i = 0; i < M; ++i) ok &= (v[i].y == tag) & (v[i].w == tag);
+                    if (ok) break;
+                    if (spins > a.spin_limit) {
+                        __hip_atomic_fetch_or((XP_GLOBAL uint32_t*)a.status, 1u, __ATOMIC_RELAXED,
+                                              __HIP_MEMORY_SCOPE_AGENT);
+                        break;
+                    }
+                    asm volatile("" ::: "memory");
+#pragma unroll
+                    for (int i = 0; i < M; ++i) v[i] = act[i] ? ld_dev16(rr, off[i]) : ready;
+                }
+                __syncthreads();
+            }
+            if (tid == 0 && t_first == 0) t_first = __builtin_amdgcn_s_memrealtime();
+            if (tid < 32) {
+                const uint32_t o = ((s * a.n + r) * 32u + tid) * 16u;
+                const u32x4 val = {__float_as_uint(float(s)), tag, __float_as_uint(float(r)), tag};
+                if (a.l2) __builtin_amdgcn_raw_buffer_store_b128(val, rr, int(o), 0, 0);
+                else __builtin_amdgcn_raw_buffer_store_b128(val, rr, int(o), 0, kAuxDev);
+            }
+            if (tid == 0) t_last = __builtin_amdgcn_s_memrealtime();
+        }
+    }
+    if (tid == 0) {
+        a.times[2 * wg] = t_first;
+        a.times[2 * wg + 1] = t_last;
+    }
 }
 
 namespace {
@@ -129,6 +208,59 @@ int xp_stream_read_rot_timed(const void* const* bufs, uint32_t nbufs, size_t byt
     (void)hipEventDestroy(e0);
     (void)hipEventDestroy(e1);
     return rc;
+}
+
+int xp_exchange_chain_timed(uint32_t producers, uint32_t stages, uint32_t stride, int l2_local,
+                            xp_stream stream, float* ns_per_stage) {
+    XP_REQUIRE(ns_per_stage, "null pointer");
+    XP_REQUIRE(stride == 1 || stride == 8, "stride=%u must be 1 or 8", stride);
+    XP_REQUIRE(!l2_local || stride == 8, "l2_local needs stride 8 (one XCD)");
+    XP_REQUIRE(stages >= 2 && stages <= 256, "stages=%u must be in [2, 256]", stages);
+    const uint32_t grid = n_cu();
+    XP_REQUIRE(producers >= 1 && producers <= 256 && producers <= grid / stride,
+               "producers=%u must be in [1, min(256, %u)]", producers, grid / stride);
+    const size_t lds = 96 * 1024;   // over half a CU's LDS: one workgroup per CU
+    const void* fn = reinterpret_cast<const void*>(&exchange_chain_kernel);
+    XP_HIP(hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, int(lds)));
+    int per_cu = 0;
+    XP_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, kXcThreads, lds));
+    XP_REQUIRE(per_cu >= 1, "a CU cannot hold the probe's workgroup");
+    hipStream_t st = as_stream(stream);
+    const size_t slot_bytes = size_t(stages) * producers * 32u * 16u;
+    char* mem = nullptr;
+    const size_t tb = slot_bytes + size_t(grid) * 16u + 256u;
+    XP_HIP(hipMalloc(&mem, tb));
+    XcArgs a{};
+    a.slots = reinterpret_cast<u32x4*>(mem);
+    a.times = reinterpret_cast<unsigned long long*>(mem + slot_bytes);
+    a.status = reinterpret_cast<uint32_t*>(mem + slot_bytes + size_t(grid) * 16u);
+    a.stages = stages;
+    a.n = producers;
+    a.tag = 1u;
+    a.stride = stride;
+    a.l2 = l2_local ? 1u : 0u;
+    a.spin_limit = 1u << 18;
+    std::vector<unsigned long long> h(size_t(grid) * 2u);
+    uint32_t status = 0;
+    void* args[] = {&a};
+    hipError_t e = hipMemsetAsync(mem, 0, tb, st);
+    if (e == hipSuccess) e = hipLaunchKernel(fn, dim3(grid), dim3(kXcThreads), args, lds, st);
+    if (e == hipSuccess) e = hipMemcpyAsync(h.data(), a.times, h.size() * 8u, hipMemcpyDeviceToHost, st);
+    if (e == hipSuccess) e = hipMemcpyAsync(&status, a.status, 4, hipMemcpyDeviceToHost, st);
+    if (e == hipSuccess) e = hipStreamSynchronize(st);
+    (void)hipFree(mem);
+    if (e != hipSuccess) return set_error(XP_E_HIP, "xp_exchange_chain_timed: %s", hipGetErrorString(e));
+    if (status != 0)
+        return set_error(XP_E_DEVICE, "xp_exchange_chain_timed: a wait ran past its spin limit "
+                         "(the grid was not resident at once)");
+    unsigned long long lo = ~0ull, hi = 0;
+    for (uint32_t w = 0; w < grid; ++w) {
+        if (h[2u * w] == 0) continue;
+        lo = h[2u * w] < lo ? h[2u * w] : lo;
+        hi = h[2u * w + 1u] > hi ? h[2u * w + 1u] : hi;
+    }
+    *ns_per_stage = hi > lo ? float(double(hi - lo) * 10.0 / double(stages - 1u)) : 0.0f;
+    return XP_OK;
 }
 
 int xp_copy(void* dst, const void* src, size_t bytes, xp_stream stream) {
