@@ -47,9 +47,12 @@ struct Batch {
     char* arena = nullptr;
     uint16_t* kc[kMaxSessionLayers] = {};
     uint16_t* vc[kMaxSessionLayers] = {};
-    float *x, *q_raw, *k_raw, *v, *q, *k, *att, *o, *gate, *up, *dn, *logits;
+    float *x, *q_raw, *k_raw, *v, *q, *k, *att, *o, *dn, *logits;
     void* a = nullptr;
     float* asum = nullptr;
+    // the down projection's operand, staged by the gate|up GEMM's GeGLU epilogue
+    void* a2 = nullptr;
+    float* asum2 = nullptr;
     float* part = nullptr;
     size_t part_cap = 0;
     uint32_t* tickets = nullptr;
@@ -89,11 +92,17 @@ int Batch::record() {
     };
     // amode 2 / 3: the GEMM stages its operand from fp32 rows xa (and xu)
     // itself, in place of a bprep mode 2 / 3 launch
+    // geglu: the GEMM's epilogue stages gelu(gate) * up into a2 / asum2; op2:
+    // the GEMM reads its operand from a2 / asum2
     auto gemm = [&](const MvMatDesc* m, uint32_t n, uint32_t K, const char* who,
-                    uint32_t amode = 0, const float* xa = nullptr, const float* xu = nullptr) {
+                    uint32_t amode = 0, const float* xa = nullptr, const float* xu = nullptr,
+                    bool geglu = false, bool op2 = false) {
         BmmArgs g{};
-        g.a = a;
-        g.asum = asum;
+        g.a = op2 ? a2 : a;
+        g.asum = op2 ? asum2 : asum;
+        g.geglu = geglu ? 1u : 0u;
+        g.a_out = geglu ? a2 : nullptr;
+        g.asum_out = geglu ? asum2 : nullptr;
         g.amode = amode;
         g.xa = xa;
         g.xu = xu;
@@ -157,15 +166,14 @@ int Batch::record() {
         const MvMatDesc om{o, L.w[XP_T_O], L.s[XP_T_O], H};
         XB(gemm(&om, 1, qd, "batch o_proj", 2, att));
         XB(prep(1, x, o, nullptr, L.norm[1], L.norm[2], H));
-        const MvMatDesc gu[2] = {{gate, L.w[XP_T_GATE], L.s[XP_T_GATE], c.ffn},
-                                 {up, L.w[XP_T_UP], L.s[XP_T_UP], c.ffn}};
-        XB(gemm(gu, 2, H, "batch gate/up"));
-        // GeGLU stays a staging launch: in the down GEMM each of its 432
-        // quarter-block workgroups would re-read both fp32 rows and recompute
-        // the tanh (measured 20 us against 8.8 + 4.5)
-        XB(prep(3, nullptr, gate, up, nullptr, nullptr, c.ffn));
+        // gate and up of the same 32 columns per workgroup; its epilogue
+        // stages gelu(gate) * up as the down projection's operand block
+        // (no fp32 gate / up rows, no staging launch)
+        const MvMatDesc gu[2] = {{nullptr, L.w[XP_T_GATE], L.s[XP_T_GATE], c.ffn},
+                                 {nullptr, L.w[XP_T_UP], L.s[XP_T_UP], c.ffn}};
+        XB(gemm(gu, 2, H, "batch gate/up", 0, nullptr, nullptr, true));
         const MvMatDesc dm{dn, L.w[XP_T_DOWN], L.s[XP_T_DOWN], H};
-        XB(gemm(&dm, 1, c.ffn, "batch down"));
+        XB(gemm(&dm, 1, c.ffn, "batch down", 0, nullptr, nullptr, false, true));
         const float* next = l + 1 < c.n_layers ? w.layer[l + 1].norm[0] : w.final_norm;
         XB(prep(1, x, dn, nullptr, L.norm[3], next, H));
     }
@@ -291,7 +299,7 @@ int make_batch(const xp_session* weights, uint32_t n_seq, uint32_t max_seq, bool
     b.steps.assign(n_seq, 0);
     const uint32_t B = n_seq, H = c.hidden, qd = c.n_heads * c.head_dim,
                    kvd = c.n_kv_heads * c.head_dim, F = c.ffn;
-    const uint32_t kmax = std::max(std::max(H, qd), F);
+    const uint32_t kmax = std::max(H, qd);   // widest k staged into a (the down operand goes to a2)
     size_t part_cap = 0;
     uint32_t tick = 1;
     auto gemm_need = [&](uint32_t cols, uint32_t K) {
@@ -311,7 +319,9 @@ int make_batch(const xp_session* weights, uint32_t n_seq, uint32_t max_seq, bool
         prefill ? 0 : size_t(c.n_layers) * 2 * B * kvseq * 2,   // KV caches
         size_t(B) * H * 4, size_t(B) * qd * 4, size_t(B) * kvd * 4, size_t(B) * kvd * 4,
         size_t(B) * qd * 4, size_t(B) * kvd * 4, size_t(B) * qd * 4, size_t(B) * H * 4,
-        size_t(B) * F * 4, size_t(B) * F * 4, size_t(B) * H * 4, size_t(B) * c.vocab * 4,
+        size_t(F / kBlkB) * 2 * 64 * 16,                         // staged down operand
+        size_t(F / kBlkB) * 16 * 4,                              // its block sums
+        size_t(B) * H * 4, size_t(B) * c.vocab * 4,
         size_t(kmax / kBlkB) * 2 * 64 * 16,                      // staged operand
         size_t(kmax / kBlkB) * 16 * 4,                           // block sums
         std::max<size_t>(part_cap, 1) * 4, size_t(tick) * 4,
@@ -340,8 +350,8 @@ int make_batch(const xp_session* weights, uint32_t n_seq, uint32_t max_seq, bool
     b.k = reinterpret_cast<float*>(nxt());
     b.att = reinterpret_cast<float*>(nxt());
     b.o = reinterpret_cast<float*>(nxt());
-    b.gate = reinterpret_cast<float*>(nxt());
-    b.up = reinterpret_cast<float*>(nxt());
+    b.a2 = nxt();
+    b.asum2 = reinterpret_cast<float*>(nxt());
     b.dn = reinterpret_cast<float*>(nxt());
     b.logits = reinterpret_cast<float*>(nxt());
     b.a = nxt();

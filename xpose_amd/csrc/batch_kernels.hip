@@ -63,6 +63,37 @@ __device__ __forceinline__ uint32_t bf16_bits_rn(float f) {
 }  // namespace
 
 // ---- staging -------------------------------------------------------------------
+// Word c of staged block blk for row b from its eight elements v (k = 32 blk +
+// 8 c + 0..7): the hi / lo bf16 operand of lane b + 16 c in slot order
+// (slot s <- element s / 2 + 4 (s % 2)), and, from the four words of the
+// block held by four adjacent lanes (c = lane % 4, whole quads active), the
+// block's sum of hi + lo for row b.
+__device__ __forceinline__ void stage_word(u32x4* A, float* asum, uint32_t blk, uint32_t c, uint32_t b,
+                                           const float (&v)[8]) {
+    uint32_t hi[8], lo[8];
+    float sum = 0.0f;
+#pragma unroll
+    for (int sl = 0; sl < 8; ++sl) {
+        const float t = v[sl / 2 + 4 * (sl % 2)];
+        const uint32_t h = bf16_bits_rn(t);
+        const float hf = __uint_as_float(h << 16);
+        const uint32_t l = bf16_bits_rn(t - hf);
+        hi[sl] = h;
+        lo[sl] = l;
+        sum += hf + __uint_as_float(l << 16);
+    }
+    const u32x4 H{hi[0] | (hi[1] << 16), hi[2] | (hi[3] << 16), hi[4] | (hi[5] << 16),
+                  hi[6] | (hi[7] << 16)};
+    const u32x4 L{lo[0] | (lo[1] << 16), lo[2] | (lo[3] << 16), lo[4] | (lo[5] << 16),
+                  lo[6] | (lo[7] << 16)};
+    const uint32_t lane = b + 16u * c;
+    A[(size_t(blk) * 2 + 0) * 64 + lane] = H;
+    A[(size_t(blk) * 2 + 1) * 64 + lane] = L;
+    sum += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(sum), 0xB1, 0xF, 0xF, false));
+    sum += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(sum), 0x4E, 0xF, 0xF, false));
+    if (c == 0) asum[size_t(blk) * 16 + b] = sum;
+}
+
 // One workgroup per sequence b; thread i holds elements 8 p .. 8 p + 7 for p =
 // i, i + 1024, ... (every width here is one pass) in registers from the load
 // through the norms to the staged operand. Modes (x, y: [batch][K] fp32, row b):
@@ -138,32 +169,7 @@ __global__ __launch_bounds__(kPrepThreads) void bprep_kernel(BprepArgs a) {
         }
     }
     if (!own) return;
-    const uint32_t blk = p / 4u, c = p % 4u;
-    // slot s <- element e(s) = s / 2 + 4 (s % 2)
-    uint32_t hi[8], lo[8];
-    float sum = 0.0f;
-#pragma unroll
-    for (int sl = 0; sl < 8; ++sl) {
-        const float t = v[sl / 2 + 4 * (sl % 2)];
-        const uint32_t h = bf16_bits_rn(t);
-        const float hf = __uint_as_float(h << 16);
-        const uint32_t l = bf16_bits_rn(t - hf);
-        hi[sl] = h;
-        lo[sl] = l;
-        sum += hf + __uint_as_float(l << 16);
-    }
-    const u32x4 H{hi[0] | (hi[1] << 16), hi[2] | (hi[3] << 16), hi[4] | (hi[5] << 16),
-                  hi[6] | (hi[7] << 16)};
-    const u32x4 L{lo[0] | (lo[1] << 16), lo[2] | (lo[3] << 16), lo[4] | (lo[5] << 16),
-                  lo[6] | (lo[7] << 16)};
-    const uint32_t lane = b + 16u * c;
-    u32x4* A = static_cast<u32x4*>(a.a);
-    A[(size_t(blk) * 2 + 0) * 64 + lane] = H;
-    A[(size_t(blk) * 2 + 1) * 64 + lane] = L;
-    // block sum over its four words: adjacent lanes (p = 4 blk + c, whole quads active)
-    sum += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(sum), 0xB1, 0xF, 0xF, false));
-    sum += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(sum), 0x4E, 0xF, 0xF, false));
-    if (c == 0) a.asum[size_t(blk) * 16 + b] = sum;
+    stage_word(static_cast<u32x4*>(a.a), a.asum, p / 4u, p % 4u, b, v);
 }
 
 // ---- embedding --------------------------------------------------------------------
@@ -227,18 +233,23 @@ __device__ __forceinline__ void stage_regs(u32x4& H, u32x4& L, float4& as, const
                 __shfl(sum, int(4 * wsel + 2), kWave), __shfl(sum, int(4 * wsel + 3), kWave)};
 }
 
-template <int FMT, int T, int AM>
+template <int FMT, int T, int AM, bool GE = false>
 __global__ __launch_bounds__(kBmmThreads) void bmm_int4_kernel(BmmArgs a) {
     constexpr uint32_t NO = 256u * T;            // outputs of a workgroup: 16 rows x 16 T columns
     constexpr uint32_t PER = (NO + kBmmThreads - 1) / kBmmThreads;
     constexpr uint32_t SUBS = 4u / T;            // column blocks per 64-column group
+    static_assert(!GE || (T == 4 && AM == 0), "the GeGLU epilogue takes four tiles of staged A");
     __shared__ float red[kBmmWaves][NO];
     __shared__ uint32_t last;
     const uint32_t tid = threadIdx.x, wave = tid / kWave, lane = tid % kWave;
     const uint32_t cb = blockIdx.x, s = blockIdx.y;
-    const uint32_t gg = cb / SUBS, c16 = (cb % SUBS) * 16u * T;   // group, first column in it
+    // GE: columns 32 (cb % 2) .. + 31 of group cb / 2 of both matrices;
+    // tiles 0, 1 from the gate, 2, 3 from the up projection
+    const uint32_t gg = GE ? cb / 2u : cb / SUBS;
+    const uint32_t c16 = GE ? (cb % 2u) * 32u : (cb % SUBS) * 16u * T;   // first column in the group
     uint32_t m = 0;
-    while (m + 1 < a.n_mats && gg >= a.groups[m + 1]) ++m;
+    if constexpr (!GE)
+        while (m + 1 < a.n_mats && gg >= a.groups[m + 1]) ++m;
     const uint32_t g = gg - a.groups[m];
     const uint32_t cols = a.mats[m].cols;
     const uint32_t* wq = static_cast<const uint32_t*>(a.mats[m].wq);
@@ -282,9 +293,18 @@ __global__ __launch_bounds__(kBmmThreads) void bmm_int4_kernel(BmmArgs a) {
         }
 #pragma unroll
         for (int t = 0; t < T; ++t) {
-            const uint32_t cg = c16 + 16u * t + col16;   // column within the group
-            o.w[t] = __builtin_nontemporal_load(wq + ((size_t(g) * a.nblk + blk) * kGrp + cg) * 4 + wsel);
-            o.sc[t] = sq[size_t(blk / 4) * cols + g * kGrp + cg];
+            if constexpr (GE) {
+                const uint32_t mt = uint32_t(t) / 2u;
+                const uint32_t cg = c16 + 16u * (uint32_t(t) % 2u) + col16;
+                const uint32_t* wt = static_cast<const uint32_t*>(a.mats[mt].wq);
+                const u32x2* st = static_cast<const u32x2*>(a.mats[mt].sc);
+                o.w[t] = __builtin_nontemporal_load(wt + ((size_t(g) * a.nblk + blk) * kGrp + cg) * 4 + wsel);
+                o.sc[t] = st[size_t(blk / 4) * cols + g * kGrp + cg];
+            } else {
+                const uint32_t cg = c16 + 16u * t + col16;   // column within the group
+                o.w[t] = __builtin_nontemporal_load(wq + ((size_t(g) * a.nblk + blk) * kGrp + cg) * 4 + wsel);
+                o.sc[t] = sq[size_t(blk / 4) * cols + g * kGrp + cg];
+            }
         }
     };
     Ops ops[kBmmMaxPerWave];
@@ -326,6 +346,34 @@ __global__ __launch_bounds__(kBmmThreads) void bmm_int4_kernel(BmmArgs a) {
 #pragma unroll
         for (int r = 0; r < 4; ++r) red[wave][lane * 4u * T + t * 4 + r] = acc[t][r];
     __syncthreads();
+    if constexpr (GE) {
+        // h[row][j] = gelu_tanh(gate) * up for the 16 rows x 32 columns, one
+        // per thread (gate tile j / 16 at o, up tile j / 16 + 2 at o + 8),
+        // each summed over the waves in order; then staged as operand block
+        // cb of the following GEMM (rows past a.rows as zeros)
+        float* hb = &red[0][0];   // [16][32] after the barrier below
+        const uint32_t row = tid / 32u, j = tid % 32u;
+        const uint32_t ol = 16u * (row / 4u) + j % 16u, t = j / 16u;
+        const uint32_t og = ol * 4u * T + t * 4u + row % 4u;
+        float gs = 0.0f, us = 0.0f;
+#pragma unroll
+        for (int w = 0; w < int(kBmmWaves); ++w) {
+            gs += red[w][og];
+            us += red[w][og + 8u];
+        }
+        const float h = row < a.rows ? gelu_tanh(gs) * us : 0.0f;
+        __syncthreads();
+        hb[row * 32u + j] = h;
+        __syncthreads();
+        if (tid < 64u) {
+            const uint32_t b = tid / 4u, c = tid % 4u;
+            float v[8];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) v[e] = hb[b * 32u + 8u * c + e];
+            stage_word(static_cast<u32x4*>(const_cast<void*>(a.a_out)), a.asum_out, cb, c, b, v);
+        }
+        return;
+    }
     float v[PER];
     uint32_t row[PER], col[PER];
     bool own[PER];
@@ -453,9 +501,23 @@ int launch_bmm(BmmArgs a, int fmt, int n_cu, hipStream_t st, const char* who) {
                          ((reinterpret_cast<uintptr_t>(a.xa) | reinterpret_cast<uintptr_t>(a.xu)) & 15u) ||
                          a.lda % 4u))
         return set_error(XP_E_ARG, "%s: fp32 operand rows must be 16-byte aligned, lda >= k", who);
-    const dim3 grid(nblocks, a.nsplit);
     if (fmt != XP_SCALE_F16_QUAD && fmt != XP_SCALE_BF16_QUAD)
         return set_error(XP_E_ARG, "%s: the batched GEMM takes fp16 or bf16 quad scales", who);
+    if (a.geglu) {
+        if (a.n_mats != 2 || a.mats[0].cols != a.mats[1].cols || a.nsplit != 1 || a.amode != 0 ||
+            !a.a_out || !a.asum_out || a.a_out == a.a || a.asum_out == a.asum)
+            return set_error(XP_E_ARG, "%s: the GeGLU epilogue takes two equal-width matrices, one "
+                             "k split, a staged operand and separate output buffers", who);
+        const dim3 ggrid(a.mats[0].cols / 32u, 1);
+        if (fmt == XP_SCALE_F16_QUAD)
+            hipLaunchKernelGGL((bmm_int4_kernel<XP_SCALE_F16_QUAD, 4, 0, true>), ggrid, dim3(kBmmThreads), 0, st, a);
+        else
+            hipLaunchKernelGGL((bmm_int4_kernel<XP_SCALE_BF16_QUAD, 4, 0, true>), ggrid, dim3(kBmmThreads), 0, st, a);
+        hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return set_error(XP_E_HIP, "%s: launch -> %s", who, hipGetErrorString(e));
+        return XP_OK;
+    }
+    const dim3 grid(nblocks, a.nsplit);
 #define XP_BMM_AM(F, TT)                                                                            \
     if (a.amode == 2) hipLaunchKernelGGL((bmm_int4_kernel<F, TT, 2>), grid, dim3(kBmmThreads), 0, st, a);      \
     else if (a.amode == 3) hipLaunchKernelGGL((bmm_int4_kernel<F, TT, 3>), grid, dim3(kBmmThreads), 0, st, a); \

@@ -168,6 +168,14 @@ struct BmmArgs {
     const float* xu;
     uint32_t amode;
     uint32_t lda;
+    // GeGLU epilogue (two matrices of equal width, gate then up, k in one
+    // split): workgroup c takes columns 32 c .. 32 c + 31 of both and writes
+    // gelu_tanh(gate) * up of its 16 rows x 32 columns as the staged operand
+    // block c of a following GEMM (a / asum, bprep_kernel's layout) instead of
+    // the two outputs. a_out / asum_out must not alias a / asum.
+    uint32_t geglu;
+    void* a_out;
+    float* asum_out;
     MvMatDesc mats[4];         // out is [rows][cols] row-major
     uint32_t n_mats;
     uint32_t groups[5];        // set by launch_bmm
