@@ -754,11 +754,17 @@ __global__ __launch_bounds__(kTkThreads) void token_kernel(TokArgs a) {
         // tile, ahead of its wait for q | k | v), or on grid - 1 - s when the
         // grid has too few of those; combine tile c on workgroup c.
         const bool xl_ok = a.xcd_local != 0u && !glob && Sh::N_COMB * 8u <= nwg;
-        const uint32_t cw = xl_ok && (span + 15u) / 16u * 8u <= nwg ? 16u : kTkC;
-        const uint32_t n_att = (span + cw - 1u) / cw;
-        const bool xl = xl_ok && n_att * 8u <= nwg;
+        // Local layers on one XCD split by head when that XCD has a
+        // workgroup for every (head, 64-key chunk): each workgroup polls one
+        // head of q, and a combine tile reads a head's few chunk records.
+        constexpr uint32_t kHK = 64u;                    // keys per head-split chunk
+        const bool hsplit = xl_ok && (span + kHK - 1u) / kHK * NH * 8u <= nwg;
+        const uint32_t cw = hsplit ? kHK : (xl_ok && (span + 15u) / 16u * 8u <= nwg ? 16u : kTkC);
+        const uint32_t n_att = (span + cw - 1u) / cw;    // chunk records per head
+        const uint32_t n_wga = hsplit ? n_att * NH : n_att;   // attention workgroups
+        const bool xl = xl_ok && n_wga * 8u <= nwg;
         const uint32_t rx = nwg - 1u - wg;
-        const bool ask = qsep && n_att + Sh::N_QKV <= nwg;
+        const bool ask = qsep && n_wga + Sh::N_QKV <= nwg;
         const uint32_t s_att = xl ? (rx % 8u == 0u ? rx / 8u : ~0u)
                                   : !ask ? rx : (t_qkv < Sh::N_QKV ? ~0u : rx - qkv_above);
         const bool xl_st = xl && on_xcd;
@@ -973,7 +979,167 @@ __global__ __launch_bounds__(kTkThreads) void token_kernel(TokArgs a) {
             }
             __syncthreads();
         };
-        if (s_att < n_att) {
+        // One query head h over keys c kHK .. c kHK + kHK - 1 (head-split
+        // local chunks). The record has the layout of the all-heads chunks'
+        // (chunk c's entry for head h), so the combine is the same.
+        auto attend_head = [&](uint32_t h, uint32_t c) {
+            constexpr uint32_t CW = kHK;
+            constexpr uint32_t TPK = kTkThreads / CW;        // 8 threads per key (scores)
+            constexpr uint32_t DPT = kTkHD / TPK;            // 32 dims per thread
+            constexpr uint32_t NKQ = kWave / 16u;            // key quarters (values)
+            constexpr uint32_t KQ4 = CW / NKQ;               // 16 keys per quarter
+            static_assert(kTkHD == 32u * kTkWaves, "values: 16 dim pairs per wave");
+            const uint32_t j0 = c * CW;
+            const uint32_t jk = tid / TPK, part = tid % TPK;
+            // the chunk's scores, then weights, one float per key (a key
+            // quarter's 16 weights are read as four float4: no bank conflicts)
+            float* ps = &S.sc[0][0];
+            // values: wave w, lane l: dims 2 dp, 2 dp + 1 (dp = 16 w + l % 16)
+            // of keys kq KQ4 .. kq KQ4 + KQ4 - 1, kq = l / 16
+            const uint32_t dp = 16u * wave + lane % 16u, kq = lane / 16u;
+            // rows past the span are clamped and dropped by selects (see attend)
+            // key part p takes dims 4 TPK i + 4 p .. + 3 (i < DPT / 4): the
+            // parts of a key read consecutive float4 of q (no LDS bank conflicts)
+            u32x2 kr[DPT / 4u];
+            uint32_t vw[KQ4];
+            {
+                const uint16_t* kp = L.kc + size_t(kv0 + min(j0 + jk, span - 1u)) * kTkHD + 4u * part;
+#pragma unroll
+                for (uint32_t i = 0; i < DPT / 4u; ++i) kr[i] = *(const XP_GLOBAL u32x2*)(kp + 4u * TPK * i);
+            }
+#pragma unroll
+            for (uint32_t i = 0; i < KQ4; ++i)
+                vw[i] = ldg32(L.vc + size_t(kv0 + min(j0 + kq * KQ4 + i, span - 1u)) * kTkHD + 2u * dp);
+            // wave 0: query head h, wave 1: the key, wave 2: the value (lane l
+            // holds elements 2 l, 2 l + 1, 2 l + 128, 2 l + 129)
+            float wqk[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+            if (wave <= 1u) {
+                const float* w = (wave == 0u ? L.norm[4] : L.norm[5]) + 2u * lane;
+                const u32x2 w0 = *(const XP_GLOBAL u32x2*)(w);
+                const u32x2 w1 = *(const XP_GLOBAL u32x2*)(w + kTkHD / 2u);
+                wqk[0] = __uint_as_float(w0.x); wqk[1] = __uint_as_float(w0.y);
+                wqk[2] = __uint_as_float(w1.x); wqk[3] = __uint_as_float(w1.y);
+            }
+            const uint32_t th = 0u;   // local layers: the local theta
+            if (wave <= 2u) {
+                uint32_t off[2];
+                const bool act[2] = {true, true};
+                u32x4 v[2];
+                const uint32_t vec = wave == 0u ? h : NH + wave - 1u;   // q head h, k, v
+                const uint32_t p0 = uint32_t(lay.qkv) + vec * kTkHD + 2u * lane;
+                off[0] = p0 * 8u;
+                off[1] = (p0 + kTkHD / 2u) * 8u;
+                ll_wait(rr, soff, off, act, v, tag, a.state);
+                float e[4] = {__uint_as_float(v[0].x), __uint_as_float(v[0].z), __uint_as_float(v[1].x),
+                              __uint_as_float(v[1].z)};
+                if (wave <= 1u) {
+                    float ss = e[0] * e[0] + e[1] * e[1] + e[2] * e[2] + e[3] * e[3];
+                    ss = wave_sum(ss);
+                    const float scale = 1.0f / sqrtf(ss / float(kTkHD) + eps);
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) e[q] = e[q] * scale * (1.0f + wqk[q]);
+#pragma unroll
+                    for (int q = 0; q < 2; ++q) {
+                        const float cv = S.cs[th][2u * lane + q], sv = S.sn[th][2u * lane + q];
+                        const float lo = e[q], hi = e[q + 2];
+                        e[q] = lo * cv - hi * sv;
+                        e[q + 2] = lo * sv + hi * cv;
+                    }
+                }
+                float* dst = wave == 0u ? S.qh[0] : (wave == 1u ? S.kn : S.vn);
+                if (wave >= 1u) {
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) e[q] = f16_round(e[q]);
+                }
+                *reinterpret_cast<float2*>(dst + 2u * lane) = float2{e[0], e[1]};
+                *reinterpret_cast<float2*>(dst + kTkHD / 2u + 2u * lane) = float2{e[2], e[3]};
+            }
+            __syncthreads();
+            t_in = tk_now(a);
+            // scores: key jk, dims DPT part .. + DPT - 1, summed over the key's
+            // eight lanes (half a DPP row)
+            {
+                const uint32_t jj = j0 + jk;
+                const bool valid = jj < span, cur = kv0 + jj == pos;
+                float dd[4] = {0.0f, 0.0f, 0.0f, 0.0f};   // four independent chains
+#pragma unroll
+                for (uint32_t i = 0; i < DPT / 4u; ++i) {
+                    const uint32_t d0 = 4u * TPK * i + 4u * part;
+                    const float4 kc = *reinterpret_cast<const float4*>(&S.kn[d0]);
+                    const float4 q = *reinterpret_cast<const float4*>(&S.qh[0][d0]);
+                    const float k0 = cur ? kc.x : f16_bits_to_f32(kr[i].x);
+                    const float k1 = cur ? kc.y : f16_bits_to_f32(kr[i].x >> 16);
+                    const float k2 = cur ? kc.z : f16_bits_to_f32(kr[i].y);
+                    const float k3 = cur ? kc.w : f16_bits_to_f32(kr[i].y >> 16);
+                    dd[i % 4u] = fmaf(q.x, k0, dd[i % 4u]);
+                    dd[i % 4u] = fmaf(q.y, k1, dd[i % 4u]);
+                    dd[i % 4u] = fmaf(q.z, k2, dd[i % 4u]);
+                    dd[i % 4u] = fmaf(q.w, k3, dd[i % 4u]);
+                }
+                float d = (dd[0] + dd[1]) + (dd[2] + dd[3]);
+                d += dpp_f<0xB1, 0xF>(d, 0.0f);    // quad_perm [1,0,3,2]
+                d += dpp_f<0x4E, 0xF>(d, 0.0f);    // quad_perm [2,3,0,1]
+                d += dpp_f<0x141, 0xF>(d, 0.0f);   // row_half_mirror
+                if (part == 0) ps[jk] = valid ? d * a.attn_scale : -INFINITY;
+            }
+            __syncthreads();
+            // the chunk's softmax: one key per lane of wave 0
+            if (wave == 0) {
+                const float v = ps[lane];
+                const bool in = v != -INFINITY;
+                const float m = wave_max(v);
+                const float e = in ? expf(v - m) : 0.0f;
+                const float l2 = wave_sum(e);
+                ps[lane] = e;
+                if (lane == 0) { S.mh[0] = m; S.lh[0] = l2; }
+            }
+            __syncthreads();
+            const uint32_t pb = uint32_t(lay.attp) + (c * NH + h) * (2u + kTkHD);
+            {
+                const float2 vc = *reinterpret_cast<const float2*>(&S.vn[2u * dp]);
+                float pw[KQ4];
+#pragma unroll
+                for (uint32_t i = 0; i < KQ4; i += 4) {
+                    const float4 q = *reinterpret_cast<const float4*>(&ps[kq * KQ4 + i]);
+                    pw[i] = q.x; pw[i + 1] = q.y; pw[i + 2] = q.z; pw[i + 3] = q.w;
+                }
+                float oa[2] = {0.0f, 0.0f}, ob[2] = {0.0f, 0.0f};   // even / odd keys
+#pragma unroll
+                for (uint32_t i = 0; i < KQ4; ++i) {
+                    const uint32_t jl = kq * KQ4 + i;
+                    const bool cur = kv0 + j0 + jl == pos, in = j0 + jl < span;
+                    const float v0 = cur ? vc.x : f16_bits_to_f32(vw[i]);
+                    const float v1 = cur ? vc.y : f16_bits_to_f32(vw[i] >> 16);
+                    oa[i % 2u] = fmaf(pw[i], in ? v0 : 0.0f, oa[i % 2u]);
+                    ob[i % 2u] = fmaf(pw[i], in ? v1 : 0.0f, ob[i % 2u]);
+                }
+                float o0 = oa[0] + oa[1], o1 = ob[0] + ob[1];
+                // the four key quarters: lanes l ^ 16 (swizzle within 32), l ^ 32
+                o0 += __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(o0), 0x401F));
+                o1 += __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(o1), 0x401F));
+                o0 += __shfl_xor(o0, 32, kWave);
+                o1 += __shfl_xor(o1, 32, kWave);
+                if (kq == 0u) {
+                    const uint32_t vo = (pb + 2u + 2u * dp) * 8u;
+                    if (xl_st) ll_st2_xcd(rr, vo, soff, o0, o1, tag);
+                    else ll_st2(rr, vo, soff, o0, o1, tag);
+                }
+            }
+            if (tid == 0) {
+                if (xl_st) ll_st2_xcd(rr, pb * 8u, soff, S.mh[0], S.lh[0], tag);
+                else ll_st2(rr, pb * 8u, soff, S.mh[0], S.lh[0], tag);
+            }
+            // head 0 of the chunk holding the current position appends its
+            // key / value to the caches for later tokens
+            if (h == 0u && c == n_att - 1u && tid < kTkHD) {
+                stg16(L.kc + size_t(pos) * kTkHD + tid, f32_to_f16_bits(S.kn[tid]));
+                stg16(L.vc + size_t(pos) * kTkHD + tid, f32_to_f16_bits(S.vn[tid]));
+            }
+            __syncthreads();
+        };
+        if (hsplit) {
+            if (s_att < n_wga) attend_head(s_att % NH, s_att / NH);
+        } else if (s_att < n_att) {
             if (cw == 16u) attend(std::integral_constant<uint32_t, 16u>{});
             else attend(std::integral_constant<uint32_t, kTkC>{});
         }

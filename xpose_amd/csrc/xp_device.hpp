@@ -72,9 +72,13 @@ __device__ __forceinline__ uint16_t f32_to_f16_bits(float f) {
 // sum_k (n_k - 8) q_k is an exact int32 (|.| <= 2^26). Per block that is 4
 // XORs, 20 dot8 and 4 shift-adds for 2048 multiply-adds per wave, against
 // two conversions and one FMA per weight in fp32.
-constexpr int      kQxPlanes = 5;
-constexpr float    kQxRange  = 262144.0f;    // 2^18
-constexpr uint32_t kQxBias   = 0x88888u;     // 8 * (1 + 16 + 16^2 + 16^3 + 16^4)
+#ifndef XP_QX_PLANES
+#define XP_QX_PLANES 5
+#endif
+constexpr int      kQxPlanes = XP_QX_PLANES;
+static_assert(kQxPlanes == 4 || kQxPlanes == 5, "16- or 20-bit block fixed point");
+constexpr float    kQxRange  = kQxPlanes == 5 ? 262144.0f : 16384.0f;   // 2^(4 planes - 2)
+constexpr uint32_t kQxBias   = kQxPlanes == 5 ? 0x88888u : 0x8888u;     // 8 * sum of 16^p
 
 struct QxBlock {
     u32x4 p[kQxPlanes];
