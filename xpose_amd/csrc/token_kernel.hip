@@ -366,13 +366,22 @@ __device__ __forceinline__ void stage_x4(QxBlock* qx, float* sx, uint32_t i, con
 #pragma unroll
     for (int e = 0; e < 4; ++e) t[e] = uint32_t(__float2int_rn(v[e] * r) + int32_t(kQxBias)) ^ kQxBias;
     const uint32_t lb = i >> 3, hw = i & 7u;   // half-word 2 c + h of each plane
-#pragma unroll
-    for (int p = 0; p < kQxPlanes; ++p) {
-        uint32_t half = 0;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) half |= ((t[e] >> (4 * p)) & 15u) << (4 * e);
-        reinterpret_cast<uint16_t*>(&qx[lb].p[p])[hw] = uint16_t(half);
-    }
+    // Plane p's half-word is digit p of t[0..3] at nibbles 0..3. Byte k of
+    // a (b) pairs digit 2 k (2 k + 1) of t[0] and t[1]; c, d the same for
+    // t[2], t[3]; a byte permute then joins a pair's byte with the matching
+    // t[2] / t[3] byte, two planes per dword.
+    const uint32_t a = (t[0] & 0x0F0F0Fu) | ((t[1] & 0x0F0F0Fu) << 4);
+    const uint32_t b = ((t[0] >> 4) & 0x0F0F0Fu) | (t[1] & 0xF0F0F0u);
+    const uint32_t c = (t[2] & 0x0F0F0Fu) | ((t[3] & 0x0F0F0Fu) << 4);
+    const uint32_t d = ((t[2] >> 4) & 0x0F0F0Fu) | (t[3] & 0xF0F0F0u);
+    const uint32_t p02 = __builtin_amdgcn_perm(c, a, 0x05010400u);   // planes 0 | 2
+    const uint32_t p13 = __builtin_amdgcn_perm(d, b, 0x05010400u);   // planes 1 | 3
+    reinterpret_cast<uint16_t*>(&qx[lb].p[0])[hw] = uint16_t(p02);
+    reinterpret_cast<uint16_t*>(&qx[lb].p[1])[hw] = uint16_t(p13);
+    reinterpret_cast<uint16_t*>(&qx[lb].p[2])[hw] = uint16_t(p02 >> 16);
+    reinterpret_cast<uint16_t*>(&qx[lb].p[3])[hw] = uint16_t(p13 >> 16);
+    if constexpr (kQxPlanes == 5)
+        reinterpret_cast<uint16_t*>(&qx[lb].p[4])[hw] = uint16_t(__builtin_amdgcn_perm(c, a, 0x07030602u));
     if (hw == 0) sx[lb] = m * (1.0f / kQxRange);
 }
 // Stages an owner vector as fixed-point planes in S.qx / S.sx: task i (i <
