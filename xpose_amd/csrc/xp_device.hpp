@@ -84,19 +84,27 @@ struct QxBlock {
     u32x4 p[kQxPlanes];
 };
 
-// sum_k (nibble_k - 8) * q_k over one block, exact.
+// sum_k (nibble_k - 8) * q_k over one block, exact. Horner's rule over the
+// digit planes in two chains (even and odd planes, 8-bit steps): each plane's
+// four dot8 accumulate onto the chain so far shifted left by 8, so no
+// per-plane zeroing, shift and add. |sum over one plane| <= 32 * 8 * 8 =
+// 2048, so every partial fits in int32.
+__device__ __forceinline__ int32_t plane_dot(u32x4 w, u32x4 q, int32_t acc) {
+    acc = __builtin_amdgcn_sdot8(int32_t(w.x), int32_t(q.x), acc, false);
+    acc = __builtin_amdgcn_sdot8(int32_t(w.y), int32_t(q.y), acc, false);
+    acc = __builtin_amdgcn_sdot8(int32_t(w.z), int32_t(q.z), acc, false);
+    return __builtin_amdgcn_sdot8(int32_t(w.w), int32_t(q.w), acc, false);
+}
 __device__ __forceinline__ int32_t block_dot(u32x4 w, const QxBlock& q) {
     w ^= 0x88888888u;
-    uint32_t d = 0;
+    constexpr int PE = (kQxPlanes - 1) & ~1, PO = (kQxPlanes - 2) | 1;   // top even / odd plane
+    int32_t e = plane_dot(w, q.p[PE], 0);
 #pragma unroll
-    for (int p = 0; p < kQxPlanes; ++p) {
-        int32_t s = __builtin_amdgcn_sdot8(int32_t(w.x), int32_t(q.p[p].x), 0, false);
-        s = __builtin_amdgcn_sdot8(int32_t(w.y), int32_t(q.p[p].y), s, false);
-        s = __builtin_amdgcn_sdot8(int32_t(w.z), int32_t(q.p[p].z), s, false);
-        s = __builtin_amdgcn_sdot8(int32_t(w.w), int32_t(q.p[p].w), s, false);
-        d += uint32_t(s) << (4 * p);   // two's-complement wrap; the total fits
-    }
-    return int32_t(d);
+    for (int p = PE - 2; p >= 0; p -= 2) e = plane_dot(w, q.p[p], e * 256);
+    int32_t o = plane_dot(w, q.p[PO], 0);
+#pragma unroll
+    for (int p = PO - 2; p >= 1; p -= 2) o = plane_dot(w, q.p[p], o * 256);
+    return e + o * 16;
 }
 
 // Quantises eight consecutive activations (task i = (block i/4, word i%4))
