@@ -159,7 +159,7 @@ struct TkSmem {
     float    cs[2][kTkHD / 2];               // RoPE cos / sin at this position,
     float    sn[2][kTkHD / 2];               // [0] local theta, [1] global theta
     alignas(16) float qh[kTkMaxQH][kTkHD];   // normed, rotated q
-    float    kn[kTkHD];                      // current key / value (fp16-rounded)
+    float    kn[kTkHD];                      // current key (fp16-rounded)
     float    vn[kTkHD];
     alignas(16) float sc[kTkC][kTkMaxQH];    // scores, then exp ([key][head])
     float    mh[kTkMaxQH];
@@ -170,6 +170,7 @@ struct TkSmem {
     float    fm[2 * kTkMaxGrid];             // combine: per-chunk factors; argmax slots
     float    amv[kTkWaves];
     uint32_t ami[kTkWaves];
+    alignas(16) uint16_t kn16[kTkHD];       // current key as fp16 bits (head-split chunks)
 };
 
 // ---- exchange slots -------------------------------------------------------------
@@ -491,6 +492,28 @@ __device__ __forceinline__ void tile_put(rsrc_t r, uint32_t soff, uint32_t s0, f
 }
 
 __device__ __forceinline__ float f16_round(float v) { return f16_bits_to_f32(f32_to_f16_bits(v)); }
+
+// An attention wave's vector after QK-norm / RoPE (lane l holds elements
+// 2 l, 2 l + 1, 2 l + 128, 2 l + 129): slot v < NH is query head v (fp32 in
+// qh[v], or qh[0] when the chunk takes one head), slot NH the key (fp16 bits,
+// as the cache will hold it), slot NH + 1 the value (fp16-rounded fp32).
+template <class Smem>
+__device__ __forceinline__ void own_kv_put(Smem& S, uint32_t v, uint32_t nh, uint32_t lane, float (&e)[4]) {
+    constexpr uint32_t HD = 256;
+    if (v == nh) {
+        const uint32_t lo = uint32_t(f32_to_f16_bits(e[0])) | (uint32_t(f32_to_f16_bits(e[1])) << 16);
+        const uint32_t hi = uint32_t(f32_to_f16_bits(e[2])) | (uint32_t(f32_to_f16_bits(e[3])) << 16);
+        *reinterpret_cast<uint32_t*>(&S.kn16[2u * lane]) = lo;
+        *reinterpret_cast<uint32_t*>(&S.kn16[HD / 2u + 2u * lane]) = hi;
+    }
+    float* dst = v < nh ? S.qh[v] : (v == nh ? S.kn : S.vn);
+    if (v >= nh) {
+#pragma unroll
+        for (int c = 0; c < 4; ++c) e[c] = f16_round(e[c]);
+    }
+    *reinterpret_cast<float2*>(dst + 2u * lane) = float2{e[0], e[1]};
+    *reinterpret_cast<float2*>(dst + HD / 2u + 2u * lane) = float2{e[2], e[3]};
+}
 
 // v, as a value the compiler cannot see through.
 __device__ __forceinline__ uint32_t opaque(uint32_t v) {
@@ -851,13 +874,7 @@ __global__ __launch_bounds__(kTkThreads) void token_kernel(TokArgs a) {
                         e[c + 2] = lo * sv + hi * cv;
                     }
                 }
-                float* dst = wave < NH ? S.qh[wave] : (wave == NH ? S.kn : S.vn);
-                if (wave >= NH) {
-#pragma unroll
-                    for (int c = 0; c < 4; ++c) e[c] = f16_round(e[c]);
-                }
-                *reinterpret_cast<float2*>(dst + 2u * lane) = float2{e[0], e[1]};
-                *reinterpret_cast<float2*>(dst + kTkHD / 2u + 2u * lane) = float2{e[2], e[3]};
+                own_kv_put(S, wave, NH, lane, e);
             }
             __syncthreads();
             t_in = tk_now(a);
@@ -983,7 +1000,7 @@ __global__ __launch_bounds__(kTkThreads) void token_kernel(TokArgs a) {
             // the chunk holding the current position appends its key / value
             // to the caches for later tokens (after the results: stores)
             if (s_att == n_att - 1u && tid < kTkHD) {
-                stg16(L.kc + size_t(pos) * kTkHD + tid, f32_to_f16_bits(S.kn[tid]));
+                stg16(L.kc + size_t(pos) * kTkHD + tid, S.kn16[tid]);
                 stg16(L.vc + size_t(pos) * kTkHD + tid, f32_to_f16_bits(S.vn[tid]));
             }
             __syncthreads();
@@ -1055,13 +1072,7 @@ __global__ __launch_bounds__(kTkThreads) void token_kernel(TokArgs a) {
                         e[q + 2] = lo * sv + hi * cv;
                     }
                 }
-                float* dst = wave == 0u ? S.qh[0] : (wave == 1u ? S.kn : S.vn);
-                if (wave >= 1u) {
-#pragma unroll
-                    for (int q = 0; q < 4; ++q) e[q] = f16_round(e[q]);
-                }
-                *reinterpret_cast<float2*>(dst + 2u * lane) = float2{e[0], e[1]};
-                *reinterpret_cast<float2*>(dst + kTkHD / 2u + 2u * lane) = float2{e[2], e[3]};
+                own_kv_put(S, wave == 0u ? 0u : NH - 1u + wave, NH, lane, e);
             }
             __syncthreads();
             t_in = tk_now(a);
@@ -1074,12 +1085,13 @@ __global__ __launch_bounds__(kTkThreads) void token_kernel(TokArgs a) {
 #pragma unroll
                 for (uint32_t i = 0; i < DPT / 4u; ++i) {
                     const uint32_t d0 = 4u * TPK * i + 4u * part;
-                    const float4 kc = *reinterpret_cast<const float4*>(&S.kn[d0]);
                     const float4 q = *reinterpret_cast<const float4*>(&S.qh[0][d0]);
-                    const float k0 = cur ? kc.x : f16_bits_to_f32(kr[i].x);
-                    const float k1 = cur ? kc.y : f16_bits_to_f32(kr[i].x >> 16);
-                    const float k2 = cur ? kc.z : f16_bits_to_f32(kr[i].y);
-                    const float k3 = cur ? kc.w : f16_bits_to_f32(kr[i].y >> 16);
+                    u32x2 kb = kr[i];
+                    if (cur) kb = *reinterpret_cast<const u32x2*>(&S.kn16[d0]);
+                    const float k0 = f16_bits_to_f32(kb.x);
+                    const float k1 = f16_bits_to_f32(kb.x >> 16);
+                    const float k2 = f16_bits_to_f32(kb.y);
+                    const float k3 = f16_bits_to_f32(kb.y >> 16);
                     dd[i % 4u] = fmaf(q.x, k0, dd[i % 4u]);
                     dd[i % 4u] = fmaf(q.y, k1, dd[i % 4u]);
                     dd[i % 4u] = fmaf(q.z, k2, dd[i % 4u]);
@@ -1141,7 +1153,7 @@ __global__ __launch_bounds__(kTkThreads) void token_kernel(TokArgs a) {
             // head 0 of the chunk holding the current position appends its
             // key / value to the caches for later tokens
             if (h == 0u && c == n_att - 1u && tid < kTkHD) {
-                stg16(L.kc + size_t(pos) * kTkHD + tid, f32_to_f16_bits(S.kn[tid]));
+                stg16(L.kc + size_t(pos) * kTkHD + tid, S.kn16[tid]);
                 stg16(L.vc + size_t(pos) * kTkHD + tid, f32_to_f16_bits(S.vn[tid]));
             }
             __syncthreads();
