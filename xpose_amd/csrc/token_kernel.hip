@@ -772,6 +772,23 @@ __global__ __launch_bounds__(kTkThreads) void token_kernel(TokArgs a) {
         tk_trace_stage(a, wg, l, 0u, t_in);
         t_in = 0;
 
+        // The O tile's weights are requested here, before the attention and
+        // combine stages: a workgroup with an attention chunk or a combine tile
+        // as well as an O tile would otherwise request them only after those.
+        TkW<RO> po;
+        auto o_tile = [&](uint32_t t, uint32_t& g, uint32_t& c, uint32_t& h) {
+            // t = (column group g KO + k part c) SO + slice h
+            h = t % Sh::SO;
+            const uint32_t tc = t / Sh::SO;
+            g = tc / Sh::KO;
+            c = tc % Sh::KO;
+        };
+        if (t_o < Sh::N_O) {
+            uint32_t g, c, h;
+            o_tile(t_o, g, c, h);
+            tile_prefetch<RO, Sh::SO>(po, L.w[3], L.s[3], QD / kBlk, H, g, h, c * Sh::OB, Sh::OB, wave, lane);
+        }
+
         // ================= attention =================
         const bool glob = L.global != 0u;
         const uint32_t kv0 = (glob || a.window == 0u || seq <= a.window) ? 0u : seq - a.window;
@@ -1254,13 +1271,12 @@ __global__ __launch_bounds__(kTkThreads) void token_kernel(TokArgs a) {
 
         // ================= O projection =================
         for (uint32_t t = t_o; t < Sh::N_O; t += nwg) {
-            // t = (column group g KO + k part c) SO + slice h: attention
-            // output [c QD / KO, (c + 1) QD / KO)
-            const uint32_t h = t % Sh::SO, tc = t / Sh::SO;
-            const uint32_t g = tc / Sh::KO, c = tc % Sh::KO;
+            // attention output [c QD / KO, (c + 1) QD / KO)
+            uint32_t g, c, h;
+            o_tile(t, g, c, h);
             constexpr uint32_t nb = Sh::OB;
-            TkW<RO> p;
-            tile_prefetch<RO, Sh::SO>(p, L.w[3], L.s[3], QD / kBlk, H, g, h, c * nb, nb, wave, lane);
+            if (t != t_o) tile_prefetch<RO, Sh::SO>(po, L.w[3], L.s[3], QD / kBlk, H, g, h, c * nb, nb, wave, lane);
+            TkW<RO>& p = po;
             if (tid < Sh::QO / Sh::KO) {
                 uint32_t off[kOwnP];
                 bool act[kOwnP];
