@@ -70,6 +70,12 @@ constexpr uint32_t kTkMaxQH     = 8;                     // query heads (one kv 
 #endif
 constexpr uint32_t kTkC         = XP_TOK_GLOBAL_KEYS;
 static_assert(kTkC == 32 || kTkC == 64, "32 or 64 keys per global attention chunk");
+// Global layers' chunks split by head pair when the grid has room (1), or
+// all heads per chunk (0).
+#ifndef XP_TOK_GLOBAL_PAIRS
+#define XP_TOK_GLOBAL_PAIRS 1
+#endif
+constexpr bool kTkGlobalPairs = XP_TOK_GLOBAL_PAIRS != 0;
 // Dims per combine tile in global layers (32 or 64; local layers use 64).
 #ifndef XP_TOK_GLOBAL_CD
 #define XP_TOK_GLOBAL_CD 32
@@ -810,7 +816,11 @@ __global__ __launch_bounds__(kTkThreads) void token_kernel(TokArgs a) {
         const bool hsplit = xl_ok && (span + kHK - 1u) / kHK * NH * 8u <= nwg;
         const uint32_t cw = hsplit ? kHK : (xl_ok && (span + 15u) / 16u * 8u <= nwg ? 16u : kTkC);
         const uint32_t n_att = (span + cw - 1u) / cw;    // chunk records per head
-        const uint32_t n_wga = hsplit ? n_att * NH : n_att;   // attention workgroups
+        // Global layers split by head pair when the grid holds a workgroup
+        // for every (pair, chunk) beside the QKV tiles: each workgroup scores
+        // and sums its keys for two heads instead of all NH.
+        const bool gsplit = kTkGlobalPairs && glob && NH % 2u == 0u && n_att * (NH / 2u) + Sh::N_QKV <= nwg;
+        const uint32_t n_wga = hsplit ? n_att * NH : gsplit ? n_att * (NH / 2u) : n_att;   // attention workgroups
         const bool xl = xl_ok && n_wga * 8u <= nwg;
         const uint32_t rx = nwg - 1u - wg;
         const bool ask = qsep && n_wga + Sh::N_QKV <= nwg;
@@ -1022,20 +1032,28 @@ __global__ __launch_bounds__(kTkThreads) void token_kernel(TokArgs a) {
             }
             __syncthreads();
         };
-        // One query head h over keys c kHK .. c kHK + kHK - 1 (head-split
-        // local chunks). The record has the layout of the all-heads chunks'
-        // (chunk c's entry for head h), so the combine is the same.
-        auto attend_head = [&](uint32_t h, uint32_t c) {
-            constexpr uint32_t CW = kHK;
-            constexpr uint32_t TPK = kTkThreads / CW;        // 8 threads per key (scores)
-            constexpr uint32_t DPT = kTkHD / TPK;            // 32 dims per thread
+        // HPW query heads h0 .. h0 + HPW - 1 over keys c CW .. c CW + CW - 1
+        // (head-split chunks: one head in local layers, a head pair in global
+        // ones). Each head's record has the layout of the all-heads chunks'
+        // (chunk c's entry for head h), so the combine is the same. The key
+        // and value loads are shared by the HPW heads (one KV head).
+        auto attend_heads = [&](auto hpw_c, auto cw_c, uint32_t h0, uint32_t c) {
+            constexpr uint32_t HPW = decltype(hpw_c)::value;
+            constexpr uint32_t CW = decltype(cw_c)::value;
+            constexpr uint32_t TPK = kTkThreads / CW;        // threads per key (scores)
+            constexpr uint32_t DPT = kTkHD / TPK;            // dims per thread
             constexpr uint32_t NKQ = kWave / 16u;            // key quarters (values)
-            constexpr uint32_t KQ4 = CW / NKQ;               // 16 keys per quarter
+            constexpr uint32_t KQ4 = CW / NKQ;               // keys per quarter
+            constexpr uint32_t NCH = 4u / HPW;               // FMA chains per head
+            static_assert(HPW == 1u || HPW == 2u, "one head or a head pair");
+            static_assert(TPK == 8u || TPK == 16u, "a key's parts span half a DPP row or one");
+            static_assert(HPW * CW <= sizeof(S.sc) / sizeof(float), "scores of the chunk's heads");
+            static_assert(KQ4 % 4u == 0u, "a key quarter's weights are read as float4");
             static_assert(kTkHD == 32u * kTkWaves, "values: 16 dim pairs per wave");
             const uint32_t j0 = c * CW;
             const uint32_t jk = tid / TPK, part = tid % TPK;
-            // the chunk's scores, then weights, one float per key (a key
-            // quarter's 16 weights are read as four float4: no bank conflicts)
+            // the chunk's scores, then weights: [head][key] (a key quarter's
+            // weights are read as float4: no bank conflicts)
             float* ps = &S.sc[0][0];
             // values: wave w, lane l: dims 2 dp, 2 dp + 1 (dp = 16 w + l % 16)
             // of keys kq KQ4 .. kq KQ4 + KQ4 - 1, kq = l / 16
@@ -1053,29 +1071,30 @@ __global__ __launch_bounds__(kTkThreads) void token_kernel(TokArgs a) {
 #pragma unroll
             for (uint32_t i = 0; i < KQ4; ++i)
                 vw[i] = ldg32(L.vc + size_t(kv0 + min(j0 + kq * KQ4 + i, span - 1u)) * kTkHD + 2u * dp);
-            // wave 0: query head h, wave 1: the key, wave 2: the value (lane l
-            // holds elements 2 l, 2 l + 1, 2 l + 128, 2 l + 129)
+            // waves 0 .. HPW - 1: the query heads, wave HPW: the key, wave
+            // HPW + 1: the value (lane l holds elements 2 l, 2 l + 1, 2 l + 128,
+            // 2 l + 129)
             float wqk[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-            if (wave <= 1u) {
-                const float* w = (wave == 0u ? L.norm[4] : L.norm[5]) + 2u * lane;
+            if (wave <= HPW) {
+                const float* w = (wave < HPW ? L.norm[4] : L.norm[5]) + 2u * lane;
                 const u32x2 w0 = *(const XP_GLOBAL u32x2*)(w);
                 const u32x2 w1 = *(const XP_GLOBAL u32x2*)(w + kTkHD / 2u);
                 wqk[0] = __uint_as_float(w0.x); wqk[1] = __uint_as_float(w0.y);
                 wqk[2] = __uint_as_float(w1.x); wqk[3] = __uint_as_float(w1.y);
             }
-            const uint32_t th = 0u;   // local layers: the local theta
-            if (wave <= 2u) {
+            const uint32_t th = glob ? 1u : 0u;
+            if (wave <= HPW + 1u) {
                 uint32_t off[2];
                 const bool act[2] = {true, true};
                 u32x4 v[2];
-                const uint32_t vec = wave == 0u ? h : NH + wave - 1u;   // q head h, k, v
+                const uint32_t vec = wave < HPW ? h0 + wave : NH + wave - HPW;   // q heads, k, v
                 const uint32_t p0 = uint32_t(lay.qkv) + vec * kTkHD + 2u * lane;
                 off[0] = p0 * 8u;
                 off[1] = (p0 + kTkHD / 2u) * 8u;
                 ll_wait(rr, soff, off, act, v, tag, a.state);
                 float e[4] = {__uint_as_float(v[0].x), __uint_as_float(v[0].z), __uint_as_float(v[1].x),
                               __uint_as_float(v[1].z)};
-                if (wave <= 1u) {
+                if (wave <= HPW) {
                     float ss = e[0] * e[0] + e[1] * e[1] + e[2] * e[2] + e[3] * e[3];
                     ss = wave_sum(ss);
                     const float scale = 1.0f / sqrtf(ss / float(kTkHD) + eps);
@@ -1089,94 +1108,127 @@ __global__ __launch_bounds__(kTkThreads) void token_kernel(TokArgs a) {
                         e[q + 2] = lo * sv + hi * cv;
                     }
                 }
-                own_kv_put(S, wave == 0u ? 0u : NH - 1u + wave, NH, lane, e);
+                own_kv_put(S, wave < HPW ? wave : NH + wave - HPW, NH, lane, e);
             }
             __syncthreads();
             t_in = tk_now(a);
             // scores: key jk, dims DPT part .. + DPT - 1, summed over the key's
-            // eight lanes (half a DPP row)
+            // TPK lanes (half a DPP row or one)
             {
                 const uint32_t jj = j0 + jk;
                 const bool valid = jj < span, cur = kv0 + jj == pos;
-                float dd[4] = {0.0f, 0.0f, 0.0f, 0.0f};   // four independent chains
+                float dd[HPW][NCH];   // independent chains
+#pragma unroll
+                for (uint32_t hh = 0; hh < HPW; ++hh)
+#pragma unroll
+                    for (uint32_t r = 0; r < NCH; ++r) dd[hh][r] = 0.0f;
 #pragma unroll
                 for (uint32_t i = 0; i < DPT / 4u; ++i) {
                     const uint32_t d0 = 4u * TPK * i + 4u * part;
-                    const float4 q = *reinterpret_cast<const float4*>(&S.qh[0][d0]);
                     u32x2 kb = kr[i];
                     if (cur) kb = *reinterpret_cast<const u32x2*>(&S.kn16[d0]);
                     const float k0 = f16_bits_to_f32(kb.x);
                     const float k1 = f16_bits_to_f32(kb.x >> 16);
                     const float k2 = f16_bits_to_f32(kb.y);
                     const float k3 = f16_bits_to_f32(kb.y >> 16);
-                    dd[i % 4u] = fmaf(q.x, k0, dd[i % 4u]);
-                    dd[i % 4u] = fmaf(q.y, k1, dd[i % 4u]);
-                    dd[i % 4u] = fmaf(q.z, k2, dd[i % 4u]);
-                    dd[i % 4u] = fmaf(q.w, k3, dd[i % 4u]);
+#pragma unroll
+                    for (uint32_t hh = 0; hh < HPW; ++hh) {
+                        const float4 q = *reinterpret_cast<const float4*>(&S.qh[hh][d0]);
+                        float& acc = dd[hh][i % NCH];
+                        acc = fmaf(q.x, k0, acc);
+                        acc = fmaf(q.y, k1, acc);
+                        acc = fmaf(q.z, k2, acc);
+                        acc = fmaf(q.w, k3, acc);
+                    }
                 }
-                float d = (dd[0] + dd[1]) + (dd[2] + dd[3]);
-                d += dpp_f<0xB1, 0xF>(d, 0.0f);    // quad_perm [1,0,3,2]
-                d += dpp_f<0x4E, 0xF>(d, 0.0f);    // quad_perm [2,3,0,1]
-                d += dpp_f<0x141, 0xF>(d, 0.0f);   // row_half_mirror
-                if (part == 0) ps[jk] = valid ? d * a.attn_scale : -INFINITY;
+#pragma unroll
+                for (uint32_t hh = 0; hh < HPW; ++hh) {
+                    float d = dd[hh][0];
+#pragma unroll
+                    for (uint32_t r = 1; r < NCH; ++r) d += dd[hh][r];
+                    if constexpr (TPK == 8u) {
+                        d += dpp_f<0xB1, 0xF>(d, 0.0f);    // quad_perm [1,0,3,2]
+                        d += dpp_f<0x4E, 0xF>(d, 0.0f);    // quad_perm [2,3,0,1]
+                        d += dpp_f<0x141, 0xF>(d, 0.0f);   // row_half_mirror
+                    } else {
+                        d = row16_sum(d);
+                    }
+                    if (part == 0) ps[hh * CW + jk] = valid ? d * a.attn_scale : -INFINITY;
+                }
             }
             __syncthreads();
-            // the chunk's softmax: one key per lane of wave 0
-            if (wave == 0) {
-                const float v = ps[lane];
+            // the chunk's softmax: wave hh takes head hh, one key per lane
+            if (wave < HPW) {
+                const float v = lane < CW ? ps[wave * CW + lane] : -INFINITY;
                 const bool in = v != -INFINITY;
                 const float m = wave_max(v);
                 const float e = in ? expf(v - m) : 0.0f;
                 const float l2 = wave_sum(e);
-                ps[lane] = e;
-                if (lane == 0) { S.mh[0] = m; S.lh[0] = l2; }
+                if (lane < CW) ps[wave * CW + lane] = e;
+                if (lane == 0) { S.mh[wave] = m; S.lh[wave] = l2; }
             }
             __syncthreads();
-            const uint32_t pb = uint32_t(lay.attp) + (c * NH + h) * (2u + kTkHD);
             {
                 const float2 vc = *reinterpret_cast<const float2*>(&S.vn[2u * dp]);
-                float pw[KQ4];
-#pragma unroll
-                for (uint32_t i = 0; i < KQ4; i += 4) {
-                    const float4 q = *reinterpret_cast<const float4*>(&ps[kq * KQ4 + i]);
-                    pw[i] = q.x; pw[i + 1] = q.y; pw[i + 2] = q.z; pw[i + 3] = q.w;
-                }
-                float oa[2] = {0.0f, 0.0f}, ob[2] = {0.0f, 0.0f};   // even / odd keys
+                float vf0[KQ4], vf1[KQ4];
 #pragma unroll
                 for (uint32_t i = 0; i < KQ4; ++i) {
                     const uint32_t jl = kq * KQ4 + i;
                     const bool cur = kv0 + j0 + jl == pos, in = j0 + jl < span;
                     const float v0 = cur ? vc.x : f16_bits_to_f32(vw[i]);
                     const float v1 = cur ? vc.y : f16_bits_to_f32(vw[i] >> 16);
-                    oa[i % 2u] = fmaf(pw[i], in ? v0 : 0.0f, oa[i % 2u]);
-                    ob[i % 2u] = fmaf(pw[i], in ? v1 : 0.0f, ob[i % 2u]);
+                    vf0[i] = in ? v0 : 0.0f;
+                    vf1[i] = in ? v1 : 0.0f;
                 }
-                float o0 = oa[0] + oa[1], o1 = ob[0] + ob[1];
-                // the four key quarters: lanes l ^ 16 (swizzle within 32), l ^ 32
-                o0 += __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(o0), 0x401F));
-                o1 += __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(o1), 0x401F));
-                o0 += __shfl_xor(o0, 32, kWave);
-                o1 += __shfl_xor(o1, 32, kWave);
-                if (kq == 0u) {
-                    const uint32_t vo = (pb + 2u + 2u * dp) * 8u;
-                    if (xl_st) ll_st2_xcd(rr, vo, soff, o0, o1, tag);
-                    else ll_st2(rr, vo, soff, o0, o1, tag);
+#pragma unroll
+                for (uint32_t hh = 0; hh < HPW; ++hh) {
+                    float pw[KQ4];
+#pragma unroll
+                    for (uint32_t i = 0; i < KQ4; i += 4) {
+                        const float4 q = *reinterpret_cast<const float4*>(&ps[hh * CW + kq * KQ4 + i]);
+                        pw[i] = q.x; pw[i + 1] = q.y; pw[i + 2] = q.z; pw[i + 3] = q.w;
+                    }
+                    float oa[2] = {0.0f, 0.0f}, ob[2] = {0.0f, 0.0f};   // even / odd keys
+#pragma unroll
+                    for (uint32_t i = 0; i < KQ4; ++i) {
+                        oa[i % 2u] = fmaf(pw[i], vf0[i], oa[i % 2u]);
+                        ob[i % 2u] = fmaf(pw[i], vf1[i], ob[i % 2u]);
+                    }
+                    float o0 = oa[0] + oa[1], o1 = ob[0] + ob[1];
+                    // the four key quarters: lanes l ^ 16 (swizzle within 32), l ^ 32
+                    o0 += __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(o0), 0x401F));
+                    o1 += __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(o1), 0x401F));
+                    o0 += __shfl_xor(o0, 32, kWave);
+                    o1 += __shfl_xor(o1, 32, kWave);
+                    if (kq == 0u) {
+                        const uint32_t pb = uint32_t(lay.attp) + (c * NH + h0 + hh) * (2u + kTkHD);
+                        const uint32_t vo = (pb + 2u + 2u * dp) * 8u;
+                        if (xl_st) ll_st2_xcd(rr, vo, soff, o0, o1, tag);
+                        else ll_st2(rr, vo, soff, o0, o1, tag);
+                    }
                 }
             }
-            if (tid == 0) {
-                if (xl_st) ll_st2_xcd(rr, pb * 8u, soff, S.mh[0], S.lh[0], tag);
-                else ll_st2(rr, pb * 8u, soff, S.mh[0], S.lh[0], tag);
+            if (tid < HPW) {
+                const uint32_t pb = uint32_t(lay.attp) + (c * NH + h0 + tid) * (2u + kTkHD);
+                if (xl_st) ll_st2_xcd(rr, pb * 8u, soff, S.mh[tid], S.lh[tid], tag);
+                else ll_st2(rr, pb * 8u, soff, S.mh[tid], S.lh[tid], tag);
             }
-            // head 0 of the chunk holding the current position appends its
-            // key / value to the caches for later tokens
-            if (h == 0u && c == n_att - 1u && tid < kTkHD) {
+            // the first heads of the chunk holding the current position append
+            // its key / value to the caches for later tokens
+            if (h0 == 0u && c == n_att - 1u && tid < kTkHD) {
                 stg16(L.kc + size_t(pos) * kTkHD + tid, S.kn16[tid]);
                 stg16(L.vc + size_t(pos) * kTkHD + tid, f32_to_f16_bits(S.vn[tid]));
             }
             __syncthreads();
         };
         if (hsplit) {
-            if (s_att < n_wga) attend_head(s_att % NH, s_att / NH);
+            if (s_att < n_wga)
+                attend_heads(std::integral_constant<uint32_t, 1u>{}, std::integral_constant<uint32_t, kHK>{},
+                             s_att % NH, s_att / NH);
+        } else if (gsplit) {
+            if (s_att < n_wga)
+                attend_heads(std::integral_constant<uint32_t, 2u>{}, std::integral_constant<uint32_t, kTkC>{},
+                             2u * (s_att % (NH / 2u)), s_att / (NH / 2u));
         } else if (s_att < n_att) {
             if (cw == 16u) attend(std::integral_constant<uint32_t, 16u>{});
             else attend(std::integral_constant<uint32_t, kTkC>{});
