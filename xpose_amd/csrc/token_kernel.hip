@@ -438,13 +438,37 @@ __device__ __forceinline__ void tile_prefetch(TkW<R>& p, const void* wq, const v
     }
 }
 
+// Readies a prefetched tile for tile_dot<..., true>: the weight nibbles as
+// two's complement (xor 0x88888888) and in s[r].x the float scale of the
+// lane's block of step r (the scale of block b0 + S (w + 8 r) + q is
+// component (b0 + S w + q) % 4 of its quad, the same for all r; zero for a
+// clamped repeat). Called before the stage's wait: the wait's loads return
+// after the prefetch's, so this work is done while the inputs are on their
+// way instead of after they arrive.
+template <int FMT, int R, uint32_t S = 1>
+__device__ __forceinline__ void tile_prep(TkW<R>& p, uint32_t b0, uint32_t nb, uint32_t wave,
+                                          uint32_t lane) {
+    const uint32_t q = lane % S;
+    const uint32_t sc = (b0 + S * wave + q) % 4u;
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        p.w[r] ^= 0x88888888u;
+        float f = tk_scale<FMT>(p.s[r], sc);
+        if (S * (wave + 8u * uint32_t(r)) + q >= nb) f = 0.0f;
+        p.s[r].x = __float_as_uint(f);
+        // done here, not sunk to the dot past the wait
+        asm volatile("" : "+v"(p.w[r]), "+v"(p.s[r].x));
+    }
+}
+
 // Dot of the wave's blocks with the staged planes (S.qx[0] = block b0; the
 // scale of block b0 + S (w + 8 r) + q is component (b0 + S w + q) % 4 of its
 // quad, the same for all r), the S block slots of a column added across
 // adjacent lanes, then reduced over the 8 waves in order. The result is valid
 // in wave 0, lane l holding column l / S; the caller publishes it. Starts
-// after the staging barrier; ends with a barrier.
-template <int FMT, int R, uint32_t S = 1>
+// after the staging barrier; ends with a barrier. PREP: p was readied by
+// tile_prep.
+template <int FMT, int R, uint32_t S = 1, bool PREP = false>
 __device__ __forceinline__ float tile_dot(const TkW<R>& p, TkSmem& Sm, uint32_t b0, uint32_t nb,
                                           uint32_t wave, uint32_t lane) {
     const uint32_t q = lane % S;
@@ -464,9 +488,13 @@ __device__ __forceinline__ float tile_dot(const TkW<R>& p, TkSmem& Sm, uint32_t 
     float acc = 0.0f;
 #pragma unroll
     for (int r = 0; r < R; ++r) {
-        float f = tk_scale<FMT>(p.s[r], sc) * sxv[r];
-        if (S * (wave + 8u * r) + q >= nb) f = 0.0f;
-        acc = fmaf(f, float(block_dot(p.w[r], qb[r])), acc);
+        if constexpr (PREP) {
+            acc = fmaf(__uint_as_float(p.s[r].x) * sxv[r], float(block_dot_signed(p.w[r], qb[r])), acc);
+        } else {
+            float f = tk_scale<FMT>(p.s[r], sc) * sxv[r];
+            if (S * (wave + 8u * r) + q >= nb) f = 0.0f;
+            acc = fmaf(f, float(block_dot(p.w[r], qb[r])), acc);
+        }
     }
     if constexpr (S >= 2) acc += dpp_f<0xB1, 0xF>(acc, 0.0f);   // quad_perm [1,0,3,2]: slot q ^ 1
     if constexpr (S >= 4) acc += dpp_f<0x4E, 0xF>(acc, 0.0f);   // quad_perm [2,3,0,1]: slot q ^ 2
@@ -715,6 +743,7 @@ __global__ __launch_bounds__(kTkThreads) void token_kernel(TokArgs a) {
             uint32_t m, g, c, h;
             qkv_tile(t, m, g, c, h);
             if (t != t_qkv) prefetch_qkv(pq, l, t);
+            tile_prep<FMT, RK, Sh::SQ>(pq, c * Sh::QB, Sh::QB, wave, lane);
             float w_in[kOwn] = {}, w_post[kOwn] = {}, x[kOwn] = {};
             if (hown) {
                 ld_own(w_in, L.norm[0] + kOwn * tid);
@@ -762,7 +791,7 @@ __global__ __launch_bounds__(kTkThreads) void token_kernel(TokArgs a) {
                 if (hown && i < Sh::QB * tpb) own_stage(S, xn, i);
             }
             __syncthreads();
-            float y = tile_dot<FMT, RK, Sh::SQ>(pq, S, c * Sh::QB, Sh::QB, wave, lane);
+            float y = tile_dot<FMT, RK, Sh::SQ, true>(pq, S, c * Sh::QB, Sh::QB, wave, lane);
             if (wave == 0) {
                 y *= norm_scale<H>(rsn, eps);
                 const uint32_t o = c * Sh::QKVD + (m == 0u ? 0u : (m == 1u ? QD : QD + kTkHD));
@@ -1329,6 +1358,7 @@ __global__ __launch_bounds__(kTkThreads) void token_kernel(TokArgs a) {
             constexpr uint32_t nb = Sh::OB;
             if (t != t_o) tile_prefetch<RO, Sh::SO>(po, L.w[3], L.s[3], QD / kBlk, H, g, h, c * nb, nb, wave, lane);
             TkW<RO>& p = po;
+            tile_prep<FMT, RO, Sh::SO>(p, c * nb, nb, wave, lane);
             if (tid < Sh::QO / Sh::KO) {
                 uint32_t off[kOwnP];
                 bool act[kOwnP];
@@ -1343,7 +1373,7 @@ __global__ __launch_bounds__(kTkThreads) void token_kernel(TokArgs a) {
             }
             __syncthreads();
             if (t == t_o) t_in = tk_now(a);
-            const float y = tile_dot<FMT, RO, Sh::SO>(p, S, c * nb, nb, wave, lane);
+            const float y = tile_dot<FMT, RO, Sh::SO, true>(p, S, c * nb, nb, wave, lane);
             if (wave == 0)
                 tile_put<Sh::SO>(rr, soff, uint32_t(lay.o) + c * H + g * kGrp + h * (kGrp / Sh::SO), y,
                                  lane, tag);
@@ -1372,6 +1402,7 @@ __global__ __launch_bounds__(kTkThreads) void token_kernel(TokArgs a) {
                     p.s[r] = ldg_stream2(sc + size_t(b / 4u) * FFN + g * kGrp + cl);
                 }
             }
+            tile_prep<FMT, RQ>(p, 0u, Sh::HB, wave, lane);
             float w_post[kOwn] = {}, w_in[kOwn] = {}, xa[kOwn] = {}, o[kOwn] = {};
             if (hown) {
                 ld_own(w_post, L.norm[1] + kOwn * tid);
@@ -1428,7 +1459,7 @@ __global__ __launch_bounds__(kTkThreads) void token_kernel(TokArgs a) {
             own_norm_defer(xn, x, w_in, rsn);
             if (hown) own_stage(S, xn, tid);
             __syncthreads();
-            float y = tile_dot<FMT>(p, S, 0u, Sh::HB, wave, lane);
+            float y = tile_dot<FMT, RQ, 1u, true>(p, S, 0u, Sh::HB, wave, lane);
             if (wave == 0) {
                 y *= norm_scale<H>(rsn, eps);
                 const float up = __shfl_xor(y, 32, kWave);
@@ -1451,6 +1482,7 @@ __global__ __launch_bounds__(kTkThreads) void token_kernel(TokArgs a) {
             const uint32_t nb = 4u * nq, k0 = 128u * q0;
             if (t != t_dn) prefetch_dn(pdn, l, t);
             if (t == t_dn && l + 1u < a.n_layers && t_qkv < Sh::N_QKV) prefetch_qkv(pq, l + 1u, t_qkv);
+            tile_prep<FMT, RD, Sh::SD>(pdn, 4u * q0, nb, wave, lane);
             if (tid < nb * (kBlk / kOwn)) {
                 // GeGLU output h of this chunk's k range (the gate/up tiles apply it)
                 uint32_t off[kOwnP];
@@ -1466,7 +1498,7 @@ __global__ __launch_bounds__(kTkThreads) void token_kernel(TokArgs a) {
             }
             __syncthreads();
             if (t == t_dn) t_in = tk_now(a);
-            const float y = tile_dot<FMT, RD, Sh::SD>(pdn, S, 4u * q0, nb, wave, lane);
+            const float y = tile_dot<FMT, RD, Sh::SD, true>(pdn, S, 4u * q0, nb, wave, lane);
             if (wave == 0)
                 tile_put<Sh::SD>(rr, soff, uint32_t(lay.dnp) + c * H + g * kGrp + h * (kGrp / Sh::SD), y,
                                  lane, tag);

@@ -95,8 +95,9 @@ __device__ __forceinline__ int32_t plane_dot(u32x4 w, u32x4 q, int32_t acc) {
     acc = __builtin_amdgcn_sdot8(int32_t(w.z), int32_t(q.z), acc, false);
     return __builtin_amdgcn_sdot8(int32_t(w.w), int32_t(q.w), acc, false);
 }
-__device__ __forceinline__ int32_t block_dot(u32x4 w, const QxBlock& q) {
-    w ^= 0x88888888u;
+// block_dot_signed: w holds two's-complement nibbles (the stored nibbles
+// xor 0x88888888); block_dot takes the stored (biased) nibbles.
+__device__ __forceinline__ int32_t block_dot_signed(u32x4 w, const QxBlock& q) {
     constexpr int PE = (kQxPlanes - 1) & ~1, PO = (kQxPlanes - 2) | 1;   // top even / odd plane
     int32_t e = plane_dot(w, q.p[PE], 0);
 #pragma unroll
@@ -105,6 +106,9 @@ __device__ __forceinline__ int32_t block_dot(u32x4 w, const QxBlock& q) {
 #pragma unroll
     for (int p = PO - 2; p >= 1; p -= 2) o = plane_dot(w, q.p[p], o * 256);
     return e + o * 16;
+}
+__device__ __forceinline__ int32_t block_dot(u32x4 w, const QxBlock& q) {
+    return block_dot_signed(w ^ 0x88888888u, q);
 }
 
 // Quantises eight consecutive activations (task i = (block i/4, word i%4))
