@@ -284,6 +284,26 @@ __device__ __forceinline__ unsigned long long tk_now(const TokArgs& a) {
     return a.trace ? __builtin_amdgcn_s_memrealtime() : 0ull;
 }
 
+// The hardware reciprocal and reciprocal square root (v_rcp_f32, v_rsq_f32:
+// about 1 ulp) in place of the correctly rounded division and square root,
+// which cost some thirty dependent instructions on a stage's critical path.
+// The quantiser's r = range * rcp(m) keeps |q| <= 2^18 + 1, inside the
+// digit planes' range.
+__device__ __forceinline__ float rcp_hw(float v) { return __builtin_amdgcn_rcpf(v); }
+__device__ __forceinline__ float rsq_hw(float v) { return __builtin_amdgcn_rsqf(v); }
+// e^v as 2^(v log2 e) on v_exp_f32: relative error ~1e-6 for |v| <= 20 (the
+// rounding of the product), against ~15 dependent instructions for expf.
+// Used where v <= 0 (softmax weights, rescale factors) or |v| <= 20 (GeGLU).
+__device__ __forceinline__ float exp_hw(float v) { return __builtin_amdgcn_exp2f(v * 1.4426950408889634f); }
+// GeGLU's tanh-approximated GELU (the form of gelu_tanh) on exp_hw.
+__device__ __forceinline__ float gelu_hw(float g) {
+    float z = 0.7978845608028654f * (g + 0.044715f * g * g * g);
+    z = fminf(fmaxf(z, -10.0f), 10.0f);
+    const float e = exp_hw(-2.0f * z);
+    const float t = (1.0f - e) * rcp_hw(1.0f + e);
+    return 0.5f * g * (1.0f + t);
+}
+
 // ---- block-wide reductions (512 threads, one barrier) ---------------------------
 // Every thread returns the same total, summed in a fixed order. rs must not be
 // written again before another barrier has passed (the kernel rotates four).
@@ -327,7 +347,7 @@ __device__ __forceinline__ void own_residual(float (&x)[kOwn], const float (&a)[
 #pragma unroll
     for (uint32_t e = 0; e < kOwn; ++e) ss = fmaf(t[e], t[e], ss);
     ss = blk_sum(ss, rs);
-    const float scale = 1.0f / sqrtf(ss / float(H) + eps);
+    const float scale = rsq_hw(ss * (1.0f / float(H)) + eps);
 #pragma unroll
     for (uint32_t e = 0; e < kOwn; ++e) x[e] = a[e] + t[e] * scale * (1.0f + w[e]);
 }
@@ -354,7 +374,7 @@ __device__ __forceinline__ float norm_scale(const float* rs, float eps) {
     const float4 p = *reinterpret_cast<const float4*>(rs);
     const float4 q = *reinterpret_cast<const float4*>(rs + 4);
     const float ss = ((p.x + p.y) + (p.z + p.w)) + ((q.x + q.y) + (q.z + q.w));
-    return 1.0f / sqrtf(ss / float(H) + eps);
+    return rsq_hw(ss * (1.0f / float(H)) + eps);
 }
 
 // Fixed-point staging (the planes of stage_x8, xp_device.hpp) from four
@@ -368,7 +388,7 @@ __device__ __forceinline__ void stage_x4(QxBlock* qx, float* sx, uint32_t i, con
     m = fmaxf(m, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(m), 0xB1, 0xF, 0xF, false)));
     m = fmaxf(m, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(m), 0x4E, 0xF, 0xF, false)));
     m = fmaxf(m, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(m), 0x141, 0xF, 0xF, false)));
-    const float r = m > 0.0f ? kQxRange / m : 0.0f;
+    const float r = m > 0.0f ? kQxRange * rcp_hw(m) : 0.0f;
     uint32_t t[4];
 #pragma unroll
     for (int e = 0; e < 4; ++e) t[e] = uint32_t(__float2int_rn(v[e] * r) + int32_t(kQxBias)) ^ kQxBias;
@@ -919,7 +939,7 @@ __global__ __launch_bounds__(kTkThreads) void token_kernel(TokArgs a) {
                     // QK-norm (wave sum) and RoPE of this head, in registers
                     float ss = e[0] * e[0] + e[1] * e[1] + e[2] * e[2] + e[3] * e[3];
                     ss = wave_sum(ss);
-                    const float scale = 1.0f / sqrtf(ss / float(kTkHD) + eps);
+                    const float scale = rsq_hw(ss * (1.0f / float(kTkHD)) + eps);
 #pragma unroll
                     for (int c = 0; c < 4; ++c) e[c] = e[c] * scale * (1.0f + wqk[c]);
 #pragma unroll
@@ -989,7 +1009,7 @@ __global__ __launch_bounds__(kTkThreads) void token_kernel(TokArgs a) {
                 const float v = S.sc[lane % CW][h];
                 const bool in = lane < CW && v != -INFINITY;
                 const float m = wave_max(in ? v : -INFINITY);
-                const float e = in ? expf(v - m) : 0.0f;
+                const float e = in ? exp_hw(v - m) : 0.0f;
                 const float l2 = wave_sum(e);
                 if (lane < CW) S.sc[lane][h] = e;
                 if (lane == 0) { S.mh[h] = m; S.lh[h] = l2; }
@@ -1126,7 +1146,7 @@ __global__ __launch_bounds__(kTkThreads) void token_kernel(TokArgs a) {
                 if (wave <= HPW) {
                     float ss = e[0] * e[0] + e[1] * e[1] + e[2] * e[2] + e[3] * e[3];
                     ss = wave_sum(ss);
-                    const float scale = 1.0f / sqrtf(ss / float(kTkHD) + eps);
+                    const float scale = rsq_hw(ss * (1.0f / float(kTkHD)) + eps);
 #pragma unroll
                     for (int q = 0; q < 4; ++q) e[q] = e[q] * scale * (1.0f + wqk[q]);
 #pragma unroll
@@ -1191,7 +1211,7 @@ __global__ __launch_bounds__(kTkThreads) void token_kernel(TokArgs a) {
                 const float v = lane < CW ? ps[wave * CW + lane] : -INFINITY;
                 const bool in = v != -INFINITY;
                 const float m = wave_max(v);
-                const float e = in ? expf(v - m) : 0.0f;
+                const float e = in ? exp_hw(v - m) : 0.0f;
                 const float l2 = wave_sum(e);
                 if (lane < CW) ps[wave * CW + lane] = e;
                 if (lane == 0) { S.mh[wave] = m; S.lh[wave] = l2; }
@@ -1321,7 +1341,7 @@ __global__ __launch_bounds__(kTkThreads) void token_kernel(TokArgs a) {
                     const float M = wave_max(m);
                     float lsum = 0.0f;
                     for (uint32_t s = lane; s < n_att; s += kWave) {
-                        const float f = expf(S.big[s * CS] - M);
+                        const float f = exp_hw(S.big[s * CS] - M);
                         S.fm[s] = f;
                         lsum += f * S.big[s * CS + 1u];
                     }
@@ -1340,7 +1360,7 @@ __global__ __launch_bounds__(kTkThreads) void token_kernel(TokArgs a) {
                     float r = 0.0f;
 #pragma unroll
                     for (uint32_t w = 0; w < NG; ++w) r += red[w * CD + d];
-                    tile_put(rr, soff, uint32_t(lay.atto) + h * kTkHD + d0, r / Ltot, lane, tag);
+                    tile_put(rr, soff, uint32_t(lay.atto) + h * kTkHD + d0, r * rcp_hw(Ltot), lane, tag);
                 }
                 __syncthreads();
             }
@@ -1463,7 +1483,7 @@ __global__ __launch_bounds__(kTkThreads) void token_kernel(TokArgs a) {
             if (wave == 0) {
                 y *= norm_scale<H>(rsn, eps);
                 const float up = __shfl_xor(y, 32, kWave);
-                const float hv = gelu_tanh(y) * up;   // lanes 0..31: index 32 t + lane
+                const float hv = gelu_hw(y) * up;   // lanes 0..31: index 32 t + lane
                 const float hn = dpp_f<0xB1, 0xF>(hv, 0.0f);
                 if (lane < 32u && (lane & 1u) == 0u)
                     ll_st2(rr, (uint32_t(lay.gu) + 32u * t + lane) * 8u, soff, hv, hn, tag);
