@@ -177,6 +177,7 @@ struct TkSmem {
     float    amv[kTkWaves];
     uint32_t ami[kTkWaves];
     alignas(16) uint16_t kn16[kTkHD];       // current key as fp16 bits (head-split chunks)
+    float    pc[kTkMaxQH];                   // weight of the current key (head-split chunks)
 };
 
 // ---- exchange slots -------------------------------------------------------------
@@ -1107,19 +1108,29 @@ __global__ __launch_bounds__(kTkThreads) void token_kernel(TokArgs a) {
             // values: wave w, lane l: dims 2 dp, 2 dp + 1 (dp = 16 w + l % 16)
             // of keys kq KQ4 .. kq KQ4 + KQ4 - 1, kq = l / 16
             const uint32_t dp = 16u * wave + lane % 16u, kq = lane / 16u;
-            // rows past the span are clamped and dropped by selects (see attend)
-            // key part p takes dims 4 TPK i + 4 p .. + 3 (i < DPT / 4): the
+            // Rows are read up to the last appended one (span - 2): the key
+            // and value loads read only rows this token attends to, the
+            // current key (row span - 1, not yet appended) comes from LDS, and
+            // every key from span - 1 on is weighted 0 in the value sum, its
+            // loaded row being a finite context row. With span 1 the only key
+            // is the current one and the loaded values are zeroed.
+            // Key part p takes dims 4 TPK i + 4 p .. + 3 (i < DPT / 4): the
             // parts of a key read consecutive float4 of q (no LDS bank conflicts)
+            const uint32_t rlast = span >= 2u ? span - 2u : 0u;
             u32x2 kr[DPT / 4u];
             uint32_t vw[KQ4];
             {
-                const uint16_t* kp = L.kc + size_t(kv0 + min(j0 + jk, span - 1u)) * kTkHD + 4u * part;
+                const uint16_t* kp = L.kc + size_t(kv0 + min(j0 + jk, rlast)) * kTkHD + 4u * part;
 #pragma unroll
                 for (uint32_t i = 0; i < DPT / 4u; ++i) kr[i] = *(const XP_GLOBAL u32x2*)(kp + 4u * TPK * i);
             }
 #pragma unroll
             for (uint32_t i = 0; i < KQ4; ++i)
-                vw[i] = ldg32(L.vc + size_t(kv0 + min(j0 + kq * KQ4 + i, span - 1u)) * kTkHD + 2u * dp);
+                vw[i] = ldg32(L.vc + size_t(kv0 + min(j0 + kq * KQ4 + i, rlast)) * kTkHD + 2u * dp);
+            if (span < 2u) {
+#pragma unroll
+                for (uint32_t i = 0; i < KQ4; ++i) vw[i] = 0u;
+            }
             // waves 0 .. HPW - 1: the query heads, wave HPW: the key, wave
             // HPW + 1: the value (lane l holds elements 2 l, 2 l + 1, 2 l + 128,
             // 2 l + 129)
@@ -1165,7 +1176,13 @@ __global__ __launch_bounds__(kTkThreads) void token_kernel(TokArgs a) {
             // TPK lanes (half a DPP row or one)
             {
                 const uint32_t jj = j0 + jk;
-                const bool valid = jj < span, cur = kv0 + jj == pos;
+                const bool valid = jj < span;
+                // the current key's lanes take it from LDS, before the loop
+                if (kv0 + jj == pos) {
+#pragma unroll
+                    for (uint32_t i = 0; i < DPT / 4u; ++i)
+                        kr[i] = *reinterpret_cast<const u32x2*>(&S.kn16[4u * TPK * i + 4u * part]);
+                }
                 float dd[HPW][NCH];   // independent chains
 #pragma unroll
                 for (uint32_t hh = 0; hh < HPW; ++hh)
@@ -1174,8 +1191,7 @@ __global__ __launch_bounds__(kTkThreads) void token_kernel(TokArgs a) {
 #pragma unroll
                 for (uint32_t i = 0; i < DPT / 4u; ++i) {
                     const uint32_t d0 = 4u * TPK * i + 4u * part;
-                    u32x2 kb = kr[i];
-                    if (cur) kb = *reinterpret_cast<const u32x2*>(&S.kn16[d0]);
+                    const u32x2 kb = kr[i];
                     const float k0 = f16_bits_to_f32(kb.x);
                     const float k1 = f16_bits_to_f32(kb.x >> 16);
                     const float k2 = f16_bits_to_f32(kb.y);
@@ -1206,29 +1222,24 @@ __global__ __launch_bounds__(kTkThreads) void token_kernel(TokArgs a) {
                 }
             }
             __syncthreads();
-            // the chunk's softmax: wave hh takes head hh, one key per lane
+            // the chunk's softmax: wave hh takes head hh, one key per lane; the
+            // current key's weight is kept apart (S.pc) and 0 in ps
             if (wave < HPW) {
                 const float v = lane < CW ? ps[wave * CW + lane] : -INFINITY;
                 const bool in = v != -INFINITY;
                 const float m = wave_max(v);
                 const float e = in ? exp_hw(v - m) : 0.0f;
                 const float l2 = wave_sum(e);
-                if (lane < CW) ps[wave * CW + lane] = e;
-                if (lane == 0) { S.mh[wave] = m; S.lh[wave] = l2; }
+                const uint32_t jc = pos - kv0 - j0;   // the current key's index, if < CW
+                const float pcur = jc < CW ? __shfl(e, int(jc), kWave) : 0.0f;
+                if (lane < CW) ps[wave * CW + lane] = lane == jc ? 0.0f : e;
+                if (lane == 0) { S.mh[wave] = m; S.lh[wave] = l2; S.pc[wave] = pcur; }
             }
             __syncthreads();
             {
+                // loaded rows from span - 1 on have weight 0 (see the loads), so
+                // the sum needs no selects: one fma with an fp16 operand per dim
                 const float2 vc = *reinterpret_cast<const float2*>(&S.vn[2u * dp]);
-                float vf0[KQ4], vf1[KQ4];
-#pragma unroll
-                for (uint32_t i = 0; i < KQ4; ++i) {
-                    const uint32_t jl = kq * KQ4 + i;
-                    const bool cur = kv0 + j0 + jl == pos, in = j0 + jl < span;
-                    const float v0 = cur ? vc.x : f16_bits_to_f32(vw[i]);
-                    const float v1 = cur ? vc.y : f16_bits_to_f32(vw[i] >> 16);
-                    vf0[i] = in ? v0 : 0.0f;
-                    vf1[i] = in ? v1 : 0.0f;
-                }
 #pragma unroll
                 for (uint32_t hh = 0; hh < HPW; ++hh) {
                     float pw[KQ4];
@@ -1240,8 +1251,8 @@ __global__ __launch_bounds__(kTkThreads) void token_kernel(TokArgs a) {
                     float oa[2] = {0.0f, 0.0f}, ob[2] = {0.0f, 0.0f};   // even / odd keys
 #pragma unroll
                     for (uint32_t i = 0; i < KQ4; ++i) {
-                        oa[i % 2u] = fmaf(pw[i], vf0[i], oa[i % 2u]);
-                        ob[i % 2u] = fmaf(pw[i], vf1[i], ob[i % 2u]);
+                        oa[i % 2u] = fmaf(pw[i], f16_bits_to_f32(vw[i]), oa[i % 2u]);
+                        ob[i % 2u] = fmaf(pw[i], f16_bits_to_f32(vw[i] >> 16), ob[i % 2u]);
                     }
                     float o0 = oa[0] + oa[1], o1 = ob[0] + ob[1];
                     // the four key quarters: lanes l ^ 16 (swizzle within 32), l ^ 32
@@ -1249,6 +1260,9 @@ __global__ __launch_bounds__(kTkThreads) void token_kernel(TokArgs a) {
                     o1 += __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(o1), 0x401F));
                     o0 += __shfl_xor(o0, 32, kWave);
                     o1 += __shfl_xor(o1, 32, kWave);
+                    const float pcur = S.pc[hh];
+                    o0 = fmaf(pcur, vc.x, o0);
+                    o1 = fmaf(pcur, vc.y, o1);
                     if (kq == 0u) {
                         const uint32_t pb = uint32_t(lay.attp) + (c * NH + h0 + hh) * (2u + kTkHD);
                         const uint32_t vo = (pb + 2u + 2u * dp) * 8u;
