@@ -305,6 +305,31 @@ __device__ __forceinline__ float gelu_hw(float g) {
     return 0.5f * g * (1.0f + t);
 }
 
+// Wave maximum of floats through order-preserving int32 keys (a float's bits,
+// the magnitude bits flipped when negative): v_max_i32 takes its DPP operand
+// in place, where fmaxf first quiets both inputs (two more instructions a
+// step). -inf orders below every finite value; the identity is INT32_MIN.
+__device__ __forceinline__ int32_t f2ord(float v) {
+    const int32_t k = __float_as_int(v);
+    return k ^ ((k >> 31) & 0x7FFFFFFF);
+}
+__device__ __forceinline__ float ord2f(int32_t k) { return __int_as_float(k ^ ((k >> 31) & 0x7FFFFFFF)); }
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ int32_t dpp_i(int32_t v, int32_t old) {
+    return __builtin_amdgcn_update_dpp(old, v, CTRL, ROW_MASK, 0xF, false);
+}
+__device__ __forceinline__ float wave_max_ord(float v) {
+    constexpr int32_t lo = INT32_MIN;
+    int32_t k = f2ord(v);
+    k = max(k, dpp_i<0xB1, 0xF>(k, lo));    // quad_perm [1,0,3,2]
+    k = max(k, dpp_i<0x4E, 0xF>(k, lo));    // quad_perm [2,3,0,1]
+    k = max(k, dpp_i<0x141, 0xF>(k, lo));   // row_half_mirror
+    k = max(k, dpp_i<0x140, 0xF>(k, lo));   // row_mirror
+    k = max(k, dpp_i<0x142, 0xA>(k, lo));   // row_bcast:15 -> rows 1, 3
+    k = max(k, dpp_i<0x143, 0xC>(k, lo));   // row_bcast:31 -> rows 2, 3
+    return ord2f(__builtin_amdgcn_readlane(k, 63));
+}
+
 // ---- block-wide reductions (512 threads, one barrier) ---------------------------
 // Every thread returns the same total, summed in a fixed order. rs must not be
 // written again before another barrier has passed (the kernel rotates four).
@@ -384,11 +409,15 @@ __device__ __forceinline__ float norm_scale(const float* rs, float eps) {
 // plane; the eight tasks of a block are adjacent lanes of one wave. The
 // block maximum, the scale and every digit are those stage_x8 computes.
 __device__ __forceinline__ void stage_x4(QxBlock* qx, float* sx, uint32_t i, const float (&v)[4]) {
-    float m = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
+    // |v| as bits: non-negative floats order as unsigned integers, so the
+    // maximum is an integer max whose DPP operand needs no quieting
+    uint32_t mb = max(max(__float_as_uint(v[0]) & 0x7FFFFFFFu, __float_as_uint(v[1]) & 0x7FFFFFFFu),
+                      max(__float_as_uint(v[2]) & 0x7FFFFFFFu, __float_as_uint(v[3]) & 0x7FFFFFFFu));
     // max over the block's eight tasks: quad_perm xor 1, xor 2, then row_half_mirror
-    m = fmaxf(m, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(m), 0xB1, 0xF, 0xF, false)));
-    m = fmaxf(m, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(m), 0x4E, 0xF, 0xF, false)));
-    m = fmaxf(m, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(m), 0x141, 0xF, 0xF, false)));
+    mb = max(mb, uint32_t(__builtin_amdgcn_update_dpp(0, int(mb), 0xB1, 0xF, 0xF, false)));
+    mb = max(mb, uint32_t(__builtin_amdgcn_update_dpp(0, int(mb), 0x4E, 0xF, 0xF, false)));
+    mb = max(mb, uint32_t(__builtin_amdgcn_update_dpp(0, int(mb), 0x141, 0xF, 0xF, false)));
+    const float m = __uint_as_float(mb);
     const float r = m > 0.0f ? kQxRange * rcp_hw(m) : 0.0f;
     uint32_t t[4];
 #pragma unroll
@@ -1009,7 +1038,7 @@ __global__ __launch_bounds__(kTkThreads) void token_kernel(TokArgs a) {
                 const uint32_t h = wave;
                 const float v = S.sc[lane % CW][h];
                 const bool in = lane < CW && v != -INFINITY;
-                const float m = wave_max(in ? v : -INFINITY);
+                const float m = wave_max_ord(in ? v : -INFINITY);
                 const float e = in ? exp_hw(v - m) : 0.0f;
                 const float l2 = wave_sum(e);
                 if (lane < CW) S.sc[lane][h] = e;
@@ -1227,7 +1256,7 @@ __global__ __launch_bounds__(kTkThreads) void token_kernel(TokArgs a) {
             if (wave < HPW) {
                 const float v = lane < CW ? ps[wave * CW + lane] : -INFINITY;
                 const bool in = v != -INFINITY;
-                const float m = wave_max(v);
+                const float m = wave_max_ord(v);
                 const float e = in ? exp_hw(v - m) : 0.0f;
                 const float l2 = wave_sum(e);
                 const uint32_t jc = pos - kv0 - j0;   // the current key's index, if < CW
@@ -1352,7 +1381,7 @@ __global__ __launch_bounds__(kTkThreads) void token_kernel(TokArgs a) {
                 if (wave == 0) {
                     float m = -INFINITY;
                     for (uint32_t s = lane; s < n_att; s += kWave) m = fmaxf(m, S.big[s * CS]);
-                    const float M = wave_max(m);
+                    const float M = wave_max_ord(m);
                     float lsum = 0.0f;
                     for (uint32_t s = lane; s < n_att; s += kWave) {
                         const float f = exp_hw(S.big[s * CS] - M);
