@@ -462,10 +462,10 @@ __device__ __forceinline__ float tk_scale(u32x2 raw, uint32_t i) {
 // ---- matvec tiles ------------------------------------------------------------------
 // A tile: columns h CW .. h CW + CW - 1 (CW = 64 / S) of column group g of a
 // KM4 matrix (nblk 32-blocks of k, cols columns), k blocks [b0, b0 + nb).
-// Lane l takes column h CW + l / S and block slot q = l % S; wave w takes the
-// S-block steps w + 8 r (r < R), i.e. block b0 + min(S (w + 8 r) + q, nb - 1);
-// a repeated (clamped) block is computed and weighted by zero. S = 1 is one
-// whole column group, lane = column.
+// Lane l takes column h CW + l % CW and block slot q = l / CW (a slot is
+// whole 16-lane rows); wave w takes the S-block steps w + 8 r (r < R), i.e.
+// block b0 + min(S (w + 8 r) + q, nb - 1); a repeated (clamped) block is
+// computed and weighted by zero. S = 1 is one whole column group, lane = column.
 template <int R>
 struct TkW {
     u32x4 w[R];
@@ -479,7 +479,7 @@ __device__ __forceinline__ void tile_prefetch(TkW<R>& p, const void* wq, const v
     constexpr uint32_t CW = kGrp / S;
     const u32x4* w = static_cast<const u32x4*>(wq);
     const u32x2* s = static_cast<const u32x2*>(sc);
-    const uint32_t cl = h * CW + lane / S, q = lane % S;
+    const uint32_t cl = h * CW + lane % CW, q = lane / CW;
 #pragma unroll
     for (int r = 0; r < R; ++r) {
         const uint32_t b = b0 + min(S * (wave + 8u * r) + q, nb - 1u);
@@ -488,17 +488,17 @@ __device__ __forceinline__ void tile_prefetch(TkW<R>& p, const void* wq, const v
     }
 }
 
-// Readies a prefetched tile for tile_dot<..., true>: the weight nibbles as
-// two's complement (xor 0x88888888) and in s[r].x the float scale of the
-// lane's block of step r (the scale of block b0 + S (w + 8 r) + q is
-// component (b0 + S w + q) % 4 of its quad, the same for all r; zero for a
-// clamped repeat). Called before the stage's wait: the wait's loads return
-// after the prefetch's, so this work is done while the inputs are on their
-// way instead of after they arrive.
+// Readies a prefetched tile for tile_dot: the weight nibbles as two's
+// complement (xor 0x88888888) and in s[r].x the float scale of the lane's
+// block of step r (the scale of block b0 + S (w + 8 r) + q is component
+// (b0 + S w + q) % 4 of its quad, the same for all r; zero for a clamped
+// repeat). Called before the stage's wait: the wait's loads return after the
+// prefetch's, so this work is done while the inputs are on their way instead
+// of after they arrive.
 template <int FMT, int R, uint32_t S = 1>
 __device__ __forceinline__ void tile_prep(TkW<R>& p, uint32_t b0, uint32_t nb, uint32_t wave,
                                           uint32_t lane) {
-    const uint32_t q = lane % S;
+    const uint32_t q = lane / (kGrp / S);
     const uint32_t sc = (b0 + S * wave + q) % 4u;
 #pragma unroll
     for (int r = 0; r < R; ++r) {
@@ -511,68 +511,114 @@ __device__ __forceinline__ void tile_prep(TkW<R>& p, uint32_t b0, uint32_t nb, u
     }
 }
 
-// Dot of the wave's blocks with the staged planes (S.qx[0] = block b0; the
-// scale of block b0 + S (w + 8 r) + q is component (b0 + S w + q) % 4 of its
-// quad, the same for all r), the S block slots of a column added across
-// adjacent lanes, then reduced over the 8 waves in order. The result is valid
-// in wave 0, lane l holding column l / S; the caller publishes it. Starts
-// after the staging barrier; ends with a barrier. PREP: p was readied by
-// tile_prep.
-template <int FMT, int R, uint32_t S = 1, bool PREP = false>
-__device__ __forceinline__ float tile_dot(const TkW<R>& p, TkSmem& Sm, uint32_t b0, uint32_t nb,
-                                          uint32_t wave, uint32_t lane) {
-    const uint32_t q = lane % S;
-    const uint32_t sc = (b0 + S * wave + q) % 4u;
-    // Every block's staged planes and scale are read before any is used: the
-    // reads return in order while the first blocks are multiplied, instead of
-    // one LDS round trip per block.
-    QxBlock qb[R];
+// The dot of one block with the staged planes, its activation words taken
+// from the lanes of the row: lane j < 2 P of each 16-lane row holds words
+// 2 j, 2 j + 1 of the block's 4 P plane words (plane p's word c is word
+// 4 p + c), and v_dot8c_i32_i4 with DPP row_newbcast:n reads lane n of the
+// row. A wave's lanes then read 8 bytes each from LDS for a block, not its
+// 16 P bytes. (The DPP form is inline assembly: the compiler does not fold a
+// DPP move into v_dot8c. Its sources come straight from LDS loads; see
+// tile_dot for the exec hazard.)
+template <int N>
+__device__ __forceinline__ int32_t dot8_bc(int32_t acc, uint32_t a, uint32_t w);
+#define XP_DOT8_BC(N)                                                                               \
+    template <>                                                                                    \
+    __device__ __forceinline__ int32_t dot8_bc<N>(int32_t acc, uint32_t a, uint32_t w) {           \
+        asm("v_dot8c_i32_i4_dpp %0, %1, %2 row_newbcast:" #N " row_mask:0xf bank_mask:0xf"         \
+            : "+v"(acc)                                                                            \
+            : "v"(a), "v"(w));                                                                     \
+        return acc;                                                                                \
+    }
+XP_DOT8_BC(0)
+XP_DOT8_BC(1)
+XP_DOT8_BC(2)
+XP_DOT8_BC(3)
+XP_DOT8_BC(4)
+XP_DOT8_BC(5)
+XP_DOT8_BC(6)
+XP_DOT8_BC(7)
+XP_DOT8_BC(8)
+XP_DOT8_BC(9)
+#undef XP_DOT8_BC
+template <int P>
+__device__ __forceinline__ int32_t plane_dot_bc(u32x4 w, u32x2 a, int32_t acc) {
+    acc = dot8_bc<2 * P>(acc, a.x, w.x);       // word 4 P     (lane 2 P, first)
+    acc = dot8_bc<2 * P>(acc, a.y, w.y);       // word 4 P + 1 (lane 2 P, second)
+    acc = dot8_bc<2 * P + 1>(acc, a.x, w.z);   // word 4 P + 2
+    return dot8_bc<2 * P + 1>(acc, a.y, w.w);  // word 4 P + 3
+}
+// planes P, P - 2, ... by Horner's rule (x 256 a step)
+template <int P>
+__device__ __forceinline__ int32_t chain_bc(u32x4 w, u32x2 a, int32_t acc) {
+    acc = plane_dot_bc<P>(w, a, acc);
+    if constexpr (P >= 2) return chain_bc<P - 2>(w, a, acc * 256);
+    else return acc;
+}
+// sum_k w_k q_k over one block for two's-complement nibbles w (block_dot_signed)
+__device__ __forceinline__ int32_t block_dot_bc(u32x4 w, u32x2 a) {
+    constexpr int PE = (kQxPlanes - 1) & ~1, PO = (kQxPlanes - 2) | 1;   // top even / odd plane
+    return chain_bc<PE>(w, a, 0) + chain_bc<PO>(w, a, 0) * 16;
+}
+
+// Dot of the wave's blocks with the staged planes (S.qx[0] = block b0) for a
+// tile readied by tile_prep, then reduced over the 8 waves and the S slots
+// in order. The result is valid in wave 0, lane l < CW holding column l; the
+// caller publishes it. Starts after the staging barrier; ends with a barrier.
+template <int R, uint32_t S = 1>
+__device__ __forceinline__ float tile_dot(const TkW<R>& p, TkSmem& Sm, uint32_t nb, uint32_t wave,
+                                          uint32_t lane) {
+    constexpr uint32_t CW = kGrp / S;
+    constexpr uint32_t NW = 2u * kQxPlanes;   // lanes of a row holding a block's words
+    static_assert(NW <= 16u && 2u * NW >= 16u, "a block's words fill one row's lanes");
+    const uint32_t q = lane / CW, j = lane % 16u;
+    const uint32_t jw = j >= NW ? j - NW : j;   // the other lanes repeat words (unused)
+    // Every block's words and scale are read before any is used: the reads
+    // return in order while the first blocks are multiplied.
+    u32x2 aw[R];
     float sxv[R];
 #pragma unroll
     for (int r = 0; r < R; ++r) {
         const uint32_t lb = min(S * (wave + 8u * r) + q, nb - 1u);
         sxv[r] = Sm.sx[lb];
-        qb[r] = Sm.qx[lb];
+        aw[r] = reinterpret_cast<const u32x2*>(&Sm.qx[lb])[jw];
     }
     __builtin_amdgcn_sched_barrier(0);
+    // A DPP operation must follow a write of exec by five wait states, which
+    // the compiler does not provide for inline assembly: one s_nop 4 before
+    // the first, ordered after the loads by the tied operands.
+#pragma unroll
+    for (int r = 0; r < R; ++r) asm volatile("s_nop 4" : "+v"(aw[r].x), "+v"(aw[r].y));
     float acc = 0.0f;
 #pragma unroll
-    for (int r = 0; r < R; ++r) {
-        if constexpr (PREP) {
-            acc = fmaf(__uint_as_float(p.s[r].x) * sxv[r], float(block_dot_signed(p.w[r], qb[r])), acc);
-        } else {
-            float f = tk_scale<FMT>(p.s[r], sc) * sxv[r];
-            if (S * (wave + 8u * r) + q >= nb) f = 0.0f;
-            acc = fmaf(f, float(block_dot(p.w[r], qb[r])), acc);
-        }
-    }
-    if constexpr (S >= 2) acc += dpp_f<0xB1, 0xF>(acc, 0.0f);   // quad_perm [1,0,3,2]: slot q ^ 1
-    if constexpr (S >= 4) acc += dpp_f<0x4E, 0xF>(acc, 0.0f);   // quad_perm [2,3,0,1]: slot q ^ 2
+    for (int r = 0; r < R; ++r)
+        acc = fmaf(__uint_as_float(p.s[r].x) * sxv[r], float(block_dot_bc(p.w[r], aw[r])), acc);
     Sm.red[wave][lane] = acc;
     __syncthreads();
     float y = 0.0f;
     if (wave == 0) {
-        // all eight partials in flight at once, then summed in wave order
-        float pw[kTkWaves];
+        // all partials in flight at once, then summed in wave, slot order
+        const uint32_t c = lane % CW;
+        float pw[kTkWaves * S];
 #pragma unroll
-        for (int w = 0; w < kTkWaves; ++w) pw[w] = Sm.red[w][lane];
+        for (int w = 0; w < kTkWaves; ++w)
+#pragma unroll
+            for (uint32_t sl = 0; sl < S; ++sl) pw[w * S + sl] = Sm.red[w][c + sl * CW];
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-        for (int w = 0; w < kTkWaves; ++w) y += pw[w];
+        for (uint32_t i = 0; i < kTkWaves * S; ++i) y += pw[i];
     }
     return y;
 }
 
-// Wave 0 publishes its 64 / S column results y (lane l holding column l / S)
-// at slots s0 + column: lane 2 S m stores columns 2 m and 2 m + 1, the second
-// read from lane 2 S m + S (row_shl within a DPP row; quad_perm xor 1 for S = 1).
+// Wave 0 publishes its CW = 64 / S column results y (lane l < CW holding
+// column l) at slots s0 + column: lane 2 m stores columns 2 m and 2 m + 1,
+// the second read from lane 2 m + 1 (quad_perm xor 1).
 template <uint32_t S = 1>
 __device__ __forceinline__ void tile_put(rsrc_t r, uint32_t soff, uint32_t s0, float y, uint32_t lane,
                                          uint32_t tag) {
-    float yn;
-    if constexpr (S == 1) yn = dpp_f<0xB1, 0xF>(y, 0.0f);
-    else yn = dpp_f<0x100 + int(S), 0xF>(y, 0.0f);
-    if (lane % (2u * S) == 0u) ll_st2(r, (s0 + lane / S) * 8u, soff, y, yn, tag);
+    constexpr uint32_t CW = kGrp / S;
+    const float yn = dpp_f<0xB1, 0xF>(y, 0.0f);
+    if (lane < CW && lane % 2u == 0u) ll_st2(r, (s0 + lane) * 8u, soff, y, yn, tag);
 }
 
 __device__ __forceinline__ float f16_round(float v) { return f16_bits_to_f32(f32_to_f16_bits(v)); }
@@ -841,7 +887,7 @@ __global__ __launch_bounds__(kTkThreads) void token_kernel(TokArgs a) {
                 if (hown && i < Sh::QB * tpb) own_stage(S, xn, i);
             }
             __syncthreads();
-            float y = tile_dot<FMT, RK, Sh::SQ, true>(pq, S, c * Sh::QB, Sh::QB, wave, lane);
+            float y = tile_dot<RK, Sh::SQ>(pq, S, Sh::QB, wave, lane);
             if (wave == 0) {
                 y *= norm_scale<H>(rsn, eps);
                 const uint32_t o = c * Sh::QKVD + (m == 0u ? 0u : (m == 1u ? QD : QD + kTkHD));
@@ -1436,7 +1482,7 @@ __global__ __launch_bounds__(kTkThreads) void token_kernel(TokArgs a) {
             }
             __syncthreads();
             if (t == t_o) t_in = tk_now(a);
-            const float y = tile_dot<FMT, RO, Sh::SO, true>(p, S, c * nb, nb, wave, lane);
+            const float y = tile_dot<RO, Sh::SO>(p, S, nb, wave, lane);
             if (wave == 0)
                 tile_put<Sh::SO>(rr, soff, uint32_t(lay.o) + c * H + g * kGrp + h * (kGrp / Sh::SO), y,
                                  lane, tag);
@@ -1522,7 +1568,7 @@ __global__ __launch_bounds__(kTkThreads) void token_kernel(TokArgs a) {
             own_norm_defer(xn, x, w_in, rsn);
             if (hown) own_stage(S, xn, tid);
             __syncthreads();
-            float y = tile_dot<FMT, RQ, 1u, true>(p, S, 0u, Sh::HB, wave, lane);
+            float y = tile_dot<RQ, 1u>(p, S, Sh::HB, wave, lane);
             if (wave == 0) {
                 y *= norm_scale<H>(rsn, eps);
                 const float up = __shfl_xor(y, 32, kWave);
@@ -1561,7 +1607,7 @@ __global__ __launch_bounds__(kTkThreads) void token_kernel(TokArgs a) {
             }
             __syncthreads();
             if (t == t_dn) t_in = tk_now(a);
-            const float y = tile_dot<FMT, RD, Sh::SD, true>(pdn, S, 4u * q0, nb, wave, lane);
+            const float y = tile_dot<RD, Sh::SD>(pdn, S, nb, wave, lane);
             if (wave == 0)
                 tile_put<Sh::SD>(rr, soff, uint32_t(lay.dnp) + c * H + g * kGrp + h * (kGrp / Sh::SD), y,
                                  lane, tag);
