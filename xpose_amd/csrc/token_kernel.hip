@@ -1662,13 +1662,25 @@ __global__ __launch_bounds__(kTkThreads) void token_kernel(TokArgs a) {
     float bv = -INFINITY;
     uint32_t bi = 0u;
     float acc = 0.0f;
+    // the staged words of a block through the row's lanes (block_dot_bc)
+    constexpr uint32_t NWL = 2u * kQxPlanes;
+    const uint32_t jl = lane % 16u, jwl = jl >= NWL ? jl - NWL : jl;
     auto mul_u = [&](int r, uint32_t u) {
         const uint32_t q = u % nqh;
+        u32x2 aw[4];
+        float sxv[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            const uint32_t lb = 4u * q + i;
-            const float f = tk_scale<FMT>(s3[r], i) * S.sx[lb];
-            acc = fmaf(f, float(block_dot(w3[r][i], S.qx[lb])), acc);
+            sxv[i] = S.sx[4u * q + i];
+            aw[i] = reinterpret_cast<const u32x2*>(&S.qx[4u * q + i])[jwl];
+        }
+        // exec may have been written just before (see tile_dot)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) asm volatile("s_nop 4" : "+v"(aw[i].x), "+v"(aw[i].y));
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const float f = tk_scale<FMT>(s3[r], i) * sxv[i];
+            acc = fmaf(f, float(block_dot_bc(w3[r][i] ^ 0x88888888u, aw[i])), acc);
         }
         if (q == nqh - 1u) {
             const uint32_t j = (gw + (u / nqh) * nw) * kGrp + lane;
