@@ -86,6 +86,7 @@ constexpr int      kTkMaxGrid   = 1024;
 constexpr uint32_t kSpinLimit   = 1u << 24;
 constexpr int      kTkBig       = 17408;                 // floats of stage scratch
 constexpr int      kTkMaxLayers = 64;
+constexpr int      kTkLmDepth   = 3;     // lm_head units in flight per wave (4 and 6 measured no faster)
 // Slot buffer operations use device scope (sc1, kAuxDev) on raw buffer
 // resources (kRsrcWord3).
 // Poll back-off of the first phase of the gate/up stage's wait (one thread
@@ -1629,8 +1630,10 @@ __global__ __launch_bounds__(kTkThreads) void token_kernel(TokArgs a) {
     // Quad stream of this wave: groups gw, gw + nw, ...; k/128 quads each.
     const uint32_t my_groups = gw < ng ? (ng - gw + nw - 1u) / nw : 0u;
     const uint32_t nu = my_groups * nqh;
-    u32x4 w3[3][4];
-    u32x2 s3[3];
+    // units in flight per wave (each 4 blocks of 64 columns: 18 VGPRs)
+    constexpr int LD = kTkLmDepth;
+    u32x4 w3[LD][4];
+    u32x2 s3[LD];
     auto load_u = [&](int r, uint32_t u) {
         const uint32_t uc = min(u, nu - 1u);
         const uint32_t g = gw + (uc / nqh) * nw, q = uc % nqh;
@@ -1641,9 +1644,8 @@ __global__ __launch_bounds__(kTkThreads) void token_kernel(TokArgs a) {
                             g * kGrp + lane);
     };
     if (nu > 0) {
-        load_u(0, 0);
-        load_u(1, 1);
-        load_u(2, 2);
+#pragma unroll
+        for (int r = 0; r < LD; ++r) load_u(r, uint32_t(r));
     }
     float* rsn_lm;
     {
@@ -1690,16 +1692,13 @@ __global__ __launch_bounds__(kTkThreads) void token_kernel(TokArgs a) {
             acc = 0.0f;
         }
     };
-    for (uint32_t u = 0; u < nu; u += 3) {
-        mul_u(0, u);
-        if (u + 3 < nu) load_u(0, u + 3);
-        if (u + 1 < nu) {
-            mul_u(1, u + 1);
-            if (u + 4 < nu) load_u(1, u + 4);
-        }
-        if (u + 2 < nu) {
-            mul_u(2, u + 2);
-            if (u + 5 < nu) load_u(2, u + 5);
+    for (uint32_t u = 0; u < nu; u += LD) {
+#pragma unroll
+        for (int r = 0; r < LD; ++r) {
+            if (u + r < nu) {
+                mul_u(r, u + r);
+                if (u + r + LD < nu) load_u(r, u + r + LD);
+            }
         }
     }
     am_wave(bv, bi);
