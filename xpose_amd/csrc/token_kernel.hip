@@ -940,12 +940,20 @@ __global__ __launch_bounds__(kTkThreads) void token_kernel(TokArgs a) {
         // head of q, and a combine tile reads a head's few chunk records.
         constexpr uint32_t kHK = 64u;                    // keys per head-split chunk
         const bool hsplit = xl_ok && (span + kHK - 1u) / kHK * NH * 8u <= nwg;
-        const uint32_t cw = hsplit ? kHK : (xl_ok && (span + 15u) / 16u * 8u <= nwg ? 16u : kTkC);
-        const uint32_t n_att = (span + cw - 1u) / cw;    // chunk records per head
         // Global layers split by head pair when the grid holds a workgroup
         // for every (pair, chunk) beside the QKV tiles: each workgroup scores
-        // and sums its keys for two heads instead of all NH.
-        const bool gsplit = kTkGlobalPairs && glob && NH % 2u == 0u && n_att * (NH / 2u) + Sh::N_QKV <= nwg;
+        // and sums its keys for two heads instead of all NH; 64-key chunks
+        // while those fit (span <= 6656 on 256 CUs), else 128-key chunks
+        // (half the workgroups, half the records a combine tile reads).
+        const bool gpair = kTkGlobalPairs && glob && NH % 2u == 0u;
+        const bool g64 = gpair && (span + 63u) / 64u * (NH / 2u) + Sh::N_QKV <= nwg;
+        const bool g128 = gpair && !g64 && (span + 127u) / 128u * (NH / 2u) + Sh::N_QKV <= nwg;
+        const bool gsplit = g64 || g128;
+        const uint32_t cw = hsplit ? kHK
+                          : g64   ? 64u
+                          : g128  ? 128u
+                                  : (xl_ok && (span + 15u) / 16u * 8u <= nwg ? 16u : kTkC);
+        const uint32_t n_att = (span + cw - 1u) / cw;    // chunk records per head
         const uint32_t n_wga = hsplit ? n_att * NH : gsplit ? n_att * (NH / 2u) : n_att;   // attention workgroups
         const bool xl = xl_ok && n_wga * 8u <= nwg;
         const uint32_t rx = nwg - 1u - wg;
@@ -1172,7 +1180,8 @@ __global__ __launch_bounds__(kTkThreads) void token_kernel(TokArgs a) {
             constexpr uint32_t KQ4 = CW / NKQ;               // keys per quarter
             constexpr uint32_t NCH = 4u / HPW;               // FMA chains per head
             static_assert(HPW == 1u || HPW == 2u, "one head or a head pair");
-            static_assert(TPK == 8u || TPK == 16u, "a key's parts span half a DPP row or one");
+            constexpr uint32_t KPL = (CW + kWave - 1u) / kWave;   // keys per lane (softmax)
+            static_assert(TPK == 4u || TPK == 8u || TPK == 16u, "a key's parts span a quad, half a DPP row or one");
             static_assert(HPW * CW <= sizeof(S.sc) / sizeof(float), "scores of the chunk's heads");
             static_assert(KQ4 % 4u == 0u, "a key quarter's weights are read as float4");
             static_assert(kTkHD == 32u * kTkWaves, "values: 16 dim pairs per wave");
@@ -1249,7 +1258,7 @@ __global__ __launch_bounds__(kTkThreads) void token_kernel(TokArgs a) {
             __syncthreads();
             t_in = tk_now(a);
             // scores: key jk, dims DPT part .. + DPT - 1, summed over the key's
-            // TPK lanes (half a DPP row or one)
+            // TPK lanes (a quad, half a DPP row or one)
             {
                 const uint32_t jj = j0 + jk;
                 const bool valid = jj < span;
@@ -1287,10 +1296,10 @@ __global__ __launch_bounds__(kTkThreads) void token_kernel(TokArgs a) {
                     float d = dd[hh][0];
 #pragma unroll
                     for (uint32_t r = 1; r < NCH; ++r) d += dd[hh][r];
-                    if constexpr (TPK == 8u) {
+                    if constexpr (TPK <= 8u) {
                         d += dpp_f<0xB1, 0xF>(d, 0.0f);    // quad_perm [1,0,3,2]
                         d += dpp_f<0x4E, 0xF>(d, 0.0f);    // quad_perm [2,3,0,1]
-                        d += dpp_f<0x141, 0xF>(d, 0.0f);   // row_half_mirror
+                        if constexpr (TPK == 8u) d += dpp_f<0x141, 0xF>(d, 0.0f);   // row_half_mirror
                     } else {
                         d = row16_sum(d);
                     }
@@ -1298,17 +1307,36 @@ __global__ __launch_bounds__(kTkThreads) void token_kernel(TokArgs a) {
                 }
             }
             __syncthreads();
-            // the chunk's softmax: wave hh takes head hh, one key per lane; the
-            // current key's weight is kept apart (S.pc) and 0 in ps
+            // the chunk's softmax: wave hh takes head hh, keys lane, lane + 64
+            // (KPL per lane); the current key's weight is kept apart (S.pc)
+            // and 0 in ps
             if (wave < HPW) {
-                const float v = lane < CW ? ps[wave * CW + lane] : -INFINITY;
-                const bool in = v != -INFINITY;
-                const float m = wave_max_ord(v);
-                const float e = in ? exp_hw(v - m) : 0.0f;
-                const float l2 = wave_sum(e);
+                float v[KPL], e[KPL];
+                float mv = -INFINITY;
+#pragma unroll
+                for (uint32_t k = 0; k < KPL; ++k) {
+                    const uint32_t idx = k * kWave + lane;
+                    v[k] = idx < CW ? ps[wave * CW + idx] : -INFINITY;
+                    mv = fmaxf(mv, v[k]);
+                }
+                const float m = wave_max_ord(mv);
+                float es = 0.0f;
+#pragma unroll
+                for (uint32_t k = 0; k < KPL; ++k) {
+                    e[k] = v[k] != -INFINITY ? exp_hw(v[k] - m) : 0.0f;
+                    es += e[k];
+                }
+                const float l2 = wave_sum(es);
                 const uint32_t jc = pos - kv0 - j0;   // the current key's index, if < CW
-                const float pcur = jc < CW ? __shfl(e, int(jc), kWave) : 0.0f;
-                if (lane < CW) ps[wave * CW + lane] = lane == jc ? 0.0f : e;
+                float pcur = 0.0f;
+#pragma unroll
+                for (uint32_t k = 0; k < KPL; ++k)
+                    if (jc < CW && jc / kWave == k) pcur = __shfl(e[k], int(jc % kWave), kWave);
+#pragma unroll
+                for (uint32_t k = 0; k < KPL; ++k) {
+                    const uint32_t idx = k * kWave + lane;
+                    if (idx < CW) ps[wave * CW + idx] = idx == jc ? 0.0f : e[k];
+                }
                 if (lane == 0) { S.mh[wave] = m; S.lh[wave] = l2; S.pc[wave] = pcur; }
             }
             __syncthreads();
@@ -1365,9 +1393,14 @@ __global__ __launch_bounds__(kTkThreads) void token_kernel(TokArgs a) {
                 attend_heads(std::integral_constant<uint32_t, 1u>{}, std::integral_constant<uint32_t, kHK>{},
                              s_att % NH, s_att / NH);
         } else if (gsplit) {
-            if (s_att < n_wga)
-                attend_heads(std::integral_constant<uint32_t, 2u>{}, std::integral_constant<uint32_t, kTkC>{},
-                             2u * (s_att % (NH / 2u)), s_att / (NH / 2u));
+            if (s_att < n_wga) {
+                if (g64)
+                    attend_heads(std::integral_constant<uint32_t, 2u>{}, std::integral_constant<uint32_t, 64u>{},
+                                 2u * (s_att % (NH / 2u)), s_att / (NH / 2u));
+                else
+                    attend_heads(std::integral_constant<uint32_t, 2u>{}, std::integral_constant<uint32_t, 128u>{},
+                                 2u * (s_att % (NH / 2u)), s_att / (NH / 2u));
+            }
         } else if (s_att < n_att) {
             if (cw == 16u) attend(std::integral_constant<uint32_t, 16u>{});
             else attend(std::integral_constant<uint32_t, kTkC>{});
