@@ -541,24 +541,65 @@ XP_DOT8_BC(7)
 XP_DOT8_BC(8)
 XP_DOT8_BC(9)
 #undef XP_DOT8_BC
-template <int P>
-__device__ __forceinline__ int32_t plane_dot_bc(u32x4 w, u32x2 a, int32_t acc) {
-    acc = dot8_bc<2 * P>(acc, a.x, w.x);       // word 4 P     (lane 2 P, first)
-    acc = dot8_bc<2 * P>(acc, a.y, w.y);       // word 4 P + 1 (lane 2 P, second)
-    acc = dot8_bc<2 * P + 1>(acc, a.x, w.z);   // word 4 P + 2
-    return dot8_bc<2 * P + 1>(acc, a.y, w.w);  // word 4 P + 3
+// Word C of plane P (word 4 P + C: lane 2 P + C / 2 of the row, component C % 2).
+template <int P, int C>
+__device__ __forceinline__ int32_t wdot_bc(int32_t acc, u32x4 w, u32x2 a) {
+    static_assert(P >= 0 && P < kQxPlanes && C >= 0 && C < 4, "plane word");
+    const uint32_t wv = C == 0 ? w.x : C == 1 ? w.y : C == 2 ? w.z : w.w;
+    return dot8_bc<2 * P + C / 2>(acc, C % 2 ? a.y : a.x, wv);
 }
-// planes P, P - 2, ... by Horner's rule (x 256 a step)
-template <int P>
-__device__ __forceinline__ int32_t chain_bc(u32x4 w, u32x2 a, int32_t acc) {
-    acc = plane_dot_bc<P>(w, a, acc);
-    if constexpr (P >= 2) return chain_bc<P - 2>(w, a, acc * 256);
-    else return acc;
-}
-// sum_k w_k q_k over one block for two's-complement nibbles w (block_dot_signed)
-__device__ __forceinline__ int32_t block_dot_bc(u32x4 w, u32x2 a) {
-    constexpr int PE = (kQxPlanes - 1) & ~1, PO = (kQxPlanes - 2) | 1;   // top even / odd plane
-    return chain_bc<PE>(w, a, 0) + chain_bc<PO>(w, a, 0) * 16;
+// sum_k w_k q_k = sum_p 16^p D_p (D_p the dot with digit plane p) for
+// two's-complement nibbles w, over NB = 1 or 2 blocks at once, in three
+// chains a block: X = D_{P-1} 2^12 + D_{P-4}, Y = D_{P-2} 2^12 + D_{P-5}
+// (absent when P = 4), Z = D_{P-3}, combined as 16^(P-4) X + ... below.
+// The chains of both blocks are interleaved word by word, so consecutive
+// dots of one chain are at least four instructions apart: no wait states
+// for the compiler to insert (it keeps two between a VALU write and any
+// operand of a following DPP operation in inline assembly). |D_p| <= 2^11.
+template <int NB>
+__device__ __forceinline__ void block_dot_bc(const u32x4 (&w)[NB], const u32x2 (&a)[NB], int32_t (&out)[NB]) {
+    static_assert(kQxPlanes == 5 || kQxPlanes == 4, "4 or 5 digit planes");
+    constexpr int P = kQxPlanes;
+    int32_t X[NB], Y[NB], Z[NB];
+#pragma unroll
+    for (int b = 0; b < NB; ++b) X[b] = Y[b] = Z[b] = 0;
+    // round 1: planes P - 1, P - 2, P - 3
+    auto round1 = [&](auto cc) {
+        constexpr int C = decltype(cc)::value;
+#pragma unroll
+        for (int b = 0; b < NB; ++b) {
+            X[b] = wdot_bc<P - 1, C>(X[b], w[b], a[b]);
+            Y[b] = wdot_bc<P - 2, C>(Y[b], w[b], a[b]);
+            Z[b] = wdot_bc<P - 3, C>(Z[b], w[b], a[b]);
+        }
+    };
+    round1(std::integral_constant<int, 0>{});
+    round1(std::integral_constant<int, 1>{});
+    round1(std::integral_constant<int, 2>{});
+    round1(std::integral_constant<int, 3>{});
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+        X[b] <<= 12;
+        if constexpr (P == 5) Y[b] <<= 12;
+    }
+    // round 2: plane P - 4 onto X, plane P - 5 (P = 5) onto Y
+    auto round2 = [&](auto cc) {
+        constexpr int C = decltype(cc)::value;
+#pragma unroll
+        for (int b = 0; b < NB; ++b) {
+            X[b] = wdot_bc<P - 4, C>(X[b], w[b], a[b]);
+            if constexpr (P == 5) Y[b] = wdot_bc<0, C>(Y[b], w[b], a[b]);
+        }
+    };
+    round2(std::integral_constant<int, 0>{});
+    round2(std::integral_constant<int, 1>{});
+    round2(std::integral_constant<int, 2>{});
+    round2(std::integral_constant<int, 3>{});
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+        if constexpr (P == 5) out[b] = (X[b] << 4) + Y[b] + (Z[b] << 8);   // 16 X + Y + 256 Z
+        else out[b] = X[b] + (Y[b] << 8) + (Z[b] << 4);                  // X + 256 Y + 16 Z
+    }
 }
 
 // Dot of the wave's blocks with the staged planes (S.qx[0] = block b0) for a
@@ -591,8 +632,22 @@ __device__ __forceinline__ float tile_dot(const TkW<R>& p, TkSmem& Sm, uint32_t 
     for (int r = 0; r < R; ++r) asm volatile("s_nop 4" : "+v"(aw[r].x), "+v"(aw[r].y));
     float acc = 0.0f;
 #pragma unroll
-    for (int r = 0; r < R; ++r)
-        acc = fmaf(__uint_as_float(p.s[r].x) * sxv[r], float(block_dot_bc(p.w[r], aw[r])), acc);
+    for (int r = 0; r < R; r += 2) {
+        if (r + 1 < R) {
+            const u32x4 w2[2] = {p.w[r], p.w[r + 1]};
+            const u32x2 a2[2] = {aw[r], aw[r + 1]};
+            int32_t d[2];
+            block_dot_bc<2>(w2, a2, d);
+            acc = fmaf(__uint_as_float(p.s[r].x) * sxv[r], float(d[0]), acc);
+            acc = fmaf(__uint_as_float(p.s[r + 1].x) * sxv[r + 1], float(d[1]), acc);
+        } else {
+            const u32x4 w1[1] = {p.w[r]};
+            const u32x2 a1[1] = {aw[r]};
+            int32_t d[1];
+            block_dot_bc<1>(w1, a1, d);
+            acc = fmaf(__uint_as_float(p.s[r].x) * sxv[r], float(d[0]), acc);
+        }
+    }
     Sm.red[wave][lane] = acc;
     __syncthreads();
     float y = 0.0f;
@@ -1713,9 +1768,13 @@ __global__ __launch_bounds__(kTkThreads) void token_kernel(TokArgs a) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) asm volatile("s_nop 4" : "+v"(aw[i].x), "+v"(aw[i].y));
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const float f = tk_scale<FMT>(s3[r], i) * sxv[i];
-            acc = fmaf(f, float(block_dot_bc(w3[r][i] ^ 0x88888888u, aw[i])), acc);
+        for (int i = 0; i < 4; i += 2) {
+            const u32x4 w2[2] = {w3[r][i] ^ 0x88888888u, w3[r][i + 1] ^ 0x88888888u};
+            const u32x2 a2[2] = {aw[i], aw[i + 1]};
+            int32_t d[2];
+            block_dot_bc<2>(w2, a2, d);
+            acc = fmaf(tk_scale<FMT>(s3[r], i) * sxv[i], float(d[0]), acc);
+            acc = fmaf(tk_scale<FMT>(s3[r], i + 1) * sxv[i + 1], float(d[1]), acc);
         }
         if (q == nqh - 1u) {
             const uint32_t j = (gw + (u / nqh) * nw) * kGrp + lane;
