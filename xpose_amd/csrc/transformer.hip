@@ -612,7 +612,14 @@ uint32_t attn_splits(uint32_t max_span, uint32_t batch, uint32_t kv_heads) {
     const uint32_t units = (batch ? batch : 1) * (kv_heads ? kv_heads : 1);
     uint32_t n = (256 + units - 1) / units;
     const uint32_t by_len = (max_span + 2 * kAttnMaxPass - 1) / (2 * kAttnMaxPass);
-    if (n < by_len) n = by_len;
+    // Where a few more splits than kAttnFan would be needed for two passes
+    // each but the CUs are shared out in kAttnFan or fewer, splits of up to
+    // three passes keep one combine level and one workgroup a CU (config 5's
+    // global layers: 16 sequences x 16 splits instead of x 17).
+    const bool three = n <= uint32_t(kAttnFan) && by_len > n &&
+                       (max_span + 3 * kAttnMaxPass - 1) / (3 * kAttnMaxPass) <= uint32_t(kAttnFan);
+    if (three) n = kAttnFan;
+    else if (n < by_len) n = by_len;
     const uint32_t most = (max_span + kAttnMinChunk - 1) / kAttnMinChunk;
     if (n > most) n = most;
     if (n > uint32_t(kAttnMaxSplit)) n = kAttnMaxSplit;
