@@ -142,7 +142,7 @@ __global__ __launch_bounds__(kPrepThreads) void bprep_kernel(BprepArgs a) {
             float ss = 0.0f;
 #pragma unroll
             for (int e = 0; e < 8; ++e) ss = fmaf(yv[e], yv[e], ss);
-            const float post = 1.0f / sqrtf(bsum(ss, 0) / float(K) + a.eps);
+            const float post = rsq_hw(bsum(ss, 0) / float(K) + a.eps);
             if (own) {
 #pragma unroll
                 for (int e = 0; e < 8; ++e) xv[e] = xv[e] + yv[e] * post * (1.0f + wpost[e]);
@@ -154,7 +154,7 @@ __global__ __launch_bounds__(kPrepThreads) void bprep_kernel(BprepArgs a) {
         float sx = 0.0f;
 #pragma unroll
         for (int e = 0; e < 8; ++e) sx = fmaf(xv[e], xv[e], sx);
-        const float pre = 1.0f / sqrtf(bsum(sx, 1) / float(K) + a.eps);
+        const float pre = rsq_hw(bsum(sx, 1) / float(K) + a.eps);
         if (own) {
 #pragma unroll
             for (int e = 0; e < 8; ++e) v[e] = xv[e] * pre * (1.0f + wpre[e]);
@@ -165,7 +165,7 @@ __global__ __launch_bounds__(kPrepThreads) void bprep_kernel(BprepArgs a) {
             float uv[8];
             ld8f(uv, u + 8 * p);
 #pragma unroll
-            for (int e = 0; e < 8; ++e) v[e] = gelu_tanh(v[e]) * uv[e];
+            for (int e = 0; e < 8; ++e) v[e] = gelu_hw(v[e]) * uv[e];
         }
     }
     if (!own) return;
@@ -323,7 +323,7 @@ __global__ __launch_bounds__(kBmmThreads) void bmm_int4_kernel(BmmArgs a) {
                 const float u[8] = {cur.raw[2].x, cur.raw[2].y, cur.raw[2].z, cur.raw[2].w,
                                     cur.raw[3].x, cur.raw[3].y, cur.raw[3].z, cur.raw[3].w};
 #pragma unroll
-                for (int e = 0; e < 8; ++e) v[e] = gelu_tanh(v[e]) * u[e];
+                for (int e = 0; e < 8; ++e) v[e] = gelu_hw(v[e]) * u[e];
             }
             stage_regs(cur.hi, cur.lo, cur.as, v, wsel);
         }
@@ -361,7 +361,7 @@ __global__ __launch_bounds__(kBmmThreads) void bmm_int4_kernel(BmmArgs a) {
             gs += red[w][og];
             us += red[w][og + 8u];
         }
-        const float h = row < a.rows ? gelu_tanh(gs) * us : 0.0f;
+        const float h = row < a.rows ? gelu_hw(gs) * us : 0.0f;
         __syncthreads();
         hb[row * 32u + j] = h;
         __syncthreads();

@@ -135,7 +135,7 @@ __global__ void rmsnorm_rows_apply_gemma_kernel(float* out, const float* in, con
     for (size_t i = size_t(blockIdx.x) * blockDim.x + threadIdx.x; i < total;
          i += size_t(gridDim.x) * blockDim.x) {
         const size_t r = i / n;
-        const float scale = 1.0f / sqrtf(rowss[r] / float(n) + eps);
+        const float scale = rsq_hw(rowss[r] / float(n) + eps);
         out[i] = in[i] * scale * (1.0f + w[i - r * n]);
     }
 }
@@ -149,7 +149,7 @@ __global__ __launch_bounds__(kPfThreads) void rmsnorm_heads_rows_gemma_kernel(
     const float* row = in + size_t(r) * head_dim;
     float ss = 0.0f;
     for (uint32_t j = lane; j < head_dim; j += kWave) ss = fmaf(row[j], row[j], ss);
-    const float scale = 1.0f / sqrtf(wave_sum(ss) / float(head_dim) + eps);
+    const float scale = rsq_hw(wave_sum(ss) / float(head_dim) + eps);
     for (uint32_t j = lane; j < head_dim; j += kWave) out[size_t(r) * head_dim + j] = row[j] * scale * (1.0f + w[j]);
 }
 

@@ -70,7 +70,7 @@ __global__ __launch_bounds__(1024) void norm_res_norm_kernel(float* x, const flo
         float ss = 0.0f;
         for (uint32_t i = threadIdx.x; i < n; i += blockDim.x) ss += y[i] * y[i];
         ss = blk_sum(ss, red);
-        const float scale = 1.0f / sqrtf(ss / float(n) + eps);
+        const float scale = rsq_hw(ss / float(n) + eps);
         for (uint32_t i = threadIdx.x; i < n; i += blockDim.x, ++c) {
             const float v = x[i] + y[i] * scale * (1.0f + w_post[i]);
             x[i] = v;
@@ -82,7 +82,7 @@ __global__ __launch_bounds__(1024) void norm_res_norm_kernel(float* x, const flo
     float ss = 0.0f;
     for (int j = 0; j < c; ++j) ss += xv[j] * xv[j];
     ss = blk_sum(ss, red);
-    const float scale = 1.0f / sqrtf(ss / float(n) + eps);
+    const float scale = rsq_hw(ss / float(n) + eps);
     c = 0;
     for (uint32_t i = threadIdx.x; i < n; i += blockDim.x, ++c)
         out[i] = xv[c] * scale * (1.0f + w_pre[i]);

@@ -286,25 +286,10 @@ __device__ __forceinline__ unsigned long long tk_now(const TokArgs& a) {
     return a.trace ? __builtin_amdgcn_s_memrealtime() : 0ull;
 }
 
-// The hardware reciprocal and reciprocal square root (v_rcp_f32, v_rsq_f32:
-// about 1 ulp) in place of the correctly rounded division and square root,
-// which cost some thirty dependent instructions on a stage's critical path.
-// The quantiser's r = range * rcp(m) keeps |q| <= 2^18 + 1, inside the
-// digit planes' range.
-__device__ __forceinline__ float rcp_hw(float v) { return __builtin_amdgcn_rcpf(v); }
-__device__ __forceinline__ float rsq_hw(float v) { return __builtin_amdgcn_rsqf(v); }
-// e^v as 2^(v log2 e) on v_exp_f32: relative error ~1e-6 for |v| <= 20 (the
-// rounding of the product), against ~15 dependent instructions for expf.
-// Used where v <= 0 (softmax weights, rescale factors) or |v| <= 20 (GeGLU).
-__device__ __forceinline__ float exp_hw(float v) { return __builtin_amdgcn_exp2f(v * 1.4426950408889634f); }
-// GeGLU's tanh-approximated GELU (the form of gelu_tanh) on exp_hw.
-__device__ __forceinline__ float gelu_hw(float g) {
-    float z = 0.7978845608028654f * (g + 0.044715f * g * g * g);
-    z = fminf(fmaxf(z, -10.0f), 10.0f);
-    const float e = exp_hw(-2.0f * z);
-    const float t = (1.0f - e) * rcp_hw(1.0f + e);
-    return 0.5f * g * (1.0f + t);
-}
+// rcp_hw / rsq_hw / exp_hw (xp_device.hpp) replace the correctly rounded
+// division, square root and expf, some 15-30 dependent instructions each on
+// a stage's critical path. The quantiser's r = range * rcp(m) keeps
+// |q| <= 2^18 + 1, inside the digit planes' range.
 
 // Wave maximum of floats through order-preserving int32 keys (a float's bits,
 // the magnitude bits flipped when negative): v_max_i32 takes its DPP operand

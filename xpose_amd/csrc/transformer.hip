@@ -40,7 +40,7 @@ __global__ __launch_bounds__(1024) void rmsnorm_gemma_kernel(float* out, const f
     float ss = 0.0f;
     for (uint32_t k = threadIdx.x; k < n; k += blockDim.x) ss += in[k] * in[k];
     ss = block_sum(ss, red);
-    const float scale = 1.0f / sqrtf(ss / float(n) + eps);
+    const float scale = rsq_hw(ss / float(n) + eps);
     for (uint32_t i = threadIdx.x; i < n; i += blockDim.x) out[i] = in[i] * scale * (1.0f + w[i]);
 }
 
@@ -53,7 +53,7 @@ __global__ __launch_bounds__(256) void rmsnorm_heads_kernel(float* out, const fl
     float ss = 0.0f;
     for (uint32_t k = threadIdx.x; k < head_dim; k += blockDim.x) ss += x[k] * x[k];
     ss = block_sum(ss, red);
-    const float scale = 1.0f / sqrtf(ss / float(head_dim) + eps);
+    const float scale = rsq_hw(ss / float(head_dim) + eps);
     for (uint32_t d = threadIdx.x; d < head_dim; d += blockDim.x)
         out[size_t(blockIdx.x) * head_dim + d] = x[d] * scale * (1.0f + w[d]);
 }
@@ -105,7 +105,7 @@ __global__ __launch_bounds__(256) void qk_norm_rope_append_kernel(QkArgs a, Rope
     const uint32_t d = threadIdx.x;   // pair index, blockDim.x == half
     float lo = x[d], hi = x[d + half];
     const float ss = block_sum(lo * lo + hi * hi, red);
-    const float scale = 1.0f / sqrtf(ss / float(a.head_dim) + a.eps);
+    const float scale = rsq_hw(ss / float(a.head_dim) + a.eps);
     lo = lo * scale * (1.0f + w[d]);
     hi = hi * scale * (1.0f + w[d + half]);
     rope_pair(lo, hi, f.inv[d], pos);
@@ -245,7 +245,7 @@ __device__ __forceinline__ void attn_combine(const float* recs, uint32_t n, bool
         const float l = live ? ld_dev(recs + size_t(lane) * REC + kAttnMaxG + hh) : 0.0f;
         const float mm = l > 0.0f ? m : -INFINITY;
         const float M = wave_max(mm);
-        const float f = mm == -INFINITY ? 0.0f : expf(mm - M);
+        const float f = mm == -INFINITY ? 0.0f : exp_hw(mm - M);
         const float L = wave_sum(l * f);
         if (live) fs[lane][hh] = f;
         if (lane == 0) {
@@ -276,7 +276,7 @@ __device__ __forceinline__ void attn_combine(const float* recs, uint32_t n, bool
         }
         const int hh = tid * 4 / HD;
         if (final) {
-            const float inv = 1.0f / run[1][hh];
+            const float inv = rcp_hw(run[1][hh]);
             reinterpret_cast<float4*>(out)[tid] = float4{t.x * inv, t.y * inv, t.z * inv, t.w * inv};
         } else {
             float* o = rec_out + kAttnStat + tid * 4;
@@ -374,7 +374,7 @@ __global__ __launch_bounds__(kAttnThreads) void attention_decode_kernel(AttnArgs
         __syncthreads();
         if (wave <= G) {
             const float ss = wave_sum(e[0] * e[0] + e[1] * e[1] + e[2] * e[2] + e[3] * e[3]);
-            const float scale = 1.0f / sqrtf(ss / float(HD) + a.eps);
+            const float scale = rsq_hw(ss * (1.0f / float(HD)) + a.eps);
 #pragma unroll
             for (int c = 0; c < 4; ++c) e[c] = e[c] * scale * (1.0f + w4[c]);
 #pragma unroll
@@ -479,13 +479,13 @@ __global__ __launch_bounds__(kAttnThreads) void attention_decode_kernel(AttnArgs
 #pragma unroll
             for (int i = 0; i < PV; ++i) {
                 const int idx = lane + kWave * i;
-                const float p = idx < PASS ? expf(sp[i] - mnew) : 0.0f;
+                const float p = idx < PASS ? exp_hw(sp[i] - mnew) : 0.0f;
                 if (idx < PASS) ps[h][idx] = p;
                 sum += p;
             }
             sum = wave_sum(sum);
             if (lane == 0) {
-                const float alpha = expf(mold - mnew);   // 0 on the first pass
+                const float alpha = exp_hw(mold - mnew);   // 0 on the first pass
                 run[0][h] = mnew;
                 run[1][h] = run[1][h] * alpha + sum;
                 run[2][h] = alpha;

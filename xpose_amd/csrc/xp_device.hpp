@@ -240,11 +240,29 @@ __device__ __forceinline__ void am_wave(float& bv, uint32_t& bi) {
 // (kernels/llm_transformer.cl:213-231). expf is the device libm exp; the
 // quotient uses the hardware reciprocal (1 ulp), not a correctly rounded
 // division.
+// The hardware reciprocal and reciprocal square root (v_rcp_f32, v_rsq_f32:
+// about 1 ulp) and e^v as 2^(v log2 e) on v_exp_f32 (relative error ~1e-6
+// for |v| <= 20, from the rounding of the product), for the latency-bound
+// kernels: each replaces a correctly rounded sequence of 15-30 dependent
+// instructions. exp_hw is used where v <= 0 (softmax weights, rescale
+// factors) or |v| <= 20 (GeGLU).
+__device__ __forceinline__ float rcp_hw(float v) { return __builtin_amdgcn_rcpf(v); }
+__device__ __forceinline__ float rsq_hw(float v) { return __builtin_amdgcn_rsqf(v); }
+__device__ __forceinline__ float exp_hw(float v) { return __builtin_amdgcn_exp2f(v * 1.4426950408889634f); }
+
 __device__ __forceinline__ float gelu_tanh(float g) {
     float z = 0.7978845608028654f * (g + 0.044715f * g * g * g);
     z = fminf(fmaxf(z, -10.0f), 10.0f);
     const float e = expf(-2.0f * z);
     const float t = (1.0f - e) * __builtin_amdgcn_rcpf(1.0f + e);
+    return 0.5f * g * (1.0f + t);
+}
+// The same GELU on exp_hw / rcp_hw (the decode kernels' critical paths).
+__device__ __forceinline__ float gelu_hw(float g) {
+    float z = 0.7978845608028654f * (g + 0.044715f * g * g * g);
+    z = fminf(fmaxf(z, -10.0f), 10.0f);
+    const float e = exp_hw(-2.0f * z);
+    const float t = (1.0f - e) * rcp_hw(1.0f + e);
     return 0.5f * g * (1.0f + t);
 }
 
