@@ -276,6 +276,26 @@ def test_gpu_attention(xp, xo, seq, kv0):
 
 
 @pytest.mark.gpu
+def test_gpu_attention_ticket_levels():
+    """Spans of more than 16 splits combine through the exchange mode when
+    every workgroup fits a CU at once (the cases above); the two-level ticket
+    chain they otherwise take is checked here, the same cases in a child
+    process with the exchange mode off (XP_ATTN_EXCHANGE=0)."""
+    import os
+    import subprocess
+    import sys
+    print("case attention ticket levels", flush=True)
+    env = dict(os.environ, XP_ATTN_EXCHANGE="0")
+    here = os.path.dirname(os.path.abspath(__file__))
+    r = subprocess.run([sys.executable, "-m", "pytest", os.path.join(here, "test_transformer.py"), "-q",
+                        "-m", "gpu", "-p", "no:cacheprovider",
+                        "-k", "test_gpu_attention and (1100 or 2047 or 4097 or 8192)"],
+                       env=env, capture_output=True, text=True, timeout=240)
+    assert r.returncode == 0, r.stdout[-2000:] + r.stderr[-2000:]
+    assert "5 passed" in r.stdout, r.stdout[-2000:]
+
+
+@pytest.mark.gpu
 def test_gpu_attention_block_chain(xp, xo):
     """norm -> rope -> attention chained on the device against the oracle's
     chain (kernel_tests.cpp:713-799)."""

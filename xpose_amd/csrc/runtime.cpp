@@ -94,6 +94,31 @@ bool ensure_tickets(DeviceScratch* s, size_t n) {
     return true;
 }
 
+bool ensure_attn_x(DeviceScratch* s, size_t floats, size_t words) {
+    if (s->attn_x_floats >= floats && s->attn_state_words >= words) return true;
+    if (s->attn_x || s->attn_state) {
+        if (hipDeviceSynchronize() != hipSuccess || hipFree(s->attn_x) != hipSuccess ||
+            hipFree(s->attn_state) != hipSuccess) {
+            set_error(XP_E_HIP, "scratch: could not release attention exchange buffers");
+            return false;
+        }
+        s->attn_x = nullptr;
+        s->attn_state = nullptr;
+        s->attn_x_floats = s->attn_state_words = 0;
+    }
+    if (hipMalloc(&s->attn_x, floats * sizeof(float)) != hipSuccess ||
+        hipMalloc(&s->attn_state, words * sizeof(uint32_t)) != hipSuccess ||
+        hipMemset(s->attn_x, 0, floats * sizeof(float)) != hipSuccess ||
+        hipMemset(s->attn_state, 0, words * sizeof(uint32_t)) != hipSuccess ||
+        hipDeviceSynchronize() != hipSuccess) {
+        set_error(XP_E_NOMEM, "scratch: attention exchange buffers (%zu floats) failed", floats);
+        return false;
+    }
+    s->attn_x_floats = floats;
+    s->attn_state_words = words;
+    return true;
+}
+
 }  // namespace xp
 
 using namespace xp;

@@ -45,7 +45,7 @@ constexpr int kNMat = 7;
 constexpr int kNNorm = 6;
 constexpr size_t kAlign = 256;
 // Ticket regions: matvec split-k, decode attention (kAttnTicketsPerHead per
-// kv head, at most 60 kv heads), argmax.
+// kv head, at most 53 kv heads), argmax.
 constexpr uint32_t kTicketMv = 0, kTicketAttn = 8192, kTicketAm = 8192 + 1024, kTickets = 8192 + 1088;
 constexpr uint32_t kMaxKvHeads = (kTicketAm - kTicketAttn) / kAttnTicketsPerHead;
 

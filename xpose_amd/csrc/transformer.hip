@@ -12,6 +12,7 @@
 #include "xp_launch.hpp"
 
 #include <cmath>
+#include <cstdlib>
 
 namespace xp {
 
@@ -167,7 +168,18 @@ constexpr int kAttnStat     = 8;                          // floats of (max[4], 
 __host__ __device__ constexpr uint32_t attn_record(uint32_t G) { return kAttnStat + G * kAttnHD; }
 // Records per (sequence, kv head): the splits', then the level-1 groups'.
 constexpr uint32_t kAttnRecords = kAttnMaxSplit + kAttnGroups;
-static_assert(kAttnTicketsPerHead == 1 + kAttnGroups, "tickets: level 2, then one per group");
+// Exchange-mode record: G pairs (max, sum of exp) then G * HD / 2 pairs of
+// value dims, each pair a 16-byte (v0, tag, v1, tag) slot.
+__host__ __device__ constexpr uint32_t attn_xrecord(uint32_t G) { return 4u * (G + G * kAttnHD / 2u); }
+// Floats of one (sequence, kv head)'s records in either mode.
+__host__ __device__ constexpr uint32_t attn_head_floats(uint32_t G) {
+    return kAttnRecords * attn_record(G) > kAttnMaxSplit * attn_xrecord(G) ? kAttnRecords * attn_record(G)
+                                                                          : kAttnMaxSplit * attn_xrecord(G);
+}
+constexpr uint32_t kAttnEpoch = 1 + kAttnGroups;   // ticket word: the last exchange launch's tag
+constexpr uint32_t kAttnXErr  = 2 + kAttnGroups;   // ticket word: set when an exchange wait timed out
+constexpr uint32_t kAttnSpinLimit = 1u << 22;       // exchange poll rounds before giving up
+static_assert(kAttnTicketsPerHead == 3 + kAttnGroups, "tickets: level 2, one per group, epoch, flag");
 
 template <int M>
 __device__ __forceinline__ float swz_xor(float x) {   // x of lane ^ M within 32 lanes
@@ -312,6 +324,13 @@ __global__ __launch_bounds__(kAttnThreads) void attention_decode_kernel(AttnArgs
     uint32_t span, kv0;
     attn_range(a, span, kv0);
     const uint32_t g = blockIdx.y, s = blockIdx.x;
+    // exchange mode: this launch's record tag, one past the last launch's
+    // (read before this workgroup's record is written; see the combine)
+    uint32_t xtag = 0u;
+    if (a.xchg) {
+        const uint32_t ep = ld_dev(a.tickets + size_t(g) * kAttnTicketsPerHead + kAttnEpoch);
+        xtag = ep + 1u != 0u ? ep + 1u : 1u;
+    }
     uint32_t chunk = (span + a.nsplit - 1) / a.nsplit;
     if (chunk < uint32_t(kAttnMinChunk)) chunk = kAttnMinChunk;
     const uint32_t j0 = min(s * chunk, span);
@@ -537,8 +556,134 @@ __global__ __launch_bounds__(kAttnThreads) void attention_decode_kernel(AttnArgs
         }
         return;
     }
-    float* part = a.part + size_t(g) * kAttnRecords * REC;
     uint32_t* tk = a.tickets + size_t(g) * kAttnTicketsPerHead;   // [0] level 2, [1 + grp] level 1
+    if (a.xchg) {
+        // ---- exchange mode (every workgroup of the launch resident at once):
+        // each split publishes its record as tagged pairs, then polls the
+        // statistics of all records and its own slice of the value dims, and
+        // writes that slice of the output — one exchange instead of the
+        // ticket chain. Split 0, once it has seen every record (so every
+        // split has read the epoch), stores this launch's tag as the epoch.
+        constexpr uint32_t NPR = G + G * HD / 2;                 // pairs per record
+        const uint32_t ns = a.nsplit;
+        float* xbase = a.part + size_t(g) * attn_head_floats(G);
+        const rsrc_t xr = make_rsrc(xbase, ns * NPR * 16u);
+        for (uint32_t i = tid; i < uint32_t(G * HD / 2); i += kAttnThreads) {
+            float v0 = 0.0f, v1 = 0.0f;
+#pragma unroll
+            for (int w = 0; w < kAttnThreads / kWave; ++w) {
+                v0 += red[w][2u * i];
+                v1 += red[w][2u * i + 1u];
+            }
+            __builtin_amdgcn_raw_buffer_store_b128(u32x4{__float_as_uint(v0), xtag, __float_as_uint(v1), xtag},
+                                                   xr, int((s * NPR + G + i) * 16u), 0, kAuxDev);
+        }
+        if (tid < G)
+            __builtin_amdgcn_raw_buffer_store_b128(
+                u32x4{__float_as_uint(run[0][tid]), xtag, __float_as_uint(run[1][tid]), xtag}, xr,
+                int((s * NPR + tid) * 16u), 0, kAuxDev);
+        constexpr uint32_t NOUT = G * HD;
+        const uint32_t D = (((NOUT + ns - 1u) / ns) + 1u) & ~1u;   // output dims a split (even)
+        const uint32_t d0 = s * D, d1 = min(d0 + D, NOUT);
+        if (d0 >= d1) return;
+        const uint32_t DD = d1 - d0, HP = DD / 2u;
+        const uint32_t nst = ns * G, np = nst + ns * HP;           // pairs to poll (<= 4 a thread)
+        __syncthreads();   // every record sum has been read from red
+        float* xm = &red[0][0];                          // [split][head] max, then the factor
+        float* xl = xm + kAttnMaxSplit * G;              // [split][head] sum of exp
+        float* xv = xl + kAttnMaxSplit * G;              // [split][DD] value dims
+        float* xp = xv + kAttnMaxSplit * G + 512;        // [group][DD] partial sums
+        static_assert(3 * kAttnMaxSplit * G + 1024 <= (kAttnThreads / kWave) * G * HD, "exchange scratch");
+        uint32_t off[4];
+        bool act[4];
+        u32x4 v[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const uint32_t i = tid + uint32_t(k) * kAttnThreads;
+            act[k] = i < np;
+            const uint32_t ic = act[k] ? i : 0u;
+            if (ic < nst) {
+                off[k] = ((ic / G) * NPR + ic % G) * 16u;
+            } else {
+                const uint32_t j = ic - nst;
+                off[k] = ((j / HP) * NPR + G + d0 / 2u + j % HP) * 16u;
+            }
+        }
+        const u32x4 ready = {0u, xtag, 0u, xtag};
+#pragma unroll
+        for (int k = 0; k < 4; ++k) v[k] = act[k] ? ld_dev16(xr, off[k]) : ready;
+        for (uint32_t spins = 0;; ++spins) {
+            bool ok = true;
+#pragma unroll
+            for (int k = 0; k < 4; ++k) ok &= (v[k].y == xtag) & (v[k].w == xtag);
+            if (ok) break;
+            if (spins > kAttnSpinLimit) {
+                st_dev(tk + kAttnXErr, 1u);
+                break;
+            }
+            asm volatile("" ::: "memory");
+#pragma unroll
+            for (int k = 0; k < 4; ++k) v[k] = act[k] ? ld_dev16(xr, off[k]) : ready;
+        }
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const uint32_t i = tid + uint32_t(k) * kAttnThreads;
+            if (!act[k]) continue;
+            if (i < nst) {
+                xm[i] = __uint_as_float(v[k].x);
+                xl[i] = __uint_as_float(v[k].z);
+            } else {
+                const uint32_t j = i - nst, r = j / HP, c = j % HP;
+                xv[r * DD + 2u * c] = __uint_as_float(v[k].x);
+                xv[r * DD + 2u * c + 1u] = __uint_as_float(v[k].z);
+            }
+        }
+        __syncthreads();
+        if (s == 0 && tid == 0) st_dev(tk + kAttnEpoch, xtag);
+        // wave h: head h's rescale factors exp(m_r - M) (0 for an empty
+        // split) into xm and the denominator into run[1]
+        if (wave < G) {
+            const int h = wave;
+            float m4[kAttnMaxSplit / kWave], l4[kAttnMaxSplit / kWave];
+            float mx = -INFINITY;
+#pragma unroll
+            for (int k = 0; k < kAttnMaxSplit / kWave; ++k) {
+                const uint32_t r = uint32_t(lane + kWave * k);
+                const bool in = r < ns;
+                l4[k] = in ? xl[r * G + h] : 0.0f;
+                m4[k] = in && l4[k] > 0.0f ? xm[r * G + h] : -INFINITY;
+                mx = fmaxf(mx, m4[k]);
+            }
+            const float M = wave_max(mx);
+            float ls = 0.0f;
+#pragma unroll
+            for (int k = 0; k < kAttnMaxSplit / kWave; ++k) {
+                const uint32_t r = uint32_t(lane + kWave * k);
+                const float f = m4[k] == -INFINITY ? 0.0f : exp_hw(m4[k] - M);
+                ls = fmaf(l4[k], f, ls);
+                if (r < ns) xm[r * G + h] = f;
+            }
+            ls = wave_sum(ls);
+            if (lane == 0) run[1][h] = ls;
+        }
+        __syncthreads();
+        // dim j of the slice: group q of Q threads sums records q, q + Q, ...
+        const uint32_t Q = kAttnThreads / DD, j = tid % DD, q = tid / DD;
+        if (q < Q) {
+            const uint32_t h = (d0 + j) / HD;
+            float acc = 0.0f;
+            for (uint32_t r = q; r < ns; r += Q) acc = fmaf(xm[r * G + h], xv[r * DD + j], acc);
+            xp[q * DD + j] = acc;
+        }
+        __syncthreads();
+        if (uint32_t(tid) < DD) {
+            float acc = 0.0f;
+            for (uint32_t qq = 0; qq < Q; ++qq) acc += xp[qq * DD + tid];
+            out[d0 + tid] = acc * rcp_hw(run[1][(d0 + tid) / HD]);
+        }
+        return;
+    }
+    float* part = a.part + size_t(g) * attn_head_floats(G);
     float* rec = part + size_t(s) * REC;
     for (int i = tid; i < G * HD; i += kAttnThreads) {
         float acc = 0.0f;
@@ -628,7 +773,7 @@ uint32_t attn_splits(uint32_t max_span, uint32_t batch, uint32_t kv_heads) {
 
 size_t attn_partial_floats(uint32_t kv_heads, uint32_t n_heads, uint32_t head_dim) {
     (void)head_dim;
-    return size_t(kv_heads) * kAttnRecords * attn_record(kv_heads ? n_heads / kv_heads : 1);
+    return size_t(kv_heads) * attn_head_floats(kv_heads ? n_heads / kv_heads : 1);
 }
 
 int launch_attention(AttnArgs a, uint32_t max_span, hipStream_t st) {
@@ -646,6 +791,31 @@ int launch_attention(AttnArgs a, uint32_t max_span, hipStream_t st) {
     a.nsplit = attn_splits(max_span, a.batch, a.kv_heads);
     if (a.batch > 1 && a.nsplit > 1 && (!a.part || !a.tickets || a.bpart == 0))
         return set_error(XP_E_ARG, "attention: a batch needs its own partials and tickets");
+    // Exchange mode: more splits than one ticket level combines (the ticket
+    // chain would take two levels) and the launch's workgroups at most one a
+    // CU, so all are resident at once and may wait for each other (bounded).
+    // Measured: one sequence at span 4096 (128 splits) 12.2 -> 10.9 us, 8192
+    // (256) 14.3 -> 13.5 us; 16 sequences x 16 splits (one ticket level)
+    // 1.461 -> 1.472 ms a batched step, so those keep the tickets.
+    // XP_ATTN_EXCHANGE=0 in the environment turns it off.
+    static const bool xchg_on = [] {
+        const char* e = std::getenv("XP_ATTN_EXCHANGE");
+        return !(e && e[0] == '0');
+    }();
+    {
+        DeviceScratch* sc = scratch();
+        if (!sc) return XP_E_HIP;
+        const uint64_t wgs = uint64_t(a.nsplit) * a.kv_heads * a.batch;
+        a.xchg = xchg_on && a.nsplit > uint32_t(kAttnFan) && sc->n_cu > 0 && wgs <= uint64_t(sc->n_cu) ? 1u : 0u;
+        if (a.xchg && (!a.part || !a.tickets)) {
+            // the exchange mode's own zeroed buffers, not the shared scratch
+            if (!ensure_attn_x(sc, attn_partial_floats(a.kv_heads, a.n_heads, a.head_dim),
+                               size_t(a.kv_heads) * kAttnTicketsPerHead))
+                return XP_E_NOMEM;
+            a.part = sc->attn_x;
+            a.tickets = sc->attn_state;
+        }
+    }
     if (a.nsplit > 1 && (!a.part || !a.tickets)) {
         DeviceScratch* sc = scratch();
         if (!sc) return XP_E_HIP;

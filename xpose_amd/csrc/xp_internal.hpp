@@ -28,6 +28,12 @@ struct DeviceScratch {
     size_t    n_tickets    = 0;
     float*    partial      = nullptr;  // split-k / split-span partial sums
     size_t    partial_floats = 0;
+    // Decode attention's exchange mode (its own, zeroed: its records carry
+    // launch tags that no other data may imitate, and its epoch words persist)
+    float*    attn_x       = nullptr;
+    size_t    attn_x_floats = 0;
+    uint32_t* attn_state   = nullptr;
+    size_t    attn_state_words = 0;
 };
 
 // Returns the scratch of the current device, creating it on first use.
@@ -36,6 +42,8 @@ DeviceScratch* scratch();
 // Grows the partial buffer to at least `floats`; returns false on failure.
 bool ensure_partial(DeviceScratch* s, size_t floats);
 bool ensure_tickets(DeviceScratch* s, size_t n);
+// The attention exchange buffers, zeroed when (re)allocated.
+bool ensure_attn_x(DeviceScratch* s, size_t floats, size_t words);
 
 inline hipStream_t as_stream(xp_stream s) { return reinterpret_cast<hipStream_t>(s); }
 

@@ -91,7 +91,7 @@ struct AttnArgs {
     float scale;
     uint32_t nsplit;
     float* part;               // [kv_heads][256 + 16][8 + group * head_dim]
-    uint32_t* tickets;         // [kv_heads][kAttnTicketsPerHead], zero at rest
+    uint32_t* tickets;         // [kv_heads][kAttnTicketsPerHead], zero at rest (epoch words aside)
     // Batched sequences (grid.z = batch): sequence b reads q + b bq, the caches
     // at + b bcache, position pos_dev[b], and writes out + b bq, its own partials
     // (+ b bpart) and tickets (+ b kv_heads kAttnTicketsPerHead).
@@ -114,10 +114,15 @@ struct AttnArgs {
     float eps = 0.0f;
     float theta = 0.0f;          // RoPE base of the layer
     uint32_t bkv = 0;
+    // Set by launch_attention: the splits combine through tagged records
+    // (every workgroup of the launch resident at once) instead of tickets.
+    uint32_t xchg = 0;
 };
 // Arrival tickets per (sequence, kv head) of the decode attention: one for
-// the final combine, one per group of 16 splits (at most 256 splits).
-constexpr uint32_t kAttnTicketsPerHead = 17;
+// the final combine, one per group of 16 splits (at most 256 splits); then
+// the exchange mode's epoch (the last launch's record tag) and its timeout
+// flag.
+constexpr uint32_t kAttnTicketsPerHead = 19;
 // Splits per (sequence, kv head) for a launch over `batch` sequences whose
 // spans are at most max_span; the partials one sequence needs (any span).
 uint32_t attn_splits(uint32_t max_span, uint32_t batch, uint32_t kv_heads);
