@@ -588,6 +588,7 @@ __global__ __launch_bounds__(kAttnThreads) void attention_decode_kernel(AttnArgs
         if (d0 >= d1) return;
         const uint32_t DD = d1 - d0, HP = DD / 2u;
         const uint32_t nst = ns * G, np = nst + ns * HP;           // pairs to poll (<= 4 a thread)
+        if (tid == 0) last = 0u;                                   // set if a wait times out
         __syncthreads();   // every record sum has been read from red
         float* xm = &red[0][0];                          // [split][head] max, then the factor
         float* xl = xm + kAttnMaxSplit * G;              // [split][head] sum of exp
@@ -619,6 +620,7 @@ __global__ __launch_bounds__(kAttnThreads) void attention_decode_kernel(AttnArgs
             if (ok) break;
             if (spins > kAttnSpinLimit) {
                 st_dev(tk + kAttnXErr, 1u);
+                last = 1u;
                 break;
             }
             asm volatile("" ::: "memory");
@@ -679,7 +681,9 @@ __global__ __launch_bounds__(kAttnThreads) void attention_decode_kernel(AttnArgs
         if (uint32_t(tid) < DD) {
             float acc = 0.0f;
             for (uint32_t qq = 0; qq < Q; ++qq) acc += xp[qq * DD + tid];
-            out[d0 + tid] = acc * rcp_hw(run[1][(d0 + tid) / HD]);
+            // a timed-out wait (the launch was not resident at once) leaves
+            // NaN, not a plausible value, besides the flag word
+            out[d0 + tid] = last ? __builtin_nanf("") : acc * rcp_hw(run[1][(d0 + tid) / HD]);
         }
         return;
     }
