@@ -427,6 +427,111 @@ __global__ __launch_bounds__(kBmmThreads) void bmm_int4_kernel(BmmArgs a) {
     if (tid == 0) st_dev(a.tickets + cb, 0u);
 }
 
+// Streamed M = 16 GEMM for wide matrices (the batched lm_head: 4096 column
+// groups of a 1152-long k): a persistent grid of one workgroup per CU takes
+// column groups wg, wg + grid, ...; wave w keeps the staged operand of its
+// k blocks (nblk / 8 or one more) in registers for every group and requests
+// the next group's weights before it multiplies the current ones, so the
+// weight stream never waits on a workgroup's launch or reduction. The eight
+// waves' partial tiles meet in LDS, double buffered (one barrier a group),
+// and are added in wave order as bmm_int4_kernel adds them. The groups
+// alternate between two weight buffers in an unrolled pair so that both keep
+// fixed registers.
+template <int FMT>
+__global__ __launch_bounds__(kBmmThreads) void bmm_stream_kernel(BmmArgs a) {
+    constexpr int MB = int(kBmmMaxPerWave);
+    constexpr uint32_t NO = 1024;                      // 16 rows x 64 columns
+    __shared__ float red[2][kBmmWaves][NO];
+    const uint32_t tid = threadIdx.x, wave = tid / kWave, lane = tid % kWave;
+    const uint32_t col16 = lane % 16u, wsel = lane / 16u;
+    const uint32_t nblk = a.nblk, base = nblk / kBmmWaves, rem = nblk % kBmmWaves;
+    const uint32_t nbw = base + (wave < rem ? 1u : 0u);       // this wave's blocks
+    const uint32_t kb0 = wave * base + min(wave, rem);
+    const u32x4* A = static_cast<const u32x4*>(a.a);
+    u32x4 ahi[MB], alo[MB];
+    float4 as[MB];
+#pragma unroll
+    for (int j = 0; j < MB; ++j) {
+        const uint32_t blk = kb0 + min(uint32_t(j), nbw - 1u);
+        ahi[j] = A[(size_t(blk) * 2 + 0) * 64 + lane];
+        alo[j] = A[(size_t(blk) * 2 + 1) * 64 + lane];
+        as[j] = *reinterpret_cast<const float4*>(a.asum + size_t(blk) * 16 + 4u * wsel);
+    }
+    const uint32_t cols = a.mats[0].cols, ng = cols / kGrp;
+    const uint32_t* wq = static_cast<const uint32_t*>(a.mats[0].wq);
+    const u32x2* sq = static_cast<const u32x2*>(a.mats[0].sc);
+    float* out = a.mats[0].out;
+    struct Wt {
+        uint32_t w[MB][4];
+        u32x2 sc[MB][4];
+    };
+    auto load = [&](Wt& o, uint32_t g) {
+#pragma unroll
+        for (int j = 0; j < MB; ++j) {
+            const uint32_t blk = kb0 + min(uint32_t(j), nbw - 1u);
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                const uint32_t cg = 16u * t + col16;
+                o.w[j][t] = __builtin_nontemporal_load(wq + ((size_t(g) * nblk + blk) * kGrp + cg) * 4 + wsel);
+                o.sc[j][t] = sq[size_t(blk / 4) * cols + g * kGrp + cg];
+            }
+        }
+    };
+    auto group = [&](const Wt& cur, uint32_t g, float (&rd)[kBmmWaves][NO]) {
+        f32x4 acc[4];
+#pragma unroll
+        for (int t = 0; t < 4; ++t) acc[t] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int j = 0; j < MB; ++j) {
+            if (uint32_t(j) >= nbw) break;
+            const uint32_t blk = kb0 + uint32_t(j);
+            const bf16x8 hi = as_bf16x8(ahi[j]), lo = as_bf16x8(alo[j]);
+            const float corr[4] = {136.0f * as[j].x, 136.0f * as[j].y, 136.0f * as[j].z, 136.0f * as[j].w};
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                const bf16x8 bw = as_bf16x8(widen_nibbles(cur.w[j][t]));
+                f32x4 c = {0.0f, 0.0f, 0.0f, 0.0f};
+                c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(hi, bw, c, 0, 0, 0);
+                c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(lo, bw, c, 0, 0, 0);
+                const float f = quad_scale<FMT>(cur.sc[j][t], blk % 4u);
+#pragma unroll
+                for (int r = 0; r < 4; ++r) acc[t][r] = fmaf(f, c[r] - corr[r], acc[t][r]);
+            }
+        }
+        // o = lane * 16 + t * 4 + r  <->  row 4 (lane / 16) + r, column 16 t + lane % 16
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) rd[wave][lane * 16u + t * 4 + r] = acc[t][r];
+        __syncthreads();
+#pragma unroll
+        for (uint32_t jo = 0; jo < NO / kBmmThreads; ++jo) {
+            const uint32_t o = tid + jo * kBmmThreads;
+            float sum = 0.0f;
+#pragma unroll
+            for (int w = 0; w < int(kBmmWaves); ++w) sum += rd[w][o];
+            const uint32_t ol = o / 16u, ot = (o % 16u) / 4u, orr = o % 4u;
+            const uint32_t row = 4u * (ol / 16u) + orr, col = g * kGrp + 16u * ot + ol % 16u;
+            if (row < a.rows) out[size_t(row) * cols + col] = sum;
+        }
+    };
+    Wt w0, w1;
+    uint32_t g = blockIdx.x;
+    if (g < ng) load(w0, g);
+    for (;;) {
+        if (g >= ng) break;
+        uint32_t gn = g + gridDim.x;
+        if (gn < ng) load(w1, gn);
+        group(w0, g, red[0]);
+        g = gn;
+        if (g >= ng) break;
+        gn = g + gridDim.x;
+        if (gn < ng) load(w0, gn);
+        group(w1, g, red[1]);
+        g = gn;
+    }
+}
+
 // Position advance for every sequence of a batch.
 __global__ void badvance_kernel(uint32_t* pos, uint32_t n) {
     const uint32_t i = threadIdx.x;
@@ -513,6 +618,18 @@ int launch_bmm(BmmArgs a, int fmt, int n_cu, hipStream_t st, const char* who) {
             hipLaunchKernelGGL((bmm_int4_kernel<XP_SCALE_F16_QUAD, 4, 0, true>), ggrid, dim3(kBmmThreads), 0, st, a);
         else
             hipLaunchKernelGGL((bmm_int4_kernel<XP_SCALE_BF16_QUAD, 4, 0, true>), ggrid, dim3(kBmmThreads), 0, st, a);
+        hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return set_error(XP_E_HIP, "%s: launch -> %s", who, hipGetErrorString(e));
+        return XP_OK;
+    }
+    // Wide single matrices (the lm_head) stream through a persistent grid.
+    if (a.n_mats == 1 && a.amode == 0 && a.nsplit == 1 && n_cu > 0 && a.n_colwg >= 4u * uint32_t(n_cu) &&
+        a.nblk >= kBmmWaves && a.nblk <= kBmmWaves * kBmmMaxPerWave) {
+        const dim3 sgrid{static_cast<uint32_t>(n_cu)};
+        if (fmt == XP_SCALE_F16_QUAD)
+            hipLaunchKernelGGL((bmm_stream_kernel<XP_SCALE_F16_QUAD>), sgrid, dim3(kBmmThreads), 0, st, a);
+        else
+            hipLaunchKernelGGL((bmm_stream_kernel<XP_SCALE_BF16_QUAD>), sgrid, dim3(kBmmThreads), 0, st, a);
         hipError_t e = hipGetLastError();
         if (e != hipSuccess) return set_error(XP_E_HIP, "%s: launch -> %s", who, hipGetErrorString(e));
         return XP_OK;
