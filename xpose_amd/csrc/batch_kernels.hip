@@ -430,23 +430,26 @@ __global__ __launch_bounds__(kBmmThreads) void bmm_int4_kernel(BmmArgs a) {
 // Streamed M = 16 GEMM for wide matrices (the batched lm_head: 4096 column
 // groups of a 1152-long k): a persistent grid of one workgroup per CU takes
 // column groups wg, wg + grid, ...; wave w keeps the staged operand of its
-// k blocks (nblk / 8 or one more) in registers for every group and requests
-// the next group's weights before it multiplies the current ones, so the
-// weight stream never waits on a workgroup's launch or reduction. The eight
-// waves' partial tiles meet in LDS, double buffered (one barrier a group),
-// and are added in wave order as bmm_int4_kernel adds them. The groups
-// alternate between two weight buffers in an unrolled pair so that both keep
-// fixed registers.
+// k blocks (nblk / 8 or one more, at most 5: at most two scale quads) in
+// registers for every group and keeps the weights of the next group in
+// flight while it multiplies the current ones, so the stream never waits on
+// a workgroup's launch or reduction. The eight waves' partial tiles meet in
+// LDS, double buffered (one barrier a group), and are added in wave order
+// as bmm_int4_kernel adds them. The groups rotate through two weight
+// buffers in an unrolled ring so that each keeps fixed registers.
 template <int FMT>
 __global__ __launch_bounds__(kBmmThreads) void bmm_stream_kernel(BmmArgs a) {
     constexpr int MB = int(kBmmMaxPerWave);
+    constexpr int NBUF = 2;                           // 3 spills registers
     constexpr uint32_t NO = 1024;                      // 16 rows x 64 columns
+    static_assert(MB <= 5, "a wave's blocks span at most two scale quads");
     __shared__ float red[2][kBmmWaves][NO];
     const uint32_t tid = threadIdx.x, wave = tid / kWave, lane = tid % kWave;
     const uint32_t col16 = lane % 16u, wsel = lane / 16u;
     const uint32_t nblk = a.nblk, base = nblk / kBmmWaves, rem = nblk % kBmmWaves;
     const uint32_t nbw = base + (wave < rem ? 1u : 0u);       // this wave's blocks
     const uint32_t kb0 = wave * base + min(wave, rem);
+    const uint32_t q0 = kb0 / 4u;                               // its first scale quad
     const u32x4* A = static_cast<const u32x4*>(a.a);
     u32x4 ahi[MB], alo[MB];
     float4 as[MB];
@@ -458,12 +461,13 @@ __global__ __launch_bounds__(kBmmThreads) void bmm_stream_kernel(BmmArgs a) {
         as[j] = *reinterpret_cast<const float4*>(a.asum + size_t(blk) * 16 + 4u * wsel);
     }
     const uint32_t cols = a.mats[0].cols, ng = cols / kGrp;
+    const uint32_t nq = (nblk + 3u) / 4u;
     const uint32_t* wq = static_cast<const uint32_t*>(a.mats[0].wq);
     const u32x2* sq = static_cast<const u32x2*>(a.mats[0].sc);
     float* out = a.mats[0].out;
     struct Wt {
         uint32_t w[MB][4];
-        u32x2 sc[MB][4];
+        u32x2 sc[2][4];                                 // scale quads q0, q0 + 1
     };
     auto load = [&](Wt& o, uint32_t g) {
 #pragma unroll
@@ -473,8 +477,13 @@ __global__ __launch_bounds__(kBmmThreads) void bmm_stream_kernel(BmmArgs a) {
             for (int t = 0; t < 4; ++t) {
                 const uint32_t cg = 16u * t + col16;
                 o.w[j][t] = __builtin_nontemporal_load(wq + ((size_t(g) * nblk + blk) * kGrp + cg) * 4 + wsel);
-                o.sc[j][t] = sq[size_t(blk / 4) * cols + g * kGrp + cg];
             }
+        }
+#pragma unroll
+        for (int qq = 0; qq < 2; ++qq) {
+            const uint32_t q = min(q0 + uint32_t(qq), nq - 1u);
+#pragma unroll
+            for (int t = 0; t < 4; ++t) o.sc[qq][t] = sq[size_t(q) * cols + g * kGrp + 16u * t + col16];
         }
     };
     auto group = [&](const Wt& cur, uint32_t g, float (&rd)[kBmmWaves][NO]) {
@@ -487,13 +496,14 @@ __global__ __launch_bounds__(kBmmThreads) void bmm_stream_kernel(BmmArgs a) {
             const uint32_t blk = kb0 + uint32_t(j);
             const bf16x8 hi = as_bf16x8(ahi[j]), lo = as_bf16x8(alo[j]);
             const float corr[4] = {136.0f * as[j].x, 136.0f * as[j].y, 136.0f * as[j].z, 136.0f * as[j].w};
+            const bool second = blk / 4u != q0;
 #pragma unroll
             for (int t = 0; t < 4; ++t) {
                 const bf16x8 bw = as_bf16x8(widen_nibbles(cur.w[j][t]));
                 f32x4 c = {0.0f, 0.0f, 0.0f, 0.0f};
                 c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(hi, bw, c, 0, 0, 0);
                 c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(lo, bw, c, 0, 0, 0);
-                const float f = quad_scale<FMT>(cur.sc[j][t], blk % 4u);
+                const float f = quad_scale<FMT>(second ? cur.sc[1][t] : cur.sc[0][t], blk % 4u);
 #pragma unroll
                 for (int r = 0; r < 4; ++r) acc[t][r] = fmaf(f, c[r] - corr[r], acc[t][r]);
             }
@@ -515,20 +525,24 @@ __global__ __launch_bounds__(kBmmThreads) void bmm_stream_kernel(BmmArgs a) {
             if (row < a.rows) out[size_t(row) * cols + col] = sum;
         }
     };
-    Wt w0, w1;
+    // Every prefetch is issued, past the last group as a repeat of it: a
+    // load under a condition leaves the compiler's wait counts unable to
+    // tell whether it was issued, and it then waits for all of them.
+    Wt wb[NBUF];
+    const uint32_t step = gridDim.x;
     uint32_t g = blockIdx.x;
-    if (g < ng) load(w0, g);
+#pragma unroll
+    for (int b = 0; b < NBUF - 1; ++b) load(wb[b], min(g + uint32_t(b) * step, ng - 1u));
+    // group i uses buffer i % NBUF and LDS half i % 2: the ring is unrolled
+    // over 2 NBUF groups so that both are fixed
     for (;;) {
-        if (g >= ng) break;
-        uint32_t gn = g + gridDim.x;
-        if (gn < ng) load(w1, gn);
-        group(w0, g, red[0]);
-        g = gn;
-        if (g >= ng) break;
-        gn = g + gridDim.x;
-        if (gn < ng) load(w0, gn);
-        group(w1, g, red[1]);
-        g = gn;
+#pragma unroll
+        for (int b = 0; b < 2 * NBUF; ++b) {
+            if (g >= ng) return;
+            load(wb[(b + NBUF - 1) % NBUF], min(g + uint32_t(NBUF - 1) * step, ng - 1u));
+            group(wb[b % NBUF], g, red[b % 2]);
+            g += step;
+        }
     }
 }
 
