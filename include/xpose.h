@@ -493,7 +493,30 @@ int  xp_session_last_trace(xp_session* s, uint64_t* host, size_t n, uint32_t* gr
  * as two bf16 terms). No reference counterpart: the reference decodes one
  * sequence per DecodeSession (decode.hpp:605-676). */
 typedef struct xp_batch xp_batch;
+/* xp_batch_create2 with exec_mode XP_EXEC_AUTO. */
 int xp_batch_create(const xp_session* weights, uint32_t n_seq, uint32_t max_seq, xp_batch** out);
+/* exec_mode: XP_EXEC_GRAPH (and XP_EXEC_AUTO) runs each step as a captured
+ * graph of one kernel per stage; XP_EXEC_TOKEN runs the layers as ONE
+ * persistent kernel (one 512-thread workgroup per CU walking the stages,
+ * per-tile flags between them; creation fails if the shape or the device's
+ * free CUs do not allow it). Both give bit-identical results; the graph is
+ * the faster (1.41 vs 1.93 ms a config-5 step, measured), so AUTO takes it.
+ * The persistent kernel's bounded waits turn a grid that is not resident
+ * after all into XP_E_DEVICE from xp_batch_forward (that step's results and
+ * KV rows are then not valid). */
+int xp_batch_create2(const xp_session* weights, uint32_t n_seq, uint32_t max_seq, int32_t exec_mode,
+                     xp_batch** out);
+/* The execution in use: XP_EXEC_TOKEN (persistent step kernel) or XP_EXEC_GRAPH. */
+int xp_batch_exec_mode(const xp_batch* b, int32_t* mode);
+/* Stage timeline of the step kernel (XP_EXEC_TOKEN only), for profiling:
+ * while enabled each forward records, per workgroup w of the grid of G, the
+ * 100 MHz realtime clock when its inputs of stage k (0 q|k|v, 1 attention,
+ * 2 o, 3 staging, 4 gate|up, 5 down, 6 staging) of layer l were ready and
+ * when its last tile of that stage ended: out[((l*7 + k)*2 + e)*G + w], e = 0
+ * / 1 (0 where it had no tile), then its start at out[n_layers*14*G + w].
+ * read with out == NULL sets *n_out to the entry count. */
+int xp_batch_step_trace(xp_batch* b, int enable);
+int xp_batch_step_trace_read(xp_batch* b, unsigned long long* out, size_t n, size_t* n_out);
 int xp_batch_destroy(xp_batch* b);
 int xp_batch_kv_upload(xp_batch* b, uint32_t seq, int layer, int which, uint32_t start,
                        uint32_t count, const uint16_t* src);

@@ -189,6 +189,86 @@ def test_gpu_batch_full_size_cfg5(xp, xo):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("shape", ["window", "global3"])
+def test_gpu_batch_step_kernel_equals_graph(xp, xo, shape):
+    """The persistent step kernel (XP_EXEC_TOKEN) against the graph of
+    per-op kernels (XP_EXEC_GRAPH) on the same weights, caches, positions and
+    tokens: both run the same tile code in the same order, so logits,
+    candidates, appended K/V rows and greedy ids are equal bit for bit.
+    window: 6 layers (one global), 16 sequences at depths 3..1000, most past
+    the 512-position window. global3: 4 layers, every second global, max_seq
+    4104 with the benchmark's depths (global attention in splits of three
+    128-key passes, the U = 8 tile)."""
+    X = xp
+    print(f"case batch step kernel vs graph {shape}", flush=True)
+    n_seq = 16
+    if shape == "window":
+        cfg = X.XpConfig.gemma3_1b(n_layers=6, vocab=32768, max_seq=1024)
+        depths = np.linspace(3, 1000, n_seq).astype(np.int64)
+    else:
+        seed = 0x5EED0005
+        cfg = X.XpConfig.gemma3_1b(n_layers=4, global_every=2, vocab=32768, max_seq=4104)
+        u = np.array([X.philox_uniform(seed, i, 0) for i in range(n_seq)])
+        depths = (128 + np.floor(u * (4096 - 128 + 1))).astype(np.int64)
+    sess, t = build(X, xo, cfg)
+    kvd = cfg.n_kv_heads * cfg.head_dim
+    bt = X.DecodeBatch(sess, n_seq, cfg.max_seq, X.XP_EXEC_TOKEN)
+    bg = X.DecodeBatch(sess, n_seq, cfg.max_seq, X.XP_EXEC_GRAPH)
+    assert bt.exec_mode() == X.XP_EXEC_TOKEN and bg.exec_mode() == X.XP_EXEC_GRAPH
+    for i, d in enumerate(depths):
+        for l in range(cfg.n_layers):
+            for which in (0, 1):
+                rows = X.synth_normal_f16(int(d) * kvd, 7000 + i, 2 * l + which)
+                bt.kv_upload(i, l, which, 0, rows)
+                bg.kv_upload(i, l, which, 0, rows)
+    bt.set_positions(depths)
+    bg.set_positions(depths)
+    toks = (np.arange(n_seq) * 7919 + 11).astype(np.uint32) % cfg.vocab
+    bt.forward(toks)
+    bg.forward(toks)
+    pos = depths.copy()
+    for step in range(3):
+        for i in range(n_seq):
+            a, b = bt.last_logits(i), bg.last_logits(i)
+            assert np.array_equal(a.view(np.uint32), b.view(np.uint32)), (step, i, np.abs(a - b).max())
+            va, ia = bt.last_candidates(i)
+            vb, ib = bg.last_candidates(i)
+            assert np.array_equal(ia, ib) and np.array_equal(va.view(np.uint32), vb.view(np.uint32)), (step, i)
+            for l in range(cfg.n_layers):
+                for which in (0, 1):
+                    ka = bt.kv_download(i, l, which, int(pos[i]), 1)
+                    kb = bg.kv_download(i, l, which, int(pos[i]), 1)
+                    assert np.array_equal(ka, kb), (step, i, l, which)
+        if step < 2:
+            ta, tb = bt.decode_step(), bg.decode_step()
+            assert np.array_equal(ta, tb), step
+            pos = pos + 1
+    assert np.array_equal(bt.positions(), bg.positions())
+    bt.close()
+    bg.close()
+    sess.close()
+
+
+@pytest.mark.gpu
+def test_gpu_batch_exec_modes(xp, xo):
+    """xp_batch_create2's modes: AUTO takes the graph (the faster), TOKEN the
+    step kernel on a free GPU, an unknown mode is refused."""
+    X = xp
+    print("case batch exec modes", flush=True)
+    cfg = X.XpConfig.gemma3_1b(n_layers=1, vocab=16384, max_seq=256)
+    sess, _ = build(X, xo, cfg)
+    b = X.DecodeBatch(sess, 3, 256)
+    assert b.exec_mode() == X.XP_EXEC_GRAPH
+    b.close()
+    b = X.DecodeBatch(sess, 3, 256, X.XP_EXEC_TOKEN)
+    assert b.exec_mode() == X.XP_EXEC_TOKEN
+    b.close()
+    with pytest.raises(X.XposeError):
+        X.DecodeBatch(sess, 3, 256, X.XP_EXEC_LAUNCH)
+    sess.close()
+
+
+@pytest.mark.gpu
 def test_gpu_batch_one_sequence_equals_session(xp, xo):
     """A batch of one sequence and the single-sequence session (persistent
     token kernel) on the same weights and KV give the same logits to the

@@ -161,6 +161,10 @@ def _declare(lib: C.CDLL) -> None:
         "xp_session_create": (i32, [P(XpConfig), P(vp)]),
         "xp_session_destroy": (i32, [vp]),
         "xp_batch_create": (i32, [vp, u32, u32, P(vp)]),
+        "xp_batch_create2": (i32, [vp, u32, u32, i32, P(vp)]),
+        "xp_batch_exec_mode": (i32, [vp, P(i32)]),
+        "xp_batch_step_trace": (i32, [vp, i32]),
+        "xp_batch_step_trace_read": (i32, [vp, vp, C.c_size_t, P(C.c_size_t)]),
         "xp_batch_destroy": (i32, [vp]),
         "xp_batch_kv_upload": (i32, [vp, u32, i32, i32, u32, u32, vp]),
         "xp_batch_kv_download": (i32, [vp, u32, i32, i32, u32, u32, vp]),
@@ -441,13 +445,32 @@ class DecodeBatch:
     """Up to 16 sequences decoded together on a DecodeSession's weights
     (xp_batch_*). The session must stay open while the batch lives."""
 
-    def __init__(self, sess: "DecodeSession", n_seq: int, max_seq: int):
+    def __init__(self, sess: "DecodeSession", n_seq: int, max_seq: int, exec_mode: int = 0):
+        """exec_mode: XP_EXEC_AUTO (0), XP_EXEC_GRAPH (1) or XP_EXEC_TOKEN (3, the
+        persistent step kernel), as xp_batch_create2."""
         self.sess = sess
         self.n = n_seq
         self.max_seq = max_seq
         h = C.c_void_p()
-        call("xp_batch_create", sess.h, n_seq, max_seq, C.byref(h))
+        call("xp_batch_create2", sess.h, n_seq, max_seq, exec_mode, C.byref(h))
         self.h = h
+
+    def exec_mode(self) -> int:
+        m = C.c_int32()
+        call("xp_batch_exec_mode", self.h, C.byref(m))
+        return m.value
+
+    def step_trace(self, enable: bool) -> None:
+        call("xp_batch_step_trace", self.h, 1 if enable else 0)
+
+    def step_trace_read(self) -> np.ndarray:
+        """The step kernel's stage timeline, [n_layers][7][2][grid] then
+        [grid] start times (100 MHz ticks), as xp_batch_step_trace."""
+        n = C.c_size_t()
+        call("xp_batch_step_trace_read", self.h, None, 0, C.byref(n))
+        out = np.empty(n.value, np.uint64)
+        call("xp_batch_step_trace_read", self.h, out.ctypes.data, out.size, C.byref(n))
+        return out
 
     def close(self) -> None:
         if self.h and self.h.value and _lib is not None:

@@ -31,7 +31,7 @@ HIP_FLAGS = [
 ]
 
 LIB_SOURCES = ["runtime.cpp", "synth.cpp", "matvec.hip", "transformer.hip", "sampling.hip",
-               "sampling_chain.hip", "token_kernel.hip", "probe.hip", "batch_kernels.hip",
+               "sampling_chain.hip", "token_kernel.hip", "probe.hip", "batch_kernels.hip", "batch_step.hip",
                "batch.cpp", "gguf.cpp", "pack.cpp", "tokenizer.cpp", "repack.cpp", "native_quant.hip", "prefill_kernels.hip",
                "session_kernels.hip", "session.cpp"]
 

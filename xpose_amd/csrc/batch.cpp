@@ -22,6 +22,7 @@
 #include <cmath>
 #include <cstring>
 #include <new>
+#include <string>
 #include <vector>
 
 namespace xp {
@@ -73,8 +74,23 @@ struct Batch {
     // Prefill mode: the rows are consecutive positions of one sequence and
     // share the session's KV cache; the step ends after the last layer.
     bool prefill = false;
+    // Decode through the persistent step kernel (batch_step.hip) instead of
+    // a graph of per-op kernels: its per-layer stage buffers and argument
+    // table (step_arena), the operand the first layer reads (a0 / asum0) and
+    // the one the lm_head reads (af / asumf), counters and status word.
+    bool step_kernel = false;
+    char* step_arena = nullptr;
+    BstepArgs bs{};
+    void* a0 = nullptr;
+    float* asum0 = nullptr;
+    void* af = nullptr;
+    float* asumf = nullptr;
+    uint32_t* h_status = nullptr;        // pinned
+    unsigned long long* d_trace = nullptr;   // the step kernel's stage timeline, when on
+    size_t trace_n = 0;
 
     int record();
+    int setup_step(int exec);
     int forward(const uint32_t* tokens);
 };
 
@@ -118,6 +134,30 @@ int Batch::record() {
         return launch_bmm(g, fmt, w.n_cu, st, who);
     };
     XB(launch_bembed(x, w.lm_w, w.lm_s, fmt, H, c.vocab, w.embed_scale, d_tok, B, w.embed, st));
+    if (step_kernel) {
+        // layer 0's operand, then every layer in one launch, then the lm_head
+        // on the operand its last stage staged
+        BprepArgs p0{0, x, nullptr, nullptr, nullptr, w.layer[0].norm[0], a0, asum0, H, eps};
+        XB(launch_bprep(p0, B, st));
+        XB(launch_bstep(bs, fmt, uint32_t(w.n_cu), st));
+        BmmArgs g{};
+        g.a = af;
+        g.asum = asumf;
+        g.lda = H;
+        g.mats[0] = {logits, w.lm_w, w.lm_s, c.vocab};
+        g.n_mats = 1;
+        g.nblk = H / kBlkB;
+        g.rows = B;
+        g.part = part;
+        g.part_cap = part_cap;
+        g.tickets = tickets;
+        g.tickets_cap = tickets_cap;
+        XB(launch_bmm(g, fmt, w.n_cu, st, "batch lm_head"));
+        XB(launch_topk4(cval, cidx, logits, c.vocab, kHarvestParts, st, B));
+        XB(launch_select_rows(oval, oidx, cval, cidx, kHarvest, kCand, B, st));
+        XB(launch_badvance(d_pos, B, st));
+        return XP_OK;
+    }
     XB(prep(0, x, nullptr, nullptr, nullptr, w.layer[0].norm[0], H));
     for (uint32_t l = 0; l < c.n_layers; ++l) {
         const SessionWeights::Layer& L = w.layer[l];
@@ -188,6 +228,194 @@ int Batch::record() {
     return XP_OK;
 }
 
+// Decode through the persistent step kernel: per-layer stage buffers (each
+// stage's output its own per layer, so no consumer reads a line it read
+// before in the same launch), the layer table built with the per-op path's
+// own plans (plan_bmm, plan_attention: results are bit-identical), and the
+// residency checks the token kernel uses (one 512-thread workgroup per CU).
+// Opt-in (XP_EXEC_TOKEN): measured slower than the graph of per-op kernels
+// (1.93 vs 1.41 ms a config-5 step), whose kernel boundaries cost less than
+// the kernel's flag hand-offs.
+int Batch::setup_step(int exec) {
+    const xp_config& c = w.cfg;
+    const uint32_t H = c.hidden, qd = c.n_heads * c.head_dim, kvd = c.n_kv_heads * c.head_dim, F = c.ffn;
+    const int fmt = c.scale_fmt;
+    const float eps = c.rms_eps;
+    step_kernel = false;
+    auto refuse = [&](const char* why) -> int {
+        if (exec == XP_EXEC_TOKEN)
+            return set_error(XP_E_ARG, "xp_batch_create: the step kernel %s", why);
+        clear_error();
+        return XP_OK;
+    };
+    (void)exec;
+    if (c.n_kv_heads == 0 || c.n_heads != 4u * c.n_kv_heads || c.head_dim != 256u)
+        return refuse("takes 4 query heads of 256 dims per kv head");
+    if (w.n_cu <= 0 || H / 8u > 512u) return refuse("needs a known CU count and hidden <= 4096");
+    int per_cu = 0;
+    if (bstep_occupancy(fmt, &per_cu) != XP_OK || per_cu < 1) return refuse("does not fit a CU");
+    // per-layer stage buffers: layer l at step_arena + l * per (layer
+    // n_layers holds only the lm_head's operand)
+    size_t off = 0;
+    auto take = [&](size_t bytes) { const size_t o = off; off += al(bytes); return o; };
+    const size_t o_q = take(size_t(B) * qd * 4), o_k = take(size_t(B) * kvd * 4),
+                 o_v = take(size_t(B) * kvd * 4), o_att = take(size_t(B) * qd * 4),
+                 o_o = take(size_t(B) * H * 4), o_xa = take(size_t(B) * H * 4), o_xb = take(size_t(B) * H * 4),
+                 o_a0 = take(size_t(H / kBlkB) * 2 * 64 * 16), o_s0 = take(size_t(H / kBlkB) * 16 * 4),
+                 o_a1 = take(size_t(H / kBlkB) * 2 * 64 * 16), o_s1 = take(size_t(H / kBlkB) * 16 * 4),
+                 o_a2 = take(size_t(F / kBlkB) * 2 * 64 * 16), o_s2 = take(size_t(F / kBlkB) * 16 * 4),
+                 o_dn = take(size_t(B) * H * 4);
+    const size_t per = off;
+    const size_t tab = al(size_t(per) * (c.n_layers + 1));
+    const size_t rope_off = tab + al(sizeof(BstepLayer) * c.n_layers);
+    const size_t cnt_off = rope_off + al(sizeof(RopeFreq) * 2);
+    const size_t total = cnt_off + al((size_t(c.n_layers) * kBsStages * kBsMaxTiles + 2) * 4);
+    if (hipMalloc(&step_arena, total) != hipSuccess) return set_error(XP_E_NOMEM, "xp_batch_create: device memory");
+    XP_HIP(hipMemset(step_arena, 0, total));
+    auto at = [&](uint32_t l, size_t o) { return step_arena + size_t(l) * per + o; };
+    std::vector<BstepLayer> T(c.n_layers);
+    RopeFreq rf[2]{};
+    uint32_t ncb_q = 0, ncb_o = 0, ncb_d = 0, ns_d = 0, n_gu = 0;
+    for (uint32_t l = 0; l < c.n_layers; ++l) {
+        const SessionWeights::Layer& L = w.layer[l];
+        BstepLayer& t = T[l];
+        t = BstepLayer{};
+        float* q_raw = reinterpret_cast<float*>(at(l, o_q));
+        float* k_raw = reinterpret_cast<float*>(at(l, o_k));
+        float* v_raw = reinterpret_cast<float*>(at(l, o_v));
+        float* att_l = reinterpret_cast<float*>(at(l, o_att));
+        float* o_l = reinterpret_cast<float*>(at(l, o_o));
+        float* xa = reinterpret_cast<float*>(at(l, o_xa));
+        float* xb = reinterpret_cast<float*>(at(l, o_xb));
+        float* dn_l = reinterpret_cast<float*>(at(l, o_dn));
+        auto gemm = [&](BmmArgs& g, uint32_t nblk, const char* who, uint32_t* ncb, bool want_quarter) {
+            g.nblk = nblk;
+            g.rows = B;
+            g.part = part;
+            g.part_cap = part_cap;
+            g.tickets = tickets;
+            g.tickets_cap = tickets_cap;
+            uint32_t nb = 0;
+            bool quarter = false;
+            if (int rc = plan_bmm(g, fmt, w.n_cu, who, &nb, &quarter); rc != XP_OK) return rc;
+            if (quarter != want_quarter) return set_error(XP_E_ARG, "%s: plan shape", who);
+            if (*ncb != 0 && *ncb != nb) return set_error(XP_E_ARG, "%s: plan differs between layers", who);
+            *ncb = nb;
+            return XP_OK;
+        };
+        t.qkv.a = at(l, o_a0);
+        t.qkv.asum = reinterpret_cast<float*>(at(l, o_s0));
+        t.qkv.lda = H;
+        t.qkv.mats[0] = {q_raw, L.w[XP_T_Q], L.s[XP_T_Q], qd};
+        t.qkv.mats[1] = {k_raw, L.w[XP_T_K], L.s[XP_T_K], kvd};
+        t.qkv.mats[2] = {v_raw, L.w[XP_T_V], L.s[XP_T_V], kvd};
+        t.qkv.n_mats = 3;
+        t.o.amode = 2;
+        t.o.xa = att_l;
+        t.o.lda = qd;
+        t.o.mats[0] = {o_l, L.w[XP_T_O], L.s[XP_T_O], H};
+        t.o.n_mats = 1;
+        t.gu.a = at(l, o_a1);
+        t.gu.asum = reinterpret_cast<float*>(at(l, o_s1));
+        t.gu.lda = H;
+        t.gu.geglu = 1;
+        t.gu.a_out = at(l, o_a2);
+        t.gu.asum_out = reinterpret_cast<float*>(at(l, o_s2));
+        t.gu.mats[0] = {nullptr, L.w[XP_T_GATE], L.s[XP_T_GATE], F};
+        t.gu.mats[1] = {nullptr, L.w[XP_T_UP], L.s[XP_T_UP], F};
+        t.gu.n_mats = 2;
+        t.dn.a = at(l, o_a2);
+        t.dn.asum = reinterpret_cast<float*>(at(l, o_s2));
+        t.dn.lda = F;
+        t.dn.mats[0] = {dn_l, L.w[XP_T_DOWN], L.s[XP_T_DOWN], H};
+        t.dn.n_mats = 1;
+        if (gemm(t.qkv, H / kBlkB, "batch step q|k|v", &ncb_q, true) != XP_OK || t.qkv.nsplit != 1 ||
+            gemm(t.o, qd / kBlkB, "batch step o_proj", &ncb_o, true) != XP_OK || t.o.nsplit != 1 ||
+            gemm(t.gu, H / kBlkB, "batch step gate/up", &n_gu, false) != XP_OK ||
+            gemm(t.dn, F / kBlkB, "batch step down", &ncb_d, true) != XP_OK)
+            return refuse("needs the per-op path's GEMM plans (quarter column blocks, one k split)");
+        if (ns_d != 0 && ns_d != t.dn.nsplit) return refuse("needs one down plan for every layer");
+        ns_d = t.dn.nsplit;
+        // attention as the per-op path plans it (record())
+        const bool glob = L.global;
+        AttnArgs& aa = t.att;
+        aa.out = att_l;
+        aa.q = q_raw;
+        aa.kc = kc[l];
+        aa.vc = vc[l];
+        aa.q_raw = q_raw;
+        aa.k_raw = k_raw;
+        aa.v_raw = v_raw;
+        aa.qw = L.norm[4];
+        aa.kw = L.norm[5];
+        aa.eps = eps;
+        aa.theta = glob ? c.rope_theta_global : c.rope_theta_local;
+        aa.bkv = kvd;
+        aa.n_heads = c.n_heads;
+        aa.kv_heads = c.n_kv_heads;
+        aa.head_dim = c.head_dim;
+        aa.pos_dev = d_pos;
+        aa.window = glob ? 0u : c.sliding_window;
+        aa.scale = w.attn_scale;
+        aa.part = attn_part;
+        aa.tickets = attn_tickets;
+        aa.batch = B;
+        aa.bq = qd;
+        aa.bcache = size_t(S) * kvd;
+        aa.bpart = attn_part_seq;
+        const uint32_t max_span = glob || c.sliding_window == 0 ? S : std::min(c.sliding_window, S);
+        int U = 0;
+        RopeFreq f{};
+        if (plan_attention(aa, max_span, true, &U, &f) != XP_OK || aa.group != 4u)
+            return refuse("needs the per-op path's attention plan");
+        t.att_u = uint32_t(U);
+        t.att_rope = glob ? 1u : 0u;
+        rf[t.att_rope] = f;
+        t.n_att = aa.nsplit * aa.kv_heads * B;
+        if (t.n_att > kBsMaxTiles) return refuse("takes at most 512 attention tiles");
+        const float* next = l + 1 < c.n_layers ? w.layer[l + 1].norm[0] : w.final_norm;
+        t.prep1 = BprepArgs{1, l == 0 ? x : reinterpret_cast<float*>(at(l - 1, o_xb)), o_l, nullptr,
+                            L.norm[1], L.norm[2], at(l, o_a1), reinterpret_cast<float*>(at(l, o_s1)), H, eps};
+        t.prep1.x_out = xa;
+        t.prep2 = BprepArgs{1, xa, dn_l, nullptr, L.norm[3], next, at(l + 1, o_a0),
+                            reinterpret_cast<float*>(at(l + 1, o_s0)), H, eps};
+        t.prep2.x_out = xb;
+    }
+    a0 = at(0, o_a0);
+    asum0 = reinterpret_cast<float*>(at(0, o_s0));
+    af = at(c.n_layers, o_a0);
+    asumf = reinterpret_cast<float*>(at(c.n_layers, o_s0));
+    XP_HIP(hipMemcpy(step_arena + tab, T.data(), sizeof(BstepLayer) * c.n_layers, hipMemcpyHostToDevice));
+    XP_HIP(hipMemcpy(step_arena + rope_off, rf, sizeof(rf), hipMemcpyHostToDevice));
+    bs = BstepArgs{};
+    bs.layers = reinterpret_cast<const BstepLayer*>(step_arena + tab);
+    bs.rope = reinterpret_cast<const RopeFreq*>(step_arena + rope_off);
+    bs.n_layers = c.n_layers;
+    bs.batch = B;
+    bs.ncb_qkv = ncb_q;
+    bs.ncb_o = ncb_o;
+    bs.ncb_dn = ncb_d;
+    bs.ns_dn = ns_d;
+    bs.n_gu = n_gu;
+    bs.flags = reinterpret_cast<uint32_t*>(step_arena + cnt_off);
+    bs.epoch = bs.flags + size_t(c.n_layers) * kBsStages * kBsMaxTiles;
+    bs.status = bs.epoch + 1;
+    if (ncb_q > kBsMaxTiles || ncb_o > kBsMaxTiles || n_gu > kBsMaxTiles || ncb_d * ns_d > kBsMaxTiles ||
+        B > kBsMaxTiles)
+        return refuse("takes at most 512 tiles a stage");
+    bs.spin_limit = 1u << 20;
+    if (hipHostMalloc(reinterpret_cast<void**>(&h_status), 16) != hipSuccess)
+        return set_error(XP_E_NOMEM, "xp_batch_create: pinned host memory");
+    h_status[0] = 0u;
+    // the grid of one workgroup per CU resident at once (the token kernel's probe)
+    std::vector<uint32_t> probe(uint32_t(w.n_cu));
+    if (probe_token_grid(uint32_t(w.n_cu), st, probe.data()) != XP_OK) return refuse("probe launch failed");
+    for (uint32_t v : probe)
+        if (!((v >> 8) & 1u)) return refuse("grid is not resident at once (another kernel holds CUs)");
+    step_kernel = true;
+    return XP_OK;
+}
+
 int Batch::forward(const uint32_t* tokens) {
     for (uint32_t i = 0; i < B; ++i) {
         XP_REQUIRE(pos[i] < S, "xp_batch_forward: sequence %u is at position %u of max_seq %u", i,
@@ -222,8 +450,21 @@ int Batch::forward(const uint32_t* tokens) {
         XP_HIP(hipMemcpyAsync(h_val, oval, size_t(B) * kCand * 4, hipMemcpyDeviceToHost, st));
         XP_HIP(hipMemcpyAsync(h_idx, oidx, size_t(B) * kCand * 4, hipMemcpyDeviceToHost, st));
     }
+    if (step_kernel) XP_HIP(hipMemcpyAsync(h_status, bs.status, 4, hipMemcpyDeviceToHost, st));
     XP_HIP(hipStreamSynchronize(st));
     (void)hipEventElapsedTime(&last_ms, ev[0], ev[1]);
+    if (step_kernel && h_status[0] != 0u) {
+        // a wait ran past its limit (the grid was not resident at once): the
+        // step's results are not valid
+        const uint32_t code = h_status[0];
+        h_status[0] = 0u;
+        XP_HIP(hipMemcpyAsync(bs.status, h_status, 4, hipMemcpyHostToDevice, st));
+        XP_HIP(hipStreamSynchronize(st));
+        logits_valid = false;
+        return set_error(XP_E_DEVICE, "xp_batch_forward: the step kernel's wait ran past its limit "
+                         "(status %u; another kernel held CUs of this GPU); the step's results and "
+                         "KV rows are not valid", code);
+    }
     for (uint32_t i = 0; i < B; ++i) ++pos[i];
     logits_valid = true;
     return XP_OK;
@@ -237,6 +478,9 @@ void release(Batch* b) {
     for (auto& e : b->ev)
         if (e) (void)hipEventDestroy(e);
     if (b->arena) (void)hipFree(b->arena);
+    if (b->step_arena) (void)hipFree(b->step_arena);
+    if (b->d_trace) (void)hipFree(b->d_trace);
+    if (b->h_status) (void)hipHostFree(b->h_status);
     if (b->h_tok) (void)hipHostFree(b->h_tok);
     if (b->h_val) (void)hipHostFree(b->h_val);
     if (b->h_idx) (void)hipHostFree(b->h_idx);
@@ -258,8 +502,10 @@ namespace {
 // positions of one sequence on the session's own KV cache (no caches of its
 // own, no lm_head or sampling).
 int make_batch(const xp_session* weights, uint32_t n_seq, uint32_t max_seq, bool prefill,
-               xp_batch** out) {
+               xp_batch** out, int exec = XP_EXEC_AUTO) {
     XP_REQUIRE(weights && out, "null pointer");
+    XP_REQUIRE(exec == XP_EXEC_AUTO || exec == XP_EXEC_GRAPH || exec == XP_EXEC_TOKEN,
+               "exec_mode=%d: XP_EXEC_AUTO, XP_EXEC_GRAPH or XP_EXEC_TOKEN", exec);
     *out = nullptr;
     XP_REQUIRE(n_seq >= 1 && n_seq <= kBatchMax, "n_seq=%u must be in [1, %u]", n_seq, kBatchMax);
     xp_batch* h = new (std::nothrow) xp_batch;
@@ -372,6 +618,14 @@ int make_batch(const xp_session* weights, uint32_t n_seq, uint32_t max_seq, bool
         return fail(XP_E_NOMEM, "pinned host memory");
     if (hipEventCreate(&b.ev[0]) != hipSuccess || hipEventCreate(&b.ev[1]) != hipSuccess)
         return fail(XP_E_HIP, "hipEventCreate failed");
+    if (!prefill && exec == XP_EXEC_TOKEN) {
+        if (int rc2 = b.setup_step(exec); rc2 != XP_OK) {
+            const std::string msg = xp_last_error();
+            release(&h->b);
+            delete h;
+            return set_error(rc2, "%s", msg.c_str());
+        }
+    }
     *out = h;
     return XP_OK;
 }
@@ -435,6 +689,52 @@ extern "C" {
 
 int xp_batch_create(const xp_session* weights, uint32_t n_seq, uint32_t max_seq, xp_batch** out) {
     return make_batch(weights, n_seq, max_seq, false, out);
+}
+
+int xp_batch_create2(const xp_session* weights, uint32_t n_seq, uint32_t max_seq, int32_t exec_mode,
+                     xp_batch** out) {
+    return make_batch(weights, n_seq, max_seq, false, out, exec_mode);
+}
+
+int xp_batch_step_trace(xp_batch* h, int enable) {
+    XP_REQUIRE(h, "null pointer");
+    Batch& b = h->b;
+    XP_REQUIRE(b.step_kernel, "xp_batch_step_trace: the batch does not run the step kernel");
+    XP_HIP(hipStreamSynchronize(b.st));
+    if (b.graph) {
+        (void)hipGraphExecDestroy(b.graph);   // recaptured with the new arguments
+        b.graph = nullptr;
+    }
+    if (!enable) {
+        b.bs.trace = nullptr;
+        return XP_OK;
+    }
+    const size_t n = (size_t(b.w.cfg.n_layers) * kBsStages * 2 + 1) * size_t(b.w.n_cu);
+    if (!b.d_trace) {
+        if (hipMalloc(reinterpret_cast<void**>(&b.d_trace), n * 8) != hipSuccess)
+            return set_error(XP_E_NOMEM, "xp_batch_step_trace: device memory");
+        b.trace_n = n;
+    }
+    XP_HIP(hipMemset(b.d_trace, 0, n * 8));
+    b.bs.trace = b.d_trace;
+    return XP_OK;
+}
+
+int xp_batch_step_trace_read(xp_batch* h, unsigned long long* out, size_t n, size_t* n_out) {
+    XP_REQUIRE(h && n_out, "null pointer");
+    Batch& b = h->b;
+    *n_out = b.trace_n;
+    if (!out) return XP_OK;
+    XP_REQUIRE(b.d_trace && n >= b.trace_n, "xp_batch_step_trace_read: no trace, or n < %zu", b.trace_n);
+    XP_HIP(hipStreamSynchronize(b.st));
+    XP_HIP(hipMemcpy(out, b.d_trace, b.trace_n * 8, hipMemcpyDeviceToHost));
+    return XP_OK;
+}
+
+int xp_batch_exec_mode(const xp_batch* h, int32_t* mode) {
+    XP_REQUIRE(h && mode, "null pointer");
+    *mode = h->b.step_kernel ? XP_EXEC_TOKEN : XP_EXEC_GRAPH;
+    return XP_OK;
 }
 
 int xp_batch_destroy(xp_batch* h) {

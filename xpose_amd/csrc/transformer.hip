@@ -8,6 +8,7 @@
 // workgroup with LDS, so the two-pass RMSNorm (rmsnorm_sumsq +
 // rmsnorm_apply_gemma) becomes one kernel, and the six per-layer QK-norm /
 // RoPE / kv_append dispatches become one.
+#include "xp_attn_device.hpp"
 #include "xp_device.hpp"
 #include "xp_launch.hpp"
 
@@ -126,599 +127,11 @@ __global__ __launch_bounds__(256) void qk_norm_rope_append_kernel(QkArgs a, Rope
     }
 }
 
-// ---- decode attention (split-span, fp16 KV) ----------------------------------
-// Grid: (nsplit, kv_heads, batch). Workgroup (s, g, b) takes a contiguous chunk
-// of sequence b's attended keys for the G query heads that share kv head g,
-// reading every key and value once for all G heads (the mq4 idea,
-// llm_transformer.cl:418-464, 499-557), in passes of 16 U keys:
-//   loads   32 lanes per 512-byte key row (16-byte loads, 8 dims per lane);
-//           lane group kp = tid / 32 takes keys kp, kp + 16, ..., and all U
-//           K and U V loads of a pass are in flight together
-//   scores  each lane dots its 8 dims with the G query heads; the G x U
-//           partial dots of a row group are summed by a reduce-scatter over
-//           its 32 lanes (each swizzle step halving the values a lane holds),
-//           so lane i ends with one (head, key) score
-//   softmax one wave per head over the pass, online across passes (running
-//           max and sum, the accumulated values rescaled by exp(m_old - m_new))
-//   values  the same lanes accumulate p x v for their 8 dims, then the 16 row
-//           groups are summed (lane pairs by shuffle, waves through LDS)
-// U (2, 4 or 8) follows the chunk length, so a 32-key chunk does a quarter
-// of a 128-key pass's arithmetic. Up to 256 splits (at least 32 keys each)
-// give every CU a workgroup at one sequence's long spans. Each split
-// publishes (max, sum of exp, unnormalised o) per head; the last workgroup
-// of each group of 16 splits to arrive (arrival ticket) rescales and sums
-// the group — softmax_rows_finish's online combine (llm_transformer.cl:
-// 385-405) — into one record of the same form, and the last group to arrive
-// combines the group records, so no workgroup reads more than 16 records;
-// one group combines straight into the output. Records are read with 16-byte
-// device-scope loads spread over all the combining workgroup's threads, and
-// summed in a fixed order (deterministic).
-constexpr int kAttnThreads  = 512;
-constexpr int kAttnHD       = 256;                        // head_dim
-constexpr int kAttnLanes    = kAttnHD / 8;                // lanes per key row
-constexpr int kAttnRows     = kAttnThreads / kAttnLanes;  // 16 row groups
-constexpr int kAttnMaxPass  = kAttnRows * 8;              // most keys per pass (U = 8)
-constexpr int kAttnMinChunk = 32;                         // fewest keys per split
-constexpr int kAttnMaxSplit = 256;                        // splits per (sequence, kv head)
-constexpr int kAttnFan      = 16;                         // records one combine reads
-constexpr int kAttnGroups   = kAttnMaxSplit / kAttnFan;   // level-1 records
-constexpr int kAttnMaxG     = 4;                          // query heads per kv head
-constexpr int kAttnStat     = 8;                          // floats of (max[4], sum[4]) per record
-
-__host__ __device__ constexpr uint32_t attn_record(uint32_t G) { return kAttnStat + G * kAttnHD; }
-// Records per (sequence, kv head): the splits', then the level-1 groups'.
-constexpr uint32_t kAttnRecords = kAttnMaxSplit + kAttnGroups;
-// Exchange-mode record: G pairs (max, sum of exp) then G * HD / 2 pairs of
-// value dims, each pair a 16-byte (v0, tag, v1, tag) slot.
-__host__ __device__ constexpr uint32_t attn_xrecord(uint32_t G) { return 4u * (G + G * kAttnHD / 2u); }
-// Floats of one (sequence, kv head)'s records in either mode.
-__host__ __device__ constexpr uint32_t attn_head_floats(uint32_t G) {
-    return kAttnRecords * attn_record(G) > kAttnMaxSplit * attn_xrecord(G) ? kAttnRecords * attn_record(G)
-                                                                          : kAttnMaxSplit * attn_xrecord(G);
-}
-constexpr uint32_t kAttnEpoch = 1 + kAttnGroups;   // ticket word: the last exchange launch's tag
-constexpr uint32_t kAttnXErr  = 2 + kAttnGroups;   // ticket word: set when an exchange wait timed out
-constexpr uint32_t kAttnSpinLimit = 1u << 22;       // exchange poll rounds before giving up
-static_assert(kAttnTicketsPerHead == 3 + kAttnGroups, "tickets: level 2, one per group, epoch, flag");
-
-template <int M>
-__device__ __forceinline__ float swz_xor(float x) {   // x of lane ^ M within 32 lanes
-    return __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(x), (M << 10) | 0x1F));
-}
-// Reduce-scatter of v[0..N) over the 32 lanes of a row group, masks M, M/2 ..
-// 1: each step keeps the lower (lane bit clear) or upper half of the values and
-// adds the partner's copy of it; once one value is left it is summed plainly.
-// Lane l ends with the sum of value (l % 32) / (32 / N) (N <= 32).
-template <int N, int M>
-__device__ __forceinline__ void reduce_scatter32(float* v, uint32_t lane) {
-    if constexpr (M >= 1) {
-        if constexpr (N >= 2) {
-            constexpr int H = N / 2;
-            const bool up = (lane & M) != 0;
-#pragma unroll
-            for (int i = 0; i < H; ++i) {
-                const float keep = up ? v[H + i] : v[i];
-                const float send = up ? v[i] : v[H + i];
-                v[i] = keep + swz_xor<M>(send);
-            }
-            reduce_scatter32<H, M / 2>(v, lane);
-        } else {
-            v[0] += swz_xor<M>(v[0]);
-            reduce_scatter32<1, M / 2>(v, lane);
-        }
-    }
-}
-
-__device__ __forceinline__ void attn_range(const AttnArgs& a, uint32_t& span, uint32_t& kv0) {
-    if (a.pos_dev) {
-        const uint32_t seq = a.pos_dev[blockIdx.z] + 1u;
-        kv0 = (a.window == 0 || seq <= a.window) ? 0u : seq - a.window;
-        span = seq - kv0;
-    } else {
-        span = a.span;
-        kv0 = a.kv_start;
-    }
-}
-
-__device__ __forceinline__ void f16x8(float (&f)[8], u32x4 w) {
-    f[0] = f16_bits_to_f32(w.x); f[1] = f16_bits_to_f32(w.x >> 16);
-    f[2] = f16_bits_to_f32(w.y); f[3] = f16_bits_to_f32(w.y >> 16);
-    f[4] = f16_bits_to_f32(w.z); f[5] = f16_bits_to_f32(w.z >> 16);
-    f[6] = f16_bits_to_f32(w.w); f[7] = f16_bits_to_f32(w.w >> 16);
-}
-
-// Combine n <= kAttnFan records (stride REC floats, in device memory) of
-// kv head g: f_p = exp(m_p - M), L = sum_p l_p f_p, o = sum_p f_p o_p in
-// record order. Final: out[h][d] = o / L. Else a record (M, L, o) at rec_out.
-// Thread (r, col) loads float4 column col over records r, r + R, ...; wave h
-// reads head h's statistics (one record per lane). All threads take part.
-template <int G>
-__device__ __forceinline__ void attn_combine(const float* recs, uint32_t n, bool final, float* out,
-                                             float* rec_out, float (&red)[kAttnThreads / kWave][G * kAttnHD],
-                                             float (&fs)[kAttnFan][G], float (&run)[3][G]) {
-    constexpr int HD = kAttnHD;
-    constexpr uint32_t REC = attn_record(G);
-    constexpr int NCOL = G * HD / 4, R = kAttnThreads / NCOL, B = kAttnFan / R;
-    static_assert(kAttnFan % R == 0, "records per thread");
-    const int tid = threadIdx.x, lane = tid % kWave, wave = tid / kWave;
-    const int col = tid % NCOL, r = tid / NCOL, h = col * 4 / HD;
-    const rsrc_t rs = make_rsrc(recs, n * REC * 4u);
-    const uint32_t off = (kAttnStat + col * 4) * 4u;
-    u32x4 v[B];
-#pragma unroll
-    for (int i = 0; i < B; ++i) {
-        const uint32_t p = r + i * R;
-        v[i] = p < n ? ld_dev16(rs, p * REC * 4u + off) : u32x4{0u, 0u, 0u, 0u};
-    }
-    if (wave < G) {
-        const int hh = wave;
-        const bool live = uint32_t(lane) < n;
-        const float m = live ? ld_dev(recs + size_t(lane) * REC + hh) : -INFINITY;
-        const float l = live ? ld_dev(recs + size_t(lane) * REC + kAttnMaxG + hh) : 0.0f;
-        const float mm = l > 0.0f ? m : -INFINITY;
-        const float M = wave_max(mm);
-        const float f = mm == -INFINITY ? 0.0f : exp_hw(mm - M);
-        const float L = wave_sum(l * f);
-        if (live) fs[lane][hh] = f;
-        if (lane == 0) {
-            run[0][hh] = M;
-            run[1][hh] = L;
-        }
-    }
-    __syncthreads();
-    float4 acc = float4{0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-    for (int i = 0; i < B; ++i) {
-        const uint32_t p = r + i * R;
-        const float f = p < n ? fs[p][h] : 0.0f;
-        acc.x = fmaf(__uint_as_float(v[i].x), f, acc.x);
-        acc.y = fmaf(__uint_as_float(v[i].y), f, acc.y);
-        acc.z = fmaf(__uint_as_float(v[i].z), f, acc.z);
-        acc.w = fmaf(__uint_as_float(v[i].w), f, acc.w);
-    }
-    reinterpret_cast<float4*>(&red[0][0])[r * NCOL + col] = acc;
-    __syncthreads();
-    if (tid < NCOL) {
-        const float4* r4 = reinterpret_cast<const float4*>(&red[0][0]);
-        float4 t = r4[tid];
-#pragma unroll
-        for (int q = 1; q < R; ++q) {
-            const float4 u = r4[q * NCOL + tid];
-            t.x += u.x; t.y += u.y; t.z += u.z; t.w += u.w;
-        }
-        const int hh = tid * 4 / HD;
-        if (final) {
-            const float inv = rcp_hw(run[1][hh]);
-            reinterpret_cast<float4*>(out)[tid] = float4{t.x * inv, t.y * inv, t.z * inv, t.w * inv};
-        } else {
-            float* o = rec_out + kAttnStat + tid * 4;
-            st_dev(o, t.x); st_dev(o + 1, t.y); st_dev(o + 2, t.z); st_dev(o + 3, t.w);
-        }
-    }
-    if (!final && tid < G) {
-        st_dev(rec_out + tid, run[0][tid]);
-        st_dev(rec_out + kAttnMaxG + tid, run[1][tid]);
-    }
-}
-
+// ---- decode attention (split-span, fp16 KV; the tile in xp_attn_device.hpp) ----
 template <int G, int U, bool FQ>
 __global__ __launch_bounds__(kAttnThreads) void attention_decode_kernel(AttnArgs a, RopeFreq f) {
-    constexpr int HD = kAttnHD, NV = G * U, DUP = 32 / NV, PASS = kAttnRows * U;
-    constexpr int PV = (PASS + kWave - 1) / kWave;           // softmax values per lane
-    constexpr uint32_t REC = attn_record(G);
-    static_assert(NV <= 32 && (32 % NV) == 0, "G x U partial dots over 32 lanes");
-    __shared__ float ps[G][PASS];
-    __shared__ float run[3][G];                  // running max, running sum, pass rescale
-    __shared__ __attribute__((aligned(16))) float red[kAttnThreads / kWave][G * HD];
-    __shared__ float fs[kAttnFan][G];
-    __shared__ uint32_t last;
-    {   // batched sequence blockIdx.z
-        const uint32_t b = blockIdx.z;
-        a.q += size_t(b) * a.bq;
-        a.out += size_t(b) * a.bq;
-        a.kc += b * a.bcache;
-        a.vc += b * a.bcache;
-        if (a.part) a.part += b * a.bpart;
-        if (a.tickets) a.tickets += size_t(b) * a.kv_heads * kAttnTicketsPerHead;
-    }
-    uint32_t span, kv0;
-    attn_range(a, span, kv0);
-    const uint32_t g = blockIdx.y, s = blockIdx.x;
-    // exchange mode: this launch's record tag, one past the last launch's
-    // (read before this workgroup's record is written; see the combine)
-    uint32_t xtag = 0u;
-    if (a.xchg) {
-        const uint32_t ep = ld_dev(a.tickets + size_t(g) * kAttnTicketsPerHead + kAttnEpoch);
-        xtag = ep + 1u != 0u ? ep + 1u : 1u;
-    }
-    uint32_t chunk = (span + a.nsplit - 1) / a.nsplit;
-    if (chunk < uint32_t(kAttnMinChunk)) chunk = kAttnMinChunk;
-    const uint32_t j0 = min(s * chunk, span);
-    const int nk = int(min(j0 + chunk, span) - j0);
-    const int tid = threadIdx.x, lane = tid % kWave, wave = tid / kWave;
-    const int sub = tid % kAttnLanes, kp = tid / kAttnLanes;
-    const size_t rowstride = size_t(a.kv_heads) * HD;   // fp16 elements per cache row
-    const uint16_t* kbase = a.kc + size_t(kv0 + j0) * rowstride + size_t(g) * HD + sub * 8;
-    const uint16_t* vbase = a.vc + size_t(kv0 + j0) * rowstride + size_t(g) * HD + sub * 8;
-
-    // K / V of one pass: U keys per lane, all loads in flight together
-    u32x4 kw[U], vw[U];
-    auto load_pass = [&](int c0) {
-#pragma unroll
-        for (int u = 0; u < U; ++u) {
-            const int j = c0 + kp + kAttnRows * u;
-            kw[u] = j < nk ? ldg4(kbase + size_t(j) * rowstride) : u32x4{0u, 0u, 0u, 0u};
-        }
-#pragma unroll
-        for (int u = 0; u < U; ++u) {
-            const int j = c0 + kp + kAttnRows * u;
-            vw[u] = j < nk ? ldg4(vbase + size_t(j) * rowstride) : u32x4{0u, 0u, 0u, 0u};
-        }
-    };
-    load_pass(0);   // the first pass's keys do not depend on q
-
-    float q[G][8], o[G][8];
-    // Fused QK-norm + RoPE (qk_norm_rope_append_kernel's arithmetic): waves
-    // 0 .. G-1 norm and rotate query head g G + wave, wave G the key, wave
-    // G + 1 rounds the value; lane l holds dims l + 64 c, so rotate-half pairs
-    // (d, d + 128) are (c, c + 2) of one lane. q lands in red[0], cos / sin
-    // in red[1], the fp16 key / value in red[2]; each thread then takes its
-    // eight dims into registers (red is free again before the combine). The
-    // raw rows are requested before the angles are computed, behind the
-    // first pass's K / V loads.
-    u32x4 kcur = {0u, 0u, 0u, 0u}, vcur = {0u, 0u, 0u, 0u};
-    if constexpr (FQ) {
-        const uint32_t b = blockIdx.z, pos = a.pos_dev[b];
-        float* cs = &red[1][0];
-        uint16_t* kv16 = reinterpret_cast<uint16_t*>(&red[2][0]);   // key [0, HD), value [HD, 2 HD)
-        float e[4] = {0.0f, 0.0f, 0.0f, 0.0f}, w4[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-        if (wave <= G + 1) {
-            const float* src = wave < G   ? a.q_raw + size_t(b) * a.bq + (size_t(g) * G + wave) * HD
-                               : wave == G ? a.k_raw + size_t(b) * a.bkv + size_t(g) * HD
-                                           : a.v_raw + size_t(b) * a.bkv + size_t(g) * HD;
-#pragma unroll
-            for (int c = 0; c < 4; ++c) e[c] = src[lane + 64 * c];
-            if (wave <= G) {
-                const float* w = wave < G ? a.qw : a.kw;
-#pragma unroll
-                for (int c = 0; c < 4; ++c) w4[c] = w[lane + 64 * c];
-            }
-        }
-        if (tid < HD / 2) {
-            float sv, cv;
-            sincosf(float(pos) * f.inv[tid], &sv, &cv);
-            cs[tid] = cv;
-            cs[HD / 2 + tid] = sv;
-        }
-        __syncthreads();
-        if (wave <= G) {
-            const float ss = wave_sum(e[0] * e[0] + e[1] * e[1] + e[2] * e[2] + e[3] * e[3]);
-            const float scale = rsq_hw(ss * (1.0f / float(HD)) + a.eps);
-#pragma unroll
-            for (int c = 0; c < 4; ++c) e[c] = e[c] * scale * (1.0f + w4[c]);
-#pragma unroll
-            for (int c = 0; c < 2; ++c) {
-                const float cv = cs[lane + 64 * c], sv = cs[HD / 2 + lane + 64 * c];
-                const float lo = e[c], hi = e[c + 2];
-                e[c] = lo * cv - hi * sv;
-                e[c + 2] = lo * sv + hi * cv;
-            }
-            if (wave < G) {
-#pragma unroll
-                for (int c = 0; c < 4; ++c) red[0][wave * HD + lane + 64 * c] = e[c];
-            } else {
-#pragma unroll
-                for (int c = 0; c < 4; ++c) kv16[lane + 64 * c] = f32_to_f16_bits(e[c]);
-            }
-        } else if (wave == G + 1) {
-#pragma unroll
-            for (int c = 0; c < 4; ++c) kv16[HD + lane + 64 * c] = f32_to_f16_bits(e[c]);
-        }
-        __syncthreads();
-#pragma unroll
-        for (int h = 0; h < G; ++h) {
-            const float4 q0 = *reinterpret_cast<const float4*>(&red[0][h * HD + sub * 8]);
-            const float4 q1 = *reinterpret_cast<const float4*>(&red[0][h * HD + sub * 8 + 4]);
-            q[h][0] = q0.x; q[h][1] = q0.y; q[h][2] = q0.z; q[h][3] = q0.w;
-            q[h][4] = q1.x; q[h][5] = q1.y; q[h][6] = q1.z; q[h][7] = q1.w;
-        }
-        kcur = *reinterpret_cast<const u32x4*>(kv16 + sub * 8);
-        vcur = *reinterpret_cast<const u32x4*>(kv16 + HD + sub * 8);
-        // the split holding the current position appends its key / value
-        // for later steps (this launch reads them from kcur / vcur)
-        if (span > 0 && (span - 1u) / chunk == s && tid < kAttnLanes) {
-            const size_t row = size_t(pos) * rowstride + size_t(g) * HD + sub * 8;
-            *reinterpret_cast<u32x4*>(const_cast<uint16_t*>(a.kc) + row) = kcur;
-            *reinterpret_cast<u32x4*>(const_cast<uint16_t*>(a.vc) + row) = vcur;
-        }
-        __syncthreads();   // red is rewritten by the combine
-    } else {
-#pragma unroll
-        for (int h = 0; h < G; ++h) {
-            const float4* qp = reinterpret_cast<const float4*>(a.q + (size_t(g) * G + h) * HD + sub * 8);
-            const float4 q0 = qp[0], q1 = qp[1];
-            q[h][0] = q0.x; q[h][1] = q0.y; q[h][2] = q0.z; q[h][3] = q0.w;
-            q[h][4] = q1.x; q[h][5] = q1.y; q[h][6] = q1.z; q[h][7] = q1.w;
-        }
-    }
-#pragma unroll
-    for (int h = 0; h < G; ++h)
-#pragma unroll
-        for (int e = 0; e < 8; ++e) o[h][e] = 0.0f;
-    if (tid < G) {
-        run[0][tid] = -INFINITY;
-        run[1][tid] = 0.0f;
-    }
-    for (int c0 = 0; c0 < nk; c0 += PASS) {
-        if (c0 > 0) load_pass(c0);
-        if constexpr (FQ) {
-            // the current position (the span's last key) from registers
-#pragma unroll
-            for (int u = 0; u < U; ++u) {
-                const bool cur = j0 + uint32_t(c0 + kp + kAttnRows * u) == span - 1u;
-                kw[u] = cur ? kcur : kw[u];
-                vw[u] = cur ? vcur : vw[u];
-            }
-        }
-        // ---- scores
-        float sv[NV];
-#pragma unroll
-        for (int u = 0; u < U; ++u) {
-            float kf[8];
-            f16x8(kf, kw[u]);
-#pragma unroll
-            for (int h = 0; h < G; ++h) {
-                float d = 0.0f;
-#pragma unroll
-                for (int e = 0; e < 8; ++e) d = fmaf(q[h][e], kf[e], d);
-                sv[h * U + u] = d;
-            }
-        }
-        reduce_scatter32<NV, 16>(sv, uint32_t(lane));
-        {
-            const int idx = (lane % 32) / DUP, h = idx / U, u = idx % U;
-            const int j = kp + kAttnRows * u;
-            if (lane % DUP == 0) ps[h][j] = (c0 + j < nk) ? sv[0] * a.scale : -INFINITY;
-        }
-        __syncthreads();
-        // ---- softmax of the pass, online across passes: wave h takes head h
-        if (wave < G) {
-            const int h = wave;
-            float sp[PV];
-            float mx = -INFINITY;
-#pragma unroll
-            for (int i = 0; i < PV; ++i) {
-                const int idx = lane + kWave * i;
-                sp[i] = idx < PASS ? ps[h][idx] : -INFINITY;
-                mx = fmaxf(mx, sp[i]);
-            }
-            const float mold = run[0][h];
-            const float mnew = fmaxf(mold, wave_max(mx));   // finite: key c0 is live
-            float sum = 0.0f;
-#pragma unroll
-            for (int i = 0; i < PV; ++i) {
-                const int idx = lane + kWave * i;
-                const float p = idx < PASS ? exp_hw(sp[i] - mnew) : 0.0f;
-                if (idx < PASS) ps[h][idx] = p;
-                sum += p;
-            }
-            sum = wave_sum(sum);
-            if (lane == 0) {
-                const float alpha = exp_hw(mold - mnew);   // 0 on the first pass
-                run[0][h] = mnew;
-                run[1][h] = run[1][h] * alpha + sum;
-                run[2][h] = alpha;
-            }
-        }
-        __syncthreads();
-        // ---- weighted values
-#pragma unroll
-        for (int h = 0; h < G; ++h) {
-            const float al = run[2][h];
-#pragma unroll
-            for (int e = 0; e < 8; ++e) o[h][e] *= al;
-        }
-#pragma unroll
-        for (int u = 0; u < U; ++u) {
-            float vf[8];
-            f16x8(vf, vw[u]);
-            const int j = kp + kAttnRows * u;
-#pragma unroll
-            for (int h = 0; h < G; ++h) {
-                const float p = ps[h][j];
-#pragma unroll
-                for (int e = 0; e < 8; ++e) o[h][e] = fmaf(p, vf[e], o[h][e]);
-            }
-        }
-        __syncthreads();   // ps and run[2] are rewritten by the next pass
-    }
-    // ---- sum the 16 row groups: lane pairs (l, l + 32), then the 8 waves
-#pragma unroll
-    for (int h = 0; h < G; ++h)
-#pragma unroll
-        for (int e = 0; e < 8; ++e) o[h][e] += __shfl_xor(o[h][e], 32, kWave);
-    if (lane < 32) {
-#pragma unroll
-        for (int h = 0; h < G; ++h) {
-            float4* r4 = reinterpret_cast<float4*>(&red[wave][h * HD + sub * 8]);
-            r4[0] = float4{o[h][0], o[h][1], o[h][2], o[h][3]};
-            r4[1] = float4{o[h][4], o[h][5], o[h][6], o[h][7]};
-        }
-    }
-    __syncthreads();
-    float* out = a.out + size_t(g) * G * HD;
-    if (a.nsplit == 1) {
-        for (int i = tid; i < G * HD; i += kAttnThreads) {
-            float acc = 0.0f;
-#pragma unroll
-            for (int w = 0; w < kAttnThreads / kWave; ++w) acc += red[w][i];
-            out[i] = acc / run[1][i / HD];
-        }
-        return;
-    }
-    uint32_t* tk = a.tickets + size_t(g) * kAttnTicketsPerHead;   // [0] level 2, [1 + grp] level 1
-    if (a.xchg) {
-        // ---- exchange mode (every workgroup of the launch resident at once):
-        // each split publishes its record as tagged pairs, then polls the
-        // statistics of all records and its own slice of the value dims, and
-        // writes that slice of the output — one exchange instead of the
-        // ticket chain. Split 0, once it has seen every record (so every
-        // split has read the epoch), stores this launch's tag as the epoch.
-        constexpr uint32_t NPR = G + G * HD / 2;                 // pairs per record
-        const uint32_t ns = a.nsplit;
-        float* xbase = a.part + size_t(g) * attn_head_floats(G);
-        const rsrc_t xr = make_rsrc(xbase, ns * NPR * 16u);
-        for (uint32_t i = tid; i < uint32_t(G * HD / 2); i += kAttnThreads) {
-            float v0 = 0.0f, v1 = 0.0f;
-#pragma unroll
-            for (int w = 0; w < kAttnThreads / kWave; ++w) {
-                v0 += red[w][2u * i];
-                v1 += red[w][2u * i + 1u];
-            }
-            __builtin_amdgcn_raw_buffer_store_b128(u32x4{__float_as_uint(v0), xtag, __float_as_uint(v1), xtag},
-                                                   xr, int((s * NPR + G + i) * 16u), 0, kAuxDev);
-        }
-        if (tid < G)
-            __builtin_amdgcn_raw_buffer_store_b128(
-                u32x4{__float_as_uint(run[0][tid]), xtag, __float_as_uint(run[1][tid]), xtag}, xr,
-                int((s * NPR + tid) * 16u), 0, kAuxDev);
-        constexpr uint32_t NOUT = G * HD;
-        const uint32_t D = (((NOUT + ns - 1u) / ns) + 1u) & ~1u;   // output dims a split (even)
-        const uint32_t d0 = s * D, d1 = min(d0 + D, NOUT);
-        if (d0 >= d1) return;
-        const uint32_t DD = d1 - d0, HP = DD / 2u;
-        const uint32_t nst = ns * G, np = nst + ns * HP;           // pairs to poll (<= 4 a thread)
-        if (tid == 0) last = 0u;                                   // set if a wait times out
-        __syncthreads();   // every record sum has been read from red
-        float* xm = &red[0][0];                          // [split][head] max, then the factor
-        float* xl = xm + kAttnMaxSplit * G;              // [split][head] sum of exp
-        float* xv = xl + kAttnMaxSplit * G;              // [split][DD] value dims
-        float* xp = xv + kAttnMaxSplit * G + 512;        // [group][DD] partial sums
-        static_assert(3 * kAttnMaxSplit * G + 1024 <= (kAttnThreads / kWave) * G * HD, "exchange scratch");
-        uint32_t off[4];
-        bool act[4];
-        u32x4 v[4];
-#pragma unroll
-        for (int k = 0; k < 4; ++k) {
-            const uint32_t i = tid + uint32_t(k) * kAttnThreads;
-            act[k] = i < np;
-            const uint32_t ic = act[k] ? i : 0u;
-            if (ic < nst) {
-                off[k] = ((ic / G) * NPR + ic % G) * 16u;
-            } else {
-                const uint32_t j = ic - nst;
-                off[k] = ((j / HP) * NPR + G + d0 / 2u + j % HP) * 16u;
-            }
-        }
-        const u32x4 ready = {0u, xtag, 0u, xtag};
-#pragma unroll
-        for (int k = 0; k < 4; ++k) v[k] = act[k] ? ld_dev16(xr, off[k]) : ready;
-        for (uint32_t spins = 0;; ++spins) {
-            bool ok = true;
-#pragma unroll
-            for (int k = 0; k < 4; ++k) ok &= (v[k].y == xtag) & (v[k].w == xtag);
-            if (ok) break;
-            if (spins > kAttnSpinLimit) {
-                st_dev(tk + kAttnXErr, 1u);
-                last = 1u;
-                break;
-            }
-            asm volatile("" ::: "memory");
-#pragma unroll
-            for (int k = 0; k < 4; ++k) v[k] = act[k] ? ld_dev16(xr, off[k]) : ready;
-        }
-#pragma unroll
-        for (int k = 0; k < 4; ++k) {
-            const uint32_t i = tid + uint32_t(k) * kAttnThreads;
-            if (!act[k]) continue;
-            if (i < nst) {
-                xm[i] = __uint_as_float(v[k].x);
-                xl[i] = __uint_as_float(v[k].z);
-            } else {
-                const uint32_t j = i - nst, r = j / HP, c = j % HP;
-                xv[r * DD + 2u * c] = __uint_as_float(v[k].x);
-                xv[r * DD + 2u * c + 1u] = __uint_as_float(v[k].z);
-            }
-        }
-        __syncthreads();
-        if (s == 0 && tid == 0) st_dev(tk + kAttnEpoch, xtag);
-        // wave h: head h's rescale factors exp(m_r - M) (0 for an empty
-        // split) into xm and the denominator into run[1]
-        if (wave < G) {
-            const int h = wave;
-            float m4[kAttnMaxSplit / kWave], l4[kAttnMaxSplit / kWave];
-            float mx = -INFINITY;
-#pragma unroll
-            for (int k = 0; k < kAttnMaxSplit / kWave; ++k) {
-                const uint32_t r = uint32_t(lane + kWave * k);
-                const bool in = r < ns;
-                l4[k] = in ? xl[r * G + h] : 0.0f;
-                m4[k] = in && l4[k] > 0.0f ? xm[r * G + h] : -INFINITY;
-                mx = fmaxf(mx, m4[k]);
-            }
-            const float M = wave_max(mx);
-            float ls = 0.0f;
-#pragma unroll
-            for (int k = 0; k < kAttnMaxSplit / kWave; ++k) {
-                const uint32_t r = uint32_t(lane + kWave * k);
-                const float f = m4[k] == -INFINITY ? 0.0f : exp_hw(m4[k] - M);
-                ls = fmaf(l4[k], f, ls);
-                if (r < ns) xm[r * G + h] = f;
-            }
-            ls = wave_sum(ls);
-            if (lane == 0) run[1][h] = ls;
-        }
-        __syncthreads();
-        // dim j of the slice: group q of Q threads sums records q, q + Q, ...
-        const uint32_t Q = kAttnThreads / DD, j = tid % DD, q = tid / DD;
-        if (q < Q) {
-            const uint32_t h = (d0 + j) / HD;
-            float acc = 0.0f;
-            for (uint32_t r = q; r < ns; r += Q) acc = fmaf(xm[r * G + h], xv[r * DD + j], acc);
-            xp[q * DD + j] = acc;
-        }
-        __syncthreads();
-        if (uint32_t(tid) < DD) {
-            float acc = 0.0f;
-            for (uint32_t qq = 0; qq < Q; ++qq) acc += xp[qq * DD + tid];
-            // a timed-out wait (the launch was not resident at once) leaves
-            // NaN, not a plausible value, besides the flag word
-            out[d0 + tid] = last ? __builtin_nanf("") : acc * rcp_hw(run[1][(d0 + tid) / HD]);
-        }
-        return;
-    }
-    float* part = a.part + size_t(g) * attn_head_floats(G);
-    float* rec = part + size_t(s) * REC;
-    for (int i = tid; i < G * HD; i += kAttnThreads) {
-        float acc = 0.0f;
-#pragma unroll
-        for (int w = 0; w < kAttnThreads / kWave; ++w) acc += red[w][i];
-        st_dev(rec + kAttnStat + i, acc);
-    }
-    if (tid < G) {
-        st_dev(rec + tid, run[0][tid]);                 // -inf for an empty split
-        st_dev(rec + kAttnMaxG + tid, run[1][tid]);     // 0 for an empty split
-    }
-    // ---- level 1: the last split of its group of kAttnFan combines the group
-    const uint32_t grp = s / kAttnFan, ng = (a.nsplit + kAttnFan - 1) / kAttnFan;
-    const uint32_t n1 = min(uint32_t(kAttnFan), a.nsplit - grp * kAttnFan);
-    wait_mem();
-    __syncthreads();
-    if (tid == 0) last = take_ticket(&tk[1 + grp]);
-    __syncthreads();
-    if (last != n1 - 1) return;
-    if (tid == 0) st_dev(&tk[1 + grp], 0u);
-    float* grec = part + size_t(kAttnMaxSplit + grp) * REC;
-    attn_combine<G>(part + size_t(grp) * kAttnFan * REC, n1, ng == 1, out, grec, red, fs, run);
-    if (ng == 1) return;
-    // ---- level 2: the last group combines the group records
-    wait_mem();
-    __syncthreads();
-    if (tid == 0) last = take_ticket(&tk[0]);
-    __syncthreads();
-    if (last != ng - 1) return;
-    if (tid == 0) st_dev(&tk[0], 0u);
-    attn_combine<G>(part + size_t(kAttnMaxSplit) * REC, ng, true, out, nullptr, red, fs, run);
+    __shared__ AttnSmem<G, U> sm;
+    (void)attn_tile<G, U, FQ, false>(a, f, blockIdx.x, blockIdx.y, blockIdx.z, sm);
 }
 
 // ---- elementwise ------------------------------------------------------------
@@ -780,7 +193,7 @@ size_t attn_partial_floats(uint32_t kv_heads, uint32_t n_heads, uint32_t head_di
     return size_t(kv_heads) * attn_head_floats(kv_heads ? n_heads / kv_heads : 1);
 }
 
-int launch_attention(AttnArgs a, uint32_t max_span, hipStream_t st) {
+int plan_attention(AttnArgs& a, uint32_t max_span, bool allow_xchg, int* U_out, RopeFreq* f_out) {
     if (a.head_dim != uint32_t(kAttnHD))
         return set_error(XP_E_ARG, "attention: head_dim=%u must be %d", a.head_dim, kAttnHD);
     if (a.kv_heads == 0 || a.n_heads % a.kv_heads)
@@ -810,7 +223,8 @@ int launch_attention(AttnArgs a, uint32_t max_span, hipStream_t st) {
         DeviceScratch* sc = scratch();
         if (!sc) return XP_E_HIP;
         const uint64_t wgs = uint64_t(a.nsplit) * a.kv_heads * a.batch;
-        a.xchg = xchg_on && a.nsplit > uint32_t(kAttnFan) && sc->n_cu > 0 && wgs <= uint64_t(sc->n_cu) ? 1u : 0u;
+        a.xchg = allow_xchg && xchg_on && a.nsplit > uint32_t(kAttnFan) && sc->n_cu > 0 &&
+                 wgs <= uint64_t(sc->n_cu) ? 1u : 0u;
         if (a.xchg && (!a.part || !a.tickets)) {
             // the exchange mode's own zeroed buffers, not the shared scratch
             if (!ensure_attn_x(sc, attn_partial_floats(a.kv_heads, a.n_heads, a.head_dim),
@@ -844,6 +258,17 @@ int launch_attention(AttnArgs a, uint32_t max_span, hipStream_t st) {
     } else if (!a.q) {
         return set_error(XP_E_ARG, "attention: null q");
     }
+    *U_out = U;
+    *f_out = f;
+    return XP_OK;
+}
+
+int launch_attention(AttnArgs a, uint32_t max_span, hipStream_t st) {
+    int U = 0;
+    RopeFreq f{};
+    if (int rc = plan_attention(a, max_span, true, &U, &f); rc != XP_OK) return rc;
+    const bool fq = a.q_raw != nullptr;
+    const uint32_t G = a.group;
     const dim3 grid(a.nsplit, a.kv_heads, a.batch), block(kAttnThreads);
 #define XP_ATTN_U(GG, FF)                                                                                 \
     if (U == 2) hipLaunchKernelGGL((attention_decode_kernel<GG, 2, FF>), grid, block, 0, st, a, f);      \

@@ -1,0 +1,431 @@
+// Device code of the batched decode step (up to 16 sequences, M = 16 MFMA
+// GEMMs on int4 weights), shared by its per-op kernels (batch_kernels.hip)
+// and the persistent step kernel (batch_step.hip). The layout of the
+// operands and the epilogue are described in batch_kernels.hip.
+//
+// Functions with a DEV template switch write their outputs with device-scope
+// stores when DEV is set: the persistent kernel's consumers are other
+// workgroups of the same launch, possibly on other XCDs, which read them
+// after a completion counter says they are complete.
+#pragma once
+
+#include "xp_device.hpp"
+#include "xp_launch.hpp"
+
+namespace xp {
+
+namespace {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+constexpr uint32_t kBmmThreads = 512;       // eight waves share one column group
+
+__device__ __forceinline__ bf16x8 as_bf16x8(u32x4 v) { return __builtin_bit_cast(bf16x8, v); }
+
+// The eight B-operand bf16 (128 + nibble) of one KM4 word, slot s = nibble e(s).
+__device__ __forceinline__ u32x4 widen_nibbles(uint32_t w) {
+    u32x4 d;
+    d.x = (w & 0x000F000Fu) | 0x43004300u;
+    d.y = ((w >> 4) & 0x000F000Fu) | 0x43004300u;
+    d.z = ((w >> 8) & 0x000F000Fu) | 0x43004300u;
+    d.w = ((w >> 12) & 0x000F000Fu) | 0x43004300u;
+    return d;
+}
+
+template <int FMT>
+__device__ __forceinline__ float quad_scale(u32x2 raw, uint32_t i) {
+    const uint32_t w = (i & 2u) ? raw.y : raw.x;
+    const uint32_t h = (w >> (16u * (i & 1u))) & 0xFFFFu;
+    if constexpr (FMT == XP_SCALE_F16_QUAD) return f16_bits_to_f32(h);
+    else return __uint_as_float(h << 16);
+}
+
+__device__ __forceinline__ uint32_t bf16_bits_rn(float f) {
+    return uint32_t(__builtin_bit_cast(uint16_t, __bf16(f)));
+}
+
+
+
+// ---- staging -------------------------------------------------------------------
+// Word c of staged block blk for row b from its eight elements v (k = 32 blk +
+// 8 c + 0..7): the hi / lo bf16 operand of lane b + 16 c in slot order
+// (slot s <- element s / 2 + 4 (s % 2)), and, from the four words of the
+// block held by four adjacent lanes (c = lane % 4, whole quads active), the
+// block's sum of hi + lo for row b.
+template <bool DEV = false>
+__device__ __forceinline__ void stage_word(u32x4* A, float* asum, uint32_t blk, uint32_t c, uint32_t b,
+                                           const float (&v)[8]) {
+    uint32_t hi[8], lo[8];
+    float sum = 0.0f;
+#pragma unroll
+    for (int sl = 0; sl < 8; ++sl) {
+        const float t = v[sl / 2 + 4 * (sl % 2)];
+        const uint32_t h = bf16_bits_rn(t);
+        const float hf = __uint_as_float(h << 16);
+        const uint32_t l = bf16_bits_rn(t - hf);
+        hi[sl] = h;
+        lo[sl] = l;
+        sum += hf + __uint_as_float(l << 16);
+    }
+    const u32x4 H{hi[0] | (hi[1] << 16), hi[2] | (hi[3] << 16), hi[4] | (hi[5] << 16),
+                  hi[6] | (hi[7] << 16)};
+    const u32x4 L{lo[0] | (lo[1] << 16), lo[2] | (lo[3] << 16), lo[4] | (lo[5] << 16),
+                  lo[6] | (lo[7] << 16)};
+    const uint32_t lane = b + 16u * c;
+    st_u4<DEV>(A + (size_t(blk) * 2 + 0) * 64 + lane, H);
+    st_u4<DEV>(A + (size_t(blk) * 2 + 1) * 64 + lane, L);
+    sum += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(sum), 0xB1, 0xF, 0xF, false));
+    sum += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(sum), 0x4E, 0xF, 0xF, false));
+    if (c == 0) st_f<DEV>(asum + size_t(blk) * 16 + b, sum);
+}
+
+// One workgroup per sequence b; thread i holds elements 8 p .. 8 p + 7 for p =
+// i, i + 1024, ... (every width here is one pass) in registers from the load
+// through the norms to the staged operand. Modes (x, y: [batch][K] fp32, row b):
+//   0  stage rmsnorm(x) (1 + w_pre)
+//   1  x += rmsnorm(y) (1 + w_post) (written back), then stage rmsnorm(x) (1 + w_pre)
+//   2  stage y
+//   3  stage gelu_tanh(y) * u
+// Staged: A[blk][0 / 1][lane] = the hi / lo bf16 operand of lane l = b + 16 c
+// for k = 32 blk + 8 c + e(s); asum[blk][b] = sum of hi + lo over the block.
+__device__ __forceinline__ void ld8f(float (&v)[8], const float* p) {
+    const float4 a = *reinterpret_cast<const float4*>(p), b = *reinterpret_cast<const float4*>(p + 4);
+    v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w; v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+}
+
+template <uint32_t NT, bool DEV>
+__device__ __forceinline__ void prep_row(const BprepArgs& a, uint32_t b, float (&red)[2][NT / kWave]) {
+    const uint32_t tid = DEV ? opaque_tid() : threadIdx.x;
+    const uint32_t K = a.K, npair = K / 8;    // (block, word) pairs of eight elements
+    const uint32_t p = tid;
+    const bool own = p < npair;
+    float* x = a.x ? a.x + size_t(b) * K : nullptr;
+    const float* y = a.y ? a.y + size_t(b) * K : nullptr;
+    const float* u = a.u ? a.u + size_t(b) * K : nullptr;
+    auto bsum = [&](float v, int slot) {
+        v = wave_sum(v);
+        if (tid % kWave == 0) red[slot][tid / kWave] = v;
+        __syncthreads();
+        float t = 0.0f;
+#pragma unroll
+        for (int w = 0; w < int(NT / kWave); ++w) t += red[slot][w];
+        return t;
+    };
+    float v[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
+    if (a.mode <= 1) {
+        float xv[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f}, wpre[8];
+        if (own) {
+            ld8f(xv, x + 8 * p);
+            ld8f(wpre, a.w_pre + 8 * p);
+        }
+        if (a.mode == 1) {
+            float yv[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f}, wpost[8];
+            if (own) {
+                ld8f(yv, y + 8 * p);
+                ld8f(wpost, a.w_post + 8 * p);
+            }
+            float ss = 0.0f;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) ss = fmaf(yv[e], yv[e], ss);
+            const float post = rsq_hw(bsum(ss, 0) / float(K) + a.eps);
+            if (own) {
+#pragma unroll
+                for (int e = 0; e < 8; ++e) xv[e] = xv[e] + yv[e] * post * (1.0f + wpost[e]);
+                float4* xo = reinterpret_cast<float4*>(a.x_out ? a.x_out + size_t(b) * K + 8 * p : x + 8 * p);
+                st_u4<DEV>(reinterpret_cast<u32x4*>(xo),
+                           u32x4{__float_as_uint(xv[0]), __float_as_uint(xv[1]), __float_as_uint(xv[2]),
+                                 __float_as_uint(xv[3])});
+                st_u4<DEV>(reinterpret_cast<u32x4*>(xo + 1),
+                           u32x4{__float_as_uint(xv[4]), __float_as_uint(xv[5]), __float_as_uint(xv[6]),
+                                 __float_as_uint(xv[7])});
+            }
+        }
+        float sx = 0.0f;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) sx = fmaf(xv[e], xv[e], sx);
+        const float pre = rsq_hw(bsum(sx, 1) / float(K) + a.eps);
+        if (own) {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) v[e] = xv[e] * pre * (1.0f + wpre[e]);
+        }
+    } else if (own) {
+        ld8f(v, y + 8 * p);
+        if (a.mode == 3) {
+            float uv[8];
+            ld8f(uv, u + 8 * p);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) v[e] = gelu_hw(v[e]) * uv[e];
+        }
+    }
+    if (!own) return;
+    stage_word<DEV>(static_cast<u32x4*>(a.a), a.asum, p / 4u, p % 4u, b, v);
+}
+
+// ---- M = 16 int4 GEMM ------------------------------------------------------------
+// Workgroup (cb, s): a block of 16 T columns (T MFMA tiles: 4 = one 64-column
+// KM4 group, 1 = a quarter of one, for narrow shapes whose groups alone would
+// leave most CUs idle), k split s; its eight waves take consecutive chunks of
+// kc <= kBmmMaxPerWave blocks, load every operand of their chunk at once (one
+// memory latency per wave, not one per block), and sum their 16 x 16 T
+// results through LDS in wave order. With nsplit > 1 the splits publish
+// partials and the last to arrive (ticket per column block) adds them in
+// split order.
+constexpr uint32_t kBmmWaves = 8;
+constexpr uint32_t kBmmMaxPerWave = 5;
+
+// The staged operand of one block from fp32 rows, in registers (the same
+// values and slot order bprep_kernel writes): lane l holds row l % 16 and k =
+// 32 blk + 8 (l / 16) + e(s); as = the block sums of rows 4 (l / 16) + 0..3.
+__device__ __forceinline__ void stage_regs(u32x4& H, u32x4& L, float4& as, const float (&v)[8],
+                                           uint32_t wsel) {
+    uint32_t hi[8], lo[8];
+    float sum = 0.0f;
+#pragma unroll
+    for (int sl = 0; sl < 8; ++sl) {
+        const float t = v[sl / 2 + 4 * (sl % 2)];
+        const uint32_t h = bf16_bits_rn(t);
+        const float hf = __uint_as_float(h << 16);
+        const uint32_t l = bf16_bits_rn(t - hf);
+        hi[sl] = h;
+        lo[sl] = l;
+        sum += hf + __uint_as_float(l << 16);
+    }
+    H = u32x4{hi[0] | (hi[1] << 16), hi[2] | (hi[3] << 16), hi[4] | (hi[5] << 16), hi[6] | (hi[7] << 16)};
+    L = u32x4{lo[0] | (lo[1] << 16), lo[2] | (lo[3] << 16), lo[4] | (lo[5] << 16), lo[6] | (lo[7] << 16)};
+    // the row's block sum over its four 8-element groups (lanes 16 apart),
+    // added as bprep_kernel adds them: (g0 + g1) + (g2 + g3)
+    sum += __shfl_xor(sum, 16, kWave);
+    sum += __shfl_xor(sum, 32, kWave);
+    as = float4{__shfl(sum, int(4 * wsel + 0), kWave), __shfl(sum, int(4 * wsel + 1), kWave),
+                __shfl(sum, int(4 * wsel + 2), kWave), __shfl(sum, int(4 * wsel + 3), kWave)};
+}
+
+template <int T>
+struct BmmSmem {
+    float red[kBmmWaves][256u * T];
+    uint32_t last;
+};
+
+// One workgroup's tile: column block cb (of ncb) and k split s. Returns true
+// when this workgroup wrote final outputs (every tile without k splits; with
+// splits, the last split of its column block to arrive). DEV: outputs go out
+// with device-scope stores (read by other workgroups of the same launch).
+template <int FMT, int T, int AM, bool GE, bool DEV>
+__device__ __forceinline__ bool bmm_tile(const BmmArgs& a, uint32_t cb, uint32_t s, uint32_t ncb,
+                                         BmmSmem<T>& sm) {
+    constexpr uint32_t NO = 256u * T;            // outputs of a workgroup: 16 rows x 16 T columns
+    constexpr uint32_t PER = (NO + kBmmThreads - 1) / kBmmThreads;
+    constexpr uint32_t SUBS = 4u / T;            // column blocks per 64-column group
+    static_assert(!GE || (T == 4 && AM == 0), "the GeGLU epilogue takes four tiles of staged A");
+    auto& red = sm.red;
+    uint32_t& last = sm.last;
+    const uint32_t tid = DEV ? opaque_tid() : threadIdx.x;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(tid / kWave), lane = tid % kWave;
+    // GE: columns 32 (cb % 2) .. + 31 of group cb / 2 of both matrices;
+    // tiles 0, 1 from the gate, 2, 3 from the up projection
+    const uint32_t gg = GE ? cb / 2u : cb / SUBS;
+    const uint32_t c16 = GE ? (cb % 2u) * 32u : (cb % SUBS) * 16u * T;   // first column in the group
+    // the matrix of column group gg, chosen without indexing the argument
+    // arrays by a variable (so that a copy of them can live in registers)
+    MvMatDesc md = a.mats[0];
+    uint32_t g0 = 0;
+    if constexpr (!GE) {
+#pragma unroll
+        for (uint32_t i = 1; i < 4; ++i)
+            if (i < a.n_mats && gg >= a.groups[i]) {
+                md = a.mats[i];
+                g0 = a.groups[i];
+            }
+    }
+    const uint32_t g = gg - g0;
+    const uint32_t cols = md.cols;
+    const uint32_t* wq = static_cast<const uint32_t*>(md.wq);
+    const u32x2* sq = static_cast<const u32x2*>(md.sc);
+    const u32x4* A = static_cast<const u32x4*>(a.a);
+    const uint32_t col16 = lane % 16u, wsel = lane / 16u;
+    const uint32_t kb0 = min((s * kBmmWaves + wave) * a.kc, a.nblk);
+    const uint32_t kb1 = min(kb0 + a.kc, a.nblk);
+    f32x4 acc[T];
+#pragma unroll
+    for (int t = 0; t < T; ++t) acc[t] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    // operands of one block (raw fp32 rows in AM 2 / 3, staged after the loads)
+    constexpr int NR = AM == 3 ? 4 : (AM == 2 ? 2 : 1);
+    struct Ops {
+        u32x4 hi, lo;
+        float4 as;
+        float4 raw[NR];
+        uint32_t w[T];
+        u32x2 sc[T];
+    };
+    auto load = [&](Ops& o, uint32_t blk) {
+        if constexpr (AM == 0) {
+            o.hi = A[(size_t(blk) * 2 + 0) * 64 + lane];
+            o.lo = A[(size_t(blk) * 2 + 1) * 64 + lane];
+            o.as = *reinterpret_cast<const float4*>(a.asum + size_t(blk) * 16 + 4u * wsel);
+        } else {
+            // row col16 (sequences past a.rows read as zeros), k 32 blk + 8 wsel ..
+#pragma unroll
+            for (int i = 0; i < NR; ++i) o.raw[i] = float4{0.0f, 0.0f, 0.0f, 0.0f};
+            if (col16 < a.rows) {
+                const size_t off = size_t(col16) * a.lda + size_t(blk) * kBlk + 8u * wsel;
+                const float4* xa4 = reinterpret_cast<const float4*>(a.xa + off);
+                o.raw[0] = xa4[0];
+                o.raw[1] = xa4[1];
+                if constexpr (AM == 3) {
+                    const float4* xu4 = reinterpret_cast<const float4*>(a.xu + off);
+                    o.raw[2] = xu4[0];
+                    o.raw[3] = xu4[1];
+                }
+            }
+        }
+#pragma unroll
+        for (int t = 0; t < T; ++t) {
+            if constexpr (GE) {
+                const uint32_t mt = uint32_t(t) / 2u;
+                const uint32_t cg = c16 + 16u * (uint32_t(t) % 2u) + col16;
+                const uint32_t* wt = static_cast<const uint32_t*>(a.mats[mt].wq);
+                const u32x2* st = static_cast<const u32x2*>(a.mats[mt].sc);
+                o.w[t] = __builtin_nontemporal_load(wt + ((size_t(g) * a.nblk + blk) * kGrp + cg) * 4 + wsel);
+                o.sc[t] = st[size_t(blk / 4) * cols + g * kGrp + cg];
+            } else {
+                const uint32_t cg = c16 + 16u * t + col16;   // column within the group
+                o.w[t] = __builtin_nontemporal_load(wq + ((size_t(g) * a.nblk + blk) * kGrp + cg) * 4 + wsel);
+                o.sc[t] = sq[size_t(blk / 4) * cols + g * kGrp + cg];
+            }
+        }
+    };
+    Ops ops[kBmmMaxPerWave];
+#pragma unroll
+    for (uint32_t j = 0; j < kBmmMaxPerWave; ++j)
+        if (kb0 + j < kb1) load(ops[j], kb0 + j);
+#pragma unroll
+    for (uint32_t j = 0; j < kBmmMaxPerWave; ++j) {
+        if (kb0 + j >= kb1) break;
+        const uint32_t blk = kb0 + j;
+        Ops& cur = ops[j];
+        if constexpr (AM != 0) {
+            float v[8] = {cur.raw[0].x, cur.raw[0].y, cur.raw[0].z, cur.raw[0].w,
+                          cur.raw[1].x, cur.raw[1].y, cur.raw[1].z, cur.raw[1].w};
+            if constexpr (AM == 3) {
+                const float u[8] = {cur.raw[2].x, cur.raw[2].y, cur.raw[2].z, cur.raw[2].w,
+                                    cur.raw[3].x, cur.raw[3].y, cur.raw[3].z, cur.raw[3].w};
+#pragma unroll
+                for (int e = 0; e < 8; ++e) v[e] = gelu_hw(v[e]) * u[e];
+            }
+            stage_regs(cur.hi, cur.lo, cur.as, v, wsel);
+        }
+        const bf16x8 ahi = as_bf16x8(cur.hi), alo = as_bf16x8(cur.lo);
+        const float corr[4] = {136.0f * cur.as.x, 136.0f * cur.as.y, 136.0f * cur.as.z, 136.0f * cur.as.w};
+#pragma unroll
+        for (int t = 0; t < T; ++t) {
+            const bf16x8 bw = as_bf16x8(widen_nibbles(cur.w[t]));
+            f32x4 c = {0.0f, 0.0f, 0.0f, 0.0f};
+            c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ahi, bw, c, 0, 0, 0);
+            c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(alo, bw, c, 0, 0, 0);
+            const float f = quad_scale<FMT>(cur.sc[t], blk % 4u);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) acc[t][r] = fmaf(f, c[r] - corr[r], acc[t][r]);
+        }
+    }
+    // o = lane * 4 T + t * 4 + r  <->  row 4 (lane / 16) + r, column 16 t + lane % 16
+#pragma unroll
+    for (int t = 0; t < T; ++t)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) red[wave][lane * 4u * T + t * 4 + r] = acc[t][r];
+    __syncthreads();
+    if constexpr (GE) {
+        // h[row][j] = gelu_tanh(gate) * up for the 16 rows x 32 columns, one
+        // per thread (gate tile j / 16 at o, up tile j / 16 + 2 at o + 8),
+        // each summed over the waves in order; then staged as operand block
+        // cb of the following GEMM (rows past a.rows as zeros)
+        float* hb = &red[0][0];   // [16][32] after the barrier below
+        const uint32_t row = tid / 32u, j = tid % 32u;
+        const uint32_t ol = 16u * (row / 4u) + j % 16u, t = j / 16u;
+        const uint32_t og = ol * 4u * T + t * 4u + row % 4u;
+        float gs = 0.0f, us = 0.0f;
+#pragma unroll
+        for (int w = 0; w < int(kBmmWaves); ++w) {
+            gs += red[w][og];
+            us += red[w][og + 8u];
+        }
+        const float h = row < a.rows ? gelu_hw(gs) * us : 0.0f;
+        __syncthreads();
+        hb[row * 32u + j] = h;
+        __syncthreads();
+        if (tid < 64u) {
+            const uint32_t b = tid / 4u, c = tid % 4u;
+            float v[8];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) v[e] = hb[b * 32u + 8u * c + e];
+            stage_word<DEV>(static_cast<u32x4*>(const_cast<void*>(a.a_out)), a.asum_out, cb, c, b, v);
+        }
+        return true;
+    }
+    float v[PER];
+    uint32_t row[PER], col[PER];
+    bool own[PER];
+#pragma unroll
+    for (uint32_t j = 0; j < PER; ++j) {
+        const uint32_t o = tid + j * kBmmThreads;
+        own[j] = o < NO;
+        const uint32_t oc = own[j] ? o : 0u;
+        float sum = 0.0f;
+#pragma unroll
+        for (int w = 0; w < int(kBmmWaves); ++w) sum += red[w][oc];
+        v[j] = sum;
+        const uint32_t ol = oc / (4u * T), ot = (oc % (4u * T)) / 4u, orr = oc % 4u;
+        row[j] = 4u * (ol / 16u) + orr;
+        col[j] = g * kGrp + c16 + 16u * ot + ol % 16u;
+    }
+    float* out = md.out;
+    if (a.nsplit == 1) {
+#pragma unroll
+        for (uint32_t j = 0; j < PER; ++j)
+            if (own[j] && row[j] < a.rows) st_f<DEV>(out + size_t(row[j]) * cols + col[j], v[j]);
+        return true;
+    }
+    float* part = a.part + (size_t(s) * ncb + cb) * NO;
+#pragma unroll
+    for (uint32_t j = 0; j < PER; ++j)
+        if (own[j]) st_dev(part + tid + j * kBmmThreads, v[j]);
+    wait_mem();
+    __syncthreads();
+    if (tid == 0) last = take_ticket(a.tickets + cb);
+    __syncthreads();
+    if (last != a.nsplit - 1) return false;
+    // last arrival: every split's partial, loaded together, added in split order
+#pragma unroll
+    for (uint32_t j = 0; j < PER; ++j) {
+        if (!own[j]) continue;
+        float sum = 0.0f;
+        for (uint32_t p0 = 0; p0 < a.nsplit; p0 += 8) {
+            float pv[8];
+#pragma unroll
+            for (uint32_t q = 0; q < 8; ++q)
+                pv[q] = p0 + q < a.nsplit
+                            ? ld_dev(a.part + (size_t(p0 + q) * ncb + cb) * NO + tid + j * kBmmThreads)
+                            : 0.0f;
+#pragma unroll
+            for (uint32_t q = 0; q < 8; ++q)
+                if (p0 + q < a.nsplit) sum += pv[q];
+        }
+        if (row[j] < a.rows) st_f<DEV>(out + size_t(row[j]) * cols + col[j], sum);
+    }
+    if (tid == 0) st_dev(a.tickets + cb, 0u);
+    return true;
+}
+
+// Streamed M = 16 GEMM for wide matrices (the batched lm_head: 4096 column
+// groups of a 1152-long k): a persistent grid of one workgroup per CU takes
+// column groups wg, wg + grid, ...; wave w keeps the staged operand of its
+// k blocks (nblk / 8 or one more, at most 5: at most two scale quads) in
+// registers for every group and keeps the weights of the next group in
+// flight while it multiplies the current ones, so the stream never waits on
+// a workgroup's launch or reduction. The eight waves' partial tiles meet in
+// LDS, double buffered (one barrier a group), and are added in wave order
+// as bmm_int4_kernel adds them. The groups rotate through two weight
+
+}  // namespace
+
+}  // namespace xp

@@ -167,6 +167,35 @@ __device__ __forceinline__ unsigned long long ld_dev64(const unsigned long long*
     return __hip_atomic_load((XP_GLOBAL unsigned long long*)p, __ATOMIC_RELAXED,
                              __HIP_MEMORY_SCOPE_AGENT);
 }
+// threadIdx.x through an opaque copy: values derived from it are computed
+// where they are used, not hoisted out of an enclosing loop by the compiler
+// (a persistent kernel that runs many different tiles in a loop would
+// otherwise keep every tile's per-thread offsets live at once).
+__device__ __forceinline__ uint32_t opaque_tid() {
+    uint32_t v = threadIdx.x;
+    asm volatile("" : "+v"(v));
+    return v;
+}
+
+// A store that is plain (DEV false) or device-scope (DEV true: read by
+// other workgroups of the same launch after a completion signal); 16 bytes
+// as two 8-byte device-scope stores.
+template <bool DEV>
+__device__ __forceinline__ void st_f(float* p, float v) {
+    if constexpr (DEV) st_dev(p, v);
+    else *p = v;
+}
+template <bool DEV>
+__device__ __forceinline__ void st_u4(u32x4* p, u32x4 v) {
+    if constexpr (DEV) {
+        unsigned long long* q = reinterpret_cast<unsigned long long*>(p);
+        st_dev64(q, (static_cast<unsigned long long>(v.y) << 32) | v.x);
+        st_dev64(q + 1, (static_cast<unsigned long long>(v.w) << 32) | v.z);
+    } else {
+        *p = v;
+    }
+}
+
 // Raw buffer resources for 16-byte device-scope accesses. Cache policy sc1
 // (aux 16) writes through to, and reads from, the point where all XCDs are
 // coherent; word 3 describes a raw (untyped, unswizzled) gfx9 buffer.

@@ -128,6 +128,10 @@ constexpr uint32_t kAttnTicketsPerHead = 19;
 uint32_t attn_splits(uint32_t max_span, uint32_t batch, uint32_t kv_heads);
 size_t attn_partial_floats(uint32_t kv_heads, uint32_t n_heads, uint32_t head_dim);
 int launch_attention(AttnArgs a, uint32_t max_span, hipStream_t st);
+// launch_attention's plan without the launch: fills group, nsplit, xchg (only
+// with allow_xchg), a fallback part / tickets, and returns the keys per lane
+// per pass (U) and the layer's RoPE frequencies.
+int plan_attention(AttnArgs& a, uint32_t max_span, bool allow_xchg, int* U_out, RopeFreq* f_out);
 
 // ---- sampling ----
 constexpr int kAmMaxWg = 256;
@@ -156,6 +160,7 @@ struct BprepArgs {
     float* asum;               // [K/32][16]
     uint32_t K;
     float eps;
+    float* x_out = nullptr;    // modes 0, 1: the updated x goes here instead of x (same layout)
 };
 int launch_bprep(const BprepArgs& a, uint32_t batch, hipStream_t st);
 int launch_bembed(float* x, const void* wq, const void* sc, int fmt, uint32_t hidden, uint32_t vocab,
@@ -195,6 +200,46 @@ struct BmmArgs {
 uint32_t bmm_split(uint32_t total_cols, uint32_t nblk, int n_cu);
 size_t bmm_partial_floats(uint32_t total_cols, uint32_t nblk, int n_cu);
 int launch_bmm(BmmArgs a, int fmt, int n_cu, hipStream_t st, const char* who);
+// launch_bmm's plan for the tiled kernel (not the streamed one): fills
+// groups, n_colwg, nsplit and kc, and returns the column blocks and whether
+// they are quarter groups (one MFMA tile) or whole groups (four).
+int plan_bmm(BmmArgs& a, int fmt, int n_cu, const char* who, uint32_t* n_blocks, bool* quarter);
+
+// ---- persistent batched decode step (batch_step.hip) ----
+// One launch runs every layer of a batched decode step: one 512-thread
+// workgroup per CU walks the stages of each layer (q|k|v GEMM, attention,
+// o GEMM, staging, gate|up GEMM, down GEMM, staging) and takes the tiles of
+// each stage the per-op kernels would run as workgroups. A stage's outputs
+// are written with device-scope stores, then each tile stores the launch's
+// tag in its own flag word; a stage's first tile on a workgroup waits
+// (bounded) for every flag of the stage before. Per-layer argument blocks come from the per-op path's plans.
+constexpr uint32_t kBsStages = 7;   // qkv, attention, o, staging, gate|up, down, staging
+constexpr uint32_t kBsMaxTiles = 512;   // tiles of one stage (one flag per waiting thread)
+struct BstepLayer {
+    BmmArgs qkv, o, gu, dn;      // planned by plan_bmm (qkv, o, dn quarter blocks)
+    AttnArgs att;                // planned by plan_attention
+    BprepArgs prep1, prep2;      // mode 1, x_out set
+    uint32_t att_u;              // keys per lane per pass (2, 4 or 8)
+    uint32_t att_rope;           // index of the layer's RoPE frequencies
+    uint32_t n_att;              // attention tiles (nsplit x kv heads x batch)
+};
+struct BstepArgs {
+    const BstepLayer* layers;    // [n_layers], device memory, read-only while the kernel runs
+    const RopeFreq* rope;        // [2] local, global
+    uint32_t n_layers, batch;
+    uint32_t ncb_qkv, ncb_o, ncb_dn, ns_dn, n_gu;   // column blocks; the down GEMM's k splits; gate|up tiles
+    uint32_t* flags;             // [n_layers][kBsStages][kBsMaxTiles] tile flags (last launch's tag)
+    uint32_t* epoch;             // the last launch's tag
+    uint32_t* status;            // set when a wait ran past spin_limit
+    uint32_t spin_limit;
+    // Stage timeline (null: off): s_memrealtime (100 MHz) of each workgroup
+    // at [((l kBsStages + k) 2 + e) grid + wg], e = 0 when its inputs of
+    // stage k were ready, 1 when its last tile of the stage ended (0 when it
+    // had none); then its start at [n_layers kBsStages 2 grid + wg].
+    unsigned long long* trace;
+};
+int launch_bstep(const BstepArgs& a, int fmt, uint32_t grid, hipStream_t st);
+int bstep_occupancy(int fmt, int* blocks_per_cu);
 
 // ---- a decode session's device weights, for the batch (session.cpp) ----
 constexpr int kMaxSessionLayers = 64;
