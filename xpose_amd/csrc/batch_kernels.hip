@@ -69,6 +69,16 @@ __global__ __launch_bounds__(kBmmThreads) void bmm_int4_kernel(BmmArgs a) {
     (void)bmm_tile<FMT, T, AM, GE, false>(a, blockIdx.x, blockIdx.y, gridDim.x, sm);
 }
 
+// Streamed M = 16 GEMM for wide matrices (the batched lm_head: 4096 column
+// groups of a 1152-long k): a persistent grid of one workgroup per CU takes
+// column groups wg, wg + grid, ...; wave w keeps the staged operand of its
+// k blocks (nblk / 8 or one more, at most 5: at most two scale quads) in
+// registers for every group and keeps the weights of the next group in
+// flight while it multiplies the current ones, so the stream never waits on
+// a workgroup's launch or reduction. The eight waves' partial tiles meet in
+// LDS, double buffered (one barrier a group), and are added in wave order
+// as bmm_int4_kernel adds them. The groups rotate through two weight
+// buffers in an unrolled ring so that each keeps fixed registers.
 template <int FMT>
 __global__ __launch_bounds__(kBmmThreads) void bmm_stream_kernel(BmmArgs a) {
     constexpr int MB = int(kBmmMaxPerWave);
@@ -178,7 +188,7 @@ __global__ __launch_bounds__(kBmmThreads) void bmm_stream_kernel(BmmArgs a) {
     }
 }
 
-
+// Position advance for every sequence of a batch.
 __global__ void badvance_kernel(uint32_t* pos, uint32_t n) {
     const uint32_t i = threadIdx.x;
     if (i < n) pos[i] += 1u;
