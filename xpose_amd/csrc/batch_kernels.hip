@@ -15,9 +15,11 @@
 //   A operand  lane l holds sequence l % 16 and the same eight k in the same
 //              slot order, as two bf16 terms x = hi + lo (|x - hi - lo| <=
 //              2^-18 |x|), staged once per step by bprep_kernel.
-//   epilogue   C = A_hi B + A_lo B over the block, then
-//              y += scale(block, column) * (C - 136 * sum_k (hi + lo)),
-//              which removes the +128 magic and the nibble bias of 8.
+//   epilogue   C = A_hi B + A_lo B - 136 * sum_k (hi + lo) over the block
+//              (the correction is the accumulator's start value, which saves
+//              four VALU subtractions a tile and block), then
+//              y += scale(block, column) * C, which removes the +128 magic
+//              and the nibble bias of 8.
 //
 // Each wave owns one 64-column KM4 group (four 16-column MFMA tiles); the four
 // waves of a workgroup share a k chunk whose staged A blocks pass through LDS.
@@ -142,12 +144,12 @@ __global__ __launch_bounds__(kBmmThreads) void bmm_stream_kernel(BmmArgs a) {
 #pragma unroll
             for (int t = 0; t < 4; ++t) {
                 const bf16x8 bw = as_bf16x8(widen_nibbles(cur.w[j][t]));
-                f32x4 c = {0.0f, 0.0f, 0.0f, 0.0f};
+                f32x4 c = {-corr[0], -corr[1], -corr[2], -corr[3]};   // bias correction as the start value
                 c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(hi, bw, c, 0, 0, 0);
                 c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(lo, bw, c, 0, 0, 0);
                 const float f = quad_scale<FMT>(second ? cur.sc[1][t] : cur.sc[0][t], blk % 4u);
 #pragma unroll
-                for (int r = 0; r < 4; ++r) acc[t][r] = fmaf(f, c[r] - corr[r], acc[t][r]);
+                for (int r = 0; r < 4; ++r) acc[t][r] = fmaf(f, c[r], acc[t][r]);
             }
         }
         // o = lane * 16 + t * 4 + r  <->  row 4 (lane / 16) + r, column 16 t + lane % 16

@@ -320,12 +320,13 @@ __device__ __forceinline__ bool bmm_tile(const BmmArgs& a, uint32_t cb, uint32_t
 #pragma unroll
         for (int t = 0; t < T; ++t) {
             const bf16x8 bw = as_bf16x8(widen_nibbles(cur.w[t]));
-            f32x4 c = {0.0f, 0.0f, 0.0f, 0.0f};
+            // the bias correction enters as the accumulator's start value
+            f32x4 c = {-corr[0], -corr[1], -corr[2], -corr[3]};
             c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ahi, bw, c, 0, 0, 0);
             c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(alo, bw, c, 0, 0, 0);
             const float f = quad_scale<FMT>(cur.sc[t], blk % 4u);
 #pragma unroll
-            for (int r = 0; r < 4; ++r) acc[t][r] = fmaf(f, c[r] - corr[r], acc[t][r]);
+            for (int r = 0; r < 4; ++r) acc[t][r] = fmaf(f, c[r], acc[t][r]);
         }
     }
     // o = lane * 4 T + t * 4 + r  <->  row 4 (lane / 16) + r, column 16 t + lane % 16
