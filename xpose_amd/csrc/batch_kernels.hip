@@ -109,6 +109,7 @@ __global__ __launch_bounds__(kBmmThreads) void bmm_stream_kernel(BmmArgs a) {
     const uint32_t* wq = static_cast<const uint32_t*>(a.mats[0].wq);
     const u32x2* sq = static_cast<const u32x2*>(a.mats[0].sc);
     float* out = a.mats[0].out;
+    const NibConst nk = nib_const();
     struct Wt {
         uint32_t w[MB][4];
         u32x2 sc[2][4];                                 // scale quads q0, q0 + 1
@@ -143,7 +144,7 @@ __global__ __launch_bounds__(kBmmThreads) void bmm_stream_kernel(BmmArgs a) {
             const bool second = blk / 4u != q0;
 #pragma unroll
             for (int t = 0; t < 4; ++t) {
-                const bf16x8 bw = as_bf16x8(widen_nibbles(cur.w[j][t]));
+                const bf16x8 bw = as_bf16x8(widen_nibbles(cur.w[j][t], nk));
                 f32x4 c = {-corr[0], -corr[1], -corr[2], -corr[3]};   // bias correction as the start value
                 c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(hi, bw, c, 0, 0, 0);
                 c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(lo, bw, c, 0, 0, 0);

@@ -23,13 +23,27 @@ constexpr uint32_t kBmmThreads = 512;       // eight waves share one column grou
 
 __device__ __forceinline__ bf16x8 as_bf16x8(u32x4 v) { return __builtin_bit_cast(bf16x8, v); }
 
+// The constants of widen_nibbles in registers the compiler cannot fold: the
+// mask in a scalar register, the bf16 128 pair in a vector register. Then
+// (w & mask) | magic is one v_and_or_b32 (gfx9's three-operand encoding has
+// no literal and takes one scalar operand, so with both constants as
+// literals it became a separate AND and OR).
+struct NibConst {
+    uint32_t mask, magic;
+};
+__device__ __forceinline__ NibConst nib_const() {
+    NibConst k{0x000F000Fu, 0x43004300u};
+    asm volatile("" : "+s"(k.mask));
+    asm volatile("" : "+v"(k.magic));
+    return k;
+}
 // The eight B-operand bf16 (128 + nibble) of one KM4 word, slot s = nibble e(s).
-__device__ __forceinline__ u32x4 widen_nibbles(uint32_t w) {
+__device__ __forceinline__ u32x4 widen_nibbles(uint32_t w, NibConst k) {
     u32x4 d;
-    d.x = (w & 0x000F000Fu) | 0x43004300u;
-    d.y = ((w >> 4) & 0x000F000Fu) | 0x43004300u;
-    d.z = ((w >> 8) & 0x000F000Fu) | 0x43004300u;
-    d.w = ((w >> 12) & 0x000F000Fu) | 0x43004300u;
+    d.x = (w & k.mask) | k.magic;
+    d.y = ((w >> 4) & k.mask) | k.magic;
+    d.z = ((w >> 8) & k.mask) | k.magic;
+    d.w = ((w >> 12) & k.mask) | k.magic;
     return d;
 }
 
@@ -295,6 +309,7 @@ __device__ __forceinline__ bool bmm_tile(const BmmArgs& a, uint32_t cb, uint32_t
             }
         }
     };
+    const NibConst nk = nib_const();
     Ops ops[kBmmMaxPerWave];
 #pragma unroll
     for (uint32_t j = 0; j < kBmmMaxPerWave; ++j)
@@ -319,7 +334,7 @@ __device__ __forceinline__ bool bmm_tile(const BmmArgs& a, uint32_t cb, uint32_t
         const float corr[4] = {136.0f * cur.as.x, 136.0f * cur.as.y, 136.0f * cur.as.z, 136.0f * cur.as.w};
 #pragma unroll
         for (int t = 0; t < T; ++t) {
-            const bf16x8 bw = as_bf16x8(widen_nibbles(cur.w[t]));
+            const bf16x8 bw = as_bf16x8(widen_nibbles(cur.w[t], nk));
             // the bias correction enters as the accumulator's start value
             f32x4 c = {-corr[0], -corr[1], -corr[2], -corr[3]};
             c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ahi, bw, c, 0, 0, 0);
