@@ -503,7 +503,8 @@ int xp_batch_create(const xp_session* weights, uint32_t n_seq, uint32_t max_seq,
  * the faster (1.41 vs 1.93 ms a config-5 step, measured), so AUTO takes it.
  * The persistent kernel's bounded waits turn a grid that is not resident
  * after all into XP_E_DEVICE from xp_batch_forward (that step's results and
- * KV rows are then not valid). */
+ * the KV rows it appended are then not valid; positions are unchanged, so
+ * the step can be run again). */
 int xp_batch_create2(const xp_session* weights, uint32_t n_seq, uint32_t max_seq, int32_t exec_mode,
                      xp_batch** out);
 /* The execution in use: XP_EXEC_TOKEN (persistent step kernel) or XP_EXEC_GRAPH. */
@@ -516,6 +517,10 @@ int xp_batch_exec_mode(const xp_batch* b, int32_t* mode);
  * / 1 (0 where it had no tile), then its start at out[n_layers*14*G + w].
  * read with out == NULL sets *n_out to the entry count. */
 int xp_batch_step_trace(xp_batch* b, int enable);
+/* Poll rounds (each ~1 us) a wait of the step kernel takes before it gives
+ * up and the step returns XP_E_DEVICE; default 2^20, at most 2^24. A small
+ * value forces that path (tests of the error handling). */
+int xp_batch_set_spin_limit(xp_batch* b, uint32_t rounds);
 int xp_batch_step_trace_read(xp_batch* b, unsigned long long* out, size_t n, size_t* n_out);
 int xp_batch_destroy(xp_batch* b);
 int xp_batch_kv_upload(xp_batch* b, uint32_t seq, int layer, int which, uint32_t start,

@@ -269,6 +269,60 @@ def test_gpu_batch_exec_modes(xp, xo):
 
 
 @pytest.mark.gpu
+def test_gpu_batch_step_kernel_timeout_recovers(xp, xo):
+    """The step kernel's bounded waits, forced from the host: with a spin
+    limit of 0 a wait gives up at its first incomplete poll, every
+    workgroup still finishes, and the step returns XP_E_DEVICE with the
+    positions unchanged; with the default limit back, the same step gives the
+    graph's results bit for bit (its KV rows rewritten)."""
+    X = xp
+    print("case batch step kernel forced timeout", flush=True)
+    cfg = X.XpConfig.gemma3_1b(n_layers=2, vocab=16384, max_seq=512)
+    sess, _ = build(X, xo, cfg)
+    kvd = cfg.n_kv_heads * cfg.head_dim
+    n_seq = 4
+    depths = np.array([5, 100, 300, 511 - 8], np.int64)
+    bt = X.DecodeBatch(sess, n_seq, 512, X.XP_EXEC_TOKEN)
+    bg = X.DecodeBatch(sess, n_seq, 512, X.XP_EXEC_GRAPH)
+    for i, d in enumerate(depths):
+        for l in range(cfg.n_layers):
+            for which in (0, 1):
+                rows = X.synth_normal_f16(int(d) * kvd, 900 + i, 2 * l + which)
+                bt.kv_upload(i, l, which, 0, rows)
+                bg.kv_upload(i, l, which, 0, rows)
+    bt.set_positions(depths)
+    bg.set_positions(depths)
+
+    def same(pos):
+        for i in range(n_seq):
+            a, b = bt.last_logits(i), bg.last_logits(i)
+            assert np.array_equal(a.view(np.uint32), b.view(np.uint32)), (i, np.abs(a - b).max())
+            for l in range(cfg.n_layers):
+                for which in (0, 1):
+                    assert np.array_equal(bt.kv_download(i, l, which, int(pos[i]), 1),
+                                          bg.kv_download(i, l, which, int(pos[i]), 1)), (i, l, which)
+
+    toks = [11, 222, 3333, 4444]
+    bt.forward(toks)
+    bg.forward(toks)
+    same(depths)
+    toks = [5, 66, 777, 8888]
+    bt.set_spin_limit(0)
+    with pytest.raises(X.XposeError) as ei:
+        bt.forward(toks)
+    assert "limit" in str(ei.value), ei.value
+    assert np.array_equal(bt.positions(), depths + 1)
+    bt.set_spin_limit(1 << 20)
+    bt.forward(toks)
+    bg.forward(toks)
+    same(depths + 1)
+    assert np.array_equal(bt.positions(), depths + 2)
+    bt.close()
+    bg.close()
+    sess.close()
+
+
+@pytest.mark.gpu
 def test_gpu_batch_one_sequence_equals_session(xp, xo):
     """A batch of one sequence and the single-sequence session (persistent
     token kernel) on the same weights and KV give the same logits to the

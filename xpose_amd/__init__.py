@@ -164,6 +164,7 @@ def _declare(lib: C.CDLL) -> None:
         "xp_batch_create2": (i32, [vp, u32, u32, i32, P(vp)]),
         "xp_batch_exec_mode": (i32, [vp, P(i32)]),
         "xp_batch_step_trace": (i32, [vp, i32]),
+        "xp_batch_set_spin_limit": (i32, [vp, u32]),
         "xp_batch_step_trace_read": (i32, [vp, vp, C.c_size_t, P(C.c_size_t)]),
         "xp_batch_destroy": (i32, [vp]),
         "xp_batch_kv_upload": (i32, [vp, u32, i32, i32, u32, u32, vp]),
@@ -459,6 +460,9 @@ class DecodeBatch:
         m = C.c_int32()
         call("xp_batch_exec_mode", self.h, C.byref(m))
         return m.value
+
+    def set_spin_limit(self, rounds: int) -> None:
+        call("xp_batch_set_spin_limit", self.h, rounds)
 
     def step_trace(self, enable: bool) -> None:
         call("xp_batch_step_trace", self.h, 1 if enable else 0)

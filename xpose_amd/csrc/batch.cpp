@@ -269,7 +269,7 @@ int Batch::setup_step(int exec) {
     const size_t tab = al(size_t(per) * (c.n_layers + 1));
     const size_t rope_off = tab + al(sizeof(BstepLayer) * c.n_layers);
     const size_t cnt_off = rope_off + al(sizeof(RopeFreq) * 2);
-    const size_t total = cnt_off + al((size_t(c.n_layers) * kBsStages * kBsMaxTiles + 2) * 4);
+    const size_t total = cnt_off + al((size_t(c.n_layers) * kBsStages * kBsMaxTiles + 3) * 4);
     if (hipMalloc(&step_arena, total) != hipSuccess) return set_error(XP_E_NOMEM, "xp_batch_create: device memory");
     XP_HIP(hipMemset(step_arena, 0, total));
     auto at = [&](uint32_t l, size_t o) { return step_arena + size_t(l) * per + o; };
@@ -400,6 +400,7 @@ int Batch::setup_step(int exec) {
     bs.flags = reinterpret_cast<uint32_t*>(step_arena + cnt_off);
     bs.epoch = bs.flags + size_t(c.n_layers) * kBsStages * kBsMaxTiles;
     bs.status = bs.epoch + 1;
+    bs.exit_cnt = bs.epoch + 2;
     if (ncb_q > kBsMaxTiles || ncb_o > kBsMaxTiles || n_gu > kBsMaxTiles || ncb_d * ns_d > kBsMaxTiles ||
         B > kBsMaxTiles)
         return refuse("takes at most 512 tiles a stage");
@@ -456,14 +457,25 @@ int Batch::forward(const uint32_t* tokens) {
     if (step_kernel && h_status[0] != 0u) {
         // a wait ran past its limit (the grid was not resident at once): the
         // step's results are not valid
+        // positions stay where they were (the graph advanced the device's).
+        // With waits given up, tiles of different layers ran at once and
+        // may have left the arrival tickets they share counted wrong: the
+        // combine state (attention records, tickets and epochs, the GEMMs'
+        // tickets and partials) starts over as at creation.
         const uint32_t code = h_status[0];
         h_status[0] = 0u;
         XP_HIP(hipMemcpyAsync(bs.status, h_status, 4, hipMemcpyHostToDevice, st));
         XP_HIP(hipStreamSynchronize(st));
+        XP_HIP(hipMemcpy(d_pos, pos.data(), B * 4, hipMemcpyHostToDevice));
+        XP_HIP(hipMemset(attn_part, 0, (size_t(B) * attn_part_seq + 1) * 4));
+        XP_HIP(hipMemset(attn_tickets, 0, size_t(B) * w.cfg.n_kv_heads * kAttnTicketsPerHead * 4));
+        XP_HIP(hipMemset(tickets, 0, size_t(tickets_cap) * 4));
+        XP_HIP(hipMemset(part, 0, std::max<size_t>(part_cap, 1) * 4));
+        XP_HIP(hipDeviceSynchronize());
         logits_valid = false;
         return set_error(XP_E_DEVICE, "xp_batch_forward: the step kernel's wait ran past its limit "
                          "(status %u; another kernel held CUs of this GPU); the step's results and "
-                         "KV rows are not valid", code);
+                         "the KV rows it appended are not valid, positions are unchanged", code);
     }
     for (uint32_t i = 0; i < B; ++i) ++pos[i];
     logits_valid = true;
@@ -717,6 +729,20 @@ int xp_batch_step_trace(xp_batch* h, int enable) {
     }
     XP_HIP(hipMemset(b.d_trace, 0, n * 8));
     b.bs.trace = b.d_trace;
+    return XP_OK;
+}
+
+int xp_batch_set_spin_limit(xp_batch* h, uint32_t rounds) {
+    XP_REQUIRE(h, "null pointer");
+    Batch& b = h->b;
+    XP_REQUIRE(b.step_kernel, "xp_batch_set_spin_limit: the batch does not run the step kernel");
+    XP_REQUIRE(rounds <= (1u << 24), "xp_batch_set_spin_limit: rounds=%u > 2^24", rounds);
+    XP_HIP(hipStreamSynchronize(b.st));
+    if (b.graph) {
+        (void)hipGraphExecDestroy(b.graph);   // recaptured with the new limit
+        b.graph = nullptr;
+    }
+    b.bs.spin_limit = rounds;
     return XP_OK;
 }
 

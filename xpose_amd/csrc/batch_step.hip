@@ -28,7 +28,8 @@
 // grid is resident, so the walk cannot deadlock; a wait past the spin limit
 // sets the status word, after which every wait gives up at once, so the grid
 // always drains and the host reports XP_E_DEVICE. The tag is one past the
-// last launch's, kept in device memory, so flags never need clearing.
+// last launch's, kept in device memory and advanced by the last workgroup
+// to exit, so flags never need clearing.
 #include "xp_attn_device.hpp"
 #include "xp_bmm_device.hpp"
 
@@ -63,15 +64,13 @@ __device__ __forceinline__ void bs_wait(const BstepArgs& a, const uint32_t* flag
     for (uint32_t spins = 1;; ++spins) {
         const bool ok = tid >= n || ld_dev(flags + tid) == tag;
         if (__syncthreads_and(ok)) return;
-        if ((spins & 63u) == 0u) {
-            if (__syncthreads_or(ld_dev(a.status) != 0u)) return;
-            if (spins > a.spin_limit) {
-                if (tid == 0)
-                    __hip_atomic_fetch_or((XP_GLOBAL uint32_t*)a.status, 1u, __ATOMIC_RELAXED,
-                                          __HIP_MEMORY_SCOPE_AGENT);
-                return;
-            }
+        if (spins > a.spin_limit) {
+            if (tid == 0)
+                __hip_atomic_fetch_or((XP_GLOBAL uint32_t*)a.status, 1u, __ATOMIC_RELAXED,
+                                      __HIP_MEMORY_SCOPE_AGENT);
+            return;
         }
+        if ((spins & 63u) == 0u && __syncthreads_or(ld_dev(a.status) != 0u)) return;
         __builtin_amdgcn_s_sleep(1);
     }
 }
@@ -97,9 +96,9 @@ __global__ __launch_bounds__(kBsThreads) void bstep_kernel(BstepArgs a) {
     extern __shared__ __align__(16) unsigned char bs_lds[];
     BsSmem& S = *reinterpret_cast<BsSmem*>(bs_lds);
     const uint32_t wg = blockIdx.x, nwg = gridDim.x;
-    // this launch's tag: one past the last launch's (workgroup 0 stores it
-    // at exit, after every workgroup with a tile has read it: its last stage
-    // depends on every tile before it)
+    // this launch's tag: one past the last launch's, which the last
+    // workgroup to exit stores (every workgroup has read it by then; after a
+    // wait gave up, workgroup 0 may finish before others have started)
     const uint32_t ep = ld_dev(a.epoch);
     const uint32_t tag = ep + 1u != 0u ? ep + 1u : 1u;
     const uint32_t n_qkv = a.ncb_qkv, n_o = a.ncb_o, n_dn = a.ncb_dn * a.ns_dn;
@@ -184,7 +183,16 @@ __global__ __launch_bounds__(kBsThreads) void bstep_kernel(BstepArgs a) {
             if (t + nwg >= a.batch) bs_trace(a, l, 6, 1);
         }
     }
-    if (wg == 0 && threadIdx.x == 0) st_dev(a.epoch, tag);
+    wait_mem();
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        const uint32_t done = __hip_atomic_fetch_add((XP_GLOBAL uint32_t*)a.exit_cnt, 1u, __ATOMIC_RELAXED,
+                                                     __HIP_MEMORY_SCOPE_AGENT);
+        if (done == nwg - 1u) {
+            st_dev(a.exit_cnt, 0u);
+            st_dev(a.epoch, tag);
+        }
+    }
 }
 
 int launch_bstep(const BstepArgs& a, int fmt, uint32_t grid, hipStream_t st) {

@@ -230,6 +230,7 @@ struct BstepArgs {
     uint32_t ncb_qkv, ncb_o, ncb_dn, ns_dn, n_gu;   // column blocks; the down GEMM's k splits; gate|up tiles
     uint32_t* flags;             // [n_layers][kBsStages][kBsMaxTiles] tile flags (last launch's tag)
     uint32_t* epoch;             // the last launch's tag
+    uint32_t* exit_cnt;          // workgroups that finished this launch (zero at rest)
     uint32_t* status;            // set when a wait ran past spin_limit
     uint32_t spin_limit;
     // Stage timeline (null: off): s_memrealtime (100 MHz) of each workgroup
