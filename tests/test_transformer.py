@@ -248,11 +248,13 @@ def run_attention(xp, q, kb, vb, span, kv0, scale):
 
 @pytest.mark.gpu
 @pytest.mark.parametrize("seq,kv0", [(131, 0), (131, 43), (1, 0), (512, 0), (513, 1),
-                                     (1100, 0), (2047, 0), (4097, 0), (8192, 0), (8192, 7680)])
+                                     (1100, 0), (2047, 0), (3600, 0), (4097, 0), (8192, 0),
+                                     (8192, 7680)])
 def test_gpu_attention(xp, xo, seq, kv0):
-    """Spans 1..8192: up to 256 splits of at least 32 keys, combined in one
+    """Spans 1..8192: up to 128 splits of at least 32 keys, combined in one
     level (at most 16 splits) or two (groups of 16; 1100 keys: 35 splits,
-    the last group of 3; 4097: 129 splits, the last group of 1)."""
+    the last group of 3; 3600: 113 splits, the last group of 1; 4097 and
+    8192: 128 splits of 33 and 64 keys)."""
     print(f"case attention seq={seq} kv0={kv0}", flush=True)
     r = rng()
     q = u(r, HEADS * HEAD_DIM)
@@ -289,10 +291,10 @@ def test_gpu_attention_ticket_levels():
     here = os.path.dirname(os.path.abspath(__file__))
     r = subprocess.run([sys.executable, "-m", "pytest", os.path.join(here, "test_transformer.py"), "-q",
                         "-m", "gpu", "-p", "no:cacheprovider",
-                        "-k", "test_gpu_attention and (1100 or 2047 or 4097 or 8192)"],
+                        "-k", "test_gpu_attention and (1100 or 2047 or 3600 or 4097 or 8192)"],
                        env=env, capture_output=True, text=True, timeout=240)
     assert r.returncode == 0, r.stdout[-2000:] + r.stderr[-2000:]
-    assert "5 passed" in r.stdout, r.stdout[-2000:]
+    assert "6 passed" in r.stdout, r.stdout[-2000:]
 
 
 @pytest.mark.gpu

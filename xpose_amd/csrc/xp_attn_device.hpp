@@ -25,8 +25,9 @@ namespace xp {
 //   values  the same lanes accumulate p x v for their 8 dims, then the 16 row
 //           groups are summed (lane pairs by shuffle, waves through LDS)
 // U (2, 4 or 8) follows the chunk length, so a 32-key chunk does a quarter
-// of a 128-key pass's arithmetic. Up to 256 splits (at least 32 keys each)
-// give every CU a workgroup at one sequence's long spans. Each split
+// of a 128-key pass's arithmetic. Up to 128 splits (at least 32 keys each)
+// give most CUs a workgroup at one sequence's long spans (256 measured
+// slower at span 8192: the splits' exchange grows with their square). Each split
 // publishes (max, sum of exp, unnormalised o) per head; the last workgroup
 // of each group of 16 splits to arrive (arrival ticket) rescales and sums
 // the group — softmax_rows_finish's online combine (llm_transformer.cl:
@@ -42,6 +43,7 @@ constexpr int kAttnRows     = kAttnThreads / kAttnLanes;  // 16 row groups
 constexpr int kAttnMaxPass  = kAttnRows * 8;              // most keys per pass (U = 8)
 constexpr int kAttnMinChunk = 32;                         // fewest keys per split
 constexpr int kAttnMaxSplit = 256;                        // splits per (sequence, kv head)
+constexpr uint32_t kAttnSplitCap = 128;                   // splits the launcher plans at most
 constexpr int kAttnFan      = 16;                         // records one combine reads
 constexpr int kAttnGroups   = kAttnMaxSplit / kAttnFan;   // level-1 records
 constexpr int kAttnMaxG     = 4;                          // query heads per kv head
