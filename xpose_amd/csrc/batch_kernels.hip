@@ -114,21 +114,25 @@ __global__ __launch_bounds__(kBmmThreads) void bmm_stream_kernel(BmmArgs a) {
         uint32_t w[MB][4];
         u32x2 sc[2][4];                                 // scale quads q0, q0 + 1
     };
+    // raw buffer loads: a fixed per-lane offset and a per-group (and block)
+    // scalar offset, no 64-bit address per lane and load
+    const rsrc_t rw = make_rsrc(wq, cols * nblk * 16u), rs = make_rsrc(sq, nq * cols * 8u);
     auto load = [&](Wt& o, uint32_t g) {
 #pragma unroll
         for (int j = 0; j < MB; ++j) {
             const uint32_t blk = kb0 + min(uint32_t(j), nbw - 1u);
 #pragma unroll
-            for (int t = 0; t < 4; ++t) {
-                const uint32_t cg = 16u * t + col16;
-                o.w[j][t] = __builtin_nontemporal_load(wq + ((size_t(g) * nblk + blk) * kGrp + cg) * 4 + wsel);
-            }
+            for (int t = 0; t < 4; ++t)
+                o.w[j][t] = __builtin_amdgcn_raw_buffer_load_b32(rw, int((16u * t + col16) * 16u + wsel * 4u),
+                                                                 int((g * nblk + blk) * 1024u), 2);
         }
 #pragma unroll
         for (int qq = 0; qq < 2; ++qq) {
             const uint32_t q = min(q0 + uint32_t(qq), nq - 1u);
 #pragma unroll
-            for (int t = 0; t < 4; ++t) o.sc[qq][t] = sq[size_t(q) * cols + g * kGrp + 16u * t + col16];
+            for (int t = 0; t < 4; ++t)
+                o.sc[qq][t] = __builtin_amdgcn_raw_buffer_load_b64(rs, int((16u * t + col16) * 8u),
+                                                                   int((q * cols + g * kGrp) * 8u), 0);
         }
     };
     auto group = [&](const Wt& cur, uint32_t g, float (&rd)[kBmmWaves][NO]) {

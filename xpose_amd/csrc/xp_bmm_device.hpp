@@ -254,15 +254,29 @@ __device__ __forceinline__ bool bmm_tile(const BmmArgs& a, uint32_t cb, uint32_t
     }
     const uint32_t g = gg - g0;
     const uint32_t cols = md.cols;
-    const uint32_t* wq = static_cast<const uint32_t*>(md.wq);
-    const u32x2* sq = static_cast<const u32x2*>(md.sc);
-    const u32x4* A = static_cast<const u32x4*>(a.a);
     const uint32_t col16 = lane % 16u, wsel = lane / 16u;
     const uint32_t kb0 = min((s * kBmmWaves + wave) * a.kc, a.nblk);
     const uint32_t kb1 = min(kb0 + a.kc, a.nblk);
     f32x4 acc[T];
 #pragma unroll
     for (int t = 0; t < T; ++t) acc[t] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    // Every operand is read through a raw buffer: a fixed per-lane offset
+    // and a per-block offset that is the same for the whole wave (a scalar),
+    // so no 64-bit address is formed per lane and load (the GEMM is
+    // VALU-bound at M = 16). Weights stream past the caches (nt).
+    constexpr int kNt = 2;
+    const uint32_t nblk = a.nblk, wbytes = cols * nblk * 16u, sbytes = ((nblk + 3u) / 4u) * cols * 8u;
+    rsrc_t rw[GE ? 2 : 1], rs[GE ? 2 : 1];
+    if constexpr (GE) {
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            rw[i] = make_rsrc(a.mats[i].wq, wbytes);
+            rs[i] = make_rsrc(a.mats[i].sc, sbytes);
+        }
+    } else {
+        rw[0] = make_rsrc(md.wq, wbytes);
+        rs[0] = make_rsrc(md.sc, sbytes);
+    }
     // operands of one block (raw fp32 rows in AM 2 / 3, staged after the loads)
     constexpr int NR = AM == 3 ? 4 : (AM == 2 ? 2 : 1);
     struct Ops {
@@ -272,41 +286,39 @@ __device__ __forceinline__ bool bmm_tile(const BmmArgs& a, uint32_t cb, uint32_t
         uint32_t w[T];
         u32x2 sc[T];
     };
+    const rsrc_t ra = make_rsrc(a.a, nblk * 2u * 64u * 16u), rsum = make_rsrc(a.asum, nblk * 16u * 4u);
+    // fp32 rows: sequences past a.rows lie past the buffer's end and read as zeros
+    const rsrc_t rxa = make_rsrc(a.xa, a.rows * a.lda * 4u), rxu = make_rsrc(a.xu, a.rows * a.lda * 4u);
+    const uint32_t vx = (col16 * a.lda + 8u * wsel) * 4u;
+    auto ldx4 = [&](rsrc_t r, uint32_t voff, uint32_t soff) {
+        const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(r, int(voff), int(soff), 0);
+        return float4{__uint_as_float(v.x), __uint_as_float(v.y), __uint_as_float(v.z), __uint_as_float(v.w)};
+    };
     auto load = [&](Ops& o, uint32_t blk) {
         if constexpr (AM == 0) {
-            o.hi = A[(size_t(blk) * 2 + 0) * 64 + lane];
-            o.lo = A[(size_t(blk) * 2 + 1) * 64 + lane];
-            o.as = *reinterpret_cast<const float4*>(a.asum + size_t(blk) * 16 + 4u * wsel);
+            o.hi = __builtin_amdgcn_raw_buffer_load_b128(ra, int(lane * 16u), int(blk * 2048u), 0);
+            o.lo = __builtin_amdgcn_raw_buffer_load_b128(ra, int(lane * 16u), int(blk * 2048u + 1024u), 0);
+            const u32x4 sv = __builtin_amdgcn_raw_buffer_load_b128(rsum, int(wsel * 16u), int(blk * 64u), 0);
+            o.as = float4{__uint_as_float(sv.x), __uint_as_float(sv.y), __uint_as_float(sv.z),
+                          __uint_as_float(sv.w)};
         } else {
-            // row col16 (sequences past a.rows read as zeros), k 32 blk + 8 wsel ..
-#pragma unroll
-            for (int i = 0; i < NR; ++i) o.raw[i] = float4{0.0f, 0.0f, 0.0f, 0.0f};
-            if (col16 < a.rows) {
-                const size_t off = size_t(col16) * a.lda + size_t(blk) * kBlk + 8u * wsel;
-                const float4* xa4 = reinterpret_cast<const float4*>(a.xa + off);
-                o.raw[0] = xa4[0];
-                o.raw[1] = xa4[1];
-                if constexpr (AM == 3) {
-                    const float4* xu4 = reinterpret_cast<const float4*>(a.xu + off);
-                    o.raw[2] = xu4[0];
-                    o.raw[3] = xu4[1];
-                }
+            // row col16, k 32 blk + 8 wsel ..
+            o.raw[0] = ldx4(rxa, vx, blk * 128u);
+            o.raw[1] = ldx4(rxa, vx + 16u, blk * 128u);
+            if constexpr (AM == 3) {
+                o.raw[2] = ldx4(rxu, vx, blk * 128u);
+                o.raw[3] = ldx4(rxu, vx + 16u, blk * 128u);
             }
         }
+        // block blk of column group g: weights at ((g nblk + blk) 64 + column) 16 + word 4,
+        // its scale quad at ((blk / 4) cols + 64 g + column) 8
+        const uint32_t sw = (g * nblk + blk) * 1024u, ss = ((blk / 4u) * cols + g * kGrp) * 8u;
 #pragma unroll
         for (int t = 0; t < T; ++t) {
-            if constexpr (GE) {
-                const uint32_t mt = uint32_t(t) / 2u;
-                const uint32_t cg = c16 + 16u * (uint32_t(t) % 2u) + col16;
-                const uint32_t* wt = static_cast<const uint32_t*>(a.mats[mt].wq);
-                const u32x2* st = static_cast<const u32x2*>(a.mats[mt].sc);
-                o.w[t] = __builtin_nontemporal_load(wt + ((size_t(g) * a.nblk + blk) * kGrp + cg) * 4 + wsel);
-                o.sc[t] = st[size_t(blk / 4) * cols + g * kGrp + cg];
-            } else {
-                const uint32_t cg = c16 + 16u * t + col16;   // column within the group
-                o.w[t] = __builtin_nontemporal_load(wq + ((size_t(g) * a.nblk + blk) * kGrp + cg) * 4 + wsel);
-                o.sc[t] = sq[size_t(blk / 4) * cols + g * kGrp + cg];
-            }
+            const uint32_t mt = GE ? uint32_t(t) / 2u : 0u;
+            const uint32_t cg = GE ? c16 + 16u * (uint32_t(t) % 2u) + col16 : c16 + 16u * t + col16;
+            o.w[t] = __builtin_amdgcn_raw_buffer_load_b32(rw[mt], int(cg * 16u + wsel * 4u), int(sw), kNt);
+            o.sc[t] = __builtin_amdgcn_raw_buffer_load_b64(rs[mt], int(cg * 8u), int(ss), 0);
         }
     };
     const NibConst nk = nib_const();
