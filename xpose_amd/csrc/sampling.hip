@@ -78,8 +78,13 @@ __global__ __launch_bounds__(kAmThreads) void argmax_kernel(AmArgs a) {
 // topk4_partial, llm_sampling.cl:318-347: one thread per strided chain
 // e = p (mod nparts), best four by strict '>' (earliest index on ties),
 // unfilled slots (-inf, 0xFFFFFFFF). Pure comparisons: bit-identical output.
-__global__ void topk4_kernel(float* cval, uint32_t* cidx, const float* x, uint32_t n,
-                             uint32_t nparts) {
+// The chain's values are loaded kT4Batch at a time, all in flight together
+// (one memory latency per batch, not one per element), then walked in chain
+// order; past the end a slot holds -inf, which never enters the four.
+constexpr uint32_t kT4Batch = 64;
+
+__global__ __launch_bounds__(256) void topk4_kernel(float* cval, uint32_t* cidx, const float* x,
+                                                    uint32_t n, uint32_t nparts) {
     x += size_t(blockIdx.y) * n;                 // batched rows (grid.y)
     cval += size_t(blockIdx.y) * nparts * 4u;
     cidx += size_t(blockIdx.y) * nparts * 4u;
@@ -87,17 +92,30 @@ __global__ void topk4_kernel(float* cval, uint32_t* cidx, const float* x, uint32
     if (p >= nparts) return;
     float v0 = -INFINITY, v1 = -INFINITY, v2 = -INFINITY, v3 = -INFINITY;
     uint32_t i0 = 0xFFFFFFFFu, i1 = 0xFFFFFFFFu, i2 = 0xFFFFFFFFu, i3 = 0xFFFFFFFFu;
-    for (uint32_t e = p; e < n; e += nparts) {
-        const float v = x[e];
-        if (!(v > v3)) continue;
-        if (v > v0) {
-            v3 = v2; i3 = i2; v2 = v1; i2 = i1; v1 = v0; i1 = i0; v0 = v; i0 = e;
-        } else if (v > v1) {
-            v3 = v2; i3 = i2; v2 = v1; i2 = i1; v1 = v; i1 = e;
-        } else if (v > v2) {
-            v3 = v2; i3 = i2; v2 = v; i2 = e;
-        } else {
-            v3 = v; i3 = e;
+    for (size_t e0 = p; e0 < n; e0 += size_t(kT4Batch) * nparts) {
+        float xv[kT4Batch];
+#pragma unroll
+        for (uint32_t j = 0; j < kT4Batch; ++j) {
+            const size_t e = e0 + size_t(j) * nparts;
+            xv[j] = e < n ? x[e] : -INFINITY;
+        }
+#pragma unroll
+        for (uint32_t j = 0; j < kT4Batch; ++j) {
+            // insertion by selects: v0 >= v1 >= v2 >= v3, so c0 implies c1
+            // implies c2 implies c3, and the four selects below are the
+            // branches "above v0 / v1 / v2 / v3" of the sequential insert
+            // (NaN and -inf compare false everywhere and change nothing)
+            const float v = xv[j];
+            const uint32_t e = uint32_t(e0 + size_t(j) * nparts);
+            const bool c0 = v > v0, c1 = v > v1, c2 = v > v2, c3 = v > v3;
+            v3 = c2 ? v2 : (c3 ? v : v3);
+            i3 = c2 ? i2 : (c3 ? e : i3);
+            v2 = c1 ? v1 : (c2 ? v : v2);
+            i2 = c1 ? i1 : (c2 ? e : i2);
+            v1 = c0 ? v0 : (c1 ? v : v1);
+            i1 = c0 ? i0 : (c1 ? e : i1);
+            v0 = c0 ? v : v0;
+            i0 = c0 ? e : i0;
         }
     }
     const uint32_t o = p * 4u;

@@ -251,10 +251,17 @@ __global__ void multinomial_strided_kernel(float* out, uint32_t* idx_out, const 
 // byte-first radix select finds the k-th largest (value, as an order-preserving
 // key); the candidates at or above it (k plus any ties) are gathered in LDS and
 // ranked among themselves by (value desc, index asc). Exact while fewer than
-// 256 - k candidates tie with the k-th largest value.
+// 256 - k candidates tie with the k-th largest value. Logits share their top
+// bytes, so most of a wave's keys fall in one bin: the histogram is kept in
+// kSelCopies copies, lane l adding to copy l % kSelCopies (a bin's copies in
+// consecutive words, different banks), which turns a 64-way same-address
+// atomic into a 4-way one, and each thread adds a run of its keys that fall
+// in one bin with one atomic; the copies are summed before the scan.
 constexpr uint32_t kSelThreads = 1024;
 constexpr uint32_t kSelPer = 16;             // candidates per thread (16384 per row)
 constexpr uint32_t kSelKeep = 256;           // survivors ranked (k + ties)
+constexpr uint32_t kSelCopies = 16;          // histogram copies
+constexpr uint32_t kSelStride = kSelCopies + 1u;   // words per bin (padded: the sum reads bins apart)
 
 __device__ __forceinline__ uint32_t order_key(float v) {
     const uint32_t u = __float_as_uint(v);
@@ -265,6 +272,7 @@ __global__ __launch_bounds__(kSelThreads) void select_rows_kernel(float* oval, u
                                                                   const float* cval,
                                                                   const uint32_t* cidx,
                                                                   uint32_t ncand, uint32_t k) {
+    __shared__ uint32_t hcopy[256 * kSelStride];
     __shared__ uint32_t hist[256];
     __shared__ uint32_t sel[3];               // prefix, needed, survivors
     __shared__ float sv[kSelKeep];
@@ -276,19 +284,50 @@ __global__ __launch_bounds__(kSelThreads) void select_rows_kernel(float* oval, u
         oval[size_t(r) * k + tid] = -INFINITY;
         oidx[size_t(r) * k + tid] = kNone;
     }
-    uint32_t key[kSelPer];
+    // every candidate's value and index loaded at once (unconditionally, an
+    // index past the end reads candidate 0), kept in registers for the gather
+    uint32_t key[kSelPer], ci[kSelPer];
+    float cv[kSelPer];
 #pragma unroll
     for (uint32_t j = 0; j < kSelPer; ++j) {
         const uint32_t i = tid + j * kSelThreads;
-        key[j] = (i < ncand && cidx[i] != kNone) ? order_key(cval[i]) : 0u;   // 0: below every value
+        const uint32_t ic = i < ncand ? i : 0u;
+        cv[j] = cval[ic];
+        ci[j] = cidx[ic];
+    }
+#pragma unroll
+    for (uint32_t j = 0; j < kSelPer; ++j) {
+        const uint32_t i = tid + j * kSelThreads;
+        key[j] = (i < ncand && ci[j] != kNone) ? order_key(cv[j]) : 0u;   // 0: below every value
     }
     uint32_t prefix = 0, mask = 0, need = k;
+    const uint32_t copy = tid % kSelCopies;
     for (int shift = 24; shift >= 0; shift -= 8) {
-        if (tid < 256) hist[tid] = 0;
+        for (uint32_t i = tid; i < 256u * kSelStride; i += kSelThreads) hcopy[i] = 0;
         __syncthreads();
+        {   // a thread's run of keys in one bin goes in with one atomic
+            uint32_t rb = 0u, rn = 0u;
 #pragma unroll
-        for (uint32_t j = 0; j < kSelPer; ++j)
-            if (key[j] != 0u && (key[j] & mask) == prefix) atomicAdd(&hist[(key[j] >> shift) & 255u], 1u);
+            for (uint32_t j = 0; j < kSelPer; ++j) {
+                if (key[j] != 0u && (key[j] & mask) == prefix) {
+                    const uint32_t bin = (key[j] >> shift) & 255u;
+                    if (bin != rb) {
+                        if (rn) atomicAdd(&hcopy[rb * kSelStride + copy], rn);
+                        rb = bin;
+                        rn = 0u;
+                    }
+                    ++rn;
+                }
+            }
+            if (rn) atomicAdd(&hcopy[rb * kSelStride + copy], rn);
+        }
+        __syncthreads();
+        if (tid < 256) {
+            uint32_t c = 0;
+#pragma unroll
+            for (uint32_t q = 0; q < kSelCopies; ++q) c += hcopy[tid * kSelStride + q];
+            hist[tid] = c;
+        }
         __syncthreads();
         if (tid < kWave) {
             // lane l covers bins 255 - 4 l .. 252 - 4 l; inclusive prefix of
@@ -331,10 +370,9 @@ __global__ __launch_bounds__(kSelThreads) void select_rows_kernel(float* oval, u
     __syncthreads();
 #pragma unroll
     for (uint32_t j = 0; j < kSelPer; ++j) {
-        const uint32_t i = tid + j * kSelThreads;
         if (key[j] != 0u && key[j] >= prefix) {
             const uint32_t slot = atomicAdd(&sel[2], 1u);
-            if (slot < kSelKeep) { sv[slot] = cval[i]; si[slot] = cidx[i]; }
+            if (slot < kSelKeep) { sv[slot] = cv[j]; si[slot] = ci[j]; }
         }
     }
     __syncthreads();
