@@ -133,12 +133,23 @@ int Batch::record() {
         g.tickets_cap = tickets_cap;
         return launch_bmm(g, fmt, w.n_cu, st, who);
     };
-    XB(launch_bembed(x, w.lm_w, w.lm_s, fmt, H, c.vocab, w.embed_scale, d_tok, B, w.embed, st));
+    // the embedding rows of the step's tokens and layer 0's operand in one
+    // staging launch
+    auto embed_prep = [&](void* a_, float* asum_) {
+        BprepArgs p0{0, x, nullptr, nullptr, nullptr, w.layer[0].norm[0], a_, asum_, H, eps};
+        p0.tok = d_tok;
+        p0.ewq = w.lm_w;
+        p0.esc = w.lm_s;
+        p0.etable = w.embed;
+        p0.vocab = c.vocab;
+        p0.efmt = fmt;
+        p0.escale = w.embed_scale;
+        return launch_bprep(p0, B, st);
+    };
     if (step_kernel) {
         // layer 0's operand, then every layer in one launch, then the lm_head
         // on the operand its last stage staged
-        BprepArgs p0{0, x, nullptr, nullptr, nullptr, w.layer[0].norm[0], a0, asum0, H, eps};
-        XB(launch_bprep(p0, B, st));
+        XB(embed_prep(a0, asum0));
         XB(launch_bstep(bs, fmt, uint32_t(w.n_cu), st));
         BmmArgs g{};
         g.a = af;
@@ -154,11 +165,10 @@ int Batch::record() {
         g.tickets_cap = tickets_cap;
         XB(launch_bmm(g, fmt, w.n_cu, st, "batch lm_head"));
         XB(launch_topk4(cval, cidx, logits, c.vocab, kHarvestParts, st, B));
-        XB(launch_select_rows(oval, oidx, cval, cidx, kHarvest, kCand, B, st));
-        XB(launch_badvance(d_pos, B, st));
+        XB(launch_select_rows(oval, oidx, cval, cidx, kHarvest, kCand, B, st, d_pos));
         return XP_OK;
     }
-    XB(prep(0, x, nullptr, nullptr, nullptr, w.layer[0].norm[0], H));
+    XB(embed_prep(a, asum));
     for (uint32_t l = 0; l < c.n_layers; ++l) {
         const SessionWeights::Layer& L = w.layer[l];
         const bool glob = L.global;
@@ -221,8 +231,7 @@ int Batch::record() {
         const MvMatDesc lm{logits, w.lm_w, w.lm_s, c.vocab};
         XB(gemm(&lm, 1, H, "batch lm_head"));
         XB(launch_topk4(cval, cidx, logits, c.vocab, kHarvestParts, st, B));
-        XB(launch_select_rows(oval, oidx, cval, cidx, kHarvest, kCand, B, st));
-        XB(launch_badvance(d_pos, B, st));
+        XB(launch_select_rows(oval, oidx, cval, cidx, kHarvest, kCand, B, st, d_pos));
     }
 #undef XB
     return XP_OK;

@@ -42,28 +42,6 @@ __global__ __launch_bounds__(kPrepThreads) void bprep_kernel(BprepArgs a) {
     prep_row<kPrepThreads, false>(a, blockIdx.x, red);
 }
 
-// ---- embedding --------------------------------------------------------------------
-// x[b][k] = dequant(tied table column tok[b])[k] * embed_scale (decode.cpp:1618-1627).
-__global__ __launch_bounds__(256) void bembed_kernel(float* x, const void* wq, const void* sc, int fmt,
-                                                     uint32_t hidden, uint32_t vocab, float embed_scale,
-                                                     const uint32_t* tok, const float* table) {
-    const uint32_t b = blockIdx.y, k = blockIdx.x * 256 + threadIdx.x;
-    if (k >= hidden) return;
-    uint32_t t = tok[b];
-    if (t >= vocab) t = 0;
-    if (table) {   // the model's own fp32 embedding rows
-        x[size_t(b) * hidden + k] = table[size_t(t) * hidden + k] * embed_scale;
-        return;
-    }
-    const uint32_t nblk = hidden / kBlk, blk = k / kBlk, i = k % kBlk;
-    const uint32_t* w = static_cast<const uint32_t*>(wq);
-    const uint32_t word = w[((size_t(t / kGrp) * nblk + blk) * kGrp + (t % kGrp)) * 4 + i / 8];
-    const float q = float(int((word >> (4 * (i % 8))) & 15u) - 8);
-    const uint16_t h = static_cast<const uint16_t*>(sc)[(size_t(blk / 4) * vocab + t) * 4 + blk % 4];
-    const float s = fmt == XP_SCALE_F16_QUAD ? f16_bits_to_f32(h) : __uint_as_float(uint32_t(h) << 16);
-    x[size_t(b) * hidden + k] = (q * s) * embed_scale;
-}
-
 // ---- M = 16 int4 GEMM (the tile in xp_bmm_device.hpp) ------------------------------
 template <int FMT, int T, int AM, bool GE = false>
 __global__ __launch_bounds__(kBmmThreads) void bmm_int4_kernel(BmmArgs a) {
@@ -195,33 +173,12 @@ __global__ __launch_bounds__(kBmmThreads) void bmm_stream_kernel(BmmArgs a) {
     }
 }
 
-// Position advance for every sequence of a batch.
-__global__ void badvance_kernel(uint32_t* pos, uint32_t n) {
-    const uint32_t i = threadIdx.x;
-    if (i < n) pos[i] += 1u;
-}
-
 // ---- launchers --------------------------------------------------------------------
 int launch_bprep(const BprepArgs& a, uint32_t batch, hipStream_t st) {
     if (a.K % 32 || a.K == 0 || a.K > 8 * kPrepThreads)
         return set_error(XP_E_ARG, "bprep: K=%u must be a multiple of 32, at most %u", a.K, 8 * kPrepThreads);
     if (batch == 0 || batch > 16) return set_error(XP_E_ARG, "bprep: batch %u outside [1, 16]", batch);
     hipLaunchKernelGGL(bprep_kernel, dim3(batch), dim3(kPrepThreads), 0, st, a);
-    XP_LAUNCHED();
-    return XP_OK;
-}
-
-int launch_bembed(float* x, const void* wq, const void* sc, int fmt, uint32_t hidden, uint32_t vocab,
-                  float embed_scale, const uint32_t* tok, uint32_t batch, const float* table,
-                  hipStream_t st) {
-    hipLaunchKernelGGL(bembed_kernel, dim3((hidden + 255) / 256, batch), dim3(256), 0, st, x, wq, sc, fmt,
-                       hidden, vocab, embed_scale, tok, table);
-    XP_LAUNCHED();
-    return XP_OK;
-}
-
-int launch_badvance(uint32_t* pos, uint32_t batch, hipStream_t st) {
-    hipLaunchKernelGGL(badvance_kernel, dim3(1), dim3(64), 0, st, pos, batch);
     XP_LAUNCHED();
     return XP_OK;
 }

@@ -271,7 +271,8 @@ __device__ __forceinline__ uint32_t order_key(float v) {
 __global__ __launch_bounds__(kSelThreads) void select_rows_kernel(float* oval, uint32_t* oidx,
                                                                   const float* cval,
                                                                   const uint32_t* cidx,
-                                                                  uint32_t ncand, uint32_t k) {
+                                                                  uint32_t ncand, uint32_t k,
+                                                                  uint32_t* pos_inc) {
     __shared__ uint32_t hcopy[256 * kSelStride];
     __shared__ uint32_t hist[256];
     __shared__ uint32_t sel[3];               // prefix, needed, survivors
@@ -284,6 +285,7 @@ __global__ __launch_bounds__(kSelThreads) void select_rows_kernel(float* oval, u
         oval[size_t(r) * k + tid] = -INFINITY;
         oidx[size_t(r) * k + tid] = kNone;
     }
+    if (pos_inc && tid == 0) pos_inc[r] += 1u;
     // every candidate's value and index loaded at once (unconditionally, an
     // index past the end reads candidate 0), kept in registers for the gather
     uint32_t key[kSelPer], ci[kSelPer];
@@ -390,12 +392,12 @@ __global__ __launch_bounds__(kSelThreads) void select_rows_kernel(float* oval, u
 }
 
 int launch_select_rows(float* oval, uint32_t* oidx, const float* cval, const uint32_t* cidx,
-                       uint32_t ncand, uint32_t k, uint32_t rows, hipStream_t st) {
+                       uint32_t ncand, uint32_t k, uint32_t rows, hipStream_t st, uint32_t* pos_inc) {
     if (k < 1 || k > kTopkMax || rows == 0 || ncand == 0 || ncand > kSelThreads * kSelPer)
         return set_error(XP_E_ARG, "select rows: k=%u rows=%u ncand=%u (<= %u)", k, rows, ncand,
                          kSelThreads * kSelPer);
     hipLaunchKernelGGL(select_rows_kernel, dim3(rows), dim3(kSelThreads), 0, st, oval, oidx, cval, cidx,
-                       ncand, k);
+                       ncand, k, pos_inc);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return set_error(XP_E_HIP, "select rows: launch -> %s", hipGetErrorString(e));
     return XP_OK;

@@ -129,7 +129,31 @@ __device__ __forceinline__ void prep_row(const BprepArgs& a, uint32_t b, float (
     float v[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
     if (a.mode <= 1) {
         float xv[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f}, wpre[8];
-        if (own) {
+        if (own && a.mode == 0 && a.tok) {
+            // the embedding (decode.cpp:1618-1627): elements 8p .. 8p + 7 are
+            // one word of the table column's block
+            uint32_t t = a.tok[b];
+            if (t >= a.vocab) t = 0;
+            if (a.etable) {
+                ld8f(xv, a.etable + size_t(t) * K + 8 * p);
+#pragma unroll
+                for (int e = 0; e < 8; ++e) xv[e] = xv[e] * a.escale;
+            } else {
+                const uint32_t nblk = K / kBlk, blk = (8 * p) / kBlk, i0 = (8 * p) % kBlk;
+                const uint32_t word = static_cast<const uint32_t*>(
+                    a.ewq)[((size_t(t / kGrp) * nblk + blk) * kGrp + (t % kGrp)) * 4 + i0 / 8];
+                const uint16_t h = static_cast<const uint16_t*>(a.esc)[(size_t(blk / 4) * a.vocab + t) * 4 + blk % 4];
+                const float sc = a.efmt == XP_SCALE_F16_QUAD ? f16_bits_to_f32(h) : __uint_as_float(uint32_t(h) << 16);
+#pragma unroll
+                for (int e = 0; e < 8; ++e) xv[e] = (float(int((word >> (4 * e)) & 15u) - 8) * sc) * a.escale;
+            }
+            float4* xo = reinterpret_cast<float4*>(x + 8 * p);
+            st_u4<DEV>(reinterpret_cast<u32x4*>(xo), u32x4{__float_as_uint(xv[0]), __float_as_uint(xv[1]),
+                                                           __float_as_uint(xv[2]), __float_as_uint(xv[3])});
+            st_u4<DEV>(reinterpret_cast<u32x4*>(xo + 1), u32x4{__float_as_uint(xv[4]), __float_as_uint(xv[5]),
+                                                               __float_as_uint(xv[6]), __float_as_uint(xv[7])});
+            ld8f(wpre, a.w_pre + 8 * p);
+        } else if (own) {
             ld8f(xv, x + 8 * p);
             ld8f(wpre, a.w_pre + 8 * p);
         }

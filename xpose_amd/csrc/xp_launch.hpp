@@ -141,9 +141,12 @@ int launch_topk4(float* cval, uint32_t* cidx, const float* x, uint32_t n, uint32
                  hipStream_t st, uint32_t rows = 1);
 // The best k (<= 64) of each of `rows` candidate lists (row r at cval / cidx +
 // r ncand), sorted by (value desc, index asc), into oval / oidx [rows][k];
-// exact. Unfilled list slots carry index 0xFFFFFFFF and are skipped.
+// exact. Unfilled list slots carry index 0xFFFFFFFF and are skipped. With
+// pos_inc, row r's workgroup also adds 1 to pos_inc[r] (the batched step's
+// position advance, which nothing in the select reads).
 int launch_select_rows(float* oval, uint32_t* oidx, const float* cval, const uint32_t* cidx,
-                       uint32_t ncand, uint32_t k, uint32_t rows, hipStream_t st);
+                       uint32_t ncand, uint32_t k, uint32_t rows, hipStream_t st,
+                       uint32_t* pos_inc = nullptr);
 
 
 // ---- batched decode (batch_kernels.hip) ----
@@ -161,12 +164,18 @@ struct BprepArgs {
     uint32_t K;
     float eps;
     float* x_out = nullptr;    // modes 0, 1: the updated x goes here instead of x (same layout)
+    // mode 0 with tok: row b of x is first set to the embedding of token
+    // tok[b] (a column of the tied int4 table ewq / esc in format efmt, or
+    // row tok[b] of the fp32 table etable) times escale, and stored to x
+    const uint32_t* tok = nullptr;
+    const void* ewq = nullptr;
+    const void* esc = nullptr;
+    const float* etable = nullptr;
+    uint32_t vocab = 0;
+    int efmt = 0;
+    float escale = 1.0f;
 };
 int launch_bprep(const BprepArgs& a, uint32_t batch, hipStream_t st);
-int launch_bembed(float* x, const void* wq, const void* sc, int fmt, uint32_t hidden, uint32_t vocab,
-                  float embed_scale, const uint32_t* tok, uint32_t batch, const float* table,
-                  hipStream_t st);
-int launch_badvance(uint32_t* pos, uint32_t batch, hipStream_t st);
 // y[m][row][col] = sum_k A[row][k] W_m[k][col] for the staged A (rows = sequences).
 struct BmmArgs {
     const void* a;             // staged operand (BprepArgs::a)
