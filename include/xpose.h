@@ -455,6 +455,17 @@ int  xp_session_kv_download(xp_session* s, int layer, int which, uint32_t pos0, 
 /* Moves the position without running the network (the cache rows below
  * `pos` must already hold keys/values, e.g. from xp_session_kv_upload). */
 int  xp_session_set_position(xp_session* s, uint32_t pos);
+/* Poll rounds (each one device round trip, ~0.4-1 us) a cross-workgroup
+ * wait takes before it gives up: the persistent token kernel's waits
+ * (XP_EXEC_TOKEN) and, on the graph paths, the exchange-mode decode
+ * attention's (chosen when all its splits fit the device at once). The step
+ * then returns XP_E_DEVICE, its logits and appended KV rows are not valid,
+ * and the session needs xp_session_set_position before the next step.
+ * Default 2^18 (~0.1-0.25 s), at most 2^24; 0 fails every wait that its
+ * first read does not satisfy (tests of the error path). No counterpart in
+ * the reference, whose dispatches never wait on each other
+ * (examples/llm/decode.cpp:1824-1826 errors, never hangs). */
+int  xp_session_set_spin_limit(xp_session* s, uint32_t rounds);
 int  xp_session_prefill(xp_session* s, const uint32_t* ids, uint32_t n);
 int  xp_session_decode_step(xp_session* s, uint32_t* token);
 /* n greedy steps queued back to back with one wait; tokens[i] is step i's id. */
@@ -517,9 +528,10 @@ int xp_batch_exec_mode(const xp_batch* b, int32_t* mode);
  * / 1 (0 where it had no tile), then its start at out[n_layers*14*G + w].
  * read with out == NULL sets *n_out to the entry count. */
 int xp_batch_step_trace(xp_batch* b, int enable);
-/* Poll rounds (each ~1 us) a wait of the step kernel takes before it gives
- * up and the step returns XP_E_DEVICE; default 2^20, at most 2^24. A small
- * value forces that path (tests of the error handling). */
+/* Poll rounds (each ~1 us) a wait takes before it gives up and the step
+ * returns XP_E_DEVICE: the step kernel's waits (default 2^20) and, on the
+ * graph path, the exchange-mode decode attention's (default 2^18); at most
+ * 2^24. A small value forces that path (tests of the error handling). */
 int xp_batch_set_spin_limit(xp_batch* b, uint32_t rounds);
 int xp_batch_step_trace_read(xp_batch* b, unsigned long long* out, size_t n, size_t* n_out);
 int xp_batch_destroy(xp_batch* b);

@@ -183,6 +183,9 @@ public:
     // The seeded synthetic model of the benchmark configurations.
     void synthesize(uint32_t seed) { check(xp_session_synthesize(s_, seed), "xp_session_synthesize"); }
     void set_position(uint32_t pos) { check(xp_session_set_position(s_, pos), "xp_session_set_position"); }
+    void set_spin_limit(uint32_t rounds) {
+        check(xp_session_set_spin_limit(s_, rounds), "xp_session_set_spin_limit");
+    }
     void kv_upload(int layer, int which, uint32_t pos0, uint32_t n, const uint16_t* rows) {
         check(xp_session_kv_upload(s_, layer, which, pos0, n, rows), "xp_session_kv_upload");
     }

@@ -372,3 +372,47 @@ def test_gpu_batch_error_paths(xp, xo):
         b.forward([1, 99999])                 # token >= vocab
     b.close()
     sess.close()
+
+
+@pytest.mark.gpu
+def test_gpu_batch_graph_attention_timeout_recovers(xp, xo):
+    """The batched graph's exchange-mode decode attention (the global layer of
+    a 6-layer model at max_seq 1024: 2 sequences x 32 splits, all resident)
+    with its spin limit forced to 0: the step returns XP_E_DEVICE, the
+    positions stay, the records and tickets start over, and the same step
+    run again with the default limit equals a second batch's, bit for bit."""
+    X = xp
+    print("case batch graph attention forced timeout", flush=True)
+    cfg = X.XpConfig.gemma3_1b(n_layers=6, vocab=16384, max_seq=1024)
+    sess, _ = build(X, xo, cfg)
+    kvd = cfg.n_kv_heads * cfg.head_dim
+    depths = np.array([300, 700], np.int64)
+    ba = X.DecodeBatch(sess, 2, 1024, X.XP_EXEC_GRAPH)
+    bb = X.DecodeBatch(sess, 2, 1024, X.XP_EXEC_GRAPH)
+    for i, d in enumerate(depths):
+        for l in range(cfg.n_layers):
+            for which in (0, 1):
+                rows = X.synth_normal_f16(int(d) * kvd, 50 + i, 2 * l + which)
+                ba.kv_upload(i, l, which, 0, rows)
+                bb.kv_upload(i, l, which, 0, rows)
+    ba.set_positions(depths)
+    bb.set_positions(depths)
+    ba.forward([11, 22])
+    bb.forward([11, 22])
+    ba.set_spin_limit(0)
+    with pytest.raises(X.XposeError) as ei:
+        ba.forward([33, 44])
+    assert ei.value.code == -5 and "limit" in str(ei.value), ei.value
+    assert np.array_equal(ba.positions(), depths + 1)
+    ba.set_spin_limit(1 << 18)
+    ba.forward([33, 44])
+    bb.forward([33, 44])
+    for i in range(2):
+        assert np.array_equal(ba.last_logits(i).view(np.uint32), bb.last_logits(i).view(np.uint32)), i
+        for l in range(cfg.n_layers):
+            for which in (0, 1):
+                assert np.array_equal(ba.kv_download(i, l, which, int(depths[i]) + 1, 1),
+                                      bb.kv_download(i, l, which, int(depths[i]) + 1, 1)), (i, l, which)
+    ba.close()
+    bb.close()
+    sess.close()

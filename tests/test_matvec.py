@@ -213,12 +213,13 @@ def test_gpu_fp16_decode_all_patterns(xp, xo):
 @pytest.mark.gpu
 @pytest.mark.parametrize("name,rows,cols", [("q", 1152, 1024), ("kv", 1152, 256),
                                             ("o_proj", 1024, 1152), ("down", 6912, 1152),
-                                            ("gate", 1152, 6912)])
+                                            ("gate", 1152, 6912), ("deep", 16384, 4096)])
 def test_gpu_matvec_auto_plan_repeatable(xp, xo, name, rows, cols):
-    """The automatic plan (split 0): workgroup tasks per (column group,
-    k-chunk) with the last arrival summing the chunks in order for the narrow
-    shapes, one workgroup per column group for the wide one. The same call
-    twice gives the same bits."""
+    """The automatic plan (split 0): column-slice workgroups over the whole k
+    for the Gemma shapes (k <= 8192: no partials, no tickets), and for the
+    deep one (k 16384) workgroup tasks per (column group, k-chunk), 8 chunks
+    whose last arrival sums the partials in order. The same call twice gives
+    the same bits."""
     print(f"case matvec auto plan {name}", flush=True)
     wq, sc, x = synth_case(xp, rows, cols)
     a = run_mv(xp, wq, sc, x, rows, cols, 0)

@@ -521,3 +521,72 @@ def test_gpu_token_trace_timeline(xp):
     assert (a[:, :, 1] >= 0).all() and (a[:, :, 2] >= 0).all()
     sess.trace(False)
     sess.close()
+
+
+@pytest.mark.gpu
+def test_gpu_token_kernel_timeout_recovers(xp):
+    """The token kernel's bounded waits, forced from the host: with a spin
+    limit of 0 every wait that its first read does not satisfy gives up,
+    every workgroup still finishes, and the step returns XP_E_DEVICE with the
+    position unchanged; after xp_session_set_position (which clears the
+    status word) and the default limit back, the session recomputes the
+    same context and its logits and next greedy ids are bit-equal to a fresh
+    session's (the reference errors, never hangs: decode.cpp:1824-1826)."""
+    X = xp
+    print("case session token kernel forced timeout", flush=True)
+    cfg = cfg_small(X, n_layers=3, vocab=16384, max_seq=64, exec_mode=X.XP_EXEC_TOKEN)
+    a, b = X.DecodeSession(cfg), X.DecodeSession(cfg)
+    for s in (a, b):
+        s.synthesize(0x5EED0006)
+        s.prefill([7, 8, 9])
+    a.set_spin_limit(0)
+    with pytest.raises(X.XposeError) as ei:
+        a.decode_step()
+    assert ei.value.code == -5 and "limit" in str(ei.value), ei.value
+    assert a.position == 3
+    with pytest.raises(X.XposeError):
+        a.decode_step()                      # the status stays set until a position is set
+    a.set_spin_limit(1 << 18)
+    a.set_position(2)
+    a.prefill([9])
+    assert np.array_equal(a.last_logits().view(np.uint32), b.last_logits().view(np.uint32))
+    got = [a.decode_step() for _ in range(3)]
+    want = [b.decode_step() for _ in range(3)]
+    assert got == want
+    assert np.array_equal(a.last_logits().view(np.uint32), b.last_logits().view(np.uint32))
+    with pytest.raises(X.XposeError):
+        a.set_spin_limit(1 << 25)
+    a.close()
+    b.close()
+
+
+@pytest.mark.gpu
+def test_gpu_graph_attention_timeout_recovers(xp):
+    """The graph path's exchange-mode decode attention (a global layer at
+    max_seq 1024: 32 splits, all resident, combining through tagged records)
+    with its spin limit forced to 0: the step returns XP_E_DEVICE instead of
+    NaN logits reported as success, the records and tickets start over, and
+    after xp_session_set_position the session's logits and next greedy ids
+    are bit-equal to a fresh session's."""
+    X = xp
+    print("case session graph attention forced timeout", flush=True)
+    cfg = cfg_small(X, n_layers=6, vocab=16384, max_seq=1024, exec_mode=X.XP_EXEC_GRAPH)
+    a, b = X.DecodeSession(cfg), X.DecodeSession(cfg)
+    for s in (a, b):
+        s.synthesize(0x5EED0007)
+        s.prefill([5, 6, 7, 8])
+    a.set_spin_limit(0)
+    with pytest.raises(X.XposeError) as ei:
+        a.decode_step()
+    assert ei.value.code == -5 and "limit" in str(ei.value), ei.value
+    assert a.position == 4
+    a.set_spin_limit(1 << 18)
+    a.set_position(3)
+    a.prefill([8])
+    assert np.array_equal(a.last_logits().view(np.uint32), b.last_logits().view(np.uint32))
+    got = [a.decode_step() for _ in range(3)]
+    want = [b.decode_step() for _ in range(3)]
+    assert got == want
+    assert np.array_equal(a.last_logits().view(np.uint32), b.last_logits().view(np.uint32))
+    a.close()
+    b.close()

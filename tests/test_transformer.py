@@ -238,10 +238,20 @@ def test_gpu_qk_norm_rope_append(xp, xo, pos, theta):
     assert np.abs(kb - f16_bits(kn).astype(np.int32)).max() <= 1
 
 
-def run_attention(xp, q, kb, vb, span, kv0, scale):
+def run_attention(xp, q, kb, vb, span, kv0, scale, timed=False):
+    """xp_attention_decode (its splits combine through the arrival tickets),
+    or with timed the measuring entry, whose launches take the exchange mode
+    when every split fits a CU at once (its error word checked after)."""
     d = sentinel(xp, HEADS * HEAD_DIM)
-    xp.call("xp_attention_decode", d.vp, hold(dev(xp, q)), hold(dev(xp, kb)), hold(dev(xp, vb)), HEADS,
-            KV_HEADS, HEAD_DIM, span, kv0, scale, None)
+    if timed:
+        K = (C.c_void_p * 1)(hold(dev(xp, kb)).value)
+        V = (C.c_void_p * 1)(hold(dev(xp, vb)).value)
+        ms = C.c_float()
+        xp.call("xp_attention_decode_timed", d.vp, hold(dev(xp, q)), K, V, 1, HEADS, KV_HEADS, HEAD_DIM,
+                span, kv0, scale, 2, None, C.byref(ms))
+    else:
+        xp.call("xp_attention_decode", d.vp, hold(dev(xp, q)), hold(dev(xp, kb)), hold(dev(xp, vb)), HEADS,
+                KV_HEADS, HEAD_DIM, span, kv0, scale, None)
     xp.synchronize()
     return d.download(np.float32)
 
@@ -254,7 +264,9 @@ def test_gpu_attention(xp, xo, seq, kv0):
     """Spans 1..8192: up to 128 splits of at least 32 keys, combined in one
     level (at most 16 splits) or two (groups of 16; 1100 keys: 35 splits,
     the last group of 3; 3600: 113 splits, the last group of 1; 4097 and
-    8192: 128 splits of 33 and 64 keys)."""
+    8192: 128 splits of 33 and 64 keys) through the kernel-level entry's
+    tickets, and through the exchange mode of the timed entry (more than 16
+    splits, all resident: tagged records, one poll)."""
     print(f"case attention seq={seq} kv0={kv0}", flush=True)
     r = rng()
     q = u(r, HEADS * HEAD_DIM)
@@ -269,6 +281,11 @@ def test_gpu_attention(xp, xo, seq, kv0):
     # the combine sums in a fixed order: the same call gives the same bits
     again = run_attention(xp, q, kb, vb, span, kv0, scale)
     assert np.array_equal(got.view(np.uint32), again.view(np.uint32))
+    xg = run_attention(xp, q, kb, vb, span, kv0, scale, timed=True)
+    ok, msg = allclose_report(xg, want, RTOL, 1e-5)
+    assert ok, "exchange mode: " + msg
+    assert np.array_equal(xg.view(np.uint32), run_attention(xp, q, kb, vb, span, kv0, scale,
+                                                            timed=True).view(np.uint32))
     if kv0:
         # Negative control (kernel_tests.cpp:538-552): ignoring kv_start gives
         # a measurably different answer, so the check above can see it.
@@ -279,10 +296,9 @@ def test_gpu_attention(xp, xo, seq, kv0):
 
 @pytest.mark.gpu
 def test_gpu_attention_ticket_levels():
-    """Spans of more than 16 splits combine through the exchange mode when
-    every workgroup fits a CU at once (the cases above); the two-level ticket
-    chain they otherwise take is checked here, the same cases in a child
-    process with the exchange mode off (XP_ATTN_EXCHANGE=0)."""
+    """XP_ATTN_EXCHANGE=0 in the environment turns the exchange mode off: the
+    cases above of more than 16 splits in a child process, where the timed
+    entry's launches take the two-level ticket chain too."""
     import os
     import subprocess
     import sys

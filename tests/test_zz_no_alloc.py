@@ -28,8 +28,20 @@ def same_bits(a, b):
 @pytest.mark.gpu
 def test_gpu_noalloc_matvec_equals_library_entry(xp, xo):
     X = xp
-    # 1. down 6912 x 1152, automatic plan: k-chunk workgroups whose partials
-    #    (8 chunks x 18 groups x 64) and tickets are in the fixed scratch
+    # 1. a shape deeper than one workgroup's k (16384 x 4096, 512 blocks):
+    #    the automatic plan's k-chunk workgroups, whose partials (8 chunks x
+    #    64 groups x 64 = 32,768 floats) and arrival tickets are in the fixed
+    #    scratch; twice, so the second call runs on tickets the first
+    #    returned to zero
+    print("case noalloc deep k-chunks 16384 x 4096", flush=True)
+    wq, sc, x = synth_case(X, 16384, 4096, seed=5)
+    b = run_mv(X, wq, sc, x, 16384, 4096, 0)
+    for _ in range(2):
+        assert same_bits(run_na(X, wq, sc, x, 16384, 4096, 0), b)
+    want = xo.mv_km4(x, wq, sc, 16384, 4096, 0)
+    assert np.abs(b - want).max() / np.abs(want).max() < 1e-5
+    # down 6912 x 1152, automatic plan: column-slice workgroups over the
+    # whole k (no partials, no tickets)
     print("case noalloc down auto", flush=True)
     wq, sc, x = synth_case(X, 6912, 1152)
     a = run_na(X, wq, sc, x, 6912, 1152, 0)

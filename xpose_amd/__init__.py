@@ -228,6 +228,7 @@ def _declare(lib: C.CDLL) -> None:
         "xp_session_kv_upload": (i32, [vp, i32, i32, u32, u32, vp]),
         "xp_session_kv_download": (i32, [vp, i32, i32, u32, u32, vp]),
         "xp_session_set_position": (i32, [vp, u32]),
+        "xp_session_set_spin_limit": (i32, [vp, u32]),
         "xp_session_prefill": (i32, [vp, vp, u32]),
         "xp_session_decode_step": (i32, [vp, P(u32)]),
         "xp_session_decode_steps": (i32, [vp, u32, vp]),
@@ -585,6 +586,11 @@ class DecodeSession:
 
     def set_position(self, pos: int) -> None:
         call("xp_session_set_position", self.h, pos)
+
+    def set_spin_limit(self, rounds: int) -> None:
+        """Poll rounds a token-kernel wait takes before the step fails with
+        XP_E_DEVICE (0: every wait not satisfied by its first read fails)."""
+        call("xp_session_set_spin_limit", self.h, rounds)
 
     def prefill(self, ids) -> None:
         ids = np.ascontiguousarray(ids, np.uint32)

@@ -86,6 +86,8 @@ struct Batch {
     void* af = nullptr;
     float* asumf = nullptr;
     uint32_t* h_status = nullptr;        // pinned
+    uint32_t* h_attn = nullptr;          // pinned: the attention tickets after a graph step
+    uint32_t attn_spin = 1u << 18;       // exchange-mode attention's spin limit (graph path)
     unsigned long long* d_trace = nullptr;   // the step kernel's stage timeline, when on
     size_t trace_n = 0;
 
@@ -207,6 +209,7 @@ int Batch::record() {
         aa.scale = w.attn_scale;
         aa.part = attn_part;
         aa.tickets = attn_tickets;
+        aa.spin_limit = attn_spin;
         aa.batch = B;
         aa.bq = qd;
         aa.bcache = prefill ? 0 : size_t(S) * kvd;
@@ -368,6 +371,9 @@ int Batch::setup_step(int exec) {
         aa.scale = w.attn_scale;
         aa.part = attn_part;
         aa.tickets = attn_tickets;
+        // an exchange-mode wait that times out sets the step's status word (bs.status)
+        aa.status = reinterpret_cast<uint32_t*>(step_arena + cnt_off) +
+                    size_t(c.n_layers) * kBsStages * kBsMaxTiles + 1;
         aa.batch = B;
         aa.bq = qd;
         aa.bcache = size_t(S) * kvd;
@@ -408,7 +414,7 @@ int Batch::setup_step(int exec) {
     bs.n_gu = n_gu;
     bs.flags = reinterpret_cast<uint32_t*>(step_arena + cnt_off);
     bs.epoch = bs.flags + size_t(c.n_layers) * kBsStages * kBsMaxTiles;
-    bs.status = bs.epoch + 1;
+    bs.status = bs.epoch + 1;   // the attention tiles' AttnArgs::status points here too
     bs.exit_cnt = bs.epoch + 2;
     if (ncb_q > kBsMaxTiles || ncb_o > kBsMaxTiles || n_gu > kBsMaxTiles || ncb_d * ns_d > kBsMaxTiles ||
         B > kBsMaxTiles)
@@ -460,9 +466,28 @@ int Batch::forward(const uint32_t* tokens) {
         XP_HIP(hipMemcpyAsync(h_val, oval, size_t(B) * kCand * 4, hipMemcpyDeviceToHost, st));
         XP_HIP(hipMemcpyAsync(h_idx, oidx, size_t(B) * kCand * 4, hipMemcpyDeviceToHost, st));
     }
+    const size_t attn_words = size_t(B) * w.cfg.n_kv_heads * kAttnTicketsPerHead;
     if (step_kernel) XP_HIP(hipMemcpyAsync(h_status, bs.status, 4, hipMemcpyDeviceToHost, st));
+    else XP_HIP(hipMemcpyAsync(h_attn, attn_tickets, attn_words * 4, hipMemcpyDeviceToHost, st));
     XP_HIP(hipStreamSynchronize(st));
     (void)hipEventElapsedTime(&last_ms, ev[0], ev[1]);
+    if (!step_kernel) {
+        uint32_t err = 0;
+        for (size_t i = kAttnXErrWord; i < attn_words; i += kAttnTicketsPerHead) err |= h_attn[i];
+        if (err) {
+            // an exchange-mode attention wait timed out (its splits were not
+            // resident at once): outputs hold NaN; the records and tickets
+            // start over from zero, positions stay where they were
+            XP_HIP(hipMemcpy(d_pos, pos.data(), B * 4, hipMemcpyHostToDevice));
+            XP_HIP(hipMemset(attn_part, 0, (size_t(B) * attn_part_seq + 1) * 4));
+            XP_HIP(hipMemset(attn_tickets, 0, attn_words * 4));
+            XP_HIP(hipDeviceSynchronize());
+            logits_valid = false;
+            return set_error(XP_E_DEVICE, "xp_batch_forward: a decode attention wait ran past its "
+                             "limit (another kernel held CUs of this GPU); the step's results and "
+                             "the KV rows it appended are not valid, positions are unchanged");
+        }
+    }
     if (step_kernel && h_status[0] != 0u) {
         // a wait ran past its limit (the grid was not resident at once): the
         // step's results are not valid
@@ -502,6 +527,7 @@ void release(Batch* b) {
     if (b->step_arena) (void)hipFree(b->step_arena);
     if (b->d_trace) (void)hipFree(b->d_trace);
     if (b->h_status) (void)hipHostFree(b->h_status);
+    if (b->h_attn) (void)hipHostFree(b->h_attn);
     if (b->h_tok) (void)hipHostFree(b->h_tok);
     if (b->h_val) (void)hipHostFree(b->h_val);
     if (b->h_idx) (void)hipHostFree(b->h_idx);
@@ -635,7 +661,9 @@ int make_batch(const xp_session* weights, uint32_t n_seq, uint32_t max_seq, bool
     b.d_pos = reinterpret_cast<uint32_t*>(nxt());
     if (hipHostMalloc(reinterpret_cast<void**>(&b.h_tok), B * 4) != hipSuccess ||
         hipHostMalloc(reinterpret_cast<void**>(&b.h_val), size_t(B) * kCand * 4) != hipSuccess ||
-        hipHostMalloc(reinterpret_cast<void**>(&b.h_idx), size_t(B) * kCand * 4) != hipSuccess)
+        hipHostMalloc(reinterpret_cast<void**>(&b.h_idx), size_t(B) * kCand * 4) != hipSuccess ||
+        hipHostMalloc(reinterpret_cast<void**>(&b.h_attn),
+                      size_t(B) * c.n_kv_heads * kAttnTicketsPerHead * 4) != hipSuccess)
         return fail(XP_E_NOMEM, "pinned host memory");
     if (hipEventCreate(&b.ev[0]) != hipSuccess || hipEventCreate(&b.ev[1]) != hipSuccess)
         return fail(XP_E_HIP, "hipEventCreate failed");
@@ -744,14 +772,14 @@ int xp_batch_step_trace(xp_batch* h, int enable) {
 int xp_batch_set_spin_limit(xp_batch* h, uint32_t rounds) {
     XP_REQUIRE(h, "null pointer");
     Batch& b = h->b;
-    XP_REQUIRE(b.step_kernel, "xp_batch_set_spin_limit: the batch does not run the step kernel");
     XP_REQUIRE(rounds <= (1u << 24), "xp_batch_set_spin_limit: rounds=%u > 2^24", rounds);
     XP_HIP(hipStreamSynchronize(b.st));
     if (b.graph) {
         (void)hipGraphExecDestroy(b.graph);   // recaptured with the new limit
         b.graph = nullptr;
     }
-    b.bs.spin_limit = rounds;
+    b.bs.spin_limit = rounds;   // the step kernel's waits
+    b.attn_spin = rounds;       // the graph's exchange-mode attention
     return XP_OK;
 }
 

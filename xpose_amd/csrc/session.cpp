@@ -172,6 +172,9 @@ struct Session {
     uint32_t* hist = nullptr;    // [max_seq] token run at each position
     uint32_t* h_ids = nullptr;   // pinned staging for host-chosen token ids
     uint32_t* h_stat = nullptr;  // pinned: [0] device status word after a step
+    uint32_t* h_attn = nullptr;  // pinned: the attention tickets after a step (graph paths)
+    uint32_t attn_spin = 1u << 18;   // exchange-mode attention's spin limit (graph paths)
+    size_t attn_floats = 0;      // attn_part's size
     hipGraphExec_t graph[3] = {nullptr, nullptr, nullptr};   // prefill, greedy, harvest
     uint32_t launches[3] = {0, 0, 0};
     int mode = XP_EXEC_GRAPH;    // XP_EXEC_TOKEN (persistent kernel), _GRAPH or _LAUNCH
@@ -241,6 +244,7 @@ int Session::record(int variant, uint32_t& n) {
         aa.scale = attn_scale();
         aa.part = attn_part;
         aa.tickets = tickets + kTicketAttn;
+        aa.spin_limit = attn_spin;
         const uint32_t max_span = glob || c.sliding_window == 0
                                       ? c.max_seq : std::min(c.sliding_window, c.max_seq);
         XP_STEP(launch_attention(aa, max_span, st));
@@ -432,6 +436,7 @@ int destroy(xp_session* h) {
     if (s.trace_buf) (void)hipFree(s.trace_buf);
     if (s.h_ids) (void)hipHostFree(s.h_ids);
     if (s.h_stat) (void)hipHostFree(s.h_stat);
+    if (s.h_attn) (void)hipHostFree(s.h_attn);
     if (s.st) (void)hipStreamDestroy(s.st);
     delete h;
     return XP_OK;
@@ -541,6 +546,7 @@ int setup_token(Session& s) {
     // exchange device-coherent.
     a.xcd_local = 0;
     a.xcd_ids = 0;
+    a.spin_limit = kTokSpinLimit;
     if (c.placement == XP_PLACE_AUTO && grid >= 8 && grid % 8 == 0) {
         auto xcc = [&](uint32_t w) { return probe[w] & 0xFFu; };
         bool periodic = true;
@@ -562,8 +568,16 @@ int setup_token(Session& s) {
 // wait for another workgroup's data ran past its spin limit. queue_status
 // copies it to pinned memory behind the queued work; check_status reads that
 // copy after the stream has been synchronised.
+// On the graph paths it copies the decode attention's tickets instead: an
+// exchange-mode wait that timed out (its splits were not resident at once)
+// leaves its head's error word set.
 int queue_status(Session& s) {
-    if (s.mode != XP_EXEC_TOKEN) return XP_OK;
+    if (s.mode != XP_EXEC_TOKEN) {
+        const size_t words = size_t(s.cfg.n_kv_heads) * kAttnTicketsPerHead;
+        XP_HIP(hipMemcpyAsync(s.h_attn, s.tickets + kTicketAttn, words * 4, hipMemcpyDeviceToHost,
+                              s.st));
+        return XP_OK;
+    }
     XP_HIP(hipMemcpyAsync(s.h_stat, s.state + 2, 4, hipMemcpyDeviceToHost, s.st));
     return XP_OK;
 }
@@ -571,7 +585,21 @@ int queue_status(Session& s) {
 // step invalid until the caller sets a position (xp_session_set_position or
 // xp_session_reset), which also clears the status word.
 int check_status(Session& s) {
-    if (s.mode != XP_EXEC_TOKEN) return XP_OK;
+    if (s.mode != XP_EXEC_TOKEN) {
+        uint32_t err = 0;
+        for (uint32_t g = 0; g < s.cfg.n_kv_heads; ++g)
+            err |= s.h_attn[size_t(g) * kAttnTicketsPerHead + kAttnXErrWord];
+        if (!err) return XP_OK;
+        // the attention's records and tickets start over from zero
+        XP_HIP(hipMemsetAsync(s.attn_part, 0, s.attn_floats * 4, s.st));
+        XP_HIP(hipMemsetAsync(s.tickets + kTicketAttn, 0,
+                              size_t(s.cfg.n_kv_heads) * kAttnTicketsPerHead * 4, s.st));
+        XP_HIP(hipStreamSynchronize(s.st));
+        s.logits_valid = false;
+        return set_error(XP_E_DEVICE, "decode attention: an exchange-mode wait ran past its spin "
+                         "limit (another kernel held CUs of this GPU); the step's results and KV "
+                         "rows are invalid: set a position to go on");
+    }
     const uint32_t st = s.h_stat[0];
     if (st & 2u) {
         // Later launches exchange every value through the device coherence
@@ -752,6 +780,7 @@ int xp_session_create(const xp_config* cfg, xp_session** out) {
         mvp = std::max(mvp, mv_partial_floats(H, c.vocab, 0, s.n_cu));
         s.mv_partial_cap = std::max<size_t>(mvp, 64);
         const size_t attnp = attn_partial_floats(c.n_kv_heads, c.n_heads, c.head_dim);
+        s.attn_floats = attnp;
         const uint32_t nc = c.sample_mode == 1 ? 4 * c.topk_parts : 4;
         const size_t sizes[] = {
             H * 4, std::max(H, qd) * 4, H * 4, qd * 4, kvd * 4, kvd * 4, qd * 4, kvd * 4, qd * 4,
@@ -777,7 +806,9 @@ int xp_session_create(const xp_config* cfg, xp_session** out) {
         s.state = (uint32_t*)nxt(); s.hist = (uint32_t*)nxt();
         if (hipHostMalloc(reinterpret_cast<void**>(&s.h_ids), size_t(c.max_seq) * 4) !=
                 hipSuccess ||
-            hipHostMalloc(reinterpret_cast<void**>(&s.h_stat), 16) != hipSuccess) {
+            hipHostMalloc(reinterpret_cast<void**>(&s.h_stat), 16) != hipSuccess ||
+            hipHostMalloc(reinterpret_cast<void**>(&s.h_attn),
+                          size_t(kMaxKvHeads) * kAttnTicketsPerHead * 4) != hipSuccess) {
             destroy(h);
             return set_error(XP_E_NOMEM, "xp_session_create: pinned staging");
         }
@@ -937,6 +968,22 @@ int xp_session_set_position(xp_session* h, uint32_t pos) {
 }
 
 int xp_session_reset(xp_session* h) { return xp_session_set_position(h, 0); }
+
+int xp_session_set_spin_limit(xp_session* h, uint32_t rounds) {
+    XP_REQUIRE(h, "null session");
+    Session& s = h->s;
+    XP_REQUIRE(rounds <= (1u << 24), "xp_session_set_spin_limit: rounds=%u > 2^24", rounds);
+    XP_HIP(hipStreamSynchronize(s.st));
+    s.ta.spin_limit = rounds;   // passed by value at each token-kernel launch
+    if (s.attn_spin != rounds) {
+        s.attn_spin = rounds;   // the graphs hold it: recaptured at their next use
+        for (auto& g : s.graph) {
+            if (g) (void)hipGraphExecDestroy(g);
+            g = nullptr;
+        }
+    }
+    return XP_OK;
+}
 
 int xp_session_prefill(xp_session* h, const uint32_t* ids, uint32_t n) {
     XP_REQUIRE(h, "null session");

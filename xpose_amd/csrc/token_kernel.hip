@@ -83,7 +83,6 @@ constexpr bool kTkGlobalPairs = XP_TOK_GLOBAL_PAIRS != 0;
 constexpr uint32_t kTkGlobalCD  = XP_TOK_GLOBAL_CD;
 constexpr uint32_t kTkMaxBlk    = 64;                    // staged 32-blocks (2048 k)
 constexpr int      kTkMaxGrid   = 1024;
-constexpr uint32_t kSpinLimit   = 1u << 24;
 constexpr int      kTkBig       = 17408;                 // floats of stage scratch
 constexpr int      kTkMaxLayers = 64;
 constexpr int      kTkLmDepth   = 3;     // lm_head units in flight per wave (4 and 6 measured no faster)
@@ -212,12 +211,15 @@ __device__ __forceinline__ bool ll_ok(u32x4 v, uint32_t tag) { return (v.y == ta
 // Loads the N slot pairs at byte offsets off[i] (+ soff) that are active and
 // re-reads them until both tags of every pair are `tag`, sleeping SLEEP x 64
 // cycles between rounds (a wait that is long by construction can poll less).
-// Bounded: past the spin limit the thread records an error in state[2] and
-// keeps what it has. Per thread; no barrier.
+// Bounded: past `limit` re-reads the thread records an error in state[2] and
+// keeps what it has; once any wait has recorded one, every other wait gives
+// up within 256 rounds (or at its own limit), so the grid drains. A limit of
+// 0 fails every wait that is not satisfied by its first read (the forced
+// error path of the tests). Per thread; no barrier.
 template <int N, int SLEEP = 0>
 __device__ __forceinline__ void ll_wait(rsrc_t r, uint32_t soff, const uint32_t (&off)[N],
                                         const bool (&act)[N], u32x4 (&v)[N], uint32_t tag,
-                                        uint32_t* state) {
+                                        uint32_t* state, uint32_t limit) {
     const u32x4 ready = {0u, tag, 0u, tag};
 #pragma unroll
     for (int i = 0; i < N; ++i) v[i] = act[i] ? ll_ld2(r, off[i], soff) : ready;
@@ -227,14 +229,12 @@ __device__ __forceinline__ void ll_wait(rsrc_t r, uint32_t soff, const uint32_t 
 #pragma unroll
         for (int i = 0; i < N; ++i) ok &= ll_ok(v[i], tag);
         if (ok) break;
-        if ((++spins & 255u) == 0u) {
-            if (ld_dev(state + 2) != 0u) break;
-            if (spins > kSpinLimit) {
-                __hip_atomic_fetch_or((XP_GLOBAL uint32_t*)(state + 2), 1u, __ATOMIC_RELAXED,
-                                      __HIP_MEMORY_SCOPE_AGENT);
-                break;
-            }
+        if (++spins > limit) {
+            __hip_atomic_fetch_or((XP_GLOBAL uint32_t*)(state + 2), 1u, __ATOMIC_RELAXED,
+                                  __HIP_MEMORY_SCOPE_AGENT);
+            break;
         }
+        if ((spins & 255u) == 0u && ld_dev(state + 2) != 0u) break;
         // The slots change under us: re-read them all (a stale-only re-read
         // does not unroll, and the ready pairs cannot change).
         if constexpr (SLEEP > 0) __builtin_amdgcn_s_sleep(SLEEP);
@@ -807,7 +807,7 @@ __global__ __launch_bounds__(kTkThreads) void token_kernel(TokArgs a) {
                 own_offsets(&off[0], uint32_t(lay.xb) + kOwn * tid);
 #pragma unroll
                 for (uint32_t i = 0; i < kOwnP; ++i) act[i] = true;
-                ll_wait(rr, soff, off, act, v, tag, a.state);
+                ll_wait(rr, soff, off, act, v, tag, a.state, a.spin_limit);
                 own_unpack(xb, &v[0]);
             }
             constexpr uint32_t NL = kOwnP * NCH;
@@ -819,7 +819,7 @@ __global__ __launch_bounds__(kTkThreads) void token_kernel(TokArgs a) {
                 own_offsets(&off[kOwnP * c], uint32_t(lay.dnp) + c * H + kOwn * tid);
 #pragma unroll
             for (uint32_t i = 0; i < NL; ++i) act[i] = true;
-            ll_wait(rr, soff, off, act, v, tag, a.state);
+            ll_wait(rr, soff, off, act, v, tag, a.state, a.spin_limit);
             own_unpack(t, &v[0]);
 #pragma unroll
             for (uint32_t c = 1; c < NCH; ++c) {
@@ -1057,7 +1057,7 @@ __global__ __launch_bounds__(kTkThreads) void token_kernel(TokArgs a) {
                 const uint32_t p0 = uint32_t(lay.qkv) + wave * kTkHD + 2u * lane;
                 off[0] = p0 * 8u;
                 off[1] = (p0 + kTkHD / 2u) * 8u;
-                ll_wait(rr, soff, off, act, v, tag, a.state);
+                ll_wait(rr, soff, off, act, v, tag, a.state, a.spin_limit);
                 float e[4] = {__uint_as_float(v[0].x), __uint_as_float(v[0].z), __uint_as_float(v[1].x),
                               __uint_as_float(v[1].z)};
                 if (wave <= NH) {
@@ -1276,7 +1276,7 @@ __global__ __launch_bounds__(kTkThreads) void token_kernel(TokArgs a) {
                 const uint32_t p0 = uint32_t(lay.qkv) + vec * kTkHD + 2u * lane;
                 off[0] = p0 * 8u;
                 off[1] = (p0 + kTkHD / 2u) * 8u;
-                ll_wait(rr, soff, off, act, v, tag, a.state);
+                ll_wait(rr, soff, off, act, v, tag, a.state, a.spin_limit);
                 float e[4] = {__uint_as_float(v[0].x), __uint_as_float(v[0].z), __uint_as_float(v[1].x),
                               __uint_as_float(v[1].z)};
                 if (wave <= HPW) {
@@ -1483,7 +1483,7 @@ __global__ __launch_bounds__(kTkThreads) void token_kernel(TokArgs a) {
                         const uint32_t s = ic / PP, e = ic % PP;
                         off[r] = (base + s * rstride + (e == 0u ? 0u : 2u + d0 + 2u * (e - 1u))) * 8u;
                     }
-                    ll_wait(rr, soff, off, act, v, tag, a.state);
+                    ll_wait(rr, soff, off, act, v, tag, a.state, a.spin_limit);
 #pragma unroll
                     for (int r = 0; r < 4; ++r) {
                         const uint32_t i = b + uint32_t(r) * kTkThreads + tid;
@@ -1549,7 +1549,7 @@ __global__ __launch_bounds__(kTkThreads) void token_kernel(TokArgs a) {
 #pragma unroll
                 for (uint32_t j = 0; j < kOwnP; ++j) act[j] = true;
                 own_offsets(off, uint32_t(lay.atto) + c * (QD / Sh::KO) + kOwn * tid);
-                ll_wait(rr, soff, off, act, v, tag, a.state);
+                ll_wait(rr, soff, off, act, v, tag, a.state, a.spin_limit);
                 float x[kOwn];
                 own_unpack(x, v);
                 own_stage(S, x, tid);
@@ -1601,7 +1601,7 @@ __global__ __launch_bounds__(kTkThreads) void token_kernel(TokArgs a) {
                 const uint32_t off1[1] = {uint32_t(lay.atto) * 8u};
                 const bool act1[1] = {true};
                 u32x4 v1[1];
-                ll_wait<1, kGuSleep>(rr, soff, off1, act1, v1, tag, a.state);
+                ll_wait<1, kGuSleep>(rr, soff, off1, act1, v1, tag, a.state, a.spin_limit);
             }
             __syncthreads();
             if (hown) {
@@ -1613,7 +1613,7 @@ __global__ __launch_bounds__(kTkThreads) void token_kernel(TokArgs a) {
 #pragma unroll
                     for (uint32_t j = 0; j < kOwnP; ++j) act[j] = true;
                     own_offsets(&off[0], uint32_t(lay.xa) + kOwn * tid);
-                    ll_wait(rr, soff, off, act, v, tag, a.state);
+                    ll_wait(rr, soff, off, act, v, tag, a.state, a.spin_limit);
                     own_unpack(xa, &v[0]);
                 }
                 constexpr uint32_t NL = Sh::KO * kOwnP;
@@ -1625,7 +1625,7 @@ __global__ __launch_bounds__(kTkThreads) void token_kernel(TokArgs a) {
 #pragma unroll
                 for (uint32_t c = 0; c < Sh::KO; ++c)
                     own_offsets(&off[kOwnP * c], uint32_t(lay.o) + c * H + kOwn * tid);
-                ll_wait(rr, soff, off, act, v, tag, a.state);
+                ll_wait(rr, soff, off, act, v, tag, a.state, a.spin_limit);
                 own_unpack(o, &v[0]);
 #pragma unroll
                 for (uint32_t c = 1; c < Sh::KO; ++c) {
@@ -1674,7 +1674,7 @@ __global__ __launch_bounds__(kTkThreads) void token_kernel(TokArgs a) {
 #pragma unroll
                 for (uint32_t j = 0; j < kOwnP; ++j) act[j] = true;
                 own_offsets(&off[0], uint32_t(lay.gu) + k0 + kOwn * tid);
-                ll_wait(rr, soff, off, act, v, tag, a.state);
+                ll_wait(rr, soff, off, act, v, tag, a.state, a.spin_limit);
                 float hx[kOwn];
                 own_unpack(hx, &v[0]);
                 own_stage(S, hx, tid);
@@ -1801,7 +1801,7 @@ __global__ __launch_bounds__(kTkThreads) void token_kernel(TokArgs a) {
             act[r] = i < nwg;
             off[r] = 16u * (act[r] ? i : 0u);
         }
-        ll_wait(rr, am_off, off, act, v, tag, a.state);
+        ll_wait(rr, am_off, off, act, v, tag, a.state, a.spin_limit);
 #pragma unroll
         for (int r = 0; r < 4; ++r)
             if (act[r]) am_better(bv, bi, __uint_as_float(v[r].x), v[r].z);

@@ -9,6 +9,9 @@
 // rmsnorm_apply_gemma) becomes one kernel, and the six per-layer QK-norm /
 // RoPE / kv_append dispatches become one.
 #include "xp_attn_device.hpp"
+#include <algorithm>
+#include <vector>
+
 #include "xp_device.hpp"
 #include "xp_launch.hpp"
 
@@ -266,10 +269,10 @@ int plan_attention(AttnArgs& a, uint32_t max_span, bool allow_xchg, int* U_out, 
     return XP_OK;
 }
 
-int launch_attention(AttnArgs a, uint32_t max_span, hipStream_t st) {
+int launch_attention(AttnArgs a, uint32_t max_span, hipStream_t st, bool allow_xchg) {
     int U = 0;
     RopeFreq f{};
-    if (int rc = plan_attention(a, max_span, true, &U, &f); rc != XP_OK) return rc;
+    if (int rc = plan_attention(a, max_span, allow_xchg, &U, &f); rc != XP_OK) return rc;
     const bool fq = a.q_raw != nullptr;
     const uint32_t G = a.group;
     const dim3 grid(a.nsplit, a.kv_heads, a.batch), block(kAttnThreads);
@@ -350,17 +353,54 @@ int xp_qk_norm_rope_append(float* q_out, float* k_out, const float* q_raw, const
     return launch_qk(a, theta, as_stream(stream));
 }
 
-int xp_attention_decode(float* out, const float* q, const uint16_t* kcache,
-                        const uint16_t* vcache, uint32_t n_heads, uint32_t kv_heads,
-                        uint32_t head_dim, uint32_t span, uint32_t kv_start, float scale,
-                        xp_stream stream) {
+}  // extern "C"
+
+namespace {
+// One decode attention on the library's own split records. xchg: the
+// exchange mode may be chosen (its error word is then the caller's to check,
+// attention_xchg_check); otherwise the splits combine through the arrival
+// tickets, which reset themselves.
+int attention_call(float* out, const float* q, const uint16_t* kcache, const uint16_t* vcache,
+                   uint32_t n_heads, uint32_t kv_heads, uint32_t head_dim, uint32_t span,
+                   uint32_t kv_start, float scale, hipStream_t st, bool xchg) {
     XP_REQUIRE(out && q && kcache && vcache, "null pointer");
     XP_REQUIRE(span > 0, "span must be positive (the query attends at least to itself)");
     AttnArgs a{};
     a.out = out; a.q = q; a.kc = kcache; a.vc = vcache;
     a.n_heads = n_heads; a.kv_heads = kv_heads; a.head_dim = head_dim;
     a.span = span; a.kv_start = kv_start; a.scale = scale;
-    return launch_attention(a, span, as_stream(stream));
+    return launch_attention(a, span, st, xchg);
+}
+// After the stream has been synchronised: XP_E_DEVICE when an exchange-mode
+// wait on the library's records timed out (another kernel held CUs, so the
+// splits were not all resident at once); the records, epochs and error
+// words then start over from zero.
+int attention_xchg_check(uint32_t kv_heads) {
+    DeviceScratch* sc = scratch();
+    if (!sc || !sc->attn_state) return XP_OK;
+    const size_t words = std::min(sc->attn_state_words, size_t(kv_heads) * kAttnTicketsPerHead);
+    std::vector<uint32_t> h(words);
+    XP_HIP(hipMemcpy(h.data(), sc->attn_state, words * 4, hipMemcpyDeviceToHost));
+    uint32_t err = 0;
+    for (size_t g = 0; g * kAttnTicketsPerHead + kAttnXErrWord < words; ++g)
+        err |= h[g * kAttnTicketsPerHead + kAttnXErrWord];
+    if (!err) return XP_OK;
+    XP_HIP(hipMemset(sc->attn_x, 0, sc->attn_x_floats * sizeof(float)));
+    XP_HIP(hipMemset(sc->attn_state, 0, sc->attn_state_words * 4));
+    XP_HIP(hipDeviceSynchronize());
+    return set_error(XP_E_DEVICE, "attention: an exchange-mode wait ran past its spin limit (the "
+                     "splits were not resident at once); the output holds NaN");
+}
+}  // namespace
+
+extern "C" {
+
+int xp_attention_decode(float* out, const float* q, const uint16_t* kcache,
+                        const uint16_t* vcache, uint32_t n_heads, uint32_t kv_heads,
+                        uint32_t head_dim, uint32_t span, uint32_t kv_start, float scale,
+                        xp_stream stream) {
+    return attention_call(out, q, kcache, vcache, n_heads, kv_heads, head_dim, span, kv_start,
+                          scale, as_stream(stream), false);
 }
 
 int xp_attention_decode_timed(float* out, const float* q, const uint16_t* const* kcaches,
@@ -374,19 +414,22 @@ int xp_attention_decode_timed(float* out, const float* q, const uint16_t* const*
     XP_HIP(hipEventCreate(&e0));
     XP_HIP(hipEventCreate(&e1));
     int rc = XP_OK;
-    // One untimed pass over every copy so the split scratch is sized before timing.
+    // One untimed pass over every copy so the split scratch is sized before
+    // timing. The timed launches may take the exchange mode: its error word
+    // is checked once the stream has drained.
     for (uint32_t i = 0; i < ncopies && rc == XP_OK; ++i)
-        rc = xp_attention_decode(out, q, kcaches[i], vcaches[i], n_heads, kv_heads, head_dim,
-                                 span, kv_start, scale, stream);
+        rc = attention_call(out, q, kcaches[i], vcaches[i], n_heads, kv_heads, head_dim, span,
+                            kv_start, scale, st, true);
     if (rc == XP_OK && hipStreamSynchronize(st) != hipSuccess) rc = set_error(XP_E_HIP, "sync");
     if (rc == XP_OK && hipEventRecord(e0, st) != hipSuccess) rc = set_error(XP_E_HIP, "event");
     for (uint32_t i = 0; i < iters && rc == XP_OK; ++i)
-        rc = xp_attention_decode(out, q, kcaches[i % ncopies], vcaches[i % ncopies], n_heads,
-                                 kv_heads, head_dim, span, kv_start, scale, stream);
+        rc = attention_call(out, q, kcaches[i % ncopies], vcaches[i % ncopies], n_heads, kv_heads,
+                            head_dim, span, kv_start, scale, st, true);
     if (rc == XP_OK && hipEventRecord(e1, st) != hipSuccess) rc = set_error(XP_E_HIP, "event");
     if (rc == XP_OK && hipEventSynchronize(e1) != hipSuccess) rc = set_error(XP_E_HIP, "sync");
     if (rc == XP_OK && hipEventElapsedTime(ms, e0, e1) != hipSuccess)
         rc = set_error(XP_E_HIP, "elapsed");
+    if (rc == XP_OK) rc = attention_xchg_check(kv_heads);
     (void)hipEventDestroy(e0);
     (void)hipEventDestroy(e1);
     return rc;

@@ -60,10 +60,10 @@ __host__ __device__ constexpr uint32_t attn_head_floats(uint32_t G) {
     return kAttnRecords * attn_record(G) > kAttnMaxSplit * attn_xrecord(G) ? kAttnRecords * attn_record(G)
                                                                           : kAttnMaxSplit * attn_xrecord(G);
 }
-constexpr uint32_t kAttnEpoch = 1 + kAttnGroups;   // ticket word: the last exchange launch's tag
-constexpr uint32_t kAttnXErr  = 2 + kAttnGroups;   // ticket word: set when an exchange wait timed out
-constexpr uint32_t kAttnSpinLimit = 1u << 22;       // exchange poll rounds before giving up
-static_assert(kAttnTicketsPerHead == 3 + kAttnGroups, "tickets: level 2, one per group, epoch, flag");
+constexpr uint32_t kAttnEpoch = kAttnEpochWord;     // ticket word: the last exchange launch's tag
+constexpr uint32_t kAttnXErr  = kAttnXErrWord;      // ticket word: set when an exchange wait timed out
+static_assert(kAttnTicketsPerHead == 3 + kAttnGroups && kAttnEpoch == 1 + kAttnGroups &&
+              kAttnXErr == 2 + kAttnGroups, "tickets: level 2, one per group, epoch, flag");
 
 template <int M>
 __device__ __forceinline__ float swz_xor(float x) {   // x of lane ^ M within 32 lanes
@@ -519,8 +519,11 @@ __device__ __forceinline__ bool attn_tile(AttnArgs a, const RopeFreq& f, uint32_
 #pragma unroll
             for (int k = 0; k < 4; ++k) ok &= (v[k].y == xtag) & (v[k].w == xtag);
             if (ok) break;
-            if (spins > kAttnSpinLimit) {
+            if (spins > a.spin_limit) {
                 st_dev(tk + kAttnXErr, 1u);
+                if (a.status)
+                    __hip_atomic_fetch_or((XP_GLOBAL uint32_t*)a.status, 1u, __ATOMIC_RELAXED,
+                                          __HIP_MEMORY_SCOPE_AGENT);
                 last = 1u;
                 break;
             }
@@ -542,7 +545,12 @@ __device__ __forceinline__ bool attn_tile(AttnArgs a, const RopeFreq& f, uint32_
             }
         }
         __syncthreads();
-        if (s == 0 && tid == 0) st_dev(tk + kAttnEpoch, xtag);
+        // Only after a complete wait: split 0 has then seen every split's
+        // record, so every split has read the epoch and none can take the
+        // next launch's tag. After a timed-out wait the epoch stays, the
+        // error word is set, and the tickets' owner zeroes the records and
+        // the epoch before the next launch.
+        if (s == 0 && tid == 0 && !last) st_dev(tk + kAttnEpoch, xtag);
         // wave h: head h's rescale factors exp(m_r - M) (0 for an empty
         // split) into xm and the denominator into run[1]
         if (wave < G) {

@@ -117,17 +117,31 @@ struct AttnArgs {
     // Set by launch_attention: the splits combine through tagged records
     // (every workgroup of the launch resident at once) instead of tickets.
     uint32_t xchg = 0;
+    // Exchange mode: poll rounds before a wait gives up (it then writes NaN
+    // into its slice of the output and sets the head's error word; when
+    // `status` is set, bit 0 of *status too, the batched step kernel's word).
+    uint32_t spin_limit = 1u << 18;
+    uint32_t* status = nullptr;
 };
 // Arrival tickets per (sequence, kv head) of the decode attention: one for
 // the final combine, one per group of 16 splits (at most 256 splits); then
 // the exchange mode's epoch (the last launch's record tag) and its timeout
 // flag.
 constexpr uint32_t kAttnTicketsPerHead = 19;
+// Words of a head's tickets: the exchange mode's epoch (the last completed
+// launch's record tag) and its error word (non-zero after a wait timed out:
+// the launch's output holds NaN and the head's records and epoch are stale;
+// the owner of the tickets reports it and zeroes the records and tickets).
+constexpr uint32_t kAttnEpochWord = 17;
+constexpr uint32_t kAttnXErrWord = 18;
 // Splits per (sequence, kv head) for a launch over `batch` sequences whose
 // spans are at most max_span; the partials one sequence needs (any span).
 uint32_t attn_splits(uint32_t max_span, uint32_t batch, uint32_t kv_heads);
 size_t attn_partial_floats(uint32_t kv_heads, uint32_t n_heads, uint32_t head_dim);
-int launch_attention(AttnArgs a, uint32_t max_span, hipStream_t st);
+// allow_xchg false keeps the ticket chain whatever the span: callers that
+// cannot check the exchange mode's error word afterwards (an asynchronous
+// kernel-level call on the library's own records) use it.
+int launch_attention(AttnArgs a, uint32_t max_span, hipStream_t st, bool allow_xchg = true);
 // launch_attention's plan without the launch: fills group, nsplit, xchg (only
 // with allow_xchg), a fallback part / tickets, and returns the keys per lane
 // per pass (U) and the layer's RoPE frequencies.
@@ -331,7 +345,15 @@ struct TokArgs {
     // L2 instead of the device coherence point.
     uint32_t xcd_local;
     uint32_t xcd_ids;
+    // Poll rounds a wait takes before it records status bit 1 and gives up
+    // (each round one device round trip, ~0.4-1 us).
+    uint32_t spin_limit;
 };
+// Default spin limit of the token kernel's waits: ~0.1-0.25 s of poll rounds,
+// far beyond any wait of a resident grid (the longest, the lm_head's final
+// argmax poll, is ~30 us), so a grid that is not resident after all reports
+// XP_E_DEVICE within a fraction of a second.
+constexpr uint32_t kTokSpinLimit = 1u << 18;
 
 // The token kernel's down projection is split along k into chunks of this
 // many quads (128 k each); the next layer adds the chunks' partial sums. The
