@@ -26,6 +26,21 @@ batched, temperature / top-k / top-p sampling, tok/s over all sequences and
 the step's algorithmic bytes) and `native` (the repacked native-format
 matvecs, Q5_0 / Q8_0 / Q4_K / Q6_K at the shapes Gemma-3-1B's Q4_K_M file
 holds them in, HBM GB/s of their planes). `--no-configs` skips them.
+
+Every timed leg is gated on parity against the oracle (the reference's order:
+poison the output, run once, compare, then time; matvec_bench.cpp:299-324),
+and the verdicts are in the line (`parity_ok`, `parity.legs`): the headline's
+logits at ctx and its whole greedy stream (warm-up, timed and per-step runs)
+against the oracle's run on the same model and KV rows, which is also the CPU
+baseline's timed work; the matvec and attention legs' outputs filled with
+-1e30, one launch, every output written and within 1e-5 / 1e-4 of the oracle's
+(and the timed launches' last output the same); config 3's 128 greedy ids
+against the oracle's generation from the same prompt; config 5's 16
+sequences' logits of the first batched step; the native matvecs on 2048
+sampled rows against the oracle's dequantiser. `step_ms` is the per-step
+distribution (min / median / mean / max of each step's device time,
+decode.cpp:2961-2972) over as many steps as the timed run, continuing its
+stream.
 """
 from __future__ import annotations
 
@@ -67,17 +82,51 @@ def lm_head_bytes(rows=1152, cols=262144) -> int:
     return rows * cols // 2 + (rows // 32) * cols * 2 + rows * 4 + cols * 4
 
 
+T_START = time.perf_counter()
+
+
+def progress(msg: str) -> None:
+    """One line per finished leg on stderr (the JSON line alone goes to stdout)."""
+    print(f"bench: {msg} ({time.perf_counter() - T_START:.1f} s)", file=sys.stderr, flush=True)
+
+
+SENTINEL = np.float32(-1e30)
+
+
+def parity(got, want, tol: float) -> dict:
+    """got against the oracle's want: every output written (no sentinel left)
+    and max|got - want| <= tol * max|want|."""
+    got = np.asarray(got, np.float64)
+    want = np.asarray(want, np.float64)
+    written = bool(not (got == float(SENTINEL)).any()) and bool(np.isfinite(got).all())
+    m = float(np.abs(want).max()) or 1.0
+    rel = float(np.abs(got - want).max()) / m if written else float("inf")
+    return {"ok": written and rel <= tol, "rel_err": rel if written else None, "tol": tol}
+
+
 def matvec_leg(X, rows: int, cols: int, copies: int, iters: int):
     """Average per-launch time of xp_mv_int4 over `iters` back-to-back launches
     cycling `copies` distinct weight planes (> 256 MB in total so the
-    Infinity Cache cannot serve them), HIP events on the launch stream."""
+    Infinity Cache cannot serve them), HIP events on the launch stream.
+    Gated on parity first (the reference's order, matvec_bench.cpp:299-324):
+    the output is filled with -1e30, one launch runs, and every output must be
+    written and within 1e-5 of max|y| of the oracle's xo_mv_km4; the timed
+    launches' last output is checked the same way."""
+    import oracle
     wq = X.synth_nibbles(rows, cols, SEED, 901)
     sc = X.synth_scales(rows, cols, SEED, 902)
     x = X.synth_normal(rows, SEED, 903)
+    want = oracle.mv_km4(x, wq, sc, rows, cols, X.XP_SCALE_F16_QUAD)
     dws = [X.DeviceBuffer.from_array(wq) for _ in range(copies)]
     dss = [X.DeviceBuffer.from_array(sc) for _ in range(copies)]
     dx = X.DeviceBuffer.from_array(x)
     dout = X.DeviceBuffer(cols * 4)
+    dout.upload(np.full(cols, SENTINEL, np.float32))
+    X.call("xp_mv_int4", dout.vp, dx.vp, dws[0].vp, dss[0].vp, X.XP_SCALE_F16_QUAD, rows, cols, 0,
+           None)
+    X.synchronize()
+    gate = parity(dout.download(np.float32), want, 1e-5)
+    dout.upload(np.full(cols, SENTINEL, np.float32))
     st = C.c_void_p()
     X.call("xp_stream_create", C.byref(st))
     W = (C.c_void_p * copies)(*[d.ptr for d in dws])
@@ -86,9 +135,12 @@ def matvec_leg(X, rows: int, cols: int, copies: int, iters: int):
     X.call("xp_mv_int4_timed", dout.vp, dx.vp, W, S, copies, X.XP_SCALE_F16_QUAD, rows, cols, 0,
            iters, st, C.byref(ms))
     X.call("xp_stream_destroy", st)
+    X.synchronize()
+    after = parity(dout.download(np.float32), want, 1e-5)
+    gate["ok"] = gate["ok"] and after["ok"]
     per_s = ms.value / 1e3 / iters
     nbytes = rows * cols // 2 + (rows // 32) * cols * 2 + rows * 4 + cols * 4
-    return nbytes, per_s
+    return nbytes, per_s, gate
 
 
 # Native-format weights at the shapes Gemma-3-1B's Q4_K_M file holds them in
@@ -118,15 +170,31 @@ def native_leg(X, iters: int = 400):
     for name, t, elems, size, fields, rows, cols in NATIVE_CASES:
         raw = native_blocks(rows * cols // elems, size, fields, 0x5EED0100 + t)
         planes = X.rq_repack(t, raw, rows, cols)
-        del raw
+        # parity gate: a sample of up to 2048 output rows against the
+        # oracle's dequantiser (ggml's block formats) times x in float64
+        import oracle
+        x = X.synth_normal(cols, SEED, 960 + t)
+        pick = np.unique(np.random.default_rng(t).integers(0, rows, min(rows, 2048)))
+        bpr = cols // elems * size                      # bytes of one row's blocks
+        sub = raw.reshape(rows, bpr)[pick].reshape(-1)
+        w = oracle.dequantize(t, sub, pick.size * cols).reshape(pick.size, cols).astype(np.float64)
+        want = w @ x.astype(np.float64)
+        del raw, sub, w
         l = planes["layout"]
         plane_bytes = l.quant_bytes + l.high_bytes + l.scale_bytes + l.bias_bytes
         copies = max(1, min(64, -(-(384 << 20) // plane_bytes)))
         ws = [X.RqWeights(planes) for _ in range(copies)]
         del planes
         T = (X.RqTensor * copies)(*[w.tensor for w in ws])
-        dx = X.DeviceBuffer.from_array(X.synth_normal(cols, SEED, 960 + t))
+        dx = X.DeviceBuffer.from_array(x)
         dout = X.DeviceBuffer(rows * 4)
+        dout.upload(np.full(rows, SENTINEL, np.float32))
+        X.call("xp_mv_rq", dout.vp, dx.vp, C.byref(ws[0].tensor), 0, None)
+        X.synchronize()
+        got = dout.download(np.float32)
+        gate = parity(got[pick], want, 1e-5)
+        gate["ok"] = gate["ok"] and not (got == SENTINEL).any()
+        gate["rows_checked"] = int(pick.size)
         st = C.c_void_p()
         X.call("xp_stream_create", C.byref(st))
         ms = C.c_float()
@@ -138,7 +206,7 @@ def native_leg(X, iters: int = 400):
         out.append({"type": name, "shape": f"{rows}x{cols}", "bytes": nbytes,
                     "native_bytes": l.native_bytes, "us_per_launch": round(per_s * 1e6, 3),
                     "GBs": round(nbytes / per_s / 1e9, 1),
-                    "frac": round(nbytes / per_s / 1e9 / HBM_PEAK_GBS, 4)})
+                    "frac": round(nbytes / per_s / 1e9 / HBM_PEAK_GBS, 4), "parity": gate})
         for w in ws:
             w.close()
     return out
@@ -223,11 +291,17 @@ def attention_leg(X, span: int, iters: int = 192):
     256) over `span` fp16 positions: per-launch time over back-to-back launches
     cycling K/V copies totalling > 256 MiB, and the HBM GB/s of 1024 * span
     bytes (K + V) per launch."""
+    import oracle
     kvd, heads = 256, 4
     per = span * kvd * 2
     copies = max(4, -(-(384 << 20) // (2 * per)))
-    k0 = X.DeviceBuffer.from_array(X.synth_normal_f16(span * kvd, SEED, 931))
-    v0 = X.DeviceBuffer.from_array(X.synth_normal_f16(span * kvd, SEED, 932))
+    kh = X.synth_normal_f16(span * kvd, SEED, 931)
+    vh = X.synth_normal_f16(span * kvd, SEED, 932)
+    qh = X.synth_normal(heads * kvd, SEED, 933)
+    want = np.empty(heads * kvd, np.float32)
+    oracle.lib().xo_attention_f16(want, qh, kh, vh, heads, 1, kvd, span, 0, np.float32(1.0 / 16.0))
+    k0 = X.DeviceBuffer.from_array(kh)
+    v0 = X.DeviceBuffer.from_array(vh)
     ks, vs = [k0], [v0]
     for _ in range(copies - 1):
         k, v = X.DeviceBuffer(per), X.DeviceBuffer(per)
@@ -235,24 +309,37 @@ def attention_leg(X, span: int, iters: int = 192):
         X.call("xp_memcpy_dtod", v.vp, v0.vp, per)
         ks.append(k)
         vs.append(v)
-    q = X.DeviceBuffer.from_array(X.synth_normal(heads * kvd, SEED, 933))
+    q = X.DeviceBuffer.from_array(qh)
     out = X.DeviceBuffer(heads * kvd * 4)
+    # parity gate: one launch into a -1e30-filled output against the
+    # oracle's serial attention (1e-4 of max|out|), then the timed launches'
+    # last output (the exchange mode) the same way
+    out.upload(np.full(heads * kvd, SENTINEL, np.float32))
+    X.call("xp_attention_decode", out.vp, q.vp, k0.vp, v0.vp, heads, 1, kvd, span, 0, 1.0 / 16.0,
+           None)
+    X.synchronize()
+    gate = parity(out.download(np.float32), want, 1e-4)
+    out.upload(np.full(heads * kvd, SENTINEL, np.float32))
     K = (C.c_void_p * copies)(*[d.ptr for d in ks])
     V = (C.c_void_p * copies)(*[d.ptr for d in vs])
     ms = C.c_float()
     X.call("xp_attention_decode_timed", out.vp, q.vp, K, V, copies, heads, 1, kvd, span, 0,
            1.0 / 16.0, iters, None, C.byref(ms))
     X.synchronize()
+    after = parity(out.download(np.float32), want, 1e-4)
+    gate["ok"] = gate["ok"] and after["ok"]
     per_s = ms.value / 1e3 / iters
     return {"span": span, "bytes": 1024 * span, "us_per_launch": round(per_s * 1e6, 3),
-            "GBs": round(1024 * span / per_s / 1e9, 1)}
+            "GBs": round(1024 * span / per_s / 1e9, 1), "parity": gate}
 
 
-def cfg3_leg(X, sess, cfg, n_gen: int = 128):
+def cfg3_leg(X, sess, cfg, omodel=None, threads: int = 0, n_gen: int = 128):
     """Benchmark config 3: prefill a 32-token prompt of uniform random ids from
     position 0 (timed on its second run: the first builds the batched prefill
     step), then greedy-decode `n_gen` tokens (decode tok/s, prefill
-    excluded)."""
+    excluded). Parity: all n_gen ids against the oracle's greedy generation
+    from the same prompt (sample-first, decode.cpp:1830-1861), when an oracle
+    model is given."""
     r = np.random.default_rng(SEED)
     prompt = r.integers(0, cfg.vocab, 32).astype(np.uint32)
     sess.set_position(0)
@@ -267,9 +354,14 @@ def cfg3_leg(X, sess, cfg, n_gen: int = 128):
     ids = sess.decode_steps(n_gen)
     X.synchronize()
     el = time.perf_counter() - t0
-    return {"prompt": 32, "generated": n_gen, "decode_tok_s": round(n_gen / el, 1),
-            "prefill_ms": round(t_pre * 1e3, 3), "prefill_tok_s": round(32 / t_pre, 1),
-            "ids_head": [int(v) for v in ids[:4]]}
+    res = {"prompt": 32, "generated": n_gen, "decode_tok_s": round(n_gen / el, 1),
+           "prefill_ms": round(t_pre * 1e3, 3), "prefill_tok_s": round(32 / t_pre, 1),
+           "ids_head": [int(v) for v in ids[:4]], "distinct_ids": int(np.unique(ids).size)}
+    if omodel is not None:
+        want = omodel.generate_greedy(prompt, n_gen, threads)
+        res["parity"] = {"ok": bool(np.array_equal(want, ids)), "ids_checked": n_gen,
+                         "first_mismatch": next((i for i in range(n_gen) if want[i] != ids[i]), None)}
+    return res
 
 
 def cfg4_leg(X, sess, cfg, ctx: int = 4096):
@@ -302,10 +394,14 @@ def batch_bytes(depths) -> int:
     return WEIGHT_BYTES + NORM_BYTES + kv + len(depths) * (LOGIT_BYTES + APPEND_BYTES)
 
 
-def cfg5_leg(X, sess, cfg, n_seq: int = 16, steps: int = 20, warmup: int = 3):
+def cfg5_leg(X, sess, cfg, n_seq: int = 16, steps: int = 20, warmup: int = 3, tensors=None,
+             threads: int = 0):
     """benchmark config 5: 16 independent sequences at depths uniform in
     [128, 4096] (Philox), temperature 0.8 / top-k 64 / top-p 0.95 with a
-    Philox draw per (sequence, step); tokens/s over all sequences."""
+    Philox draw per (sequence, step); tokens/s over all sequences. Parity
+    (with the model's tensors given): every sequence's logits of the first
+    batched step within 1e-3 of max|logits| of the oracle run alone on its
+    own KV rows and token."""
     seed = 0x5EED0005
     u = np.array([X.philox_uniform(seed, i, 0) for i in range(n_seq)])
     depths = (128 + np.floor(u * (4096 - 128 + 1))).astype(np.int64)
@@ -319,7 +415,25 @@ def cfg5_leg(X, sess, cfg, n_seq: int = 16, steps: int = 20, warmup: int = 3):
             for i, d in enumerate(depths):
                 b.kv_upload(i, l, which, 0, rows[:int(d) * kvd])
     b.set_positions(depths)
-    b.forward(np.arange(n_seq) * 1000 + 7)
+    toks = np.arange(n_seq) * 1000 + 7
+    b.forward(toks)
+    gate = None
+    if tensors is not None:
+        import oracle
+        # every sequence's rows are a prefix of the same rows: one oracle
+        # cache holds them; sequences run deepest first, so the row each
+        # appends lies past every shallower sequence's context
+        om = oracle.OracleModel(cfg, lambda l, k: tensors[(l, k)])
+        for l in range(cfg.n_layers):
+            om.kcache[l][:dmax * kvd] = X.synth_normal_f16(dmax * kvd, seed, 2 * l)
+            om.vcache[l][:dmax * kvd] = X.synth_normal_f16(dmax * kvd, seed, 2 * l + 1)
+        worst = 0.0
+        for i in np.argsort(-depths, kind="stable"):
+            want = om.forward(int(toks[i]), int(depths[i]), True, threads)
+            got = b.last_logits(int(i)).astype(np.float64)
+            worst = max(worst, float(np.abs(got - want).max()) / float(np.abs(want).max()))
+        gate = {"ok": worst <= 1e-3, "rel_err": worst, "tol": 1e-3, "sequences_checked": n_seq}
+        del om
     for _ in range(warmup):
         b.decode_step()
     X.synchronize()
@@ -339,13 +453,12 @@ def cfg5_leg(X, sess, cfg, n_seq: int = 16, steps: int = 20, warmup: int = 3):
             "device_ms_per_step": round(ms_dev, 4),
             "bytes_per_step": nb, "GBs": round(nb / (ms_dev / 1e3) / 1e9, 1),
             "frac": round(nb / (ms_dev / 1e3) / 1e9 / HBM_PEAK_GBS, 4),
-            "sampling": "T 0.8, top-k 64, top-p 0.95, Philox(seed, seq, step)"}
+            "sampling": "T 0.8, top-k 64, top-p 0.95, Philox(seed, seq, step)", "parity": gate}
 
 
-def cpu_baseline(X, cfg, ctx: int, seconds: float, threads: int):
-    """The oracle (C restatement, OpenMP over output columns) decoding greedy
-    tokens of the same model from position ctx, for about `seconds`."""
-    import oracle
+def model_tensors(X, cfg) -> dict:
+    """The benchmark model's packed tensors (host copies, as the session's
+    xp_session_synthesize makes them), for the oracle."""
     tensors = {}
     for l in range(cfg.n_layers):
         for m in X.MATRICES:
@@ -355,22 +468,36 @@ def cpu_baseline(X, cfg, ctx: int, seconds: float, threads: int):
             tensors[(l, n)] = X.synth_tensor(cfg, SEED, l, n)
     for k in (X.T_LM_HEAD, X.T_LM_HEAD | X.T_SCALES, X.T_FINAL_NORM):
         tensors[(-1, k)] = X.synth_tensor(cfg, SEED, -1, k)
+    return tensors
+
+
+def cpu_baseline(X, cfg, tensors, ctx: int, seconds: float, threads: int, min_tokens: int):
+    """The oracle (C restatement, OpenMP over output columns) on the
+    headline's workload: the same model and KV rows, token 4242 at position
+    ctx, then greedy decode from ctx + 1 for about `seconds` (at least
+    min_tokens tokens, so that the GPU's checked stream is covered). Returns
+    the logits at ctx, the greedy ids, and the decode rate over the timed
+    tokens."""
+    import oracle
     model = oracle.OracleModel(cfg, lambda l, k: tensors[(l, k)])
     kvd = cfg.n_kv_heads * cfg.head_dim
     for l in range(cfg.n_layers):
         model.kcache[l][:ctx * kvd] = X.synth_normal_f16(ctx * kvd, ctx, 2 * l)
         model.vcache[l][:ctx * kvd] = X.synth_normal_f16(ctx * kvd, ctx, 2 * l + 1)
-    lg = model.forward(4242, ctx, True, threads)
+    lg0 = model.forward(4242, ctx, True, threads)
+    lg = lg0
+    ids = []
     pos, n, t0 = ctx + 1, 0, time.perf_counter()
     while True:
         tok = oracle.argmax_tree(lg)[0]
+        ids.append(tok)
         lg = model.forward(tok, pos, True, threads)
         pos += 1
         n += 1
         el = time.perf_counter() - t0
-        if el >= seconds or n >= 1000:
+        if (el >= seconds and n >= min_tokens) or n >= 1000:
             break
-    return n / el, n, el
+    return lg0, ids, n / el, n, el
 
 
 def main() -> int:
@@ -406,8 +533,8 @@ def main() -> int:
     X.init(0)
     info = X.device_info()
     if args.only == "matvec":
-        nbytes, per_s = matvec_leg(X, 1152, 262144, copies=3, iters=args.mv_iters)
-        nb1, per1 = matvec_leg(X, 1152, 6912, copies=64, iters=640)
+        nbytes, per_s, _ = matvec_leg(X, 1152, 262144, copies=3, iters=args.mv_iters)
+        nb1, per1, _ = matvec_leg(X, 1152, 6912, copies=64, iters=640)
         ceil = stream_ceiling(X)
         # A 256 MiB copy: 256 MiB fetched and 256 MiB written, the calibration
         # point for rocprofv3's FETCH_SIZE / WRITE_SIZE counters.
@@ -448,6 +575,12 @@ def main() -> int:
         print("bench.py: ctx + steps exceed max_seq 8192", file=sys.stderr)
         return 2
 
+    # Every host core this process may run on, capped by OMP_NUM_THREADS
+    # when the host sets it (the GPU box gives one GPU's job 16 threads).
+    affinity = len(os.sched_getaffinity(0))
+    omp = int(os.environ.get("OMP_NUM_THREADS", "0") or 0)
+    threads = min(affinity, omp) if omp > 0 else affinity
+
     sess = X.DecodeSession(cfg)
     sess.synthesize(SEED)
     kvd = cfg.n_kv_heads * cfg.head_dim
@@ -456,8 +589,8 @@ def main() -> int:
         sess.kv_upload(l, 1, 0, X.synth_normal_f16(ctx * kvd, ctx, 2 * l + 1))
     sess.set_position(ctx)
     sess.prefill([4242])                    # runs position ctx, leaves logits
-    if args.warmup:
-        sess.decode_steps(args.warmup)
+    logits0 = sess.last_logits()
+    warm_ids = sess.decode_steps(args.warmup) if args.warmup else np.empty(0, np.uint32)
     X.synchronize()
     t0 = time.perf_counter()
     ids = sess.decode_steps(args.steps)
@@ -471,43 +604,86 @@ def main() -> int:
     launches = met.launches
     kern_s = met.gpu_ms / 1e3 / args.steps          # device time per token-kernel launch
     exec_mode = {1: "graph", 2: "launch", 3: "token-kernel"}.get(met.exec_mode, str(met.exec_mode))
+    # Per-step distribution (the reference reports min / median / mean a step,
+    # decode.cpp:2961-2972): the same greedy stream continued one step per
+    # call, each step's device time from HIP events around its launch.
+    per_step, step_ids = [], []
+    for _ in range(args.steps):
+        step_ids.append(int(sess.decode_steps(1)[0]))
+        per_step.append(sess.last_metrics().gpu_ms)
+    per_step = np.array(per_step)
+    step_stats = {"n": int(per_step.size), "min_ms": round(float(per_step.min()), 4),
+                  "median_ms": round(float(np.median(per_step)), 4),
+                  "mean_ms": round(float(per_step.mean()), 4),
+                  "max_ms": round(float(per_step.max()), 4),
+                  "positions": [ctx + 1 + args.warmup + args.steps,
+                                ctx + args.warmup + 2 * args.steps]}
+    gpu_stream = [int(v) for v in warm_ids] + [int(v) for v in ids] + step_ids
+    progress(f"headline decode {tok_s:.1f} tok/s")
+
+    tensors = model_tensors(X, cfg)
     extra = {}
     if not args.no_configs:
+        import oracle
         extra["cfg4"] = cfg4_leg(X, sess, cfg, ctx)       # reads the pre-filled rows 0..ctx-1
-        extra["cfg3"] = cfg3_leg(X, sess, cfg)
+        progress("cfg4")
+        om3 = oracle.OracleModel(cfg, lambda l, k: tensors[(l, k)])
+        extra["cfg3"] = cfg3_leg(X, sess, cfg, om3, threads)
+        del om3
+        progress("cfg3 (128 ids checked)")
         extra["attention"] = [attention_leg(X, sp) for sp in (4096, 8192)]
+        progress("attention")
         scfg = X.XpConfig.gemma3_1b(max_seq=8192, sample_mode=1, temperature=0.8, top_k=64,
                                     top_p=0.95, seed=0x5EED0005)
         bsess = X.DecodeSession(scfg)
         bsess.synthesize(SEED)
-        extra["cfg5"] = cfg5_leg(X, bsess, scfg)
+        extra["cfg5"] = cfg5_leg(X, bsess, scfg, tensors=tensors, threads=threads)
         bsess.close()
+        progress("cfg5")
         extra["native"] = native_leg(X)
+        progress("native")
         extra["graph_path"] = graph_leg(X, ctx)
+        progress("graph path")
     sess.close()
 
     # Roofline leg: the dominant kernel of the step, the lm_head int4 matvec.
-    nbytes, per_s = matvec_leg(X, 1152, 262144, copies=3, iters=args.mv_iters)
+    nbytes, per_s, mv_gate = matvec_leg(X, 1152, 262144, copies=3, iters=args.mv_iters)
     achieved = nbytes / per_s / 1e9
     # benchmark config 1 shape (gate 6912 x 1152), 64 rotating copies.
-    nb1, per1 = matvec_leg(X, 1152, 6912, copies=64, iters=640)
+    nb1, per1, mv1_gate = matvec_leg(X, 1152, 6912, copies=64, iters=640)
     ceil = stream_ceiling(X)
     ceil1_us, floor_us = same_size_ceiling(X, nb1)
+    progress("matvec and streaming")
 
+    # Parity of the headline: the oracle on the same model, KV rows and token
+    # (the logits at ctx, then the greedy stream as far as the GPU's checked
+    # stream reaches); with --no-cpu only as far as two tokens, untimed.
+    n_check = len(gpu_stream)
+    seconds = args.cpu_seconds if not args.no_cpu else 0.0
+    lg0, o_ids, cpu_tok_s, n_cpu, cpu_el = cpu_baseline(
+        X, cfg, tensors, ctx, seconds, threads, n_check if not args.no_cpu else 2)
+    k = min(len(o_ids), n_check)
+    lg_gate = parity(logits0, lg0, 1e-3)
+    head_gate = {"ok": bool(lg_gate["ok"] and o_ids[:k] == gpu_stream[:k]),
+                 "logits_rel_err": lg_gate["rel_err"], "logits_tol": 1e-3,
+                 "ids_checked": k, "ids_equal": o_ids[:k] == gpu_stream[:k],
+                 "distinct_ids": len(set(gpu_stream[:k]))}
+    progress("CPU baseline and headline parity")
     cpu = None
     if not args.no_cpu:
-        # Every host core this process may run on, capped by OMP_NUM_THREADS
-        # when the host sets it (the GPU box gives one GPU's job 16 threads).
-        affinity = len(os.sched_getaffinity(0))
-        omp = int(os.environ.get("OMP_NUM_THREADS", "0") or 0)
-        threads = min(affinity, omp) if omp > 0 else affinity
-        cpu_tok_s, n_cpu, cpu_el = cpu_baseline(X, cfg, ctx, args.cpu_seconds, threads)
         cpu = {"value": round(cpu_tok_s, 3), "unit": "tok/s", "cores": threads, "kind": "port",
                "host_cpus_affinity": affinity, "omp_num_threads": omp or None,
                "sample": f"{n_cpu} greedy decode steps of the same Gemma-3-1B int4 model from "
                          f"position {ctx + 1} (KV pre-filled), oracle C restatement, "
                          f"{threads} OpenMP threads ({affinity} CPUs in this process's "
                          f"affinity mask), {cpu_el:.1f} s"}
+    gates = {"headline": head_gate["ok"], "matvec_lm_head": mv_gate["ok"],
+             "matvec_cfg1": mv1_gate["ok"]}
+    if "cfg3" in extra:
+        gates["cfg3"] = extra["cfg3"]["parity"]["ok"]
+        gates["cfg5"] = extra["cfg5"]["parity"]["ok"]
+        gates["attention"] = all(a["parity"]["ok"] for a in extra["attention"])
+        gates["native"] = all(n["parity"]["ok"] for n in extra["native"])
 
     line = {
         "metric": "decode tok/s Gemma-3-1B int4 bs=1 @ctx 4096; int4 matvec HBM GB/s vs peak",
@@ -530,6 +706,9 @@ def main() -> int:
                    "layers": 26, "hidden": 1152, "vocab": 262144, "weights": "int4 g32 + fp16",
                    "kv": "fp16", "launches_per_step": launches,
                    "exec": exec_mode},
+        "parity_ok": all(gates.values()),
+        "parity": {"legs": gates, "headline": head_gate},
+        "step_ms": step_stats,
         "roofline": {"bound": "hbm", "kernel": "token_kernel (whole decode token)",
                      "achieved": round(tb / kern_s / 1e9, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(tb / kern_s / 1e9 / HBM_PEAK_GBS, 4),
@@ -540,7 +719,7 @@ def main() -> int:
         "matvec_lm_head": {"shape": "262144x1152", "bytes": nbytes,
                            "us_per_launch": round(per_s * 1e6, 3),
                            "GBs": round(achieved, 1), "frac": round(achieved / HBM_PEAK_GBS, 4),
-                           "frac_of_stream_ceiling": round(achieved / ceil, 4)},
+                           "frac_of_stream_ceiling": round(achieved / ceil, 4), "parity": mv_gate},
         "stream_ceiling_GBs": round(ceil, 1),
         "matvec_cfg1": {"shape": "6912x1152", "bytes": nb1, "us_per_launch": round(per1 * 1e6, 3),
                         "GBs": round(nb1 / per1 / 1e9, 1),
@@ -550,7 +729,8 @@ def main() -> int:
                         "launch_floor_us": round(floor_us, 3),
                         "frac_of_same_size_stream": round(ceil1_us / (per1 * 1e6), 4),
                         "note": "back-to-back launches; a launch that reads 16 B per thread "
-                                "takes launch_floor_us, which bounds any kernel of this size"},
+                                "takes launch_floor_us, which bounds any kernel of this size",
+                        "parity": mv1_gate},
         "cpu_baseline": cpu,
         **extra,
         "device": info["arch"],
