@@ -590,3 +590,57 @@ def test_gpu_graph_attention_timeout_recovers(xp):
     assert np.array_equal(a.last_logits().view(np.uint32), b.last_logits().view(np.uint32))
     a.close()
     b.close()
+
+
+@pytest.mark.gpu
+def test_gpu_cfg3_full_length(xp, xo, mode):
+    """Benchmark config 3 at its stated length: full Gemma-3-1B, the tied
+    262144 x 1152 int4 table, a 32-token prompt of uniform random ids from
+    position 0, then 128 greedy tokens in the reference's sample-first order
+    (decode.cpp:1830-1861); every id equal to the oracle's generation."""
+    X = xp
+    print(f"case session cfg3 32 + 128 mode {mode}", flush=True)
+    cfg = X.XpConfig.gemma3_1b(max_seq=512, exec_mode=mode)
+    sess, model = make_pair(X, xo, cfg)
+    prompt = np.random.default_rng(0x5EED0003).integers(0, cfg.vocab, 32).astype(np.uint32)
+    want = model.generate_greedy(prompt, 128, 16)
+    sess.prefill(prompt)
+    got = sess.decode_steps(128)
+    assert np.array_equal(got, want), int(np.argmax(got != want))
+    assert sess.position == 32 + 128
+    sess.close()
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("exec_mode,placement", DEEP_MODES)
+def test_gpu_cfg4_chunk_switch_and_buckets(xp, xo, exec_mode, placement):
+    """Benchmark config 4's positions the shortened checks do not reach: the
+    token kernel's switch of global attention from 64-key to 128-key head-pair
+    chunks (global span 6656 -> 6657, positions 6655 and 6656) and one
+    position per 512-position bucket of the 4097 -> 8192 run (4097, 4609, ...,
+    7681, and 8191); KV of all 26 layers pre-filled with fp16 N(0,1) rows, each position
+    run as a one-token prefill against the oracle at the same position (the
+    positions run deepest first, so the row each run appends lies past every
+    later context). Logits within 1e-3 and the greedy id equal."""
+    X = xp
+    print(f"case session cfg4 positions exec {exec_mode} placement {placement}", flush=True)
+    cfg = X.XpConfig.gemma3_1b(exec_mode=exec_mode, placement=placement)
+    sess, model = make_pair(X, xo, cfg)
+    kvd = cfg.n_kv_heads * cfg.head_dim
+    fill = cfg.max_seq - 1
+    for l in range(cfg.n_layers):
+        for which, cache in ((0, model.kcache), (1, model.vcache)):
+            rows = X.synth_normal_f16(fill * kvd, 4096, 2 * l + which)
+            sess.kv_upload(l, which, 0, rows)
+            cache[l][:fill * kvd] = rows
+    positions = sorted([6655, 6656] + [4097 + 512 * k for k in range(8)] + [8191], reverse=True)
+    for p in positions:
+        tok = 1000 + p
+        sess.set_position(p)
+        sess.prefill([tok])
+        want = model.forward(tok, p, True, 16)
+        got = sess.last_logits()
+        ok, msg = logits_close(got, want)
+        assert ok, f"position {p}: {msg}"
+        assert xo.argmax_tree(got)[0] == xo.argmax_tree(want)[0], p
+    sess.close()
