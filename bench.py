@@ -243,6 +243,30 @@ def exchange_leg(X, stages: int = 64, reps: int = 10):
     return rows
 
 
+def handoff_leg(X, iters: int = 2000):
+    """The token kernel's exchange split into its parts
+    (xp_handoff_pingpong_timed, xp_load_latency): round trips of a payload
+    hand-off plus a one-pair answer, same XCD / across XCDs, payloads of 1 to
+    4096 pairs (16 B to 64 KiB), device-scope or L2-kept stores; dependent-load
+    latency at footprints from L1 to past the Infinity Cache."""
+    rows = []
+    for same, l2 in ((1, 0), (0, 0), (1, 1)):
+        for pairs in (1, 32, 512, 1024, 2048, 2304, 4096):
+            ns, xcc = C.c_float(), C.c_uint32()
+            X.call("xp_handoff_pingpong_timed", same, pairs, l2, iters, None, C.byref(ns), C.byref(xcc))
+            rows.append({"same_xcd": bool(same), "stores": "L2" if l2 else "device",
+                         "payload_bytes": 16 * pairs, "round_trip_ns": round(ns.value, 1),
+                         "xcc": [int(xcc.value & 0xFF), int(xcc.value >> 8)]})
+    lat = []
+    for nbytes, stride in ((16 << 10, 256), (2 << 20, 4096), (64 << 20, 128), (512 << 20, 128)):
+        for dev in (0, 1):
+            clk = C.c_float()
+            X.call("xp_load_latency", nbytes, stride, dev, None, C.byref(clk))
+            lat.append({"bytes": nbytes, "stride": stride, "device_scope": bool(dev),
+                        "clk_per_load": round(clk.value, 1)})
+    return {"pingpong": rows, "load_latency": lat}
+
+
 def same_size_ceiling(X, nbytes: int, copies: int = 64, iters: int = 640):
     """The streaming probe at the matvec's own size, back to back over
     `copies` buffers (> 256 MiB together, so HBM serves them), at the grid
@@ -550,7 +574,8 @@ def main() -> int:
                           "stream_ceiling_GBs": round(ceil, 1)}), flush=True)
         return 0
     if args.only == "exchange":
-        print(json.dumps({"exchange_chain": exchange_leg(X), "device": info.get("arch", "")}))
+        print(json.dumps({"exchange_chain": exchange_leg(X), "handoff": handoff_leg(X),
+                          "device": info.get("arch", "")}))
         return 0
     if args.only == "native":
         print(json.dumps({"native": native_leg(X)}), flush=True)

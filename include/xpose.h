@@ -168,6 +168,18 @@ int xp_copy(void* dst, const void* src, size_t bytes, xp_stream stream);
  * (the grid was not resident at once). */
 int xp_exchange_chain_timed(uint32_t producers, uint32_t stages, uint32_t stride, int l2_local,
                             xp_stream stream, float* ns_per_stage);
+/* Hand-off probes (no reference counterpart), splitting one exchange of the
+ * token kernel into its parts. xp_handoff_pingpong_timed: workgroup 0 stores
+ * payload_pairs tagged 16-byte pairs (device-scope, or with l2_local kept in
+ * its XCD's L2), the 512 threads of a workgroup on the same XCD (same_xcd)
+ * or another poll them all, pass a barrier and answer with one pair;
+ * *ns_round_trip is the mean round trip over `iters` rounds, *xcc_pair the
+ * two workgroups' XCC ids (low byte ping). xp_load_latency: one lane's chain
+ * of dependent 4-byte loads over `bytes` (nodes `stride` bytes apart, random
+ * cyclic order), plain or device-scope: shader clocks per load. */
+int xp_handoff_pingpong_timed(uint32_t same_xcd, uint32_t payload_pairs, int l2_local, uint32_t iters,
+                              xp_stream stream, float* ns_round_trip, uint32_t* xcc_pair);
+int xp_load_latency(uint32_t bytes, uint32_t stride, int device_scope, xp_stream stream, float* clk_per_load);
 
 /* Two-pass Gemma RMSNorm in one launch: out = in * rsqrt(mean(in^2)+eps) *
  * (1 + w). Replaces rmsnorm_sumsq + rmsnorm_apply_gemma

@@ -30,3 +30,36 @@ def test_gpu_exchange_chain_rejects(xp, producers, stages, stride, l2):
     ns = C.c_float()
     with pytest.raises(xp.XposeError):
         xp.call("xp_exchange_chain_timed", producers, stages, stride, l2, None, C.byref(ns))
+
+
+@pytest.mark.parametrize("same_xcd,pairs,l2", [(1, 1, 0), (0, 1, 0), (1, 2304, 0), (0, 4096, 0), (1, 32, 1)])
+def test_gpu_handoff_pingpong_runs(xp, same_xcd, pairs, l2):
+    """The two-workgroup hand-off probe finishes every placement and payload;
+    a round trip is two hand-offs, each at least a store and a load through
+    the cache hierarchy; a payload of several loads a polling thread takes
+    longer than one pair (up to 512 pairs, one load a thread, it need not)."""
+    ns, xcc = C.c_float(), C.c_uint32()
+    xp.call("xp_handoff_pingpong_timed", same_xcd, pairs, l2, 200, None, C.byref(ns), C.byref(xcc))
+    assert 200.0 < ns.value < 1e5, ns.value
+    if pairs > 1024:
+        one = C.c_float()
+        xp.call("xp_handoff_pingpong_timed", same_xcd, 1, l2, 200, None, C.byref(one), C.byref(xcc))
+        assert ns.value > one.value, (ns.value, one.value)
+
+
+def test_gpu_handoff_pingpong_rejects(xp):
+    ns, xcc = C.c_float(), C.c_uint32()
+    for args in ((1, 0, 0, 10), (1, 4097, 0, 10), (0, 1, 1, 10), (1, 1, 0, 0)):
+        with pytest.raises(xp.XposeError):
+            xp.call("xp_handoff_pingpong_timed", *args, None, C.byref(ns), C.byref(xcc))
+
+
+def test_gpu_load_latency(xp):
+    """Dependent loads: a footprint past the L2 (64 MiB of 128-byte nodes)
+    takes longer per load than one that fits its L1 (16 KiB)."""
+    small, big = C.c_float(), C.c_float()
+    xp.call("xp_load_latency", 16 << 10, 256, 0, None, C.byref(small))
+    xp.call("xp_load_latency", 64 << 20, 128, 1, None, C.byref(big))
+    assert 10.0 < small.value < big.value < 1e5, (small.value, big.value)
+    with pytest.raises(xp.XposeError):
+        xp.call("xp_load_latency", 100, 256, 0, None, C.byref(small))

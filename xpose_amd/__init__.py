@@ -150,6 +150,8 @@ def _declare(lib: C.CDLL) -> None:
         "xp_stream_read_timed": (i32, [vp, sz, u32, vp, P(f32)]),
         "xp_stream_read_rot_timed": (i32, [P(vp), u32, sz, u32, u32, vp, P(f32)]),
         "xp_exchange_chain_timed": (i32, [u32, u32, u32, i32, vp, P(f32)]),
+        "xp_handoff_pingpong_timed": (i32, [u32, u32, i32, u32, vp, P(f32), P(u32)]),
+        "xp_load_latency": (i32, [u32, u32, i32, vp, P(f32)]),
         "xp_copy": (i32, [vp, vp, sz, vp]),
         "xp_philox4x32_10": (None, [P(u32), P(u32), P(u32)]),
         "xp_synth_nibbles": (i32, [vp, u32, u32, u32, u32]),

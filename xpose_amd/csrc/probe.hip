@@ -8,6 +8,7 @@
 // highest in a sweep of chunked and grid-stride layouts on MI355X). As in the
 // reference, the only store is guarded by a value the sum cannot take, so
 // every load stays live and nothing is written.
+#include <algorithm>
 #include <vector>
 
 #include "xp_device.hpp"
@@ -58,6 +59,11 @@ __global__ __launch_bounds__(kProbeThreads) void copy_kernel(u32x4* dst, const u
 // bounded and a timeout sets status. Each workgroup records the 100 MHz
 // s_memrealtime of its first and last publish.
 constexpr int kXcThreads = 512;
+__device__ __forceinline__ uint32_t xcc_of_wave() {
+    uint32_t x;
+    asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(x));
+    return x & 0xFu;
+}
 struct XcArgs {
     u32x4* slots;                 // [stages][n][32] pairs
     unsigned long long* times;    // [grid][2]
@@ -119,6 +125,105 @@ __global__ __launch_bounds__(kXcThreads) void exchange_chain_kernel(XcArgs a) {
         a.times[2 * wg] = t_first;
         a.times[2 * wg + 1] = t_last;
     }
+}
+
+// Hand-off ping-pong: the token kernel's exchange reduced to two
+// workgroups, to split a stage's wait into its parts. Workgroup 0 (ping)
+// stores `np` tagged 16-byte pairs; workgroup `peer` (pong) has its 512
+// threads poll all np pairs (device-scope loads) until every tag is the
+// round's, passes a barrier, and answers with one pair, which ping's wave 0
+// polls. Stores are device-scope (sc1) or, with l2, kept in the XCD's L2
+// (pong on the same XCD only). A round trip is one payload hand-off plus one
+// 16-byte one; every wait is bounded and a timeout sets status.
+constexpr uint32_t kPpMaxPerThread = 8;   // pairs a pong thread polls (np <= 4096)
+__global__ __launch_bounds__(512) void handoff_pingpong_kernel(u32x4* buf, uint32_t peer, uint32_t iters,
+                                                               uint32_t np, uint32_t l2, uint32_t spin_limit,
+                                                               unsigned long long* out, uint32_t* status) {
+    const uint32_t wg = blockIdx.x, tid = threadIdx.x;
+    if (wg != 0u && wg != peer) return;
+    // [0, 2 x 4096) payload pairs of even / odd rounds, then the answers
+    const rsrc_t r = make_rsrc(buf, (2u * 4096u + 2u) * 16u);
+    __shared__ uint32_t sh_err[2];
+    uint32_t err = 0;
+    const bool ping = wg == 0u;
+    const unsigned long long r0 = __builtin_amdgcn_s_memrealtime();
+    for (uint32_t i = 1; i <= iters && !err; ++i) {
+        const uint32_t base = (i & 1u) * 4096u, ans = 2u * 4096u + (i & 1u);
+        const u32x4 val = {i, i, i, i};
+        if (ping) {
+            for (uint32_t p = tid; p < np; p += 512u) {
+                if (l2) __builtin_amdgcn_raw_buffer_store_b128(val, r, int((base + p) * 16u), 0, 0);
+                else __builtin_amdgcn_raw_buffer_store_b128(val, r, int((base + p) * 16u), 0, kAuxDev);
+            }
+            if (tid < 64u) {
+                for (uint32_t s = 0;; ++s) {
+                    asm volatile("" ::: "memory");
+                    const u32x4 v = ld_dev16(r, ans * 16u);
+                    if (__builtin_amdgcn_ballot_w64((v.y != i) | (v.w != i)) == 0ull) break;
+                    if (s > spin_limit) { err = i; break; }
+                }
+            }
+        } else {
+            bool act[kPpMaxPerThread];
+            uint32_t off[kPpMaxPerThread];
+#pragma unroll
+            for (uint32_t k = 0; k < kPpMaxPerThread; ++k) {
+                const uint32_t p = tid + 512u * k;
+                act[k] = p < np;
+                off[k] = (base + (act[k] ? p : 0u)) * 16u;
+            }
+            for (uint32_t s = 0;; ++s) {
+                asm volatile("" ::: "memory");
+                bool ok = true;
+#pragma unroll
+                for (uint32_t k = 0; k < kPpMaxPerThread; ++k) {
+                    const u32x4 v = act[k] ? ld_dev16(r, off[k]) : val;
+                    ok &= (v.y == i) & (v.w == i);
+                }
+                if (ok) break;
+                if (s > spin_limit) { err = i; break; }
+            }
+        }
+        if (tid == 0u) sh_err[i & 1u] = 0u;
+        __syncthreads();
+        if (err) sh_err[i & 1u] = err;
+        __syncthreads();
+        err = sh_err[i & 1u];
+        if (!ping && tid == 0u && !err) {
+            if (l2) __builtin_amdgcn_raw_buffer_store_b128(val, r, int(ans * 16u), 0, 0);
+            else __builtin_amdgcn_raw_buffer_store_b128(val, r, int(ans * 16u), 0, kAuxDev);
+        }
+    }
+    const unsigned long long r1 = __builtin_amdgcn_s_memrealtime();
+    if (tid == 0u) {
+        if (err)
+            __hip_atomic_fetch_or((XP_GLOBAL uint32_t*)status, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (ping) {
+            out[0] = r1 - r0;
+            out[1] = xcc_of_wave();
+        } else {
+            out[2] = xcc_of_wave();
+        }
+    }
+}
+
+// One lane walks a cyclic chain of dependent loads (next index in 4-byte
+// words), plain or device-scope (sc1): clocks per load once warm.
+__global__ void load_chase_kernel(const uint32_t* buf, uint32_t bytes, uint32_t steps, uint32_t dev,
+                                  unsigned long long* out) {
+    if (blockIdx.x != 0u || threadIdx.x != 0u) return;
+    const rsrc_t r = make_rsrc(buf, bytes);
+    uint32_t idx = 0;
+    for (uint32_t i = 0; i < steps; ++i)
+        idx = dev ? __builtin_amdgcn_raw_buffer_load_b32(r, int(idx * 4u), 0, kAuxDev)
+                  : __builtin_amdgcn_raw_buffer_load_b32(r, int(idx * 4u), 0, 0);
+    const unsigned long long t0 = __builtin_amdgcn_s_memtime();
+    for (uint32_t i = 0; i < steps; ++i)
+        idx = dev ? __builtin_amdgcn_raw_buffer_load_b32(r, int(idx * 4u), 0, kAuxDev)
+                  : __builtin_amdgcn_raw_buffer_load_b32(r, int(idx * 4u), 0, 0);
+    const unsigned long long t1 = __builtin_amdgcn_s_memtime();
+    out[0] = t1 - t0;
+    out[1] = idx;
 }
 
 namespace {
@@ -260,6 +365,80 @@ int xp_exchange_chain_timed(uint32_t producers, uint32_t stages, uint32_t stride
         hi = h[2u * w + 1u] > hi ? h[2u * w + 1u] : hi;
     }
     *ns_per_stage = hi > lo ? float(double(hi - lo) * 10.0 / double(stages - 1u)) : 0.0f;
+    return XP_OK;
+}
+
+int xp_handoff_pingpong_timed(uint32_t same_xcd, uint32_t payload_pairs, int l2_local, uint32_t iters,
+                              xp_stream stream, float* ns_round_trip, uint32_t* xcc_pair) {
+    XP_REQUIRE(ns_round_trip, "null pointer");
+    XP_REQUIRE(payload_pairs >= 1 && payload_pairs <= 512u * kPpMaxPerThread,
+               "payload_pairs=%u must be in [1, %u]", payload_pairs, 512u * kPpMaxPerThread);
+    XP_REQUIRE(!l2_local || same_xcd, "l2_local needs the pong on ping's XCD");
+    XP_REQUIRE(iters >= 1 && iters <= 100000, "iters=%u must be in [1, 100000]", iters);
+    hipStream_t st = as_stream(stream);
+    const size_t slot_bytes = (2u * 4096u + 2u) * 16u;
+    char* mem = nullptr;
+    XP_HIP(hipMalloc(&mem, slot_bytes + 64));
+    u32x4* slots = reinterpret_cast<u32x4*>(mem);
+    unsigned long long* out = reinterpret_cast<unsigned long long*>(mem + slot_bytes);
+    uint32_t* status = reinterpret_cast<uint32_t*>(mem + slot_bytes + 32);
+    // workgroups w and w + 8 share an XCD under the cyclic dealing (the
+    // XCC ids are returned so the caller can see it held)
+    const uint32_t peer = same_xcd ? 8u : 1u;
+    unsigned long long h[3] = {};
+    uint32_t stat = 0;
+    hipError_t e = hipMemsetAsync(mem, 0, slot_bytes + 64, st);
+    if (e == hipSuccess) {
+        hipLaunchKernelGGL(handoff_pingpong_kernel, dim3(16), dim3(512), 0, st, slots, peer, iters, payload_pairs,
+                           uint32_t(l2_local ? 1 : 0), 1u << 18, out, status);
+        e = hipGetLastError();
+    }
+    if (e == hipSuccess) e = hipMemcpyAsync(h, out, sizeof(h), hipMemcpyDeviceToHost, st);
+    if (e == hipSuccess) e = hipMemcpyAsync(&stat, status, 4, hipMemcpyDeviceToHost, st);
+    if (e == hipSuccess) e = hipStreamSynchronize(st);
+    (void)hipFree(mem);
+    if (e != hipSuccess) return set_error(XP_E_HIP, "xp_handoff_pingpong_timed: %s", hipGetErrorString(e));
+    if (stat) return set_error(XP_E_DEVICE, "xp_handoff_pingpong_timed: a wait ran past its spin limit");
+    *ns_round_trip = float(double(h[0]) * 10.0 / iters);
+    if (xcc_pair) *xcc_pair = uint32_t(h[1] & 0xFFu) | (uint32_t(h[2] & 0xFFu) << 8);
+    return XP_OK;
+}
+
+int xp_load_latency(uint32_t bytes, uint32_t stride, int device_scope, xp_stream stream, float* clk_per_load) {
+    XP_REQUIRE(clk_per_load, "null pointer");
+    XP_REQUIRE(stride >= 4 && stride % 4 == 0 && bytes >= 2 * stride && bytes % stride == 0 &&
+                   bytes <= (1u << 30),
+               "bytes=%u / stride=%u: a multiple of stride, 2 nodes to 1 GiB, stride a multiple of 4", bytes,
+               stride);
+    const uint32_t n = bytes / stride, w = stride / 4;
+    // a random cyclic order of the nodes (fixed seed): node order[i] points to order[i + 1]
+    std::vector<uint32_t> order(n);
+    for (uint32_t i = 0; i < n; ++i) order[i] = i;
+    uint64_t x = 0x9E3779B97F4A7C15ull;
+    for (uint32_t i = n - 1; i > 1; --i) {
+        x ^= x << 13; x ^= x >> 7; x ^= x << 17;
+        const uint32_t j = 1u + uint32_t(x % i);
+        std::swap(order[i], order[j]);
+    }
+    std::vector<uint32_t> host(size_t(bytes) / 4, 0u);
+    for (uint32_t i = 0; i < n; ++i) host[size_t(order[i]) * w] = order[(i + 1) % n] * w;
+    hipStream_t st = as_stream(stream);
+    char* mem = nullptr;
+    XP_HIP(hipMalloc(&mem, size_t(bytes) + 16));
+    unsigned long long* out = reinterpret_cast<unsigned long long*>(mem + bytes);
+    unsigned long long h[2] = {};
+    const uint32_t steps = 4096;
+    hipError_t e = hipMemcpyAsync(mem, host.data(), bytes, hipMemcpyHostToDevice, st);
+    if (e == hipSuccess) {
+        hipLaunchKernelGGL(load_chase_kernel, dim3(1), dim3(64), 0, st, reinterpret_cast<const uint32_t*>(mem), bytes,
+                           steps, uint32_t(device_scope ? 1 : 0), out);
+        e = hipGetLastError();
+    }
+    if (e == hipSuccess) e = hipMemcpyAsync(h, out, sizeof(h), hipMemcpyDeviceToHost, st);
+    if (e == hipSuccess) e = hipStreamSynchronize(st);
+    (void)hipFree(mem);
+    if (e != hipSuccess) return set_error(XP_E_HIP, "xp_load_latency: %s", hipGetErrorString(e));
+    *clk_per_load = float(double(h[0]) / steps);
     return XP_OK;
 }
 
