@@ -36,17 +36,25 @@
 //  * Each stage's weights (the attention stage's KV rows) are loaded into
 //    registers before the workgroup waits for the stage's inputs: weights
 //    do not depend on activations, so HBM streaming overlaps the waiting.
-//  * Matvec tiles are (64-column group, a range of k blocks); wave w takes
-//    blocks w, w + 8, ... (clamped to the range, the excess ones zeroed, so
-//    the loop has no branches) and the 8 wave partials are summed through LDS
-//    in a fixed order. The down projection (k = 6912) is split into chunks of
-//    kTokDownQuads quads, and q|k|v and o into kTokQkvSplit / kTokOSplit k
-//    halves, whose partial sums the consumer adds in chunk order, so every
-//    result is deterministic.
-//  * Attention: one workgroup per 32 keys of [kv_start, pos]; each computes
-//    QK-norm + RoPE of q and k itself, scores, a chunk softmax (max, sum of
-//    exp) and the unnormalised weighted values; 4 workgroups per query head
-//    then combine the chunks (softmax_rows_finish's rescale,
+//  * Matvec tiles: gate/up tiles are 32 ffn indices of the gate (lanes 0-31)
+//    and the up projection (lanes 32-63) over the whole k, ending with the
+//    GeGLU of those indices; q|k|v and o tiles are column slices (32 columns
+//    of a 64-column group over the whole k, lane l taking column l % 32 and
+//    block slot l / 32 of each two-block step); down tiles are 32-column
+//    slices of kTokDownQuads-quad k chunks, whose partial sums the next
+//    layer adds in chunk order. Wave w takes the steps w, w + 8, ...
+//    (clamped to the range, the repeats weighted zero, so the loop has no
+//    branches) and the 8 wave partials are summed through LDS in a fixed
+//    order, so every result is deterministic.
+//  * Attention, local layers (span <= 512, placement verified): 32
+//    workgroups of one XCD, each one query head x 64 keys, exchanging their
+//    chunk records through that XCD's L2 with 16 combine tiles of 64 dims;
+//    global layers: a head pair x 64 keys a workgroup (128 keys past span
+//    6656), 32 combine tiles of 32 dims; without a verified placement, all
+//    heads x 32 / 16 keys a workgroup. Each attention workgroup computes
+//    QK-norm + RoPE of its query head(s) and of the key itself, scores, a
+//    chunk softmax (max, sum of exp) and the unnormalised weighted values;
+//    the combine tiles rescale and sum the chunks (softmax_rows_finish,
 //    llm_transformer.cl:385-405). The current key/value are used from LDS
 //    (fp16-rounded, as the cache holds them) and appended to the cache by the
 //    chunk that contains them, for later tokens.
