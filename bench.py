@@ -535,7 +535,7 @@ def main() -> int:
     ap.add_argument("--no-configs", action="store_true",
                     help="skip the benchmark config 3 / 4 / 5 and attention legs")
     ap.add_argument("--mv-iters", type=int, default=60)
-    ap.add_argument("--only", choices=["all", "matvec", "attention", "cfg5", "native", "graph",
+    ap.add_argument("--only", choices=["all", "matvec", "cfg1", "attention", "cfg5", "native", "graph",
                                        "exchange"],
                     default="all",
                     help="one leg alone, for profiling: the standalone matvec and streaming "
@@ -572,6 +572,16 @@ def main() -> int:
                           "matvec_cfg1": {"us_per_launch": round(per1 * 1e6, 3),
                                           "GBs": round(nb1 / per1 / 1e9, 1)},
                           "stream_ceiling_GBs": round(ceil, 1)}), flush=True)
+        return 0
+    if args.only == "cfg1":
+        # config 1's matvec beside the streaming probe over the same bytes
+        # and the launch floor, back to back (one kernel trace prices all three)
+        nb1, per1, gate = matvec_leg(X, 1152, 6912, copies=64, iters=640)
+        ceil1_us, floor_us = same_size_ceiling(X, nb1)
+        print(json.dumps({"matvec_cfg1": {"us_per_launch": round(per1 * 1e6, 3),
+                                          "GBs": round(nb1 / per1 / 1e9, 1), "parity": gate,
+                                          "same_size_stream_us": round(ceil1_us, 3),
+                                          "launch_floor_us": round(floor_us, 3)}}), flush=True)
         return 0
     if args.only == "exchange":
         print(json.dumps({"exchange_chain": exchange_leg(X), "handoff": handoff_leg(X),

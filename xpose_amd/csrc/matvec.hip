@@ -419,17 +419,57 @@ __global__ __launch_bounds__(kMvWgWaves * kWave) void mv_int4_slice_kernel(MvArg
         const uint32_t i = threadIdx.x + k * NT;
         if (i < ntask) stage_x8(qx, sx, i, xv[k][0], xv[k][1]);
     }
-    __syncthreads();
-    float acc = 0.0f;
+    // while the staging completes: the nibbles as two's complement and each
+    // step's weight scale (zero past the end)
+    float ws[R];
 #pragma unroll
     for (int r = 0; r < R; ++r) {
         const uint32_t t = wave + uint32_t(kMvWgWaves) * r, b = t * S + bs;
-        if (t < nsteps) {
-            const uint32_t bb = min(b, nblk - 1u);
-            const uint32_t hb = (sw[r] >> (16u * (bb & 1u))) & 0xFFFFu;
-            const float scale = FMT == XP_SCALE_F16_QUAD ? f16_bits_to_f32(hb) : __uint_as_float(hb << 16);
-            const float f = b < nblk ? scale * sx[bb] : 0.0f;
-            acc = fmaf(f, float(block_dot(w[r], qx[bb])), acc);
+        const uint32_t bb = min(b, nblk - 1u);
+        const uint32_t hb = (sw[r] >> (16u * (bb & 1u))) & 0xFFFFu;
+        const float scale = FMT == XP_SCALE_F16_QUAD ? f16_bits_to_f32(hb) : __uint_as_float(hb << 16);
+        ws[r] = t < nsteps && b < nblk ? scale : 0.0f;
+        w[r] ^= 0x88888888u;
+    }
+    __syncthreads();
+    // The dots read the staged words through the lanes of a 16-lane row
+    // (block_dot_bc): every lane of a row takes the same block (slot bs is
+    // whole rows), lane jw < 10 holding words 2 jw, 2 jw + 1 of it. All of a
+    // wave's words and block scales are read before any is used.
+    const uint32_t jr = lane % 16u, jw = jr >= 2u * kQxPlanes ? jr - 2u * kQxPlanes : jr;
+    u32x2 aw[R];
+    float sxv[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        const uint32_t t = min(wave + uint32_t(kMvWgWaves) * r, nsteps - 1u);
+        const uint32_t bb = min(t * S + bs, nblk - 1u);
+        sxv[r] = sx[bb];
+        aw[r] = reinterpret_cast<const u32x2*>(&qx[bb])[jw];
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    // a DPP operation must follow an exec write by five wait states, which
+    // the compiler does not provide for inline assembly: one s_nop 4 before
+    // the first, ordered after the loads by the tied operands
+#pragma unroll
+    for (int r = 0; r < R; ++r) asm volatile("s_nop 4" : "+v"(aw[r].x), "+v"(aw[r].y));
+    float acc = 0.0f;
+#pragma unroll
+    for (int r = 0; r < R; r += 2) {
+        // steps of the whole wave past the end are skipped (t is uniform)
+        if (wave + uint32_t(kMvWgWaves) * uint32_t(r) >= nsteps) break;
+        if (r + 1 < R) {
+            const u32x4 w2[2] = {w[r], w[r + 1]};
+            const u32x2 a2[2] = {aw[r], aw[r + 1]};
+            int32_t d[2];
+            block_dot_bc<2>(w2, a2, d);
+            acc = fmaf(ws[r] * sxv[r], float(d[0]), acc);
+            acc = fmaf(ws[r + 1] * sxv[r + 1], float(d[1]), acc);
+        } else {
+            const u32x4 w1[1] = {w[r]};
+            const u32x2 a1[1] = {aw[r]};
+            int32_t d[1];
+            block_dot_bc<1>(w1, a1, d);
+            acc = fmaf(ws[r] * sxv[r], float(d[0]), acc);
         }
     }
     red[wave * kGrp + lane] = acc;

@@ -505,96 +505,6 @@ __device__ __forceinline__ void tile_prep(TkW<R>& p, uint32_t b0, uint32_t nb, u
     }
 }
 
-// The dot of one block with the staged planes, its activation words taken
-// from the lanes of the row: lane j < 2 P of each 16-lane row holds words
-// 2 j, 2 j + 1 of the block's 4 P plane words (plane p's word c is word
-// 4 p + c), and v_dot8c_i32_i4 with DPP row_newbcast:n reads lane n of the
-// row. A wave's lanes then read 8 bytes each from LDS for a block, not its
-// 16 P bytes. (The DPP form is inline assembly: the compiler does not fold a
-// DPP move into v_dot8c. Its sources come straight from LDS loads; see
-// tile_dot for the exec hazard.)
-template <int N>
-__device__ __forceinline__ int32_t dot8_bc(int32_t acc, uint32_t a, uint32_t w);
-#define XP_DOT8_BC(N)                                                                               \
-    template <>                                                                                    \
-    __device__ __forceinline__ int32_t dot8_bc<N>(int32_t acc, uint32_t a, uint32_t w) {           \
-        asm("v_dot8c_i32_i4_dpp %0, %1, %2 row_newbcast:" #N " row_mask:0xf bank_mask:0xf"         \
-            : "+v"(acc)                                                                            \
-            : "v"(a), "v"(w));                                                                     \
-        return acc;                                                                                \
-    }
-XP_DOT8_BC(0)
-XP_DOT8_BC(1)
-XP_DOT8_BC(2)
-XP_DOT8_BC(3)
-XP_DOT8_BC(4)
-XP_DOT8_BC(5)
-XP_DOT8_BC(6)
-XP_DOT8_BC(7)
-XP_DOT8_BC(8)
-XP_DOT8_BC(9)
-#undef XP_DOT8_BC
-// Word C of plane P (word 4 P + C: lane 2 P + C / 2 of the row, component C % 2).
-template <int P, int C>
-__device__ __forceinline__ int32_t wdot_bc(int32_t acc, u32x4 w, u32x2 a) {
-    static_assert(P >= 0 && P < kQxPlanes && C >= 0 && C < 4, "plane word");
-    const uint32_t wv = C == 0 ? w.x : C == 1 ? w.y : C == 2 ? w.z : w.w;
-    return dot8_bc<2 * P + C / 2>(acc, C % 2 ? a.y : a.x, wv);
-}
-// sum_k w_k q_k = sum_p 16^p D_p (D_p the dot with digit plane p) for
-// two's-complement nibbles w, over NB = 1 or 2 blocks at once, in three
-// chains a block: X = D_{P-1} 2^12 + D_{P-4}, Y = D_{P-2} 2^12 + D_{P-5}
-// (absent when P = 4), Z = D_{P-3}, combined as 16^(P-4) X + ... below.
-// The chains of both blocks are interleaved word by word, so consecutive
-// dots of one chain are at least four instructions apart: no wait states
-// for the compiler to insert (it keeps two between a VALU write and any
-// operand of a following DPP operation in inline assembly). |D_p| <= 2^11.
-template <int NB>
-__device__ __forceinline__ void block_dot_bc(const u32x4 (&w)[NB], const u32x2 (&a)[NB], int32_t (&out)[NB]) {
-    static_assert(kQxPlanes == 5 || kQxPlanes == 4, "4 or 5 digit planes");
-    constexpr int P = kQxPlanes;
-    int32_t X[NB], Y[NB], Z[NB];
-#pragma unroll
-    for (int b = 0; b < NB; ++b) X[b] = Y[b] = Z[b] = 0;
-    // round 1: planes P - 1, P - 2, P - 3
-    auto round1 = [&](auto cc) {
-        constexpr int C = decltype(cc)::value;
-#pragma unroll
-        for (int b = 0; b < NB; ++b) {
-            X[b] = wdot_bc<P - 1, C>(X[b], w[b], a[b]);
-            Y[b] = wdot_bc<P - 2, C>(Y[b], w[b], a[b]);
-            Z[b] = wdot_bc<P - 3, C>(Z[b], w[b], a[b]);
-        }
-    };
-    round1(std::integral_constant<int, 0>{});
-    round1(std::integral_constant<int, 1>{});
-    round1(std::integral_constant<int, 2>{});
-    round1(std::integral_constant<int, 3>{});
-#pragma unroll
-    for (int b = 0; b < NB; ++b) {
-        X[b] <<= 12;
-        if constexpr (P == 5) Y[b] <<= 12;
-    }
-    // round 2: plane P - 4 onto X, plane P - 5 (P = 5) onto Y
-    auto round2 = [&](auto cc) {
-        constexpr int C = decltype(cc)::value;
-#pragma unroll
-        for (int b = 0; b < NB; ++b) {
-            X[b] = wdot_bc<P - 4, C>(X[b], w[b], a[b]);
-            if constexpr (P == 5) Y[b] = wdot_bc<0, C>(Y[b], w[b], a[b]);
-        }
-    };
-    round2(std::integral_constant<int, 0>{});
-    round2(std::integral_constant<int, 1>{});
-    round2(std::integral_constant<int, 2>{});
-    round2(std::integral_constant<int, 3>{});
-#pragma unroll
-    for (int b = 0; b < NB; ++b) {
-        if constexpr (P == 5) out[b] = (X[b] << 4) + Y[b] + (Z[b] << 8);   // 16 X + Y + 256 Z
-        else out[b] = X[b] + (Y[b] << 8) + (Z[b] << 4);                  // X + 256 Y + 16 Z
-    }
-}
-
 // Dot of the wave's blocks with the staged planes (S.qx[0] = block b0) for a
 // tile readied by tile_prep, then reduced over the 8 waves and the S slots
 // in order. The result is valid in wave 0, lane l < CW holding column l; the
