@@ -230,7 +230,7 @@ int plan_attention(AttnArgs& a, uint32_t max_span, bool allow_xchg, int* U_out, 
         if (!sc) return XP_E_HIP;
         const uint64_t wgs = uint64_t(a.nsplit) * a.kv_heads * a.batch;
         a.xchg = allow_xchg && xchg_on && a.nsplit > uint32_t(kAttnFan) && sc->n_cu > 0 &&
-                 wgs <= uint64_t(sc->n_cu) ? 1u : 0u;
+                 wgs <= uint64_t(sc->n_cu) && a.nsplit <= kAttnSplitCap ? 1u : 0u;
         if (a.xchg && (!a.part || !a.tickets)) {
             // the exchange mode's own zeroed buffers, not the shared scratch
             if (!ensure_attn_x(sc, attn_partial_floats(a.kv_heads, a.n_heads, a.head_dim),

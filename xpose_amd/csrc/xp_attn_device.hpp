@@ -23,7 +23,7 @@ namespace xp {
 //   softmax one wave per head over the pass, online across passes (running
 //           max and sum, the accumulated values rescaled by exp(m_old - m_new))
 //   values  the same lanes accumulate p x v for their 8 dims, then the 16 row
-//           groups are summed (lane pairs by shuffle, waves through LDS)
+//           groups are summed (lane pairs by permlane32 swap, waves through LDS)
 // U (2, 4 or 8) follows the chunk length, so a 32-key chunk does a quarter
 // of a 128-key pass's arithmetic. Up to 128 splits (at least 32 keys each)
 // give most CUs a workgroup at one sequence's long spans (256 measured
@@ -60,6 +60,24 @@ __host__ __device__ constexpr uint32_t attn_head_floats(uint32_t G) {
     return kAttnRecords * attn_record(G) > kAttnMaxSplit * attn_xrecord(G) ? kAttnRecords * attn_record(G)
                                                                           : kAttnMaxSplit * attn_xrecord(G);
 }
+// Exchange mode (at most kAttnSplitCap splits): output dims a split
+// combines, the least power of two (at least 2) that covers G * HD over ns
+// splits, so a slice never crosses a head. Lane l of a polling wave takes
+// records l and l + 64; per record its head's statistics and HPW of the
+// slice's value pairs, spread over all eight waves (measured faster than
+// fewer waves polling more pairs each: their wave sums then run in series).
+__host__ __device__ constexpr uint32_t attn_xdims(uint32_t G, uint32_t ns) {
+    uint32_t D = 2u;
+    while (D * ns < G * kAttnHD) D *= 2u;
+    return D;
+}
+constexpr uint32_t kAttnXRec = kAttnSplitCap / 64u;   // records a lane
+constexpr uint32_t kAttnXPer = 5;                     // pairs a lane polls per record
+__host__ __device__ constexpr uint32_t attn_xpairs(uint32_t G, uint32_t ns) {   // HPW
+    return (attn_xdims(G, ns) / 2u + 7u) / 8u;
+}
+static_assert(kAttnXRec == 2u && attn_xpairs(4, kAttnFan + 1) <= kAttnXPer - 1u,
+              "exchange polling within one workgroup's waves");
 constexpr uint32_t kAttnEpoch = kAttnEpochWord;     // ticket word: the last exchange launch's tag
 constexpr uint32_t kAttnXErr  = kAttnXErrWord;      // ticket word: set when an exchange wait timed out
 static_assert(kAttnTicketsPerHead == 3 + kAttnGroups && kAttnEpoch == 1 + kAttnGroups &&
@@ -256,9 +274,19 @@ __device__ __forceinline__ bool attn_tile(AttnArgs a, const RopeFreq& f, uint32_
             vw[u] = j < nk ? ldg4(vbase + size_t(j) * rowstride) : u32x4{0u, 0u, 0u, 0u};
         }
     };
+    float q[G][8], o[G][8];
+    if constexpr (!FQ) {
+        // q first: the scores then wait for q and K only, V still in flight
+#pragma unroll
+        for (int h = 0; h < G; ++h) {
+            const float4* qp = reinterpret_cast<const float4*>(a.q + (size_t(g) * G + h) * HD + sub * 8);
+            const float4 q0 = qp[0], q1 = qp[1];
+            q[h][0] = q0.x; q[h][1] = q0.y; q[h][2] = q0.z; q[h][3] = q0.w;
+            q[h][4] = q1.x; q[h][5] = q1.y; q[h][6] = q1.z; q[h][7] = q1.w;
+        }
+    }
     load_pass(0);   // the first pass's keys do not depend on q
 
-    float q[G][8], o[G][8];
     // Fused QK-norm + RoPE (qk_norm_rope_append_kernel's arithmetic): waves
     // 0 .. G-1 norm and rotate query head g G + wave, wave G the key, wave
     // G + 1 rounds the value; lane l holds dims l + 64 c, so rotate-half pairs
@@ -333,14 +361,6 @@ __device__ __forceinline__ bool attn_tile(AttnArgs a, const RopeFreq& f, uint32_
             *reinterpret_cast<u32x4*>(const_cast<uint16_t*>(a.vc) + row) = vcur;
         }
         __syncthreads();   // red is rewritten by the combine
-    } else {
-#pragma unroll
-        for (int h = 0; h < G; ++h) {
-            const float4* qp = reinterpret_cast<const float4*>(a.q + (size_t(g) * G + h) * HD + sub * 8);
-            const float4 q0 = qp[0], q1 = qp[1];
-            q[h][0] = q0.x; q[h][1] = q0.y; q[h][2] = q0.z; q[h][3] = q0.w;
-            q[h][4] = q1.x; q[h][5] = q1.y; q[h][6] = q1.z; q[h][7] = q1.w;
-        }
     }
 #pragma unroll
     for (int h = 0; h < G; ++h)
@@ -434,16 +454,27 @@ __device__ __forceinline__ bool attn_tile(AttnArgs a, const RopeFreq& f, uint32_
         __syncthreads();   // ps and run[2] are rewritten by the next pass
     }
     // ---- sum the 16 row groups: lane pairs (l, l + 32), then the 8 waves
+    // v_permlane32_swap of values k and k + NO/2 (o flattened, NO = 8 G)
+    // hands lane l < 32 the pair (o_k[l], o_k[l + 32]) and lane l + 32 the
+    // pair of value k + NO/2, so one swap and one add sum two values and
+    // every lane writes: lanes 0..31 the first half of the values, 32..63
+    // the second (each sum in the order o[l] + o[l + 32]).
+    {
+        constexpr int NO = G * 8, NH2 = NO / 2;
+        const float* of = &o[0][0];
+        float sm2[NH2];
 #pragma unroll
-    for (int h = 0; h < G; ++h)
+        for (int k = 0; k < NH2; ++k) {
+            const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(of[k]),
+                                                            __float_as_uint(of[k + NH2]), false, false);
+            sm2[k] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+        }
+        const int kb = lane < 32 ? 0 : NH2;
 #pragma unroll
-        for (int e = 0; e < 8; ++e) o[h][e] += __shfl_xor(o[h][e], 32, kWave);
-    if (lane < 32) {
-#pragma unroll
-        for (int h = 0; h < G; ++h) {
-            float4* r4 = reinterpret_cast<float4*>(&red[wave][h * HD + sub * 8]);
-            r4[0] = float4{o[h][0], o[h][1], o[h][2], o[h][3]};
-            r4[1] = float4{o[h][4], o[h][5], o[h][6], o[h][7]};
+        for (int k = 0; k < NH2; k += 4) {
+            const int kk = kb + k, h = kk / 8, e = kk % 8;
+            *reinterpret_cast<float4*>(&red[wave][h * HD + sub * 8 + e]) =
+                float4{sm2[k], sm2[k + 1], sm2[k + 2], sm2[k + 3]};
         }
     }
     __syncthreads();
@@ -460,9 +491,9 @@ __device__ __forceinline__ bool attn_tile(AttnArgs a, const RopeFreq& f, uint32_
     uint32_t* tk = a.tickets + size_t(g) * kAttnTicketsPerHead;   // [0] level 2, [1 + grp] level 1
     if (a.xchg) {
         // ---- exchange mode (every workgroup of the launch resident at once):
-        // each split publishes its record as tagged pairs, then polls the
-        // statistics of all records and its own slice of the value dims, and
-        // writes that slice of the output — one exchange instead of the
+        // each split publishes its record as tagged pairs, then polls, in
+        // every record, its own slice of the value dims and the statistics
+        // of the heads that slice spans, and writes that slice of the output — one exchange instead of the
         // ticket chain. Split 0, once it has seen every record (so every
         // split has read the epoch), stores this launch's tag as the epoch.
         constexpr uint32_t NPR = G + G * HD / 2;                 // pairs per record
@@ -484,115 +515,106 @@ __device__ __forceinline__ bool attn_tile(AttnArgs a, const RopeFreq& f, uint32_
                 u32x4{__float_as_uint(run[0][tid]), xtag, __float_as_uint(run[1][tid]), xtag}, xr,
                 int((s * NPR + tid) * 16u), 0, kAuxDev);
         constexpr uint32_t NOUT = G * HD;
-        const uint32_t D = (((NOUT + ns - 1u) / ns) + 1u) & ~1u;   // output dims a split (even)
+        const uint32_t D = attn_xdims(G, ns);                      // output dims a split
         const uint32_t d0 = s * D, d1 = min(d0 + D, NOUT);
         if (d0 >= d1) return false;
-        const uint32_t DD = d1 - d0, HP = DD / 2u;
-        const uint32_t nst = ns * G, np = nst + ns * HP;           // pairs to poll (<= 4 a thread)
-        if (tid == 0) last = 0u;                                   // set if a wait times out
-        __syncthreads();   // every record sum has been read from red
-        float* xm = &red[0][0];                          // [split][head] max, then the factor
-        float* xl = xm + kAttnMaxSplit * G;              // [split][head] sum of exp
-        float* xv = xl + kAttnMaxSplit * G;              // [split][DD] value dims
-        float* xp = xv + kAttnMaxSplit * G + 512;        // [group][DD] partial sums
-        static_assert(3 * kAttnMaxSplit * G + 1024 <= (kAttnThreads / kWave) * G * HD, "exchange scratch");
-        uint32_t off[4];
-        bool act[4];
-        u32x4 v[4];
+        // The slice's combine, wave by wave with no barrier: wave w takes value
+        // pairs [c0, c1) of the slice (HPW a wave) in every record, and the
+        // statistics of the slice's head hs. Lane l polls, for records l and
+        // l + 64, slot (t, i) = item t of record slot i: t = 0 the
+        // statistics, t = 1 + c value pair c0 + c.
+        const uint32_t HP = (d1 - d0) / 2u, HPW = attn_xpairs(G, ns);
+        const uint32_t c0 = uint32_t(wave) * HPW, c1 = min(HP, c0 + HPW);
+        if (c0 >= c1) return true;
+        const uint32_t hs = d0 / HD, NI = 1u + (c1 - c0);
+        constexpr int RPL = int(kAttnXRec), TP = int(kAttnXPer);
+        uint32_t off[TP][RPL];
+        bool act[TP][RPL];
 #pragma unroll
-        for (int k = 0; k < 4; ++k) {
-            const uint32_t i = tid + uint32_t(k) * kAttnThreads;
-            act[k] = i < np;
-            const uint32_t ic = act[k] ? i : 0u;
-            if (ic < nst) {
-                off[k] = ((ic / G) * NPR + ic % G) * 16u;
-            } else {
-                const uint32_t j = ic - nst;
-                off[k] = ((j / HP) * NPR + G + d0 / 2u + j % HP) * 16u;
+        for (int t = 0; t < TP; ++t)
+#pragma unroll
+            for (int i = 0; i < RPL; ++i) {
+                const uint32_t r = uint32_t(lane) + kWave * uint32_t(i);
+                act[t][i] = r < ns && uint32_t(t) < NI;
+                const uint32_t pr = t == 0 ? hs : G + d0 / 2u + c0 + uint32_t(t - 1);
+                off[t][i] = act[t][i] ? (r * NPR + pr) * 16u : 0u;
             }
-        }
         const u32x4 ready = {0u, xtag, 0u, xtag};
+        u32x4 v[TP][RPL];
 #pragma unroll
-        for (int k = 0; k < 4; ++k) v[k] = act[k] ? ld_dev16(xr, off[k]) : ready;
+        for (int t = 0; t < TP; ++t)
+#pragma unroll
+            for (int i = 0; i < RPL; ++i) v[t][i] = act[t][i] ? ld_dev16(xr, off[t][i]) : ready;
+        bool timed_out = false;
         for (uint32_t spins = 0;; ++spins) {
             bool ok = true;
 #pragma unroll
-            for (int k = 0; k < 4; ++k) ok &= (v[k].y == xtag) & (v[k].w == xtag);
-            if (ok) break;
+            for (int t = 0; t < TP; ++t)
+#pragma unroll
+                for (int i = 0; i < RPL; ++i) ok &= (v[t][i].y == xtag) & (v[t][i].w == xtag);
+            if (__builtin_amdgcn_ballot_w64(!ok) == 0ull) break;
             if (spins > a.spin_limit) {
-                st_dev(tk + kAttnXErr, 1u);
-                if (a.status)
-                    __hip_atomic_fetch_or((XP_GLOBAL uint32_t*)a.status, 1u, __ATOMIC_RELAXED,
-                                          __HIP_MEMORY_SCOPE_AGENT);
-                last = 1u;
+                if (lane == 0) {
+                    st_dev(tk + kAttnXErr, 1u);
+                    if (a.status)
+                        __hip_atomic_fetch_or((XP_GLOBAL uint32_t*)a.status, 1u, __ATOMIC_RELAXED,
+                                              __HIP_MEMORY_SCOPE_AGENT);
+                }
+                timed_out = true;
                 break;
             }
             asm volatile("" ::: "memory");
 #pragma unroll
-            for (int k = 0; k < 4; ++k) v[k] = act[k] ? ld_dev16(xr, off[k]) : ready;
-        }
+            for (int t = 0; t < TP; ++t)
 #pragma unroll
-        for (int k = 0; k < 4; ++k) {
-            const uint32_t i = tid + uint32_t(k) * kAttnThreads;
-            if (!act[k]) continue;
-            if (i < nst) {
-                xm[i] = __uint_as_float(v[k].x);
-                xl[i] = __uint_as_float(v[k].z);
-            } else {
-                const uint32_t j = i - nst, r = j / HP, c = j % HP;
-                xv[r * DD + 2u * c] = __uint_as_float(v[k].x);
-                xv[r * DD + 2u * c + 1u] = __uint_as_float(v[k].z);
-            }
+                for (int i = 0; i < RPL; ++i)
+                    if (act[t][i] && ((v[t][i].y != xtag) | (v[t][i].w != xtag)))
+                        v[t][i] = ld_dev16(xr, off[t][i]);
         }
-        __syncthreads();
-        // Only after a complete wait: split 0 has then seen every split's
-        // record, so every split has read the epoch and none can take the
-        // next launch's tag. After a timed-out wait the epoch stays, the
-        // error word is set, and the tickets' owner zeroes the records and
-        // the epoch before the next launch.
-        if (s == 0 && tid == 0 && !last) st_dev(tk + kAttnEpoch, xtag);
-        // wave h: head h's rescale factors exp(m_r - M) (0 for an empty
-        // split) into xm and the denominator into run[1]
-        if (wave < G) {
-            const int h = wave;
-            float m4[kAttnMaxSplit / kWave], l4[kAttnMaxSplit / kWave];
-            float mx = -INFINITY;
+        // Only after a complete wait: wave 0 of split 0 has then seen a pair
+        // of every split's record, each stored after its split read the
+        // epoch, so none can take the next launch's tag. After a timed-out
+        // wait the epoch stays, the error word is set, and the tickets' owner
+        // zeroes the records and the epoch before the next launch.
+        if (s == 0 && wave == 0 && lane == 0 && !timed_out) st_dev(tk + kAttnEpoch, xtag);
+        // M = max over records, factors exp(m_r - M) (0 for an empty
+        // split), L = sum_r l_r f_r
+        float fr[RPL];
+        float mx = -INFINITY;
 #pragma unroll
-            for (int k = 0; k < kAttnMaxSplit / kWave; ++k) {
-                const uint32_t r = uint32_t(lane + kWave * k);
-                const bool in = r < ns;
-                l4[k] = in ? xl[r * G + h] : 0.0f;
-                m4[k] = in && l4[k] > 0.0f ? xm[r * G + h] : -INFINITY;
-                mx = fmaxf(mx, m4[k]);
-            }
-            const float M = wave_max(mx);
-            float ls = 0.0f;
+        for (int i = 0; i < RPL; ++i) {
+            const float l = act[0][i] ? __uint_as_float(v[0][i].z) : 0.0f;
+            fr[i] = l > 0.0f ? __uint_as_float(v[0][i].x) : -INFINITY;   // the max, for now
+            mx = fmaxf(mx, fr[i]);
+        }
+        const float M = wave_max(mx);
+        float ls = 0.0f;
 #pragma unroll
-            for (int k = 0; k < kAttnMaxSplit / kWave; ++k) {
-                const uint32_t r = uint32_t(lane + kWave * k);
-                const float f = m4[k] == -INFINITY ? 0.0f : exp_hw(m4[k] - M);
-                ls = fmaf(l4[k], f, ls);
-                if (r < ns) xm[r * G + h] = f;
+        for (int i = 0; i < RPL; ++i) {
+            fr[i] = fr[i] == -INFINITY ? 0.0f : exp_hw(fr[i] - M);
+            if (act[0][i]) ls = fmaf(__uint_as_float(v[0][i].z), fr[i], ls);
+        }
+        const float inv = rcp_hw(wave_sum(ls));
+        // value dims: per lane over its records in order, then the wave sum
+#pragma unroll
+        for (int t = 1; t < TP; ++t) {
+            if (uint32_t(t) >= NI) break;
+            float acc0 = 0.0f, acc1 = 0.0f;
+#pragma unroll
+            for (int i = 0; i < RPL; ++i) {
+                if (act[t][i]) {
+                    acc0 = fmaf(fr[i], __uint_as_float(v[t][i].x), acc0);
+                    acc1 = fmaf(fr[i], __uint_as_float(v[t][i].z), acc1);
+                }
             }
-            ls = wave_sum(ls);
-            if (lane == 0) run[1][h] = ls;
-        }
-        __syncthreads();
-        // dim j of the slice: group q of Q threads sums records q, q + Q, ...
-        const uint32_t Q = kAttnThreads / DD, j = tid % DD, q = tid / DD;
-        if (q < Q) {
-            const uint32_t h = (d0 + j) / HD;
-            float acc = 0.0f;
-            for (uint32_t r = q; r < ns; r += Q) acc = fmaf(xm[r * G + h], xv[r * DD + j], acc);
-            xp[q * DD + j] = acc;
-        }
-        __syncthreads();
-        if (uint32_t(tid) < DD) {
-            float acc = 0.0f;
-            for (uint32_t qq = 0; qq < Q; ++qq) acc += xp[qq * DD + tid];
+            const float s0 = wave_sum(acc0), s1 = wave_sum(acc1);
             // a timed-out wait (the launch was not resident at once) leaves
             // NaN, not a plausible value, besides the flag word
-            st_f<DEV>(out + d0 + tid, last ? __builtin_nanf("") : acc * rcp_hw(run[1][(d0 + tid) / HD]));
+            if (lane == 0) {
+                const uint32_t d = d0 + 2u * (c0 + uint32_t(t - 1));
+                st_f<DEV>(out + d, timed_out ? __builtin_nanf("") : s0 * inv);
+                st_f<DEV>(out + d + 1u, timed_out ? __builtin_nanf("") : s1 * inv);
+            }
         }
         return true;
     }
