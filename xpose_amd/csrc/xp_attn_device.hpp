@@ -78,6 +78,18 @@ __host__ __device__ constexpr uint32_t attn_xpairs(uint32_t G, uint32_t ns) {   
 }
 static_assert(kAttnXRec == 2u && attn_xpairs(4, kAttnFan + 1) <= kAttnXPer - 1u,
               "exchange polling within one workgroup's waves");
+// Floats of one (sequence, kv head)'s exchange records at ns splits: G HD / D
+// slices of 1 + D / 2 tagged pairs (16 bytes) per split.
+__host__ __device__ constexpr uint32_t attn_xfloats(uint32_t G, uint32_t ns) {
+    return 4u * (G * kAttnHD / attn_xdims(G, ns)) * (1u + attn_xdims(G, ns) / 2u) * ns;
+}
+constexpr bool attn_xfits() {
+    for (uint32_t G = 1; G <= uint32_t(kAttnMaxG); G *= 2u)
+        for (uint32_t ns = kAttnFan + 1; ns <= kAttnSplitCap; ++ns)
+            if (attn_xfloats(G, ns) > attn_head_floats(G)) return false;
+    return true;
+}
+static_assert(attn_xfits(), "exchange records within the partials of a kv head");
 constexpr uint32_t kAttnEpoch = kAttnEpochWord;     // ticket word: the last exchange launch's tag
 constexpr uint32_t kAttnXErr  = kAttnXErrWord;      // ticket word: set when an exchange wait timed out
 static_assert(kAttnTicketsPerHead == 3 + kAttnGroups && kAttnEpoch == 1 + kAttnGroups &&
@@ -493,40 +505,50 @@ __device__ __forceinline__ bool attn_tile(AttnArgs a, const RopeFreq& f, uint32_
         // ---- exchange mode (every workgroup of the launch resident at once):
         // each split publishes its record as tagged pairs, then polls, in
         // every record, its own slice of the value dims and the statistics
-        // of the heads that slice spans, and writes that slice of the output — one exchange instead of the
-        // ticket chain. Split 0, once it has seen every record (so every
+        // of the slice's head, and writes that slice of the output: one
+        // exchange instead of the ticket chain. Split 0, once it has seen every record (so every
         // split has read the epoch), stores this launch's tag as the epoch.
-        constexpr uint32_t NPR = G + G * HD / 2;                 // pairs per record
+        constexpr uint32_t NOUT = G * HD;
         const uint32_t ns = a.nsplit;
+        const uint32_t D = attn_xdims(G, ns);                      // output dims a slice
+        const uint32_t NSC = NOUT / D, IT = 1u + D / 2u;           // slices, items a slice
+        // Slice-major layout: item t of slice k of record r is the pair at
+        // (k IT + t) ns + r (item 0: the slice head's statistics, 1 + c: value
+        // dims 2c, 2c + 1 of the slice), so a poller reads each item of its
+        // slice for 64 records as 1 KiB contiguous.
         float* xbase = a.part + size_t(g) * attn_head_floats(G);
-        const rsrc_t xr = make_rsrc(xbase, ns * NPR * 16u);
-        for (uint32_t i = tid; i < uint32_t(G * HD / 2); i += kAttnThreads) {
-            float v0 = 0.0f, v1 = 0.0f;
+        const rsrc_t xr = make_rsrc(xbase, NSC * IT * ns * 16u);
+        for (uint32_t i = tid; i < NSC * IT; i += kAttnThreads) {
+            const uint32_t k = i / IT, t = i % IT;
+            float v0, v1;
+            if (t == 0u) {
+                const uint32_t h = k * D / HD;
+                v0 = run[0][h];      // -inf for an empty split
+                v1 = run[1][h];      // 0 for an empty split
+            } else {
+                const uint32_t d = k * D + 2u * (t - 1u);
+                v0 = 0.0f;
+                v1 = 0.0f;
 #pragma unroll
-            for (int w = 0; w < kAttnThreads / kWave; ++w) {
-                v0 += red[w][2u * i];
-                v1 += red[w][2u * i + 1u];
+                for (int w = 0; w < kAttnThreads / kWave; ++w) {
+                    v0 += red[w][d];
+                    v1 += red[w][d + 1u];
+                }
             }
             __builtin_amdgcn_raw_buffer_store_b128(u32x4{__float_as_uint(v0), xtag, __float_as_uint(v1), xtag},
-                                                   xr, int((s * NPR + G + i) * 16u), 0, kAuxDev);
+                                                   xr, int((i * ns + s) * 16u), 0, kAuxDev);
         }
-        if (tid < G)
-            __builtin_amdgcn_raw_buffer_store_b128(
-                u32x4{__float_as_uint(run[0][tid]), xtag, __float_as_uint(run[1][tid]), xtag}, xr,
-                int((s * NPR + tid) * 16u), 0, kAuxDev);
-        constexpr uint32_t NOUT = G * HD;
-        const uint32_t D = attn_xdims(G, ns);                      // output dims a split
-        const uint32_t d0 = s * D, d1 = min(d0 + D, NOUT);
-        if (d0 >= d1) return false;
+        if (s >= NSC) return false;
+        const uint32_t d0 = s * D;
         // The slice's combine, wave by wave with no barrier: wave w takes value
         // pairs [c0, c1) of the slice (HPW a wave) in every record, and the
-        // statistics of the slice's head hs. Lane l polls, for records l and
-        // l + 64, slot (t, i) = item t of record slot i: t = 0 the
-        // statistics, t = 1 + c value pair c0 + c.
-        const uint32_t HP = (d1 - d0) / 2u, HPW = attn_xpairs(G, ns);
+        // statistics of the slice's head. Lane l polls, for records l and
+        // l + 64, slot (t, i) = record slot i's item 0 (statistics) for t = 0,
+        // item 1 + c0 + t - 1 (value pair c0 + t - 1) for t >= 1.
+        const uint32_t HP = D / 2u, HPW = attn_xpairs(G, ns);
         const uint32_t c0 = uint32_t(wave) * HPW, c1 = min(HP, c0 + HPW);
         if (c0 >= c1) return true;
-        const uint32_t hs = d0 / HD, NI = 1u + (c1 - c0);
+        const uint32_t NI = 1u + (c1 - c0);
         constexpr int RPL = int(kAttnXRec), TP = int(kAttnXPer);
         uint32_t off[TP][RPL];
         bool act[TP][RPL];
@@ -536,8 +558,8 @@ __device__ __forceinline__ bool attn_tile(AttnArgs a, const RopeFreq& f, uint32_
             for (int i = 0; i < RPL; ++i) {
                 const uint32_t r = uint32_t(lane) + kWave * uint32_t(i);
                 act[t][i] = r < ns && uint32_t(t) < NI;
-                const uint32_t pr = t == 0 ? hs : G + d0 / 2u + c0 + uint32_t(t - 1);
-                off[t][i] = act[t][i] ? (r * NPR + pr) * 16u : 0u;
+                const uint32_t it = t == 0 ? 0u : 1u + c0 + uint32_t(t - 1);
+                off[t][i] = act[t][i] ? ((s * IT + it) * ns + r) * 16u : 0u;
             }
         const u32x4 ready = {0u, xtag, 0u, xtag};
         u32x4 v[TP][RPL];
