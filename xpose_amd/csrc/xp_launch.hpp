@@ -228,7 +228,7 @@ int launch_bmm(BmmArgs a, int fmt, int n_cu, hipStream_t st, const char* who);
 // they are quarter groups (one MFMA tile) or whole groups (four).
 int plan_bmm(BmmArgs& a, int fmt, int n_cu, const char* who, uint32_t* n_blocks, bool* quarter);
 
-// ---- persistent batched decode step (batch_step.hip) ----
+// ---- persistent batched decode step (batch_step.hip; experimental, opt-in) ----
 // One launch runs every layer of a batched decode step: one 512-thread
 // workgroup per CU walks the stages of each layer (q|k|v GEMM, attention,
 // o GEMM, staging, gate|up GEMM, down GEMM, staging) and takes the tiles of
