@@ -1086,7 +1086,7 @@ __global__ __launch_bounds__(kTkThreads) void token_kernel(TokArgs a) {
                 }
                 // the other key half (lane ^ 32), then the neighbouring dim (lane ^ 1)
 #pragma unroll
-                for (uint32_t h = 0; h < NH; ++h) o[h] += __shfl_xor(o[h], 32, kWave);
+                for (uint32_t h = 0; h < NH; ++h) o[h] = add_xor32(o[h]);
                 // chunk record: per head (max, sum of exp, unnormalised output[256]);
                 // lane l stores dims (dv & ~1, dv | 1) of head 2 kh + (l & 1) (and
                 // of the heads NH / 2 further on when NH > 4)
@@ -1320,8 +1320,8 @@ __global__ __launch_bounds__(kTkThreads) void token_kernel(TokArgs a) {
                     // the four key quarters: lanes l ^ 16 (swizzle within 32), l ^ 32
                     o0 += __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(o0), 0x401F));
                     o1 += __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(o1), 0x401F));
-                    o0 += __shfl_xor(o0, 32, kWave);
-                    o1 += __shfl_xor(o1, 32, kWave);
+                    o0 = add_xor32(o0);
+                    o1 = add_xor32(o1);
                     const float pcur = S.pc[hh];
                     o0 = fmaf(pcur, vc.x, o0);
                     o1 = fmaf(pcur, vc.y, o1);
@@ -1563,7 +1563,7 @@ __global__ __launch_bounds__(kTkThreads) void token_kernel(TokArgs a) {
             float y = tile_dot<RQ, 1u>(p, S, Sh::HB, wave, lane);
             if (wave == 0) {
                 y *= norm_scale<H>(rsn, eps);
-                const float up = __shfl_xor(y, 32, kWave);
+                const float up = from_lane_plus32(y);   // lanes 0..31 use it
                 const float hv = gelu_hw(y) * up;   // lanes 0..31: index 32 t + lane
                 const float hn = dpp_f<0xB1, 0xF>(hv, 0.0f);
                 if (lane < 32u && (lane & 1u) == 0u)

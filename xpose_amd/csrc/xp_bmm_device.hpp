@@ -234,7 +234,7 @@ __device__ __forceinline__ void stage_regs(u32x4& H, u32x4& L, float4& as, const
     // the row's block sum over its four 8-element groups (lanes 16 apart),
     // added as bprep_kernel adds them: (g0 + g1) + (g2 + g3)
     sum += __shfl_xor(sum, 16, kWave);
-    sum += __shfl_xor(sum, 32, kWave);
+    sum = add_xor32(sum);
     as = float4{__shfl(sum, int(4 * wsel + 0), kWave), __shfl(sum, int(4 * wsel + 1), kWave),
                 __shfl(sum, int(4 * wsel + 2), kWave), __shfl(sum, int(4 * wsel + 3), kWave)};
 }

@@ -324,6 +324,20 @@ __device__ __forceinline__ float row16_sum(float v) {
     v += dpp_f<0x140, 0xF>(v, 0.0f);   // row_mirror
     return v;
 }
+// x + (x of lane ^ 32) through v_permlane32_swap (a VALU op; ds_bpermute
+// would take the LDS pipe): the swap of x with itself hands lane l < 32
+// (x[l], x[l + 32]) and lane l + 32 (x[l], x[l + 32]), so every lane gets
+// the pair's sum, bit-identical to x + __shfl_xor(x, 32) (fp addition
+// commutes).
+__device__ __forceinline__ float add_xor32(float x) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+// The value of lane l + 32 in lanes l < 32 (lanes 32..63 get their own).
+__device__ __forceinline__ float from_lane_plus32(float x) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return __uint_as_float(r[1]);
+}
 __device__ __forceinline__ float wave_sum(float v) {
     v = row16_sum(v);
     v += dpp_f<0x142, 0xA>(v, 0.0f);   // row_bcast:15 -> rows 1, 3
