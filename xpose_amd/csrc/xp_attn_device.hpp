@@ -297,22 +297,11 @@ __device__ __forceinline__ bool attn_tile(AttnArgs a, const RopeFreq& f, uint32_
             q[h][4] = q1.x; q[h][5] = q1.y; q[h][6] = q1.z; q[h][7] = q1.w;
         }
     }
-    load_pass(0);   // the first pass's keys do not depend on q
-
-    // Fused QK-norm + RoPE (qk_norm_rope_append_kernel's arithmetic): waves
-    // 0 .. G-1 norm and rotate query head g G + wave, wave G the key, wave
-    // G + 1 rounds the value; lane l holds dims l + 64 c, so rotate-half pairs
-    // (d, d + 128) are (c, c + 2) of one lane. q lands in red[0], cos / sin
-    // in red[1], the fp16 key / value in red[2]; each thread then takes its
-    // eight dims into registers (red is free again before the combine). The
-    // raw rows are requested before the angles are computed, behind the
-    // first pass's K / V loads.
-    u32x4 kcur = {0u, 0u, 0u, 0u}, vcur = {0u, 0u, 0u, 0u};
+    // fused QK-norm: the raw q / k / v rows and the norm weights are
+    // requested first as well, so the norms and RoPE below run while the
+    // first pass's keys and values are still in flight
+    float e[4] = {0.0f, 0.0f, 0.0f, 0.0f}, w4[4] = {0.0f, 0.0f, 0.0f, 0.0f};
     if constexpr (FQ) {
-        const uint32_t pos = a.pos_dev[b];
-        float* cs = &red[1][0];
-        uint16_t* kv16 = reinterpret_cast<uint16_t*>(&red[2][0]);   // key [0, HD), value [HD, 2 HD)
-        float e[4] = {0.0f, 0.0f, 0.0f, 0.0f}, w4[4] = {0.0f, 0.0f, 0.0f, 0.0f};
         if (wave <= G + 1) {
             const float* src = wave < G   ? a.q_raw + size_t(b) * a.bq + (size_t(g) * G + wave) * HD
                                : wave == G ? a.k_raw + size_t(b) * a.bkv + size_t(g) * HD
@@ -325,6 +314,22 @@ __device__ __forceinline__ bool attn_tile(AttnArgs a, const RopeFreq& f, uint32_
                 for (int c = 0; c < 4; ++c) w4[c] = w[lane + 64 * c];
             }
         }
+    }
+    load_pass(0);   // the first pass's keys do not depend on q
+
+    // Fused QK-norm + RoPE (qk_norm_rope_append_kernel's arithmetic): waves
+    // 0 .. G-1 norm and rotate query head g G + wave, wave G the key, wave
+    // G + 1 rounds the value; lane l holds dims l + 64 c, so rotate-half pairs
+    // (d, d + 128) are (c, c + 2) of one lane. q lands in red[0], cos / sin
+    // in red[1], the fp16 key / value in red[2]; each thread then takes its
+    // eight dims into registers (red is free again before the combine). The
+    // raw rows (e, w4) were requested above, ahead of the first pass's K / V
+    // loads, so waiting for them does not wait for the keys.
+    u32x4 kcur = {0u, 0u, 0u, 0u}, vcur = {0u, 0u, 0u, 0u};
+    if constexpr (FQ) {
+        const uint32_t pos = a.pos_dev[b];
+        float* cs = &red[1][0];
+        uint16_t* kv16 = reinterpret_cast<uint16_t*>(&red[2][0]);   // key [0, HD), value [HD, 2 HD)
         if (tid < HD / 2) {
             float sv, cv;
             sincosf(float(pos) * f.inv[tid], &sv, &cv);
