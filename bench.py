@@ -65,6 +65,16 @@ TRAFFIC_SOURCE = ("rocprofv3 --pmc FETCH_SIZE and --pmc WRITE_SIZE of this bench
                   "(profiles/token_kernel_gemma3_1b_ctx4096.md), scaled by a 256 MiB copy's "
                   "readings; a constant of this build, not counted in this run")
 SEED = 0x5EED0003
+# The headline model's embedding rows: an fp32 N(0, 1) table apart from the
+# tied int4 lm_head (uploaded as XP_T_EMBED, as a GGUF's own embedding rows
+# are). With the table tied, a random model's greedy stream settles on one
+# fixed-point token; untied, it moves from token to token, so the timed and
+# checked decode takes a different decision each step.
+EMBED_SEED, EMBED_STREAM = 0x5EED0004, 931
+
+
+def embed_table(X, cfg):
+    return X.synth_normal(cfg.vocab * cfg.hidden, EMBED_SEED, EMBED_STREAM).reshape(cfg.vocab, cfg.hidden)
 # Algorithmic HBM bytes of one token at seq_len s (weights + fp16 scales,
 # KV reads, norm weights, logits write + argmax read, KV append).
 WEIGHT_BYTES = 562_360_320
@@ -495,7 +505,7 @@ def model_tensors(X, cfg) -> dict:
     return tensors
 
 
-def cpu_baseline(X, cfg, tensors, ctx: int, seconds: float, threads: int, min_tokens: int):
+def cpu_baseline(X, cfg, tensors, ctx: int, seconds: float, threads: int, min_tokens: int, embed=None):
     """The oracle (C restatement, OpenMP over output columns) on the
     headline's workload: the same model and KV rows, token 4242 at position
     ctx, then greedy decode from ctx + 1 for about `seconds` (at least
@@ -503,7 +513,7 @@ def cpu_baseline(X, cfg, tensors, ctx: int, seconds: float, threads: int, min_to
     the logits at ctx, the greedy ids, and the decode rate over the timed
     tokens."""
     import oracle
-    model = oracle.OracleModel(cfg, lambda l, k: tensors[(l, k)])
+    model = oracle.OracleModel(cfg, lambda l, k: tensors[(l, k)], embed=embed)
     kvd = cfg.n_kv_heads * cfg.head_dim
     for l in range(cfg.n_layers):
         model.kcache[l][:ctx * kvd] = X.synth_normal_f16(ctx * kvd, ctx, 2 * l)
@@ -618,6 +628,8 @@ def main() -> int:
 
     sess = X.DecodeSession(cfg)
     sess.synthesize(SEED)
+    emb = embed_table(X, cfg)
+    sess.upload(-1, X.T_EMBED, emb)
     kvd = cfg.n_kv_heads * cfg.head_dim
     for l in range(cfg.n_layers):
         sess.kv_upload(l, 0, 0, X.synth_normal_f16(ctx * kvd, ctx, 2 * l))
@@ -662,7 +674,7 @@ def main() -> int:
         import oracle
         extra["cfg4"] = cfg4_leg(X, sess, cfg, ctx)       # reads the pre-filled rows 0..ctx-1
         progress("cfg4")
-        om3 = oracle.OracleModel(cfg, lambda l, k: tensors[(l, k)])
+        om3 = oracle.OracleModel(cfg, lambda l, k: tensors[(l, k)], embed=emb)
         extra["cfg3"] = cfg3_leg(X, sess, cfg, om3, threads)
         del om3
         progress("cfg3 (128 ids checked)")
@@ -696,7 +708,7 @@ def main() -> int:
     n_check = len(gpu_stream)
     seconds = args.cpu_seconds if not args.no_cpu else 0.0
     lg0, o_ids, cpu_tok_s, n_cpu, cpu_el = cpu_baseline(
-        X, cfg, tensors, ctx, seconds, threads, n_check if not args.no_cpu else 2)
+        X, cfg, tensors, ctx, seconds, threads, n_check if not args.no_cpu else 2, embed=emb)
     k = min(len(o_ids), n_check)
     lg_gate = parity(logits0, lg0, 1e-3)
     head_gate = {"ok": bool(lg_gate["ok"] and o_ids[:k] == gpu_stream[:k]),
@@ -736,7 +748,8 @@ def main() -> int:
                       "int32 against the activations as 20-bit block fixed point (|x - s q| <= "
                       "2^-19 max|x| per block), scaled and accumulated in fp32; norms, RoPE, "
                       "attention, softmax, GeGLU fp32; KV cache fp16",
-        "data": "synthetic (random int4 weights, fp16 group-32 scales, fp16 KV N(0,1))",
+        "data": "synthetic (random int4 weights, fp16 group-32 scales, fp16 KV N(0,1), untied fp32 "
+                "N(0,1) embedding rows so the greedy stream moves)",
         "config": {"workload": "gemma3-1b-int4-greedy-decode", "ctx": ctx, "batch": 1,
                    "layers": 26, "hidden": 1152, "vocab": 262144, "weights": "int4 g32 + fp16",
                    "kv": "fp16", "launches_per_step": launches,
