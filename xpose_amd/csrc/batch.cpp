@@ -61,11 +61,22 @@ struct Batch {
     float* attn_part = nullptr;
     size_t attn_part_seq = 0;
     uint32_t* attn_tickets = nullptr;
-    float *cval, *oval;
-    uint32_t *cidx, *oidx, *d_tok, *d_pos;
-    uint32_t* h_tok = nullptr;           // pinned
-    float* h_val = nullptr;              // pinned [B][64]
+    float* cval;
+    uint32_t *cidx, *d_pos;
+    // Pinned, coherent host memory the device reads and writes in place
+    // (mapped, not cached on the device): the step's tokens, read by the
+    // embedding gather, and the 64 candidates of each sequence, written by
+    // the select, so a step needs no copy either way; m_* are their device
+    // addresses.
+    uint32_t* h_tok = nullptr;           // [B]
+    float* h_val = nullptr;              // [B][64]
     uint32_t* h_idx = nullptr;
+    uint32_t* m_tok = nullptr;
+    float* m_val = nullptr;
+    uint32_t* m_idx = nullptr;
+    // any layer's attention in exchange mode (whose error words the host
+    // reads after each step)
+    bool any_xchg = false;
     hipGraphExec_t graph = nullptr;
     hipEvent_t ev[2] = {nullptr, nullptr};
     std::vector<uint32_t> pos, steps;
@@ -139,7 +150,7 @@ int Batch::record() {
     // staging launch
     auto embed_prep = [&](void* a_, float* asum_) {
         BprepArgs p0{0, x, nullptr, nullptr, nullptr, w.layer[0].norm[0], a_, asum_, H, eps};
-        p0.tok = d_tok;
+        p0.tok = m_tok;
         p0.ewq = w.lm_w;
         p0.esc = w.lm_s;
         p0.etable = w.embed;
@@ -167,7 +178,7 @@ int Batch::record() {
         g.tickets_cap = tickets_cap;
         XB(launch_bmm(g, fmt, w.n_cu, st, "batch lm_head"));
         XB(launch_topk4(cval, cidx, logits, c.vocab, kHarvestParts, st, B));
-        XB(launch_select_rows(oval, oidx, cval, cidx, kHarvest, kCand, B, st, d_pos));
+        XB(launch_select_rows(m_val, m_idx, cval, cidx, kHarvest, kCand, B, st, d_pos));
         return XP_OK;
     }
     XB(embed_prep(a, asum));
@@ -215,6 +226,12 @@ int Batch::record() {
         aa.bcache = prefill ? 0 : size_t(S) * kvd;
         aa.bpart = attn_part_seq;
         const uint32_t max_span = glob || c.sliding_window == 0 ? S : std::min(c.sliding_window, S);
+        {
+            AttnArgs pa = aa;
+            int pu = 0;
+            RopeFreq pf{};
+            if (plan_attention(pa, max_span, true, &pu, &pf) == XP_OK && pa.xchg) any_xchg = true;
+        }
         XB(launch_attention(aa, max_span, st));
         const MvMatDesc om{o, L.w[XP_T_O], L.s[XP_T_O], H};
         XB(gemm(&om, 1, qd, "batch o_proj", 2, att));
@@ -234,7 +251,7 @@ int Batch::record() {
         const MvMatDesc lm{logits, w.lm_w, w.lm_s, c.vocab};
         XB(gemm(&lm, 1, H, "batch lm_head"));
         XB(launch_topk4(cval, cidx, logits, c.vocab, kHarvestParts, st, B));
-        XB(launch_select_rows(oval, oidx, cval, cidx, kHarvest, kCand, B, st, d_pos));
+        XB(launch_select_rows(m_val, m_idx, cval, cidx, kHarvest, kCand, B, st, d_pos));
     }
 #undef XB
     return XP_OK;
@@ -457,21 +474,19 @@ int Batch::forward(const uint32_t* tokens) {
             return set_error(XP_E_HIP, "xp_batch_forward: instantiate: %s", hipGetErrorString(ie));
         }
     }
+    // the tokens go to the device as the graph's embedding gather reads them
+    // from this pinned array; the previous step has finished (synchronised
+    // below), so nothing reads it while it changes
     std::memcpy(h_tok, tokens, B * 4);
-    XP_HIP(hipMemcpyAsync(d_tok, h_tok, B * 4, hipMemcpyHostToDevice, st));
     XP_HIP(hipEventRecord(ev[0], st));
     XP_HIP(hipGraphLaunch(graph, st));
     XP_HIP(hipEventRecord(ev[1], st));
-    if (!prefill) {
-        XP_HIP(hipMemcpyAsync(h_val, oval, size_t(B) * kCand * 4, hipMemcpyDeviceToHost, st));
-        XP_HIP(hipMemcpyAsync(h_idx, oidx, size_t(B) * kCand * 4, hipMemcpyDeviceToHost, st));
-    }
     const size_t attn_words = size_t(B) * w.cfg.n_kv_heads * kAttnTicketsPerHead;
     if (step_kernel) XP_HIP(hipMemcpyAsync(h_status, bs.status, 4, hipMemcpyDeviceToHost, st));
-    else XP_HIP(hipMemcpyAsync(h_attn, attn_tickets, attn_words * 4, hipMemcpyDeviceToHost, st));
+    else if (any_xchg) XP_HIP(hipMemcpyAsync(h_attn, attn_tickets, attn_words * 4, hipMemcpyDeviceToHost, st));
     XP_HIP(hipStreamSynchronize(st));
     (void)hipEventElapsedTime(&last_ms, ev[0], ev[1]);
-    if (!step_kernel) {
+    if (!step_kernel && any_xchg) {
         uint32_t err = 0;
         for (size_t i = kAttnXErrWord; i < attn_words; i += kAttnTicketsPerHead) err |= h_attn[i];
         if (err) {
@@ -619,8 +634,7 @@ int make_batch(const xp_session* weights, uint32_t n_seq, uint32_t max_seq, bool
         size_t(kmax / kBlkB) * 16 * 4,                           // block sums
         std::max<size_t>(part_cap, 1) * 4, size_t(tick) * 4,
         size_t(B) * b.attn_part_seq * 4 + 4, size_t(B) * c.n_kv_heads * kAttnTicketsPerHead * 4,
-        size_t(B) * kHarvest * 4, size_t(B) * kHarvest * 4,
-        size_t(B) * kCand * 4, size_t(B) * kCand * 4, size_t(B) * 4, size_t(B) * 4};
+        size_t(B) * kHarvest * 4, size_t(B) * kHarvest * 4, size_t(B) * 4};
     size_t total = 0;
     for (size_t z : sz) total += al(z);
     if (hipStreamCreateWithFlags(&b.st, hipStreamNonBlocking) != hipSuccess)
@@ -655,16 +669,21 @@ int make_batch(const xp_session* weights, uint32_t n_seq, uint32_t max_seq, bool
     b.attn_tickets = reinterpret_cast<uint32_t*>(nxt());
     b.cval = reinterpret_cast<float*>(nxt());
     b.cidx = reinterpret_cast<uint32_t*>(nxt());
-    b.oval = reinterpret_cast<float*>(nxt());
-    b.oidx = reinterpret_cast<uint32_t*>(nxt());
-    b.d_tok = reinterpret_cast<uint32_t*>(nxt());
     b.d_pos = reinterpret_cast<uint32_t*>(nxt());
-    if (hipHostMalloc(reinterpret_cast<void**>(&b.h_tok), B * 4) != hipSuccess ||
-        hipHostMalloc(reinterpret_cast<void**>(&b.h_val), size_t(B) * kCand * 4) != hipSuccess ||
-        hipHostMalloc(reinterpret_cast<void**>(&b.h_idx), size_t(B) * kCand * 4) != hipSuccess ||
+    const unsigned mapped = hipHostMallocMapped | hipHostMallocCoherent;
+    if (hipHostMalloc(reinterpret_cast<void**>(&b.h_tok), B * 4, mapped) != hipSuccess ||
+        hipHostMalloc(reinterpret_cast<void**>(&b.h_val), size_t(B) * kCand * 4, mapped) != hipSuccess ||
+        hipHostMalloc(reinterpret_cast<void**>(&b.h_idx), size_t(B) * kCand * 4, mapped) != hipSuccess ||
         hipHostMalloc(reinterpret_cast<void**>(&b.h_attn),
                       size_t(B) * c.n_kv_heads * kAttnTicketsPerHead * 4) != hipSuccess)
         return fail(XP_E_NOMEM, "pinned host memory");
+    if (hipHostGetDevicePointer(reinterpret_cast<void**>(&b.m_tok), b.h_tok, 0) != hipSuccess ||
+        hipHostGetDevicePointer(reinterpret_cast<void**>(&b.m_val), b.h_val, 0) != hipSuccess ||
+        hipHostGetDevicePointer(reinterpret_cast<void**>(&b.m_idx), b.h_idx, 0) != hipSuccess)
+        return fail(XP_E_HIP, "device addresses of the pinned token / candidate arrays");
+    // no candidates before the first step
+    std::fill(b.h_val, b.h_val + size_t(B) * kCand, -INFINITY);
+    std::fill(b.h_idx, b.h_idx + size_t(B) * kCand, 0xFFFFFFFFu);
     if (hipEventCreate(&b.ev[0]) != hipSuccess || hipEventCreate(&b.ev[1]) != hipSuccess)
         return fail(XP_E_HIP, "hipEventCreate failed");
     if (!prefill && exec == XP_EXEC_TOKEN) {

@@ -260,6 +260,7 @@ __global__ void multinomial_strided_kernel(float* out, uint32_t* idx_out, const 
 constexpr uint32_t kSelThreads = 1024;
 constexpr uint32_t kSelPer = 16;             // candidates per thread (16384 per row)
 constexpr uint32_t kSelKeep = 256;           // survivors ranked (k + ties)
+static_assert(kTopkMax <= kSelKeep, "the ranked output fits the survivors' slots");
 constexpr uint32_t kSelCopies = 16;          // histogram copies
 constexpr uint32_t kSelStride = kSelCopies + 1u;   // words per bin (padded: the sum reads bins apart)
 
@@ -278,12 +279,17 @@ __global__ __launch_bounds__(kSelThreads) void select_rows_kernel(float* oval, u
     __shared__ uint32_t sel[3];               // prefix, needed, survivors
     __shared__ float sv[kSelKeep];
     __shared__ uint32_t si[kSelKeep];
+    // the ranked output, written to oval / oidx once per slot at the end
+    // (the outputs may be host memory, where two stores to one slot from
+    // different waves need not land in order)
+    __shared__ float ov[kSelKeep];
+    __shared__ uint32_t oi[kSelKeep];
     const uint32_t r = blockIdx.x, tid = threadIdx.x;
     cval += size_t(r) * ncand;
     cidx += size_t(r) * ncand;
     if (tid < k) {   // slots no candidate reaches stay unfilled
-        oval[size_t(r) * k + tid] = -INFINITY;
-        oidx[size_t(r) * k + tid] = kNone;
+        ov[tid] = -INFINITY;
+        oi[tid] = kNone;
     }
     if (pos_inc && tid == 0) pos_inc[r] += 1u;
     // every candidate's value and index loaded at once (unconditionally, an
@@ -385,9 +391,14 @@ __global__ __launch_bounds__(kSelThreads) void select_rows_kernel(float* oval, u
         uint32_t rank = 0;
         for (uint32_t j = 0; j < m; ++j) rank += (sv[j] > v) | ((sv[j] == v) & (si[j] < d));
         if (rank < k) {
-            oval[size_t(r) * k + rank] = v;
-            oidx[size_t(r) * k + rank] = d;
+            ov[rank] = v;
+            oi[rank] = d;
         }
+    }
+    __syncthreads();
+    if (tid < k) {
+        oval[size_t(r) * k + tid] = ov[tid];
+        oidx[size_t(r) * k + tid] = oi[tid];
     }
 }
 
