@@ -24,18 +24,26 @@ namespace xp {
 //           max and sum, the accumulated values rescaled by exp(m_old - m_new))
 //   values  the same lanes accumulate p x v for their 8 dims, then the 16 row
 //           groups are summed (lane pairs by permlane32 swap, waves through LDS)
+// The query is loaded ahead of the first pass's K / V (and, fused, the raw
+// q / k / v rows), so the scores wait for q and K while V is in flight.
 // U (2, 4 or 8) follows the chunk length, so a 32-key chunk does a quarter
 // of a 128-key pass's arithmetic. Up to 128 splits (at least 32 keys each)
-// give most CUs a workgroup at one sequence's long spans (256 measured
-// slower at span 8192: the splits' exchange grows with their square). Each split
-// publishes (max, sum of exp, unnormalised o) per head; the last workgroup
-// of each group of 16 splits to arrive (arrival ticket) rescales and sums
-// the group — softmax_rows_finish's online combine (llm_transformer.cl:
-// 385-405) — into one record of the same form, and the last group to arrive
-// combines the group records, so no workgroup reads more than 16 records;
-// one group combines straight into the output. Records are read with 16-byte
-// device-scope loads spread over all the combining workgroup's threads, and
-// summed in a fixed order (deterministic).
+// give most CUs a workgroup at one sequence's long spans (256 splits of 32
+// keys and 64 of 128 measured slower at span 8192). Each split publishes
+// (max, sum of exp, unnormalised o) per head, combined as
+// softmax_rows_finish's online combine (llm_transformer.cl:385-405) in one
+// of two ways:
+//  * tickets (up to 16 splits, or some workgroups not resident at once): the
+//    last workgroup of each group of 16 splits to arrive (arrival ticket)
+//    rescales and sums the group into one record of the same form, and the
+//    last group to arrive combines the group records, so no workgroup reads
+//    more than 16 records; records are read with 16-byte device-scope loads
+//    spread over all the combining workgroup's threads;
+//  * exchange (more splits, every workgroup resident): records as tagged
+//    16-byte pairs in a slice-major layout; each split polls its output
+//    slice's pairs and its head's statistics in every record and combines
+//    them wave-locally (see the exchange block below).
+// Either way the sums run in a fixed order (deterministic).
 constexpr int kAttnThreads  = 512;
 constexpr int kAttnHD       = 256;                        // head_dim
 constexpr int kAttnLanes    = kAttnHD / 8;                // lanes per key row
