@@ -295,10 +295,46 @@ def test_gpu_attention(xp, xo, seq, kv0):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("heads,kv_heads", [(1, 1), (4, 4), (4, 2), (8, 2)])
+@pytest.mark.parametrize("seq", [131, 4097, 8192])
+def test_gpu_attention_head_groups(xp, xo, heads, kv_heads, seq):
+    """Query heads per KV head 1, 2 and 4 over one to four KV heads: both
+    entries against the oracle. At spans 4097 and 8192 the splits number more
+    than 16 and the timed entry's launches take the exchange mode (128 splits
+    over one or two KV heads, 64 over four), whose per-slice items then hold
+    one head's statistics beside 1, 2 or 4 heads' dims."""
+    print(f"case attention groups heads={heads} kv={kv_heads} seq={seq}", flush=True)
+    r = rng()
+    q = u(r, heads * HEAD_DIM)
+    kb = f16_bits(u(r, seq * kv_heads * HEAD_DIM))
+    vb = f16_bits(u(r, seq * kv_heads * HEAD_DIM))
+    scale = np.float32(1 / 16)
+    want = np.empty(heads * HEAD_DIM, np.float32)
+    xo.lib().xo_attention_f16(want, q, kb, vb, heads, kv_heads, HEAD_DIM, seq, 0, scale)
+    dq, dk, dv = dev(xp, q), dev(xp, kb), dev(xp, vb)
+    outs = []
+    for timed in (False, True, True):
+        d = sentinel(xp, heads * HEAD_DIM)
+        if timed:
+            K, V, ms = (C.c_void_p * 1)(dk.ptr), (C.c_void_p * 1)(dv.ptr), C.c_float()
+            xp.call("xp_attention_decode_timed", d.vp, dq.vp, K, V, 1, heads, kv_heads, HEAD_DIM,
+                    seq, 0, scale, 2, None, C.byref(ms))
+        else:
+            xp.call("xp_attention_decode", d.vp, dq.vp, dk.vp, dv.vp, heads, kv_heads, HEAD_DIM,
+                    seq, 0, scale, None)
+        xp.synchronize()
+        outs.append(d.download(np.float32))
+        ok, msg = allclose_report(outs[-1], want, RTOL, 1e-5)
+        assert ok, ("timed: " if timed else "") + msg
+    assert np.array_equal(outs[1].view(np.uint32), outs[2].view(np.uint32))
+
+
+@pytest.mark.gpu
 def test_gpu_attention_ticket_levels():
     """XP_ATTN_EXCHANGE=0 in the environment turns the exchange mode off: the
-    cases above of more than 16 splits in a child process, where the timed
-    entry's launches take the two-level ticket chain too."""
+    cases above of more than 16 splits (six spans, and the head groupings at
+    spans 4097 and 8192) in a child process, where the timed entry's launches
+    take the two-level ticket chain too."""
     import os
     import subprocess
     import sys
@@ -310,7 +346,7 @@ def test_gpu_attention_ticket_levels():
                         "-k", "test_gpu_attention and (1100 or 2047 or 3600 or 4097 or 8192)"],
                        env=env, capture_output=True, text=True, timeout=240)
     assert r.returncode == 0, r.stdout[-2000:] + r.stderr[-2000:]
-    assert "6 passed" in r.stdout, r.stdout[-2000:]
+    assert "14 passed" in r.stdout, r.stdout[-2000:]
 
 
 @pytest.mark.gpu
