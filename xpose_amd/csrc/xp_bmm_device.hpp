@@ -27,14 +27,22 @@ __device__ __forceinline__ bf16x8 as_bf16x8(u32x4 v) { return __builtin_bit_cast
 // mask in a scalar register, the bf16 128 pair in a vector register. Then
 // (w & mask) | magic is one v_and_or_b32 (gfx9's three-operand encoding has
 // no literal and takes one scalar operand, so with both constants as
-// literals it became a separate AND and OR).
+// literals it became a separate AND and OR). The bias correction's 136 is
+// held the same way: a block's operands are loaded under a test of the
+// wave's chunk, and a product of a loaded value with a literal was moved by
+// the compiler into that test's branch (an operation on a phi with one
+// loaded and one undefined input is folded into the input's block), where
+// it waited for the block's operands before the next block's loads could
+// issue: one memory round trip per block, in series.
 struct NibConst {
     uint32_t mask, magic;
+    float bias;
 };
 __device__ __forceinline__ NibConst nib_const() {
-    NibConst k{0x000F000Fu, 0x43004300u};
+    NibConst k{0x000F000Fu, 0x43004300u, 136.0f};
     asm volatile("" : "+s"(k.mask));
     asm volatile("" : "+v"(k.magic));
+    asm volatile("" : "+s"(k.bias));
     return k;
 }
 // The eight B-operand bf16 (128 + nibble) of one KM4 word, slot s = nibble e(s).
@@ -367,7 +375,7 @@ __device__ __forceinline__ bool bmm_tile(const BmmArgs& a, uint32_t cb, uint32_t
             stage_regs(cur.hi, cur.lo, cur.as, v, wsel);
         }
         const bf16x8 ahi = as_bf16x8(cur.hi), alo = as_bf16x8(cur.lo);
-        const float corr[4] = {136.0f * cur.as.x, 136.0f * cur.as.y, 136.0f * cur.as.z, 136.0f * cur.as.w};
+        const float corr[4] = {nk.bias * cur.as.x, nk.bias * cur.as.y, nk.bias * cur.as.z, nk.bias * cur.as.w};
 #pragma unroll
         for (int t = 0; t < T; ++t) {
             const bf16x8 bw = as_bf16x8(widen_nibbles(cur.w[t], nk));
