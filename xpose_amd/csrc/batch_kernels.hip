@@ -43,10 +43,10 @@ __global__ __launch_bounds__(kPrepThreads) void bprep_kernel(BprepArgs a) {
 }
 
 // ---- M = 16 int4 GEMM (the tile in xp_bmm_device.hpp) ------------------------------
-template <int FMT, int T, int AM, bool GE = false>
+template <int FMT, int T, int AM, bool GE = false, int KC = 0>
 __global__ __launch_bounds__(kBmmThreads) void bmm_int4_kernel(BmmArgs a) {
     __shared__ BmmSmem<T> sm;
-    (void)bmm_tile<FMT, T, AM, GE, false>(a, blockIdx.x, blockIdx.y, gridDim.x, sm);
+    (void)bmm_tile<FMT, T, AM, GE, false, KC>(a, blockIdx.x, blockIdx.y, gridDim.x, sm);
 }
 
 // Streamed M = 16 GEMM for wide matrices (the batched lm_head: 4096 column
@@ -245,10 +245,16 @@ int launch_bmm(BmmArgs a, int fmt, int n_cu, hipStream_t st, const char* who) {
     if (int rc = plan_bmm(a, fmt, n_cu, who, &nblocks, &quarter); rc != XP_OK) return rc;
     if (a.geglu) {
         const dim3 ggrid(nblocks, 1);
-        if (fmt == XP_SCALE_F16_QUAD)
-            hipLaunchKernelGGL((bmm_int4_kernel<XP_SCALE_F16_QUAD, 4, 0, true>), ggrid, dim3(kBmmThreads), 0, st, a);
-        else
-            hipLaunchKernelGGL((bmm_int4_kernel<XP_SCALE_BF16_QUAD, 4, 0, true>), ggrid, dim3(kBmmThreads), 0, st, a);
+#define XP_BMM_GE(F)                                                                                           \
+    if (a.kc == 5) hipLaunchKernelGGL((bmm_int4_kernel<F, 4, 0, true, 5>), ggrid, dim3(kBmmThreads), 0, st, a);      \
+    else if (a.kc == 4) hipLaunchKernelGGL((bmm_int4_kernel<F, 4, 0, true, 4>), ggrid, dim3(kBmmThreads), 0, st, a); \
+    else hipLaunchKernelGGL((bmm_int4_kernel<F, 4, 0, true>), ggrid, dim3(kBmmThreads), 0, st, a);
+        if (fmt == XP_SCALE_F16_QUAD) {
+            XP_BMM_GE(XP_SCALE_F16_QUAD)
+        } else {
+            XP_BMM_GE(XP_SCALE_BF16_QUAD)
+        }
+#undef XP_BMM_GE
         hipError_t e = hipGetLastError();
         if (e != hipSuccess) return set_error(XP_E_HIP, "%s: launch -> %s", who, hipGetErrorString(e));
         return XP_OK;
@@ -266,16 +272,23 @@ int launch_bmm(BmmArgs a, int fmt, int n_cu, hipStream_t st, const char* who) {
         return XP_OK;
     }
     const dim3 grid(nblocks, a.nsplit);
-#define XP_BMM_AM(F, TT)                                                                            \
-    if (a.amode == 2) hipLaunchKernelGGL((bmm_int4_kernel<F, TT, 2>), grid, dim3(kBmmThreads), 0, st, a);      \
-    else if (a.amode == 3) hipLaunchKernelGGL((bmm_int4_kernel<F, TT, 3>), grid, dim3(kBmmThreads), 0, st, a); \
-    else hipLaunchKernelGGL((bmm_int4_kernel<F, TT, 0>), grid, dim3(kBmmThreads), 0, st, a);
+    // blocks per wave 4 and 5 (every Gemma-3 shape: k = 1024, 1152, 6912)
+    // as compile-time counts, other counts under the chunk test
+#define XP_BMM_KC(F, TT, AM)                                                                               \
+    if (a.kc == 5) hipLaunchKernelGGL((bmm_int4_kernel<F, TT, AM, false, 5>), grid, dim3(kBmmThreads), 0, st, a);      \
+    else if (a.kc == 4) hipLaunchKernelGGL((bmm_int4_kernel<F, TT, AM, false, 4>), grid, dim3(kBmmThreads), 0, st, a); \
+    else hipLaunchKernelGGL((bmm_int4_kernel<F, TT, AM>), grid, dim3(kBmmThreads), 0, st, a);
+#define XP_BMM_AM(F, TT)                                  \
+    if (a.amode == 2) { XP_BMM_KC(F, TT, 2) }             \
+    else if (a.amode == 3) { XP_BMM_KC(F, TT, 3) }        \
+    else { XP_BMM_KC(F, TT, 0) }
     if (fmt == XP_SCALE_F16_QUAD) {
         if (quarter) { XP_BMM_AM(XP_SCALE_F16_QUAD, 1) } else { XP_BMM_AM(XP_SCALE_F16_QUAD, 4) }
     } else {
         if (quarter) { XP_BMM_AM(XP_SCALE_BF16_QUAD, 1) } else { XP_BMM_AM(XP_SCALE_BF16_QUAD, 4) }
     }
 #undef XP_BMM_AM
+#undef XP_BMM_KC
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return set_error(XP_E_HIP, "%s: launch -> %s", who, hipGetErrorString(e));
     return XP_OK;

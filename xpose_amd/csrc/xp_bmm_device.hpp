@@ -55,6 +55,12 @@ __device__ __forceinline__ u32x4 widen_nibbles(uint32_t w, NibConst k) {
     return d;
 }
 
+// The 32-bit word of lane 4 (l / 4) + R, as a float, in every lane l.
+template <int R>
+__device__ __forceinline__ float dpp_quad_bcast(uint32_t v) {
+    return __uint_as_float(uint32_t(__builtin_amdgcn_mov_dpp(int(v), R * 0x55, 0xF, 0xF, false)));
+}
+
 template <int FMT>
 __device__ __forceinline__ float quad_scale(u32x2 raw, uint32_t i) {
     const uint32_t w = (i & 2u) ? raw.y : raw.x;
@@ -257,7 +263,13 @@ struct BmmSmem {
 // when this workgroup wrote final outputs (every tile without k splits; with
 // splits, the last split of its column block to arrive). DEV: outputs go out
 // with device-scope stores (read by other workgroups of the same launch).
-template <int FMT, int T, int AM, bool GE, bool DEV>
+// KC > 0: every wave loads exactly KC blocks (a.kc == KC), its blocks past
+// its chunk re-reading its last one (not multiplied), so the loads are
+// unconditional and each block's multiply waits for that block's operands
+// only. KC = 0: blocks loaded under the chunk test; the compiler cannot then
+// count the loads issued after a block, and the first multiply waited for
+// nearly every load of the wave.
+template <int FMT, int T, int AM, bool GE, bool DEV, int KC = 0>
 __device__ __forceinline__ bool bmm_tile(const BmmArgs& a, uint32_t cb, uint32_t s, uint32_t ncb,
                                          BmmSmem<T>& sm) {
     constexpr uint32_t NO = 256u * T;            // outputs of a workgroup: 16 rows x 16 T columns
@@ -314,9 +326,9 @@ __device__ __forceinline__ bool bmm_tile(const BmmArgs& a, uint32_t cb, uint32_t
     struct Ops {
         u32x4 hi, lo;
         float4 as;
+        uint32_t asr;   // AM 0: lane l's word of the block sums, row 4 (l / 16) + l % 4
         float4 raw[NR];
         uint32_t w[T];
-        u32x2 sc[T];
     };
     const rsrc_t ra = make_rsrc(a.a, nblk * 2u * 64u * 16u), rsum = make_rsrc(a.asum, nblk * 16u * 4u);
     // fp32 rows: sequences past a.rows lie past the buffer's end and read as zeros
@@ -330,9 +342,9 @@ __device__ __forceinline__ bool bmm_tile(const BmmArgs& a, uint32_t cb, uint32_t
         if constexpr (AM == 0) {
             o.hi = __builtin_amdgcn_raw_buffer_load_b128(ra, int(lane * 16u), int(blk * 2048u), 0);
             o.lo = __builtin_amdgcn_raw_buffer_load_b128(ra, int(lane * 16u), int(blk * 2048u + 1024u), 0);
-            const u32x4 sv = __builtin_amdgcn_raw_buffer_load_b128(rsum, int(wsel * 16u), int(blk * 64u), 0);
-            o.as = float4{__uint_as_float(sv.x), __uint_as_float(sv.y), __uint_as_float(sv.z),
-                          __uint_as_float(sv.w)};
+            // one word a lane; the four rows of its quad are read by DPP
+            o.asr = __builtin_amdgcn_raw_buffer_load_b32(rsum, int(wsel * 16u + (lane % 4u) * 4u),
+                                                         int(blk * 64u), 0);
         } else {
             // row col16, k 32 blk + 8 wsel ..
             o.raw[0] = ldx4(rxa, vx, blk * 128u);
@@ -342,24 +354,52 @@ __device__ __forceinline__ bool bmm_tile(const BmmArgs& a, uint32_t cb, uint32_t
                 o.raw[3] = ldx4(rxu, vx + 16u, blk * 128u);
             }
         }
-        // block blk of column group g: weights at ((g nblk + blk) 64 + column) 16 + word 4,
-        // its scale quad at ((blk / 4) cols + 64 g + column) 8
-        const uint32_t sw = (g * nblk + blk) * 1024u, ss = ((blk / 4u) * cols + g * kGrp) * 8u;
+        // block blk of column group g: weights at ((g nblk + blk) 64 + column) 16 + word 4
+        const uint32_t sw = (g * nblk + blk) * 1024u;
 #pragma unroll
         for (int t = 0; t < T; ++t) {
             const uint32_t mt = GE ? uint32_t(t) / 2u : 0u;
             const uint32_t cg = GE ? c16 + 16u * (uint32_t(t) % 2u) + col16 : c16 + 16u * t + col16;
             o.w[t] = __builtin_amdgcn_raw_buffer_load_b32(rw[mt], int(cg * 16u + wsel * 4u), int(sw), kNt);
-            o.sc[t] = __builtin_amdgcn_raw_buffer_load_b64(rs[mt], int(cg * 8u), int(ss), 0);
         }
     };
     const NibConst nk = nib_const();
-    Ops ops[kBmmMaxPerWave];
+    // The scale quads of the wave's blocks (at most kBmmMaxPerWave = 5
+    // consecutive blocks: two quads), each loaded once: quad q of column
+    // group g at ((q cols + 64 g + column) 8.
+    const uint32_t nq = (nblk + 3u) / 4u, q0 = min(kb0 / 4u, nq - 1u);
+    u32x2 scq[2][T];
 #pragma unroll
-    for (uint32_t j = 0; j < kBmmMaxPerWave; ++j)
-        if (kb0 + j < kb1) load(ops[j], kb0 + j);
+    for (uint32_t qq = 0; qq < 2; ++qq) {
+        const uint32_t ss = (min(q0 + qq, nq - 1u) * cols + g * kGrp) * 8u;
 #pragma unroll
-    for (uint32_t j = 0; j < kBmmMaxPerWave; ++j) {
+        for (int t = 0; t < T; ++t) {
+            const uint32_t mt = GE ? uint32_t(t) / 2u : 0u;
+            const uint32_t cg = GE ? c16 + 16u * (uint32_t(t) % 2u) + col16 : c16 + 16u * t + col16;
+            scq[qq][t] = __builtin_amdgcn_raw_buffer_load_b64(rs[mt], int(cg * 8u), int(ss), 0);
+        }
+    }
+    static_assert(KC >= 0 && KC <= int(kBmmMaxPerWave), "blocks per wave");
+    constexpr uint32_t NB = KC > 0 ? uint32_t(KC) : kBmmMaxPerWave;
+    Ops ops[NB];
+    if constexpr (KC > 0) {
+        const uint32_t blast = kb1 > kb0 ? kb1 - 1u : nblk - 1u;
+#pragma unroll
+        for (uint32_t j = 0; j < NB; ++j) {
+            load(ops[j], min(kb0 + j, blast));
+            // in block order, and all before the first multiply (the
+            // scheduler would otherwise group the loads by kind, putting a
+            // block's last operand near the end, or move later blocks' loads
+            // behind earlier blocks' waits)
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    } else {
+#pragma unroll
+        for (uint32_t j = 0; j < NB; ++j)
+            if (kb0 + j < kb1) load(ops[j], kb0 + j);
+    }
+#pragma unroll
+    for (uint32_t j = 0; j < NB; ++j) {
         if (kb0 + j >= kb1) break;
         const uint32_t blk = kb0 + j;
         Ops& cur = ops[j];
@@ -373,6 +413,9 @@ __device__ __forceinline__ bool bmm_tile(const BmmArgs& a, uint32_t cb, uint32_t
                 for (int e = 0; e < 8; ++e) v[e] = gelu_hw(v[e]) * u[e];
             }
             stage_regs(cur.hi, cur.lo, cur.as, v, wsel);
+        } else {
+            cur.as = float4{dpp_quad_bcast<0>(cur.asr), dpp_quad_bcast<1>(cur.asr), dpp_quad_bcast<2>(cur.asr),
+                            dpp_quad_bcast<3>(cur.asr)};
         }
         const bf16x8 ahi = as_bf16x8(cur.hi), alo = as_bf16x8(cur.lo);
         const float corr[4] = {nk.bias * cur.as.x, nk.bias * cur.as.y, nk.bias * cur.as.z, nk.bias * cur.as.w};
@@ -383,7 +426,7 @@ __device__ __forceinline__ bool bmm_tile(const BmmArgs& a, uint32_t cb, uint32_t
             f32x4 c = {-corr[0], -corr[1], -corr[2], -corr[3]};
             c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ahi, bw, c, 0, 0, 0);
             c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(alo, bw, c, 0, 0, 0);
-            const float f = quad_scale<FMT>(cur.sc[t], blk % 4u);
+            const float f = quad_scale<FMT>(blk / 4u != q0 ? scq[1][t] : scq[0][t], blk % 4u);
 #pragma unroll
             for (int r = 0; r < 4; ++r) acc[t][r] = fmaf(f, c[r], acc[t][r]);
         }
