@@ -262,13 +262,11 @@ __device__ __forceinline__ bool attn_tile(AttnArgs a, const RopeFreq& f, uint32_
     }
     uint32_t span, kv0;
     attn_range(a, span, kv0, b);
-    // exchange mode: this launch's record tag, one past the last launch's
-    // (read before this workgroup's record is written; see the combine)
-    uint32_t xtag = 0u;
-    if (a.xchg) {
-        const uint32_t ep = ld_dev(a.tickets + size_t(g) * kAttnTicketsPerHead + kAttnEpoch);
-        xtag = ep + 1u != 0u ? ep + 1u : 1u;
-    }
+    // exchange mode: the last launch's epoch, read before this workgroup's
+    // record is written (see the combine); this launch's tag is one past it.
+    // Requested here, used only there: nothing waits for it on the way.
+    uint32_t xep = opaque_v(0u);
+    if (a.xchg) xep = ld_dev(a.tickets + size_t(g) * kAttnTicketsPerHead + kAttnEpoch);
     uint32_t chunk = (span + a.nsplit - 1) / a.nsplit;
     if (chunk < uint32_t(kAttnMinChunk)) chunk = kAttnMinChunk;
     const uint32_t j0 = min(s * chunk, span);
@@ -277,21 +275,27 @@ __device__ __forceinline__ bool attn_tile(AttnArgs a, const RopeFreq& f, uint32_
               wave = int(__builtin_amdgcn_readfirstlane(uint32_t(tid) / kWave));
     const int sub = tid % kAttnLanes, kp = tid / kAttnLanes;
     const size_t rowstride = size_t(a.kv_heads) * HD;   // fp16 elements per cache row
-    const uint16_t* kbase = a.kc + size_t(kv0 + j0) * rowstride + size_t(g) * HD + sub * 8;
-    const uint16_t* vbase = a.vc + size_t(kv0 + j0) * rowstride + size_t(g) * HD + sub * 8;
+    const uint16_t* kbase = a.kc + size_t(kv0) * rowstride + size_t(g) * HD + sub * 8;
+    const uint16_t* vbase = a.vc + size_t(kv0) * rowstride + size_t(g) * HD + sub * 8;
+    const uint32_t rlast = span > 0u ? span - 1u : 0u;
 
-    // K / V of one pass: U keys per lane, all loads in flight together
+    // K / V of one pass: U keys per lane, all loads in flight together. The
+    // loads are unconditional: a key past the split's chunk reads a row of
+    // the span (clamped to its last) and is masked where it is used (score
+    // -inf, value words zero). Loads under the key test compiled to branches
+    // whose merges waited for the loads (a copy of a loaded register inside
+    // the branch), so a pass's later loads issued behind its earlier ones.
     u32x4 kw[U], vw[U];
     auto load_pass = [&](int c0) {
 #pragma unroll
         for (int u = 0; u < U; ++u) {
-            const int j = c0 + kp + kAttnRows * u;
-            kw[u] = j < nk ? ldg4(kbase + size_t(j) * rowstride) : u32x4{0u, 0u, 0u, 0u};
+            const uint32_t r = min(j0 + uint32_t(c0 + kp + kAttnRows * u), rlast);
+            kw[u] = ldg4(kbase + size_t(r) * rowstride);
         }
 #pragma unroll
         for (int u = 0; u < U; ++u) {
-            const int j = c0 + kp + kAttnRows * u;
-            vw[u] = j < nk ? ldg4(vbase + size_t(j) * rowstride) : u32x4{0u, 0u, 0u, 0u};
+            const uint32_t r = min(j0 + uint32_t(c0 + kp + kAttnRows * u), rlast);
+            vw[u] = ldg4(vbase + size_t(r) * rowstride);
         }
     };
     float q[G][8], o[G][8];
@@ -308,7 +312,10 @@ __device__ __forceinline__ bool attn_tile(AttnArgs a, const RopeFreq& f, uint32_
     // fused QK-norm: the raw q / k / v rows and the norm weights are
     // requested first as well, so the norms and RoPE below run while the
     // first pass's keys and values are still in flight
-    float e[4] = {0.0f, 0.0f, 0.0f, 0.0f}, w4[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    // (opaque zeros where a wave loads nothing, so that no use of the rows
+    // is moved up to their loads, ahead of the K / V requests)
+    const float z = opaque_v(0.0f);
+    float e[4] = {z, z, z, z}, w4[4] = {z, z, z, z};
     if constexpr (FQ) {
         if (wave <= G + 1) {
             const float* src = wave < G   ? a.q_raw + size_t(b) * a.bq + (size_t(g) * G + wave) * HD
@@ -323,6 +330,10 @@ __device__ __forceinline__ bool attn_tile(AttnArgs a, const RopeFreq& f, uint32_
             }
         }
     }
+    // this thread's RoPE frequency (a kernel argument indexed by thread, so
+    // a memory load), requested before the keys as well
+    float inv_t = 0.0f;
+    if constexpr (FQ) inv_t = f.inv[tid % (HD / 2)];
     load_pass(0);   // the first pass's keys do not depend on q
 
     // Fused QK-norm + RoPE (qk_norm_rope_append_kernel's arithmetic): waves
@@ -335,14 +346,20 @@ __device__ __forceinline__ bool attn_tile(AttnArgs a, const RopeFreq& f, uint32_
     // loads, so waiting for them does not wait for the keys.
     u32x4 kcur = {0u, 0u, 0u, 0u}, vcur = {0u, 0u, 0u, 0u};
     if constexpr (FQ) {
-        const uint32_t pos = a.pos_dev[b];
+        const uint32_t pos = kv0 + span - 1u;   // pos_dev[b], as attn_range read it
         float* cs = &red[1][0];
         uint16_t* kv16 = reinterpret_cast<uint16_t*>(&red[2][0]);   // key [0, HD), value [HD, 2 HD)
-        if (tid < HD / 2) {
+        {
+            // every thread (frequency tid % (HD / 2)), the first HD / 2 store:
+            // computed only where stored, the frequency's load was moved into
+            // that branch, behind the keys, and waited for all of them
             float sv, cv;
-            sincosf(float(pos) * f.inv[tid], &sv, &cv);
-            cs[tid] = cv;
-            cs[HD / 2 + tid] = sv;
+            sincosf(float(pos) * inv_t, &sv, &cv);
+            asm volatile("" ::"v"(sv), "v"(cv));
+            if (tid < HD / 2) {
+                cs[tid] = cv;
+                cs[HD / 2 + tid] = sv;
+            }
         }
         __syncthreads();
         if (wave <= G) {
@@ -466,9 +483,9 @@ __device__ __forceinline__ bool attn_tile(AttnArgs a, const RopeFreq& f, uint32_
         }
 #pragma unroll
         for (int u = 0; u < U; ++u) {
-            float vf[8];
-            f16x8(vf, vw[u]);
             const int j = kp + kAttnRows * u;
+            float vf[8];
+            f16x8(vf, c0 + j < nk ? vw[u] : u32x4{0u, 0u, 0u, 0u});
 #pragma unroll
             for (int h = 0; h < G; ++h) {
                 const float p = ps[h][j];
@@ -522,6 +539,7 @@ __device__ __forceinline__ bool attn_tile(AttnArgs a, const RopeFreq& f, uint32_
         // exchange instead of the ticket chain. Split 0, once it has seen every record (so every
         // split has read the epoch), stores this launch's tag as the epoch.
         constexpr uint32_t NOUT = G * HD;
+        const uint32_t xtag = xep + 1u != 0u ? xep + 1u : 1u;
         const uint32_t ns = a.nsplit;
         const uint32_t D = attn_xdims(G, ns);                      // output dims a slice
         const uint32_t NSC = NOUT / D, IT = 1u + D / 2u;           // slices, items a slice

@@ -258,6 +258,17 @@ __device__ __forceinline__ unsigned long long ld_dev64(const unsigned long long*
     return __hip_atomic_load((XP_GLOBAL unsigned long long*)p, __ATOMIC_RELAXED,
                              __HIP_MEMORY_SCOPE_AGENT);
 }
+// v through an opaque copy in a vector register. A variable that is a
+// loaded value on one path and v on the other then has no constant input,
+// and the compiler leaves an operation on it where the source puts it (with
+// a constant input it folds the operation into the loading branch, and the
+// wait for the load lands right after the load).
+template <typename T>
+__device__ __forceinline__ T opaque_v(T v) {
+    asm volatile("" : "+v"(v));
+    return v;
+}
+
 // threadIdx.x through an opaque copy: values derived from it are computed
 // where they are used, not hoisted out of an enclosing loop by the compiler
 // (a persistent kernel that runs many different tiles in a loop would
