@@ -277,12 +277,18 @@ __device__ __forceinline__ bool attn_tile(AttnArgs a, const RopeFreq& f, uint32_
     const size_t rowstride = size_t(a.kv_heads) * HD;   // fp16 elements per cache row
     const uint16_t* kbase = a.kc + size_t(kv0) * rowstride + size_t(g) * HD + sub * 8;
     const uint16_t* vbase = a.vc + size_t(kv0) * rowstride + size_t(g) * HD + sub * 8;
-    const uint32_t rlast = span > 0u ? span - 1u : 0u;
+    // The last row a key of this split may read. With 128-key passes (U =
+    // 8) over chunks that can be far shorter (a batch's short sequences),
+    // the split's own last row, so the surplus keys re-read it from the
+    // cache (config 5's global layers: 52 -> 34 MB fetched a step, 18.8 ->
+    // 18.2 us a launch); with shorter passes the span's last row, the
+    // surplus keys then reading the next split's rows (one sequence's
+    // splits re-reading one row made its local-layer launch 8.3 -> 9.2 us).
+    const uint32_t rlast = U >= 8 && nk > 0 ? j0 + uint32_t(nk) - 1u : (span > 0u ? span - 1u : 0u);
 
     // K / V of one pass: U keys per lane, all loads in flight together. The
-    // loads are unconditional: a key past the split's chunk reads a row of
-    // the span (clamped to its last) and is masked where it is used (score
-    // -inf, value words zero). Loads under the key test compiled to branches
+    // loads are unconditional: a key past the split's chunk reads a clamped
+    // row and is masked where it is used (score -inf, value words zero). Loads under the key test compiled to branches
     // whose merges waited for the loads (a copy of a loaded register inside
     // the branch), so a pass's later loads issued behind its earlier ones.
     u32x4 kw[U], vw[U];
