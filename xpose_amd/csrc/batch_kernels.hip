@@ -66,7 +66,12 @@ __global__ __launch_bounds__(kBmmThreads) void bmm_stream_kernel(BmmArgs a) {
     constexpr uint32_t NO = 1024;                      // 16 rows x 64 columns
     static_assert(MB <= 5, "a wave's blocks span at most two scale quads");
     __shared__ float red[2][kBmmWaves][NO];
-    const uint32_t tid = threadIdx.x, wave = tid / kWave, lane = tid % kWave;
+    // the wave index as a uniform value: the blocks, quads and scalar load
+    // offsets derived from it then stay in scalar registers (derived from a
+    // per-lane value, every raw buffer load with such an offset compiled to
+    // a loop over the offset's distinct values, one pass at run time but
+    // ~10 instructions and a branch per load)
+    const uint32_t tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid / kWave), lane = tid % kWave;
     const uint32_t col16 = lane % 16u, wsel = lane / 16u;
     const uint32_t nblk = a.nblk, base = nblk / kBmmWaves, rem = nblk % kBmmWaves;
     const uint32_t nbw = base + (wave < rem ? 1u : 0u);       // this wave's blocks
