@@ -49,13 +49,20 @@ def test_batch_argument_errors(xh):
 # ---------------------------------------------------------------- GPU ----
 
 @pytest.mark.gpu
-def test_gpu_batch_matches_oracle_per_sequence(xp, xo):
+@pytest.mark.parametrize("shape", ["gemma3", "narrow"])
+def test_gpu_batch_matches_oracle_per_sequence(xp, xo, shape):
     """Five sequences at different depths (two past the 512-position window of
     the local layers), greedy, three steps; the oracle runs each sequence
-    alone."""
+    alone. narrow: hidden 512, ffn 1024, 2 query heads, so the GEMMs take 2
+    k blocks a wave (the loads under the chunk test) except the down
+    projection's 4, and the lm_head is a plain GEMM, not the streamed one."""
     X = xp
-    print("case batch vs oracle", flush=True)
-    cfg = X.XpConfig.gemma3_1b(n_layers=6, vocab=32768, max_seq=1024)
+    print(f"case batch vs oracle {shape}", flush=True)
+    if shape == "gemma3":
+        cfg = X.XpConfig.gemma3_1b(n_layers=6, vocab=32768, max_seq=1024)
+    else:
+        cfg = X.XpConfig.gemma3_1b(n_layers=3, hidden=512, ffn=1024, n_heads=2, n_kv_heads=1,
+                                   vocab=32768, max_seq=1024, global_every=3)
     sess, t = build(X, xo, cfg)
     kvd = cfg.n_kv_heads * cfg.head_dim
     depths = [3, 130, 511, 600, 1000]
