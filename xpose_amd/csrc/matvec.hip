@@ -47,6 +47,13 @@ struct MvArgs {
     uint32_t     wg_per_chunk; // ceil(groups / kMvWaves)
     float*       partial;      // [split][groups * 64]
     uint32_t*    tickets;      // [groups], zero at rest
+    // the column-slice kernel's input operation (MvIn; the mode is a
+    // template argument of the kernel)
+    const float* in_u;         // GeGLU: up; norm: y
+    const float* in_wpost;
+    const float* in_wpre;
+    float*       in_xout;
+    float        in_eps;
 };
 
 // Raw scale bits for one quad of blocks, held in registers across the load
@@ -354,7 +361,7 @@ __global__ __launch_bounds__(kMvWgWaves * kWave) void mv_int4_wg_kernel(MvArgs a
 constexpr uint32_t kMvSliceRounds = 8;
 constexpr uint32_t kMvSliceMaxBlk = 256;
 
-template <int FMT, int S, int R>
+template <int FMT, int S, int R, int XM = kMvInPlain>
 __global__ __launch_bounds__(kMvWgWaves * kWave) void mv_int4_slice_kernel(MvArgs a) {
     constexpr uint32_t CPS = kGrp / S;                                 // columns per slice
     static_assert(R >= 1 && R <= int(kMvSliceRounds), "steps per wave");
@@ -366,6 +373,7 @@ __global__ __launch_bounds__(kMvWgWaves * kWave) void mv_int4_slice_kernel(MvArg
     QxBlock* qx = smem_qx;
     float* sx = reinterpret_cast<float*>(smem_qx + nblk);
     float* red = sx + nblk;   // [kMvWgWaves][64]
+    float* xs2 = red + kMvWgWaves * kGrp;   // [kMvWgWaves]: norm mode, the waves' sums of x_new^2
     uint32_t mi = 0;
 #pragma unroll
     for (int i = 1; i < kMvMaxMats; ++i)
@@ -390,13 +398,36 @@ __global__ __launch_bounds__(kMvWgWaves * kWave) void mv_int4_slice_kernel(MvArg
     const float4* x4 = reinterpret_cast<const float4*>(a.x);
     const uint32_t ntask = nblk * 4u;
     float4 xv[NX][2];
+    [[maybe_unused]] float4 uv[NX][2], pv[NX][2], qv[NX][2];   // up or y; w_post; w_pre
+    if constexpr (XM == kMvInPlain) {
 #pragma unroll
-    for (uint32_t k = 0; k < NX; ++k) {
-        const uint32_t i = threadIdx.x + k * NT;
-        xv[k][0] = xv[k][1] = float4{0.0f, 0.0f, 0.0f, 0.0f};
-        if (i < ntask) {
+        for (uint32_t k = 0; k < NX; ++k) {
+            const uint32_t i = threadIdx.x + k * NT;
+            xv[k][0] = xv[k][1] = float4{0.0f, 0.0f, 0.0f, 0.0f};
+            if (i < ntask) {
+                xv[k][0] = x4[2 * i];
+                xv[k][1] = x4[2 * i + 1];
+            }
+        }
+    } else {
+        // every thread loads (past the last task, the last task again), so
+        // that no use of these values is placed in a load's branch
+        const float4* u4 = reinterpret_cast<const float4*>(a.in_u);
+        const float4* p4 = reinterpret_cast<const float4*>(a.in_wpost);
+        const float4* q4 = reinterpret_cast<const float4*>(a.in_wpre);
+#pragma unroll
+        for (uint32_t k = 0; k < NX; ++k) {
+            const uint32_t i = min(threadIdx.x + k * NT, ntask - 1u);
             xv[k][0] = x4[2 * i];
             xv[k][1] = x4[2 * i + 1];
+            uv[k][0] = u4[2 * i];
+            uv[k][1] = u4[2 * i + 1];
+            if constexpr (XM == kMvInNorm) {
+                pv[k][0] = p4[2 * i];
+                pv[k][1] = p4[2 * i + 1];
+                qv[k][0] = q4[2 * i];
+                qv[k][1] = q4[2 * i + 1];
+            }
         }
     }
     // step t = wave + 8 r covers blocks S t .. S t + S - 1; this lane's block
@@ -414,10 +445,69 @@ __global__ __launch_bounds__(kMvWgWaves * kWave) void mv_int4_slice_kernel(MvArg
         sw[r] = __builtin_nontemporal_load(sc32 + (size_t(b >> 2) * cols + j) * 2u +
                                            ((b >> 1) & 1u));
     }
+    [[maybe_unused]] float s2 = 0.0f;   // norm mode: this thread's sum of x_new^2
+    if constexpr (XM == kMvInPlain) {
 #pragma unroll
-    for (uint32_t k = 0; k < NX; ++k) {
-        const uint32_t i = threadIdx.x + k * NT;
-        if (i < ntask) stage_x8(qx, sx, i, xv[k][0], xv[k][1]);
+        for (uint32_t k = 0; k < NX; ++k) {
+            const uint32_t i = threadIdx.x + k * NT;
+            if (i < ntask) stage_x8(qx, sx, i, xv[k][0], xv[k][1]);
+        }
+    } else if constexpr (XM == kMvInGeglu) {
+#pragma unroll
+        for (uint32_t k = 0; k < NX; ++k) {
+            const uint32_t i = threadIdx.x + k * NT;
+            const float4 h0{gelu_tanh(xv[k][0].x) * uv[k][0].x, gelu_tanh(xv[k][0].y) * uv[k][0].y,
+                            gelu_tanh(xv[k][0].z) * uv[k][0].z, gelu_tanh(xv[k][0].w) * uv[k][0].w};
+            const float4 h1{gelu_tanh(xv[k][1].x) * uv[k][1].x, gelu_tanh(xv[k][1].y) * uv[k][1].y,
+                            gelu_tanh(xv[k][1].z) * uv[k][1].z, gelu_tanh(xv[k][1].w) * uv[k][1].w};
+            if (i < ntask) stage_x8(qx, sx, i, h0, h1);
+        }
+    } else {
+        // x_new = x + y rsqrt(mean y^2 + eps) (1 + w_post): the sum of y^2
+        // over the whole vector (every workgroup stages all of it)
+        float ss = 0.0f;
+#pragma unroll
+        for (uint32_t k = 0; k < NX; ++k) {
+            const float live = threadIdx.x + k * NT < ntask ? 1.0f : 0.0f;
+            const float yy[8] = {uv[k][0].x, uv[k][0].y, uv[k][0].z, uv[k][0].w,
+                                 uv[k][1].x, uv[k][1].y, uv[k][1].z, uv[k][1].w};
+#pragma unroll
+            for (int e = 0; e < 8; ++e) ss = fmaf(yy[e] * live, yy[e], ss);
+        }
+        ss = wave_sum(ss);
+        if (lane == 0) red[wave] = ss;
+        __syncthreads();
+        float tot = 0.0f;
+#pragma unroll
+        for (uint32_t v = 0; v < uint32_t(kMvWgWaves); ++v) tot += red[v];
+        const float post = rsq_hw(tot / float(nblk * kBlk) + a.in_eps);
+#pragma unroll
+        for (uint32_t k = 0; k < NX; ++k) {
+            const uint32_t i = threadIdx.x + k * NT;
+            const bool live = i < ntask;
+            const float xx[8] = {xv[k][0].x, xv[k][0].y, xv[k][0].z, xv[k][0].w,
+                                 xv[k][1].x, xv[k][1].y, xv[k][1].z, xv[k][1].w};
+            const float yy[8] = {uv[k][0].x, uv[k][0].y, uv[k][0].z, uv[k][0].w,
+                                 uv[k][1].x, uv[k][1].y, uv[k][1].z, uv[k][1].w};
+            const float wp[8] = {pv[k][0].x, pv[k][0].y, pv[k][0].z, pv[k][0].w,
+                                 pv[k][1].x, pv[k][1].y, pv[k][1].z, pv[k][1].w};
+            const float wq8[8] = {qv[k][0].x, qv[k][0].y, qv[k][0].z, qv[k][0].w,
+                                  qv[k][1].x, qv[k][1].y, qv[k][1].z, qv[k][1].w};
+            float xn[8], st[8];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                xn[e] = xx[e] + yy[e] * post * (1.0f + wp[e]);
+                s2 = fmaf(live ? xn[e] : 0.0f, xn[e], s2);
+                st[e] = xn[e] * (1.0f + wq8[e]);
+            }
+            if (live && blockIdx.x == 0) {
+                float4* xo = reinterpret_cast<float4*>(a.in_xout) + 2 * i;
+                xo[0] = float4{xn[0], xn[1], xn[2], xn[3]};
+                xo[1] = float4{xn[4], xn[5], xn[6], xn[7]};
+            }
+            if (live)
+                stage_x8(qx, sx, i, float4{st[0], st[1], st[2], st[3]}, float4{st[4], st[5], st[6], st[7]});
+        }
     }
     // while the staging completes: the nibbles as two's complement and each
     // step's weight scale (zero past the end)
@@ -473,6 +563,10 @@ __global__ __launch_bounds__(kMvWgWaves * kWave) void mv_int4_slice_kernel(MvArg
         }
     }
     red[wave * kGrp + lane] = acc;
+    if constexpr (XM == kMvInNorm) {
+        const float w2 = wave_sum(s2);
+        if (lane == 0) xs2[wave] = w2;
+    }
     __syncthreads();
     if (wave != 0 || lane >= CPS) return;
     float y = 0.0f;
@@ -480,6 +574,13 @@ __global__ __launch_bounds__(kMvWgWaves * kWave) void mv_int4_slice_kernel(MvArg
     for (uint32_t v = 0; v < uint32_t(kMvWgWaves); ++v)
 #pragma unroll
         for (uint32_t q = 0; q < uint32_t(S); ++q) y += red[v * kGrp + q * CPS + lane];
+    if constexpr (XM == kMvInNorm) {
+        // the input norm's scalar rsqrt(mean x_new^2 + eps), applied here
+        float t2 = 0.0f;
+#pragma unroll
+        for (uint32_t v = 0; v < uint32_t(kMvWgWaves); ++v) t2 += xs2[v];
+        y *= rsq_hw(t2 / float(nblk * kBlk) + a.in_eps);
+    }
     out[j] = y;
 }
 
@@ -536,10 +637,45 @@ size_t mv_partial_floats(uint32_t rows, uint32_t total_cols, uint32_t split, int
     return sp > 1 ? size_t(sp) * groups * kGrp : 0;
 }
 
+namespace {
+// Column slices per group for the column-slice plan (0: the plan does not
+// apply): two per group for wide shapes (>= 64 groups; config 1: 216
+// workgroups), four for narrow ones, as long as each workgroup can hold its
+// column group's whole k (at most kMvSliceRounds steps per wave).
+uint32_t slice_count(uint32_t nblk, uint32_t groups, int fmt, int n_cu) {
+    if (fmt == XP_SCALE_F32 || groups >= uint32_t(n_cu) * 8u) return 0;
+    uint32_t S = groups >= 64 ? 2u : 4u;
+    while (S < 4u && (nblk + S - 1) / S > kMvWgWaves * kMvSliceRounds) S *= 2u;
+    if (nblk <= kMvSliceMaxBlk && (nblk + S - 1) / S <= kMvWgWaves * kMvSliceRounds) return S;
+    return 0;
+}
+}  // namespace
+
+bool mv_slice_plan(uint32_t rows, uint32_t total_cols, int fmt, int n_cu) {
+    if (rows == 0 || rows % (4u * kBlk) != 0 || total_cols % kGrp != 0) return false;
+    return slice_count(rows / kBlk, total_cols / kGrp, fmt, n_cu > 0 ? n_cu : 256) != 0;
+}
+
 int launch_mv(const MvMatDesc* mats, uint32_t n, const float* x, int fmt, uint32_t rows,
               uint32_t split, float* partial, size_t partial_cap, uint32_t* tickets,
-              size_t tickets_cap, hipStream_t st, const char* who, int n_cu_hint) {
+              size_t tickets_cap, hipStream_t st, const char* who, int n_cu_hint, const MvIn* in) {
     if (!x) return set_error(XP_E_ARG, "%s: in is null", who);
+    const int xm = in ? in->mode : kMvInPlain;
+    if (xm != kMvInPlain && xm != kMvInGeglu && xm != kMvInNorm)
+        return set_error(XP_E_ARG, "%s: input operation %d", who, xm);
+    if (xm != kMvInPlain) {
+        // GeGLU reads `up`, the norm `y` (and both weights, writing x_out)
+        const float* u = xm == kMvInGeglu ? in->up : in->y;
+        auto bad = [](const void* p) { return !p || (reinterpret_cast<uintptr_t>(p) & 15u); };
+        if (bad(u) || (xm == kMvInNorm && (bad(in->w_post) || bad(in->w_pre) || bad(in->x_out))))
+            return set_error(XP_E_ARG, "%s: the input operation's vectors must be non-null and 16-byte aligned",
+                             who);
+        if (xm == kMvInNorm && (in->x_out == x || in->x_out == u || !(in->eps >= 0.0f)))
+            return set_error(XP_E_ARG, "%s: the norm's x_out aliases its inputs (or eps < 0)", who);
+        for (uint32_t i = 0; i < n && i < uint32_t(kMvMaxMats); ++i)
+            if (mats[i].out == u || (xm == kMvInNorm && mats[i].out == in->x_out))
+                return set_error(XP_E_ARG, "%s: an output aliases the input operation's vectors", who);
+    }
     if (reinterpret_cast<uintptr_t>(x) & 15u)
         return set_error(XP_E_ARG, "%s: in must be 16-byte aligned", who);
     if (n < 1 || n > uint32_t(kMvMaxMats))
@@ -584,20 +720,26 @@ int launch_mv(const MvMatDesc* mats, uint32_t n, const float* x, int fmt, uint32
     // chunks as give every CU a task, at most eight, each within kMvWgChunk
     // quads. A caller-provided partial buffer too small for that plan keeps
     // the split-k plan it was sized for.
+    if (xm != kMvInPlain && (split != 0 || slice_count(nblk, groups, fmt, n_cu) == 0))
+        return set_error(XP_E_ARG, "%s: an input operation needs the column-slice plan", who);
     if (split == 0 && fmt != XP_SCALE_F32 && groups < uint32_t(n_cu) * 8u) {
-        // Column slices when each workgroup can hold its column group's whole
-        // k (at most kMvSliceRounds steps per wave): two per group for wide
-        // shapes (>= 64 groups; config 1: 216 workgroups), four for narrow
-        // ones. Measured per launch on MI355X (back to back, 2.8 us launch
-        // floor): config 1 3.3 us (one workgroup per group: 3.9), q 2.9 us,
-        // o 2.9 us (k-chunks with a last-arrival sum: 5.7, 6.1).
-        uint32_t S = groups >= 64 ? 2u : 4u;
-        while (S < 4u && (nblk + S - 1) / S > kMvWgWaves * kMvSliceRounds) S *= 2u;
-        if (nblk <= kMvSliceMaxBlk && (nblk + S - 1) / S <= kMvWgWaves * kMvSliceRounds) {
+        // Column slices (slice_count). Measured per launch on MI355X (back to
+        // back, 2.8 us launch floor): config 1 3.3 us (one workgroup per
+        // group: 3.9), q 2.9 us, o 2.9 us (k-chunks with a last-arrival sum:
+        // 5.7, 6.1).
+        const uint32_t S = slice_count(nblk, groups, fmt, n_cu);
+        if (S != 0) {
             a.split = 1;
             a.qpc = a.nquads;
+            if (xm != kMvInPlain) {
+                a.in_u = xm == kMvInGeglu ? in->up : in->y;
+                a.in_wpost = in->w_post;
+                a.in_wpre = in->w_pre;
+                a.in_xout = in->x_out;
+                a.in_eps = in->eps;
+            }
             const size_t lds = size_t(nblk) * (sizeof(QxBlock) + sizeof(float)) +
-                               size_t(kMvWgWaves) * kGrp * sizeof(float);
+                               size_t(kMvWgWaves) * (kGrp + 1) * sizeof(float);
             const dim3 grid(groups * S), block(kMvWgWaves * kWave);
             // steps per wave, rounded up to 1, 2, 3, 4 or 8 (one instance
             // each). A step past the end still loads (a clamped block, weighed
@@ -605,22 +747,26 @@ int launch_mv(const MvMatDesc* mats, uint32_t n, const float* x, int fmt, uint32
             // wave-blocks for 18 instead of 32, config 1 3.47 -> 3.31 us.
             const uint32_t need = ((nblk + S - 1) / S + kMvWgWaves - 1) / kMvWgWaves;
             const uint32_t R = need <= 1 ? 1 : need <= 2 ? 2 : need <= 3 ? 3 : need <= 4 ? 4 : 8;
-#define XP_MV_SLICE_R(F, SS)                                                                         \
-    if (R == 1) hipLaunchKernelGGL((mv_int4_slice_kernel<F, SS, 1>), grid, block, lds, st, a);       \
-    else if (R == 2) hipLaunchKernelGGL((mv_int4_slice_kernel<F, SS, 2>), grid, block, lds, st, a);  \
-    else if (R == 3) hipLaunchKernelGGL((mv_int4_slice_kernel<F, SS, 3>), grid, block, lds, st, a);  \
-    else if (R == 4) hipLaunchKernelGGL((mv_int4_slice_kernel<F, SS, 4>), grid, block, lds, st, a);  \
-    else hipLaunchKernelGGL((mv_int4_slice_kernel<F, SS, 8>), grid, block, lds, st, a);
-#define XP_MV_SLICE_LAUNCH(F)                                                                 \
-    if (S == 4) { XP_MV_SLICE_R(F, 4) }                                                        \
-    else if (S == 2) { XP_MV_SLICE_R(F, 2) }                                                   \
-    else { XP_MV_SLICE_R(F, 1) }
+#define XP_MV_SLICE_R(F, SS, XX)                                                                          \
+    if (R == 1) hipLaunchKernelGGL((mv_int4_slice_kernel<F, SS, 1, XX>), grid, block, lds, st, a);       \
+    else if (R == 2) hipLaunchKernelGGL((mv_int4_slice_kernel<F, SS, 2, XX>), grid, block, lds, st, a);  \
+    else if (R == 3) hipLaunchKernelGGL((mv_int4_slice_kernel<F, SS, 3, XX>), grid, block, lds, st, a);  \
+    else if (R == 4) hipLaunchKernelGGL((mv_int4_slice_kernel<F, SS, 4, XX>), grid, block, lds, st, a);  \
+    else hipLaunchKernelGGL((mv_int4_slice_kernel<F, SS, 8, XX>), grid, block, lds, st, a);
+#define XP_MV_SLICE_X(F, SS)                                  \
+    if (xm == kMvInGeglu) { XP_MV_SLICE_R(F, SS, kMvInGeglu) } \
+    else if (xm == kMvInNorm) { XP_MV_SLICE_R(F, SS, kMvInNorm) } \
+    else { XP_MV_SLICE_R(F, SS, kMvInPlain) }
+#define XP_MV_SLICE_LAUNCH(F)                   \
+    if (S == 4) { XP_MV_SLICE_X(F, 4) }          \
+    else { XP_MV_SLICE_X(F, 2) }
             if (fmt == XP_SCALE_F16_QUAD) {
                 XP_MV_SLICE_LAUNCH(XP_SCALE_F16_QUAD)
             } else {
                 XP_MV_SLICE_LAUNCH(XP_SCALE_BF16_QUAD)
             }
 #undef XP_MV_SLICE_LAUNCH
+#undef XP_MV_SLICE_X
 #undef XP_MV_SLICE_R
             hipError_t e = hipGetLastError();
             if (e != hipSuccess) return set_error(XP_E_HIP, "%s: launch -> %s", who, hipGetErrorString(e));

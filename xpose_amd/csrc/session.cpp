@@ -222,6 +222,16 @@ int Session::record(int variant, uint32_t& n) {
     } while (0)
     XP_STEP(launch_embed(x, lm_w, lm_s, fmt, H, c.vocab, embed_scale(), state, hist, embed, st));
     XP_STEP(launch_norm_res_norm(x, nullptr, nullptr, L[0].norm[0], xb, H, eps, st));
+    // Where the column-slice matvec takes the shape, the residual add and
+    // the two RMSNorms before the q|k|v and gate/up matvecs, and the GeGLU
+    // before the down matvec, run inside those matvecs' staging instead of
+    // as launches of their own (3 launches fewer a layer). The fused norm
+    // writes the new residual to the other of two buffers, x and xb (xb is
+    // free once layer 0's q|k|v has read its normed input).
+    const bool fuse_norm = mv_slice_plan(H, qd + 2 * kvd, fmt, n_cu) && mv_slice_plan(H, 2 * c.ffn, fmt, n_cu);
+    const bool fuse_geglu = mv_slice_plan(c.ffn, H, fmt, n_cu);
+    float* xr = x;                        // the residual stream
+    float* xo = fuse_norm ? xb : nullptr;  // the other buffer (fused norms)
     for (uint32_t l = 0; l < c.n_layers; ++l) {
         Layer& w = L[l];
         const bool glob = is_global(l);
@@ -229,8 +239,21 @@ int Session::record(int variant, uint32_t& n) {
         const MvMatDesc qkv[3] = {{q_raw, w.w[XP_T_Q], w.s[XP_T_Q], qd},
                                   {k_raw, w.w[XP_T_K], w.s[XP_T_K], kvd},
                                   {v, w.w[XP_T_V], w.s[XP_T_V], kvd}};
-        XP_STEP(launch_mv(qkv, 3, xb, fmt, H, 0, mv_partial, mv_partial_cap, tickets + kTicketMv,
-                          8192, st, "session qkv", n_cu));
+        if (fuse_norm && l > 0) {
+            MvIn in;
+            in.mode = kMvInNorm;
+            in.y = xb2;                       // the previous layer's down projection
+            in.w_post = L[l - 1].norm[3];
+            in.w_pre = w.norm[0];
+            in.x_out = xo;
+            in.eps = eps;
+            XP_STEP(launch_mv(qkv, 3, xr, fmt, H, 0, mv_partial, mv_partial_cap, tickets + kTicketMv,
+                              8192, st, "session qkv", n_cu, &in));
+            std::swap(xr, xo);
+        } else {
+            XP_STEP(launch_mv(qkv, 3, xb, fmt, H, 0, mv_partial, mv_partial_cap, tickets + kTicketMv,
+                              8192, st, "session qkv", n_cu));
+        }
         // QK-norm, RoPE and the KV append run inside the attention launch
         AttnArgs aa{};
         aa.out = att; aa.kc = w.kc; aa.vc = w.vc;
@@ -251,21 +274,48 @@ int Session::record(int variant, uint32_t& n) {
         const MvMatDesc o{xb2, w.w[XP_T_O], w.s[XP_T_O], H};
         XP_STEP(launch_mv(&o, 1, att, fmt, qd, 0, mv_partial, mv_partial_cap, tickets + kTicketMv,
                           8192, st, "session o_proj", n_cu));
-        XP_STEP(launch_norm_res_norm(x, xb2, w.norm[1], w.norm[2], xb, H, eps, st));
         const MvMatDesc gu[2] = {{gate, w.w[XP_T_GATE], w.s[XP_T_GATE], c.ffn},
                                  {up, w.w[XP_T_UP], w.s[XP_T_UP], c.ffn}};
-        XP_STEP(launch_mv(gu, 2, xb, fmt, H, 0, mv_partial, mv_partial_cap, tickets + kTicketMv,
-                          8192, st, "session gate/up", n_cu));
-        XP_STEP(xp_geglu(hb, gate, up, c.ffn, st));
+        if (fuse_norm) {
+            MvIn in;
+            in.mode = kMvInNorm;
+            in.y = xb2;                       // the o projection
+            in.w_post = w.norm[1];
+            in.w_pre = w.norm[2];
+            in.x_out = xo;
+            in.eps = eps;
+            XP_STEP(launch_mv(gu, 2, xr, fmt, H, 0, mv_partial, mv_partial_cap, tickets + kTicketMv,
+                              8192, st, "session gate/up", n_cu, &in));
+            std::swap(xr, xo);
+        } else {
+            XP_STEP(launch_norm_res_norm(x, xb2, w.norm[1], w.norm[2], xb, H, eps, st));
+            XP_STEP(launch_mv(gu, 2, xb, fmt, H, 0, mv_partial, mv_partial_cap, tickets + kTicketMv,
+                              8192, st, "session gate/up", n_cu));
+        }
         const MvMatDesc d{xb2, w.w[XP_T_DOWN], w.s[XP_T_DOWN], H};
-        XP_STEP(launch_mv(&d, 1, hb, fmt, c.ffn, 0, mv_partial, mv_partial_cap,
-                          tickets + kTicketMv, 8192, st, "session down", n_cu));
-        const float* next = (l + 1 < c.n_layers) ? L[l + 1].norm[0] : final_norm;
-        XP_STEP(launch_norm_res_norm(x, xb2, w.norm[3], next, xb, H, eps, st));
+        if (fuse_geglu) {
+            MvIn in;
+            in.mode = kMvInGeglu;
+            in.up = up;
+            XP_STEP(launch_mv(&d, 1, gate, fmt, c.ffn, 0, mv_partial, mv_partial_cap,
+                              tickets + kTicketMv, 8192, st, "session down", n_cu, &in));
+        } else {
+            XP_STEP(xp_geglu(hb, gate, up, c.ffn, st));
+            XP_STEP(launch_mv(&d, 1, hb, fmt, c.ffn, 0, mv_partial, mv_partial_cap,
+                              tickets + kTicketMv, 8192, st, "session down", n_cu));
+        }
+        if (!fuse_norm) {
+            const float* next = (l + 1 < c.n_layers) ? L[l + 1].norm[0] : final_norm;
+            XP_STEP(launch_norm_res_norm(x, xb2, w.norm[3], next, xb, H, eps, st));
+        } else if (l + 1 == c.n_layers) {
+            // the final norm, into the other buffer (the lm_head's input)
+            XP_STEP(launch_norm_res_norm(xr, xb2, w.norm[3], final_norm, xo, H, eps, st));
+        }
     }
+    const float* lm_in = fuse_norm ? xo : xb;
     if (variant >= 1) {
         const MvMatDesc lm{logits, lm_w, lm_s, c.vocab};
-        XP_STEP(launch_mv(&lm, 1, xb, fmt, H, 0, mv_partial, mv_partial_cap, tickets + kTicketMv,
+        XP_STEP(launch_mv(&lm, 1, lm_in, fmt, H, 0, mv_partial, mv_partial_cap, tickets + kTicketMv,
                           8192, st, "session lm_head", n_cu));
         if (variant == 1)
             XP_STEP(launch_argmax(state + 1, am_out, logits, c.vocab, am_val, am_idx,

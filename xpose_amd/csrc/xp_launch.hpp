@@ -34,11 +34,34 @@ struct MvMatDesc {
 };
 // Partial floats a call with these shapes needs for a given split (0 = auto).
 size_t mv_partial_floats(uint32_t rows, uint32_t total_cols, uint32_t split, int n_cu);
+// An operation the column-slice matvec applies to its input while staging
+// it, so that the elementwise launch before the matvec is not needed (the
+// graph path's GeGLU and residual + RMSNorm):
+//   kMvInGeglu  the input is gelu_tanh(x) * up;
+//   kMvInNorm   x_new = x + rmsnorm(y) (1 + w_post); the input is
+//               rmsnorm(x_new) (1 + w_pre), with the scalar of that norm
+//               applied to the outputs (the staged block fixed point does
+//               not depend on a common scale); workgroup 0 writes x_new to
+//               x_out (which must not alias x, y or the outputs).
+enum : int { kMvInPlain = 0, kMvInGeglu = 1, kMvInNorm = 2 };
+struct MvIn {
+    int mode = kMvInPlain;
+    const float* up = nullptr;
+    const float* y = nullptr;
+    const float* w_post = nullptr;
+    const float* w_pre = nullptr;
+    float* x_out = nullptr;
+    float eps = 0.0f;
+};
+// Whether launch_mv takes the column-slice plan for these shapes (the only
+// plan that accepts an MvIn other than kMvInPlain).
+bool mv_slice_plan(uint32_t rows, uint32_t total_cols, int fmt, int n_cu);
 // With caller-provided partial and ticket buffers, n_cu is the CU count the
 // plan is made for (0: 256); without them the library's scratch is used.
 int launch_mv(const MvMatDesc* mats, uint32_t n, const float* x, int fmt, uint32_t rows,
               uint32_t split, float* partial, size_t partial_cap, uint32_t* tickets,
-              size_t tickets_cap, hipStream_t st, const char* who, int n_cu = 0);
+              size_t tickets_cap, hipStream_t st, const char* who, int n_cu = 0,
+              const MvIn* in = nullptr);
 // Set-up of the allocation-free matvec entry point on the current device:
 // the device address of its fixed scratch (partial sums, then tickets), its
 // tickets cleared once by a fill kernel on `st` (synchronised when `sync`).
