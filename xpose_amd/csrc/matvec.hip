@@ -456,10 +456,10 @@ __global__ __launch_bounds__(kMvWgWaves * kWave) void mv_int4_slice_kernel(MvArg
 #pragma unroll
         for (uint32_t k = 0; k < NX; ++k) {
             const uint32_t i = threadIdx.x + k * NT;
-            const float4 h0{gelu_tanh(xv[k][0].x) * uv[k][0].x, gelu_tanh(xv[k][0].y) * uv[k][0].y,
-                            gelu_tanh(xv[k][0].z) * uv[k][0].z, gelu_tanh(xv[k][0].w) * uv[k][0].w};
-            const float4 h1{gelu_tanh(xv[k][1].x) * uv[k][1].x, gelu_tanh(xv[k][1].y) * uv[k][1].y,
-                            gelu_tanh(xv[k][1].z) * uv[k][1].z, gelu_tanh(xv[k][1].w) * uv[k][1].w};
+            const float4 h0{gelu_hw(xv[k][0].x) * uv[k][0].x, gelu_hw(xv[k][0].y) * uv[k][0].y,
+                            gelu_hw(xv[k][0].z) * uv[k][0].z, gelu_hw(xv[k][0].w) * uv[k][0].w};
+            const float4 h1{gelu_hw(xv[k][1].x) * uv[k][1].x, gelu_hw(xv[k][1].y) * uv[k][1].y,
+                            gelu_hw(xv[k][1].z) * uv[k][1].z, gelu_hw(xv[k][1].w) * uv[k][1].w};
             if (i < ntask) stage_x8(qx, sx, i, h0, h1);
         }
     } else {

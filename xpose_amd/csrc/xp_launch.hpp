@@ -37,7 +37,8 @@ size_t mv_partial_floats(uint32_t rows, uint32_t total_cols, uint32_t split, int
 // An operation the column-slice matvec applies to its input while staging
 // it, so that the elementwise launch before the matvec is not needed (the
 // graph path's GeGLU and residual + RMSNorm):
-//   kMvInGeglu  the input is gelu_tanh(x) * up;
+//   kMvInGeglu  the input is gelu(x) * up (the tanh form on the hardware
+//               exponential and reciprocal, as the token kernel's tiles);
 //   kMvInNorm   x_new = x + rmsnorm(y) (1 + w_post); the input is
 //               rmsnorm(x_new) (1 + w_pre), with the scalar of that norm
 //               applied to the outputs (the staged block fixed point does
