@@ -361,15 +361,20 @@ __global__ __launch_bounds__(kMvWgWaves * kWave) void mv_int4_wg_kernel(MvArgs a
 constexpr uint32_t kMvSliceRounds = 8;
 constexpr uint32_t kMvSliceMaxBlk = 256;
 
-template <int FMT, int S, int R, int XM = kMvInPlain>
+// GO (GeGLU output; S = 2, two matrices of equal width, gate then up): lane
+// l takes column c of the gate (l < 32) or of the up matrix, both halves the
+// same block each step (one block a step), and the workgroup writes
+// gelu(gate) * up for its 32 columns into the first matrix's output.
+template <int FMT, int S, int R, int XM = kMvInPlain, bool GO = false>
 __global__ __launch_bounds__(kMvWgWaves * kWave) void mv_int4_slice_kernel(MvArgs a) {
     constexpr uint32_t CPS = kGrp / S;                                 // columns per slice
     static_assert(R >= 1 && R <= int(kMvSliceRounds), "steps per wave");
+    static_assert(!GO || S == 2, "the GeGLU output pairs two 32-column halves");
     extern __shared__ QxBlock smem_qx[];
     const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
     const uint32_t lane = threadIdx.x % kWave;
     const uint32_t gg = blockIdx.x / S, h = blockIdx.x % S;
-    const uint32_t nblk = a.nblk, nsteps = (nblk + S - 1) / S;
+    const uint32_t nblk = a.nblk, nsteps = GO ? nblk : (nblk + S - 1) / S;
     QxBlock* qx = smem_qx;
     float* sx = reinterpret_cast<float*>(smem_qx + nblk);
     float* red = sx + nblk;   // [kMvWgWaves][64]
@@ -388,9 +393,15 @@ __global__ __launch_bounds__(kMvWgWaves * kWave) void mv_int4_slice_kernel(MvArg
             out = a.m[i].out; wq = a.m[i].wq; sc = a.m[i].sc; cols = a.m[i].cols; grp0 = a.m[i].grp0;
         }
     }
-    const uint32_t gl = gg - grp0, c = h * CPS + lane % CPS, bs = lane / CPS;
+    if constexpr (GO) {
+        wq = lane < CPS ? a.m[0].wq : a.m[1].wq;
+        sc = lane < CPS ? a.m[0].sc : a.m[1].sc;
+    }
+    const uint32_t gl = gg - grp0, c = h * CPS + lane % CPS, bs = GO ? 0u : lane / CPS;
     const uint32_t j = gl * kGrp + c;
     const u32x4* wp = wq + size_t(gl) * nblk * kGrp + c;
+    // the block of step t for this lane (S blocks a step, or one with GO)
+    auto blk_of = [&](uint32_t t) { return GO ? t : t * S + bs; };
     // all of x, staging tasks (8 elements each) i and i + 512 of thread i
     // (the second only past 128 blocks), loaded ahead of the weights
     constexpr uint32_t NT = kMvWgWaves * kWave;
@@ -439,7 +450,7 @@ __global__ __launch_bounds__(kMvWgWaves * kWave) void mv_int4_slice_kernel(MvArg
     for (int r = 0; r < R; ++r) {
         // steps past the end load a valid block (clamped) and weigh it by zero
         const uint32_t t = min(wave + uint32_t(kMvWgWaves) * r, nsteps - 1u);
-        const uint32_t b = min(t * S + bs, nblk - 1u);
+        const uint32_t b = min(blk_of(t), nblk - 1u);
         w[r] = ld_stream4(wp + size_t(b) * kGrp);
         // the 32-bit word holding scale b % 4 of quad b / 4 of column j
         sw[r] = __builtin_nontemporal_load(sc32 + (size_t(b >> 2) * cols + j) * 2u +
@@ -514,7 +525,7 @@ __global__ __launch_bounds__(kMvWgWaves * kWave) void mv_int4_slice_kernel(MvArg
     float ws[R];
 #pragma unroll
     for (int r = 0; r < R; ++r) {
-        const uint32_t t = wave + uint32_t(kMvWgWaves) * r, b = t * S + bs;
+        const uint32_t t = wave + uint32_t(kMvWgWaves) * r, b = blk_of(t);
         const uint32_t bb = min(b, nblk - 1u);
         const uint32_t hb = (sw[r] >> (16u * (bb & 1u))) & 0xFFFFu;
         const float scale = FMT == XP_SCALE_F16_QUAD ? f16_bits_to_f32(hb) : __uint_as_float(hb << 16);
@@ -532,7 +543,7 @@ __global__ __launch_bounds__(kMvWgWaves * kWave) void mv_int4_slice_kernel(MvArg
 #pragma unroll
     for (int r = 0; r < R; ++r) {
         const uint32_t t = min(wave + uint32_t(kMvWgWaves) * r, nsteps - 1u);
-        const uint32_t bb = min(t * S + bs, nblk - 1u);
+        const uint32_t bb = min(blk_of(t), nblk - 1u);
         sxv[r] = sx[bb];
         aw[r] = reinterpret_cast<const u32x2*>(&qx[bb])[jw];
     }
@@ -569,19 +580,35 @@ __global__ __launch_bounds__(kMvWgWaves * kWave) void mv_int4_slice_kernel(MvArg
     }
     __syncthreads();
     if (wave != 0 || lane >= CPS) return;
-    float y = 0.0f;
-#pragma unroll
-    for (uint32_t v = 0; v < uint32_t(kMvWgWaves); ++v)
-#pragma unroll
-        for (uint32_t q = 0; q < uint32_t(S); ++q) y += red[v * kGrp + q * CPS + lane];
+    // the input norm's scalar rsqrt(mean x_new^2 + eps), applied here
+    float nsc = 1.0f;
     if constexpr (XM == kMvInNorm) {
-        // the input norm's scalar rsqrt(mean x_new^2 + eps), applied here
         float t2 = 0.0f;
 #pragma unroll
         for (uint32_t v = 0; v < uint32_t(kMvWgWaves); ++v) t2 += xs2[v];
-        y *= rsq_hw(t2 / float(nblk * kBlk) + a.in_eps);
+        nsc = rsq_hw(t2 / float(nblk * kBlk) + a.in_eps);
     }
-    out[j] = y;
+    if constexpr (GO) {
+        float g = 0.0f, u = 0.0f;
+#pragma unroll
+        for (uint32_t v = 0; v < uint32_t(kMvWgWaves); ++v) {
+            g += red[v * kGrp + lane];
+            u += red[v * kGrp + CPS + lane];
+        }
+        if constexpr (XM == kMvInNorm) {
+            g *= nsc;
+            u *= nsc;
+        }
+        out[j] = gelu_hw(g) * u;
+    } else {
+        float y = 0.0f;
+#pragma unroll
+        for (uint32_t v = 0; v < uint32_t(kMvWgWaves); ++v)
+#pragma unroll
+            for (uint32_t q = 0; q < uint32_t(S); ++q) y += red[v * kGrp + q * CPS + lane];
+        if constexpr (XM == kMvInNorm) y *= nsc;
+        out[j] = y;
+    }
 }
 
 __global__ void unpack_km4_kernel(int8_t* out, const u32x4* wq, uint32_t rows, uint32_t cols) {
@@ -656,6 +683,15 @@ bool mv_slice_plan(uint32_t rows, uint32_t total_cols, int fmt, int n_cu) {
     return slice_count(rows / kBlk, total_cols / kGrp, fmt, n_cu > 0 ? n_cu : 256) != 0;
 }
 
+bool mv_geglu_plan(uint32_t rows, uint32_t cols, int fmt, int n_cu) {
+    // two 32-column halves a group (the two-slice plan of one matrix's
+    // groups), one block a step: at most kMvSliceRounds steps a wave
+    if (rows == 0 || rows % (4u * kBlk) != 0 || cols % kGrp != 0) return false;
+    const uint32_t nblk = rows / kBlk;
+    return slice_count(nblk, cols / kGrp, fmt, n_cu > 0 ? n_cu : 256) == 2u &&
+           nblk <= kMvWgWaves * kMvSliceRounds;
+}
+
 int launch_mv(const MvMatDesc* mats, uint32_t n, const float* x, int fmt, uint32_t rows,
               uint32_t split, float* partial, size_t partial_cap, uint32_t* tickets,
               size_t tickets_cap, hipStream_t st, const char* who, int n_cu_hint, const MvIn* in) {
@@ -720,6 +756,13 @@ int launch_mv(const MvMatDesc* mats, uint32_t n, const float* x, int fmt, uint32
     // chunks as give every CU a task, at most eight, each within kMvWgChunk
     // quads. A caller-provided partial buffer too small for that plan keeps
     // the split-k plan it was sized for.
+    const bool go = in && in->geglu_out;
+    if (go && (xm == kMvInGeglu || n != 2 || mats[0].cols != mats[1].cols || split != 0 ||
+               !mv_geglu_plan(rows, mats[0].cols, fmt, n_cu)))
+        return set_error(XP_E_ARG, "%s: the GeGLU output takes a gate and an up matrix of equal width "
+                                   "within the column-slice plan", who);
+    if (go && in->x_out && in->x_out == mats[0].out)
+        return set_error(XP_E_ARG, "%s: the GeGLU output aliases the norm's x_out", who);
     if (xm != kMvInPlain && (split != 0 || slice_count(nblk, groups, fmt, n_cu) == 0))
         return set_error(XP_E_ARG, "%s: an input operation needs the column-slice plan", who);
     if (split == 0 && fmt != XP_SCALE_F32 && groups < uint32_t(n_cu) * 8u) {
@@ -727,7 +770,7 @@ int launch_mv(const MvMatDesc* mats, uint32_t n, const float* x, int fmt, uint32
         // back, 2.8 us launch floor): config 1 3.3 us (one workgroup per
         // group: 3.9), q 2.9 us, o 2.9 us (k-chunks with a last-arrival sum:
         // 5.7, 6.1).
-        const uint32_t S = slice_count(nblk, groups, fmt, n_cu);
+        const uint32_t S = go ? 2u : slice_count(nblk, groups, fmt, n_cu);
         if (S != 0) {
             a.split = 1;
             a.qpc = a.nquads;
@@ -740,25 +783,30 @@ int launch_mv(const MvMatDesc* mats, uint32_t n, const float* x, int fmt, uint32
             }
             const size_t lds = size_t(nblk) * (sizeof(QxBlock) + sizeof(float)) +
                                size_t(kMvWgWaves) * (kGrp + 1) * sizeof(float);
-            const dim3 grid(groups * S), block(kMvWgWaves * kWave);
-            // steps per wave, rounded up to 1, 2, 3, 4 or 8 (one instance
+            // GO: the gate's groups only, two workgroups each
+            const dim3 grid((go ? mats[0].cols / kGrp : groups) * S), block(kMvWgWaves * kWave);
+            // steps per wave, rounded up to 1, 2, 3, 4, 5 or 8 (one instance
             // each). A step past the end still loads (a clamped block, weighed
             // by zero): k = 1152 (18 steps) in 3 rounds instead of 4 loads 24
             // wave-blocks for 18 instead of 32, config 1 3.47 -> 3.31 us.
-            const uint32_t need = ((nblk + S - 1) / S + kMvWgWaves - 1) / kMvWgWaves;
-            const uint32_t R = need <= 1 ? 1 : need <= 2 ? 2 : need <= 3 ? 3 : need <= 4 ? 4 : 8;
-#define XP_MV_SLICE_R(F, SS, XX)                                                                          \
-    if (R == 1) hipLaunchKernelGGL((mv_int4_slice_kernel<F, SS, 1, XX>), grid, block, lds, st, a);       \
-    else if (R == 2) hipLaunchKernelGGL((mv_int4_slice_kernel<F, SS, 2, XX>), grid, block, lds, st, a);  \
-    else if (R == 3) hipLaunchKernelGGL((mv_int4_slice_kernel<F, SS, 3, XX>), grid, block, lds, st, a);  \
-    else if (R == 4) hipLaunchKernelGGL((mv_int4_slice_kernel<F, SS, 4, XX>), grid, block, lds, st, a);  \
-    else hipLaunchKernelGGL((mv_int4_slice_kernel<F, SS, 8, XX>), grid, block, lds, st, a);
-#define XP_MV_SLICE_X(F, SS)                                  \
-    if (xm == kMvInGeglu) { XP_MV_SLICE_R(F, SS, kMvInGeglu) } \
-    else if (xm == kMvInNorm) { XP_MV_SLICE_R(F, SS, kMvInNorm) } \
-    else { XP_MV_SLICE_R(F, SS, kMvInPlain) }
-#define XP_MV_SLICE_LAUNCH(F)                   \
-    if (S == 4) { XP_MV_SLICE_X(F, 4) }          \
+            const uint32_t steps = go ? nblk : (nblk + S - 1) / S;
+            const uint32_t need = (steps + kMvWgWaves - 1) / kMvWgWaves;
+            const uint32_t R = need <= 1 ? 1 : need <= 2 ? 2 : need <= 3 ? 3 : need <= 4 ? 4 : need <= 5 ? 5 : 8;
+#define XP_MV_SLICE_R(F, SS, XX, GG)                                                                          \
+    if (R == 1) hipLaunchKernelGGL((mv_int4_slice_kernel<F, SS, 1, XX, GG>), grid, block, lds, st, a);       \
+    else if (R == 2) hipLaunchKernelGGL((mv_int4_slice_kernel<F, SS, 2, XX, GG>), grid, block, lds, st, a);  \
+    else if (R == 3) hipLaunchKernelGGL((mv_int4_slice_kernel<F, SS, 3, XX, GG>), grid, block, lds, st, a);  \
+    else if (R == 4) hipLaunchKernelGGL((mv_int4_slice_kernel<F, SS, 4, XX, GG>), grid, block, lds, st, a);  \
+    else if (R == 5) hipLaunchKernelGGL((mv_int4_slice_kernel<F, SS, 5, XX, GG>), grid, block, lds, st, a);  \
+    else hipLaunchKernelGGL((mv_int4_slice_kernel<F, SS, 8, XX, GG>), grid, block, lds, st, a);
+#define XP_MV_SLICE_X(F, SS)                                         \
+    if (xm == kMvInGeglu) { XP_MV_SLICE_R(F, SS, kMvInGeglu, false) } \
+    else if (xm == kMvInNorm) { XP_MV_SLICE_R(F, SS, kMvInNorm, false) } \
+    else { XP_MV_SLICE_R(F, SS, kMvInPlain, false) }
+#define XP_MV_SLICE_LAUNCH(F)                                                    \
+    if (go && xm == kMvInNorm) { XP_MV_SLICE_R(F, 2, kMvInNorm, true) }          \
+    else if (go) { XP_MV_SLICE_R(F, 2, kMvInPlain, true) }                        \
+    else if (S == 4) { XP_MV_SLICE_X(F, 4) }                                      \
     else { XP_MV_SLICE_X(F, 2) }
             if (fmt == XP_SCALE_F16_QUAD) {
                 XP_MV_SLICE_LAUNCH(XP_SCALE_F16_QUAD)

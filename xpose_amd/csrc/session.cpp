@@ -229,7 +229,10 @@ int Session::record(int variant, uint32_t& n) {
     // writes the new residual to the other of two buffers, x and xb (xb is
     // free once layer 0's q|k|v has read its normed input).
     const bool fuse_norm = mv_slice_plan(H, qd + 2 * kvd, fmt, n_cu) && mv_slice_plan(H, 2 * c.ffn, fmt, n_cu);
-    const bool fuse_geglu = mv_slice_plan(c.ffn, H, fmt, n_cu);
+    // the GeGLU as the gate/up matvec's output (each workgroup pairs the
+    // same 32 columns of both), else staged by the down matvec
+    const bool geglu_out = fuse_norm && mv_geglu_plan(H, c.ffn, fmt, n_cu);
+    const bool fuse_geglu = !geglu_out && mv_slice_plan(c.ffn, H, fmt, n_cu);
     float* xr = x;                        // the residual stream
     float* xo = fuse_norm ? xb : nullptr;  // the other buffer (fused norms)
     for (uint32_t l = 0; l < c.n_layers; ++l) {
@@ -284,8 +287,11 @@ int Session::record(int variant, uint32_t& n) {
             in.w_pre = w.norm[2];
             in.x_out = xo;
             in.eps = eps;
-            XP_STEP(launch_mv(gu, 2, xr, fmt, H, 0, mv_partial, mv_partial_cap, tickets + kTicketMv,
-                              8192, st, "session gate/up", n_cu, &in));
+            in.geglu_out = geglu_out;
+            const MvMatDesc guh[2] = {{hb, w.w[XP_T_GATE], w.s[XP_T_GATE], c.ffn},
+                                      {up, w.w[XP_T_UP], w.s[XP_T_UP], c.ffn}};
+            XP_STEP(launch_mv(geglu_out ? guh : gu, 2, xr, fmt, H, 0, mv_partial, mv_partial_cap,
+                              tickets + kTicketMv, 8192, st, "session gate/up", n_cu, &in));
             std::swap(xr, xo);
         } else {
             XP_STEP(launch_norm_res_norm(x, xb2, w.norm[1], w.norm[2], xb, H, eps, st));
@@ -293,7 +299,10 @@ int Session::record(int variant, uint32_t& n) {
                               8192, st, "session gate/up", n_cu));
         }
         const MvMatDesc d{xb2, w.w[XP_T_DOWN], w.s[XP_T_DOWN], H};
-        if (fuse_geglu) {
+        if (geglu_out) {
+            XP_STEP(launch_mv(&d, 1, hb, fmt, c.ffn, 0, mv_partial, mv_partial_cap,
+                              tickets + kTicketMv, 8192, st, "session down", n_cu));
+        } else if (fuse_geglu) {
             MvIn in;
             in.mode = kMvInGeglu;
             in.up = up;

@@ -44,6 +44,10 @@ size_t mv_partial_floats(uint32_t rows, uint32_t total_cols, uint32_t split, int
 //               applied to the outputs (the staged block fixed point does
 //               not depend on a common scale); workgroup 0 writes x_new to
 //               x_out (which must not alias x, y or the outputs).
+// geglu_out (with kMvInPlain or kMvInNorm): the call's two matrices are a
+// gate and an up projection of equal width, and the output, into the first
+// matrix's `out`, is gelu(gate) * up (each workgroup takes the same 32
+// columns of both; the second matrix's `out` is not written).
 enum : int { kMvInPlain = 0, kMvInGeglu = 1, kMvInNorm = 2 };
 struct MvIn {
     int mode = kMvInPlain;
@@ -53,10 +57,13 @@ struct MvIn {
     const float* w_pre = nullptr;
     float* x_out = nullptr;
     float eps = 0.0f;
+    bool geglu_out = false;
 };
 // Whether launch_mv takes the column-slice plan for these shapes (the only
-// plan that accepts an MvIn other than kMvInPlain).
+// plan that accepts an MvIn other than kMvInPlain), and whether it can
+// produce a gate / up pair's GeGLU (geglu_out) for rows x cols matrices.
 bool mv_slice_plan(uint32_t rows, uint32_t total_cols, int fmt, int n_cu);
+bool mv_geglu_plan(uint32_t rows, uint32_t cols, int fmt, int n_cu);
 // With caller-provided partial and ticket buffers, n_cu is the CU count the
 // plan is made for (0: 256); without them the library's scratch is used.
 int launch_mv(const MvMatDesc* mats, uint32_t n, const float* x, int fmt, uint32_t rows,
