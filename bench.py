@@ -37,7 +37,9 @@ baseline's timed work; the matvec and attention legs' outputs filled with
 (and the timed launches' last output the same); config 3's 128 greedy ids
 against the oracle's generation from the same prompt; config 5's 16
 sequences' logits of the first batched step; the native matvecs on 2048
-sampled rows against the oracle's dequantiser. `step_ms` is the per-step
+sampled rows against the oracle's dequantiser; the graph path's logits at
+ctx against the oracle's and its 36 greedy ids against the oracle's stream
+(as far as that is computed) and the token kernel's. `step_ms` is the per-step
 distribution (min / median / mean / max of each step's device time,
 decode.cpp:2961-2972) over as many steps as the timed run, continuing its
 stream.
@@ -297,27 +299,34 @@ def same_size_ceiling(X, nbytes: int, copies: int = 64, iters: int = 640):
     return ceil_us, floor_us
 
 
-def graph_leg(X, ctx: int, steps: int = 32):
-    """The same decode on the captured-graph path (per-op kernels), tok/s."""
+def graph_leg(X, ctx: int, emb=None, steps: int = 32):
+    """The same decode on the captured-graph path (per-op kernels), tok/s;
+    with the headline's model (its embedding rows `emb`) also the logits at
+    ctx and the greedy ids, which the caller checks against the oracle and
+    the token kernel's stream."""
     cfg = X.XpConfig.gemma3_1b(max_seq=8192, exec_mode=X.XP_EXEC_GRAPH)
     sess = X.DecodeSession(cfg)
     sess.synthesize(SEED)
+    if emb is not None:
+        sess.upload(-1, X.T_EMBED, emb)
     kvd = cfg.n_kv_heads * cfg.head_dim
     for l in range(cfg.n_layers):
         sess.kv_upload(l, 0, 0, X.synth_normal_f16(ctx * kvd, ctx, 2 * l))
         sess.kv_upload(l, 1, 0, X.synth_normal_f16(ctx * kvd, ctx, 2 * l + 1))
     sess.set_position(ctx)
     sess.prefill([4242])
-    sess.decode_steps(4)
+    logits = sess.last_logits()
+    warm = sess.decode_steps(4)
     X.synchronize()
     t0 = time.perf_counter()
-    sess.decode_steps(steps)
+    ids = sess.decode_steps(steps)
     X.synchronize()
     el = time.perf_counter() - t0
     launches = sess.last_metrics().launches
     sess.close()
-    return {"tok_s": round(steps / el, 1), "ms_per_step": round(el * 1e3 / steps, 4),
-            "launches_per_step": launches}
+    out = {"tok_s": round(steps / el, 1), "ms_per_step": round(el * 1e3 / steps, 4),
+           "launches_per_step": launches}
+    return out, logits, [int(v) for v in warm] + [int(v) for v in ids]
 
 
 def attention_leg(X, span: int, iters: int = 192):
@@ -604,7 +613,7 @@ def main() -> int:
         print(json.dumps({"attention": [attention_leg(X, sp) for sp in (4096, 8192)]}), flush=True)
         return 0
     if args.only == "graph":
-        print(json.dumps({"graph_path": graph_leg(X, args.ctx)}), flush=True)
+        print(json.dumps({"graph_path": graph_leg(X, args.ctx)[0]}), flush=True)
         return 0
     if args.only == "cfg5":
         scfg = X.XpConfig.gemma3_1b(max_seq=8192, sample_mode=1, temperature=0.8, top_k=64,
@@ -689,7 +698,7 @@ def main() -> int:
         progress("cfg5")
         extra["native"] = native_leg(X)
         progress("native")
-        extra["graph_path"] = graph_leg(X, ctx)
+        extra["graph_path"], graph_logits, graph_ids = graph_leg(X, ctx, emb)
         progress("graph path")
     sess.close()
 
@@ -731,6 +740,16 @@ def main() -> int:
         gates["cfg5"] = extra["cfg5"]["parity"]["ok"]
         gates["attention"] = all(a["parity"]["ok"] for a in extra["attention"])
         gates["native"] = all(n["parity"]["ok"] for n in extra["native"])
+        # the graph path on the same model, position and token: its logits
+        # against the oracle's, its greedy ids against the oracle's and the
+        # token kernel's stream
+        g_lg = parity(graph_logits, lg0, 1e-3)
+        kg = min(len(o_ids), len(graph_ids))
+        kt = min(len(gpu_stream), len(graph_ids))
+        g_ok = bool(g_lg["ok"] and graph_ids[:kg] == o_ids[:kg] and graph_ids[:kt] == gpu_stream[:kt])
+        extra["graph_path"]["parity"] = {"ok": g_ok, "logits_rel_err": g_lg["rel_err"], "logits_tol": 1e-3,
+                                         "ids_vs_oracle": kg, "ids_vs_token_kernel": kt}
+        gates["graph_path"] = g_ok
 
     line = {
         "metric": "decode tok/s Gemma-3-1B int4 bs=1 @ctx 4096; int4 matvec HBM GB/s vs peak",
