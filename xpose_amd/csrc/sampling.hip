@@ -25,6 +25,7 @@ struct AmArgs {
     float* pval;            // [gridDim.x]
     uint32_t* pidx;
     uint32_t* ticket;
+    uint32_t* advance;      // when set, the last workgroup adds 1 here (a session's position)
 };
 
 __global__ __launch_bounds__(kAmThreads) void argmax_kernel(AmArgs a) {
@@ -71,6 +72,7 @@ __global__ __launch_bounds__(kAmThreads) void argmax_kernel(AmArgs a) {
         for (int w = 1; w < kAmThreads / kWave; ++w) am_better(bv, bi, sv[w], si[w]);
         *a.out_idx = bi;
         if (a.out_val) *a.out_val = bv;
+        if (a.advance) *a.advance += 1u;
         st_dev(a.ticket, 0u);
     }
 }
@@ -127,8 +129,8 @@ __global__ __launch_bounds__(256) void topk4_kernel(float* cval, uint32_t* cidx,
 
 // Shared with the decode session, which owns its own partial/ticket buffers.
 int launch_argmax(uint32_t* out_idx, float* out_val, const float* logits, uint32_t n,
-                  float* pval, uint32_t* pidx, uint32_t* ticket, hipStream_t st) {
-    AmArgs a{out_idx, out_val, logits, n, 0, pval, pidx, ticket};
+                  float* pval, uint32_t* pidx, uint32_t* ticket, hipStream_t st, uint32_t* advance) {
+    AmArgs a{out_idx, out_val, logits, n, 0, pval, pidx, ticket, advance};
     uint32_t nwg = (n + 4095) / 4096;
     if (nwg > uint32_t(kAmMaxWg)) nwg = kAmMaxWg;
     if (nwg < 1) nwg = 1;

@@ -31,6 +31,9 @@ int launch_embed(float* x, const void* wq, const void* sc, int fmt, uint32_t hid
                  const float* table, hipStream_t st);
 int launch_norm_res_norm(float* x, const float* y, const float* w_post, const float* w_pre,
                          float* out, uint32_t n, float eps, hipStream_t st);
+int launch_embed_norm(float* x, float* xn, const float* w_pre, float eps, const void* wq, const void* sc,
+                      int fmt, uint32_t hidden, uint32_t vocab, float embed_scale, const uint32_t* state,
+                      uint32_t* hist, const float* table, hipStream_t st);
 int launch_advance(uint32_t* state, hipStream_t st);
 uint16_t f32_to_f16(float f);
 
@@ -220,8 +223,9 @@ int Session::record(int variant, uint32_t& n) {
         if ((rc = (call)) != XP_OK) return rc; \
         ++n;                         \
     } while (0)
-    XP_STEP(launch_embed(x, lm_w, lm_s, fmt, H, c.vocab, embed_scale(), state, hist, embed, st));
-    XP_STEP(launch_norm_res_norm(x, nullptr, nullptr, L[0].norm[0], xb, H, eps, st));
+    // the embedding row and the first input norm (one launch)
+    XP_STEP(launch_embed_norm(x, xb, L[0].norm[0], eps, lm_w, lm_s, fmt, H, c.vocab, embed_scale(), state,
+                              hist, embed, st));
     // Where the column-slice matvec takes the shape, the residual add and
     // the two RMSNorms before the q|k|v and gate/up matvecs, and the GeGLU
     // before the down matvec, run inside those matvecs' staging instead of
@@ -326,13 +330,13 @@ int Session::record(int variant, uint32_t& n) {
         const MvMatDesc lm{logits, lm_w, lm_s, c.vocab};
         XP_STEP(launch_mv(&lm, 1, lm_in, fmt, H, 0, mv_partial, mv_partial_cap, tickets + kTicketMv,
                           8192, st, "session lm_head", n_cu));
-        if (variant == 1)
+        if (variant == 1)   // the greedy argmax also advances the position
             XP_STEP(launch_argmax(state + 1, am_out, logits, c.vocab, am_val, am_idx,
-                                  tickets + kTicketAm, st));
+                                  tickets + kTicketAm, st, state));
         else
             XP_STEP(launch_topk4(cand_val, cand_idx, logits, c.vocab, c.topk_parts, st));
     }
-    XP_STEP(launch_advance(state, st));
+    if (variant != 1) XP_STEP(launch_advance(state, st));
 #undef XP_STEP
     return XP_OK;
 }

@@ -9,7 +9,10 @@
 //                   w_pre): the post-sublayer norm, the residual add and the
 //                   next sublayer's pre-norm of record_token
 //                   (decode.cpp:1739-1751, 1668) in one workgroup.
-//  advance          position += 1 after a step.
+//  embed_norm       the embedding row and the first layer's input norm in
+//                   one launch (the graph path).
+//  advance          position += 1 after a step (the greedy step's argmax
+//                   does it itself).
 #include "xp_device.hpp"
 #include "xp_launch.hpp"
 
@@ -27,20 +30,12 @@ __device__ __forceinline__ float blk_sum(float v, float* red) {
     return t;
 }
 
-// state[0] = position, state[1] = token to run.
-__global__ void embed_kernel(float* x, const u32x4* wq, const void* sc, int fmt,
-                             uint32_t hidden, uint32_t vocab, float embed_scale,
-                             const uint32_t* state, uint32_t* hist, const float* table) {
-    const uint32_t pos = state[0];
-    uint32_t tok = state[1];
-    if (tok >= vocab) tok = 0;   // the host validates ids; never read out of bounds
-    const uint32_t k = blockIdx.x * blockDim.x + threadIdx.x;
-    if (k == 0) hist[pos] = tok;
-    if (k >= hidden) return;
-    if (table) {   // the model's own fp32 embedding rows
-        x[k] = table[size_t(tok) * hidden + k] * embed_scale;
-        return;
-    }
+// Element k of token tok's embedding row: the model's fp32 row when it has
+// one, else the tied int4 table's column, dequantised; times embed_scale.
+__device__ __forceinline__ float embed_value(uint32_t k, uint32_t tok, const u32x4* wq, const void* sc,
+                                             int fmt, uint32_t hidden, uint32_t vocab, float embed_scale,
+                                             const float* table) {
+    if (table) return table[size_t(tok) * hidden + k] * embed_scale;
     const uint32_t nblk = hidden / kBlk, b = k / kBlk;
     const u32x4 w = wq[(size_t(tok / kGrp) * nblk + b) * kGrp + (tok % kGrp)];
     const uint32_t t = k % kBlk;
@@ -54,7 +49,49 @@ __global__ void embed_kernel(float* x, const u32x4* wq, const void* sc, int fmt,
                                                                  (b % 4)];
         s = (fmt == XP_SCALE_F16_QUAD) ? f16_bits_to_f32(h) : __uint_as_float(uint32_t(h) << 16);
     }
-    x[k] = (q * s) * embed_scale;
+    return (q * s) * embed_scale;
+}
+
+// state[0] = position, state[1] = token to run.
+__global__ void embed_kernel(float* x, const u32x4* wq, const void* sc, int fmt,
+                             uint32_t hidden, uint32_t vocab, float embed_scale,
+                             const uint32_t* state, uint32_t* hist, const float* table) {
+    const uint32_t pos = state[0];
+    uint32_t tok = state[1];
+    if (tok >= vocab) tok = 0;   // the host validates ids; never read out of bounds
+    const uint32_t k = blockIdx.x * blockDim.x + threadIdx.x;
+    if (k == 0) hist[pos] = tok;
+    if (k >= hidden) return;
+    x[k] = embed_value(k, tok, wq, sc, fmt, hidden, vocab, embed_scale, table);
+}
+
+// The embedding row and the first layer's input norm in one workgroup:
+// x = the row, xn = rmsnorm(x) (1 + w_pre), the sums in norm_res_norm's order
+// (the same bits as embed_kernel followed by norm_res_norm without y).
+__global__ __launch_bounds__(1024) void embed_norm_kernel(float* x, float* xn, const float* w_pre, float eps,
+                                                          const u32x4* wq, const void* sc, int fmt,
+                                                          uint32_t hidden, uint32_t vocab, float embed_scale,
+                                                          const uint32_t* state, uint32_t* hist,
+                                                          const float* table) {
+    __shared__ float red[16];
+    constexpr int kMaxPer = 8;   // hidden <= 8 * 1024
+    const uint32_t pos = state[0];
+    uint32_t tok = state[1];
+    if (tok >= vocab) tok = 0;
+    if (threadIdx.x == 0) hist[pos] = tok;
+    float xv[kMaxPer];
+    int c = 0;
+    for (uint32_t i = threadIdx.x; i < hidden; i += blockDim.x, ++c) {
+        xv[c] = embed_value(i, tok, wq, sc, fmt, hidden, vocab, embed_scale, table);
+        x[i] = xv[c];
+    }
+    float ss = 0.0f;
+    for (int j = 0; j < c; ++j) ss += xv[j] * xv[j];
+    ss = blk_sum(ss, red);
+    const float scale = rsq_hw(ss / float(hidden) + eps);
+    c = 0;
+    for (uint32_t i = threadIdx.x; i < hidden; i += blockDim.x, ++c)
+        xn[i] = xv[c] * scale * (1.0f + w_pre[i]);
 }
 
 // y == nullptr: out = rmsnorm(x) * (1 + w_pre) only.
@@ -98,6 +135,18 @@ int launch_embed(float* x, const void* wq, const void* sc, int fmt, uint32_t hid
                        state, hist, table);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return set_error(XP_E_HIP, "embed: launch -> %s", hipGetErrorString(e));
+    return XP_OK;
+}
+
+int launch_embed_norm(float* x, float* xn, const float* w_pre, float eps, const void* wq, const void* sc,
+                      int fmt, uint32_t hidden, uint32_t vocab, float embed_scale, const uint32_t* state,
+                      uint32_t* hist, const float* table, hipStream_t st) {
+    if (hidden > 8 * 1024) return set_error(XP_E_ARG, "embed_norm: hidden=%u > 8192", hidden);
+    hipLaunchKernelGGL(embed_norm_kernel, dim3(1), dim3(1024), 0, st, x, xn, w_pre, eps,
+                       reinterpret_cast<const u32x4*>(wq), sc, fmt, hidden, vocab, embed_scale, state, hist,
+                       table);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return set_error(XP_E_HIP, "embed_norm: launch -> %s", hipGetErrorString(e));
     return XP_OK;
 }
 

@@ -180,8 +180,11 @@ int plan_attention(AttnArgs& a, uint32_t max_span, bool allow_xchg, int* U_out, 
 
 // ---- sampling ----
 constexpr int kAmMaxWg = 256;
+// advance: when set, the launch also adds 1 to *advance once its result is
+// written (the session's position, saving the step a launch of its own).
 int launch_argmax(uint32_t* out_idx, float* out_val, const float* logits, uint32_t n,
-                  float* pval, uint32_t* pidx, uint32_t* ticket, hipStream_t st);
+                  float* pval, uint32_t* pidx, uint32_t* ticket, hipStream_t st,
+                  uint32_t* advance = nullptr);
 int launch_topk4(float* cval, uint32_t* cidx, const float* x, uint32_t n, uint32_t nparts,
                  hipStream_t st, uint32_t rows = 1);
 // The best k (<= 64) of each of `rows` candidate lists (row r at cval / cidx +
