@@ -131,6 +131,18 @@ int xp_mv_int4_timed(float* out, const float* in, const void* const* wqs,
                      uint32_t rows, uint32_t cols, uint32_t split, uint32_t iters,
                      xp_stream stream, float* ms);
 
+/* Measurement as the reference's matvec bench takes it (one batch of `count`
+ * dispatches recorded into one submission, best of R:
+ * examples/llm/matvec_bench.cpp:326-353): `count` xp_mv_int4 launches
+ * cycling through `ncopies` weight/scale planes are captured into one HIP
+ * graph, which is replayed once untimed and then `reps` times on `stream`,
+ * each replay between two events; *best_ms = the fastest replay (divide by
+ * `count` for one launch). */
+int xp_mv_int4_batch_timed(float* out, const float* in, const void* const* wqs,
+                           const void* const* scales, uint32_t ncopies, int scale_fmt,
+                           uint32_t rows, uint32_t cols, uint32_t split, uint32_t count,
+                           uint32_t reps, xp_stream stream, float* best_ms);
+
 /* Debug/unpack entry: expands a KM4 nibble plane to int8 weights w[k*cols+j]
  * = nibble - 8 (row-major [rows][cols]), for bit-exact unpack checks. */
 int xp_unpack_km4(int8_t* out, const void* wq, uint32_t rows, uint32_t cols,
@@ -154,6 +166,11 @@ int xp_stream_read_timed(const void* buf, size_t bytes, uint32_t iters, xp_strea
  * buffers together exceed the 256 MiB Infinity Cache. */
 int xp_stream_read_rot_timed(const void* const* bufs, uint32_t nbufs, size_t bytes, uint32_t grid,
                              uint32_t iters, xp_stream stream, float* ms);
+/* The same read in the batch form of xp_mv_int4_batch_timed: `count`
+ * launches (launch i reads buffer i % nbufs) captured into one HIP graph,
+ * best of `reps` replays. */
+int xp_stream_read_rot_batch_timed(const void* const* bufs, uint32_t nbufs, size_t bytes, uint32_t grid,
+                                   uint32_t count, uint32_t reps, xp_stream stream, float* best_ms);
 int xp_copy(void* dst, const void* src, size_t bytes, xp_stream stream);
 /* Exchange-latency probe (no reference counterpart: it measures the
  * cross-workgroup hand-off the persistent token kernel is built on, alone).

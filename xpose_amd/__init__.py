@@ -146,9 +146,12 @@ def _declare(lib: C.CDLL) -> None:
         "xp_unpack_km4": (i32, [vp, vp, u32, u32, vp]),
         "xp_mv_int4_timed": (i32, [vp, vp, P(vp), P(vp), u32, i32, u32, u32, u32, u32, vp,
                                    P(f32)]),
+        "xp_mv_int4_batch_timed": (i32, [vp, vp, P(vp), P(vp), u32, i32, u32, u32, u32, u32, u32,
+                                         vp, P(f32)]),
         "xp_fp16_decode": (i32, [vp, vp, u32, vp]),
         "xp_stream_read_timed": (i32, [vp, sz, u32, vp, P(f32)]),
         "xp_stream_read_rot_timed": (i32, [P(vp), u32, sz, u32, u32, vp, P(f32)]),
+        "xp_stream_read_rot_batch_timed": (i32, [P(vp), u32, sz, u32, u32, u32, vp, P(f32)]),
         "xp_exchange_chain_timed": (i32, [u32, u32, u32, i32, vp, P(f32)]),
         "xp_handoff_pingpong_timed": (i32, [u32, u32, i32, u32, vp, P(f32), P(u32)]),
         "xp_load_latency": (i32, [u32, u32, i32, vp, P(f32)]),

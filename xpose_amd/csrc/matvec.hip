@@ -1021,6 +1021,30 @@ int xp_mv_int4_timed(float* out, const float* in, const void* const* wqs,
     return rc;
 }
 
+int xp_mv_int4_batch_timed(float* out, const float* in, const void* const* wqs,
+                           const void* const* scales, uint32_t ncopies, int scale_fmt, uint32_t rows,
+                           uint32_t cols, uint32_t split, uint32_t count, uint32_t reps,
+                           xp_stream stream, float* best_ms) {
+    XP_REQUIRE(wqs && scales && best_ms && ncopies > 0 && count > 0 && reps > 0, "bad arguments");
+    hipStream_t st = as_stream(stream);
+    int rc = XP_OK;
+    // One untimed pass over every copy: any scratch is sized before the capture.
+    for (uint32_t i = 0; i < ncopies && rc == XP_OK; ++i)
+        rc = xp_mv_int4(out, in, wqs[i], scales[i], scale_fmt, rows, cols, split, stream);
+    if (rc != XP_OK) return rc;
+    XP_HIP(hipStreamSynchronize(st));
+    return graph_batch_timed(
+        [&](hipStream_t cs) {
+            for (uint32_t i = 0; i < count; ++i) {
+                const int r = xp_mv_int4(out, in, wqs[i % ncopies], scales[i % ncopies], scale_fmt, rows,
+                                         cols, split, reinterpret_cast<xp_stream>(cs));
+                if (r != XP_OK) return r;
+            }
+            return int(XP_OK);
+        },
+        reps, st, best_ms);
+}
+
 int xp_unpack_km4(int8_t* out, const void* wq, uint32_t rows, uint32_t cols, xp_stream stream) {
     XP_REQUIRE(out && wq, "null pointer");
     XP_REQUIRE(rows > 0 && rows % kBlk == 0, "rows=%u must be a positive multiple of 32", rows);

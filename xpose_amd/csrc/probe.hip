@@ -315,6 +315,33 @@ int xp_stream_read_rot_timed(const void* const* bufs, uint32_t nbufs, size_t byt
     return rc;
 }
 
+int xp_stream_read_rot_batch_timed(const void* const* bufs, uint32_t nbufs, size_t bytes, uint32_t grid,
+                                   uint32_t count, uint32_t reps, xp_stream stream, float* best_ms) {
+    XP_REQUIRE(bufs && best_ms && nbufs > 0, "null pointer or no buffers");
+    XP_REQUIRE(bytes >= 16 && bytes % 16 == 0, "bytes=%zu must be a positive multiple of 16",
+               bytes);
+    for (uint32_t i = 0; i < nbufs; ++i)
+        XP_REQUIRE(bufs[i] && (reinterpret_cast<uintptr_t>(bufs[i]) & 15u) == 0,
+                   "buffer %u is null or not 16-byte aligned", i);
+    XP_REQUIRE(count > 0 && reps > 0, "count and reps must be positive");
+    XP_REQUIRE(grid <= 65536, "grid=%u > 65536", grid);
+    DeviceScratch* sc = scratch();
+    if (!sc) return XP_E_HIP;
+    if (!ensure_partial(sc, 4)) return XP_E_NOMEM;
+    uint32_t* sink = reinterpret_cast<uint32_t*>(sc->partial);   // never written in practice
+    const uint32_t g = grid ? grid : n_cu();
+    return graph_batch_timed(
+        [&](hipStream_t cs) {
+            for (uint32_t i = 0; i < count; ++i)
+                hipLaunchKernelGGL(stream_read_kernel, dim3(g), dim3(kStreamThreads), 0, cs, sink,
+                                   static_cast<const u32x4*>(bufs[i % nbufs]), bytes / 16);
+            if (hipGetLastError() != hipSuccess)
+                return set_error(XP_E_HIP, "xp_stream_read_rot_batch_timed: launch failed");
+            return int(XP_OK);
+        },
+        reps, as_stream(stream), best_ms);
+}
+
 int xp_exchange_chain_timed(uint32_t producers, uint32_t stages, uint32_t stride, int l2_local,
                             xp_stream stream, float* ns_per_stage) {
     XP_REQUIRE(ns_per_stage, "null pointer");

@@ -7,6 +7,7 @@
 
 #include <cstdio>
 #include <cstring>
+#include <functional>
 #include <mutex>
 #include <vector>
 
@@ -117,6 +118,50 @@ bool ensure_attn_x(DeviceScratch* s, size_t floats, size_t words) {
     s->attn_x_floats = floats;
     s->attn_state_words = words;
     return true;
+}
+
+int graph_batch_timed(const std::function<int(hipStream_t)>& record, uint32_t reps, hipStream_t replay,
+                      float* best_ms) {
+    hipStream_t cap = nullptr;
+    XP_HIP(hipStreamCreateWithFlags(&cap, hipStreamNonBlocking));
+    hipGraph_t g = nullptr;
+    hipGraphExec_t ge = nullptr;
+    hipEvent_t e0 = nullptr, e1 = nullptr;
+    int rc = XP_OK;
+    if (hipStreamBeginCapture(cap, hipStreamCaptureModeThreadLocal) != hipSuccess) {
+        rc = set_error(XP_E_HIP, "graph_batch_timed: hipStreamBeginCapture failed");
+    } else {
+        rc = record(cap);
+        const hipError_t ee = hipStreamEndCapture(cap, &g);
+        if (rc == XP_OK && ee != hipSuccess)
+            rc = set_error(XP_E_HIP, "graph_batch_timed: hipStreamEndCapture -> %s", hipGetErrorString(ee));
+    }
+    if (rc == XP_OK && hipGraphInstantiate(&ge, g, nullptr, nullptr, 0) != hipSuccess)
+        rc = set_error(XP_E_HIP, "graph_batch_timed: hipGraphInstantiate failed");
+    if (rc == XP_OK && (hipEventCreate(&e0) != hipSuccess || hipEventCreate(&e1) != hipSuccess))
+        rc = set_error(XP_E_HIP, "graph_batch_timed: hipEventCreate failed");
+    // one untimed replay, then `reps` replays each between two events
+    if (rc == XP_OK && hipGraphLaunch(ge, replay) != hipSuccess)
+        rc = set_error(XP_E_HIP, "graph_batch_timed: hipGraphLaunch failed");
+    if (rc == XP_OK && hipStreamSynchronize(replay) != hipSuccess)
+        rc = set_error(XP_E_HIP, "graph_batch_timed: sync failed");
+    float best = 1e30f;
+    for (uint32_t r = 0; r < reps && rc == XP_OK; ++r) {
+        float ms = 0.0f;
+        if (hipEventRecord(e0, replay) != hipSuccess || hipGraphLaunch(ge, replay) != hipSuccess ||
+            hipEventRecord(e1, replay) != hipSuccess || hipEventSynchronize(e1) != hipSuccess ||
+            hipEventElapsedTime(&ms, e0, e1) != hipSuccess)
+            rc = set_error(XP_E_HIP, "graph_batch_timed: replay %u failed", r);
+        else if (ms < best)
+            best = ms;
+    }
+    if (rc == XP_OK) *best_ms = best;
+    if (e0) (void)hipEventDestroy(e0);
+    if (e1) (void)hipEventDestroy(e1);
+    if (ge) (void)hipGraphExecDestroy(ge);
+    if (g) (void)hipGraphDestroy(g);
+    (void)hipStreamDestroy(cap);
+    return rc;
 }
 
 }  // namespace xp

@@ -9,6 +9,7 @@
 #include <cstdarg>
 #include <cstddef>
 #include <cstdint>
+#include <functional>
 #include <string>
 
 #include "../../include/xpose.h"
@@ -46,6 +47,14 @@ bool ensure_tickets(DeviceScratch* s, size_t n);
 bool ensure_attn_x(DeviceScratch* s, size_t floats, size_t words);
 
 inline hipStream_t as_stream(xp_stream s) { return reinterpret_cast<hipStream_t>(s); }
+
+// Measurement in the form of a decode step's submission: `record` enqueues a
+// batch of launches on the stream it is given, which is captured into one
+// HIP graph; the graph is replayed once untimed and then `reps` times on
+// `replay`, each replay between two events. *best_ms = the fastest replay.
+// `record` must not allocate, synchronise or enqueue memsets.
+int graph_batch_timed(const std::function<int(hipStream_t)>& record, uint32_t reps, hipStream_t replay,
+                      float* best_ms);
 
 }  // namespace xp
 
