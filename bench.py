@@ -62,7 +62,7 @@ HBM_PEAK_GBS = 8000.0          # MI355X HBM3E
 # Measured HBM bytes of one token-kernel launch at this workload: rocprofv3
 # FETCH_SIZE x 2.0 + WRITE_SIZE x 1.0 (factors from a 256 MiB copy), see
 # profiles/token_kernel_gemma3_1b_ctx4096.md.
-TOKEN_TRAFFIC_BYTES = 655_485_460 + 8_959_549
+TOKEN_TRAFFIC_BYTES = 655_360_224 + 8_956_970
 TRAFFIC_SOURCE = ("rocprofv3 --pmc FETCH_SIZE and --pmc WRITE_SIZE of this bench's token step "
                   "(profiles/token_kernel_gemma3_1b_ctx4096.md), scaled by a 256 MiB copy's "
                   "readings; a constant of this build, not counted in this run")
