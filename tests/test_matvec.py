@@ -260,3 +260,40 @@ def test_gpu_matvec_multi_matches_oracle(xp, xo, cols):
         want = xo.mv_km4(x, mats[i][0], mats[i][1], rows, c, 0)
         assert not (got == np.float32(-1e30)).any(), i
         assert np.abs(got - want).max() / np.abs(want).max() < 1e-5, i
+
+
+@pytest.mark.gpu
+def test_gpu_matvec_batch_timed_leaves_the_product(xp, xo):
+    """xp_mv_int4_batch_timed (launches captured into one HIP graph, best of
+    the replays) computes what xp_mv_int4 computes, bit for bit, on every
+    replay: after 4 copies x 3 replays the output equals a single launch's,
+    and the reported time is positive; the same-size read in the batch form
+    reports a positive time too."""
+    import ctypes as C
+    rows, cols, copies = 1152, 6912, 4
+    print(f"case matvec batch timed {rows}x{cols} x{copies}", flush=True)
+    wq, sc, x = synth_case(xp, rows, cols, seed=21)
+    want = run_mv(xp, wq, sc, x, rows, cols, 0)
+    dws = [xp.DeviceBuffer.from_array(wq) for _ in range(copies)]
+    dss = [xp.DeviceBuffer.from_array(sc) for _ in range(copies)]
+    dx = xp.DeviceBuffer.from_array(x)
+    dout = xp.DeviceBuffer(cols * 4)
+    dout.upload(np.full(cols, -1e30, np.float32))
+    W = (C.c_void_p * copies)(*[d.ptr for d in dws])
+    S = (C.c_void_p * copies)(*[d.ptr for d in dss])
+    ms = C.c_float()
+    xp.call("xp_mv_int4_batch_timed", dout.vp, dx.vp, W, S, copies, 0, rows, cols, 0, copies, 3, None,
+            C.byref(ms))
+    xp.synchronize()
+    got = dout.download(np.float32)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    assert ms.value > 0.0
+    ref = xo.mv_km4(x, wq, sc, rows, cols, 0)
+    assert np.abs(got - ref).max() / np.abs(ref).max() < 1e-5
+    nb = 1 << 20
+    bufs = [xp.DeviceBuffer(nb) for _ in range(2)]
+    for b in bufs:
+        xp.call("xp_memset", b.vp, 1, nb)
+    P = (C.c_void_p * 2)(*[b.ptr for b in bufs])
+    xp.call("xp_stream_read_rot_batch_timed", P, 2, nb, 0, 4, 3, None, C.byref(ms))
+    assert ms.value > 0.0
