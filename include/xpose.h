@@ -540,7 +540,7 @@ int xp_batch_create(const xp_session* weights, uint32_t n_seq, uint32_t max_seq,
  * persistent kernel (one 512-thread workgroup per CU walking the stages,
  * per-tile flags between them; creation fails if the shape or the device's
  * free CUs do not allow it). EXPERIMENTAL: both give bit-identical results,
- * but the graph is the faster (1.41 vs 1.93 ms a config-5 step, measured:
+ * but the graph is the faster (1.2 vs 1.8 ms a config-5 step, measured:
  * each stage's flag hand-off costs 1.3-3.6 us where a kernel boundary inside
  * the graph costs next to nothing), so AUTO takes the graph; the persistent
  * kernel is kept as a measured alternative and for its stage timeline.

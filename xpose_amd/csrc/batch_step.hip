@@ -1,5 +1,5 @@
 // EXPERIMENTAL (opt-in XP_EXEC_TOKEN; XP_EXEC_AUTO takes the graph, which
-// measures faster: 1.41 vs 1.93 ms a config-5 step).
+// measures faster: 1.2 vs 1.8 ms a config-5 step).
 //
 // The batched decode step (up to 16 sequences) as ONE
 // persistent kernel on gfx950: every layer's q|k|v GEMM, attention (with
