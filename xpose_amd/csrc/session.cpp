@@ -26,9 +26,6 @@
 
 namespace xp {
 
-int launch_embed(float* x, const void* wq, const void* sc, int fmt, uint32_t hidden,
-                 uint32_t vocab, float embed_scale, const uint32_t* state, uint32_t* hist,
-                 const float* table, hipStream_t st);
 int launch_norm_res_norm(float* x, const float* y, const float* w_post, const float* w_pre,
                          float* out, uint32_t n, float eps, hipStream_t st);
 int launch_embed_norm(float* x, float* xn, const float* w_pre, float eps, const void* wq, const void* sc,

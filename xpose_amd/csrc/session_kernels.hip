@@ -1,16 +1,16 @@
 // Small kernels that exist only for the decode session's token step.
 //
-//  embed            token row of the tied int4 table, dequantised and scaled
-//                   by sqrt(hidden) — the reference does this on the CPU from
-//                   the GGUF mapping and uploads it (decode.cpp:1618-1627);
-//                   here the token id is read from device memory so a whole
-//                   token step can be replayed from one captured graph.
+//  embed_norm       the token's embedding row (the model's fp32 row, or the
+//                   tied int4 table's, dequantised) scaled by sqrt(hidden),
+//                   and the first layer's input norm, in one launch — the
+//                   reference forms the row on the CPU from the GGUF mapping
+//                   and uploads it (decode.cpp:1618-1627); here the token id
+//                   is read from device memory so a whole token step can be
+//                   replayed from one captured graph.
 //  norm_res_norm    x += rmsnorm(y) * (1 + w_post); out = rmsnorm(x) * (1 +
 //                   w_pre): the post-sublayer norm, the residual add and the
 //                   next sublayer's pre-norm of record_token
 //                   (decode.cpp:1739-1751, 1668) in one workgroup.
-//  embed_norm       the embedding row and the first layer's input norm in
-//                   one launch (the graph path).
 //  advance          position += 1 after a step (the greedy step's argmax
 //                   does it itself).
 #include "xp_device.hpp"
@@ -52,22 +52,10 @@ __device__ __forceinline__ float embed_value(uint32_t k, uint32_t tok, const u32
     return (q * s) * embed_scale;
 }
 
-// state[0] = position, state[1] = token to run.
-__global__ void embed_kernel(float* x, const u32x4* wq, const void* sc, int fmt,
-                             uint32_t hidden, uint32_t vocab, float embed_scale,
-                             const uint32_t* state, uint32_t* hist, const float* table) {
-    const uint32_t pos = state[0];
-    uint32_t tok = state[1];
-    if (tok >= vocab) tok = 0;   // the host validates ids; never read out of bounds
-    const uint32_t k = blockIdx.x * blockDim.x + threadIdx.x;
-    if (k == 0) hist[pos] = tok;
-    if (k >= hidden) return;
-    x[k] = embed_value(k, tok, wq, sc, fmt, hidden, vocab, embed_scale, table);
-}
-
 // The embedding row and the first layer's input norm in one workgroup:
 // x = the row, xn = rmsnorm(x) (1 + w_pre), the sums in norm_res_norm's order
-// (the same bits as embed_kernel followed by norm_res_norm without y).
+// (the same bits as writing the row and then norm_res_norm without y).
+// state[0] = position, state[1] = token to run.
 __global__ __launch_bounds__(1024) void embed_norm_kernel(float* x, float* xn, const float* w_pre, float eps,
                                                           const u32x4* wq, const void* sc, int fmt,
                                                           uint32_t hidden, uint32_t vocab, float embed_scale,
@@ -126,17 +114,6 @@ __global__ __launch_bounds__(1024) void norm_res_norm_kernel(float* x, const flo
 }
 
 __global__ void advance_kernel(uint32_t* state) { state[0] += 1u; }
-
-int launch_embed(float* x, const void* wq, const void* sc, int fmt, uint32_t hidden,
-                 uint32_t vocab, float embed_scale, const uint32_t* state, uint32_t* hist,
-                 const float* table, hipStream_t st) {
-    hipLaunchKernelGGL(embed_kernel, dim3((hidden + 255) / 256), dim3(256), 0, st, x,
-                       reinterpret_cast<const u32x4*>(wq), sc, fmt, hidden, vocab, embed_scale,
-                       state, hist, table);
-    hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return set_error(XP_E_HIP, "embed: launch -> %s", hipGetErrorString(e));
-    return XP_OK;
-}
 
 int launch_embed_norm(float* x, float* xn, const float* w_pre, float eps, const void* wq, const void* sc,
                       int fmt, uint32_t hidden, uint32_t vocab, float embed_scale, const uint32_t* state,
