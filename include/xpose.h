@@ -579,6 +579,16 @@ int xp_batch_forward(xp_batch* b, const uint32_t* tokens);
 /* Sample-first step for every sequence (decode.cpp:1830-1850): draws
  * tokens_out from the last logits, then runs xp_batch_forward on them. */
 int xp_batch_decode_step(xp_batch* b, uint32_t* tokens_out);
+/* n sample-first steps, the same tokens as n calls of xp_batch_decode_step
+ * (tokens_out[k * n_seq + i]: step k's token of sequence i): the first draw
+ * on the host from the last candidates, the following ones by a kernel at
+ * the end of each step's graph (the host draw's arithmetic: the candidates
+ * in (value desc, index asc) order, exp in float, sums in double, the same
+ * Philox uniforms), so the steps are queued back to back with no host round
+ * trip between them (the reference's loop draws on the host between steps,
+ * decode.cpp:1830-1861). Falls back to n xp_batch_decode_step calls for the
+ * persistent step kernel. */
+int xp_batch_decode_steps(xp_batch* b, uint32_t n, uint32_t* tokens_out);
 int xp_batch_last_logits(xp_batch* b, uint32_t seq, float* out, uint32_t n);
 /* The best n <= 64 candidates of sequence seq, (value desc, index asc). */
 int xp_batch_last_candidates(xp_batch* b, uint32_t seq, float* val, uint32_t* idx, uint32_t n);

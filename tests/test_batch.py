@@ -137,6 +137,56 @@ def test_gpu_batch_sampling_draws(xp, xo):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("mode", ["sample", "greedy"])
+def test_gpu_batch_decode_steps_equals_steps(xp, xo, mode):
+    """xp_batch_decode_steps (the draws after the first on the device, the
+    steps queued back to back) gives the tokens, positions, last candidates
+    and appended K/V rows of as many xp_batch_decode_step calls on a batch
+    built alike: 270 steps, i.e. a chain of 257 and one of 13 (the device
+    keeps 256 draws between host reads), then one more step each way."""
+    X = xp
+    print(f"case batch decode_steps {mode}", flush=True)
+    sample = mode == "sample"
+    # an untied fp32 N(0, 1) embedding table and temperature 2 so that the
+    # streams move and the draws spread over several candidates
+    cfg = X.XpConfig.gemma3_1b(n_layers=2, vocab=16384, max_seq=512, sample_mode=1 if sample else 0,
+                               temperature=2.0, top_k=64, top_p=0.95, seed=1234, seq_id=40)
+    sess, t = build(X, xo, cfg)
+    emb = np.random.default_rng(11).normal(0, 1, (cfg.vocab, cfg.hidden)).astype(np.float32)
+    sess.upload(-1, X.T_EMBED, emb)
+    B = 16
+    r = np.random.default_rng(7)
+    pos0 = r.integers(0, 200, B)
+    tok0 = r.integers(0, cfg.vocab, B)
+    a = X.DecodeBatch(sess, B, cfg.max_seq)
+    b = X.DecodeBatch(sess, B, cfg.max_seq)
+    for x in (a, b):
+        x.set_positions(pos0)
+        x.forward(tok0)
+    n = 270
+    want = np.stack([a.decode_step() for _ in range(n)])
+    got = b.decode_steps(n)
+    assert np.array_equal(got, want)
+    # the streams move
+    assert min(len(np.unique(want[:, i])) for i in range(B)) > 5
+    assert np.array_equal(a.positions(), b.positions())
+    for i in range(B):
+        va, ia = a.last_candidates(i)
+        vb, ib = b.last_candidates(i)
+        assert np.array_equal(ia, ib) and np.array_equal(va.view(np.uint32), vb.view(np.uint32)), i
+    for i in (0, 7, 15):
+        for layer in (0, 1):
+            for which in (0, 1):
+                ka = a.kv_download(i, layer, which, int(pos0[i]), n + 1)
+                kb = b.kv_download(i, layer, which, int(pos0[i]), n + 1)
+                assert np.array_equal(ka, kb), (i, layer, which)
+    assert np.array_equal(a.decode_step(), b.decode_step())
+    a.close()
+    b.close()
+    sess.close()
+
+
+@pytest.mark.gpu
 def test_gpu_batch_full_size_cfg5(xp, xo):
     """Benchmark config 5 at full size: 26 layers, vocab 262144, 16 sequences
     at the benchmark's Philox depths in [128, 4096] (global-layer spans to

@@ -178,6 +178,7 @@ def _declare(lib: C.CDLL) -> None:
         "xp_batch_positions": (i32, [vp, vp]),
         "xp_batch_forward": (i32, [vp, vp]),
         "xp_batch_decode_step": (i32, [vp, vp]),
+        "xp_batch_decode_steps": (i32, [vp, u32, vp]),
         "xp_batch_last_logits": (i32, [vp, u32, vp, u32]),
         "xp_batch_last_candidates": (i32, [vp, u32, vp, vp, u32]),
         "xp_batch_last_ms": (i32, [vp, P(f32)]),
@@ -522,6 +523,14 @@ class DecodeBatch:
     def decode_step(self) -> np.ndarray:
         out = np.empty(self.n, np.uint32)
         call("xp_batch_decode_step", self.h, out.ctypes.data)
+        return out
+
+    def decode_steps(self, steps: int) -> np.ndarray:
+        """steps sample-first steps queued back to back (the draws after the
+        first on the device): [steps][n_seq] tokens, those of as many
+        decode_step calls."""
+        out = np.empty((steps, self.n), np.uint32)
+        call("xp_batch_decode_steps", self.h, steps, out.ctypes.data)
         return out
 
     def last_logits(self, seq: int) -> np.ndarray:

@@ -32,6 +32,7 @@ constexpr uint32_t kBatchMax = 16;
 constexpr uint32_t kBlkB = 32;           // quantisation block along k
 constexpr uint32_t kGrpB = 64;           // KM4 column group
 constexpr uint32_t kCand = 64;           // candidates per sequence (top-k <= 64)
+constexpr uint32_t kHistCap = 256;       // steps a chained decode records between host reads
 // The candidates are the reference's harvest, the best 4 of each of 4096
 // strided chains (topk4_partial, llm_sampling.cl:318-347); the 64 best of
 // those are selected exactly on the device.
@@ -78,6 +79,14 @@ struct Batch {
     // reads after each step)
     bool any_xchg = false;
     hipGraphExec_t graph = nullptr;
+    // Chained decode (xp_batch_decode_steps): the step's graph with the
+    // draw on the device appended, reading its tokens from d_tok and writing
+    // the candidates to d_val / d_idx, the drawn tokens to d_tok and d_hist
+    // ([kHistCap][B], slot = Philox step % kHistCap); d_steps the sequences'
+    // Philox step counters.
+    hipGraphExec_t graph_fd = nullptr;
+    float* d_val = nullptr;
+    uint32_t *d_idx = nullptr, *d_tok = nullptr, *d_steps = nullptr, *d_hist = nullptr;
     hipEvent_t ev[2] = {nullptr, nullptr};
     std::vector<uint32_t> pos, steps;
     bool logits_valid = false;
@@ -102,12 +111,16 @@ struct Batch {
     unsigned long long* d_trace = nullptr;   // the step kernel's stage timeline, when on
     size_t trace_n = 0;
 
-    int record();
+    int record(bool chain = false);
     int setup_step(int exec);
     int forward(const uint32_t* tokens);
+    int decode_steps(uint32_t n, uint32_t* tokens_out);
+    int capture(bool chain, hipGraphExec_t* out);
+    int attn_error_check();
+    void host_draw(uint32_t* tokens_out);
 };
 
-int Batch::record() {
+int Batch::record(bool chain) {
     const xp_config& c = w.cfg;
     const uint32_t H = c.hidden, qd = c.n_heads * c.head_dim, kvd = c.n_kv_heads * c.head_dim;
     const int fmt = c.scale_fmt;
@@ -150,7 +163,7 @@ int Batch::record() {
     // staging launch
     auto embed_prep = [&](void* a_, float* asum_) {
         BprepArgs p0{0, x, nullptr, nullptr, nullptr, w.layer[0].norm[0], a_, asum_, H, eps};
-        p0.tok = m_tok;
+        p0.tok = chain ? d_tok : m_tok;
         p0.ewq = w.lm_w;
         p0.esc = w.lm_s;
         p0.etable = w.embed;
@@ -251,7 +264,11 @@ int Batch::record() {
         const MvMatDesc lm{logits, w.lm_w, w.lm_s, c.vocab};
         XB(gemm(&lm, 1, H, "batch lm_head"));
         XB(launch_topk4(cval, cidx, logits, c.vocab, kHarvestParts, st, B));
-        XB(launch_select_rows(m_val, m_idx, cval, cidx, kHarvest, kCand, B, st, d_pos));
+        XB(launch_select_rows(chain ? d_val : m_val, chain ? d_idx : m_idx, cval, cidx, kHarvest, kCand, B, st,
+                              d_pos));
+        if (chain)
+            XB(launch_draw_rows(d_val, d_idx, kCand, B, c.sample_mode, c.temperature, c.top_k, c.top_p, c.seed,
+                                c.seq_id, d_steps, d_tok, d_hist, kHistCap, st));
     }
 #undef XB
     return XP_OK;
@@ -449,6 +466,130 @@ int Batch::setup_step(int exec) {
     return XP_OK;
 }
 
+// Captures the step (with the device draw appended when `chain`) into *out.
+int Batch::capture(bool chain, hipGraphExec_t* out) {
+    hipGraph_t g = nullptr;
+    XP_HIP(hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal));
+    const int rc = record(chain);
+    const hipError_t e = hipStreamEndCapture(st, &g);
+    if (rc != XP_OK) {
+        if (g) (void)hipGraphDestroy(g);
+        return rc;
+    }
+    if (e != hipSuccess)
+        return set_error(XP_E_HIP, "xp_batch_forward: capture failed: %s", hipGetErrorString(e));
+    const hipError_t ie = hipGraphInstantiate(out, g, nullptr, nullptr, 0);
+    (void)hipGraphDestroy(g);
+    if (ie != hipSuccess) {
+        *out = nullptr;
+        return set_error(XP_E_HIP, "xp_batch_forward: instantiate: %s", hipGetErrorString(ie));
+    }
+    return XP_OK;
+}
+
+// After a synchronised graph step: the exchange-mode attention's error words
+// (copied to h_attn by the step).
+int Batch::attn_error_check() {
+    if (!any_xchg) return XP_OK;
+    const size_t attn_words = size_t(B) * w.cfg.n_kv_heads * kAttnTicketsPerHead;
+    uint32_t err = 0;
+    for (size_t i = kAttnXErrWord; i < attn_words; i += kAttnTicketsPerHead) err |= h_attn[i];
+    if (!err) return XP_OK;
+    // an exchange-mode attention wait timed out (its splits were not
+    // resident at once): outputs hold NaN; the records and tickets start
+    // over from zero, positions stay where they were
+    XP_HIP(hipMemcpy(d_pos, pos.data(), B * 4, hipMemcpyHostToDevice));
+    XP_HIP(hipMemset(attn_part, 0, (size_t(B) * attn_part_seq + 1) * 4));
+    XP_HIP(hipMemset(attn_tickets, 0, attn_words * 4));
+    XP_HIP(hipDeviceSynchronize());
+    logits_valid = false;
+    return set_error(XP_E_DEVICE, "xp_batch_forward: a decode attention wait ran past its "
+                     "limit (another kernel held CUs of this GPU); the step's results and "
+                     "the KV rows it appended are not valid, positions are unchanged");
+}
+
+// The sample-first draw from the last step's candidates (decode.cpp:1830-1850),
+// on the host: greedy takes each sequence's best candidate; sampling draws
+// with Philox(seed, seq_id + i, step) and advances the step.
+void Batch::host_draw(uint32_t* tokens_out) {
+    const xp_config& c = w.cfg;
+    std::vector<float> val(kCand);
+    std::vector<uint32_t> idx(kCand);
+    for (uint32_t i = 0; i < B; ++i) {
+        const float* cv = h_val + size_t(i) * kCand;
+        const uint32_t* ci = h_idx + size_t(i) * kCand;
+        if (c.sample_mode == 0) {
+            tokens_out[i] = ci[0];    // the maximum, lowest index on ties
+            continue;
+        }
+        uint32_t n = 0;
+        for (uint32_t j = 0; j < kCand; ++j)
+            if (ci[j] != 0xFFFFFFFFu) { val[n] = cv[j]; idx[n] = ci[j]; ++n; }
+        const double u = philox_uniform(c.seed, c.seq_id + i, steps[i]++);
+        tokens_out[i] = draw(val.data(), idx.data(), n, c.temperature, c.top_k, c.top_p, u);
+    }
+}
+
+// n sample-first steps (n x xp_batch_decode_step, the same tokens): the
+// first draw on the host from the last candidates, the next n - 1 on the
+// device at the end of each step's graph, the steps replayed back to back
+// with no host round trip between them; the last step is the plain graph,
+// so its candidates are in the pinned arrays as after xp_batch_forward.
+int Batch::decode_steps(uint32_t n, uint32_t* out) {
+    XP_REQUIRE(logits_valid, "xp_batch_decode_steps: no logits yet (run xp_batch_forward first)");
+    if (n == 0) return XP_OK;
+    if (step_kernel || prefill || n == 1) {
+        for (uint32_t k = 0; k < n; ++k) {
+            host_draw(out + size_t(k) * B);
+            if (const int rc = forward(out + size_t(k) * B); rc != XP_OK) return rc;
+        }
+        return XP_OK;
+    }
+    for (uint32_t i = 0; i < B; ++i)
+        XP_REQUIRE(pos[i] + n <= S, "xp_batch_decode_steps: sequence %u at position %u + %u steps > max_seq %u",
+                   i, pos[i], n, S);
+    if (!graph)
+        if (const int rc = capture(false, &graph); rc != XP_OK) return rc;
+    if (!graph_fd)
+        if (const int rc = capture(true, &graph_fd); rc != XP_OK) return rc;
+    float total_ms = 0.0f;
+    for (uint32_t k0 = 0; k0 < n;) {
+        const uint32_t m = std::min(n - k0, kHistCap + 1u);   // steps in this chain
+        uint32_t* o = out + size_t(k0) * B;
+        host_draw(o);
+        for (uint32_t i = 0; i < B; ++i)
+            XP_REQUIRE(o[i] < w.cfg.vocab, "xp_batch_decode_steps: token %u of sequence %u >= vocab", o[i], i);
+        const std::vector<uint32_t> s0 = steps;   // the device draws' first counters
+        XP_HIP(hipMemcpyAsync(d_tok, o, B * 4, hipMemcpyHostToDevice, st));
+        XP_HIP(hipMemcpyAsync(d_steps, s0.data(), B * 4, hipMemcpyHostToDevice, st));
+        XP_HIP(hipEventRecord(ev[0], st));
+        for (uint32_t k = 1; k < m; ++k) XP_HIP(hipGraphLaunch(graph_fd, st));
+        // the last step reads its tokens from the pinned array
+        XP_HIP(hipMemcpyAsync(h_tok, d_tok, B * 4, hipMemcpyDeviceToHost, st));
+        XP_HIP(hipGraphLaunch(graph, st));
+        XP_HIP(hipEventRecord(ev[1], st));
+        const size_t attn_words = size_t(B) * w.cfg.n_kv_heads * kAttnTicketsPerHead;
+        if (any_xchg) XP_HIP(hipMemcpyAsync(h_attn, attn_tickets, attn_words * 4, hipMemcpyDeviceToHost, st));
+        std::vector<uint32_t> hist(size_t(kHistCap) * B);
+        XP_HIP(hipMemcpyAsync(hist.data(), d_hist, hist.size() * 4, hipMemcpyDeviceToHost, st));
+        XP_HIP(hipStreamSynchronize(st));
+        float ms = 0.0f;
+        (void)hipEventElapsedTime(&ms, ev[0], ev[1]);
+        total_ms += ms;
+        if (const int rc = attn_error_check(); rc != XP_OK) return rc;
+        for (uint32_t k = 1; k < m; ++k)
+            for (uint32_t i = 0; i < B; ++i)
+                o[size_t(k) * B + i] = hist[size_t((s0[i] + k - 1u) % kHistCap) * B + i];
+        if (w.cfg.sample_mode != 0)
+            for (uint32_t i = 0; i < B; ++i) steps[i] += m - 1u;
+        for (uint32_t i = 0; i < B; ++i) pos[i] += m;
+        k0 += m;
+    }
+    last_ms = total_ms / float(n);
+    logits_valid = true;
+    return XP_OK;
+}
+
 int Batch::forward(const uint32_t* tokens) {
     for (uint32_t i = 0; i < B; ++i) {
         XP_REQUIRE(pos[i] < S, "xp_batch_forward: sequence %u is at position %u of max_seq %u", i,
@@ -456,24 +597,8 @@ int Batch::forward(const uint32_t* tokens) {
         XP_REQUIRE(tokens[i] < w.cfg.vocab, "xp_batch_forward: token %u of sequence %u >= vocab",
                    tokens[i], i);
     }
-    if (!graph) {
-        hipGraph_t g = nullptr;
-        XP_HIP(hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal));
-        const int rc = record();
-        const hipError_t e = hipStreamEndCapture(st, &g);
-        if (rc != XP_OK) {
-            if (g) (void)hipGraphDestroy(g);
-            return rc;
-        }
-        if (e != hipSuccess)
-            return set_error(XP_E_HIP, "xp_batch_forward: capture failed: %s", hipGetErrorString(e));
-        const hipError_t ie = hipGraphInstantiate(&graph, g, nullptr, nullptr, 0);
-        (void)hipGraphDestroy(g);
-        if (ie != hipSuccess) {
-            graph = nullptr;
-            return set_error(XP_E_HIP, "xp_batch_forward: instantiate: %s", hipGetErrorString(ie));
-        }
-    }
+    if (!graph)
+        if (const int rc = capture(false, &graph); rc != XP_OK) return rc;
     // the tokens go to the device as the graph's embedding gather reads them
     // from this pinned array; the previous step has finished (synchronised
     // below), so nothing reads it while it changes
@@ -486,23 +611,8 @@ int Batch::forward(const uint32_t* tokens) {
     else if (any_xchg) XP_HIP(hipMemcpyAsync(h_attn, attn_tickets, attn_words * 4, hipMemcpyDeviceToHost, st));
     XP_HIP(hipStreamSynchronize(st));
     (void)hipEventElapsedTime(&last_ms, ev[0], ev[1]);
-    if (!step_kernel && any_xchg) {
-        uint32_t err = 0;
-        for (size_t i = kAttnXErrWord; i < attn_words; i += kAttnTicketsPerHead) err |= h_attn[i];
-        if (err) {
-            // an exchange-mode attention wait timed out (its splits were not
-            // resident at once): outputs hold NaN; the records and tickets
-            // start over from zero, positions stay where they were
-            XP_HIP(hipMemcpy(d_pos, pos.data(), B * 4, hipMemcpyHostToDevice));
-            XP_HIP(hipMemset(attn_part, 0, (size_t(B) * attn_part_seq + 1) * 4));
-            XP_HIP(hipMemset(attn_tickets, 0, attn_words * 4));
-            XP_HIP(hipDeviceSynchronize());
-            logits_valid = false;
-            return set_error(XP_E_DEVICE, "xp_batch_forward: a decode attention wait ran past its "
-                             "limit (another kernel held CUs of this GPU); the step's results and "
-                             "the KV rows it appended are not valid, positions are unchanged");
-        }
-    }
+    if (!step_kernel)
+        if (const int rc = attn_error_check(); rc != XP_OK) return rc;
     if (step_kernel && h_status[0] != 0u) {
         // a wait ran past its limit (the grid was not resident at once): the
         // step's results are not valid
@@ -536,6 +646,7 @@ void release(Batch* b) {
     if (!b) return;
     if (b->st) (void)hipStreamSynchronize(b->st);
     if (b->graph) (void)hipGraphExecDestroy(b->graph);
+    if (b->graph_fd) (void)hipGraphExecDestroy(b->graph_fd);
     for (auto& e : b->ev)
         if (e) (void)hipEventDestroy(e);
     if (b->arena) (void)hipFree(b->arena);
@@ -634,7 +745,9 @@ int make_batch(const xp_session* weights, uint32_t n_seq, uint32_t max_seq, bool
         size_t(kmax / kBlkB) * 16 * 4,                           // block sums
         std::max<size_t>(part_cap, 1) * 4, size_t(tick) * 4,
         size_t(B) * b.attn_part_seq * 4 + 4, size_t(B) * c.n_kv_heads * kAttnTicketsPerHead * 4,
-        size_t(B) * kHarvest * 4, size_t(B) * kHarvest * 4, size_t(B) * 4};
+        size_t(B) * kHarvest * 4, size_t(B) * kHarvest * 4, size_t(B) * 4,
+        size_t(B) * kCand * 4, size_t(B) * kCand * 4, size_t(B) * 4, size_t(B) * 4,
+        size_t(kHistCap) * B * 4};
     size_t total = 0;
     for (size_t z : sz) total += al(z);
     if (hipStreamCreateWithFlags(&b.st, hipStreamNonBlocking) != hipSuccess)
@@ -670,6 +783,11 @@ int make_batch(const xp_session* weights, uint32_t n_seq, uint32_t max_seq, bool
     b.cval = reinterpret_cast<float*>(nxt());
     b.cidx = reinterpret_cast<uint32_t*>(nxt());
     b.d_pos = reinterpret_cast<uint32_t*>(nxt());
+    b.d_val = reinterpret_cast<float*>(nxt());
+    b.d_idx = reinterpret_cast<uint32_t*>(nxt());
+    b.d_tok = reinterpret_cast<uint32_t*>(nxt());
+    b.d_steps = reinterpret_cast<uint32_t*>(nxt());
+    b.d_hist = reinterpret_cast<uint32_t*>(nxt());
     const unsigned mapped = hipHostMallocMapped | hipHostMallocCoherent;
     if (hipHostMalloc(reinterpret_cast<void**>(&b.h_tok), B * 4, mapped) != hipSuccess ||
         hipHostMalloc(reinterpret_cast<void**>(&b.h_val), size_t(B) * kCand * 4, mapped) != hipSuccess ||
@@ -886,23 +1004,13 @@ int xp_batch_decode_step(xp_batch* h, uint32_t* tokens_out) {
     XP_REQUIRE(h && tokens_out, "null pointer");
     Batch& b = h->b;
     XP_REQUIRE(b.logits_valid, "xp_batch_decode_step: no logits yet (run xp_batch_forward first)");
-    const xp_config& c = b.w.cfg;
-    std::vector<float> val(kCand);
-    std::vector<uint32_t> idx(kCand);
-    for (uint32_t i = 0; i < b.B; ++i) {
-        const float* cv = b.h_val + size_t(i) * kCand;
-        const uint32_t* ci = b.h_idx + size_t(i) * kCand;
-        if (c.sample_mode == 0) {
-            tokens_out[i] = ci[0];    // the maximum, lowest index on ties
-            continue;
-        }
-        uint32_t n = 0;
-        for (uint32_t j = 0; j < kCand; ++j)
-            if (ci[j] != 0xFFFFFFFFu) { val[n] = cv[j]; idx[n] = ci[j]; ++n; }
-        const double u = philox_uniform(c.seed, c.seq_id + i, b.steps[i]++);
-        tokens_out[i] = draw(val.data(), idx.data(), n, c.temperature, c.top_k, c.top_p, u);
-    }
+    b.host_draw(tokens_out);
     return b.forward(tokens_out);
+}
+
+int xp_batch_decode_steps(xp_batch* h, uint32_t n, uint32_t* tokens_out) {
+    XP_REQUIRE(h && tokens_out, "null pointer");
+    return h->b.decode_steps(n, tokens_out);
 }
 
 int xp_batch_last_logits(xp_batch* h, uint32_t seq, float* out, uint32_t n) {

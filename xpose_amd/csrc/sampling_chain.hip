@@ -402,6 +402,122 @@ __global__ __launch_bounds__(kSelThreads) void select_rows_kernel(float* oval, u
     }
 }
 
+// The sample-first draw of a batched step on the device, one wave per
+// sequence, in the host draw's arithmetic (session.cpp draw(), after
+// decode.cpp:1893-1915), so that steps can follow each other with no host
+// round trip: the candidates are select_rows' output, already in the host
+// draw's (value desc, index asc) order; e = exp((v - max) / T) in float (the
+// exponential in double, rounded once); the sums, the top-p cut and the
+// inverse-CDF walk in double, in candidate order, on one lane; u from
+// Philox4x32-10 (Salmon et al. 2011) at (seed, seq0 + row, step), 53 bits.
+// Greedy (mode 0) takes candidate 0. Writes the token to tok[row] and to
+// hist[(steps[row] % hist_cap) * rows + row], and advances steps[row] (in
+// greedy mode a history counter only).
+__device__ __forceinline__ void philox4x32_10_dev(uint32_t c0, uint32_t c1, uint32_t c2, uint32_t c3,
+                                                  uint32_t k0, uint32_t k1, uint32_t (&o)[4]) {
+#pragma unroll
+    for (int r = 0; r < 10; ++r) {
+        if (r) {
+            k0 += 0x9E3779B9u;
+            k1 += 0xBB67AE85u;
+        }
+        const uint32_t hi0 = __umulhi(0xD2511F53u, c0), lo0 = 0xD2511F53u * c0;
+        const uint32_t hi1 = __umulhi(0xCD9E8D57u, c2), lo1 = 0xCD9E8D57u * c2;
+        const uint32_t n0 = hi1 ^ c1 ^ k0, n2 = hi0 ^ c3 ^ k1;
+        c0 = n0;
+        c1 = lo1;
+        c2 = n2;
+        c3 = lo0;
+    }
+    o[0] = c0;
+    o[1] = c1;
+    o[2] = c2;
+    o[3] = c3;
+}
+
+__global__ __launch_bounds__(kWave) void draw_rows_kernel(const float* val, const uint32_t* idx, uint32_t k,
+                                                          int mode, float temperature, uint32_t top_k,
+                                                          float top_p, uint32_t seed, uint32_t seq0,
+                                                          uint32_t* steps, uint32_t* tok, uint32_t* hist,
+                                                          uint32_t hist_cap) {
+    __shared__ float sv[kWave], se[kWave];
+    __shared__ uint32_t si[kWave];
+    const uint32_t row = blockIdx.x, lane = threadIdx.x, rows = gridDim.x;
+    if (mode == 0) {
+        if (lane == 0) {
+            const uint32_t t = idx[size_t(row) * k];
+            tok[row] = t;
+            hist[(steps[row] % hist_cap) * rows + row] = t;
+            steps[row] += 1u;   // the history slot only (greedy draws no uniform)
+        }
+        return;
+    }
+    // the valid candidates, compacted in order (the host skips empty slots)
+    const float v = lane < k ? val[size_t(row) * k + lane] : -INFINITY;
+    const uint32_t d = lane < k ? idx[size_t(row) * k + lane] : 0xFFFFFFFFu;
+    const bool ok = d != 0xFFFFFFFFu;
+    const unsigned long long m = __ballot(ok);
+    const uint32_t at = uint32_t(__popcll(m & ((1ull << lane) - 1ull))), n = uint32_t(__popcll(m));
+    if (ok) {
+        sv[at] = v;
+        si[at] = d;
+    }
+    __syncthreads();
+    const float t = temperature > 0.0f ? temperature : 1.0f;
+    const uint32_t kk = top_k ? min(top_k, n) : n;
+    float maxl = -INFINITY;
+    for (uint32_t i = 0; i < kk; ++i) maxl = maxl < sv[i] ? sv[i] : maxl;
+    if (lane < kk) se[lane] = float(exp(double((sv[lane] - maxl) / t)));
+    __syncthreads();
+    if (lane != 0) return;
+    uint32_t token = 0u;
+    if (n > 0) {
+        uint32_t nn = kk;
+        double sum = 0.0;
+        for (uint32_t i = 0; i < nn; ++i) sum += double(se[i]);
+        if (top_p > 0.0f && top_p < 1.0f && sum > 0.0) {
+            double acc = 0.0;
+            const double cut = double(top_p) * sum;
+            uint32_t keep = 0;
+            for (; keep < nn; ++keep) {
+                acc += double(se[keep]);
+                if (acc >= cut) break;
+            }
+            nn = min(nn, keep + 1u);
+            sum = 0.0;
+            for (uint32_t i = 0; i < nn; ++i) sum += double(se[i]);
+        }
+        uint32_t o[4];
+        philox4x32_10_dev(steps[row], 0u, 0u, 0u, seed, seq0 + row, o);
+        const uint64_t bits = (uint64_t(o[0]) << 21) | (o[1] >> 11);
+        const double u = double(bits) * (1.0 / 9007199254740992.0);
+        double r = u * sum;
+        token = si[nn - 1u];
+        for (uint32_t i = 0; i < nn; ++i) {
+            r -= double(se[i]);
+            if (r <= 0.0) {
+                token = si[i];
+                break;
+            }
+        }
+    }
+    tok[row] = token;
+    hist[(steps[row] % hist_cap) * rows + row] = token;
+    steps[row] += 1u;
+}
+
+int launch_draw_rows(const float* val, const uint32_t* idx, uint32_t k, uint32_t rows, int mode,
+                     float temperature, uint32_t top_k, float top_p, uint32_t seed, uint32_t seq0,
+                     uint32_t* steps, uint32_t* tok, uint32_t* hist, uint32_t hist_cap, hipStream_t st) {
+    if (k < 1 || k > uint32_t(kWave) || rows == 0 || hist_cap == 0)
+        return set_error(XP_E_ARG, "draw rows: k=%u rows=%u hist_cap=%u", k, rows, hist_cap);
+    hipLaunchKernelGGL(draw_rows_kernel, dim3(rows), dim3(kWave), 0, st, val, idx, k, mode, temperature,
+                       top_k, top_p, seed, seq0, steps, tok, hist, hist_cap);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return set_error(XP_E_HIP, "draw rows: launch -> %s", hipGetErrorString(e));
+    return XP_OK;
+}
+
 int launch_select_rows(float* oval, uint32_t* oidx, const float* cval, const uint32_t* cidx,
                        uint32_t ncand, uint32_t k, uint32_t rows, hipStream_t st, uint32_t* pos_inc) {
     if (k < 1 || k > kTopkMax || rows == 0 || ncand == 0 || ncand > kSelThreads * kSelPer)

@@ -192,6 +192,12 @@ int launch_topk4(float* cval, uint32_t* cidx, const float* x, uint32_t n, uint32
 // exact. Unfilled list slots carry index 0xFFFFFFFF and are skipped. With
 // pos_inc, row r's workgroup also adds 1 to pos_inc[r] (the batched step's
 // position advance, which nothing in the select reads).
+// The batched step's sample-first draw on the device (one wave per row, the
+// host draw's arithmetic): token of row r to tok[r] and to
+// hist[(steps[r] % hist_cap) * rows + r]; steps[r] advances (sampling only).
+int launch_draw_rows(const float* val, const uint32_t* idx, uint32_t k, uint32_t rows, int mode,
+                     float temperature, uint32_t top_k, float top_p, uint32_t seed, uint32_t seq0,
+                     uint32_t* steps, uint32_t* tok, uint32_t* hist, uint32_t hist_cap, hipStream_t st);
 int launch_select_rows(float* oval, uint32_t* oidx, const float* cval, const uint32_t* cidx,
                        uint32_t ncand, uint32_t k, uint32_t rows, hipStream_t st,
                        uint32_t* pos_inc = nullptr);
