@@ -224,18 +224,19 @@ def native_leg(X, iters: int = 400):
     return out
 
 
-def stream_ceiling(X, nbytes: int = 1 << 30, iters: int = 20, rounds: int = 5) -> float:
+def stream_ceiling(X, nbytes: int = 1 << 30, iters: int = 20, rounds: int = 5, grid: int = 512) -> float:
     """Achievable HBM read bandwidth (GB/s): the 16-byte streaming probe over a
-    1 GiB buffer (4x the Infinity Cache), `iters` launches a round, the best
-    of `rounds` rounds (single rounds of one process have read 5.5-6.4 TB/s
-    on one box; the reference keeps the best of R for the same reason,
-    matvec_bench.cpp:340-353)."""
+    1 GiB buffer (4x the Infinity Cache) with `grid` workgroups of 512 threads
+    (512, two a CU, read 7.2 TB/s where one a CU read 6.45 and 1024-4096
+    6.8-6.9), `iters` launches a round, the best of `rounds` rounds (the
+    reference keeps the best of R, matvec_bench.cpp:340-353)."""
     buf = X.DeviceBuffer(nbytes)
     X.call("xp_memset", buf.vp, 0, nbytes)
+    P = (C.c_void_p * 1)(buf.ptr)
     best = 0.0
     for _ in range(rounds):
         ms = C.c_float()
-        X.call("xp_stream_read_timed", buf.vp, nbytes, iters, None, C.byref(ms))
+        X.call("xp_stream_read_rot_timed", P, 1, nbytes, grid, iters, None, C.byref(ms))
         best = max(best, nbytes * iters / (ms.value / 1e3) / 1e9)
     buf.close()
     return best
