@@ -163,7 +163,7 @@ __device__ __forceinline__ void block_dot_bc(const u32x4 (&w)[NB], const u32x2 (
     int32_t X[NB], Y[NB], Z[NB];
 #pragma unroll
     for (int b = 0; b < NB; ++b) X[b] = Y[b] = Z[b] = 0;
-    // round 1: planes P - 1, P - 2, P - 3
+    // first pass: planes P - 1, P - 2, P - 3
     auto round1 = [&](auto cc) {
         constexpr int C = decltype(cc)::value;
 #pragma unroll
@@ -182,7 +182,7 @@ __device__ __forceinline__ void block_dot_bc(const u32x4 (&w)[NB], const u32x2 (
         X[b] <<= 12;
         if constexpr (P == 5) Y[b] <<= 12;
     }
-    // round 2: plane P - 4 onto X, plane P - 5 (P = 5) onto Y
+    // second pass: plane P - 4 onto X, plane P - 5 (P = 5) onto Y
     auto round2 = [&](auto cc) {
         constexpr int C = decltype(cc)::value;
 #pragma unroll
